@@ -1,0 +1,259 @@
+/*
+ * vla_simd_hip.h - C ABI of libvla_simd_hip.so, the MI355X (gfx950) backend of
+ * vla.simd's int8 linear + attention hot path.
+ *
+ * Two layers, as in the reference:
+ *   1. the handshake symbols every vla.simd library exports
+ *      (include/vla_simd.h:60-62, src/capi_version.cpp:13-15);
+ *   2. the op API the reference's src/nn layers call (src/ops/quant_ops.h,
+ *      src/ops/lm_ops.h), as extern "C" functions on plain pointers, plus the
+ *      device-resident int8 Linear that replaces nn::Linear's int8 state
+ *      (src/nn/linear.h:40-48, 85-99).
+ *
+ * Each op comes in two forms:
+ *   vla_<op>(...)        host pointers; copies in, runs on the library's stream,
+ *                        copies out, synchronizes. Same argument meaning as the
+ *                        reference op of the same name.
+ *   vla_<op>_dev(...)    device pointers and a hipStream_t (passed as void*,
+ *                        NULL = the null stream); asynchronous, allocates nothing.
+ *
+ * Layouts (row-major, as src/ops/lm_ops.h:11-14):
+ *   activations [seq, K] fp32; quantized activations [seq, ldq] int8 with
+ *   ldq >= i8_kpad(K) and columns [K, ldq) zero; int8 weights [N, ldw] int8
+ *   (one output channel per row, K contiguous - the GPU layout; the CPU panel
+ *   layout of pack_weights_i8 is not used on the device); heads
+ *   [seq, n_heads, head_dim].
+ *
+ * Errors: every fallible call returns vla_status (0 = VLA_OK). HIP runtime
+ * failures and C++ exceptions never cross the boundary: they come back as
+ * VLA_ERR_EXCEPTION and the message is kept per thread for vla_last_error().
+ * Where the reference asserts a precondition (e.g. the int8 K bound,
+ * src/nn/linear.cpp:67, tests/test_ops.cpp:79-92) this library returns
+ * VLA_ERR_ARG instead of running.
+ *
+ * Threading: calls on one stream are ordered; the host-pointer forms share one
+ * library stream and one grow-only staging arena guarded by a mutex.
+ */
+#ifndef VLA_SIMD_HIP_H
+#define VLA_SIMD_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VLA_API __attribute__((visibility("default")))
+
+#ifndef VLA_ABI_VERSION
+#define VLA_ABI_VERSION 1
+typedef enum {
+    VLA_OK            =  0,
+    VLA_ERR_ARG       = -1,
+    VLA_ERR_SHAPE     = -2,
+    VLA_ERR_EXCEPTION = -3
+} vla_status;
+#endif
+
+/* Epilogue activation of the int8 linear (applied after dequant + bias). */
+typedef enum {
+    VLA_ACT_NONE      = 0,
+    VLA_ACT_RELU      = 1,  /* relu, src/hal/common/eltwise.cpp:209 */
+    VLA_ACT_GELU_TANH = 2,  /* gelu_tanh, eltwise.cpp:74 */
+    VLA_ACT_GELU_ERF  = 3   /* gelu_erf, eltwise.cpp:143 */
+} vla_act;
+
+/* Attention mask kinds. The reference takes only an additive [seq_q, seq_k]
+ * array (src/ops/lm_ops.h:33); the generated kinds produce the same blocked
+ * set as the masks its graphs build without reading a [T,T] array. */
+typedef enum {
+    VLA_MASK_NONE   = 0,  /* gqa_attention_dense semantics */
+    VLA_MASK_DENSE  = 1,  /* mask [seq_q, seq_k] additive fp32, lowest()/-inf = blocked */
+    VLA_MASK_CAUSAL = 2,  /* key j blocked when j > i + causal_offset */
+    VLA_MASK_GROUPS = 3   /* key j blocked when !allow[qg[i]*n_groups + kg[j]] */
+} vla_mask_kind;
+
+typedef struct {
+    int32_t kind;            /* vla_mask_kind */
+    const float* dense;      /* VLA_MASK_DENSE: device or host pointer per call form */
+    int32_t causal_offset;   /* VLA_MASK_CAUSAL: usually seq_k - seq_q */
+    int32_t n_groups;        /* VLA_MASK_GROUPS: <= 256 */
+    const uint8_t* q_group;  /* [seq_q] */
+    const uint8_t* k_group;  /* [seq_k] */
+    const uint8_t* allow;    /* [n_groups * n_groups], 1 = query group may see key group */
+} vla_mask;
+
+/* ---------------------------------------------------------- handshake ---- */
+
+/* include/vla_simd.h:44,60 - returns VLA_ABI_VERSION (1). */
+VLA_API int32_t vla_abi_version(void);
+/* include/vla_simd.h:61, src/hal/arch.h:54 backend_name() - "hip-gfx950". */
+VLA_API const char* vla_backend_name(void);
+/* include/vla_simd.h:62, int8_gemm_available() (src/ops/quant_ops.h:41):
+ * 1 when a gfx950 device is visible and the int8 kernels can run on it. */
+VLA_API int32_t vla_int8_available(void);
+/* Message of the last call on this thread that did not return VLA_OK. */
+VLA_API const char* vla_last_error(void);
+
+/* ------------------------------------------------ device memory helpers -- */
+/* For callers with no allocator of their own (ctypes harnesses, C tests). */
+VLA_API int32_t vla_hip_malloc(void** ptr, size_t bytes);
+VLA_API int32_t vla_hip_free(void* ptr);
+VLA_API int32_t vla_hip_memcpy_h2d(void* dst, const void* src, size_t bytes);
+VLA_API int32_t vla_hip_memcpy_d2h(void* dst, const void* src, size_t bytes);
+VLA_API int32_t vla_hip_memset(void* dst, int32_t value, size_t bytes);
+VLA_API int32_t vla_hip_synchronize(void);
+VLA_API int32_t vla_hip_device_name(char* buf, int32_t len);
+
+/* -------------------------------------------- quant_ops.h (int8 linear) -- */
+
+/* i8_kpad (src/ops/quant_ops.h:45, gemm_i8.cpp:30): (K+3) & ~3. */
+VLA_API int32_t vla_i8_kpad(int32_t K);
+
+/* quantize_act_i8 (quant_ops.h:76, gemm_i8.cpp:209-244): per row t,
+ * s = amax>0 ? max(amax/127, FLT_MIN) : 1, xq = clamp(rne(x/s... as x*(1/s)), +-127),
+ * ascale[t] = s. xq is [seq, i8_kpad(K)]; the _dev form takes its stride ldq. */
+VLA_API int32_t vla_quantize_act_i8(const float* x, int8_t* xq, float* ascale,
+                                    int32_t seq, int32_t K);
+VLA_API int32_t vla_quantize_act_i8_dev(const float* x, int8_t* xq, int32_t ldq, float* ascale,
+                                        int32_t seq, int32_t K, void* stream);
+
+/* pack_weights_i8 (quant_ops.h:58, gemm_i8.cpp:56-89): the same per-row absmax
+ * quantizer over W [N, K] fp32, written as device-layout rows Wq [N, i8_kpad(K)]
+ * (no panels, no row sums: the i8 MFMA is signed x signed). */
+VLA_API int32_t vla_pack_weights_i8(const float* W, int8_t* Wq, float* wscale,
+                                    int32_t N, int32_t K);
+
+/* dense_linear_i8_pre (quant_ops.h:83, reference math gemm_i8.cpp:262-281):
+ * out[t,n] = fma((float)acc*wscale[n], ascale[t], bias ? bias[n] : 0) with
+ * acc the exact int32 dot of xq row t and Wq row n. xq [seq, i8_kpad(K)],
+ * Wq [N, i8_kpad(K)]. bias may be NULL. */
+VLA_API int32_t vla_dense_linear_i8_pre(float* out, const int8_t* xq, const float* ascale,
+                                        const int8_t* Wq, const float* wscale, const float* bias,
+                                        int32_t seq, int32_t N, int32_t K);
+
+/* dense_linear_i8 (quant_ops.h:69, gemm_i8.cpp:246-256): quantize x then the
+ * above. The host form allocates its own staging; the _dev form takes the
+ * caller-owned scratch the reference takes (xq [seq, ldq], ascale [seq]). */
+VLA_API int32_t vla_dense_linear_i8(float* out, const float* x, const int8_t* Wq,
+                                    const float* wscale, const float* bias,
+                                    int32_t seq, int32_t N, int32_t K);
+
+/* Device form of dense_linear_i8_pre with the fused epilogue options the
+ * reference graphs apply right after an int8 forward: act (vla_act, e.g.
+ * Linear::forward_gelu, src/nn/linear.cpp:159-168) and accumulate != 0 for
+ * out += result (Linear::forward_add, linear.cpp:174-185). ldx/ldw are the
+ * int8 row strides (>= i8_kpad(K)), ldo the fp32 output row stride (>= N). */
+VLA_API int32_t vla_dense_linear_i8_pre_dev(float* out, int32_t ldo, const int8_t* xq,
+                                            int32_t ldx, const float* ascale, const int8_t* Wq,
+                                            int32_t ldw, const float* wscale, const float* bias,
+                                            int32_t seq, int32_t N, int32_t K, int32_t act,
+                                            int32_t accumulate, void* stream);
+
+/* Exact int32 accumulators acc[t*N+n] (the value gemm_i8.cpp:270-277 forms
+ * before its epilogue), for bit-exact parity checks. */
+VLA_API int32_t vla_gemm_i8_i32(int32_t* acc, const int8_t* xq, const int8_t* Wq,
+                                int32_t seq, int32_t N, int32_t K);
+VLA_API int32_t vla_gemm_i8_i32_dev(int32_t* acc, const int8_t* xq, int32_t ldx,
+                                    const int8_t* Wq, int32_t ldw, int32_t seq, int32_t N,
+                                    int32_t K, void* stream);
+
+/* ------------------------------------ device-resident int8 linear (nn) -- */
+/* Replaces nn::Linear's int8 state (src/nn/linear.h:40-48,85-99): the weights
+ * are uploaded and quantized once, then live in HBM as int8 rows + per-channel
+ * scales + bias. NULL on failure (vla_last_error()); like Linear::init_int8
+ * (linear.cpp:66-68) it refuses K > INT_MAX/(255*127). */
+typedef struct vla_linear_i8 vla_linear_i8;
+/* From fp32 weights W [N,K] (host): quantized on the device with the
+ * pack_weights_i8 formula. bias [N] or NULL. */
+VLA_API vla_linear_i8* vla_linear_i8_create(const float* W, const float* bias,
+                                            int32_t N, int32_t K);
+/* From already-quantized weights (host): Wq [N,K] int8 row-major, wscale [N]. */
+VLA_API vla_linear_i8* vla_linear_i8_create_q(const int8_t* Wq, const float* wscale,
+                                              const float* bias, int32_t N, int32_t K);
+VLA_API void vla_linear_i8_free(vla_linear_i8* lin);
+/* Device pointers of the resident weights (row stride = vla_linear_i8_ldw). */
+VLA_API const int8_t* vla_linear_i8_weights(const vla_linear_i8* lin);
+VLA_API const float* vla_linear_i8_wscale(const vla_linear_i8* lin);
+VLA_API int32_t vla_linear_i8_ldw(const vla_linear_i8* lin);
+/* Linear::forward (linear.cpp:121-133): out [seq,N] = x [seq,K] W^T + bias on
+ * the device, quantizing x into the caller's scratch (xq [seq, ldw] int8,
+ * ascale [seq]). act / accumulate as in vla_dense_linear_i8_pre_dev. */
+VLA_API int32_t vla_linear_i8_forward_dev(const vla_linear_i8* lin, float* out, const float* x,
+                                          int32_t seq, int8_t* xq_scratch, float* ascale_scratch,
+                                          int32_t act, int32_t accumulate, void* stream);
+/* Linear::forward_quantized (linear.cpp:170-172): activations already
+ * quantized (xq [seq, ldx]). */
+VLA_API int32_t vla_linear_i8_forward_quantized_dev(const vla_linear_i8* lin, float* out,
+                                                    const int8_t* xq, int32_t ldx,
+                                                    const float* ascale, int32_t seq, int32_t act,
+                                                    int32_t accumulate, void* stream);
+
+/* ---------------------------------------------------- lm_ops.h (fp32) ---- */
+
+/* gqa_attention_masked (src/ops/lm_ops.h:33-35; semantics of the scalar
+ * reference src/hal/scalar/attn.cpp:22-87 and the AVX2 engine
+ * src/hal/avx2/attn.cpp:266-447): out = softmax(Q K^T * scale + mask) V per
+ * head, kv head = h / (n_q / n_kv); a key with mask == lowest() or score -inf
+ * has weight 0; a row with every key blocked is the uniform mean of V.
+ * mask [seq_q, seq_k] additive, NULL = dense (gqa_attention_dense,
+ * lm_ops.h:43, common/attn.cpp:23-28). head_dim <= 256, head_dim % 4 == 0. */
+VLA_API int32_t vla_gqa_attention_masked(float* out, const float* Q, const float* K,
+                                         const float* V, int32_t seq_q, int32_t seq_k,
+                                         int32_t n_q, int32_t n_kv, int32_t head_dim,
+                                         float scale, const float* mask);
+VLA_API int32_t vla_gqa_attention_dense(float* out, const float* Q, const float* K,
+                                        const float* V, int32_t seq_q, int32_t seq_k,
+                                        int32_t n_q, int32_t n_kv, int32_t head_dim, float scale);
+/* Device form with explicit row strides (floats between consecutive tokens;
+ * 0 = n_heads*head_dim, the lm_ops.h layout) and a mask descriptor whose
+ * pointers are device pointers. */
+VLA_API int32_t vla_attention_dev(float* out, int32_t ldo, const float* Q, int32_t ldq,
+                                  const float* K, int32_t ldk, const float* V, int32_t ldv,
+                                  int32_t seq_q, int32_t seq_k, int32_t n_q, int32_t n_kv,
+                                  int32_t head_dim, float scale, const vla_mask* mask,
+                                  void* stream);
+/* Host form of the same, mask pointers on the host (for parity tests). */
+VLA_API int32_t vla_attention(float* out, const float* Q, const float* K, const float* V,
+                              int32_t seq_q, int32_t seq_k, int32_t n_q, int32_t n_kv,
+                              int32_t head_dim, float scale, const vla_mask* mask);
+
+/* layernorm (lm_ops.h:61, src/hal/common/norms.cpp:69-97): per row, mean and
+ * variance accumulated in double, out = (float)(x-mean)*inv*w + b; b may be
+ * NULL; out may alias x. */
+VLA_API int32_t vla_layernorm(float* out, const float* x, const float* w, const float* b,
+                              int32_t seq, int32_t hidden, float eps);
+VLA_API int32_t vla_layernorm_dev(float* out, const float* x, const float* w, const float* b,
+                                  int32_t seq, int32_t hidden, float eps, void* stream);
+/* rmsnorm (lm_ops.h:21, norms.cpp:19-35): sum of squares in double. */
+VLA_API int32_t vla_rmsnorm(float* out, const float* x, const float* w, int32_t seq,
+                            int32_t hidden, float eps);
+VLA_API int32_t vla_rmsnorm_dev(float* out, const float* x, const float* w, int32_t seq,
+                                int32_t hidden, float eps, void* stream);
+/* rope_neox (lm_ops.h:26, norms.cpp:37-67), in place on x [seq, n_heads, head_dim]
+ * with row stride ld (0 = n_heads*head_dim). */
+VLA_API int32_t vla_rope_neox(float* x, const int32_t* pos, int32_t seq, int32_t n_heads,
+                              int32_t head_dim, float base);
+VLA_API int32_t vla_rope_neox_dev(float* x, int32_t ld, const int32_t* pos, int32_t seq,
+                                  int32_t n_heads, int32_t head_dim, float base, void* stream);
+
+/* Elementwise ops (lm_ops.h:55-73, src/hal/common/eltwise.cpp), in place
+ * except silu_gate (out may alias g or u). */
+VLA_API int32_t vla_gelu_tanh(float* x, int32_t n);
+VLA_API int32_t vla_gelu_erf(float* x, int32_t n);
+VLA_API int32_t vla_relu(float* x, int32_t n);
+VLA_API int32_t vla_silu_gate(float* out, const float* g, const float* u, int32_t n);
+VLA_API int32_t vla_gelu_tanh_dev(float* x, int64_t n, void* stream);
+VLA_API int32_t vla_gelu_erf_dev(float* x, int64_t n, void* stream);
+VLA_API int32_t vla_relu_dev(float* x, int64_t n, void* stream);
+VLA_API int32_t vla_silu_gate_dev(float* out, const float* g, const float* u, int64_t n,
+                                  void* stream);
+/* out[i] = a[i] + b[i] (residual adds and positional embeddings of the
+ * reference graphs, e.g. act_transformer.cpp:227-281). */
+VLA_API int32_t vla_add_dev(float* out, const float* a, const float* b, int64_t n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* VLA_SIMD_HIP_H */

@@ -1,0 +1,326 @@
+"""ctypes bindings of the CPU checker. TEST INFRASTRUCTURE ONLY.
+
+Imported only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+leg. Two libraries, both built by oracle/Makefile:
+
+  liboracle.so          this repo's C restatement (oracle.c)
+  _ref/libvla_ref.so    the real reference kernels + ref_shim.cpp (built in the
+                        container that holds the reference sources; the .so
+                        travels with the tree)
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import c_float, c_int, c_size_t, c_uint64, c_void_p
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_PATH = os.path.join(HERE, "liboracle.so")
+REF_PATH = os.path.join(HERE, "_ref", "libvla_ref.so")
+
+_orc = None
+_ref = None
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(c_void_p)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def kpad(K: int) -> int:
+    return (K + 3) & ~3
+
+
+def oracle():
+    global _orc
+    if _orc is None:
+        if not os.path.exists(ORACLE_PATH):
+            raise RuntimeError(f"{ORACLE_PATH} missing: run make -C oracle")
+        L = ctypes.CDLL(ORACLE_PATH)
+        P, i, f = c_void_p, c_int, c_float
+        L.orc_i8_kpad.argtypes, L.orc_i8_kpad.restype = [i], i
+        L.orc_frand_fill.argtypes = [ctypes.POINTER(c_uint64), P, c_size_t, f, f]
+        L.orc_quantize_act_i8.argtypes = [P, P, P, i, i, i]
+        L.orc_quantize_weights_i8.argtypes = [P, P, P, i, i, i]
+        L.orc_gemm_i8_acc.argtypes = [P, P, i, P, i, i, i, i]
+        L.orc_dense_linear_i8_pre.argtypes = [P, P, i, P, P, i, P, P, i, i, i]
+        L.orc_apply_act.argtypes = [P, c_size_t, i]
+        L.orc_gqa_attention_masked.argtypes = [P, P, P, P, i, i, i, i, i, f, P]
+        L.orc_layernorm.argtypes = [P, P, P, P, i, i, f]
+        L.orc_rmsnorm.argtypes = [P, P, P, i, i, f]
+        L.orc_rope_neox.argtypes = [P, P, i, i, i, f]
+        L.orc_gelu_tanh.argtypes = [P, c_size_t]
+        L.orc_gelu_erf.argtypes = [P, c_size_t]
+        L.orc_silu_gate.argtypes = [P, P, P, c_size_t]
+        L.orc_relu.argtypes = [P, c_size_t]
+        _orc = L
+    return _orc
+
+
+def ref_available() -> bool:
+    return os.path.exists(REF_PATH)
+
+
+def ref():
+    global _ref
+    if _ref is None:
+        if not ref_available():
+            raise RuntimeError(f"{REF_PATH} missing: run make -C oracle ref (needs the reference sources)")
+        L = ctypes.CDLL(REF_PATH)
+        P, i, f = c_void_p, c_int, c_float
+        L.ref_int8_available.restype = i
+        L.ref_backend_name.restype = ctypes.c_char_p
+        L.ref_omp_max_threads.restype = i
+        L.ref_i8_kpad.argtypes, L.ref_i8_kpad.restype = [i], i
+        L.ref_packed_i8_words.argtypes, L.ref_packed_i8_words.restype = [i, i], c_size_t
+        L.ref_pack_weights_i8.argtypes = [P, P, P, i, i]
+        L.ref_panels_from_rows.argtypes = [P, i, i, i, P]
+        L.ref_rows_from_panels.argtypes = [P, i, i, P, i]
+        L.ref_quantize_act_i8.argtypes = [P, P, P, i, i]
+        L.ref_dense_linear_i8.argtypes = [P, P, P, P, P, i, i, i, P, P]
+        L.ref_dense_linear_i8_pre.argtypes = [P, P, P, P, P, P, i, i, i]
+        L.ref_dense_linear_i8_ref.argtypes = [P, P, P, P, P, P, i, i, i]
+        L.ref_gqa_attention_masked.argtypes = [P, P, P, P, i, i, i, i, i, f, P]
+        L.ref_gqa_attention_dense.argtypes = [P, P, P, P, i, i, i, i, i, f]
+        L.ref_layernorm.argtypes = [P, P, P, P, i, i, f]
+        L.ref_rmsnorm.argtypes = [P, P, P, i, i, f]
+        L.ref_rope_neox.argtypes = [P, P, i, i, i, f]
+        L.ref_gelu_tanh.argtypes = [P, i]
+        L.ref_gelu_erf.argtypes = [P, i]
+        L.ref_silu_gate.argtypes = [P, P, P, i]
+        L.ref_relu.argtypes = [P, i]
+        _ref = L
+    return _ref
+
+
+# ------------------------------------------------------------------ frand --
+
+class Frand:
+    """tests/test_ops.cpp:31-40 xorshift64 stream (state 0x243F6A8885A308D3)."""
+
+    def __init__(self, state: int = 0x243F6A8885A308D3):
+        self.state = c_uint64(state)
+
+    def rv(self, n: int, lo: float = -1.0, hi: float = 1.0) -> np.ndarray:
+        v = np.empty(n, np.float32)
+        oracle().orc_frand_fill(ctypes.byref(self.state), _p(v), n, lo, hi)
+        return v
+
+
+# ------------------------------------------------------------ oracle ops --
+
+def quantize_act_i8(x, ldq=None):
+    x = _f32(x)
+    seq, K = x.shape
+    ldq = ldq or kpad(K)
+    xq = np.empty((seq, ldq), np.int8)
+    s = np.empty(seq, np.float32)
+    oracle().orc_quantize_act_i8(_p(x), _p(xq), _p(s), seq, K, ldq)
+    return xq, s
+
+
+def quantize_weights_i8(W, ldq=None):
+    W = _f32(W)
+    N, K = W.shape
+    ldq = ldq or kpad(K)
+    Wq = np.empty((N, ldq), np.int8)
+    s = np.empty(N, np.float32)
+    oracle().orc_quantize_weights_i8(_p(W), _p(Wq), _p(s), N, K, ldq)
+    return Wq, s
+
+
+def gemm_i8_acc(xq, Wq, K):
+    xq = np.ascontiguousarray(xq, np.int8)
+    Wq = np.ascontiguousarray(Wq, np.int8)
+    seq, N = xq.shape[0], Wq.shape[0]
+    acc = np.empty((seq, N), np.int32)
+    oracle().orc_gemm_i8_acc(_p(acc), _p(xq), xq.shape[1], _p(Wq), Wq.shape[1], seq, N, K)
+    return acc
+
+
+def dense_linear_i8_pre(xq, ascale, Wq, wscale, bias, K):
+    xq = np.ascontiguousarray(xq, np.int8)
+    Wq = np.ascontiguousarray(Wq, np.int8)
+    seq, N = xq.shape[0], Wq.shape[0]
+    out = np.empty((seq, N), np.float32)
+    b = None if bias is None else _f32(bias)
+    oracle().orc_dense_linear_i8_pre(_p(out), _p(xq), xq.shape[1], _p(_f32(ascale)), _p(Wq),
+                                     Wq.shape[1], _p(_f32(wscale)), _p(b), seq, N, K)
+    return out
+
+
+def apply_act(x, act: int):
+    x = _f32(x).copy()
+    oracle().orc_apply_act(_p(x), x.size, act)
+    return x
+
+
+def attention(Q, K, V, seq_q, seq_k, n_q, n_kv, head_dim, scale, mask=None):
+    out = np.empty((seq_q, n_q * head_dim), np.float32)
+    m = None if mask is None else _f32(mask)
+    oracle().orc_gqa_attention_masked(_p(out), _p(_f32(Q)), _p(_f32(K)), _p(_f32(V)), seq_q, seq_k,
+                                      n_q, n_kv, head_dim, scale, _p(m))
+    return out
+
+
+def layernorm(x, w, b, eps):
+    x = _f32(x)
+    out = np.empty_like(x)
+    oracle().orc_layernorm(_p(out), _p(x), _p(_f32(w)), _p(None if b is None else _f32(b)),
+                           x.shape[0], x.shape[1], eps)
+    return out
+
+
+def rmsnorm(x, w, eps):
+    x = _f32(x)
+    out = np.empty_like(x)
+    oracle().orc_rmsnorm(_p(out), _p(x), _p(_f32(w)), x.shape[0], x.shape[1], eps)
+    return out
+
+
+def rope_neox(x, pos, n_heads, head_dim, base):
+    x = _f32(x).copy()
+    p = np.ascontiguousarray(pos, np.int32)
+    oracle().orc_rope_neox(_p(x), _p(p), len(p), n_heads, head_dim, base)
+    return x
+
+
+def gelu_tanh(x):
+    x = _f32(x).copy()
+    oracle().orc_gelu_tanh(_p(x), x.size)
+    return x
+
+
+def gelu_erf(x):
+    x = _f32(x).copy()
+    oracle().orc_gelu_erf(_p(x), x.size)
+    return x
+
+
+def relu(x):
+    x = _f32(x).copy()
+    oracle().orc_relu(_p(x), x.size)
+    return x
+
+
+def silu_gate(g, u):
+    g, u = _f32(g), _f32(u)
+    out = np.empty_like(g)
+    oracle().orc_silu_gate(_p(out), _p(g), _p(u), g.size)
+    return out
+
+
+# ------------------------------------------------------ reference (real) --
+
+def ref_pack_weights(W):
+    """The reference packer: returns (row-major Wq [N, Kp], wscale, panel blob)."""
+    W = _f32(W)
+    N, K = W.shape
+    L = ref()
+    words = L.ref_packed_i8_words(N, K)
+    blob = np.zeros(words * 4, np.int8)
+    ws = np.empty(N, np.float32)
+    L.ref_pack_weights_i8(_p(W), _p(blob), _p(ws), N, K)
+    rows = np.empty((N, kpad(K)), np.int8)
+    L.ref_rows_from_panels(_p(blob), N, K, _p(rows), kpad(K))
+    return rows, ws, blob
+
+
+def ref_panels(Wrows, K):
+    """Row-major int8 [N, >=K] -> the reference's panel blob (+ row sums)."""
+    Wrows = np.ascontiguousarray(Wrows, np.int8)
+    N = Wrows.shape[0]
+    L = ref()
+    blob = np.zeros(L.ref_packed_i8_words(N, K) * 4, np.int8)
+    L.ref_panels_from_rows(_p(Wrows), Wrows.shape[1], N, K, _p(blob))
+    return blob
+
+
+def ref_quantize_act_i8(x):
+    x = _f32(x)
+    seq, K = x.shape
+    xq = np.empty((seq, kpad(K)), np.int8)
+    s = np.empty(seq, np.float32)
+    ref().ref_quantize_act_i8(_p(x), _p(xq), _p(s), seq, K)
+    return xq, s
+
+
+def ref_dense_linear_i8_ref(xq, ascale, blob, wscale, bias, N, K):
+    seq = xq.shape[0]
+    out = np.empty((seq, N), np.float32)
+    ref().ref_dense_linear_i8_ref(_p(out), _p(np.ascontiguousarray(xq, np.int8)), _p(_f32(ascale)),
+                                  _p(blob), _p(_f32(wscale)), _p(None if bias is None else _f32(bias)),
+                                  seq, N, K)
+    return out
+
+
+def ref_dense_linear_i8_pre(xq, ascale, blob, wscale, bias, N, K):
+    seq = xq.shape[0]
+    out = np.empty((seq, N), np.float32)
+    ref().ref_dense_linear_i8_pre(_p(out), _p(np.ascontiguousarray(xq, np.int8)), _p(_f32(ascale)),
+                                  _p(blob), _p(_f32(wscale)), _p(None if bias is None else _f32(bias)),
+                                  seq, N, K)
+    return out
+
+
+def ref_dense_linear_i8(x, blob, wscale, bias, N, K, xq_scratch=None, as_scratch=None):
+    x = _f32(x)
+    seq = x.shape[0]
+    out = np.empty((seq, N), np.float32)
+    xq = xq_scratch if xq_scratch is not None else np.empty((seq, kpad(K)), np.int8)
+    s = as_scratch if as_scratch is not None else np.empty(seq, np.float32)
+    ref().ref_dense_linear_i8(_p(out), _p(x), _p(blob), _p(_f32(wscale)),
+                              _p(None if bias is None else _f32(bias)), seq, N, K, _p(xq), _p(s))
+    return out
+
+
+def ref_attention(Q, K, V, seq_q, seq_k, n_q, n_kv, head_dim, scale, mask=None):
+    out = np.empty((seq_q, n_q * head_dim), np.float32)
+    if mask is None:
+        ref().ref_gqa_attention_dense(_p(out), _p(_f32(Q)), _p(_f32(K)), _p(_f32(V)), seq_q, seq_k,
+                                      n_q, n_kv, head_dim, scale)
+    else:
+        ref().ref_gqa_attention_masked(_p(out), _p(_f32(Q)), _p(_f32(K)), _p(_f32(V)), seq_q, seq_k,
+                                       n_q, n_kv, head_dim, scale, _p(_f32(mask)))
+    return out
+
+
+def ref_layernorm(x, w, b, eps):
+    x = _f32(x)
+    out = np.empty_like(x)
+    ref().ref_layernorm(_p(out), _p(x), _p(_f32(w)), _p(None if b is None else _f32(b)), x.shape[0],
+                        x.shape[1], eps)
+    return out
+
+
+def ref_rmsnorm(x, w, eps):
+    x = _f32(x)
+    out = np.empty_like(x)
+    ref().ref_rmsnorm(_p(out), _p(x), _p(_f32(w)), x.shape[0], x.shape[1], eps)
+    return out
+
+
+def ref_rope_neox(x, pos, n_heads, head_dim, base):
+    x = _f32(x).copy()
+    p = np.ascontiguousarray(pos, np.int32)
+    ref().ref_rope_neox(_p(x), _p(p), len(p), n_heads, head_dim, base)
+    return x
+
+
+def ref_eltwise(name, x):
+    x = _f32(x).copy()
+    getattr(ref(), name)(_p(x), x.size)
+    return x
+
+
+def ref_silu_gate(g, u):
+    g, u = _f32(g), _f32(u)
+    out = np.empty_like(g)
+    ref().ref_silu_gate(_p(out), _p(g), _p(u), g.size)
+    return out

@@ -1,0 +1,451 @@
+"""vla.simd_amd - MI355X (gfx950) backend of vla.simd's int8 linear + attention path.
+
+The product is the C-ABI shared library ``libvla_simd_hip.so`` built from
+``csrc/`` (declared in ``include/vla_simd_hip.h``). This module is its Python
+face: a ctypes loader plus numpy-level wrappers named after the reference op
+API (``tcpu::quantize_act_i8``, ``tcpu::dense_linear_i8``, ... in
+src/ops/quant_ops.h and src/ops/lm_ops.h of the reference), the way the
+reference's own Python layer drives its libraries through ctypes
+(vla_simd/policy_server.py:203-273).
+
+There is no CPU fallback: if the library is missing, or no gfx950 device is
+present, the calls raise.
+
+Load it by path (the directory name is not an importable identifier)::
+
+    import importlib.util, sys
+    spec = importlib.util.spec_from_file_location(
+        "vla_simd_amd", "<repo>/vla.simd_amd/__init__.py",
+        submodule_search_locations=["<repo>/vla.simd_amd"])
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_char_p, c_float, c_int32, c_int64, c_size_t, c_uint8, c_void_p
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libvla_simd_hip.so")
+
+VLA_OK, VLA_ERR_ARG, VLA_ERR_SHAPE, VLA_ERR_EXCEPTION = 0, -1, -2, -3
+ACT = {"none": 0, "relu": 1, "gelu_tanh": 2, "gelu_erf": 3}
+MASK_NONE, MASK_DENSE, MASK_CAUSAL, MASK_GROUPS = 0, 1, 2, 3
+
+# Every symbol include/vla_simd_hip.h declares, in declaration order.
+EXPORTS = (
+    "vla_abi_version", "vla_backend_name", "vla_int8_available", "vla_last_error",
+    "vla_hip_malloc", "vla_hip_free", "vla_hip_memcpy_h2d", "vla_hip_memcpy_d2h",
+    "vla_hip_memset", "vla_hip_synchronize", "vla_hip_device_name",
+    "vla_i8_kpad", "vla_quantize_act_i8", "vla_quantize_act_i8_dev", "vla_pack_weights_i8",
+    "vla_dense_linear_i8_pre", "vla_dense_linear_i8", "vla_dense_linear_i8_pre_dev",
+    "vla_gemm_i8_i32", "vla_gemm_i8_i32_dev",
+    "vla_linear_i8_create", "vla_linear_i8_create_q", "vla_linear_i8_free",
+    "vla_linear_i8_weights", "vla_linear_i8_wscale", "vla_linear_i8_ldw",
+    "vla_linear_i8_forward_dev", "vla_linear_i8_forward_quantized_dev",
+    "vla_gqa_attention_masked", "vla_gqa_attention_dense", "vla_attention_dev", "vla_attention",
+    "vla_layernorm", "vla_layernorm_dev", "vla_rmsnorm", "vla_rmsnorm_dev",
+    "vla_rope_neox", "vla_rope_neox_dev",
+    "vla_gelu_tanh", "vla_gelu_erf", "vla_relu", "vla_silu_gate",
+    "vla_gelu_tanh_dev", "vla_gelu_erf_dev", "vla_relu_dev", "vla_silu_gate_dev", "vla_add_dev",
+)
+
+
+class VlaError(RuntimeError):
+    """A libvla_simd_hip call returned a status other than VLA_OK."""
+
+    def __init__(self, fn: str, status: int, msg: str):
+        super().__init__(f"{fn} -> {status}: {msg}")
+        self.status = status
+
+
+class VlaMask(ctypes.Structure):
+    """vla_mask (include/vla_simd_hip.h)."""
+
+    _fields_ = [
+        ("kind", c_int32),
+        ("dense", c_void_p),
+        ("causal_offset", c_int32),
+        ("n_groups", c_int32),
+        ("q_group", c_void_p),
+        ("k_group", c_void_p),
+        ("allow", c_void_p),
+    ]
+
+
+_lib = None
+
+
+def _declare(L):
+    P = c_void_p
+    i32, f32, i64 = c_int32, c_float, c_int64
+    sig = {
+        "vla_abi_version": (i32, []),
+        "vla_backend_name": (c_char_p, []),
+        "vla_int8_available": (i32, []),
+        "vla_last_error": (c_char_p, []),
+        "vla_hip_malloc": (i32, [POINTER(c_void_p), c_size_t]),
+        "vla_hip_free": (i32, [P]),
+        "vla_hip_memcpy_h2d": (i32, [P, P, c_size_t]),
+        "vla_hip_memcpy_d2h": (i32, [P, P, c_size_t]),
+        "vla_hip_memset": (i32, [P, i32, c_size_t]),
+        "vla_hip_synchronize": (i32, []),
+        "vla_hip_device_name": (i32, [c_char_p, i32]),
+        "vla_i8_kpad": (i32, [i32]),
+        "vla_quantize_act_i8": (i32, [P, P, P, i32, i32]),
+        "vla_quantize_act_i8_dev": (i32, [P, P, i32, P, i32, i32, P]),
+        "vla_pack_weights_i8": (i32, [P, P, P, i32, i32]),
+        "vla_dense_linear_i8_pre": (i32, [P, P, P, P, P, P, i32, i32, i32]),
+        "vla_dense_linear_i8": (i32, [P, P, P, P, P, i32, i32, i32]),
+        "vla_dense_linear_i8_pre_dev": (i32, [P, i32, P, i32, P, P, i32, P, P, i32, i32, i32, i32, i32, P]),
+        "vla_gemm_i8_i32": (i32, [P, P, P, i32, i32, i32]),
+        "vla_gemm_i8_i32_dev": (i32, [P, P, i32, P, i32, i32, i32, i32, P]),
+        "vla_linear_i8_create": (P, [P, P, i32, i32]),
+        "vla_linear_i8_create_q": (P, [P, P, P, i32, i32]),
+        "vla_linear_i8_free": (None, [P]),
+        "vla_linear_i8_weights": (P, [P]),
+        "vla_linear_i8_wscale": (P, [P]),
+        "vla_linear_i8_ldw": (i32, [P]),
+        "vla_linear_i8_forward_dev": (i32, [P, P, P, i32, P, P, i32, i32, P]),
+        "vla_linear_i8_forward_quantized_dev": (i32, [P, P, P, i32, P, i32, i32, i32, P]),
+        "vla_gqa_attention_masked": (i32, [P, P, P, P, i32, i32, i32, i32, i32, f32, P]),
+        "vla_gqa_attention_dense": (i32, [P, P, P, P, i32, i32, i32, i32, i32, f32]),
+        "vla_attention_dev": (i32, [P, i32, P, i32, P, i32, P, i32, i32, i32, i32, i32, i32, f32,
+                                    POINTER(VlaMask), P]),
+        "vla_attention": (i32, [P, P, P, P, i32, i32, i32, i32, i32, f32, POINTER(VlaMask)]),
+        "vla_layernorm": (i32, [P, P, P, P, i32, i32, f32]),
+        "vla_layernorm_dev": (i32, [P, P, P, P, i32, i32, f32, P]),
+        "vla_rmsnorm": (i32, [P, P, P, i32, i32, f32]),
+        "vla_rmsnorm_dev": (i32, [P, P, P, i32, i32, f32, P]),
+        "vla_rope_neox": (i32, [P, P, i32, i32, i32, f32]),
+        "vla_rope_neox_dev": (i32, [P, i32, P, i32, i32, i32, f32, P]),
+        "vla_gelu_tanh": (i32, [P, i32]),
+        "vla_gelu_erf": (i32, [P, i32]),
+        "vla_relu": (i32, [P, i32]),
+        "vla_silu_gate": (i32, [P, P, P, i32]),
+        "vla_gelu_tanh_dev": (i32, [P, i64, P]),
+        "vla_gelu_erf_dev": (i32, [P, i64, P]),
+        "vla_relu_dev": (i32, [P, i64, P]),
+        "vla_silu_gate_dev": (i32, [P, P, P, i64, P]),
+        "vla_add_dev": (i32, [P, P, P, i64, P]),
+    }
+    for name, (res, args) in sig.items():
+        f = getattr(L, name)
+        f.restype = res
+        f.argtypes = args
+
+
+def lib(path: str | None = None):
+    """Load libvla_simd_hip.so (once). Raises if it is not built."""
+    global _lib
+    if _lib is None:
+        p = path or os.environ.get("VLA_SIMD_HIP_LIB", LIB_PATH)
+        if not os.path.exists(p):
+            raise RuntimeError(f"{p} is not built: run __graft_entry__.build() (make -C vla.simd_amd/csrc)")
+        L = ctypes.CDLL(p)
+        _declare(L)
+        _lib = L
+    return _lib
+
+
+def check(fn: str, status: int) -> None:
+    if status != VLA_OK:
+        raise VlaError(fn, status, (lib().vla_last_error() or b"").decode(errors="replace"))
+
+
+def _call(name: str, *args) -> int:
+    st = getattr(lib(), name)(*args)
+    check(name, st)
+    return st
+
+
+def _ptr(a):
+    if a is None:
+        return None
+    return a.ctypes.data_as(c_void_p)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _i8(a):
+    return np.ascontiguousarray(a, dtype=np.int8)
+
+
+# ------------------------------------------------------------- handshake --
+
+def abi_version() -> int:
+    return lib().vla_abi_version()
+
+
+def backend_name() -> str:
+    return lib().vla_backend_name().decode()
+
+
+def int8_available() -> bool:
+    return bool(lib().vla_int8_available())
+
+
+def device_name() -> str:
+    buf = ctypes.create_string_buffer(256)
+    _call("vla_hip_device_name", buf, 256)
+    return buf.value.decode()
+
+
+def i8_kpad(K: int) -> int:
+    return (K + 3) & ~3
+
+
+# ------------------------------------------------- host-pointer op forms --
+
+def quantize_act_i8(x):
+    """tcpu::quantize_act_i8: x [seq, K] -> (xq [seq, i8_kpad(K)] int8, ascale [seq])."""
+    x = _f32(x)
+    seq, K = x.shape
+    xq = np.empty((seq, i8_kpad(K)), np.int8)
+    s = np.empty(seq, np.float32)
+    _call("vla_quantize_act_i8", _ptr(x), _ptr(xq), _ptr(s), seq, K)
+    return xq, s
+
+
+def pack_weights_i8(W):
+    """tcpu::pack_weights_i8 formula, device row layout: W [N,K] -> (Wq [N, Kp], wscale [N])."""
+    W = _f32(W)
+    N, K = W.shape
+    Wq = np.empty((N, i8_kpad(K)), np.int8)
+    s = np.empty(N, np.float32)
+    _call("vla_pack_weights_i8", _ptr(W), _ptr(Wq), _ptr(s), N, K)
+    return Wq, s
+
+
+def _pad_rows(a, Kp):
+    a = _i8(a)
+    if a.shape[1] == Kp:
+        return a
+    out = np.zeros((a.shape[0], Kp), np.int8)
+    out[:, : a.shape[1]] = a
+    return out
+
+
+def dense_linear_i8_pre(xq, ascale, Wq, wscale, bias, K):
+    """tcpu::dense_linear_i8_pre with row-major Wq [N, K or Kp]."""
+    Kp = i8_kpad(K)
+    xq, Wq = _pad_rows(xq, Kp), _pad_rows(Wq, Kp)
+    seq, N = xq.shape[0], Wq.shape[0]
+    ascale, wscale = _f32(ascale), _f32(wscale)
+    b = None if bias is None else _f32(bias)
+    out = np.empty((seq, N), np.float32)
+    _call("vla_dense_linear_i8_pre", _ptr(out), _ptr(xq), _ptr(ascale), _ptr(Wq), _ptr(wscale),
+          _ptr(b), seq, N, K)
+    return out
+
+
+def dense_linear_i8(x, Wq, wscale, bias):
+    """tcpu::dense_linear_i8: quantize x per row, then the int8 GEMM."""
+    x = _f32(x)
+    seq, K = x.shape
+    Wq = _pad_rows(Wq, i8_kpad(K))
+    N = Wq.shape[0]
+    wscale = _f32(wscale)
+    b = None if bias is None else _f32(bias)
+    out = np.empty((seq, N), np.float32)
+    _call("vla_dense_linear_i8", _ptr(out), _ptr(x), _ptr(Wq), _ptr(wscale), _ptr(b), seq, N, K)
+    return out
+
+
+def gemm_i8_i32(xq, Wq, K):
+    """Exact int32 accumulators [seq, N]."""
+    Kp = i8_kpad(K)
+    xq, Wq = _pad_rows(xq, Kp), _pad_rows(Wq, Kp)
+    seq, N = xq.shape[0], Wq.shape[0]
+    acc = np.empty((seq, N), np.int32)
+    _call("vla_gemm_i8_i32", _ptr(acc), _ptr(xq), _ptr(Wq), seq, N, K)
+    return acc
+
+
+def _mask_struct(kind=MASK_NONE, dense=None, causal_offset=0, q_group=None, k_group=None, allow=None):
+    keep = []
+    m = VlaMask()
+    m.kind = kind
+    if dense is not None:
+        d = _f32(dense)
+        keep.append(d)
+        m.dense = d.ctypes.data
+    m.causal_offset = causal_offset
+    if kind == MASK_GROUPS:
+        qg = np.ascontiguousarray(q_group, np.uint8)
+        kg = np.ascontiguousarray(k_group, np.uint8)
+        al = np.ascontiguousarray(allow, np.uint8)
+        keep += [qg, kg, al]
+        m.n_groups = int(round(np.sqrt(al.size)))
+        m.q_group, m.k_group, m.allow = qg.ctypes.data, kg.ctypes.data, al.ctypes.data
+    return m, keep
+
+
+def attention(Q, K, V, n_q, n_kv, head_dim, scale, kind=MASK_NONE, dense=None, causal_offset=0,
+              q_group=None, k_group=None, allow=None):
+    """Fused attention, host arrays. Q [seq_q, n_q*hd], K/V [seq_k, n_kv*hd]."""
+    Q, K, V = _f32(Q), _f32(K), _f32(V)
+    sq = Q.size // (n_q * head_dim)
+    sk = K.size // (n_kv * head_dim)
+    out = np.empty((sq, n_q * head_dim), np.float32)
+    m, keep = _mask_struct(kind, dense, causal_offset, q_group, k_group, allow)
+    _call("vla_attention", _ptr(out), _ptr(Q), _ptr(K), _ptr(V), sq, sk, n_q, n_kv, head_dim,
+          float(scale), ctypes.byref(m))
+    del keep
+    return out
+
+
+def gqa_attention_masked(Q, K, V, seq_q, seq_k, n_q, n_kv, head_dim, scale, mask):
+    """tcpu::gqa_attention_masked (mask [seq_q, seq_k] additive or None)."""
+    Q, K, V = _f32(Q), _f32(K), _f32(V)
+    out = np.empty((seq_q, n_q * head_dim), np.float32)
+    m = None if mask is None else _f32(mask)
+    _call("vla_gqa_attention_masked", _ptr(out), _ptr(Q), _ptr(K), _ptr(V), seq_q, seq_k, n_q,
+          n_kv, head_dim, float(scale), _ptr(m))
+    return out
+
+
+def gqa_attention_dense(Q, K, V, seq_q, seq_k, n_q, n_kv, head_dim, scale):
+    Q, K, V = _f32(Q), _f32(K), _f32(V)
+    out = np.empty((seq_q, n_q * head_dim), np.float32)
+    _call("vla_gqa_attention_dense", _ptr(out), _ptr(Q), _ptr(K), _ptr(V), seq_q, seq_k, n_q,
+          n_kv, head_dim, float(scale))
+    return out
+
+
+def layernorm(x, w, b, eps):
+    x = _f32(x).copy()
+    seq, H = x.shape
+    bb = None if b is None else _f32(b)
+    _call("vla_layernorm", _ptr(x), _ptr(x), _ptr(_f32(w)), _ptr(bb), seq, H, float(eps))
+    return x
+
+
+def rmsnorm(x, w, eps):
+    x = _f32(x).copy()
+    seq, H = x.shape
+    _call("vla_rmsnorm", _ptr(x), _ptr(x), _ptr(_f32(w)), seq, H, float(eps))
+    return x
+
+
+def rope_neox(x, pos, n_heads, head_dim, base):
+    x = _f32(x).copy()
+    p = np.ascontiguousarray(pos, np.int32)
+    _call("vla_rope_neox", _ptr(x), _ptr(p), len(p), n_heads, head_dim, float(base))
+    return x
+
+
+def _eltwise(name, x):
+    x = _f32(x).copy()
+    _call(name, _ptr(x), x.size)
+    return x
+
+
+def gelu_tanh(x):
+    return _eltwise("vla_gelu_tanh", x)
+
+
+def gelu_erf(x):
+    return _eltwise("vla_gelu_erf", x)
+
+
+def relu(x):
+    return _eltwise("vla_relu", x)
+
+
+def silu_gate(g, u):
+    g, u = _f32(g), _f32(u)
+    out = np.empty_like(g)
+    _call("vla_silu_gate", _ptr(out), _ptr(g), _ptr(u), g.size)
+    return out
+
+
+# ------------------------------------------- device forms (torch tensors) --
+
+def _dp(t):
+    return None if t is None else c_void_p(t.data_ptr())
+
+
+def _stream(stream):
+    if stream is None:
+        import torch
+        return c_void_p(torch.cuda.current_stream().cuda_stream)
+    return c_void_p(stream)
+
+
+def quantize_act_i8_dev(x, xq, ascale, stream=None):
+    seq, K = x.shape
+    _call("vla_quantize_act_i8_dev", _dp(x), _dp(xq), xq.shape[1], _dp(ascale), seq, K,
+          _stream(stream))
+
+
+def dense_linear_i8_pre_dev(out, xq, ascale, Wq, wscale, bias, K, act=0, accumulate=0, stream=None):
+    seq, N = out.shape[0], Wq.shape[0]
+    _call("vla_dense_linear_i8_pre_dev", _dp(out), out.stride(0), _dp(xq), xq.stride(0),
+          _dp(ascale), _dp(Wq), Wq.stride(0), _dp(wscale), _dp(bias), seq, N, K, act, accumulate,
+          _stream(stream))
+
+
+def gemm_i8_i32_dev(acc, xq, Wq, K, stream=None):
+    seq, N = acc.shape
+    _call("vla_gemm_i8_i32_dev", _dp(acc), _dp(xq), xq.stride(0), _dp(Wq), Wq.stride(0), seq, N,
+          K, _stream(stream))
+
+
+def attention_dev(out, Q, K, V, n_q, n_kv, head_dim, scale, mask: VlaMask | None = None,
+                  stream=None):
+    _call("vla_attention_dev", _dp(out), out.stride(0), _dp(Q), Q.stride(0), _dp(K), K.stride(0),
+          _dp(V), V.stride(0), Q.shape[0], K.shape[0], n_q, n_kv, head_dim, float(scale),
+          None if mask is None else ctypes.byref(mask), _stream(stream))
+
+
+class LinearI8:
+    """Device-resident int8 linear (vla_linear_i8_*)."""
+
+    def __init__(self, handle, N, K):
+        self.h = c_void_p(handle)
+        self.N, self.K = N, K
+        self.ldw = lib().vla_linear_i8_ldw(self.h)
+
+    @classmethod
+    def from_f32(cls, W, bias=None):
+        W = _f32(W)
+        N, K = W.shape
+        b = None if bias is None else _f32(bias)
+        h = lib().vla_linear_i8_create(_ptr(W), _ptr(b), N, K)
+        if not h:
+            raise VlaError("vla_linear_i8_create", VLA_ERR_ARG, lib().vla_last_error().decode())
+        return cls(h, N, K)
+
+    @classmethod
+    def from_i8(cls, Wq, wscale, bias=None):
+        Wq = _i8(Wq)
+        N, K = Wq.shape
+        b = None if bias is None else _f32(bias)
+        h = lib().vla_linear_i8_create_q(_ptr(Wq), _ptr(_f32(wscale)), _ptr(b), N, K)
+        if not h:
+            raise VlaError("vla_linear_i8_create_q", VLA_ERR_ARG, lib().vla_last_error().decode())
+        return cls(h, N, K)
+
+    def forward_dev(self, out, x, xq_scratch, ascale_scratch, act=0, accumulate=0, stream=None):
+        _call("vla_linear_i8_forward_dev", self.h, _dp(out), _dp(x), x.shape[0], _dp(xq_scratch),
+              _dp(ascale_scratch), act, accumulate, _stream(stream))
+
+    def forward_quantized_dev(self, out, xq, ascale, act=0, accumulate=0, stream=None):
+        _call("vla_linear_i8_forward_quantized_dev", self.h, _dp(out), _dp(xq), xq.stride(0),
+              _dp(ascale), xq.shape[0], act, accumulate, _stream(stream))
+
+    def close(self):
+        if self.h:
+            lib().vla_linear_i8_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

@@ -1,0 +1,266 @@
+// attn.hip - fused masked GQA attention (QK^T -> online softmax -> PV) on gfx950.
+//
+// Semantics are the reference's gqa_attention_masked (src/ops/lm_ops.h:33;
+// scalar reference src/hal/scalar/attn.cpp:22-87, AVX2 engine
+// src/hal/avx2/attn.cpp:266-447):
+//   score = (q . k) * scale + mask;  a key whose mask entry is lowest() or whose
+//   score is -inf gets weight exactly 0;  out = sum_j softmax_j * v_j;  a row
+//   with every key blocked is the uniform mean of V over all seq_k keys
+//   (attn_uniform_row, avx2/attn.cpp:45-52).
+// fp32 throughout; results are tolerance-class against the reference (its exp
+// is a Cephes polynomial, its sums run in another order).
+//
+// One wave owns 16 queries of one head; a block of WAVES waves shares K/V
+// tiles of KT keys staged in LDS. Both products run on the fp32 matrix cores
+// (v_mfma_f32_16x16x4_f32, one float per lane per operand):
+//   S^T = K Q^T : A = K tile rows (keys), B = Q^T; lane l's result holds
+//                 S[q = l%16][key = 16*kt + 4*(l/16) + r], r = 0..3;
+//   O^T = V^T P^T: A = V^T, B = P^T. The B operand lane l must supply is
+//                 P[q = l%16][key = 16*kt + 4*(l/16) + r] - exactly the value
+//                 lane l already holds from S^T, so P never moves between lanes.
+// The head dimension is walked as d = g*(HDP/4) + s for lane group g = l/16,
+// so each lane's Q slice and each K row read are contiguous (ds_read_b128).
+// LDS rows are HDP+4 floats: the 16 rows of one read land on distinct banks,
+// and the four lane groups of a V read land 16 banks apart.
+// Scores and the running max stay in the natural domain (dot*scale + mask, as
+// the reference forms them); exp(x) is evaluated as v_exp_f32(x * log2 e).
+
+#include "common.h"
+
+#include <cfloat>
+
+namespace vla {
+namespace hip {
+namespace {
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.44269504088896340736f;
+
+__device__ __forceinline__ v4f mfma_f32(float a, float b, v4f c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+template <int HDP, int KT, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void attn_fwd(AttnArgs a) {
+    constexpr int SK = HDP + 4;
+    constexpr int NT = KT / 16;
+    constexpr int QS = HDP / 4;
+    constexpr int DT = HDP / 16;
+    constexpr int NTH = WAVES * 64;
+    __shared__ __attribute__((aligned(16))) float Ks[KT * SK];
+    __shared__ __attribute__((aligned(16))) float Vs[KT * SK];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, c = lane & 15;
+    const int h = blockIdx.y;
+    const int kvh = h / (a.n_q / a.n_kv);
+    const int HD = a.head_dim;
+    const int qb0 = blockIdx.x * 16 * WAVES;
+    const int qi = qb0 + wave * 16 + c;
+    const bool qok = qi < a.seq_q;
+
+    float qreg[QS];
+#pragma unroll
+    for (int s = 0; s < QS; s += 4) {
+        const int d = g * QS + s;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (qok && d < HD) v = *reinterpret_cast<const float4*>(a.Q + (size_t)qi * a.ldq + h * HD + d);
+        qreg[s] = v.x;
+        qreg[s + 1] = v.y;
+        qreg[s + 2] = v.z;
+        qreg[s + 3] = v.w;
+    }
+
+    const float scale = a.scale;
+    const int mk = a.mask_kind;
+    const int qg = (mk == 3 && qok) ? a.q_group[qi] : 0;
+
+    // keys past kv_end are blocked for every query of the block (causal bound)
+    int kv_end = a.seq_k;
+    if (mk == 2) {
+        const int qlast = (qb0 + 16 * WAVES < a.seq_q ? qb0 + 16 * WAVES : a.seq_q) - 1;
+        const int e = qlast + a.causal_offset + 1;
+        kv_end = e < 0 ? 0 : (e < kv_end ? e : kv_end);
+    }
+    const int nkt = (kv_end + KT - 1) / KT;
+
+    auto load_tile = [&](float* S, const float* G, int ld, int kv0) {
+        constexpr int F4 = HDP / 4;
+        for (int e = tid; e < KT * F4; e += NTH) {
+            const int kr = e / F4, d = (e % F4) * 4;
+            const int j = kv0 + kr;
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (j < a.seq_k && d < HD) v = *reinterpret_cast<const float4*>(G + (size_t)j * ld + kvh * HD + d);
+            *reinterpret_cast<float4*>(S + kr * SK + d) = v;
+        }
+    };
+
+    float m = -INFINITY, lsum = 0.0f;
+    v4f oacc[DT];
+#pragma unroll
+    for (int i = 0; i < DT; i++) oacc[i] = v4f{0.f, 0.f, 0.f, 0.f};
+
+    for (int t = 0; t < nkt; t++) {
+        const int kv0 = t * KT;
+        __syncthreads();
+        load_tile(Ks, a.K, a.ldk, kv0);
+        load_tile(Vs, a.V, a.ldv, kv0);
+        __syncthreads();
+
+        v4f sacc[NT];
+#pragma unroll
+        for (int kt = 0; kt < NT; kt++) {
+            sacc[kt] = v4f{0.f, 0.f, 0.f, 0.f};
+            const float* kr = Ks + (kt * 16 + c) * SK + g * QS;
+#pragma unroll
+            for (int s = 0; s < QS; s += 4) {
+                const float4 kv = *reinterpret_cast<const float4*>(kr + s);
+                sacc[kt] = mfma_f32(kv.x, qreg[s], sacc[kt]);
+                sacc[kt] = mfma_f32(kv.y, qreg[s + 1], sacc[kt]);
+                sacc[kt] = mfma_f32(kv.z, qreg[s + 2], sacc[kt]);
+                sacc[kt] = mfma_f32(kv.w, qreg[s + 3], sacc[kt]);
+            }
+        }
+
+        // scale, mask, tile max
+        float mt = -INFINITY;
+#pragma unroll
+        for (int kt = 0; kt < NT; kt++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int j = kv0 + kt * 16 + 4 * g + r;
+                float x = sacc[kt][r] * scale;
+                bool blocked = !qok || j >= kv_end;
+                if (!blocked) {
+                    if (mk == 1) {
+                        const float mv = a.mask[(size_t)qi * a.ldm + j];
+                        if (mv == -FLT_MAX) blocked = true;
+                        else x = x + mv;
+                    } else if (mk == 2) {
+                        blocked = j > qi + a.causal_offset;
+                    } else if (mk == 3) {
+                        blocked = !a.allow[qg * a.n_groups + a.k_group[j]];
+                    }
+                }
+                x = blocked ? -INFINITY : x;
+                sacc[kt][r] = x;
+                mt = fmaxf(mt, x);
+            }
+        mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        const float mnew = fmaxf(m, mt);
+
+        float alpha = 1.0f;
+        if (mnew == -INFINITY) {
+#pragma unroll
+            for (int kt = 0; kt < NT; kt++) sacc[kt] = v4f{0.f, 0.f, 0.f, 0.f};
+        } else {
+            alpha = fast_exp2((m - mnew) * kLog2e);
+            float ps = 0.0f;
+#pragma unroll
+            for (int kt = 0; kt < NT; kt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float p = fast_exp2((sacc[kt][r] - mnew) * kLog2e);
+                    sacc[kt][r] = p;
+                    ps += p;
+                }
+            lsum = lsum * alpha + ps;
+            m = mnew;
+        }
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) {
+            oacc[dt] *= alpha;
+#pragma unroll
+            for (int kt = 0; kt < NT; kt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++)
+                    oacc[dt] = mfma_f32(Vs[(kt * 16 + 4 * g + r) * SK + dt * 16 + c], sacc[kt][r], oacc[dt]);
+        }
+    }
+
+    lsum += __shfl_xor(lsum, 16, 64);
+    lsum += __shfl_xor(lsum, 32, 64);
+
+    // rows with every key blocked: uniform mean of V over all keys
+    const bool masked = qok && m == -INFINITY;
+    if (__syncthreads_or(masked)) {
+        const int nall = (a.seq_k + KT - 1) / KT;
+        for (int t = 0; t < nall; t++) {
+            const int kv0 = t * KT;
+            __syncthreads();
+            load_tile(Vs, a.V, a.ldv, kv0);
+            __syncthreads();
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+                for (int kt = 0; kt < NT; kt++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int j = kv0 + kt * 16 + 4 * g + r;
+                        const float p = (masked && j < a.seq_k) ? 1.0f : 0.0f;
+                        oacc[dt] = mfma_f32(Vs[(kt * 16 + 4 * g + r) * SK + dt * 16 + c], p, oacc[dt]);
+                    }
+        }
+    }
+
+    if (!qok) return;
+    const float inv = masked ? 1.0f / (float)a.seq_k : 1.0f / lsum;
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++) {
+        const int d = dt * 16 + 4 * g;
+        if (d < HD) {
+            float4 v = make_float4(oacc[dt][0] * inv, oacc[dt][1] * inv, oacc[dt][2] * inv, oacc[dt][3] * inv);
+            *reinterpret_cast<float4*>(a.out + (size_t)qi * a.ldo + h * HD + d) = v;
+        }
+    }
+}
+
+template <int HDP, int KT>
+void run_attn(const AttnArgs& a, hipStream_t st) {
+    auto blocks = [&](int w) { return (long)((a.seq_q + 16 * w - 1) / (16 * w)) * a.n_q; };
+    if (blocks(4) >= 256) {
+        attn_fwd<HDP, KT, 4><<<dim3((a.seq_q + 63) / 64, a.n_q), 256, 0, st>>>(a);
+    } else if (blocks(2) >= 256) {
+        attn_fwd<HDP, KT, 2><<<dim3((a.seq_q + 31) / 32, a.n_q), 128, 0, st>>>(a);
+    } else {
+        attn_fwd<HDP, KT, 1><<<dim3((a.seq_q + 15) / 16, a.n_q), 64, 0, st>>>(a);
+    }
+    VLA_LAUNCH_CHECK();
+}
+
+}  // namespace
+
+void launch_attention(const AttnArgs& a, hipStream_t st) {
+    VLA_REQUIRE(a.seq_q >= 0 && a.seq_k > 0 && a.n_q > 0 && a.n_kv > 0,
+                "attention: need seq_q >= 0, seq_k > 0, n_q > 0, n_kv > 0");
+    VLA_REQUIRE(a.n_q % a.n_kv == 0, "attention: n_q must be a multiple of n_kv");
+    VLA_REQUIRE(a.head_dim > 0 && a.head_dim <= 256 && a.head_dim % 4 == 0,
+                "attention: head_dim must be a multiple of 4 in [4, 256]");
+    VLA_REQUIRE(a.ldq % 4 == 0 && a.ldk % 4 == 0 && a.ldv % 4 == 0 && a.ldo % 4 == 0,
+                "attention: row strides must be multiples of 4 floats");
+    VLA_REQUIRE(aligned(a.Q, 16) && aligned(a.K, 16) && aligned(a.V, 16) && aligned(a.out, 16),
+                "attention: Q, K, V and out must be 16-byte aligned");
+    VLA_REQUIRE(a.ldq >= a.n_q * a.head_dim && a.ldo >= a.n_q * a.head_dim &&
+                    a.ldk >= a.n_kv * a.head_dim && a.ldv >= a.n_kv * a.head_dim,
+                "attention: row stride shorter than heads * head_dim");
+    VLA_REQUIRE(a.mask_kind >= 0 && a.mask_kind <= 3, "attention: unknown mask kind");
+    VLA_REQUIRE(a.mask_kind != 1 || (a.mask && a.ldm >= a.seq_k), "attention: dense mask missing");
+    VLA_REQUIRE(a.mask_kind != 3 || (a.q_group && a.k_group && a.allow && a.n_groups > 0 &&
+                                     a.n_groups <= 256),
+                "attention: group mask needs q_group, k_group, allow and 1..256 groups");
+    if (a.seq_q == 0) return;
+    if (a.head_dim <= 64)
+        run_attn<64, 64>(a, st);
+    else if (a.head_dim <= 128)
+        run_attn<128, 32>(a, st);
+    else
+        run_attn<256, 16>(a, st);
+}
+
+}  // namespace hip
+}  // namespace vla

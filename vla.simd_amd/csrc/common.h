@@ -1,0 +1,110 @@
+// common.h - shared plumbing of the gfx950 backend: error types that the C ABI
+// maps to vla_status, HIP call checking, and small device helpers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+
+namespace vla {
+namespace hip {
+
+// A HIP runtime failure. The C ABI turns it into VLA_ERR_EXCEPTION.
+struct HipError : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
+// A precondition the reference asserts (or an out-of-range argument). The C ABI
+// turns it into VLA_ERR_ARG.
+struct ArgError : std::invalid_argument {
+    using std::invalid_argument::invalid_argument;
+};
+
+[[noreturn]] void throw_hip(hipError_t e, const char* what, const char* file, int line);
+
+#define VLA_HIP_CHECK(expr)                                                    \
+    do {                                                                       \
+        hipError_t vla_e_ = (expr);                                            \
+        if (vla_e_ != hipSuccess) ::vla::hip::throw_hip(vla_e_, #expr, __FILE__, __LINE__); \
+    } while (0)
+
+#define VLA_LAUNCH_CHECK() VLA_HIP_CHECK(hipGetLastError())
+
+#define VLA_REQUIRE(cond, msg)                                                 \
+    do {                                                                       \
+        if (!(cond)) throw ::vla::hip::ArgError(msg);                          \
+    } while (0)
+
+inline int kpad4(int K) { return (K + 3) & ~3; }
+inline int round_up(int v, int m) { return (v + m - 1) / m * m; }
+inline bool aligned(const void* p, size_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+// int8 K bound of nn::Linear::init_int8 (src/nn/linear.cpp:67): the x86
+// kernel's unsigned-biased accumulator must stay in int32. The GPU one is
+// signed (|acc| <= K*127*127) but keeps the same bound so the two backends
+// accept the same layers.
+constexpr int kMaxI8K = 2147483647 / (255 * 127);
+
+// Fixed widths of the device code.
+constexpr int kWave = 64;
+
+// ---- kernel launchers (defined in the .hip files) ----
+
+// quant.hip
+void launch_quantize_rows(const float* x, int ldx, int8_t* xq, int ldq, float* scale,
+                          int rows, int K, hipStream_t st);
+
+// gemm_i8.hip: epilogue selects raw int32 output (acc32 != nullptr) or the
+// fused dequant/bias/act(/accumulate) fp32 store.
+struct GemmArgs {
+    const int8_t* A;  int lda;   // quantized activations [M, lda]
+    const int8_t* B;  int ldb;   // int8 weights [N, ldb]
+    const float* ascale;         // [M]
+    const float* wscale;         // [N]
+    const float* bias;           // [N] or null
+    float* out;       int ldo;   // [M, ldo]
+    int32_t* acc32;              // raw accumulators [M, N] (test path) or null
+    int M, N, K;
+    int act;                     // vla_act
+    int accumulate;              // out += result
+};
+void launch_gemm_i8(const GemmArgs& a, hipStream_t st);
+
+// attn.hip
+struct AttnArgs {
+    float* out; int ldo;
+    const float* Q; int ldq;
+    const float* K; int ldk;
+    const float* V; int ldv;
+    int seq_q, seq_k, n_q, n_kv, head_dim;
+    float scale;
+    int mask_kind;
+    const float* mask; int ldm;
+    int causal_offset;
+    int n_groups;
+    const uint8_t* q_group;
+    const uint8_t* k_group;
+    const uint8_t* allow;
+};
+void launch_attention(const AttnArgs& a, hipStream_t st);
+
+// eltwise.hip
+void launch_layernorm(float* out, const float* x, const float* w, const float* b, int rows,
+                      int hidden, float eps, hipStream_t st);
+void launch_rmsnorm(float* out, const float* x, const float* w, int rows, int hidden, float eps,
+                    hipStream_t st);
+void launch_act(float* x, int64_t n, int act, hipStream_t st);
+void launch_silu_gate(float* out, const float* g, const float* u, int64_t n, hipStream_t st);
+void launch_add(float* out, const float* a, const float* b, int64_t n, hipStream_t st);
+void launch_rope_neox(float* x, int ld, const int32_t* pos, int seq, int n_heads, int head_dim,
+                      float base, hipStream_t st);
+
+// runtime.cpp
+hipStream_t library_stream();  // stream of the host-pointer forms
+bool device_is_gfx950();
+
+}  // namespace hip
+}  // namespace vla

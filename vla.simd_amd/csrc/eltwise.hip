@@ -1,0 +1,174 @@
+// eltwise.hip - token-wise norms, RoPE and elementwise activations on gfx950.
+//
+// LayerNorm / RMSNorm follow src/hal/common/norms.cpp:19-35 and 69-97: per row
+// the mean, variance and sum of squares accumulate in double (fp64 is a full
+// rate path on CDNA4, and these kernels are HBM-bound), inv is computed in
+// double and rounded once to float, and the output is formed in float from
+// (float)(x - mean) exactly as the reference does. One wave64 owns a row and
+// each lane reads and writes the same elements, so out may alias x (ACT calls
+// layernorm(x, x), src/models/act/act_transformer.cpp:259).
+//
+// RoPE NeoX follows norms.cpp:37-67: theta_i = pos * base^(-2i/d) built by the
+// same repeated double multiplication, double cos/sin, and the rotated pair
+// formed in double then rounded to float.
+//
+// Activations are the device functions in act.h (also used by the GEMM
+// epilogue). Every kernel here reads its input once and writes once.
+
+#include "act.h"
+#include "common.h"
+
+namespace vla {
+namespace hip {
+namespace {
+
+__device__ __forceinline__ double wave_sum(double v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__global__ __launch_bounds__(256) void layernorm_kernel(float* out, const float* x, const float* w,
+                                                        const float* b, int rows, int H, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float* xr = x + (size_t)row * H;
+    float* orow = out + (size_t)row * H;
+
+    double s = 0.0;
+    for (int k = lane; k < H; k += 64) s += (double)xr[k];
+    const double mean = wave_sum(s) / H;
+    double v = 0.0;
+    for (int k = lane; k < H; k += 64) {
+        const double d = (double)xr[k] - mean;
+        v += d * d;
+    }
+    const double var = wave_sum(v);
+    const float inv = (float)(1.0 / sqrt(var / H + (double)eps));
+    for (int k = lane; k < H; k += 64) {
+        const float c = (float)((double)xr[k] - mean);
+        orow[k] = b ? fmaf(c * inv, w[k], b[k]) : c * inv * w[k];
+    }
+}
+
+__global__ __launch_bounds__(256) void rmsnorm_kernel(float* out, const float* x, const float* w,
+                                                      int rows, int H, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float* xr = x + (size_t)row * H;
+    float* orow = out + (size_t)row * H;
+    double ss = 0.0;
+    for (int k = lane; k < H; k += 64) {
+        const double d = (double)xr[k];
+        ss += d * d;
+    }
+    ss = wave_sum(ss);
+    const float inv = (float)(1.0 / sqrt(ss / H + (double)eps));
+    for (int k = lane; k < H; k += 64) orow[k] = xr[k] * inv * w[k];
+}
+
+template <int ACT>
+__global__ __launch_bounds__(256) void act_kernel(float* x, int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        x[i] = apply_act<ACT>(x[i]);
+}
+
+__global__ __launch_bounds__(256) void silu_gate_kernel(float* out, const float* g, const float* u,
+                                                        int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        out[i] = act_silu_gate(g[i], u[i]);
+}
+
+__global__ __launch_bounds__(256) void add_kernel(float* out, const float* a, const float* b,
+                                                  int64_t n) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
+        out[i] = a[i] + b[i];
+}
+
+// one thread per (token, pair index i); loops over heads
+__global__ __launch_bounds__(256) void rope_kernel(float* x, int ld, const int32_t* pos, int seq,
+                                                   int n_heads, int head_dim, double theta_scale) {
+    const int half = head_dim / 2;
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= seq * half) return;
+    const int t = idx / half, i = idx % half;
+    double theta = (double)pos[t];
+    for (int j = 0; j < i; j++) theta *= theta_scale;
+    const double c = cos(theta), s = sin(theta);
+    float* row = x + (size_t)t * ld;
+    for (int hh = 0; hh < n_heads; hh++) {
+        float* v = row + hh * head_dim;
+        const float x0 = v[i], x1 = v[i + half];
+        v[i] = (float)(x0 * c - x1 * s);
+        v[i + half] = (float)(x0 * s + x1 * c);
+    }
+}
+
+int grid_for(int64_t n) {
+    const int64_t b = (n + 255) / 256;
+    return (int)(b < 4096 ? (b > 0 ? b : 1) : 4096);
+}
+
+}  // namespace
+
+void launch_layernorm(float* out, const float* x, const float* w, const float* b, int rows,
+                      int hidden, float eps, hipStream_t st) {
+    VLA_REQUIRE(rows >= 0 && hidden > 0, "layernorm: need rows >= 0 and hidden > 0");
+    if (rows == 0) return;
+    layernorm_kernel<<<(rows + 3) / 4, 256, 0, st>>>(out, x, w, b, rows, hidden, eps);
+    VLA_LAUNCH_CHECK();
+}
+
+void launch_rmsnorm(float* out, const float* x, const float* w, int rows, int hidden, float eps,
+                    hipStream_t st) {
+    VLA_REQUIRE(rows >= 0 && hidden > 0, "rmsnorm: need rows >= 0 and hidden > 0");
+    if (rows == 0) return;
+    rmsnorm_kernel<<<(rows + 3) / 4, 256, 0, st>>>(out, x, w, rows, hidden, eps);
+    VLA_LAUNCH_CHECK();
+}
+
+void launch_act(float* x, int64_t n, int act, hipStream_t st) {
+    VLA_REQUIRE(n >= 0, "activation: n < 0");
+    if (n == 0 || act == 0) return;
+    switch (act) {
+    case 1: act_kernel<1><<<grid_for(n), 256, 0, st>>>(x, n); break;
+    case 2: act_kernel<2><<<grid_for(n), 256, 0, st>>>(x, n); break;
+    case 3: act_kernel<3><<<grid_for(n), 256, 0, st>>>(x, n); break;
+    default: throw ArgError("activation: unknown kind");
+    }
+    VLA_LAUNCH_CHECK();
+}
+
+void launch_silu_gate(float* out, const float* g, const float* u, int64_t n, hipStream_t st) {
+    VLA_REQUIRE(n >= 0, "silu_gate: n < 0");
+    if (n == 0) return;
+    silu_gate_kernel<<<grid_for(n), 256, 0, st>>>(out, g, u, n);
+    VLA_LAUNCH_CHECK();
+}
+
+void launch_add(float* out, const float* a, const float* b, int64_t n, hipStream_t st) {
+    VLA_REQUIRE(n >= 0, "add: n < 0");
+    if (n == 0) return;
+    add_kernel<<<grid_for(n), 256, 0, st>>>(out, a, b, n);
+    VLA_LAUNCH_CHECK();
+}
+
+void launch_rope_neox(float* x, int ld, const int32_t* pos, int seq, int n_heads, int head_dim,
+                      float base, hipStream_t st) {
+    VLA_REQUIRE(seq >= 0 && n_heads > 0 && head_dim > 0 && head_dim % 2 == 0,
+                "rope_neox: need seq >= 0, n_heads > 0 and an even head_dim");
+    VLA_REQUIRE(ld >= n_heads * head_dim, "rope_neox: row stride shorter than heads * head_dim");
+    if (seq == 0) return;
+    const double theta_scale = pow((double)base, -2.0 / head_dim);
+    const int n = seq * (head_dim / 2);
+    rope_kernel<<<(n + 255) / 256, 256, 0, st>>>(x, ld, pos, seq, n_heads, head_dim, theta_scale);
+    VLA_LAUNCH_CHECK();
+}
+
+}  // namespace hip
+}  // namespace vla

@@ -1,0 +1,111 @@
+// quant.hip - per-row dynamic int8 quantization on gfx950.
+//
+// Numeric contract (src/ops/quant_ops.h:17-21, src/hal/common/gemm_i8.cpp:49-54,
+// 132-171, 209-244): per row, amax = max_k |x|; s = amax > 0 ?
+// max(amax/127, FLT_MIN) : 1; inv = 1/s; q = clamp(rne(x*inv), -127, 127);
+// columns [K, ldq) are zero. Every step is exact or a single IEEE-rounded
+// operation (max is exact; the two divisions are correctly rounded - hipcc
+// emits the v_div_scale/v_div_fmas/v_div_fixup sequence for '/', never v_rcp
+// alone; the product is one v_mul_f32; v_rndne_f32 is round-half-even), so the
+// result does not depend on the order lanes visit the row and is bit-identical
+// to the reference's scalar and AVX2 quantizers. fp32 denormals are preserved
+// (no -fgpu-flush-denormals-to-zero), which the FLT_MIN floor relies on.
+//
+// Layout: one wave64 per row, four rows per 256-thread block. A lane reads
+// float4 runs (coalesced 1 KiB per wave instruction), so HBM sees the row once;
+// the second pass re-reads it from L1/L2.
+
+#include "common.h"
+
+#include <cfloat>
+
+#pragma clang fp contract(off)
+
+namespace vla {
+namespace hip {
+namespace {
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+__device__ __forceinline__ int q8(float v, float inv) {
+    int q = (int)rintf(v * inv);
+    q = q > 127 ? 127 : q;
+    q = q < -127 ? -127 : q;
+    return q;
+}
+
+// VEC: rows are 16-byte aligned and K % 4 == 0, so float4 loads cover the row.
+template <bool VEC>
+__global__ __launch_bounds__(256) void quantize_rows_kernel(const float* __restrict__ x, int ldx,
+                                                            int8_t* __restrict__ xq, int ldq,
+                                                            float* __restrict__ scale, int rows,
+                                                            int K) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;  // wave-uniform
+    const float* xr = x + (size_t)row * ldx;
+
+    float amax = 0.0f;
+    if (VEC) {
+        for (int k = lane * 4; k < K; k += 256) {
+            const float4 v = *reinterpret_cast<const float4*>(xr + k);
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
+    } else {
+        for (int k = lane; k < K; k += 64) amax = fmaxf(amax, fabsf(xr[k]));
+    }
+    amax = wave_max(amax);
+
+    float s = 1.0f;
+    if (amax > 0.0f) {
+        s = amax / 127.0f;
+        s = s > FLT_MIN ? s : FLT_MIN;
+    }
+    const float inv = 1.0f / s;
+    if (lane == 0) scale[row] = s;
+
+    // ldq % 4 == 0 and the row base is 4-byte aligned (checked by the launcher),
+    // so each lane writes whole 32-bit words covering [0, ldq).
+    int8_t* qr = xq + (size_t)row * ldq;
+    for (int k = lane * 4; k < ldq; k += 256) {
+        uint32_t word = 0;
+        if (VEC && k + 4 <= K) {
+            const float4 v = *reinterpret_cast<const float4*>(xr + k);
+            word = (uint32_t)(q8(v.x, inv) & 0xff) | ((uint32_t)(q8(v.y, inv) & 0xff) << 8) |
+                   ((uint32_t)(q8(v.z, inv) & 0xff) << 16) | ((uint32_t)(q8(v.w, inv) & 0xff) << 24);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int kk = k + j;
+                const int q = kk < K ? q8(xr[kk], inv) : 0;
+                word |= (uint32_t)(q & 0xff) << (8 * j);
+            }
+        }
+        *reinterpret_cast<uint32_t*>(qr + k) = word;
+    }
+}
+
+}  // namespace
+
+void launch_quantize_rows(const float* x, int ldx, int8_t* xq, int ldq, float* scale, int rows,
+                          int K, hipStream_t st) {
+    VLA_REQUIRE(rows >= 0 && K > 0, "quantize: rows must be >= 0 and K > 0");
+    VLA_REQUIRE(ldx >= K, "quantize: ldx < K");
+    VLA_REQUIRE(ldq >= kpad4(K) && ldq % 4 == 0, "quantize: ldq must be >= i8_kpad(K) and a multiple of 4");
+    VLA_REQUIRE(aligned(xq, 4), "quantize: xq must be 4-byte aligned");
+    if (rows == 0) return;
+    const bool vec = K % 4 == 0 && ldx % 4 == 0 && aligned(x, 16);
+    const dim3 grid((rows + 3) / 4), block(256);
+    if (vec)
+        quantize_rows_kernel<true><<<grid, block, 0, st>>>(x, ldx, xq, ldq, scale, rows, K);
+    else
+        quantize_rows_kernel<false><<<grid, block, 0, st>>>(x, ldx, xq, ldq, scale, rows, K);
+    VLA_LAUNCH_CHECK();
+}
+
+}  // namespace hip
+}  // namespace vla
