@@ -1,0 +1,303 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X int8 linear path on BASELINE.json's int8 GEMM sweep.
+
+Workload: M in {1, 50, 100, 512, 2048, 8192} x
+(K, N) in {(512,3200), (960,2560), (2560,960), (768,3072), (4096,4096)}, the
+reference op path dense_linear_i8: fp32 activations ~N(0,1) quantized per row
+on the device, int8 weights uniform in [-127,127] with per-channel scales
+~U(1e-3,1e-2) and bias ~N(0,0.02), int32 accumulate, fp32 out. One step is one
+pass over all 30 shapes (a quantize launch + a GEMM launch each), inputs and
+weights resident in HBM; small shapes cycle through rotating copies of their
+weights and outputs (>= 512 MiB per shape) so every launch streams from HBM
+rather than from L2/MALL.
+
+value = int8 TOPS of the whole step (sum of 2*M*N*K over the shapes / step
+time). roofline = the dominant kernel (the M=8192, K=N=4096 GEMM) measured
+with HIP events on the stream it runs on. cpu_baseline = the reference's own
+dense_linear_i8 (its AVX-VNNI kernel when the host CPU has AVX-VNNI, else its
+scalar dense_linear_i8_ref) built from the reference sources into
+oracle/_ref/, timed on this host on a bounded sample of the same shapes.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA (POP/s x 1000)
+PEAK_HBM_GBS = 8000.0    # MI355X HBM3E
+ROTATE_BYTES = 512 << 20
+
+
+def load_pkg():
+    import importlib.util
+
+    d = os.path.join(ROOT, "vla.simd_amd")
+    spec = importlib.util.spec_from_file_location("vla_simd_amd", os.path.join(d, "__init__.py"),
+                                                  submodule_search_locations=[d])
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["vla_simd_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+def gemm_bytes(M, K, N):
+    """Algorithmic HBM bytes of the GEMM kernel: int8 x and W in, scales and bias, fp32 out."""
+    Kp = (K + 3) & ~3
+    return M * Kp + N * Kp + 4 * M + 8 * N + 4 * M * N
+
+
+def op_bytes(M, K, N):
+    """The whole op from fp32 x (quantize reads 4*M*K and writes M*Kp + 4*M)."""
+    Kp = (K + 3) & ~3
+    return gemm_bytes(M, K, N) + 4 * M * K + M * Kp + 4 * M
+
+
+def roof_us(M, K, N):
+    ops = 2.0 * M * N * K
+    t_mfma = ops / (PEAK_INT8_TOPS * 1e12) * 1e6
+    t_hbm = gemm_bytes(M, K, N) / (PEAK_HBM_GBS * 1e9) * 1e6
+    return max(t_mfma, t_hbm), ("mfma" if t_mfma >= t_hbm else "hbm")
+
+
+class Shape:
+    def __init__(self, vla, torch, synth, M, K, N):
+        self.M, self.K, self.N = M, K, N
+        dev = torch.device("cuda")
+        x, Wq, ws, b = synth.linear_case(M, K, N)
+        self.ldw = (((K + 3) & ~3) + 63) // 64 * 64
+        per = self.ldw * N + 4 * M * N
+        self.R = max(1, min(256, math.ceil(ROTATE_BYTES / per))) if per < ROTATE_BYTES else 1
+        Wp = np.zeros((N, self.ldw), np.int8)
+        Wp[:, :K] = Wq
+        Wd = torch.from_numpy(Wp).to(dev)
+        self.W = [Wd] + [Wd.clone() for _ in range(self.R - 1)]
+        self.out = [torch.empty((M, N), dtype=torch.float32, device=dev) for _ in range(self.R)]
+        self.x = torch.from_numpy(x).to(dev)
+        self.xq = torch.zeros((M, self.ldw), dtype=torch.int8, device=dev)
+        self.sa = torch.empty(M, dtype=torch.float32, device=dev)
+        self.ws = torch.from_numpy(ws).to(dev)
+        self.b = torch.from_numpy(b).to(dev)
+        self.i = 0
+
+    def quantize(self, vla, stream):
+        vla.quantize_act_i8_dev(self.x, self.xq, self.sa, stream)
+
+    def gemm(self, vla, stream):
+        r = self.i % self.R
+        self.i += 1
+        vla.dense_linear_i8_pre_dev(self.out[r], self.xq, self.sa, self.W[r], self.ws, self.b, self.K,
+                                    stream=stream)
+
+    def op(self, vla, stream):
+        self.quantize(vla, stream)
+        self.gemm(vla, stream)
+
+
+def cur(torch):
+    return torch.cuda.current_stream().cuda_stream
+
+
+def capture(torch, fn, n):
+    """A HIP graph of n calls of fn(stream) (torch.cuda.graph capture; the library's
+    launches go to the capturing stream, so the graph holds exactly those kernels)."""
+    fn(cur(torch))  # eager warm-up: grows any workspace outside the capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(n):
+            fn(cur(torch))
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(torch, g, replays, stream_obj):
+    """Average us per replay, HIP events on the stream the replays run on."""
+    g.replay()
+    stream_obj.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream_obj)
+    for _ in range(replays):
+        g.replay()
+    end.record(stream_obj)
+    end.synchronize()
+    return start.elapsed_time(end) * 1e3 / replays
+
+
+def cpu_baseline(synth, budget_s=15.0):
+    """The reference's dense_linear_i8 on this host (oracle/_ref build)."""
+    from oracle import bindings as ob
+
+    if not ob.ref_available():
+        return None
+    L = ob.ref()
+    sample = [(100, 512, 3200), (50, 960, 2560), (100, 2560, 960), (100, 768, 3072),
+              (100, 4096, 4096), (512, 512, 3200), (512, 960, 2560), (512, 2560, 960),
+              (512, 768, 3072), (512, 4096, 4096)]
+    tot_ops, tot_t, done = 0.0, 0.0, []
+    t_start = time.time()
+    for M, K, N in sample:
+        x, Wq, ws, b = synth.linear_case(M, K, N)
+        blob = ob.ref_panels(Wq, K)
+        xq = np.empty((M, (K + 3) & ~3), np.int8)
+        sa = np.empty(M, np.float32)
+        ob.ref_dense_linear_i8(x, blob, ws, b, N, K, xq, sa)  # warm
+        reps = 0
+        t0 = time.perf_counter()
+        while True:
+            ob.ref_dense_linear_i8(x, blob, ws, b, N, K, xq, sa)
+            reps += 1
+            el = time.perf_counter() - t0
+            if reps >= 5 and el > 0.5 or el > 3.0:
+                break
+        tot_ops += 2.0 * M * N * K * reps
+        tot_t += el
+        done.append(f"{M}x{K}x{N}")
+        if time.time() - t_start > budget_s:
+            break
+    return {
+        "value": round(tot_ops / tot_t / 1e12, 4),
+        "unit": "TOPS (int8, 2*M*N*K per dense_linear_i8 call)",
+        "cores": int(L.ref_omp_max_threads()),
+        "kind": "reference",
+        "sample": "reference dense_linear_i8 (quantize + " +
+                  ("AVX-VNNI kernel" if L.ref_int8_available() else "scalar dense_linear_i8_ref: host has no AVX-VNNI") +
+                  ", backend " + L.ref_backend_name().decode() + ") over shapes " + ", ".join(done) +
+                  f"; sum ops / sum wall time, {tot_t:.1f} s of CPU work",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
+    ap.add_argument("--shapes", default="", help="comma list MxKxN to restrict the sweep (debug)")
+    ap.add_argument("--profile-only", action="store_true",
+                    help="only the dominant GEMM, back to back (for rocprofv3 runs)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the "
+              "multi-GPU sharding of this path is a design, not a measured configuration",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    vla = load_pkg()
+    vla.lib()
+    if not vla.int8_available():
+        print("bench.py: no gfx950 device visible", file=sys.stderr)
+        sys.exit(1)
+    import vla_simd_amd.synth as synth
+
+    stream_obj = torch.cuda.Stream()
+    torch.cuda.set_stream(stream_obj)
+    stream = stream_obj.cuda_stream
+
+    shapes_spec = [(M, K, N) for (K, N) in synth.SWEEP_KN for M in synth.SWEEP_M]
+    if args.shapes:
+        want = {tuple(int(v) for v in s.split("x")) for s in args.shapes.split(",")}
+        shapes_spec = [s for s in shapes_spec if s in want]
+    dominant = (8192, 4096, 4096)
+
+    if args.profile_only:
+        sh = Shape(vla, torch, synth, *dominant)
+        sh.quantize(vla, stream)
+        for _ in range(20):
+            sh.gemm(vla, stream)  # eager launches: the profiler sees 20 GEMM dispatches
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_only": "gemm 8192x4096x4096 x20"}))
+        return
+
+    shapes = [Shape(vla, torch, synth, *s) for s in shapes_spec]
+    torch.cuda.synchronize()
+    print(f"bench: {len(shapes)} shapes resident on {vla.device_name()}", file=sys.stderr, flush=True)
+
+    # per-shape kernel times: a graph of n back-to-back GEMM launches (cycling the
+    # rotating copies), and a graph of n whole ops (quantize + GEMM)
+    rows = []
+    dom_us = None
+    for sh in shapes:
+        sh.quantize(vla, stream)
+        torch.cuda.synchronize()
+        n = max(sh.R, max(8, min(200, int(2000 / max(1.0, roof_us(sh.M, sh.K, sh.N)[0])))))
+        g_gemm = capture(torch, lambda st: sh.gemm(vla, st), n)
+        g_us = time_graph(torch, g_gemm, 3, stream_obj) / n
+        g_op = capture(torch, lambda st: sh.op(vla, st), n)
+        op_us = time_graph(torch, g_op, 3, stream_obj) / n
+        del g_gemm, g_op
+        ops = 2.0 * sh.M * sh.N * sh.K
+        t_roof, bound = roof_us(sh.M, sh.K, sh.N)
+        rows.append({
+            "M": sh.M, "K": sh.K, "N": sh.N, "gemm_us": round(g_us, 3), "op_us": round(op_us, 3),
+            "gemm_tops": round(ops / g_us / 1e6, 2),
+            "gemm_gbs": round(gemm_bytes(sh.M, sh.K, sh.N) / g_us / 1e3, 1),
+            "bound": bound, "roof_us": round(t_roof, 3), "frac": round(t_roof / g_us, 4),
+            "rotating_copies": sh.R,
+        })
+        if (sh.M, sh.K, sh.N) == dominant:
+            dom_us = g_us
+        print(f"  {sh.M}x{sh.K}x{sh.N}: gemm {g_us:.2f} us ({rows[-1]['gemm_tops']} TOPS, "
+              f"{rows[-1]['gemm_gbs']} GB/s, {bound} frac {rows[-1]['frac']}), op {op_us:.2f} us",
+              file=sys.stderr, flush=True)
+
+    # the step: every shape once (quantize + GEMM), captured as one graph
+    def step(st):
+        for sh in shapes:
+            sh.op(vla, st)
+
+    g_step = capture(torch, step, 1)
+    for _ in range(args.warmup):
+        g_step.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    start.record(stream_obj)
+    for _ in range(args.steps):
+        g_step.replay()
+    end.record(stream_obj)
+    end.synchronize()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms = start.elapsed_time(end) / args.steps
+    total_ops = sum(2.0 * s.M * s.N * s.K for s in shapes)
+    value = total_ops / (ms * 1e-3) / 1e12
+
+    roofline = None
+    if dom_us is not None:
+        ach = 2.0 * 8192 * 4096 * 4096 / dom_us / 1e6
+        roofline = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_INT8_TOPS,
+                    "unit": "TFLOP/s", "frac": round(ach / PEAK_INT8_TOPS, 4), "traffic": None,
+                    "kernel": "gemm_i8_tiled 8192x4096x4096 (int8 ops = 2*M*N*K per launch)",
+                    "avg_launch_us": round(dom_us, 3)}
+
+    cpu = None if args.no_cpu else cpu_baseline(synth)
+
+    print(json.dumps({
+        "metric": "int8 GEMM TOPS (% MFMA peak) + per-chunk policy latency ms, batch 1",
+        "value": round(value, 3), "unit": "TOPS", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8 (int32 accumulate, fp32 out)",
+        "data": "synthetic (seeded BASELINE distributions, vla.simd_amd/synth.py)",
+        "config": {"workload": "int8 GEMM sweep, BASELINE.json configs[1]: 30 dense_linear_i8 "
+                               "calls (device quantize + i8 MFMA GEMM) per step",
+                   "shapes": len(shapes), "wall_s_timed": round(wall, 3)},
+        "roofline": roofline, "cpu_baseline": cpu, "sweep": rows,
+    }), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,221 @@
+"""GPU parity of the int8 path: quantizer, int32 accumulators, fused epilogue.
+
+Bar: quantized activations, scales and int32
+accumulators bit-exact; the fp32 epilogue is the reference's single
+expression fma((float)acc*ws, sa, b) (src/hal/common/gemm_i8.cpp:278), so the
+fp32 outputs are required bit-exact too. The checker is the CPU oracle
+(oracle/oracle.c) on the same seeded inputs, itself pinned to the real
+reference build in tests/test_oracle.py.
+"""
+
+import os
+
+import numpy as np
+import pytest
+
+from helpers import load_synth, max_rel, same_bits
+
+pytestmark = pytest.mark.gpu
+
+# tests/test_ops.cpp:138 shapes (seq, N, K), plus tails and BASELINE-like ones
+TESTOPS_SHAPES = [(1, 16, 3), (7, 48, 64), (50, 768, 1027), (13, 64, 17), (257, 96, 48)]
+EXTRA_SHAPES = [(1, 3200, 512), (100, 3200, 512), (129, 100, 70), (300, 512, 512),
+                (302, 3200, 512), (64, 2560, 960), (100, 960, 2560), (16, 4096, 4096),
+                (600, 200, 36), (2, 40, 1)]
+
+
+def _case(orc, seq, N, K):
+    fr = orc.Frand()
+    x = fr.rv(seq * K).reshape(seq, K)
+    W = fr.rv(N * K, -0.2, 0.2).reshape(N, K)
+    b = fr.rv(N)
+    return x, W, b
+
+
+@pytest.mark.parametrize("magnitude", [0.0, np.finfo(np.float32).smallest_subnormal, 1e-37, 1.0])
+@pytest.mark.parametrize("width", [3, 16, 33])
+def test_quantize_edge_cases(vla, orc, magnitude, width):
+    """test_ops.cpp:93-112: zero, denormal, tiny and unit rows."""
+    x = np.array([(1 if i % 2 == 0 else -1) * magnitude for i in range(width)], np.float32)[None]
+    q, s = vla.quantize_act_i8(x)
+    qo, so = orc.quantize_act_i8(x)
+    assert same_bits(q, qo) and same_bits(s, so)
+    assert np.isfinite(s[0]) and s[0] > 0
+    assert q.min() >= -127
+    assert np.all(np.abs(q[0, :width].astype(np.float64) * s[0] - x[0]) <= s[0] * 0.51)
+    assert np.all(q[0, width:] == 0)
+
+
+@pytest.mark.parametrize("seq,K", [(1, 3), (5, 17), (100, 512), (302, 512), (177, 960), (50, 720),
+                                   (64, 4096), (1000, 2560), (3, 1027)])
+def test_quantize_rows(vla, orc, seq, K):
+    synth = load_synth()
+    x = synth.normal(f"q.{seq}x{K}", (seq, K))
+    x[0, :] *= 1e-3
+    if seq > 2:
+        x[2, :] = 0.0
+    q, s = vla.quantize_act_i8(x)
+    qo, so = orc.quantize_act_i8(x)
+    assert same_bits(q, qo), "int8 activations differ from the oracle"
+    assert same_bits(s, so), "activation scales differ from the oracle"
+
+
+@pytest.mark.parametrize("seq,N,K", TESTOPS_SHAPES + EXTRA_SHAPES)
+def test_gemm_int32_and_epilogue(vla, orc, seq, N, K):
+    x, W, b = _case(orc, seq, N, K)
+    Wq, ws = orc.quantize_weights_i8(W)
+    xq, sa = orc.quantize_act_i8(x)
+    acc = vla.gemm_i8_i32(xq, Wq, K)
+    acc_o = orc.gemm_i8_acc(xq, Wq, K)
+    assert same_bits(acc, acc_o), "int32 accumulators differ"
+    out = vla.dense_linear_i8_pre(xq, sa, Wq, ws, b, K)
+    out_o = orc.dense_linear_i8_pre(xq, sa, Wq, ws, b, K)
+    assert same_bits(out, out_o), "fp32 epilogue differs"
+    out_nb = vla.dense_linear_i8_pre(xq, sa, Wq, ws, None, K)
+    assert same_bits(out_nb, orc.dense_linear_i8_pre(xq, sa, Wq, ws, None, K))
+    full = vla.dense_linear_i8(x, Wq, ws, b)
+    assert same_bits(full, out_o), "quantize + GEMM differs from the two-step oracle"
+
+
+def test_int8_accuracy_vs_double(vla, orc):
+    """test_ops.cpp:153: the int8 linear within 2e-2 of the double product, scaled
+    by the magnitude sum."""
+    for seq, N, K in TESTOPS_SHAPES:
+        x, W, b = _case(orc, seq, N, K)
+        Wq, ws = vla.pack_weights_i8(W)
+        out = vla.dense_linear_i8(x, Wq, ws, b)
+        ref = x.astype(np.float64) @ W.T.astype(np.float64) + b
+        mag = np.abs(x.astype(np.float64)) @ np.abs(W.T.astype(np.float64)) + np.abs(b)
+        assert np.max(np.abs(out - ref) / (mag + 1e-30)) <= 2e-2
+
+
+@pytest.mark.parametrize("M,K,N", [(100, 512, 3200), (1, 4096, 4096), (50, 960, 2560),
+                                   (100, 2560, 960), (100, 768, 3072), (512, 512, 3200),
+                                   (512, 960, 2560)])
+def test_baseline_shapes(vla, orc, M, K, N):
+    """BASELINE.json distributions: x ~ N(0,1), int8 W uniform, scales U(1e-3,1e-2), bias N(0,.02)."""
+    synth = load_synth()
+    x, Wq, ws, b = synth.linear_case(M, K, N)
+    xq, sa = vla.quantize_act_i8(x)
+    xqo, sao = orc.quantize_act_i8(x)
+    assert same_bits(xq, xqo) and same_bits(sa, sao)
+    Wp = np.zeros((N, (K + 3) & ~3), np.int8)
+    Wp[:, :K] = Wq
+    out = vla.dense_linear_i8(x, Wp, ws, b)
+    out_o = orc.dense_linear_i8_pre(xqo, sao, Wp, ws, b, K)
+    assert same_bits(out, out_o)
+
+
+@pytest.mark.parametrize("act", [1, 2, 3])
+def test_fused_activation_and_accumulate(vla, orc, torch_cuda, act):
+    torch = torch_cuda
+    seq, N, K = 302, 3200, 512
+    x, W, b = _case(orc, seq, N, K)
+    lin = vla.LinearI8.from_f32(W, b)
+    dev = torch.device("cuda")
+    xd = torch.from_numpy(x).to(dev)
+    xq = torch.zeros((seq, lin.ldw), dtype=torch.int8, device=dev)
+    sa = torch.zeros(seq, dtype=torch.float32, device=dev)
+    out = torch.zeros((seq, N), dtype=torch.float32, device=dev)
+    lin.forward_dev(out, xd, xq, sa, act=act)
+    torch.cuda.synchronize()
+    Wq, ws = orc.quantize_weights_i8(W)
+    xqo, sao = orc.quantize_act_i8(x)
+    lin_o = orc.dense_linear_i8_pre(xqo, sao, Wq, ws, b, K)
+    got = out.cpu().numpy()
+    want = orc.apply_act(lin_o, act)
+    if act == 1:
+        assert same_bits(got, want), "relu epilogue must be exact"
+    else:
+        assert max_rel(got, want) <= 2e-6
+    # accumulate: out += linear(x) on top of a residual
+    res = torch.from_numpy(np.full((seq, N), 0.5, np.float32)).to(dev)
+    lin.forward_dev(res, xd, xq, sa, act=0, accumulate=1)
+    torch.cuda.synchronize()
+    assert same_bits(res.cpu().numpy(), (np.float32(0.5) + lin_o).astype(np.float32))
+    lin.close()
+
+
+def test_resident_linear_from_int8(vla, orc, torch_cuda):
+    torch = torch_cuda
+    synth = load_synth()
+    M, K, N = 100, 512, 3200
+    x, Wq, ws, b = synth.linear_case(M, K, N)
+    lin = vla.LinearI8.from_i8(Wq, ws, b)
+    dev = torch.device("cuda")
+    xd = torch.from_numpy(x).to(dev)
+    xq = torch.zeros((M, lin.ldw), dtype=torch.int8, device=dev)
+    sa = torch.zeros(M, dtype=torch.float32, device=dev)
+    out = torch.empty((M, N), dtype=torch.float32, device=dev)
+    lin.forward_dev(out, xd, xq, sa)
+    torch.cuda.synchronize()
+    xqo, sao = orc.quantize_act_i8(x)
+    assert same_bits(out.cpu().numpy(), orc.dense_linear_i8_pre(xqo, sao, Wq, ws, b, K))
+    # quantized-input entry (Linear::forward_quantized)
+    out2 = torch.empty_like(out)
+    lin.forward_quantized_dev(out2, xq, sa)
+    torch.cuda.synchronize()
+    assert same_bits(out2.cpu().numpy(), out.cpu().numpy())
+    lin.close()
+
+
+def test_k_bound_rejected(vla):
+    """test_ops.cpp:79-92: K > INT_MAX/(255*127) is refused, not computed."""
+    K = 2147483647 // (255 * 127) + 1
+    with pytest.raises(vla.VlaError) as e:
+        vla.LinearI8.from_f32(np.ones((16, K), np.float32))
+    assert e.value.status == vla.VLA_ERR_ARG
+
+
+TILES = ["256x256x64", "256x128x128", "256x128x64", "128x128x128", "128x128x64", "64x128x64",
+         "64x64x64"]
+
+
+@pytest.mark.parametrize("tile", TILES)
+@pytest.mark.parametrize("M,N,K", [(300, 200, 200), (257, 130, 48), (520, 272, 1024), (129, 17, 64)])
+def test_every_tile_config(vla, orc, torch_cuda, tile, M, N, K):
+    """Each aligned-kernel tile, forced, on shapes off the tile grid: M and N
+    edges, a K tail, K below one slab (device rows padded to 16 bytes)."""
+    torch = torch_cuda
+    ld = (K + 15) // 16 * 16
+    x, W, b = _case(orc, M, N, K)
+    Wq, ws = orc.quantize_weights_i8(W, ldq=ld)
+    xq, sa = orc.quantize_act_i8(x, ldq=ld)
+    dev = torch.device("cuda")
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    acc = torch.zeros((M, N), dtype=torch.int32, device=dev)
+    out = torch.zeros((M, N), dtype=torch.float32, device=dev)
+    os.environ["VLA_HIP_GEMM_TILE"] = tile
+    try:
+        vla.gemm_i8_i32_dev(acc, d(xq), d(Wq), K)
+        vla.dense_linear_i8_pre_dev(out, d(xq), d(sa), d(Wq), d(ws), d(b), K)
+        torch.cuda.synchronize()
+    finally:
+        del os.environ["VLA_HIP_GEMM_TILE"]
+    assert same_bits(acc.cpu().numpy(), orc.gemm_i8_acc(xq, Wq, K)), f"int32 differs with tile {tile}"
+    assert same_bits(out.cpu().numpy(), orc.dense_linear_i8_pre(xq, sa, Wq, ws, b, K))
+
+
+@pytest.mark.parametrize("tile", TILES)
+def test_tile_epilogue_options(vla, orc, torch_cuda, tile):
+    """act + accumulate through each tile's LDS-staged epilogue, with an output
+    row stride wider than N."""
+    torch = torch_cuda
+    M, N, K = 300, 200, 192
+    x, W, b = _case(orc, M, N, K)
+    Wq, ws = orc.quantize_weights_i8(W, ldq=192)
+    xq, sa = orc.quantize_act_i8(x, ldq=192)
+    dev = torch.device("cuda")
+    out = torch.full((M, 260), 0.25, dtype=torch.float32, device=dev)
+    os.environ["VLA_HIP_GEMM_TILE"] = tile
+    try:
+        vla.dense_linear_i8_pre_dev(out[:, :N], torch.from_numpy(xq).to(dev), torch.from_numpy(sa).to(dev),
+                                    torch.from_numpy(Wq).to(dev), torch.from_numpy(ws).to(dev),
+                                    torch.from_numpy(b).to(dev), K, act=1, accumulate=1)
+        torch.cuda.synchronize()
+    finally:
+        del os.environ["VLA_HIP_GEMM_TILE"]
+    got = out.cpu().numpy()
+    want = np.float32(0.25) + orc.apply_act(orc.dense_linear_i8_pre(xq, sa, Wq, ws, b, K), 1)
+    assert same_bits(got[:, :N], want.astype(np.float32))
+    assert np.all(got[:, N:] == np.float32(0.25)), "wrote past N"

@@ -138,9 +138,19 @@ def _declare(L):
 
 
 def lib(path: str | None = None):
-    """Load libvla_simd_hip.so (once). Raises if it is not built."""
+    """Load libvla_simd_hip.so (once). Raises if it is not built.
+
+    PyTorch wheels for ROCm carry their own libamdhip64.so.7. Whichever copy a
+    process loads first serves every later library with that soname, so torch
+    is imported (when installed) before this library: the process then holds a
+    single HIP runtime and torch's device pointers and streams are valid here.
+    """
     global _lib
     if _lib is None:
+        try:
+            import torch  # noqa: F401
+        except ImportError:
+            pass
         p = path or os.environ.get("VLA_SIMD_HIP_LIB", LIB_PATH)
         if not os.path.exists(p):
             raise RuntimeError(f"{p} is not built: run __graft_entry__.build() (make -C vla.simd_amd/csrc)")

@@ -331,6 +331,12 @@ VLA_API int32_t vla_attention(float* out, const float* Q, const float* K, const 
         VLA_REQUIRE(kind != VLA_MASK_GROUPS || (mask->q_group && mask->k_group && mask->allow &&
                                                 mask->n_groups > 0 && mask->n_groups <= 256),
                     "group mask incomplete");
+        if (kind == VLA_MASK_GROUPS) {
+            for (int i = 0; i < seq_q; i++)
+                VLA_REQUIRE(mask->q_group[i] < mask->n_groups, "q_group id >= n_groups");
+            for (int j = 0; j < seq_k; j++)
+                VLA_REQUIRE(mask->k_group[j] < mask->n_groups, "k_group id >= n_groups");
+        }
         if (seq_q == 0) return;
         const size_t nqo = (size_t)seq_q * n_q * head_dim, nkv = (size_t)seq_k * n_kv * head_dim;
         Staging& S = staging();

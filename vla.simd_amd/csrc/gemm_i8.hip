@@ -11,33 +11,44 @@
 // product and one fma per output, in the reference's order. Contraction is off
 // in this file so the product stays a separate rounding.
 //
+// All kernels use v_mfma_i32_16x16x64_i8: lane l supplies 16 contiguous bytes
+// of row (l % 16) at k offset 16*(l / 16) for both operands, so whatever k
+// order the unit uses inside one instruction it pairs equal k on both sides.
+// Output lane l holds column l % 16, rows 4*(l/16) + r.
+//
 // Kernels
-//   gemm_i8_tiled   BM x BN block tile, 4 waves in a WM x WN grid, K staged
-//                   through LDS in BK-byte slabs, double buffered (global loads
-//                   of slab k+1 are in flight while slab k feeds the MFMAs).
-//                   v_mfma_i32_16x16x64_i8: lane l supplies 16 contiguous bytes
-//                   of row (l % 16) at k offset 16*(l / 16) for both operands,
-//                   so whatever k order the unit uses inside one instruction it
-//                   pairs equal k on both sides. Output lane l holds column
-//                   l % 16, rows 4*(l/16) + r.
-//                   LDS rows are padded by 16 bytes so the 16 rows one
-//                   ds_read_b128 touches fall on distinct bank groups.
-//                   Workgroups are remapped so each XCD (the hardware deals
-//                   workgroup i to XCD i % 8) owns a contiguous run of tiles,
-//                   grouped 8 tile-rows deep, which keeps the A and B panels a
-//                   run shares in that XCD's L2.
-//   gemm_i8_skinny  M <= 128 (action chunks, decode rows): one block owns a
-//                   16*FN-column slab of the output and every row; its waves
-//                   split K, stream Wq straight from HBM into MFMA registers
-//                   (each weight byte is read once) and sum their int32
-//                   partials with LDS atomics before one epilogue. A second
-//                   grid dimension splits K across blocks when the slab count
-//                   alone cannot fill the chip; those partials meet in a global
-//                   int32 workspace and the last block of a slab runs the
-//                   epilogue.
+//   gemm_i8_tiled   16-byte aligned rows (every resident layout of this
+//                   library). BM x BN block tile, 4 waves in a 2 x 2 grid, K
+//                   staged through LDS in BK-byte slabs, double buffered: the
+//                   global loads of slab k+2 are issued as soon as slab k+1 is
+//                   in LDS, and overlap the MFMAs of slab k+1. The main loop is
+//                   branch-free: rows past M or N are clamped to the last row
+//                   (their results are never stored) and only the last, partial
+//                   K slab is read with byte masks. LDS rows are padded by 16
+//                   bytes so the 16 rows one ds_read_b128 touches fall on
+//                   distinct bank groups. Workgroups are remapped so each XCD
+//                   (the hardware deals workgroup i to XCD i % 8) owns a
+//                   contiguous run of tiles, grouped 8 tile-rows deep, which
+//                   keeps the A and B panels a run shares in that XCD's L2.
+//                   The epilogue goes through LDS so each row segment leaves as
+//                   16-byte stores.
+//   gemm_i8_skinny  M <= 128, aligned rows (action chunks, decode rows): one
+//                   block owns a 16-column slab of the output and every row; its
+//                   waves take interleaved 64-byte k-steps, stream Wq straight
+//                   from HBM into MFMA registers (each weight byte is read once)
+//                   and sum their int32 partials with LDS atomics before one
+//                   epilogue. No cross-block reduction: no global atomics and no
+//                   device-scope fences (which write back L2 on a multi-XCD part).
+//   gemm_i8_generic any 4-byte aligned strides (the op API accepts the
+//                   reference's [seq, i8_kpad(K)] rows, e.g. K = 1027): 64 x 64
+//                   tiles, every chunk masked at K.
 
 #include "act.h"
 #include "common.h"
+
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
 
 #pragma clang fp contract(off)
 
@@ -85,13 +96,8 @@ __device__ __forceinline__ v4i load_chunk(const int8_t* row, int k, int K) {
     return r;
 }
 
-// One output element of the fused epilogue. mode: 0 store, 1 accumulate,
-// 2 raw int32.
-__device__ __forceinline__ void store_out(const GemmArgs& a, int m, int n, int acc) {
-    if (a.acc32) {
-        a.acc32[(size_t)m * a.N + n] = acc;
-        return;
-    }
+// The fused epilogue value of one output (before an accumulate).
+__device__ __forceinline__ float epi_value(const GemmArgs& a, int m, int n, int acc) {
     const float p = (float)acc * a.wscale[n];
     float v = fmaf(p, a.ascale[m], a.bias ? a.bias[n] : 0.0f);
     switch (a.act) {
@@ -100,6 +106,16 @@ __device__ __forceinline__ void store_out(const GemmArgs& a, int m, int n, int a
     case 3: v = act_gelu_erf(v); break;
     default: break;
     }
+    return v;
+}
+
+// One output element, straight to global (generic and skinny kernels).
+__device__ __forceinline__ void store_out(const GemmArgs& a, int m, int n, int acc) {
+    if (a.acc32) {
+        a.acc32[(size_t)m * a.N + n] = acc;
+        return;
+    }
+    float v = epi_value(a, m, n, acc);
     float* o = a.out + (size_t)m * a.ldo + n;
     if (a.accumulate) v = *o + v;
     *o = v;
@@ -121,22 +137,33 @@ __device__ __forceinline__ void tile_coords(int bid, int nbm, int nbn, int& tm, 
     tn = in / gm;
 }
 
-template <int BM, int BN, int BK, int WM, int WN, bool ALIGNED>
-__global__ __launch_bounds__(256) void gemm_i8_tiled(GemmArgs a) {
-    constexpr int TM = BM / WM, TN = BN / WN;
-    constexpr int FM = TM / 16, FN = TN / 16;
-    constexpr int SA = BK + 16;                 // padded LDS row, bytes
-    constexpr int CPR = BK / 16;                // 16-byte chunks per row
-    constexpr int CA = (BM * CPR + 255) / 256;  // chunks per thread, A slab
-    constexpr int CB = (BN * CPR + 255) / 256;
-    static_assert(WM * WN == 4, "4 waves");
-    static_assert(TM % 16 == 0 && TN % 16 == 0 && BK % 64 == 0, "tile shape");
+// ----------------------------------------------------------------- tiled --
 
-    __shared__ __attribute__((aligned(16))) int8_t smem[2 * (BM + BN) * SA];
+template <int BM, int BN, int BK>
+struct TileCfg {
+    static constexpr int TM = BM / 2, TN = BN / 2;
+    static constexpr int FM = TM / 16, FN = TN / 16;
+    static constexpr int SA = BK + 16;   // padded LDS row, bytes
+    static constexpr int CPR = BK / 16;  // 16-byte chunks per row
+    static constexpr int CA = BM * CPR / 256, CB = BN * CPR / 256;
+    static constexpr int LDW = TN + 4;   // epilogue staging row, floats
+    static constexpr int MAIN = 2 * (BM + BN) * SA;
+    static constexpr int EPI = 4 * 16 * LDW * 4;
+    static constexpr int LDS = MAIN > EPI ? MAIN : EPI;
+    static_assert(BM * CPR % 256 == 0 && BN * CPR % 256 == 0, "chunks must split evenly");
+    static_assert(TM % 16 == 0 && TN % 16 == 0 && BK % 64 == 0, "tile shape");
+};
+
+template <int BM, int BN, int BK>
+__global__ __launch_bounds__(256) void gemm_i8_tiled(GemmArgs a) {
+    using C = TileCfg<BM, BN, BK>;
+    constexpr int TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN, SA = C::SA, CPR = C::CPR;
+    constexpr int CA = C::CA, CB = C::CB, LDW = C::LDW;
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / WN, wn = wave % WN;
+    const int wm = wave >> 1, wn = wave & 1;
 
     int tm, tn;
     tile_coords(blockIdx.x, (a.M + BM - 1) / BM, (a.N + BN - 1) / BN, tm, tn);
@@ -144,52 +171,51 @@ __global__ __launch_bounds__(256) void gemm_i8_tiled(GemmArgs a) {
     const int K = a.K;
 
     // Per-thread slab chunks, fixed across K: chunk c of a slab is row c / CPR,
-    // bytes [16*(c % CPR), +16). act: the chunk exists in this slab shape;
-    // ok: it also lies inside the matrix (rows past M or N load as zero).
+    // bytes [16*(c % CPR), +16). Rows past the matrix are clamped to its last row.
     const int8_t* arow[CA];
-    int akc[CA], aoff[CA];
-    bool aact[CA], aok[CA];
+    int aoff[CA];
 #pragma unroll
     for (int j = 0; j < CA; j++) {
-        const int c = tid + 256 * j;
-        const int r = c / CPR;
-        akc[j] = (c % CPR) * 16;
-        aact[j] = c < BM * CPR;
-        aok[j] = aact[j] && m0 + r < a.M;
-        arow[j] = a.A + (size_t)(aok[j] ? m0 + r : 0) * a.lda;
-        aoff[j] = r * SA + akc[j];
+        const int c = tid + 256 * j, r = c / CPR, kc = (c % CPR) * 16;
+        const int m = m0 + r < a.M ? m0 + r : a.M - 1;
+        arow[j] = a.A + (size_t)m * a.lda + kc;
+        aoff[j] = r * SA + kc;
     }
     const int8_t* brow[CB];
-    int bkc[CB], boff[CB];
-    bool bact[CB], bok[CB];
+    int boff[CB];
 #pragma unroll
     for (int j = 0; j < CB; j++) {
-        const int c = tid + 256 * j;
-        const int r = c / CPR;
-        bkc[j] = (c % CPR) * 16;
-        bact[j] = c < BN * CPR;
-        bok[j] = bact[j] && n0 + r < a.N;
-        brow[j] = a.B + (size_t)(bok[j] ? n0 + r : 0) * a.ldb;
-        boff[j] = BM * SA + r * SA + bkc[j];
+        const int c = tid + 256 * j, r = c / CPR, kc = (c % CPR) * 16;
+        const int n = n0 + r < a.N ? n0 + r : a.N - 1;
+        brow[j] = a.B + (size_t)n * a.ldb + kc;
+        boff[j] = BM * SA + r * SA + kc;
     }
 
     v4i ra[CA], rb[CB];
     auto gload = [&](int k0) {
 #pragma unroll
-        for (int j = 0; j < CA; j++)
-            ra[j] = aok[j] ? load_chunk<ALIGNED>(arow[j], k0 + akc[j], K) : v4i{0, 0, 0, 0};
+        for (int j = 0; j < CA; j++) ra[j] = *reinterpret_cast<const v4i*>(arow[j] + k0);
 #pragma unroll
-        for (int j = 0; j < CB; j++)
-            rb[j] = bok[j] ? load_chunk<ALIGNED>(brow[j], k0 + bkc[j], K) : v4i{0, 0, 0, 0};
+        for (int j = 0; j < CB; j++) rb[j] = *reinterpret_cast<const v4i*>(brow[j] + k0);
+    };
+    auto gload_tail = [&](int k0) {
+#pragma unroll
+        for (int j = 0; j < CA; j++) {
+            const int kc = ((tid + 256 * j) % CPR) * 16;
+            ra[j] = load_chunk<true>(arow[j] - kc, k0 + kc, K);
+        }
+#pragma unroll
+        for (int j = 0; j < CB; j++) {
+            const int kc = ((tid + 256 * j) % CPR) * 16;
+            rb[j] = load_chunk<true>(brow[j] - kc, k0 + kc, K);
+        }
     };
     auto lstore = [&](int buf) {
         int8_t* s = smem + buf * (BM + BN) * SA;
 #pragma unroll
-        for (int j = 0; j < CA; j++)
-            if (aact[j]) *reinterpret_cast<v4i*>(s + aoff[j]) = ra[j];
+        for (int j = 0; j < CA; j++) *reinterpret_cast<v4i*>(s + aoff[j]) = ra[j];
 #pragma unroll
-        for (int j = 0; j < CB; j++)
-            if (bact[j]) *reinterpret_cast<v4i*>(s + boff[j]) = rb[j];
+        for (int j = 0; j < CB; j++) *reinterpret_cast<v4i*>(s + boff[j]) = rb[j];
     };
 
     v4i acc[FM][FN];
@@ -198,17 +224,9 @@ __global__ __launch_bounds__(256) void gemm_i8_tiled(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < FN; j++) acc[i][j] = v4i{0, 0, 0, 0};
 
-    const int nk = (K + BK - 1) / BK;
-    gload(0);
-    lstore(0);
-    __syncthreads();
-
     const int arow_l = (wm * TM + (lane & 15)) * SA + (lane >> 4) * 16;
     const int brow_l = BM * SA + (wn * TN + (lane & 15)) * SA + (lane >> 4) * 16;
-
-    for (int kt = 0; kt < nk; kt++) {
-        const int buf = kt & 1;
-        if (kt + 1 < nk) gload((kt + 1) * BK);
+    auto compute = [&](int buf) {
         const int8_t* s = smem + buf * (BM + BN) * SA;
 #pragma unroll
         for (int ks = 0; ks < BK / 64; ks++) {
@@ -224,204 +242,292 @@ __global__ __launch_bounds__(256) void gemm_i8_tiled(GemmArgs a) {
 #pragma unroll
                 for (int j = 0; j < FN; j++) acc[i][j] = mfma_i8(af[i], bf[j], acc[i][j]);
         }
-        if (kt + 1 < nk) lstore(buf ^ 1);
+    };
+
+    const int nfull = K / BK;            // slabs read without masks
+    const int nk = nfull + (K % BK ? 1 : 0);
+    if (nfull > 0) gload(0);
+    else gload_tail(0);
+    lstore(0);
+    if (nk > 1) {
+        if (1 < nfull) gload(BK);
+        else gload_tail(BK);
+    }
+    __syncthreads();
+
+    for (int kt = 0; kt < nk; kt++) {
+        const int buf = kt & 1;
+        compute(buf);
+        if (kt + 1 < nk) {
+            lstore(buf ^ 1);  // slab kt+1, loaded during the previous compute
+            if (kt + 2 < nfull) gload((kt + 2) * BK);
+            else if (kt + 2 < nk) gload_tail((kt + 2) * BK);
+        }
         __syncthreads();
     }
 
-    // epilogue straight from the accumulator layout
-    const int mb = m0 + wm * TM + 4 * (lane >> 4);
-    const int nb = n0 + wn * TN + (lane & 15);
+    // Epilogue: per 16-row strip, each wave stages its 16 x TN results in LDS
+    // (the MFMA layout holds 4 rows of one column per lane), then writes whole
+    // row segments as 16-byte stores.
+    float* stage = reinterpret_cast<float*>(smem) + wave * 16 * LDW;
+    const int g4 = 4 * (lane >> 4), c16 = lane & 15;
+    constexpr int LPR = TN / 4;         // lanes per staged row
+    constexpr int RPI = 64 / LPR;       // rows per store instruction
+    const int mw = m0 + wm * TM, nw = n0 + wn * TN;
+    const bool vec = (a.acc32 ? (a.N % 4 == 0) : (a.ldo % 4 == 0)) && nw + TN <= a.N;
 #pragma unroll
-    for (int i = 0; i < FM; i++)
+    for (int i = 0; i < FM; i++) {
 #pragma unroll
         for (int j = 0; j < FN; j++) {
-            const int n = nb + j * 16;
-            if (n >= a.N) continue;
+            const int n = nw + j * 16 + c16;
+            const int nc = n < a.N ? n : a.N - 1;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int m = mb + i * 16 + r;
-                if (m < a.M) store_out(a, m, n, acc[i][j][r]);
+                const int m = mw + i * 16 + g4 + r;
+                const int mc = m < a.M ? m : a.M - 1;
+                const int av = acc[i][j][r];
+                stage[(g4 + r) * LDW + j * 16 + c16] =
+                    a.acc32 ? __int_as_float(av) : epi_value(a, mc, nc, av);
             }
         }
+        __syncthreads();
+#pragma unroll
+        for (int rr = 0; rr < 16; rr += RPI) {
+            const int row = rr + lane / LPR, col = (lane % LPR) * 4;
+            const int m = mw + i * 16 + row;
+            if (m < a.M) {
+                const float4 v = *reinterpret_cast<const float4*>(stage + row * LDW + col);
+                const int n = nw + col;
+                if (a.acc32) {
+                    int32_t* o = a.acc32 + (size_t)m * a.N + n;
+                    if (vec) {
+                        *reinterpret_cast<int4*>(o) = make_int4(__float_as_int(v.x), __float_as_int(v.y),
+                                                                __float_as_int(v.z), __float_as_int(v.w));
+                    } else {
+                        const float e[4] = {v.x, v.y, v.z, v.w};
+                        for (int q = 0; q < 4; q++)
+                            if (n + q < a.N) o[q] = __float_as_int(e[q]);
+                    }
+                } else {
+                    float* o = a.out + (size_t)m * a.ldo + n;
+                    if (vec) {
+                        float4 w = v;
+                        if (a.accumulate) {
+                            const float4 old = *reinterpret_cast<const float4*>(o);
+                            w = make_float4(old.x + v.x, old.y + v.y, old.z + v.z, old.w + v.w);
+                        }
+                        *reinterpret_cast<float4*>(o) = w;
+                    } else {
+                        const float e[4] = {v.x, v.y, v.z, v.w};
+                        for (int q = 0; q < 4; q++)
+                            if (n + q < a.N) o[q] = a.accumulate ? o[q] + e[q] : e[q];
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
 }
 
 // ---------------------------------------------------------------- skinny --
 
-template <int FM, int FN, int WAVES, bool ALIGNED>
-__global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a, int ksplit,
-                                                             int32_t* ws, int32_t* counters) {
-    constexpr int TM = FM * 16, TN = FN * 16;
-    __shared__ int32_t red[TM * TN];
+template <int FM, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
+    constexpr int TM = FM * 16;
+    __shared__ int32_t red[TM * 16];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int n0 = blockIdx.x * TN;
-    const int split = blockIdx.y;
+    const int n0 = blockIdx.x * 16;
     const int K = a.K;
-
-    for (int i = tid; i < TM * TN; i += WAVES * 64) red[i] = 0;
-
-    // k-steps of 64 bytes owned by this block, then by this wave
-    const int steps = (K + 63) / 64;
-    const int bs0 = (int)((long)steps * split / ksplit), bs1 = (int)((long)steps * (split + 1) / ksplit);
-    const int ws0 = bs0 + (int)((long)(bs1 - bs0) * wave / WAVES);
-    const int ws1 = bs0 + (int)((long)(bs1 - bs0) * (wave + 1) / WAVES);
+    for (int i = tid; i < TM * 16; i += WAVES * 64) red[i] = 0;
 
     const int r16 = lane & 15, kq = (lane >> 4) * 16;
     const int8_t* arow[FM];
-    bool aok[FM];
 #pragma unroll
     for (int i = 0; i < FM; i++) {
-        aok[i] = i * 16 + r16 < a.M;
-        arow[i] = a.A + (size_t)(aok[i] ? i * 16 + r16 : 0) * a.lda;
+        const int m = i * 16 + r16 < a.M ? i * 16 + r16 : a.M - 1;
+        arow[i] = a.A + (size_t)m * a.lda + kq;
     }
-    const int8_t* brow[FN];
-    bool bok[FN];
+    const int n = n0 + r16 < a.N ? n0 + r16 : a.N - 1;
+    const int8_t* brow = a.B + (size_t)n * a.ldb + kq;
+
+    v4i acc[FM];
 #pragma unroll
-    for (int j = 0; j < FN; j++) {
-        bok[j] = n0 + j * 16 + r16 < a.N;
-        brow[j] = a.B + (size_t)(bok[j] ? n0 + j * 16 + r16 : 0) * a.ldb;
+    for (int i = 0; i < FM; i++) acc[i] = v4i{0, 0, 0, 0};
+
+    const int full = K / 64;  // 64-byte steps read without masks
+    int s = wave;
+    for (; s + WAVES < full; s += 2 * WAVES) {
+        const v4i b0 = *reinterpret_cast<const v4i*>(brow + s * 64);
+        const v4i b1 = *reinterpret_cast<const v4i*>(brow + (s + WAVES) * 64);
+        v4i a0[FM], a1[FM];
+#pragma unroll
+        for (int i = 0; i < FM; i++) {
+            a0[i] = *reinterpret_cast<const v4i*>(arow[i] + s * 64);
+            a1[i] = *reinterpret_cast<const v4i*>(arow[i] + (s + WAVES) * 64);
+        }
+#pragma unroll
+        for (int i = 0; i < FM; i++) acc[i] = mfma_i8(a0[i], b0, acc[i]);
+#pragma unroll
+        for (int i = 0; i < FM; i++) acc[i] = mfma_i8(a1[i], b1, acc[i]);
     }
-
-    v4i acc[FM][FN];
-#pragma unroll
-    for (int i = 0; i < FM; i++)
-#pragma unroll
-        for (int j = 0; j < FN; j++) acc[i][j] = v4i{0, 0, 0, 0};
-
-    for (int s = ws0; s < ws1; s++) {
-        const int k = s * 64 + kq;
-        v4i bf[FN], af[FM];
-#pragma unroll
-        for (int j = 0; j < FN; j++)
-            bf[j] = bok[j] ? load_chunk<ALIGNED>(brow[j], k, K) : v4i{0, 0, 0, 0};
+    for (; s < full; s += WAVES) {
+        const v4i b0 = *reinterpret_cast<const v4i*>(brow + s * 64);
 #pragma unroll
         for (int i = 0; i < FM; i++)
-            af[i] = aok[i] ? load_chunk<ALIGNED>(arow[i], k, K) : v4i{0, 0, 0, 0};
+            acc[i] = mfma_i8(*reinterpret_cast<const v4i*>(arow[i] + s * 64), b0, acc[i]);
+    }
+    if (K % 64 && wave == full % WAVES) {
+        const int k = full * 64 + kq;
+        const v4i b0 = load_chunk<true>(brow - kq, k, K);
 #pragma unroll
-        for (int i = 0; i < FM; i++)
-#pragma unroll
-            for (int j = 0; j < FN; j++) acc[i][j] = mfma_i8(af[i], bf[j], acc[i][j]);
+        for (int i = 0; i < FM; i++) acc[i] = mfma_i8(load_chunk<true>(arow[i] - kq, k, K), b0, acc[i]);
     }
 
     __syncthreads();
-    // exact int32 reduction of the waves' partials
 #pragma unroll
     for (int i = 0; i < FM; i++)
 #pragma unroll
-        for (int j = 0; j < FN; j++)
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int mm = i * 16 + 4 * (lane >> 4) + r;
-                const int nn = j * 16 + r16;
-                if (ws0 < ws1) atomicAdd(&red[mm * TN + nn], acc[i][j][r]);
-            }
+        for (int r = 0; r < 4; r++) atomicAdd(&red[(i * 16 + 4 * (lane >> 4) + r) * 16 + r16], acc[i][r]);
     __syncthreads();
 
-    if (ksplit > 1) {
-        // cross-block split: add this block's slab into the global workspace,
-        // then the last block to arrive for this slab finishes it.
-        for (int e = tid; e < TM * TN; e += WAVES * 64) {
-            const int mm = e / TN, nn = e % TN;
-            if (mm < a.M && n0 + nn < a.N) atomicAdd(&ws[(size_t)mm * a.N + n0 + nn], red[e]);
-        }
-        __threadfence();
+    for (int e = tid; e < TM * 16; e += WAVES * 64) {
+        const int mm = e >> 4, nn = n0 + (e & 15);
+        if (mm < a.M && nn < a.N) store_out(a, mm, nn, red[e]);
+    }
+}
+
+// --------------------------------------------------------------- generic --
+
+__global__ __launch_bounds__(256) void gemm_i8_generic(GemmArgs a) {
+    constexpr int BM = 64, BN = 64, BK = 64, SA = BK + 16, TM = 32, TN = 32;
+    __shared__ __attribute__((aligned(16))) int8_t smem[(BM + BN) * SA];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    int tm, tn;
+    tile_coords(blockIdx.x, (a.M + BM - 1) / BM, (a.N + BN - 1) / BN, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int K = a.K;
+    // one A chunk and one B chunk per thread per slab
+    const int r = tid >> 2, kc = (tid & 3) * 16;
+    const bool aok = m0 + r < a.M, bok = n0 + r < a.N;
+    const int8_t* arow = a.A + (size_t)(aok ? m0 + r : 0) * a.lda;
+    const int8_t* brow = a.B + (size_t)(bok ? n0 + r : 0) * a.ldb;
+
+    v4i acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = v4i{0, 0, 0, 0};
+
+    for (int k0 = 0; k0 < K; k0 += BK) {
+        const v4i va = aok ? load_chunk<false>(arow, k0 + kc, K) : v4i{0, 0, 0, 0};
+        const v4i vb = bok ? load_chunk<false>(brow, k0 + kc, K) : v4i{0, 0, 0, 0};
         __syncthreads();
-        __shared__ int last;
-        if (tid == 0) last = atomicAdd(&counters[blockIdx.x], 1) == ksplit - 1;
+        *reinterpret_cast<v4i*>(smem + r * SA + kc) = va;
+        *reinterpret_cast<v4i*>(smem + BM * SA + r * SA + kc) = vb;
         __syncthreads();
-        if (!last) return;
-        __threadfence();
-        for (int e = tid; e < TM * TN; e += WAVES * 64) {
-            const int mm = e / TN, nn = e % TN;
-            if (mm < a.M && n0 + nn < a.N) {
-                int32_t* p = &ws[(size_t)mm * a.N + n0 + nn];
-                red[e] = atomicExch(p, 0);  // read the sum, leave the workspace zeroed
+        v4i af[2], bf[2];
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+            af[i] = *reinterpret_cast<const v4i*>(smem + (wm * TM + i * 16 + (lane & 15)) * SA + (lane >> 4) * 16);
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            bf[j] = *reinterpret_cast<const v4i*>(smem + BM * SA + (wn * TN + j * 16 + (lane & 15)) * SA +
+                                                  (lane >> 4) * 16);
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) acc[i][j] = mfma_i8(af[i], bf[j], acc[i][j]);
+    }
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int n = n0 + wn * TN + j * 16 + (lane & 15);
+            if (n >= a.N) continue;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int m = m0 + wm * TM + i * 16 + 4 * (lane >> 4) + q;
+                if (m < a.M) store_out(a, m, n, acc[i][j][q]);
             }
         }
-        if (tid == 0) counters[blockIdx.x] = 0;
-        __syncthreads();
-    }
-
-    for (int e = tid; e < TM * TN; e += WAVES * 64) {
-        const int mm = e / TN, nn = e % TN;
-        if (mm < a.M && n0 + nn < a.N) store_out(a, mm, n0 + nn, red[e]);
-    }
 }
 
 // ---------------------------------------------------------------- launch --
 
-// Grow-only, zero-initialised split-K workspace on the current device. The
-// skinny kernel leaves it zeroed after every launch, so one clear suffices.
-struct SplitWorkspace {
-    int32_t* ws = nullptr;
-    int32_t* counters = nullptr;
-    size_t ws_elems = 0, n_counters = 0;
-    int device = -1;
-};
-SplitWorkspace g_split[16];
-
-void ensure_split_ws(int dev, size_t elems, size_t counters, hipStream_t st) {
-    SplitWorkspace& w = g_split[dev & 15];
-    if (w.ws_elems >= elems && w.n_counters >= counters) return;
-    VLA_HIP_CHECK(hipStreamSynchronize(st));
-    if (w.ws) VLA_HIP_CHECK(hipFree(w.ws));
-    if (w.counters) VLA_HIP_CHECK(hipFree(w.counters));
-    w.ws_elems = elems > w.ws_elems ? elems : w.ws_elems;
-    w.n_counters = counters > w.n_counters ? counters : w.n_counters;
-    VLA_HIP_CHECK(hipMalloc(&w.ws, w.ws_elems * sizeof(int32_t)));
-    VLA_HIP_CHECK(hipMalloc(&w.counters, w.n_counters * sizeof(int32_t)));
-    VLA_HIP_CHECK(hipMemset(w.ws, 0, w.ws_elems * sizeof(int32_t)));
-    VLA_HIP_CHECK(hipMemset(w.counters, 0, w.n_counters * sizeof(int32_t)));
-    VLA_HIP_CHECK(hipDeviceSynchronize());
-}
-
-template <int BM, int BN, int BK, int WM, int WN>
-void run_tiled(const GemmArgs& a, bool al, hipStream_t st) {
-    const int blocks = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-    if (al)
-        gemm_i8_tiled<BM, BN, BK, WM, WN, true><<<blocks, 256, 0, st>>>(a);
-    else
-        gemm_i8_tiled<BM, BN, BK, WM, WN, false><<<blocks, 256, 0, st>>>(a);
-    VLA_LAUNCH_CHECK();
-}
-
-template <int FM, int FN, int WAVES>
-void run_skinny_fm(const GemmArgs& a, bool al, int ksplit, hipStream_t st) {
-    const int nb = (a.N + FN * 16 - 1) / (FN * 16);
-    int32_t* ws = nullptr;
-    int32_t* counters = nullptr;
-    if (ksplit > 1) {
-        int dev = 0;
-        VLA_HIP_CHECK(hipGetDevice(&dev));
-        ensure_split_ws(dev, (size_t)a.M * a.N, (size_t)nb, st);
-        ws = g_split[dev & 15].ws;
-        counters = g_split[dev & 15].counters;
-    }
-    const dim3 grid(nb, ksplit);
-    if (al)
-        gemm_i8_skinny<FM, FN, WAVES, true><<<grid, WAVES * 64, 0, st>>>(a, ksplit, ws, counters);
-    else
-        gemm_i8_skinny<FM, FN, WAVES, false><<<grid, WAVES * 64, 0, st>>>(a, ksplit, ws, counters);
-    VLA_LAUNCH_CHECK();
-}
-
-template <int FN, int WAVES>
-void run_skinny(const GemmArgs& a, bool al, int ksplit, hipStream_t st) {
-    const int fm = (a.M + 15) / 16;
-    switch (fm) {
-    case 1: run_skinny_fm<1, FN, WAVES>(a, al, ksplit, st); break;
-    case 2: run_skinny_fm<2, FN, WAVES>(a, al, ksplit, st); break;
-    case 3: run_skinny_fm<3, FN, WAVES>(a, al, ksplit, st); break;
-    case 4: run_skinny_fm<4, FN, WAVES>(a, al, ksplit, st); break;
-    case 5: run_skinny_fm<5, FN, WAVES>(a, al, ksplit, st); break;
-    case 6: run_skinny_fm<6, FN, WAVES>(a, al, ksplit, st); break;
-    case 7: run_skinny_fm<7, FN, WAVES>(a, al, ksplit, st); break;
-    default: run_skinny_fm<8, FN, WAVES>(a, al, ksplit, st); break;
-    }
-}
-
 constexpr int kCUs = 256;
+
+template <int BM, int BN, int BK>
+void run_tiled(const GemmArgs& a, hipStream_t st) {
+    using C = TileCfg<BM, BN, BK>;
+    static const bool attr = [] {
+        // above 64 KiB a kernel must opt in to the larger LDS allocation
+        if (C::LDS > 65536)
+            VLA_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_i8_tiled<BM, BN, BK>),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS));
+        return true;
+    }();
+    (void)attr;
+    const int blocks = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+    gemm_i8_tiled<BM, BN, BK><<<blocks, 256, C::LDS, st>>>(a);
+    VLA_LAUNCH_CHECK();
+}
+
+template <int WAVES>
+void run_skinny(const GemmArgs& a, hipStream_t st) {
+    const int nb = (a.N + 15) / 16;
+    switch ((a.M + 15) / 16) {
+    case 1: gemm_i8_skinny<1, WAVES><<<nb, WAVES * 64, 0, st>>>(a); break;
+    case 2: gemm_i8_skinny<2, WAVES><<<nb, WAVES * 64, 0, st>>>(a); break;
+    case 3: gemm_i8_skinny<3, WAVES><<<nb, WAVES * 64, 0, st>>>(a); break;
+    case 4: gemm_i8_skinny<4, WAVES><<<nb, WAVES * 64, 0, st>>>(a); break;
+    case 5: gemm_i8_skinny<5, WAVES><<<nb, WAVES * 64, 0, st>>>(a); break;
+    case 6: gemm_i8_skinny<6, WAVES><<<nb, WAVES * 64, 0, st>>>(a); break;
+    case 7: gemm_i8_skinny<7, WAVES><<<nb, WAVES * 64, 0, st>>>(a); break;
+    default: gemm_i8_skinny<8, WAVES><<<nb, WAVES * 64, 0, st>>>(a); break;
+    }
+    VLA_LAUNCH_CHECK();
+}
+
+// Tile of the aligned kernel: the largest that still gives every CU a tile,
+// or VLA_HIP_GEMM_TILE=<BM>x<BN>x<BK> to force one (A/B runs; the values do
+// not change, only the schedule).
+struct Tile {
+    int bm, bn, bk;
+};
+const Tile kTiles[] = {{256, 256, 64}, {256, 128, 128}, {256, 128, 64}, {128, 128, 128},
+                       {128, 128, 64}, {64, 128, 64}, {64, 64, 64}};
+
+Tile pick_tile(int M, int N) {
+    const char* env = std::getenv("VLA_HIP_GEMM_TILE");
+    if (env && *env) {
+        for (const Tile& t : kTiles) {
+            char name[32];
+            std::snprintf(name, sizeof name, "%dx%dx%d", t.bm, t.bn, t.bk);
+            if (std::strcmp(name, env) == 0) return t;
+        }
+    }
+    // 256x256 is kept for forced A/B runs only: its accumulators leave too few
+    // registers for the epilogue and it spills.
+    auto tiles = [&](int bm, int bn) { return (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
+    if (tiles(256, 128) >= kCUs) return {256, 128, 64};
+    if (tiles(128, 128) >= kCUs) return {128, 128, 64};
+    if (tiles(64, 128) >= kCUs) return {64, 128, 64};
+    return {64, 64, 64};
+}
+
+void dispatch_tile(const Tile& t, const GemmArgs& a, hipStream_t st) {
+    if (t.bm == 256 && t.bn == 256) run_tiled<256, 256, 64>(a, st);
+    else if (t.bm == 256 && t.bk == 128) run_tiled<256, 128, 128>(a, st);
+    else if (t.bm == 256) run_tiled<256, 128, 64>(a, st);
+    else if (t.bm == 128 && t.bk == 128) run_tiled<128, 128, 128>(a, st);
+    else if (t.bm == 128) run_tiled<128, 128, 64>(a, st);
+    else if (t.bn == 128) run_tiled<64, 128, 64>(a, st);
+    else run_tiled<64, 64, 64>(a, st);
+}
 
 }  // namespace
 
@@ -436,30 +542,22 @@ void launch_gemm_i8(const GemmArgs& a, hipStream_t st) {
     VLA_REQUIRE(a.act >= 0 && a.act <= 3, "gemm_i8: unknown activation");
     if (a.M == 0) return;
 
-    const bool al = a.lda % 16 == 0 && a.ldb % 16 == 0 && aligned(a.A, 16) && aligned(a.B, 16);
-
-    if (a.M <= 128) {
-        // one block per 16-column slab; split K across blocks until the grid
-        // covers the chip about twice (each split adds one int32 pass over the
-        // [M, slab] tile through L2 atomics)
-        const int nb = (a.N + 15) / 16;
-        const int steps = (a.K + 63) / 64;
-        int ksplit = 1;
-        while (nb * ksplit < 2 * kCUs && steps / (ksplit * 2) >= 4) ksplit *= 2;
-        run_skinny<1, 4>(a, al, ksplit, st);
+    const bool al = a.lda % 16 == 0 && a.ldb % 16 == 0 && aligned(a.A, 16) && aligned(a.B, 16) &&
+                    (a.acc32 ? aligned(a.acc32, 16) : aligned(a.out, 16));
+    if (!al) {
+        const int blocks = ((a.M + 63) / 64) * ((a.N + 63) / 64);
+        gemm_i8_generic<<<blocks, 256, 0, st>>>(a);
+        VLA_LAUNCH_CHECK();
         return;
     }
-    const long t256 = (long)((a.M + 255) / 256) * ((a.N + 127) / 128);
-    const long t128 = (long)((a.M + 127) / 128) * ((a.N + 127) / 128);
-    const long t64 = (long)((a.M + 63) / 64) * ((a.N + 127) / 128);
-    if (t256 >= kCUs)
-        run_tiled<256, 128, 64, 2, 2>(a, al, st);
-    else if (t128 >= kCUs)
-        run_tiled<128, 128, 64, 2, 2>(a, al, st);
-    else if (t64 >= kCUs)
-        run_tiled<64, 128, 64, 2, 2>(a, al, st);
-    else
-        run_tiled<64, 64, 64, 2, 2>(a, al, st);
+    if (a.M <= 128) {
+        const int steps = (a.K + 63) / 64;
+        if (steps >= 32) run_skinny<16>(a, st);
+        else if (steps >= 8) run_skinny<8>(a, st);
+        else run_skinny<4>(a, st);
+        return;
+    }
+    dispatch_tile(pick_tile(a.M, a.N), a, st);
 }
 
 }  // namespace hip
