@@ -329,6 +329,214 @@ __global__ __launch_bounds__(256) void gemm_i8_tiled(GemmArgs a) {
     }
 }
 
+// ------------------------------------------------------ direct-to-LDS --
+
+// 16 zero bytes: the source of every chunk of the last K slab that lies past
+// the (16-rounded) row length.
+__device__ __attribute__((aligned(16))) int8_t g_zero16[16] = {0};
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their max).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// XOR swizzle of the 16-byte chunks within one LDS row, so the 16 rows one
+// ds_read_b128 touches (same logical chunk) land on distinct bank groups.
+// Workgroup barrier for the LDS-DMA pipeline. __syncthreads() carries a
+// release fence that waits for every outstanding vector load (vmcnt(0)), which
+// would drain the slabs in flight; here only this wave's LDS reads must be
+// done (lgkmcnt(0)) - the slab being consumed was awaited with wait_vmcnt.
+// The empty asm statements keep the compiler from moving memory accesses
+// across the barrier.
+__device__ __forceinline__ void pipeline_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4));  // lgkmcnt(0) only
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int BK>
+__device__ __forceinline__ int swz(int r) {
+    return BK == 64 ? (r >> 1) & 3 : r & 7;
+}
+
+template <int BM, int BN, int BK, int S>
+struct LdsCfg {
+    static constexpr int TM = BM / 2, TN = BN / 2;
+    static constexpr int FM = TM / 16, FN = TN / 16;
+    static constexpr int CPR = BK / 16;
+    static constexpr int IA = BM * CPR / 256, IB = BN * CPR / 256;  // load instrs per wave per slab
+    static constexpr int LPS = IA + IB;
+    static constexpr int STAGE = (BM + BN) * BK;
+    static constexpr int LDW = TN + 4;
+    static constexpr int MAIN = S * STAGE;
+    static constexpr int EPI = 4 * 16 * LDW * 4;
+    static constexpr int LDS = MAIN > EPI ? MAIN : EPI;
+    static_assert(BM * CPR % 256 == 0 && BN * CPR % 256 == 0, "slab chunks must split evenly");
+    static_assert(S >= 2 && (S - 2) * LPS < 64, "pipeline depth");
+};
+
+template <int BM, int BN, int BK, int S>
+__global__ __launch_bounds__(256) void gemm_i8_lds(GemmArgs a) {
+    using C = LdsCfg<BM, BN, BK, S>;
+    constexpr int TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN, CPR = C::CPR;
+    constexpr int IA = C::IA, IB = C::IB, LPS = C::LPS, STAGE = C::STAGE, LDW = C::LDW;
+    extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    int tm, tn;
+    tile_coords(blockIdx.x, (a.M + BM - 1) / BM, (a.N + BN - 1) / BN, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int K16 = (a.K + 15) & ~15;
+
+    // Load slots: instruction j of this wave fills LDS chunks [64*slot, +64) of
+    // the slab, slot = j*4 + wave; lane l writes chunk 64*slot + l, which holds
+    // row q / CPR, logical chunk (q % CPR) ^ swz(row).
+    const int8_t* asrc[IA];
+    int acb[IA];
+#pragma unroll
+    for (int j = 0; j < IA; j++) {
+        const int q = (j * 4 + wave) * 64 + lane, r = q / CPR;
+        const int c = (q % CPR) ^ swz<BK>(r);
+        const int m = m0 + r < a.M ? m0 + r : a.M - 1;
+        acb[j] = c * 16;
+        asrc[j] = a.A + (size_t)m * a.lda + acb[j];
+    }
+    const int8_t* bsrc[IB];
+    int bcb[IB];
+#pragma unroll
+    for (int j = 0; j < IB; j++) {
+        const int q = (j * 4 + wave) * 64 + lane, r = q / CPR;
+        const int c = (q % CPR) ^ swz<BK>(r);
+        const int n = n0 + r < a.N ? n0 + r : a.N - 1;
+        bcb[j] = c * 16;
+        bsrc[j] = a.B + (size_t)n * a.ldb + bcb[j];
+    }
+
+    typedef __attribute__((address_space(1))) const void* gptr;
+    typedef __attribute__((address_space(3))) void* lptr;
+    auto issue = [&](int kt) {
+        const int k0 = kt * BK;
+        int8_t* st = smem + (kt % S) * STAGE;
+        const bool full = k0 + BK <= K16;
+#pragma unroll
+        for (int j = 0; j < IA; j++) {
+            const int8_t* p = full || k0 + acb[j] < K16 ? asrc[j] + k0 : g_zero16;
+            __builtin_amdgcn_global_load_lds((gptr)p, (lptr)(st + (j * 4 + wave) * 1024), 16, 0, 0);
+        }
+#pragma unroll
+        for (int j = 0; j < IB; j++) {
+            const int8_t* p = full || k0 + bcb[j] < K16 ? bsrc[j] + k0 : g_zero16;
+            __builtin_amdgcn_global_load_lds((gptr)p, (lptr)(st + BM * BK + (j * 4 + wave) * 1024), 16, 0, 0);
+        }
+    };
+
+    v4i acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) acc[i][j] = v4i{0, 0, 0, 0};
+
+    const int r16 = lane & 15, cq = lane >> 4;
+    const int sz = swz<BK>(r16);  // swz depends on the row's low bits only
+    const int arow_l = (wm * TM + r16) * BK;
+    const int brow_l = BM * BK + (wn * TN + r16) * BK;
+
+    const int nk = K16 / BK + (K16 % BK ? 1 : 0);
+#pragma unroll
+    for (int s = 0; s < S - 1; s++)
+        if (s < nk) issue(s);
+
+    for (int kt = 0; kt < nk; kt++) {
+        // slab kt has landed for this wave once at most the later slabs' loads are pending
+        const int later = nk - 1 - kt < S - 2 ? nk - 1 - kt : S - 2;
+        if (later >= S - 2) wait_vmcnt<(S - 2) * LPS>();
+        else if (S > 3 && later == 1) wait_vmcnt<(S > 3 ? LPS : 0)>();
+        else if (S > 4 && later == 2) wait_vmcnt<(S > 4 ? 2 * LPS : 0)>();
+        else wait_vmcnt<0>();
+        pipeline_barrier();  // every wave's part of slab kt is in LDS; slab kt-1 is consumed
+        if (kt + S - 1 < nk) issue(kt + S - 1);
+        const int8_t* st = smem + (kt % S) * STAGE;
+#pragma unroll
+        for (int ks = 0; ks < BK / 64; ks++) {
+            const int co = 16 * ((ks * 4 + cq) ^ sz);
+            v4i af[FM], bf[FN];
+#pragma unroll
+            for (int i = 0; i < FM; i++) af[i] = *reinterpret_cast<const v4i*>(st + arow_l + i * 16 * BK + co);
+#pragma unroll
+            for (int j = 0; j < FN; j++) bf[j] = *reinterpret_cast<const v4i*>(st + brow_l + j * 16 * BK + co);
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++) acc[i][j] = mfma_i8(af[i], bf[j], acc[i][j]);
+        }
+    }
+    __syncthreads();
+
+    // LDS-staged epilogue (as gemm_i8_tiled)
+    float* stage = reinterpret_cast<float*>(smem) + wave * 16 * LDW;
+    const int g4 = 4 * (lane >> 4), c16 = lane & 15;
+    constexpr int LPR = TN / 4, RPI = 64 / LPR;
+    const int mw = m0 + wm * TM, nw = n0 + wn * TN;
+    const bool vec = (a.acc32 ? (a.N % 4 == 0) : (a.ldo % 4 == 0)) && nw + TN <= a.N;
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+            const int n = nw + j * 16 + c16;
+            const int nc = n < a.N ? n : a.N - 1;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = mw + i * 16 + g4 + r;
+                const int mc = m < a.M ? m : a.M - 1;
+                const int av = acc[i][j][r];
+                stage[(g4 + r) * LDW + j * 16 + c16] = a.acc32 ? __int_as_float(av) : epi_value(a, mc, nc, av);
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int rr = 0; rr < 16; rr += RPI) {
+            const int row = rr + lane / LPR, col = (lane % LPR) * 4;
+            const int m = mw + i * 16 + row;
+            if (m < a.M) {
+                const float4 v = *reinterpret_cast<const float4*>(stage + row * LDW + col);
+                const int n = nw + col;
+                if (a.acc32) {
+                    int32_t* o = a.acc32 + (size_t)m * a.N + n;
+                    if (vec) {
+                        *reinterpret_cast<int4*>(o) = make_int4(__float_as_int(v.x), __float_as_int(v.y),
+                                                                __float_as_int(v.z), __float_as_int(v.w));
+                    } else {
+                        const float e[4] = {v.x, v.y, v.z, v.w};
+                        for (int q = 0; q < 4; q++)
+                            if (n + q < a.N) o[q] = __float_as_int(e[q]);
+                    }
+                } else {
+                    float* o = a.out + (size_t)m * a.ldo + n;
+                    if (vec) {
+                        float4 w = v;
+                        if (a.accumulate) {
+                            const float4 old = *reinterpret_cast<const float4*>(o);
+                            w = make_float4(old.x + v.x, old.y + v.y, old.z + v.z, old.w + v.w);
+                        }
+                        *reinterpret_cast<float4*>(o) = w;
+                    } else {
+                        const float e[4] = {v.x, v.y, v.z, v.w};
+                        for (int q = 0; q < 4; q++)
+                            if (n + q < a.N) o[q] = a.accumulate ? o[q] + e[q] : e[q];
+                    }
+                }
+            }
+        }
+        __syncthreads();
+    }
+}
+
 // ---------------------------------------------------------------- skinny --
 
 template <int FM, int WAVES>
@@ -476,6 +684,21 @@ void run_tiled(const GemmArgs& a, hipStream_t st) {
     VLA_LAUNCH_CHECK();
 }
 
+template <int BM, int BN, int BK, int S>
+void run_lds(const GemmArgs& a, hipStream_t st) {
+    using C = LdsCfg<BM, BN, BK, S>;
+    static const bool attr = [] {
+        if (C::LDS > 65536)
+            VLA_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_i8_lds<BM, BN, BK, S>),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS));
+        return true;
+    }();
+    (void)attr;
+    const int blocks = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
+    gemm_i8_lds<BM, BN, BK, S><<<blocks, 256, C::LDS, st>>>(a);
+    VLA_LAUNCH_CHECK();
+}
+
 template <int WAVES>
 void run_skinny(const GemmArgs& a, hipStream_t st) {
     const int nb = (a.N + 15) / 16;
@@ -495,31 +718,47 @@ void run_skinny(const GemmArgs& a, hipStream_t st) {
 // Tile of the aligned kernel: the largest that still gives every CU a tile,
 // or VLA_HIP_GEMM_TILE=<BM>x<BN>x<BK> to force one (A/B runs; the values do
 // not change, only the schedule).
+// stages == 0: the register-staged gemm_i8_tiled; > 0: gemm_i8_lds with that
+// many LDS stages (named "<BM>x<BN>x<BK>s<S>").
 struct Tile {
-    int bm, bn, bk;
+    int bm, bn, bk, stages;
 };
-const Tile kTiles[] = {{256, 256, 64}, {256, 128, 128}, {256, 128, 64}, {128, 128, 128},
-                       {128, 128, 64}, {64, 128, 64}, {64, 64, 64}};
+const Tile kTiles[] = {{256, 256, 64, 0}, {256, 128, 128, 0}, {256, 128, 64, 0}, {128, 128, 128, 0},
+                       {128, 128, 64, 0},  {64, 128, 64, 0},   {64, 64, 64, 0},   {128, 128, 128, 4},
+                       {128, 128, 64, 4},  {256, 128, 64, 4},  {256, 128, 128, 3}, {64, 128, 64, 4},
+                       {128, 128, 128, 3}, {256, 256, 64, 3}};
 
 Tile pick_tile(int M, int N) {
     const char* env = std::getenv("VLA_HIP_GEMM_TILE");
     if (env && *env) {
         for (const Tile& t : kTiles) {
             char name[32];
-            std::snprintf(name, sizeof name, "%dx%dx%d", t.bm, t.bn, t.bk);
+            if (t.stages)
+                std::snprintf(name, sizeof name, "%dx%dx%ds%d", t.bm, t.bn, t.bk, t.stages);
+            else
+                std::snprintf(name, sizeof name, "%dx%dx%d", t.bm, t.bn, t.bk);
             if (std::strcmp(name, env) == 0) return t;
         }
     }
     // 256x256 is kept for forced A/B runs only: its accumulators leave too few
     // registers for the epilogue and it spills.
     auto tiles = [&](int bm, int bn) { return (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-    if (tiles(256, 128) >= kCUs) return {256, 128, 64};
-    if (tiles(128, 128) >= kCUs) return {128, 128, 64};
-    if (tiles(64, 128) >= kCUs) return {64, 128, 64};
-    return {64, 64, 64};
+    if (tiles(128, 128) >= kCUs) return {128, 128, 64, 0};
+    if (tiles(64, 128) >= kCUs) return {64, 128, 64, 0};
+    return {64, 64, 64, 0};
 }
 
 void dispatch_tile(const Tile& t, const GemmArgs& a, hipStream_t st) {
+    if (t.stages) {
+        if (t.bm == 128 && t.bk == 128 && t.stages == 4) run_lds<128, 128, 128, 4>(a, st);
+        else if (t.bm == 128 && t.bk == 128) run_lds<128, 128, 128, 3>(a, st);
+        else if (t.bm == 128) run_lds<128, 128, 64, 4>(a, st);
+        else if (t.bm == 256 && t.bn == 256) run_lds<256, 256, 64, 3>(a, st);
+        else if (t.bm == 256 && t.bk == 128) run_lds<256, 128, 128, 3>(a, st);
+        else if (t.bm == 256) run_lds<256, 128, 64, 4>(a, st);
+        else run_lds<64, 128, 64, 4>(a, st);
+        return;
+    }
     if (t.bm == 256 && t.bn == 256) run_tiled<256, 256, 64>(a, st);
     else if (t.bm == 256 && t.bk == 128) run_tiled<256, 128, 128>(a, st);
     else if (t.bm == 256) run_tiled<256, 128, 64>(a, st);
