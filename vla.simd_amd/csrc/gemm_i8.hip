@@ -728,7 +728,7 @@ const Tile kTiles[] = {{256, 256, 64, 0}, {256, 128, 128, 0}, {256, 128, 64, 0},
                        {128, 128, 64, 4},  {256, 128, 64, 4},  {256, 128, 128, 3}, {64, 128, 64, 4},
                        {128, 128, 128, 3}, {256, 256, 64, 3}};
 
-Tile pick_tile(int M, int N) {
+Tile pick_tile(int M, int N, int K) {
     const char* env = std::getenv("VLA_HIP_GEMM_TILE");
     if (env && *env) {
         for (const Tile& t : kTiles) {
@@ -740,11 +740,15 @@ Tile pick_tile(int M, int N) {
             if (std::strcmp(name, env) == 0) return t;
         }
     }
-    // 256x256 is kept for forced A/B runs only: its accumulators leave too few
-    // registers for the epilogue and it spills.
+    // Measured on MI355X over the BASELINE sweep (bench.py, forced tiles):
+    // short K (<= 1024) is dominated by the fp32 output write and wants many
+    // small register-staged tiles in flight; long K wants the LDS-DMA pipeline,
+    // 128x128 when that still gives every CU a tile. The 256-wide tiles lose
+    // occupancy (256x256 spills) and are kept for forced A/B runs only.
     auto tiles = [&](int bm, int bn) { return (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-    if (tiles(128, 128) >= kCUs) return {128, 128, 64, 0};
-    if (tiles(64, 128) >= kCUs) return {64, 128, 64, 0};
+    if (K <= 1024) return tiles(64, 128) >= kCUs ? Tile{64, 128, 64, 0} : Tile{64, 64, 64, 0};
+    if (tiles(128, 128) >= kCUs) return {128, 128, 64, 4};
+    if (tiles(64, 128) >= kCUs) return {64, 128, 64, 4};
     return {64, 64, 64, 0};
 }
 
@@ -796,7 +800,7 @@ void launch_gemm_i8(const GemmArgs& a, hipStream_t st) {
         else run_skinny<4>(a, st);
         return;
     }
-    dispatch_tile(pick_tile(a.M, a.N), a, st);
+    dispatch_tile(pick_tile(a.M, a.N, a.K), a, st);
 }
 
 }  // namespace hip

@@ -35,9 +35,10 @@ def _fnv1a64(name: str) -> int:
     return h
 
 
-def _splitmix64(seed: int, n: int) -> np.ndarray:
+def _splitmix64(seed: int, n: int, start: int = 0) -> np.ndarray:
+    """Outputs start+1 .. start+n of the splitmix64 stream seeded with seed."""
     with np.errstate(over="ignore"):
-        i = np.arange(1, n + 1, dtype=np.uint64)
+        i = np.arange(start + 1, start + n + 1, dtype=np.uint64)
         z = np.uint64(seed & _M64) + i * np.uint64(0x9E3779B97F4A7C15)
         z = (z ^ (z >> np.uint64(30))) * np.uint64(0xBF58476D1CE4E5B9)
         z = (z ^ (z >> np.uint64(27))) * np.uint64(0x94D049BB133111EB)
@@ -62,50 +63,78 @@ _S8 = np.array([0.3826834323650898, 0.9238795325112867, 0.9238795325112867, 0.38
                 -0.38268343236508967, -0.9238795325112864, -0.9238795325112867, -0.38268343236509045])
 
 
+_INV_ODD = [1.0 / k for k in range(23, 0, -2)]  # 1/23, 1/21, ..., 1/1
+_COS_C = []  # (-1)^j / (2j)!, j = 9 .. 0 (Horner order)
+_SIN_C = []  # (-1)^j / (2j+1)!, j = 9 .. 0
+for _j in range(9, -1, -1):
+    _f2, _f3 = 1.0, 1.0
+    for _t in range(1, 2 * _j + 1):
+        _f2 *= _t
+    _f3 = _f2 * (2 * _j + 1)
+    _COS_C.append((-1.0) ** _j / _f2)
+    _SIN_C.append((-1.0) ** _j / _f3)
+
+
 def _ln(u: np.ndarray) -> np.ndarray:
     """ln(u), u > 0, from exact frexp and the series ln m = 2 atanh((m-1)/(m+1))."""
     m, e = np.frexp(u)  # u = m * 2^e, m in [0.5, 1)
     small = m < 0.7071067811865476
-    m = np.where(small, m * 2.0, m)
-    e = np.where(small, e - 1, e).astype(np.float64)
+    m[small] *= 2.0
+    e = (e - small).astype(np.float64)
     s = (m - 1.0) / (m + 1.0)
     s2 = s * s
-    acc = np.zeros_like(s)
-    for k in range(23, 0, -2):  # 1/23 .. 1/1
-        acc = acc * s2 + 1.0 / k
-    return 2.0 * s * acc + e * _LN2
+    acc = np.full_like(s, _INV_ODD[0])
+    for c in _INV_ODD[1:]:
+        acc *= s2
+        acc += c
+    acc *= s
+    acc *= 2.0
+    e *= _LN2
+    acc += e
+    return acc
 
 
 def _sincos_turns(t: np.ndarray):
     """(cos, sin) of 2*pi*t for t in [0, 1)."""
     x = t * 8.0
     k = np.floor(x)
-    a = (x - k - 0.5) * (np.pi / 4.0)  # [-pi/8, pi/8)
+    a = x - k
+    a -= 0.5
+    a *= np.pi / 4.0  # [-pi/8, pi/8)
     a2 = a * a
-    c = np.ones_like(a)
-    sn = np.ones_like(a)
-    tc, ts = np.ones_like(a), np.ones_like(a)
-    for j in range(1, 10):
-        tc = tc * (-a2) / ((2 * j - 1) * (2 * j))
-        ts = ts * (-a2) / ((2 * j) * (2 * j + 1))
-        c = c + tc
-        sn = sn + ts
-    sn = sn * a
+    c = np.full_like(a, _COS_C[0])
+    sn = np.full_like(a, _SIN_C[0])
+    for cc, sc in zip(_COS_C[1:], _SIN_C[1:]):
+        c *= a2
+        c += cc
+        sn *= a2
+        sn += sc
+    sn *= a
     ki = np.minimum(k.astype(np.int64), 7)
     C, S = _C8[ki], _S8[ki]
     return C * c - S * sn, S * c + C * sn
 
 
 def normal(name: str, shape, std=1.0, seed: int = BASE_SEED) -> np.ndarray:
+    """Draw 2i and 2i+1 of the stream form pair i; pair i gives element i
+    (cos branch) and element m + i (sin branch), m = ceil(n/2). Computed in
+    cache-sized chunks of pairs; every step is elementwise, so chunking does
+    not change a value."""
     n = int(np.prod(shape))
     m = (n + 1) // 2
-    z = _splitmix64(_seed(name, seed), 2 * m) >> np.uint64(11)
-    u1 = (z[0::2].astype(np.float64) + 1.0) * (1.0 / (1 << 53))  # (0, 1]
-    u2 = z[1::2].astype(np.float64) * (1.0 / (1 << 53))
-    r = np.sqrt(-2.0 * _ln(u1))
-    cs, sn = _sincos_turns(u2)
-    v = np.concatenate([r * cs, r * sn])[:n]
-    return (std * v).astype(np.float32).reshape(shape)
+    sd = _seed(name, seed)
+    v = np.empty(2 * m, np.float64)
+    CH = 1 << 16
+    for p0 in range(0, m, CH):
+        p1 = min(m, p0 + CH)
+        z = _splitmix64(sd, 2 * (p1 - p0), 2 * p0) >> np.uint64(11)
+        u1 = (z[0::2].astype(np.float64) + 1.0) * (1.0 / (1 << 53))  # (0, 1]
+        u2 = z[1::2].astype(np.float64) * (1.0 / (1 << 53))
+        r = np.sqrt(-2.0 * _ln(u1))
+        cs, sn = _sincos_turns(u2)
+        v[p0:p1] = r * cs
+        v[m + p0:m + p1] = r * sn
+    return (std * v[:n]).astype(np.float32).reshape(shape)
 
 
 def int8_uniform(name: str, shape, seed: int = BASE_SEED) -> np.ndarray:
