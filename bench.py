@@ -134,6 +134,21 @@ def time_graph(torch, g, replays, stream_obj):
     return start.elapsed_time(end) * 1e3 / replays
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "gemm_i8_8192x4096x4096_traffic.txt")
+
+
+def profiled_traffic():
+    """HBM bytes per launch of the dominant GEMM, from the two rocprofv3 --pmc
+    passes (FETCH_SIZE, WRITE_SIZE, calibrated) summarised in TRAFFIC_PROFILE."""
+    try:
+        for line in open(TRAFFIC_PROFILE):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(synth, budget_s=15.0):
     """The reference's dense_linear_i8 on this host (oracle/_ref build)."""
     from oracle import bindings as ob
@@ -286,9 +301,13 @@ def main():
     if dom_us is not None:
         ach = 2.0 * 8192 * 4096 * 4096 / dom_us / 1e6
         roofline = {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_INT8_TOPS,
-                    "unit": "TFLOP/s", "frac": round(ach / PEAK_INT8_TOPS, 4), "traffic": None,
-                    "kernel": "gemm_i8_tiled 8192x4096x4096 (int8 ops = 2*M*N*K per launch)",
-                    "avg_launch_us": round(dom_us, 3)}
+                    "unit": "TFLOP/s", "frac": round(ach / PEAK_INT8_TOPS, 4),
+                    "traffic": profiled_traffic(),
+                    "kernel": "int8 GEMM launch M=8192 K=4096 N=4096 (int8 ops = 2*M*N*K per "
+                              "launch; unit TFLOP/s counts int8 ops)",
+                    "avg_launch_us": round(dom_us, 3),
+                    "algorithmic_bytes": gemm_bytes(*dominant),
+                    "traffic_source": "profiles/gemm_i8_8192x4096x4096_traffic.txt"}
 
     cpu = None if args.no_cpu else cpu_baseline(synth)
 
