@@ -222,9 +222,8 @@ def main():
     stream = stream_obj.cuda_stream
 
     shapes_spec = [(M, K, N) for (K, N) in synth.SWEEP_KN for M in synth.SWEEP_M]
-    if args.shapes:
-        want = {tuple(int(v) for v in s.split("x")) for s in args.shapes.split(",")}
-        shapes_spec = [s for s in shapes_spec if s in want]
+    if args.shapes:  # any MxKxN list (A/B and scaling runs); the default is the sweep
+        shapes_spec = [tuple(int(v) for v in s.split("x")) for s in args.shapes.split(",")]
     dominant = (8192, 4096, 4096)
 
     if args.profile_only:

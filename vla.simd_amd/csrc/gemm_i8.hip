@@ -121,6 +121,122 @@ __device__ __forceinline__ void store_out(const GemmArgs& a, int m, int n, int a
     *o = v;
 }
 
+// Per-lane epilogue operands: weight scale and bias of the lane's columns,
+// loaded before the main loop so their latency hides under it.
+template <int FN>
+struct EpiRegs {
+    float ws[FN], b[FN];
+    __device__ __forceinline__ void load(const GemmArgs& a, int nw, int lane) {
+        if (a.acc32) return;
+        const int c16 = lane & 15;
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+            const int n = nw + j * 16 + c16;
+            const int nc = n < a.N ? n : a.N - 1;
+            ws[j] = a.wscale[nc];
+            b[j] = a.bias ? a.bias[nc] : 0.0f;
+        }
+    }
+};
+
+// Activation scales of the 4 rows a lane holds in 16-row strip m16.
+__device__ __forceinline__ void load_row_scales(const GemmArgs& a, int m16, int lane, float (&sa)[4]) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const int m = m16 + 4 * (lane >> 4) + r;
+        sa[r] = a.acc32 ? 0.0f : a.ascale[m < a.M ? m : a.M - 1];
+    }
+}
+
+// Orders this wave's LDS accesses: its earlier writes are complete before its
+// later reads (other lanes' values), with no block barrier.
+__device__ __forceinline__ void wave_lds_sync() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4));  // lgkmcnt(0) only
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+}
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// Epilogue of one wave's TM x TN accumulator tile. Per 16-row strip the wave
+// stages its results in its own LDS region (the MFMA layout holds 4 rows of
+// one column per lane), then writes whole row segments as 16-byte stores;
+// plain stores are non-temporal (the output is not re-read by this kernel).
+template <int TM, int TN, int FM, int FN>
+__device__ __forceinline__ void epilogue(const GemmArgs& a, const v4i (&acc)[FM][FN],
+                                         const EpiRegs<FN>& e, float* stage, int lane, int mw,
+                                         int nw) {
+    constexpr int LDW = TN + 4;
+    constexpr int LPR = TN / 4;    // lanes per staged row
+    constexpr int RPI = 64 / LPR;  // rows per store instruction
+    const int g4 = 4 * (lane >> 4), c16 = lane & 15;
+    const bool vec = (a.acc32 ? (a.N % 4 == 0) : (a.ldo % 4 == 0)) && nw + TN <= a.N;
+    float sa[4], sn[4];
+    load_row_scales(a, mw, lane, sa);
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+        if (i + 1 < FM) load_row_scales(a, mw + (i + 1) * 16, lane, sn);  // next strip's
+#pragma unroll
+        for (int j = 0; j < FN; j++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int av = acc[i][j][r];
+                float v;
+                if (a.acc32) {
+                    v = __int_as_float(av);
+                } else {
+                    const float p = (float)av * e.ws[j];
+                    v = fmaf(p, sa[r], e.b[j]);
+                    switch (a.act) {
+                    case 1: v = act_relu(v); break;
+                    case 2: v = act_gelu_tanh(v); break;
+                    case 3: v = act_gelu_erf(v); break;
+                    default: break;
+                    }
+                }
+                stage[(g4 + r) * LDW + j * 16 + c16] = v;
+            }
+        wave_lds_sync();
+#pragma unroll
+        for (int rr = 0; rr < 16; rr += RPI) {
+            const int row = rr + lane / LPR, col = (lane % LPR) * 4;
+            const int m = mw + i * 16 + row;
+            if (m < a.M) {
+                const v4f v = *reinterpret_cast<const v4f*>(stage + row * LDW + col);
+                const int n = nw + col;
+                if (a.acc32) {
+                    int32_t* o = a.acc32 + (size_t)m * a.N + n;
+                    if (vec) {
+                        *reinterpret_cast<int4*>(o) = make_int4(__float_as_int(v.x), __float_as_int(v.y),
+                                                                __float_as_int(v.z), __float_as_int(v.w));
+                    } else {
+                        for (int q = 0; q < 4; q++)
+                            if (n + q < a.N) o[q] = __float_as_int(v[q]);
+                    }
+                } else {
+                    float* o = a.out + (size_t)m * a.ldo + n;
+                    if (vec) {
+                        if (a.accumulate) {
+                            const v4f old = *reinterpret_cast<const v4f*>(o);
+                            *reinterpret_cast<v4f*>(o) = old + v;
+                        } else {
+                            __builtin_nontemporal_store(v, reinterpret_cast<v4f*>(o));
+                        }
+                    } else {
+                        for (int q = 0; q < 4; q++)
+                            if (n + q < a.N) o[q] = a.accumulate ? o[q] + v[q] : v[q];
+                    }
+                }
+            }
+        }
+        wave_lds_sync();
+        if (i + 1 < FM)
+#pragma unroll
+            for (int r = 0; r < 4; r++) sa[r] = sn[r];
+    }
+}
+
 // XCD-aware tile order (see the file comment).
 __device__ __forceinline__ void tile_coords(int bid, int nbm, int nbn, int& tm, int& tn) {
     const int total = nbm * nbn;
@@ -244,6 +360,9 @@ __global__ __launch_bounds__(256) void gemm_i8_tiled(GemmArgs a) {
         }
     };
 
+    EpiRegs<FN> epi;
+    epi.load(a, n0 + wn * TN, lane);
+
     const int nfull = K / BK;            // slabs read without masks
     const int nk = nfull + (K % BK ? 1 : 0);
     if (nfull > 0) gload(0);
@@ -266,67 +385,8 @@ __global__ __launch_bounds__(256) void gemm_i8_tiled(GemmArgs a) {
         __syncthreads();
     }
 
-    // Epilogue: per 16-row strip, each wave stages its 16 x TN results in LDS
-    // (the MFMA layout holds 4 rows of one column per lane), then writes whole
-    // row segments as 16-byte stores.
-    float* stage = reinterpret_cast<float*>(smem) + wave * 16 * LDW;
-    const int g4 = 4 * (lane >> 4), c16 = lane & 15;
-    constexpr int LPR = TN / 4;         // lanes per staged row
-    constexpr int RPI = 64 / LPR;       // rows per store instruction
-    const int mw = m0 + wm * TM, nw = n0 + wn * TN;
-    const bool vec = (a.acc32 ? (a.N % 4 == 0) : (a.ldo % 4 == 0)) && nw + TN <= a.N;
-#pragma unroll
-    for (int i = 0; i < FM; i++) {
-#pragma unroll
-        for (int j = 0; j < FN; j++) {
-            const int n = nw + j * 16 + c16;
-            const int nc = n < a.N ? n : a.N - 1;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int m = mw + i * 16 + g4 + r;
-                const int mc = m < a.M ? m : a.M - 1;
-                const int av = acc[i][j][r];
-                stage[(g4 + r) * LDW + j * 16 + c16] =
-                    a.acc32 ? __int_as_float(av) : epi_value(a, mc, nc, av);
-            }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int rr = 0; rr < 16; rr += RPI) {
-            const int row = rr + lane / LPR, col = (lane % LPR) * 4;
-            const int m = mw + i * 16 + row;
-            if (m < a.M) {
-                const float4 v = *reinterpret_cast<const float4*>(stage + row * LDW + col);
-                const int n = nw + col;
-                if (a.acc32) {
-                    int32_t* o = a.acc32 + (size_t)m * a.N + n;
-                    if (vec) {
-                        *reinterpret_cast<int4*>(o) = make_int4(__float_as_int(v.x), __float_as_int(v.y),
-                                                                __float_as_int(v.z), __float_as_int(v.w));
-                    } else {
-                        const float e[4] = {v.x, v.y, v.z, v.w};
-                        for (int q = 0; q < 4; q++)
-                            if (n + q < a.N) o[q] = __float_as_int(e[q]);
-                    }
-                } else {
-                    float* o = a.out + (size_t)m * a.ldo + n;
-                    if (vec) {
-                        float4 w = v;
-                        if (a.accumulate) {
-                            const float4 old = *reinterpret_cast<const float4*>(o);
-                            w = make_float4(old.x + v.x, old.y + v.y, old.z + v.z, old.w + v.w);
-                        }
-                        *reinterpret_cast<float4*>(o) = w;
-                    } else {
-                        const float e[4] = {v.x, v.y, v.z, v.w};
-                        for (int q = 0; q < 4; q++)
-                            if (n + q < a.N) o[q] = a.accumulate ? o[q] + e[q] : e[q];
-                    }
-                }
-            }
-        }
-        __syncthreads();
-    }
+    epilogue<TM, TN, FM, FN>(a, acc, epi, reinterpret_cast<float*>(smem) + wave * 16 * LDW, lane,
+                             m0 + wm * TM, n0 + wn * TN);
 }
 
 // ------------------------------------------------------ direct-to-LDS --
@@ -363,45 +423,47 @@ __device__ __forceinline__ int swz(int r) {
     return BK == 64 ? (r >> 1) & 3 : r & 7;
 }
 
-template <int BM, int BN, int BK, int S>
+template <int BM, int BN, int BK, int S, int WM, int WN>
 struct LdsCfg {
-    static constexpr int TM = BM / 2, TN = BN / 2;
+    static constexpr int NW = WM * WN, NT = 64 * NW;  // waves, threads per block
+    static constexpr int TM = BM / WM, TN = BN / WN;
     static constexpr int FM = TM / 16, FN = TN / 16;
     static constexpr int CPR = BK / 16;
-    static constexpr int IA = BM * CPR / 256, IB = BN * CPR / 256;  // load instrs per wave per slab
+    static constexpr int IA = BM * CPR / NT, IB = BN * CPR / NT;  // load instrs per wave per slab
     static constexpr int LPS = IA + IB;
     static constexpr int STAGE = (BM + BN) * BK;
     static constexpr int LDW = TN + 4;
     static constexpr int MAIN = S * STAGE;
-    static constexpr int EPI = 4 * 16 * LDW * 4;
+    static constexpr int EPI = NW * 16 * LDW * 4;
     static constexpr int LDS = MAIN > EPI ? MAIN : EPI;
-    static_assert(BM * CPR % 256 == 0 && BN * CPR % 256 == 0, "slab chunks must split evenly");
+    static_assert(BM * CPR % NT == 0 && BN * CPR % NT == 0, "slab chunks must split evenly");
+    static_assert(TM % 16 == 0 && TN % 16 == 0, "wave tile");
     static_assert(S >= 2 && (S - 2) * LPS < 64, "pipeline depth");
 };
 
-template <int BM, int BN, int BK, int S>
-__global__ __launch_bounds__(256) void gemm_i8_lds(GemmArgs a) {
-    using C = LdsCfg<BM, BN, BK, S>;
-    constexpr int TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN, CPR = C::CPR;
+template <int BM, int BN, int BK, int S, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds(GemmArgs a) {
+    using C = LdsCfg<BM, BN, BK, S, WM, WN>;
+    constexpr int TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN, CPR = C::CPR, NW = C::NW;
     constexpr int IA = C::IA, IB = C::IB, LPS = C::LPS, STAGE = C::STAGE, LDW = C::LDW;
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int wm = wave >> 1, wn = wave & 1;
+    const int wm = wave / WN, wn = wave % WN;
     int tm, tn;
     tile_coords(blockIdx.x, (a.M + BM - 1) / BM, (a.N + BN - 1) / BN, tm, tn);
     const int m0 = tm * BM, n0 = tn * BN;
     const int K16 = (a.K + 15) & ~15;
 
     // Load slots: instruction j of this wave fills LDS chunks [64*slot, +64) of
-    // the slab, slot = j*4 + wave; lane l writes chunk 64*slot + l, which holds
+    // the slab, slot = j*NW + wave; lane l writes chunk 64*slot + l, which holds
     // row q / CPR, logical chunk (q % CPR) ^ swz(row).
     const int8_t* asrc[IA];
     int acb[IA];
 #pragma unroll
     for (int j = 0; j < IA; j++) {
-        const int q = (j * 4 + wave) * 64 + lane, r = q / CPR;
+        const int q = (j * NW + wave) * 64 + lane, r = q / CPR;
         const int c = (q % CPR) ^ swz<BK>(r);
         const int m = m0 + r < a.M ? m0 + r : a.M - 1;
         acb[j] = c * 16;
@@ -411,7 +473,7 @@ __global__ __launch_bounds__(256) void gemm_i8_lds(GemmArgs a) {
     int bcb[IB];
 #pragma unroll
     for (int j = 0; j < IB; j++) {
-        const int q = (j * 4 + wave) * 64 + lane, r = q / CPR;
+        const int q = (j * NW + wave) * 64 + lane, r = q / CPR;
         const int c = (q % CPR) ^ swz<BK>(r);
         const int n = n0 + r < a.N ? n0 + r : a.N - 1;
         bcb[j] = c * 16;
@@ -427,12 +489,12 @@ __global__ __launch_bounds__(256) void gemm_i8_lds(GemmArgs a) {
 #pragma unroll
         for (int j = 0; j < IA; j++) {
             const int8_t* p = full || k0 + acb[j] < K16 ? asrc[j] + k0 : g_zero16;
-            __builtin_amdgcn_global_load_lds((gptr)p, (lptr)(st + (j * 4 + wave) * 1024), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((gptr)p, (lptr)(st + (j * NW + wave) * 1024), 16, 0, 0);
         }
 #pragma unroll
         for (int j = 0; j < IB; j++) {
             const int8_t* p = full || k0 + bcb[j] < K16 ? bsrc[j] + k0 : g_zero16;
-            __builtin_amdgcn_global_load_lds((gptr)p, (lptr)(st + BM * BK + (j * 4 + wave) * 1024), 16, 0, 0);
+            __builtin_amdgcn_global_load_lds((gptr)p, (lptr)(st + BM * BK + (j * NW + wave) * 1024), 16, 0, 0);
         }
     };
 
@@ -446,6 +508,9 @@ __global__ __launch_bounds__(256) void gemm_i8_lds(GemmArgs a) {
     const int sz = swz<BK>(r16);  // swz depends on the row's low bits only
     const int arow_l = (wm * TM + r16) * BK;
     const int brow_l = BM * BK + (wn * TN + r16) * BK;
+
+    EpiRegs<FN> epi;  // issued before the slab loads, so it is the oldest vmcnt entry
+    epi.load(a, n0 + wn * TN, lane);
 
     const int nk = K16 / BK + (K16 % BK ? 1 : 0);
 #pragma unroll
@@ -478,63 +543,8 @@ __global__ __launch_bounds__(256) void gemm_i8_lds(GemmArgs a) {
     }
     __syncthreads();
 
-    // LDS-staged epilogue (as gemm_i8_tiled)
-    float* stage = reinterpret_cast<float*>(smem) + wave * 16 * LDW;
-    const int g4 = 4 * (lane >> 4), c16 = lane & 15;
-    constexpr int LPR = TN / 4, RPI = 64 / LPR;
-    const int mw = m0 + wm * TM, nw = n0 + wn * TN;
-    const bool vec = (a.acc32 ? (a.N % 4 == 0) : (a.ldo % 4 == 0)) && nw + TN <= a.N;
-#pragma unroll
-    for (int i = 0; i < FM; i++) {
-#pragma unroll
-        for (int j = 0; j < FN; j++) {
-            const int n = nw + j * 16 + c16;
-            const int nc = n < a.N ? n : a.N - 1;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int m = mw + i * 16 + g4 + r;
-                const int mc = m < a.M ? m : a.M - 1;
-                const int av = acc[i][j][r];
-                stage[(g4 + r) * LDW + j * 16 + c16] = a.acc32 ? __int_as_float(av) : epi_value(a, mc, nc, av);
-            }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int rr = 0; rr < 16; rr += RPI) {
-            const int row = rr + lane / LPR, col = (lane % LPR) * 4;
-            const int m = mw + i * 16 + row;
-            if (m < a.M) {
-                const float4 v = *reinterpret_cast<const float4*>(stage + row * LDW + col);
-                const int n = nw + col;
-                if (a.acc32) {
-                    int32_t* o = a.acc32 + (size_t)m * a.N + n;
-                    if (vec) {
-                        *reinterpret_cast<int4*>(o) = make_int4(__float_as_int(v.x), __float_as_int(v.y),
-                                                                __float_as_int(v.z), __float_as_int(v.w));
-                    } else {
-                        const float e[4] = {v.x, v.y, v.z, v.w};
-                        for (int q = 0; q < 4; q++)
-                            if (n + q < a.N) o[q] = __float_as_int(e[q]);
-                    }
-                } else {
-                    float* o = a.out + (size_t)m * a.ldo + n;
-                    if (vec) {
-                        float4 w = v;
-                        if (a.accumulate) {
-                            const float4 old = *reinterpret_cast<const float4*>(o);
-                            w = make_float4(old.x + v.x, old.y + v.y, old.z + v.z, old.w + v.w);
-                        }
-                        *reinterpret_cast<float4*>(o) = w;
-                    } else {
-                        const float e[4] = {v.x, v.y, v.z, v.w};
-                        for (int q = 0; q < 4; q++)
-                            if (n + q < a.N) o[q] = a.accumulate ? o[q] + e[q] : e[q];
-                    }
-                }
-            }
-        }
-        __syncthreads();
-    }
+    epilogue<TM, TN, FM, FN>(a, acc, epi, reinterpret_cast<float*>(smem) + wave * 16 * LDW, lane,
+                             m0 + wm * TM, n0 + wn * TN);
 }
 
 // ---------------------------------------------------------------- skinny --
@@ -684,18 +694,19 @@ void run_tiled(const GemmArgs& a, hipStream_t st) {
     VLA_LAUNCH_CHECK();
 }
 
-template <int BM, int BN, int BK, int S>
+template <int BM, int BN, int BK, int S, int WM = 2, int WN = 2>
 void run_lds(const GemmArgs& a, hipStream_t st) {
-    using C = LdsCfg<BM, BN, BK, S>;
+    using C = LdsCfg<BM, BN, BK, S, WM, WN>;
     static const bool attr = [] {
         if (C::LDS > 65536)
-            VLA_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_i8_lds<BM, BN, BK, S>),
-                                              hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS));
+            VLA_HIP_CHECK(hipFuncSetAttribute(
+                reinterpret_cast<const void*>(&gemm_i8_lds<BM, BN, BK, S, WM, WN>),
+                hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS));
         return true;
     }();
     (void)attr;
     const int blocks = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-    gemm_i8_lds<BM, BN, BK, S><<<blocks, 256, C::LDS, st>>>(a);
+    gemm_i8_lds<BM, BN, BK, S, WM, WN><<<blocks, C::NT, C::LDS, st>>>(a);
     VLA_LAUNCH_CHECK();
 }
 
@@ -721,19 +732,22 @@ void run_skinny(const GemmArgs& a, hipStream_t st) {
 // stages == 0: the register-staged gemm_i8_tiled; > 0: gemm_i8_lds with that
 // many LDS stages (named "<BM>x<BN>x<BK>s<S>").
 struct Tile {
-    int bm, bn, bk, stages;
+    int bm, bn, bk, stages, waves = 4;
 };
 const Tile kTiles[] = {{256, 256, 64, 0}, {256, 128, 128, 0}, {256, 128, 64, 0}, {128, 128, 128, 0},
                        {128, 128, 64, 0},  {64, 128, 64, 0},   {64, 64, 64, 0},   {128, 128, 128, 4},
                        {128, 128, 64, 4},  {256, 128, 64, 4},  {256, 128, 128, 3}, {64, 128, 64, 4},
-                       {128, 128, 128, 3}, {256, 256, 64, 3}};
+                       {128, 128, 128, 3}, {256, 256, 64, 3},  {256, 256, 128, 2, 8},
+                       {256, 256, 64, 3, 8}, {256, 256, 128, 2}, {256, 128, 128, 3, 8}};
 
 Tile pick_tile(int M, int N, int K) {
     const char* env = std::getenv("VLA_HIP_GEMM_TILE");
     if (env && *env) {
         for (const Tile& t : kTiles) {
             char name[32];
-            if (t.stages)
+            if (t.stages && t.waves != 4)
+                std::snprintf(name, sizeof name, "%dx%dx%ds%dw%d", t.bm, t.bn, t.bk, t.stages, t.waves);
+            else if (t.stages)
                 std::snprintf(name, sizeof name, "%dx%dx%ds%d", t.bm, t.bn, t.bk, t.stages);
             else
                 std::snprintf(name, sizeof name, "%dx%dx%d", t.bm, t.bn, t.bk);
@@ -753,8 +767,15 @@ Tile pick_tile(int M, int N, int K) {
 }
 
 void dispatch_tile(const Tile& t, const GemmArgs& a, hipStream_t st) {
+    if (t.stages && t.waves == 8) {
+        if (t.bn == 256 && t.bk == 128) run_lds<256, 256, 128, 2, 2, 4>(a, st);
+        else if (t.bn == 256) run_lds<256, 256, 64, 3, 2, 4>(a, st);
+        else run_lds<256, 128, 128, 3, 4, 2>(a, st);
+        return;
+    }
     if (t.stages) {
-        if (t.bm == 128 && t.bk == 128 && t.stages == 4) run_lds<128, 128, 128, 4>(a, st);
+        if (t.bn == 256 && t.bk == 128) run_lds<256, 256, 128, 2>(a, st);
+        else if (t.bm == 128 && t.bk == 128 && t.stages == 4) run_lds<128, 128, 128, 4>(a, st);
         else if (t.bm == 128 && t.bk == 128) run_lds<128, 128, 128, 3>(a, st);
         else if (t.bm == 128) run_lds<128, 128, 64, 4>(a, st);
         else if (t.bm == 256 && t.bn == 256) run_lds<256, 256, 64, 3>(a, st);
