@@ -253,6 +253,94 @@ VLA_API int32_t vla_silu_gate_dev(float* out, const float* g, const float* u, in
  * reference graphs, e.g. act_transformer.cpp:227-281). */
 VLA_API int32_t vla_add_dev(float* out, const float* a, const float* b, int64_t n, void* stream);
 
+/* ------------------------------------------------ device policy graphs ---- */
+/* The reference's transformer graphs with every linear, attention, norm and
+ * activation on the device and the whole pass replayed as one HIP graph. Each
+ * loader reads the reference's own checkpoint files and takes the int8 mask
+ * its model reads from the environment (ACT_INT8 / OCTO_INT8 / SMOLVLA_INT8):
+ * the selected layers are quantized once on the device with the
+ * pack_weights_i8 formula, the rest stay fp32. NULL on failure
+ * (vla_last_error()). One inference per handle at a time
+ * (include/vla_simd.h:22-25). Host forms copy in, run and synchronize; _dev
+ * forms take device pointers and a hipStream_t (void*, NULL = null stream),
+ * run asynchronously and allocate nothing after the first call with a shape. */
+
+/* ACT transformer (ActTransformer, src/models/act/act_transformer.h:36-102):
+ * <dir>/act.meta + act.bin as ActTransformer::load (act_transformer.cpp:29-170),
+ * img_ch the backbone feature width, int8_mask the ACT_INT8 bits
+ * (act_transformer.cpp:27: 1 encoder attention, 2 w1, 4 w2, 8 img_proj,
+ * 16 decoder). */
+typedef struct vla_act_tf vla_act_tf;
+VLA_API vla_act_tf* vla_act_tf_load(const char* dir, int32_t img_ch, int32_t int8_mask);
+VLA_API void vla_act_tf_free(vla_act_tf* h);
+VLA_API int32_t vla_act_tf_chunk(const vla_act_tf* h);
+VLA_API int32_t vla_act_tf_action_dim(const vla_act_tf* h);
+VLA_API int32_t vla_act_tf_state_dim(const vla_act_tf* h);
+VLA_API int32_t vla_act_tf_dim(const vla_act_tf* h);
+/* number of linear layers held as int8 (the count load() prints, :164-167) */
+VLA_API int32_t vla_act_tf_int8_layers(const vla_act_tf* h);
+/* kernel nodes of the captured graph (0 before the second call with a shape) */
+VLA_API int32_t vla_act_tf_graph_nodes(const vla_act_tf* h);
+/* ActTransformer::forward (act_transformer.h:98-101, .cpp:358-366) without
+ * text tokens: feats [n_cams, fh*fw, img_ch] (the backbone feature maps, NHWC
+ * tokens, cameras back to back), state_norm [state_dim] ->
+ * actions_norm [chunk, action_dim]. */
+VLA_API int32_t vla_act_tf_forward(vla_act_tf* h, const float* feats, int32_t n_cams, int32_t fh,
+                                   int32_t fw, const float* state_norm, float* actions_norm);
+VLA_API int32_t vla_act_tf_forward_dev(vla_act_tf* h, const float* feats, int32_t n_cams, int32_t fh,
+                                       int32_t fw, const float* state_norm, float* actions_norm,
+                                       void* stream);
+
+/* Octo block transformer (OctoTransformer, src/models/octo/octo_transformer.h:37-82):
+ * <dir>/octo.meta + octo.bin as OctoTransformer::load (octo_transformer.cpp:17-99),
+ * int8_mask the OCTO_INT8 bits (octo_model.cpp:60: 1 attention, 2 w1, 4 w2,
+ * 8 token projections). An extra meta key "repeat_task 0" drops the per-step
+ * copy of the task tokens (the reference always repeats them). */
+typedef struct vla_octo_tf vla_octo_tf;
+VLA_API vla_octo_tf* vla_octo_tf_load(const char* dir, int32_t int8_mask);
+VLA_API void vla_octo_tf_free(vla_octo_tf* h);
+VLA_API int32_t vla_octo_tf_dim(const vla_octo_tf* h);
+VLA_API int32_t vla_octo_tf_total_tokens(const vla_octo_tf* h, int32_t wnd);
+VLA_API int32_t vla_octo_tf_readout_index(const vla_octo_tf* h, int32_t wnd);
+VLA_API int32_t vla_octo_tf_int8_layers(const vla_octo_tf* h);
+VLA_API int32_t vla_octo_tf_graph_nodes(const vla_octo_tf* h);
+/* OctoTransformer::forward (octo_transformer.h:75-81, .cpp:144-219):
+ * t5_out [n_task, t5_dim], stem_p [wnd, tok_primary, stem_dim], stem_w
+ * [wnd, tok_wrist, stem_dim] or NULL, timestep_mask [wnd] (host memory in both
+ * forms). out [d] receives the one row the reference writes, out + ro*d with
+ * ro = vla_octo_tf_readout_index(wnd): the final-LayerNorm readout token. */
+VLA_API int32_t vla_octo_tf_forward(vla_octo_tf* h, const float* t5_out, const float* stem_p,
+                                    const float* stem_w, int32_t wnd, const uint8_t* timestep_mask,
+                                    float* out);
+VLA_API int32_t vla_octo_tf_forward_dev(vla_octo_tf* h, const float* t5_out, const float* stem_p,
+                                        const float* stem_w, int32_t wnd, const uint8_t* timestep_mask,
+                                        float* out, void* stream);
+
+/* SmolVLA action chunk: the SmolLM2 prefix tower and the action expert
+ * (SmollmVlm, src/models/smolvla/smollm2_lm.h:31-47; ActionExpert,
+ * action_expert.h:55-93). <dir>/vlm.meta + vlm.bin and aex.meta + aex.bin as
+ * their load() (smollm2_lm.cpp:17-83, action_expert.cpp:60-172); int8_mask the
+ * SMOLVLA_INT8 bits (smolvla_model.cpp:44: 16 text tower, 32 expert). */
+typedef struct vla_smolvla_tf vla_smolvla_tf;
+VLA_API vla_smolvla_tf* vla_smolvla_tf_load(const char* dir, int32_t int8_mask);
+VLA_API void vla_smolvla_tf_free(vla_smolvla_tf* h);
+VLA_API int32_t vla_smolvla_tf_chunk(const vla_smolvla_tf* h);
+VLA_API int32_t vla_smolvla_tf_max_action_dim(const vla_smolvla_tf* h);
+VLA_API int32_t vla_smolvla_tf_hidden(const vla_smolvla_tf* h);
+VLA_API int32_t vla_smolvla_tf_int8_layers(const vla_smolvla_tf* h);
+VLA_API int32_t vla_smolvla_tf_graph_nodes(const vla_smolvla_tf* h);
+/* SmolvlaModel::predict_normalized after the vision tower and the embedding
+ * lookup (smolvla_model.cpp:252-285): prefix [n_prefix, hidden] the assembled
+ * prefix embeddings (image and text tokens already scaled by sqrt(hidden),
+ * the state token last), pad [n_prefix] (host memory in both forms; 1 real,
+ * 0 padding, the last token must be real), noise [chunk, max_action_dim] ->
+ * actions [chunk, max_action_dim] (normalized; no RTC guidance). */
+VLA_API int32_t vla_smolvla_tf_chunk_run(vla_smolvla_tf* h, const float* prefix, const int32_t* pad,
+                                         int32_t n_prefix, const float* noise, float* actions);
+VLA_API int32_t vla_smolvla_tf_chunk_dev(vla_smolvla_tf* h, const float* prefix, const int32_t* pad,
+                                         int32_t n_prefix, const float* noise, float* actions,
+                                         void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -324,3 +324,92 @@ def ref_silu_gate(g, u):
     out = np.empty_like(g)
     ref().ref_silu_gate(_p(out), _p(g), _p(u), g.size)
     return out
+
+
+# ------------------------------------------- reference policy graphs ------
+# ref_models_shim.cpp: the reference's own ActTransformer / OctoTransformer /
+# SmollmVlm + ActionExpert, loading the same checkpoint files as the device
+# graphs.
+
+def _ref_models():
+    L = ref()
+    if getattr(L, "_models_declared", False):
+        return L
+    P, i = c_void_p, c_int
+    L.ref_act_load.argtypes, L.ref_act_load.restype = [ctypes.c_char_p, i, i], P
+    L.ref_act_free.argtypes = [P]
+    L.ref_act_forward.argtypes, L.ref_act_forward.restype = [P, P, i, i, i, P, P], i
+    L.ref_octo_load.argtypes, L.ref_octo_load.restype = [ctypes.c_char_p, i], P
+    L.ref_octo_free.argtypes = [P]
+    L.ref_octo_forward.argtypes, L.ref_octo_forward.restype = [P, P, P, P, i, P, P], i
+    L.ref_octo_total_tokens.argtypes, L.ref_octo_total_tokens.restype = [P, i], i
+    L.ref_smolvla_load.argtypes, L.ref_smolvla_load.restype = [ctypes.c_char_p, i], P
+    L.ref_smolvla_free.argtypes = [P]
+    L.ref_smolvla_chunk.argtypes, L.ref_smolvla_chunk.restype = [P, P, P, i, P, P], i
+    L.ref_smolvla_chunk_len.argtypes, L.ref_smolvla_chunk_len.restype = [P], i
+    L.ref_smolvla_max_action_dim.argtypes, L.ref_smolvla_max_action_dim.restype = [P], i
+    L._models_declared = True
+    return L
+
+
+class RefAct:
+    def __init__(self, dirpath, img_ch, int8_mask, chunk, action_dim):
+        L = _ref_models()
+        self.h = L.ref_act_load(dirpath.encode(), img_ch, int8_mask)
+        if not self.h:
+            raise RuntimeError(f"reference ActTransformer::load failed for {dirpath}")
+        self.chunk, self.action_dim = chunk, action_dim
+
+    def forward(self, feats, n_cams, fh, fw, state):
+        out = np.empty((self.chunk, self.action_dim), np.float32)
+        f, s = _f32(feats), _f32(state)
+        _ref_models().ref_act_forward(self.h, _p(f), n_cams, fh, fw, _p(s), _p(out))
+        return out
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            _ref_models().ref_act_free(self.h)
+
+
+class RefOcto:
+    def __init__(self, dirpath, int8_mask, d):
+        L = _ref_models()
+        self.h = L.ref_octo_load(dirpath.encode(), int8_mask)
+        if not self.h:
+            raise RuntimeError(f"reference OctoTransformer::load failed for {dirpath}")
+        self.d = d
+
+    def forward(self, t5, stem_p, stem_w, wnd, tmask):
+        L = _ref_models()
+        total = L.ref_octo_total_tokens(self.h, wnd)
+        out = np.zeros((total, self.d), np.float32)
+        a, b = _f32(t5), _f32(stem_p)
+        c = None if stem_w is None else _f32(stem_w)
+        tm = np.ascontiguousarray(tmask, dtype=np.uint8)
+        ro = L.ref_octo_forward(self.h, _p(a), _p(b), _p(c), wnd, _p(tm), _p(out))
+        return out[ro].copy()
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            _ref_models().ref_octo_free(self.h)
+
+
+class RefSmolvla:
+    def __init__(self, dirpath, int8_mask):
+        L = _ref_models()
+        self.h = L.ref_smolvla_load(dirpath.encode(), int8_mask)
+        if not self.h:
+            raise RuntimeError(f"reference SmolVLA load failed for {dirpath}")
+        self.chunk = L.ref_smolvla_chunk_len(self.h)
+        self.mad = L.ref_smolvla_max_action_dim(self.h)
+
+    def run(self, prefix, pad, noise):
+        out = np.empty((self.chunk, self.mad), np.float32)
+        p, n = _f32(prefix), _f32(noise)
+        pd = np.ascontiguousarray(pad, dtype=np.int32)
+        _ref_models().ref_smolvla_chunk(self.h, _p(p), _p(pd), p.shape[0], _p(n), _p(out))
+        return out
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            _ref_models().ref_smolvla_free(self.h)

@@ -1,0 +1,168 @@
+/*
+ * ref_models_shim.cpp - extern "C" wrapper over the REAL reference policy
+ * graphs (ActTransformer, OctoTransformer, SmollmVlm + ActionExpert), compiled
+ * from the reference's own sources where they lie (oracle/Makefile names them)
+ * into oracle/_ref/libvla_ref.so next to ref_shim.cpp.
+ *
+ * TEST INFRASTRUCTURE ONLY: the graph parity tests load the same checkpoint
+ * files into these and into the device graphs and compare the outputs. The
+ * product never loads it.
+ *
+ * Beyond forwarding, this file does what the reference's model classes do
+ * around the graphs and that the tests need without images or tokenizers:
+ *   - the OCTO_INT8 / SMOLVLA_INT8 per-layer init_int8 calls of
+ *     OctoModel::apply_int8 (src/models/octo/octo_model.cpp:104-140) and
+ *     SmolvlaModel::apply_int8 (src/models/smolvla/smolvla_model.cpp:111-155),
+ *     with the mask passed in instead of read from the environment;
+ *   - the prefix-LM mask, positions and denoise mask of
+ *     SmolvlaModel::predict_normalized (smolvla_model.cpp:252-275) built from a
+ *     pad vector, so the chunk starts from given prefix embeddings.
+ */
+#include "models/act/act_transformer.h"
+#include "models/octo/octo_transformer.h"
+#include "models/smolvla/action_expert.h"
+#include "models/smolvla/smollm2_lm.h"
+
+#include <cstdint>
+#include <cstdio>
+#include <exception>
+#include <limits>
+#include <vector>
+
+#define REF_API extern "C" __attribute__((visibility("default")))
+
+using namespace tcpu;
+
+REF_API void* ref_act_load(const char* dir, int img_ch, int int8_mask) {
+    try {
+        auto* t = new ActTransformer();
+        if (!t->load(dir, img_ch, int8_mask)) {
+            delete t;
+            return nullptr;
+        }
+        return t;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "ref_act_load: %s\n", e.what());
+        return nullptr;
+    }
+}
+
+REF_API void ref_act_free(void* h) { delete static_cast<ActTransformer*>(h); }
+
+REF_API int ref_act_forward(void* h, const float* feats, int n_cams, int fh, int fw,
+                            const float* state_norm, float* actions_norm) {
+    auto* t = static_cast<ActTransformer*>(h);
+    const int img_ch = t->img_proj.K;
+    std::vector<const float*> cams(n_cams);
+    for (int c = 0; c < n_cams; c++) cams[c] = feats + (size_t)c * fh * fw * img_ch;
+    t->forward(cams.data(), n_cams, fh, fw, state_norm, actions_norm);
+    return 0;
+}
+
+REF_API void* ref_octo_load(const char* dir, int int8_mask) {
+    try {
+        auto* t = new OctoTransformer();
+        if (!t->load(dir)) {
+            delete t;
+            return nullptr;
+        }
+        for (nn::EncoderLayer& l : t->layers) {
+            if (int8_mask & 1) {
+                l.attn.wq.init_int8();
+                l.attn.wk.init_int8();
+                l.attn.wv.init_int8();
+                l.attn.wo.init_int8();
+            }
+            if (int8_mask & 2) l.w1.init_int8();
+            if (int8_mask & 4) l.w2.init_int8();
+        }
+        if (int8_mask & 8) {
+            t->proj_task.init_int8();
+            t->proj_prim.init_int8();
+            t->proj_wrist.init_int8();
+        }
+        return t;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "ref_octo_load: %s\n", e.what());
+        return nullptr;
+    }
+}
+
+REF_API void ref_octo_free(void* h) { delete static_cast<OctoTransformer*>(h); }
+
+/* out [total_tokens(wnd), d]; only the readout row is written */
+REF_API int ref_octo_forward(void* h, const float* t5, const float* stem_p, const float* stem_w, int wnd,
+                             const uint8_t* tmask, float* out) {
+    auto* t = static_cast<OctoTransformer*>(h);
+    t->forward(t5, stem_p, stem_w, wnd, tmask, out);
+    return t->readout_index(wnd, wnd - 1);
+}
+
+REF_API int ref_octo_total_tokens(void* h, int wnd) {
+    return static_cast<OctoTransformer*>(h)->total_tokens(wnd);
+}
+
+struct RefSmolvla {
+    SmollmVlm vlm;
+    ActionExpert aex;
+};
+
+REF_API void* ref_smolvla_load(const char* dir, int int8_mask) {
+    try {
+        auto* m = new RefSmolvla();
+        if (!m->vlm.load(dir) || !m->aex.load(dir)) {
+            delete m;
+            return nullptr;
+        }
+        if (int8_mask & 16)
+            for (VlmLayerW& w : m->vlm.layers)
+                for (nn::Linear* l : {&w.q, &w.k, &w.v, &w.o, &w.gate, &w.up, &w.down}) l->init_int8();
+        if (int8_mask & 32)
+            for (ExpertLayerW& w : m->aex.layers)
+                for (nn::Linear* l : {&w.q, &w.k, &w.v, &w.o, &w.gate, &w.up, &w.down}) l->init_int8();
+        return m;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "ref_smolvla_load: %s\n", e.what());
+        return nullptr;
+    }
+}
+
+REF_API void ref_smolvla_free(void* h) { delete static_cast<RefSmolvla*>(h); }
+
+/* prefix [n_prefix, hidden], pad [n_prefix] (last = state token), noise and
+ * actions [chunk, max_action_dim] */
+REF_API int ref_smolvla_chunk(void* h, const float* prefix, const int* pad, int n_prefix,
+                              const float* noise, float* actions) {
+    auto* m = static_cast<RefSmolvla*>(h);
+    const int C = m->aex.cfg.chunk, np = n_prefix, SK = np + C;
+    const float NEG = std::numeric_limits<float>::lowest();
+    const int state_idx = np - 1;
+    std::vector<float> pmask((size_t)np * np);
+    for (int i = 0; i < np; i++)
+        for (int j = 0; j < np; j++) {
+            const int ai = i >= state_idx, aj = j >= state_idx;
+            pmask[(size_t)i * np + j] = (aj <= ai && pad[i] && pad[j]) ? 0.0f : NEG;
+        }
+    std::vector<int> pos(np);
+    int c = 0;
+    for (int i = 0; i < np; i++) {
+        c += pad[i] ? 1 : 0;
+        pos[i] = c - 1;
+    }
+    std::vector<VlmKV> kv;
+    m->vlm.prefix_forward(prefix, pmask.data(), pos.data(), np, kv);
+    std::vector<float> dmask((size_t)C * SK);
+    std::vector<int> pos_full(C);
+    for (int i = 0; i < C; i++) {
+        for (int j = 0; j < np; j++) dmask[(size_t)i * SK + j] = pad[j] ? 0.0f : NEG;
+        for (int j = 0; j < C; j++) dmask[(size_t)i * SK + np + j] = j <= i ? 0.0f : NEG;
+        pos_full[i] = c + i;
+    }
+    m->aex.denoise(kv, np, noise, dmask.data(), pos_full.data(), actions, nullptr, nullptr, 0.0f);
+    return 0;
+}
+
+REF_API int ref_smolvla_chunk_len(void* h) { return static_cast<RefSmolvla*>(h)->aex.cfg.chunk; }
+REF_API int ref_smolvla_max_action_dim(void* h) {
+    return static_cast<RefSmolvla*>(h)->aex.cfg.max_action_dim;
+}

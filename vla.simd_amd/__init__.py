@@ -50,6 +50,15 @@ EXPORTS = (
     "vla_rope_neox", "vla_rope_neox_dev",
     "vla_gelu_tanh", "vla_gelu_erf", "vla_relu", "vla_silu_gate",
     "vla_gelu_tanh_dev", "vla_gelu_erf_dev", "vla_relu_dev", "vla_silu_gate_dev", "vla_add_dev",
+    "vla_act_tf_load", "vla_act_tf_free", "vla_act_tf_chunk", "vla_act_tf_action_dim",
+    "vla_act_tf_state_dim", "vla_act_tf_dim", "vla_act_tf_int8_layers", "vla_act_tf_graph_nodes",
+    "vla_act_tf_forward", "vla_act_tf_forward_dev",
+    "vla_octo_tf_load", "vla_octo_tf_free", "vla_octo_tf_dim", "vla_octo_tf_total_tokens",
+    "vla_octo_tf_readout_index", "vla_octo_tf_int8_layers", "vla_octo_tf_graph_nodes",
+    "vla_octo_tf_forward", "vla_octo_tf_forward_dev",
+    "vla_smolvla_tf_load", "vla_smolvla_tf_free", "vla_smolvla_tf_chunk",
+    "vla_smolvla_tf_max_action_dim", "vla_smolvla_tf_hidden", "vla_smolvla_tf_int8_layers",
+    "vla_smolvla_tf_graph_nodes", "vla_smolvla_tf_chunk_run", "vla_smolvla_tf_chunk_dev",
 )
 
 
@@ -130,6 +139,34 @@ def _declare(L):
         "vla_relu_dev": (i32, [P, i64, P]),
         "vla_silu_gate_dev": (i32, [P, P, P, i64, P]),
         "vla_add_dev": (i32, [P, P, P, i64, P]),
+        "vla_act_tf_load": (P, [c_char_p, i32, i32]),
+        "vla_act_tf_free": (None, [P]),
+        "vla_act_tf_chunk": (i32, [P]),
+        "vla_act_tf_action_dim": (i32, [P]),
+        "vla_act_tf_state_dim": (i32, [P]),
+        "vla_act_tf_dim": (i32, [P]),
+        "vla_act_tf_int8_layers": (i32, [P]),
+        "vla_act_tf_graph_nodes": (i32, [P]),
+        "vla_act_tf_forward": (i32, [P, P, i32, i32, i32, P, P]),
+        "vla_act_tf_forward_dev": (i32, [P, P, i32, i32, i32, P, P, P]),
+        "vla_octo_tf_load": (P, [c_char_p, i32]),
+        "vla_octo_tf_free": (None, [P]),
+        "vla_octo_tf_dim": (i32, [P]),
+        "vla_octo_tf_total_tokens": (i32, [P, i32]),
+        "vla_octo_tf_readout_index": (i32, [P, i32]),
+        "vla_octo_tf_int8_layers": (i32, [P]),
+        "vla_octo_tf_graph_nodes": (i32, [P]),
+        "vla_octo_tf_forward": (i32, [P, P, P, P, i32, P, P]),
+        "vla_octo_tf_forward_dev": (i32, [P, P, P, P, i32, P, P, P]),
+        "vla_smolvla_tf_load": (P, [c_char_p, i32]),
+        "vla_smolvla_tf_free": (None, [P]),
+        "vla_smolvla_tf_chunk": (i32, [P]),
+        "vla_smolvla_tf_max_action_dim": (i32, [P]),
+        "vla_smolvla_tf_hidden": (i32, [P]),
+        "vla_smolvla_tf_int8_layers": (i32, [P]),
+        "vla_smolvla_tf_graph_nodes": (i32, [P]),
+        "vla_smolvla_tf_chunk_run": (i32, [P, P, P, i32, P, P]),
+        "vla_smolvla_tf_chunk_dev": (i32, [P, P, P, i32, P, P, P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -459,3 +496,117 @@ class LinearI8:
             self.close()
         except Exception:
             pass
+
+
+# ------------------------------------------------ device policy graphs ----
+
+class _Handle:
+    _free = ""
+
+    def __init__(self, h):
+        if not h:
+            raise VlaError(self._load, VLA_ERR_ARG, (lib().vla_last_error() or b"").decode())
+        self.h = c_void_p(h)
+
+    def close(self):
+        if getattr(self, "h", None):
+            getattr(lib(), self._free)(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class ActTransformer(_Handle):
+    """Device ACT transformer (vla_act_tf_*, ActTransformer of the reference)."""
+
+    _load, _free = "vla_act_tf_load", "vla_act_tf_free"
+
+    def __init__(self, dirpath: str, img_ch: int, int8_mask: int = 31):
+        super().__init__(lib().vla_act_tf_load(dirpath.encode(), img_ch, int8_mask))
+        L = lib()
+        self.chunk, self.action_dim = L.vla_act_tf_chunk(self.h), L.vla_act_tf_action_dim(self.h)
+        self.state_dim, self.img_ch = L.vla_act_tf_state_dim(self.h), img_ch
+        self.int8_layers = L.vla_act_tf_int8_layers(self.h)
+
+    @property
+    def graph_nodes(self):
+        return lib().vla_act_tf_graph_nodes(self.h)
+
+    def forward(self, feats, n_cams, fh, fw, state):
+        feats, state = _f32(feats), _f32(state)
+        out = np.empty((self.chunk, self.action_dim), np.float32)
+        _call("vla_act_tf_forward", self.h, _ptr(feats), n_cams, fh, fw, _ptr(state), _ptr(out))
+        return out
+
+    def forward_dev(self, feats, n_cams, fh, fw, state, out, stream=None):
+        _call("vla_act_tf_forward_dev", self.h, _dp(feats), n_cams, fh, fw, _dp(state), _dp(out),
+              _stream(stream))
+
+
+class OctoTransformer(_Handle):
+    """Device Octo block transformer (vla_octo_tf_*)."""
+
+    _load, _free = "vla_octo_tf_load", "vla_octo_tf_free"
+
+    def __init__(self, dirpath: str, int8_mask: int = 7):
+        super().__init__(lib().vla_octo_tf_load(dirpath.encode(), int8_mask))
+        self.d = lib().vla_octo_tf_dim(self.h)
+        self.int8_layers = lib().vla_octo_tf_int8_layers(self.h)
+
+    @property
+    def graph_nodes(self):
+        return lib().vla_octo_tf_graph_nodes(self.h)
+
+    def total_tokens(self, wnd):
+        return lib().vla_octo_tf_total_tokens(self.h, wnd)
+
+    def readout_index(self, wnd):
+        return lib().vla_octo_tf_readout_index(self.h, wnd)
+
+    def forward(self, t5, stem_p, stem_w, wnd, tmask):
+        t5, stem_p = _f32(t5), _f32(stem_p)
+        stem_w = None if stem_w is None else _f32(stem_w)
+        tm = np.ascontiguousarray(tmask, dtype=np.uint8)
+        out = np.empty(self.d, np.float32)
+        _call("vla_octo_tf_forward", self.h, _ptr(t5), _ptr(stem_p), _ptr(stem_w), wnd, _ptr(tm),
+              _ptr(out))
+        return out
+
+    def forward_dev(self, t5, stem_p, stem_w, wnd, tmask, out, stream=None):
+        tm = np.ascontiguousarray(tmask, dtype=np.uint8)
+        _call("vla_octo_tf_forward_dev", self.h, _dp(t5), _dp(stem_p), _dp(stem_w), wnd, _ptr(tm),
+              _dp(out), _stream(stream))
+
+
+class SmolvlaChunk(_Handle):
+    """Device SmolVLA action chunk: text-tower prefix + expert denoise (vla_smolvla_tf_*)."""
+
+    _load, _free = "vla_smolvla_tf_load", "vla_smolvla_tf_free"
+
+    def __init__(self, dirpath: str, int8_mask: int = 48):
+        super().__init__(lib().vla_smolvla_tf_load(dirpath.encode(), int8_mask))
+        L = lib()
+        self.chunk, self.max_action_dim = L.vla_smolvla_tf_chunk(self.h), L.vla_smolvla_tf_max_action_dim(self.h)
+        self.hidden = L.vla_smolvla_tf_hidden(self.h)
+        self.int8_layers = L.vla_smolvla_tf_int8_layers(self.h)
+
+    @property
+    def graph_nodes(self):
+        return lib().vla_smolvla_tf_graph_nodes(self.h)
+
+    def run(self, prefix, pad, noise):
+        prefix, noise = _f32(prefix), _f32(noise)
+        pad = np.ascontiguousarray(pad, dtype=np.int32)
+        out = np.empty((self.chunk, self.max_action_dim), np.float32)
+        _call("vla_smolvla_tf_chunk_run", self.h, _ptr(prefix), _ptr(pad), prefix.shape[0], _ptr(noise),
+              _ptr(out))
+        return out
+
+    def run_dev(self, prefix, pad, noise, out, stream=None):
+        pad = np.ascontiguousarray(pad, dtype=np.int32)
+        _call("vla_smolvla_tf_chunk_dev", self.h, _dp(prefix), _ptr(pad), prefix.shape[0], _dp(noise),
+              _dp(out), _stream(stream))

@@ -1,0 +1,233 @@
+"""Random-init checkpoints in the reference's own file layouts, for the graph
+parity tests and the per-chunk latency bench (there is no network for real
+checkpoints; BASELINE.json's configs 3-5 are random-init).
+
+Each writer produces exactly what the reference's loader reads, in its order:
+
+  ACT      act.meta ("key value" lines) + act.bin, the float arena walk of
+           ActTransformer::load (src/models/act/act_transformer.cpp:29-170)
+  Octo     octo.meta + octo.bin, OctoTransformer::load
+           (src/models/octo/octo_transformer.cpp:17-99)
+  SmolVLA  vlm.meta + vlm.bin (fp32 norms, then bf16 matrices,
+           src/models/smolvla/smollm2_lm.cpp:17-83) and aex.meta + aex.bin
+           (fp32, src/models/smolvla/action_expert.cpp:60-172)
+
+Values come from vla_simd_amd.synth (seeded, machine-independent bytes):
+linear weights U(-1/sqrt(K), 1/sqrt(K)) (torch nn.Linear's default scale),
+biases N(0, 0.02^2), norm scales 1 + N(0, 0.02^2), norm biases N(0, 0.02^2),
+learned position embeddings N(0, 0.02^2) (Octo, flax) or N(0, 1) (ACT, torch
+nn.Embedding).
+"""
+
+from __future__ import annotations
+
+import math
+import os
+
+import numpy as np
+
+from . import synth
+
+# ACT, encoder 4 x 302 tokens (15 x 20 feature grid
+# + latent + state), d 512, 8 heads, FFN 3200 ReLU, decoder 1 x 100 queries,
+# 14-dim action head.
+ACT_BASE = dict(dim=512, heads=8, head_dim=64, ff=3200, n_enc=4, n_dec=1, chunk=100,
+                state_dim=14, action_dim=14, n_1d=2, n_text=0, ln_eps=1e-5,
+                img_ch=512, n_cams=1, fh=15, fw=20)
+
+# Octo-base shape, 12 x 768, 12 heads, MLP 3072
+# gelu-tanh, 2 timesteps of 256 primary + 64 wrist patches and one readout,
+# 16 task tokens (658 tokens without the per-step task copy).
+OCTO_BASE = dict(d=768, n_layers=12, heads=12, head_dim=64, mlp=3072, max_horizon=10, n_task=16,
+                 tok_primary=256, tok_wrist=64, n_readout=1, t5_dim=768, stem_dim=512,
+                 ln_eps=1e-6, gelu_erf=0, repeat_task=0, wnd=2)
+
+# SmolVLA-shaped chunk, 16 text layers (960, 15q/5kv,
+# hd 64, FFN 2560), prefix 2 x 64 image + 48 text + 1 state = 177 tokens,
+# expert 16 layers of 720 (FFN 2048), chunk 50, 10 Euler steps.
+SMOLVLA_BASE = dict(hidden=960, n_q=15, n_kv=5, head_dim=64, ffn=2560, eps=1e-5, rope_base=10000.0,
+                    n_layers=16, expert_h=720, expert_ffn=2048, expert_layers=16,
+                    self_attn_every_n=2, chunk=50, num_steps=10, max_action_dim=32,
+                    min_period=4e-3, max_period=4.0, n_prefix=177)
+
+
+class _Arena:
+    """Collects float32 blocks in file order."""
+
+    def __init__(self, tag: str, seed: int):
+        self.tag, self.seed, self.parts = tag, seed, []
+
+    def linear(self, name, N, K, bias=True):
+        a = 1.0 / math.sqrt(K)
+        self.parts.append(synth.uniform(f"{self.tag}.{name}.w", (N, K), -a, a, self.seed))
+        if bias:
+            self.parts.append(synth.normal(f"{self.tag}.{name}.b", (N,), 0.02, self.seed))
+
+    def norm(self, name, n, bias=True):
+        self.parts.append(1.0 + synth.normal(f"{self.tag}.{name}.s", (n,), 0.02, self.seed))
+        if bias:
+            self.parts.append(synth.normal(f"{self.tag}.{name}.b", (n,), 0.02, self.seed))
+
+    def normal(self, name, shape, std):
+        self.parts.append(synth.normal(f"{self.tag}.{name}", shape, std, self.seed))
+
+    def write(self, path):
+        with open(path, "wb") as f:
+            for p in self.parts:
+                f.write(np.ascontiguousarray(p, dtype=np.float32).tobytes())
+
+
+def _meta(path, kv):
+    with open(path, "w") as f:
+        for k, v in kv.items():
+            f.write(f"{k} {v}\n")
+
+
+def write_act(dirpath: str, cfg: dict = ACT_BASE, seed: int = synth.BASE_SEED) -> str:
+    os.makedirs(dirpath, exist_ok=True)
+    c = cfg
+    d = c["dim"]
+    _meta(os.path.join(dirpath, "act.meta"),
+          {k: c[k] for k in ("dim", "heads", "head_dim", "ff", "n_enc", "n_dec", "chunk", "state_dim",
+                             "action_dim", "n_1d", "n_text", "ln_eps")})
+    a = _Arena("act", seed)
+    a.linear("img_proj", d, c["img_ch"])
+    a.linear("state_proj", d, c["state_dim"])
+    a.normal("latent", (d,), 1.0)
+    a.normal("pos1d", (c["n_1d"], d), 1.0)
+
+    def mha(p):
+        for w in ("q", "k", "v", "o"):
+            a.linear(f"{p}.{w}", d, d)
+
+    for i in range(c["n_enc"]):
+        mha(f"enc{i}.attn")
+        a.norm(f"enc{i}.n1", d)
+        a.linear(f"enc{i}.w1", c["ff"], d)
+        a.linear(f"enc{i}.w2", d, c["ff"])
+        a.norm(f"enc{i}.n2", d)
+    for i in range(c["n_dec"]):
+        mha(f"dec{i}.self")
+        a.norm(f"dec{i}.n1", d)
+        mha(f"dec{i}.cross")
+        a.norm(f"dec{i}.n2", d)
+        a.linear(f"dec{i}.w1", c["ff"], d)
+        a.linear(f"dec{i}.w2", d, c["ff"])
+        a.norm(f"dec{i}.n3", d)
+    a.normal("dec_pos", (c["chunk"], d), 1.0)
+    a.norm("dec_norm", d)
+    a.linear("head", c["action_dim"], d)
+    a.write(os.path.join(dirpath, "act.bin"))
+    return dirpath
+
+
+def act_inputs(cfg: dict = ACT_BASE, seed: int = synth.BASE_SEED):
+    feats = synth.normal("act.in.feats", (cfg["n_cams"] * cfg["fh"] * cfg["fw"], cfg["img_ch"]), 1.0, seed)
+    state = synth.normal("act.in.state", (cfg["state_dim"],), 1.0, seed)
+    return feats, state
+
+
+def write_octo(dirpath: str, cfg: dict = OCTO_BASE, seed: int = synth.BASE_SEED) -> str:
+    os.makedirs(dirpath, exist_ok=True)
+    c = cfg
+    D = c["d"]
+    keys = ("d", "n_layers", "heads", "head_dim", "mlp", "max_horizon", "n_task", "tok_primary",
+            "tok_wrist", "n_readout", "t5_dim", "stem_dim", "ln_eps", "gelu_erf", "repeat_task")
+    _meta(os.path.join(dirpath, "octo.meta"), {k: c[k] for k in keys if k in c})
+    a = _Arena("octo", seed)
+    a.linear("proj_task", D, c["t5_dim"])
+    a.linear("proj_prim", D, c["stem_dim"])
+    a.linear("proj_wrist", D, c["stem_dim"])
+    a.normal("pos_task", (c["n_task"], D), 0.02)
+    a.normal("pos_prim", (c["max_horizon"], c["tok_primary"], D), 0.02)
+    a.normal("pos_wrist", (c["max_horizon"], c["tok_wrist"], D), 0.02)
+    a.normal("pos_readout", (c["max_horizon"], c["n_readout"], D), 0.02)
+    for i in range(c["n_layers"]):
+        a.norm(f"l{i}.ln1", D)
+        for w in ("q", "k", "v", "o"):
+            a.linear(f"l{i}.{w}", D, D)
+        a.norm(f"l{i}.ln2", D)
+        a.linear(f"l{i}.w1", c["mlp"], D)
+        a.linear(f"l{i}.w2", D, c["mlp"])
+    a.norm("final", D)
+    a.write(os.path.join(dirpath, "octo.bin"))
+    return dirpath
+
+
+def octo_inputs(cfg: dict = OCTO_BASE, seed: int = synth.BASE_SEED):
+    w = cfg["wnd"]
+    t5 = synth.normal("octo.in.t5", (cfg["n_task"], cfg["t5_dim"]), 1.0, seed)
+    sp = synth.normal("octo.in.prim", (w, cfg["tok_primary"], cfg["stem_dim"]), 1.0, seed)
+    sw = synth.normal("octo.in.wrist", (w, cfg["tok_wrist"], cfg["stem_dim"]), 1.0, seed)
+    tmask = np.ones(w, np.uint8)
+    return t5, sp, sw, tmask
+
+
+def _bf16(x: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bits, round to nearest even (what a bf16 checkpoint holds)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    r = (u + np.uint32(0x7FFF) + ((u >> np.uint32(16)) & np.uint32(1))) >> np.uint32(16)
+    return r.astype(np.uint16)
+
+
+def write_smolvla(dirpath: str, cfg: dict = SMOLVLA_BASE, seed: int = synth.BASE_SEED) -> str:
+    os.makedirs(dirpath, exist_ok=True)
+    c = cfg
+    H, NL, F = c["hidden"], c["n_layers"], c["ffn"]
+    QF, KV = c["n_q"] * c["head_dim"], c["n_kv"] * c["head_dim"]
+    _meta(os.path.join(dirpath, "vlm.meta"),
+          {"hidden": H, "n_q": c["n_q"], "n_kv": c["n_kv"], "head_dim": c["head_dim"], "ffn": F,
+           "eps": c["eps"], "rope_base": c["rope_base"], "n_layers": NL})
+    norms = []
+    for L in range(NL):
+        norms.append(1.0 + synth.normal(f"vlm.l{L}.ln_in", (H,), 0.02, seed))
+        norms.append(1.0 + synth.normal(f"vlm.l{L}.ln_post", (H,), 0.02, seed))
+    norms.append(1.0 + synth.normal("vlm.out_norm", (H,), 0.02, seed))
+    with open(os.path.join(dirpath, "vlm.bin"), "wb") as f:
+        for p in norms:
+            f.write(np.asarray(p, np.float32).tobytes())
+        for L in range(NL):
+            for name, (N, K) in (("q", (QF, H)), ("k", (KV, H)), ("v", (KV, H)), ("o", (H, QF)),
+                                 ("gate", (F, H)), ("up", (F, H)), ("down", (H, F))):
+                a = 1.0 / math.sqrt(K)
+                f.write(_bf16(synth.uniform(f"vlm.l{L}.{name}", (N, K), -a, a, seed)).tobytes())
+
+    EH, EF, ENL = c["expert_h"], c["expert_ffn"], c["expert_layers"]
+    MAD, san = c["max_action_dim"], c["self_attn_every_n"]
+    _meta(os.path.join(dirpath, "aex.meta"),
+          {"expert_h": EH, "expert_ffn": EF, "n_q": c["n_q"], "n_kv": c["n_kv"],
+           "head_dim": c["head_dim"], "eps": c["eps"], "rope_base": c["rope_base"], "n_layers": ENL,
+           "self_attn_every_n": san, "chunk": c["chunk"], "num_steps": c["num_steps"],
+           "max_action_dim": MAD, "min_period": c["min_period"], "max_period": c["max_period"]})
+    a = _Arena("aex", seed)
+    for L in range(ENL):
+        self_attn = san > 0 and L % san == 0
+        kk = EH if self_attn else KV
+        a.norm(f"l{L}.ln_in", EH, bias=False)
+        a.linear(f"l{L}.q", QF, EH, bias=False)
+        a.linear(f"l{L}.k", KV, kk, bias=False)
+        a.linear(f"l{L}.v", KV, kk, bias=False)
+        a.linear(f"l{L}.o", EH, QF, bias=False)
+        a.norm(f"l{L}.ln_post", EH, bias=False)
+        a.linear(f"l{L}.gate", EF, EH, bias=False)
+        a.linear(f"l{L}.up", EF, EH, bias=False)
+        a.linear(f"l{L}.down", EH, EF, bias=False)
+    a.norm("out_norm", EH, bias=False)
+    a.linear("action_in", EH, MAD)
+    a.linear("action_time_in", EH, 2 * EH)
+    a.linear("action_time_out", EH, EH)
+    a.linear("action_out", MAD, EH)
+    a.write(os.path.join(dirpath, "aex.bin"))
+    return dirpath
+
+
+def smolvla_inputs(cfg: dict = SMOLVLA_BASE, seed: int = synth.BASE_SEED, n_pad: int = 0):
+    """prefix [n_prefix, hidden] ~ N(0,1), pad [n_prefix] (n_pad text slots
+    before the state token marked as padding), noise [chunk, max_action_dim] ~ N(0,1)."""
+    n = cfg["n_prefix"]
+    prefix = synth.normal("smolvla.in.prefix", (n, cfg["hidden"]), 1.0, seed)
+    pad = np.ones(n, np.int32)
+    if n_pad:
+        pad[n - 1 - n_pad:n - 1] = 0
+    noise = synth.normal("smolvla.in.noise", (cfg["chunk"], cfg["max_action_dim"]), 1.0, seed)
+    return prefix, pad, noise

@@ -7,6 +7,7 @@
 //   gelu_tanh  0.5 x (1 + tanh(c (x + 0.044715 x^3))), c = sqrt(2/pi)  (:120-127)
 //   gelu_erf   0.5 x (1 + erf(x / sqrt 2))          (:200-206)
 //   silu_gate  (g / (1 + exp(-g))) * u              (:58-63)
+//   silu       x / (1 + exp(-x))                    (:66-72)
 // evaluated with ROCm's device libm (tanhf, erff, expf). The reference's SIMD
 // paths replace tanh/erf/exp with Cephes-style polynomials; both sit within
 // the tests' 2e-6 relative class of the double-precision formula.
@@ -33,12 +34,17 @@ __device__ __forceinline__ float act_silu_gate(float g, float u) {
     return (g / (1.0f + expf(-g))) * u;
 }
 
-// act: 0 none, 1 relu, 2 gelu_tanh, 3 gelu_erf (vla_act)
+// x / (1 + exp(-x)): the SiLU of action_time_mlp_in
+// (src/models/smolvla/action_expert.cpp:209)
+__device__ __forceinline__ float act_silu(float v) { return v / (1.0f + expf(-v)); }
+
+// act: 0 none, 1 relu, 2 gelu_tanh, 3 gelu_erf, 4 silu (vla_act)
 template <int ACT>
 __device__ __forceinline__ float apply_act(float v) {
     if (ACT == 1) return act_relu(v);
     if (ACT == 2) return act_gelu_tanh(v);
     if (ACT == 3) return act_gelu_erf(v);
+    if (ACT == 4) return act_silu(v);
     return v;
 }
 

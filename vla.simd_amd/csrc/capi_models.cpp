@@ -1,0 +1,203 @@
+// capi_models.cpp - extern "C" entry points of the device policy graphs
+// (models.h). Handles own their weights, buffers, stream and captured graph;
+// one inference per handle at a time (include/vla_simd.h:22-25). Host-pointer
+// forms upload, run on a private stream and synchronize; _dev forms take
+// device pointers and a hipStream_t and return without waiting.
+
+#include "vla_simd_hip.h"
+
+#include "models.h"
+#include "runtime.h"
+
+#include <memory>
+
+using namespace vla::hip;
+
+struct vla_act_tf {
+    std::unique_ptr<ActTf> m;
+};
+struct vla_octo_tf {
+    std::unique_ptr<OctoTf> m;
+};
+struct vla_smolvla_tf {
+    std::unique_ptr<SmolvlaTf> m;
+};
+
+namespace {
+
+hipStream_t as_stream(void* s) { return static_cast<hipStream_t>(s); }
+
+// Upload / run / download on a private stream for the host-pointer forms.
+struct HostCall {
+    hipStream_t st = nullptr;
+    std::vector<void*> bufs;
+    HostCall() { VLA_HIP_CHECK(hipStreamCreateWithFlags(&st, hipStreamNonBlocking)); }
+    ~HostCall() {
+        if (st) (void)hipStreamSynchronize(st);
+        for (void* p : bufs) (void)hipFree(p);
+        if (st) (void)hipStreamDestroy(st);
+    }
+    void* raw(size_t bytes) {
+        void* p = nullptr;
+        VLA_HIP_CHECK(hipMalloc(&p, bytes ? bytes : 16));
+        bufs.push_back(p);
+        return p;
+    }
+    template <class T>
+    T* up(const T* h, size_t n) {
+        if (!h) return nullptr;
+        T* p = static_cast<T*>(raw(n * sizeof(T)));
+        VLA_HIP_CHECK(hipMemcpyAsync(p, h, n * sizeof(T), hipMemcpyHostToDevice, st));
+        return p;
+    }
+    float* out(size_t n) { return static_cast<float*>(raw(n * 4)); }
+    void down(float* h, const float* d, size_t n) {
+        VLA_HIP_CHECK(hipMemcpyAsync(h, d, n * 4, hipMemcpyDeviceToHost, st));
+        VLA_HIP_CHECK(hipStreamSynchronize(st));
+    }
+};
+
+template <class H, class F>
+H* load_handle(const char* where, F&& make) {
+    H* h = nullptr;
+    const int32_t rc = guarded(where, [&] {
+        auto p = std::make_unique<H>();
+        p->m = make();
+        h = p.release();
+    });
+    return rc == 0 ? h : nullptr;
+}
+
+}  // namespace
+
+extern "C" {
+
+// ------------------------------------------------------------------- ACT --
+
+VLA_API vla_act_tf* vla_act_tf_load(const char* dir, int32_t img_ch, int32_t int8_mask) {
+    return load_handle<vla_act_tf>("vla_act_tf_load", [&] {
+        VLA_REQUIRE(dir, "null directory");
+        return std::make_unique<ActTf>(dir, img_ch, int8_mask);
+    });
+}
+VLA_API void vla_act_tf_free(vla_act_tf* h) { delete h; }
+VLA_API int32_t vla_act_tf_chunk(const vla_act_tf* h) { return h ? h->m->chunk() : 0; }
+VLA_API int32_t vla_act_tf_action_dim(const vla_act_tf* h) { return h ? h->m->action_dim() : 0; }
+VLA_API int32_t vla_act_tf_state_dim(const vla_act_tf* h) { return h ? h->m->state_dim() : 0; }
+VLA_API int32_t vla_act_tf_dim(const vla_act_tf* h) { return h ? h->m->dim() : 0; }
+VLA_API int32_t vla_act_tf_int8_layers(const vla_act_tf* h) { return h ? h->m->int8_layers() : 0; }
+VLA_API int32_t vla_act_tf_graph_nodes(const vla_act_tf* h) { return h ? h->m->graph_nodes() : 0; }
+
+VLA_API int32_t vla_act_tf_forward_dev(vla_act_tf* h, const float* feats, int32_t n_cams, int32_t fh,
+                                       int32_t fw, const float* state_norm, float* actions_norm,
+                                       void* stream) {
+    return guarded("vla_act_tf_forward_dev", [&] {
+        VLA_REQUIRE(h, "null handle");
+        h->m->forward_dev(feats, n_cams, fh, fw, state_norm, actions_norm, as_stream(stream));
+    });
+}
+
+VLA_API int32_t vla_act_tf_forward(vla_act_tf* h, const float* feats, int32_t n_cams, int32_t fh,
+                                   int32_t fw, const float* state_norm, float* actions_norm) {
+    return guarded("vla_act_tf_forward", [&] {
+        VLA_REQUIRE(h && feats && state_norm && actions_norm, "null handle or buffer");
+        VLA_REQUIRE(n_cams > 0 && fh > 0 && fw > 0, "camera grid out of range");
+        ActTf& m = *h->m;
+        HostCall hc;
+        const float* df = hc.up(feats, (size_t)n_cams * fh * fw * m.img_ch());
+        const float* ds = hc.up(state_norm, (size_t)m.state_dim());
+        const size_t na = (size_t)m.chunk() * m.action_dim();
+        float* da = hc.out(na);
+        m.forward_dev(df, n_cams, fh, fw, ds, da, hc.st);
+        hc.down(actions_norm, da, na);
+    });
+}
+
+// ------------------------------------------------------------------ Octo --
+
+VLA_API vla_octo_tf* vla_octo_tf_load(const char* dir, int32_t int8_mask) {
+    return load_handle<vla_octo_tf>("vla_octo_tf_load", [&] {
+        VLA_REQUIRE(dir, "null directory");
+        return std::make_unique<OctoTf>(dir, int8_mask);
+    });
+}
+VLA_API void vla_octo_tf_free(vla_octo_tf* h) { delete h; }
+VLA_API int32_t vla_octo_tf_dim(const vla_octo_tf* h) { return h ? h->m->d() : 0; }
+VLA_API int32_t vla_octo_tf_total_tokens(const vla_octo_tf* h, int32_t wnd) {
+    return h ? h->m->total_tokens(wnd) : 0;
+}
+VLA_API int32_t vla_octo_tf_readout_index(const vla_octo_tf* h, int32_t wnd) {
+    return h ? h->m->readout_index(wnd) : 0;
+}
+VLA_API int32_t vla_octo_tf_int8_layers(const vla_octo_tf* h) { return h ? h->m->int8_layers() : 0; }
+VLA_API int32_t vla_octo_tf_graph_nodes(const vla_octo_tf* h) { return h ? h->m->graph_nodes() : 0; }
+
+VLA_API int32_t vla_octo_tf_forward_dev(vla_octo_tf* h, const float* t5_out, const float* stem_p,
+                                        const float* stem_w, int32_t wnd, const uint8_t* timestep_mask,
+                                        float* out, void* stream) {
+    return guarded("vla_octo_tf_forward_dev", [&] {
+        VLA_REQUIRE(h, "null handle");
+        h->m->forward_dev(t5_out, stem_p, stem_w, wnd, timestep_mask, out, as_stream(stream));
+    });
+}
+
+VLA_API int32_t vla_octo_tf_forward(vla_octo_tf* h, const float* t5_out, const float* stem_p,
+                                    const float* stem_w, int32_t wnd, const uint8_t* timestep_mask,
+                                    float* out) {
+    return guarded("vla_octo_tf_forward", [&] {
+        VLA_REQUIRE(h && t5_out && stem_p && timestep_mask && out, "null handle or buffer");
+        OctoTf& m = *h->m;
+        VLA_REQUIRE(wnd >= 1 && wnd <= m.max_horizon(), "window must be in [1, max_horizon]");
+        HostCall hc;
+        const float* dt = hc.up(t5_out, (size_t)m.n_task() * m.t5_dim());
+        const float* dp = hc.up(stem_p, (size_t)wnd * m.tok_primary() * m.stem_dim());
+        const float* dw = stem_w ? hc.up(stem_w, (size_t)wnd * m.tok_wrist() * m.stem_dim()) : nullptr;
+        float* dout = hc.out((size_t)m.d());
+        m.forward_dev(dt, dp, dw, wnd, timestep_mask, dout, hc.st);
+        hc.down(out, dout, (size_t)m.d());
+    });
+}
+
+// --------------------------------------------------------------- SmolVLA --
+
+VLA_API vla_smolvla_tf* vla_smolvla_tf_load(const char* dir, int32_t int8_mask) {
+    return load_handle<vla_smolvla_tf>("vla_smolvla_tf_load", [&] {
+        VLA_REQUIRE(dir, "null directory");
+        return std::make_unique<SmolvlaTf>(dir, int8_mask);
+    });
+}
+VLA_API void vla_smolvla_tf_free(vla_smolvla_tf* h) { delete h; }
+VLA_API int32_t vla_smolvla_tf_chunk(const vla_smolvla_tf* h) { return h ? h->m->chunk() : 0; }
+VLA_API int32_t vla_smolvla_tf_max_action_dim(const vla_smolvla_tf* h) {
+    return h ? h->m->max_action_dim() : 0;
+}
+VLA_API int32_t vla_smolvla_tf_hidden(const vla_smolvla_tf* h) { return h ? h->m->hidden() : 0; }
+VLA_API int32_t vla_smolvla_tf_int8_layers(const vla_smolvla_tf* h) { return h ? h->m->int8_layers() : 0; }
+VLA_API int32_t vla_smolvla_tf_graph_nodes(const vla_smolvla_tf* h) { return h ? h->m->graph_nodes() : 0; }
+
+VLA_API int32_t vla_smolvla_tf_chunk_dev(vla_smolvla_tf* h, const float* prefix, const int32_t* pad,
+                                         int32_t n_prefix, const float* noise, float* actions,
+                                         void* stream) {
+    return guarded("vla_smolvla_tf_chunk_dev", [&] {
+        VLA_REQUIRE(h, "null handle");
+        h->m->chunk_dev(prefix, pad, n_prefix, noise, actions, as_stream(stream));
+    });
+}
+
+VLA_API int32_t vla_smolvla_tf_chunk_run(vla_smolvla_tf* h, const float* prefix, const int32_t* pad,
+                                         int32_t n_prefix, const float* noise, float* actions) {
+    return guarded("vla_smolvla_tf_chunk_run", [&] {
+        VLA_REQUIRE(h && prefix && pad && noise && actions, "null handle or buffer");
+        VLA_REQUIRE(n_prefix >= 2, "prefix too short");
+        SmolvlaTf& m = *h->m;
+        HostCall hc;
+        const float* dp = hc.up(prefix, (size_t)n_prefix * m.hidden());
+        const size_t na = (size_t)m.chunk() * m.max_action_dim();
+        const float* dn = hc.up(noise, na);
+        float* da = hc.out(na);
+        m.chunk_dev(dp, pad, n_prefix, dn, da, hc.st);
+        hc.down(actions, da, na);
+    });
+}
+
+}  // extern "C"

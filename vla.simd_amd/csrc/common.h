@@ -99,8 +99,19 @@ void launch_rmsnorm(float* out, const float* x, const float* w, int rows, int hi
 void launch_act(float* x, int64_t n, int act, hipStream_t st);
 void launch_silu_gate(float* out, const float* g, const float* u, int64_t n, hipStream_t st);
 void launch_add(float* out, const float* a, const float* b, int64_t n, hipStream_t st);
+void launch_silu_gate_rows(float* out, int ldo, const float* g, int ldg, const float* u, int ldu,
+                           int rows, int cols, hipStream_t st);
 void launch_rope_neox(float* x, int ld, const int32_t* pos, int seq, int n_heads, int head_dim,
                       float base, hipStream_t st);
+// dst[r, c] = src[r, c] for a [rows, cols] block with row strides ldd / lds
+void launch_copy_rows(float* dst, int ldd, const float* src, int lds, int rows, int cols,
+                      hipStream_t st);
+
+// linear_f32.hip: out[m, n] = act(x[m,:] . W[n,:] + bias[n]); accumulate != 0
+// adds it as fmaf(alpha, v, out[m, n]). act as vla_act, plus 4 = silu.
+void launch_linear_f32(float* out, int ldo, const float* x, int ldx, const float* W, int ldw,
+                       const float* bias, int M, int N, int K, int act, int accumulate, float alpha,
+                       hipStream_t st);
 
 // runtime.cpp
 hipStream_t library_stream();  // stream of the host-pointer forms

@@ -83,6 +83,16 @@ __global__ __launch_bounds__(256) void silu_gate_kernel(float* out, const float*
         out[i] = act_silu_gate(g[i], u[i]);
 }
 
+// silu_gate over a [rows, cols] block whose g and u rows are strided (the
+// gate|up halves of one concatenated GEMM output)
+__global__ __launch_bounds__(256) void silu_gate_rows_kernel(float* out, int ldo, const float* g,
+                                                             int ldg, const float* u, int ldu,
+                                                             int cols) {
+    const int r = blockIdx.y;
+    for (int c = blockIdx.x * 256 + threadIdx.x; c < cols; c += gridDim.x * 256)
+        out[(size_t)r * ldo + c] = act_silu_gate(g[(size_t)r * ldg + c], u[(size_t)r * ldu + c]);
+}
+
 __global__ __launch_bounds__(256) void add_kernel(float* out, const float* a, const float* b,
                                                   int64_t n) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -107,6 +117,16 @@ __global__ __launch_bounds__(256) void rope_kernel(float* x, int ld, const int32
         v[i] = (float)(x0 * c - x1 * s);
         v[i + half] = (float)(x0 * s + x1 * c);
     }
+}
+
+// one block per row segment of 1024 floats
+__global__ __launch_bounds__(256) void copy_rows_kernel(float* dst, int ldd, const float* src,
+                                                        int lds, int cols) {
+    const int r = blockIdx.y;
+    const int c = blockIdx.x * 1024 + threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        if (c + 256 * j < cols) dst[(size_t)r * ldd + c + 256 * j] = src[(size_t)r * lds + c + 256 * j];
 }
 
 int grid_for(int64_t n) {
@@ -151,10 +171,29 @@ void launch_silu_gate(float* out, const float* g, const float* u, int64_t n, hip
     VLA_LAUNCH_CHECK();
 }
 
+void launch_silu_gate_rows(float* out, int ldo, const float* g, int ldg, const float* u, int ldu,
+                           int rows, int cols, hipStream_t st) {
+    VLA_REQUIRE(rows >= 0 && rows < 65536 && cols >= 0 && ldo >= cols && ldg >= cols && ldu >= cols,
+                "silu_gate_rows: bad shape");
+    if (rows == 0 || cols == 0) return;
+    const int gx = (cols + 255) / 256 < 8 ? (cols + 255) / 256 : 8;
+    silu_gate_rows_kernel<<<dim3(gx, rows), 256, 0, st>>>(out, ldo, g, ldg, u, ldu, cols);
+    VLA_LAUNCH_CHECK();
+}
+
 void launch_add(float* out, const float* a, const float* b, int64_t n, hipStream_t st) {
     VLA_REQUIRE(n >= 0, "add: n < 0");
     if (n == 0) return;
     add_kernel<<<grid_for(n), 256, 0, st>>>(out, a, b, n);
+    VLA_LAUNCH_CHECK();
+}
+
+void launch_copy_rows(float* dst, int ldd, const float* src, int lds, int rows, int cols,
+                      hipStream_t st) {
+    VLA_REQUIRE(rows >= 0 && cols >= 0 && ldd >= cols && lds >= cols, "copy_rows: bad shape");
+    VLA_REQUIRE(rows < 65536, "copy_rows: too many rows");
+    if (rows == 0 || cols == 0) return;
+    copy_rows_kernel<<<dim3((cols + 1023) / 1024, rows), 256, 0, st>>>(dst, ldd, src, lds, cols);
     VLA_LAUNCH_CHECK();
 }
 

@@ -1,0 +1,225 @@
+// graph.cpp - see graph.h.
+#include "graph.h"
+
+#include <cstdlib>
+#include <fstream>
+#include <sstream>
+
+namespace vla {
+namespace hip {
+
+DeviceArena::~DeviceArena() {
+    for (void* p : blocks_) (void)hipFree(p);
+}
+
+void* DeviceArena::raw(size_t bytes) {
+    const size_t b = (bytes + 255) & ~(size_t)255;
+    void* p = nullptr;
+    VLA_HIP_CHECK(hipMalloc(&p, b ? b : 256));
+    blocks_.push_back(p);
+    VLA_HIP_CHECK(hipMemset(p, 0, b ? b : 256));
+    bytes_ += b;
+    return p;
+}
+
+void DLinear::init(DeviceArena& A, const std::vector<RowBlock>& blocks, int K_, bool to_int8) {
+    VLA_REQUIRE(K_ > 0 && !blocks.empty(), "linear: need K > 0 and at least one block");
+    int n = 0;
+    for (const RowBlock& r : blocks) {
+        VLA_REQUIRE(r.W && r.N > 0, "linear: null weights or empty block");
+        n += r.N;
+    }
+    N = n;
+    K = K_;
+    std::vector<float> W32((size_t)N * K), b32((size_t)N, 0.0f);
+    bool any_bias = false;
+    size_t row = 0;
+    for (const RowBlock& r : blocks) {
+        std::memcpy(W32.data() + row * K, r.W, (size_t)r.N * K * sizeof(float));
+        if (r.bias) {
+            std::memcpy(b32.data() + row, r.bias, (size_t)r.N * sizeof(float));
+            any_bias = true;
+        }
+        row += r.N;
+    }
+    if (to_int8) {
+        q8 = vla_linear_i8::from_f32(W32.data(), any_bias ? b32.data() : nullptr, N, K);
+    } else {
+        W = A.upload(W32.data(), W32.size());
+        b = any_bias ? A.upload(b32.data(), b32.size()) : nullptr;
+    }
+}
+
+void quantize(const Ctx& c, const float* x, int ldx, int seq, int K, int ldq) {
+    VLA_REQUIRE((size_t)seq * ldq <= c.xq_bytes && seq <= c.xs_rows,
+                "graph: activation quantization scratch too small");
+    launch_quantize_rows(x, ldx, c.xq, ldq, c.xs, seq, K, c.st);
+}
+
+static void gemm_q(const Ctx& c, const DLinear& L, float* out, int ldo, int seq, int act, int acc,
+                   int n0, int n1) {
+    const vla_linear_i8& q = *L.q8;
+    GemmArgs a{};
+    a.A = c.xq;
+    a.lda = q.ldw();
+    a.B = q.Wq() + (size_t)n0 * q.ldw();
+    a.ldb = q.ldw();
+    a.ascale = c.xs;
+    a.wscale = q.wscale() + n0;
+    a.bias = q.bias() ? q.bias() + n0 : nullptr;
+    a.out = out;
+    a.ldo = ldo;
+    a.M = seq;
+    a.N = n1 - n0;
+    a.K = L.K;
+    a.act = act;
+    a.accumulate = acc;
+    launch_gemm_i8(a, c.st);
+}
+
+void linear(const Ctx& c, const DLinear& L, float* out, int ldo, const float* x, int ldx, int seq,
+            int act, int acc, int n0, int n1, float alpha) {
+    if (n1 < 0) n1 = L.N;
+    VLA_REQUIRE(0 <= n0 && n0 < n1 && n1 <= L.N, "linear: bad output row range");
+    if (seq == 0) return;
+    if (L.int8()) {
+        VLA_REQUIRE(alpha == 1.0f, "linear: the int8 epilogue accumulates with alpha = 1 only");
+        VLA_REQUIRE(act <= 3, "linear: the int8 epilogue has no silu");
+        quantize(c, x, ldx, seq, L.K, L.ldq());
+        gemm_q(c, L, out, ldo, seq, act, acc, n0, n1);
+    } else {
+        launch_linear_f32(out, ldo, x, ldx, L.W + (size_t)n0 * L.K, L.K, L.b ? L.b + n0 : nullptr, seq,
+                          n1 - n0, L.K, act, acc, alpha, c.st);
+    }
+}
+
+void linear_q(const Ctx& c, const DLinear& L, float* out, int ldo, int seq, int act, int acc, int n0,
+              int n1) {
+    if (n1 < 0) n1 = L.N;
+    VLA_REQUIRE(L.int8(), "linear_q: layer is not int8");
+    VLA_REQUIRE(0 <= n0 && n0 < n1 && n1 <= L.N, "linear: bad output row range");
+    if (seq == 0) return;
+    gemm_q(c, L, out, ldo, seq, act, acc, n0, n1);
+}
+
+void attend(hipStream_t st, float* out, int ldo, const float* Q, int ldq, const float* K, int ldk,
+            const float* V, int ldv, int sq, int sk, int nq, int nkv, int hd, float scale,
+            const MaskSpec& m) {
+    AttnArgs a{};
+    a.out = out;
+    a.ldo = ldo;
+    a.Q = Q;
+    a.ldq = ldq;
+    a.K = K;
+    a.ldk = ldk;
+    a.V = V;
+    a.ldv = ldv;
+    a.seq_q = sq;
+    a.seq_k = sk;
+    a.n_q = nq;
+    a.n_kv = nkv;
+    a.head_dim = hd;
+    a.scale = scale;
+    a.mask_kind = m.kind;
+    a.mask = m.dense;
+    a.ldm = m.ldm;
+    a.causal_offset = m.causal_offset;
+    a.n_groups = m.n_groups;
+    a.q_group = m.qg;
+    a.k_group = m.kg;
+    a.allow = m.allow;
+    launch_attention(a, st);
+}
+
+void copy_f32(float* dst, const float* src, int64_t n, hipStream_t st) {
+    VLA_REQUIRE(n >= 0 && n < (int64_t)1 << 31, "copy: size out of range");
+    launch_copy_rows(dst, (int)n, src, (int)n, 1, (int)n, st);
+}
+
+void copy_rows_f32(float* dst, int ldd, const float* src, int lds, int rows, int cols, hipStream_t st) {
+    launch_copy_rows(dst, ldd, src, lds, rows, cols, st);
+}
+
+// ---------------------------------------------------------------- replay --
+
+GraphReplay::~GraphReplay() { reset(); }
+
+void GraphReplay::reset() {
+    if (exec_) (void)hipGraphExecDestroy(exec_);
+    if (graph_) (void)hipGraphDestroy(graph_);
+    exec_ = nullptr;
+    graph_ = nullptr;
+    nodes_ = 0;
+}
+
+static bool graphs_enabled() {
+    static const bool on = [] {
+        const char* e = std::getenv("VLA_HIP_GRAPH");
+        return !(e && e[0] == '0');
+    }();
+    return on;
+}
+
+void GraphReplay::run(uint64_t key, hipStream_t own, hipStream_t caller,
+                      const std::function<void(hipStream_t)>& f) {
+    if (key != key_) {
+        reset();
+        key_ = key;
+        calls_ = 0;
+    }
+    calls_++;
+    if (!graphs_enabled() || calls_ == 1) {
+        // eager: on the caller's stream, ordered with its other work
+        f(caller);
+        return;
+    }
+    if (!exec_) {
+        // the caller's stream may be the null stream, which cannot be captured
+        VLA_HIP_CHECK(hipStreamSynchronize(caller));
+        VLA_HIP_CHECK(hipStreamBeginCapture(own, hipStreamCaptureModeThreadLocal));
+        try {
+            f(own);
+        } catch (...) {
+            hipGraph_t g = nullptr;
+            (void)hipStreamEndCapture(own, &g);
+            if (g) (void)hipGraphDestroy(g);
+            throw;
+        }
+        VLA_HIP_CHECK(hipStreamEndCapture(own, &graph_));
+        size_t n = 0;
+        VLA_HIP_CHECK(hipGraphGetNodes(graph_, nullptr, &n));
+        nodes_ = (int)n;
+        VLA_HIP_CHECK(hipGraphInstantiate(&exec_, graph_, nullptr, nullptr, 0));
+    }
+    VLA_HIP_CHECK(hipGraphLaunch(exec_, caller));
+}
+
+// ------------------------------------------------------------------ files --
+
+std::map<std::string, double> read_meta(const std::string& path) {
+    std::ifstream f(path);
+    if (!f) throw ArgError("cannot open " + path);
+    std::map<std::string, double> m;
+    std::string key;
+    double v;
+    while (f >> key) {
+        if (!(f >> v)) throw ArgError(path + ": key " + key + " has no numeric value");
+        m[key] = v;
+    }
+    return m;
+}
+
+std::vector<char> read_file(const std::string& path) {
+    std::ifstream f(path, std::ios::binary);
+    if (!f) throw ArgError("cannot open " + path);
+    f.seekg(0, std::ios::end);
+    const std::streamoff n = f.tellg();
+    f.seekg(0);
+    std::vector<char> d((size_t)n);
+    if (n > 0) f.read(d.data(), n);
+    if (!f) throw ArgError("cannot read " + path);
+    return d;
+}
+
+}  // namespace hip
+}  // namespace vla

@@ -1,0 +1,161 @@
+// graph.h - building blocks of the device-resident policy graphs: model-owned
+// device memory, a linear layer that is int8 or fp32 as the model's int8 mask
+// decides, the shared activation-quantization scratch, and HIP-graph replay of
+// a whole forward pass.
+//
+// These replace the pieces of the reference's src/nn layer that the ACT, Octo
+// and SmolVLA graphs drive: nn::Linear (src/nn/linear.h:40-99) with its int8
+// state held in HBM, the shared quantization of MhaQKV (src/nn/attention.cpp:40-59)
+// and nn::Scratch (src/nn/attention.h:17-22) as device buffers sized once.
+#pragma once
+
+#include "common.h"
+#include "linear.h"
+
+#include <cstdint>
+#include <cstring>
+#include <functional>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+namespace vla {
+namespace hip {
+
+// Device memory a model owns: every buffer is allocated at load (or on the
+// first call with a new shape) and freed with the model.
+class DeviceArena {
+public:
+    DeviceArena() = default;
+    DeviceArena(const DeviceArena&) = delete;
+    DeviceArena& operator=(const DeviceArena&) = delete;
+    ~DeviceArena();
+    void* raw(size_t bytes);  // zero-filled, 256-byte aligned
+    template <class T>
+    T* alloc(size_t n) {
+        return static_cast<T*>(raw(n * sizeof(T)));
+    }
+    template <class T>
+    T* upload(const T* host, size_t n) {
+        T* d = alloc<T>(n);
+        if (n) VLA_HIP_CHECK(hipMemcpy(d, host, n * sizeof(T), hipMemcpyHostToDevice));
+        return d;
+    }
+    size_t bytes() const { return bytes_; }
+
+private:
+    std::vector<void*> blocks_;
+    size_t bytes_ = 0;
+};
+
+// One block of rows of a (possibly row-concatenated) weight matrix, host fp32.
+struct RowBlock {
+    const float* W;     // [N, K]
+    const float* bias;  // [N] or null (a null bias adds +0.0f, as the reference's epilogue does)
+    int N;
+};
+
+// A linear layer as a model holds it. int8: device rows + per-row scales from
+// the pack_weights_i8 quantizer (bit-identical per row whether or not rows are
+// concatenated). fp32: the raw [N, K] weights. Row-concatenating layers that
+// read the same input (q|k|v, k|v, gate|up) keeps one quantization of that
+// input and one GEMM launch; each output block is bit-identical to its own
+// layer's forward.
+struct DLinear {
+    int N = 0, K = 0;
+    std::unique_ptr<vla_linear_i8> q8;
+    float* W = nullptr;  // fp32 form [N, K]
+    float* b = nullptr;  // fp32 form bias [N] (zeros where a block had none)
+    bool int8() const { return q8 != nullptr; }
+    int ldq() const { return q8 ? q8->ldw() : 0; }
+    void init(DeviceArena& A, const std::vector<RowBlock>& blocks, int K, bool to_int8);
+    void init(DeviceArena& A, const float* W, const float* bias, int N, int K, bool to_int8) {
+        init(A, {{W, bias, N}}, K, to_int8);
+    }
+};
+
+// Per-model stream state: the activation-quantization scratch shared by every
+// int8 layer (the reference's thread_local xq/ascale, src/nn/linear.cpp:123-127).
+struct Ctx {
+    hipStream_t st = nullptr;
+    int8_t* xq = nullptr;
+    float* xs = nullptr;
+    size_t xq_bytes = 0;
+    int xs_rows = 0;
+};
+
+// x [seq, K] (row stride ldx) -> ctx.xq [seq, ldq], ctx.xs [seq].
+void quantize(const Ctx& c, const float* x, int ldx, int seq, int K, int ldq);
+
+// out[:, n0:n1] (+)= act(x W[n0:n1]^T + b). int8 layers quantize x into the
+// context scratch first. acc != 0 adds into out (fmaf(alpha, v, out) for fp32
+// layers; the int8 epilogue adds v, alpha must be 1).
+void linear(const Ctx& c, const DLinear& L, float* out, int ldo, const float* x, int ldx, int seq,
+            int act = 0, int acc = 0, int n0 = 0, int n1 = -1, float alpha = 1.0f);
+// int8 layer on activations already in ctx.xq / ctx.xs (quantized with ldq = L.ldq()).
+void linear_q(const Ctx& c, const DLinear& L, float* out, int ldo, int seq, int act = 0, int acc = 0,
+              int n0 = 0, int n1 = -1);
+
+// Which keys a query may see (AttnArgs' mask fields): kind 0 none, 1 dense
+// additive [sq, ldm], 2 causal (key j blocked when j > i + causal_offset),
+// 3 group table (key j blocked when !allow[qg[i] * n_groups + kg[j]]).
+struct MaskSpec {
+    int kind = 0;
+    const float* dense = nullptr;
+    int ldm = 0;
+    int causal_offset = 0;
+    int n_groups = 0;
+    const uint8_t* qg = nullptr;
+    const uint8_t* kg = nullptr;
+    const uint8_t* allow = nullptr;
+};
+
+// gqa attention over row-strided Q [sq, ldq], K/V [sk, ldk/ldv] -> out [sq, ldo]
+void attend(hipStream_t st, float* out, int ldo, const float* Q, int ldq, const float* K, int ldk,
+            const float* V, int ldv, int sq, int sk, int nq, int nkv, int hd, float scale,
+            const MaskSpec& m);
+
+// device copy of n floats (a kernel, so it records as a kernel node in a graph)
+void copy_f32(float* dst, const float* src, int64_t n, hipStream_t st);
+// dst rows [rows, cols] with strides from src rows
+void copy_rows_f32(float* dst, int ldd, const float* src, int lds, int rows, int cols, hipStream_t st);
+
+// Replays one forward pass as a HIP graph. The first call with a new key runs
+// f eagerly (it also sets up lazily initialised kernels); the second captures
+// f on the model's own stream; later calls launch the captured graph on the
+// caller's stream. VLA_HIP_GRAPH=0 keeps every call eager.
+class GraphReplay {
+public:
+    GraphReplay() = default;
+    GraphReplay(const GraphReplay&) = delete;
+    GraphReplay& operator=(const GraphReplay&) = delete;
+    ~GraphReplay();
+    void run(uint64_t key, hipStream_t own, hipStream_t caller, const std::function<void(hipStream_t)>& f);
+    int nodes() const { return nodes_; }
+
+private:
+    void reset();
+    uint64_t key_ = ~0ull;
+    int calls_ = 0;
+    int nodes_ = 0;
+    hipGraph_t graph_ = nullptr;
+    hipGraphExec_t exec_ = nullptr;
+};
+
+// "key value" pairs of a reference .meta file (whitespace separated; the ACT
+// writer puts one per line, the Octo/SmolVLA writers the same).
+std::map<std::string, double> read_meta(const std::string& path);
+// A whole .bin as raw bytes.
+std::vector<char> read_file(const std::string& path);
+
+// Host fp32 -> the bf16 the reference's converters store (top 16 bits), and back.
+inline float bf16_to_f32(uint16_t h) {
+    uint32_t u = (uint32_t)h << 16;
+    float f;
+    std::memcpy(&f, &u, 4);
+    return f;
+}
+
+}  // namespace hip
+}  // namespace vla

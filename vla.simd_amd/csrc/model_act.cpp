@@ -1,0 +1,278 @@
+// model_act.cpp - the ACT transformer on the device (see models.h).
+//
+// Follows src/models/act/act_transformer.cpp: load() reads act.meta / act.bin
+// in the order of :29-170 (the same float arena walk), build_tokens :212-250,
+// encode :252-301, decode :303-356. What differs is only where values live and
+// how launches are grouped, never a value:
+//   - q and k of a self-attention read the same input (x + pos), so their
+//     weights are row-concatenated into one int8 layer: one quantization of the
+//     input (MhaQKV's shared_qk, src/nn/attention.cpp:40-59) and one GEMM;
+//   - the wo and w2 residual adds (x[i] += resid[i], :273-277, :286-290) are the
+//     GEMM epilogue's accumulate (x + v, the same single rounding);
+//   - relu after w1 (:283) is the GEMM epilogue's activation;
+//   - all cameras' tokens go through img_proj as one GEMM (quantization is per
+//     row, so batching rows changes nothing).
+#include "models.h"
+
+#include <cmath>
+
+namespace vla {
+namespace hip {
+
+namespace {
+
+// Float-arena cursor over a .bin (ArenaCursor, src/models/arena.h:68-80).
+struct Cursor {
+    const float* p;
+    size_t n, off = 0;
+    const float* take(size_t k) {
+        if (k > n - off) throw ArgError("checkpoint .bin is shorter than its .meta says");
+        const float* r = p + off;
+        off += k;
+        return r;
+    }
+};
+
+int meta_int(const std::map<std::string, double>& m, const char* k, int def) {
+    auto it = m.find(k);
+    if (it == m.end()) return def;
+    const double v = it->second;
+    VLA_REQUIRE(std::isfinite(v) && v == std::trunc(v) && v >= -2147483648.0 && v <= 2147483647.0,
+                std::string("meta key ") + k + " is not an integer");
+    return (int)v;
+}
+
+// ActTransformer::sinusoid_pos_2d (act_transformer.cpp:189-210): the 2D
+// sinusoidal camera embedding, the y half then the x half; float arithmetic
+// and float libm, as the reference computes it on the host.
+void sinusoid_pos_2d(int fh, int fw, int dim, float* out) {
+    const int half = dim / 2;
+    const float two_pi = 6.283185307179586f, eps = 1e-6f;
+    std::vector<float> inv_freq(half);
+    for (int c = 0; c < half; c++) inv_freq[c] = std::pow(10000.0f, (float)(2 * (c / 2)) / (float)half);
+    for (int i = 0; i < fh; i++) {
+        const float yr = (float)(i + 1) / ((float)fh + eps) * two_pi;
+        for (int j = 0; j < fw; j++) {
+            const float xr = (float)(j + 1) / ((float)fw + eps) * two_pi;
+            float* o = out + (size_t)(i * fw + j) * dim;
+            for (int c = 0; c < half; c++) {
+                const float y = yr / inv_freq[c], x = xr / inv_freq[c];
+                o[c] = (c & 1) ? std::cos(y) : std::sin(y);
+                o[half + c] = (c & 1) ? std::cos(x) : std::sin(x);
+            }
+        }
+    }
+}
+
+}  // namespace
+
+ActTf::ActTf(const std::string& dir, int img_ch, int int8_mask) {
+    const auto m = read_meta(dir + "/act.meta");
+    d_ = meta_int(m, "dim", d_);
+    heads_ = meta_int(m, "heads", heads_);
+    hd_ = meta_int(m, "head_dim", hd_);
+    ff_ = meta_int(m, "ff", ff_);
+    n_enc_ = meta_int(m, "n_enc", n_enc_);
+    n_dec_ = meta_int(m, "n_dec", n_dec_);
+    chunk_ = meta_int(m, "chunk", chunk_);
+    state_dim_ = meta_int(m, "state_dim", state_dim_);
+    action_dim_ = meta_int(m, "action_dim", action_dim_);
+    n_1d_ = meta_int(m, "n_1d", n_1d_);
+    if (m.count("ln_eps")) eps_ = (float)m.at("ln_eps");
+    img_ch_ = img_ch;
+    VLA_REQUIRE(d_ > 0 && d_ % 4 == 0 && heads_ > 0 && hd_ > 0 && heads_ * hd_ == d_ && ff_ > 0 &&
+                    chunk_ > 0 && state_dim_ > 0 && action_dim_ > 0 && img_ch > 0 && n_enc_ >= 1 &&
+                    n_dec_ >= 1 && n_1d_ == 2 && std::isfinite(eps_) && eps_ > 0,
+                "act.meta: invalid configuration (act_transformer.cpp:56-62 bounds)");
+
+    const std::vector<char> raw = read_file(dir + "/act.bin");
+    VLA_REQUIRE(raw.size() % 4 == 0, "act.bin: size is not a whole number of floats");
+    Cursor take{reinterpret_cast<const float*>(raw.data()), raw.size() / 4};
+    const int d = d_;
+    auto lin = [&](DLinear& L, int N, int K, bool i8) {
+        const float* w = take.take((size_t)N * K);
+        const float* b = take.take(N);
+        L.init(A_, w, b, N, K, i8);
+        n_int8_ += i8;
+    };
+    struct Mha {
+        const float *wq, *bq, *wk, *bk, *wv, *bv, *wo, *bo;
+    };
+    auto mha = [&]() {
+        Mha h;
+        h.wq = take.take((size_t)d * d); h.bq = take.take(d);
+        h.wk = take.take((size_t)d * d); h.bk = take.take(d);
+        h.wv = take.take((size_t)d * d); h.bv = take.take(d);
+        h.wo = take.take((size_t)d * d); h.bo = take.take(d);
+        return h;
+    };
+    auto vec = [&](size_t k) { return A_.upload(take.take(k), k); };
+
+    lin(img_proj_, d, img_ch, int8_mask & 8);
+    lin(state_proj_, d, state_dim_, false);  // Role::Generic, kept fp32 (:142-145)
+    latent_ = vec(d);
+    pos1d_ = vec((size_t)n_1d_ * d);
+
+    const bool ia = int8_mask & 1, i1 = int8_mask & 2, i2 = int8_mask & 4, idec = int8_mask & 16;
+    enc_.resize(n_enc_);
+    for (Enc& l : enc_) {
+        const Mha h = mha();
+        l.qk.init(A_, {{h.wq, h.bq, d}, {h.wk, h.bk, d}}, d, ia);
+        l.v.init(A_, h.wv, h.bv, d, d, ia);
+        l.o.init(A_, h.wo, h.bo, d, d, ia);
+        n_int8_ += ia ? 4 : 0;
+        l.n1s = vec(d);
+        l.n1b = vec(d);
+        lin(l.w1, ff_, d, i1);
+        lin(l.w2, d, ff_, i2);
+        l.n2s = vec(d);
+        l.n2b = vec(d);
+    }
+    dec_.resize(n_dec_);
+    for (Dec& l : dec_) {
+        const Mha s = mha();
+        l.sqk.init(A_, {{s.wq, s.bq, d}, {s.wk, s.bk, d}}, d, idec);
+        l.sv.init(A_, s.wv, s.bv, d, d, idec);
+        l.so.init(A_, s.wo, s.bo, d, d, idec);
+        l.n1s = vec(d);
+        l.n1b = vec(d);
+        const Mha c = mha();
+        l.cq.init(A_, c.wq, c.bq, d, d, idec);
+        l.ck.init(A_, c.wk, c.bk, d, d, idec);
+        l.cv.init(A_, c.wv, c.bv, d, d, idec);
+        l.co.init(A_, c.wo, c.bo, d, d, idec);
+        n_int8_ += idec ? 8 : 0;
+        l.n2s = vec(d);
+        l.n2b = vec(d);
+        lin(l.w1, ff_, d, idec);
+        lin(l.w2, d, ff_, idec);
+        l.n3s = vec(d);
+        l.n3b = vec(d);
+    }
+    dec_pos_ = vec((size_t)chunk_ * d);
+    dec_ns_ = vec(d);
+    dec_nb_ = vec(d);
+    lin(head_, action_dim_, d, false);  // Role::Generic, fp32 (:142-145)
+    VLA_REQUIRE(take.off == take.n, "act.bin: size does not match act.meta");
+    VLA_HIP_CHECK(hipStreamCreateWithFlags(&own_, hipStreamNonBlocking));
+}
+
+ActTf::~ActTf() {
+    if (own_) (void)hipStreamDestroy(own_);
+}
+
+void ActTf::ensure(int n_cams, int fh, int fw) {
+    if (n_cams == n_cams_ && fh == fh_ && fw == fw_) return;
+    VLA_REQUIRE(n_cams > 0 && fh > 0 && fw > 0 && (long)n_cams * fh * fw < (1 << 20),
+                "act: camera grid out of range");
+    VLA_HIP_CHECK(hipDeviceSynchronize());
+    S_.reset();
+    auto S = std::make_unique<DeviceArena>();
+    const int T = n_tokens(n_cams, fh, fw), d = d_, C = chunk_;
+    const int n_img = fh * fw;
+    feats_ = S->alloc<float>((size_t)n_cams * n_img * img_ch_);
+    state_ = S->alloc<float>(state_dim_);
+    act_out_ = S->alloc<float>((size_t)C * action_dim_);
+    // buffers the encoder (T rows) and the decoder (C rows) share take the larger
+    const int R = T > C ? T : C;
+    x_ = S->alloc<float>((size_t)T * d);
+    xp_ = S->alloc<float>((size_t)R * d);
+    qk_ = S->alloc<float>((size_t)R * 2 * d);
+    v_ = S->alloc<float>((size_t)R * d);
+    att_ = S->alloc<float>((size_t)R * d);
+    ff_buf_ = S->alloc<float>((size_t)R * ff_);
+    dx_ = S->alloc<float>((size_t)C * d);
+    zero_ = S->alloc<float>((size_t)C * d);
+    kpos_ = S->alloc<float>((size_t)T * d);
+    ckb_ = S->alloc<float>((size_t)T * d);
+    cvb_ = S->alloc<float>((size_t)T * d);
+    dq_ = S->alloc<float>((size_t)C * d);
+    // positions: [pos1d | camera embedding per camera] (build_tokens :218-229)
+    std::vector<float> pos((size_t)T * d), cam((size_t)n_img * d);
+    sinusoid_pos_2d(fh, fw, d, cam.data());
+    std::vector<float> p1((size_t)n_1d_ * d);
+    VLA_HIP_CHECK(hipMemcpy(p1.data(), pos1d_, p1.size() * 4, hipMemcpyDeviceToHost));
+    std::copy(p1.begin(), p1.end(), pos.begin());
+    for (int c = 0; c < n_cams; c++)
+        std::copy(cam.begin(), cam.end(), pos.begin() + ((size_t)n_1d_ + (size_t)c * n_img) * d);
+    pos_ = S->upload(pos.data(), pos.size());
+    // quantization scratch: the widest int8 input is ff (w2) over T rows
+    int maxld = round_up(kpad4(ff_ > img_ch_ ? ff_ : img_ch_), 64);
+    if (round_up(kpad4(d), 64) > maxld) maxld = round_up(kpad4(d), 64);
+    const int rows = T > C ? T : C;
+    ctx_.xq_bytes = (size_t)rows * maxld;
+    ctx_.xq = S->alloc<int8_t>(ctx_.xq_bytes);
+    ctx_.xs_rows = rows;
+    ctx_.xs = S->alloc<float>(rows);
+    S_ = std::move(S);
+    n_cams_ = n_cams;
+    fh_ = fh;
+    fw_ = fw;
+    T_ = T;
+}
+
+void ActTf::run(hipStream_t st) {
+    Ctx c = ctx_;
+    c.st = st;
+    const int T = T_, d = d_, C = chunk_, n_img = fh_ * fw_;
+    const float scale = 1.0f / std::sqrt((float)hd_);
+    const MaskSpec none;
+
+    // build_tokens (:212-250): latent, state projection, camera tokens
+    copy_f32(x_, latent_, d, st);
+    linear(c, state_proj_, x_ + d, d, state_, state_dim_, 1);
+    linear(c, img_proj_, x_ + (size_t)n_1d_ * d, d, feats_, img_ch_, n_cams_ * n_img);
+
+    // encode (:252-301)
+    for (const Enc& l : enc_) {
+        launch_add(xp_, x_, pos_, (int64_t)T * d, st);
+        linear(c, l.qk, qk_, 2 * d, xp_, d, T);  // q | k from x + pos
+        linear(c, l.v, v_, d, x_, d, T);         // v from x
+        attend(st, att_, d, qk_, 2 * d, qk_ + d, 2 * d, v_, d, T, T, heads_, heads_, hd_, scale, none);
+        linear(c, l.o, x_, d, att_, d, T, 0, 1);  // x += wo(att)
+        launch_layernorm(x_, x_, l.n1s, l.n1b, T, d, eps_, st);
+        linear(c, l.w1, ff_buf_, ff_, x_, d, T, 1);  // relu
+        linear(c, l.w2, x_, d, ff_buf_, ff_, T, 0, 1);
+        launch_layernorm(x_, x_, l.n2s, l.n2b, T, d, eps_, st);
+    }
+
+    // decode (:303-356)
+    launch_add(kpos_, x_, pos_, (int64_t)T * d, st);
+    copy_f32(dx_, zero_, (int64_t)C * d, st);  // queries start at zero
+    for (const Dec& l : dec_) {
+        launch_add(xp_, dx_, dec_pos_, (int64_t)C * d, st);
+        linear(c, l.sqk, qk_, 2 * d, xp_, d, C);
+        linear(c, l.sv, v_, d, dx_, d, C);
+        attend(st, att_, d, qk_, 2 * d, qk_ + d, 2 * d, v_, d, C, C, heads_, heads_, hd_, scale, none);
+        linear(c, l.so, dx_, d, att_, d, C, 0, 1);
+        launch_layernorm(dx_, dx_, l.n1s, l.n1b, C, d, eps_, st);
+
+        launch_add(xp_, dx_, dec_pos_, (int64_t)C * d, st);
+        linear(c, l.cq, dq_, d, xp_, d, C);
+        linear(c, l.ck, ckb_, d, kpos_, d, T);  // keys carry the encoder positions
+        linear(c, l.cv, cvb_, d, x_, d, T);     // values do not
+        attend(st, att_, d, dq_, d, ckb_, d, cvb_, d, C, T, heads_, heads_, hd_, scale, none);
+        linear(c, l.co, dx_, d, att_, d, C, 0, 1);
+        launch_layernorm(dx_, dx_, l.n2s, l.n2b, C, d, eps_, st);
+
+        linear(c, l.w1, ff_buf_, ff_, dx_, d, C, 1);
+        linear(c, l.w2, dx_, d, ff_buf_, ff_, C, 0, 1);
+        launch_layernorm(dx_, dx_, l.n3s, l.n3b, C, d, eps_, st);
+    }
+    launch_layernorm(dx_, dx_, dec_ns_, dec_nb_, C, d, eps_, st);
+    linear(c, head_, act_out_, action_dim_, dx_, d, C);
+}
+
+void ActTf::forward_dev(const float* feats, int n_cams, int fh, int fw, const float* state_norm,
+                        float* actions_norm, hipStream_t caller) {
+    VLA_REQUIRE(feats && state_norm && actions_norm, "act: null buffer");
+    ensure(n_cams, fh, fw);
+    copy_f32(feats_, feats, (int64_t)n_cams * fh * fw * img_ch_, caller);
+    copy_f32(state_, state_norm, state_dim_, caller);
+    const uint64_t key = ((uint64_t)n_cams << 40) | ((uint64_t)fh << 20) | (uint64_t)fw;
+    replay_.run(key, own_, caller, [this](hipStream_t st) { run(st); });
+    copy_f32(actions_norm, act_out_, (int64_t)chunk_ * action_dim_, caller);
+}
+
+}  // namespace hip
+}  // namespace vla

@@ -1,0 +1,206 @@
+// models.h - the policy graphs of the reference on the device: the ACT
+// transformer, the Octo block transformer and the SmolVLA action chunk (SmolLM2
+// prefix + action expert flow-matching denoise). Each loads the reference's own
+// .meta/.bin checkpoint layout, holds its weights in HBM (int8 rows + scales for
+// the layers its int8 mask selects, fp32 otherwise), and runs a whole forward
+// pass as one HIP graph on inputs already on the device.
+#pragma once
+
+#include "graph.h"
+
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+namespace vla {
+namespace hip {
+
+// ------------------------------------------------------------------- ACT --
+// src/models/act/act_transformer.{h,cpp}: DETR-style post-norm encoder over
+// [latent | state | camera tokens], decoder with `chunk` zero-initialised
+// queries, final LayerNorm and an fp32 action head. int8 mask bits as
+// act_transformer.cpp:27 (1 encoder attention, 2 w1, 4 w2, 8 img_proj,
+// 16 decoder).
+class ActTf {
+public:
+    ActTf(const std::string& dir, int img_ch, int int8_mask);
+    ~ActTf();
+    int chunk() const { return chunk_; }
+    int action_dim() const { return action_dim_; }
+    int state_dim() const { return state_dim_; }
+    int dim() const { return d_; }
+    int img_ch() const { return img_ch_; }
+    int n_tokens(int n_cams, int fh, int fw) const { return n_1d_ + n_cams * fh * fw; }
+    int int8_layers() const { return n_int8_; }
+    // device pointers; feats [n_cams * fh * fw, img_ch], state_norm [state_dim],
+    // actions_norm [chunk, action_dim]
+    void forward_dev(const float* feats, int n_cams, int fh, int fw, const float* state_norm,
+                     float* actions_norm, hipStream_t caller);
+    int graph_nodes() const { return replay_.nodes(); }
+
+private:
+    struct Enc {
+        DLinear qk, v, o, w1, w2;
+        const float *n1s, *n1b, *n2s, *n2b;
+    };
+    struct Dec {
+        DLinear sqk, sv, so, cq, ck, cv, co, w1, w2;
+        const float *n1s, *n1b, *n2s, *n2b, *n3s, *n3b;
+    };
+    void ensure(int n_cams, int fh, int fw);
+    void run(hipStream_t st);
+
+    int d_ = 512, heads_ = 8, hd_ = 64, ff_ = 3200, n_enc_ = 4, n_dec_ = 1, chunk_ = 100;
+    int state_dim_ = 6, action_dim_ = 6, n_1d_ = 2, img_ch_ = 0, n_int8_ = 0;
+    float eps_ = 1e-5f;
+    DeviceArena A_;
+    DLinear img_proj_, state_proj_, head_;
+    const float *latent_ = nullptr, *pos1d_ = nullptr, *dec_pos_ = nullptr, *dec_ns_ = nullptr,
+                *dec_nb_ = nullptr;
+    std::vector<Enc> enc_;
+    std::vector<Dec> dec_;
+    // per-shape state
+    int n_cams_ = -1, fh_ = -1, fw_ = -1, T_ = 0;
+    std::unique_ptr<DeviceArena> S_;
+    float *feats_ = nullptr, *state_ = nullptr, *act_out_ = nullptr, *x_ = nullptr, *pos_ = nullptr,
+          *xp_ = nullptr, *qk_ = nullptr, *v_ = nullptr, *att_ = nullptr, *ff_buf_ = nullptr,
+          *dx_ = nullptr, *zero_ = nullptr, *kpos_ = nullptr, *ckb_ = nullptr, *cvb_ = nullptr,
+          *dq_ = nullptr;
+    Ctx ctx_;
+    hipStream_t own_ = nullptr;
+    GraphReplay replay_;
+};
+
+// ------------------------------------------------------------------ Octo --
+// src/models/octo/octo_transformer.{h,cpp}: pre-LN ViT blocks over
+// [task | per timestep: primary, wrist, (repeated task), readout] with the
+// block-causal attends() rule, the final layer computed for the last readout
+// row only. int8 mask bits as octo_model.cpp:60 (1 attention, 2 w1, 4 w2,
+// 8 token projections). meta key repeat_task 0 drops the per-step task copy
+// (the 16 + wnd * (256 + 64 + 1) token layout); the reference always repeats.
+class OctoTf {
+public:
+    OctoTf(const std::string& dir, int int8_mask);
+    ~OctoTf();
+    int d() const { return d_; }
+    int total_tokens(int wnd) const { return n_task_ + wnd * per_step(); }
+    int readout_index(int wnd) const { return n_task_ + wnd * per_step() - 1; }
+    int per_step() const { return tok_p_ + tok_w_ + (repeat_task_ ? n_task_ : 0) + n_readout_; }
+    int max_horizon() const { return max_h_; }
+    int n_task() const { return n_task_; }
+    int tok_primary() const { return tok_p_; }
+    int tok_wrist() const { return tok_w_; }
+    int t5_dim() const { return t5_dim_; }
+    int stem_dim() const { return stem_dim_; }
+    int int8_layers() const { return n_int8_; }
+    // device pointers; t5 [n_task, t5_dim], stem_p [wnd, tok_primary, stem_dim],
+    // stem_w [wnd, tok_wrist, stem_dim] or null; timestep_mask host [wnd];
+    // out [d] = the final-LayerNorm readout row.
+    void forward_dev(const float* t5, const float* stem_p, const float* stem_w, int wnd,
+                     const uint8_t* timestep_mask, float* out, hipStream_t caller);
+    int graph_nodes() const { return replay_.nodes(); }
+
+private:
+    struct Layer {
+        DLinear qkv, o, w1, w2;
+        const float *ln1s, *ln1b, *ln2s, *ln2b;
+    };
+    void ensure(int wnd, const uint8_t* tmask, bool wrist);
+    void run(hipStream_t st);
+
+    int d_ = 384, n_layers_ = 12, heads_ = 6, hd_ = 64, mlp_ = 1536, max_h_ = 10, n_task_ = 16;
+    int tok_p_ = 256, tok_w_ = 64, n_readout_ = 1, t5_dim_ = 768, stem_dim_ = 512;
+    int repeat_task_ = 1, n_int8_ = 0;
+    float eps_ = 1e-6f;
+    bool gelu_erf_ = false;
+    DeviceArena A_;
+    DLinear proj_task_, proj_prim_, proj_wrist_;
+    const float *pos_task_ = nullptr, *pos_prim_ = nullptr, *pos_wrist_ = nullptr,
+                *pos_readout_ = nullptr, *final_s_ = nullptr, *final_b_ = nullptr;
+    std::vector<Layer> layers_;
+    // per-shape state
+    uint64_t key_ = ~0ull;
+    int wnd_ = 0, total_ = 0, n_groups_ = 0;
+    bool wrist_ = false;
+    std::unique_ptr<DeviceArena> S_;
+    float *t5_ = nullptr, *sp_ = nullptr, *sw_ = nullptr, *out_ = nullptr, *x_ = nullptr, *P_ = nullptr,
+          *h_ = nullptr, *qkv_ = nullptr, *att_ = nullptr, *ff_buf_ = nullptr;
+    uint8_t *qg_ = nullptr, *allow_ = nullptr;
+    Ctx ctx_;
+    hipStream_t own_ = nullptr;
+    GraphReplay replay_;
+};
+
+// --------------------------------------------------------------- SmolVLA --
+// src/models/smolvla/{smollm2_lm,action_expert,smolvla_model}.cpp: the SmolLM2
+// prefix tower (RMSNorm, GQA with RoPE-NeoX, SwiGLU; K/V cached per layer)
+// over the assembled prefix embeddings, then the action expert's flow-matching
+// denoise (self-attention layers over prefix + suffix K/V, cross-attention
+// layers over the re-projected prefix K/V) for num_steps Euler steps. int8
+// mask bits as smolvla_model.cpp:44 (16 the text tower, 32 the expert).
+class SmolvlaTf {
+public:
+    SmolvlaTf(const std::string& dir, int int8_mask);
+    ~SmolvlaTf();
+    int chunk() const { return C_; }
+    int max_action_dim() const { return mad_; }
+    int hidden() const { return H_; }
+    int num_steps() const { return steps_; }
+    int int8_layers() const { return n_int8_; }
+    // device pointers; prefix [n_prefix, hidden] (scaled image/text embeddings
+    // + the state token, as smolvla_model.cpp:231-250 assembles them); pad host
+    // [n_prefix] (1 real, 0 padding; the last token is the state token);
+    // noise [chunk, max_action_dim]; actions [chunk, max_action_dim] normalized.
+    void chunk_dev(const float* prefix, const int32_t* pad, int n_prefix, const float* noise,
+                   float* actions, hipStream_t caller);
+    int graph_nodes() const { return replay_.nodes(); }
+
+private:
+    struct VlmLayer {
+        DLinear qkv, o, gu, down;
+        const float *ln_in, *ln_post;
+    };
+    struct ExpLayer {
+        bool self;
+        DLinear q_or_qkv, k, v, o, gu, down;  // self: q_or_qkv = q|k|v; cross: q, k, v apart
+        const float *ln_in, *ln_post;
+    };
+    void ensure(const int32_t* pad, int n_prefix);
+    void run(hipStream_t st);
+
+    // text tower
+    int H_ = 960, nq_ = 15, nkv_ = 5, hd_ = 64, F_ = 2560, NL_ = 32;
+    float eps_ = 1e-5f, rope_base_ = 10000.0f;
+    // expert
+    int EH_ = 480, EF_ = 1280, ENL_ = 32, enq_ = 15, enkv_ = 5, ehd_ = 64, san_ = 2, C_ = 50,
+        steps_ = 10, mad_ = 32;
+    float eeps_ = 1e-5f, erope_ = 10000.0f;
+    double min_period_ = 4e-3, max_period_ = 4.0;
+    int n_int8_ = 0;
+    DeviceArena A_;
+    std::vector<VlmLayer> vlm_;
+    std::vector<ExpLayer> exp_;
+    const float* out_norm_ = nullptr;
+    DLinear ain_, at1_, at2_, aout_;
+    // per-shape state
+    uint64_t key_ = ~0ull;
+    int np_ = 0, SK_ = 0, QKVW_ = 0;
+    std::unique_ptr<DeviceArena> S_;
+    float *prefix_in_ = nullptr, *noise_in_ = nullptr, *act_out_ = nullptr, *h_ = nullptr,
+          *xn_ = nullptr, *att_ = nullptr, *gu_raw_ = nullptr, *gu_ = nullptr, *eh_ = nullptr,
+          *ehn_ = nullptr, *eq_ = nullptr, *mlp1_ = nullptr, *x_ = nullptr, *hf_ = nullptr;
+    std::vector<float*> qkv_;        // per text layer [np + C, QKVW]: prefix rows from the tower, suffix rows from the expert
+    std::vector<float*> ck_, cv_;    // per cross layer [np, kv_full]
+    std::vector<float*> at_;         // per step [C, 2 EH], right half = the step's time embedding
+    int32_t *pos_ = nullptr, *pos_full_ = nullptr, *pos_reb_ = nullptr;
+    uint8_t *pgroup_ = nullptr, *pallow_ = nullptr;
+    float *dmask_ = nullptr, *cmask_ = nullptr;
+    bool dcausal_ = true, cnone_ = true;
+    Ctx ctx_;
+    hipStream_t own_ = nullptr;
+    GraphReplay replay_;
+};
+
+}  // namespace hip
+}  // namespace vla
