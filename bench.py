@@ -17,6 +17,12 @@ with HIP events on the stream it runs on. cpu_baseline = the reference's own
 dense_linear_i8 (its AVX-VNNI kernel when the host CPU has AVX-VNNI, else its
 scalar dense_linear_i8_ref) built from the reference sources into
 oracle/_ref/, timed on this host on a bounded sample of the same shapes.
+
+policy_latency_ms = the metric's second half, per-chunk latency at batch 1 of
+BASELINE.json configs[2..4] (ACT transformer, Octo-base transformer, SmolVLA
+chunk) on random-init checkpoints written in the reference's file layouts:
+the device graph (one HIP-graph replay per forward, inputs resident in HBM,
+HIP events) next to the reference's own graph on this host's cores.
 """
 
 from __future__ import annotations
@@ -192,6 +198,119 @@ def cpu_baseline(synth, budget_s=15.0):
     }
 
 
+def _time_calls(torch, fn, stream_obj, min_calls=20, min_s=0.5):
+    """ms per call of fn() (each call one replay of a captured policy graph),
+    HIP events on the stream the graphs run on."""
+    for _ in range(3):  # eager call, capture, first replay
+        fn()
+    stream_obj.synchronize()
+    n, t = 0, 0.0
+    while n < min_calls or t < min_s * 1e3:
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream_obj)
+        for _ in range(10):
+            fn()
+        end.record(stream_obj)
+        end.synchronize()
+        t += start.elapsed_time(end)
+        n += 10
+    return t / n
+
+
+def _time_cpu(fn, min_calls=3, min_s=1.0):
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while n < min_calls or time.perf_counter() - t0 < min_s:
+        fn()
+        n += 1
+    return (time.perf_counter() - t0) * 1e3 / n
+
+
+def policy_latency(vla, torch, stream_obj, with_cpu=True):
+    """Per-chunk latency of BASELINE.json configs[2..4] at batch 1: the device
+    graphs (one captured HIP graph per forward, inputs resident in HBM) and the
+    reference's own graphs (oracle/_ref) on this host, on the same random-init
+    checkpoints and inputs."""
+    import tempfile
+
+    import vla_simd_amd.checkpoints as ck
+
+    ob = None
+    if with_cpu:
+        from oracle import bindings as ob
+        if not ob.ref_available():
+            ob = None
+    dev = torch.device("cuda")
+    out = {}
+    with tempfile.TemporaryDirectory(prefix="vla_ck_") as tmp:
+        # ACT: 4 x 302-token encoder, 100-query decoder, ACT_INT8=31
+        c = ck.ACT_BASE
+        d = ck.write_act(os.path.join(tmp, "act"), c)
+        f, s = ck.act_inputs(c)
+        m = vla.ActTransformer(d, c["img_ch"], 31)
+        tf, ts = torch.from_numpy(f).to(dev), torch.from_numpy(s).to(dev)
+        ta = torch.empty((c["chunk"], c["action_dim"]), dtype=torch.float32, device=dev)
+        st = stream_obj.cuda_stream
+        gpu = _time_calls(torch, lambda: m.forward_dev(tf, 1, c["fh"], c["fw"], ts, ta, st), stream_obj)
+        row = {"gpu_ms": round(gpu, 4), "tokens": 302, "int8_mask": 31, "int8_layers": m.int8_layers,
+               "graph_nodes": m.graph_nodes}
+        if ob is not None:
+            r = ob.RefAct(d, c["img_ch"], 31, c["chunk"], c["action_dim"])
+            row["cpu_ref_ms"] = round(_time_cpu(lambda: r.forward(f, 1, c["fh"], c["fw"], s)), 3)
+            del r
+        out["act"] = row
+        del m
+        print(f"  ACT transformer: {row}", file=sys.stderr, flush=True)
+
+        # Octo-base: 12 x 768, BASELINE layout (658 tokens) and the reference's
+        # repeated-task layout (690 tokens, which is what the reference runs)
+        for rep in (0, 1):
+            c = dict(ck.OCTO_BASE, repeat_task=rep)
+            d = ck.write_octo(os.path.join(tmp, f"octo{rep}"), c)
+            t5, sp, sw, tm = ck.octo_inputs(c)
+            m = vla.OctoTransformer(d, 7)
+            a, b, w = (torch.from_numpy(v).to(dev) for v in (t5, sp, sw))
+            o = torch.empty(c["d"], dtype=torch.float32, device=dev)
+            gpu = _time_calls(torch, lambda: m.forward_dev(a, b, w, 2, tm, o, st), stream_obj)
+            row = {"gpu_ms": round(gpu, 4), "tokens": m.total_tokens(2), "int8_mask": 7,
+                   "int8_layers": m.int8_layers, "graph_nodes": m.graph_nodes}
+            if ob is not None and rep == 1:
+                r = ob.RefOcto(d, 7, c["d"])
+                row["cpu_ref_ms"] = round(_time_cpu(lambda: r.forward(t5, sp, sw, 2, tm)), 3)
+                del r
+            out["octo" if rep == 0 else "octo_repeat_task"] = row
+            del m
+            print(f"  Octo transformer ({m_tokens(c)} tokens): {row}", file=sys.stderr, flush=True)
+
+        # SmolVLA chunk: 16-layer prefix over 177 tokens + 10 Euler steps of the
+        # 16-layer expert, SMOLVLA_INT8=48
+        c = ck.SMOLVLA_BASE
+        d = ck.write_smolvla(os.path.join(tmp, "smol"), c)
+        p, pad, n = ck.smolvla_inputs(c)
+        m = vla.SmolvlaChunk(d, 48)
+        tp, tn = torch.from_numpy(p).to(dev), torch.from_numpy(n).to(dev)
+        ta = torch.empty((c["chunk"], c["max_action_dim"]), dtype=torch.float32, device=dev)
+        gpu = _time_calls(torch, lambda: m.run_dev(tp, pad, tn, ta, st), stream_obj, min_calls=10)
+        row = {"gpu_ms": round(gpu, 4), "prefix_tokens": c["n_prefix"], "steps": c["num_steps"],
+               "int8_mask": 48, "int8_layers": m.int8_layers, "graph_nodes": m.graph_nodes}
+        if ob is not None:
+            r = ob.RefSmolvla(d, 48)
+            row["cpu_ref_ms"] = round(_time_cpu(lambda: r.run(p, pad, n)), 3)
+            del r
+        out["smolvla"] = row
+        del m
+        print(f"  SmolVLA chunk: {row}", file=sys.stderr, flush=True)
+    if ob is not None:
+        out["cpu_ref_threads"] = int(ob.ref().ref_omp_max_threads())
+    return out
+
+
+def m_tokens(c):
+    per = c["tok_primary"] + c["tok_wrist"] + (c["n_task"] if c.get("repeat_task") else 0) + c["n_readout"]
+    return c["n_task"] + c["wnd"] * per
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -199,6 +318,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the cpu_baseline leg")
     ap.add_argument("--shapes", default="", help="comma list MxKxN to restrict the sweep (debug)")
+    ap.add_argument("--no-policy", action="store_true", help="skip the per-chunk policy latency leg")
+    ap.add_argument("--policy-only", action="store_true",
+                    help="only the per-chunk policy latency leg (for rocprofv3 runs)")
     ap.add_argument("--profile-only", action="store_true",
                     help="only the dominant GEMM, back to back (for rocprofv3 runs)")
     args = ap.parse_args()
@@ -220,6 +342,11 @@ def main():
     stream_obj = torch.cuda.Stream()
     torch.cuda.set_stream(stream_obj)
     stream = stream_obj.cuda_stream
+
+    if args.policy_only:
+        print(json.dumps({"policy_latency_ms": policy_latency(vla, torch, stream_obj,
+                                                              with_cpu=not args.no_cpu)}), flush=True)
+        return
 
     shapes_spec = [(M, K, N) for (K, N) in synth.SWEEP_KN for M in synth.SWEEP_M]
     if args.shapes:  # any MxKxN list (A/B and scaling runs); the default is the sweep
@@ -309,6 +436,7 @@ def main():
                     "traffic_source": "profiles/gemm_i8_8192x4096x4096_traffic.txt"}
 
     cpu = None if args.no_cpu else cpu_baseline(synth)
+    policy = None if args.no_policy else policy_latency(vla, torch, stream_obj, with_cpu=not args.no_cpu)
 
     print(json.dumps({
         "metric": "int8 GEMM TOPS (% MFMA peak) + per-chunk policy latency ms, batch 1",
@@ -319,7 +447,7 @@ def main():
         "config": {"workload": "int8 GEMM sweep, BASELINE.json configs[1]: 30 dense_linear_i8 "
                                "calls (device quantize + i8 MFMA GEMM) per step",
                    "shapes": len(shapes), "wall_s_timed": round(wall, 3)},
-        "roofline": roofline, "cpu_baseline": cpu, "sweep": rows,
+        "roofline": roofline, "cpu_baseline": cpu, "policy_latency_ms": policy, "sweep": rows,
     }), flush=True)
 
 

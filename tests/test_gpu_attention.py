@@ -88,9 +88,12 @@ def test_fully_masked_is_uniform(vla, orc, cfg, block):
     assert np.max(np.abs(got - want)) < 2e-6
 
 
-def test_partially_masked_rows(vla, orc):
-    """Some rows fully blocked, others not, in one tile."""
-    sq, sk, nq, nkv, hd = 40, 70, 4, 2, 64
+@pytest.mark.parametrize("sk", [70, 300])
+def test_partially_masked_rows(vla, orc, sk):
+    """Some rows fully blocked, others not, in one 16-query block; sk = 300
+    splits the keys over 8 waves, so the merged rows and the uniform rows meet
+    in the same block merge."""
+    sq, nq, nkv, hd = 40, 4, 2, 64
     Q, K, V = _qkv(orc, sq, sk, nq, nkv, hd)
     rng = np.random.default_rng(7)
     mask = np.where(rng.random((sq, sk)) < 0.5, LOWEST, rng.normal(0, 1, (sq, sk))).astype(np.float32)

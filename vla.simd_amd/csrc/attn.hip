@@ -10,9 +10,14 @@
 // fp32 throughout; results are tolerance-class against the reference (its exp
 // is a Cephes polynomial, its sums run in another order).
 //
-// One wave owns 16 queries of one head; a block of WAVES waves shares K/V
-// tiles of KT keys staged in LDS. Both products run on the fp32 matrix cores
-// (v_mfma_f32_16x16x4_f32, one float per lane per operand):
+// A block owns 16 queries of one head; its W waves split the key range: wave w
+// takes key tiles w, w + W, ... (KT keys each), stages each tile in its own
+// LDS region (no block barrier in the main loop) and keeps its own online
+// softmax state; at the end the waves merge their (max, sum, output) through
+// LDS. Small problems (the batch-1 action chunks) thereby still occupy many
+// waves, and large ones get W-fold more waves than query tiles.
+// Both products run on the fp32 matrix cores (v_mfma_f32_16x16x4_f32, one
+// float per lane per operand):
 //   S^T = K Q^T : A = K tile rows (keys), B = Q^T; lane l's result holds
 //                 S[q = l%16][key = 16*kt + 4*(l/16) + r], r = 0..3;
 //   O^T = V^T P^T: A = V^T, B = P^T. The B operand lane l must supply is
@@ -21,7 +26,8 @@
 // The head dimension is walked as d = g*(HDP/4) + s for lane group g = l/16,
 // so each lane's Q slice and each K row read are contiguous (ds_read_b128).
 // LDS rows are HDP+4 floats: the 16 rows of one read land on distinct banks,
-// and the four lane groups of a V read land 16 banks apart.
+// and the four lane groups of a V read land 16 banks apart. The next tile's
+// K/V rows are loaded into registers while the current tile computes.
 // Scores and the running max stay in the natural domain (dot*scale + mask, as
 // the reference forms them); exp(x) is evaluated as v_exp_f32(x * log2 e).
 
@@ -43,15 +49,33 @@ __device__ __forceinline__ v4f mfma_f32(float a, float b, v4f c) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-template <int HDP, int KT, int WAVES>
-__global__ __launch_bounds__(WAVES * 64) void attn_fwd(AttnArgs a) {
-    constexpr int SK = HDP + 4;
+// Orders this wave's LDS accesses (its writes before other lanes' reads) with
+// no block barrier.
+__device__ __forceinline__ void wave_lds_sync() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((15) | (3 << 14) | (7 << 4));  // lgkmcnt(0) only
+    __builtin_amdgcn_wave_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int HDP, int KT, int W>
+struct AttnCfg {
+    static constexpr int SK = HDP + 4;               // LDS row, floats
+    static constexpr int TILE = 2 * KT * SK;         // K + V of one wave, floats
+    static constexpr int F4 = KT * HDP / 4 / 64;     // float4 loads per lane per K (or V) tile
+    static constexpr int MERGE = W * (32 + 16 * HDP);
+    static constexpr int LDS = 4 * (W * TILE > MERGE ? W * TILE : MERGE);
+    static_assert(KT % 16 == 0 && (KT * HDP / 4) % 64 == 0, "tile shape");
+};
+
+template <int HDP, int KT, int W>
+__global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
+    using C = AttnCfg<HDP, KT, W>;
+    constexpr int SK = C::SK, F4 = C::F4;
     constexpr int NT = KT / 16;
     constexpr int QS = HDP / 4;
     constexpr int DT = HDP / 16;
-    constexpr int NTH = WAVES * 64;
-    __shared__ __attribute__((aligned(16))) float Ks[KT * SK];
-    __shared__ __attribute__((aligned(16))) float Vs[KT * SK];
+    extern __shared__ __attribute__((aligned(16))) float smem[];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
@@ -59,9 +83,10 @@ __global__ __launch_bounds__(WAVES * 64) void attn_fwd(AttnArgs a) {
     const int h = blockIdx.y;
     const int kvh = h / (a.n_q / a.n_kv);
     const int HD = a.head_dim;
-    const int qb0 = blockIdx.x * 16 * WAVES;
-    const int qi = qb0 + wave * 16 + c;
+    const int qi = blockIdx.x * 16 + c;
     const bool qok = qi < a.seq_q;
+    float* Ks = smem + wave * C::TILE;
+    float* Vs = Ks + KT * SK;
 
     float qreg[QS];
 #pragma unroll
@@ -82,20 +107,32 @@ __global__ __launch_bounds__(WAVES * 64) void attn_fwd(AttnArgs a) {
     // keys past kv_end are blocked for every query of the block (causal bound)
     int kv_end = a.seq_k;
     if (mk == 2) {
-        const int qlast = (qb0 + 16 * WAVES < a.seq_q ? qb0 + 16 * WAVES : a.seq_q) - 1;
+        const int qlast = (blockIdx.x * 16 + 16 < a.seq_q ? blockIdx.x * 16 + 16 : a.seq_q) - 1;
         const int e = qlast + a.causal_offset + 1;
         kv_end = e < 0 ? 0 : (e < kv_end ? e : kv_end);
     }
-    const int nkt = (kv_end + KT - 1) / KT;
 
-    auto load_tile = [&](float* S, const float* G, int ld, int kv0) {
-        constexpr int F4 = HDP / 4;
-        for (int e = tid; e < KT * F4; e += NTH) {
-            const int kr = e / F4, d = (e % F4) * 4;
-            const int j = kv0 + kr;
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (j < a.seq_k && d < HD) v = *reinterpret_cast<const float4*>(G + (size_t)j * ld + kvh * HD + d);
-            *reinterpret_cast<float4*>(S + kr * SK + d) = v;
+    // this lane's share of a tile load: float4 number e = lane + 64 * i of the
+    // KT x HDP/4 tile is row e / (HDP/4), dims 4 * (e % (HDP/4))
+    float4 kr[F4], vr[F4];
+    auto gload = [&](int kv0, int end) {
+#pragma unroll
+        for (int i = 0; i < F4; i++) {
+            const int e = lane + 64 * i, row = e / (HDP / 4), d = 4 * (e % (HDP / 4));
+            const int j = kv0 + row;
+            kr[i] = vr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (j < end && d < HD) {
+                kr[i] = *reinterpret_cast<const float4*>(a.K + (size_t)j * a.ldk + kvh * HD + d);
+                vr[i] = *reinterpret_cast<const float4*>(a.V + (size_t)j * a.ldv + kvh * HD + d);
+            }
+        }
+    };
+    auto lstore = [&]() {
+#pragma unroll
+        for (int i = 0; i < F4; i++) {
+            const int e = lane + 64 * i, row = e / (HDP / 4), d = 4 * (e % (HDP / 4));
+            *reinterpret_cast<float4*>(Ks + row * SK + d) = kr[i];
+            *reinterpret_cast<float4*>(Vs + row * SK + d) = vr[i];
         }
     };
 
@@ -104,21 +141,22 @@ __global__ __launch_bounds__(WAVES * 64) void attn_fwd(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < DT; i++) oacc[i] = v4f{0.f, 0.f, 0.f, 0.f};
 
-    for (int t = 0; t < nkt; t++) {
+    const int nkt = (kv_end + KT - 1) / KT;
+    if (wave < nkt) gload(wave * KT, a.seq_k);
+    for (int t = wave; t < nkt; t += W) {
         const int kv0 = t * KT;
-        __syncthreads();
-        load_tile(Ks, a.K, a.ldk, kv0);
-        load_tile(Vs, a.V, a.ldv, kv0);
-        __syncthreads();
+        lstore();
+        wave_lds_sync();
+        if (t + W < nkt) gload((t + W) * KT, a.seq_k);  // next tile, under this one's math
 
         v4f sacc[NT];
 #pragma unroll
         for (int kt = 0; kt < NT; kt++) {
             sacc[kt] = v4f{0.f, 0.f, 0.f, 0.f};
-            const float* kr = Ks + (kt * 16 + c) * SK + g * QS;
+            const float* krow = Ks + (kt * 16 + c) * SK + g * QS;
 #pragma unroll
             for (int s = 0; s < QS; s += 4) {
-                const float4 kv = *reinterpret_cast<const float4*>(kr + s);
+                const float4 kv = *reinterpret_cast<const float4*>(krow + s);
                 sacc[kt] = mfma_f32(kv.x, qreg[s], sacc[kt]);
                 sacc[kt] = mfma_f32(kv.y, qreg[s + 1], sacc[kt]);
                 sacc[kt] = mfma_f32(kv.z, qreg[s + 2], sacc[kt]);
@@ -181,20 +219,49 @@ __global__ __launch_bounds__(WAVES * 64) void attn_fwd(AttnArgs a) {
                 for (int r = 0; r < 4; r++)
                     oacc[dt] = mfma_f32(Vs[(kt * 16 + 4 * g + r) * SK + dt * 16 + c], sacc[kt][r], oacc[dt]);
         }
+        wave_lds_sync();  // this tile's reads are done before the next lstore
     }
 
     lsum += __shfl_xor(lsum, 16, 64);
     lsum += __shfl_xor(lsum, 32, 64);
 
-    // rows with every key blocked: uniform mean of V over all keys
-    const bool masked = qok && m == -INFINITY;
+    // merge the waves' partial states: m*, then sum_w e^(m_w - m*) (l_w, O_w)
+    __syncthreads();
+    float* Mm = smem;               // [W][16]
+    float* Ml = smem + 16 * W;      // [W][16]
+    float* Mo = smem + 32 * W;      // [W][16][HDP]
+    if (g == 0) {
+        Mm[wave * 16 + c] = m;
+        Ml[wave * 16 + c] = lsum;
+    }
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++)
+        *reinterpret_cast<float4*>(Mo + (wave * 16 + c) * HDP + dt * 16 + 4 * g) =
+            make_float4(oacc[dt][0], oacc[dt][1], oacc[dt][2], oacc[dt][3]);
+    __syncthreads();
+    // every wave's (m, l) for this lane's query, in registers: the uniform pass
+    // below reuses this LDS for V tiles
+    float mw[W], lw[W], mstar = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < W; w++) {
+        mw[w] = Mm[w * 16 + c];
+        lw[w] = Ml[w * 16 + c];
+        mstar = fmaxf(mstar, mw[w]);
+    }
+    const bool masked = qok && mstar == -INFINITY;
+    // rows with every key blocked: uniform mean of V over all seq_k keys
+    // (attn_uniform_row); the waves sum V over their tiles with p = 1
     if (__syncthreads_or(masked)) {
+        // a row that is not masked keeps its softmax partial (it adds p = 0 below)
+        if (masked)
+#pragma unroll
+            for (int i = 0; i < DT; i++) oacc[i] = v4f{0.f, 0.f, 0.f, 0.f};
         const int nall = (a.seq_k + KT - 1) / KT;
-        for (int t = 0; t < nall; t++) {
+        for (int t = wave; t < nall; t += W) {
             const int kv0 = t * KT;
-            __syncthreads();
-            load_tile(Vs, a.V, a.ldv, kv0);
-            __syncthreads();
+            gload(kv0, a.seq_k);
+            lstore();
+            wave_lds_sync();
 #pragma unroll
             for (int dt = 0; dt < DT; dt++)
 #pragma unroll
@@ -205,31 +272,72 @@ __global__ __launch_bounds__(WAVES * 64) void attn_fwd(AttnArgs a) {
                         const float p = (masked && j < a.seq_k) ? 1.0f : 0.0f;
                         oacc[dt] = mfma_f32(Vs[(kt * 16 + 4 * g + r) * SK + dt * 16 + c], p, oacc[dt]);
                     }
+            wave_lds_sync();
         }
+        __syncthreads();
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++)
+            *reinterpret_cast<float4*>(Mo + (wave * 16 + c) * HDP + dt * 16 + 4 * g) =
+                make_float4(oacc[dt][0], oacc[dt][1], oacc[dt][2], oacc[dt][3]);
+        __syncthreads();
     }
+    if (wave != 0 || !qok) return;
 
-    if (!qok) return;
-    const float inv = masked ? 1.0f / (float)a.seq_k : 1.0f / lsum;
+    float f[W], l = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; w++) {
+        f[w] = masked ? 1.0f : (mw[w] == -INFINITY ? 0.0f : fast_exp2((mw[w] - mstar) * kLog2e));
+        l += f[w] * lw[w];
+    }
+    const float inv = masked ? 1.0f / (float)a.seq_k : 1.0f / l;
 #pragma unroll
     for (int dt = 0; dt < DT; dt++) {
         const int d = dt * 16 + 4 * g;
         if (d < HD) {
-            float4 v = make_float4(oacc[dt][0] * inv, oacc[dt][1] * inv, oacc[dt][2] * inv, oacc[dt][3] * inv);
-            *reinterpret_cast<float4*>(a.out + (size_t)qi * a.ldo + h * HD + d) = v;
+            float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int w = 0; w < W; w++) {
+                const float4 v = *reinterpret_cast<const float4*>(Mo + (w * 16 + c) * HDP + d);
+                o.x += f[w] * v.x;
+                o.y += f[w] * v.y;
+                o.z += f[w] * v.z;
+                o.w += f[w] * v.w;
+            }
+            o.x *= inv;
+            o.y *= inv;
+            o.z *= inv;
+            o.w *= inv;
+            *reinterpret_cast<float4*>(a.out + (size_t)qi * a.ldo + h * HD + d) = o;
         }
     }
 }
 
-template <int HDP, int KT>
+template <int HDP, int KT, int W>
+void launch_w(const AttnArgs& a, hipStream_t st) {
+    using C = AttnCfg<HDP, KT, W>;
+    static const bool attr = [] {
+        if (C::LDS > 65536)
+            VLA_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_fwd<HDP, KT, W>),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS));
+        return true;
+    }();
+    (void)attr;
+    attn_fwd<HDP, KT, W><<<dim3((a.seq_q + 15) / 16, a.n_q), W * 64, C::LDS, st>>>(a);
+}
+
+// W: enough waves that each walks a few key tiles, capped at WMAX (LDS).
+template <int HDP, int KT, int WMAX>
 void run_attn(const AttnArgs& a, hipStream_t st) {
-    auto blocks = [&](int w) { return (long)((a.seq_q + 16 * w - 1) / (16 * w)) * a.n_q; };
-    if (blocks(4) >= 256) {
-        attn_fwd<HDP, KT, 4><<<dim3((a.seq_q + 63) / 64, a.n_q), 256, 0, st>>>(a);
-    } else if (blocks(2) >= 256) {
-        attn_fwd<HDP, KT, 2><<<dim3((a.seq_q + 31) / 32, a.n_q), 128, 0, st>>>(a);
-    } else {
-        attn_fwd<HDP, KT, 1><<<dim3((a.seq_q + 15) / 16, a.n_q), 64, 0, st>>>(a);
+    int kv = a.seq_k;
+    if (a.mask_kind == 2) {  // keys no query of the problem can see are never walked
+        const int e = a.seq_q + a.causal_offset;
+        kv = e < 1 ? 1 : (e < kv ? e : kv);
     }
+    const int tiles = (kv + KT - 1) / KT;
+    if (tiles <= 1) launch_w<HDP, KT, 1>(a, st);
+    else if (tiles <= 2 || WMAX == 2) launch_w<HDP, KT, 2>(a, st);
+    else if (tiles <= 4 || WMAX == 4) launch_w<HDP, KT, (WMAX < 4 ? WMAX : 4)>(a, st);
+    else launch_w<HDP, KT, WMAX>(a, st);
     VLA_LAUNCH_CHECK();
 }
 
@@ -255,11 +363,11 @@ void launch_attention(const AttnArgs& a, hipStream_t st) {
                 "attention: group mask needs q_group, k_group, allow and 1..256 groups");
     if (a.seq_q == 0) return;
     if (a.head_dim <= 64)
-        run_attn<64, 64>(a, st);
+        run_attn<64, 32, 8>(a, st);
     else if (a.head_dim <= 128)
-        run_attn<128, 32>(a, st);
+        run_attn<128, 32, 4>(a, st);
     else
-        run_attn<256, 16>(a, st);
+        run_attn<256, 16, 4>(a, st);
 }
 
 }  // namespace hip
