@@ -103,6 +103,27 @@ void launch_silu_gate_rows(float* out, int ldo, const float* g, int ldg, const f
                            int rows, int cols, hipStream_t st);
 void launch_rope_neox(float* x, int ld, const int32_t* pos, int seq, int n_heads, int head_dim,
                       float base, hipStream_t st);
+// Row kernels that end in the int8 quantizer (eltwise.hip). Per row, y is
+// op 0 x itself, 1 LayerNorm(x; w, b), 2 RMSNorm(x; w), 3 silu_gate(x, u) (x
+// the gate rows); then y goes to out (fp32, optional), to q/qs quantized (optional),
+// and y + add (ACT's x + pos) to out2 / q2 / qs2 (each optional). The
+// quantized bytes are those of launch_quantize_rows on the fp32 result.
+struct RowQArgs {
+    int op = 0;
+    const float* x = nullptr;   int ldx = 0;
+    const float* u = nullptr;   int ldu = 0;
+    const float* w = nullptr;
+    const float* b = nullptr;
+    float eps = 0.0f;
+    float* out = nullptr;       int ldo = 0;
+    int8_t* q = nullptr;        int ldq = 0;  float* qs = nullptr;
+    const float* add = nullptr; int ld_add = 0;
+    float* out2 = nullptr;      int ldo2 = 0;
+    int8_t* q2 = nullptr;       int ldq2 = 0; float* qs2 = nullptr;
+    int rows = 0, H = 0;
+};
+void launch_rowq(const RowQArgs& a, hipStream_t st);
+
 // dst[r, c] = src[r, c] for a [rows, cols] block with row strides ldd / lds
 void launch_copy_rows(float* dst, int ldd, const float* src, int lds, int rows, int cols,
                       hipStream_t st);

@@ -17,6 +17,7 @@
 
 #include "act.h"
 #include "common.h"
+#include "quant_row.h"
 
 namespace vla {
 namespace hip {
@@ -129,6 +130,148 @@ __global__ __launch_bounds__(256) void copy_rows_kernel(float* dst, int ldd, con
         if (c + 256 * j < cols) dst[(size_t)r * ldd + c + 256 * j] = src[(size_t)r * lds + c + 256 * j];
 }
 
+// One wave per row; the row lives in registers (NV float4 per lane, element
+// 4 * lane + 256 * i), so the norm statistics, the fp32 result and the
+// absmax of the quantizer all come from one read of the row. The norms
+// accumulate in double as layernorm_kernel / rmsnorm_kernel do.
+template <int OP, int NV>
+__global__ __launch_bounds__(256) void rowq_kernel(RowQArgs a) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= a.rows) return;  // wave-uniform
+    const int H = a.H;
+    const float* xr = a.x + (size_t)row * a.ldx;
+    float4 y[NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int k = 4 * lane + 256 * i;
+        y[i] = k < H ? *reinterpret_cast<const float4*>(xr + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    if (OP == 1) {
+        double s = 0.0;
+#pragma unroll
+        for (int i = 0; i < NV; i++)
+            s += ((double)y[i].x + (double)y[i].y) + ((double)y[i].z + (double)y[i].w);
+        const double mean = wave_sum(s) / H;
+        double v = 0.0;
+#pragma unroll
+        for (int i = 0; i < NV; i++)
+            if (4 * lane + 256 * i < H) {
+                const double d0 = (double)y[i].x - mean, d1 = (double)y[i].y - mean;
+                const double d2 = (double)y[i].z - mean, d3 = (double)y[i].w - mean;
+                v += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+            }
+        const float inv = (float)(1.0 / sqrt(wave_sum(v) / H + (double)a.eps));
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int k = 4 * lane + 256 * i;
+            if (k < H) {
+                const float4 w = *reinterpret_cast<const float4*>(a.w + k);
+                float4 r;
+                if (a.b) {
+                    const float4 b = *reinterpret_cast<const float4*>(a.b + k);
+                    r.x = fmaf((float)((double)y[i].x - mean) * inv, w.x, b.x);
+                    r.y = fmaf((float)((double)y[i].y - mean) * inv, w.y, b.y);
+                    r.z = fmaf((float)((double)y[i].z - mean) * inv, w.z, b.z);
+                    r.w = fmaf((float)((double)y[i].w - mean) * inv, w.w, b.w);
+                } else {
+                    r.x = (float)((double)y[i].x - mean) * inv * w.x;
+                    r.y = (float)((double)y[i].y - mean) * inv * w.y;
+                    r.z = (float)((double)y[i].z - mean) * inv * w.z;
+                    r.w = (float)((double)y[i].w - mean) * inv * w.w;
+                }
+                y[i] = r;
+            }
+        }
+    } else if (OP == 2) {
+        double ss = 0.0;
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const double d0 = y[i].x, d1 = y[i].y, d2 = y[i].z, d3 = y[i].w;
+            ss += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+        }
+        const float inv = (float)(1.0 / sqrt(wave_sum(ss) / H + (double)a.eps));
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int k = 4 * lane + 256 * i;
+            if (k < H) {
+                const float4 w = *reinterpret_cast<const float4*>(a.w + k);
+                y[i] = make_float4(y[i].x * inv * w.x, y[i].y * inv * w.y, y[i].z * inv * w.z,
+                                   y[i].w * inv * w.w);
+            }
+        }
+    } else if (OP == 3) {
+        const float* ur = a.u + (size_t)row * a.ldu;
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int k = 4 * lane + 256 * i;
+            if (k < H) {
+                const float4 u = *reinterpret_cast<const float4*>(ur + k);
+                y[i] = make_float4(act_silu_gate(y[i].x, u.x), act_silu_gate(y[i].y, u.y),
+                                   act_silu_gate(y[i].z, u.z), act_silu_gate(y[i].w, u.w));
+            }
+        }
+    }
+
+    // y -> out (fp32) and q (int8); then y + add -> out2 and q2
+#pragma unroll
+    for (int pass = 0; pass < 2; pass++) {
+        float* out = pass ? a.out2 : a.out;
+        int8_t* q = pass ? a.q2 : a.q;
+        if (pass == 1) {
+            if (!a.add) break;
+            const float* ar = a.add + (size_t)row * a.ld_add;
+#pragma unroll
+            for (int i = 0; i < NV; i++) {
+                const int k = 4 * lane + 256 * i;
+                if (k < H) {
+                    const float4 p = *reinterpret_cast<const float4*>(ar + k);
+                    y[i] = make_float4(y[i].x + p.x, y[i].y + p.y, y[i].z + p.z, y[i].w + p.w);
+                }
+            }
+        }
+        if (out) {
+            float* orow = out + (size_t)row * (pass ? a.ldo2 : a.ldo);
+#pragma unroll
+            for (int i = 0; i < NV; i++) {
+                const int k = 4 * lane + 256 * i;
+                if (k < H) *reinterpret_cast<float4*>(orow + k) = y[i];
+            }
+        }
+        if (q) {
+            float amax = 0.0f;
+#pragma unroll
+            for (int i = 0; i < NV; i++)
+                if (4 * lane + 256 * i < H)
+                    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(y[i].x), fabsf(y[i].y)),
+                                             fmaxf(fabsf(y[i].z), fabsf(y[i].w))));
+            amax = wave_max_f32(amax);
+            const float s = row_scale(amax);
+            const float inv = 1.0f / s;
+            const int ldq = pass ? a.ldq2 : a.ldq;
+            if (lane == 0) (pass ? a.qs2 : a.qs)[row] = s;
+            int8_t* qr = q + (size_t)row * ldq;
+#pragma unroll
+            for (int i = 0; i < NV; i++) {
+                const int k = 4 * lane + 256 * i;
+                if (k < H) *reinterpret_cast<uint32_t*>(qr + k) = q8x4(y[i], inv);
+            }
+            for (int k = H + 4 * lane; k < ldq; k += 256) *reinterpret_cast<uint32_t*>(qr + k) = 0u;
+        }
+    }
+}
+
+template <int OP>
+void launch_rowq_op(const RowQArgs& a, hipStream_t st) {
+    const int nv = (a.H + 255) / 256;
+    const dim3 grid((a.rows + 3) / 4), block(256);
+    if (nv <= 1) rowq_kernel<OP, 1><<<grid, block, 0, st>>>(a);
+    else if (nv <= 2) rowq_kernel<OP, 2><<<grid, block, 0, st>>>(a);
+    else if (nv <= 4) rowq_kernel<OP, 4><<<grid, block, 0, st>>>(a);
+    else if (nv <= 8) rowq_kernel<OP, 8><<<grid, block, 0, st>>>(a);
+    else rowq_kernel<OP, 16><<<grid, block, 0, st>>>(a);
+}
+
 int grid_for(int64_t n) {
     const int64_t b = (n + 255) / 256;
     return (int)(b < 4096 ? (b > 0 ? b : 1) : 4096);
@@ -194,6 +337,30 @@ void launch_copy_rows(float* dst, int ldd, const float* src, int lds, int rows, 
     VLA_REQUIRE(rows < 65536, "copy_rows: too many rows");
     if (rows == 0 || cols == 0) return;
     copy_rows_kernel<<<dim3((cols + 1023) / 1024, rows), 256, 0, st>>>(dst, ldd, src, lds, cols);
+    VLA_LAUNCH_CHECK();
+}
+
+void launch_rowq(const RowQArgs& a, hipStream_t st) {
+    VLA_REQUIRE(a.op >= 0 && a.op <= 3, "rowq: unknown row op");
+    VLA_REQUIRE(a.rows >= 0 && a.H > 0 && a.H % 4 == 0 && a.H <= 16 * 256,
+                "rowq: rows must be >= 0 and H a multiple of 4 in [4, 4096]");
+    VLA_REQUIRE(a.x && a.ldx >= a.H && a.ldx % 4 == 0 && aligned(a.x, 16), "rowq: x rows must be 16-byte aligned");
+    VLA_REQUIRE(a.op == 0 || a.op == 3 || (a.w && aligned(a.w, 16) && (!a.b || aligned(a.b, 16))),
+                "rowq: norm weights must be 16-byte aligned");
+    VLA_REQUIRE(a.op != 3 || (a.u && a.ldu >= a.H && a.ldu % 4 == 0 && aligned(a.u, 16)),
+                "rowq: silu_gate needs 16-byte aligned u rows");
+    VLA_REQUIRE(!a.out || (a.ldo >= a.H && a.ldo % 4 == 0 && aligned(a.out, 16)), "rowq: bad out");
+    VLA_REQUIRE(!a.q || (a.qs && a.ldq >= a.H && a.ldq % 4 == 0 && aligned(a.q, 4)), "rowq: bad q");
+    VLA_REQUIRE(!a.add || (a.ld_add >= a.H && a.ld_add % 4 == 0 && aligned(a.add, 16)), "rowq: bad add");
+    VLA_REQUIRE(!a.out2 || (a.add && a.ldo2 >= a.H && a.ldo2 % 4 == 0 && aligned(a.out2, 16)),
+                "rowq: bad out2");
+    VLA_REQUIRE(!a.q2 || (a.add && a.qs2 && a.ldq2 >= a.H && a.ldq2 % 4 == 0 && aligned(a.q2, 4)),
+                "rowq: bad q2");
+    if (a.rows == 0) return;
+    if (a.op == 0) launch_rowq_op<0>(a, st);
+    else if (a.op == 1) launch_rowq_op<1>(a, st);
+    else if (a.op == 2) launch_rowq_op<2>(a, st);
+    else launch_rowq_op<3>(a, st);
     VLA_LAUNCH_CHECK();
 }
 

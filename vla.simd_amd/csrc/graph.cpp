@@ -50,21 +50,39 @@ void DLinear::init(DeviceArena& A, const std::vector<RowBlock>& blocks, int K_, 
     }
 }
 
-void quantize(const Ctx& c, const float* x, int ldx, int seq, int K, int ldq) {
-    VLA_REQUIRE((size_t)seq * ldq <= c.xq_bytes && seq <= c.xs_rows,
-                "graph: activation quantization scratch too small");
-    launch_quantize_rows(x, ldx, c.xq, ldq, c.xs, seq, K, c.st);
+QAct Ctx::slot(int i, int ld) const {
+    QAct a;
+    a.q = xq[i];
+    a.s = xs[i];
+    a.ld = ld;
+    return a;
 }
 
-static void gemm_q(const Ctx& c, const DLinear& L, float* out, int ldo, int seq, int act, int acc,
-                   int n0, int n1) {
+void Ctx::alloc(DeviceArena& A, int rows, int ld_max) {
+    xq_bytes = (size_t)rows * ld_max;
+    xs_rows = rows;
+    for (int i = 0; i < 2; i++) {
+        xq[i] = A.alloc<int8_t>(xq_bytes);
+        xs[i] = A.alloc<float>(rows);
+    }
+}
+
+void quantize(const Ctx& c, const QAct& dst, const float* x, int ldx, int seq, int K) {
+    VLA_REQUIRE((size_t)seq * dst.ld <= c.xq_bytes && seq <= c.xs_rows,
+                "graph: activation quantization scratch too small");
+    launch_quantize_rows(x, ldx, dst.q, dst.ld, dst.s, seq, K, c.st);
+}
+
+static void gemm_q(const Ctx& c, const DLinear& L, const QAct& x, float* out, int ldo, int seq, int act,
+                   int acc, int n0, int n1) {
     const vla_linear_i8& q = *L.q8;
+    VLA_REQUIRE(x.ld == q.ldw(), "linear: quantized input laid out for another layer width");
     GemmArgs a{};
-    a.A = c.xq;
-    a.lda = q.ldw();
+    a.A = x.q;
+    a.lda = x.ld;
     a.B = q.Wq() + (size_t)n0 * q.ldw();
     a.ldb = q.ldw();
-    a.ascale = c.xs;
+    a.ascale = x.s;
     a.wscale = q.wscale() + n0;
     a.bias = q.bias() ? q.bias() + n0 : nullptr;
     a.out = out;
@@ -77,29 +95,48 @@ static void gemm_q(const Ctx& c, const DLinear& L, float* out, int ldo, int seq,
     launch_gemm_i8(a, c.st);
 }
 
-void linear(const Ctx& c, const DLinear& L, float* out, int ldo, const float* x, int ldx, int seq,
-            int act, int acc, int n0, int n1, float alpha) {
+void linear(const Ctx& c, const DLinear& L, const In& in, float* out, int ldo, int seq, int act, int acc,
+            int n0, int n1, float alpha) {
     if (n1 < 0) n1 = L.N;
     VLA_REQUIRE(0 <= n0 && n0 < n1 && n1 <= L.N, "linear: bad output row range");
     if (seq == 0) return;
     if (L.int8()) {
         VLA_REQUIRE(alpha == 1.0f, "linear: the int8 epilogue accumulates with alpha = 1 only");
         VLA_REQUIRE(act <= 3, "linear: the int8 epilogue has no silu");
-        quantize(c, x, ldx, seq, L.K, L.ldq());
-        gemm_q(c, L, out, ldo, seq, act, acc, n0, n1);
+        if (in.quantized) {
+            gemm_q(c, L, in.q, out, ldo, seq, act, acc, n0, n1);
+        } else {
+            VLA_REQUIRE(in.f, "linear: no input");
+            const QAct s0 = c.slot(0, L.ldq());
+            quantize(c, s0, in.f, in.ldf, seq, L.K);
+            gemm_q(c, L, s0, out, ldo, seq, act, acc, n0, n1);
+        }
     } else {
-        launch_linear_f32(out, ldo, x, ldx, L.W + (size_t)n0 * L.K, L.K, L.b ? L.b + n0 : nullptr, seq,
+        VLA_REQUIRE(in.f, "linear: an fp32 layer needs fp32 input rows");
+        launch_linear_f32(out, ldo, in.f, in.ldf, L.W + (size_t)n0 * L.K, L.K, L.b ? L.b + n0 : nullptr, seq,
                           n1 - n0, L.K, act, acc, alpha, c.st);
     }
 }
 
-void linear_q(const Ctx& c, const DLinear& L, float* out, int ldo, int seq, int act, int acc, int n0,
-              int n1) {
-    if (n1 < 0) n1 = L.N;
-    VLA_REQUIRE(L.int8(), "linear_q: layer is not int8");
-    VLA_REQUIRE(0 <= n0 && n0 < n1 && n1 <= L.N, "linear: bad output row range");
-    if (seq == 0) return;
-    gemm_q(c, L, out, ldo, seq, act, acc, n0, n1);
+In rowop_for(const Ctx& c, const DLinear& L, RowQArgs r, float* f, int ldf, int slot) {
+    In in;
+    r.out = f;
+    r.ldo = ldf;
+    if (L.int8()) {
+        VLA_REQUIRE((size_t)r.rows * L.ldq() <= c.xq_bytes && r.rows <= c.xs_rows,
+                    "graph: activation quantization scratch too small");
+        in.q = c.slot(slot, L.ldq());
+        in.quantized = true;
+        r.q = in.q.q;
+        r.ldq = in.q.ld;
+        r.qs = in.q.s;
+    } else {
+        VLA_REQUIRE(f, "graph: an fp32 consumer needs the fp32 rows");
+    }
+    in.f = f;
+    in.ldf = ldf;
+    launch_rowq(r, c.st);
+    return in;
 }
 
 void attend(hipStream_t st, float* out, int ldo, const float* Q, int ldq, const float* K, int ldk,

@@ -75,27 +75,57 @@ struct DLinear {
     }
 };
 
-// Per-model stream state: the activation-quantization scratch shared by every
-// int8 layer (the reference's thread_local xq/ascale, src/nn/linear.cpp:123-127).
-struct Ctx {
-    hipStream_t st = nullptr;
-    int8_t* xq = nullptr;
-    float* xs = nullptr;
-    size_t xq_bytes = 0;
-    int xs_rows = 0;
+// Quantized activations: int8 rows [seq, ld] + per-row scales [seq].
+struct QAct {
+    int8_t* q = nullptr;
+    float* s = nullptr;
+    int ld = 0;
 };
 
-// x [seq, K] (row stride ldx) -> ctx.xq [seq, ldq], ctx.xs [seq].
-void quantize(const Ctx& c, const float* x, int ldx, int seq, int K, int ldq);
+// Per-model stream state: two activation-quantization slots shared by every
+// int8 layer (the reference's thread_local xq/ascale, src/nn/linear.cpp:123-127),
+// each [rows, ld_max] int8 + [rows] scales.
+struct Ctx {
+    hipStream_t st = nullptr;
+    int8_t* xq[2] = {nullptr, nullptr};
+    float* xs[2] = {nullptr, nullptr};
+    size_t xq_bytes = 0;
+    int xs_rows = 0;
+    // slot i laid out for a layer of row stride ld
+    QAct slot(int i, int ld) const;
+    void alloc(class DeviceArena& A, int rows, int ld_max);
+};
 
-// out[:, n0:n1] (+)= act(x W[n0:n1]^T + b). int8 layers quantize x into the
-// context scratch first. acc != 0 adds into out (fmaf(alpha, v, out) for fp32
-// layers; the int8 epilogue adds v, alpha must be 1).
-void linear(const Ctx& c, const DLinear& L, float* out, int ldo, const float* x, int ldx, int seq,
-            int act = 0, int acc = 0, int n0 = 0, int n1 = -1, float alpha = 1.0f);
-// int8 layer on activations already in ctx.xq / ctx.xs (quantized with ldq = L.ldq()).
-void linear_q(const Ctx& c, const DLinear& L, float* out, int ldo, int seq, int act = 0, int acc = 0,
-              int n0 = 0, int n1 = -1);
+// The input of a linear layer: fp32 rows, or rows already quantized for it
+// (q.ld == the layer's ldq()).
+struct In {
+    const float* f = nullptr;
+    int ldf = 0;
+    QAct q;               // valid when quantized
+    bool quantized = false;
+};
+
+// x [seq, K] (row stride ldx) -> dst
+void quantize(const Ctx& c, const QAct& dst, const float* x, int ldx, int seq, int K);
+
+// out[:, n0:n1] (+)= act(x W[n0:n1]^T + b). An int8 layer takes in.q when
+// in.quantized, else quantizes in.f into slot 0. acc != 0 adds into out
+// (fmaf(alpha, v, out) for fp32 layers; the int8 epilogue adds v, alpha must
+// be 1).
+void linear(const Ctx& c, const DLinear& L, const In& in, float* out, int ldo, int seq, int act = 0,
+            int acc = 0, int n0 = 0, int n1 = -1, float alpha = 1.0f);
+inline void linear(const Ctx& c, const DLinear& L, float* out, int ldo, const float* x, int ldx,
+                   int seq, int act = 0, int acc = 0, int n0 = 0, int n1 = -1, float alpha = 1.0f) {
+    In in;
+    in.f = x;
+    in.ldf = ldx;
+    linear(c, L, in, out, ldo, seq, act, acc, n0, n1, alpha);
+}
+
+// A row op (RowQArgs op / x / u / w / b / eps / rows / H) whose result feeds
+// layer L: an int8 L gets it quantized in the same kernel, into `slot` (and
+// fp32 rows into f when f is non-null); an fp32 L gets fp32 rows in f.
+In rowop_for(const Ctx& c, const DLinear& L, RowQArgs r, float* f, int ldf, int slot);
 
 // Which keys a query may see (AttnArgs' mask fields): kind 0 none, 1 dense
 // additive [sq, ldm], 2 causal (key j blocked when j > i + causal_offset),

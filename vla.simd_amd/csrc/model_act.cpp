@@ -184,8 +184,8 @@ void ActTf::ensure(int n_cams, int fh, int fw) {
     dx_ = S->alloc<float>((size_t)C * d);
     zero_ = S->alloc<float>((size_t)C * d);
     kpos_ = S->alloc<float>((size_t)T * d);
-    ckb_ = S->alloc<float>((size_t)T * d);
-    cvb_ = S->alloc<float>((size_t)T * d);
+    ckb_ = S->alloc<float>((size_t)n_dec_ * T * d);
+    cvb_ = S->alloc<float>((size_t)n_dec_ * T * d);
     dq_ = S->alloc<float>((size_t)C * d);
     // positions: [pos1d | camera embedding per camera] (build_tokens :218-229)
     std::vector<float> pos((size_t)T * d), cam((size_t)n_img * d);
@@ -199,11 +199,7 @@ void ActTf::ensure(int n_cams, int fh, int fw) {
     // quantization scratch: the widest int8 input is ff (w2) over T rows
     int maxld = round_up(kpad4(ff_ > img_ch_ ? ff_ : img_ch_), 64);
     if (round_up(kpad4(d), 64) > maxld) maxld = round_up(kpad4(d), 64);
-    const int rows = T > C ? T : C;
-    ctx_.xq_bytes = (size_t)rows * maxld;
-    ctx_.xq = S->alloc<int8_t>(ctx_.xq_bytes);
-    ctx_.xs_rows = rows;
-    ctx_.xs = S->alloc<float>(rows);
+    ctx_.alloc(*S, R, maxld);
     S_ = std::move(S);
     n_cams_ = n_cams;
     fh_ = fh;
@@ -218,46 +214,143 @@ void ActTf::run(hipStream_t st) {
     const float scale = 1.0f / std::sqrt((float)hd_);
     const MaskSpec none;
 
+    // The row kernel that ends each block (and the token assembly) also
+    // quantizes what the next block's projections read: x + pos for q | k
+    // (slot 0) and x for v (slot 1), so no layer quantizes its own input.
+    // row op over x (in place), quantizing x -> slot 1 and x + add -> slot 0 for
+    // the consumers qk / v (fp32 consumers get xp_ / x_ rows instead)
+    auto feed = [&](int op, float* x, int rows, const float* w, const float* b, const float* add,
+                    const DLinear& qk, const DLinear& v, In& in_qk, In& in_v) {
+        RowQArgs r;
+        r.op = op;
+        r.x = x;
+        r.ldx = d;
+        r.w = w;
+        r.b = b;
+        r.eps = eps_;
+        r.rows = rows;
+        r.H = d;
+        r.out = op ? x : nullptr;
+        r.ldo = d;
+        r.add = add;
+        r.ld_add = d;
+        in_qk = In();
+        in_v = In();
+        in_v.f = x;
+        in_v.ldf = d;
+        if (v.int8()) {
+            in_v.q = c.slot(1, v.ldq());
+            in_v.quantized = true;
+            r.q = in_v.q.q;
+            r.ldq = in_v.q.ld;
+            r.qs = in_v.q.s;
+        }
+        in_qk.f = xp_;
+        in_qk.ldf = d;
+        if (qk.int8()) {
+            in_qk.q = c.slot(0, qk.ldq());
+            in_qk.quantized = true;
+            r.q2 = in_qk.q.q;
+            r.ldq2 = in_qk.q.ld;
+            r.qs2 = in_qk.q.s;
+        } else {
+            r.out2 = xp_;
+            r.ldo2 = d;
+        }
+        launch_rowq(r, st);
+    };
+    auto norm_for = [&](float* x, int rows, const float* w, const float* b, const DLinear& next) {
+        RowQArgs r;
+        r.op = 1;
+        r.x = x;
+        r.ldx = d;
+        r.w = w;
+        r.b = b;
+        r.eps = eps_;
+        r.rows = rows;
+        r.H = d;
+        return rowop_for(c, next, r, x, d, 0);  // in place, as layernorm(x, x)
+    };
+
     // build_tokens (:212-250): latent, state projection, camera tokens
     copy_f32(x_, latent_, d, st);
     linear(c, state_proj_, x_ + d, d, state_, state_dim_, 1);
     linear(c, img_proj_, x_ + (size_t)n_1d_ * d, d, feats_, img_ch_, n_cams_ * n_img);
 
     // encode (:252-301)
-    for (const Enc& l : enc_) {
-        launch_add(xp_, x_, pos_, (int64_t)T * d, st);
-        linear(c, l.qk, qk_, 2 * d, xp_, d, T);  // q | k from x + pos
-        linear(c, l.v, v_, d, x_, d, T);         // v from x
+    In in_qk, in_v;
+    feed(0, x_, T, nullptr, nullptr, pos_, enc_[0].qk, enc_[0].v, in_qk, in_v);
+    for (size_t li = 0; li < enc_.size(); li++) {
+        const Enc& l = enc_[li];
+        linear(c, l.qk, in_qk, qk_, 2 * d, T);  // q | k from x + pos
+        linear(c, l.v, in_v, v_, d, T);         // v from x
         attend(st, att_, d, qk_, 2 * d, qk_ + d, 2 * d, v_, d, T, T, heads_, heads_, hd_, scale, none);
         linear(c, l.o, x_, d, att_, d, T, 0, 1);  // x += wo(att)
-        launch_layernorm(x_, x_, l.n1s, l.n1b, T, d, eps_, st);
-        linear(c, l.w1, ff_buf_, ff_, x_, d, T, 1);  // relu
+        const In h = norm_for(x_, T, l.n1s, l.n1b, l.w1);
+        linear(c, l.w1, h, ff_buf_, ff_, T, 1);  // relu
         linear(c, l.w2, x_, d, ff_buf_, ff_, T, 0, 1);
-        launch_layernorm(x_, x_, l.n2s, l.n2b, T, d, eps_, st);
+        // LN2, then the next block's inputs (or, after the last, the memory the
+        // decoder's cross-attention reads: keys from x + pos, values from x)
+        const DLinear& nqk = li + 1 < enc_.size() ? enc_[li + 1].qk : dec_[0].ck;
+        const DLinear& nv = li + 1 < enc_.size() ? enc_[li + 1].v : dec_[0].cv;
+        feed(1, x_, T, l.n2s, l.n2b, pos_, nqk, nv, in_qk, in_v);
     }
 
-    // decode (:303-356)
-    launch_add(kpos_, x_, pos_, (int64_t)T * d, st);
+    // decode (:303-356). The cross-attention keys and values depend only on the
+    // encoder output, so each layer's are projected here, before the decoder.
+    for (size_t li = 0; li < dec_.size(); li++) {
+        const Dec& l = dec_[li];
+        if (li > 0) feed(0, x_, T, nullptr, nullptr, pos_, l.ck, l.cv, in_qk, in_v);
+        linear(c, l.ck, in_qk, ckb_ + (size_t)li * T * d, d, T);
+        linear(c, l.cv, in_v, cvb_ + (size_t)li * T * d, d, T);
+    }
     copy_f32(dx_, zero_, (int64_t)C * d, st);  // queries start at zero
-    for (const Dec& l : dec_) {
-        launch_add(xp_, dx_, dec_pos_, (int64_t)C * d, st);
-        linear(c, l.sqk, qk_, 2 * d, xp_, d, C);
-        linear(c, l.sv, v_, d, dx_, d, C);
+    feed(0, dx_, C, nullptr, nullptr, dec_pos_, dec_[0].sqk, dec_[0].sv, in_qk, in_v);
+    for (size_t li = 0; li < dec_.size(); li++) {
+        const Dec& l = dec_[li];
+        linear(c, l.sqk, in_qk, qk_, 2 * d, C);
+        linear(c, l.sv, in_v, v_, d, C);
         attend(st, att_, d, qk_, 2 * d, qk_ + d, 2 * d, v_, d, C, C, heads_, heads_, hd_, scale, none);
         linear(c, l.so, dx_, d, att_, d, C, 0, 1);
-        launch_layernorm(dx_, dx_, l.n1s, l.n1b, C, d, eps_, st);
-
-        launch_add(xp_, dx_, dec_pos_, (int64_t)C * d, st);
-        linear(c, l.cq, dq_, d, xp_, d, C);
-        linear(c, l.ck, ckb_, d, kpos_, d, T);  // keys carry the encoder positions
-        linear(c, l.cv, cvb_, d, x_, d, T);     // values do not
-        attend(st, att_, d, dq_, d, ckb_, d, cvb_, d, C, T, heads_, heads_, hd_, scale, none);
+        // LN1, then the cross query input dx + dec_pos
+        RowQArgs r;
+        r.op = 1;
+        r.x = dx_;
+        r.ldx = d;
+        r.w = l.n1s;
+        r.b = l.n1b;
+        r.eps = eps_;
+        r.rows = C;
+        r.H = d;
+        r.out = dx_;
+        r.ldo = d;
+        r.add = dec_pos_;
+        r.ld_add = d;
+        In in_q;
+        in_q.f = xp_;
+        in_q.ldf = d;
+        if (l.cq.int8()) {
+            in_q.q = c.slot(0, l.cq.ldq());
+            in_q.quantized = true;
+            r.q2 = in_q.q.q;
+            r.ldq2 = in_q.q.ld;
+            r.qs2 = in_q.q.s;
+        } else {
+            r.out2 = xp_;
+            r.ldo2 = d;
+        }
+        launch_rowq(r, st);
+        linear(c, l.cq, in_q, dq_, d, C);
+        attend(st, att_, d, dq_, d, ckb_ + (size_t)li * T * d, d, cvb_ + (size_t)li * T * d, d, C, T,
+               heads_, heads_, hd_, scale, none);
         linear(c, l.co, dx_, d, att_, d, C, 0, 1);
-        launch_layernorm(dx_, dx_, l.n2s, l.n2b, C, d, eps_, st);
-
-        linear(c, l.w1, ff_buf_, ff_, dx_, d, C, 1);
+        const In h = norm_for(dx_, C, l.n2s, l.n2b, l.w1);
+        linear(c, l.w1, h, ff_buf_, ff_, C, 1);
         linear(c, l.w2, dx_, d, ff_buf_, ff_, C, 0, 1);
-        launch_layernorm(dx_, dx_, l.n3s, l.n3b, C, d, eps_, st);
+        if (li + 1 < dec_.size())
+            feed(1, dx_, C, l.n3s, l.n3b, dec_pos_, dec_[li + 1].sqk, dec_[li + 1].sv, in_qk, in_v);
+        else
+            launch_layernorm(dx_, dx_, l.n3s, l.n3b, C, d, eps_, st);
     }
     launch_layernorm(dx_, dx_, dec_ns_, dec_nb_, C, d, eps_, st);
     linear(c, head_, act_out_, action_dim_, dx_, d, C);

@@ -199,10 +199,7 @@ void OctoTf::ensure(int wnd, const uint8_t* tmask, bool wrist) {
     int maxld = round_up(kpad4(mlp_), 64);
     for (int k : {D, t5_dim_, stem_dim_})
         if (round_up(kpad4(k), 64) > maxld) maxld = round_up(kpad4(k), 64);
-    ctx_.xq_bytes = (size_t)total * maxld;
-    ctx_.xq = S->alloc<int8_t>(ctx_.xq_bytes);
-    ctx_.xs_rows = total;
-    ctx_.xs = S->alloc<float>(total);
+    ctx_.alloc(*S, total, maxld);
     S_ = std::move(S);
     key_ = key;
     wnd_ = wnd;
@@ -235,16 +232,31 @@ void OctoTf::run(hipStream_t st) {
         if (repeat_task_) linear(c, proj_task_, row, D, t5_, t5_dim_, n_task_, 0, 1);
     }
 
+    // LayerNorm rows of x feeding layer L: quantized in the same kernel when L
+    // is int8 (h_ gets the fp32 rows only when L is fp32)
+    auto ln_for = [&](const float* x, int rows, const float* w, const float* b, const DLinear& L) {
+        RowQArgs r;
+        r.op = 1;
+        r.x = x;
+        r.ldx = D;
+        r.w = w;
+        r.b = b;
+        r.eps = eps_;
+        r.rows = rows;
+        r.H = D;
+        return rowop_for(c, L, r, L.int8() ? nullptr : h_, D, 0);
+    };
+
     // blocks 0 .. n-2 (EncoderLayer::forward)
     for (int li = 0; li + 1 < n_layers_; li++) {
         const Layer& L = layers_[li];
-        launch_layernorm(h_, x_, L.ln1s, L.ln1b, T, D, eps_, st);
-        linear(c, L.qkv, qkv_, 3 * D, h_, D, T);
+        const In h1 = ln_for(x_, T, L.ln1s, L.ln1b, L.qkv);
+        linear(c, L.qkv, h1, qkv_, 3 * D, T);
         attend(st, att_, D, qkv_, 3 * D, qkv_ + D, 3 * D, qkv_ + 2 * D, 3 * D, T, T, heads_, heads_, hd_,
                scale, mask);
         linear(c, L.o, x_, D, att_, D, T, 0, 1);
-        launch_layernorm(h_, x_, L.ln2s, L.ln2b, T, D, eps_, st);
-        linear(c, L.w1, ff_buf_, mlp_, h_, D, T, gelu);
+        const In h2 = ln_for(x_, T, L.ln2s, L.ln2b, L.w1);
+        linear(c, L.w1, h2, ff_buf_, mlp_, T, gelu);
         linear(c, L.w2, x_, D, ff_buf_, mlp_, T, 0, 1);
     }
 
@@ -252,25 +264,22 @@ void OctoTf::run(hipStream_t st) {
     const Layer& L = layers_.back();
     const int ro = readout_index(wnd);
     float* xr = x_ + (size_t)ro * D;
-    launch_layernorm(h_, x_, L.ln1s, L.ln1b, T, D, eps_, st);
-    if (L.qkv.int8()) {
-        quantize(c, h_, D, T, D, L.qkv.ldq());
-        linear_q(c, L.qkv, qkv_ + D, 3 * D, T, 0, 0, D, 3 * D);  // k | v, every row
-        Ctx cr = c;                                                // q of the readout row
-        cr.xq += (size_t)ro * L.qkv.ldq();
-        cr.xs += ro;
-        linear_q(cr, L.qkv, qkv_ + (size_t)ro * 3 * D, 3 * D, 1, 0, 0, 0, D);
-    } else {
-        linear(c, L.qkv, qkv_ + D, 3 * D, h_, D, T, 0, 0, D, 3 * D);
-        linear(c, L.qkv, qkv_ + (size_t)ro * 3 * D, 3 * D, h_ + (size_t)ro * D, D, 1, 0, 0, 0, D);
+    const In h1 = ln_for(x_, T, L.ln1s, L.ln1b, L.qkv);
+    linear(c, L.qkv, h1, qkv_ + D, 3 * D, T, 0, 0, D, 3 * D);  // k | v, every row
+    In hr = h1;                                                   // q of the readout row
+    if (hr.quantized) {
+        hr.q.q += (size_t)ro * hr.q.ld;
+        hr.q.s += ro;
     }
+    if (hr.f) hr.f += (size_t)ro * D;
+    linear(c, L.qkv, hr, qkv_ + (size_t)ro * 3 * D, 3 * D, 1, 0, 0, 0, D);
     MaskSpec mr = mask;
     mr.qg = qg_ + ro;
     attend(st, att_, D, qkv_ + (size_t)ro * 3 * D, 3 * D, qkv_ + D, 3 * D, qkv_ + 2 * D, 3 * D, 1, T,
            heads_, heads_, hd_, scale, mr);
     linear(c, L.o, xr, D, att_, D, 1, 0, 1);
-    launch_layernorm(h_, xr, L.ln2s, L.ln2b, 1, D, eps_, st);
-    linear(c, L.w1, ff_buf_, mlp_, h_, D, 1, gelu);
+    const In h2 = ln_for(xr, 1, L.ln2s, L.ln2b, L.w1);
+    linear(c, L.w1, h2, ff_buf_, mlp_, 1, gelu);
     linear(c, L.w2, xr, D, ff_buf_, mlp_, 1, 0, 1);
     launch_layernorm(out_, xr, final_s_, final_b_, 1, D, eps_, st);
 }

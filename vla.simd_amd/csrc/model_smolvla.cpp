@@ -273,11 +273,7 @@ void SmolvlaTf::ensure(const int32_t* pad, int np) {
     int maxld = 0;
     for (int k : {H_, QF, F_, EH, EF_, KV, 2 * EH})
         if (round_up(kpad4(k), 64) > maxld) maxld = round_up(kpad4(k), 64);
-    const int rows = np > C ? np : C;
-    ctx_.xq_bytes = (size_t)rows * maxld;
-    ctx_.xq = S->alloc<int8_t>(ctx_.xq_bytes);
-    ctx_.xs_rows = rows;
-    ctx_.xs = S->alloc<float>(rows);
+    ctx_.alloc(*S, R, maxld);
     S_ = std::move(S);
     key_ = key;
     np_ = np;
@@ -291,6 +287,32 @@ void SmolvlaTf::run(hipStream_t st) {
     const int EH = EH_, EF = EF_, F = F_;
     const float scale = 1.0f / std::sqrt((float)hd_);
 
+    // row op feeding layer L: quantized in the same kernel for an int8 L, fp32
+    // rows in f for an fp32 L
+    auto rms_for = [&](const float* x, int rows, int H_, const float* w, float eps, const DLinear& L,
+                       float* f) {
+        RowQArgs r;
+        r.op = 2;
+        r.x = x;
+        r.ldx = H_;
+        r.w = w;
+        r.eps = eps;
+        r.rows = rows;
+        r.H = H_;
+        return rowop_for(c, L, r, L.int8() ? nullptr : f, H_, 0);
+    };
+    auto silu_for = [&](const float* gu_raw, int rows, int Fw, const DLinear& L) {
+        RowQArgs r;
+        r.op = 3;
+        r.x = gu_raw;
+        r.ldx = 2 * Fw;
+        r.u = gu_raw + Fw;
+        r.ldu = 2 * Fw;
+        r.rows = rows;
+        r.H = Fw;
+        return rowop_for(c, L, r, L.int8() ? nullptr : gu_, Fw, 0);
+    };
+
     // ---- prefix_forward (smollm2_lm.cpp:85-132)
     MaskSpec pm;
     pm.kind = 3;
@@ -302,20 +324,20 @@ void SmolvlaTf::run(hipStream_t st) {
     for (int L = 0; L < NL_; L++) {
         const VlmLayer& w = vlm_[L];
         float* buf = qkv_[L];
-        launch_rmsnorm(xn_, h_, w.ln_in, np, H, eps_, st);
+        const In xn = rms_for(h_, np, H, w.ln_in, eps_, w.qkv, xn_);
         if (L + 1 == NL_) {  // the last layer's K/V only (:107)
-            linear(c, w.qkv, buf + QF, W, xn_, H, np, 0, 0, QF, QF + 2 * KV);
+            linear(c, w.qkv, xn, buf + QF, W, np, 0, 0, QF, QF + 2 * KV);
             launch_rope_neox(buf + QF, W, pos_, np, nkv_, hd_, rope_base_, st);
             break;
         }
-        linear(c, w.qkv, buf, W, xn_, H, np);
+        linear(c, w.qkv, xn, buf, W, np);
         launch_rope_neox(buf, W, pos_, np, nq_ + nkv_, hd_, rope_base_, st);  // q and k heads
         attend(st, att_, QF, buf, W, buf + QF, W, buf + QF + KV, W, np, np, nq_, nkv_, hd_, scale, pm);
         linear(c, w.o, h_, H, att_, QF, np, 0, 1);
-        launch_rmsnorm(xn_, h_, w.ln_post, np, H, eps_, st);
-        linear(c, w.gu, gu_raw_, 2 * F, xn_, H, np);
-        launch_silu_gate_rows(gu_, F, gu_raw_, 2 * F, gu_raw_ + F, 2 * F, np, F, st);
-        linear(c, w.down, h_, H, gu_, F, np, 0, 1);
+        const In x2 = rms_for(h_, np, H, w.ln_post, eps_, w.gu, xn_);
+        linear(c, w.gu, x2, gu_raw_, 2 * F, np);
+        const In g = silu_for(gu_raw_, np, F, w.down);
+        linear(c, w.down, g, h_, H, np, 0, 1);
     }
 
     // ---- denoise (action_expert.cpp:325-395): cross-layer K/V re-projections once
@@ -347,24 +369,24 @@ void SmolvlaTf::run(hipStream_t st) {
         linear(c, at2_, eh_, EH, mlp1_, EH, C);
         for (int L = 0; L < ENL_; L++) {
             const ExpLayer& w = exp_[L];
-            launch_rmsnorm(ehn_, eh_, w.ln_in, C, EH, eeps_, st);
+            const In hn = rms_for(eh_, C, EH, w.ln_in, eeps_, w.q_or_qkv, ehn_);
             if (w.self) {
                 float* buf = qkv_[L];
                 float* suf = buf + (size_t)np * W;
-                linear(c, w.q_or_qkv, suf, W, ehn_, EH, C);
+                linear(c, w.q_or_qkv, hn, suf, W, C);
                 launch_rope_neox(suf, W, pos_full_, C, enq_ + enkv_, ehd_, erope_, st);
                 attend(st, att_, QF, suf, W, buf + QF, W, buf + QF + KV, W, C, SK, enq_, enkv_, ehd_,
                        scale, dm);
             } else {
-                linear(c, w.q_or_qkv, eq_, QF, ehn_, EH, C);
+                linear(c, w.q_or_qkv, hn, eq_, QF, C);
                 launch_rope_neox(eq_, QF, pos_reb_, C, enq_, ehd_, erope_, st);
                 attend(st, att_, QF, eq_, QF, ck_[L], KV, cv_[L], KV, C, np, enq_, enkv_, ehd_, scale, cm);
             }
             linear(c, w.o, eh_, EH, att_, QF, C, 0, 1);
-            launch_rmsnorm(ehn_, eh_, w.ln_post, C, EH, eeps_, st);
-            linear(c, w.gu, gu_raw_, 2 * EF, ehn_, EH, C);
-            launch_silu_gate_rows(gu_, EF, gu_raw_, 2 * EF, gu_raw_ + EF, 2 * EF, C, EF, st);
-            linear(c, w.down, eh_, EH, gu_, EF, C, 0, 1);
+            const In h2 = rms_for(eh_, C, EH, w.ln_post, eeps_, w.gu, ehn_);
+            linear(c, w.gu, h2, gu_raw_, 2 * EF, C);
+            const In g = silu_for(gu_raw_, C, EF, w.down);
+            linear(c, w.down, g, eh_, EH, C, 0, 1);
         }
         launch_rmsnorm(hf_, eh_, out_norm_, C, EH, eeps_, st);
         linear(c, aout_, x_, mad_, hf_, EH, C, 0, 1, 0, -1, dt);  // x += dt * v_t

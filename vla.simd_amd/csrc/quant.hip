@@ -16,27 +16,13 @@
 // the second pass re-reads it from L1/L2.
 
 #include "common.h"
-
-#include <cfloat>
+#include "quant_row.h"
 
 #pragma clang fp contract(off)
 
 namespace vla {
 namespace hip {
 namespace {
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
-
-__device__ __forceinline__ int q8(float v, float inv) {
-    int q = (int)rintf(v * inv);
-    q = q > 127 ? 127 : q;
-    q = q < -127 ? -127 : q;
-    return q;
-}
 
 // VEC: rows are 16-byte aligned and K % 4 == 0, so float4 loads cover the row.
 template <bool VEC>
@@ -58,13 +44,8 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const float* __restr
     } else {
         for (int k = lane; k < K; k += 64) amax = fmaxf(amax, fabsf(xr[k]));
     }
-    amax = wave_max(amax);
-
-    float s = 1.0f;
-    if (amax > 0.0f) {
-        s = amax / 127.0f;
-        s = s > FLT_MIN ? s : FLT_MIN;
-    }
+    amax = wave_max_f32(amax);
+    const float s = row_scale(amax);
     const float inv = 1.0f / s;
     if (lane == 0) scale[row] = s;
 
@@ -75,8 +56,7 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const float* __restr
         uint32_t word = 0;
         if (VEC && k + 4 <= K) {
             const float4 v = *reinterpret_cast<const float4*>(xr + k);
-            word = (uint32_t)(q8(v.x, inv) & 0xff) | ((uint32_t)(q8(v.y, inv) & 0xff) << 8) |
-                   ((uint32_t)(q8(v.z, inv) & 0xff) << 16) | ((uint32_t)(q8(v.w, inv) & 0xff) << 24);
+            word = q8x4(v, inv);
         } else {
 #pragma unroll
             for (int j = 0; j < 4; j++) {
