@@ -227,7 +227,63 @@ def _time_cpu(fn, min_calls=3, min_s=1.0):
     return (time.perf_counter() - t0) * 1e3 / n
 
 
-def policy_latency(vla, torch, stream_obj, with_cpu=True):
+def _lat_act(vla, torch, ck, ob, tmp, stream_obj):
+    """ACT: 4 x 302-token encoder, 100-query decoder, ACT_INT8=31."""
+    dev, st = torch.device("cuda"), stream_obj.cuda_stream
+    c = ck.ACT_BASE
+    d = ck.write_act(os.path.join(tmp, "act"), c)
+    f, s = ck.act_inputs(c)
+    m = vla.ActTransformer(d, c["img_ch"], 31)
+    tf, ts = torch.from_numpy(f).to(dev), torch.from_numpy(s).to(dev)
+    ta = torch.empty((c["chunk"], c["action_dim"]), dtype=torch.float32, device=dev)
+    gpu = _time_calls(torch, lambda: m.forward_dev(tf, 1, c["fh"], c["fw"], ts, ta, st), stream_obj)
+    row = {"gpu_ms": round(gpu, 4), "tokens": m_tokens_act(c), "int8_mask": 31,
+           "int8_layers": m.int8_layers, "graph_nodes": m.graph_nodes}
+    if ob is not None:
+        r = ob.RefAct(d, c["img_ch"], 31, c["chunk"], c["action_dim"])
+        row["cpu_ref_ms"] = round(_time_cpu(lambda: r.forward(f, 1, c["fh"], c["fw"], s)), 3)
+    return row
+
+
+def _lat_octo(vla, torch, ck, ob, tmp, stream_obj, repeat_task):
+    """Octo-base: 12 x 768; repeat_task 0 is BASELINE's 658-token layout, 1 the
+    reference's 690-token layout (the only one the reference runs)."""
+    dev, st = torch.device("cuda"), stream_obj.cuda_stream
+    c = dict(ck.OCTO_BASE, repeat_task=repeat_task)
+    d = ck.write_octo(os.path.join(tmp, f"octo{repeat_task}"), c)
+    t5, sp, sw, tm = ck.octo_inputs(c)
+    m = vla.OctoTransformer(d, 7)
+    a, b, w = (torch.from_numpy(v).to(dev) for v in (t5, sp, sw))
+    o = torch.empty(c["d"], dtype=torch.float32, device=dev)
+    gpu = _time_calls(torch, lambda: m.forward_dev(a, b, w, 2, tm, o, st), stream_obj)
+    row = {"gpu_ms": round(gpu, 4), "tokens": m.total_tokens(2), "int8_mask": 7,
+           "int8_layers": m.int8_layers, "graph_nodes": m.graph_nodes}
+    if ob is not None and repeat_task:
+        r = ob.RefOcto(d, 7, c["d"])
+        row["cpu_ref_ms"] = round(_time_cpu(lambda: r.forward(t5, sp, sw, 2, tm)), 3)
+    return row
+
+
+def _lat_smolvla(vla, torch, ck, ob, tmp, stream_obj):
+    """SmolVLA chunk: 16-layer prefix over 177 tokens + 10 Euler steps of the
+    16-layer expert, SMOLVLA_INT8=48."""
+    dev, st = torch.device("cuda"), stream_obj.cuda_stream
+    c = ck.SMOLVLA_BASE
+    d = ck.write_smolvla(os.path.join(tmp, "smol"), c)
+    p, pad, n = ck.smolvla_inputs(c)
+    m = vla.SmolvlaChunk(d, 48)
+    tp, tn = torch.from_numpy(p).to(dev), torch.from_numpy(n).to(dev)
+    ta = torch.empty((c["chunk"], c["max_action_dim"]), dtype=torch.float32, device=dev)
+    gpu = _time_calls(torch, lambda: m.run_dev(tp, pad, tn, ta, st), stream_obj, min_calls=10)
+    row = {"gpu_ms": round(gpu, 4), "prefix_tokens": c["n_prefix"], "steps": c["num_steps"],
+           "int8_mask": 48, "int8_layers": m.int8_layers, "graph_nodes": m.graph_nodes}
+    if ob is not None:
+        r = ob.RefSmolvla(d, 48)
+        row["cpu_ref_ms"] = round(_time_cpu(lambda: r.run(p, pad, n)), 3)
+    return row
+
+
+def policy_latency(vla, torch, stream_obj, with_cpu=True, models=("act", "octo", "smolvla")):
     """Per-chunk latency of BASELINE.json configs[2..4] at batch 1: the device
     graphs (one captured HIP graph per forward, inputs resident in HBM) and the
     reference's own graphs (oracle/_ref) on this host, on the same random-init
@@ -241,74 +297,27 @@ def policy_latency(vla, torch, stream_obj, with_cpu=True):
         from oracle import bindings as ob
         if not ob.ref_available():
             ob = None
-    dev = torch.device("cuda")
     out = {}
     with tempfile.TemporaryDirectory(prefix="vla_ck_") as tmp:
-        # ACT: 4 x 302-token encoder, 100-query decoder, ACT_INT8=31
-        c = ck.ACT_BASE
-        d = ck.write_act(os.path.join(tmp, "act"), c)
-        f, s = ck.act_inputs(c)
-        m = vla.ActTransformer(d, c["img_ch"], 31)
-        tf, ts = torch.from_numpy(f).to(dev), torch.from_numpy(s).to(dev)
-        ta = torch.empty((c["chunk"], c["action_dim"]), dtype=torch.float32, device=dev)
-        st = stream_obj.cuda_stream
-        gpu = _time_calls(torch, lambda: m.forward_dev(tf, 1, c["fh"], c["fw"], ts, ta, st), stream_obj)
-        row = {"gpu_ms": round(gpu, 4), "tokens": 302, "int8_mask": 31, "int8_layers": m.int8_layers,
-               "graph_nodes": m.graph_nodes}
-        if ob is not None:
-            r = ob.RefAct(d, c["img_ch"], 31, c["chunk"], c["action_dim"])
-            row["cpu_ref_ms"] = round(_time_cpu(lambda: r.forward(f, 1, c["fh"], c["fw"], s)), 3)
-            del r
-        out["act"] = row
-        del m
-        print(f"  ACT transformer: {row}", file=sys.stderr, flush=True)
-
-        # Octo-base: 12 x 768, BASELINE layout (658 tokens) and the reference's
-        # repeated-task layout (690 tokens, which is what the reference runs)
-        for rep in (0, 1):
-            c = dict(ck.OCTO_BASE, repeat_task=rep)
-            d = ck.write_octo(os.path.join(tmp, f"octo{rep}"), c)
-            t5, sp, sw, tm = ck.octo_inputs(c)
-            m = vla.OctoTransformer(d, 7)
-            a, b, w = (torch.from_numpy(v).to(dev) for v in (t5, sp, sw))
-            o = torch.empty(c["d"], dtype=torch.float32, device=dev)
-            gpu = _time_calls(torch, lambda: m.forward_dev(a, b, w, 2, tm, o, st), stream_obj)
-            row = {"gpu_ms": round(gpu, 4), "tokens": m.total_tokens(2), "int8_mask": 7,
-                   "int8_layers": m.int8_layers, "graph_nodes": m.graph_nodes}
-            if ob is not None and rep == 1:
-                r = ob.RefOcto(d, 7, c["d"])
-                row["cpu_ref_ms"] = round(_time_cpu(lambda: r.forward(t5, sp, sw, 2, tm)), 3)
-                del r
-            out["octo" if rep == 0 else "octo_repeat_task"] = row
-            del m
-            print(f"  Octo transformer ({m_tokens(c)} tokens): {row}", file=sys.stderr, flush=True)
-
-        # SmolVLA chunk: 16-layer prefix over 177 tokens + 10 Euler steps of the
-        # 16-layer expert, SMOLVLA_INT8=48
-        c = ck.SMOLVLA_BASE
-        d = ck.write_smolvla(os.path.join(tmp, "smol"), c)
-        p, pad, n = ck.smolvla_inputs(c)
-        m = vla.SmolvlaChunk(d, 48)
-        tp, tn = torch.from_numpy(p).to(dev), torch.from_numpy(n).to(dev)
-        ta = torch.empty((c["chunk"], c["max_action_dim"]), dtype=torch.float32, device=dev)
-        gpu = _time_calls(torch, lambda: m.run_dev(tp, pad, tn, ta, st), stream_obj, min_calls=10)
-        row = {"gpu_ms": round(gpu, 4), "prefix_tokens": c["n_prefix"], "steps": c["num_steps"],
-               "int8_mask": 48, "int8_layers": m.int8_layers, "graph_nodes": m.graph_nodes}
-        if ob is not None:
-            r = ob.RefSmolvla(d, 48)
-            row["cpu_ref_ms"] = round(_time_cpu(lambda: r.run(p, pad, n)), 3)
-            del r
-        out["smolvla"] = row
-        del m
-        print(f"  SmolVLA chunk: {row}", file=sys.stderr, flush=True)
+        if "act" in models:
+            out["act"] = _lat_act(vla, torch, ck, ob, tmp, stream_obj)
+            print(f"  ACT transformer: {out['act']}", file=sys.stderr, flush=True)
+        if "octo" in models:
+            out["octo"] = _lat_octo(vla, torch, ck, ob, tmp, stream_obj, 0)
+            print(f"  Octo transformer (658 tokens): {out['octo']}", file=sys.stderr, flush=True)
+            out["octo_repeat_task"] = _lat_octo(vla, torch, ck, ob, tmp, stream_obj, 1)
+            print(f"  Octo transformer (690 tokens): {out['octo_repeat_task']}", file=sys.stderr,
+                  flush=True)
+        if "smolvla" in models:
+            out["smolvla"] = _lat_smolvla(vla, torch, ck, ob, tmp, stream_obj)
+            print(f"  SmolVLA chunk: {out['smolvla']}", file=sys.stderr, flush=True)
     if ob is not None:
         out["cpu_ref_threads"] = int(ob.ref().ref_omp_max_threads())
     return out
 
 
-def m_tokens(c):
-    per = c["tok_primary"] + c["tok_wrist"] + (c["n_task"] if c.get("repeat_task") else 0) + c["n_readout"]
-    return c["n_task"] + c["wnd"] * per
+def m_tokens_act(c):
+    return c["n_1d"] + c["n_cams"] * c["fh"] * c["fw"]
 
 
 def main():
@@ -321,6 +330,7 @@ def main():
     ap.add_argument("--no-policy", action="store_true", help="skip the per-chunk policy latency leg")
     ap.add_argument("--policy-only", action="store_true",
                     help="only the per-chunk policy latency leg (for rocprofv3 runs)")
+    ap.add_argument("--models", default="act,octo,smolvla", help="policy graphs to time")
     ap.add_argument("--profile-only", action="store_true",
                     help="only the dominant GEMM, back to back (for rocprofv3 runs)")
     args = ap.parse_args()
@@ -344,8 +354,8 @@ def main():
     stream = stream_obj.cuda_stream
 
     if args.policy_only:
-        print(json.dumps({"policy_latency_ms": policy_latency(vla, torch, stream_obj,
-                                                              with_cpu=not args.no_cpu)}), flush=True)
+        print(json.dumps({"policy_latency_ms": policy_latency(
+            vla, torch, stream_obj, with_cpu=not args.no_cpu, models=args.models.split(","))}), flush=True)
         return
 
     shapes_spec = [(M, K, N) for (K, N) in synth.SWEEP_KN for M in synth.SWEEP_M]

@@ -253,6 +253,20 @@ VLA_API int32_t vla_silu_gate_dev(float* out, const float* g, const float* u, in
  * reference graphs, e.g. act_transformer.cpp:227-281). */
 VLA_API int32_t vla_add_dev(float* out, const float* a, const float* b, int64_t n, void* stream);
 
+/* dense_linear (lm_ops.h:81-84, src/hal/common/gemm.cpp): the fp32 linear
+ * out[t,n] = sum_k x[t,k] W[n,k] + bias[n], W [N,K] row-major, bias may be
+ * NULL. fp32 sums in another order than the reference (tolerance class). The
+ * graphs use it for the layers their int8 mask leaves in fp32. The _dev form
+ * takes row strides, an epilogue act (vla_act, or 4 = silu) and accumulate != 0
+ * for out = fmaf(alpha, result, out) (the Euler step x += dt * v of the
+ * SmolVLA denoise loop, action_expert.cpp:388). */
+VLA_API int32_t vla_dense_linear(float* out, const float* x, const float* W, const float* bias,
+                                 int32_t seq, int32_t N, int32_t K);
+VLA_API int32_t vla_dense_linear_dev(float* out, int32_t ldo, const float* x, int32_t ldx,
+                                     const float* W, int32_t ldw, const float* bias, int32_t seq,
+                                     int32_t N, int32_t K, int32_t act, int32_t accumulate,
+                                     float alpha, void* stream);
+
 /* ------------------------------------------------ device policy graphs ---- */
 /* The reference's transformer graphs with every linear, attention, norm and
  * activation on the device and the whole pass replayed as one HIP graph. Each

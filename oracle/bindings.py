@@ -95,6 +95,7 @@ def ref():
         L.ref_gelu_erf.argtypes = [P, i]
         L.ref_silu_gate.argtypes = [P, P, P, i]
         L.ref_relu.argtypes = [P, i]
+        L.ref_dense_linear.argtypes = [P, P, P, P, i, i, i]
         _ref = L
     return _ref
 
@@ -413,3 +414,12 @@ class RefSmolvla:
     def __del__(self):
         if getattr(self, "h", None):
             _ref_models().ref_smolvla_free(self.h)
+
+
+def ref_dense_linear(x, W, bias=None):
+    """The reference's fp32 dense_linear (Linear::Role::Generic)."""
+    x, W = _f32(x), _f32(W)
+    b = None if bias is None else _f32(bias)
+    out = np.empty((x.shape[0], W.shape[0]), np.float32)
+    ref().ref_dense_linear(_p(out), _p(x), _p(W), _p(b), x.shape[0], W.shape[0], W.shape[1])
+    return out

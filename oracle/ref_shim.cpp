@@ -125,3 +125,8 @@ REF_API void ref_silu_gate(float* out, const float* g, const float* u, int n) {
     tcpu::silu_gate(out, g, u, n);
 }
 REF_API void ref_relu(float* x, int n) { tcpu::relu(x, n); }
+
+REF_API void ref_dense_linear(float* out, const float* x, const float* W, const float* bias, int seq,
+                              int N, int K) {
+    tcpu::dense_linear(out, x, W, bias, seq, N, K);
+}

@@ -50,6 +50,7 @@ EXPORTS = (
     "vla_rope_neox", "vla_rope_neox_dev",
     "vla_gelu_tanh", "vla_gelu_erf", "vla_relu", "vla_silu_gate",
     "vla_gelu_tanh_dev", "vla_gelu_erf_dev", "vla_relu_dev", "vla_silu_gate_dev", "vla_add_dev",
+    "vla_dense_linear", "vla_dense_linear_dev",
     "vla_act_tf_load", "vla_act_tf_free", "vla_act_tf_chunk", "vla_act_tf_action_dim",
     "vla_act_tf_state_dim", "vla_act_tf_dim", "vla_act_tf_int8_layers", "vla_act_tf_graph_nodes",
     "vla_act_tf_forward", "vla_act_tf_forward_dev",
@@ -139,6 +140,8 @@ def _declare(L):
         "vla_relu_dev": (i32, [P, i64, P]),
         "vla_silu_gate_dev": (i32, [P, P, P, i64, P]),
         "vla_add_dev": (i32, [P, P, P, i64, P]),
+        "vla_dense_linear": (i32, [P, P, P, P, i32, i32, i32]),
+        "vla_dense_linear_dev": (i32, [P, i32, P, i32, P, i32, P, i32, i32, i32, i32, i32, f32, P]),
         "vla_act_tf_load": (P, [c_char_p, i32, i32]),
         "vla_act_tf_free": (None, [P]),
         "vla_act_tf_chunk": (i32, [P]),
@@ -496,6 +499,22 @@ class LinearI8:
             self.close()
         except Exception:
             pass
+
+
+# ------------------------------------------------------ fp32 linear ------
+
+def dense_linear(x, W, bias=None):
+    """tcpu::dense_linear: x [seq, K] fp32, W [N, K] -> out [seq, N]."""
+    x, W = _f32(x), _f32(W)
+    b = None if bias is None else _f32(bias)
+    out = np.empty((x.shape[0], W.shape[0]), np.float32)
+    _call("vla_dense_linear", _ptr(out), _ptr(x), _ptr(W), _ptr(b), x.shape[0], W.shape[0], W.shape[1])
+    return out
+
+
+def dense_linear_dev(out, x, W, bias=None, act=0, accumulate=0, alpha=1.0, stream=None):
+    _call("vla_dense_linear_dev", _dp(out), out.stride(0), _dp(x), x.stride(0), _dp(W), W.stride(0),
+          _dp(bias), x.shape[0], W.shape[0], W.shape[1], act, accumulate, float(alpha), _stream(stream))
 
 
 # ------------------------------------------------ device policy graphs ----

@@ -516,4 +516,37 @@ VLA_API int32_t vla_add_dev(float* out, const float* a, const float* b, int64_t 
     return guarded("vla_add_dev", [&] { launch_add(out, a, b, n, as_stream(stream)); });
 }
 
+// ------------------------------------------------------- fp32 linear --
+
+VLA_API int32_t vla_dense_linear(float* out, const float* x, const float* W, const float* bias,
+                                 int32_t seq, int32_t N, int32_t K) {
+    return guarded("vla_dense_linear", [&] {
+        VLA_REQUIRE(seq >= 0 && N > 0 && K > 0, "need seq >= 0, N > 0 and K > 0");
+        VLA_REQUIRE(seq == 0 || (out && x && W), "null buffer");
+        if (seq == 0) return;
+        Staging& S = staging();
+        auto lk = S.lock();
+        hipStream_t st = library_stream();
+        S.reset(align256((size_t)seq * K * 4) + align256((size_t)N * K * 4) + align256((size_t)N * 4) +
+                align256((size_t)seq * N * 4));
+        const float* dx = S.upload(x, (size_t)seq * K, st);
+        const float* dW = S.upload(W, (size_t)N * K, st);
+        const float* db = S.upload(bias, (size_t)N, st);
+        float* dout = S.alloc<float>((size_t)seq * N);
+        launch_linear_f32(dout, N, dx, K, dW, K, db, seq, N, K, 0, 0, 1.0f, st);
+        VLA_HIP_CHECK(hipMemcpyAsync(out, dout, (size_t)seq * N * 4, hipMemcpyDeviceToHost, st));
+        VLA_HIP_CHECK(hipStreamSynchronize(st));
+    });
+}
+
+VLA_API int32_t vla_dense_linear_dev(float* out, int32_t ldo, const float* x, int32_t ldx,
+                                     const float* W, int32_t ldw, const float* bias, int32_t seq,
+                                     int32_t N, int32_t K, int32_t act, int32_t accumulate,
+                                     float alpha, void* stream) {
+    return guarded("vla_dense_linear_dev", [&] {
+        launch_linear_f32(out, ldo, x, ldx, W, ldw, bias, seq, N, K, act, accumulate, alpha,
+                          as_stream(stream));
+    });
+}
+
 }  // extern "C"

@@ -124,6 +124,11 @@ struct RowQArgs {
 };
 void launch_rowq(const RowQArgs& a, hipStream_t st);
 
+// RoPE-NeoX from a cos/sin table cs[(t * head_dim/2 + i) * 2 + {0, 1}]
+// (double; rope_cos_sin in graph.h builds it the way rope_neox does)
+void launch_rope_table(float* x, int ld, const double* cs, int seq, int n_heads, int head_dim,
+                       hipStream_t st);
+
 // dst[r, c] = src[r, c] for a [rows, cols] block with row strides ldd / lds
 void launch_copy_rows(float* dst, int ldd, const float* src, int lds, int rows, int cols,
                       hipStream_t st);

@@ -101,6 +101,20 @@ __global__ __launch_bounds__(256) void add_kernel(float* out, const float* a, co
         out[i] = a[i] + b[i];
 }
 
+// one thread per (token, head, pair index i); cos/sin of (token, i) from a
+// table built on the host exactly as rope_neox builds its per-token table
+__global__ __launch_bounds__(256) void rope_table_kernel(float* x, int ld, const double* cs, int seq,
+                                                         int n_heads, int half) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= seq * n_heads * half) return;
+    const int i = idx % half, hh = (idx / half) % n_heads, t = idx / (half * n_heads);
+    const double c = cs[((size_t)t * half + i) * 2], s = cs[((size_t)t * half + i) * 2 + 1];
+    float* v = x + (size_t)t * ld + hh * 2 * half;
+    const float x0 = v[i], x1 = v[i + half];
+    v[i] = (float)(x0 * c - x1 * s);
+    v[i + half] = (float)(x0 * s + x1 * c);
+}
+
 // one thread per (token, pair index i); loops over heads
 __global__ __launch_bounds__(256) void rope_kernel(float* x, int ld, const int32_t* pos, int seq,
                                                    int n_heads, int head_dim, double theta_scale) {
@@ -361,6 +375,17 @@ void launch_rowq(const RowQArgs& a, hipStream_t st) {
     else if (a.op == 1) launch_rowq_op<1>(a, st);
     else if (a.op == 2) launch_rowq_op<2>(a, st);
     else launch_rowq_op<3>(a, st);
+    VLA_LAUNCH_CHECK();
+}
+
+void launch_rope_table(float* x, int ld, const double* cs, int seq, int n_heads, int head_dim,
+                       hipStream_t st) {
+    VLA_REQUIRE(seq >= 0 && n_heads > 0 && head_dim > 0 && head_dim % 2 == 0 && cs,
+                "rope: need seq >= 0, n_heads > 0, an even head_dim and a table");
+    VLA_REQUIRE(ld >= n_heads * head_dim, "rope: row stride shorter than heads * head_dim");
+    if (seq == 0) return;
+    const int n = seq * n_heads * (head_dim / 2);
+    rope_table_kernel<<<(n + 255) / 256, 256, 0, st>>>(x, ld, cs, seq, n_heads, head_dim / 2);
     VLA_LAUNCH_CHECK();
 }
 

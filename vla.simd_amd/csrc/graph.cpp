@@ -1,6 +1,7 @@
 // graph.cpp - see graph.h.
 #include "graph.h"
 
+#include <cmath>
 #include <cstdlib>
 #include <fstream>
 #include <sstream>
@@ -229,6 +230,21 @@ void GraphReplay::run(uint64_t key, hipStream_t own, hipStream_t caller,
         VLA_HIP_CHECK(hipGraphInstantiate(&exec_, graph_, nullptr, nullptr, 0));
     }
     VLA_HIP_CHECK(hipGraphLaunch(exec_, caller));
+}
+
+std::vector<double> rope_cos_sin(const int32_t* pos, int seq, int head_dim, float base) {
+    const int half = head_dim / 2;
+    const double theta_scale = std::pow((double)base, -2.0 / head_dim);
+    std::vector<double> cs((size_t)seq * half * 2);
+    for (int t = 0; t < seq; t++) {
+        double theta = (double)pos[t];
+        for (int i = 0; i < half; i++) {
+            cs[((size_t)t * half + i) * 2] = std::cos(theta);
+            cs[((size_t)t * half + i) * 2 + 1] = std::sin(theta);
+            theta *= theta_scale;
+        }
+    }
+    return cs;
 }
 
 // ------------------------------------------------------------------ files --

@@ -173,6 +173,11 @@ private:
     hipGraphExec_t exec_ = nullptr;
 };
 
+// rope_neox's per-token table (src/hal/common/norms.cpp:37-67): for token t,
+// theta_0 = pos[t], theta_{i+1} = theta_i * base^(-2/head_dim) in double,
+// entries (cos theta_i, sin theta_i) at [(t * head_dim/2 + i) * 2].
+std::vector<double> rope_cos_sin(const int32_t* pos, int seq, int head_dim, float base);
+
 // "key value" pairs of a reference .meta file (whitespace separated; the ACT
 // writer puts one per line, the Octo/SmolVLA writers the same).
 std::map<std::string, double> read_meta(const std::string& path);

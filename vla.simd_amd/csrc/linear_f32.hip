@@ -14,7 +14,8 @@
 // B[col l % 16][k l / 16]; output lane l holds column l % 16, rows
 // 4 * (l / 16) + r. A block owns a BM x BN tile with four waves in a 2 x 2 grid;
 // K advances in 16-wide slabs staged through LDS (rows padded by one float so
-// the column reads of the fragment loads do not collide on a bank).
+// the column reads of the fragment loads do not collide on a bank). M <= 128
+// takes a split-K kernel instead (see linear_f32_skinny).
 
 #include "act.h"
 #include "common.h"
@@ -98,6 +99,115 @@ __global__ __launch_bounds__(256) void linear_f32_kernel(float* __restrict__ out
     }
 }
 
+// M <= 128 (the batch-1 action heads and flow-matching projections): a block
+// owns 16 output columns and every row; its W waves split K in 16-wide steps
+// and read their MFMA operands straight from global memory as float4 runs
+// (lane group g takes k = 4g .. 4g+3 of a step; A and B use the same k order,
+// so each MFMA still sums matching products). The waves' partial sums meet in
+// LDS before the epilogue.
+template <int FM, int W, bool VEC>
+__global__ __launch_bounds__(W * 64) void linear_f32_skinny(float* __restrict__ out, int ldo,
+                                                            const float* __restrict__ x, int ldx,
+                                                            const float* __restrict__ Wt, int ldw,
+                                                            const float* __restrict__ bias, int M,
+                                                            int N, int K, int act, int accumulate,
+                                                            float alpha) {
+    __shared__ float red[W * FM * 256];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int c = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.x * 16;
+    const int n = n0 + c < N ? n0 + c : N - 1;
+    const float* brow = Wt + (size_t)n * ldw;
+    const float* arow[FM];
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+        const int m = 16 * i + c < M ? 16 * i + c : M - 1;
+        arow[i] = x + (size_t)m * ldx;
+    }
+    auto load4 = [&](const float* row, int k) {
+        if (VEC && k + 4 <= K) return *reinterpret_cast<const float4*>(row + k);
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (k < K) v.x = row[k];
+        if (k + 1 < K) v.y = row[k + 1];
+        if (k + 2 < K) v.z = row[k + 2];
+        if (k + 3 < K) v.w = row[k + 3];
+        return v;
+    };
+    v4f acc[FM];
+#pragma unroll
+    for (int i = 0; i < FM; i++) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
+    for (int k16 = wave * 16; k16 < K; k16 += W * 16) {
+        const int k = k16 + 4 * g;
+        const float4 b = load4(brow, k);
+        float4 a[FM];
+#pragma unroll
+        for (int i = 0; i < FM; i++) a[i] = load4(arow[i], k);
+#pragma unroll
+        for (int i = 0; i < FM; i++) {
+            acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].x, b.x, acc[i], 0, 0, 0);
+            acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].y, b.y, acc[i], 0, 0, 0);
+            acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].z, b.z, acc[i], 0, 0, 0);
+            acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].w, b.w, acc[i], 0, 0, 0);
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) red[((wave * FM + i) * 4 + r) * 64 + lane] = acc[i][r];
+    __syncthreads();
+    // thread e sums element e of the FM x 4 x 64 lane-major tile over the waves
+    for (int e = tid; e < FM * 256; e += W * 64) {
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; w++) v += red[w * FM * 256 + e];
+        const int l = e & 63, r = (e >> 6) & 3, i = e >> 8;
+        const int m = 16 * i + 4 * (l >> 4) + r, nn = n0 + (l & 15);
+        if (m >= M || nn >= N) continue;
+        v = v + (bias ? bias[nn] : 0.0f);
+        switch (act) {
+        case 1: v = act_relu(v); break;
+        case 2: v = act_gelu_tanh(v); break;
+        case 3: v = act_gelu_erf(v); break;
+        case 4: v = act_silu(v); break;
+        default: break;
+        }
+        float* o = out + (size_t)m * ldo + nn;
+        *o = accumulate ? fmaf(alpha, v, *o) : v;
+    }
+}
+
+template <int FM, bool VEC>
+void launch_skinny_fm(float* out, int ldo, const float* x, int ldx, const float* W, int ldw,
+                      const float* bias, int M, int N, int K, int act, int accumulate, float alpha,
+                      hipStream_t st) {
+    const int steps = (K + 15) / 16;
+    const int blocks = (N + 15) / 16;
+    // about four K steps per wave, at most 8 waves
+    const int w = steps >= 32 ? 8 : steps >= 16 ? 4 : steps >= 8 ? 2 : 1;
+    switch (w) {
+    case 8: linear_f32_skinny<FM, 8, VEC><<<blocks, 512, 0, st>>>(out, ldo, x, ldx, W, ldw, bias, M, N, K, act, accumulate, alpha); break;
+    case 4: linear_f32_skinny<FM, 4, VEC><<<blocks, 256, 0, st>>>(out, ldo, x, ldx, W, ldw, bias, M, N, K, act, accumulate, alpha); break;
+    case 2: linear_f32_skinny<FM, 2, VEC><<<blocks, 128, 0, st>>>(out, ldo, x, ldx, W, ldw, bias, M, N, K, act, accumulate, alpha); break;
+    default: linear_f32_skinny<FM, 1, VEC><<<blocks, 64, 0, st>>>(out, ldo, x, ldx, W, ldw, bias, M, N, K, act, accumulate, alpha); break;
+    }
+}
+
+template <bool VEC>
+void launch_skinny(float* out, int ldo, const float* x, int ldx, const float* W, int ldw,
+                   const float* bias, int M, int N, int K, int act, int accumulate, float alpha,
+                   hipStream_t st) {
+    switch ((M + 15) / 16) {
+    case 1: launch_skinny_fm<1, VEC>(out, ldo, x, ldx, W, ldw, bias, M, N, K, act, accumulate, alpha, st); break;
+    case 2: launch_skinny_fm<2, VEC>(out, ldo, x, ldx, W, ldw, bias, M, N, K, act, accumulate, alpha, st); break;
+    case 3: launch_skinny_fm<3, VEC>(out, ldo, x, ldx, W, ldw, bias, M, N, K, act, accumulate, alpha, st); break;
+    case 4: launch_skinny_fm<4, VEC>(out, ldo, x, ldx, W, ldw, bias, M, N, K, act, accumulate, alpha, st); break;
+    case 5: launch_skinny_fm<5, VEC>(out, ldo, x, ldx, W, ldw, bias, M, N, K, act, accumulate, alpha, st); break;
+    case 6: launch_skinny_fm<6, VEC>(out, ldo, x, ldx, W, ldw, bias, M, N, K, act, accumulate, alpha, st); break;
+    case 7: launch_skinny_fm<7, VEC>(out, ldo, x, ldx, W, ldw, bias, M, N, K, act, accumulate, alpha, st); break;
+    default: launch_skinny_fm<8, VEC>(out, ldo, x, ldx, W, ldw, bias, M, N, K, act, accumulate, alpha, st); break;
+    }
+}
+
 }  // namespace
 
 void launch_linear_f32(float* out, int ldo, const float* x, int ldx, const float* W, int ldw,
@@ -108,7 +218,14 @@ void launch_linear_f32(float* out, int ldo, const float* x, int ldx, const float
     VLA_REQUIRE(out && x && W, "linear_f32: null buffer");
     VLA_REQUIRE(act >= 0 && act <= 4, "linear_f32: unknown activation");
     if (M == 0) return;
-    // small grids (the batch-1 action heads) take 32 x 32 tiles so more CUs get work
+    if (M <= 128) {
+        const bool vec = ldx % 4 == 0 && ldw % 4 == 0 && aligned(x, 16) && aligned(W, 16);
+        if (vec) launch_skinny<true>(out, ldo, x, ldx, W, ldw, bias, M, N, K, act, accumulate, alpha, st);
+        else launch_skinny<false>(out, ldo, x, ldx, W, ldw, bias, M, N, K, act, accumulate, alpha, st);
+        VLA_LAUNCH_CHECK();
+        return;
+    }
+    // small grids take 32 x 32 tiles so more CUs get work
     const long big = (long)((M + 63) / 64) * ((N + 63) / 64);
     if (big >= 128) {
         const dim3 grid((N + 63) / 64, (M + 63) / 64);

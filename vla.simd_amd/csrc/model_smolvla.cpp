@@ -233,9 +233,13 @@ void SmolvlaTf::ensure(const int32_t* pad, int np) {
         pos_full[i] = cum + i;
         pos_reb[i] = i;
     }
-    pos_ = S->upload(pos.data(), pos.size());
-    pos_full_ = S->upload(pos_full.data(), pos_full.size());
-    pos_reb_ = S->upload(pos_reb.data(), pos_reb.size());
+    // the positions are fixed per prefix layout, so the RoPE tables are built once
+    const std::vector<double> tp = rope_cos_sin(pos.data(), np, hd_, rope_base_);
+    const std::vector<double> tf = rope_cos_sin(pos_full.data(), C, ehd_, erope_);
+    const std::vector<double> tr = rope_cos_sin(pos_reb.data(), C, ehd_, erope_);
+    rope_p_ = S->upload(tp.data(), tp.size());
+    rope_full_ = S->upload(tf.data(), tf.size());
+    rope_reb_ = S->upload(tr.data(), tr.size());
     bool all_real = true;
     for (int j = 0; j < np; j++) all_real = all_real && pad[j] != 0;
     dcausal_ = all_real;
@@ -327,11 +331,11 @@ void SmolvlaTf::run(hipStream_t st) {
         const In xn = rms_for(h_, np, H, w.ln_in, eps_, w.qkv, xn_);
         if (L + 1 == NL_) {  // the last layer's K/V only (:107)
             linear(c, w.qkv, xn, buf + QF, W, np, 0, 0, QF, QF + 2 * KV);
-            launch_rope_neox(buf + QF, W, pos_, np, nkv_, hd_, rope_base_, st);
+            launch_rope_table(buf + QF, W, rope_p_, np, nkv_, hd_, st);
             break;
         }
         linear(c, w.qkv, xn, buf, W, np);
-        launch_rope_neox(buf, W, pos_, np, nq_ + nkv_, hd_, rope_base_, st);  // q and k heads
+        launch_rope_table(buf, W, rope_p_, np, nq_ + nkv_, hd_, st);  // q and k heads
         attend(st, att_, QF, buf, W, buf + QF, W, buf + QF + KV, W, np, np, nq_, nkv_, hd_, scale, pm);
         linear(c, w.o, h_, H, att_, QF, np, 0, 1);
         const In x2 = rms_for(h_, np, H, w.ln_post, eps_, w.gu, xn_);
@@ -374,12 +378,12 @@ void SmolvlaTf::run(hipStream_t st) {
                 float* buf = qkv_[L];
                 float* suf = buf + (size_t)np * W;
                 linear(c, w.q_or_qkv, hn, suf, W, C);
-                launch_rope_neox(suf, W, pos_full_, C, enq_ + enkv_, ehd_, erope_, st);
+                launch_rope_table(suf, W, rope_full_, C, enq_ + enkv_, ehd_, st);
                 attend(st, att_, QF, suf, W, buf + QF, W, buf + QF + KV, W, C, SK, enq_, enkv_, ehd_,
                        scale, dm);
             } else {
                 linear(c, w.q_or_qkv, hn, eq_, QF, C);
-                launch_rope_neox(eq_, QF, pos_reb_, C, enq_, ehd_, erope_, st);
+                launch_rope_table(eq_, QF, rope_reb_, C, enq_, ehd_, st);
                 attend(st, att_, QF, eq_, QF, ck_[L], KV, cv_[L], KV, C, np, enq_, enkv_, ehd_, scale, cm);
             }
             linear(c, w.o, eh_, EH, att_, QF, C, 0, 1);

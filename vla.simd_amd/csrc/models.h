@@ -193,7 +193,7 @@ private:
     std::vector<float*> qkv_;        // per text layer [np + C, QKVW]: prefix rows from the tower, suffix rows from the expert
     std::vector<float*> ck_, cv_;    // per cross layer [np, kv_full]
     std::vector<float*> at_;         // per step [C, 2 EH], right half = the step's time embedding
-    int32_t *pos_ = nullptr, *pos_full_ = nullptr, *pos_reb_ = nullptr;
+    double *rope_p_ = nullptr, *rope_full_ = nullptr, *rope_reb_ = nullptr;  // cos/sin tables
     uint8_t *pgroup_ = nullptr, *pallow_ = nullptr;
     float *dmask_ = nullptr, *cmask_ = nullptr;
     bool dcausal_ = true, cnone_ = true;
