@@ -35,10 +35,11 @@
 //   gemm_i8_skinny  M <= 128, aligned rows (action chunks, decode rows): one
 //                   block owns a 16-column slab of the output and every row; its
 //                   waves take interleaved 64-byte k-steps, stream Wq straight
-//                   from HBM into MFMA registers (each weight byte is read once)
-//                   and sum their int32 partials with LDS atomics before one
-//                   epilogue. No cross-block reduction: no global atomics and no
-//                   device-scope fences (which write back L2 on a multi-XCD part).
+//                   from HBM into MFMA registers (each weight byte is read once),
+//                   write their int32 partial tiles to LDS, and each thread sums
+//                   one output over the waves before one epilogue. No
+//                   cross-block reduction: no global atomics and no device-scope
+//                   fences (which write back L2 on a multi-XCD part).
 //   gemm_i8_generic any 4-byte aligned strides (the op API accepts the
 //                   reference's [seq, i8_kpad(K)] rows, e.g. K = 1027): 64 x 64
 //                   tiles, every chunk masked at K.
@@ -49,6 +50,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <type_traits>
 
 #pragma clang fp contract(off)
 
@@ -159,6 +161,24 @@ __device__ __forceinline__ void wave_lds_sync() {
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
+// Calls f(std::integral_constant<int, I>) for I = B .. E-1 at compile time, so
+// bodies that index register arrays by I keep them in registers however large
+// the body (a plain unrolled loop may be left rolled, which forces such arrays
+// to scratch).
+template <int B, int E>
+struct StaticFor {
+    template <class F>
+    __device__ __forceinline__ static void run(F&& f) {
+        f(std::integral_constant<int, B>{});
+        StaticFor<B + 1, E>::run(f);
+    }
+};
+template <int E>
+struct StaticFor<E, E> {
+    template <class F>
+    __device__ __forceinline__ static void run(F&&) {}
+};
+
 // Epilogue of one wave's TM x TN accumulator tile. Per 16-row strip the wave
 // stages its results in its own LDS region (the MFMA layout holds 4 rows of
 // one column per lane), then writes whole row segments as 16-byte stores;
@@ -174,8 +194,8 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, const v4i (&acc)[FM]
     const bool vec = (a.acc32 ? (a.N % 4 == 0) : (a.ldo % 4 == 0)) && nw + TN <= a.N;
     float sa[4], sn[4];
     load_row_scales(a, mw, lane, sa);
-#pragma unroll
-    for (int i = 0; i < FM; i++) {
+    StaticFor<0, FM>::run([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
         if (i + 1 < FM) load_row_scales(a, mw + (i + 1) * 16, lane, sn);  // next strip's
 #pragma unroll
         for (int j = 0; j < FN; j++)
@@ -234,7 +254,7 @@ __device__ __forceinline__ void epilogue(const GemmArgs& a, const v4i (&acc)[FM]
         if (i + 1 < FM)
 #pragma unroll
             for (int r = 0; r < 4; r++) sa[r] = sn[r];
-    }
+    });
 }
 
 // XCD-aware tile order (see the file comment).
@@ -551,14 +571,14 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds(GemmArgs a) {
 
 template <int FM, int WAVES>
 __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
-    constexpr int TM = FM * 16;
-    __shared__ int32_t red[TM * 16];
+    static_assert(FM * WAVES <= 64, "partial tiles must fit in 64 KiB of LDS");
+    // per wave, its partial int32 tile in MFMA lane order: [i][r][lane]
+    __shared__ int32_t part[WAVES * FM * 256];
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int n0 = blockIdx.x * 16;
     const int K = a.K;
-    for (int i = tid; i < TM * 16; i += WAVES * 64) red[i] = 0;
 
     const int r16 = lane & 15, kq = (lane >> 4) * 16;
     const int8_t* arow[FM];
@@ -569,6 +589,28 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
     }
     const int n = n0 + r16 < a.N ? n0 + r16 : a.N - 1;
     const int8_t* brow = a.B + (size_t)n * a.ldb + kq;
+
+    // The outputs this thread stores after the reduction (element e of the
+    // FM x 4 x 64 lane-major tile), and their epilogue operands, fetched now so
+    // their latency hides under the main loop rather than after the barrier.
+    constexpr int NT = WAVES * 64, EPT = (FM * 256 + NT - 1) / NT;
+    float esa[EPT], ews[EPT], eb[EPT], eold[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; j++) {
+        const int e = tid + j * NT;
+        const int l = e & 63, r = (e >> 6) & 3, i = e >> 8;
+        int mm = 16 * i + 4 * (l >> 4) + r, nn = n0 + (l & 15);
+        const bool ok = e < FM * 256 && mm < a.M && nn < a.N;
+        mm = ok ? mm : 0;
+        nn = ok ? nn : 0;
+        esa[j] = ews[j] = eb[j] = eold[j] = 0.0f;
+        if (!a.acc32) {
+            esa[j] = a.ascale[mm];
+            ews[j] = a.wscale[nn];
+            eb[j] = a.bias ? a.bias[nn] : 0.0f;
+            if (a.accumulate && ok) eold[j] = a.out[(size_t)mm * a.ldo + nn];
+        }
+    }
 
     v4i acc[FM];
 #pragma unroll
@@ -603,16 +645,36 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
         for (int i = 0; i < FM; i++) acc[i] = mfma_i8(load_chunk<true>(arow[i] - kq, k, K), b0, acc[i]);
     }
 
-    __syncthreads();
+    // partial tiles to LDS (no two waves share an address), then each thread
+    // sums one element over the waves (exact int32) and stores it
 #pragma unroll
     for (int i = 0; i < FM; i++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) atomicAdd(&red[(i * 16 + 4 * (lane >> 4) + r) * 16 + r16], acc[i][r]);
+        for (int r = 0; r < 4; r++) part[((wave * FM + i) * 4 + r) * 64 + lane] = acc[i][r];
     __syncthreads();
-
-    for (int e = tid; e < TM * 16; e += WAVES * 64) {
-        const int mm = e >> 4, nn = n0 + (e & 15);
-        if (mm < a.M && nn < a.N) store_out(a, mm, nn, red[e]);
+#pragma unroll
+    for (int j = 0; j < EPT; j++) {
+        const int e = tid + j * NT;
+        if (e >= FM * 256) break;
+        int32_t v = 0;
+#pragma unroll
+        for (int w = 0; w < WAVES; w++) v += part[w * FM * 256 + e];
+        const int l = e & 63, r = (e >> 6) & 3, i = e >> 8;
+        const int mm = 16 * i + 4 * (l >> 4) + r, nn = n0 + (l & 15);
+        if (mm >= a.M || nn >= a.N) continue;
+        if (a.acc32) {
+            a.acc32[(size_t)mm * a.N + nn] = v;
+            continue;
+        }
+        const float p = (float)v * ews[j];
+        float o = fmaf(p, esa[j], eb[j]);
+        switch (a.act) {
+        case 1: o = act_relu(o); break;
+        case 2: o = act_gelu_tanh(o); break;
+        case 3: o = act_gelu_erf(o); break;
+        default: break;
+        }
+        a.out[(size_t)mm * a.ldo + nn] = a.accumulate ? eold[j] + o : o;
     }
 }
 
@@ -713,15 +775,16 @@ void run_lds(const GemmArgs& a, hipStream_t st) {
 template <int WAVES>
 void run_skinny(const GemmArgs& a, hipStream_t st) {
     const int nb = (a.N + 15) / 16;
+    constexpr int W8 = WAVES < 8 ? WAVES : 8;  // FM > 4 keeps the partial tiles within 64 KiB
     switch ((a.M + 15) / 16) {
     case 1: gemm_i8_skinny<1, WAVES><<<nb, WAVES * 64, 0, st>>>(a); break;
     case 2: gemm_i8_skinny<2, WAVES><<<nb, WAVES * 64, 0, st>>>(a); break;
     case 3: gemm_i8_skinny<3, WAVES><<<nb, WAVES * 64, 0, st>>>(a); break;
     case 4: gemm_i8_skinny<4, WAVES><<<nb, WAVES * 64, 0, st>>>(a); break;
-    case 5: gemm_i8_skinny<5, WAVES><<<nb, WAVES * 64, 0, st>>>(a); break;
-    case 6: gemm_i8_skinny<6, WAVES><<<nb, WAVES * 64, 0, st>>>(a); break;
-    case 7: gemm_i8_skinny<7, WAVES><<<nb, WAVES * 64, 0, st>>>(a); break;
-    default: gemm_i8_skinny<8, WAVES><<<nb, WAVES * 64, 0, st>>>(a); break;
+    case 5: gemm_i8_skinny<5, W8><<<nb, W8 * 64, 0, st>>>(a); break;
+    case 6: gemm_i8_skinny<6, W8><<<nb, W8 * 64, 0, st>>>(a); break;
+    case 7: gemm_i8_skinny<7, W8><<<nb, W8 * 64, 0, st>>>(a); break;
+    default: gemm_i8_skinny<8, W8><<<nb, W8 * 64, 0, st>>>(a); break;
     }
     VLA_LAUNCH_CHECK();
 }
@@ -756,11 +819,17 @@ Tile pick_tile(int M, int N, int K) {
     }
     // Measured on MI355X over the BASELINE sweep (bench.py, forced tiles):
     // short K (<= 1024) is dominated by the fp32 output write and wants many
-    // small register-staged tiles in flight; long K wants the LDS-DMA pipeline,
-    // 128x128 when that still gives every CU a tile. The 256-wide tiles lose
-    // occupancy (256x256 spills) and are kept for forced A/B runs only.
+    // small register-staged tiles in flight. Long K wants the LDS-DMA pipeline
+    // with the largest tile that still fills the chip: 256 x 256 with 8 waves
+    // when there are two tiles per CU (8192 x 4096 x 4096: 174 us against 185
+    // at 128 x 128), else 256 x 128 with 8 waves when every CU gets a tile
+    // (2048 x 4096 x 4096: 43 us against 48; 8192 x 2560 x 960: 30 us against
+    // 34), else smaller tiles. The 4-wave 256 x 256 forms spill and are kept
+    // for forced A/B runs only.
     auto tiles = [&](int bm, int bn) { return (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
     if (K <= 1024) return tiles(64, 128) >= kCUs ? Tile{64, 128, 64, 0} : Tile{64, 64, 64, 0};
+    if (tiles(256, 256) >= 2 * kCUs) return {256, 256, 128, 2, 8};
+    if (tiles(256, 128) >= kCUs) return {256, 128, 128, 3, 8};
     if (tiles(128, 128) >= kCUs) return {128, 128, 64, 4};
     if (tiles(64, 128) >= kCUs) return {64, 128, 64, 4};
     return {64, 64, 64, 0};
