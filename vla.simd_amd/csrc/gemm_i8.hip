@@ -32,6 +32,14 @@
 //                   keeps the A and B panels a run shares in that XCD's L2.
 //                   The epilogue goes through LDS so each row segment leaves as
 //                   16-byte stores.
+//   gemm_i8_lds     long K (> 1024), aligned rows. Operand slabs go straight
+//                   from global memory into LDS (global_load_lds_dwordx4, no
+//                   VGPR staging) with S-1 slabs in flight; LDS rows are
+//                   XOR-swizzled by 16-byte chunk instead of padded; the
+//                   pipeline barrier waits only for LDS reads (lgkmcnt), not
+//                   for the slabs still in flight. Block tiles up to 256 x 256
+//                   with 8 waves (WM x WN); same XCD-aware order and epilogue
+//                   as gemm_i8_tiled.
 //   gemm_i8_skinny  M <= 128, aligned rows (action chunks, decode rows): one
 //                   block owns a 16-column slab of the output and every row; its
 //                   waves take interleaved 64-byte k-steps, stream Wq straight

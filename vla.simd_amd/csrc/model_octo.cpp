@@ -128,10 +128,12 @@ OctoTf::~OctoTf() {
 void OctoTf::ensure(int wnd, const uint8_t* tmask, bool wrist) {
     VLA_REQUIRE(wnd >= 1 && wnd <= max_h_, "octo: window must be in [1, max_horizon]");
     VLA_REQUIRE(1 + 4 * wnd <= 256, "octo: window too long for the group mask");
-    uint64_t key = (uint64_t)wnd;
-    for (int t = 0; t < wnd; t++) key = key * 2 + (tmask[t] ? 1 : 0);
-    key = key * 2 + (wrist ? 1 : 0);
-    if (key == key_) return;
+    // the token layout and the mask tables depend on exactly these
+    std::vector<uint8_t> layout(2 + wnd);
+    layout[0] = (uint8_t)wnd;
+    layout[1] = wrist ? 1 : 0;
+    for (int t = 0; t < wnd; t++) layout[2 + t] = tmask[t] ? 1 : 0;
+    if (S_ && layout == layout_) return;
     VLA_HIP_CHECK(hipDeviceSynchronize());
     S_.reset();
     auto S = std::make_unique<DeviceArena>();
@@ -201,7 +203,8 @@ void OctoTf::ensure(int wnd, const uint8_t* tmask, bool wrist) {
         if (round_up(kpad4(k), 64) > maxld) maxld = round_up(kpad4(k), 64);
     ctx_.alloc(*S, total, maxld);
     S_ = std::move(S);
-    key_ = key;
+    layout_ = std::move(layout);
+    key_++;  // a new layout: the captured graph is rebuilt
     wnd_ = wnd;
     total_ = total;
     wrist_ = wrist;

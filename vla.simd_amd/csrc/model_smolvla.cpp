@@ -178,9 +178,10 @@ SmolvlaTf::~SmolvlaTf() {
 void SmolvlaTf::ensure(const int32_t* pad, int np) {
     VLA_REQUIRE(np >= 2 && np <= 65536 - C_, "smolvla: prefix length out of range");
     VLA_REQUIRE(pad[np - 1] != 0, "smolvla: the last prefix token (state) must be real");
-    uint64_t key = 1469598103934665603ull ^ (uint64_t)np;
-    for (int j = 0; j < np; j++) key = (key ^ (uint64_t)(pad[j] != 0)) * 1099511628211ull;
-    if (key == key_) return;
+    // the masks and positions depend on exactly which prefix tokens are real
+    std::vector<uint8_t> real(np);
+    for (int j = 0; j < np; j++) real[j] = pad[j] != 0;
+    if (S_ && real == real_) return;
     VLA_HIP_CHECK(hipDeviceSynchronize());
     S_.reset();
     auto S = std::make_unique<DeviceArena>();
@@ -279,7 +280,8 @@ void SmolvlaTf::ensure(const int32_t* pad, int np) {
         if (round_up(kpad4(k), 64) > maxld) maxld = round_up(kpad4(k), 64);
     ctx_.alloc(*S, R, maxld);
     S_ = std::move(S);
-    key_ = key;
+    real_ = std::move(real);
+    key_++;  // a new layout: the captured graph is rebuilt
     np_ = np;
     SK_ = SK;
 }

@@ -119,8 +119,10 @@ private:
     const float *pos_task_ = nullptr, *pos_prim_ = nullptr, *pos_wrist_ = nullptr,
                 *pos_readout_ = nullptr, *final_s_ = nullptr, *final_b_ = nullptr;
     std::vector<Layer> layers_;
-    // per-shape state
-    uint64_t key_ = ~0ull;
+    // per-shape state: layout_ is (wnd, wrist, timestep mask) the buffers and
+    // tables were built for, key_ counts layouts (the graph replay key)
+    std::vector<uint8_t> layout_;
+    uint64_t key_ = 0;
     int wnd_ = 0, total_ = 0, n_groups_ = 0;
     bool wrist_ = false;
     std::unique_ptr<DeviceArena> S_;
@@ -183,8 +185,10 @@ private:
     std::vector<ExpLayer> exp_;
     const float* out_norm_ = nullptr;
     DLinear ain_, at1_, at2_, aout_;
-    // per-shape state
-    uint64_t key_ = ~0ull;
+    // per-shape state: real_ is the pad layout the buffers and tables were
+    // built for, key_ counts layouts (the graph replay key)
+    std::vector<uint8_t> real_;
+    uint64_t key_ = 0;
     int np_ = 0, SK_ = 0, QKVW_ = 0;
     std::unique_ptr<DeviceArena> S_;
     float *prefix_in_ = nullptr, *noise_in_ = nullptr, *act_out_ = nullptr, *h_ = nullptr,
