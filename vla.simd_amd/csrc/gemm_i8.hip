@@ -14,7 +14,10 @@
 // All kernels use v_mfma_i32_16x16x64_i8: lane l supplies 16 contiguous bytes
 // of row (l % 16) at k offset 16*(l / 16) for both operands, so whatever k
 // order the unit uses inside one instruction it pairs equal k on both sides.
-// Output lane l holds column l % 16, rows 4*(l/16) + r.
+// Output lane l holds column l % 16, rows 4*(l/16) + r. The tiled and LDS
+// kernels pass the weight fragment first, so their accumulators hold the
+// output transposed: lane l has output row l % 16 and the 4 consecutive output
+// columns 4*(l/16) + r, which it stores as one 16-byte vector.
 //
 // Kernels
 //   gemm_i8_tiled   16-byte aligned rows (every resident layout of this
@@ -30,8 +33,7 @@
 //                   (the hardware deals workgroup i to XCD i % 8) owns a
 //                   contiguous run of tiles, grouped 8 tile-rows deep, which
 //                   keeps the A and B panels a run shares in that XCD's L2.
-//                   The epilogue goes through LDS so each row segment leaves as
-//                   16-byte stores.
+//                   The epilogue stores straight from the accumulators.
 //   gemm_i8_lds     long K (> 1024), aligned rows. Operand slabs go straight
 //                   from global memory into LDS (global_load_lds_dwordx4, no
 //                   VGPR staging) with S-1 slabs in flight; LDS rows are
@@ -133,32 +135,7 @@ __device__ __forceinline__ void store_out(const GemmArgs& a, int m, int n, int a
     *o = v;
 }
 
-// Per-lane epilogue operands: weight scale and bias of the lane's columns,
-// loaded before the main loop so their latency hides under it.
-template <int FN>
-struct EpiRegs {
-    float ws[FN], b[FN];
-    __device__ __forceinline__ void load(const GemmArgs& a, int nw, int lane) {
-        if (a.acc32) return;
-        const int c16 = lane & 15;
-#pragma unroll
-        for (int j = 0; j < FN; j++) {
-            const int n = nw + j * 16 + c16;
-            const int nc = n < a.N ? n : a.N - 1;
-            ws[j] = a.wscale[nc];
-            b[j] = a.bias ? a.bias[nc] : 0.0f;
-        }
-    }
-};
-
-// Activation scales of the 4 rows a lane holds in 16-row strip m16.
-__device__ __forceinline__ void load_row_scales(const GemmArgs& a, int m16, int lane, float (&sa)[4]) {
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const int m = m16 + 4 * (lane >> 4) + r;
-        sa[r] = a.acc32 ? 0.0f : a.ascale[m < a.M ? m : a.M - 1];
-    }
-}
+typedef float v4f __attribute__((ext_vector_type(4)));
 
 // Orders this wave's LDS accesses: its earlier writes are complete before its
 // later reads (other lanes' values), with no block barrier.
@@ -168,8 +145,6 @@ __device__ __forceinline__ void wave_lds_sync() {
     __builtin_amdgcn_wave_barrier();
     asm volatile("" ::: "memory");
 }
-
-typedef float v4f __attribute__((ext_vector_type(4)));
 
 // Calls f(std::integral_constant<int, I>) for I = B .. E-1 at compile time, so
 // bodies that index register arrays by I keep them in registers however large
@@ -189,88 +164,141 @@ struct StaticFor<E, E> {
     __device__ __forceinline__ static void run(F&&) {}
 };
 
-// Epilogue of one wave's TM x TN accumulator tile. Per 16-row strip the wave
-// stages its results in its own LDS region (the MFMA layout holds 4 rows of
-// one column per lane), then writes whole row segments as 16-byte stores;
-// plain stores are non-temporal (the output is not re-read by this kernel).
-// KIND (0 store, 1 accumulate into out, 2 raw int32 to acc32) and ACT are
-// compile-time: the strips are unrolled (the accumulators are registers), and
-// a run-time switch inside them would multiply the code many times over and
-// leave the epilogue bound by instruction fetch.
-template <int TM, int TN, int FM, int FN, int KIND, int ACT>
-__device__ __forceinline__ void epilogue_k(const GemmArgs& a, const v4i (&acc)[FM][FN],
-                                           const EpiRegs<FN>& e, float* stage, int lane, int mw,
-                                           int nw) {
-    constexpr int LDW = TN + 4;
-    constexpr int LPR = TN / 4;    // lanes per staged row
-    constexpr int RPI = 64 / LPR;  // rows per store instruction
-    const int g4 = 4 * (lane >> 4), c16 = lane & 15;
-    const bool vec = (KIND == 2 ? (a.N % 4 == 0) : (a.ldo % 4 == 0)) && nw + TN <= a.N;
-    // Every strip's row scales up front: the loads share one wait, and later
-    // waits (which on this target also count the output stores in flight)
-    // are not needed.
-    float sa[FM][4];
+// Weight scales and biases of the 4 consecutive output columns a lane holds
+// in each of its FN 16-column blocks (transposed accumulator layout). Loaded
+// as 16-byte vectors when the wave's columns are all in range and aligned.
+template <int FN>
+struct ColOps {
+    float ws[FN][4], bs[FN][4];
+    __device__ __forceinline__ void load(const GemmArgs& a, int nw, int lane) {
+        if (a.acc32) return;
+        const int c4 = 4 * (lane >> 4);
+        const bool vec = nw + 16 * FN <= a.N && (reinterpret_cast<uintptr_t>(a.wscale) & 15) == 0 &&
+                         (!a.bias || (reinterpret_cast<uintptr_t>(a.bias) & 15) == 0);
+        if (vec) {
 #pragma unroll
-    for (int i = 0; i < FM; i++) load_row_scales(a, mw + i * 16, lane, sa[i]);
-    StaticFor<0, FM>::run([&](auto ic) {
-        constexpr int i = decltype(ic)::value;
+            for (int j = 0; j < FN; j++) {
+                const int n = nw + 16 * j + c4;
+                const v4f w = *reinterpret_cast<const v4f*>(a.wscale + n);
+                const v4f b = a.bias ? *reinterpret_cast<const v4f*>(a.bias + n) : v4f{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    ws[j][q] = w[q];
+                    bs[j][q] = b[q];
+                }
+            }
+            return;
+        }
 #pragma unroll
         for (int j = 0; j < FN; j++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int av = acc[i][j][r];
-                float v;
-                if (KIND == 2) {
-                    v = __int_as_float(av);
-                } else {
-                    const float p = (float)av * e.ws[j];
-                    v = apply_act<ACT>(fmaf(p, sa[i][r], e.b[j]));
-                }
-                stage[(g4 + r) * LDW + j * 16 + c16] = v;
+            for (int q = 0; q < 4; q++) {
+                const int n = nw + 16 * j + c4 + q;
+                const int nc = n < a.N ? n : a.N - 1;
+                ws[j][q] = a.wscale[nc];
+                bs[j][q] = a.bias ? a.bias[nc] : 0.0f;
             }
-        wave_lds_sync();
+    }
+};
+
+// Epilogue of one wave's TM x TN tile, from accumulators computed transposed
+// (mfma_i8(B fragment, A fragment)): lane l of acc[i][j] holds row
+// mw + 16 i + (l & 15) and the 4 consecutive columns nw + 16 j + 4 (l >> 4)
+// + r. Each lane writes those 4 values to the wave's LDS rows as one 16-byte
+// vector, and whole row segments leave as 16-byte stores (NT: non-temporal).
+// KIND (0 store, 1 accumulate into out, 2 raw int32 to acc32) and ACT are
+// compile-time: the strips are unrolled (the accumulators are registers), and
+// a run-time switch inside them would multiply the code many times over and
+// leave the epilogue bound by instruction fetch. All row-scale loads are
+// issued before the first use, so they share one wait (a later wait would
+// also count the output stores in flight).
+template <int TM, int TN, int FM, int FN, int KIND, int ACT, bool NT>
+__device__ __forceinline__ void epilogue_k(const GemmArgs& a, const v4i (&acc)[FM][FN], const ColOps<FN>& co,
+                                           int lane, int mw, int nw, float* stage) {
+    const int r16 = lane & 15, c4 = 4 * (lane >> 4);
+    float sa[FM];
+    if (KIND != 2) {
 #pragma unroll
-        for (int rr = 0; rr < 16; rr += RPI) {
-            const int row = rr + lane / LPR, col = (lane % LPR) * 4;
-            const int m = mw + i * 16 + row;
-            if (m < a.M) {
-                const v4f v = *reinterpret_cast<const v4f*>(stage + row * LDW + col);
-                const int n = nw + col;
+        for (int i = 0; i < FM; i++) {
+            const int m = mw + 16 * i + r16;
+            sa[i] = a.ascale[m < a.M ? m : a.M - 1];
+        }
+    }
+    // wave-uniform: whole 16-byte vectors for every column of this wave's tile
+    const bool fast = (KIND == 2 ? a.N % 4 == 0 : a.ldo % 4 == 0) && nw + TN <= a.N;
+    auto value = [&](int i, int j, int q) {
+        const float p = (float)acc[i][j][q] * co.ws[j][q];
+        return apply_act<ACT>(fmaf(p, sa[i], co.bs[j][q]));
+    };
+    if (fast) {
+        // per 16-row strip: stage, then row segments of TN * 4 bytes (16 lanes each)
+        constexpr int LDW = TN + 4;    // staged row, floats (16-byte multiple)
+        constexpr int LPR = TN / 4;    // lanes per row segment
+        constexpr int RPI = 64 / LPR;  // rows per store instruction
+        StaticFor<0, FM>::run([&](auto ic) {
+            constexpr int i = decltype(ic)::value;
+#pragma unroll
+            for (int j = 0; j < FN; j++) {
+                v4f v;
                 if (KIND == 2) {
-                    int32_t* o = a.acc32 + (size_t)m * a.N + n;
-                    if (vec) {
-                        *reinterpret_cast<int4*>(o) = make_int4(__float_as_int(v.x), __float_as_int(v.y),
-                                                                __float_as_int(v.z), __float_as_int(v.w));
-                    } else {
-                        for (int q = 0; q < 4; q++)
-                            if (n + q < a.N) o[q] = __float_as_int(v[q]);
-                    }
+                    v = {__int_as_float(acc[i][j][0]), __int_as_float(acc[i][j][1]),
+                         __int_as_float(acc[i][j][2]), __int_as_float(acc[i][j][3])};
                 } else {
-                    float* o = a.out + (size_t)m * a.ldo + n;
-                    if (vec) {
-                        if (KIND == 1) {
-                            const v4f old = *reinterpret_cast<const v4f*>(o);
-                            *reinterpret_cast<v4f*>(o) = old + v;
-                        } else {
-                            __builtin_nontemporal_store(v, reinterpret_cast<v4f*>(o));
-                        }
+                    v = {value(i, j, 0), value(i, j, 1), value(i, j, 2), value(i, j, 3)};
+                }
+                *reinterpret_cast<v4f*>(stage + r16 * LDW + 16 * j + c4) = v;
+            }
+            wave_lds_sync();
+#pragma unroll
+            for (int rr = 0; rr < 16; rr += RPI) {
+                const int row = rr + lane / LPR, col = (lane % LPR) * 4;
+                const int m = mw + 16 * i + row;
+                if (m < a.M) {
+                    const v4f v = *reinterpret_cast<const v4f*>(stage + row * LDW + col);
+                    const int n = nw + col;
+                    if (KIND == 2) {
+                        *reinterpret_cast<v4f*>(a.acc32 + (size_t)m * a.N + n) = v;
                     } else {
-                        for (int q = 0; q < 4; q++)
-                            if (n + q < a.N) o[q] = KIND == 1 ? o[q] + v[q] : v[q];
+                        float* o = a.out + (size_t)m * a.ldo + n;
+                        if (KIND == 1) *reinterpret_cast<v4f*>(o) = *reinterpret_cast<const v4f*>(o) + v;
+                        else if (NT) __builtin_nontemporal_store(v, reinterpret_cast<v4f*>(o));
+                        else *reinterpret_cast<v4f*>(o) = v;
                     }
                 }
             }
+            wave_lds_sync();
+        });
+        return;
+    }
+    // tiles on the N edge, or row strides that are not whole vectors
+    StaticFor<0, FM>::run([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        const int m = mw + 16 * i + r16;
+        if (m < a.M) {
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const int n = nw + 16 * j + c4 + q;
+                    if (n < a.N) {
+                        if (KIND == 2) {
+                            a.acc32[(size_t)m * a.N + n] = acc[i][j][q];
+                        } else {
+                            float* o = a.out + (size_t)m * a.ldo + n;
+                            const float v = value(i, j, q);
+                            *o = KIND == 1 ? *o + v : v;
+                        }
+                    }
+                }
         }
-        wave_lds_sync();
     });
 }
 
 // One run-time dispatch to the compile-time epilogue for this launch.
-template <int TM, int TN, int FM, int FN>
-__device__ __forceinline__ void epilogue(const GemmArgs& a, const v4i (&acc)[FM][FN],
-                                         const EpiRegs<FN>& e, float* stage, int lane, int mw,
-                                         int nw) {
-#define VLA_EPI(KIND, ACT) epilogue_k<TM, TN, FM, FN, KIND, ACT>(a, acc, e, stage, lane, mw, nw)
+template <int TM, int TN, int FM, int FN, bool NT>
+__device__ __forceinline__ void epilogue(const GemmArgs& a, const v4i (&acc)[FM][FN], const ColOps<FN>& co,
+                                         int lane, int mw, int nw, float* stage) {
+#define VLA_EPI(KIND, ACT) epilogue_k<TM, TN, FM, FN, KIND, ACT, NT>(a, acc, co, lane, mw, nw, stage)
     if (a.acc32) {
         VLA_EPI(2, 0);
     } else if (a.accumulate) {
@@ -316,9 +344,8 @@ struct TileCfg {
     static constexpr int SA = BK + 16;   // padded LDS row, bytes
     static constexpr int CPR = BK / 16;  // 16-byte chunks per row
     static constexpr int CA = BM * CPR / 256, CB = BN * CPR / 256;
-    static constexpr int LDW = TN + 4;   // epilogue staging row, floats
     static constexpr int MAIN = 2 * (BM + BN) * SA;
-    static constexpr int EPI = 4 * 16 * LDW * 4;
+    static constexpr int EPI = 4 * 16 * (TN + 4) * 4;  // staged epilogue, per wave 16 rows
     static constexpr int LDS = MAIN > EPI ? MAIN : EPI;
     static_assert(BM * CPR % 256 == 0 && BN * CPR % 256 == 0, "chunks must split evenly");
     static_assert(TM % 16 == 0 && TN % 16 == 0 && BK % 64 == 0, "tile shape");
@@ -328,7 +355,7 @@ template <int BM, int BN, int BK>
 __global__ __launch_bounds__(256) void gemm_i8_tiled(GemmArgs a) {
     using C = TileCfg<BM, BN, BK>;
     constexpr int TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN, SA = C::SA, CPR = C::CPR;
-    constexpr int CA = C::CA, CB = C::CB, LDW = C::LDW;
+    constexpr int CA = C::CA, CB = C::CB;
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
 
     const int tid = threadIdx.x;
@@ -410,12 +437,10 @@ __global__ __launch_bounds__(256) void gemm_i8_tiled(GemmArgs a) {
 #pragma unroll
             for (int i = 0; i < FM; i++)
 #pragma unroll
-                for (int j = 0; j < FN; j++) acc[i][j] = mfma_i8(af[i], bf[j], acc[i][j]);
+                for (int j = 0; j < FN; j++) acc[i][j] = mfma_i8(bf[j], af[i], acc[i][j]);
         }
     };
 
-    EpiRegs<FN> epi;
-    epi.load(a, n0 + wn * TN, lane);
 
     const int nfull = K / BK;            // slabs read without masks
     const int nk = nfull + (K % BK ? 1 : 0);
@@ -439,8 +464,12 @@ __global__ __launch_bounds__(256) void gemm_i8_tiled(GemmArgs a) {
         __syncthreads();
     }
 
-    epilogue<TM, TN, FM, FN>(a, acc, epi, reinterpret_cast<float*>(smem) + wave * 16 * LDW, lane,
-                             m0 + wm * TM, n0 + wn * TN);
+    // loaded after the loop: held across it they would cost a wave of occupancy
+    ColOps<FN> co;
+    co.load(a, n0 + wn * TN, lane);
+    __syncthreads();  // the staging rows reuse the slab buffers
+    epilogue<TM, TN, FM, FN, true>(a, acc, co, lane, m0 + wm * TM, n0 + wn * TN,
+                                   reinterpret_cast<float*>(smem) + wave * 16 * (TN + 4));
 }
 
 // ------------------------------------------------------ direct-to-LDS --
@@ -486,9 +515,8 @@ struct LdsCfg {
     static constexpr int IA = BM * CPR / NT, IB = BN * CPR / NT;  // load instrs per wave per slab
     static constexpr int LPS = IA + IB;
     static constexpr int STAGE = (BM + BN) * BK;
-    static constexpr int LDW = TN + 4;
     static constexpr int MAIN = S * STAGE;
-    static constexpr int EPI = NW * 16 * LDW * 4;
+    static constexpr int EPI = NW * 16 * (TN + 4) * 4;  // staged epilogue, per wave 16 rows
     static constexpr int LDS = MAIN > EPI ? MAIN : EPI;
     static_assert(BM * CPR % NT == 0 && BN * CPR % NT == 0, "slab chunks must split evenly");
     static_assert(TM % 16 == 0 && TN % 16 == 0, "wave tile");
@@ -497,9 +525,12 @@ struct LdsCfg {
 
 template <int BM, int BN, int BK, int S, int WM, int WN, bool PF>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds(GemmArgs a) {
+    // Plain output stores on the 256 x 256 tile (every CU writes its tiles at
+    // the same moment; measured faster), non-temporal ones elsewhere.
+    constexpr bool NT = BN != 256;
     using C = LdsCfg<BM, BN, BK, S, WM, WN>;
     constexpr int TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN, CPR = C::CPR, NW = C::NW;
-    constexpr int IA = C::IA, IB = C::IB, LPS = C::LPS, STAGE = C::STAGE, LDW = C::LDW;
+    constexpr int IA = C::IA, IB = C::IB, LPS = C::LPS, STAGE = C::STAGE;
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
 
     const int tid = threadIdx.x;
@@ -561,14 +592,14 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds(GemmArgs a) {
     for (int i = 0; i < FM; i++)
 #pragma unroll
         for (int j = 0; j < FN; j++) acc[i][j] = v4i{0, 0, 0, 0};
+    ColOps<FN> co;  // the plain loop has registers to spare: loaded now, latency hidden
+    if constexpr (!PF) co.load(a, n0 + wn * TN, lane);
 
     const int r16 = lane & 15, cq = lane >> 4;
     const int sz = swz<BK>(r16);  // swz depends on the row's low bits only
     const int arow_l = (wm * TM + r16) * BK;
     const int brow_l = BM * BK + (wn * TN + r16) * BK;
 
-    EpiRegs<FN> epi;  // issued before the slab loads, so it is the oldest vmcnt entry
-    epi.load(a, n0 + wn * TN, lane);
 
 #pragma unroll
     for (int s = 0; s < S - 1; s++)
@@ -604,7 +635,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds(GemmArgs a) {
 #pragma unroll
             for (int i = 0; i < FM; i++)
 #pragma unroll
-                for (int j = 0; j < FN; j++) acc[i][j] = mfma_i8(af[i], bf[j], acc[i][j]);
+                for (int j = 0; j < FN; j++) acc[i][j] = mfma_i8(bf[j], af[i], acc[i][j]);
         };
         // one LDS read after each of the first FM+FN MFMAs, then the rest
         auto interleave = [&]() {
@@ -650,10 +681,11 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds(GemmArgs a) {
             mma(fa1, fb1);
             interleave_dma();
         }
-        wait_vmcnt<0>();  // the reloads past the last slab land before LDS is reused
-        __syncthreads();
-        epilogue<TM, TN, FM, FN>(a, acc, epi, reinterpret_cast<float*>(smem) + wave * 16 * LDW, lane,
-                                 m0 + wm * TM, n0 + wn * TN);
+        wait_vmcnt<0>();  // the reloads past the last slab land before LDS is reused or released
+        __syncthreads();  // the staging rows reuse the slab buffers
+        co.load(a, n0 + wn * TN, lane);  // after the loop: no registers to spare during it
+        epilogue<TM, TN, FM, FN, NT>(a, acc, co, lane, m0 + wm * TM, n0 + wn * TN,
+                                     reinterpret_cast<float*>(smem) + wave * 16 * (TN + 4));
         return;
     }
 
@@ -673,13 +705,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds(GemmArgs a) {
 #pragma unroll
             for (int i = 0; i < FM; i++)
 #pragma unroll
-                for (int j = 0; j < FN; j++) acc[i][j] = mfma_i8(af[i], bf[j], acc[i][j]);
+                for (int j = 0; j < FN; j++) acc[i][j] = mfma_i8(bf[j], af[i], acc[i][j]);
         }
     }
-    __syncthreads();
-
-    epilogue<TM, TN, FM, FN>(a, acc, epi, reinterpret_cast<float*>(smem) + wave * 16 * LDW, lane,
-                             m0 + wm * TM, n0 + wn * TN);
+    __syncthreads();  // the staging rows reuse the slab buffers
+    epilogue<TM, TN, FM, FN, NT>(a, acc, co, lane, m0 + wm * TM, n0 + wn * TN,
+                                 reinterpret_cast<float*>(smem) + wave * 16 * (TN + 4));
 }
 
 // ---------------------------------------------------------------- skinny --
@@ -876,9 +907,8 @@ void run_lds(const GemmArgs& a, hipStream_t st) {
     using C = LdsCfg<BM, BN, BK, S, WM, WN>;
     static const bool attr = [] {
         if (C::LDS > 65536)
-            VLA_HIP_CHECK(hipFuncSetAttribute(
-                reinterpret_cast<const void*>(&gemm_i8_lds<BM, BN, BK, S, WM, WN, PF>),
-                hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS));
+            VLA_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_i8_lds<BM, BN, BK, S, WM, WN, PF>),
+                                              hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS));
         return true;
     }();
     (void)attr;
