@@ -12,8 +12,9 @@
 // (no -fgpu-flush-denormals-to-zero), which the FLT_MIN floor relies on.
 //
 // Layout: one wave64 per row, four rows per 256-thread block. A lane reads
-// float4 runs (coalesced 1 KiB per wave instruction), so HBM sees the row once;
-// the second pass re-reads it from L1/L2.
+// float4 runs (coalesced 1 KiB per wave instruction). Rows up to 4096 floats
+// stay in registers between the max and the quantize pass, so each element is
+// read once; longer rows are read twice, the second time from L1/L2.
 
 #include "common.h"
 #include "quant_row.h"
@@ -69,6 +70,38 @@ __global__ __launch_bounds__(256) void quantize_rows_kernel(const float* __restr
     }
 }
 
+// Rows of at most 256 * NV floats, 16-byte aligned, K % 4 == 0: the row is
+// held in registers (NV float4 per lane), so it is read once, from HBM.
+template <int NV>
+__global__ __launch_bounds__(256) void quantize_rows_reg(const float* __restrict__ x, int ldx,
+                                                         int8_t* __restrict__ xq, int ldq,
+                                                         float* __restrict__ scale, int rows, int K) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;  // wave-uniform
+    const float* xr = x + (size_t)row * ldx;
+    float4 v[NV];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int k = 4 * lane + 256 * i;
+        v[i] = k < K ? *reinterpret_cast<const float4*>(xr + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    }
+    amax = wave_max_f32(amax);
+    const float s = row_scale(amax);
+    const float inv = 1.0f / s;
+    if (lane == 0) scale[row] = s;
+    int8_t* qr = xq + (size_t)row * ldq;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int k = 4 * lane + 256 * i;
+        if (k < K) *reinterpret_cast<uint32_t*>(qr + k) = q8x4(v[i], inv);
+    }
+    // the zero pad [K, ldq) (whole words: K % 4 == 0 and ldq % 4 == 0)
+    for (int k = K + 4 * lane; k < ldq; k += 256) *reinterpret_cast<uint32_t*>(qr + k) = 0u;
+}
+
 }  // namespace
 
 void launch_quantize_rows(const float* x, int ldx, int8_t* xq, int ldq, float* scale, int rows,
@@ -80,7 +113,14 @@ void launch_quantize_rows(const float* x, int ldx, int8_t* xq, int ldq, float* s
     if (rows == 0) return;
     const bool vec = K % 4 == 0 && ldx % 4 == 0 && aligned(x, 16);
     const dim3 grid((rows + 3) / 4), block(256);
-    if (vec)
+    if (vec && K <= 16 * 256) {
+        const int nv = (K + 255) / 256;
+        if (nv <= 1) quantize_rows_reg<1><<<grid, block, 0, st>>>(x, ldx, xq, ldq, scale, rows, K);
+        else if (nv <= 2) quantize_rows_reg<2><<<grid, block, 0, st>>>(x, ldx, xq, ldq, scale, rows, K);
+        else if (nv <= 4) quantize_rows_reg<4><<<grid, block, 0, st>>>(x, ldx, xq, ldq, scale, rows, K);
+        else if (nv <= 8) quantize_rows_reg<8><<<grid, block, 0, st>>>(x, ldx, xq, ldq, scale, rows, K);
+        else quantize_rows_reg<16><<<grid, block, 0, st>>>(x, ldx, xq, ldq, scale, rows, K);
+    } else if (vec)
         quantize_rows_kernel<true><<<grid, block, 0, st>>>(x, ldx, xq, ldq, scale, rows, K);
     else
         quantize_rows_kernel<false><<<grid, block, 0, st>>>(x, ldx, xq, ldq, scale, rows, K);
