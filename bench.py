@@ -9,7 +9,9 @@ on the device, int8 weights uniform in [-127,127] with per-channel scales
 pass over all 30 shapes (a quantize launch + a GEMM launch each), inputs and
 weights resident in HBM; small shapes cycle through rotating copies of their
 weights and outputs (>= 512 MiB per shape) so every launch streams from HBM
-rather than from L2/MALL.
+rather than from L2/MALL. For M <= 128 the quantize writes the library's
+panel layout (vla_quantize_act_i8_panel_dev) and the GEMM reads it
+(vla_dense_linear_i8_panel_dev): the same values, byte-identical output.
 
 value = int8 TOPS of the whole step (sum of 2*M*N*K over the shapes / step
 time). roofline = the dominant kernel (the M=8192, K=N=4096 GEMM) measured
@@ -89,20 +91,34 @@ class Shape:
         self.W = [Wd] + [Wd.clone() for _ in range(self.R - 1)]
         self.out = [torch.empty((M, N), dtype=torch.float32, device=dev) for _ in range(self.R)]
         self.x = torch.from_numpy(x).to(dev)
-        self.xq = torch.zeros((M, self.ldw), dtype=torch.int8, device=dev)
+        # M <= 128: the library's panel layout for the quantized rows (the
+        # skinny GEMM then reads each 16-row fragment as 1 KiB of contiguous
+        # memory); the same quantize + GEMM arithmetic, bit-identical output
+        self.panel = M <= 128
+        if self.panel:
+            self.xq = torch.zeros((vla.i8_panel_bytes(M, K),), dtype=torch.int8, device=dev)
+        else:
+            self.xq = torch.zeros((M, self.ldw), dtype=torch.int8, device=dev)
         self.sa = torch.empty(M, dtype=torch.float32, device=dev)
         self.ws = torch.from_numpy(ws).to(dev)
         self.b = torch.from_numpy(b).to(dev)
         self.i = 0
 
     def quantize(self, vla, stream):
-        vla.quantize_act_i8_dev(self.x, self.xq, self.sa, stream)
+        if self.panel:
+            vla.quantize_act_i8_panel_dev(self.x, self.xq, self.sa, stream)
+        else:
+            vla.quantize_act_i8_dev(self.x, self.xq, self.sa, stream)
 
     def gemm(self, vla, stream):
         r = self.i % self.R
         self.i += 1
-        vla.dense_linear_i8_pre_dev(self.out[r], self.xq, self.sa, self.W[r], self.ws, self.b, self.K,
-                                    stream=stream)
+        if self.panel:
+            vla.dense_linear_i8_panel_dev(self.out[r], self.xq, self.sa, self.W[r], self.ws, self.b, self.K,
+                                          stream=stream)
+        else:
+            vla.dense_linear_i8_pre_dev(self.out[r], self.xq, self.sa, self.W[r], self.ws, self.b, self.K,
+                                        stream=stream)
 
     def op(self, vla, stream):
         self.quantize(vla, stream)
@@ -402,7 +418,7 @@ def main():
             "gemm_tops": round(ops / g_us / 1e6, 2),
             "gemm_gbs": round(gemm_bytes(sh.M, sh.K, sh.N) / g_us / 1e3, 1),
             "bound": bound, "roof_us": round(t_roof, 3), "frac": round(t_roof / g_us, 4),
-            "rotating_copies": sh.R,
+            "rotating_copies": sh.R, "a_layout": "panel" if sh.panel else "row-major",
         })
         if (sh.M, sh.K, sh.N) == dominant:
             dom_us = g_us

@@ -151,6 +151,26 @@ VLA_API int32_t vla_dense_linear_i8_pre_dev(float* out, int32_t ldo, const int8_
                                             int32_t seq, int32_t N, int32_t K, int32_t act,
                                             int32_t accumulate, void* stream);
 
+/* Panel layout of quantized activations for seq <= 128 rows (the shape of
+ * action chunks and decode rows; no counterpart in the reference, whose
+ * xq is [seq, i8_kpad(K)]): K is cut into 64-byte panels, each holding all
+ * rows' 64 bytes back to back over round_up(seq, 16) rows, so element (t, k)
+ * is at byte (k/64) * round_up(seq,16) * 64 + t*64 + k%64; bytes past K in a
+ * row's last panel are zero. A 16-row x 64-byte MFMA fragment is then 1 KiB
+ * of contiguous memory. vla_i8_panel_bytes gives the buffer size (-1 outside
+ * 0..128 rows). The values are exactly those of vla_quantize_act_i8 and
+ * vla_dense_linear_i8_pre_dev; only the byte order of xq differs. */
+VLA_API int64_t vla_i8_panel_bytes(int32_t seq, int32_t K);
+VLA_API int32_t vla_quantize_act_i8_panel_dev(const float* x, int32_t ldx, int8_t* xq,
+                                              float* ascale, int32_t seq, int32_t K,
+                                              void* stream);
+VLA_API int32_t vla_dense_linear_i8_panel_dev(float* out, int32_t ldo, const int8_t* xq,
+                                              const float* ascale, const int8_t* Wq,
+                                              int32_t ldw, const float* wscale,
+                                              const float* bias, int32_t seq, int32_t N,
+                                              int32_t K, int32_t act, int32_t accumulate,
+                                              void* stream);
+
 /* Exact int32 accumulators acc[t*N+n] (the value gemm_i8.cpp:270-277 forms
  * before its epilogue), for bit-exact parity checks. */
 VLA_API int32_t vla_gemm_i8_i32(int32_t* acc, const int8_t* xq, const int8_t* Wq,

@@ -219,3 +219,86 @@ def test_tile_epilogue_options(vla, orc, torch_cuda, tile):
     want = np.float32(0.25) + orc.apply_act(orc.dense_linear_i8_pre(xq, sa, Wq, ws, b, K), 1)
     assert same_bits(got[:, :N], want.astype(np.float32))
     assert np.all(got[:, N:] == np.float32(0.25)), "wrote past N"
+
+
+def _from_panel(buf, seq, K):
+    """Row-major [seq, K] view of panel-layout bytes (the layout vla_simd_hip.h
+    documents: byte (k/64)*round16(seq)*64 + t*64 + k%64), plus each row's
+    bytes [K, round64(K))."""
+    mp, k64 = (seq + 15) // 16 * 16, (K + 63) // 64 * 64
+    p = np.asarray(buf, np.int8)[: mp * k64].reshape(k64 // 64, mp, 64)
+    rows = p.transpose(1, 0, 2).reshape(mp, k64)[:seq]
+    return rows[:, :K], rows[:, K:]
+
+
+@pytest.mark.parametrize("seq,K", [(1, 3), (5, 17), (16, 64), (50, 720), (100, 512), (128, 960),
+                                   (3, 1027), (77, 4100)])
+def test_quantize_panel_layout(vla, orc, torch_cuda, seq, K):
+    """Panel-layout quantization: the same bytes and scales as the oracle's
+    row-major quantize_act_i8, at the documented panel offsets, pads zero."""
+    torch = torch_cuda
+    synth = load_synth()
+    x = synth.normal(f"qp.{seq}x{K}", (seq, K))
+    if seq > 2:
+        x[1, :] = 0.0
+    n = vla.i8_panel_bytes(seq, K)
+    assert n == (seq + 15) // 16 * 16 * ((K + 63) // 64 * 64)
+    dev = torch.device("cuda")
+    xd = torch.from_numpy(x).to(dev)
+    xq = torch.full((n,), 99, dtype=torch.int8, device=dev)  # pads must be overwritten
+    sa = torch.zeros(seq, dtype=torch.float32, device=dev)
+    vla.quantize_act_i8_panel_dev(xd, xq, sa)
+    torch.cuda.synchronize()
+    got, pad = _from_panel(xq.cpu().numpy(), seq, K)
+    qo, so = orc.quantize_act_i8(x)
+    assert same_bits(got, qo[:, :K]), "panel bytes differ from the oracle's row-major quantization"
+    assert same_bits(sa.cpu().numpy(), so)
+    assert np.all(pad == 0), "bytes past K in a row's last panel must be zero"
+
+
+@pytest.mark.parametrize("seq,N,K", [(1, 16, 3), (7, 48, 64), (50, 768, 1027), (13, 64, 17),
+                                     (100, 3200, 512), (64, 2560, 960), (100, 960, 2560),
+                                     (50, 4096, 4096), (128, 720, 2048), (2, 40, 1)])
+@pytest.mark.parametrize("act,accumulate", [(0, 0), (1, 1), (2, 0)])
+def test_panel_gemm_bitexact(vla, orc, torch_cuda, seq, N, K, act, accumulate):
+    """The skinny GEMM over panel-layout activations: bit-exact with the
+    oracle's dense_linear_i8_pre (ReLU exact; GELU within device libm)."""
+    torch = torch_cuda
+    x, W, b = _case(orc, seq, N, K)
+    Wq, ws = orc.quantize_weights_i8(W)
+    ld = (K + 63) // 64 * 64
+    Wp = np.zeros((N, ld), np.int8)
+    Wp[:, :Wq.shape[1]] = Wq
+    dev = torch.device("cuda")
+    xd = torch.from_numpy(x).to(dev)
+    xq = torch.empty((vla.i8_panel_bytes(seq, K),), dtype=torch.int8, device=dev)
+    sa = torch.empty(seq, dtype=torch.float32, device=dev)
+    vla.quantize_act_i8_panel_dev(xd, xq, sa)
+    Wd = torch.from_numpy(Wp).to(dev)
+    wsd = torch.from_numpy(ws).to(dev)
+    bd = torch.from_numpy(b).to(dev)
+    base = np.full((seq, N), 0.25, np.float32)
+    out = torch.from_numpy(base.copy()).to(dev)
+    vla.dense_linear_i8_panel_dev(out, xq, sa, Wd, wsd, bd, K, act=act, accumulate=accumulate)
+    torch.cuda.synchronize()
+    xqo, sao = orc.quantize_act_i8(x)
+    want = orc.apply_act(orc.dense_linear_i8_pre(xqo, sao, Wq, ws, b, K), act)
+    if accumulate:
+        want = (base + want).astype(np.float32)
+    got = out.cpu().numpy()
+    if act == 2:
+        assert max_rel(got, want) <= 2e-6
+    else:
+        assert same_bits(got, want), "panel-layout GEMM differs from the oracle"
+
+
+def test_panel_rejects_large_m(vla, torch_cuda):
+    torch = torch_cuda
+    assert vla.i8_panel_bytes(129, 64) == -1
+    dev = torch.device("cuda")
+    x = torch.zeros((129, 64), dtype=torch.float32, device=dev)
+    xq = torch.zeros((144 * 64,), dtype=torch.int8, device=dev)
+    sa = torch.zeros(129, dtype=torch.float32, device=dev)
+    with pytest.raises(vla.VlaError) as e:
+        vla.quantize_act_i8_panel_dev(x, xq, sa)
+    assert e.value.status == vla.VLA_ERR_ARG

@@ -41,6 +41,7 @@ EXPORTS = (
     "vla_hip_memset", "vla_hip_synchronize", "vla_hip_device_name",
     "vla_i8_kpad", "vla_quantize_act_i8", "vla_quantize_act_i8_dev", "vla_pack_weights_i8",
     "vla_dense_linear_i8_pre", "vla_dense_linear_i8", "vla_dense_linear_i8_pre_dev",
+    "vla_i8_panel_bytes", "vla_quantize_act_i8_panel_dev", "vla_dense_linear_i8_panel_dev",
     "vla_gemm_i8_i32", "vla_gemm_i8_i32_dev",
     "vla_linear_i8_create", "vla_linear_i8_create_q", "vla_linear_i8_free",
     "vla_linear_i8_weights", "vla_linear_i8_wscale", "vla_linear_i8_ldw",
@@ -110,6 +111,9 @@ def _declare(L):
         "vla_dense_linear_i8_pre": (i32, [P, P, P, P, P, P, i32, i32, i32]),
         "vla_dense_linear_i8": (i32, [P, P, P, P, P, i32, i32, i32]),
         "vla_dense_linear_i8_pre_dev": (i32, [P, i32, P, i32, P, P, i32, P, P, i32, i32, i32, i32, i32, P]),
+        "vla_i8_panel_bytes": (ctypes.c_int64, [i32, i32]),
+        "vla_quantize_act_i8_panel_dev": (i32, [P, i32, P, P, i32, i32, P]),
+        "vla_dense_linear_i8_panel_dev": (i32, [P, i32, P, P, P, i32, P, P, i32, i32, i32, i32, i32, P]),
         "vla_gemm_i8_i32": (i32, [P, P, P, i32, i32, i32]),
         "vla_gemm_i8_i32_dev": (i32, [P, P, i32, P, i32, i32, i32, i32, P]),
         "vla_linear_i8_create": (P, [P, P, i32, i32]),
@@ -438,6 +442,25 @@ def dense_linear_i8_pre_dev(out, xq, ascale, Wq, wscale, bias, K, act=0, accumul
     _call("vla_dense_linear_i8_pre_dev", _dp(out), out.stride(0), _dp(xq), xq.stride(0),
           _dp(ascale), _dp(Wq), Wq.stride(0), _dp(wscale), _dp(bias), seq, N, K, act, accumulate,
           _stream(stream))
+
+
+def i8_panel_bytes(seq: int, K: int) -> int:
+    """Bytes of the panel layout of [seq, K] int8 activations (seq <= 128)."""
+    return int(lib().vla_i8_panel_bytes(seq, K))
+
+
+def quantize_act_i8_panel_dev(x, xq, ascale, stream=None):
+    """quantize_act_i8 of x [seq, K] into the panel layout (xq: >= i8_panel_bytes bytes)."""
+    seq, K = x.shape
+    _call("vla_quantize_act_i8_panel_dev", _dp(x), x.stride(0), _dp(xq), _dp(ascale), seq, K,
+          _stream(stream))
+
+
+def dense_linear_i8_panel_dev(out, xq, ascale, Wq, wscale, bias, K, act=0, accumulate=0, stream=None):
+    """dense_linear_i8_pre_dev with panel-layout activations (seq = out rows <= 128)."""
+    seq, N = out.shape[0], Wq.shape[0]
+    _call("vla_dense_linear_i8_panel_dev", _dp(out), out.stride(0), _dp(xq), _dp(ascale), _dp(Wq),
+          Wq.stride(0), _dp(wscale), _dp(bias), seq, N, K, act, accumulate, _stream(stream))
 
 
 def gemm_i8_i32_dev(acc, xq, Wq, K, stream=None):

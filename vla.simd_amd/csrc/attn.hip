@@ -64,7 +64,9 @@ struct AttnCfg {
     static constexpr int TILE = 2 * KT * SK;         // K + V of one wave, floats
     static constexpr int F4 = KT * HDP / 4 / 64;     // float4 loads per lane per K (or V) tile
     static constexpr int MERGE = W * (32 + 16 * HDP);
-    static constexpr int LDS = 4 * (W * TILE > MERGE ? W * TILE : MERGE);
+    static constexpr int MAIN = 4 * (W * TILE > MERGE ? W * TILE : MERGE);  // bytes
+    static constexpr int ALLOW = 4096;  // group table bytes kept in LDS (n_groups <= 64)
+    static constexpr int LDS = MAIN + ALLOW;
     static_assert(KT % 16 == 0 && (KT * HDP / 4) % 64 == 0, "tile shape");
 };
 
@@ -103,6 +105,15 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
     const float scale = a.scale;
     const int mk = a.mask_kind;
     const int qg = (mk == 3 && qok) ? a.q_group[qi] : 0;
+    const int G = a.n_groups;
+    // small group tables live in LDS, so the per-key test is an LDS read
+    const uint8_t* allow = a.allow;
+    if (mk == 3 && G * G <= C::ALLOW) {
+        uint8_t* al = reinterpret_cast<uint8_t*>(smem) + C::MAIN;
+        for (int i = tid; i < G * G; i += W * 64) al[i] = a.allow[i];
+        __syncthreads();
+        allow = al;
+    }
 
     // keys past kv_end are blocked for every query of the block (causal bound)
     int kv_end = a.seq_k;
@@ -115,6 +126,10 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
     // this lane's share of a tile load: float4 number e = lane + 64 * i of the
     // KT x HDP/4 tile is row e / (HDP/4), dims 4 * (e % (HDP/4))
     float4 kr[F4], vr[F4];
+    // with the tile: the mask data of the lane's keys kv0 + 16 kt + 4 g + r
+    // (dense mask values or key groups), so the masking step waits on nothing
+    float mnext[4 * NT];
+    int gnext[4 * NT];
     auto gload = [&](int kv0, int end) {
 #pragma unroll
         for (int i = 0; i < F4; i++) {
@@ -124,6 +139,16 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
             if (j < end && d < HD) {
                 kr[i] = *reinterpret_cast<const float4*>(a.K + (size_t)j * a.ldk + kvh * HD + d);
                 vr[i] = *reinterpret_cast<const float4*>(a.V + (size_t)j * a.ldv + kvh * HD + d);
+            }
+        }
+#pragma unroll
+        for (int x = 0; x < 4 * NT; x++) {
+            const int j = kv0 + (x >> 2) * 16 + 4 * g + (x & 3);
+            mnext[x] = 0.0f;
+            gnext[x] = 0;
+            if (j < end) {
+                if (mk == 1 && qok) mnext[x] = a.mask[(size_t)qi * a.ldm + j];
+                else if (mk == 3) gnext[x] = a.k_group[j];
             }
         }
     };
@@ -146,6 +171,13 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
     for (int t = wave; t < nkt; t += W) {
         const int kv0 = t * KT;
         lstore();
+        float mcur[4 * NT];
+        int gcur[4 * NT];
+#pragma unroll
+        for (int x = 0; x < 4 * NT; x++) {
+            mcur[x] = mnext[x];
+            gcur[x] = gnext[x];
+        }
         wave_lds_sync();
         if (t + W < nkt) gload((t + W) * KT, a.seq_k);  // next tile, under this one's math
 
@@ -175,13 +207,13 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
                 bool blocked = !qok || j >= kv_end;
                 if (!blocked) {
                     if (mk == 1) {
-                        const float mv = a.mask[(size_t)qi * a.ldm + j];
+                        const float mv = mcur[kt * 4 + r];
                         if (mv == -FLT_MAX) blocked = true;
                         else x = x + mv;
                     } else if (mk == 2) {
                         blocked = j > qi + a.causal_offset;
                     } else if (mk == 3) {
-                        blocked = !a.allow[qg * a.n_groups + a.k_group[j]];
+                        blocked = !allow[qg * G + gcur[kt * 4 + r]];
                     }
                 }
                 x = blocked ? -INFINITY : x;
@@ -363,7 +395,7 @@ void launch_attention(const AttnArgs& a, hipStream_t st) {
                 "attention: group mask needs q_group, k_group, allow and 1..256 groups");
     if (a.seq_q == 0) return;
     if (a.head_dim <= 64)
-        run_attn<64, 32, 8>(a, st);
+        run_attn<64, 16, 8>(a, st);
     else if (a.head_dim <= 128)
         run_attn<128, 32, 4>(a, st);
     else

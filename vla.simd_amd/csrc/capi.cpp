@@ -249,6 +249,43 @@ VLA_API int32_t vla_dense_linear_i8_pre_dev(float* out, int32_t ldo, const int8_
     });
 }
 
+VLA_API int64_t vla_i8_panel_bytes(int32_t seq, int32_t K) {
+    if (seq < 0 || seq > kPanelMaxRows || K <= 0) return -1;
+    return (int64_t)panel_bytes(seq, K);
+}
+
+VLA_API int32_t vla_quantize_act_i8_panel_dev(const float* x, int32_t ldx, int8_t* xq, float* ascale,
+                                              int32_t seq, int32_t K, void* stream) {
+    return guarded("vla_quantize_act_i8_panel_dev", [&] {
+        launch_quantize_rows_panel(x, ldx, xq, ascale, seq, K, as_stream(stream));
+    });
+}
+
+VLA_API int32_t vla_dense_linear_i8_panel_dev(float* out, int32_t ldo, const int8_t* xq,
+                                              const float* ascale, const int8_t* Wq, int32_t ldw,
+                                              const float* wscale, const float* bias, int32_t seq,
+                                              int32_t N, int32_t K, int32_t act, int32_t accumulate,
+                                              void* stream) {
+    return guarded("vla_dense_linear_i8_panel_dev", [&] {
+        GemmArgs a{};
+        a.A = xq;
+        a.a_panel = 1;
+        a.B = Wq;
+        a.ldb = ldw;
+        a.ascale = ascale;
+        a.wscale = wscale;
+        a.bias = bias;
+        a.out = out;
+        a.ldo = ldo;
+        a.M = seq;
+        a.N = N;
+        a.K = K;
+        a.act = act;
+        a.accumulate = accumulate;
+        launch_gemm_i8(a, as_stream(stream));
+    });
+}
+
 VLA_API int32_t vla_gemm_i8_i32_dev(int32_t* acc, const int8_t* xq, int32_t ldx, const int8_t* Wq,
                                     int32_t ldw, int32_t seq, int32_t N, int32_t K, void* stream) {
     return guarded("vla_gemm_i8_i32_dev", [&] {

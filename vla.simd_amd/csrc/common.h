@@ -54,13 +54,29 @@ constexpr int kWave = 64;
 // ---- kernel launchers (defined in the .hip files) ----
 
 // quant.hip
+// the same quantization written in the panel layout (rows <= kPanelMaxRows),
+// panel_bytes(rows, K) bytes at xq
+void launch_quantize_rows_panel(const float* x, int ldx, int8_t* xq, float* scale, int rows, int K,
+                                hipStream_t st);
 void launch_quantize_rows(const float* x, int ldx, int8_t* xq, int ldq, float* scale,
                           int rows, int K, hipStream_t st);
 
 // gemm_i8.hip: epilogue selects raw int32 output (acc32 != nullptr) or the
 // fused dequant/bias/act(/accumulate) fp32 store.
+// Panel layout of quantized activations (M <= 128, the skinny GEMM's input):
+// K is cut into 64-byte panels, each holding every row's 64 bytes back to
+// back over round_up(M, 16) rows, so element (m, k) sits at byte
+// (k / 64) * panel_rows(M) * 64 + m * 64 + k % 64. One MFMA fragment (16 rows x
+// 64 bytes) is then 1 KiB of contiguous memory, which one wave load reads as
+// whole cache lines; row-major rows would cost 16 half-lines per load.
+// Bytes [K, round_up(K, 64)) of every row are zero; rows [M, panel_rows(M))
+// are never read into a stored output.
+__host__ __device__ inline int panel_rows(int M) { return (M + 15) & ~15; }
+inline size_t panel_bytes(int M, int K) { return (size_t)panel_rows(M) * (size_t)((K + 63) & ~63); }
+constexpr int kPanelMaxRows = 128;
+
 struct GemmArgs {
-    const int8_t* A;  int lda;   // quantized activations [M, lda]
+    const int8_t* A;  int lda;   // quantized activations [M, lda] (row-major; unused when a_panel)
     const int8_t* B;  int ldb;   // int8 weights [N, ldb]
     const float* ascale;         // [M]
     const float* wscale;         // [N]
@@ -70,6 +86,7 @@ struct GemmArgs {
     int M, N, K;
     int act;                     // vla_act
     int accumulate;              // out += result
+    int a_panel;                 // A in the panel layout above (M <= kPanelMaxRows)
 };
 void launch_gemm_i8(const GemmArgs& a, hipStream_t st);
 
@@ -121,6 +138,7 @@ struct RowQArgs {
     float* out2 = nullptr;      int ldo2 = 0;
     int8_t* q2 = nullptr;       int ldq2 = 0; float* qs2 = nullptr;
     int rows = 0, H = 0;
+    int q_panel = 0;            // q and q2 in the panel layout (ldq, ldq2 unused)
 };
 void launch_rowq(const RowQArgs& a, hipStream_t st);
 

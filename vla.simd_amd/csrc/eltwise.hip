@@ -262,15 +262,28 @@ __global__ __launch_bounds__(256) void rowq_kernel(RowQArgs a) {
             amax = wave_max_f32(amax);
             const float s = row_scale(amax);
             const float inv = 1.0f / s;
-            const int ldq = pass ? a.ldq2 : a.ldq;
             if (lane == 0) (pass ? a.qs2 : a.qs)[row] = s;
-            int8_t* qr = q + (size_t)row * ldq;
+            if (a.q_panel) {
+                // panel layout (common.h): word k of the row at (k / 64) * mp * 64 + row * 64 + k % 64
+                const size_t pstride = (size_t)panel_rows(a.rows) * 64;
+                int8_t* qr = q + (size_t)row * 64;
 #pragma unroll
-            for (int i = 0; i < NV; i++) {
-                const int k = 4 * lane + 256 * i;
-                if (k < H) *reinterpret_cast<uint32_t*>(qr + k) = q8x4(y[i], inv);
+                for (int i = 0; i < NV; i++) {
+                    const int k = 4 * lane + 256 * i;
+                    if (k < H) *reinterpret_cast<uint32_t*>(qr + (k >> 6) * pstride + (k & 63)) = q8x4(y[i], inv);
+                }
+                for (int k = H + 4 * lane; k < ((H + 63) & ~63); k += 256)
+                    *reinterpret_cast<uint32_t*>(qr + (k >> 6) * pstride + (k & 63)) = 0u;
+            } else {
+                const int ldq = pass ? a.ldq2 : a.ldq;
+                int8_t* qr = q + (size_t)row * ldq;
+#pragma unroll
+                for (int i = 0; i < NV; i++) {
+                    const int k = 4 * lane + 256 * i;
+                    if (k < H) *reinterpret_cast<uint32_t*>(qr + k) = q8x4(y[i], inv);
+                }
+                for (int k = H + 4 * lane; k < ldq; k += 256) *reinterpret_cast<uint32_t*>(qr + k) = 0u;
             }
-            for (int k = H + 4 * lane; k < ldq; k += 256) *reinterpret_cast<uint32_t*>(qr + k) = 0u;
         }
     }
 }
@@ -364,11 +377,14 @@ void launch_rowq(const RowQArgs& a, hipStream_t st) {
     VLA_REQUIRE(a.op != 3 || (a.u && a.ldu >= a.H && a.ldu % 4 == 0 && aligned(a.u, 16)),
                 "rowq: silu_gate needs 16-byte aligned u rows");
     VLA_REQUIRE(!a.out || (a.ldo >= a.H && a.ldo % 4 == 0 && aligned(a.out, 16)), "rowq: bad out");
-    VLA_REQUIRE(!a.q || (a.qs && a.ldq >= a.H && a.ldq % 4 == 0 && aligned(a.q, 4)), "rowq: bad q");
+    VLA_REQUIRE(!a.q_panel || a.rows <= kPanelMaxRows, "rowq: the panel layout holds at most 128 rows");
+    VLA_REQUIRE(!a.q || (a.qs && (a.q_panel || (a.ldq >= a.H && a.ldq % 4 == 0)) && aligned(a.q, 4)),
+                "rowq: bad q");
     VLA_REQUIRE(!a.add || (a.ld_add >= a.H && a.ld_add % 4 == 0 && aligned(a.add, 16)), "rowq: bad add");
     VLA_REQUIRE(!a.out2 || (a.add && a.ldo2 >= a.H && a.ldo2 % 4 == 0 && aligned(a.out2, 16)),
                 "rowq: bad out2");
-    VLA_REQUIRE(!a.q2 || (a.add && a.qs2 && a.ldq2 >= a.H && a.ldq2 % 4 == 0 && aligned(a.q2, 4)),
+    VLA_REQUIRE(!a.q2 || (a.add && a.qs2 && (a.q_panel || (a.ldq2 >= a.H && a.ldq2 % 4 == 0)) &&
+                          aligned(a.q2, 4)),
                 "rowq: bad q2");
     if (a.rows == 0) return;
     if (a.op == 0) launch_rowq_op<0>(a, st);

@@ -726,12 +726,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
     const int n0 = blockIdx.x * 16;
     const int K = a.K;
 
+    // A fragment i of k-step s is at arow[i] + s * astep: row-major rows
+    // (clamped to the last row), or the panel layout, where the fragment's 16
+    // rows x 64 bytes are contiguous (rows past M are padding, never stored)
     const int r16 = lane & 15, kq = (lane >> 4) * 16;
+    const size_t astep = a.a_panel ? (size_t)panel_rows(a.M) * 64 : 64;
     const int8_t* arow[FM];
 #pragma unroll
     for (int i = 0; i < FM; i++) {
         const int m = i * 16 + r16 < a.M ? i * 16 + r16 : a.M - 1;
-        arow[i] = a.A + (size_t)m * a.lda + kq;
+        arow[i] = a.a_panel ? a.A + (size_t)(i * 16 + r16) * 64 + kq : a.A + (size_t)m * a.lda + kq;
     }
     const int n = n0 + r16 < a.N ? n0 + r16 : a.N - 1;
     const int8_t* brow = a.B + (size_t)n * a.ldb + kq;
@@ -762,33 +766,51 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
 #pragma unroll
     for (int i = 0; i < FM; i++) acc[i] = v4i{0, 0, 0, 0};
 
+    // This wave's 64-byte k-steps are wave, wave + WAVES, ... < full, rotated
+    // by a per-block offset: every block reads all of A, and without the
+    // rotation the blocks of an XCD would all read the same A lines at the
+    // same moment and queue on the same L2 channels (the int32 sums do not
+    // depend on the order). The loads run P steps ahead of the MFMAs in a
+    // register ring.
     const int full = K / 64;  // 64-byte steps read without masks
-    int s = wave;
-    for (; s + WAVES < full; s += 2 * WAVES) {
-        const v4i b0 = *reinterpret_cast<const v4i*>(brow + s * 64);
-        const v4i b1 = *reinterpret_cast<const v4i*>(brow + (s + WAVES) * 64);
-        v4i a0[FM], a1[FM];
+    constexpr int P = (FM <= 3 || (FM == 4 && WAVES < 16)) ? 4 : 3;  // within the VGPR budget
+    // blocks i, i + 8, i + 16, ... share an XCD; (WAVES + 1) is odd, so their
+    // offsets differ for up to `full` blocks when full is a power of two
+    const int rot = full > 0 ? (int)(((unsigned)blockIdx.x >> 3) * (WAVES + 1) % (unsigned)full) : 0;
+    v4i ra[P][FM], rb[P];
+    auto load = [&](int p, int k) {
+        int step = wave + k * WAVES + rot;
+        step = step < full ? step : step - full;
+        rb[p] = *reinterpret_cast<const v4i*>(brow + step * 64);
+        const size_t aoff = (size_t)step * astep;
 #pragma unroll
-        for (int i = 0; i < FM; i++) {
-            a0[i] = *reinterpret_cast<const v4i*>(arow[i] + s * 64);
-            a1[i] = *reinterpret_cast<const v4i*>(arow[i] + (s + WAVES) * 64);
-        }
+        for (int i = 0; i < FM; i++) ra[p][i] = *reinterpret_cast<const v4i*>(arow[i] + aoff);
+    };
+    const int nst = wave < full ? (full - wave + WAVES - 1) / WAVES : 0;
+    StaticFor<0, P>::run([&](auto pc) {
+        constexpr int p = decltype(pc)::value;
+        if (p < nst) load(p, p);
+    });
+    for (int k0 = 0; k0 < nst; k0 += P) {
+        StaticFor<0, P>::run([&](auto pc) {
+            constexpr int p = decltype(pc)::value;
+            const int k = k0 + p;
+            if (k < nst) {
 #pragma unroll
-        for (int i = 0; i < FM; i++) acc[i] = mfma_i8(a0[i], b0, acc[i]);
-#pragma unroll
-        for (int i = 0; i < FM; i++) acc[i] = mfma_i8(a1[i], b1, acc[i]);
-    }
-    for (; s < full; s += WAVES) {
-        const v4i b0 = *reinterpret_cast<const v4i*>(brow + s * 64);
-#pragma unroll
-        for (int i = 0; i < FM; i++)
-            acc[i] = mfma_i8(*reinterpret_cast<const v4i*>(arow[i] + s * 64), b0, acc[i]);
+                for (int i = 0; i < FM; i++) acc[i] = mfma_i8(ra[p][i], rb[p], acc[i]);
+                if (k + P < nst) load(p, k + P);
+            }
+        });
     }
     if (K % 64 && wave == full % WAVES) {
         const int k = full * 64 + kq;
-        const v4i b0 = load_chunk<true>(brow - kq, k, K);
+        const v4i b0 = load_chunk<true>(brow - kq, k, K);  // zero past K: A bytes there add nothing
 #pragma unroll
-        for (int i = 0; i < FM; i++) acc[i] = mfma_i8(load_chunk<true>(arow[i] - kq, k, K), b0, acc[i]);
+        for (int i = 0; i < FM; i++) {
+            const v4i av = a.a_panel ? *reinterpret_cast<const v4i*>(arow[i] + (size_t)full * astep)
+                                     : load_chunk<true>(arow[i] - kq, k, K);
+            acc[i] = mfma_i8(av, b0, acc[i]);
+        }
     }
 
     // partial tiles to LDS (no two waves share an address), then each thread
@@ -1003,7 +1025,7 @@ void dispatch_tile(const Tile& t, const GemmArgs& a, hipStream_t st) {
 void launch_gemm_i8(const GemmArgs& a, hipStream_t st) {
     VLA_REQUIRE(a.M >= 0 && a.N > 0 && a.K > 0, "gemm_i8: need M >= 0, N > 0, K > 0");
     VLA_REQUIRE(a.K <= kMaxI8K, "gemm_i8: K exceeds the int8 accumulator bound INT_MAX/(255*127)");
-    VLA_REQUIRE(a.lda >= kpad4(a.K) && a.ldb >= kpad4(a.K) && a.lda % 4 == 0 && a.ldb % 4 == 0,
+    VLA_REQUIRE((a.a_panel || (a.lda >= kpad4(a.K) && a.lda % 4 == 0)) && a.ldb >= kpad4(a.K) && a.ldb % 4 == 0,
                 "gemm_i8: int8 row strides must be multiples of 4 and >= i8_kpad(K)");
     VLA_REQUIRE(aligned(a.A, 4) && aligned(a.B, 4), "gemm_i8: int8 operands must be 4-byte aligned");
     VLA_REQUIRE(a.acc32 || (a.out && a.wscale && a.ascale && a.ldo >= a.N),
@@ -1011,8 +1033,10 @@ void launch_gemm_i8(const GemmArgs& a, hipStream_t st) {
     VLA_REQUIRE(a.act >= 0 && a.act <= 3, "gemm_i8: unknown activation");
     if (a.M == 0) return;
 
-    const bool al = a.lda % 16 == 0 && a.ldb % 16 == 0 && aligned(a.A, 16) && aligned(a.B, 16) &&
-                    (a.acc32 ? aligned(a.acc32, 16) : aligned(a.out, 16));
+    const bool al = (a.a_panel || a.lda % 16 == 0) && a.ldb % 16 == 0 && aligned(a.A, 16) &&
+                    aligned(a.B, 16) && (a.acc32 ? aligned(a.acc32, 16) : aligned(a.out, 16));
+    VLA_REQUIRE(!a.a_panel || (a.M <= kPanelMaxRows && al),
+                "gemm_i8: panel-layout activations need M <= 128 and 16-byte aligned operands");
     if (!al) {
         const int blocks = ((a.M + 63) / 64) * ((a.N + 63) / 64);
         gemm_i8_generic<<<blocks, 256, 0, st>>>(a);

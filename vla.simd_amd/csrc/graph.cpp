@@ -51,16 +51,20 @@ void DLinear::init(DeviceArena& A, const std::vector<RowBlock>& blocks, int K_, 
     }
 }
 
-QAct Ctx::slot(int i, int ld) const {
+QAct Ctx::slot(int i, int ld, int rows) const {
     QAct a;
     a.q = xq[i];
     a.s = xs[i];
     a.ld = ld;
+    a.panel = rows <= kPanelMaxRows;
+    const size_t need = a.panel ? (size_t)panel_rows(rows) * ld : (size_t)rows * ld;
+    VLA_REQUIRE(need <= xq_bytes && rows <= xs_rows, "graph: activation quantization scratch too small");
     return a;
 }
 
 void Ctx::alloc(DeviceArena& A, int rows, int ld_max) {
-    xq_bytes = (size_t)rows * ld_max;
+    // room for the panel layout's rows rounded up to 16 as well
+    xq_bytes = (size_t)panel_rows(rows) * ld_max;
     xs_rows = rows;
     for (int i = 0; i < 2; i++) {
         xq[i] = A.alloc<int8_t>(xq_bytes);
@@ -69,9 +73,10 @@ void Ctx::alloc(DeviceArena& A, int rows, int ld_max) {
 }
 
 void quantize(const Ctx& c, const QAct& dst, const float* x, int ldx, int seq, int K) {
-    VLA_REQUIRE((size_t)seq * dst.ld <= c.xq_bytes && seq <= c.xs_rows,
-                "graph: activation quantization scratch too small");
-    launch_quantize_rows(x, ldx, dst.q, dst.ld, dst.s, seq, K, c.st);
+    const size_t need = dst.panel ? (size_t)panel_rows(seq) * dst.ld : (size_t)seq * dst.ld;
+    VLA_REQUIRE(need <= c.xq_bytes && seq <= c.xs_rows, "graph: activation quantization scratch too small");
+    if (dst.panel) launch_quantize_rows_panel(x, ldx, dst.q, dst.s, seq, K, c.st);
+    else launch_quantize_rows(x, ldx, dst.q, dst.ld, dst.s, seq, K, c.st);
 }
 
 static void gemm_q(const Ctx& c, const DLinear& L, const QAct& x, float* out, int ldo, int seq, int act,
@@ -93,6 +98,7 @@ static void gemm_q(const Ctx& c, const DLinear& L, const QAct& x, float* out, in
     a.K = L.K;
     a.act = act;
     a.accumulate = acc;
+    a.a_panel = x.panel ? 1 : 0;
     launch_gemm_i8(a, c.st);
 }
 
@@ -108,7 +114,7 @@ void linear(const Ctx& c, const DLinear& L, const In& in, float* out, int ldo, i
             gemm_q(c, L, in.q, out, ldo, seq, act, acc, n0, n1);
         } else {
             VLA_REQUIRE(in.f, "linear: no input");
-            const QAct s0 = c.slot(0, L.ldq());
+            const QAct s0 = c.slot(0, L.ldq(), seq);
             quantize(c, s0, in.f, in.ldf, seq, L.K);
             gemm_q(c, L, s0, out, ldo, seq, act, acc, n0, n1);
         }
@@ -124,13 +130,12 @@ In rowop_for(const Ctx& c, const DLinear& L, RowQArgs r, float* f, int ldf, int 
     r.out = f;
     r.ldo = ldf;
     if (L.int8()) {
-        VLA_REQUIRE((size_t)r.rows * L.ldq() <= c.xq_bytes && r.rows <= c.xs_rows,
-                    "graph: activation quantization scratch too small");
-        in.q = c.slot(slot, L.ldq());
+        in.q = c.slot(slot, L.ldq(), r.rows);
         in.quantized = true;
         r.q = in.q.q;
         r.ldq = in.q.ld;
         r.qs = in.q.s;
+        r.q_panel = in.q.panel ? 1 : 0;
     } else {
         VLA_REQUIRE(f, "graph: an fp32 consumer needs the fp32 rows");
     }

@@ -80,6 +80,7 @@ struct QAct {
     int8_t* q = nullptr;
     float* s = nullptr;
     int ld = 0;
+    bool panel = false;  // q in the panel layout (common.h) rather than [rows, ld]
 };
 
 // Per-model stream state: two activation-quantization slots shared by every
@@ -91,8 +92,10 @@ struct Ctx {
     float* xs[2] = {nullptr, nullptr};
     size_t xq_bytes = 0;
     int xs_rows = 0;
-    // slot i laid out for a layer of row stride ld
-    QAct slot(int i, int ld) const;
+    // slot i laid out for a layer of row stride ld, for `rows` rows: the
+    // panel layout when the rows feed the skinny GEMM (rows <= 128), else
+    // row-major [rows, ld]
+    QAct slot(int i, int ld, int rows) const;
     void alloc(class DeviceArena& A, int rows, int ld_max);
 };
 

@@ -239,20 +239,22 @@ void ActTf::run(hipStream_t st) {
         in_v.f = x;
         in_v.ldf = d;
         if (v.int8()) {
-            in_v.q = c.slot(1, v.ldq());
+            in_v.q = c.slot(1, v.ldq(), rows);
             in_v.quantized = true;
             r.q = in_v.q.q;
             r.ldq = in_v.q.ld;
             r.qs = in_v.q.s;
+            r.q_panel = in_v.q.panel ? 1 : 0;
         }
         in_qk.f = xp_;
         in_qk.ldf = d;
         if (qk.int8()) {
-            in_qk.q = c.slot(0, qk.ldq());
+            in_qk.q = c.slot(0, qk.ldq(), rows);  // same rows: same layout as q
             in_qk.quantized = true;
             r.q2 = in_qk.q.q;
             r.ldq2 = in_qk.q.ld;
             r.qs2 = in_qk.q.s;
+            r.q_panel = in_qk.q.panel ? 1 : 0;
         } else {
             r.out2 = xp_;
             r.ldo2 = d;
@@ -330,11 +332,12 @@ void ActTf::run(hipStream_t st) {
         in_q.f = xp_;
         in_q.ldf = d;
         if (l.cq.int8()) {
-            in_q.q = c.slot(0, l.cq.ldq());
+            in_q.q = c.slot(0, l.cq.ldq(), C);
             in_q.quantized = true;
             r.q2 = in_q.q.q;
             r.ldq2 = in_q.q.ld;
             r.qs2 = in_q.q.s;
+            r.q_panel = in_q.q.panel ? 1 : 0;
         } else {
             r.out2 = xp_;
             r.ldo2 = d;

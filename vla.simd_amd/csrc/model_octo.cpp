@@ -271,6 +271,7 @@ void OctoTf::run(hipStream_t st) {
     linear(c, L.qkv, h1, qkv_ + D, 3 * D, T, 0, 0, D, 3 * D);  // k | v, every row
     In hr = h1;                                                   // q of the readout row
     if (hr.quantized) {
+        VLA_REQUIRE(!hr.q.panel, "octo: the readout row needs row-major quantized rows");
         hr.q.q += (size_t)ro * hr.q.ld;
         hr.q.s += ro;
     }

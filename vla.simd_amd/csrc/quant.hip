@@ -102,7 +102,66 @@ __global__ __launch_bounds__(256) void quantize_rows_reg(const float* __restrict
     for (int k = K + 4 * lane; k < ldq; k += 256) *reinterpret_cast<uint32_t*>(qr + k) = 0u;
 }
 
+// The same quantization written in the panel layout (common.h): word (m, k)
+// of a row lands at (k / 64) * mp * 64 + m * 64 + k % 64; bytes [K, K64) of
+// the row are zero. Rows are few (<= 128), so the row is simply read twice.
+template <bool VEC>
+__global__ __launch_bounds__(256) void quantize_rows_panel_kernel(const float* __restrict__ x, int ldx,
+                                                                  int8_t* __restrict__ xq, int mp,
+                                                                  float* __restrict__ scale, int rows,
+                                                                  int K) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;  // wave-uniform
+    const float* xr = x + (size_t)row * ldx;
+    float amax = 0.0f;
+    if (VEC) {
+        for (int k = lane * 4; k < K; k += 256) {
+            const float4 v = *reinterpret_cast<const float4*>(xr + k);
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
+    } else {
+        for (int k = lane; k < K; k += 64) amax = fmaxf(amax, fabsf(xr[k]));
+    }
+    amax = wave_max_f32(amax);
+    const float s = row_scale(amax);
+    const float inv = 1.0f / s;
+    if (lane == 0) scale[row] = s;
+    const int k64 = (K + 63) & ~63;
+    int8_t* base = xq + (size_t)row * 64;
+    for (int k = lane * 4; k < k64; k += 256) {
+        uint32_t word = 0;
+        if (VEC && k + 4 <= K) {
+            word = q8x4(*reinterpret_cast<const float4*>(xr + k), inv);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int kk = k + j;
+                const int q = kk < K ? q8(xr[kk], inv) : 0;
+                word |= (uint32_t)(q & 0xff) << (8 * j);
+            }
+        }
+        *reinterpret_cast<uint32_t*>(base + (size_t)(k >> 6) * mp * 64 + (k & 63)) = word;
+    }
+}
+
 }  // namespace
+
+void launch_quantize_rows_panel(const float* x, int ldx, int8_t* xq, float* scale, int rows, int K,
+                                hipStream_t st) {
+    VLA_REQUIRE(rows >= 0 && rows <= kPanelMaxRows && K > 0,
+                "quantize (panel): rows must be in [0, 128] and K > 0");
+    VLA_REQUIRE(ldx >= K, "quantize (panel): ldx < K");
+    VLA_REQUIRE(aligned(xq, 4), "quantize (panel): xq must be 4-byte aligned");
+    if (rows == 0) return;
+    const int mp = panel_rows(rows);
+    const dim3 grid((rows + 3) / 4), block(256);
+    if (K % 4 == 0 && ldx % 4 == 0 && aligned(x, 16))
+        quantize_rows_panel_kernel<true><<<grid, block, 0, st>>>(x, ldx, xq, mp, scale, rows, K);
+    else
+        quantize_rows_panel_kernel<false><<<grid, block, 0, st>>>(x, ldx, xq, mp, scale, rows, K);
+    VLA_LAUNCH_CHECK();
+}
 
 void launch_quantize_rows(const float* x, int ldx, int8_t* xq, int ldq, float* scale, int rows,
                           int K, hipStream_t st) {
