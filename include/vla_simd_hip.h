@@ -171,6 +171,33 @@ VLA_API int32_t vla_dense_linear_i8_panel_dev(float* out, int32_t ldo, const int
                                               int32_t K, int32_t act, int32_t accumulate,
                                               void* stream);
 
+/* A row op and the int8 quantization of its result in one pass (no
+ * counterpart in the reference, which calls rmsnorm or silu_gate and then
+ * quantize_act_i8: src/hal/common/norms.cpp:19-35, src/ops/eltwise.cpp:29-64,
+ * src/ops/quant_ops.h:17-21): y = op(x) with op 0 identity, 2 RMSNorm with
+ * weights w and eps, 3 silu_gate(x, u) (u rows of stride ldu); xq (panel
+ * layout, as above) and ascale are what vla_quantize_act_i8_panel_dev gives
+ * for y. Rows 16-byte aligned, K a multiple of 4 up to 4096, seq <= 128. */
+VLA_API int32_t vla_rowop_quantize_i8_panel_dev(int32_t op, const float* x, int32_t ldx,
+                                                const float* u, int32_t ldu, const float* w,
+                                                float eps, int8_t* xq, float* ascale,
+                                                int32_t seq, int32_t K, void* stream);
+
+/* The same row op fused into the int8 linear that consumes it (no counterpart
+ * in the reference; one kernel instead of two): out (+)= exactly what
+ * vla_dense_linear_i8_panel_dev gives for the xq / ascale of
+ * vla_rowop_quantize_i8_panel_dev. vla_rowop_linear_i8_fits says whether op,
+ * seq and K are supported (op 0, 2 or 3; 1 <= seq <= 128; K a multiple of 4
+ * up to 2048); out must not overlap x or u; Wq 16-byte aligned with ldw a
+ * multiple of 16. */
+VLA_API int32_t vla_rowop_linear_i8_fits(int32_t op, int32_t seq, int32_t K);
+VLA_API int32_t vla_rowop_linear_i8_dev(float* out, int32_t ldo, int32_t op, const float* x,
+                                        int32_t ldx, const float* u, int32_t ldu,
+                                        const float* w, float eps, const int8_t* Wq,
+                                        int32_t ldw, const float* wscale, const float* bias,
+                                        int32_t seq, int32_t N, int32_t K, int32_t act,
+                                        int32_t accumulate, void* stream);
+
 /* Exact int32 accumulators acc[t*N+n] (the value gemm_i8.cpp:270-277 forms
  * before its epilogue), for bit-exact parity checks. */
 VLA_API int32_t vla_gemm_i8_i32(int32_t* acc, const int8_t* xq, const int8_t* Wq,

@@ -173,3 +173,28 @@ def test_smolvla_chunk(vla, ckdir, mask, n_pad):
           flush=True)
     assert err <= bar
     _check_replay(lambda: m.run(prefix, pad, noise), got)
+
+
+@pytest.mark.parametrize("mask", [0, 48])
+def test_smolvla_short_chunk(vla, ckdir, mask):
+    """A 12-action chunk (4 layers, 60 prefix tokens): the expert's int8 layers
+    take at most 16 rows, so their RMSNorm / silu_gate / quantize row ops run
+    inside the GEMM (gemm_i8_rowop) rather than as separate kernels; same bar."""
+    ck = _ck()
+    from helpers import oracle
+    ob = oracle()
+    c = dict(ck.SMOLVLA_BASE, chunk=12, n_layers=4, expert_layers=4, n_prefix=60)
+    d = str(ckdir / "smol12")
+    if not os.path.exists(os.path.join(d, "aex.bin")):
+        ck.write_smolvla(d, c)
+    prefix, pad, noise = ck.smolvla_inputs(c, n_pad=3)
+    print(f"smolvla chunk 12 mask {mask}", flush=True)
+    r = ob.RefSmolvla(d, mask)
+    ref = r.run(prefix, pad, noise)
+    bar, sens = _bar(mask, lambda x: r.run(x, pad, noise), prefix, ref)
+    m = vla.SmolvlaChunk(d, mask)
+    got = m.run(prefix, pad, noise)
+    err = _rel(got, ref)
+    print(f"smolvla chunk 12 mask {mask}: rel err {err:.3e} (reference ulp spread {sens:.3e})", flush=True)
+    assert err <= bar
+    _check_replay(lambda: m.run(prefix, pad, noise), got)

@@ -42,6 +42,7 @@ EXPORTS = (
     "vla_i8_kpad", "vla_quantize_act_i8", "vla_quantize_act_i8_dev", "vla_pack_weights_i8",
     "vla_dense_linear_i8_pre", "vla_dense_linear_i8", "vla_dense_linear_i8_pre_dev",
     "vla_i8_panel_bytes", "vla_quantize_act_i8_panel_dev", "vla_dense_linear_i8_panel_dev",
+    "vla_rowop_quantize_i8_panel_dev", "vla_rowop_linear_i8_fits", "vla_rowop_linear_i8_dev",
     "vla_gemm_i8_i32", "vla_gemm_i8_i32_dev",
     "vla_linear_i8_create", "vla_linear_i8_create_q", "vla_linear_i8_free",
     "vla_linear_i8_weights", "vla_linear_i8_wscale", "vla_linear_i8_ldw",
@@ -114,6 +115,10 @@ def _declare(L):
         "vla_i8_panel_bytes": (ctypes.c_int64, [i32, i32]),
         "vla_quantize_act_i8_panel_dev": (i32, [P, i32, P, P, i32, i32, P]),
         "vla_dense_linear_i8_panel_dev": (i32, [P, i32, P, P, P, i32, P, P, i32, i32, i32, i32, i32, P]),
+        "vla_rowop_quantize_i8_panel_dev": (i32, [i32, P, i32, P, i32, P, ctypes.c_float, P, P, i32, i32, P]),
+        "vla_rowop_linear_i8_fits": (i32, [i32, i32, i32]),
+        "vla_rowop_linear_i8_dev": (i32, [P, i32, i32, P, i32, P, i32, P, ctypes.c_float, P, i32, P, P, i32,
+                                          i32, i32, i32, i32, P]),
         "vla_gemm_i8_i32": (i32, [P, P, P, i32, i32, i32]),
         "vla_gemm_i8_i32_dev": (i32, [P, P, i32, P, i32, i32, i32, i32, P]),
         "vla_linear_i8_create": (P, [P, P, i32, i32]),
@@ -461,6 +466,33 @@ def dense_linear_i8_panel_dev(out, xq, ascale, Wq, wscale, bias, K, act=0, accum
     seq, N = out.shape[0], Wq.shape[0]
     _call("vla_dense_linear_i8_panel_dev", _dp(out), out.stride(0), _dp(xq), _dp(ascale), _dp(Wq),
           Wq.stride(0), _dp(wscale), _dp(bias), seq, N, K, act, accumulate, _stream(stream))
+
+
+ROWOP_IDENTITY, ROWOP_RMSNORM, ROWOP_SILU_GATE = 0, 2, 3
+
+
+def rowop_quantize_i8_panel_dev(op, x, xq, ascale, u=None, w=None, eps=0.0, stream=None):
+    """op(x) quantized into the panel layout: op 0 identity, 2 RMSNorm(w, eps),
+    3 silu_gate(x, u); x and u are [seq, K] fp32 views (row-strided)."""
+    seq, K = x.shape
+    _call("vla_rowop_quantize_i8_panel_dev", op, _dp(x), x.stride(0), _dp(u), u.stride(0) if u is not None else 0,
+          _dp(w), float(eps), _dp(xq), _dp(ascale), seq, K, _stream(stream))
+
+
+def rowop_linear_i8_fits(op: int, seq: int, K: int) -> bool:
+    """Whether rowop_linear_i8_dev supports this row op and shape."""
+    return bool(lib().vla_rowop_linear_i8_fits(op, seq, K))
+
+
+def rowop_linear_i8_dev(out, op, x, Wq, wscale, bias, u=None, w=None, eps=0.0, act=0, accumulate=0,
+                        stream=None):
+    """out (+)= the int8 linear of op(x) (rowop_quantize_i8_panel_dev, then
+    dense_linear_i8_panel_dev) in one kernel; out [seq, N] must not overlap x or u."""
+    seq, K = x.shape
+    N = Wq.shape[0]
+    _call("vla_rowop_linear_i8_dev", _dp(out), out.stride(0), op, _dp(x), x.stride(0), _dp(u),
+          u.stride(0) if u is not None else 0, _dp(w), float(eps), _dp(Wq), Wq.stride(0), _dp(wscale),
+          _dp(bias), seq, N, K, act, accumulate, _stream(stream))
 
 
 def gemm_i8_i32_dev(acc, xq, Wq, K, stream=None):

@@ -286,6 +286,62 @@ VLA_API int32_t vla_dense_linear_i8_panel_dev(float* out, int32_t ldo, const int
     });
 }
 
+static RowQArgs rowop_args(int32_t op, const float* x, int32_t ldx, const float* u, int32_t ldu,
+                           const float* w, float eps, int32_t seq, int32_t K) {
+    VLA_REQUIRE(op == 0 || op == 2 || op == 3, "row op must be 0 (identity), 2 (RMSNorm) or 3 (silu_gate)");
+    RowQArgs r;
+    r.op = op;
+    r.x = x;
+    r.ldx = ldx;
+    r.u = op == 3 ? u : nullptr;
+    r.ldu = ldu;
+    r.w = op == 2 ? w : nullptr;
+    r.eps = eps;
+    r.rows = seq;
+    r.H = K;
+    return r;
+}
+
+VLA_API int32_t vla_rowop_quantize_i8_panel_dev(int32_t op, const float* x, int32_t ldx, const float* u,
+                                                int32_t ldu, const float* w, float eps, int8_t* xq,
+                                                float* ascale, int32_t seq, int32_t K, void* stream) {
+    return guarded("vla_rowop_quantize_i8_panel_dev", [&] {
+        RowQArgs r = rowop_args(op, x, ldx, u, ldu, w, eps, seq, K);
+        VLA_REQUIRE(xq && ascale && seq >= 0 && seq <= kPanelMaxRows, "need xq, ascale and seq in [0, 128]");
+        r.q = xq;
+        r.qs = ascale;
+        r.q_panel = 1;
+        launch_rowq(r, as_stream(stream));
+    });
+}
+
+VLA_API int32_t vla_rowop_linear_i8_fits(int32_t op, int32_t seq, int32_t K) {
+    return rowop_gemm_fits(op, seq, K) ? 1 : 0;
+}
+
+VLA_API int32_t vla_rowop_linear_i8_dev(float* out, int32_t ldo, int32_t op, const float* x, int32_t ldx,
+                                        const float* u, int32_t ldu, const float* w, float eps,
+                                        const int8_t* Wq, int32_t ldw, const float* wscale, const float* bias,
+                                        int32_t seq, int32_t N, int32_t K, int32_t act, int32_t accumulate,
+                                        void* stream) {
+    return guarded("vla_rowop_linear_i8_dev", [&] {
+        const RowQArgs r = rowop_args(op, x, ldx, u, ldu, w, eps, seq, K);
+        GemmArgs a{};
+        a.B = Wq;
+        a.ldb = ldw;
+        a.wscale = wscale;
+        a.bias = bias;
+        a.out = out;
+        a.ldo = ldo;
+        a.M = seq;
+        a.N = N;
+        a.K = K;
+        a.act = act;
+        a.accumulate = accumulate;
+        launch_gemm_i8_rowop(r, a, as_stream(stream));
+    });
+}
+
 VLA_API int32_t vla_gemm_i8_i32_dev(int32_t* acc, const int8_t* xq, int32_t ldx, const int8_t* Wq,
                                     int32_t ldw, int32_t seq, int32_t N, int32_t K, void* stream) {
     return guarded("vla_gemm_i8_i32_dev", [&] {

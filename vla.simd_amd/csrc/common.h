@@ -142,6 +142,17 @@ struct RowQArgs {
 };
 void launch_rowq(const RowQArgs& a, hipStream_t st);
 
+// A skinny int8 GEMM that builds its own activations: every block applies the
+// row op of `r` (op 0 identity, 2 RMSNorm or 3 silu_gate; no add, no fp32 out)
+// to the fp32 rows, quantizes them per row into LDS (panel layout) exactly as
+// launch_rowq would, and multiplies by g's int8 weights. g: B, ldb, wscale,
+// bias, out, ldo, M (= r.rows), N, K (= r.H), act, accumulate (A, lda, ascale,
+// acc32, a_panel unused); out must not overlap the rows read. rowop_gemm_fits
+// says whether op and shape are supported (M <= 128, K % 4 == 0, K <= 2048,
+// the panel within LDS).
+bool rowop_gemm_fits(int op, int M, int K);
+void launch_gemm_i8_rowop(const RowQArgs& r, const GemmArgs& g, hipStream_t st);
+
 // RoPE-NeoX from a cos/sin table cs[(t * head_dim/2 + i) * 2 + {0, 1}]
 // (double; rope_cos_sin in graph.h builds it the way rope_neox does)
 void launch_rope_table(float* x, int ld, const double* cs, int seq, int n_heads, int head_dim,

@@ -18,6 +18,7 @@
 #include "act.h"
 #include "common.h"
 #include "quant_row.h"
+#include "rowop.h"
 
 namespace vla {
 namespace hip {
@@ -154,78 +155,9 @@ __global__ __launch_bounds__(256) void rowq_kernel(RowQArgs a) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= a.rows) return;  // wave-uniform
     const int H = a.H;
-    const float* xr = a.x + (size_t)row * a.ldx;
     float4 y[NV];
-#pragma unroll
-    for (int i = 0; i < NV; i++) {
-        const int k = 4 * lane + 256 * i;
-        y[i] = k < H ? *reinterpret_cast<const float4*>(xr + k) : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    if (OP == 1) {
-        double s = 0.0;
-#pragma unroll
-        for (int i = 0; i < NV; i++)
-            s += ((double)y[i].x + (double)y[i].y) + ((double)y[i].z + (double)y[i].w);
-        const double mean = wave_sum(s) / H;
-        double v = 0.0;
-#pragma unroll
-        for (int i = 0; i < NV; i++)
-            if (4 * lane + 256 * i < H) {
-                const double d0 = (double)y[i].x - mean, d1 = (double)y[i].y - mean;
-                const double d2 = (double)y[i].z - mean, d3 = (double)y[i].w - mean;
-                v += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
-            }
-        const float inv = (float)(1.0 / sqrt(wave_sum(v) / H + (double)a.eps));
-#pragma unroll
-        for (int i = 0; i < NV; i++) {
-            const int k = 4 * lane + 256 * i;
-            if (k < H) {
-                const float4 w = *reinterpret_cast<const float4*>(a.w + k);
-                float4 r;
-                if (a.b) {
-                    const float4 b = *reinterpret_cast<const float4*>(a.b + k);
-                    r.x = fmaf((float)((double)y[i].x - mean) * inv, w.x, b.x);
-                    r.y = fmaf((float)((double)y[i].y - mean) * inv, w.y, b.y);
-                    r.z = fmaf((float)((double)y[i].z - mean) * inv, w.z, b.z);
-                    r.w = fmaf((float)((double)y[i].w - mean) * inv, w.w, b.w);
-                } else {
-                    r.x = (float)((double)y[i].x - mean) * inv * w.x;
-                    r.y = (float)((double)y[i].y - mean) * inv * w.y;
-                    r.z = (float)((double)y[i].z - mean) * inv * w.z;
-                    r.w = (float)((double)y[i].w - mean) * inv * w.w;
-                }
-                y[i] = r;
-            }
-        }
-    } else if (OP == 2) {
-        double ss = 0.0;
-#pragma unroll
-        for (int i = 0; i < NV; i++) {
-            const double d0 = y[i].x, d1 = y[i].y, d2 = y[i].z, d3 = y[i].w;
-            ss += (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
-        }
-        const float inv = (float)(1.0 / sqrt(wave_sum(ss) / H + (double)a.eps));
-#pragma unroll
-        for (int i = 0; i < NV; i++) {
-            const int k = 4 * lane + 256 * i;
-            if (k < H) {
-                const float4 w = *reinterpret_cast<const float4*>(a.w + k);
-                y[i] = make_float4(y[i].x * inv * w.x, y[i].y * inv * w.y, y[i].z * inv * w.z,
-                                   y[i].w * inv * w.w);
-            }
-        }
-    } else if (OP == 3) {
-        const float* ur = a.u + (size_t)row * a.ldu;
-#pragma unroll
-        for (int i = 0; i < NV; i++) {
-            const int k = 4 * lane + 256 * i;
-            if (k < H) {
-                const float4 u = *reinterpret_cast<const float4*>(ur + k);
-                y[i] = make_float4(act_silu_gate(y[i].x, u.x), act_silu_gate(y[i].y, u.y),
-                                   act_silu_gate(y[i].z, u.z), act_silu_gate(y[i].w, u.w));
-            }
-        }
-    }
+    rowop_apply<OP, NV>(y, a.x + (size_t)row * a.ldx, OP == 3 ? a.u + (size_t)row * a.ldu : nullptr, a.w, a.b,
+                        a.eps, H, lane);
 
     // y -> out (fp32) and q (int8); then y + add -> out2 and q2
 #pragma unroll
@@ -253,14 +185,7 @@ __global__ __launch_bounds__(256) void rowq_kernel(RowQArgs a) {
             }
         }
         if (q) {
-            float amax = 0.0f;
-#pragma unroll
-            for (int i = 0; i < NV; i++)
-                if (4 * lane + 256 * i < H)
-                    amax = fmaxf(amax, fmaxf(fmaxf(fabsf(y[i].x), fabsf(y[i].y)),
-                                             fmaxf(fabsf(y[i].z), fabsf(y[i].w))));
-            amax = wave_max_f32(amax);
-            const float s = row_scale(amax);
+            const float s = rowop_scale<NV>(y, H, lane);
             const float inv = 1.0f / s;
             if (lane == 0) (pass ? a.qs2 : a.qs)[row] = s;
             if (a.q_panel) {

@@ -58,6 +58,7 @@
 
 #include "act.h"
 #include "common.h"
+#include "rowop.h"
 
 #include <cstdio>
 #include <cstdlib>
@@ -846,6 +847,169 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
     }
 }
 
+// ------------------------------------------------------- row op + skinny --
+
+// Rows the fused row-op GEMM below computes: M rounded up to 16, 32, 64 or 128
+// (16 x its FM template value); the LDS it needs for K: the quantized panel
+// [K64 / 64][rows][64] or, after the product, the 16 waves' int32 partial
+// tiles (16 x FM KiB), whichever is larger, then the rows' scales.
+__host__ __device__ inline int rowop_fm(int M) { return M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : 8; }
+__host__ __device__ inline int rowop_lds_main(int fm, int K) {
+    const int panel = 16 * fm * ((K + 63) & ~63), part = 16 * fm * 1024;
+    return panel > part ? panel : part;
+}
+constexpr int kRowopMaxLds = 160 * 1024;
+
+// gemm_i8_skinny with its activations built in the block (launch_gemm_i8_rowop):
+// each block first loads its weight chunks (16 output columns; the 16 waves
+// take interleaved 64-byte k-steps, at most two each for K <= 2048), so their
+// latency hides under the row op; then wave w applies the row op to rows
+// w, w + 16, ... (RB rows in flight, their reductions interleaved), quantizes
+// each row exactly as rowq_kernel does (same functions, same order) into the
+// LDS panel, and keeps its scale in LDS. After a barrier each wave multiplies
+// its k-steps of the panel by its weight chunks; the partial tiles reuse the
+// panel's LDS and are summed as in gemm_i8_skinny. Panel rows past M and
+// panel bytes past K are never written: the former only reach discarded
+// outputs, the latter meet weight bytes masked to zero.
+template <int OP, int NV, int FM>
+__global__ __launch_bounds__(1024) void gemm_i8_rowop(RowQArgs r, GemmArgs a) {
+    constexpr int WAVES = 16, NT = WAVES * 64, MP = 16 * FM;
+    // rows in flight per wave: at most 4, and 16 float4 per lane, within 128
+    // VGPRs. (LayerNorm's double statistics spill at this thread count: op 1
+    // stays on rowq_kernel + gemm_i8_skinny.)
+    static_assert(OP != 1, "LayerNorm is not fused");
+    constexpr int RB = FM < (16 / NV > 4 ? 4 : 16 / NV) ? FM : (16 / NV > 4 ? 4 : 16 / NV);
+    static_assert(FM % RB == 0, "row batches must tile the wave's rows");
+    extern __shared__ __attribute__((aligned(16))) int8_t lds[];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int M = a.M, K = a.K, n0 = blockIdx.x * 16;
+    const int ns = (K + 63) >> 6, full = K >> 6;
+    int8_t* panel = lds;
+    int32_t* part = reinterpret_cast<int32_t*>(lds);
+    float* sa = reinterpret_cast<float*>(lds + rowop_lds_main(FM, K));
+
+    // this wave's weight chunks: k-steps wave and wave + 16 (the last one
+    // masked to zero past K)
+    const int r16 = lane & 15, kq = (lane >> 4) * 16;
+    const int n = n0 + r16 < a.N ? n0 + r16 : a.N - 1;
+    const int8_t* brow = a.B + (size_t)n * a.ldb;
+    v4i rb[2];
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+        const int step = wave + WAVES * s;
+        rb[s] = v4i{0, 0, 0, 0};
+        if (step < full) rb[s] = *reinterpret_cast<const v4i*>(brow + step * 64 + kq);
+        else if (step < ns) rb[s] = load_chunk<true>(brow, step * 64 + kq, K);
+    }
+
+    // epilogue operands of the outputs this thread stores (as gemm_i8_skinny)
+    constexpr int EPT = (FM * 256 + NT - 1) / NT;
+    float ews[EPT], eb[EPT], eold[EPT];
+#pragma unroll
+    for (int j = 0; j < EPT; j++) {
+        const int e = tid + j * NT;
+        const int l = e & 63, rr = (e >> 6) & 3, i = e >> 8;
+        int mm = 16 * i + 4 * (l >> 4) + rr, nn = n0 + (l & 15);
+        const bool ok = e < FM * 256 && mm < M && nn < a.N;
+        mm = ok ? mm : 0;
+        nn = ok ? nn : 0;
+        ews[j] = a.wscale[nn];
+        eb[j] = a.bias ? a.bias[nn] : 0.0f;
+        eold[j] = a.accumulate && ok ? a.out[(size_t)mm * a.ldo + nn] : 0.0f;
+    }
+
+    // row op + quantize into the panel
+    StaticFor<0, FM / RB>::run([&](auto bc) {
+        constexpr int j0 = decltype(bc)::value * RB;
+        float4 y[RB][NV];
+        int row[RB];
+        RowStat st[RB];
+        float am[RB];
+        StaticFor<0, RB>::run([&](auto jc) {
+            constexpr int jj = decltype(jc)::value;
+            row[jj] = wave + WAVES * (j0 + jj);
+            const int rc = row[jj] < M ? row[jj] : M - 1;  // rows past M: a duplicate, never stored
+            rowop_load<NV>(y[jj], r.x + (size_t)rc * r.ldx, K, lane);
+        });
+        StaticFor<0, RB>::run([&](auto jc) {
+            constexpr int jj = decltype(jc)::value;
+            st[jj] = rowop_stat<OP, NV>(y[jj], r.eps, K, lane);
+        });
+        StaticFor<0, RB>::run([&](auto jc) {
+            constexpr int jj = decltype(jc)::value;
+            const int rc = row[jj] < M ? row[jj] : M - 1;
+            rowop_finish<OP, NV>(y[jj], st[jj], OP == 3 ? r.u + (size_t)rc * r.ldu : nullptr, r.w, r.b, K,
+                                 lane);
+            am[jj] = rowop_amax<NV>(y[jj], K, lane);
+        });
+        StaticFor<0, RB>::run([&](auto jc) {
+            constexpr int jj = decltype(jc)::value;
+            am[jj] = wave_max_f32(am[jj]);
+        });
+        StaticFor<0, RB>::run([&](auto jc) {
+            constexpr int jj = decltype(jc)::value;
+            if (row[jj] < M) {
+                const float s = row_scale(am[jj]);
+                const float inv = 1.0f / s;
+                if (lane == 0) sa[row[jj]] = s;
+                int8_t* qr = panel + row[jj] * 64;
+#pragma unroll
+                for (int i = 0; i < NV; i++) {
+                    const int k = 4 * lane + 256 * i;
+                    if (k < K) *reinterpret_cast<uint32_t*>(qr + (k >> 6) * (MP * 64) + (k & 63)) = q8x4(y[jj][i], inv);
+                }
+            }
+        });
+    });
+    __syncthreads();
+
+    v4i acc[FM];
+#pragma unroll
+    for (int i = 0; i < FM; i++) acc[i] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int s = 0; s < 2; s++) {
+        const int step = wave + WAVES * s;
+        if (step < ns) {
+            const int8_t* ap = panel + step * (MP * 64) + r16 * 64 + kq;
+            v4i av[FM];
+#pragma unroll
+            for (int i = 0; i < FM; i++) av[i] = *reinterpret_cast<const v4i*>(ap + i * 1024);
+#pragma unroll
+            for (int i = 0; i < FM; i++) acc[i] = mfma_i8(av[i], rb[s], acc[i]);
+        }
+    }
+    __syncthreads();  // the panel's LDS becomes the partial tiles
+    const int nw = ns < WAVES ? ns : WAVES;  // waves that hold a k-step
+    if (wave < nw) {
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) part[((wave * FM + i) * 4 + q) * 64 + lane] = acc[i][q];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < EPT; j++) {
+        const int e = tid + j * NT;
+        if (e >= FM * 256) break;
+        int32_t v = 0;
+        for (int w = 0; w < nw; w++) v += part[w * FM * 256 + e];
+        const int l = e & 63, rr = (e >> 6) & 3, i = e >> 8;
+        const int mm = 16 * i + 4 * (l >> 4) + rr, nn = n0 + (l & 15);
+        if (mm >= M || nn >= a.N) continue;
+        const float p = (float)v * ews[j];
+        float o = fmaf(p, sa[mm], eb[j]);
+        switch (a.act) {
+        case 1: o = act_relu(o); break;
+        case 2: o = act_gelu_tanh(o); break;
+        case 3: o = act_gelu_erf(o); break;
+        default: break;
+        }
+        a.out[(size_t)mm * a.ldo + nn] = a.accumulate ? eold[j] + o : o;
+    }
+}
+
 // --------------------------------------------------------------- generic --
 
 __global__ __launch_bounds__(256) void gemm_i8_generic(GemmArgs a) {
@@ -956,6 +1120,41 @@ void run_skinny(const GemmArgs& a, hipStream_t st) {
     VLA_LAUNCH_CHECK();
 }
 
+template <int OP, int NV, int FM>
+void run_rowop(const RowQArgs& r, const GemmArgs& a, hipStream_t st) {
+    static const bool attr = [] {
+        VLA_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_i8_rowop<OP, NV, FM>),
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, kRowopMaxLds));
+        return true;
+    }();
+    (void)attr;
+    const int lds = rowop_lds_main(FM, a.K) + 16 * FM * 4;
+    gemm_i8_rowop<OP, NV, FM><<<(a.N + 15) / 16, 1024, lds, st>>>(r, a);
+    VLA_LAUNCH_CHECK();
+}
+
+template <int OP, int NV>
+void run_rowop_fm(const RowQArgs& r, const GemmArgs& a, hipStream_t st) {
+    switch (rowop_fm(a.M)) {
+    case 1: run_rowop<OP, NV, 1>(r, a, st); break;
+    case 2: run_rowop<OP, NV, 2>(r, a, st); break;
+    case 4: run_rowop<OP, NV, 4>(r, a, st); break;
+    default:
+        if constexpr (NV <= 4) run_rowop<OP, NV, 8>(r, a, st);
+        else throw ArgError("gemm_i8_rowop: 128 rows need K <= 1024");
+        break;
+    }
+}
+
+template <int OP>
+void run_rowop_nv(const RowQArgs& r, const GemmArgs& a, hipStream_t st) {
+    const int nv = (a.K + 255) / 256;
+    if (nv <= 1) run_rowop_fm<OP, 1>(r, a, st);
+    else if (nv <= 2) run_rowop_fm<OP, 2>(r, a, st);
+    else if (nv <= 4) run_rowop_fm<OP, 4>(r, a, st);
+    else run_rowop_fm<OP, 8>(r, a, st);
+}
+
 // Tile of the aligned kernel: the largest that still gives every CU a tile,
 // or VLA_HIP_GEMM_TILE=<BM>x<BN>x<BK> to force one (A/B runs; the values do
 // not change, only the schedule).
@@ -1051,6 +1250,43 @@ void launch_gemm_i8(const GemmArgs& a, hipStream_t st) {
         return;
     }
     dispatch_tile(pick_tile(a.M, a.N, a.K), a, st);
+}
+
+bool rowop_gemm_fits(int op, int M, int K) {
+    if (op == 1 || op < 0 || op > 3) return false;
+    if (M < 1 || M > kPanelMaxRows || K < 4 || K % 4 || K > 2048) return false;
+    const int fm = rowop_fm(M);
+    return rowop_lds_main(fm, K) + 16 * fm * 4 <= kRowopMaxLds;
+}
+
+static bool ranges_overlap(const void* p, size_t pn, const void* q, size_t qn) {
+    const char *a = static_cast<const char*>(p), *b = static_cast<const char*>(q);
+    return a < b + qn && b < a + pn;
+}
+
+void launch_gemm_i8_rowop(const RowQArgs& r, const GemmArgs& a, hipStream_t st) {
+    VLA_REQUIRE(r.op == 0 || r.op == 2 || r.op == 3, "gemm_i8_rowop: the fused row ops are 0, 2 and 3");
+    VLA_REQUIRE(r.rows == a.M && r.H == a.K, "gemm_i8_rowop: the row op's rows and width must be M and K");
+    VLA_REQUIRE(rowop_gemm_fits(r.op, a.M, a.K),
+                "gemm_i8_rowop: need 1 <= M <= 128, K a multiple of 4 in [4, 2048] and the panel within LDS");
+    VLA_REQUIRE(!r.out && !r.add && !r.out2 && !r.q2, "gemm_i8_rowop: the fused row op has no fp32 or second output");
+    VLA_REQUIRE(r.x && r.ldx >= a.K && r.ldx % 4 == 0 && aligned(r.x, 16),
+                "gemm_i8_rowop: x rows must be 16-byte aligned");
+    VLA_REQUIRE(r.op == 0 || r.op == 3 || (r.w && aligned(r.w, 16) && (!r.b || aligned(r.b, 16))),
+                "gemm_i8_rowop: norm weights must be 16-byte aligned");
+    VLA_REQUIRE(r.op != 3 || (r.u && r.ldu >= a.K && r.ldu % 4 == 0 && aligned(r.u, 16)),
+                "gemm_i8_rowop: silu_gate needs 16-byte aligned u rows");
+    VLA_REQUIRE(a.N > 0 && a.K <= kMaxI8K && a.B && a.ldb >= kpad4(a.K) && a.ldb % 16 == 0 && aligned(a.B, 16),
+                "gemm_i8_rowop: weights must be 16-byte aligned rows of stride >= i8_kpad(K)");
+    VLA_REQUIRE(a.out && a.wscale && a.ldo >= a.N && !a.acc32, "gemm_i8_rowop: needs out, wscale and ldo >= N");
+    VLA_REQUIRE(a.act >= 0 && a.act <= 3, "gemm_i8_rowop: unknown activation");
+    const size_t ob = ((size_t)(a.M - 1) * a.ldo + a.N) * sizeof(float);
+    VLA_REQUIRE(!ranges_overlap(a.out, ob, r.x, ((size_t)(a.M - 1) * r.ldx + a.K) * sizeof(float)) &&
+                    (r.op != 3 || !ranges_overlap(a.out, ob, r.u, ((size_t)(a.M - 1) * r.ldu + a.K) * sizeof(float))),
+                "gemm_i8_rowop: out must not overlap the rows the row op reads");
+    if (r.op == 0) run_rowop_nv<0>(r, a, st);
+    else if (r.op == 2) run_rowop_nv<2>(r, a, st);
+    else run_rowop_nv<3>(r, a, st);
 }
 
 }  // namespace hip

@@ -79,6 +79,59 @@ void quantize(const Ctx& c, const QAct& dst, const float* x, int ldx, int seq, i
     else launch_quantize_rows(x, ldx, dst.q, dst.ld, dst.s, seq, K, c.st);
 }
 
+static GemmArgs gemm_args(const DLinear& L, float* out, int ldo, int seq, int act, int acc, int n0, int n1) {
+    const vla_linear_i8& q = *L.q8;
+    GemmArgs a{};
+    a.B = q.Wq() + (size_t)n0 * q.ldw();
+    a.ldb = q.ldw();
+    a.wscale = q.wscale() + n0;
+    a.bias = q.bias() ? q.bias() + n0 : nullptr;
+    a.out = out;
+    a.ldo = ldo;
+    a.M = seq;
+    a.N = n1 - n0;
+    a.K = L.K;
+    a.act = act;
+    a.accumulate = acc;
+    return a;
+}
+
+// Whether linear() runs a row op inside the GEMM. Every block of the fused
+// kernel applies the row op to all rows (about 1000 VALU cycles per 720-wide
+// RMSNorm row and SIMD, 3x that for a 2048-wide silu_gate row), so the fused
+// kernel beats row kernel + GEMM only while each SIMD has a row or so: on
+// MI355X at 16 rows it saved 4 us of 9.7 (RMSNorm, N = 4096, K = 720); at 50
+// rows it lost 3 us (RMSNorm, N = 4096) to 22 us (silu_gate, K = 2048).
+// VLA_HIP_ROWOP_FUSE=0 turns it off.
+constexpr int kRowopFuseMaxRows = 16;
+
+static bool fuse_rowop(int op, int seq, int K) {
+    static const bool on = [] {
+        const char* e = std::getenv("VLA_HIP_ROWOP_FUSE");
+        return !(e && e[0] == '0');
+    }();
+    return on && seq <= kRowopFuseMaxRows && rowop_gemm_fits(op, seq, K);
+}
+
+static bool overlaps(const float* p, size_t pn, const float* q, size_t qn) {
+    return p < q + qn && q < p + pn;
+}
+
+// Runs the row op r inside the GEMM when the fused kernel takes this shape.
+static bool try_rowop_gemm(const Ctx& c, const DLinear& L, const RowQArgs& r, float* out, int ldo, int seq,
+                           int act, int acc, int n0, int n1) {
+    if (!fuse_rowop(r.op, seq, L.K) || L.q8->ldw() % 16) return false;
+    const size_t on = (size_t)(seq - 1) * ldo + (n1 - n0);
+    if (overlaps(out, on, r.x, (size_t)(seq - 1) * r.ldx + L.K)) return false;
+    if (r.op == 3 && overlaps(out, on, r.u, (size_t)(seq - 1) * r.ldu + L.K)) return false;
+    RowQArgs f = r;
+    f.q = nullptr;
+    f.qs = nullptr;
+    f.q_panel = 0;
+    launch_gemm_i8_rowop(f, gemm_args(L, out, ldo, seq, act, acc, n0, n1), c.st);
+    return true;
+}
+
 static void gemm_q(const Ctx& c, const DLinear& L, const QAct& x, float* out, int ldo, int seq, int act,
                    int acc, int n0, int n1) {
     const vla_linear_i8& q = *L.q8;
@@ -110,10 +163,25 @@ void linear(const Ctx& c, const DLinear& L, const In& in, float* out, int ldo, i
     if (L.int8()) {
         VLA_REQUIRE(alpha == 1.0f, "linear: the int8 epilogue accumulates with alpha = 1 only");
         VLA_REQUIRE(act <= 3, "linear: the int8 epilogue has no silu");
-        if (in.quantized) {
+        if (in.deferred) {
+            VLA_REQUIRE(in.r.rows == seq && in.r.H == L.K && in.q.ld == L.ldq(),
+                        "linear: deferred row op made for another layer or row count");
+            if (try_rowop_gemm(c, L, in.r, out, ldo, seq, act, acc, n0, n1)) return;
+            launch_rowq(in.r, c.st);
+            gemm_q(c, L, in.q, out, ldo, seq, act, acc, n0, n1);
+        } else if (in.quantized) {
             gemm_q(c, L, in.q, out, ldo, seq, act, acc, n0, n1);
         } else {
             VLA_REQUIRE(in.f, "linear: no input");
+            if (seq <= kRowopFuseMaxRows && in.ldf % 4 == 0 && (reinterpret_cast<uintptr_t>(in.f) & 15) == 0) {
+                RowQArgs r;  // identity row op: quantize_rows_panel's bytes and scales
+                r.op = 0;
+                r.x = in.f;
+                r.ldx = in.ldf;
+                r.rows = seq;
+                r.H = L.K;
+                if (try_rowop_gemm(c, L, r, out, ldo, seq, act, acc, n0, n1)) return;
+            }
             const QAct s0 = c.slot(0, L.ldq(), seq);
             quantize(c, s0, in.f, in.ldf, seq, L.K);
             gemm_q(c, L, s0, out, ldo, seq, act, acc, n0, n1);
@@ -141,6 +209,12 @@ In rowop_for(const Ctx& c, const DLinear& L, RowQArgs r, float* f, int ldf, int 
     }
     in.f = f;
     in.ldf = ldf;
+    if (L.int8() && !f && !r.add && fuse_rowop(r.op, r.rows, L.K)) {
+        in.quantized = false;
+        in.deferred = true;
+        in.r = r;
+        return in;
+    }
     launch_rowq(r, c.st);
     return in;
 }

@@ -100,21 +100,27 @@ struct Ctx {
 };
 
 // The input of a linear layer: fp32 rows, or rows already quantized for it
-// (q.ld == the layer's ldq()).
+// (q.ld == the layer's ldq()), or a row op not yet run (deferred: r, whose
+// q / qs name the slot it quantizes into when it runs on its own).
 struct In {
     const float* f = nullptr;
     int ldf = 0;
-    QAct q;               // valid when quantized
+    QAct q;               // valid when quantized or deferred
     bool quantized = false;
+    bool deferred = false;
+    RowQArgs r;
 };
 
 // x [seq, K] (row stride ldx) -> dst
 void quantize(const Ctx& c, const QAct& dst, const float* x, int ldx, int seq, int K);
 
 // out[:, n0:n1] (+)= act(x W[n0:n1]^T + b). An int8 layer takes in.q when
-// in.quantized, else quantizes in.f into slot 0. acc != 0 adds into out
-// (fmaf(alpha, v, out) for fp32 layers; the int8 epilogue adds v, alpha must
-// be 1).
+// in.quantized, else quantizes in.f into slot 0; a deferred row op, or the
+// quantization of fp32 rows, runs inside the GEMM (gemm_i8_rowop) for at most
+// 16 rows when the shape allows it (K <= 2048, out apart from the rows read;
+// VLA_HIP_ROWOP_FUSE=0 turns this off), else on its own first: the values
+// are the same either way. acc != 0 adds into out (fmaf(alpha, v, out)
+// for fp32 layers; the int8 epilogue adds v, alpha must be 1).
 void linear(const Ctx& c, const DLinear& L, const In& in, float* out, int ldo, int seq, int act = 0,
             int acc = 0, int n0 = 0, int n1 = -1, float alpha = 1.0f);
 inline void linear(const Ctx& c, const DLinear& L, float* out, int ldo, const float* x, int ldx,
@@ -127,7 +133,9 @@ inline void linear(const Ctx& c, const DLinear& L, float* out, int ldo, const fl
 
 // A row op (RowQArgs op / x / u / w / b / eps / rows / H) whose result feeds
 // layer L: an int8 L gets it quantized in the same kernel, into `slot` (and
-// fp32 rows into f when f is non-null); an fp32 L gets fp32 rows in f.
+// fp32 rows into f when f is non-null); an fp32 L gets fp32 rows in f. For an
+// int8 L without f, the op may be deferred to the linear() call that takes
+// the returned In (the rows it reads must not change in between).
 In rowop_for(const Ctx& c, const DLinear& L, RowQArgs r, float* f, int ldf, int slot);
 
 // Which keys a query may see (AttnArgs' mask fields): kind 0 none, 1 dense
