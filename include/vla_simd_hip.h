@@ -314,10 +314,37 @@ VLA_API int32_t vla_dense_linear_dev(float* out, int32_t ldo, const float* x, in
                                      int32_t N, int32_t K, int32_t act, int32_t accumulate,
                                      float alpha, void* stream);
 
+/* ------------------------------------------------------ checkpoint files -- */
+/* The files of a model path, as the policy loaders below read them: a
+ * converted directory (<dir>/<name>.meta / .bin), or a vla.simd GGUF that
+ * carries them (replaces src/io/files.h:8-17 Mount + InFile with the mount rule
+ * of files.cpp find_gguf, and src/io/gguf.cpp + gguf_vla_simd.cpp:29-77 for the
+ * format tools/_gguf.py:6-28 writes). A path is a GGUF when it is a *.gguf
+ * file, or a directory holding exactly one *.gguf and no *.meta; files the
+ * GGUF does not carry are read from disk beside it. vla_ckpt_open returns NULL
+ * (vla_last_error()) for a GGUF that is malformed, of another architecture or
+ * format version, or names an embedded file outside the model directory.
+ * No GPU is used. */
+typedef struct vla_ckpt vla_ckpt;
+VLA_API vla_ckpt* vla_ckpt_open(const char* path);
+VLA_API void vla_ckpt_free(vla_ckpt* c);
+/* 1 when the path mounted as a GGUF, 0 for a directory */
+VLA_API int32_t vla_ckpt_is_gguf(const vla_ckpt* c);
+/* bytes of file `rel` (GGUF, else disk beside it); -1 when there is none */
+VLA_API int64_t vla_ckpt_file_size(const vla_ckpt* c, const char* rel);
+/* copies file `rel` into buf (cap >= its size); returns a vla_status */
+VLA_API int32_t vla_ckpt_read(const vla_ckpt* c, const char* rel, void* buf, int64_t cap);
+/* the names of the files the GGUF carries, sorted, '\n'-separated and
+ * NUL-terminated into buf when cap is large enough; returns the length
+ * needed including the NUL (1 for a directory), or -1 on a null handle */
+VLA_API int64_t vla_ckpt_names(const vla_ckpt* c, char* buf, int64_t cap);
+
 /* ------------------------------------------------ device policy graphs ---- */
 /* The reference's transformer graphs with every linear, attention, norm and
  * activation on the device and the whole pass replayed as one HIP graph. Each
- * loader reads the reference's own checkpoint files and takes the int8 mask
+ * loader reads the reference's own checkpoint files -- from a directory or a
+ * vla.simd GGUF, as vla_ckpt_open mounts it (`dir` may name either) -- and
+ * takes the int8 mask
  * its model reads from the environment (ACT_INT8 / OCTO_INT8 / SMOLVLA_INT8):
  * the selected layers are quantized once on the device with the
  * pack_weights_i8 formula, the rest stay fp32. NULL on failure

@@ -349,8 +349,26 @@ def _ref_models():
     L.ref_smolvla_chunk.argtypes, L.ref_smolvla_chunk.restype = [P, P, P, i, P, P], i
     L.ref_smolvla_chunk_len.argtypes, L.ref_smolvla_chunk_len.restype = [P], i
     L.ref_smolvla_max_action_dim.argtypes, L.ref_smolvla_max_action_dim.restype = [P], i
+    L.ref_mount_read.argtypes = [ctypes.c_char_p, ctypes.c_char_p, P, ctypes.c_longlong]
+    L.ref_mount_read.restype = ctypes.c_longlong
     L._models_declared = True
     return L
+
+
+def ref_mount_read(path, rel):
+    """The bytes of <path>/<rel> through the reference's own model-file layer
+    (io::Mount + io::InFile: a vla.simd GGUF's embedded file, else the file on
+    disk). None when there is no such file; raises when the path does not
+    mount (a GGUF the reference rejects)."""
+    L = _ref_models()
+    n = L.ref_mount_read(str(path).encode(), rel.encode(), None, 0)
+    if n == -2:
+        raise ValueError(f"reference mount failed for {path}")
+    if n < 0:
+        return None
+    buf = ctypes.create_string_buffer(max(int(n), 1))
+    L.ref_mount_read(str(path).encode(), rel.encode(), ctypes.cast(buf, c_void_p), n)
+    return buf.raw[:n]
 
 
 class RefAct:

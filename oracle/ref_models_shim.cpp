@@ -10,6 +10,9 @@
  *
  * Beyond forwarding, this file does what the reference's model classes do
  * around the graphs and that the tests need without images or tokenizers:
+ *   - the io::Mount of the model path (act_model.cpp:23, octo_model.cpp:66,
+ *     smolvla_model.cpp:54), so a vla.simd GGUF loads through the reference's
+ *     own reader; ref_mount_read exposes that reader's bytes for one file;
  *   - the OCTO_INT8 / SMOLVLA_INT8 per-layer init_int8 calls of
  *     OctoModel::apply_int8 (src/models/octo/octo_model.cpp:104-140) and
  *     SmolvlaModel::apply_int8 (src/models/smolvla/smolvla_model.cpp:111-155),
@@ -18,12 +21,16 @@
  *     SmolvlaModel::predict_normalized (smolvla_model.cpp:252-275) built from a
  *     pad vector, so the chunk starts from given prefix embeddings.
  */
+#include "io/files.h"
 #include "models/act/act_transformer.h"
 #include "models/octo/octo_transformer.h"
 #include "models/smolvla/action_expert.h"
 #include "models/smolvla/smollm2_lm.h"
 
 #include <cstdint>
+#include <cstring>
+#include <iterator>
+#include <string>
 #include <cstdio>
 #include <exception>
 #include <limits>
@@ -35,6 +42,8 @@ using namespace tcpu;
 
 REF_API void* ref_act_load(const char* dir, int img_ch, int int8_mask) {
     try {
+        const io::Mount mount(dir);
+        if (!mount.ok()) return nullptr;
         auto* t = new ActTransformer();
         if (!t->load(dir, img_ch, int8_mask)) {
             delete t;
@@ -44,6 +53,25 @@ REF_API void* ref_act_load(const char* dir, int img_ch, int int8_mask) {
     } catch (const std::exception& e) {
         std::fprintf(stderr, "ref_act_load: %s\n", e.what());
         return nullptr;
+    }
+}
+
+/* The bytes of <path>/<rel> as the reference's loaders see them (a mounted
+ * GGUF's generated file, else the file on disk): the size, or -1 when there
+ * is no such file, -2 when the path does not mount; copies min(size, cap). */
+REF_API long long ref_mount_read(const char* path, const char* rel, char* buf, long long cap) {
+    try {
+        const io::Mount mount(path);
+        if (!mount.ok()) return -2;
+        io::InFile f(std::string(path) + "/" + rel, std::ios::binary);
+        if (!f) return -1;
+        std::string all((std::istreambuf_iterator<char>(f)), std::istreambuf_iterator<char>());
+        const long long n = (long long)all.size();
+        if (buf && cap > 0) std::memcpy(buf, all.data(), (size_t)(n < cap ? n : cap));
+        return n;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "ref_mount_read: %s\n", e.what());
+        return -2;
     }
 }
 
@@ -61,6 +89,8 @@ REF_API int ref_act_forward(void* h, const float* feats, int n_cams, int fh, int
 
 REF_API void* ref_octo_load(const char* dir, int int8_mask) {
     try {
+        const io::Mount mount(dir);
+        if (!mount.ok()) return nullptr;
         auto* t = new OctoTransformer();
         if (!t->load(dir)) {
             delete t;
@@ -109,6 +139,8 @@ struct RefSmolvla {
 
 REF_API void* ref_smolvla_load(const char* dir, int int8_mask) {
     try {
+        const io::Mount mount(dir);
+        if (!mount.ok()) return nullptr;
         auto* m = new RefSmolvla();
         if (!m->vlm.load(dir) || !m->aex.load(dir)) {
             delete m;

@@ -198,3 +198,35 @@ def test_smolvla_short_chunk(vla, ckdir, mask):
     print(f"smolvla chunk 12 mask {mask}: rel err {err:.3e} (reference ulp spread {sens:.3e})", flush=True)
     assert err <= bar
     _check_replay(lambda: m.run(prefix, pad, noise), got)
+
+
+def test_models_load_from_gguf(vla, ckdir):
+    """The device graphs loaded from a vla.simd GGUF (vla_ckpt_open's mount of
+    the single-file checkpoint) give bit-identical outputs to the same graphs
+    loaded from the converted directory; tests/test_gguf.py pins the file
+    layer itself against the reference's reader."""
+    ck = _ck()
+    act = dict(ck.ACT_BASE, n_enc=2, fh=6, fw=8)
+    d, g = str(ckdir / "act_g"), str(ckdir / "act_g.gguf")
+    ck.write_act(d, act)
+    ck.write_gguf(d, g, "act")
+    feats, state = ck.act_inputs(act)
+    outs = [vla.ActTransformer(p, act["img_ch"], 31).forward(feats, 1, 6, 8, state) for p in (d, g)]
+    assert outs[0].tobytes() == outs[1].tobytes()
+
+    octo = dict(ck.OCTO_BASE, n_layers=3, repeat_task=1)
+    d, g = str(ckdir / "octo_g"), str(ckdir / "octo_g.gguf")
+    ck.write_octo(d, octo)
+    ck.write_gguf(d, g, "octo")
+    t5, sp, sw, tm = ck.octo_inputs(octo)
+    outs = [vla.OctoTransformer(p, 7).forward(t5, sp, sw, 2, tm) for p in (d, g)]
+    assert outs[0].tobytes() == outs[1].tobytes()
+
+    smol = dict(ck.SMOLVLA_BASE, n_layers=4, expert_layers=4)
+    d, g = str(ckdir / "smol_g"), str(ckdir / "smol_g.gguf")
+    ck.write_smolvla(d, smol)
+    ck.write_gguf(d, g, "smolvla", layout=ck.smolvla_gguf_layout(smol))
+    prefix, pad, noise = ck.smolvla_inputs(smol, n_pad=2)
+    outs = [vla.SmolvlaChunk(p, 48).run(prefix, pad, noise) for p in (d, g)]
+    assert outs[0].tobytes() == outs[1].tobytes()
+    print("act / octo / smolvla from GGUF: identical to the directory loads", flush=True)

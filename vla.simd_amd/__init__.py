@@ -43,6 +43,8 @@ EXPORTS = (
     "vla_dense_linear_i8_pre", "vla_dense_linear_i8", "vla_dense_linear_i8_pre_dev",
     "vla_i8_panel_bytes", "vla_quantize_act_i8_panel_dev", "vla_dense_linear_i8_panel_dev",
     "vla_rowop_quantize_i8_panel_dev", "vla_rowop_linear_i8_fits", "vla_rowop_linear_i8_dev",
+    "vla_ckpt_open", "vla_ckpt_free", "vla_ckpt_is_gguf", "vla_ckpt_file_size", "vla_ckpt_read",
+    "vla_ckpt_names",
     "vla_gemm_i8_i32", "vla_gemm_i8_i32_dev",
     "vla_linear_i8_create", "vla_linear_i8_create_q", "vla_linear_i8_free",
     "vla_linear_i8_weights", "vla_linear_i8_wscale", "vla_linear_i8_ldw",
@@ -117,6 +119,12 @@ def _declare(L):
         "vla_dense_linear_i8_panel_dev": (i32, [P, i32, P, P, P, i32, P, P, i32, i32, i32, i32, i32, P]),
         "vla_rowop_quantize_i8_panel_dev": (i32, [i32, P, i32, P, i32, P, ctypes.c_float, P, P, i32, i32, P]),
         "vla_rowop_linear_i8_fits": (i32, [i32, i32, i32]),
+        "vla_ckpt_open": (P, [c_char_p]),
+        "vla_ckpt_free": (None, [P]),
+        "vla_ckpt_is_gguf": (i32, [P]),
+        "vla_ckpt_file_size": (ctypes.c_int64, [P, c_char_p]),
+        "vla_ckpt_read": (i32, [P, c_char_p, P, ctypes.c_int64]),
+        "vla_ckpt_names": (ctypes.c_int64, [P, c_char_p, ctypes.c_int64]),
         "vla_rowop_linear_i8_dev": (i32, [P, i32, i32, P, i32, P, i32, P, ctypes.c_float, P, i32, P, P, i32,
                                           i32, i32, i32, i32, P]),
         "vla_gemm_i8_i32": (i32, [P, P, P, i32, i32, i32]),
@@ -592,6 +600,39 @@ class _Handle:
             self.close()
         except Exception:
             pass
+
+
+class CkptFiles(_Handle):
+    """The files of a model path as the policy loaders read them (vla_ckpt_*):
+    a converted directory, or a vla.simd GGUF that carries them."""
+
+    _load, _free = "vla_ckpt_open", "vla_ckpt_free"
+
+    def __init__(self, path: str):
+        super().__init__(lib().vla_ckpt_open(str(path).encode()))
+
+    @property
+    def gguf(self) -> bool:
+        return bool(lib().vla_ckpt_is_gguf(self.h))
+
+    def names(self):
+        L = lib()
+        n = L.vla_ckpt_names(self.h, None, 0)
+        buf = ctypes.create_string_buffer(int(n))
+        L.vla_ckpt_names(self.h, buf, n)
+        text = buf.value.decode()
+        return text.split("\n") if text else []
+
+    def size(self, rel: str) -> int:
+        return int(lib().vla_ckpt_file_size(self.h, rel.encode()))
+
+    def read(self, rel: str) -> bytes:
+        n = self.size(rel)
+        if n < 0:
+            raise VlaError("vla_ckpt_read", VLA_ERR_ARG, f"no file {rel}")
+        buf = ctypes.create_string_buffer(max(n, 1))
+        _call("vla_ckpt_read", self.h, rel.encode(), ctypes.cast(buf, c_void_p), n)
+        return buf.raw[:n]
 
 
 class ActTransformer(_Handle):

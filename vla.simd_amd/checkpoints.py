@@ -23,6 +23,7 @@ from __future__ import annotations
 
 import math
 import os
+import struct
 
 import numpy as np
 
@@ -231,3 +232,118 @@ def smolvla_inputs(cfg: dict = SMOLVLA_BASE, seed: int = synth.BASE_SEED, n_pad:
         pad[n - 1 - n_pad:n - 1] = 0
     noise = synth.normal("smolvla.in.noise", (cfg["chunk"], cfg["max_action_dim"]), 1.0, seed)
     return prefix, pad, noise
+
+
+# ------------------------------------------------------------ vla.simd GGUF --
+# The single-file form of a converted directory that the reference's
+# converters write (tools/_gguf.py:6-28) and its engine mounts
+# (src/io/gguf_vla_simd.cpp:29-77): GGUF v3, general.architecture "vla-simd",
+# vla_simd.format 1, every text file as the string vla_simd.file.<path>, every
+# .bin as a 1-D tensor <path> (F32 unless a layout says otherwise) or, when it
+# mixes element types, as parts <path>:0, <path>:1, ... in order; tensor data
+# 32-byte aligned.
+
+GGUF_TYPES = {"F32": (0, 4), "F16": (1, 2), "BF16": (30, 2), "I8": (24, 1), "I32": (26, 4)}
+_KV_FMT = {0: "<B", 1: "<b", 2: "<H", 3: "<h", 4: "<I", 5: "<i", 6: "<f", 7: "<?", 10: "<Q",
+           11: "<q", 12: "<d"}
+
+
+class GgufBuilder:
+    """Byte-level GGUF writer: metadata of any type, tensors with explicit dims,
+    element type and (optionally forced) offsets. write_gguf is built on it;
+    the reader tests use it to make malformed files too."""
+
+    def __init__(self, version: int = 3, align: int = 32):
+        self.version, self.align = version, align
+        self.kv, self.infos, self.blobs = [], [], []
+
+    @staticmethod
+    def _s(text) -> bytes:
+        b = text.encode("utf-8") if isinstance(text, str) else bytes(text)
+        return struct.pack("<Q", len(b)) + b
+
+    def string(self, key, value):
+        self.kv.append(self._s(key) + struct.pack("<I", 8) + self._s(value))
+
+    def scalar(self, key, gtype: int, value):
+        self.kv.append(self._s(key) + struct.pack("<I", gtype) + struct.pack(_KV_FMT[gtype], value))
+
+    def array(self, key, elem: int, values):
+        body = b"".join(self._s(v) for v in values) if elem == 8 else \
+            b"".join(struct.pack(_KV_FMT[elem], v) for v in values)
+        self.kv.append(self._s(key) + struct.pack("<IIQ", 9, elem, len(values)) + body)
+
+    def raw_kv(self, data: bytes):
+        self.kv.append(bytes(data))
+
+    def tensor(self, name, data: bytes, ggml_type: int, dims=None, offset=None):
+        """dims (ggml order) default to the element count of data."""
+        if dims is None:
+            size = next(s for t, s in GGUF_TYPES.values() if t == ggml_type)
+            dims = [len(data) // size]
+        self.infos.append([name, list(dims), ggml_type, offset])
+        self.blobs.append(bytes(data))
+
+    def tobytes(self) -> bytes:
+        head = b"GGUF" + struct.pack("<IQQ", self.version, len(self.infos), len(self.kv)) + b"".join(self.kv)
+        offsets, off = [], 0
+        for (name, dims, ty, forced), blob in zip(self.infos, self.blobs):
+            off = (off + self.align - 1) // self.align * self.align
+            offsets.append(off if forced is None else forced)
+            head += self._s(name) + struct.pack("<I", len(dims)) + b"".join(struct.pack("<Q", d) for d in dims)
+            head += struct.pack("<IQ", ty, offsets[-1])
+            off += len(blob)
+        head += b"\0" * (-len(head) % self.align)
+        data = bytearray()
+        for o, blob in zip(offsets, self.blobs):
+            if o < len(data):  # a forced offset may point anywhere; keep the data where the file asks
+                continue
+            data += b"\0" * (o - len(data))
+            data += blob
+        return head + bytes(data)
+
+
+def write_gguf(src_dir: str, path: str, model: str, source: str = "", layout: dict | None = None,
+               version: int = 3) -> str:
+    """Pack a converted directory into one vla.simd GGUF. layout maps a .bin
+    (relative path) to [(type, nbytes or None for the rest), ...] when it is not
+    all F32, e.g. SmolVLA's vlm.bin = fp32 norms then bf16 matrices."""
+    layout = layout or {}
+    g = GgufBuilder(version)
+    g.string("general.architecture", "vla-simd")
+    g.string("general.name", os.path.splitext(os.path.basename(path))[0])
+    g.string("vla_simd.model", model)
+    g.scalar("vla_simd.format", 4, 1)
+    g.string("vla_simd.source", source)
+    files = []
+    for d, dirs, names in os.walk(src_dir):
+        dirs.sort()
+        for n in sorted(names):
+            full = os.path.join(d, n)
+            files.append((os.path.relpath(full, src_dir).replace(os.sep, "/"), full))
+    for rel, full in files:
+        with open(full, "rb") as f:
+            data = f.read()
+        if not rel.endswith(".bin") or not data:
+            g.string(f"vla_simd.file.{rel}", data.decode("utf-8"))
+            continue
+        parts = layout.get(rel, [("F32", None)])
+        at = 0
+        for i, (ty, n) in enumerate(parts):
+            n = len(data) - at if n is None else n
+            tid, size = GGUF_TYPES[ty]
+            if n <= 0 or n % size or at + n > len(data):
+                raise ValueError(f"{rel}: invalid {ty} part {i} of {n} bytes")
+            g.tensor(rel if len(parts) == 1 else f"{rel}:{i}", data[at:at + n], tid)
+            at += n
+        if at != len(data):
+            raise ValueError(f"{rel}: layout covers {at} of {len(data)} bytes")
+    with open(path, "wb") as f:
+        f.write(g.tobytes())
+    return path
+
+
+def smolvla_gguf_layout(cfg: dict = SMOLVLA_BASE) -> dict:
+    """vlm.bin as the converter stores it: the fp32 norms, then bf16 matrices."""
+    n_norm = (2 * cfg["n_layers"] + 1) * cfg["hidden"] * 4
+    return {"vlm.bin": [("F32", n_norm), ("BF16", None)]}

@@ -6,13 +6,18 @@
 
 #include "vla_simd_hip.h"
 
+#include "ckpt.h"
 #include "models.h"
 #include "runtime.h"
 
+#include <cstring>
 #include <memory>
 
 using namespace vla::hip;
 
+struct vla_ckpt {
+    std::unique_ptr<CkptFiles> f;
+};
 struct vla_act_tf {
     std::unique_ptr<ActTf> m;
 };
@@ -71,6 +76,51 @@ H* load_handle(const char* where, F&& make) {
 }  // namespace
 
 extern "C" {
+
+// ------------------------------------------------------ checkpoint files --
+
+VLA_API vla_ckpt* vla_ckpt_open(const char* path) {
+    vla_ckpt* h = nullptr;
+    const int32_t rc = guarded("vla_ckpt_open", [&] {
+        VLA_REQUIRE(path, "null path");
+        auto p = std::make_unique<vla_ckpt>();
+        p->f = std::make_unique<CkptFiles>(path);
+        h = p.release();
+    });
+    return rc == 0 ? h : nullptr;
+}
+
+VLA_API void vla_ckpt_free(vla_ckpt* c) { delete c; }
+
+VLA_API int32_t vla_ckpt_is_gguf(const vla_ckpt* c) { return c && c->f->gguf() ? 1 : 0; }
+
+VLA_API int64_t vla_ckpt_file_size(const vla_ckpt* c, const char* rel) {
+    if (!c || !rel) return -1;
+    int64_t n = -1;
+    (void)guarded("vla_ckpt_file_size", [&] { n = c->f->size(rel); });
+    return n;
+}
+
+VLA_API int32_t vla_ckpt_read(const vla_ckpt* c, const char* rel, void* buf, int64_t cap) {
+    return guarded("vla_ckpt_read", [&] {
+        VLA_REQUIRE(c && rel, "null handle or name");
+        const std::vector<char> d = c->f->bytes(rel);
+        VLA_REQUIRE((int64_t)d.size() <= cap && (buf || d.empty()), "buffer too small");
+        if (!d.empty()) std::memcpy(buf, d.data(), d.size());
+    });
+}
+
+VLA_API int64_t vla_ckpt_names(const vla_ckpt* c, char* buf, int64_t cap) {
+    if (!c) return -1;
+    std::string all;
+    for (const std::string& n : c->f->names()) {
+        if (!all.empty()) all += '\n';
+        all += n;
+    }
+    const int64_t need = (int64_t)all.size() + 1;
+    if (buf && cap >= need) std::memcpy(buf, all.c_str(), (size_t)need);
+    return need;
+}
 
 // ------------------------------------------------------------------- ACT --
 

@@ -326,32 +326,5 @@ std::vector<double> rope_cos_sin(const int32_t* pos, int seq, int head_dim, floa
     return cs;
 }
 
-// ------------------------------------------------------------------ files --
-
-std::map<std::string, double> read_meta(const std::string& path) {
-    std::ifstream f(path);
-    if (!f) throw ArgError("cannot open " + path);
-    std::map<std::string, double> m;
-    std::string key;
-    double v;
-    while (f >> key) {
-        if (!(f >> v)) throw ArgError(path + ": key " + key + " has no numeric value");
-        m[key] = v;
-    }
-    return m;
-}
-
-std::vector<char> read_file(const std::string& path) {
-    std::ifstream f(path, std::ios::binary);
-    if (!f) throw ArgError("cannot open " + path);
-    f.seekg(0, std::ios::end);
-    const std::streamoff n = f.tellg();
-    f.seekg(0);
-    std::vector<char> d((size_t)n);
-    if (n > 0) f.read(d.data(), n);
-    if (!f) throw ArgError("cannot read " + path);
-    return d;
-}
-
 }  // namespace hip
 }  // namespace vla

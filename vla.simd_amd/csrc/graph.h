@@ -189,12 +189,6 @@ private:
 // entries (cos theta_i, sin theta_i) at [(t * head_dim/2 + i) * 2].
 std::vector<double> rope_cos_sin(const int32_t* pos, int seq, int head_dim, float base);
 
-// "key value" pairs of a reference .meta file (whitespace separated; the ACT
-// writer puts one per line, the Octo/SmolVLA writers the same).
-std::map<std::string, double> read_meta(const std::string& path);
-// A whole .bin as raw bytes.
-std::vector<char> read_file(const std::string& path);
-
 // Host fp32 -> the bf16 the reference's converters store (top 16 bits), and back.
 inline float bf16_to_f32(uint16_t h) {
     uint32_t u = (uint32_t)h << 16;

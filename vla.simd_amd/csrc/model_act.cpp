@@ -12,6 +12,7 @@
 //   - relu after w1 (:283) is the GEMM epilogue's activation;
 //   - all cameras' tokens go through img_proj as one GEMM (quantization is per
 //     row, so batching rows changes nothing).
+#include "ckpt.h"
 #include "models.h"
 
 #include <cmath>
@@ -67,7 +68,8 @@ void sinusoid_pos_2d(int fh, int fw, int dim, float* out) {
 }  // namespace
 
 ActTf::ActTf(const std::string& dir, int img_ch, int int8_mask) {
-    const auto m = read_meta(dir + "/act.meta");
+    const CkptFiles files(dir);  // a converted directory or a vla.simd GGUF
+    const auto m = files.meta("act.meta");
     d_ = meta_int(m, "dim", d_);
     heads_ = meta_int(m, "heads", heads_);
     hd_ = meta_int(m, "head_dim", hd_);
@@ -85,7 +87,7 @@ ActTf::ActTf(const std::string& dir, int img_ch, int int8_mask) {
                     n_dec_ >= 1 && n_1d_ == 2 && std::isfinite(eps_) && eps_ > 0,
                 "act.meta: invalid configuration (act_transformer.cpp:56-62 bounds)");
 
-    const std::vector<char> raw = read_file(dir + "/act.bin");
+    const std::vector<char> raw = files.bytes("act.bin");
     VLA_REQUIRE(raw.size() % 4 == 0, "act.bin: size is not a whole number of floats");
     Cursor take{reinterpret_cast<const float*>(raw.data()), raw.size() / 4};
     const int d = d_;

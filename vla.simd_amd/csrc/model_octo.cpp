@@ -15,6 +15,7 @@
 //   - the additive [T, T] mask (:196-205) is a group table: a token's group is
 //     (kind, timestep) and allow[gi][gj] = attends() && key not padded, which
 //     blocks exactly the keys the mask sets to lowest().
+#include "ckpt.h"
 #include "models.h"
 
 #include <cmath>
@@ -56,7 +57,8 @@ bool attends(int gi, int ti, int gj, int tj) {
 }  // namespace
 
 OctoTf::OctoTf(const std::string& dir, int int8_mask) {
-    const auto m = read_meta(dir + "/octo.meta");
+    const CkptFiles files(dir);  // a converted directory or a vla.simd GGUF
+    const auto m = files.meta("octo.meta");
     d_ = meta_int(m, "d", d_);
     n_layers_ = meta_int(m, "n_layers", n_layers_);
     heads_ = meta_int(m, "heads", heads_);
@@ -77,7 +79,7 @@ OctoTf::OctoTf(const std::string& dir, int int8_mask) {
                     n_readout_ > 0 && n_layers_ >= 1 && std::isfinite(eps_) && eps_ > 0,
                 "octo.meta: invalid configuration (octo_transformer.cpp:40-48 bounds)");
 
-    const std::vector<char> raw = read_file(dir + "/octo.bin");
+    const std::vector<char> raw = files.bytes("octo.bin");
     VLA_REQUIRE(raw.size() % 4 == 0, "octo.bin: size is not a whole number of floats");
     Cursor take{reinterpret_cast<const float*>(raw.data()), raw.size() / 4};
     const int D = d_;

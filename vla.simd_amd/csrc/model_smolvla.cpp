@@ -18,6 +18,7 @@
 // GEMM epilogues, one RoPE launch over the q and k heads when they share
 // positions, the Euler update x += dt * v_t as the action_out_proj epilogue
 // fmaf(dt, v, x).
+#include "ckpt.h"
 #include "models.h"
 
 #include <cmath>
@@ -45,8 +46,9 @@ double meta_f(const std::map<std::string, double>& m, const char* k, double def)
 }  // namespace
 
 SmolvlaTf::SmolvlaTf(const std::string& dir, int int8_mask) {
+    const CkptFiles files(dir);  // a converted directory or a vla.simd GGUF
     // ---- text tower (smollm2_lm.cpp:17-83)
-    const auto vm = read_meta(dir + "/vlm.meta");
+    const auto vm = files.meta("vlm.meta");
     H_ = meta_int(vm, "hidden", H_);
     nq_ = meta_int(vm, "n_q", nq_);
     nkv_ = meta_int(vm, "n_kv", nkv_);
@@ -61,7 +63,7 @@ SmolvlaTf::SmolvlaTf(const std::string& dir, int int8_mask) {
     const int QF = nq_ * hd_, KV = nkv_ * hd_;
     const bool ilm = int8_mask & 16, iex = int8_mask & 32;
     {
-        const std::vector<char> raw = read_file(dir + "/vlm.bin");
+        const std::vector<char> raw = files.bytes("vlm.bin");
         const size_t fcount = (size_t)2 * H_ * NL_ + H_;
         const size_t per = (size_t)QF * H_ + (size_t)KV * H_ * 2 + (size_t)H_ * QF + (size_t)F_ * H_ * 2 +
                            (size_t)H_ * F_;
@@ -95,7 +97,7 @@ SmolvlaTf::SmolvlaTf(const std::string& dir, int int8_mask) {
     }
 
     // ---- action expert (action_expert.cpp:60-172)
-    const auto am = read_meta(dir + "/aex.meta");
+    const auto am = files.meta("aex.meta");
     EH_ = meta_int(am, "expert_h", EH_);
     EF_ = meta_int(am, "expert_ffn", EF_);
     enq_ = meta_int(am, "n_q", enq_);
@@ -120,7 +122,7 @@ SmolvlaTf::SmolvlaTf(const std::string& dir, int int8_mask) {
     VLA_REQUIRE(EKV == KV && ENL_ <= NL_ && ehd_ == hd_ && enkv_ == nkv_ && EQF == QF,
                 "smolvla: expert and text tower disagree on heads / layers");
     {
-        const std::vector<char> raw = read_file(dir + "/aex.bin");
+        const std::vector<char> raw = files.bytes("aex.bin");
         VLA_REQUIRE(raw.size() % 4 == 0, "aex.bin: size is not a whole number of floats");
         const float* p = reinterpret_cast<const float*>(raw.data());
         const size_t n = raw.size() / 4;
