@@ -314,6 +314,30 @@ VLA_API int32_t vla_dense_linear_dev(float* out, int32_t ldo, const float* x, in
                                      int32_t N, int32_t K, int32_t act, int32_t accumulate,
                                      float alpha, void* stream);
 
+/* ------------------------------------------------------------ convolution -- */
+/* W8A8 2-D convolution, tcpu::conv2d_i8 (src/ops/conv_ops.h:31-35,
+ * src/hal/common/conv.cpp:424-526): x [H, Wd, Cin] fp32 NHWC -> out
+ * [Hout, Wout, Cout], Hout = (H + 2 pad - k) / stride + 1 (square kernel,
+ * symmetric zero padding). One activation scale for the whole input tensor,
+ * s = max|x| * clip / 127 with clip = TCPU_I8_CLIP (0, 1], default 1, as the
+ * reference reads it; weights per output channel over K = k*k*Cin in the patch
+ * order [ky][kx][ci] (W [Cout][k][k][Cin] row-major). The values are exactly
+ * the reference's. Host form: Wq / wscale as vla_pack_weights_i8 writes them
+ * for W viewed as [Cout, K] ([Cout][i8_kpad(K)] rows); any Cout. _dev form:
+ * device-resident weights from vla_linear_i8_create(W, bias, Cout, K)
+ * (nn::Conv2d::init_int8, src/nn/conv.cpp:50-61), device x / out, and a
+ * 256-byte aligned device workspace of vla_conv2d_i8_workspace_bytes (the
+ * im2col rows, their scales and the block maxima; the reference's caller-
+ * owned xq_scratch); -1 for an invalid shape. */
+VLA_API int32_t vla_conv2d_i8(float* out, const float* x, const int8_t* Wq, const float* wscale,
+                              const float* bias, int32_t H, int32_t Wd, int32_t Cin, int32_t Cout,
+                              int32_t k, int32_t stride, int32_t pad);
+VLA_API int64_t vla_conv2d_i8_workspace_bytes(int32_t H, int32_t Wd, int32_t Cin, int32_t k,
+                                              int32_t stride, int32_t pad);
+VLA_API int32_t vla_conv2d_i8_dev(const vla_linear_i8* lin, float* out, const float* x, int32_t H,
+                                  int32_t Wd, int32_t Cin, int32_t k, int32_t stride, int32_t pad,
+                                  void* work, int64_t work_bytes, void* stream);
+
 /* ------------------------------------------------------ checkpoint files -- */
 /* The files of a model path, as the policy loaders below read them: a
  * converted directory (<dir>/<name>.meta / .bin), or a vla.simd GGUF that

@@ -59,6 +59,9 @@ def oracle():
         L.orc_gelu_erf.argtypes = [P, c_size_t]
         L.orc_silu_gate.argtypes = [P, P, P, c_size_t]
         L.orc_relu.argtypes = [P, c_size_t]
+        L.orc_quantize_tensor_i8.argtypes, L.orc_quantize_tensor_i8.restype = [P, P, c_size_t, f], f
+        L.orc_im2col_i8.argtypes = [P, i, P, i, i, i, i, i, i]
+        L.orc_conv2d_i8.argtypes = [P, P, P, i, P, P, i, i, i, i, i, i, i, f]
         _orc = L
     return _orc
 
@@ -96,6 +99,7 @@ def ref():
         L.ref_silu_gate.argtypes = [P, P, P, i]
         L.ref_relu.argtypes = [P, i]
         L.ref_dense_linear.argtypes = [P, P, P, P, i, i, i]
+        L.ref_conv2d_i8.argtypes = [P, P, P, P, i, i, i, i, i, i, i]
         _ref = L
     return _ref
 
@@ -217,6 +221,42 @@ def silu_gate(g, u):
     return out
 
 
+def conv_out(H, Wd, k, stride, pad):
+    return (H + 2 * pad - k) // stride + 1, (Wd + 2 * pad - k) // stride + 1
+
+
+def quantize_tensor_i8(x, clip=1.0):
+    x = _f32(x)
+    q = np.empty(x.shape, np.int8)
+    s = oracle().orc_quantize_tensor_i8(_p(x), _p(q), x.size, clip)
+    return q, np.float32(s)
+
+
+def im2col_i8(xq, k, stride, pad, ldc=None):
+    """xq int8 [H, Wd, Cin] -> [Hout*Wout, ldc] patch rows [ky][kx][ci]."""
+    xq = np.ascontiguousarray(xq, np.int8)
+    H, Wd, Cin = xq.shape
+    Ho, Wo = conv_out(H, Wd, k, stride, pad)
+    ldc = ldc or kpad(k * k * Cin)
+    col = np.empty((Ho * Wo, ldc), np.int8)
+    oracle().orc_im2col_i8(_p(col), ldc, _p(xq), H, Wd, Cin, k, stride, pad)
+    return col
+
+
+def conv2d_i8(x, Wq, wscale, bias, k, stride, pad, clip=1.0):
+    """x fp32 [H, Wd, Cin], Wq int8 [Cout, >= k*k*Cin] -> out [Hout, Wout, Cout]."""
+    x = _f32(x)
+    H, Wd, Cin = x.shape
+    Wq = np.ascontiguousarray(Wq, np.int8)
+    Cout = Wq.shape[0]
+    Ho, Wo = conv_out(H, Wd, k, stride, pad)
+    out = np.empty((Ho, Wo, Cout), np.float32)
+    b = None if bias is None else _f32(bias)
+    oracle().orc_conv2d_i8(_p(out), _p(x), _p(Wq), Wq.shape[1], _p(_f32(wscale)), _p(b), H, Wd, Cin, Cout,
+                           k, stride, pad, clip)
+    return out
+
+
 # ------------------------------------------------------ reference (real) --
 
 def ref_pack_weights(W):
@@ -318,6 +358,19 @@ def ref_eltwise(name, x):
     x = _f32(x).copy()
     getattr(ref(), name)(_p(x), x.size)
     return x
+
+
+def ref_conv2d_i8(x, W, bias, k, stride, pad):
+    """The reference's conv2d_i8 with its own pack_weights_i8 of fp32 W [Cout, k, k, Cin]."""
+    x = _f32(x)
+    H, Wd, Cin = x.shape
+    W = _f32(W)
+    Cout = W.shape[0]
+    Ho, Wo = conv_out(H, Wd, k, stride, pad)
+    out = np.empty((Ho, Wo, Cout), np.float32)
+    b = None if bias is None else _f32(bias)
+    ref().ref_conv2d_i8(_p(out), _p(x), _p(W), _p(b), H, Wd, Cin, Cout, k, stride, pad)
+    return out
 
 
 def ref_silu_gate(g, u):

@@ -253,3 +253,64 @@ void orc_relu(float* x, size_t n) {
     for (size_t i = 0; i < n; i++)
         if (x[i] < 0.0f) x[i] = 0.0f;
 }
+
+/* conv2d_i8 (src/hal/common/conv.cpp:424-526, with quantize_tensor_i8 :448-465
+ * and im2col_row / im2col_panel :117-176): one scale for the whole NHWC input,
+ * s = amax > 0 ? max(amax * clip / 127, FLT_MIN) : 1 (clip = TCPU_I8_CLIP),
+ * q = q8(x * (1 / s)) (quantize_span_i8, gemm_i8.cpp:177-206: clamping before
+ * or after the rounding gives the same byte); im2col row of output pixel
+ * (oy, ox) = taps [ky][kx][ci] at (oy*stride - pad + ky, ox*stride - pad + kx),
+ * zero outside the image; then dense_linear_i8_pre with every row scale s.
+ * Wq [Cout, ldw] rows over K = k*k*Cin. */
+float orc_quantize_tensor_i8(const float* x, int8_t* q, size_t n, float clip) {
+    float amax = 0.0f;
+    for (size_t i = 0; i < n; i++) {
+        const float a = fabsf(x[i]);
+        if (a > amax) amax = a;
+    }
+    float s = 1.0f;
+    if (amax > 0.0f) {
+        const float t = amax * clip;
+        s = t / 127.0f;
+        if (!(s > FLT_MIN)) s = FLT_MIN;
+    }
+    const float inv = 1.0f / s;
+    for (size_t i = 0; i < n; i++) q[i] = q8(x[i] * inv);
+    return s;
+}
+
+void orc_im2col_i8(int8_t* col, int ldc, const int8_t* xq, int H, int Wd, int Cin, int k, int stride,
+                   int pad) {
+    const int Hout = (H + 2 * pad - k) / stride + 1, Wout = (Wd + 2 * pad - k) / stride + 1;
+    const int K = k * k * Cin;
+    for (int oy = 0; oy < Hout; oy++)
+        for (int ox = 0; ox < Wout; ox++) {
+            int8_t* row = col + ((size_t)oy * Wout + ox) * ldc;
+            for (int ky = 0; ky < k; ky++)
+                for (int kx = 0; kx < k; kx++)
+                    for (int ci = 0; ci < Cin; ci++) {
+                        const int iy = oy * stride - pad + ky, ix = ox * stride - pad + kx;
+                        const int in = iy >= 0 && iy < H && ix >= 0 && ix < Wd;
+                        row[(ky * k + kx) * Cin + ci] = in ? xq[((size_t)iy * Wd + ix) * Cin + ci] : 0;
+                    }
+            for (int c = K; c < ldc; c++) row[c] = 0;
+        }
+}
+
+void orc_conv2d_i8(float* out, const float* x, const int8_t* Wq, int ldw, const float* wscale,
+                   const float* bias, int H, int Wd, int Cin, int Cout, int k, int stride, int pad,
+                   float clip) {
+    const int Hout = (H + 2 * pad - k) / stride + 1, Wout = (Wd + 2 * pad - k) / stride + 1;
+    const int K = k * k * Cin, Kp = orc_i8_kpad(K), npix = Hout * Wout;
+    const size_t nin = (size_t)H * Wd * Cin;
+    int8_t* xq = (int8_t*)malloc(nin ? nin : 1);
+    int8_t* col = (int8_t*)malloc((size_t)npix * Kp + 1);
+    float* as = (float*)malloc(sizeof(float) * (size_t)(npix ? npix : 1));
+    const float s = orc_quantize_tensor_i8(x, xq, nin, clip);
+    for (int p = 0; p < npix; p++) as[p] = s;
+    orc_im2col_i8(col, Kp, xq, H, Wd, Cin, k, stride, pad);
+    orc_dense_linear_i8_pre(out, col, Kp, as, Wq, ldw, wscale, bias, npix, Cout, K);
+    free(as);
+    free(col);
+    free(xq);
+}

@@ -27,6 +27,11 @@
  *   orc_layernorm/rmsnorm    golden vectors; double formula (test_ops.cpp:296-321).
  *   orc_gelu_* / silu / relu golden vectors; libm double formula (test_ops.cpp:272-294).
  *   orc_rope_neox            golden vectors from the reference's rope_neox.
+ *   orc_conv2d_i8            bit-exact vs the reference's conv2d_i8 built
+ *                            from its sources (ref_conv2d_i8), stem / 3x3 /
+ *                            1x1-stride-2 / ragged shapes, clip 1 and < 1;
+ *                            the im2col against a direct per-tap
+ *                            convolution of the quantized input (int64).
  */
 #ifndef VLA_ORACLE_H
 #define VLA_ORACLE_H
@@ -94,6 +99,13 @@ void orc_gelu_tanh(float* x, size_t n);
 void orc_gelu_erf(float* x, size_t n);
 void orc_silu_gate(float* out, const float* g, const float* u, size_t n);
 void orc_relu(float* x, size_t n);
+
+float orc_quantize_tensor_i8(const float* x, int8_t* q, size_t n, float clip);
+void orc_im2col_i8(int8_t* col, int ldc, const int8_t* xq, int H, int Wd, int Cin, int k, int stride,
+                   int pad);
+void orc_conv2d_i8(float* out, const float* x, const int8_t* Wq, int ldw, const float* wscale,
+                   const float* bias, int H, int Wd, int Cin, int Cout, int k, int stride, int pad,
+                   float clip);
 
 #ifdef __cplusplus
 }

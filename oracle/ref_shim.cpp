@@ -16,11 +16,13 @@
  */
 #include "hal/arch.h"
 #include "ops/lm_ops.h"
+#include "ops/conv_ops.h"
 #include "ops/quant_ops.h"
 
 #include <cstddef>
 #include <cstdint>
 #include <cstring>
+#include <vector>
 
 #if defined(_OPENMP)
 #include <omp.h>
@@ -117,6 +119,21 @@ REF_API void ref_rmsnorm(float* out, const float* x, const float* w, int seq, in
 REF_API void ref_rope_neox(float* x, const int* pos, int seq, int n_heads, int head_dim,
                            float base) {
     tcpu::rope_neox(x, pos, seq, n_heads, head_dim, base);
+}
+
+/* conv2d_i8 (src/hal/common/conv.cpp:424-526) with weights packed by the
+ * reference's pack_weights_i8 over K = k*k*Cin (nn::Conv2d::init_int8,
+ * src/nn/conv.cpp:50-61; Cout % 16 == 0). The activation clip is the
+ * reference's TCPU_I8_CLIP, read once per process. */
+REF_API void ref_conv2d_i8(float* out, const float* x, const float* W, const float* bias, int H, int Wd,
+                           int Cin, int Cout, int k, int stride, int pad) {
+    const int K = k * k * Cin;
+    std::vector<int32_t> packed(tcpu::packed_i8_words(Cout, K));
+    std::vector<float> wscale(Cout);
+    tcpu::pack_weights_i8(W, reinterpret_cast<int8_t*>(packed.data()), wscale.data(), Cout, K);
+    std::vector<int8_t> scratch;
+    tcpu::conv2d_i8(out, x, reinterpret_cast<const int8_t*>(packed.data()), wscale.data(), bias, H, Wd, Cin,
+                    Cout, k, stride, pad, scratch);
 }
 
 REF_API void ref_gelu_tanh(float* x, int n) { tcpu::gelu_tanh(x, n); }

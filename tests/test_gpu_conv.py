@@ -1,0 +1,99 @@
+"""GPU parity of the W8A8 convolution (vla_conv2d_i8 / _dev).
+
+Bar: bit-exact with the oracle's orc_conv2d_i8 (int8 bytes, int32 sums and the
+fp32 epilogue are all exact), which tests/test_conv_oracle.py pins to the
+reference's own conv2d_i8 (src/hal/common/conv.cpp:424-526). Shapes: a ResNet
+stem (7x7 stride 2 over RGB, the per-byte im2col path), 3x3 blocks and 1x1
+stride-2 downsamples (the float4 path), ragged sizes, a Cout that is not a
+multiple of 16 (the reference requires one; the GPU does not), an all-zero
+input (scale 1, output = bias) and repeated calls on one workspace.
+"""
+
+import numpy as np
+import pytest
+
+from helpers import same_bits
+
+pytestmark = pytest.mark.gpu
+
+# (H, Wd, Cin, Cout, k, stride, pad)
+SHAPES = [(224, 224, 3, 64, 7, 2, 3), (56, 56, 64, 64, 3, 1, 1), (56, 56, 64, 128, 1, 2, 0),
+          (28, 28, 128, 128, 3, 1, 1), (9, 13, 5, 24, 3, 2, 1), (2, 2, 4, 16, 3, 1, 1),
+          (20, 20, 32, 40, 5, 3, 2), (64, 48, 3, 32, 3, 2, 1)]
+
+
+def _case(shape, seed=5):
+    H, Wd, Cin, Cout, k, s, p = shape
+    r = np.random.default_rng(seed + 7 * H + Cin)
+    x = r.normal(0.0, 1.0, (H, Wd, Cin)).astype(np.float32)
+    W = r.uniform(-0.2, 0.2, (Cout, k, k, Cin)).astype(np.float32)
+    b = r.normal(0.0, 0.02, Cout).astype(np.float32)
+    return x, W, b
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_conv2d_i8_host_form(vla, orc, shape):
+    H, Wd, Cin, Cout, k, s, p = shape
+    x, W, b = _case(shape)
+    Wq, ws = orc.quantize_weights_i8(W.reshape(Cout, -1))
+    print(f"conv host {shape}", flush=True)
+    got = vla.conv2d_i8(x, Wq, ws, b, k, s, p)
+    want = orc.conv2d_i8(x, Wq, ws, b, k, s, p)
+    assert same_bits(got, want), "conv2d_i8 differs from the oracle"
+
+
+@pytest.mark.parametrize("shape", SHAPES[:5])
+def test_conv2d_i8_dev_form(vla, orc, torch_cuda, shape):
+    torch = torch_cuda
+    H, Wd, Cin, Cout, k, s, p = shape
+    x, W, b = _case(shape)
+    lin = vla.LinearI8.from_f32(W.reshape(Cout, -1), b)
+    Ho, Wo = (H + 2 * p - k) // s + 1, (Wd + 2 * p - k) // s + 1
+    n = vla.conv2d_i8_workspace_bytes(H, Wd, Cin, k, s, p)
+    work = torch.empty(n, dtype=torch.uint8, device="cuda")
+    xd = torch.from_numpy(x).cuda()
+    out = torch.full((Ho, Wo, Cout), 7.0, device="cuda")
+    print(f"conv dev {shape}", flush=True)
+    vla.conv2d_i8_dev(lin, out, xd, k, s, p, work)
+    torch.cuda.synchronize()
+    Wq, ws = orc.quantize_weights_i8(W.reshape(Cout, -1))
+    assert same_bits(out.cpu().numpy(), orc.conv2d_i8(x, Wq, ws, b, k, s, p))
+
+
+def test_conv2d_i8_repeat_and_zero_input(vla, orc, torch_cuda):
+    """One workspace, two calls in a row (the second on an all-zero input:
+    scale 1, every byte 0, every output the bias), then the first again."""
+    torch = torch_cuda
+    shape = (56, 56, 64, 64, 3, 1, 1)
+    H, Wd, Cin, Cout, k, s, p = shape
+    x, W, b = _case(shape)
+    lin = vla.LinearI8.from_f32(W.reshape(Cout, -1), b)
+    work = torch.empty(vla.conv2d_i8_workspace_bytes(H, Wd, Cin, k, s, p), dtype=torch.uint8, device="cuda")
+    out = torch.empty((H, Wd, Cout), device="cuda")
+    Wq, ws = orc.quantize_weights_i8(W.reshape(Cout, -1))
+    want = orc.conv2d_i8(x, Wq, ws, b, k, s, p)
+    vla.conv2d_i8_dev(lin, out, torch.from_numpy(x).cuda(), k, s, p, work)
+    torch.cuda.synchronize()
+    assert same_bits(out.cpu().numpy(), want)
+    vla.conv2d_i8_dev(lin, out, torch.zeros((H, Wd, Cin), device="cuda"), k, s, p, work)
+    torch.cuda.synchronize()
+    assert same_bits(out.cpu().numpy(), np.broadcast_to(b, (H, Wd, Cout)))
+    vla.conv2d_i8_dev(lin, out, torch.from_numpy(x).cuda(), k, s, p, work)
+    torch.cuda.synchronize()
+    assert same_bits(out.cpu().numpy(), want)
+
+
+def test_conv2d_i8_rejects_bad_calls(vla, torch_cuda):
+    torch = torch_cuda
+    assert vla.conv2d_i8_workspace_bytes(2, 2, 3, 7, 1, 0) == -1      # kernel larger than the input
+    assert vla.conv2d_i8_workspace_bytes(8, 8, 3, 3, 0, 1) == -1      # stride 0
+    lin = vla.LinearI8.from_f32(np.ones((16, 27), np.float32))
+    x = torch.zeros((8, 8, 3), device="cuda")
+    out = torch.zeros((8, 8, 16), device="cuda")
+    small = torch.empty(64, dtype=torch.uint8, device="cuda")
+    with pytest.raises(vla.VlaError) as e:                             # workspace too small
+        vla.conv2d_i8_dev(lin, out, x, 3, 1, 1, small)
+    assert e.value.status == vla.VLA_ERR_ARG
+    with pytest.raises(vla.VlaError) as e:                             # K != k*k*Cin
+        vla.conv2d_i8_dev(lin, out, x, 5, 1, 2, small)
+    assert e.value.status == vla.VLA_ERR_ARG

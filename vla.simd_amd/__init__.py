@@ -44,7 +44,7 @@ EXPORTS = (
     "vla_i8_panel_bytes", "vla_quantize_act_i8_panel_dev", "vla_dense_linear_i8_panel_dev",
     "vla_rowop_quantize_i8_panel_dev", "vla_rowop_linear_i8_fits", "vla_rowop_linear_i8_dev",
     "vla_ckpt_open", "vla_ckpt_free", "vla_ckpt_is_gguf", "vla_ckpt_file_size", "vla_ckpt_read",
-    "vla_ckpt_names",
+    "vla_ckpt_names", "vla_conv2d_i8", "vla_conv2d_i8_workspace_bytes", "vla_conv2d_i8_dev",
     "vla_gemm_i8_i32", "vla_gemm_i8_i32_dev",
     "vla_linear_i8_create", "vla_linear_i8_create_q", "vla_linear_i8_free",
     "vla_linear_i8_weights", "vla_linear_i8_wscale", "vla_linear_i8_ldw",
@@ -119,6 +119,9 @@ def _declare(L):
         "vla_dense_linear_i8_panel_dev": (i32, [P, i32, P, P, P, i32, P, P, i32, i32, i32, i32, i32, P]),
         "vla_rowop_quantize_i8_panel_dev": (i32, [i32, P, i32, P, i32, P, ctypes.c_float, P, P, i32, i32, P]),
         "vla_rowop_linear_i8_fits": (i32, [i32, i32, i32]),
+        "vla_conv2d_i8": (i32, [P, P, P, P, P, i32, i32, i32, i32, i32, i32, i32]),
+        "vla_conv2d_i8_workspace_bytes": (ctypes.c_int64, [i32, i32, i32, i32, i32, i32]),
+        "vla_conv2d_i8_dev": (i32, [P, P, P, i32, i32, i32, i32, i32, i32, P, ctypes.c_int64, P]),
         "vla_ckpt_open": (P, [c_char_p]),
         "vla_ckpt_free": (None, [P]),
         "vla_ckpt_is_gguf": (i32, [P]),
@@ -600,6 +603,32 @@ class _Handle:
             self.close()
         except Exception:
             pass
+
+
+def conv2d_i8(x, Wq, wscale, bias, k, stride, pad):
+    """conv2d_i8 of x [H, Wd, Cin] (host arrays): Wq [Cout, i8_kpad(k*k*Cin)]
+    from pack_weights_i8 -> out [Hout, Wout, Cout]."""
+    x = _f32(x)
+    H, Wd, Cin = x.shape
+    Wq = np.ascontiguousarray(Wq, np.int8)
+    Cout = Wq.shape[0]
+    Ho, Wo = (H + 2 * pad - k) // stride + 1, (Wd + 2 * pad - k) // stride + 1
+    out = np.empty((Ho, Wo, Cout), np.float32)
+    _call("vla_conv2d_i8", _ptr(out), _ptr(x), _ptr(Wq), _ptr(_f32(wscale)), _ptr(None if bias is None else _f32(bias)),
+          H, Wd, Cin, Cout, k, stride, pad)
+    return out
+
+
+def conv2d_i8_workspace_bytes(H, Wd, Cin, k, stride, pad) -> int:
+    return int(lib().vla_conv2d_i8_workspace_bytes(H, Wd, Cin, k, stride, pad))
+
+
+def conv2d_i8_dev(lin, out, x, k, stride, pad, work, stream=None):
+    """Device conv2d_i8: lin a LinearI8 over [Cout, k*k*Cin], x [H, Wd, Cin] and
+    out [Hout, Wout, Cout] torch tensors, work a device byte buffer."""
+    H, Wd, Cin = x.shape
+    _call("vla_conv2d_i8_dev", lin.h, _dp(out), _dp(x), H, Wd, Cin, k, stride, pad, _dp(work),
+          work.numel() * work.element_size(), _stream(stream))
 
 
 class CkptFiles(_Handle):

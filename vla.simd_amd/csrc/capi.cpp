@@ -399,6 +399,83 @@ VLA_API int32_t vla_linear_i8_forward_quantized_dev(const vla_linear_i8* lin, fl
     });
 }
 
+// ---------------------------------------------------------- convolution --
+
+VLA_API int64_t vla_conv2d_i8_workspace_bytes(int32_t H, int32_t Wd, int32_t Cin, int32_t k, int32_t stride,
+                                              int32_t pad) {
+    int64_t n = -1;
+    (void)guarded("vla_conv2d_i8_workspace_bytes",
+                  [&] { n = (int64_t)conv_shape(H, Wd, Cin, k, stride, pad).work; });
+    return n;
+}
+
+VLA_API int32_t vla_conv2d_i8_dev(const vla_linear_i8* lin, float* out, const float* x, int32_t H, int32_t Wd,
+                                  int32_t Cin, int32_t k, int32_t stride, int32_t pad, void* work,
+                                  int64_t work_bytes, void* stream) {
+    return guarded("vla_conv2d_i8_dev", [&] {
+        VLA_REQUIRE(lin, "null weights");
+        VLA_REQUIRE((int64_t)k * k * Cin == lin->K(), "the weights' K is not k*k*Cin");
+        VLA_REQUIRE(work_bytes >= 0, "negative workspace size");
+        ConvArgs a{};
+        a.out = out;
+        a.x = x;
+        a.Wq = lin->Wq();
+        a.ldw = lin->ldw();
+        a.wscale = lin->wscale();
+        a.bias = lin->bias();
+        a.H = H;
+        a.Wd = Wd;
+        a.Cin = Cin;
+        a.Cout = lin->N();
+        a.k = k;
+        a.stride = stride;
+        a.pad = pad;
+        a.work = work;
+        a.work_bytes = (size_t)work_bytes;
+        launch_conv2d_i8(a, as_stream(stream));
+    });
+}
+
+VLA_API int32_t vla_conv2d_i8(float* out, const float* x, const int8_t* Wq, const float* wscale,
+                              const float* bias, int32_t H, int32_t Wd, int32_t Cin, int32_t Cout, int32_t k,
+                              int32_t stride, int32_t pad) {
+    return guarded("vla_conv2d_i8", [&] {
+        const ConvShape c = conv_shape(H, Wd, Cin, k, stride, pad);
+        VLA_REQUIRE(Cout > 0, "need Cout > 0");
+        VLA_REQUIRE(out && x && Wq && wscale, "null buffer");
+        const int Kp = kpad4(c.K), ldw = (Kp + 63) & ~63;
+        const size_t nin = (size_t)H * Wd * Cin, nout = (size_t)c.npix * Cout;
+        Staging& S = staging();
+        auto lk = S.lock();
+        hipStream_t st = library_stream();
+        S.reset(align256(nin * 4) + align256((size_t)Cout * ldw) + 2 * align256((size_t)Cout * 4) +
+                align256(nout * 4) + align256(c.work));
+        ConvArgs a{};
+        a.x = S.upload(x, nin, st);
+        // [Cout][i8_kpad(K)] rows (vla_pack_weights_i8) into 64-byte rows for the aligned GEMM
+        int8_t* w = S.alloc<int8_t>((size_t)Cout * ldw);
+        VLA_HIP_CHECK(hipMemsetAsync(w, 0, (size_t)Cout * ldw, st));
+        VLA_HIP_CHECK(hipMemcpy2DAsync(w, ldw, Wq, Kp, Kp, Cout, hipMemcpyHostToDevice, st));
+        a.Wq = w;
+        a.ldw = ldw;
+        a.wscale = S.upload(wscale, (size_t)Cout, st);
+        a.bias = S.upload(bias, (size_t)Cout, st);
+        a.out = S.alloc<float>(nout);
+        a.H = H;
+        a.Wd = Wd;
+        a.Cin = Cin;
+        a.Cout = Cout;
+        a.k = k;
+        a.stride = stride;
+        a.pad = pad;
+        a.work = S.alloc<char>(c.work);
+        a.work_bytes = c.work;
+        launch_conv2d_i8(a, st);
+        VLA_HIP_CHECK(hipMemcpyAsync(out, a.out, nout * 4, hipMemcpyDeviceToHost, st));
+        VLA_HIP_CHECK(hipStreamSynchronize(st));
+    });
+}
+
 // ------------------------------------------------------------ attention --
 
 VLA_API int32_t vla_attention_dev(float* out, int32_t ldo, const float* Q, int32_t ldq,

@@ -153,6 +153,30 @@ void launch_rowq(const RowQArgs& a, hipStream_t st);
 bool rowop_gemm_fits(int op, int M, int K);
 void launch_gemm_i8_rowop(const RowQArgs& r, const GemmArgs& g, hipStream_t st);
 
+// conv.hip: conv2d_i8 (NHWC x [H, Wd, Cin] -> out [Hout, Wout, Cout]) as
+// per-tensor quantize + im2col + the int8 GEMM. Weights Wq [Cout, ldw] over
+// K = k*k*Cin (taps [ky][kx][ci]), per-channel wscale, optional bias. work:
+// device scratch of at least conv_shape().work bytes, 256-byte aligned.
+// clip <= 0 takes TCPU_I8_CLIP from the environment (default 1).
+struct ConvShape {
+    int Hout, Wout, npix, K, lda;
+    size_t work;
+};
+ConvShape conv_shape(int H, int Wd, int Cin, int k, int stride, int pad);
+struct ConvArgs {
+    float* out;
+    const float* x;
+    const int8_t* Wq;
+    int ldw;
+    const float* wscale;
+    const float* bias;
+    int H, Wd, Cin, Cout, k, stride, pad;
+    float clip;
+    void* work;
+    size_t work_bytes;
+};
+void launch_conv2d_i8(const ConvArgs& a, hipStream_t st);
+
 // RoPE-NeoX from a cos/sin table cs[(t * head_dim/2 + i) * 2 + {0, 1}]
 // (double; rope_cos_sin in graph.h builds it the way rope_neox does)
 void launch_rope_table(float* x, int ld, const double* cs, int seq, int n_heads, int head_dim,
