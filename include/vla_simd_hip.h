@@ -151,6 +151,22 @@ VLA_API int32_t vla_dense_linear_i8_pre_dev(float* out, int32_t ldo, const int8_
                                             int32_t seq, int32_t N, int32_t K, int32_t act,
                                             int32_t accumulate, void* stream);
 
+/* dense_linear_i8_pre_dev with a caller-owned device workspace for split-K
+ * (no counterpart in the reference): when the output tiles of a long-K GEMM
+ * of more than 128 rows would leave most CUs idle, K is cut into chunks whose
+ * int32 partial sums go to `work` and are reduced before the epilogue; the
+ * values equal vla_dense_linear_i8_pre_dev's exactly. vla_gemm_i8_split_bytes
+ * gives the bytes that shape uses (0: it is not split; at most 8 MiB); a
+ * smaller or null workspace just runs unsplit. work: 16-byte aligned. */
+VLA_API int64_t vla_gemm_i8_split_bytes(int32_t seq, int32_t N, int32_t K);
+VLA_API int32_t vla_dense_linear_i8_pre_split_dev(float* out, int32_t ldo, const int8_t* xq,
+                                                  int32_t ldx, const float* ascale,
+                                                  const int8_t* Wq, int32_t ldw,
+                                                  const float* wscale, const float* bias,
+                                                  int32_t seq, int32_t N, int32_t K, int32_t act,
+                                                  int32_t accumulate, void* work,
+                                                  int64_t work_bytes, void* stream);
+
 /* Panel layout of quantized activations for seq <= 128 rows (the shape of
  * action chunks and decode rows; no counterpart in the reference, whose
  * xq is [seq, i8_kpad(K)]): K is cut into 64-byte panels, each holding all
@@ -327,13 +343,13 @@ VLA_API int32_t vla_dense_linear_dev(float* out, int32_t ldo, const float* x, in
  * device-resident weights from vla_linear_i8_create(W, bias, Cout, K)
  * (nn::Conv2d::init_int8, src/nn/conv.cpp:50-61), device x / out, and a
  * 256-byte aligned device workspace of vla_conv2d_i8_workspace_bytes (the
- * im2col rows, their scales and the block maxima; the reference's caller-
- * owned xq_scratch); -1 for an invalid shape. */
+ * im2col rows, their scales, the block maxima and the GEMM's split-K sums;
+ * the reference's caller-owned xq_scratch); -1 for an invalid shape. */
 VLA_API int32_t vla_conv2d_i8(float* out, const float* x, const int8_t* Wq, const float* wscale,
                               const float* bias, int32_t H, int32_t Wd, int32_t Cin, int32_t Cout,
                               int32_t k, int32_t stride, int32_t pad);
-VLA_API int64_t vla_conv2d_i8_workspace_bytes(int32_t H, int32_t Wd, int32_t Cin, int32_t k,
-                                              int32_t stride, int32_t pad);
+VLA_API int64_t vla_conv2d_i8_workspace_bytes(int32_t H, int32_t Wd, int32_t Cin, int32_t Cout,
+                                              int32_t k, int32_t stride, int32_t pad);
 VLA_API int32_t vla_conv2d_i8_dev(const vla_linear_i8* lin, float* out, const float* x, int32_t H,
                                   int32_t Wd, int32_t Cin, int32_t k, int32_t stride, int32_t pad,
                                   void* work, int64_t work_bytes, void* stream);

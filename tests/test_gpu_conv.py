@@ -49,7 +49,7 @@ def test_conv2d_i8_dev_form(vla, orc, torch_cuda, shape):
     x, W, b = _case(shape)
     lin = vla.LinearI8.from_f32(W.reshape(Cout, -1), b)
     Ho, Wo = (H + 2 * p - k) // s + 1, (Wd + 2 * p - k) // s + 1
-    n = vla.conv2d_i8_workspace_bytes(H, Wd, Cin, k, s, p)
+    n = vla.conv2d_i8_workspace_bytes(H, Wd, Cin, Cout, k, s, p)
     work = torch.empty(n, dtype=torch.uint8, device="cuda")
     xd = torch.from_numpy(x).cuda()
     out = torch.full((Ho, Wo, Cout), 7.0, device="cuda")
@@ -68,7 +68,7 @@ def test_conv2d_i8_repeat_and_zero_input(vla, orc, torch_cuda):
     H, Wd, Cin, Cout, k, s, p = shape
     x, W, b = _case(shape)
     lin = vla.LinearI8.from_f32(W.reshape(Cout, -1), b)
-    work = torch.empty(vla.conv2d_i8_workspace_bytes(H, Wd, Cin, k, s, p), dtype=torch.uint8, device="cuda")
+    work = torch.empty(vla.conv2d_i8_workspace_bytes(H, Wd, Cin, Cout, k, s, p), dtype=torch.uint8, device="cuda")
     out = torch.empty((H, Wd, Cout), device="cuda")
     Wq, ws = orc.quantize_weights_i8(W.reshape(Cout, -1))
     want = orc.conv2d_i8(x, Wq, ws, b, k, s, p)
@@ -85,8 +85,8 @@ def test_conv2d_i8_repeat_and_zero_input(vla, orc, torch_cuda):
 
 def test_conv2d_i8_rejects_bad_calls(vla, torch_cuda):
     torch = torch_cuda
-    assert vla.conv2d_i8_workspace_bytes(2, 2, 3, 7, 1, 0) == -1      # kernel larger than the input
-    assert vla.conv2d_i8_workspace_bytes(8, 8, 3, 3, 0, 1) == -1      # stride 0
+    assert vla.conv2d_i8_workspace_bytes(2, 2, 3, 16, 7, 1, 0) == -1      # kernel larger than the input
+    assert vla.conv2d_i8_workspace_bytes(8, 8, 3, 16, 3, 0, 1) == -1      # stride 0
     lin = vla.LinearI8.from_f32(np.ones((16, 27), np.float32))
     x = torch.zeros((8, 8, 3), device="cuda")
     out = torch.zeros((8, 8, 16), device="cuda")

@@ -302,3 +302,63 @@ def test_panel_rejects_large_m(vla, torch_cuda):
     with pytest.raises(vla.VlaError) as e:
         vla.quantize_act_i8_panel_dev(x, xq, sa)
     assert e.value.status == vla.VLA_ERR_ARG
+
+
+# ---------------------------------------------------------------- split K --
+
+# long-K GEMMs of a few hundred rows whose tiles leave most CUs idle: Octo's
+# w2 (658 x 768 x 3072), SmolLM2's down (177 x 960 x 2560), ACT's w2
+# (302 x 512 x 3200), a ResNet 3x3/512 conv (300 x 512 x 4608), a K tail
+# (2050) and a 129-row case
+SPLIT_SHAPES = [(658, 768, 3072), (177, 960, 2560), (302, 512, 3200), (300, 512, 4608), (129, 100, 2050),
+                (200, 48, 1500)]
+
+
+@pytest.mark.parametrize("seq,N,K", SPLIT_SHAPES)
+@pytest.mark.parametrize("act,accumulate", [(0, 0), (1, 1), (2, 0)])
+def test_split_k_bitexact(vla, orc, torch_cuda, seq, N, K, act, accumulate):
+    """Split-K (int32 partial sums over K chunks, then one reduce + epilogue)
+    equals the unsplit launch and the oracle bit for bit."""
+    torch = torch_cuda
+    n = vla.gemm_i8_split_bytes(seq, N, K)
+    assert n > 0, "shape expected to split"
+    x, W, b = _case(orc, seq, N, K)
+    xq, sa = orc.quantize_act_i8(x)
+    Wq, ws = orc.quantize_weights_i8(W)
+    ld = (K + 63) // 64 * 64
+    Xp = np.zeros((seq, ld), np.int8)
+    Xp[:, :xq.shape[1]] = xq
+    Wp = np.zeros((N, ld), np.int8)
+    Wp[:, :Wq.shape[1]] = Wq
+    dev = torch.device("cuda")
+    Xd, Wd = torch.from_numpy(Xp).to(dev), torch.from_numpy(Wp).to(dev)
+    sad, wsd, bd = torch.from_numpy(sa).to(dev), torch.from_numpy(ws).to(dev), torch.from_numpy(b).to(dev)
+    base = np.full((seq, N), 0.25, np.float32)
+    work = torch.empty(n, dtype=torch.uint8, device=dev)
+    split = torch.from_numpy(base.copy()).to(dev)
+    vla.dense_linear_i8_pre_split_dev(split, Xd, sad, Wd, wsd, bd, K, work, act=act, accumulate=accumulate)
+    plain = torch.from_numpy(base.copy()).to(dev)
+    vla.dense_linear_i8_pre_dev(plain, Xd, sad, Wd, wsd, bd, K, act=act, accumulate=accumulate)
+    small = torch.from_numpy(base.copy()).to(dev)  # a workspace one byte short runs unsplit
+    vla.dense_linear_i8_pre_split_dev(small, Xd, sad, Wd, wsd, bd, K, work[: n - 1], act=act,
+                                      accumulate=accumulate)
+    torch.cuda.synchronize()
+    got = split.cpu().numpy()
+    assert same_bits(got, plain.cpu().numpy()) and same_bits(small.cpu().numpy(), got)
+    want = orc.apply_act(orc.dense_linear_i8_pre(xq, sa, Wq, ws, b, K), act)
+    if accumulate:
+        want = (base + want).astype(np.float32)
+    if act == 2:
+        assert max_rel(got, want) <= 2e-6
+    else:
+        assert same_bits(got, want)
+
+
+def test_split_k_plan_bounds(vla):
+    """Short K, skinny M and tile-rich shapes are not split; the workspace a
+    split asks for stays within 8 MiB."""
+    assert vla.gemm_i8_split_bytes(100, 4096, 4096) == 0      # skinny kernel
+    assert vla.gemm_i8_split_bytes(658, 768, 768) == 0        # K < 1024
+    assert vla.gemm_i8_split_bytes(8192, 4096, 4096) == 0     # fills the chip
+    for seq, N, K in SPLIT_SHAPES:
+        assert 0 < vla.gemm_i8_split_bytes(seq, N, K) <= 8 << 20

@@ -45,6 +45,7 @@ EXPORTS = (
     "vla_rowop_quantize_i8_panel_dev", "vla_rowop_linear_i8_fits", "vla_rowop_linear_i8_dev",
     "vla_ckpt_open", "vla_ckpt_free", "vla_ckpt_is_gguf", "vla_ckpt_file_size", "vla_ckpt_read",
     "vla_ckpt_names", "vla_conv2d_i8", "vla_conv2d_i8_workspace_bytes", "vla_conv2d_i8_dev",
+    "vla_gemm_i8_split_bytes", "vla_dense_linear_i8_pre_split_dev",
     "vla_gemm_i8_i32", "vla_gemm_i8_i32_dev",
     "vla_linear_i8_create", "vla_linear_i8_create_q", "vla_linear_i8_free",
     "vla_linear_i8_weights", "vla_linear_i8_wscale", "vla_linear_i8_ldw",
@@ -120,7 +121,10 @@ def _declare(L):
         "vla_rowop_quantize_i8_panel_dev": (i32, [i32, P, i32, P, i32, P, ctypes.c_float, P, P, i32, i32, P]),
         "vla_rowop_linear_i8_fits": (i32, [i32, i32, i32]),
         "vla_conv2d_i8": (i32, [P, P, P, P, P, i32, i32, i32, i32, i32, i32, i32]),
-        "vla_conv2d_i8_workspace_bytes": (ctypes.c_int64, [i32, i32, i32, i32, i32, i32]),
+        "vla_conv2d_i8_workspace_bytes": (ctypes.c_int64, [i32, i32, i32, i32, i32, i32, i32]),
+        "vla_gemm_i8_split_bytes": (ctypes.c_int64, [i32, i32, i32]),
+        "vla_dense_linear_i8_pre_split_dev": (i32, [P, i32, P, i32, P, P, i32, P, P, i32, i32, i32, i32, i32, P,
+                                                    ctypes.c_int64, P]),
         "vla_conv2d_i8_dev": (i32, [P, P, P, i32, i32, i32, i32, i32, i32, P, ctypes.c_int64, P]),
         "vla_ckpt_open": (P, [c_char_p]),
         "vla_ckpt_free": (None, [P]),
@@ -619,8 +623,22 @@ def conv2d_i8(x, Wq, wscale, bias, k, stride, pad):
     return out
 
 
-def conv2d_i8_workspace_bytes(H, Wd, Cin, k, stride, pad) -> int:
-    return int(lib().vla_conv2d_i8_workspace_bytes(H, Wd, Cin, k, stride, pad))
+def conv2d_i8_workspace_bytes(H, Wd, Cin, Cout, k, stride, pad) -> int:
+    return int(lib().vla_conv2d_i8_workspace_bytes(H, Wd, Cin, Cout, k, stride, pad))
+
+
+def gemm_i8_split_bytes(seq: int, N: int, K: int) -> int:
+    """Split-K workspace bytes dense_linear_i8_pre_split_dev uses for this shape (0: unsplit)."""
+    return int(lib().vla_gemm_i8_split_bytes(seq, N, K))
+
+
+def dense_linear_i8_pre_split_dev(out, xq, ascale, Wq, wscale, bias, K, work, act=0, accumulate=0, stream=None):
+    """dense_linear_i8_pre_dev with a split-K workspace (a device byte tensor or None)."""
+    seq, N = out.shape[0], Wq.shape[0]
+    nbytes = 0 if work is None else work.numel() * work.element_size()
+    _call("vla_dense_linear_i8_pre_split_dev", _dp(out), out.stride(0), _dp(xq), xq.stride(0), _dp(ascale),
+          _dp(Wq), Wq.stride(0), _dp(wscale), _dp(bias), seq, N, K, act, accumulate, _dp(work), nbytes,
+          _stream(stream))
 
 
 def conv2d_i8_dev(lin, out, x, k, stride, pad, work, stream=None):

@@ -249,6 +249,39 @@ VLA_API int32_t vla_dense_linear_i8_pre_dev(float* out, int32_t ldo, const int8_
     });
 }
 
+VLA_API int64_t vla_gemm_i8_split_bytes(int32_t seq, int32_t N, int32_t K) {
+    if (seq < 0 || N <= 0 || K <= 0) return -1;
+    return (int64_t)gemm_split_bytes(seq, N, K);
+}
+
+VLA_API int32_t vla_dense_linear_i8_pre_split_dev(float* out, int32_t ldo, const int8_t* xq, int32_t ldx,
+                                                  const float* ascale, const int8_t* Wq, int32_t ldw,
+                                                  const float* wscale, const float* bias, int32_t seq,
+                                                  int32_t N, int32_t K, int32_t act, int32_t accumulate,
+                                                  void* work, int64_t work_bytes, void* stream) {
+    return guarded("vla_dense_linear_i8_pre_split_dev", [&] {
+        VLA_REQUIRE(work_bytes >= 0 && (work || work_bytes == 0), "bad workspace");
+        GemmArgs a{};
+        a.A = xq;
+        a.lda = ldx;
+        a.B = Wq;
+        a.ldb = ldw;
+        a.ascale = ascale;
+        a.wscale = wscale;
+        a.bias = bias;
+        a.out = out;
+        a.ldo = ldo;
+        a.M = seq;
+        a.N = N;
+        a.K = K;
+        a.act = act;
+        a.accumulate = accumulate;
+        a.split_ws = static_cast<int32_t*>(work);
+        a.split_bytes = (size_t)work_bytes;
+        launch_gemm_i8(a, as_stream(stream));
+    });
+}
+
 VLA_API int64_t vla_i8_panel_bytes(int32_t seq, int32_t K) {
     if (seq < 0 || seq > kPanelMaxRows || K <= 0) return -1;
     return (int64_t)panel_bytes(seq, K);
@@ -401,11 +434,13 @@ VLA_API int32_t vla_linear_i8_forward_quantized_dev(const vla_linear_i8* lin, fl
 
 // ---------------------------------------------------------- convolution --
 
-VLA_API int64_t vla_conv2d_i8_workspace_bytes(int32_t H, int32_t Wd, int32_t Cin, int32_t k, int32_t stride,
-                                              int32_t pad) {
+VLA_API int64_t vla_conv2d_i8_workspace_bytes(int32_t H, int32_t Wd, int32_t Cin, int32_t Cout, int32_t k,
+                                              int32_t stride, int32_t pad) {
     int64_t n = -1;
-    (void)guarded("vla_conv2d_i8_workspace_bytes",
-                  [&] { n = (int64_t)conv_shape(H, Wd, Cin, k, stride, pad).work; });
+    (void)guarded("vla_conv2d_i8_workspace_bytes", [&] {
+        VLA_REQUIRE(Cout > 0, "need Cout > 0");
+        n = (int64_t)conv_shape(H, Wd, Cin, k, stride, pad, Cout).work;
+    });
     return n;
 }
 
@@ -440,8 +475,8 @@ VLA_API int32_t vla_conv2d_i8(float* out, const float* x, const int8_t* Wq, cons
                               const float* bias, int32_t H, int32_t Wd, int32_t Cin, int32_t Cout, int32_t k,
                               int32_t stride, int32_t pad) {
     return guarded("vla_conv2d_i8", [&] {
-        const ConvShape c = conv_shape(H, Wd, Cin, k, stride, pad);
         VLA_REQUIRE(Cout > 0, "need Cout > 0");
+        const ConvShape c = conv_shape(H, Wd, Cin, k, stride, pad, Cout);
         VLA_REQUIRE(out && x && Wq && wscale, "null buffer");
         const int Kp = kpad4(c.K), ldw = (Kp + 63) & ~63;
         const size_t nin = (size_t)H * Wd * Cin, nout = (size_t)c.npix * Cout;

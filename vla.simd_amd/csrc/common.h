@@ -87,8 +87,18 @@ struct GemmArgs {
     int act;                     // vla_act
     int accumulate;              // out += result
     int a_panel;                 // A in the panel layout above (M <= kPanelMaxRows)
+    // Split-K workspace (device, 16-byte aligned) or null. With it, a GEMM
+    // whose tiles would leave most CUs idle and whose K is long runs as
+    // gemm_split_plan's S partial products over K chunks (raw int32 sums into
+    // the workspace) plus one reduce + epilogue pass; int32 sums are exact, so
+    // the values are the same as without it.
+    int32_t* split_ws;
+    size_t split_bytes;
+    int kchunk;                  // set by launch_gemm_i8 for a split launch
 };
 void launch_gemm_i8(const GemmArgs& a, hipStream_t st);
+// Workspace bytes launch_gemm_i8 uses to split K for this shape (0: no split).
+size_t gemm_split_bytes(int M, int N, int K);
 
 // attn.hip
 struct AttnArgs {
@@ -160,9 +170,10 @@ void launch_gemm_i8_rowop(const RowQArgs& r, const GemmArgs& g, hipStream_t st);
 // clip <= 0 takes TCPU_I8_CLIP from the environment (default 1).
 struct ConvShape {
     int Hout, Wout, npix, K, lda;
-    size_t work;
+    size_t split;  // split-K workspace of the GEMM (gemm_split_bytes)
+    size_t work;   // everything, split workspace last
 };
-ConvShape conv_shape(int H, int Wd, int Cin, int k, int stride, int pad);
+ConvShape conv_shape(int H, int Wd, int Cin, int k, int stride, int pad, int Cout);
 struct ConvArgs {
     float* out;
     const float* x;

@@ -186,9 +186,9 @@ float clip_from_env() {
 
 }  // namespace
 
-ConvShape conv_shape(int H, int Wd, int Cin, int k, int stride, int pad) {
-    VLA_REQUIRE(H > 0 && Wd > 0 && Cin > 0 && k > 0 && stride > 0 && pad >= 0,
-                "conv2d_i8: need positive H, Wd, Cin, k, stride and pad >= 0");
+ConvShape conv_shape(int H, int Wd, int Cin, int k, int stride, int pad, int Cout) {
+    VLA_REQUIRE(H > 0 && Wd > 0 && Cin > 0 && Cout > 0 && k > 0 && stride > 0 && pad >= 0,
+                "conv2d_i8: need positive H, Wd, Cin, Cout, k, stride and pad >= 0");
     VLA_REQUIRE(H + 2 * pad >= k && Wd + 2 * pad >= k, "conv2d_i8: kernel larger than the padded input");
     VLA_REQUIRE((int64_t)k * k * Cin <= kMaxI8K, "conv2d_i8: K = k*k*Cin exceeds INT_MAX/(255*127)");
     ConvShape c;
@@ -199,18 +199,21 @@ ConvShape conv_shape(int H, int Wd, int Cin, int k, int stride, int pad) {
                 "conv2d_i8: input or output too large");
     c.npix = c.Hout * c.Wout;
     c.lda = (kpad4(c.K) + 63) & ~63;
-    c.work = (size_t)kAbsmaxBlocks * 4 + ((size_t)c.npix * 4 + 255) / 256 * 256 + (size_t)c.npix * c.lda;
+    c.split = gemm_split_bytes(c.npix, Cout, c.K);
+    c.work = (size_t)kAbsmaxBlocks * 4 + ((size_t)c.npix * 4 + 255) / 256 * 256 +
+             ((size_t)c.npix * c.lda + 255) / 256 * 256 + c.split;
     return c;
 }
 
 void launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
-    const ConvShape c = conv_shape(a.H, a.Wd, a.Cin, a.k, a.stride, a.pad);
+    const ConvShape c = conv_shape(a.H, a.Wd, a.Cin, a.k, a.stride, a.pad, a.Cout);
     VLA_REQUIRE(a.x && a.out && a.Wq && a.wscale && a.work, "conv2d_i8: null buffer");
-    VLA_REQUIRE(a.Cout > 0 && a.ldw >= kpad4(c.K) && a.ldw % 4 == 0, "conv2d_i8: bad weight rows");
+    VLA_REQUIRE(a.ldw >= kpad4(c.K) && a.ldw % 4 == 0, "conv2d_i8: bad weight rows");
     VLA_REQUIRE(a.work_bytes >= c.work, "conv2d_i8: workspace too small (vla_conv2d_i8_workspace_bytes)");
     VLA_REQUIRE((reinterpret_cast<uintptr_t>(a.work) & 255) == 0, "conv2d_i8: workspace must be 256-byte aligned");
     char* w = static_cast<char*>(a.work);
-    // [block maxima: 512 floats][row scales: npix floats, 256-byte rounded][im2col rows]
+    // [block maxima: 512 floats][row scales: npix floats][im2col rows][split-K sums],
+    // each 256-byte rounded
     float* part = reinterpret_cast<float*>(w);
     float* ascale = reinterpret_cast<float*>(w + (size_t)kAbsmaxBlocks * 4);
     int8_t* A = reinterpret_cast<int8_t*>(w + (size_t)kAbsmaxBlocks * 4 + ((size_t)c.npix * 4 + 255) / 256 * 256);
@@ -249,6 +252,10 @@ void launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
     m.M = c.npix;
     m.N = a.Cout;
     m.K = c.K;
+    if (c.split) {
+        m.split_ws = reinterpret_cast<int32_t*>(w + c.work - c.split);
+        m.split_bytes = c.split;
+    }
     launch_gemm_i8(m, st);
 }
 

@@ -359,6 +359,14 @@ __global__ __launch_bounds__(256) void gemm_i8_tiled(GemmArgs a) {
     constexpr int CA = C::CA, CB = C::CB;
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
 
+    if (gridDim.y > 1) {  // split K: chunk blockIdx.y of K, raw int32 sums into its workspace slice
+        const int k0 = blockIdx.y * a.kchunk;
+        a.A += k0;
+        a.B += k0;
+        a.K = a.K - k0 < a.kchunk ? a.K - k0 : a.kchunk;
+        a.acc32 = a.split_ws + (size_t)blockIdx.y * a.M * a.N;
+    }
+
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
@@ -1010,6 +1018,36 @@ __global__ __launch_bounds__(1024) void gemm_i8_rowop(RowQArgs r, GemmArgs a) {
     }
 }
 
+// ------------------------------------------------------------- split K --
+
+// out = epilogue(sum over the S chunk slices of the int32 partial products):
+// the sums are exact, and the epilogue is epi_value, the expression every
+// other kernel applies, so the outputs equal the unsplit GEMM's bit for bit.
+// VEC: 4 consecutive outputs per thread (N, ldo multiples of 4, out aligned).
+template <bool VEC>
+__global__ __launch_bounds__(256) void gemm_i8_split_reduce(GemmArgs a, int S) {
+    const int64_t MN = (int64_t)a.M * a.N;
+    const int64_t step = (int64_t)gridDim.x * blockDim.x * (VEC ? 4 : 1);
+    for (int64_t e = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * (VEC ? 4 : 1); e < MN; e += step) {
+        const int m = (int)(e / a.N), n = (int)(e % a.N);
+        if (VEC) {
+            v4i acc = *reinterpret_cast<const v4i*>(a.split_ws + e);
+            for (int z = 1; z < S; z++) acc += *reinterpret_cast<const v4i*>(a.split_ws + z * MN + e);
+            float* o = a.out + (size_t)m * a.ldo + n;
+            v4f v = {epi_value(a, m, n, acc.x), epi_value(a, m, n + 1, acc.y), epi_value(a, m, n + 2, acc.z),
+                     epi_value(a, m, n + 3, acc.w)};
+            if (a.accumulate) v = *reinterpret_cast<const v4f*>(o) + v;
+            *reinterpret_cast<v4f*>(o) = v;
+        } else {
+            int32_t acc = a.split_ws[e];
+            for (int z = 1; z < S; z++) acc += a.split_ws[z * MN + e];
+            float* o = a.out + (size_t)m * a.ldo + n;
+            const float v = epi_value(a, m, n, acc);
+            *o = a.accumulate ? *o + v : v;
+        }
+    }
+}
+
 // --------------------------------------------------------------- generic --
 
 __global__ __launch_bounds__(256) void gemm_i8_generic(GemmArgs a) {
@@ -1073,7 +1111,7 @@ __global__ __launch_bounds__(256) void gemm_i8_generic(GemmArgs a) {
 constexpr int kCUs = 256;
 
 template <int BM, int BN, int BK>
-void run_tiled(const GemmArgs& a, hipStream_t st) {
+void run_tiled(const GemmArgs& a, hipStream_t st, int splits = 1) {
     using C = TileCfg<BM, BN, BK>;
     static const bool attr = [] {
         // above 64 KiB a kernel must opt in to the larger LDS allocation
@@ -1084,7 +1122,7 @@ void run_tiled(const GemmArgs& a, hipStream_t st) {
     }();
     (void)attr;
     const int blocks = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-    gemm_i8_tiled<BM, BN, BK><<<blocks, 256, C::LDS, st>>>(a);
+    gemm_i8_tiled<BM, BN, BK><<<dim3(blocks, splits), 256, C::LDS, st>>>(a);
     VLA_LAUNCH_CHECK();
 }
 
@@ -1201,6 +1239,31 @@ Tile pick_tile(int M, int N, int K) {
     return {64, 64, 64, 0};
 }
 
+// Split-K plan: for M > 128 on the register-staged tiles (the LDS kernels are
+// picked only when the grid already fills the chip) with K >= 1024 and fewer
+// tiles than CUs, S chunks of K (multiples of 64 bytes, each >= 512) so that
+// S x tiles reaches about two blocks per CU, S <= 8. S x tiles <= 2 x CUs
+// bounds the workspace: S x M x N <= 512 x 64 x 64 int32s (8 MiB).
+struct SplitPlan {
+    int S = 1, kchunk = 0;
+};
+SplitPlan split_plan(int M, int N, int K) {
+    SplitPlan p;
+    if (M <= kPanelMaxRows || K < 1024) return p;
+    const Tile t = pick_tile(M, N, K);
+    if (t.stages != 0) return p;
+    const long tiles = (long)((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
+    if (tiles >= kCUs) return p;
+    int S = (int)(2 * kCUs / tiles);
+    S = S < 8 ? S : 8;
+    S = S < K / 512 ? S : K / 512;
+    if (S < 2) return p;
+    p.kchunk = ((K + S - 1) / S + 63) / 64 * 64;
+    p.S = (K + p.kchunk - 1) / p.kchunk;
+    if (p.S < 2) p = SplitPlan{};
+    return p;
+}
+
 void dispatch_tile(const Tile& t, const GemmArgs& a, hipStream_t st) {
     if (t.stages && t.waves == 8) {
         if (t.bn == 256 && t.pf) run_lds<256, 256, 128, 2, 2, 4, true>(a, st);
@@ -1249,7 +1312,30 @@ void launch_gemm_i8(const GemmArgs& a, hipStream_t st) {
         else run_skinny<4>(a, st);
         return;
     }
-    dispatch_tile(pick_tile(a.M, a.N, a.K), a, st);
+    const Tile t = pick_tile(a.M, a.N, a.K);
+    if (a.split_ws && !a.acc32) {
+        const SplitPlan p = split_plan(a.M, a.N, a.K);
+        if (p.S > 1 && a.split_bytes >= (size_t)p.S * a.M * a.N * 4 && aligned(a.split_ws, 16)) {
+            GemmArgs s = a;
+            s.kchunk = p.kchunk;
+            if (t.bm == 128) run_tiled<128, 128, 64>(s, st, p.S);
+            else if (t.bn == 128) run_tiled<64, 128, 64>(s, st, p.S);
+            else run_tiled<64, 64, 64>(s, st, p.S);
+            const bool vec = a.N % 4 == 0 && a.ldo % 4 == 0 && aligned(a.out, 16);
+            const int64_t work = (int64_t)a.M * a.N / (vec ? 4 : 1);
+            const int blocks = (int)((work + 255) / 256 < 4096 ? (work + 255) / 256 : 4096);
+            if (vec) gemm_i8_split_reduce<true><<<blocks, 256, 0, st>>>(s, p.S);
+            else gemm_i8_split_reduce<false><<<blocks, 256, 0, st>>>(s, p.S);
+            VLA_LAUNCH_CHECK();
+            return;
+        }
+    }
+    dispatch_tile(t, a, st);
+}
+
+size_t gemm_split_bytes(int M, int N, int K) {
+    const SplitPlan p = split_plan(M, N, K);
+    return p.S > 1 ? (size_t)p.S * M * N * 4 : 0;
 }
 
 bool rowop_gemm_fits(int op, int M, int K) {

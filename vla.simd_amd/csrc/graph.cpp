@@ -70,6 +70,8 @@ void Ctx::alloc(DeviceArena& A, int rows, int ld_max) {
         xq[i] = A.alloc<int8_t>(xq_bytes);
         xs[i] = A.alloc<float>(rows);
     }
+    split_bytes = (size_t)8 << 20;  // the most any split-K plan asks for
+    split_ws = A.alloc<int32_t>(split_bytes / 4);
 }
 
 void quantize(const Ctx& c, const QAct& dst, const float* x, int ldx, int seq, int K) {
@@ -152,6 +154,8 @@ static void gemm_q(const Ctx& c, const DLinear& L, const QAct& x, float* out, in
     a.act = act;
     a.accumulate = acc;
     a.a_panel = x.panel ? 1 : 0;
+    a.split_ws = c.split_ws;
+    a.split_bytes = c.split_bytes;
     launch_gemm_i8(a, c.st);
 }
 

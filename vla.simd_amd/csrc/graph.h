@@ -92,6 +92,8 @@ struct Ctx {
     float* xs[2] = {nullptr, nullptr};
     size_t xq_bytes = 0;
     int xs_rows = 0;
+    int32_t* split_ws = nullptr;  // split-K partial sums of the int8 GEMMs (8 MiB)
+    size_t split_bytes = 0;
     // slot i laid out for a layer of row stride ld, for `rows` rows: the
     // panel layout when the rows feed the skinny GEMM (rows <= 128), else
     // row-major [rows, ld]
