@@ -102,6 +102,10 @@ class Shape:
         self.sa = torch.empty(M, dtype=torch.float32, device=dev)
         self.ws = torch.from_numpy(ws).to(dev)
         self.b = torch.from_numpy(b).to(dev)
+        # split-K workspace for long-K shapes whose tiles leave CUs idle (the
+        # same values as the unsplit GEMM; the op API's caller-owned scratch)
+        nsplit = 0 if self.panel else vla.gemm_i8_split_bytes(M, N, K)
+        self.split = torch.empty(nsplit, dtype=torch.uint8, device=dev) if nsplit > 0 else None
         self.i = 0
 
     def quantize(self, vla, stream):
@@ -116,6 +120,9 @@ class Shape:
         if self.panel:
             vla.dense_linear_i8_panel_dev(self.out[r], self.xq, self.sa, self.W[r], self.ws, self.b, self.K,
                                           stream=stream)
+        elif self.split is not None:
+            vla.dense_linear_i8_pre_split_dev(self.out[r], self.xq, self.sa, self.W[r], self.ws, self.b, self.K,
+                                              self.split, stream=stream)
         else:
             vla.dense_linear_i8_pre_dev(self.out[r], self.xq, self.sa, self.W[r], self.ws, self.b, self.K,
                                         stream=stream)
@@ -419,6 +426,7 @@ def main():
             "gemm_gbs": round(gemm_bytes(sh.M, sh.K, sh.N) / g_us / 1e3, 1),
             "bound": bound, "roof_us": round(t_roof, 3), "frac": round(t_roof / g_us, 4),
             "rotating_copies": sh.R, "a_layout": "panel" if sh.panel else "row-major",
+            "split_k": sh.split is not None,
         })
         if (sh.M, sh.K, sh.N) == dominant:
             dom_us = g_us

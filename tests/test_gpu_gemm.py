@@ -309,9 +309,9 @@ def test_panel_rejects_large_m(vla, torch_cuda):
 # long-K GEMMs of a few hundred rows whose tiles leave most CUs idle: Octo's
 # w2 (658 x 768 x 3072), SmolLM2's down (177 x 960 x 2560), ACT's w2
 # (302 x 512 x 3200), a ResNet 3x3/512 conv (300 x 512 x 4608), a K tail
-# (2050) and a 129-row case
+# (2050), a 129-row case and a sweep shape (512 x 960 x 2560)
 SPLIT_SHAPES = [(658, 768, 3072), (177, 960, 2560), (302, 512, 3200), (300, 512, 4608), (129, 100, 2050),
-                (200, 48, 1500)]
+                (200, 48, 1500), (512, 960, 2560)]
 
 
 @pytest.mark.parametrize("seq,N,K", SPLIT_SHAPES)
@@ -360,5 +360,6 @@ def test_split_k_plan_bounds(vla):
     assert vla.gemm_i8_split_bytes(100, 4096, 4096) == 0      # skinny kernel
     assert vla.gemm_i8_split_bytes(658, 768, 768) == 0        # K < 1024
     assert vla.gemm_i8_split_bytes(8192, 4096, 4096) == 0     # fills the chip
+    assert vla.gemm_i8_split_bytes(512, 4096, 4096) == 0      # one LDS-DMA tile per CU: measured slower split
     for seq, N, K in SPLIT_SHAPES:
         assert 0 < vla.gemm_i8_split_bytes(seq, N, K) <= 8 << 20

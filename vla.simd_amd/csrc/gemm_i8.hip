@@ -1239,11 +1239,14 @@ Tile pick_tile(int M, int N, int K) {
     return {64, 64, 64, 0};
 }
 
-// Split-K plan: for M > 128 on the register-staged tiles (the LDS kernels are
-// picked only when the grid already fills the chip) with K >= 1024 and fewer
-// tiles than CUs, S chunks of K (multiples of 64 bytes, each >= 512) so that
-// S x tiles reaches about two blocks per CU, S <= 8. S x tiles <= 2 x CUs
-// bounds the workspace: S x M x N <= 512 x 64 x 64 int32s (8 MiB).
+// Split-K plan: for M > 128 on the register-staged tiles with K >= 1024 and
+// fewer tiles than CUs, S chunks of K (multiples of 128 bytes, each >= 512)
+// so that S x tiles reaches about two blocks per CU, S <= 8. S x tiles <= 2 x
+// CUs bounds the workspace: S x M x N <= 512 x 64 x 64 int32s (8 MiB).
+// Measured on MI355X: splitting the LDS-DMA tiles when they number one per
+// CU made 512 x 4096 x 4096 and 2048 x 960 x 2560 slower (23.7 -> 31.5 and
+// 16.1 -> 27.4 us: the partial sums' round trip costs more than the idle
+// half of each CU), so those keep one launch.
 struct SplitPlan {
     int S = 1, kchunk = 0;
 };
@@ -1258,7 +1261,7 @@ SplitPlan split_plan(int M, int N, int K) {
     S = S < 8 ? S : 8;
     S = S < K / 512 ? S : K / 512;
     if (S < 2) return p;
-    p.kchunk = ((K + S - 1) / S + 63) / 64 * 64;
+    p.kchunk = ((K + S - 1) / S + 127) / 128 * 128;
     p.S = (K + p.kchunk - 1) / p.kchunk;
     if (p.S < 2) p = SplitPlan{};
     return p;
