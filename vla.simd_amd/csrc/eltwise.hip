@@ -213,8 +213,89 @@ __global__ __launch_bounds__(256) void rowq_kernel(RowQArgs a) {
     }
 }
 
+// rowq_kernel for the element-wise row ops (0 identity, 3 silu_gate) without
+// an add: a whole 256-thread block per row, so a 2048-wide SiLU-gate row is
+// 8 elements per lane instead of 32 and the rows' expf / divisions spread
+// over rows x 4 waves. Thread t holds elements 4 t + 1024 i. The values are
+// the single-wave kernel's: the element ops are the same functions and the
+// row max does not depend on the reduction order.
+template <int OP, int NV>
+__global__ __launch_bounds__(256) void rowq_wide_kernel(RowQArgs a) {
+    static_assert(OP == 0 || OP == 3, "element-wise row ops only");
+    __shared__ float red[4];
+    const int row = blockIdx.x, t = threadIdx.x, H = a.H;
+    const float* xr = a.x + (size_t)row * a.ldx;
+    const float* ur = OP == 3 ? a.u + (size_t)row * a.ldu : nullptr;
+    float4 y[NV];
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int k = 4 * t + 1024 * i;
+        y[i] = k < H ? *reinterpret_cast<const float4*>(xr + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    if (OP == 3) {
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int k = 4 * t + 1024 * i;
+            if (k < H) {
+                const float4 u = *reinterpret_cast<const float4*>(ur + k);
+                y[i] = make_float4(act_silu_gate(y[i].x, u.x), act_silu_gate(y[i].y, u.y),
+                                   act_silu_gate(y[i].z, u.z), act_silu_gate(y[i].w, u.w));
+            }
+        }
+    }
+    if (a.out) {
+        float* orow = a.out + (size_t)row * a.ldo;
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int k = 4 * t + 1024 * i;
+            if (k < H) *reinterpret_cast<float4*>(orow + k) = y[i];
+        }
+    }
+    if (!a.q) return;  // block-uniform
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; i++)
+        if (4 * t + 1024 * i < H)
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(y[i].x), fabsf(y[i].y)), fmaxf(fabsf(y[i].z), fabsf(y[i].w))));
+    amax = wave_max_f32(amax);
+    if ((t & 63) == 0) red[t >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float s = row_scale(amax), inv = 1.0f / s;
+    if (t == 0) a.qs[row] = s;
+    if (a.q_panel) {
+        const size_t pstride = (size_t)panel_rows(a.rows) * 64;
+        int8_t* qr = a.q + (size_t)row * 64;
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int k = 4 * t + 1024 * i;
+            if (k < H) *reinterpret_cast<uint32_t*>(qr + (k >> 6) * pstride + (k & 63)) = q8x4(y[i], inv);
+        }
+        for (int k = H + 4 * t; k < ((H + 63) & ~63); k += 1024)
+            *reinterpret_cast<uint32_t*>(qr + (k >> 6) * pstride + (k & 63)) = 0u;
+    } else {
+        int8_t* qr = a.q + (size_t)row * a.ldq;
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int k = 4 * t + 1024 * i;
+            if (k < H) *reinterpret_cast<uint32_t*>(qr + k) = q8x4(y[i], inv);
+        }
+        for (int k = H + 4 * t; k < a.ldq; k += 1024) *reinterpret_cast<uint32_t*>(qr + k) = 0u;
+    }
+}
+
 template <int OP>
 void launch_rowq_op(const RowQArgs& a, hipStream_t st) {
+    if constexpr (OP == 0 || OP == 3) {
+        // wide rows of an element-wise op (and no second output): a block per row
+        if (!a.add && a.H >= 1024) {
+            const int nw = (a.H + 1023) / 1024;
+            if (nw <= 1) rowq_wide_kernel<OP, 1><<<a.rows, 256, 0, st>>>(a);
+            else if (nw <= 2) rowq_wide_kernel<OP, 2><<<a.rows, 256, 0, st>>>(a);
+            else rowq_wide_kernel<OP, 4><<<a.rows, 256, 0, st>>>(a);
+            return;
+        }
+    }
     const int nv = (a.H + 255) / 256;
     const dim3 grid((a.rows + 3) / 4), block(256);
     if (nv <= 1) rowq_kernel<OP, 1><<<grid, block, 0, st>>>(a);

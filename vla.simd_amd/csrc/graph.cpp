@@ -104,15 +104,18 @@ static GemmArgs gemm_args(const DLinear& L, float* out, int ldo, int seq, int ac
 // kernel beats row kernel + GEMM only while each SIMD has a row or so: on
 // MI355X at 16 rows it saved 4 us of 9.7 (RMSNorm, N = 4096, K = 720); at 50
 // rows it lost 3 us (RMSNorm, N = 4096) to 22 us (silu_gate, K = 2048).
-// VLA_HIP_ROWOP_FUSE=0 turns it off.
+// The identity op (quantize only) is cheap enough to repeat up to 64 rows
+// on a narrow output: 50 x 720 x 960 ran 8.6 us fused against 9.7 us as
+// quantize + GEMM. VLA_HIP_ROWOP_FUSE=0 turns it off.
 constexpr int kRowopFuseMaxRows = 16;
 
-static bool fuse_rowop(int op, int seq, int K) {
+static bool fuse_rowop(int op, int seq, int K, int N) {
     static const bool on = [] {
         const char* e = std::getenv("VLA_HIP_ROWOP_FUSE");
         return !(e && e[0] == '0');
     }();
-    return on && seq <= kRowopFuseMaxRows && rowop_gemm_fits(op, seq, K);
+    const bool cheap = seq <= kRowopFuseMaxRows || (op == 0 && seq <= 64 && N <= 1024);
+    return on && cheap && rowop_gemm_fits(op, seq, K);
 }
 
 static bool overlaps(const float* p, size_t pn, const float* q, size_t qn) {
@@ -122,7 +125,7 @@ static bool overlaps(const float* p, size_t pn, const float* q, size_t qn) {
 // Runs the row op r inside the GEMM when the fused kernel takes this shape.
 static bool try_rowop_gemm(const Ctx& c, const DLinear& L, const RowQArgs& r, float* out, int ldo, int seq,
                            int act, int acc, int n0, int n1) {
-    if (!fuse_rowop(r.op, seq, L.K) || L.q8->ldw() % 16) return false;
+    if (!fuse_rowop(r.op, seq, L.K, n1 - n0) || L.q8->ldw() % 16) return false;
     const size_t on = (size_t)(seq - 1) * ldo + (n1 - n0);
     if (overlaps(out, on, r.x, (size_t)(seq - 1) * r.ldx + L.K)) return false;
     if (r.op == 3 && overlaps(out, on, r.u, (size_t)(seq - 1) * r.ldu + L.K)) return false;
@@ -177,7 +180,7 @@ void linear(const Ctx& c, const DLinear& L, const In& in, float* out, int ldo, i
             gemm_q(c, L, in.q, out, ldo, seq, act, acc, n0, n1);
         } else {
             VLA_REQUIRE(in.f, "linear: no input");
-            if (seq <= kRowopFuseMaxRows && in.ldf % 4 == 0 && (reinterpret_cast<uintptr_t>(in.f) & 15) == 0) {
+            if (seq <= 64 && in.ldf % 4 == 0 && (reinterpret_cast<uintptr_t>(in.f) & 15) == 0) {
                 RowQArgs r;  // identity row op: quantize_rows_panel's bytes and scales
                 r.op = 0;
                 r.x = in.f;
@@ -213,7 +216,7 @@ In rowop_for(const Ctx& c, const DLinear& L, RowQArgs r, float* f, int ldf, int 
     }
     in.f = f;
     in.ldf = ldf;
-    if (L.int8() && !f && !r.add && fuse_rowop(r.op, r.rows, L.K)) {
+    if (L.int8() && !f && !r.add && fuse_rowop(r.op, r.rows, L.K, L.N)) {
         in.quantized = false;
         in.deferred = true;
         in.r = r;
