@@ -25,6 +25,12 @@ BASELINE.json configs[2..4] (ACT transformer, Octo-base transformer, SmolVLA
 chunk) on random-init checkpoints written in the reference's file layouts:
 the device graph (one HIP-graph replay per forward, inputs resident in HBM,
 HIP events) next to the reference's own graph on this host's cores.
+
+conv_resnet18_480x640 = conv2d_i8 over ResNet-18's convolutions at 480 x 640
+(ACT's backbone), per distinct layer: device time per call, its roofline
+fraction, and the reference's conv2d_i8 on this host. Long-K GEMMs of a few
+hundred rows in the sweep run with a split-K workspace (dense_linear_i8 takes
+caller-owned scratch in the reference too); the values do not change.
 """
 
 from __future__ import annotations
@@ -339,6 +345,77 @@ def policy_latency(vla, torch, stream_obj, with_cpu=True, models=("act", "octo",
     return out
 
 
+# ResNet-18 at 480 x 640 (ACT's backbone; src/models/act): (H, W, Cin, Cout, k, stride, pad, count)
+RESNET18_480x640 = [(480, 640, 3, 64, 7, 2, 3, 1), (120, 160, 64, 64, 3, 1, 1, 4),
+                    (120, 160, 64, 128, 3, 2, 1, 1), (60, 80, 128, 128, 3, 1, 1, 3),
+                    (120, 160, 64, 128, 1, 2, 0, 1), (60, 80, 128, 256, 3, 2, 1, 1),
+                    (30, 40, 256, 256, 3, 1, 1, 3), (60, 80, 128, 256, 1, 2, 0, 1),
+                    (30, 40, 256, 512, 3, 2, 1, 1), (15, 20, 512, 512, 3, 1, 1, 3),
+                    (30, 40, 256, 512, 1, 2, 0, 1)]
+
+
+def conv_resnet18(vla, torch, stream_obj, with_cpu=True):
+    """conv2d_i8 (section f.3 of the hot path) over ResNet-18's 20 convolutions at
+    480 x 640: per distinct layer the device time per call (vla_conv2d_i8_dev,
+    HIP events on the launch stream, inputs resident in HBM), its roofline
+    (max(2*npix*Cout*K / int8 peak, algorithmic bytes / HBM peak) with bytes =
+    4 H W Cin + Cout K + 8 Cout + 4 npix Cout), and the reference's conv2d_i8 on
+    this host (oracle/_ref, weights packed once)."""
+    ob = None
+    if with_cpu:
+        from oracle import bindings as ob
+        if not ob.ref_available():
+            ob = None
+    st = stream_obj.cuda_stream
+    rows, g_tot, c_tot = [], 0.0, 0.0
+    for (H, Wd, Cin, Cout, k, s, p, count) in RESNET18_480x640:
+        r = np.random.default_rng(H * 7 + Cin)
+        x = r.normal(0.0, 1.0, (H, Wd, Cin)).astype(np.float32)
+        K = k * k * Cin
+        W = r.uniform(-0.2, 0.2, (Cout, K)).astype(np.float32)
+        b = r.normal(0.0, 0.02, Cout).astype(np.float32)
+        lin = vla.LinearI8.from_f32(W, b)
+        Ho, Wo = (H + 2 * p - k) // s + 1, (Wd + 2 * p - k) // s + 1
+        xd = torch.from_numpy(x).cuda()
+        out = torch.empty((Ho, Wo, Cout), device="cuda")
+        work = torch.empty(vla.conv2d_i8_workspace_bytes(H, Wd, Cin, Cout, k, s, p), dtype=torch.uint8,
+                           device="cuda")
+        call = lambda: vla.conv2d_i8_dev(lin, out, xd, k, s, p, work, stream=st)
+        for _ in range(3):
+            call()
+        stream_obj.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream_obj)
+        for _ in range(20):
+            call()
+        e1.record(stream_obj)
+        e1.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / 20
+        npix = Ho * Wo
+        ops = 2.0 * npix * Cout * K
+        byt = 4.0 * H * Wd * Cin + Cout * K + 8.0 * Cout + 4.0 * npix * Cout
+        roof = max(ops / (PEAK_INT8_TOPS * 1e12), byt / (PEAK_HBM_GBS * 1e9)) * 1e6
+        row = {"layer": f"{H}x{Wd}x{Cin}->{Cout} k{k} s{s} p{p}", "count": count, "gpu_us": round(us, 2),
+               "tops": round(ops / us / 1e6, 1), "roof_us": round(roof, 2), "frac": round(roof / us, 4)}
+        g_tot += count * us
+        if ob is not None:
+            Wq, ws, blob = ob.ref_pack_weights(W) if Cout % 16 == 0 else (None, None, None)
+            if blob is not None:
+                o = np.empty((Ho, Wo, Cout), np.float32)
+                L = ob.ref()
+                f = lambda: L.ref_conv2d_i8_packed(ob._p(o), ob._p(x), ob._p(blob), ob._p(ws), ob._p(b), H, Wd,
+                                                   Cin, Cout, k, s, p)
+                row["cpu_ref_us"] = round(_time_cpu(f, min_calls=2, min_s=0.3) * 1e3, 1)
+                c_tot += count * row["cpu_ref_us"]
+        rows.append(row)
+        print(f"  conv {row}", file=sys.stderr, flush=True)
+    out = {"layers": rows, "gpu_ms_total": round(g_tot / 1e3, 4)}
+    if ob is not None:
+        out["cpu_ref_ms_total"] = round(c_tot / 1e3, 3)
+        out["cpu_ref_threads"] = int(ob.ref().ref_omp_max_threads())
+    return out
+
+
 def m_tokens_act(c):
     return c["n_1d"] + c["n_cams"] * c["fh"] * c["fw"]
 
@@ -354,6 +431,8 @@ def main():
     ap.add_argument("--policy-only", action="store_true",
                     help="only the per-chunk policy latency leg (for rocprofv3 runs)")
     ap.add_argument("--models", default="act,octo,smolvla", help="policy graphs to time")
+    ap.add_argument("--no-conv", action="store_true", help="skip the ResNet-18 conv2d_i8 leg")
+    ap.add_argument("--conv-only", action="store_true", help="only the ResNet-18 conv2d_i8 leg")
     ap.add_argument("--profile-only", action="store_true",
                     help="only the dominant GEMM, back to back (for rocprofv3 runs)")
     args = ap.parse_args()
@@ -375,6 +454,11 @@ def main():
     stream_obj = torch.cuda.Stream()
     torch.cuda.set_stream(stream_obj)
     stream = stream_obj.cuda_stream
+
+    if args.conv_only:
+        print(json.dumps({"conv_resnet18_480x640": conv_resnet18(vla, torch, stream_obj,
+                                                                 with_cpu=not args.no_cpu)}), flush=True)
+        return
 
     if args.policy_only:
         print(json.dumps({"policy_latency_ms": policy_latency(
@@ -471,6 +555,7 @@ def main():
 
     cpu = None if args.no_cpu else cpu_baseline(synth)
     policy = None if args.no_policy else policy_latency(vla, torch, stream_obj, with_cpu=not args.no_cpu)
+    conv = None if args.no_conv else conv_resnet18(vla, torch, stream_obj, with_cpu=not args.no_cpu)
 
     print(json.dumps({
         "metric": "int8 GEMM TOPS (% MFMA peak) + per-chunk policy latency ms, batch 1",
@@ -482,6 +567,7 @@ def main():
                                "calls (device quantize + i8 MFMA GEMM) per step",
                    "shapes": len(shapes), "wall_s_timed": round(wall, 3)},
         "roofline": roofline, "cpu_baseline": cpu, "policy_latency_ms": policy, "sweep": rows,
+        "conv_resnet18_480x640": conv,
     }), flush=True)
 
 

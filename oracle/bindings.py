@@ -100,6 +100,7 @@ def ref():
         L.ref_relu.argtypes = [P, i]
         L.ref_dense_linear.argtypes = [P, P, P, P, i, i, i]
         L.ref_conv2d_i8.argtypes = [P, P, P, P, i, i, i, i, i, i, i]
+        L.ref_conv2d_i8_packed.argtypes = [P, P, P, P, P, i, i, i, i, i, i, i]
         _ref = L
     return _ref
 

@@ -136,6 +136,15 @@ REF_API void ref_conv2d_i8(float* out, const float* x, const float* W, const flo
                     Cout, k, stride, pad, scratch);
 }
 
+/* conv2d_i8 with weights already packed by ref_pack_weights_i8 (the timed
+ * CPU baseline: nn::Conv2d::forward's int8 branch, src/nn/conv.cpp:63-69). */
+REF_API void ref_conv2d_i8_packed(float* out, const float* x, const int8_t* Wq, const float* wscale,
+                                  const float* bias, int H, int Wd, int Cin, int Cout, int k, int stride,
+                                  int pad) {
+    static thread_local std::vector<int8_t> scratch;
+    tcpu::conv2d_i8(out, x, Wq, wscale, bias, H, Wd, Cin, Cout, k, stride, pad, scratch);
+}
+
 REF_API void ref_gelu_tanh(float* x, int n) { tcpu::gelu_tanh(x, n); }
 REF_API void ref_gelu_erf(float* x, int n) { tcpu::gelu_erf(x, n); }
 REF_API void ref_silu_gate(float* out, const float* g, const float* u, int n) {
