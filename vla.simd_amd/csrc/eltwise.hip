@@ -24,11 +24,6 @@ namespace vla {
 namespace hip {
 namespace {
 
-__device__ __forceinline__ double wave_sum(double v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
 
 __global__ __launch_bounds__(256) void layernorm_kernel(float* out, const float* x, const float* w,
                                                         const float* b, int rows, int H, float eps) {
@@ -40,13 +35,13 @@ __global__ __launch_bounds__(256) void layernorm_kernel(float* out, const float*
 
     double s = 0.0;
     for (int k = lane; k < H; k += 64) s += (double)xr[k];
-    const double mean = wave_sum(s) / H;
+    const double mean = wave_sum_f64(s) / H;
     double v = 0.0;
     for (int k = lane; k < H; k += 64) {
         const double d = (double)xr[k] - mean;
         v += d * d;
     }
-    const double var = wave_sum(v);
+    const double var = wave_sum_f64(v);
     const float inv = (float)(1.0 / sqrt(var / H + (double)eps));
     for (int k = lane; k < H; k += 64) {
         const float c = (float)((double)xr[k] - mean);
@@ -66,7 +61,7 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(float* out, const float* x
         const double d = (double)xr[k];
         ss += d * d;
     }
-    ss = wave_sum(ss);
+    ss = wave_sum_f64(ss);
     const float inv = (float)(1.0 / sqrt(ss / H + (double)eps));
     for (int k = lane; k < H; k += 64) orow[k] = xr[k] * inv * w[k];
 }

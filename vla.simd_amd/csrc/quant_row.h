@@ -10,17 +10,14 @@
 
 #include <hip/hip_runtime.h>
 
+#include "wave.h"
+
 #include <cfloat>
 #include <cstdint>
 
 namespace vla {
 namespace hip {
 
-__device__ __forceinline__ float wave_max_f32(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
 
 __device__ __forceinline__ float row_scale(float amax) {
     float s = 1.0f;

@@ -17,12 +17,6 @@
 namespace vla {
 namespace hip {
 
-__device__ __forceinline__ double wave_sum_f64(double v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
 // y <- the row xr[0, H) (zero past H). Rows are 16-byte aligned.
 template <int NV>
 __device__ __forceinline__ void rowop_load(float4 (&y)[NV], const float* xr, int H, int lane) {
