@@ -34,6 +34,7 @@
 #include "common.h"
 
 #include <cfloat>
+#include <cstdlib>
 
 namespace vla {
 namespace hip {
@@ -357,6 +358,17 @@ void launch_w(const AttnArgs& a, hipStream_t st) {
     attn_fwd<HDP, KT, W><<<dim3((a.seq_q + 15) / 16, a.n_q), W * 64, C::LDS, st>>>(a);
 }
 
+// VLA_HIP_ATTN_W=<1|2|4|8> forces the waves per block (A/B runs; the values
+// only change by fp32 summation order across waves).
+int forced_waves() {
+    static const int w = [] {
+        const char* e = std::getenv("VLA_HIP_ATTN_W");
+        const int v = e ? std::atoi(e) : 0;
+        return v == 1 || v == 2 || v == 4 || v == 8 ? v : 0;
+    }();
+    return w;
+}
+
 // W: enough waves that each walks a few key tiles, capped at WMAX (LDS).
 template <int HDP, int KT, int WMAX>
 void run_attn(const AttnArgs& a, hipStream_t st) {
@@ -365,7 +377,14 @@ void run_attn(const AttnArgs& a, hipStream_t st) {
         const int e = a.seq_q + a.causal_offset;
         kv = e < 1 ? 1 : (e < kv ? e : kv);
     }
-    const int tiles = (kv + KT - 1) / KT;
+    int tiles = (kv + KT - 1) / KT;
+    // grids of 1.5+ blocks per CU (Octo's 658-690 tokens x 12 heads): 4 waves,
+    // so two blocks share a CU and hide each other's load latency (measured
+    // 1.268 -> 1.235 ms and 1.457 -> 1.335 ms per Octo forward); smaller grids
+    // (ACT, SmolVLA) keep 8 waves per block (their latency grew with 4)
+    const long blocks = (long)((a.seq_q + 15) / 16) * a.n_q;
+    if (blocks >= 384 && tiles > 4) tiles = 4;
+    if (const int fw = forced_waves()) tiles = fw;
     if (tiles <= 1) launch_w<HDP, KT, 1>(a, st);
     else if (tiles <= 2 || WMAX == 2) launch_w<HDP, KT, 2>(a, st);
     else if (tiles <= 4 || WMAX == 4) launch_w<HDP, KT, (WMAX < 4 ? WMAX : 4)>(a, st);
