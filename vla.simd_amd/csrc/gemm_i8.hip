@@ -1223,7 +1223,9 @@ Tile pick_tile(int M, int N, int K) {
     }
     // Measured on MI355X over the BASELINE sweep (bench.py, forced tiles):
     // short K (<= 1024) is dominated by the fp32 output write and wants many
-    // small register-staged tiles in flight. Long K wants the LDS-DMA pipeline
+    // small register-staged tiles in flight: 64 x 128 only from two such tiles
+    // per CU (Octo's 658 x 3072 x 768 MLP runs faster as 528 64 x 64 tiles than
+    // as 264 64 x 128 ones: 1.227 -> 1.183 ms per forward). Long K wants the LDS-DMA pipeline
     // with the largest tile that still fills the chip: 256 x 256 with 8 waves
     // when there are two tiles per CU, else 256 x 128 with 8 waves when every
     // CU gets a tile, else smaller tiles; the fragment-pipelined main loop
@@ -1231,7 +1233,7 @@ Tile pick_tile(int M, int N, int K) {
     // 256 x 256 form needs more than 256 VGPRs for its fragments and
     // accumulators, and spills.
     auto tiles = [&](int bm, int bn) { return (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-    if (K <= 1024) return tiles(64, 128) >= kCUs ? Tile{64, 128, 64, 0} : Tile{64, 64, 64, 0};
+    if (K <= 1024) return tiles(64, 128) >= 2 * kCUs ? Tile{64, 128, 64, 0} : Tile{64, 64, 64, 0};
     if (tiles(256, 256) >= 2 * kCUs) return {256, 256, 128, 2, 8, true};
     if (tiles(256, 128) >= kCUs) return {256, 128, 128, 3, 8, true};
     if (tiles(128, 128) >= kCUs) return {128, 128, 64, 4};
