@@ -312,8 +312,29 @@ def _lat_smolvla(vla, torch, ck, ob, tmp, stream_obj):
     return row
 
 
-def policy_latency(vla, torch, stream_obj, with_cpu=True, models=("act", "octo", "smolvla")):
-    """Per-chunk latency of BASELINE.json configs[2..4] at batch 1: the device
+def _lat_siglip(vla, torch, ck, ob, tmp, stream_obj):
+    """SmolVLA's SigLIP vision tower + connector per camera image: 12 x 768
+    layers over 1024 patches (512 x 512), pixel shuffle to 64 tokens, the
+    vision int8 bits 1|2|4|8 (SMOLVLA_INT8=15)."""
+    dev, st = torch.device("cuda"), stream_obj.cuda_stream
+    c = ck.SIGLIP_BASE
+    d = ck.write_siglip(os.path.join(tmp, "vit"), c)
+    px = ck.siglip_inputs(c)
+    m = vla.SiglipVision(d, 15)
+    tp = torch.from_numpy(px).to(dev)
+    to = torch.empty((c["n_img_tok"], c["mm_out"]), dtype=torch.float32, device=dev)
+    gpu = _time_calls(torch, lambda: m.encode_dev(tp, to, st), stream_obj)
+    row = {"gpu_ms": round(gpu, 4), "patches": c["n_patches"], "int8_mask": 15,
+           "int8_layers": m.int8_layers, "graph_nodes": m.graph_nodes}
+    if ob is not None:
+        r = ob.RefSiglip(d, 15, c["n_img_tok"], c["mm_out"])
+        row["cpu_ref_ms"] = round(_time_cpu(lambda: r.encode(px)), 3)
+    return row
+
+
+def policy_latency(vla, torch, stream_obj, with_cpu=True, models=("act", "octo", "smolvla", "siglip")):
+    """Per-chunk latency of BASELINE.json configs[2..4] at batch 1, and of
+    SmolVLA's SigLIP vision tower per camera image: the device
     graphs (one captured HIP graph per forward, inputs resident in HBM) and the
     reference's own graphs (oracle/_ref) on this host, on the same random-init
     checkpoints and inputs."""
@@ -340,6 +361,9 @@ def policy_latency(vla, torch, stream_obj, with_cpu=True, models=("act", "octo",
         if "smolvla" in models:
             out["smolvla"] = _lat_smolvla(vla, torch, ck, ob, tmp, stream_obj)
             print(f"  SmolVLA chunk: {out['smolvla']}", file=sys.stderr, flush=True)
+        if "siglip" in models:
+            out["siglip"] = _lat_siglip(vla, torch, ck, ob, tmp, stream_obj)
+            print(f"  SigLIP vision tower: {out['siglip']}", file=sys.stderr, flush=True)
     if ob is not None:
         out["cpu_ref_threads"] = int(ob.ref().ref_omp_max_threads())
     return out
@@ -430,7 +454,7 @@ def main():
     ap.add_argument("--no-policy", action="store_true", help="skip the per-chunk policy latency leg")
     ap.add_argument("--policy-only", action="store_true",
                     help="only the per-chunk policy latency leg (for rocprofv3 runs)")
-    ap.add_argument("--models", default="act,octo,smolvla", help="policy graphs to time")
+    ap.add_argument("--models", default="act,octo,smolvla,siglip", help="policy graphs to time")
     ap.add_argument("--no-conv", action="store_true", help="skip the ResNet-18 conv2d_i8 leg")
     ap.add_argument("--conv-only", action="store_true", help="only the ResNet-18 conv2d_i8 leg")
     ap.add_argument("--profile-only", action="store_true",

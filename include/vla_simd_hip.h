@@ -469,6 +469,27 @@ VLA_API int32_t vla_smolvla_tf_chunk_dev(vla_smolvla_tf* h, const float* prefix,
                                          int32_t n_prefix, const float* noise, float* actions,
                                          void* stream);
 
+
+/* SmolVLA's SigLIP vision tower and connector (SiglipVision,
+ * src/models/smolvla/siglip_vision.h:23-59): <dir>/vit.meta + vit.bin as
+ * SiglipVision::load (siglip_vision.cpp:21-140); int8_mask the vision bits of
+ * SMOLVLA_INT8 (smolvla_model.cpp:127-140: 1 attention, 2 w1, 4 w2, 8 patch
+ * embedding + modality projection). */
+typedef struct vla_siglip_tf vla_siglip_tf;
+VLA_API vla_siglip_tf* vla_siglip_tf_load(const char* dir, int32_t int8_mask);
+VLA_API void vla_siglip_tf_free(vla_siglip_tf* h);
+VLA_API int32_t vla_siglip_tf_img(const vla_siglip_tf* h);
+VLA_API int32_t vla_siglip_tf_n_tokens(const vla_siglip_tf* h);
+VLA_API int32_t vla_siglip_tf_out_dim(const vla_siglip_tf* h);
+VLA_API int32_t vla_siglip_tf_int8_layers(const vla_siglip_tf* h);
+VLA_API int32_t vla_siglip_tf_graph_nodes(const vla_siglip_tf* h);
+/* SiglipVision::encode (siglip_vision.cpp:151-202): pixels [3, img, img]
+ * (CHW, the preprocessed image) -> out [n_tokens, out_dim], the image tokens
+ * before SmolvlaModel scales them by sqrt(hidden). The _dev form takes device
+ * pointers (16-byte aligned) and a stream and does not synchronize. */
+VLA_API int32_t vla_siglip_tf_encode(vla_siglip_tf* h, const float* pixels, float* out);
+VLA_API int32_t vla_siglip_tf_encode_dev(vla_siglip_tf* h, const float* pixels, float* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

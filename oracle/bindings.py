@@ -403,10 +403,34 @@ def _ref_models():
     L.ref_smolvla_chunk.argtypes, L.ref_smolvla_chunk.restype = [P, P, P, i, P, P], i
     L.ref_smolvla_chunk_len.argtypes, L.ref_smolvla_chunk_len.restype = [P], i
     L.ref_smolvla_max_action_dim.argtypes, L.ref_smolvla_max_action_dim.restype = [P], i
+    L.ref_siglip_load.argtypes, L.ref_siglip_load.restype = [ctypes.c_char_p, i], P
+    L.ref_siglip_free.argtypes = [P]
+    L.ref_siglip_encode.argtypes = [P, P, P]
     L.ref_mount_read.argtypes = [ctypes.c_char_p, ctypes.c_char_p, P, ctypes.c_longlong]
     L.ref_mount_read.restype = ctypes.c_longlong
     L._models_declared = True
     return L
+
+
+class RefSiglip:
+    """The reference's SigLIP vision tower + connector (SiglipVision::encode)."""
+
+    def __init__(self, dirpath, int8_mask, n_tok, mm_out):
+        L = _ref_models()
+        self.h = L.ref_siglip_load(dirpath.encode(), int8_mask)
+        if not self.h:
+            raise RuntimeError(f"reference SiglipVision::load failed for {dirpath}")
+        self.n_tok, self.mm_out = n_tok, mm_out
+
+    def encode(self, pixels):
+        out = np.empty((self.n_tok, self.mm_out), np.float32)
+        px = _f32(pixels)
+        _ref_models().ref_siglip_encode(self.h, _p(px), _p(out))
+        return out
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            _ref_models().ref_siglip_free(self.h)
 
 
 def ref_mount_read(path, rel):

@@ -25,6 +25,7 @@
 #include "models/act/act_transformer.h"
 #include "models/octo/octo_transformer.h"
 #include "models/smolvla/action_expert.h"
+#include "models/smolvla/siglip_vision.h"
 #include "models/smolvla/smollm2_lm.h"
 
 #include <cstdint>
@@ -157,6 +158,48 @@ REF_API void* ref_smolvla_load(const char* dir, int int8_mask) {
         std::fprintf(stderr, "ref_smolvla_load: %s\n", e.what());
         return nullptr;
     }
+}
+
+/* SmolVLA's SigLIP vision tower + connector (SiglipVision, siglip_vision.cpp),
+ * with SmolvlaModel::apply_int8's vision bits (smolvla_model.cpp:49, 127-140):
+ * 1 attention, 2 w1, 4 w2, 8 patch embed + modality projection. */
+REF_API void* ref_siglip_load(const char* dir, int int8_mask) {
+    try {
+        const io::Mount mount(dir);
+        if (!mount.ok()) return nullptr;
+        auto* v = new SiglipVision();
+        if (!v->load(dir)) {
+            delete v;
+            return nullptr;
+        }
+        for (nn::EncoderLayer& l : v->layers) {
+            if (int8_mask & 1) {
+                l.attn.wq.init_int8();
+                l.attn.wk.init_int8();
+                l.attn.wv.init_int8();
+                l.attn.wo.init_int8();
+            }
+            if (int8_mask & 2) l.w1.init_int8();
+            if (int8_mask & 4) l.w2.init_int8();
+        }
+        if (int8_mask & 8) {
+            v->patch_lin.init_int8();
+            v->mm_proj.init_int8();
+        }
+        return v;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "ref_siglip_load: %s\n", e.what());
+        return nullptr;
+    }
+}
+
+REF_API void ref_siglip_free(void* h) { delete static_cast<SiglipVision*>(h); }
+
+/* pixels [3, img, img] CHW in [-1, 1] -> out [n_img_tok, mm_out] */
+REF_API void ref_siglip_encode(void* h, const float* pixels, float* out) {
+    auto* v = static_cast<SiglipVision*>(h);
+    nn::Scratch sc;
+    v->encode(pixels, out, sc);
 }
 
 REF_API void ref_smolvla_free(void* h) { delete static_cast<RefSmolvla*>(h); }

@@ -65,6 +65,9 @@ EXPORTS = (
     "vla_smolvla_tf_load", "vla_smolvla_tf_free", "vla_smolvla_tf_chunk",
     "vla_smolvla_tf_max_action_dim", "vla_smolvla_tf_hidden", "vla_smolvla_tf_int8_layers",
     "vla_smolvla_tf_graph_nodes", "vla_smolvla_tf_chunk_run", "vla_smolvla_tf_chunk_dev",
+    "vla_siglip_tf_load", "vla_siglip_tf_free", "vla_siglip_tf_img", "vla_siglip_tf_n_tokens",
+    "vla_siglip_tf_out_dim", "vla_siglip_tf_int8_layers", "vla_siglip_tf_graph_nodes",
+    "vla_siglip_tf_encode", "vla_siglip_tf_encode_dev",
 )
 
 
@@ -194,6 +197,15 @@ def _declare(L):
         "vla_smolvla_tf_graph_nodes": (i32, [P]),
         "vla_smolvla_tf_chunk_run": (i32, [P, P, P, i32, P, P]),
         "vla_smolvla_tf_chunk_dev": (i32, [P, P, P, i32, P, P, P]),
+        "vla_siglip_tf_load": (P, [c_char_p, i32]),
+        "vla_siglip_tf_free": (None, [P]),
+        "vla_siglip_tf_img": (i32, [P]),
+        "vla_siglip_tf_n_tokens": (i32, [P]),
+        "vla_siglip_tf_out_dim": (i32, [P]),
+        "vla_siglip_tf_int8_layers": (i32, [P]),
+        "vla_siglip_tf_graph_nodes": (i32, [P]),
+        "vla_siglip_tf_encode": (i32, [P, P, P]),
+        "vla_siglip_tf_encode_dev": (i32, [P, P, P, P]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -772,3 +784,32 @@ class SmolvlaChunk(_Handle):
         pad = np.ascontiguousarray(pad, dtype=np.int32)
         _call("vla_smolvla_tf_chunk_dev", self.h, _dp(prefix), _ptr(pad), prefix.shape[0], _dp(noise),
               _dp(out), _stream(stream))
+
+
+class SiglipVision(_Handle):
+    """Device SigLIP vision tower + connector of SmolVLA (vla_siglip_tf_*)."""
+
+    _load, _free = "vla_siglip_tf_load", "vla_siglip_tf_free"
+
+    def __init__(self, dirpath: str, int8_mask: int = 15):
+        super().__init__(lib().vla_siglip_tf_load(dirpath.encode(), int8_mask))
+        L = lib()
+        self.img, self.n_tokens = L.vla_siglip_tf_img(self.h), L.vla_siglip_tf_n_tokens(self.h)
+        self.out_dim = L.vla_siglip_tf_out_dim(self.h)
+        self.int8_layers = L.vla_siglip_tf_int8_layers(self.h)
+
+    @property
+    def graph_nodes(self):
+        return lib().vla_siglip_tf_graph_nodes(self.h)
+
+    def encode(self, pixels):
+        pixels = _f32(pixels)
+        if pixels.shape != (3, self.img, self.img):
+            raise ValueError(f"pixels must be [3, {self.img}, {self.img}]")
+        out = np.empty((self.n_tokens, self.out_dim), np.float32)
+        _call("vla_siglip_tf_encode", self.h, _ptr(pixels), _ptr(out))
+        return out
+
+    def encode_dev(self, pixels, out, stream=None):
+        _call("vla_siglip_tf_encode_dev", self.h, _dp(pixels), _dp(out), _stream(stream))
+

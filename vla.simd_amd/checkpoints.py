@@ -222,6 +222,66 @@ def write_smolvla(dirpath: str, cfg: dict = SMOLVLA_BASE, seed: int = synth.BASE
     return dirpath
 
 
+# SmolVLM2-500M's SigLIP vision tower (src/models/smolvla/siglip_vision.h:23-38):
+# 512 x 512 images, 16 x 16 patches (1024), 12 layers of 768 (12 heads, MLP
+# 3072 gelu-tanh), pixel shuffle by 4 into 64 tokens, projection to 960.
+SIGLIP_BASE = dict(hidden=768, n_heads=12, head_dim=64, inter=3072, n_layers=12, patch=16, img=512,
+                   n_patches=1024, ln_eps=1e-6, scale_factor=4, mm_out=960, n_img_tok=64)
+
+
+def write_siglip(dirpath: str, cfg: dict = SIGLIP_BASE, seed: int = synth.BASE_SEED) -> str:
+    """vit.meta + vit.bin as SiglipVision::load reads them
+    (src/models/smolvla/siglip_vision.cpp:21-140): an fp32 region (patch bias,
+    position embedding, per layer ln1 w/b, q/k/v/o biases, ln2 w/b, fc1/fc2
+    biases, post-LN w/b) then a bf16 region (patch weight [H, 3 p p], per
+    layer Wq Wk Wv Wo fc1 fc2, the modality projection [mm_out, H sf sf])."""
+    os.makedirs(dirpath, exist_ok=True)
+    c = cfg
+    H, I, NL, P = c["hidden"], c["inter"], c["n_layers"], c["patch"]
+    PD, NP, SD = 3 * P * P, c["n_patches"], c["hidden"] * c["scale_factor"] ** 2
+    _meta(os.path.join(dirpath, "vit.meta"), {k: c[k] for k in (
+        "hidden", "n_heads", "head_dim", "inter", "n_layers", "patch", "img", "n_patches", "ln_eps",
+        "scale_factor", "mm_out", "n_img_tok")})
+    f32 = [synth.normal("vit.patch.b", (H,), 0.02, seed), synth.normal("vit.pos", (NP, H), 0.02, seed)]
+    for L in range(NL):
+        f32 += [1.0 + synth.normal(f"vit.l{L}.ln1.s", (H,), 0.02, seed),
+                synth.normal(f"vit.l{L}.ln1.b", (H,), 0.02, seed)]
+        f32 += [synth.normal(f"vit.l{L}.b{n}", (H,), 0.02, seed) for n in "qkvo"]
+        f32 += [1.0 + synth.normal(f"vit.l{L}.ln2.s", (H,), 0.02, seed),
+                synth.normal(f"vit.l{L}.ln2.b", (H,), 0.02, seed),
+                synth.normal(f"vit.l{L}.fc1.b", (I,), 0.02, seed),
+                synth.normal(f"vit.l{L}.fc2.b", (H,), 0.02, seed)]
+    f32 += [1.0 + synth.normal("vit.post.s", (H,), 0.02, seed), synth.normal("vit.post.b", (H,), 0.02, seed)]
+
+    def w(name, N, K):
+        a = 1.0 / math.sqrt(K)
+        return _bf16(synth.uniform(name, (N, K), -a, a, seed))
+
+    with open(os.path.join(dirpath, "vit.bin"), "wb") as f:
+        for p in f32:
+            f.write(np.asarray(p, np.float32).tobytes())
+        f.write(w("vit.patch.w", H, PD).tobytes())
+        for L in range(NL):
+            for n in "qkvo":
+                f.write(w(f"vit.l{L}.w{n}", H, H).tobytes())
+            f.write(w(f"vit.l{L}.fc1.w", I, H).tobytes())
+            f.write(w(f"vit.l{L}.fc2.w", H, I).tobytes())
+        f.write(w("vit.mm_proj", c["mm_out"], SD).tobytes())
+    return dirpath
+
+
+def siglip_inputs(cfg: dict = SIGLIP_BASE, seed: int = synth.BASE_SEED):
+    """pixels [3, img, img] CHW, uniform in [-1, 1] (normalized image)."""
+    return synth.uniform("vit.in.pixels", (3, cfg["img"], cfg["img"]), -1.0, 1.0, seed)
+
+
+def siglip_gguf_layout(cfg: dict = SIGLIP_BASE) -> dict:
+    """vit.bin as the converter stores it: the fp32 region, then bf16."""
+    H, I, NL, NP = cfg["hidden"], cfg["inter"], cfg["n_layers"], cfg["n_patches"]
+    n_f32 = H + NP * H + NL * (2 * H + 4 * H + 2 * H + I + H) + 2 * H
+    return {"vit.bin": [("F32", n_f32 * 4), ("BF16", None)]}
+
+
 def smolvla_inputs(cfg: dict = SMOLVLA_BASE, seed: int = synth.BASE_SEED, n_pad: int = 0):
     """prefix [n_prefix, hidden] ~ N(0,1), pad [n_prefix] (n_pad text slots
     before the state token marked as padding), noise [chunk, max_action_dim] ~ N(0,1)."""

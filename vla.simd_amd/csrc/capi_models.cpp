@@ -27,6 +27,9 @@ struct vla_octo_tf {
 struct vla_smolvla_tf {
     std::unique_ptr<SmolvlaTf> m;
 };
+struct vla_siglip_tf {
+    std::unique_ptr<SiglipTf> m;
+};
 
 namespace {
 
@@ -251,3 +254,38 @@ VLA_API int32_t vla_smolvla_tf_chunk_run(vla_smolvla_tf* h, const float* prefix,
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------- SigLIP --
+
+VLA_API vla_siglip_tf* vla_siglip_tf_load(const char* dir, int32_t int8_mask) {
+    return load_handle<vla_siglip_tf>("vla_siglip_tf_load", [&] {
+        VLA_REQUIRE(dir, "null directory");
+        return std::make_unique<SiglipTf>(dir, int8_mask);
+    });
+}
+VLA_API void vla_siglip_tf_free(vla_siglip_tf* h) { delete h; }
+VLA_API int32_t vla_siglip_tf_img(const vla_siglip_tf* h) { return h ? h->m->img() : 0; }
+VLA_API int32_t vla_siglip_tf_n_tokens(const vla_siglip_tf* h) { return h ? h->m->n_tokens() : 0; }
+VLA_API int32_t vla_siglip_tf_out_dim(const vla_siglip_tf* h) { return h ? h->m->out_dim() : 0; }
+VLA_API int32_t vla_siglip_tf_int8_layers(const vla_siglip_tf* h) { return h ? h->m->int8_layers() : 0; }
+VLA_API int32_t vla_siglip_tf_graph_nodes(const vla_siglip_tf* h) { return h ? h->m->graph_nodes() : 0; }
+
+VLA_API int32_t vla_siglip_tf_encode_dev(vla_siglip_tf* h, const float* pixels, float* out, void* stream) {
+    return guarded("vla_siglip_tf_encode_dev", [&] {
+        VLA_REQUIRE(h, "null handle");
+        h->m->encode_dev(pixels, out, as_stream(stream));
+    });
+}
+
+VLA_API int32_t vla_siglip_tf_encode(vla_siglip_tf* h, const float* pixels, float* out) {
+    return guarded("vla_siglip_tf_encode", [&] {
+        VLA_REQUIRE(h && pixels && out, "null handle or buffer");
+        SiglipTf& m = *h->m;
+        HostCall hc;
+        const float* dp = hc.up(pixels, (size_t)3 * m.img() * m.img());
+        const size_t n = (size_t)m.n_tokens() * m.out_dim();
+        float* dout = hc.out(n);
+        m.encode_dev(dp, dout, hc.st);
+        hc.down(out, dout, n);
+    });
+}

@@ -197,6 +197,13 @@ void launch_rope_table(float* x, int ld, const double* cs, int seq, int n_heads,
 void launch_copy_rows(float* dst, int ldd, const float* src, int lds, int rows, int cols,
                       hipStream_t st);
 
+// vision.hip: SigLIP patch extraction, pixels [3, img, img] (CHW) ->
+// out [(img/patch)^2, 3*patch^2] rows (ic, kh, kw) (conv.cpp:179-190), and the
+// pixel shuffle of [side*side, hidden] patch rows into [(side/sf)^2,
+// sf*sf*hidden] tokens (siglip_vision.cpp:188-198)
+void launch_extract_patches(float* out, const float* pixels, int img, int patch, hipStream_t st);
+void launch_pixel_shuffle(float* dst, const float* src, int side, int hidden, int sf, hipStream_t st);
+
 // linear_f32.hip: out[m, n] = act(x[m,:] . W[n,:] + bias[n]); accumulate != 0
 // adds it as fmaf(alpha, v, out[m, n]). act as vla_act, plus 4 = silu.
 void launch_linear_f32(float* out, int ldo, const float* x, int ldx, const float* W, int ldw,

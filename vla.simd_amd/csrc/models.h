@@ -1,6 +1,7 @@
 // models.h - the policy graphs of the reference on the device: the ACT
-// transformer, the Octo block transformer and the SmolVLA action chunk (SmolLM2
-// prefix + action expert flow-matching denoise). Each loads the reference's own
+// transformer, the Octo block transformer, the SmolVLA action chunk (SmolLM2
+// prefix + action expert flow-matching denoise) and SmolVLA's SigLIP vision
+// tower. Each loads the reference's own
 // .meta/.bin checkpoint layout, holds its weights in HBM (int8 rows + scales for
 // the layers its int8 mask selects, fp32 otherwise), and runs a whole forward
 // pass as one HIP graph on inputs already on the device.
@@ -201,6 +202,48 @@ private:
     uint8_t *pgroup_ = nullptr, *pallow_ = nullptr;
     float *dmask_ = nullptr, *cmask_ = nullptr;
     bool dcausal_ = true, cnone_ = true;
+    Ctx ctx_;
+    hipStream_t own_ = nullptr;
+    GraphReplay replay_;
+};
+
+// ---------------------------------------------------------------- SigLIP --
+// src/models/smolvla/siglip_vision.{h,cpp}: SmolVLA's vision tower (patch
+// embedding + positions, n_layers pre-LN encoder layers with GELU tanh and
+// full attention, post-LayerNorm) and its connector (pixel shuffle by
+// scale_factor, bias-free modality projection). int8 mask bits as
+// SmolvlaModel::apply_int8 (smolvla_model.cpp:127-140): 1 attention, 2 w1,
+// 4 w2, 8 patch embedding + modality projection.
+class SiglipTf {
+public:
+    SiglipTf(const std::string& dir, int int8_mask);
+    ~SiglipTf();
+    int img() const { return img_; }
+    int n_tokens() const { return ntok_; }
+    int out_dim() const { return mm_out_; }
+    int hidden() const { return H_; }
+    int int8_layers() const { return n_int8_; }
+    // device pointers; pixels [3, img, img] (CHW, the preprocessed image),
+    // out [n_tokens, out_dim] the image tokens before SmolVLA's sqrt(hidden)
+    void encode_dev(const float* pixels, float* out, hipStream_t caller);
+    int graph_nodes() const { return replay_.nodes(); }
+
+private:
+    struct Layer {
+        DLinear qkv, o, w1, w2;
+        const float *ln1s, *ln1b, *ln2s, *ln2b;
+    };
+    void run(hipStream_t st);
+
+    int H_ = 768, heads_ = 12, hd_ = 64, I_ = 3072, NL_ = 12, P_ = 16, img_ = 512, NP_ = 1024, sf_ = 4,
+        mm_out_ = 960, ntok_ = 64, side_ = 32, n_int8_ = 0;
+    float eps_ = 1e-6f;
+    DeviceArena A_;
+    DLinear patch_, mm_;
+    const float *pos_ = nullptr, *post_s_ = nullptr, *post_b_ = nullptr;
+    std::vector<Layer> layers_;
+    float *patches_ = nullptr, *x_ = nullptr, *h_ = nullptr, *qkv_ = nullptr, *att_ = nullptr, *ff_ = nullptr,
+          *shuf_ = nullptr, *out_ = nullptr;
     Ctx ctx_;
     hipStream_t own_ = nullptr;
     GraphReplay replay_;
