@@ -71,7 +71,9 @@ struct AttnCfg {
     static_assert(KT % 16 == 0 && (KT * HDP / 4) % 64 == 0, "tile shape");
 };
 
-template <int HDP, int KT, int W>
+// KD: the mask kind reads per-key data (1 dense, 3 groups); kinds 0 and 2
+// (none, causal) compile without the per-key prefetch.
+template <int HDP, int KT, int W, bool KD>
 __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
     using C = AttnCfg<HDP, KT, W>;
     constexpr int SK = C::SK, F4 = C::F4;
@@ -132,16 +134,27 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
     float mnext[4 * NT];
     int gnext[4 * NT];
     auto gload = [&](int kv0, int end) {
+        if (kv0 + KT <= end && HD == HDP) {  // wave-uniform: every row and column is in range
 #pragma unroll
-        for (int i = 0; i < F4; i++) {
-            const int e = lane + 64 * i, row = e / (HDP / 4), d = 4 * (e % (HDP / 4));
-            const int j = kv0 + row;
-            kr[i] = vr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (j < end && d < HD) {
+            for (int i = 0; i < F4; i++) {
+                const int e = lane + 64 * i, row = e / (HDP / 4), d = 4 * (e % (HDP / 4));
+                const int j = kv0 + row;
                 kr[i] = *reinterpret_cast<const float4*>(a.K + (size_t)j * a.ldk + kvh * HD + d);
                 vr[i] = *reinterpret_cast<const float4*>(a.V + (size_t)j * a.ldv + kvh * HD + d);
             }
+        } else {
+#pragma unroll
+            for (int i = 0; i < F4; i++) {
+                const int e = lane + 64 * i, row = e / (HDP / 4), d = 4 * (e % (HDP / 4));
+                const int j = kv0 + row;
+                kr[i] = vr[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (j < end && d < HD) {
+                    kr[i] = *reinterpret_cast<const float4*>(a.K + (size_t)j * a.ldk + kvh * HD + d);
+                    vr[i] = *reinterpret_cast<const float4*>(a.V + (size_t)j * a.ldv + kvh * HD + d);
+                }
+            }
         }
+        if (!KD) return;
 #pragma unroll
         for (int x = 0; x < 4 * NT; x++) {
             const int j = kv0 + (x >> 2) * 16 + 4 * g + (x & 3);
@@ -174,10 +187,12 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
         lstore();
         float mcur[4 * NT];
         int gcur[4 * NT];
+        if (KD) {
 #pragma unroll
-        for (int x = 0; x < 4 * NT; x++) {
-            mcur[x] = mnext[x];
-            gcur[x] = gnext[x];
+            for (int x = 0; x < 4 * NT; x++) {
+                mcur[x] = mnext[x];
+                gcur[x] = gnext[x];
+            }
         }
         wave_lds_sync();
         if (t + W < nkt) gload((t + W) * KT, a.seq_k);  // next tile, under this one's math
@@ -207,13 +222,13 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
                 float x = sacc[kt][r] * scale;
                 bool blocked = !qok || j >= kv_end;
                 if (!blocked) {
-                    if (mk == 1) {
+                    if (KD && mk == 1) {
                         const float mv = mcur[kt * 4 + r];
                         if (mv == -FLT_MAX) blocked = true;
                         else x = x + mv;
                     } else if (mk == 2) {
                         blocked = j > qi + a.causal_offset;
-                    } else if (mk == 3) {
+                    } else if (KD && mk == 3) {
                         blocked = !allow[qg * G + gcur[kt * 4 + r]];
                     }
                 }
@@ -230,7 +245,8 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
 #pragma unroll
             for (int kt = 0; kt < NT; kt++) sacc[kt] = v4f{0.f, 0.f, 0.f, 0.f};
         } else {
-            alpha = fast_exp2((m - mnew) * kLog2e);
+            // mnew == m gives alpha = exp2(0) = 1 exactly
+            alpha = mnew == m ? 1.0f : fast_exp2((m - mnew) * kLog2e);
             float ps = 0.0f;
 #pragma unroll
             for (int kt = 0; kt < NT; kt++)
@@ -243,9 +259,14 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
             lsum = lsum * alpha + ps;
             m = mnew;
         }
+        // the accumulators are rescaled only when some query's running max
+        // moved (multiplying by alpha = 1 changes nothing)
+        if (__any(alpha != 1.0f)) {
+#pragma unroll
+            for (int dt = 0; dt < DT; dt++) oacc[dt] *= alpha;
+        }
 #pragma unroll
         for (int dt = 0; dt < DT; dt++) {
-            oacc[dt] *= alpha;
 #pragma unroll
             for (int kt = 0; kt < NT; kt++)
 #pragma unroll
@@ -345,17 +366,23 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
     }
 }
 
-template <int HDP, int KT, int W>
-void launch_w(const AttnArgs& a, hipStream_t st) {
+template <int HDP, int KT, int W, bool KD>
+void launch_kd(const AttnArgs& a, hipStream_t st) {
     using C = AttnCfg<HDP, KT, W>;
     static const bool attr = [] {
         if (C::LDS > 65536)
-            VLA_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_fwd<HDP, KT, W>),
+            VLA_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_fwd<HDP, KT, W, KD>),
                                               hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS));
         return true;
     }();
     (void)attr;
-    attn_fwd<HDP, KT, W><<<dim3((a.seq_q + 15) / 16, a.n_q), W * 64, C::LDS, st>>>(a);
+    attn_fwd<HDP, KT, W, KD><<<dim3((a.seq_q + 15) / 16, a.n_q), W * 64, C::LDS, st>>>(a);
+}
+
+template <int HDP, int KT, int W>
+void launch_w(const AttnArgs& a, hipStream_t st) {
+    if (a.mask_kind == 1 || a.mask_kind == 3) launch_kd<HDP, KT, W, true>(a, st);
+    else launch_kd<HDP, KT, W, false>(a, st);
 }
 
 // VLA_HIP_ATTN_W=<1|2|4|8> forces the waves per block (A/B runs; the values
