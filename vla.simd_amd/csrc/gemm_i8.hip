@@ -1203,6 +1203,7 @@ struct Tile {
     bool pf = false;  // fragment-pipelined main loop (gemm_i8_lds PF)
 };
 const Tile kTiles[] = {{128, 128, 64, 0},       {64, 128, 64, 0},         {64, 64, 64, 0},
+                       {64, 64, 128, 0},        {64, 128, 128, 0},
                        {128, 128, 64, 4},       {64, 128, 64, 4},         {256, 128, 128, 3, 8},
                        {256, 256, 128, 2, 8},   {256, 128, 128, 3, 8, true}, {256, 256, 128, 2, 8, true}};
 
@@ -1233,12 +1234,16 @@ Tile pick_tile(int M, int N, int K) {
     // 256 x 256 form needs more than 256 VGPRs for its fragments and
     // accumulators, and spills.
     auto tiles = [&](int bm, int bn) { return (long)((M + bm - 1) / bm) * ((N + bn - 1) / bn); };
-    if (K <= 1024) return tiles(64, 128) >= 2 * kCUs ? Tile{64, 128, 64, 0} : Tile{64, 64, 64, 0};
+    // 64 x 64 tiles walk K in 128-byte slabs once K has two of them: half the
+    // barriers and twice the MFMA work per slab (ACT 0.409 -> 0.402 ms, Octo
+    // 1.159 -> 1.141 ms per forward)
+    const Tile small{64, 64, K >= 256 ? 128 : 64, 0};
+    if (K <= 1024) return tiles(64, 128) >= 2 * kCUs ? Tile{64, 128, 64, 0} : small;
     if (tiles(256, 256) >= 2 * kCUs) return {256, 256, 128, 2, 8, true};
     if (tiles(256, 128) >= kCUs) return {256, 128, 128, 3, 8, true};
     if (tiles(128, 128) >= kCUs) return {128, 128, 64, 4};
     if (tiles(64, 128) >= kCUs) return {64, 128, 64, 4};
-    return {64, 64, 64, 0};
+    return small;
 }
 
 // Split-K plan: for M > 128 on the register-staged tiles with K >= 1024 and
@@ -1283,7 +1288,9 @@ void dispatch_tile(const Tile& t, const GemmArgs& a, hipStream_t st) {
         return;
     }
     if (t.bm == 128) run_tiled<128, 128, 64>(a, st);
+    else if (t.bn == 128 && t.bk == 128) run_tiled<64, 128, 128>(a, st);
     else if (t.bn == 128) run_tiled<64, 128, 64>(a, st);
+    else if (t.bk == 128) run_tiled<64, 64, 128>(a, st);
     else run_tiled<64, 64, 64>(a, st);
 }
 
