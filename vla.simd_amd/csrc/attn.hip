@@ -71,10 +71,12 @@ struct AttnCfg {
     static_assert(KT % 16 == 0 && (KT * HDP / 4) % 64 == 0, "tile shape");
 };
 
-// KD: the mask kind reads per-key data (1 dense, 3 groups); kinds 0 and 2
-// (none, causal) compile without the per-key prefetch.
-template <int HDP, int KT, int W, bool KD>
+// MKC: the mask class compiled in - 1 dense, 3 group table (per-key data
+// prefetched with each tile), 0 for kinds 0 and 2 (none, causal), which read
+// no per-key data.
+template <int HDP, int KT, int W, int MKC>
 __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
+    constexpr bool KD = MKC != 0;
     using C = AttnCfg<HDP, KT, W>;
     constexpr int SK = C::SK, F4 = C::F4;
     constexpr int NT = KT / 16;
@@ -107,11 +109,11 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
 
     const float scale = a.scale;
     const int mk = a.mask_kind;
-    const int qg = (mk == 3 && qok) ? a.q_group[qi] : 0;
+    const int qg = (MKC == 3 && qok) ? a.q_group[qi] : 0;
     const int G = a.n_groups;
     // small group tables live in LDS, so the per-key test is an LDS read
     const uint8_t* allow = a.allow;
-    if (mk == 3 && G * G <= C::ALLOW) {
+    if (MKC == 3 && G * G <= C::ALLOW) {
         uint8_t* al = reinterpret_cast<uint8_t*>(smem) + C::MAIN;
         for (int i = tid; i < G * G; i += W * 64) al[i] = a.allow[i];
         __syncthreads();
@@ -161,8 +163,8 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
             mnext[x] = 0.0f;
             gnext[x] = 0;
             if (j < end) {
-                if (mk == 1 && qok) mnext[x] = a.mask[(size_t)qi * a.ldm + j];
-                else if (mk == 3) gnext[x] = a.k_group[j];
+                if (MKC == 1 && qok) mnext[x] = a.mask[(size_t)qi * a.ldm + j];
+                else if (MKC == 3) gnext[x] = a.k_group[j];
             }
         }
     };
@@ -197,6 +199,23 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
         wave_lds_sync();
         if (t + W < nkt) gload((t + W) * KT, a.seq_k);  // next tile, under this one's math
 
+        // group masks: which of this lane's scores the table blocks, decided
+        // before the products; a tile the table blocks for every query of the
+        // wave adds p = 0 everywhere and leaves (m, l, O) as they are, so it
+        // is skipped (Octo's later timesteps for earlier queries)
+        bool mblk[4 * NT];
+        if (MKC == 3) {
+            bool live = false;
+#pragma unroll
+            for (int x = 0; x < 4 * NT; x++) {
+                const int j = kv0 + (x >> 2) * 16 + 4 * g + (x & 3);
+                const bool b = !qok || j >= kv_end || !allow[qg * G + gcur[x]];
+                mblk[x] = b;
+                live = live || !b;
+            }
+            if (!__any(live)) continue;
+        }
+
         v4f sacc[NT];
 #pragma unroll
         for (int kt = 0; kt < NT; kt++) {
@@ -220,17 +239,15 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
             for (int r = 0; r < 4; r++) {
                 const int j = kv0 + kt * 16 + 4 * g + r;
                 float x = sacc[kt][r] * scale;
-                bool blocked = !qok || j >= kv_end;
-                if (!blocked) {
-                    if (KD && mk == 1) {
-                        const float mv = mcur[kt * 4 + r];
-                        if (mv == -FLT_MAX) blocked = true;
-                        else x = x + mv;
-                    } else if (mk == 2) {
-                        blocked = j > qi + a.causal_offset;
-                    } else if (KD && mk == 3) {
-                        blocked = !allow[qg * G + gcur[kt * 4 + r]];
-                    }
+                bool blocked;
+                if (MKC == 3) {
+                    blocked = mblk[kt * 4 + r];
+                } else if (MKC == 1) {
+                    const float mv = mcur[kt * 4 + r];
+                    blocked = !qok || j >= kv_end || mv == -FLT_MAX;
+                    if (!blocked) x = x + mv;
+                } else {
+                    blocked = !qok || j >= kv_end || (mk == 2 && j > qi + a.causal_offset);
                 }
                 x = blocked ? -INFINITY : x;
                 sacc[kt][r] = x;
@@ -366,23 +383,24 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
     }
 }
 
-template <int HDP, int KT, int W, bool KD>
+template <int HDP, int KT, int W, int MKC>
 void launch_kd(const AttnArgs& a, hipStream_t st) {
     using C = AttnCfg<HDP, KT, W>;
     static const bool attr = [] {
         if (C::LDS > 65536)
-            VLA_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_fwd<HDP, KT, W, KD>),
+            VLA_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_fwd<HDP, KT, W, MKC>),
                                               hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS));
         return true;
     }();
     (void)attr;
-    attn_fwd<HDP, KT, W, KD><<<dim3((a.seq_q + 15) / 16, a.n_q), W * 64, C::LDS, st>>>(a);
+    attn_fwd<HDP, KT, W, MKC><<<dim3((a.seq_q + 15) / 16, a.n_q), W * 64, C::LDS, st>>>(a);
 }
 
 template <int HDP, int KT, int W>
 void launch_w(const AttnArgs& a, hipStream_t st) {
-    if (a.mask_kind == 1 || a.mask_kind == 3) launch_kd<HDP, KT, W, true>(a, st);
-    else launch_kd<HDP, KT, W, false>(a, st);
+    if (a.mask_kind == 1) launch_kd<HDP, KT, W, 1>(a, st);
+    else if (a.mask_kind == 3) launch_kd<HDP, KT, W, 3>(a, st);
+    else launch_kd<HDP, KT, W, 0>(a, st);
 }
 
 // VLA_HIP_ATTN_W=<1|2|4|8> forces the waves per block (A/B runs; the values
