@@ -232,7 +232,8 @@ def _from_panel(buf, seq, K):
 
 
 @pytest.mark.parametrize("seq,K", [(1, 3), (5, 17), (16, 64), (50, 720), (100, 512), (128, 960),
-                                   (3, 1027), (77, 4100)])
+                                   (3, 1027), (77, 4100), (128, 2048), (9, 2052), (64, 12288),
+                                   (3, 16384), (4, 16388)])
 def test_quantize_panel_layout(vla, orc, torch_cuda, seq, K):
     """Panel-layout quantization: the same bytes and scales as the oracle's
     row-major quantize_act_i8, at the documented panel offsets, pads zero."""
