@@ -153,9 +153,11 @@ VLA_API int32_t vla_dense_linear_i8_pre_dev(float* out, int32_t ldo, const int8_
 
 /* dense_linear_i8_pre_dev with a caller-owned device workspace for split-K
  * (no counterpart in the reference): when the output tiles of a long-K GEMM
- * of more than 128 rows would leave most CUs idle, K is cut into chunks whose
- * int32 partial sums go to `work` and are reduced before the epilogue; the
- * values equal vla_dense_linear_i8_pre_dev's exactly. vla_gemm_i8_split_bytes
+ * would leave most CUs idle (more than 128 rows: K >= 1024 on the
+ * register-staged tiles; at most 128 rows: K >= 4096 with N/16 column blocks
+ * under half the CUs), K is cut into chunks whose int32 partial sums go to
+ * `work` and are reduced before the epilogue; the values equal
+ * vla_dense_linear_i8_pre_dev's exactly. vla_gemm_i8_split_bytes
  * gives the bytes that shape uses (0: it is not split; at most 8 MiB); a
  * smaller or null workspace just runs unsplit. work: 16-byte aligned. */
 VLA_API int64_t vla_gemm_i8_split_bytes(int32_t seq, int32_t N, int32_t K);
@@ -186,6 +188,14 @@ VLA_API int32_t vla_dense_linear_i8_panel_dev(float* out, int32_t ldo, const int
                                               const float* bias, int32_t seq, int32_t N,
                                               int32_t K, int32_t act, int32_t accumulate,
                                               void* stream);
+/* The same with a split-K workspace, as vla_dense_linear_i8_pre_split_dev
+ * (sized by vla_gemm_i8_split_bytes; a smaller or null one runs unsplit). */
+VLA_API int32_t vla_dense_linear_i8_panel_split_dev(float* out, int32_t ldo, const int8_t* xq,
+                                                    const float* ascale, const int8_t* Wq,
+                                                    int32_t ldw, const float* wscale,
+                                                    const float* bias, int32_t seq, int32_t N,
+                                                    int32_t K, int32_t act, int32_t accumulate,
+                                                    void* work, int64_t work_bytes, void* stream);
 
 /* A row op and the int8 quantization of its result in one pass (no
  * counterpart in the reference, which calls rmsnorm or silu_gate and then

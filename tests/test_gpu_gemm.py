@@ -312,7 +312,10 @@ def test_panel_rejects_large_m(vla, torch_cuda):
 # (302 x 512 x 3200), a ResNet 3x3/512 conv (300 x 512 x 4608), a K tail
 # (2050), a 129-row case and a sweep shape (512 x 960 x 2560)
 SPLIT_SHAPES = [(658, 768, 3072), (177, 960, 2560), (302, 512, 3200), (300, 512, 4608), (129, 100, 2050),
-                (200, 48, 1500), (512, 960, 2560)]
+                (200, 48, 1500), (512, 960, 2560),
+                # at most 128 rows (the skinny kernel): SigLIP's projection
+                # (64 x 960 x 12288), a K tail, one row, 16 columns
+                (64, 960, 12288), (100, 1000, 4100), (1, 16, 4096), (16, 200, 8192)]
 
 
 @pytest.mark.parametrize("seq,N,K", SPLIT_SHAPES)
@@ -353,6 +356,37 @@ def test_split_k_bitexact(vla, orc, torch_cuda, seq, N, K, act, accumulate):
         assert max_rel(got, want) <= 2e-6
     else:
         assert same_bits(got, want)
+
+
+@pytest.mark.parametrize("seq,N,K", [(64, 960, 12288), (100, 1000, 4100), (5, 48, 8200)])
+def test_split_k_panel_bitexact(vla, orc, torch_cuda, seq, N, K):
+    """Split-K over panel-layout activations (the chunks start at whole
+    64-byte panels): equal to the unsplit panel GEMM and the oracle."""
+    torch = torch_cuda
+    n = vla.gemm_i8_split_bytes(seq, N, K)
+    assert n > 0, "shape expected to split"
+    x, W, b = _case(orc, seq, N, K)
+    Wq, ws = orc.quantize_weights_i8(W)
+    ld = (K + 63) // 64 * 64
+    Wp = np.zeros((N, ld), np.int8)
+    Wp[:, :Wq.shape[1]] = Wq
+    dev = torch.device("cuda")
+    xd = torch.from_numpy(x).to(dev)
+    xq = torch.empty((vla.i8_panel_bytes(seq, K),), dtype=torch.int8, device=dev)
+    sa = torch.empty(seq, dtype=torch.float32, device=dev)
+    vla.quantize_act_i8_panel_dev(xd, xq, sa)
+    Wd, wsd, bd = torch.from_numpy(Wp).to(dev), torch.from_numpy(ws).to(dev), torch.from_numpy(b).to(dev)
+    work = torch.empty(n, dtype=torch.uint8, device=dev)
+    split = torch.full((seq, N), 0.5, device=dev)
+    vla.dense_linear_i8_panel_split_dev(split, xq, sa, Wd, wsd, bd, K, work, act=1, accumulate=1)
+    plain = torch.full((seq, N), 0.5, device=dev)
+    vla.dense_linear_i8_panel_dev(plain, xq, sa, Wd, wsd, bd, K, act=1, accumulate=1)
+    torch.cuda.synchronize()
+    got = split.cpu().numpy()
+    assert same_bits(got, plain.cpu().numpy())
+    xo, so = orc.quantize_act_i8(x)
+    want = (np.float32(0.5) + orc.apply_act(orc.dense_linear_i8_pre(xo, so, Wq, ws, b, K), 1)).astype(np.float32)
+    assert same_bits(got, want)
 
 
 def test_split_k_plan_bounds(vla):

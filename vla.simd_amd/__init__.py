@@ -42,6 +42,7 @@ EXPORTS = (
     "vla_i8_kpad", "vla_quantize_act_i8", "vla_quantize_act_i8_dev", "vla_pack_weights_i8",
     "vla_dense_linear_i8_pre", "vla_dense_linear_i8", "vla_dense_linear_i8_pre_dev",
     "vla_i8_panel_bytes", "vla_quantize_act_i8_panel_dev", "vla_dense_linear_i8_panel_dev",
+    "vla_dense_linear_i8_panel_split_dev",
     "vla_rowop_quantize_i8_panel_dev", "vla_rowop_linear_i8_fits", "vla_rowop_linear_i8_dev",
     "vla_ckpt_open", "vla_ckpt_free", "vla_ckpt_is_gguf", "vla_ckpt_file_size", "vla_ckpt_read",
     "vla_ckpt_names", "vla_conv2d_i8", "vla_conv2d_i8_workspace_bytes", "vla_conv2d_i8_dev",
@@ -121,6 +122,8 @@ def _declare(L):
         "vla_i8_panel_bytes": (ctypes.c_int64, [i32, i32]),
         "vla_quantize_act_i8_panel_dev": (i32, [P, i32, P, P, i32, i32, P]),
         "vla_dense_linear_i8_panel_dev": (i32, [P, i32, P, P, P, i32, P, P, i32, i32, i32, i32, i32, P]),
+        "vla_dense_linear_i8_panel_split_dev": (i32, [P, i32, P, P, P, i32, P, P, i32, i32, i32, i32, i32, P,
+                                                      c_int64, P]),
         "vla_rowop_quantize_i8_panel_dev": (i32, [i32, P, i32, P, i32, P, ctypes.c_float, P, P, i32, i32, P]),
         "vla_rowop_linear_i8_fits": (i32, [i32, i32, i32]),
         "vla_conv2d_i8": (i32, [P, P, P, P, P, i32, i32, i32, i32, i32, i32, i32]),
@@ -493,6 +496,16 @@ def dense_linear_i8_panel_dev(out, xq, ascale, Wq, wscale, bias, K, act=0, accum
     seq, N = out.shape[0], Wq.shape[0]
     _call("vla_dense_linear_i8_panel_dev", _dp(out), out.stride(0), _dp(xq), _dp(ascale), _dp(Wq),
           Wq.stride(0), _dp(wscale), _dp(bias), seq, N, K, act, accumulate, _stream(stream))
+
+
+def dense_linear_i8_panel_split_dev(out, xq, ascale, Wq, wscale, bias, K, work, act=0, accumulate=0,
+                                    stream=None):
+    """dense_linear_i8_panel_dev with a split-K workspace (a device byte tensor or None)."""
+    seq, N = out.shape[0], Wq.shape[0]
+    nbytes = 0 if work is None else work.numel() * work.element_size()
+    _call("vla_dense_linear_i8_panel_split_dev", _dp(out), out.stride(0), _dp(xq), _dp(ascale), _dp(Wq),
+          Wq.stride(0), _dp(wscale), _dp(bias), seq, N, K, act, accumulate, _dp(work), nbytes,
+          _stream(stream))
 
 
 ROWOP_IDENTITY, ROWOP_RMSNORM, ROWOP_SILU_GATE = 0, 2, 3

@@ -319,6 +319,34 @@ VLA_API int32_t vla_dense_linear_i8_panel_dev(float* out, int32_t ldo, const int
     });
 }
 
+VLA_API int32_t vla_dense_linear_i8_panel_split_dev(float* out, int32_t ldo, const int8_t* xq,
+                                                    const float* ascale, const int8_t* Wq, int32_t ldw,
+                                                    const float* wscale, const float* bias, int32_t seq,
+                                                    int32_t N, int32_t K, int32_t act, int32_t accumulate,
+                                                    void* work, int64_t work_bytes, void* stream) {
+    return guarded("vla_dense_linear_i8_panel_split_dev", [&] {
+        VLA_REQUIRE(work_bytes >= 0 && (work || work_bytes == 0), "bad workspace");
+        GemmArgs a{};
+        a.A = xq;
+        a.a_panel = 1;
+        a.B = Wq;
+        a.ldb = ldw;
+        a.ascale = ascale;
+        a.wscale = wscale;
+        a.bias = bias;
+        a.out = out;
+        a.ldo = ldo;
+        a.M = seq;
+        a.N = N;
+        a.K = K;
+        a.act = act;
+        a.accumulate = accumulate;
+        a.split_ws = static_cast<int32_t*>(work);
+        a.split_bytes = (size_t)work_bytes;
+        launch_gemm_i8(a, as_stream(stream));
+    });
+}
+
 static RowQArgs rowop_args(int32_t op, const float* x, int32_t ldx, const float* u, int32_t ldu,
                            const float* w, float eps, int32_t seq, int32_t K) {
     VLA_REQUIRE(op == 0 || op == 2 || op == 3, "row op must be 0 (identity), 2 (RMSNorm) or 3 (silu_gate)");

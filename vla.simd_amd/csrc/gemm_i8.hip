@@ -730,6 +730,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
     // per wave, its partial int32 tile in MFMA lane order: [i][r][lane]
     __shared__ int32_t part[WAVES * FM * 256];
 
+    if (gridDim.y > 1) {  // split K: chunk blockIdx.y of K (a multiple of 128 bytes), raw int32 sums
+        const int k0 = blockIdx.y * a.kchunk;
+        a.A += a.a_panel ? (size_t)(k0 / 64) * panel_rows(a.M) * 64 : (size_t)k0;
+        a.B += k0;
+        a.K = a.K - k0 < a.kchunk ? a.K - k0 : a.kchunk;
+        a.acc32 = a.split_ws + (size_t)blockIdx.y * a.M * a.N;
+    }
+
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int n0 = blockIdx.x * 16;
@@ -1142,8 +1150,8 @@ void run_lds(const GemmArgs& a, hipStream_t st) {
 }
 
 template <int WAVES>
-void run_skinny(const GemmArgs& a, hipStream_t st) {
-    const int nb = (a.N + 15) / 16;
+void run_skinny(const GemmArgs& a, hipStream_t st, int splits = 1) {
+    const dim3 nb((a.N + 15) / 16, splits);
     constexpr int W8 = WAVES < 8 ? WAVES : 8;  // FM > 4 keeps the partial tiles within 64 KiB
     switch ((a.M + 15) / 16) {
     case 1: gemm_i8_skinny<1, WAVES><<<nb, WAVES * 64, 0, st>>>(a); break;
@@ -1257,9 +1265,27 @@ Tile pick_tile(int M, int N, int K) {
 struct SplitPlan {
     int S = 1, kchunk = 0;
 };
+// The skinny kernel (M <= 128) runs one block per 16 columns; with fewer
+// than half a block per CU and K >= 4096 it splits K into S <= 8 chunks of
+// >= 2048 bytes (multiples of 128) so that S x blocks is about one per CU.
+SplitPlan skinny_split_plan(int N, int K) {
+    SplitPlan p;
+    const int nb = (N + 15) / 16;
+    if (K < 4096 || 2 * nb > kCUs) return p;
+    int S = kCUs / nb;
+    S = S < 8 ? S : 8;
+    S = S < K / 2048 ? S : K / 2048;
+    if (S < 2) return p;
+    p.kchunk = ((K + S - 1) / S + 127) / 128 * 128;
+    p.S = (K + p.kchunk - 1) / p.kchunk;
+    if (p.S < 2) p = SplitPlan{};
+    return p;
+}
+
 SplitPlan split_plan(int M, int N, int K) {
     SplitPlan p;
-    if (M <= kPanelMaxRows || K < 1024) return p;
+    if (M <= kPanelMaxRows) return skinny_split_plan(N, K);
+    if (K < 1024) return p;
     const Tile t = pick_tile(M, N, K);
     if (t.stages != 0) return p;
     const long tiles = (long)((M + t.bm - 1) / t.bm) * ((N + t.bn - 1) / t.bn);
@@ -1318,10 +1344,25 @@ void launch_gemm_i8(const GemmArgs& a, hipStream_t st) {
         return;
     }
     if (a.M <= 128) {
-        const int steps = (a.K + 63) / 64;
-        if (steps >= 32) run_skinny<16>(a, st);
-        else if (steps >= 8) run_skinny<8>(a, st);
-        else run_skinny<4>(a, st);
+        SplitPlan p;
+        if (a.split_ws && !a.acc32) {
+            p = split_plan(a.M, a.N, a.K);
+            if (p.S > 1 && !(a.split_bytes >= (size_t)p.S * a.M * a.N * 4 && aligned(a.split_ws, 16))) p = SplitPlan{};
+        }
+        GemmArgs s = a;
+        s.kchunk = p.kchunk;
+        const int steps = ((p.S > 1 ? p.kchunk : a.K) + 63) / 64;
+        if (steps >= 32) run_skinny<16>(s, st, p.S);
+        else if (steps >= 8) run_skinny<8>(s, st, p.S);
+        else run_skinny<4>(s, st, p.S);
+        if (p.S > 1) {
+            const bool vec = a.N % 4 == 0 && a.ldo % 4 == 0 && aligned(a.out, 16);
+            const int64_t work = (int64_t)a.M * a.N / (vec ? 4 : 1);
+            const int blocks = (int)((work + 255) / 256 < 4096 ? (work + 255) / 256 : 4096);
+            if (vec) gemm_i8_split_reduce<true><<<blocks, 256, 0, st>>>(s, p.S);
+            else gemm_i8_split_reduce<false><<<blocks, 256, 0, st>>>(s, p.S);
+            VLA_LAUNCH_CHECK();
+        }
         return;
     }
     const Tile t = pick_tile(a.M, a.N, a.K);
