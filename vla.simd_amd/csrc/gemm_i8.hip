@@ -1373,6 +1373,7 @@ void launch_gemm_i8(const GemmArgs& a, hipStream_t st) {
             s.kchunk = p.kchunk;
             if (t.bm == 128) run_tiled<128, 128, 64>(s, st, p.S);
             else if (t.bn == 128) run_tiled<64, 128, 64>(s, st, p.S);
+            else if (t.bk == 128) run_tiled<64, 64, 128>(s, st, p.S);
             else run_tiled<64, 64, 64>(s, st, p.S);
             const bool vec = a.N % 4 == 0 && a.ldo % 4 == 0 && aligned(a.out, 16);
             const int64_t work = (int64_t)a.M * a.N / (vec ? 4 : 1);
