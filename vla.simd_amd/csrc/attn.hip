@@ -352,7 +352,9 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
                 make_float4(oacc[dt][0], oacc[dt][1], oacc[dt][2], oacc[dt][3]);
         __syncthreads();
     }
-    if (wave != 0 || !qok) return;
+    // wave w writes the 16-dim output slices w, w + W, ... (every wave holds
+    // all (m, l) already; the sums over waves run in the same order for each)
+    if (wave >= DT || !qok) return;
 
     float f[W], l = 0.0f;
 #pragma unroll
@@ -361,8 +363,7 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
         l += f[w] * lw[w];
     }
     const float inv = masked ? 1.0f / (float)a.seq_k : 1.0f / l;
-#pragma unroll
-    for (int dt = 0; dt < DT; dt++) {
+    for (int dt = wave; dt < DT; dt += W) {
         const int d = dt * 16 + 4 * g;
         if (d < HD) {
             float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
