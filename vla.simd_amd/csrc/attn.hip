@@ -128,6 +128,9 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
         kv_end = e < 0 ? 0 : (e < kv_end ? e : kv_end);
     }
 
+    const bool vec_kg = MKC == 3 && (reinterpret_cast<uintptr_t>(a.k_group) & 3) == 0;
+    const bool vec_mask = MKC == 1 && (reinterpret_cast<uintptr_t>(a.mask) & 15) == 0 && (a.ldm & 3) == 0;
+
     // this lane's share of a tile load: float4 number e = lane + 64 * i of the
     // KT x HDP/4 tile is row e / (HDP/4), dims 4 * (e % (HDP/4))
     float4 kr[F4], vr[F4];
@@ -157,14 +160,34 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
             }
         }
         if (!KD) return;
+        // a lane's keys come in runs of 4 consecutive (4 g .. 4 g + 3 of each
+        // 16): whole in-range runs take one 4-byte group load or one float4
+        // mask load when the table allows it
 #pragma unroll
-        for (int x = 0; x < 4 * NT; x++) {
-            const int j = kv0 + (x >> 2) * 16 + 4 * g + (x & 3);
-            mnext[x] = 0.0f;
-            gnext[x] = 0;
-            if (j < end) {
-                if (MKC == 1 && qok) mnext[x] = a.mask[(size_t)qi * a.ldm + j];
-                else if (MKC == 3) gnext[x] = a.k_group[j];
+        for (int kt = 0; kt < NT; kt++) {
+            const int j0 = kv0 + kt * 16 + 4 * g;
+            if (MKC == 3 && j0 + 4 <= end && vec_kg) {
+                const uint32_t w = *reinterpret_cast<const uint32_t*>(a.k_group + j0);
+#pragma unroll
+                for (int r = 0; r < 4; r++) gnext[kt * 4 + r] = (int)((w >> (8 * r)) & 0xffu);
+            } else if (MKC == 1 && j0 + 4 <= end && vec_mask) {
+                float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (qok) v = *reinterpret_cast<const float4*>(a.mask + (size_t)qi * a.ldm + j0);
+                mnext[kt * 4] = v.x;
+                mnext[kt * 4 + 1] = v.y;
+                mnext[kt * 4 + 2] = v.z;
+                mnext[kt * 4 + 3] = v.w;
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int j = j0 + r;
+                    mnext[kt * 4 + r] = 0.0f;
+                    gnext[kt * 4 + r] = 0;
+                    if (j < end) {
+                        if (MKC == 1 && qok) mnext[kt * 4 + r] = a.mask[(size_t)qi * a.ldm + j];
+                        else if (MKC == 3) gnext[kt * 4 + r] = a.k_group[j];
+                    }
+                }
             }
         }
     };
