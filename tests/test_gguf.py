@@ -55,10 +55,13 @@ def models(ck, tmp_path_factory):
     """Small ACT / Octo / SmolVLA checkpoints as directories and as GGUFs."""
     root = tmp_path_factory.mktemp("gguf")
     smol = dict(ck.SMOLVLA_BASE, chunk=12, n_layers=2, expert_layers=2, n_prefix=60)
+    vit = dict(hidden=192, n_heads=3, head_dim=64, inter=768, n_layers=2, patch=16, img=128, n_patches=64,
+               ln_eps=1e-6, scale_factor=2, mm_out=256, n_img_tok=16)
     out = {}
     for name, write, cfg, layout in (("act", ck.write_act, ACT_SMALL, None),
                                      ("octo", ck.write_octo, OCTO_SMALL, None),
-                                     ("smolvla", ck.write_smolvla, smol, ck.smolvla_gguf_layout(smol))):
+                                     ("smolvla", ck.write_smolvla, smol, ck.smolvla_gguf_layout(smol)),
+                                     ("siglip", ck.write_siglip, vit, ck.siglip_gguf_layout(vit))):
         d = str(root / name)
         write(d, cfg)
         g = str(root / f"{name}.gguf")
@@ -71,7 +74,7 @@ def _disk_files(d):
     return sorted(n for n in os.listdir(d) if os.path.isfile(os.path.join(d, n)))
 
 
-@pytest.mark.parametrize("name", ["act", "octo", "smolvla"])
+@pytest.mark.parametrize("name", ["act", "octo", "smolvla", "siglip"])
 def test_gguf_serves_the_directory_bytes(vla, ob, models, name):
     d, g, _ = models[name]
     f = vla.CkptFiles(g)
@@ -110,6 +113,10 @@ def test_reference_loaders_read_the_gguf(ob, models, ck):
     d, g, c = models["smolvla"]
     prefix, pad, noise = ck.smolvla_inputs(c, n_pad=2)
     outs = [ob.RefSmolvla(p, 48).run(prefix, pad, noise) for p in (d, g)]
+    assert outs[0].tobytes() == outs[1].tobytes()
+    d, g, c = models["siglip"]
+    px = ck.siglip_inputs(c)
+    outs = [ob.RefSiglip(p, 15, c["n_img_tok"], c["mm_out"]).encode(px) for p in (d, g)]
     assert outs[0].tobytes() == outs[1].tobytes()
 
 
