@@ -9,6 +9,7 @@
 #include <sys/stat.h>
 #include <unistd.h>
 
+#include <cmath>
 #include <cstring>
 #include <fstream>
 #include <limits>
@@ -365,6 +366,15 @@ std::map<std::string, double> CkptFiles::meta(const std::string& rel) const {
         m[key] = v;
     }
     return m;
+}
+
+int meta_int(const std::map<std::string, double>& m, const char* file, const char* k, int def) {
+    auto it = m.find(k);
+    if (it == m.end()) return def;
+    const double v = it->second;
+    VLA_REQUIRE(std::isfinite(v) && v == std::trunc(v) && v >= -2147483648.0 && v <= 2147483647.0,
+                std::string(file) + " key " + k + " is not an integer");
+    return (int)v;
 }
 
 }  // namespace hip

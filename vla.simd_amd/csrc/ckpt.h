@@ -71,5 +71,10 @@ private:
 // Whether `path` mounts as a GGUF, and which file ("" otherwise).
 std::string find_gguf(const std::string& path);
 
+// The integer value of key k of a parsed .meta file (def when absent), with
+// the reference's metadata_int bounds (src/models/arena.h:21-25): a finite
+// integer in int range, else an error naming `file`.
+int meta_int(const std::map<std::string, double>& m, const char* file, const char* k, int def);
+
 }  // namespace hip
 }  // namespace vla

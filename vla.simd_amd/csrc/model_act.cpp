@@ -35,12 +35,7 @@ struct Cursor {
 };
 
 int meta_int(const std::map<std::string, double>& m, const char* k, int def) {
-    auto it = m.find(k);
-    if (it == m.end()) return def;
-    const double v = it->second;
-    VLA_REQUIRE(std::isfinite(v) && v == std::trunc(v) && v >= -2147483648.0 && v <= 2147483647.0,
-                std::string("meta key ") + k + " is not an integer");
-    return (int)v;
+    return vla::hip::meta_int(m, "act.meta", k, def);
 }
 
 // ActTransformer::sinusoid_pos_2d (act_transformer.cpp:189-210): the 2D

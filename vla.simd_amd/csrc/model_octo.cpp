@@ -37,12 +37,7 @@ struct Cursor {
 };
 
 int meta_int(const std::map<std::string, double>& m, const char* k, int def) {
-    auto it = m.find(k);
-    if (it == m.end()) return def;
-    const double v = it->second;
-    VLA_REQUIRE(std::isfinite(v) && v == std::trunc(v) && std::fabs(v) < 2147483647.0,
-                std::string("octo.meta key ") + k + " is not an integer");
-    return (int)v;
+    return vla::hip::meta_int(m, "octo.meta", k, def);
 }
 
 // octo_transformer.cpp:103-109. Kinds: 0 task prefix (timestep -1), 1 primary,

@@ -26,12 +26,7 @@ namespace hip {
 namespace {
 
 int vit_int(const std::map<std::string, double>& m, const char* k, int def) {
-    auto it = m.find(k);
-    if (it == m.end()) return def;
-    const double v = it->second;
-    VLA_REQUIRE(std::isfinite(v) && v == std::trunc(v) && std::fabs(v) < 2147483647.0,
-                std::string("vit.meta key ") + k + " is not an integer");
-    return (int)v;
+    return vla::hip::meta_int(m, "vit.meta", k, def);
 }
 
 }  // namespace
