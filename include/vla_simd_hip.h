@@ -135,10 +135,19 @@ VLA_API int32_t vla_dense_linear_i8_pre(float* out, const int8_t* xq, const floa
 
 /* dense_linear_i8 (quant_ops.h:69, gemm_i8.cpp:246-256): quantize x then the
  * above. The host form allocates its own staging; the _dev form takes the
- * caller-owned scratch the reference takes (xq [seq, ldq], ascale [seq]). */
+ * caller-owned scratch the reference takes (quant_ops.h:66-72: xq_scratch
+ * holds seq rows of ldq >= i8_kpad(K) bytes, ldq a multiple of 4, and
+ * ascale_scratch seq floats), device pointers with row strides (ldx >= K,
+ * ldw >= i8_kpad(K), ldo >= N), act / accumulate as in
+ * vla_dense_linear_i8_pre_dev, and runs asynchronously on `stream`. */
 VLA_API int32_t vla_dense_linear_i8(float* out, const float* x, const int8_t* Wq,
                                     const float* wscale, const float* bias,
                                     int32_t seq, int32_t N, int32_t K);
+VLA_API int32_t vla_dense_linear_i8_dev(float* out, int32_t ldo, const float* x, int32_t ldx,
+                                        const int8_t* Wq, int32_t ldw, const float* wscale,
+                                        const float* bias, int32_t seq, int32_t N, int32_t K,
+                                        int8_t* xq_scratch, int32_t ldq, float* ascale_scratch,
+                                        int32_t act, int32_t accumulate, void* stream);
 
 /* Device form of dense_linear_i8_pre with the fused epilogue options the
  * reference graphs apply right after an int8 forward: act (vla_act, e.g.
@@ -499,6 +508,37 @@ VLA_API int32_t vla_siglip_tf_graph_nodes(const vla_siglip_tf* h);
  * pointers (16-byte aligned) and a stream and does not synchronize. */
 VLA_API int32_t vla_siglip_tf_encode(vla_siglip_tf* h, const float* pixels, float* out);
 VLA_API int32_t vla_siglip_tf_encode_dev(vla_siglip_tf* h, const float* pixels, float* out, void* stream);
+
+/* ------------------------------------------------ int8-step probe (tests) -- */
+
+/* Test support with no counterpart in the reference: a record of every int8
+ * GEMM one policy-graph pass runs, so a test can check each int8 step on its
+ * own against a CPU restatement. While the probe is on (vla_probe_begin until
+ * vla_probe_end), the graphs run eagerly (no HIP-graph replay), row ops are
+ * not fused into the GEMM (same values), and each int8 GEMM, up to
+ * max_records, is copied to the host with a device synchronization per step:
+ * the fp32 rows its activations were quantized from (SRC, [M, K]; present
+ * when shape[6] = 1), the int8 activations and scales it read (XQ [M, K],
+ * ASCALE [M]), its weights (W [N, K] int8, WSCALE [N], BIAS [N] when
+ * shape[5] = 1) and its output before and after the launch (BEFORE / AFTER
+ * [M, N]). vla_probe_shape writes {M, K, N, act, accumulate, has_bias,
+ * has_src}; vla_probe_read copies one field into a host buffer of exactly its
+ * size. One probe per process; not for concurrent use. */
+enum {
+    VLA_PROBE_SRC = 0,
+    VLA_PROBE_XQ = 1,
+    VLA_PROBE_ASCALE = 2,
+    VLA_PROBE_BEFORE = 3,
+    VLA_PROBE_AFTER = 4,
+    VLA_PROBE_W = 5,
+    VLA_PROBE_WSCALE = 6,
+    VLA_PROBE_BIAS = 7
+};
+VLA_API int32_t vla_probe_begin(int32_t max_records);
+VLA_API int32_t vla_probe_end(void);
+VLA_API int32_t vla_probe_count(void);
+VLA_API int32_t vla_probe_shape(int32_t i, int32_t* shape);
+VLA_API int32_t vla_probe_read(int32_t i, int32_t what, void* dst, int64_t bytes);
 
 #ifdef __cplusplus
 }

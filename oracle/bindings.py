@@ -398,6 +398,8 @@ def _ref_models():
     L.ref_octo_free.argtypes = [P]
     L.ref_octo_forward.argtypes, L.ref_octo_forward.restype = [P, P, P, P, i, P, P], i
     L.ref_octo_total_tokens.argtypes, L.ref_octo_total_tokens.restype = [P, i], i
+    L.ref_octo_forward_layout.argtypes = [P, P, P, P, i, P, i, P]
+    L.ref_octo_forward_layout.restype = i
     L.ref_smolvla_load.argtypes, L.ref_smolvla_load.restype = [ctypes.c_char_p, i], P
     L.ref_smolvla_free.argtypes = [P]
     L.ref_smolvla_chunk.argtypes, L.ref_smolvla_chunk.restype = [P, P, P, i, P, P], i
@@ -485,6 +487,17 @@ class RefOcto:
         tm = np.ascontiguousarray(tmask, dtype=np.uint8)
         ro = L.ref_octo_forward(self.h, _p(a), _p(b), _p(c), wnd, _p(tm), _p(out))
         return out[ro].copy()
+
+    def forward_layout(self, t5, stem_p, stem_w, wnd, tmask, repeat_task):
+        """The reference's own layers over either token layout (ref_octo_forward_layout):
+        repeat_task 1 is forward()'s layout, 0 drops the per-step task copy."""
+        L = _ref_models()
+        out = np.zeros(self.d, np.float32)
+        a, b = _f32(t5), _f32(stem_p)
+        c = None if stem_w is None else _f32(stem_w)
+        tm = np.ascontiguousarray(tmask, dtype=np.uint8)
+        L.ref_octo_forward_layout(self.h, _p(a), _p(b), _p(c), wnd, _p(tm), int(repeat_task), _p(out))
+        return out
 
     def __del__(self):
         if getattr(self, "h", None):

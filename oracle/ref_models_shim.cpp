@@ -27,6 +27,7 @@
 #include "models/smolvla/action_expert.h"
 #include "models/smolvla/siglip_vision.h"
 #include "models/smolvla/smollm2_lm.h"
+#include "ops/lm_ops.h"
 
 #include <cstdint>
 #include <cstring>
@@ -131,6 +132,72 @@ REF_API int ref_octo_forward(void* h, const float* t5, const float* stem_p, cons
 
 REF_API int ref_octo_total_tokens(void* h, int wnd) {
     return static_cast<OctoTransformer*>(h)->total_tokens(wnd);
+}
+
+/* OctoTransformer::forward (octo_transformer.cpp:144-219) driven over either
+ * token layout: repeat_task 1 is the reference's own (each timestep repeats
+ * the task tokens, 690 tokens at the Octo-base config; the result must equal
+ * ref_octo_forward bit for bit), repeat_task 0 drops the per-step copy (the
+ * 658-token layout), which the reference's forward cannot produce. The tokens,
+ * the block-causal keep rule of attends() (:103-109, key-side pad as
+ * build_mask :111-142) and the layer calls are the reference's; the layers,
+ * projections and final LayerNorm are the loaded model's own objects. Writes
+ * the final readout row to out [d]; returns the token count. */
+REF_API int ref_octo_forward_layout(void* h, const float* t5, const float* stem_p, const float* stem_w,
+                                    int wnd, const uint8_t* tmask, int repeat_task, float* out) {
+    auto* t = static_cast<OctoTransformer*>(h);
+    const OctoConfig& c = t->cfg;
+    const int D = c.d;
+    const int rep = repeat_task ? c.n_task : 0;
+    const int per = c.tok_primary + c.tok_wrist + rep + c.n_readout;
+    const int total = c.n_task + wnd * per;
+    std::vector<float> x((size_t)total * D), task((size_t)c.n_task * D);
+    t->proj_task.forward(task.data(), t5, c.n_task);
+    for (size_t i = 0; i < task.size(); i++) task[i] += t->pos_task[i];
+    std::memcpy(x.data(), task.data(), task.size() * sizeof(float));
+    // token kinds: 0 task prefix (timestep -1), 1 primary, 2 wrist, 3 repeated task, 4 readout
+    std::vector<int> kind(total, 0), step(total, -1);
+    std::vector<uint8_t> key_ok(total, 1);
+    for (int s = 0; s < wnd; s++) {
+        const int base = c.n_task + s * per;
+        float* row = x.data() + (size_t)base * D;
+        t->proj_prim.forward(row, stem_p + (size_t)s * c.tok_primary * c.stem_dim, c.tok_primary);
+        const float* pp = t->pos_prim + (size_t)s * c.tok_primary * D;
+        for (size_t i = 0; i < (size_t)c.tok_primary * D; i++) row[i] += pp[i];
+        row += (size_t)c.tok_primary * D;
+        if (stem_w) {
+            t->proj_wrist.forward(row, stem_w + (size_t)s * c.tok_wrist * c.stem_dim, c.tok_wrist);
+            const float* pw = t->pos_wrist + (size_t)s * c.tok_wrist * D;
+            for (size_t i = 0; i < (size_t)c.tok_wrist * D; i++) row[i] += pw[i];
+        }
+        row += (size_t)c.tok_wrist * D;
+        if (rep) {
+            std::memcpy(row, task.data(), task.size() * sizeof(float));
+            row += task.size();
+        }
+        std::memcpy(row, t->pos_readout + (size_t)s * c.n_readout * D, (size_t)c.n_readout * D * sizeof(float));
+        for (int i = 0; i < per; i++) {
+            const int k = i < c.tok_primary ? 1 : i < c.tok_primary + c.tok_wrist ? 2
+                        : i < c.tok_primary + c.tok_wrist + rep ? 3 : 4;
+            kind[base + i] = k;
+            step[base + i] = s;
+            key_ok[base + i] = k == 1 ? tmask[s] != 0 : k == 2 ? (stem_w != nullptr && tmask[s] != 0) : 1;
+        }
+    }
+    const float NEG = std::numeric_limits<float>::lowest();
+    std::vector<float> mask((size_t)total * total);
+    for (int i = 0; i < total; i++)
+        for (int j = 0; j < total; j++) {
+            const int gi = kind[i], gj = kind[j], ti = step[i], tj = step[j];
+            const bool see = gi == 0 ? gj == 0 : gj == 0 ? true : gj <= 3 ? tj <= ti : (gi == 4 && tj <= ti);
+            mask[(size_t)i * total + j] = see && key_ok[j] ? 0.0f : NEG;
+        }
+    const int ro = c.n_task + wnd * per - 1;
+    nn::Scratch s;
+    for (size_t li = 0; li + 1 < t->layers.size(); li++) t->layers[li].forward(x.data(), total, mask.data(), s, nullptr);
+    t->layers.back().forward_last_row(x.data(), ro, total, mask.data(), s);
+    layernorm(out, x.data() + (size_t)ro * D, t->final_s, t->final_b, 1, D, c.ln_eps);
+    return total;
 }
 
 struct RefSmolvla {

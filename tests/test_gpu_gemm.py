@@ -398,3 +398,37 @@ def test_split_k_plan_bounds(vla):
     assert vla.gemm_i8_split_bytes(512, 4096, 4096) == 0      # one LDS-DMA tile per CU: measured slower split
     for seq, N, K in SPLIT_SHAPES:
         assert 0 < vla.gemm_i8_split_bytes(seq, N, K) <= 8 << 20
+
+
+@pytest.mark.parametrize("seq,N,K,act,accumulate", [(100, 3200, 512, 0, 0), (7, 48, 1027, 1, 1),
+                                                    (302, 512, 512, 2, 0), (1, 16, 3, 0, 1),
+                                                    (2048, 960, 2560, 0, 0)])
+def test_dense_linear_i8_dev_caller_scratch(vla, orc, torch_cuda, seq, N, K, act, accumulate):
+    """tcpu::dense_linear_i8 with caller-owned scratch (quant_ops.h:66-72) on
+    device pointers: the scratch holds exactly seq x i8_kpad(K) bytes and seq
+    scales, as the reference's contract sizes it; the quantized bytes it leaves
+    there and the output equal the oracle's quantize + dense_linear_i8_pre."""
+    torch = torch_cuda
+    x, W, b = _case(orc, seq, N, K)
+    Kp = (K + 3) & ~3
+    Wq, ws = orc.quantize_weights_i8(W, Kp)
+    dev = torch.device("cuda")
+    xd = torch.from_numpy(x).to(dev)
+    Wd = torch.from_numpy(np.ascontiguousarray(Wq)).to(dev)
+    wsd, bd = torch.from_numpy(ws).to(dev), torch.from_numpy(b).to(dev)
+    xq = torch.full((seq, Kp), 99, dtype=torch.int8, device=dev)
+    sa = torch.zeros(seq, dtype=torch.float32, device=dev)
+    base = np.full((seq, N), 0.25, np.float32)
+    out = torch.from_numpy(base).to(dev)
+    vla.dense_linear_i8_dev(out, xd, Wd, wsd, bd, K, xq, sa, act=act, accumulate=accumulate)
+    torch.cuda.synchronize()
+    xqo, sao = orc.quantize_act_i8(x)
+    assert same_bits(xq.cpu().numpy(), xqo) and same_bits(sa.cpu().numpy(), sao)
+    want = orc.apply_act(orc.dense_linear_i8_pre(xqo, sao, Wq, ws, b, K), act)
+    if accumulate:
+        want = (base + want).astype(np.float32)
+    got = out.cpu().numpy()
+    if act in (0, 1):
+        assert same_bits(got, want)
+    else:
+        assert max_rel(got, want) <= 2e-6

@@ -150,6 +150,40 @@ def test_octo_transformer(vla, ckdir, mask, wrist, tmask):
     _check_replay(lambda: m.forward(t5, sp, sw, 2, tm), got)
 
 
+@pytest.mark.parametrize("mask,wrist,tmask", [(0, True, (1, 1)), (7, True, (1, 1)), (15, True, (1, 1)),
+                                              (7, False, (1, 1)), (7, True, (0, 1))])
+def test_octo_658_tokens(vla, ckdir, mask, wrist, tmask):
+    """the Octo-base graph over the 658-token layout (16
+    task tokens, then per timestep 256 primary + 64 wrist + 1 readout, with no
+    per-step task copy; checkpoint meta repeat_task 0). The reference's
+    forward() always repeats the task tokens, so the checker is the
+    reference's own loaded layers driven over the 658-token layout
+    (RefOcto.forward_layout, oracle/ref_models_shim.cpp), which reproduces
+    forward() bit for bit at the 690-token layout (tests/test_ref_layouts.py).
+    Same bars as the 690-token test."""
+    ck = _ck()
+    from helpers import oracle
+    ob = oracle()
+    c = dict(ck.OCTO_BASE, repeat_task=0)
+    d = str(ckdir / "octo658")
+    if not os.path.exists(os.path.join(d, "octo.bin")):
+        ck.write_octo(d, c)
+    t5, sp, sw, _ = ck.octo_inputs(c)
+    tm = np.array(tmask, np.uint8)
+    sw = sw if wrist else None
+    print(f"octo 658 mask {mask} wrist {wrist} tmask {tmask}", flush=True)
+    r = ob.RefOcto(d, mask, c["d"])
+    ref = r.forward_layout(t5, sp, sw, 2, tm, 0)
+    bar, sens = _bar(mask, lambda x: r.forward_layout(t5, x, sw, 2, tm, 0), sp, ref)
+    m = vla.OctoTransformer(d, mask)
+    assert m.total_tokens(2) == 658
+    got = m.forward(t5, sp, sw, 2, tm)
+    err = _rel(got, ref)
+    print(f"octo 658 mask {mask}: rel err {err:.3e} (reference ulp spread {sens:.3e}, bar {bar:.3e})", flush=True)
+    assert err <= bar
+    _check_replay(lambda: m.forward(t5, sp, sw, 2, tm), got)
+
+
 # ------------------------------------------------------------- SmolVLA ----
 
 @pytest.mark.parametrize("mask,n_pad", [(0, 0), (48, 0), (48, 5)])

@@ -40,7 +40,7 @@ EXPORTS = (
     "vla_hip_malloc", "vla_hip_free", "vla_hip_memcpy_h2d", "vla_hip_memcpy_d2h",
     "vla_hip_memset", "vla_hip_synchronize", "vla_hip_device_name",
     "vla_i8_kpad", "vla_quantize_act_i8", "vla_quantize_act_i8_dev", "vla_pack_weights_i8",
-    "vla_dense_linear_i8_pre", "vla_dense_linear_i8", "vla_dense_linear_i8_pre_dev",
+    "vla_dense_linear_i8_pre", "vla_dense_linear_i8", "vla_dense_linear_i8_dev", "vla_dense_linear_i8_pre_dev",
     "vla_i8_panel_bytes", "vla_quantize_act_i8_panel_dev", "vla_dense_linear_i8_panel_dev",
     "vla_dense_linear_i8_panel_split_dev",
     "vla_rowop_quantize_i8_panel_dev", "vla_rowop_linear_i8_fits", "vla_rowop_linear_i8_dev",
@@ -69,6 +69,7 @@ EXPORTS = (
     "vla_siglip_tf_load", "vla_siglip_tf_free", "vla_siglip_tf_img", "vla_siglip_tf_n_tokens",
     "vla_siglip_tf_out_dim", "vla_siglip_tf_int8_layers", "vla_siglip_tf_graph_nodes",
     "vla_siglip_tf_encode", "vla_siglip_tf_encode_dev",
+    "vla_probe_begin", "vla_probe_end", "vla_probe_count", "vla_probe_shape", "vla_probe_read",
 )
 
 
@@ -119,6 +120,7 @@ def _declare(L):
         "vla_dense_linear_i8_pre": (i32, [P, P, P, P, P, P, i32, i32, i32]),
         "vla_dense_linear_i8": (i32, [P, P, P, P, P, i32, i32, i32]),
         "vla_dense_linear_i8_pre_dev": (i32, [P, i32, P, i32, P, P, i32, P, P, i32, i32, i32, i32, i32, P]),
+        "vla_dense_linear_i8_dev": (i32, [P, i32, P, i32, P, i32, P, P, i32, i32, i32, P, i32, P, i32, i32, P]),
         "vla_i8_panel_bytes": (ctypes.c_int64, [i32, i32]),
         "vla_quantize_act_i8_panel_dev": (i32, [P, i32, P, P, i32, i32, P]),
         "vla_dense_linear_i8_panel_dev": (i32, [P, i32, P, P, P, i32, P, P, i32, i32, i32, i32, i32, P]),
@@ -209,6 +211,11 @@ def _declare(L):
         "vla_siglip_tf_graph_nodes": (i32, [P]),
         "vla_siglip_tf_encode": (i32, [P, P, P]),
         "vla_siglip_tf_encode_dev": (i32, [P, P, P, P]),
+        "vla_probe_begin": (i32, [i32]),
+        "vla_probe_end": (i32, []),
+        "vla_probe_count": (i32, []),
+        "vla_probe_shape": (i32, [i32, P]),
+        "vla_probe_read": (i32, [i32, i32, P, i64]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -477,6 +484,16 @@ def dense_linear_i8_pre_dev(out, xq, ascale, Wq, wscale, bias, K, act=0, accumul
     _call("vla_dense_linear_i8_pre_dev", _dp(out), out.stride(0), _dp(xq), xq.stride(0),
           _dp(ascale), _dp(Wq), Wq.stride(0), _dp(wscale), _dp(bias), seq, N, K, act, accumulate,
           _stream(stream))
+
+
+def dense_linear_i8_dev(out, x, Wq, wscale, bias, K, xq_scratch, ascale_scratch, act=0, accumulate=0,
+                        stream=None):
+    """tcpu::dense_linear_i8 on device tensors with the caller-owned scratch the
+    reference takes: xq_scratch [seq, ldq >= i8_kpad(K)] int8, ascale_scratch [seq]."""
+    seq, N = out.shape[0], Wq.shape[0]
+    _call("vla_dense_linear_i8_dev", _dp(out), out.stride(0), _dp(x), x.stride(0), _dp(Wq), Wq.stride(0),
+          _dp(wscale), _dp(bias), seq, N, K, _dp(xq_scratch), xq_scratch.stride(0), _dp(ascale_scratch),
+          act, accumulate, _stream(stream))
 
 
 def i8_panel_bytes(seq: int, K: int) -> int:
@@ -826,3 +843,35 @@ class SiglipVision(_Handle):
     def encode_dev(self, pixels, out, stream=None):
         _call("vla_siglip_tf_encode_dev", self.h, _dp(pixels), _dp(out), _stream(stream))
 
+
+# ------------------------------------------------------ int8-step probe --
+
+_PROBE_FIELDS = {"src": (0, np.float32, "MK"), "xq": (1, np.int8, "MK"), "ascale": (2, np.float32, "M"),
+                 "before": (3, np.float32, "MN"), "after": (4, np.float32, "MN"), "W": (5, np.int8, "NK"),
+                 "wscale": (6, np.float32, "N"), "bias": (7, np.float32, "N")}
+
+
+def probe_records(run, max_records=512):
+    """Runs run() with the int8-step probe on; returns one dict per int8 GEMM
+    the pass ran (M, K, N, act, acc and the arrays of _PROBE_FIELDS)."""
+    _call("vla_probe_begin", max_records)
+    try:
+        run()
+        recs = []
+        for i in range(int(lib().vla_probe_count())):
+            sh = np.zeros(7, np.int32)
+            _call("vla_probe_shape", i, _ptr(sh))
+            M, K, N, act, acc, has_bias, has_src = (int(v) for v in sh)
+            r = dict(M=M, K=K, N=N, act=act, acc=acc)
+            dims = {"M": M, "K": K, "N": N}
+            for name, (what, dt, shape) in _PROBE_FIELDS.items():
+                if (name == "bias" and not has_bias) or (name == "src" and not has_src):
+                    r[name] = None
+                    continue
+                a = np.empty(tuple(dims[c] for c in shape), dt)
+                _call("vla_probe_read", i, what, _ptr(a), a.nbytes)
+                r[name] = a
+            recs.append(r)
+        return recs
+    finally:
+        _call("vla_probe_end")

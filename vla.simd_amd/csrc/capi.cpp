@@ -224,6 +224,39 @@ VLA_API int32_t vla_dense_linear_i8(float* out, const float* x, const int8_t* Wq
     });
 }
 
+VLA_API int32_t vla_dense_linear_i8_dev(float* out, int32_t ldo, const float* x, int32_t ldx,
+                                        const int8_t* Wq, int32_t ldw, const float* wscale,
+                                        const float* bias, int32_t seq, int32_t N, int32_t K,
+                                        int8_t* xq_scratch, int32_t ldq, float* ascale_scratch,
+                                        int32_t act, int32_t accumulate, void* stream) {
+    return guarded("vla_dense_linear_i8_dev", [&] {
+        VLA_REQUIRE(seq >= 0 && N > 0 && K > 0, "need seq >= 0, N > 0, K > 0");
+        VLA_REQUIRE(K <= kMaxI8K, "K exceeds the int8 accumulator bound INT_MAX/(255*127)");
+        VLA_REQUIRE(seq == 0 || (out && x && Wq && wscale && xq_scratch && ascale_scratch), "null buffer");
+        if (seq == 0) return;
+        hipStream_t st = as_stream(stream);
+        // the reference's contract: xq_scratch holds seq x i8_kpad(K) bytes
+        // (here with row stride ldq), ascale_scratch seq floats
+        launch_quantize_rows(x, ldx, xq_scratch, ldq, ascale_scratch, seq, K, st);
+        GemmArgs a{};
+        a.A = xq_scratch;
+        a.lda = ldq;
+        a.B = Wq;
+        a.ldb = ldw;
+        a.ascale = ascale_scratch;
+        a.wscale = wscale;
+        a.bias = bias;
+        a.out = out;
+        a.ldo = ldo;
+        a.M = seq;
+        a.N = N;
+        a.K = K;
+        a.act = act;
+        a.accumulate = accumulate;
+        launch_gemm_i8(a, st);
+    });
+}
+
 VLA_API int32_t vla_dense_linear_i8_pre_dev(float* out, int32_t ldo, const int8_t* xq, int32_t ldx,
                                             const float* ascale, const int8_t* Wq, int32_t ldw,
                                             const float* wscale, const float* bias, int32_t seq,

@@ -289,3 +289,51 @@ VLA_API int32_t vla_siglip_tf_encode(vla_siglip_tf* h, const float* pixels, floa
         hc.down(out, dout, n);
     });
 }
+
+// ----------------------------------------------------------------- probe --
+
+VLA_API int32_t vla_probe_begin(int32_t max_records) {
+    return guarded("vla_probe_begin", [&] {
+        VLA_REQUIRE(max_records >= 0, "max_records must be >= 0");
+        probe_begin(max_records);
+    });
+}
+
+VLA_API int32_t vla_probe_end(void) {
+    return guarded("vla_probe_end", [&] { probe_end(); });
+}
+
+VLA_API int32_t vla_probe_count(void) { return (int32_t)probe_records().size(); }
+
+VLA_API int32_t vla_probe_shape(int32_t i, int32_t* shape) {
+    return guarded("vla_probe_shape", [&] {
+        const auto& R = probe_records();
+        VLA_REQUIRE(i >= 0 && (size_t)i < R.size() && shape, "record index out of range or null shape");
+        const ProbeRecord& r = R[i];
+        const int32_t v[7] = {r.M, r.K, r.N, r.act, r.acc, r.has_bias, r.has_src};
+        std::memcpy(shape, v, sizeof v);
+    });
+}
+
+VLA_API int32_t vla_probe_read(int32_t i, int32_t what, void* dst, int64_t bytes) {
+    return guarded("vla_probe_read", [&] {
+        const auto& R = probe_records();
+        VLA_REQUIRE(i >= 0 && (size_t)i < R.size() && dst, "record index out of range or null buffer");
+        const ProbeRecord& r = R[i];
+        const void* src = nullptr;
+        size_t n = 0;
+        switch (what) {
+        case VLA_PROBE_SRC: src = r.src.data(); n = r.src.size() * 4; break;
+        case VLA_PROBE_XQ: src = r.xq.data(); n = r.xq.size(); break;
+        case VLA_PROBE_ASCALE: src = r.as.data(); n = r.as.size() * 4; break;
+        case VLA_PROBE_BEFORE: src = r.before.data(); n = r.before.size() * 4; break;
+        case VLA_PROBE_AFTER: src = r.after.data(); n = r.after.size() * 4; break;
+        case VLA_PROBE_W: src = r.W.data(); n = r.W.size(); break;
+        case VLA_PROBE_WSCALE: src = r.ws.data(); n = r.ws.size() * 4; break;
+        case VLA_PROBE_BIAS: src = r.bias.data(); n = r.bias.size() * 4; break;
+        default: throw ArgError("unknown probe field");
+        }
+        VLA_REQUIRE(bytes == (int64_t)n, "buffer size does not match the field");
+        if (n) std::memcpy(dst, src, n);
+    });
+}

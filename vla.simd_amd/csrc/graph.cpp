@@ -4,6 +4,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <fstream>
+#include <map>
 #include <sstream>
 
 namespace vla {
@@ -21,6 +22,133 @@ void* DeviceArena::raw(size_t bytes) {
     VLA_HIP_CHECK(hipMemset(p, 0, b ? b : 256));
     bytes_ += b;
     return p;
+}
+
+// ------------------------------------------------------------------ probe --
+
+namespace {
+
+struct ProbeSrc {
+    std::vector<float> rows;  // [M, K], copied when the slot was written
+    int M = 0, K = 0;
+    int ldq = 0;              // the slot's int8 row stride (0: panel layout)
+};
+
+struct ProbeState {
+    bool on = false;
+    int max_records = 0;
+    std::map<const void*, ProbeSrc> src;  // quantization slot -> the rows last quantized into it
+    std::vector<ProbeRecord> recs;
+    std::vector<void*> bufs;              // fp32 rows a row op wrote only for the probe
+};
+
+ProbeState& probe_state() {
+    static ProbeState p;
+    return p;
+}
+
+std::vector<float> d2h_f32(const float* src, int ld, int rows, int cols) {
+    std::vector<float> h((size_t)rows * cols);
+    if (rows > 0 && cols > 0)
+        VLA_HIP_CHECK(hipMemcpy2D(h.data(), (size_t)cols * 4, src, (size_t)ld * 4, (size_t)cols * 4, rows,
+                                  hipMemcpyDeviceToHost));
+    return h;
+}
+
+// the int8 activations of a slot as [M, K] rows, from either layout
+std::vector<int8_t> d2h_q(const QAct& q, int M, int K) {
+    std::vector<int8_t> h((size_t)M * K);
+    if (q.panel) {
+        const int mp = panel_rows(M);
+        std::vector<int8_t> raw(panel_bytes(M, K));
+        VLA_HIP_CHECK(hipMemcpy(raw.data(), q.q, raw.size(), hipMemcpyDeviceToHost));
+        for (int m = 0; m < M; m++)
+            for (int k = 0; k < K; k++) h[(size_t)m * K + k] = raw[(size_t)(k / 64) * mp * 64 + m * 64 + k % 64];
+    } else {
+        VLA_HIP_CHECK(hipMemcpy2D(h.data(), K, q.q, q.ld, K, M, hipMemcpyDeviceToHost));
+    }
+    return h;
+}
+
+void probe_note(const void* slot, int ldq, const float* rows, int ld, int M, int K, hipStream_t st) {
+    VLA_HIP_CHECK(hipStreamSynchronize(st));
+    ProbeSrc s;
+    s.rows = d2h_f32(rows, ld, M, K);
+    s.M = M;
+    s.K = K;
+    s.ldq = ldq;
+    probe_state().src[slot] = std::move(s);
+}
+
+// The fp32 rows behind int8 rows [q, q + M rows): the whole of a recorded
+// slot, or (row-major slots) a run of its rows.
+bool probe_source(const QAct& q, int M, int K, std::vector<float>& rows) {
+    for (const auto& e : probe_state().src) {
+        const ProbeSrc& s = e.second;
+        const int8_t* base = static_cast<const int8_t*>(e.first);
+        if (s.K != K) continue;
+        if (q.q == base && s.M == M && (s.ldq == 0) == q.panel) {
+            rows = s.rows;
+            return true;
+        }
+        if (s.ldq == 0 || q.panel || q.ld != s.ldq || q.q < base) continue;
+        const size_t off = (size_t)(q.q - base);
+        if (off % s.ldq || off / s.ldq + M > (size_t)s.M) continue;
+        const size_t r0 = off / s.ldq;
+        rows.assign(s.rows.begin() + r0 * K, s.rows.begin() + (r0 + M) * K);
+        return true;
+    }
+    return false;
+}
+
+}  // namespace
+
+void probe_begin(int max_records) {
+    probe_end();
+    ProbeState& P = probe_state();
+    P.on = true;
+    P.max_records = max_records;
+}
+
+void probe_end() {
+    ProbeState& P = probe_state();
+    for (void* p : P.bufs) (void)hipFree(p);
+    P.bufs.clear();
+    P.src.clear();
+    P.recs.clear();
+    P.on = false;
+}
+
+bool probe_on() { return probe_state().on; }
+
+const std::vector<ProbeRecord>& probe_records() { return probe_state().recs; }
+
+void rowq(const RowQArgs& r0, hipStream_t st) {
+    ProbeState& P = probe_state();
+    if (!P.on) {
+        launch_rowq(r0, st);
+        return;
+    }
+    // the fp32 rows behind each quantization, written to probe buffers where
+    // the graph itself keeps only the int8 form
+    RowQArgs r = r0;
+    auto rows_buf = [&]() {
+        void* p = nullptr;
+        VLA_HIP_CHECK(hipMalloc(&p, (size_t)r.rows * r.H * 4 + 16));
+        P.bufs.push_back(p);
+        return static_cast<float*>(p);
+    };
+    if (r.q && !r.out) {
+        r.out = rows_buf();
+        r.ldo = r.H;
+    }
+    if (r.q2 && r.add && !r.out2) {
+        r.out2 = rows_buf();
+        r.ldo2 = r.H;
+    }
+    launch_rowq(r, st);
+    if (r.q) probe_note(r.q, r.q_panel ? 0 : r.ldq, r.out, r.ldo, r.rows, r.H, st);
+    if (r.q2 && r.add) probe_note(r.q2, r.q_panel ? 0 : r.ldq2, r.out2, r.ldo2, r.rows, r.H, st);
 }
 
 void DLinear::init(DeviceArena& A, const std::vector<RowBlock>& blocks, int K_, bool to_int8) {
@@ -79,6 +207,7 @@ void quantize(const Ctx& c, const QAct& dst, const float* x, int ldx, int seq, i
     VLA_REQUIRE(need <= c.xq_bytes && seq <= c.xs_rows, "graph: activation quantization scratch too small");
     if (dst.panel) launch_quantize_rows_panel(x, ldx, dst.q, dst.s, seq, K, c.st);
     else launch_quantize_rows(x, ldx, dst.q, dst.ld, dst.s, seq, K, c.st);
+    if (probe_on()) probe_note(dst.q, dst.panel ? 0 : dst.ld, x, ldx, seq, K, c.st);
 }
 
 static GemmArgs gemm_args(const DLinear& L, float* out, int ldo, int seq, int act, int acc, int n0, int n1) {
@@ -115,7 +244,7 @@ static bool fuse_rowop(int op, int seq, int K, int N) {
         return !(e && e[0] == '0');
     }();
     const bool cheap = seq <= kRowopFuseMaxRows || (op == 0 && seq <= 64 && N <= 1024);
-    return on && cheap && rowop_gemm_fits(op, seq, K);
+    return on && !probe_on() && cheap && rowop_gemm_fits(op, seq, K);
 }
 
 static bool overlaps(const float* p, size_t pn, const float* q, size_t qn) {
@@ -159,7 +288,31 @@ static void gemm_q(const Ctx& c, const DLinear& L, const QAct& x, float* out, in
     a.a_panel = x.panel ? 1 : 0;
     a.split_ws = c.split_ws;
     a.split_bytes = c.split_bytes;
+    ProbeState& P = probe_state();
+    if (!P.on || (int)P.recs.size() >= P.max_records) {
+        launch_gemm_i8(a, c.st);
+        return;
+    }
+    VLA_HIP_CHECK(hipStreamSynchronize(c.st));
+    ProbeRecord rec;
+    rec.M = seq;
+    rec.K = L.K;
+    rec.N = n1 - n0;
+    rec.act = act;
+    rec.acc = acc;
+    rec.has_bias = q.bias() ? 1 : 0;
+    rec.has_src = probe_source(x, seq, L.K, rec.src) ? 1 : 0;
+    rec.xq = d2h_q(x, seq, L.K);
+    rec.as = d2h_f32(x.s, seq, 1, seq);
+    rec.W.resize((size_t)rec.N * L.K);
+    VLA_HIP_CHECK(hipMemcpy2D(rec.W.data(), L.K, a.B, a.ldb, L.K, rec.N, hipMemcpyDeviceToHost));
+    rec.ws = d2h_f32(a.wscale, rec.N, 1, rec.N);
+    if (a.bias) rec.bias = d2h_f32(a.bias, rec.N, 1, rec.N);
+    rec.before = d2h_f32(out, ldo, seq, rec.N);
     launch_gemm_i8(a, c.st);
+    VLA_HIP_CHECK(hipStreamSynchronize(c.st));
+    rec.after = d2h_f32(out, ldo, seq, rec.N);
+    P.recs.push_back(std::move(rec));
 }
 
 void linear(const Ctx& c, const DLinear& L, const In& in, float* out, int ldo, int seq, int act, int acc,
@@ -174,7 +327,7 @@ void linear(const Ctx& c, const DLinear& L, const In& in, float* out, int ldo, i
             VLA_REQUIRE(in.r.rows == seq && in.r.H == L.K && in.q.ld == L.ldq(),
                         "linear: deferred row op made for another layer or row count");
             if (try_rowop_gemm(c, L, in.r, out, ldo, seq, act, acc, n0, n1)) return;
-            launch_rowq(in.r, c.st);
+            rowq(in.r, c.st);
             gemm_q(c, L, in.q, out, ldo, seq, act, acc, n0, n1);
         } else if (in.quantized) {
             gemm_q(c, L, in.q, out, ldo, seq, act, acc, n0, n1);
@@ -222,7 +375,7 @@ In rowop_for(const Ctx& c, const DLinear& L, RowQArgs r, float* f, int ldf, int 
         in.r = r;
         return in;
     }
-    launch_rowq(r, c.st);
+    rowq(r, c.st);
     return in;
 }
 
@@ -292,7 +445,7 @@ void GraphReplay::run(uint64_t key, hipStream_t own, hipStream_t caller,
         calls_ = 0;
     }
     calls_++;
-    if (!graphs_enabled() || calls_ == 1) {
+    if (!graphs_enabled() || calls_ == 1 || probe_on()) {
         // eager: on the caller's stream, ordered with its other work
         f(caller);
         return;

@@ -140,6 +140,27 @@ inline void linear(const Ctx& c, const DLinear& L, float* out, int ldo, const fl
 // the returned In (the rows it reads must not change in between).
 In rowop_for(const Ctx& c, const DLinear& L, RowQArgs r, float* f, int ldf, int slot);
 
+// launch_rowq for the graphs: the same launch, plus the probe's bookkeeping
+// when the probe is on.
+void rowq(const RowQArgs& r, hipStream_t st);
+
+// The int8-step probe (test support, vla_probe_*): while it is on, graphs run
+// eagerly, no row op is fused into a GEMM (the values are the same either
+// way), and each int8 GEMM of a pass is recorded on the host, up to
+// max_records of them: the fp32 rows its activations were quantized from,
+// the int8 activations and scales it read, its weight rows, scales and bias,
+// and its output before and after the launch. Every record costs a device
+// synchronization; nothing of this runs while the probe is off.
+struct ProbeRecord {
+    int M = 0, K = 0, N = 0, act = 0, acc = 0, has_bias = 0, has_src = 0;
+    std::vector<float> src, as, before, after, ws, bias;  // src [M, K], before / after [M, N]
+    std::vector<int8_t> xq, W;                            // xq [M, K], W [N, K]
+};
+void probe_begin(int max_records);
+void probe_end();
+bool probe_on();
+const std::vector<ProbeRecord>& probe_records();
+
 // Which keys a query may see (AttnArgs' mask fields): kind 0 none, 1 dense
 // additive [sq, ldm], 2 causal (key j blocked when j > i + causal_offset),
 // 3 group table (key j blocked when !allow[qg[i] * n_groups + kg[j]]).

@@ -256,7 +256,7 @@ void ActTf::run(hipStream_t st) {
             r.out2 = xp_;
             r.ldo2 = d;
         }
-        launch_rowq(r, st);
+        rowq(r, st);
     };
     auto norm_for = [&](float* x, int rows, const float* w, const float* b, const DLinear& next) {
         RowQArgs r;
@@ -339,7 +339,7 @@ void ActTf::run(hipStream_t st) {
             r.out2 = xp_;
             r.ldo2 = d;
         }
-        launch_rowq(r, st);
+        rowq(r, st);
         linear(c, l.cq, in_q, dq_, d, C);
         attend(st, att_, d, dq_, d, ckb_ + (size_t)li * T * d, d, cvb_ + (size_t)li * T * d, d, C, T,
                heads_, heads_, hd_, scale, none);
