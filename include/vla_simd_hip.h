@@ -149,6 +149,22 @@ VLA_API int32_t vla_dense_linear_i8_dev(float* out, int32_t ldo, const float* x,
                                         int8_t* xq_scratch, int32_t ldq, float* ascale_scratch,
                                         int32_t act, int32_t accumulate, void* stream);
 
+/* No counterpart in the reference: vla_dense_linear_i8_dev for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). Same arguments without the
+ * scratch, same values; it allocates nothing. Its scratch is a fixed array in
+ * the library's device memory, one per GPU, held until the process ends:
+ * 32 MiB of quantized activations (vla_dense_linear_i8_noalloc_max_bytes; the
+ * panel layout up to 128 rows, else seq rows of i8_kpad(K) rounded up to 16
+ * bytes), 65536 row scales and 8 MiB of split-K partial sums. Larger calls
+ * return VLA_ERR_ARG before any launch. Every call on a GPU shares that GPU's
+ * array: calls that overlap on one GPU (two streams or threads) race. */
+VLA_API int32_t vla_dense_linear_i8_noalloc_dev(float* out, int32_t ldo, const float* x, int32_t ldx,
+                                                const int8_t* Wq, int32_t ldw, const float* wscale,
+                                                const float* bias, int32_t seq, int32_t N, int32_t K,
+                                                int32_t act, int32_t accumulate, void* stream);
+VLA_API int64_t vla_dense_linear_i8_noalloc_max_bytes(void);
+
 /* Device form of dense_linear_i8_pre with the fused epilogue options the
  * reference graphs apply right after an int8 forward: act (vla_act, e.g.
  * Linear::forward_gelu, src/nn/linear.cpp:159-168) and accumulate != 0 for

@@ -41,6 +41,7 @@ EXPORTS = (
     "vla_hip_memset", "vla_hip_synchronize", "vla_hip_device_name",
     "vla_i8_kpad", "vla_quantize_act_i8", "vla_quantize_act_i8_dev", "vla_pack_weights_i8",
     "vla_dense_linear_i8_pre", "vla_dense_linear_i8", "vla_dense_linear_i8_dev", "vla_dense_linear_i8_pre_dev",
+    "vla_dense_linear_i8_noalloc_dev", "vla_dense_linear_i8_noalloc_max_bytes",
     "vla_i8_panel_bytes", "vla_quantize_act_i8_panel_dev", "vla_dense_linear_i8_panel_dev",
     "vla_dense_linear_i8_panel_split_dev",
     "vla_rowop_quantize_i8_panel_dev", "vla_rowop_linear_i8_fits", "vla_rowop_linear_i8_dev",
@@ -121,6 +122,8 @@ def _declare(L):
         "vla_dense_linear_i8": (i32, [P, P, P, P, P, i32, i32, i32]),
         "vla_dense_linear_i8_pre_dev": (i32, [P, i32, P, i32, P, P, i32, P, P, i32, i32, i32, i32, i32, P]),
         "vla_dense_linear_i8_dev": (i32, [P, i32, P, i32, P, i32, P, P, i32, i32, i32, P, i32, P, i32, i32, P]),
+        "vla_dense_linear_i8_noalloc_dev": (i32, [P, i32, P, i32, P, i32, P, P, i32, i32, i32, i32, i32, P]),
+        "vla_dense_linear_i8_noalloc_max_bytes": (i64, []),
         "vla_i8_panel_bytes": (ctypes.c_int64, [i32, i32]),
         "vla_quantize_act_i8_panel_dev": (i32, [P, i32, P, P, i32, i32, P]),
         "vla_dense_linear_i8_panel_dev": (i32, [P, i32, P, P, P, i32, P, P, i32, i32, i32, i32, i32, P]),
@@ -494,6 +497,14 @@ def dense_linear_i8_dev(out, x, Wq, wscale, bias, K, xq_scratch, ascale_scratch,
     _call("vla_dense_linear_i8_dev", _dp(out), out.stride(0), _dp(x), x.stride(0), _dp(Wq), Wq.stride(0),
           _dp(wscale), _dp(bias), seq, N, K, _dp(xq_scratch), xq_scratch.stride(0), _dp(ascale_scratch),
           act, accumulate, _stream(stream))
+
+
+def dense_linear_i8_noalloc_dev(out, x, Wq, wscale, bias, K, act=0, accumulate=0, stream=None):
+    """dense_linear_i8_dev with the library's fixed device scratch instead of
+    caller scratch: allocates nothing. Calls that overlap on one GPU race."""
+    seq, N = out.shape[0], Wq.shape[0]
+    _call("vla_dense_linear_i8_noalloc_dev", _dp(out), out.stride(0), _dp(x), x.stride(0), _dp(Wq),
+          Wq.stride(0), _dp(wscale), _dp(bias), seq, N, K, act, accumulate, _stream(stream))
 
 
 def i8_panel_bytes(seq: int, K: int) -> int:
