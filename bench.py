@@ -47,6 +47,13 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
+# The CPU legs follow the baseline protocol: OpenMP threads bound close, one
+# per core (set before any OpenMP runtime in this process starts; a value the
+# caller exported wins), 5 warm-up calls, then the median of >= 50 timed ones.
+os.environ.setdefault("OMP_PROC_BIND", "close")
+os.environ.setdefault("OMP_PLACES", "cores")
+CPU_WARMUP, CPU_TIMED = 5, 50
+
 PEAK_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA (POP/s x 1000)
 PEAK_HBM_GBS = 8000.0    # MI355X HBM3E
 ROTATE_BYTES = 512 << 20
@@ -184,8 +191,33 @@ def profiled_traffic():
     return None
 
 
-def cpu_baseline(synth, budget_s=15.0):
-    """The reference's dense_linear_i8 on this host (oracle/_ref build)."""
+def host_cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo, what lscpu prints as Model name)."""
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_ms(fn, warmup=CPU_WARMUP, timed=CPU_TIMED):
+    """Median wall time in ms of `timed` calls of fn() after `warmup` calls."""
+    for _ in range(warmup):
+        fn()
+    t = []
+    for _ in range(timed):
+        t0 = time.perf_counter()
+        fn()
+        t.append((time.perf_counter() - t0) * 1e3)
+    return float(np.median(t))
+
+
+def cpu_baseline(synth):
+    """The reference's dense_linear_i8 on this host (oracle/_ref build): per
+    shape the median of 50 calls after 5 warm-ups; value = sum of the shapes'
+    ops / sum of their median times."""
     from oracle import bindings as ob
 
     if not ob.ref_available():
@@ -194,36 +226,28 @@ def cpu_baseline(synth, budget_s=15.0):
     sample = [(100, 512, 3200), (50, 960, 2560), (100, 2560, 960), (100, 768, 3072),
               (100, 4096, 4096), (512, 512, 3200), (512, 960, 2560), (512, 2560, 960),
               (512, 768, 3072), (512, 4096, 4096)]
-    tot_ops, tot_t, done = 0.0, 0.0, []
-    t_start = time.time()
+    tot_ops, tot_ms, per = 0.0, 0.0, {}
     for M, K, N in sample:
         x, Wq, ws, b = synth.linear_case(M, K, N)
         blob = ob.ref_panels(Wq, K)
         xq = np.empty((M, (K + 3) & ~3), np.int8)
         sa = np.empty(M, np.float32)
-        ob.ref_dense_linear_i8(x, blob, ws, b, N, K, xq, sa)  # warm
-        reps = 0
-        t0 = time.perf_counter()
-        while True:
-            ob.ref_dense_linear_i8(x, blob, ws, b, N, K, xq, sa)
-            reps += 1
-            el = time.perf_counter() - t0
-            if reps >= 5 and el > 0.5 or el > 3.0:
-                break
-        tot_ops += 2.0 * M * N * K * reps
-        tot_t += el
-        done.append(f"{M}x{K}x{N}")
-        if time.time() - t_start > budget_s:
-            break
+        ms = _median_ms(lambda: ob.ref_dense_linear_i8(x, blob, ws, b, N, K, xq, sa))
+        tot_ops += 2.0 * M * N * K
+        tot_ms += ms
+        per[f"{M}x{K}x{N}"] = round(ms, 4)
+    vnni = bool(L.ref_int8_available())
     return {
-        "value": round(tot_ops / tot_t / 1e12, 4),
+        "value": round(tot_ops / (tot_ms * 1e-3) / 1e12, 4),
         "unit": "TOPS (int8, 2*M*N*K per dense_linear_i8 call)",
         "cores": int(L.ref_omp_max_threads()),
         "kind": "reference",
-        "sample": "reference dense_linear_i8 (quantize + " +
-                  ("AVX-VNNI kernel" if L.ref_int8_available() else "scalar dense_linear_i8_ref: host has no AVX-VNNI") +
-                  ", backend " + L.ref_backend_name().decode() + ") over shapes " + ", ".join(done) +
-                  f"; sum ops / sum wall time, {tot_t:.1f} s of CPU work",
+        "sample": f"reference dense_linear_i8 ({'AVX-VNNI' if vnni else 'scalar ref, no AVX-VNNI'}), "
+                  f"{len(sample)} configs[1] shapes M<=512",
+        "host_cpu": host_cpu_model(),
+        "omp": {k: os.environ.get(k) for k in ("OMP_NUM_THREADS", "OMP_PROC_BIND", "OMP_PLACES")},
+        "protocol": f"{CPU_WARMUP} warm-up + median of {CPU_TIMED} calls per shape; sum ops / sum medians",
+        "median_ms_per_shape": per,
     }
 
 
@@ -247,13 +271,10 @@ def _time_calls(torch, fn, stream_obj, min_calls=20, min_s=0.5):
     return t / n
 
 
-def _time_cpu(fn, min_calls=3, min_s=1.0):
-    fn()
-    n, t0 = 0, time.perf_counter()
-    while n < min_calls or time.perf_counter() - t0 < min_s:
-        fn()
-        n += 1
-    return (time.perf_counter() - t0) * 1e3 / n
+def _time_cpu(fn):
+    """ms per call of a reference CPU leg: the baseline protocol's median of 50
+    after 5 warm-ups."""
+    return _median_ms(fn)
 
 
 def _lat_act(vla, torch, ck, ob, tmp, stream_obj):
@@ -429,7 +450,7 @@ def conv_resnet18(vla, torch, stream_obj, with_cpu=True):
                 L = ob.ref()
                 f = lambda: L.ref_conv2d_i8_packed(ob._p(o), ob._p(x), ob._p(blob), ob._p(ws), ob._p(b), H, Wd,
                                                    Cin, Cout, k, s, p)
-                row["cpu_ref_us"] = round(_time_cpu(f, min_calls=2, min_s=0.3) * 1e3, 1)
+                row["cpu_ref_us"] = round(_time_cpu(f) * 1e3, 1)
                 c_tot += count * row["cpu_ref_us"]
         rows.append(row)
         print(f"  conv {row}", file=sys.stderr, flush=True)

@@ -465,6 +465,9 @@ VLA_API void vla_octo_tf_free(vla_octo_tf* h);
 VLA_API int32_t vla_octo_tf_dim(const vla_octo_tf* h);
 VLA_API int32_t vla_octo_tf_total_tokens(const vla_octo_tf* h, int32_t wnd);
 VLA_API int32_t vla_octo_tf_readout_index(const vla_octo_tf* h, int32_t wnd);
+/* The checkpoint's shapes the inputs must match: cfg[0..6] = {d, n_task,
+ * t5_dim, stem_dim, tok_primary, tok_wrist, max_horizon} (octo.meta keys). */
+VLA_API int32_t vla_octo_tf_config(const vla_octo_tf* h, int32_t* cfg);
 VLA_API int32_t vla_octo_tf_int8_layers(const vla_octo_tf* h);
 VLA_API int32_t vla_octo_tf_graph_nodes(const vla_octo_tf* h);
 /* OctoTransformer::forward (octo_transformer.h:75-81, .cpp:144-219):

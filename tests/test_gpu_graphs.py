@@ -264,3 +264,54 @@ def test_models_load_from_gguf(vla, ckdir):
     outs = [vla.SmolvlaChunk(p, 48).run(prefix, pad, noise) for p in (d, g)]
     assert outs[0].tobytes() == outs[1].tobytes()
     print("act / octo / smolvla from GGUF: identical to the directory loads", flush=True)
+
+
+@pytest.mark.parametrize("line,ok", [("dim 512", True), ("dim   512   ", True), ("dim 512.0", False),
+                                     ("dim 5e2", False), ("n_text -1", False), ("n_text 0", True),
+                                     ("ln_eps 1e-5", True), ("ln_eps x", False), ("extra 1.5 junk", True)])
+def test_act_meta_read_like_the_reference(vla, ckdir, line, ok):
+    """act.meta values are read as the reference reads them
+    (act_transformer.cpp:31-52: `ss >> int` per known key, nothing after it;
+    n_text >= 0): the device loader accepts exactly what the reference accepts."""
+    ck = _ck()
+    from helpers import oracle
+    ob = oracle()
+    c = dict(ck.ACT_BASE, n_enc=1, fh=2, fw=3)
+    d = str(ckdir / f"actmeta_{abs(hash(line))}")
+    ck.write_act(d, c)
+    meta = os.path.join(d, "act.meta")
+    key = line.split()[0]
+    lines = [ln for ln in open(meta).read().splitlines() if ln.split()[0] != key] + [line]
+    with open(meta, "w") as f:
+        f.write("\n".join(lines) + "\n")
+    try:
+        ob.RefAct(d, c["img_ch"], 31, c["chunk"], c["action_dim"])
+        ref_ok = True
+    except RuntimeError:
+        ref_ok = False
+    try:
+        vla.ActTransformer(d, c["img_ch"], 31).close()
+        dev_ok = True
+    except vla.VlaError:
+        dev_ok = False
+    assert ref_ok == ok and dev_ok == ok
+
+
+def test_smolvla_rejects_pad_values_beyond_0_1(vla, ckdir):
+    """The reference sums the raw pad entries into the positions
+    (smolvla_model.cpp:238,245); the device graph refuses anything but 0/1
+    rather than normalising it."""
+    ck = _ck()
+    c = dict(ck.SMOLVLA_BASE, chunk=12, n_layers=2, expert_layers=2, n_prefix=20)
+    d = str(ckdir / "smolpad")
+    ck.write_smolvla(d, c)
+    prefix, pad, noise = ck.smolvla_inputs(c, n_pad=2)
+    m = vla.SmolvlaChunk(d, 48)
+    pad = np.array(pad, np.int32)
+    pad[0] = 2
+    out = np.empty((m.chunk, m.max_action_dim), np.float32)
+    st = vla.lib().vla_smolvla_tf_chunk_run(m.h, vla._ptr(np.ascontiguousarray(prefix, np.float32)),
+                                            vla._ptr(pad), prefix.shape[0],
+                                            vla._ptr(np.ascontiguousarray(noise, np.float32)), vla._ptr(out))
+    assert st == vla.VLA_ERR_ARG
+    assert b"pad entries" in vla.lib().vla_last_error()

@@ -62,7 +62,7 @@ EXPORTS = (
     "vla_act_tf_state_dim", "vla_act_tf_dim", "vla_act_tf_int8_layers", "vla_act_tf_graph_nodes",
     "vla_act_tf_forward", "vla_act_tf_forward_dev",
     "vla_octo_tf_load", "vla_octo_tf_free", "vla_octo_tf_dim", "vla_octo_tf_total_tokens",
-    "vla_octo_tf_readout_index", "vla_octo_tf_int8_layers", "vla_octo_tf_graph_nodes",
+    "vla_octo_tf_readout_index", "vla_octo_tf_config", "vla_octo_tf_int8_layers", "vla_octo_tf_graph_nodes",
     "vla_octo_tf_forward", "vla_octo_tf_forward_dev",
     "vla_smolvla_tf_load", "vla_smolvla_tf_free", "vla_smolvla_tf_chunk",
     "vla_smolvla_tf_max_action_dim", "vla_smolvla_tf_hidden", "vla_smolvla_tf_int8_layers",
@@ -192,6 +192,7 @@ def _declare(L):
         "vla_octo_tf_dim": (i32, [P]),
         "vla_octo_tf_total_tokens": (i32, [P, i32]),
         "vla_octo_tf_readout_index": (i32, [P, i32]),
+        "vla_octo_tf_config": (i32, [P, P]),
         "vla_octo_tf_int8_layers": (i32, [P]),
         "vla_octo_tf_graph_nodes": (i32, [P]),
         "vla_octo_tf_forward": (i32, [P, P, P, P, i32, P, P]),
@@ -735,6 +736,13 @@ class CkptFiles(_Handle):
         return buf.raw[:n]
 
 
+def _need_size(name, a, n, at_least=False):
+    """Raise ValueError unless array a holds n elements (at least n with at_least)."""
+    size = int(np.asarray(a).size)
+    if size < n if at_least else size != n:
+        raise ValueError(f"{name} holds {size} values, the model reads {'at least ' if at_least else ''}{n}")
+
+
 class ActTransformer(_Handle):
     """Device ACT transformer (vla_act_tf_*, ActTransformer of the reference)."""
 
@@ -751,8 +759,16 @@ class ActTransformer(_Handle):
     def graph_nodes(self):
         return lib().vla_act_tf_graph_nodes(self.h)
 
+    def _check(self, feats, n_cams, fh, fw, state):
+        """The sizes the C ABI reads from the host buffers (it cannot see them)."""
+        if min(n_cams, fh, fw) < 1:
+            raise ValueError(f"need n_cams, fh, fw >= 1, got {n_cams}, {fh}, {fw}")
+        _need_size("feats", feats, n_cams * fh * fw * self.img_ch)
+        _need_size("state", state, self.state_dim)
+
     def forward(self, feats, n_cams, fh, fw, state):
         feats, state = _f32(feats), _f32(state)
+        self._check(feats, n_cams, fh, fw, state)
         out = np.empty((self.chunk, self.action_dim), np.float32)
         _call("vla_act_tf_forward", self.h, _ptr(feats), n_cams, fh, fw, _ptr(state), _ptr(out))
         return out
@@ -771,6 +787,19 @@ class OctoTransformer(_Handle):
         super().__init__(lib().vla_octo_tf_load(dirpath.encode(), int8_mask))
         self.d = lib().vla_octo_tf_dim(self.h)
         self.int8_layers = lib().vla_octo_tf_int8_layers(self.h)
+        cfg = np.zeros(7, np.int32)
+        _call("vla_octo_tf_config", self.h, _ptr(cfg))
+        (_, self.n_task, self.t5_dim, self.stem_dim, self.tok_primary, self.tok_wrist,
+         self.max_horizon) = (int(v) for v in cfg)
+
+    def _check(self, t5, stem_p, stem_w, wnd, tm):
+        if not 1 <= wnd <= self.max_horizon:
+            raise ValueError(f"wnd must be in [1, {self.max_horizon}], got {wnd}")
+        _need_size("timestep_mask", tm, wnd, at_least=True)
+        _need_size("t5", t5, self.n_task * self.t5_dim)
+        _need_size("stem_p", stem_p, wnd * self.tok_primary * self.stem_dim)
+        if stem_w is not None:
+            _need_size("stem_w", stem_w, wnd * self.tok_wrist * self.stem_dim)
 
     @property
     def graph_nodes(self):
@@ -786,6 +815,7 @@ class OctoTransformer(_Handle):
         t5, stem_p = _f32(t5), _f32(stem_p)
         stem_w = None if stem_w is None else _f32(stem_w)
         tm = np.ascontiguousarray(tmask, dtype=np.uint8)
+        self._check(t5, stem_p, stem_w, wnd, tm)
         out = np.empty(self.d, np.float32)
         _call("vla_octo_tf_forward", self.h, _ptr(t5), _ptr(stem_p), _ptr(stem_w), wnd, _ptr(tm),
               _ptr(out))
@@ -813,9 +843,18 @@ class SmolvlaChunk(_Handle):
     def graph_nodes(self):
         return lib().vla_smolvla_tf_graph_nodes(self.h)
 
+    def _check(self, prefix, pad, noise):
+        if prefix.ndim != 2 or prefix.shape[1] != self.hidden:
+            raise ValueError(f"prefix must be [n_prefix, {self.hidden}], got {prefix.shape}")
+        _need_size("pad", pad, prefix.shape[0])
+        if not np.all((pad == 0) | (pad == 1)):
+            raise ValueError("pad entries must be 0 (padding) or 1 (real)")
+        _need_size("noise", noise, self.chunk * self.max_action_dim)
+
     def run(self, prefix, pad, noise):
         prefix, noise = _f32(prefix), _f32(noise)
         pad = np.ascontiguousarray(pad, dtype=np.int32)
+        self._check(prefix, pad, noise)
         out = np.empty((self.chunk, self.max_action_dim), np.float32)
         _call("vla_smolvla_tf_chunk_run", self.h, _ptr(prefix), _ptr(pad), prefix.shape[0], _ptr(noise),
               _ptr(out))

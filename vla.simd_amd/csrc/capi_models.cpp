@@ -179,6 +179,16 @@ VLA_API int32_t vla_octo_tf_dim(const vla_octo_tf* h) { return h ? h->m->d() : 0
 VLA_API int32_t vla_octo_tf_total_tokens(const vla_octo_tf* h, int32_t wnd) {
     return h ? h->m->total_tokens(wnd) : 0;
 }
+VLA_API int32_t vla_octo_tf_config(const vla_octo_tf* h, int32_t* cfg) {
+    return guarded("vla_octo_tf_config", [&] {
+        VLA_REQUIRE(h && cfg, "null handle or buffer");
+        const OctoTf& m = *h->m;
+        const int32_t v[7] = {m.d(), m.n_task(), m.t5_dim(), m.stem_dim(), m.tok_primary(), m.tok_wrist(),
+                              m.max_horizon()};
+        std::memcpy(cfg, v, sizeof v);
+    });
+}
+
 VLA_API int32_t vla_octo_tf_readout_index(const vla_octo_tf* h, int32_t wnd) {
     return h ? h->m->readout_index(wnd) : 0;
 }

@@ -11,6 +11,7 @@
 
 #include <cmath>
 #include <cstring>
+#include <filesystem>
 #include <fstream>
 #include <limits>
 #include <set>
@@ -127,27 +128,30 @@ double scalar_value(Cursor& c, uint32_t t) {
 
 }  // namespace
 
+// The mount rule of the reference's io::Mount (find_gguf, src/io/files.cpp:91-108):
+// a model path names a vla.simd GGUF when it is a regular file whose name ends
+// in ".gguf", or a directory in which exactly one entry ends in ".gguf" and no
+// entry ends in ".meta" (a converted .meta/.bin directory is read as files even
+// with a GGUF beside it). Anything else, or a path that does not exist, is not
+// a GGUF: "" is returned.
 std::string find_gguf(const std::string& path_in) {
-    const std::string path = without_trailing_slash(path_in);
-    struct stat st;
-    if (path.empty() || ::stat(path.c_str(), &st) != 0) return {};
-    if (S_ISREG(st.st_mode)) return ends_with(path, ".gguf") ? path : std::string();
-    if (!S_ISDIR(st.st_mode)) return {};
-    DIR* d = ::opendir(path.c_str());
-    if (!d) return {};
-    std::string one;
-    int ggufs = 0, metas = 0;
-    while (const dirent* e = ::readdir(d)) {
-        const std::string name = e->d_name;
-        if (ends_with(name, ".gguf")) {
-            ggufs++;
-            one = name;
-        } else if (ends_with(name, ".meta")) {
-            metas++;
-        }
+    namespace fs = std::filesystem;
+    const fs::path p(without_trailing_slash(path_in));
+    std::error_code ec;
+    if (p.empty()) return {};
+    const fs::file_status st = fs::status(p, ec);  // follows links, as stat() does
+    if (ec) return {};
+    if (fs::is_regular_file(st)) return ends_with(p.string(), ".gguf") ? p.string() : std::string();
+    if (!fs::is_directory(st)) return {};
+    std::vector<std::string> ggufs;
+    bool has_meta = false;
+    for (fs::directory_iterator it(p, ec), end; !ec && it != end; it.increment(ec)) {
+        const std::string name = it->path().filename().string();
+        if (ends_with(name, ".gguf")) ggufs.push_back(name);
+        else if (ends_with(name, ".meta")) has_meta = true;
     }
-    ::closedir(d);
-    return ggufs == 1 && metas == 0 ? path + "/" + one : std::string();
+    if (ec || has_meta || ggufs.size() != 1) return {};
+    return p.string() + "/" + ggufs.front();
 }
 
 CkptFiles::CkptFiles(const std::string& path) : where_(without_trailing_slash(path)) {
@@ -366,6 +370,38 @@ std::map<std::string, double> CkptFiles::meta(const std::string& rel) const {
         m[key] = v;
     }
     return m;
+}
+
+std::vector<std::pair<std::string, std::string>> CkptFiles::meta_lines(const std::string& rel) const {
+    const std::vector<char> raw = bytes(rel);
+    std::istringstream in(std::string(raw.begin(), raw.end()));
+    std::vector<std::pair<std::string, std::string>> out;
+    std::string line;
+    while (std::getline(in, line)) {
+        std::istringstream ls(line);
+        std::string key;
+        if (!(ls >> key)) continue;
+        std::string rest;
+        std::getline(ls, rest);
+        out.emplace_back(key, rest);
+    }
+    return out;
+}
+
+int meta_value_int(const std::string& file, const std::string& key, const std::string& text) {
+    std::istringstream ss(text);
+    int v = 0;
+    ss >> v;
+    VLA_REQUIRE(!ss.fail() && (ss >> std::ws).eof(), file + " key " + key + " is not a plain integer: '" + text + "'");
+    return v;
+}
+
+float meta_value_float(const std::string& file, const std::string& key, const std::string& text) {
+    std::istringstream ss(text);
+    float v = 0.0f;
+    ss >> v;
+    VLA_REQUIRE(!ss.fail() && (ss >> std::ws).eof(), file + " key " + key + " is not a number: '" + text + "'");
+    return v;
 }
 
 int meta_int(const std::map<std::string, double>& m, const char* file, const char* k, int def) {

@@ -25,6 +25,7 @@
 #include <cstdint>
 #include <map>
 #include <string>
+#include <utility>
 #include <vector>
 
 namespace vla {
@@ -46,6 +47,10 @@ public:
     std::vector<char> bytes(const std::string& rel) const;
     // "key value" pairs of a .meta file (whitespace separated, numeric values).
     std::map<std::string, double> meta(const std::string& rel) const;
+    // The lines of a .meta file as (key, rest of the line), in file order, for
+    // loaders that read each value as the reference's getline + `ss >> value` +
+    // end-of-line check does (blank lines skipped).
+    std::vector<std::pair<std::string, std::string>> meta_lines(const std::string& rel) const;
 
 private:
     struct Piece {
@@ -70,6 +75,12 @@ private:
 
 // Whether `path` mounts as a GGUF, and which file ("" otherwise).
 std::string find_gguf(const std::string& path);
+
+// One value of a meta_lines() line read the reference's way: `ss >> int` (or
+// float) must succeed and leave nothing but whitespace ("512.0" and "1e3" are
+// not integers); otherwise ArgError naming the file and key.
+int meta_value_int(const std::string& file, const std::string& key, const std::string& text);
+float meta_value_float(const std::string& file, const std::string& key, const std::string& text);
 
 // The integer value of key k of a parsed .meta file (def when absent), with
 // the reference's metadata_int bounds (src/models/arena.h:21-25): a finite

@@ -189,11 +189,17 @@ float clip_from_env() {
 ConvShape conv_shape(int H, int Wd, int Cin, int k, int stride, int pad, int Cout) {
     VLA_REQUIRE(H > 0 && Wd > 0 && Cin > 0 && Cout > 0 && k > 0 && stride > 0 && pad >= 0,
                 "conv2d_i8: need positive H, Wd, Cin, Cout, k, stride and pad >= 0");
-    VLA_REQUIRE(H + 2 * pad >= k && Wd + 2 * pad >= k, "conv2d_i8: kernel larger than the padded input");
+    // all extents in 64-bit before any of them is derived (a pad near 2^30
+    // must not wrap H + 2 * pad)
+    const int64_t hp = (int64_t)H + 2 * (int64_t)pad, wp = (int64_t)Wd + 2 * (int64_t)pad;
+    VLA_REQUIRE(hp >= k && wp >= k, "conv2d_i8: kernel larger than the padded input");
     VLA_REQUIRE((int64_t)k * k * Cin <= kMaxI8K, "conv2d_i8: K = k*k*Cin exceeds INT_MAX/(255*127)");
+    const int64_t ho = (hp - k) / stride + 1, wo = (wp - k) / stride + 1;
+    VLA_REQUIRE(ho * wo < (1 << 30) && (int64_t)H * Wd * Cin < ((int64_t)1 << 31),
+                "conv2d_i8: input or output too large");
     ConvShape c;
-    c.Hout = (H + 2 * pad - k) / stride + 1;
-    c.Wout = (Wd + 2 * pad - k) / stride + 1;
+    c.Hout = (int)ho;
+    c.Wout = (int)wo;
     c.K = k * k * Cin;
     VLA_REQUIRE((int64_t)c.Hout * c.Wout < (1 << 30) && (int64_t)H * Wd * Cin < ((int64_t)1 << 31),
                 "conv2d_i8: input or output too large");

@@ -34,10 +34,6 @@ struct Cursor {
     }
 };
 
-int meta_int(const std::map<std::string, double>& m, const char* k, int def) {
-    return vla::hip::meta_int(m, "act.meta", k, def);
-}
-
 // ActTransformer::sinusoid_pos_2d (act_transformer.cpp:189-210): the 2D
 // sinusoidal camera embedding, the y half then the x half; float arithmetic
 // and float libm, as the reference computes it on the host.
@@ -64,22 +60,23 @@ void sinusoid_pos_2d(int fh, int fw, int dim, float* out) {
 
 ActTf::ActTf(const std::string& dir, int img_ch, int int8_mask) {
     const CkptFiles files(dir);  // a converted directory or a vla.simd GGUF
-    const auto m = files.meta("act.meta");
-    d_ = meta_int(m, "dim", d_);
-    heads_ = meta_int(m, "heads", heads_);
-    hd_ = meta_int(m, "head_dim", hd_);
-    ff_ = meta_int(m, "ff", ff_);
-    n_enc_ = meta_int(m, "n_enc", n_enc_);
-    n_dec_ = meta_int(m, "n_dec", n_dec_);
-    chunk_ = meta_int(m, "chunk", chunk_);
-    state_dim_ = meta_int(m, "state_dim", state_dim_);
-    action_dim_ = meta_int(m, "action_dim", action_dim_);
-    n_1d_ = meta_int(m, "n_1d", n_1d_);
-    if (m.count("ln_eps")) eps_ = (float)m.at("ln_eps");
+    // act_transformer.cpp:31-52: each known key's value is read as `ss >> int`
+    // (ln_eps as float) and the rest of its line must be blank; unknown keys
+    // are skipped
+    int n_text = 0;
+    for (const auto& kv : files.meta_lines("act.meta")) {
+        const std::string& k = kv.first;
+        int* dst = k == "dim" ? &d_ : k == "heads" ? &heads_ : k == "head_dim" ? &hd_ : k == "ff" ? &ff_
+                 : k == "n_enc" ? &n_enc_ : k == "n_dec" ? &n_dec_ : k == "chunk" ? &chunk_
+                 : k == "state_dim" ? &state_dim_ : k == "action_dim" ? &action_dim_ : k == "n_1d" ? &n_1d_
+                 : k == "n_text" ? &n_text : nullptr;
+        if (dst) *dst = meta_value_int("act.meta", k, kv.second);
+        else if (k == "ln_eps") eps_ = meta_value_float("act.meta", k, kv.second);
+    }
     img_ch_ = img_ch;
     VLA_REQUIRE(d_ > 0 && d_ % 4 == 0 && heads_ > 0 && hd_ > 0 && heads_ * hd_ == d_ && ff_ > 0 &&
                     chunk_ > 0 && state_dim_ > 0 && action_dim_ > 0 && img_ch > 0 && n_enc_ >= 1 &&
-                    n_dec_ >= 1 && n_1d_ == 2 && std::isfinite(eps_) && eps_ > 0,
+                    n_dec_ >= 1 && n_1d_ == 2 && n_text >= 0 && std::isfinite(eps_) && eps_ > 0,
                 "act.meta: invalid configuration (act_transformer.cpp:56-62 bounds)");
 
     const std::vector<char> raw = files.bytes("act.bin");

@@ -174,6 +174,10 @@ SmolvlaTf::~SmolvlaTf() {
 
 void SmolvlaTf::ensure(const int32_t* pad, int np) {
     VLA_REQUIRE(np >= 2 && np <= 65536 - C_, "smolvla: prefix length out of range");
+    // The reference sums the raw entries into the positions
+    // (smolvla_model.cpp:238,245), so only 0 / 1 mean what the masks assume.
+    for (int j = 0; j < np; j++)
+        VLA_REQUIRE(pad[j] == 0 || pad[j] == 1, "smolvla: pad entries must be 0 (padding) or 1 (real)");
     VLA_REQUIRE(pad[np - 1] != 0, "smolvla: the last prefix token (state) must be real");
     // the masks and positions depend on exactly which prefix tokens are real
     std::vector<uint8_t> real(np);
