@@ -119,6 +119,12 @@ VLA_API int32_t vla_quantize_act_i8(const float* x, int8_t* xq, float* ascale,
 VLA_API int32_t vla_quantize_act_i8_dev(const float* x, int8_t* xq, int32_t ldq, float* ascale,
                                         int32_t seq, int32_t K, void* stream);
 
+/* quantize_span_i8 (quant_ops.h:78-80, gemm_i8.cpp:177-207): q[i] =
+ * clamp(rne(x[i] * inv), +-127) over n elements with one shared inverse scale
+ * (the per-tensor activation quantization of conv2d_i8). */
+VLA_API int32_t vla_quantize_span_i8(const float* x, int8_t* q, int64_t n, float inv);
+VLA_API int32_t vla_quantize_span_i8_dev(const float* x, int8_t* q, int64_t n, float inv, void* stream);
+
 /* pack_weights_i8 (quant_ops.h:58, gemm_i8.cpp:56-89): the same per-row absmax
  * quantizer over W [N, K] fp32, written as device-layout rows Wq [N, i8_kpad(K)]
  * (no panels, no row sums: the i8 MFMA is signed x signed). */

@@ -105,6 +105,73 @@ def ref():
     return _ref
 
 
+# -------------------------------------- the reference's nn on two backends --
+
+REF_HIP_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_ref", "libvla_ref_hip.so")
+_nn_libs = {}
+
+
+def ref_hip_available() -> bool:
+    return os.path.exists(REF_HIP_PATH)
+
+
+def ref_nn(backend: str):
+    """The reference's own nn::Linear / MhaQKV driven by oracle/ref_nn_shim.cpp,
+    on its CPU op backend ("cpu": _ref/libvla_ref.so) or on
+    vla.simd_amd/hal/ops_hip.cpp over libvla_simd_hip.so ("hip":
+    _ref/libvla_ref_hip.so; load the vla package first so one HIP runtime and
+    one copy of libvla_simd_hip.so serve the process)."""
+    if backend not in _nn_libs:
+        L = ref() if backend == "cpu" else ctypes.CDLL(REF_HIP_PATH)
+        P, i = c_void_p, c_int
+        L.ref_nn_linear_forward.argtypes = [P, P, i, i, i, P, i, P]
+        L.ref_nn_linear_forward.restype = i
+        L.ref_nn_mha_forward.argtypes = [i, i, P, P, i, P, P, P, i, i, P, P, P, P]
+        L.ref_nn_mha_forward.restype = i
+        L.ref_nn_pre_vs_ref.argtypes = [P, i, i, P, i, P, P, P]
+        L.ref_nn_pre_vs_ref.restype = i
+        _nn_libs[backend] = L
+    return _nn_libs[backend]
+
+
+def nn_linear_forward(backend, W, b, x, int8=1):
+    W, x = _f32(W), _f32(x)
+    N, K = W.shape
+    out = np.empty((x.shape[0], N), np.float32)
+    q = ref_nn(backend).ref_nn_linear_forward(_p(W), _p(None if b is None else _f32(b)), N, K, int8, _p(x),
+                                              x.shape[0], _p(out))
+    if q < 0:
+        raise RuntimeError("ref_nn_linear_forward failed")
+    return out, bool(q)
+
+
+def nn_mha_forward(backend, dim, heads, W, b, xq, xk, xv, rows, seq_kv, int8=1):
+    """MhaQKV.forward(out, xq, xk, xv, rows, seq_kv): pass the same array object
+    for aliased inputs (the shared-quantization branches key on pointer
+    equality). Returns out, q, k, v."""
+    out = np.empty((rows, dim), np.float32)
+    q = np.empty((rows, dim), np.float32)
+    k = np.zeros((seq_kv, dim), np.float32)
+    v = np.empty((seq_kv, dim), np.float32)
+    st = ref_nn(backend).ref_nn_mha_forward(dim, heads, _p(W), _p(b), int8, _p(xq), _p(xk), _p(xv), rows, seq_kv,
+                                           _p(out), _p(q), _p(k), _p(v))
+    if st != 0:
+        raise RuntimeError("ref_nn_mha_forward failed")
+    return out, q, k, v
+
+
+def nn_pre_vs_ref(backend, W, x, bias):
+    W, x = _f32(W), _f32(x)
+    N, K = W.shape
+    pre = np.empty((x.shape[0], N), np.float32)
+    refo = np.empty((x.shape[0], N), np.float32)
+    st = ref_nn(backend).ref_nn_pre_vs_ref(_p(W), N, K, _p(x), x.shape[0], _p(None if bias is None else _f32(bias)),
+                                          _p(pre), _p(refo))
+    if st != 0:
+        raise RuntimeError("ref_nn_pre_vs_ref failed")
+    return pre, refo
+
+
 # ------------------------------------------------------------------ frand --
 
 class Frand:

@@ -1,0 +1,87 @@
+/*
+ * ref_nn_shim.cpp - extern "C" entry points that drive the REFERENCE's own
+ * nn::Linear and nn::MhaQKV (src/nn/linear.cpp, src/nn/attention.cpp) on
+ * whichever op backend the library is linked with:
+ *   _ref/libvla_ref.so      the reference's CPU backend (AVX2 / AVX-VNNI)
+ *   _ref/libvla_ref_hip.so  vla.simd_amd/hal/ops_hip.cpp, i.e. libvla_simd_hip.so
+ * so one test can run the reference's layer code on both and compare.
+ *
+ * TEST INFRASTRUCTURE ONLY; the product never loads it.
+ */
+#include "nn/attention.h"
+#include "nn/linear.h"
+#include "ops/quant_ops.h"
+
+#include <cstdio>
+#include <cstring>
+#include <exception>
+#include <vector>
+
+#define REF_API extern "C" __attribute__((visibility("default")))
+
+using namespace tcpu;
+
+/* nn::Linear(W [N, K], b [N], Role::Gemm), init_int8 when int8 != 0, then
+ * forward(out [seq, N], x [seq, K]). Returns 1 if the layer is int8, 0 if
+ * fp32, -1 on an exception. */
+REF_API int ref_nn_linear_forward(const float* W, const float* b, int N, int K, int int8, const float* x,
+                                  int seq, float* out) {
+    try {
+        nn::Linear lin;
+        lin.init(W, b, N, K, nn::Linear::Role::Gemm);
+        const bool q = int8 && lin.init_int8();
+        lin.forward(out, x, seq);
+        return q ? 1 : 0;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "ref_nn_linear_forward: %s\n", e.what());
+        return -1;
+    }
+}
+
+/* test_ops.cpp:195-220's layer: an nn::MhaQKV of `heads` heads over dim whose
+ * four projections all take W [dim, dim] and b [dim] (int8 when int8 != 0),
+ * run as forward(out, xq, xk, xv, rows, seq_kv): inputs that alias take the
+ * shared-quantization branches (attention.cpp:40-59). q/k/v get the projected
+ * rows the attention read (Scratch q, k, v). Returns 0, or -1 on an exception. */
+REF_API int ref_nn_mha_forward(int dim, int heads, const float* W, const float* b, int int8, const float* xq,
+                               const float* xk, const float* xv, int rows, int seq_kv, float* out, float* q,
+                               float* k, float* v) {
+    try {
+        nn::MhaQKV layer;
+        layer.set_shape(heads, dim / heads);
+        for (nn::Linear* lin : {&layer.wq, &layer.wk, &layer.wv, &layer.wo}) {
+            lin->init(W, b, dim, dim, nn::Linear::Role::Gemm);
+            if (int8) lin->init_int8();
+        }
+        nn::Scratch s;
+        layer.forward(out, xq, xk, xv, rows, seq_kv, s);
+        std::memcpy(q, s.q.data(), (size_t)rows * dim * sizeof(float));
+        std::memcpy(v, s.v.data(), (size_t)seq_kv * dim * sizeof(float));
+        if (!layer.wk.kt_ok()) std::memcpy(k, s.k.data(), (size_t)seq_kv * dim * sizeof(float));
+        return 0;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "ref_nn_mha_forward: %s\n", e.what());
+        return -1;
+    }
+}
+
+/* The backend's pack + pre kernel against its scalar statement of the same
+ * call (test_ops.cpp:138-157): W [N, K] fp32 packed by pack_weights_i8, x
+ * quantized by quantize_act_i8; pre [seq, N] from dense_linear_i8_pre, ref
+ * from dense_linear_i8_ref. Returns 0, or -1 on an exception. */
+REF_API int ref_nn_pre_vs_ref(const float* W, int N, int K, const float* x, int seq, const float* bias, float* pre,
+                              float* ref) {
+    try {
+        std::vector<int32_t> packed(packed_i8_words(N, K));
+        std::vector<float> ws(N), as(seq);
+        std::vector<int8_t> xq((size_t)seq * i8_kpad(K));
+        pack_weights_i8(W, (int8_t*)packed.data(), ws.data(), N, K);
+        quantize_act_i8(x, xq.data(), as.data(), seq, K);
+        dense_linear_i8_pre(pre, xq.data(), as.data(), (const int8_t*)packed.data(), ws.data(), bias, seq, N, K);
+        dense_linear_i8_ref(ref, xq.data(), as.data(), (const int8_t*)packed.data(), ws.data(), bias, seq, N, K);
+        return 0;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "ref_nn_pre_vs_ref: %s\n", e.what());
+        return -1;
+    }
+}

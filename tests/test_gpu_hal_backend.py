@@ -1,0 +1,111 @@
+"""The reference's own nn layer on the HIP op backend.
+
+vla.simd_amd/hal/ops_hip.cpp implements the reference's op layer
+(src/ops/quant_ops.h, lm_ops.h, conv_ops.h) over libvla_simd_hip.so;
+oracle/Makefile's ref_hip target compiles it against the reference's headers
+and links it with the reference's own nn::Linear, nn::MhaQKV, nn::EncoderLayer
+and fp32 GEMM objects into oracle/_ref/libvla_ref_hip.so, exactly as a
+maintainer would build the TCPU_HAL_HIP backend. These tests drive that build
+(through oracle/ref_nn_shim.cpp) next to the reference's CPU build.
+
+Bars: the reference's own assertions hold on the HIP backend bit for bit
+(test_ops.cpp:138-157 dense_linear_i8_pre == dense_linear_i8_ref;
+test_ops.cpp:188-220 shared quantization == separate quantization); int8
+linears and the q/k/v projections equal the CPU build bit for bit; the
+attention output (fp32 softmax, ulp differences between backends) is within
+1e-5 of the output scale when wo is fp32, and within a few int8 steps of
+the output scale (2e-2) when wo re-quantizes it.
+"""
+
+import numpy as np
+import pytest
+
+from helpers import same_bits
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def nn(vla):
+    from helpers import oracle
+    ob = oracle()
+    if not ob.ref_hip_available():
+        pytest.fail("oracle/_ref/libvla_ref_hip.so is not built (make -C oracle ref_hip)")
+    ob.ref_nn("hip")
+    return ob
+
+
+def _rv(fr, n, lo=-1.0, hi=1.0):
+    return fr.rv(n, lo, hi)
+
+
+@pytest.mark.parametrize("seq,N,K", [(1, 16, 3), (7, 48, 64), (50, 768, 1027), (13, 64, 17), (257, 96, 48),
+                                     (100, 3200, 512)])
+def test_pre_equals_ref_on_hip_backend(nn, seq, N, K):
+    """test_ops.cpp:138-157 on the HIP backend: pack_weights_i8 +
+    quantize_act_i8, then the device dense_linear_i8_pre against the
+    backend's scalar dense_linear_i8_ref, bit for bit."""
+    fr = nn.Frand()
+    x = _rv(fr, seq * K).reshape(seq, K)
+    W = _rv(fr, N * K, -0.2, 0.2).reshape(N, K)
+    b = _rv(fr, N)
+    pre, ref = nn.nn_pre_vs_ref("hip", W, x, b)
+    assert same_bits(pre, ref)
+    # and the CPU build computes the same values (its panels, its VNNI kernel)
+    pre_cpu, _ = nn.nn_pre_vs_ref("cpu", W, x, b)
+    assert same_bits(pre, pre_cpu)
+
+
+@pytest.mark.parametrize("seq,N,K", [(100, 3200, 512), (50, 2560, 960), (302, 512, 512), (1, 768, 3072)])
+def test_linear_int8_forward_matches_cpu_build(nn, seq, N, K):
+    """nn::Linear::init_int8 + forward (linear.cpp:66-133) on both backends."""
+    fr = nn.Frand()
+    x = _rv(fr, seq * K).reshape(seq, K)
+    W = _rv(fr, N * K, -0.05, 0.05).reshape(N, K)
+    b = _rv(fr, N, -0.02, 0.02)
+    got, q1 = nn.nn_linear_forward("hip", W, b, x)
+    want, q2 = nn.nn_linear_forward("cpu", W, b, x)
+    assert q1 and q2
+    assert same_bits(got, want)
+
+
+@pytest.mark.parametrize("rows", [7, 1])
+def test_shared_quantization_on_hip_backend(nn, rows):
+    """test_ops.cpp:188-220 on the HIP backend: MhaQKV with aliasing inputs
+    (one quantize_act_i8 shared by q|k and k|v, attention.cpp:40-59) equals the
+    same layer on separate copies of the inputs, bit for bit, for every
+    sharing pattern; and both equal the CPU build's projections."""
+    dim, seq = 32, 7
+    fr = nn.Frand()
+    W = _rv(fr, dim * dim)
+    b = _rv(fr, dim)
+    source = _rv(fr, seq * dim).reshape(seq, dim)
+    qcopy, kcopy, vcopy = source.copy(), source.copy(), source.copy()
+    for sharing in range(4):
+        q_in = source if sharing & 1 else qcopy
+        v_in = source if sharing & 2 else vcopy
+        actual = nn.nn_mha_forward("hip", dim, 4, W, b, q_in, source, v_in, rows, seq)
+        expected = nn.nn_mha_forward("hip", dim, 4, W, b, qcopy, kcopy, vcopy, rows, seq)
+        for a, e, what in zip(actual, expected, ("out", "q", "k", "v")):
+            assert same_bits(a, e), f"shared quantization changed {what} (sharing {sharing}, rows {rows})"
+        cpu = nn.nn_mha_forward("cpu", dim, 4, W, b, q_in, source, v_in, rows, seq)
+        for a, c, what in zip(actual[1:], cpu[1:], ("q", "k", "v")):
+            assert same_bits(a, c), f"{what} projection differs from the CPU build"
+        scale = float(np.max(np.abs(cpu[0])))
+        assert float(np.max(np.abs(actual[0] - cpu[0]))) <= 2e-2 * scale
+
+
+def test_mha_fp32_layers_match_cpu_build(nn):
+    """The same layer with fp32 projections: the projections are the
+    reference's own CPU GEMM in both builds (bit-identical); only the
+    attention runs on the device, so the output agrees to 1e-5."""
+    dim, seq, rows = 64, 33, 33
+    fr = nn.Frand()
+    W = _rv(fr, dim * dim, -0.2, 0.2)
+    b = _rv(fr, dim)
+    x = _rv(fr, seq * dim).reshape(seq, dim)
+    hip = nn.nn_mha_forward("hip", dim, 4, W, b, x, x, x, rows, seq, int8=0)
+    cpu = nn.nn_mha_forward("cpu", dim, 4, W, b, x, x, x, rows, seq, int8=0)
+    assert same_bits(hip[1], cpu[1]) and same_bits(hip[3], cpu[3])
+    scale = float(np.max(np.abs(cpu[0])))
+    assert float(np.max(np.abs(hip[0] - cpu[0]))) <= 1e-5 * scale

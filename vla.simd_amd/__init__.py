@@ -40,6 +40,7 @@ EXPORTS = (
     "vla_hip_malloc", "vla_hip_free", "vla_hip_memcpy_h2d", "vla_hip_memcpy_d2h",
     "vla_hip_memset", "vla_hip_synchronize", "vla_hip_device_name",
     "vla_i8_kpad", "vla_quantize_act_i8", "vla_quantize_act_i8_dev", "vla_pack_weights_i8",
+    "vla_quantize_span_i8", "vla_quantize_span_i8_dev",
     "vla_dense_linear_i8_pre", "vla_dense_linear_i8", "vla_dense_linear_i8_dev", "vla_dense_linear_i8_pre_dev",
     "vla_dense_linear_i8_noalloc_dev", "vla_dense_linear_i8_noalloc_max_bytes",
     "vla_i8_panel_bytes", "vla_quantize_act_i8_panel_dev", "vla_dense_linear_i8_panel_dev",
@@ -122,6 +123,8 @@ def _declare(L):
         "vla_dense_linear_i8": (i32, [P, P, P, P, P, i32, i32, i32]),
         "vla_dense_linear_i8_pre_dev": (i32, [P, i32, P, i32, P, P, i32, P, P, i32, i32, i32, i32, i32, P]),
         "vla_dense_linear_i8_dev": (i32, [P, i32, P, i32, P, i32, P, P, i32, i32, i32, P, i32, P, i32, i32, P]),
+        "vla_quantize_span_i8": (i32, [P, P, i64, f32]),
+        "vla_quantize_span_i8_dev": (i32, [P, P, i64, f32, P]),
         "vla_dense_linear_i8_noalloc_dev": (i32, [P, i32, P, i32, P, i32, P, P, i32, i32, i32, i32, i32, P]),
         "vla_dense_linear_i8_noalloc_max_bytes": (i64, []),
         "vla_i8_panel_bytes": (ctypes.c_int64, [i32, i32]),
@@ -488,6 +491,14 @@ def dense_linear_i8_pre_dev(out, xq, ascale, Wq, wscale, bias, K, act=0, accumul
     _call("vla_dense_linear_i8_pre_dev", _dp(out), out.stride(0), _dp(xq), xq.stride(0),
           _dp(ascale), _dp(Wq), Wq.stride(0), _dp(wscale), _dp(bias), seq, N, K, act, accumulate,
           _stream(stream))
+
+
+def quantize_span_i8(x, inv):
+    """tcpu::quantize_span_i8: clamp(rne(x * inv), +-127) with one shared inverse scale."""
+    x = _f32(x)
+    q = np.empty(x.shape, np.int8)
+    _call("vla_quantize_span_i8", _ptr(x), _ptr(q), x.size, float(inv))
+    return q
 
 
 def dense_linear_i8_dev(out, x, Wq, wscale, bias, K, xq_scratch, ascale_scratch, act=0, accumulate=0,

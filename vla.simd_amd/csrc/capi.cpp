@@ -132,6 +132,26 @@ VLA_API int32_t vla_quantize_act_i8_dev(const float* x, int8_t* xq, int32_t ldq,
     });
 }
 
+VLA_API int32_t vla_quantize_span_i8_dev(const float* x, int8_t* q, int64_t n, float inv, void* stream) {
+    return guarded("vla_quantize_span_i8_dev", [&] { launch_quantize_span(x, q, n, inv, as_stream(stream)); });
+}
+
+VLA_API int32_t vla_quantize_span_i8(const float* x, int8_t* q, int64_t n, float inv) {
+    return guarded("vla_quantize_span_i8", [&] {
+        VLA_REQUIRE(n >= 0 && (n == 0 || (x && q)), "need n >= 0 and non-null buffers");
+        if (n == 0) return;
+        Staging& S = staging();
+        auto lk = S.lock();
+        hipStream_t st = library_stream();
+        S.reset(align256((size_t)n * 4) + align256((size_t)n));
+        const float* dx = S.upload(x, (size_t)n, st);
+        int8_t* dq = S.alloc<int8_t>((size_t)n);
+        launch_quantize_span(dx, dq, n, inv, st);
+        VLA_HIP_CHECK(hipMemcpyAsync(q, dq, (size_t)n, hipMemcpyDeviceToHost, st));
+        VLA_HIP_CHECK(hipStreamSynchronize(st));
+    });
+}
+
 VLA_API int32_t vla_pack_weights_i8(const float* W, int8_t* Wq, float* wscale, int32_t N,
                                     int32_t K) {
     // pack_weights_i8 (gemm_i8.cpp:56-89) is the same per-row quantizer over W.

@@ -60,6 +60,8 @@ void launch_quantize_rows_panel(const float* x, int ldx, int8_t* xq, float* scal
                                 hipStream_t st);
 void launch_quantize_rows(const float* x, int ldx, int8_t* xq, int ldq, float* scale,
                           int rows, int K, hipStream_t st);
+// q[i] = clamp(rne(x[i] * inv), +-127) over n elements (quantize_span_i8)
+void launch_quantize_span(const float* x, int8_t* q, int64_t n, float inv, hipStream_t st);
 
 // gemm_i8.hip: epilogue selects raw int32 output (acc32 != nullptr) or the
 // fused dequant/bias/act(/accumulate) fp32 store.

@@ -184,7 +184,39 @@ __global__ __launch_bounds__(256) void quantize_rows_panel_wide(const float* __r
     }
 }
 
+// quantize_span_i8 (src/ops/quant_ops.h:78-80, gemm_i8.cpp:177-207): one
+// shared inverse scale, q = clamp(rne(x * inv), +-127), the same q8 as the row
+// quantizers. VEC: 4 elements per thread (x 16-byte and q 4-byte aligned).
+template <bool VEC>
+__global__ __launch_bounds__(256) void quantize_span_kernel(const float* __restrict__ x, int8_t* __restrict__ q,
+                                                            int64_t n, float inv) {
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (VEC) {
+        for (; 4 * i + 3 < n; i += stride)
+            reinterpret_cast<uint32_t*>(q)[i] = q8x4(reinterpret_cast<const float4*>(x)[i], inv);
+        // the tail (n % 4 elements) by the first threads
+        const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+        const int64_t e = (n & ~(int64_t)3) + t;
+        if (t < 4 && e < n) q[e] = (int8_t)q8(x[e], inv);
+    } else {
+        for (; i < n; i += stride) q[i] = (int8_t)q8(x[i], inv);
+    }
+}
+
 }  // namespace
+
+void launch_quantize_span(const float* x, int8_t* q, int64_t n, float inv, hipStream_t st) {
+    VLA_REQUIRE(n >= 0, "quantize_span: n must be >= 0");
+    VLA_REQUIRE(n == 0 || (x && q), "quantize_span: null buffer");
+    if (n == 0) return;
+    const bool vec = aligned(x, 16) && aligned(q, 4);
+    const int64_t work = vec ? (n + 3) / 4 : n;
+    const int blocks = (int)((work + 255) / 256 < 4096 ? (work + 255) / 256 : 4096);
+    if (vec) quantize_span_kernel<true><<<blocks, 256, 0, st>>>(x, q, n, inv);
+    else quantize_span_kernel<false><<<blocks, 256, 0, st>>>(x, q, n, inv);
+    VLA_LAUNCH_CHECK();
+}
 
 void launch_quantize_rows_panel(const float* x, int ldx, int8_t* xq, float* scale, int rows, int K,
                                 hipStream_t st) {
