@@ -295,6 +295,36 @@ def _lat_act(vla, torch, ck, ob, tmp, stream_obj):
     return row
 
 
+def _lat_act_model(vla, torch, ck, ob, tmp, stream_obj, act_int8):
+    """ACT end to end (vla_act_predict_dev): one 480 x 640 uint8 camera ->
+    normalization -> ResNet-18 -> the ACT_BASE transformer -> un-normalized
+    actions; ACT_INT8 as given (31: transformer int8, 63: backbone too)."""
+    dev, st = torch.device("cuda"), stream_obj.cuda_stream
+    c = ck.ACT_MODEL_BASE
+    d = os.path.join(tmp, "act_model")
+    if not os.path.exists(os.path.join(d, "stats.bin")):
+        ck.write_act_model(d, c)
+    images, state = ck.act_model_inputs(c)
+    saved = os.environ.get("ACT_INT8")
+    os.environ["ACT_INT8"] = str(act_int8)
+    try:
+        m = vla.ActModel(d)
+        r = ob.RefActModel(d) if ob is not None else None
+    finally:
+        if saved is None:
+            os.environ.pop("ACT_INT8", None)
+        else:
+            os.environ["ACT_INT8"] = saved
+    ti, ts = torch.from_numpy(images).to(dev), torch.from_numpy(state).to(dev)
+    ta = torch.empty((c["chunk"], c["action_dim"]), dtype=torch.float32, device=dev)
+    gpu = _time_calls(torch, lambda: m.predict_dev(ti, ts, ta, True, st), stream_obj)
+    row = {"gpu_ms": round(gpu, 4), "image": f"{c['n_cams']}x{c['img_h']}x{c['img_w']}", "act_int8": act_int8,
+           "int8_convs": m.int8_convs, "int8_layers": m.int8_layers, "graph_nodes": m.graph_nodes}
+    if r is not None:
+        row["cpu_ref_ms"] = round(_time_cpu(lambda: r.predict(images, state)), 3)
+    return row
+
+
 def _lat_octo(vla, torch, ck, ob, tmp, stream_obj, repeat_task):
     """Octo-base: 12 x 768; repeat_task 0 is BASELINE's 658-token layout, 1 the
     reference's 690-token layout (the only one the reference runs)."""
@@ -353,7 +383,8 @@ def _lat_siglip(vla, torch, ck, ob, tmp, stream_obj):
     return row
 
 
-def policy_latency(vla, torch, stream_obj, with_cpu=True, models=("act", "octo", "smolvla", "siglip")):
+def policy_latency(vla, torch, stream_obj, with_cpu=True,
+                   models=("act", "act_model", "octo", "smolvla", "siglip")):
     """Per-chunk latency of BASELINE.json configs[2..4] at batch 1, and of
     SmolVLA's SigLIP vision tower per camera image: the device
     graphs (one captured HIP graph per forward, inputs resident in HBM) and the
@@ -373,6 +404,11 @@ def policy_latency(vla, torch, stream_obj, with_cpu=True, models=("act", "octo",
         if "act" in models:
             out["act"] = _lat_act(vla, torch, ck, ob, tmp, stream_obj)
             print(f"  ACT transformer: {out['act']}", file=sys.stderr, flush=True)
+        if "act_model" in models:
+            for mask in (31, 63):
+                out[f"act_model_int8_{mask}"] = _lat_act_model(vla, torch, ck, ob, tmp, stream_obj, mask)
+                print(f"  ACT end to end (ACT_INT8={mask}): {out[f'act_model_int8_{mask}']}", file=sys.stderr,
+                      flush=True)
         if "octo" in models:
             out["octo"] = _lat_octo(vla, torch, ck, ob, tmp, stream_obj, 0)
             print(f"  Octo transformer (658 tokens): {out['octo']}", file=sys.stderr, flush=True)
@@ -475,7 +511,7 @@ def main():
     ap.add_argument("--no-policy", action="store_true", help="skip the per-chunk policy latency leg")
     ap.add_argument("--policy-only", action="store_true",
                     help="only the per-chunk policy latency leg (for rocprofv3 runs)")
-    ap.add_argument("--models", default="act,octo,smolvla,siglip", help="policy graphs to time")
+    ap.add_argument("--models", default="act,act_model,octo,smolvla,siglip", help="policy graphs to time")
     ap.add_argument("--no-conv", action="store_true", help="skip the ResNet-18 conv2d_i8 leg")
     ap.add_argument("--conv-only", action="store_true", help="only the ResNet-18 conv2d_i8 leg")
     ap.add_argument("--profile-only", action="store_true",

@@ -534,6 +534,44 @@ VLA_API int32_t vla_siglip_tf_graph_nodes(const vla_siglip_tf* h);
 VLA_API int32_t vla_siglip_tf_encode(vla_siglip_tf* h, const float* pixels, float* out);
 VLA_API int32_t vla_siglip_tf_encode_dev(vla_siglip_tf* h, const float* pixels, float* out, void* stream);
 
+/* ------------------------------------------------ ACT, model level ------- */
+
+/* The reference's ACT entry points, same names and signatures
+ * (include/vla_simd.h:66-81, src/models/act/act_capi.cpp), for callers that
+ * bind the model library by name (vla_simd/policy_server.py:203-273 binds
+ * vla_act_load / _free / _chunk / _action_dim / _state_dim / _n_cams / _img_h /
+ * _img_w / _predict). model_dir holds config.txt, backbone.meta/.bin,
+ * act.meta/.bin and stats.bin (tools/convert_act.py's files), or is a vla.simd
+ * GGUF carrying them. ACT_INT8 is read at load as act_model.cpp:57-64 reads it
+ * (bits 1..16 the transformer's int8 layers, bit 32 the backbone convs from
+ * ACT_I8_CONV_FROM to ACT_I8_CONV_TO). predict: images = n_cams uint8 HWC
+ * frames at img_h x img_w back to back, state [state_dim] raw, actions
+ * [chunk * action_dim] out, un-normalized when unnormalize != 0; the whole
+ * pass (normalization, ResNet-18, transformer) runs on the device.
+ * Returns VLA_ERR_ARG on a null handle or buffer. */
+VLA_API void* vla_act_load(const char* model_dir);
+VLA_API void vla_act_free(void* h);
+VLA_API int32_t vla_act_chunk(void* h);
+VLA_API int32_t vla_act_action_dim(void* h);
+VLA_API int32_t vla_act_state_dim(void* h);
+VLA_API int32_t vla_act_n_cams(void* h);
+VLA_API int32_t vla_act_img_h(void* h);
+VLA_API int32_t vla_act_img_w(void* h);
+VLA_API int32_t vla_act_predict(void* h, const uint8_t* images, const float* state,
+                                int32_t unnormalize, float* actions);
+/* Extensions with no counterpart in vla_simd.h: predict on device pointers
+ * and a stream (asynchronous; the frames are copied before the call returns
+ * to the stream's order), the backbone alone (ActModel::encode_view for every
+ * camera: feats [n_cams * fh * fw, ch], host pointers), its feature grid, and
+ * the counts of int8 backbone convs / transformer layers and graph nodes. */
+VLA_API int32_t vla_act_predict_dev(void* h, const uint8_t* images, const float* state,
+                                    int32_t unnormalize, float* actions, void* stream);
+VLA_API int32_t vla_act_encode(void* h, const uint8_t* images, float* feats);
+VLA_API int32_t vla_act_feat_shape(void* h, int32_t* fh, int32_t* fw, int32_t* ch);
+VLA_API int32_t vla_act_int8_convs(void* h);
+VLA_API int32_t vla_act_int8_layers(void* h);
+VLA_API int32_t vla_act_graph_nodes(void* h);
+
 /* ------------------------------------------------ int8-step probe (tests) -- */
 
 /* Test support with no counterpart in the reference: a record of every int8

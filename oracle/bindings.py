@@ -475,6 +475,11 @@ def _ref_models():
     L.ref_siglip_load.argtypes, L.ref_siglip_load.restype = [ctypes.c_char_p, i], P
     L.ref_siglip_free.argtypes = [P]
     L.ref_siglip_encode.argtypes = [P, P, P]
+    L.ref_act_model_load.argtypes, L.ref_act_model_load.restype = [ctypes.c_char_p], P
+    L.ref_act_model_free.argtypes = [P]
+    L.ref_act_model_dims.argtypes = [P, P]
+    L.ref_act_model_predict.argtypes, L.ref_act_model_predict.restype = [P, P, P, i, P], i
+    L.ref_act_model_encode.argtypes, L.ref_act_model_encode.restype = [P, P, P], i
     L.ref_mount_read.argtypes = [ctypes.c_char_p, ctypes.c_char_p, P, ctypes.c_longlong]
     L.ref_mount_read.restype = ctypes.c_longlong
     L._models_declared = True
@@ -535,6 +540,36 @@ class RefAct:
     def __del__(self):
         if getattr(self, "h", None):
             _ref_models().ref_act_free(self.h)
+
+
+class RefActModel:
+    """The reference's ActModel (backbone + transformer + stats); ACT_INT8 is
+    read from the environment at load, as the reference reads it."""
+
+    def __init__(self, dirpath):
+        L = _ref_models()
+        self.h = L.ref_act_model_load(dirpath.encode())
+        if not self.h:
+            raise RuntimeError(f"reference ActModel::load failed for {dirpath}")
+        d = np.zeros(9, np.int32)
+        L.ref_act_model_dims(self.h, _p(d))
+        (self.chunk, self.action_dim, self.state_dim, self.n_cams, self.img_h, self.img_w, self.feat_h,
+         self.feat_w, self.feat_ch) = (int(v) for v in d)
+
+    def predict(self, images, state, unnormalize=True):
+        out = np.empty((self.chunk, self.action_dim), np.float32)
+        _ref_models().ref_act_model_predict(self.h, _p(np.ascontiguousarray(images, np.uint8)), _p(_f32(state)),
+                                            int(bool(unnormalize)), _p(out))
+        return out
+
+    def encode(self, images):
+        out = np.empty((self.n_cams * self.feat_h * self.feat_w, self.feat_ch), np.float32)
+        _ref_models().ref_act_model_encode(self.h, _p(np.ascontiguousarray(images, np.uint8)), _p(out))
+        return out
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            _ref_models().ref_act_model_free(self.h)
 
 
 class RefOcto:

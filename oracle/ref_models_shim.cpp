@@ -22,6 +22,7 @@
  *     pad vector, so the chunk starts from given prefix embeddings.
  */
 #include "io/files.h"
+#include "models/act/act_model.h"
 #include "models/act/act_transformer.h"
 #include "models/octo/octo_transformer.h"
 #include "models/smolvla/action_expert.h"
@@ -307,4 +308,53 @@ REF_API int ref_smolvla_chunk(void* h, const float* prefix, const int* pad, int 
 REF_API int ref_smolvla_chunk_len(void* h) { return static_cast<RefSmolvla*>(h)->aex.cfg.chunk; }
 REF_API int ref_smolvla_max_action_dim(void* h) {
     return static_cast<RefSmolvla*>(h)->aex.cfg.max_action_dim;
+}
+
+/* ActModel (src/models/act/act_model.cpp): load reads ACT_INT8 from the
+ * environment as the reference does. dims: chunk, action_dim, state_dim,
+ * n_cams, img_h, img_w, feat_h, feat_w, feat_ch. */
+REF_API void* ref_act_model_load(const char* dir) {
+    try {
+        auto* m = new ActModel();
+        if (!m->load(dir)) {
+            delete m;
+            return nullptr;
+        }
+        return m;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "ref_act_model_load: %s\n", e.what());
+        return nullptr;
+    }
+}
+
+REF_API void ref_act_model_free(void* h) { delete static_cast<ActModel*>(h); }
+
+REF_API void ref_act_model_dims(void* h, int* d) {
+    auto* m = static_cast<ActModel*>(h);
+    int fh = 0, fw = 0;
+    m->backbone.feat_size(m->img_h, m->img_w, &fh, &fw);
+    const int v[9] = {m->chunk(), m->action_dim(), m->state_dim(), m->n_cams, m->img_h, m->img_w,
+                      fh, fw, m->backbone.out_channels()};
+    std::memcpy(d, v, sizeof v);
+}
+
+/* images: n_cams uint8 HWC frames back to back (act_capi.cpp:42-53) */
+REF_API int ref_act_model_predict(void* h, const uint8_t* images, const float* state, int unnormalize,
+                                  float* actions) {
+    auto* m = static_cast<ActModel*>(h);
+    std::vector<const uint8_t*> ip(m->n_cams);
+    for (int c = 0; c < m->n_cams; c++) ip[c] = images + (size_t)c * m->img_h * m->img_w * 3;
+    m->predict(ip.data(), state, unnormalize != 0, actions);
+    return 0;
+}
+
+/* encode_view per camera: feats [n_cams, fh * fw, ch] */
+REF_API int ref_act_model_encode(void* h, const uint8_t* images, float* feats) {
+    auto* m = static_cast<ActModel*>(h);
+    int fh = 0, fw = 0;
+    m->backbone.feat_size(m->img_h, m->img_w, &fh, &fw);
+    const size_t nf = (size_t)fh * fw * m->backbone.out_channels();
+    for (int c = 0; c < m->n_cams; c++)
+        m->encode_view(images + (size_t)c * m->img_h * m->img_w * 3, c, feats + (size_t)c * nf);
+    return 0;
 }

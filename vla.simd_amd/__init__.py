@@ -72,6 +72,9 @@ EXPORTS = (
     "vla_siglip_tf_out_dim", "vla_siglip_tf_int8_layers", "vla_siglip_tf_graph_nodes",
     "vla_siglip_tf_encode", "vla_siglip_tf_encode_dev",
     "vla_probe_begin", "vla_probe_end", "vla_probe_count", "vla_probe_shape", "vla_probe_read",
+    "vla_act_load", "vla_act_free", "vla_act_chunk", "vla_act_action_dim", "vla_act_state_dim",
+    "vla_act_n_cams", "vla_act_img_h", "vla_act_img_w", "vla_act_predict", "vla_act_predict_dev",
+    "vla_act_encode", "vla_act_feat_shape", "vla_act_int8_convs", "vla_act_int8_layers", "vla_act_graph_nodes",
 )
 
 
@@ -218,6 +221,21 @@ def _declare(L):
         "vla_siglip_tf_graph_nodes": (i32, [P]),
         "vla_siglip_tf_encode": (i32, [P, P, P]),
         "vla_siglip_tf_encode_dev": (i32, [P, P, P, P]),
+        "vla_act_load": (P, [c_char_p]),
+        "vla_act_free": (None, [P]),
+        "vla_act_chunk": (i32, [P]),
+        "vla_act_action_dim": (i32, [P]),
+        "vla_act_state_dim": (i32, [P]),
+        "vla_act_n_cams": (i32, [P]),
+        "vla_act_img_h": (i32, [P]),
+        "vla_act_img_w": (i32, [P]),
+        "vla_act_predict": (i32, [P, P, P, i32, P]),
+        "vla_act_predict_dev": (i32, [P, P, P, i32, P, P]),
+        "vla_act_encode": (i32, [P, P, P]),
+        "vla_act_feat_shape": (i32, [P, P, P, P]),
+        "vla_act_int8_convs": (i32, [P]),
+        "vla_act_int8_layers": (i32, [P]),
+        "vla_act_graph_nodes": (i32, [P]),
         "vla_probe_begin": (i32, [i32]),
         "vla_probe_end": (i32, []),
         "vla_probe_count": (i32, []),
@@ -787,6 +805,51 @@ class ActTransformer(_Handle):
     def forward_dev(self, feats, n_cams, fh, fw, state, out, stream=None):
         _call("vla_act_tf_forward_dev", self.h, _dp(feats), n_cams, fh, fw, _dp(state), _dp(out),
               _stream(stream))
+
+
+class ActModel(_Handle):
+    """ACT end to end on the device through the reference's own entry points
+    (vla_act_load / vla_act_predict): uint8 frames + raw state -> actions."""
+
+    _load, _free = "vla_act_load", "vla_act_free"
+
+    def __init__(self, dirpath: str):
+        super().__init__(lib().vla_act_load(dirpath.encode()))
+        L = lib()
+        self.chunk, self.action_dim = L.vla_act_chunk(self.h), L.vla_act_action_dim(self.h)
+        self.state_dim, self.n_cams = L.vla_act_state_dim(self.h), L.vla_act_n_cams(self.h)
+        self.img_h, self.img_w = L.vla_act_img_h(self.h), L.vla_act_img_w(self.h)
+        fh, fw, ch = (c_int32(), c_int32(), c_int32())
+        _call("vla_act_feat_shape", self.h, ctypes.byref(fh), ctypes.byref(fw), ctypes.byref(ch))
+        self.feat_h, self.feat_w, self.feat_ch = fh.value, fw.value, ch.value
+        self.int8_convs, self.int8_layers = L.vla_act_int8_convs(self.h), L.vla_act_int8_layers(self.h)
+
+    @property
+    def graph_nodes(self):
+        return lib().vla_act_graph_nodes(self.h)
+
+    def _check(self, images, state):
+        _need_size("images", images, self.n_cams * self.img_h * self.img_w * 3)
+        _need_size("state", state, self.state_dim)
+
+    def predict(self, images, state, unnormalize=True):
+        images = np.ascontiguousarray(images, np.uint8)
+        state = _f32(state)
+        self._check(images, state)
+        out = np.empty((self.chunk, self.action_dim), np.float32)
+        _call("vla_act_predict", self.h, _ptr(images), _ptr(state), int(bool(unnormalize)), _ptr(out))
+        return out
+
+    def predict_dev(self, images, state, out, unnormalize=True, stream=None):
+        _call("vla_act_predict_dev", self.h, _dp(images), _dp(state), int(bool(unnormalize)), _dp(out),
+              _stream(stream))
+
+    def encode(self, images):
+        images = np.ascontiguousarray(images, np.uint8)
+        _need_size("images", images, self.n_cams * self.img_h * self.img_w * 3)
+        out = np.empty((self.n_cams * self.feat_h * self.feat_w, self.feat_ch), np.float32)
+        _call("vla_act_encode", self.h, _ptr(images), _ptr(out))
+        return out
 
 
 class OctoTransformer(_Handle):

@@ -128,6 +128,80 @@ def act_inputs(cfg: dict = ACT_BASE, seed: int = synth.BASE_SEED):
     return feats, state
 
 
+# ACT end to end (ActModel, src/models/act/act_model.cpp): one 480 x 640
+# camera through ResNet-18 (15 x 20 x 512 features) into ACT_BASE's
+# transformer. width scales the trunk's channels (64 for ResNet-18).
+ACT_MODEL_BASE = dict(ACT_BASE, img_h=480, img_w=640, n_cams=1, width=64, norm_eps=1e-8)
+
+
+def resnet18_blocks(width: int = 64):
+    """ResNet-18's basic blocks as backbone.meta lists them (cin, cout, stride,
+    has_down): two per stage, the first of stages 2-4 strided with a 1x1
+    projection (tools/_common.py:112-133)."""
+    out, cin = [], width
+    for si in range(4):
+        cout = width << si
+        for b in range(2):
+            stride = 2 if si > 0 and b == 0 else 1
+            down = int(stride != 1 or cin != cout)
+            out.append((cin, cout, stride, down))
+            cin = cout
+    return out
+
+
+def write_act_model(dirpath: str, cfg: dict = ACT_MODEL_BASE, seed: int = synth.BASE_SEED) -> str:
+    """A whole ACT checkpoint as tools/convert_act.py writes it: config.txt,
+    backbone.meta/.bin (BatchNorm folded into conv biases; weights NHWC
+    [Cout][k][k][Cin]), act.meta/.bin (the transformer over the trunk's
+    channels) and stats.bin (state, action, then per-camera image mean/std)."""
+    os.makedirs(dirpath, exist_ok=True)
+    c = cfg
+    w = c["width"]
+    blocks = resnet18_blocks(w)
+    with open(os.path.join(dirpath, "config.txt"), "w") as f:
+        f.write(f"img_h {c['img_h']}\nimg_w {c['img_w']}\nn_cams {c['n_cams']}\nnorm_eps {c['norm_eps']}\n")
+        for i in range(c["n_cams"]):
+            f.write(f"cam{i} cam_{i}\n")
+    lines = ["in_ch 3", f"stem_out {w}", "stem_k 7", "stem_stride 2", "stem_pad 3", "pool_k 3",
+             "pool_stride 2", "pool_pad 1"] + [f"block {a} {b} {st} {d}" for a, b, st, d in blocks]
+    with open(os.path.join(dirpath, "backbone.meta"), "w") as f:
+        f.write("\n".join(lines) + "\n")
+    a = _Arena("bb", seed)
+
+    def conv(name, cout, k, cin):
+        bound = math.sqrt(3.0 / (k * k * cin))
+        a.parts.append(synth.uniform(f"bb.{name}.w", (cout, k, k, cin), -bound, bound, seed))
+        a.parts.append(synth.normal(f"bb.{name}.b", (cout,), 0.05, seed))
+
+    conv("stem", w, 7, 3)
+    for i, (cin, cout, st, d) in enumerate(blocks):
+        conv(f"b{i}.c1", cout, 3, cin)
+        conv(f"b{i}.c2", cout, 3, cout)
+        if d:
+            conv(f"b{i}.down", cout, 1, cin)
+    a.write(os.path.join(dirpath, "backbone.bin"))
+    write_act(dirpath, dict(c, img_ch=blocks[-1][1]), seed)
+    sd, ad = c["state_dim"], c["action_dim"]
+    parts = [synth.normal("act.stats.state_mean", (sd,), 1.0, seed),
+             0.5 + synth.uniform("act.stats.state_std", (sd,), 0.0, 1.0, seed),
+             synth.normal("act.stats.action_mean", (ad,), 1.0, seed),
+             0.5 + synth.uniform("act.stats.action_std", (ad,), 0.0, 1.0, seed)]
+    for i in range(c["n_cams"]):
+        parts.append(np.array([0.485, 0.456, 0.406], np.float32))
+        parts.append(np.array([0.229, 0.224, 0.225], np.float32))
+    np.concatenate([np.asarray(p, np.float32).reshape(-1) for p in parts]).tofile(
+        os.path.join(dirpath, "stats.bin"))
+    return dirpath
+
+
+def act_model_inputs(cfg: dict = ACT_MODEL_BASE, seed: int = synth.BASE_SEED):
+    """uint8 frames [n_cams, img_h, img_w, 3] and a raw state [state_dim]."""
+    u = synth.uniform("act.in.images", (cfg["n_cams"], cfg["img_h"], cfg["img_w"], 3), 0.0, 256.0, seed)
+    images = np.clip(np.floor(u), 0, 255).astype(np.uint8)
+    state = synth.normal("act.in.raw_state", (cfg["state_dim"],), 2.0, seed)
+    return images, state
+
+
 def write_octo(dirpath: str, cfg: dict = OCTO_BASE, seed: int = synth.BASE_SEED) -> str:
     os.makedirs(dirpath, exist_ok=True)
     c = cfg

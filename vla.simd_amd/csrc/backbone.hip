@@ -1,0 +1,159 @@
+// backbone.hip - the element-wise and gather kernels of ACT's ResNet-18 image
+// backbone (src/models/act/resnet_backbone.cpp) and its camera/state
+// processing (src/models/act/act_model.cpp). The convolutions themselves are
+// GEMMs: fp32 ones as im2col + the fp32 matrix-core linear (linear_f32.hip),
+// int8 ones (ACT_INT8 bit 32) as conv2d_i8 (conv.hip).
+//
+// Layouts are the reference's: images uint8 HWC, feature maps NHWC fp32
+// [H, W, C], conv weights [Cout][k][k][Cin], so an im2col row is the taps
+// [ky][kx][ci] of one output pixel (src/hal/common/conv.cpp:117-176).
+#include "common.h"
+
+#include <cmath>
+
+#pragma clang fp contract(off)
+
+namespace vla {
+namespace hip {
+namespace {
+
+// act_model.cpp:109-123: (pixel / 255 - mean[c]) / (std[c] + eps), the
+// lerobot NormalizerProcessorStep order, one camera's [npx, 3] block per
+// blockIdx.y (stats [n_cams][3]).
+__global__ __launch_bounds__(256) void normalize_u8_kernel(float* __restrict__ out, const uint8_t* __restrict__ img,
+                                                           int64_t npx3, const float* __restrict__ mean,
+                                                           const float* __restrict__ stdv, float eps) {
+    const int cam = blockIdx.y;
+    const uint8_t* src = img + (int64_t)cam * npx3;
+    float* dst = out + (int64_t)cam * npx3;
+    const float* m = mean + cam * 3;
+    const float* s = stdv + cam * 3;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < npx3; i += (int64_t)gridDim.x * blockDim.x) {
+        const int c = (int)(i % 3);
+        dst[i] = ((float)src[i] / 255.0f - m[c]) / (s[c] + eps);
+    }
+}
+
+// im2col of an NHWC map for a k x k conv: row p = output pixel (oy, ox),
+// column (ky * k + kx) * Cin + ci = x[oy*stride - pad + ky][ox*stride - pad + kx][ci],
+// zero outside the image; columns [K, ldc) are left alone (never read).
+__global__ __launch_bounds__(256) void im2col_f32_kernel(float* __restrict__ col, int ldc, const float* __restrict__ x,
+                                                         int H, int Wd, int Cin, int k, int stride, int pad, int Wout,
+                                                         int64_t total) {
+    const int K = k * k * Cin;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t p = e / K;
+        const int r = (int)(e - p * K);
+        const int ci = r % Cin, t = r / Cin, kx = t % k, ky = t / k;
+        const int oy = (int)(p / Wout), ox = (int)(p % Wout);
+        const int iy = oy * stride - pad + ky, ix = ox * stride - pad + kx;
+        const bool in = iy >= 0 && iy < H && ix >= 0 && ix < Wd;
+        col[p * ldc + r] = in ? x[((int64_t)iy * Wd + ix) * Cin + ci] : 0.0f;
+    }
+}
+
+// maxpool2d_relu (src/hal/common/conv.cpp:192-224): padded taps count as -inf,
+// then the folded ReLU (!(v > 0) -> 0).
+__global__ __launch_bounds__(256) void maxpool_relu_kernel(float* __restrict__ out, const float* __restrict__ x, int H,
+                                                           int Wd, int C, int k, int stride, int pad, int Hout,
+                                                           int Wout) {
+    const int64_t total = (int64_t)Hout * Wout * C;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
+        const int c = (int)(e % C);
+        const int64_t p = e / C;
+        const int oy = (int)(p / Wout), ox = (int)(p % Wout);
+        float o = -INFINITY;
+        for (int ky = 0; ky < k; ky++) {
+            const int iy = oy * stride - pad + ky;
+            if (iy < 0 || iy >= H) continue;
+            for (int kx = 0; kx < k; kx++) {
+                const int ix = ox * stride - pad + kx;
+                if (ix < 0 || ix >= Wd) continue;
+                const float v = x[((int64_t)iy * Wd + ix) * C + c];
+                o = v > o ? v : o;
+            }
+        }
+        out[e] = o > 0.0f ? o : 0.0f;
+    }
+}
+
+// the basic block's tail (resnet_backbone.cpp:296-303): o = max(o + identity, 0)
+// as v > 0 ? v : 0
+__global__ __launch_bounds__(256) void add_relu_kernel(float* __restrict__ o, const float* __restrict__ idn, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const float v = o[i] + idn[i];
+        o[i] = v > 0.0f ? v : 0.0f;
+    }
+}
+
+// relu in place as the reference's relu (eltwise.cpp:209-215): x < 0 -> 0
+__global__ __launch_bounds__(256) void relu_kernel(float* __restrict__ x, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        if (x[i] < 0.0f) x[i] = 0.0f;
+}
+
+// per-column affine of [rows, cols]: mode 0 (x - a[c]) / (b[c] + eps) (the
+// state normalization, act_model.cpp:145-147), mode 1 fma(x, b[c], a[c]) (the
+// action un-normalization v * std + mean, :152-157, which the reference's
+// -ffp-contract=fast build emits as one fma)
+__global__ __launch_bounds__(256) void col_affine_kernel(float* __restrict__ out, const float* __restrict__ x, int rows,
+                                                         int cols, const float* __restrict__ a,
+                                                         const float* __restrict__ b, float eps, int mode) {
+    const int64_t n = (int64_t)rows * cols;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const int c = (int)(i % cols);
+        out[i] = mode == 0 ? (x[i] - a[c]) / (b[c] + eps) : fmaf(x[i], b[c], a[c]);
+    }
+}
+
+int grid_for(int64_t n) {
+    const int64_t b = (n + 255) / 256;
+    return (int)(b < 8192 ? (b > 0 ? b : 1) : 8192);
+}
+
+}  // namespace
+
+void launch_normalize_u8(float* out, const uint8_t* img, int n_cams, int64_t npx, const float* mean,
+                         const float* stdv, float eps, hipStream_t st) {
+    VLA_REQUIRE(n_cams > 0 && npx > 0 && out && img && mean && stdv, "normalize: bad arguments");
+    const dim3 grid(grid_for(npx * 3) < 1024 ? grid_for(npx * 3) : 1024, n_cams);
+    normalize_u8_kernel<<<grid, 256, 0, st>>>(out, img, npx * 3, mean, stdv, eps);
+    VLA_LAUNCH_CHECK();
+}
+
+void launch_im2col_f32(float* col, int ldc, const float* x, int H, int Wd, int Cin, int k, int stride, int pad,
+                       int Hout, int Wout, hipStream_t st) {
+    const int64_t K = (int64_t)k * k * Cin;
+    VLA_REQUIRE(ldc >= K && col && x, "im2col: bad arguments");
+    const int64_t total = (int64_t)Hout * Wout * K;
+    im2col_f32_kernel<<<grid_for(total), 256, 0, st>>>(col, ldc, x, H, Wd, Cin, k, stride, pad, Wout, total);
+    VLA_LAUNCH_CHECK();
+}
+
+void launch_maxpool_relu(float* out, const float* x, int H, int Wd, int C, int k, int stride, int pad, int Hout,
+                         int Wout, hipStream_t st) {
+    VLA_REQUIRE(out && x && Hout > 0 && Wout > 0 && C > 0, "maxpool: bad arguments");
+    maxpool_relu_kernel<<<grid_for((int64_t)Hout * Wout * C), 256, 0, st>>>(out, x, H, Wd, C, k, stride, pad, Hout,
+                                                                           Wout);
+    VLA_LAUNCH_CHECK();
+}
+
+void launch_add_relu(float* o, const float* idn, int64_t n, hipStream_t st) {
+    add_relu_kernel<<<grid_for(n), 256, 0, st>>>(o, idn, n);
+    VLA_LAUNCH_CHECK();
+}
+
+void launch_relu_inplace(float* x, int64_t n, hipStream_t st) {
+    relu_kernel<<<grid_for(n), 256, 0, st>>>(x, n);
+    VLA_LAUNCH_CHECK();
+}
+
+void launch_col_affine(float* out, const float* x, int rows, int cols, const float* a, const float* b, float eps,
+                       int mode, hipStream_t st) {
+    VLA_REQUIRE(rows > 0 && cols > 0 && out && x && a && b, "col_affine: bad arguments");
+    col_affine_kernel<<<grid_for((int64_t)rows * cols), 256, 0, st>>>(out, x, rows, cols, a, b, eps, mode);
+    VLA_LAUNCH_CHECK();
+}
+
+}  // namespace hip
+}  // namespace vla

@@ -347,3 +347,76 @@ VLA_API int32_t vla_probe_read(int32_t i, int32_t what, void* dst, int64_t bytes
         if (n) std::memcpy(dst, src, n);
     });
 }
+
+// ------------------------------------------------------ ACT (model level) --
+// The reference's own ACT entry points (include/vla_simd.h:66-81,
+// src/models/act/act_capi.cpp): void* handles, 0 from the accessors on a null
+// handle, VLA_ERR_ARG for null buffers, exceptions as VLA_ERR_EXCEPTION.
+
+namespace {
+ActModel* act_model(void* h) { return static_cast<ActModel*>(h); }
+}  // namespace
+
+VLA_API void* vla_act_load(const char* model_dir) {
+    ActModel* m = nullptr;
+    const int32_t rc = guarded("vla_act_load", [&] {
+        VLA_REQUIRE(model_dir, "null model directory");
+        m = new ActModel(model_dir);
+    });
+    return rc == 0 ? m : nullptr;
+}
+VLA_API void vla_act_free(void* h) { delete act_model(h); }
+VLA_API int32_t vla_act_chunk(void* h) { return h ? act_model(h)->chunk() : 0; }
+VLA_API int32_t vla_act_action_dim(void* h) { return h ? act_model(h)->action_dim() : 0; }
+VLA_API int32_t vla_act_state_dim(void* h) { return h ? act_model(h)->state_dim() : 0; }
+VLA_API int32_t vla_act_n_cams(void* h) { return h ? act_model(h)->n_cams() : 0; }
+VLA_API int32_t vla_act_img_h(void* h) { return h ? act_model(h)->img_h() : 0; }
+VLA_API int32_t vla_act_img_w(void* h) { return h ? act_model(h)->img_w() : 0; }
+VLA_API int32_t vla_act_int8_convs(void* h) { return h ? act_model(h)->int8_convs() : 0; }
+VLA_API int32_t vla_act_int8_layers(void* h) { return h ? act_model(h)->int8_layers() : 0; }
+VLA_API int32_t vla_act_graph_nodes(void* h) { return h ? act_model(h)->graph_nodes() : 0; }
+VLA_API int32_t vla_act_feat_shape(void* h, int32_t* fh, int32_t* fw, int32_t* ch) {
+    return guarded("vla_act_feat_shape", [&] {
+        VLA_REQUIRE(h && fh && fw && ch, "null handle or buffer");
+        *fh = act_model(h)->feat_h();
+        *fw = act_model(h)->feat_w();
+        *ch = act_model(h)->feat_ch();
+    });
+}
+
+VLA_API int32_t vla_act_predict(void* h, const uint8_t* images, const float* state, int32_t unnormalize,
+                                float* actions) {
+    if (!h || !images || !state || !actions) return VLA_ERR_ARG;
+    return guarded("vla_act_predict", [&] {
+        ActModel& m = *act_model(h);
+        HostCall hc;
+        const size_t nimg = (size_t)m.n_cams() * m.img_h() * m.img_w() * 3;
+        const uint8_t* di = hc.up(images, nimg);
+        const float* ds = hc.up(state, (size_t)m.state_dim());
+        const size_t na = (size_t)m.chunk() * m.action_dim();
+        float* da = hc.out(na);
+        m.predict_dev(di, ds, unnormalize != 0, da, hc.st);
+        hc.down(actions, da, na);
+    });
+}
+
+VLA_API int32_t vla_act_predict_dev(void* h, const uint8_t* images, const float* state, int32_t unnormalize,
+                                    float* actions, void* stream) {
+    if (!h || !images || !state || !actions) return VLA_ERR_ARG;
+    return guarded("vla_act_predict_dev", [&] {
+        act_model(h)->predict_dev(images, state, unnormalize != 0, actions, as_stream(stream));
+    });
+}
+
+VLA_API int32_t vla_act_encode(void* h, const uint8_t* images, float* feats) {
+    if (!h || !images || !feats) return VLA_ERR_ARG;
+    return guarded("vla_act_encode", [&] {
+        ActModel& m = *act_model(h);
+        HostCall hc;
+        const uint8_t* di = hc.up(images, (size_t)m.n_cams() * m.img_h() * m.img_w() * 3);
+        const size_t nf = (size_t)m.n_cams() * m.feat_h() * m.feat_w() * m.feat_ch();
+        float* df = hc.out(nf);
+        m.encode_dev(di, df, hc.st);
+        hc.down(feats, df, nf);
+    });
+}

@@ -190,6 +190,24 @@ struct ConvArgs {
 };
 void launch_conv2d_i8(const ConvArgs& a, hipStream_t st);
 
+// backbone.hip: ACT's image backbone around its GEMMs (NHWC fp32 maps)
+// (pixel / 255 - mean[cam][c]) / (std[cam][c] + eps) for n_cams frames of npx pixels
+void launch_normalize_u8(float* out, const uint8_t* img, int n_cams, int64_t npx, const float* mean,
+                         const float* stdv, float eps, hipStream_t st);
+// col [Hout * Wout, ldc]: the k x k taps [ky][kx][ci] of every output pixel, zero outside
+void launch_im2col_f32(float* col, int ldc, const float* x, int H, int Wd, int Cin, int k, int stride, int pad,
+                       int Hout, int Wout, hipStream_t st);
+// max pool with -inf padding, then the folded relu (!(v > 0) -> 0)
+void launch_maxpool_relu(float* out, const float* x, int H, int Wd, int C, int k, int stride, int pad, int Hout,
+                         int Wout, hipStream_t st);
+// o = o + idn > 0 ? o + idn : 0
+void launch_add_relu(float* o, const float* idn, int64_t n, hipStream_t st);
+// x < 0 -> 0
+void launch_relu_inplace(float* x, int64_t n, hipStream_t st);
+// [rows, cols] per column: mode 0 (x - a) / (b + eps), mode 1 fma(x, b, a)
+void launch_col_affine(float* out, const float* x, int rows, int cols, const float* a, const float* b, float eps,
+                       int mode, hipStream_t st);
+
 // RoPE-NeoX from a cos/sin table cs[(t * head_dim/2 + i) * 2 + {0, 1}]
 // (double; rope_cos_sin in graph.h builds it the way rope_neox does)
 void launch_rope_table(float* x, int ld, const double* cs, int seq, int n_heads, int head_dim,

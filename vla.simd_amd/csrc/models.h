@@ -73,6 +73,76 @@ private:
     GraphReplay replay_;
 };
 
+// ------------------------------------------------------------ ACT policy --
+// src/models/act/act_model.{h,cpp} + resnet_backbone.{h,cpp}: uint8 camera
+// frames -> per-camera normalization -> ResNet-18 trunk (BatchNorm folded into
+// conv biases, 7x7/s2 stem, 3x3/s2 max pool with the folded ReLU, basic
+// blocks) -> ActTf -> action un-normalization. Files: config.txt,
+// backbone.meta/.bin, act.meta/.bin, stats.bin (a directory or a vla.simd
+// GGUF carrying them). ACT_INT8 is read at load as act_model.cpp:57-64 reads
+// it: bits 1..16 pick the transformer's int8 layers, bit 32 routes the
+// backbone convs of stages [ACT_I8_CONV_FROM, ACT_I8_CONV_TO) through
+// conv2d_i8 (stage 0 the stem, 1.. the blocks).
+class ActModel {
+public:
+    explicit ActModel(const std::string& dir);
+    ~ActModel();
+    int chunk() const { return tf_->chunk(); }
+    int action_dim() const { return tf_->action_dim(); }
+    int state_dim() const { return tf_->state_dim(); }
+    int n_cams() const { return n_cams_; }
+    int img_h() const { return img_h_; }
+    int img_w() const { return img_w_; }
+    int feat_h() const { return fh_; }
+    int feat_w() const { return fw_; }
+    int feat_ch() const { return feat_ch_; }
+    int int8_convs() const { return n_int8_convs_; }
+    int int8_layers() const { return tf_->int8_layers(); }
+    int graph_nodes() const { return replay_.nodes() + tf_->graph_nodes(); }
+    // device pointers: images [n_cams, img_h, img_w, 3] uint8, state
+    // [state_dim] raw, actions [chunk, action_dim]
+    void predict_dev(const uint8_t* images, const float* state, bool unnormalize, float* actions,
+                     hipStream_t caller);
+    // the backbone alone (encode_view per camera): feats [n_cams * fh * fw, C]
+    void encode_dev(const uint8_t* images, float* feats, hipStream_t caller);
+
+private:
+    struct Conv {
+        int cin = 0, cout = 0, k = 0, stride = 1, pad = 0;
+        float* W = nullptr;  // fp32 [cout, k * k * cin]
+        float* b = nullptr;  // [cout]
+        std::unique_ptr<vla_linear_i8> q8;  // conv2d_i8 weights when the stage is int8
+    };
+    struct Block {
+        Conv c1, c2, down;
+        bool has_down = false;
+    };
+    // out [Hout * Wout, cout] = conv(x [H, W, cin]); relu applies the
+    // reference's relu afterwards
+    void conv(const Conv& c, const float* x, int H, int W, float* out, bool relu, hipStream_t st);
+    void run_backbone(hipStream_t st);
+
+    int img_h_ = 480, img_w_ = 640, n_cams_ = 2;
+    float norm_eps_ = 1e-8f;
+    int pool_k_ = 3, pool_stride_ = 2, pool_pad_ = 1;
+    int fh_ = 0, fw_ = 0, feat_ch_ = 0, n_int8_convs_ = 0;
+    DeviceArena A_;
+    Conv stem_;
+    std::vector<Block> blocks_;
+    std::unique_ptr<ActTf> tf_;
+    float *img_mean_ = nullptr, *img_std_ = nullptr, *state_mean_ = nullptr, *state_std_ = nullptr,
+          *action_mean_ = nullptr, *action_std_ = nullptr;
+    // buffers: the cameras' normalized frames, the trunk's activation maps
+    // (reused camera after camera), the im2col rows, the conv2d_i8 workspace
+    uint8_t* img_in_ = nullptr;  // the frames the captured graph reads
+    float *norm_ = nullptr, *a_ = nullptr, *b_ = nullptr, *c_ = nullptr, *res_ = nullptr, *col_ = nullptr,
+          *feats_ = nullptr, *state_n_ = nullptr, *act_n_ = nullptr;
+    void* work_ = nullptr;
+    size_t work_bytes_ = 0;
+    hipStream_t own_ = nullptr;
+    GraphReplay replay_;
+};
+
 // ------------------------------------------------------------------ Octo --
 // src/models/octo/octo_transformer.{h,cpp}: pre-LN ViT blocks over
 // [task | per timestep: primary, wrist, (repeated task), readout] with the
