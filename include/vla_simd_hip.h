@@ -456,6 +456,24 @@ VLA_API int32_t vla_act_tf_graph_nodes(const vla_act_tf* h);
  * actions_norm [chunk, action_dim]. */
 VLA_API int32_t vla_act_tf_forward(vla_act_tf* h, const float* feats, int32_t n_cams, int32_t fh,
                                    int32_t fw, const float* state_norm, float* actions_norm);
+
+/* IMPACT's transformer (src/models/impact/impact_model.cpp:59-68,
+ * act_transformer.cpp:127-130, 212-250): the same graph loaded with
+ * int8_state != 0 (the state projection joins the img_proj int8 group, mask
+ * bit 8) and run with a text tail: text / text_pos [n_text_real, dim], of which
+ * min(max(n_text_real, 0), act.meta's n_text) rows are appended after the
+ * camera tokens (clamp_text). vla_act_tf_forward(_dev) is this with no text. */
+VLA_API vla_act_tf* vla_act_tf_load_ex(const char* dir, int32_t img_ch, int32_t int8_mask,
+                                       int32_t int8_state);
+VLA_API int32_t vla_act_tf_n_text(const vla_act_tf* h);
+VLA_API int32_t vla_act_tf_forward_text(vla_act_tf* h, const float* feats, int32_t n_cams, int32_t fh,
+                                        int32_t fw, const float* state_norm, const float* text,
+                                        const float* text_pos, int32_t n_text_real,
+                                        float* actions_norm);
+VLA_API int32_t vla_act_tf_forward_text_dev(vla_act_tf* h, const float* feats, int32_t n_cams,
+                                            int32_t fh, int32_t fw, const float* state_norm,
+                                            const float* text, const float* text_pos,
+                                            int32_t n_text_real, float* actions_norm, void* stream);
 VLA_API int32_t vla_act_tf_forward_dev(vla_act_tf* h, const float* feats, int32_t n_cams, int32_t fh,
                                        int32_t fw, const float* state_norm, float* actions_norm,
                                        void* stream);

@@ -130,6 +130,9 @@ def ref_nn(backend: str):
         L.ref_nn_mha_forward.restype = i
         L.ref_nn_pre_vs_ref.argtypes = [P, i, i, P, i, P, P, P]
         L.ref_nn_pre_vs_ref.restype = i
+        L.ref_unet_load.argtypes, L.ref_unet_load.restype = [ctypes.c_char_p, P, i, P], P
+        L.ref_unet_free.argtypes = [P]
+        L.ref_unet_forward.argtypes, L.ref_unet_forward.restype = [P, P, P, P, i], i
         _nn_libs[backend] = L
     return _nn_libs[backend]
 
@@ -158,6 +161,33 @@ def nn_mha_forward(backend, dim, heads, W, b, xq, xk, xv, rows, seq_kv, int8=1):
     if st != 0:
         raise RuntimeError("ref_nn_mha_forward failed")
     return out, q, k, v
+
+
+class NnUnet:
+    """The reference's Diffusion Policy UNet (DPUNet1d) on one op backend."""
+
+    def __init__(self, backend, dirpath, cfg, int8):
+        self.L = ref_nn(backend)
+        vals = np.array([cfg[k] for k in ("action_dim", "horizon")] + list(cfg["down_dims"]) +
+                        [cfg[k] for k in ("kernel_size", "n_groups", "step_embed_dim", "film_scale", "state_dim",
+                                          "n_cams", "num_keypoints")], np.int32)
+        n = np.zeros(1, np.int32)
+        self.h = self.L.ref_unet_load(dirpath.encode(), _p(vals), int(int8), _p(n))
+        if not self.h:
+            raise RuntimeError(f"reference DPUNet1d::load failed for {dirpath}")
+        self.n_int8 = int(n[0])
+        self.cfg = cfg
+
+    def forward(self, sample, gc, t):
+        c = self.cfg
+        eps = np.empty((c["horizon"], c["action_dim"]), np.float32)
+        if self.L.ref_unet_forward(self.h, _p(eps), _p(_f32(sample)), _p(_f32(gc)), int(t)) != 0:
+            raise RuntimeError("ref_unet_forward failed")
+        return eps
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            self.L.ref_unet_free(self.h)
 
 
 def nn_pre_vs_ref(backend, W, x, bias):
@@ -475,6 +505,8 @@ def _ref_models():
     L.ref_siglip_load.argtypes, L.ref_siglip_load.restype = [ctypes.c_char_p, i], P
     L.ref_siglip_free.argtypes = [P]
     L.ref_siglip_encode.argtypes = [P, P, P]
+    L.ref_act_load_ex.argtypes, L.ref_act_load_ex.restype = [ctypes.c_char_p, i, i, i], P
+    L.ref_act_forward_text.argtypes, L.ref_act_forward_text.restype = [P, P, i, i, i, P, P, P, i, P], i
     L.ref_act_model_load.argtypes, L.ref_act_model_load.restype = [ctypes.c_char_p], P
     L.ref_act_model_free.argtypes = [P]
     L.ref_act_model_dims.argtypes = [P, P]
@@ -524,12 +556,18 @@ def ref_mount_read(path, rel):
 
 
 class RefAct:
-    def __init__(self, dirpath, img_ch, int8_mask, chunk, action_dim):
+    def __init__(self, dirpath, img_ch, int8_mask, chunk, action_dim, int8_state=False):
         L = _ref_models()
-        self.h = L.ref_act_load(dirpath.encode(), img_ch, int8_mask)
+        self.h = L.ref_act_load_ex(dirpath.encode(), img_ch, int8_mask, int(bool(int8_state)))
         if not self.h:
             raise RuntimeError(f"reference ActTransformer::load failed for {dirpath}")
         self.chunk, self.action_dim = chunk, action_dim
+
+    def forward_text(self, feats, n_cams, fh, fw, state, text, text_pos, n_text_real):
+        out = np.empty((self.chunk, self.action_dim), np.float32)
+        _ref_models().ref_act_forward_text(self.h, _p(_f32(feats)), n_cams, fh, fw, _p(_f32(state)),
+                                           _p(_f32(text)), _p(_f32(text_pos)), int(n_text_real), _p(out))
+        return out
 
     def forward(self, feats, n_cams, fh, fw, state):
         out = np.empty((self.chunk, self.action_dim), np.float32)

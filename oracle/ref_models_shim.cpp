@@ -80,6 +80,34 @@ REF_API long long ref_mount_read(const char* path, const char* rel, char* buf, l
 
 REF_API void ref_act_free(void* h) { delete static_cast<ActTransformer*>(h); }
 
+/* IMPACT's transformer: load with int8_state (impact_model.cpp:65) and run
+ * with a text tail (act_transformer.cpp:343-360). */
+REF_API void* ref_act_load_ex(const char* dir, int img_ch, int int8_mask, int int8_state) {
+    try {
+        const io::Mount mount(dir);
+        if (!mount.ok()) return nullptr;
+        auto* t = new ActTransformer();
+        if (!t->load(dir, img_ch, int8_mask, int8_state != 0)) {
+            delete t;
+            return nullptr;
+        }
+        return t;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "ref_act_load_ex: %s\n", e.what());
+        return nullptr;
+    }
+}
+
+REF_API int ref_act_forward_text(void* h, const float* feats, int n_cams, int fh, int fw, const float* state_norm,
+                                 const float* text, const float* text_pos, int n_text_real, float* actions_norm) {
+    auto* t = static_cast<ActTransformer*>(h);
+    const int img_ch = t->img_proj.K;
+    std::vector<const float*> cams(n_cams);
+    for (int c = 0; c < n_cams; c++) cams[c] = feats + (size_t)c * fh * fw * img_ch;
+    t->forward(cams.data(), n_cams, fh, fw, state_norm, actions_norm, text, text_pos, n_text_real);
+    return 0;
+}
+
 REF_API int ref_act_forward(void* h, const float* feats, int n_cams, int fh, int fw,
                             const float* state_norm, float* actions_norm) {
     auto* t = static_cast<ActTransformer*>(h);

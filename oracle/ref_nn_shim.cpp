@@ -8,6 +8,7 @@
  *
  * TEST INFRASTRUCTURE ONLY; the product never loads it.
  */
+#include "models/diffusion/unet1d.h"
 #include "nn/attention.h"
 #include "nn/linear.h"
 #include "ops/quant_ops.h"
@@ -82,6 +83,52 @@ REF_API int ref_nn_pre_vs_ref(const float* W, int N, int K, const float* x, int 
         return 0;
     } catch (const std::exception& e) {
         std::fprintf(stderr, "ref_nn_pre_vs_ref: %s\n", e.what());
+        return -1;
+    }
+}
+
+/* Diffusion Policy's noise-prediction UNet (src/models/diffusion/unet1d.cpp)
+ * loaded from <dir>/unet.bin with its W8A8 GEMMs when int8 != 0
+ * (diffusion_model.cpp:113-114: the Gemm-role conv / residual / downsample
+ * linears). cfg[12] = {action_dim, horizon, down0, down1, down2, kernel_size,
+ * n_groups, step_embed_dim, film_scale, state_dim, n_cams, num_keypoints};
+ * n_obs_steps 2. Returns the handle (null on failure); n_int8 gets the count. */
+REF_API void* ref_unet_load(const char* dir, const int* cfg, int int8, int* n_int8) {
+    try {
+        DPConfig c;
+        c.action_dim = cfg[0];
+        c.horizon = cfg[1];
+        c.down_dims = {cfg[2], cfg[3], cfg[4]};
+        c.kernel_size = cfg[5];
+        c.n_groups = cfg[6];
+        c.step_embed_dim = cfg[7];
+        c.film_scale = cfg[8] != 0;
+        c.state_dim = cfg[9];
+        c.n_cams = cfg[10];
+        c.num_keypoints = cfg[11];
+        c.n_obs_steps = 2;
+        auto* u = new DPUNet1d();
+        if (!u->load(dir, "unet", c, int8 != 0)) {
+            delete u;
+            return nullptr;
+        }
+        *n_int8 = u->n_int8;
+        return u;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "ref_unet_load: %s\n", e.what());
+        return nullptr;
+    }
+}
+
+REF_API void ref_unet_free(void* h) { delete static_cast<DPUNet1d*>(h); }
+
+/* eps [horizon, action_dim] = UNet(sample [horizon, action_dim], gc [global_cond_dim], t) */
+REF_API int ref_unet_forward(void* h, float* eps, const float* sample, const float* gc, int t) {
+    try {
+        static_cast<DPUNet1d*>(h)->forward(eps, sample, gc, t);
+        return 0;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "ref_unet_forward: %s\n", e.what());
         return -1;
     }
 }

@@ -122,6 +122,46 @@ def test_act_two_cameras(vla, ckdir):
     assert err <= bar
 
 
+# -------------------------------------------------------------- IMPACT ----
+
+@pytest.mark.parametrize("mask,n_real", [(0, 11), (31, 11), (31, 16), (31, 40), (31, 0), (15, 5)])
+def test_impact_transformer(vla, ckdir, mask, n_real):
+    """IMPACT's W8A8 transformer (impact_model.cpp:59-68): the ACT graph loaded
+    with int8_state (the state projection joins mask bit 8,
+    act_transformer.cpp:127-130) and run with its text tower's tokens and
+    positions appended after the cameras, clamped to act.meta's n_text
+    (build_tokens :212-250). Against the reference's ActTransformer loaded and
+    run the same way; same bars as test_act_transformer."""
+    ck = _ck()
+    from helpers import oracle
+    ob = oracle()
+    c = dict(ck.ACT_BASE, n_text=16, n_enc=2, fh=6, fw=8)
+    d = str(ckdir / "impact")
+    if not os.path.exists(os.path.join(d, "act.bin")):
+        ck.write_act(d, c)
+    feats, state = ck.act_inputs(c)
+    import vla_simd_amd.synth as synth
+    text = synth.normal("impact.text", (c["n_text"], c["dim"]), 1.0)
+    tpos = synth.normal("impact.text_pos", (c["n_text"], c["dim"]), 0.02)
+    print(f"impact mask {mask} n_text_real {n_real}", flush=True)
+    r = ob.RefAct(d, c["img_ch"], mask, c["chunk"], c["action_dim"], int8_state=True)
+    ref = r.forward_text(feats, 1, c["fh"], c["fw"], state, text, tpos, n_real)
+    bar, sens = _bar(mask, lambda f: r.forward_text(f, 1, c["fh"], c["fw"], state, text, tpos, n_real), feats, ref)
+    m = vla.ActTransformer(d, c["img_ch"], mask, int8_state=True)
+    n_i8 = (2 * 4 if mask & 1 else 0) + (2 if mask & 2 else 0) + (2 if mask & 4 else 0) + \
+           (2 if mask & 8 else 0) + (10 if mask & 16 else 0)
+    assert m.n_text == 16 and m.int8_layers == n_i8
+    got = m.forward_text(feats, 1, c["fh"], c["fw"], state, text, tpos, n_real)
+    err = _rel(got, ref)
+    print(f"impact mask {mask} n_text_real {n_real}: rel err {err:.3e} (reference ulp spread {sens:.3e})",
+          flush=True)
+    assert err <= bar
+    _check_replay(lambda: m.forward_text(feats, 1, c["fh"], c["fw"], state, text, tpos, n_real), got)
+    # without text the same handle is the plain ACT transformer (the reference with n_text_real = 0)
+    if n_real == 0:
+        assert m.forward(feats, 1, c["fh"], c["fw"], state).tobytes() == got.tobytes()
+
+
 # ---------------------------------------------------------------- Octo ----
 
 @pytest.mark.parametrize("mask,wrist,tmask", [(0, True, (1, 1)), (7, True, (1, 1)), (15, True, (1, 1)),

@@ -109,3 +109,30 @@ def test_mha_fp32_layers_match_cpu_build(nn):
     assert same_bits(hip[1], cpu[1]) and same_bits(hip[3], cpu[3])
     scale = float(np.max(np.abs(cpu[0])))
     assert float(np.max(np.abs(hip[0] - cpu[0]))) <= 1e-5 * scale
+
+
+@pytest.mark.parametrize("full", [False, True])
+def test_diffusion_unet_int8_linears_on_device(nn, tmp_path, full):
+    """Diffusion Policy's noise-prediction UNet (src/models/diffusion/unet1d.cpp)
+    with DIFFUSION_INT8 bit 1 (diffusion_model.cpp:113-114): the reference's own
+    DPUNet1d on the HIP backend runs its Gemm-role conv, residual and
+    downsample linears (unet1d.cpp:70-80) as dense_linear_i8 on the device;
+    group norm, mish, the 1-D im2col, the transposed convs and the fp32 step /
+    FiLM / output linears are the reference's CPU code in both builds. The int8
+    GEMMs are exact, so the noise prediction equals the CPU build bit for bit,
+    at every timestep. full: lerobot's stock widths (512, 1024, 2048), horizon 64."""
+    from helpers import load_pkg
+    load_pkg()
+    import vla_simd_amd.checkpoints as ck
+    import vla_simd_amd.synth as synth
+    c = dict(ck.DP_UNET_BASE) if full else dict(ck.DP_UNET_BASE, horizon=16, down_dims=(64, 128, 256),
+                                                 step_embed_dim=32, num_keypoints=8)
+    d = ck.write_dp_unet(str(tmp_path / "unet"), c)
+    hip = nn.NnUnet("hip", d, c, 1)
+    cpu = nn.NnUnet("cpu", d, c, 1)
+    assert hip.n_int8 == cpu.n_int8 > 0
+    sample = synth.normal("dp.sample", (c["horizon"], c["action_dim"]))
+    gc = synth.normal("dp.gc", (ck.dp_cond_dim(c) - c["step_embed_dim"],))
+    for t in (0, 37, 99):
+        a, b = hip.forward(sample, gc, t), cpu.forward(sample, gc, t)
+        assert same_bits(a, b), f"UNet noise prediction differs at t={t}"

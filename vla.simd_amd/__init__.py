@@ -61,7 +61,8 @@ EXPORTS = (
     "vla_dense_linear", "vla_dense_linear_dev",
     "vla_act_tf_load", "vla_act_tf_free", "vla_act_tf_chunk", "vla_act_tf_action_dim",
     "vla_act_tf_state_dim", "vla_act_tf_dim", "vla_act_tf_int8_layers", "vla_act_tf_graph_nodes",
-    "vla_act_tf_forward", "vla_act_tf_forward_dev",
+    "vla_act_tf_forward", "vla_act_tf_forward_dev", "vla_act_tf_load_ex", "vla_act_tf_n_text",
+    "vla_act_tf_forward_text", "vla_act_tf_forward_text_dev",
     "vla_octo_tf_load", "vla_octo_tf_free", "vla_octo_tf_dim", "vla_octo_tf_total_tokens",
     "vla_octo_tf_readout_index", "vla_octo_tf_config", "vla_octo_tf_int8_layers", "vla_octo_tf_graph_nodes",
     "vla_octo_tf_forward", "vla_octo_tf_forward_dev",
@@ -193,6 +194,10 @@ def _declare(L):
         "vla_act_tf_graph_nodes": (i32, [P]),
         "vla_act_tf_forward": (i32, [P, P, i32, i32, i32, P, P]),
         "vla_act_tf_forward_dev": (i32, [P, P, i32, i32, i32, P, P, P]),
+        "vla_act_tf_load_ex": (P, [c_char_p, i32, i32, i32]),
+        "vla_act_tf_n_text": (i32, [P]),
+        "vla_act_tf_forward_text": (i32, [P, P, i32, i32, i32, P, P, P, i32, P]),
+        "vla_act_tf_forward_text_dev": (i32, [P, P, i32, i32, i32, P, P, P, i32, P, P]),
         "vla_octo_tf_load": (P, [c_char_p, i32]),
         "vla_octo_tf_free": (None, [P]),
         "vla_octo_tf_dim": (i32, [P]),
@@ -777,11 +782,13 @@ class ActTransformer(_Handle):
 
     _load, _free = "vla_act_tf_load", "vla_act_tf_free"
 
-    def __init__(self, dirpath: str, img_ch: int, int8_mask: int = 31):
-        super().__init__(lib().vla_act_tf_load(dirpath.encode(), img_ch, int8_mask))
+    def __init__(self, dirpath: str, img_ch: int, int8_mask: int = 31, int8_state: bool = False):
+        super().__init__(lib().vla_act_tf_load_ex(dirpath.encode(), img_ch, int8_mask, int(bool(int8_state))))
         L = lib()
+        self.n_text = L.vla_act_tf_n_text(self.h)
         self.chunk, self.action_dim = L.vla_act_tf_chunk(self.h), L.vla_act_tf_action_dim(self.h)
         self.state_dim, self.img_ch = L.vla_act_tf_state_dim(self.h), img_ch
+        self.dim = L.vla_act_tf_dim(self.h)
         self.int8_layers = L.vla_act_tf_int8_layers(self.h)
 
     @property
@@ -805,6 +812,19 @@ class ActTransformer(_Handle):
     def forward_dev(self, feats, n_cams, fh, fw, state, out, stream=None):
         _call("vla_act_tf_forward_dev", self.h, _dp(feats), n_cams, fh, fw, _dp(state), _dp(out),
               _stream(stream))
+
+    def forward_text(self, feats, n_cams, fh, fw, state, text, text_pos, n_text_real):
+        """IMPACT's form: the text tail (its T5 tower's tokens and positions) after the cameras."""
+        feats, state = _f32(feats), _f32(state)
+        self._check(feats, n_cams, fh, fw, state)
+        nt = max(0, min(int(n_text_real), self.n_text))
+        text, text_pos = _f32(text), _f32(text_pos)
+        _need_size("text", text, nt * self.dim, at_least=True)
+        _need_size("text_pos", text_pos, nt * self.dim, at_least=True)
+        out = np.empty((self.chunk, self.action_dim), np.float32)
+        _call("vla_act_tf_forward_text", self.h, _ptr(feats), n_cams, fh, fw, _ptr(state), _ptr(text),
+              _ptr(text_pos), int(n_text_real), _ptr(out))
+        return out
 
 
 class ActModel(_Handle):

@@ -202,6 +202,74 @@ def act_model_inputs(cfg: dict = ACT_MODEL_BASE, seed: int = synth.BASE_SEED):
     return images, state
 
 
+# Diffusion Policy's noise-prediction UNet (src/models/diffusion/unet1d.cpp)
+# at lerobot's stock shape, and a small one for tests.
+DP_UNET_BASE = dict(action_dim=6, horizon=64, down_dims=(512, 1024, 2048), kernel_size=5, n_groups=8,
+                    step_embed_dim=128, film_scale=1, state_dim=6, n_cams=2, num_keypoints=32, n_obs_steps=2)
+
+
+def dp_cond_dim(c: dict) -> int:
+    """DPConfig::cond_dim (config.h:66-69): step embedding + (state + cameras) per obs step."""
+    return c["step_embed_dim"] + (c["state_dim"] + c["n_cams"] * 2 * c["num_keypoints"]) * c["n_obs_steps"]
+
+
+def write_dp_unet(dirpath: str, cfg: dict = DP_UNET_BASE, seed: int = synth.BASE_SEED) -> str:
+    """unet.bin in the order DPUNet1d::load reads it (unet1d.cpp:18-34): step
+    encoder, down blocks (two FiLM res blocks + a k3/s2 downsample but the
+    last), two mid blocks, up blocks (two res blocks + a k4/s2 transposed conv),
+    the final conv block and the 1x1 output conv."""
+    os.makedirs(dirpath, exist_ok=True)
+    c = cfg
+    A, D, k, CD = c["action_dim"], c["step_embed_dim"], c["kernel_size"], dp_cond_dim(cfg)
+    a = _Arena("unet", seed)
+    n = [0]
+
+    def lin(N, K, std=None):
+        n[0] += 1
+        bound = 1.0 / math.sqrt(K)
+        a.parts.append(synth.uniform(f"unet.{n[0]}.w", (N, K), -bound, bound, seed))
+        a.parts.append(synth.normal(f"unet.{n[0]}.b", (N,), 0.02, seed))
+
+    def gn(C):
+        n[0] += 1
+        a.parts.append(1.0 + synth.normal(f"unet.{n[0]}.gs", (C,), 0.02, seed))
+        a.parts.append(synth.normal(f"unet.{n[0]}.gb", (C,), 0.02, seed))
+
+    def res(cin, cout):
+        lin(cout, k * cin)
+        gn(cout)
+        lin(2 * cout if c["film_scale"] else cout, CD)
+        lin(cout, k * cout)
+        gn(cout)
+        if cin != cout:
+            lin(cout, cin)
+
+    lin(4 * D, D)
+    lin(D, 4 * D)
+    dims = list(c["down_dims"])
+    in_out = [(A, dims[0])] + [(dims[i], dims[i + 1]) for i in range(len(dims) - 1)]
+    for i, (ci, co) in enumerate(in_out):
+        res(ci, co)
+        res(co, co)
+        if i + 1 < len(in_out):
+            lin(co, 3 * co)
+    res(dims[-1], dims[-1])
+    res(dims[-1], dims[-1])
+    for ind in range(len(in_out) - 1):
+        dim_out, dim_in = in_out[len(in_out) - 1 - ind]
+        res(dim_in * 2, dim_out)
+        res(dim_out, dim_out)
+        n[0] += 1
+        bound = 1.0 / math.sqrt(4 * dim_out)
+        a.parts.append(synth.uniform(f"unet.{n[0]}.up", (dim_out, 4, dim_out), -bound, bound, seed))
+        a.parts.append(synth.normal(f"unet.{n[0]}.upb", (dim_out,), 0.02, seed))
+    lin(dims[0], k * dims[0])
+    gn(dims[0])
+    lin(A, dims[0])
+    a.write(os.path.join(dirpath, "unet.bin"))
+    return dirpath
+
+
 def write_octo(dirpath: str, cfg: dict = OCTO_BASE, seed: int = synth.BASE_SEED) -> str:
     os.makedirs(dirpath, exist_ok=True)
     c = cfg

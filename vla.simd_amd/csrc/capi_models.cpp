@@ -166,6 +166,46 @@ VLA_API int32_t vla_act_tf_forward(vla_act_tf* h, const float* feats, int32_t n_
     });
 }
 
+VLA_API vla_act_tf* vla_act_tf_load_ex(const char* dir, int32_t img_ch, int32_t int8_mask, int32_t int8_state) {
+    return load_handle<vla_act_tf>("vla_act_tf_load_ex", [&] {
+        VLA_REQUIRE(dir, "null directory");
+        return std::make_unique<ActTf>(dir, img_ch, int8_mask, int8_state != 0);
+    });
+}
+VLA_API int32_t vla_act_tf_n_text(const vla_act_tf* h) { return h ? h->m->n_text() : 0; }
+
+VLA_API int32_t vla_act_tf_forward_text_dev(vla_act_tf* h, const float* feats, int32_t n_cams, int32_t fh,
+                                            int32_t fw, const float* state_norm, const float* text,
+                                            const float* text_pos, int32_t n_text_real, float* actions_norm,
+                                            void* stream) {
+    return guarded("vla_act_tf_forward_text_dev", [&] {
+        VLA_REQUIRE(h, "null handle");
+        h->m->forward_text_dev(feats, n_cams, fh, fw, state_norm, text, text_pos, n_text_real, actions_norm,
+                               as_stream(stream));
+    });
+}
+
+VLA_API int32_t vla_act_tf_forward_text(vla_act_tf* h, const float* feats, int32_t n_cams, int32_t fh, int32_t fw,
+                                        const float* state_norm, const float* text, const float* text_pos,
+                                        int32_t n_text_real, float* actions_norm) {
+    return guarded("vla_act_tf_forward_text", [&] {
+        VLA_REQUIRE(h && feats && state_norm && actions_norm, "null handle or buffer");
+        VLA_REQUIRE(n_cams > 0 && fh > 0 && fw > 0, "camera grid out of range");
+        ActTf& m = *h->m;
+        const int nt = n_text_real < 0 ? 0 : n_text_real > m.n_text() ? m.n_text() : n_text_real;
+        VLA_REQUIRE(nt == 0 || (text && text_pos), "text tokens without their positions");
+        HostCall hc;
+        const float* df = hc.up(feats, (size_t)n_cams * fh * fw * m.img_ch());
+        const float* ds = hc.up(state_norm, (size_t)m.state_dim());
+        const float* dt = nt ? hc.up(text, (size_t)nt * m.dim()) : nullptr;
+        const float* dp = nt ? hc.up(text_pos, (size_t)nt * m.dim()) : nullptr;
+        const size_t na = (size_t)m.chunk() * m.action_dim();
+        float* da = hc.out(na);
+        m.forward_text_dev(df, n_cams, fh, fw, ds, dt, dp, nt, da, hc.st);
+        hc.down(actions_norm, da, na);
+    });
+}
+
 // ------------------------------------------------------------------ Octo --
 
 VLA_API vla_octo_tf* vla_octo_tf_load(const char* dir, int32_t int8_mask) {

@@ -58,12 +58,12 @@ void sinusoid_pos_2d(int fh, int fw, int dim, float* out) {
 
 }  // namespace
 
-ActTf::ActTf(const std::string& dir, int img_ch, int int8_mask) {
+ActTf::ActTf(const std::string& dir, int img_ch, int int8_mask, bool int8_state) {
     const CkptFiles files(dir);  // a converted directory or a vla.simd GGUF
     // act_transformer.cpp:31-52: each known key's value is read as `ss >> int`
     // (ln_eps as float) and the rest of its line must be blank; unknown keys
     // are skipped
-    int n_text = 0;
+    int& n_text = n_text_;
     for (const auto& kv : files.meta_lines("act.meta")) {
         const std::string& k = kv.first;
         int* dst = k == "dim" ? &d_ : k == "heads" ? &heads_ : k == "head_dim" ? &hd_ : k == "ff" ? &ff_
@@ -103,7 +103,9 @@ ActTf::ActTf(const std::string& dir, int img_ch, int int8_mask) {
     auto vec = [&](size_t k) { return A_.upload(take.take(k), k); };
 
     lin(img_proj_, d, img_ch, int8_mask & 8);
-    lin(state_proj_, d, state_dim_, false);  // Role::Generic, kept fp32 (:142-145)
+    // Role::Generic, fp32 (:142-145) unless IMPACT's int8_state joins it to
+    // the img_proj group (:127-130)
+    lin(state_proj_, d, state_dim_, int8_state && (int8_mask & 8));
     latent_ = vec(d);
     pos1d_ = vec((size_t)n_1d_ * d);
 
@@ -155,14 +157,14 @@ ActTf::~ActTf() {
     if (own_) (void)hipStreamDestroy(own_);
 }
 
-void ActTf::ensure(int n_cams, int fh, int fw) {
-    if (n_cams == n_cams_ && fh == fh_ && fw == fw_) return;
+void ActTf::ensure(int n_cams, int fh, int fw, int nt) {
+    if (n_cams == n_cams_ && fh == fh_ && fw == fw_ && nt == nt_) return;
     VLA_REQUIRE(n_cams > 0 && fh > 0 && fw > 0 && (long)n_cams * fh * fw < (1 << 20),
                 "act: camera grid out of range");
     VLA_HIP_CHECK(hipDeviceSynchronize());
     S_.reset();
     auto S = std::make_unique<DeviceArena>();
-    const int T = n_tokens(n_cams, fh, fw), d = d_, C = chunk_;
+    const int T = n_tokens(n_cams, fh, fw, nt), d = d_, C = chunk_;
     const int n_img = fh * fw;
     feats_ = S->alloc<float>((size_t)n_cams * n_img * img_ch_);
     state_ = S->alloc<float>(state_dim_);
@@ -181,7 +183,9 @@ void ActTf::ensure(int n_cams, int fh, int fw) {
     ckb_ = S->alloc<float>((size_t)n_dec_ * T * d);
     cvb_ = S->alloc<float>((size_t)n_dec_ * T * d);
     dq_ = S->alloc<float>((size_t)C * d);
-    // positions: [pos1d | camera embedding per camera] (build_tokens :218-229)
+    text_ = nt ? S->alloc<float>((size_t)nt * d) : nullptr;
+    // positions: [pos1d | camera embedding per camera | text positions, copied
+    // in per call] (build_tokens :218-249)
     std::vector<float> pos((size_t)T * d), cam((size_t)n_img * d);
     sinusoid_pos_2d(fh, fw, d, cam.data());
     std::vector<float> p1((size_t)n_1d_ * d);
@@ -198,6 +202,7 @@ void ActTf::ensure(int n_cams, int fh, int fw) {
     n_cams_ = n_cams;
     fh_ = fh;
     fw_ = fw;
+    nt_ = nt;
     T_ = T;
 }
 
@@ -272,6 +277,7 @@ void ActTf::run(hipStream_t st) {
     copy_f32(x_, latent_, d, st);
     linear(c, state_proj_, x_ + d, d, state_, state_dim_, 1);
     linear(c, img_proj_, x_ + (size_t)n_1d_ * d, d, feats_, img_ch_, n_cams_ * n_img);
+    if (nt_ > 0) copy_f32(x_ + ((size_t)n_1d_ + (size_t)n_cams_ * n_img) * d, text_, (int64_t)nt_ * d, st);
 
     // encode (:252-301)
     In in_qk, in_v;
@@ -353,13 +359,21 @@ void ActTf::run(hipStream_t st) {
     linear(c, head_, act_out_, action_dim_, dx_, d, C);
 }
 
-void ActTf::forward_dev(const float* feats, int n_cams, int fh, int fw, const float* state_norm,
-                        float* actions_norm, hipStream_t caller) {
+void ActTf::forward_text_dev(const float* feats, int n_cams, int fh, int fw, const float* state_norm,
+                             const float* text, const float* text_pos, int n_text_real, float* actions_norm,
+                             hipStream_t caller) {
     VLA_REQUIRE(feats && state_norm && actions_norm, "act: null buffer");
-    ensure(n_cams, fh, fw);
+    // clamp_text (act_transformer.h:79): only real text tokens enter the sequence
+    const int nt = n_text_real < 0 ? 0 : n_text_real > n_text_ ? n_text_ : n_text_real;
+    VLA_REQUIRE(nt == 0 || (text && text_pos), "act: text tokens without their positions");
+    ensure(n_cams, fh, fw, nt);
     copy_f32(feats_, feats, (int64_t)n_cams * fh * fw * img_ch_, caller);
     copy_f32(state_, state_norm, state_dim_, caller);
-    const uint64_t key = ((uint64_t)n_cams << 40) | ((uint64_t)fh << 20) | (uint64_t)fw;
+    if (nt > 0) {
+        copy_f32(text_, text, (int64_t)nt * d_, caller);
+        copy_f32(pos_ + ((size_t)n_1d_ + (size_t)n_cams * fh * fw) * d_, text_pos, (int64_t)nt * d_, caller);
+    }
+    const uint64_t key = ((uint64_t)nt << 50) | ((uint64_t)n_cams << 40) | ((uint64_t)fh << 20) | (uint64_t)fw;
     replay_.run(key, own_, caller, [this](hipStream_t st) { run(st); });
     copy_f32(actions_norm, act_out_, (int64_t)chunk_ * action_dim_, caller);
 }

@@ -23,21 +23,35 @@ namespace hip {
 // queries, final LayerNorm and an fp32 action head. int8 mask bits as
 // act_transformer.cpp:27 (1 encoder attention, 2 w1, 4 w2, 8 img_proj,
 // 16 decoder).
+//
+// IMPACT (src/models/impact/impact_model.cpp:59-68) drives the same
+// transformer with int8_state (the state projection joins the img_proj int8
+// group, act_transformer.cpp:127-130) and a text tail: up to act.meta's n_text
+// tokens of its T5 tower appended after the camera tokens, their positions
+// after the camera positions (build_tokens, :212-250).
 class ActTf {
 public:
-    ActTf(const std::string& dir, int img_ch, int int8_mask);
+    ActTf(const std::string& dir, int img_ch, int int8_mask, bool int8_state = false);
     ~ActTf();
     int chunk() const { return chunk_; }
     int action_dim() const { return action_dim_; }
     int state_dim() const { return state_dim_; }
     int dim() const { return d_; }
     int img_ch() const { return img_ch_; }
-    int n_tokens(int n_cams, int fh, int fw) const { return n_1d_ + n_cams * fh * fw; }
+    int n_tokens(int n_cams, int fh, int fw, int nt = 0) const { return n_1d_ + n_cams * fh * fw + nt; }
+    int n_text() const { return n_text_; }
     int int8_layers() const { return n_int8_; }
     // device pointers; feats [n_cams * fh * fw, img_ch], state_norm [state_dim],
     // actions_norm [chunk, action_dim]
     void forward_dev(const float* feats, int n_cams, int fh, int fw, const float* state_norm,
-                     float* actions_norm, hipStream_t caller);
+                     float* actions_norm, hipStream_t caller) {
+        forward_text_dev(feats, n_cams, fh, fw, state_norm, nullptr, nullptr, 0, actions_norm, caller);
+    }
+    // with the text tail: text / text_pos [n_text_real, dim] (device), of which
+    // min(max(n_text_real, 0), n_text) rows enter the sequence (clamp_text)
+    void forward_text_dev(const float* feats, int n_cams, int fh, int fw, const float* state_norm,
+                          const float* text, const float* text_pos, int n_text_real, float* actions_norm,
+                          hipStream_t caller);
     int graph_nodes() const { return replay_.nodes(); }
 
 private:
@@ -49,11 +63,11 @@ private:
         DLinear sqk, sv, so, cq, ck, cv, co, w1, w2;
         const float *n1s, *n1b, *n2s, *n2b, *n3s, *n3b;
     };
-    void ensure(int n_cams, int fh, int fw);
+    void ensure(int n_cams, int fh, int fw, int nt);
     void run(hipStream_t st);
 
     int d_ = 512, heads_ = 8, hd_ = 64, ff_ = 3200, n_enc_ = 4, n_dec_ = 1, chunk_ = 100;
-    int state_dim_ = 6, action_dim_ = 6, n_1d_ = 2, img_ch_ = 0, n_int8_ = 0;
+    int state_dim_ = 6, action_dim_ = 6, n_1d_ = 2, img_ch_ = 0, n_int8_ = 0, n_text_ = 0;
     float eps_ = 1e-5f;
     DeviceArena A_;
     DLinear img_proj_, state_proj_, head_;
@@ -62,12 +76,12 @@ private:
     std::vector<Enc> enc_;
     std::vector<Dec> dec_;
     // per-shape state
-    int n_cams_ = -1, fh_ = -1, fw_ = -1, T_ = 0;
+    int n_cams_ = -1, fh_ = -1, fw_ = -1, nt_ = -1, T_ = 0;
     std::unique_ptr<DeviceArena> S_;
     float *feats_ = nullptr, *state_ = nullptr, *act_out_ = nullptr, *x_ = nullptr, *pos_ = nullptr,
           *xp_ = nullptr, *qk_ = nullptr, *v_ = nullptr, *att_ = nullptr, *ff_buf_ = nullptr,
           *dx_ = nullptr, *zero_ = nullptr, *kpos_ = nullptr, *ckb_ = nullptr, *cvb_ = nullptr,
-          *dq_ = nullptr;
+          *dq_ = nullptr, *text_ = nullptr;
     Ctx ctx_;
     hipStream_t own_ = nullptr;
     GraphReplay replay_;
