@@ -552,10 +552,14 @@ def main():
     dominant = (8192, 4096, 4096)
 
     if args.profile_only:
-        sh = Shape(vla, torch, synth, *dominant)
-        sh.quantize(vla, stream)
-        for _ in range(20):
-            sh.gemm(vla, stream)  # eager launches: the profiler sees 20 GEMM dispatches
+        # the dominant GEMM, or the --shapes given, each quantized once and
+        # launched 20 times eagerly (the profiler sees 20 dispatches per shape,
+        # told apart by grid size)
+        for spec in (shapes_spec if args.shapes else [dominant]):
+            sh = Shape(vla, torch, synth, *spec)
+            sh.quantize(vla, stream)
+            for _ in range(20):
+                sh.gemm(vla, stream)
         # calibration for the HBM byte counters: a plain device copy of 256 MiB
         # (reads 256 MiB, writes 256 MiB), well past the 256 MiB MALL
         src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
@@ -563,7 +567,7 @@ def main():
         for _ in range(3):
             dst.copy_(src)
         torch.cuda.synchronize()
-        print(json.dumps({"profile_only": "gemm 8192x4096x4096 x20, copy 256 MiB x3"}))
+        print(json.dumps({"profile_only": f"gemm {args.shapes or '8192x4096x4096'} x20 each, copy 256 MiB x3"}))
         return
 
     shapes = [Shape(vla, torch, synth, *s) for s in shapes_spec]
