@@ -383,8 +383,39 @@ def _lat_siglip(vla, torch, ck, ob, tmp, stream_obj):
     return row
 
 
+def _lat_smolvla_model(vla, torch, ck, ob, tmp, stream_obj):
+    """SmolVLA end to end through vla_smolvla_predict (host pointers, the
+    caller's view): two 480 x 640 uint8 frames uploaded, resized to 512 x 512,
+    SigLIP per view, a 48-token instruction, the state token, the 16-layer
+    prefix tower and 10 Euler steps of the expert, actions downloaded;
+    SMOLVLA_INT8=63. Wall-clock median of host calls (PCIe included)."""
+    c = ck.SMOLVLA_MODEL_BASE
+    d = os.path.join(tmp, "smol_model")
+    if not os.path.exists(os.path.join(d, "heads.bin")):
+        ck.write_smolvla_model(d, c)
+    frames, state, noise = ck.smolvla_model_inputs(c)
+    saved = os.environ.pop("SMOLVLA_INT8", None)
+    try:
+        r = ob.RefSmolvlaModel(d, int8_mask=63) if ob is not None else None  # the reference's latch stays 0
+        os.environ["SMOLVLA_INT8"] = "63"
+        m = vla.SmolvlaModel(d)
+    finally:
+        os.environ.pop("SMOLVLA_INT8", None)
+        if saved is not None:
+            os.environ["SMOLVLA_INT8"] = saved
+    ids, lmask, _ = m.tokenize("pick up the red block and put it in the box, then " * 6)
+    gpu = _median_ms(lambda: m.predict(frames, ids, lmask, state, noise=noise), warmup=3, timed=20)
+    row = {"host_call_ms": round(gpu, 4), "frames": "2x480x640", "prefix_tokens": 2 * 64 + 48 + 1,
+           "steps": c["tf"]["num_steps"], "smolvla_int8": 63, "int8_layers": m.int8_layers,
+           "graph_nodes": m.graph_nodes}
+    if r is not None:
+        row["cpu_ref_ms"] = round(_median_ms(lambda: r.predict(frames, ids, lmask, state, m.chunk, m.action_dim,
+                                                               noise=noise), warmup=2, timed=10), 3)
+    return row
+
+
 def policy_latency(vla, torch, stream_obj, with_cpu=True,
-                   models=("act", "act_model", "octo", "smolvla", "siglip")):
+                   models=("act", "act_model", "octo", "smolvla", "siglip", "smolvla_model")):
     """Per-chunk latency of BASELINE.json configs[2..4] at batch 1, and of
     SmolVLA's SigLIP vision tower per camera image: the device
     graphs (one captured HIP graph per forward, inputs resident in HBM) and the
@@ -421,6 +452,9 @@ def policy_latency(vla, torch, stream_obj, with_cpu=True,
         if "siglip" in models:
             out["siglip"] = _lat_siglip(vla, torch, ck, ob, tmp, stream_obj)
             print(f"  SigLIP vision tower: {out['siglip']}", file=sys.stderr, flush=True)
+        if "smolvla_model" in models:
+            out["smolvla_model"] = _lat_smolvla_model(vla, torch, ck, ob, tmp, stream_obj)
+            print(f"  SmolVLA end to end: {out['smolvla_model']}", file=sys.stderr, flush=True)
     if ob is not None:
         out["cpu_ref_threads"] = int(ob.ref().ref_omp_max_threads())
     return out
@@ -511,7 +545,7 @@ def main():
     ap.add_argument("--no-policy", action="store_true", help="skip the per-chunk policy latency leg")
     ap.add_argument("--policy-only", action="store_true",
                     help="only the per-chunk policy latency leg (for rocprofv3 runs)")
-    ap.add_argument("--models", default="act,act_model,octo,smolvla,siglip", help="policy graphs to time")
+    ap.add_argument("--models", default="act,act_model,octo,smolvla,siglip,smolvla_model", help="policy graphs to time")
     ap.add_argument("--no-conv", action="store_true", help="skip the ResNet-18 conv2d_i8 leg")
     ap.add_argument("--conv-only", action="store_true", help="only the ResNet-18 conv2d_i8 leg")
     ap.add_argument("--profile-only", action="store_true",

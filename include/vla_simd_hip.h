@@ -590,6 +590,62 @@ VLA_API int32_t vla_act_int8_convs(void* h);
 VLA_API int32_t vla_act_int8_layers(void* h);
 VLA_API int32_t vla_act_graph_nodes(void* h);
 
+/* -------------------------------------------- SmolVLA, model level ------- */
+
+/* The reference's SmolVLA entry points, same names and signatures
+ * (include/vla_simd.h:83-124, src/models/smolvla/smolvla_capi.cpp), bound by
+ * vla_simd/policy_server.py as a model library. load reads the converted
+ * directory (or vla.simd GGUF) and the tokenizer's vocab.txt + merges.txt in
+ * tok_dir; SMOLVLA_INT8 is read at load (smolvla_model.cpp:44 bits).
+ * tokenize: ids / mask [tok_maxlen] as lerobot's tokenizer step produces them
+ * (a newline appended, right-padded with pad_token_id / 0, the last
+ * tok_maxlen tokens kept); returns the token count, VLA_ERR_ARG on a null
+ * argument. predict: n_views native-size uint8 RGB frames [height, width, 3]
+ * back to back, the language ids and mask [n_lang] (mask values 0 or 1; the
+ * reference adds other values into the positions, the device graph refuses
+ * them with VLA_ERR_ARG), state [state_dim] raw, noise [chunk *
+ * max_action_dim] or NULL to draw N(0, 1) from mt19937_64(seed), actions
+ * [chunk * action_dim] out, un-normalized. VLA_ERR_SHAPE for a view count
+ * other than the checkpoint's or a token id outside its vocabulary.
+ * predict_rtc adds real-time-chunking guidance: prev [n_prev * action_dim]
+ * raw actions of the previous chunk (n_prev <= chunk), weights [chunk], a
+ * positive finite max_guidance. Resize, vision tower, prefix and denoise all
+ * run on the device. */
+VLA_API void* vla_smolvla_load(const char* model_dir, const char* tok_dir);
+VLA_API void vla_smolvla_free(void* h);
+VLA_API int32_t vla_smolvla_chunk(void* h);
+VLA_API int32_t vla_smolvla_action_dim(void* h);
+VLA_API int32_t vla_smolvla_state_dim(void* h);
+VLA_API int32_t vla_smolvla_n_views(void* h);
+VLA_API int32_t vla_smolvla_img_size(void* h);
+VLA_API int32_t vla_smolvla_tok_maxlen(void* h);
+VLA_API int32_t vla_smolvla_tokenize(void* h, const char* text, int32_t* ids, int32_t* mask);
+VLA_API int32_t vla_smolvla_predict(void* h, const uint8_t* frames, int32_t n_views, int32_t height,
+                                    int32_t width, const int32_t* lang_tokens, const int32_t* lang_mask,
+                                    int32_t n_lang, const float* state, const float* noise, uint64_t seed,
+                                    float* actions);
+VLA_API int32_t vla_smolvla_predict_rtc(void* h, const uint8_t* frames, int32_t n_views, int32_t height,
+                                        int32_t width, const int32_t* lang_tokens, const int32_t* lang_mask,
+                                        int32_t n_lang, const float* state, const float* noise, uint64_t seed,
+                                        float* actions, const float* prev, int32_t n_prev,
+                                        const float* weights, float max_guidance);
+/* Extensions with no counterpart in vla_simd.h: the preprocessed views
+ * [n_views, 3, img_size, img_size] (resize_with_pad on the device, host
+ * pointers), and the counts of int8 layers and graph nodes. */
+VLA_API int32_t vla_smolvla_preprocess(void* h, const uint8_t* frames, int32_t n_views, int32_t height,
+                                       int32_t width, float* pixels);
+VLA_API int32_t vla_smolvla_int8_layers(void* h);
+VLA_API int32_t vla_smolvla_graph_nodes(void* h);
+
+/* SmolVLA's byte-level BPE tokenizer alone (src/tokenizer/tokenizer.h:16-30,
+ * Tokenizer::load + encode), host code that needs no device: tok_dir holds
+ * vocab.txt and merges.txt. encode writes at most cap ids and returns the
+ * full count (no newline appended, no truncation: vla_smolvla_tokenize adds
+ * those). No counterpart in vla_simd.h. */
+VLA_API void* vla_bpe_load(const char* tok_dir);
+VLA_API void vla_bpe_free(void* h);
+VLA_API int32_t vla_bpe_encode(void* h, const char* text, int32_t* ids, int32_t cap);
+
 /* ------------------------------------------------ int8-step probe (tests) -- */
 
 /* Test support with no counterpart in the reference: a record of every int8

@@ -514,6 +514,24 @@ def _ref_models():
     L.ref_act_model_encode.argtypes, L.ref_act_model_encode.restype = [P, P, P], i
     L.ref_mount_read.argtypes = [ctypes.c_char_p, ctypes.c_char_p, P, ctypes.c_longlong]
     L.ref_mount_read.restype = ctypes.c_longlong
+    L.ref_smolvla_model_load.argtypes, L.ref_smolvla_model_load.restype = [ctypes.c_char_p, i], P
+    L.ref_smolvla_model_free.argtypes = [P]
+    L.ref_smolvla_model_predict.argtypes = [P, P, i, i, i, P, P, i, P, P, P, P, i, P, c_float, i]
+    L.ref_smolvla_model_predict.restype = i
+    L.ref_resize_with_pad.argtypes = [P, i, i, i, P]
+    L.ref_bpe_load.argtypes, L.ref_bpe_load.restype = [ctypes.c_char_p], P
+    L.ref_bpe_free.argtypes = [P]
+    L.ref_bpe_encode.argtypes, L.ref_bpe_encode.restype = [P, ctypes.c_char_p, P, i], i
+    # the reference's own SmolVLA entry points (smolvla_capi.cpp)
+    i32 = ctypes.c_int32
+    L.vla_smolvla_load.argtypes, L.vla_smolvla_load.restype = [ctypes.c_char_p, ctypes.c_char_p], P
+    L.vla_smolvla_free.argtypes, L.vla_smolvla_free.restype = [P], None
+    for n in ("chunk", "action_dim", "state_dim", "n_views", "img_size", "tok_maxlen"):
+        f = getattr(L, f"vla_smolvla_{n}")
+        f.argtypes, f.restype = [P], i32
+    L.vla_smolvla_tokenize.argtypes, L.vla_smolvla_tokenize.restype = [P, ctypes.c_char_p, P, P], i32
+    L.vla_smolvla_predict_rtc.argtypes = [P, P, i32, i32, i32, P, P, i32, P, P, c_uint64, P, P, i32, P, c_float]
+    L.vla_smolvla_predict_rtc.restype = i32
     L._models_declared = True
     return L
 
@@ -672,3 +690,92 @@ def ref_dense_linear(x, W, bias=None):
     out = np.empty((x.shape[0], W.shape[0]), np.float32)
     ref().ref_dense_linear(_p(out), _p(x), _p(W), _p(b), x.shape[0], W.shape[0], W.shape[1])
     return out
+
+
+class RefSmolvlaModel:
+    """The reference's SmolvlaModel. int8_mask None: through its own C ABI
+    (vla_smolvla_load / _tokenize / _predict_rtc, SMOLVLA_INT8 as the
+    environment had it at the process's first load); an int mask: loaded by
+    ref_smolvla_model_load with that mask's groups and run by the body of
+    vla_smolvla_predict_rtc (ref_smolvla_model_predict, noise required)."""
+
+    def __init__(self, dirpath, tok_dir=None, int8_mask=None):
+        L = _ref_models()
+        self.abi = int8_mask is None
+        if self.abi:
+            tok_dir = tok_dir or os.path.join(dirpath, "tok")
+            self.h = L.vla_smolvla_load(dirpath.encode(), tok_dir.encode())
+        else:
+            self.h = L.ref_smolvla_model_load(dirpath.encode(), int8_mask)
+        if not self.h:
+            raise RuntimeError(f"reference SmolvlaModel::load failed for {dirpath}")
+
+    def dims(self):
+        L = _ref_models()
+        assert self.abi
+        return {n: getattr(L, f"vla_smolvla_{n}")(self.h)
+                for n in ("chunk", "action_dim", "state_dim", "n_views", "img_size", "tok_maxlen")}
+
+    def tokenize(self, text, maxlen):
+        ids = np.zeros(maxlen, np.int32)
+        mask = np.zeros(maxlen, np.int32)
+        n = _ref_models().vla_smolvla_tokenize(self.h, text.encode(), _p(ids), _p(mask))
+        return ids, mask, n
+
+    def predict(self, frames, ids, mask, state, chunk, action_dim, noise=None, seed=0, prev=None, weights=None,
+                max_guidance=0.0, perturb=0):
+        """-> (status, actions [chunk, action_dim]); perturb > 0 (shim path
+        only) moves the preprocessed pixels by seeded 1-ulp steps"""
+        L = _ref_models()
+        frames = np.ascontiguousarray(frames, np.uint8)
+        ids, mask = np.ascontiguousarray(ids, np.int32), np.ascontiguousarray(mask, np.int32)
+        out = np.zeros((chunk, action_dim), np.float32)
+        noise = None if noise is None else _f32(noise)
+        prev = None if prev is None else _f32(prev)
+        weights = None if weights is None else _f32(weights)
+        n_prev = 0 if prev is None else prev.size // action_dim
+        nv, h, w = frames.shape[:3]
+        if self.abi:
+            st = L.vla_smolvla_predict_rtc(self.h, _p(frames), nv, h, w, _p(ids), _p(mask), ids.size,
+                                           _p(_f32(state)), _p(noise), seed, _p(out), _p(prev), n_prev,
+                                           _p(weights), float(max_guidance))
+        else:
+            assert noise is not None
+            st = L.ref_smolvla_model_predict(self.h, _p(frames), nv, h, w, _p(ids), _p(mask), ids.size,
+                                             _p(_f32(state)), _p(noise), _p(out), _p(prev), n_prev, _p(weights),
+                                             float(max_guidance), int(perturb))
+        return int(st), out
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            L = _ref_models()
+            (L.vla_smolvla_free if self.abi else L.ref_smolvla_model_free)(self.h)
+
+
+def ref_resize_with_pad(frame, S):
+    """src/preprocess/image.cpp resize_with_pad: [h, w, 3] uint8 -> [3, S, S]"""
+    frame = np.ascontiguousarray(frame, np.uint8)
+    out = np.empty((3, S, S), np.float32)
+    _ref_models().ref_resize_with_pad(_p(frame), frame.shape[0], frame.shape[1], S, _p(out))
+    return out
+
+
+class RefBpe:
+    """The reference's Tokenizer (src/tokenizer/tokenizer.cpp)."""
+
+    def __init__(self, tok_dir):
+        self.h = _ref_models().ref_bpe_load(tok_dir.encode())
+        if not self.h:
+            raise RuntimeError(f"reference Tokenizer::load failed for {tok_dir}")
+
+    def encode(self, text):
+        b = text.encode() if isinstance(text, str) else bytes(text)
+        L = _ref_models()
+        n = L.ref_bpe_encode(self.h, b, None, 0)
+        ids = np.zeros(max(n, 1), np.int32)
+        L.ref_bpe_encode(self.h, b, _p(ids), n)
+        return [int(v) for v in ids[:n]]
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            _ref_models().ref_bpe_free(self.h)

@@ -19,7 +19,13 @@
  *     with the mask passed in instead of read from the environment;
  *   - the prefix-LM mask, positions and denoise mask of
  *     SmolvlaModel::predict_normalized (smolvla_model.cpp:252-275) built from a
- *     pad vector, so the chunk starts from given prefix embeddings.
+ *     pad vector, so the chunk starts from given prefix embeddings;
+ *   - the whole SmolvlaModel with SMOLVLA_INT8's groups for a given mask and
+ *     the body of vla_smolvla_predict_rtc (smolvla_capi.cpp:123-167) around
+ *     it, since SmolvlaModel::apply_int8 latches the variable once per
+ *     process (a static); the library's own vla_smolvla_* entry points
+ *     (compiled in from smolvla_capi.cpp) serve the environment's mask;
+ *   - resize_with_pad and the BPE tokenizer on their own.
  */
 #include "io/files.h"
 #include "models/act/act_model.h"
@@ -28,8 +34,12 @@
 #include "models/smolvla/action_expert.h"
 #include "models/smolvla/siglip_vision.h"
 #include "models/smolvla/smollm2_lm.h"
+#include "models/smolvla/smolvla_model.h"
 #include "ops/lm_ops.h"
+#include "preprocess/image.h"
+#include "tokenizer/tokenizer.h"
 
+#include <cmath>
 #include <cstdint>
 #include <cstring>
 #include <iterator>
@@ -385,4 +395,101 @@ REF_API int ref_act_model_encode(void* h, const uint8_t* images, float* feats) {
     for (int c = 0; c < m->n_cams; c++)
         m->encode_view(images + (size_t)c * m->img_h * m->img_w * 3, c, feats + (size_t)c * nf);
     return 0;
+}
+
+/* SmolvlaModel::load, then SmolvlaModel::apply_int8's groups for int8_mask
+ * (smolvla_model.cpp:111-155). The caller leaves SMOLVLA_INT8 unset so that
+ * load's own apply_int8 quantizes nothing. */
+REF_API void* ref_smolvla_model_load(const char* dir, int int8_mask) {
+    try {
+        const io::Mount mount(dir);
+        if (!mount.ok()) return nullptr;
+        auto* m = new SmolvlaModel();
+        if (!m->load(dir)) {
+            delete m;
+            return nullptr;
+        }
+        for (nn::EncoderLayer& l : m->vit.layers) {
+            if (int8_mask & 1)
+                for (nn::Linear* x : {&l.attn.wq, &l.attn.wk, &l.attn.wv, &l.attn.wo}) x->init_int8();
+            if (int8_mask & 2) l.w1.init_int8();
+            if (int8_mask & 4) l.w2.init_int8();
+        }
+        if (int8_mask & 8) {
+            m->vit.patch_lin.init_int8();
+            m->vit.mm_proj.init_int8();
+        }
+        if (int8_mask & 16)
+            for (VlmLayerW& w : m->vlm.layers)
+                for (nn::Linear* l : {&w.q, &w.k, &w.v, &w.o, &w.gate, &w.up, &w.down}) l->init_int8();
+        if (int8_mask & 32)
+            for (ExpertLayerW& w : m->aex.layers)
+                for (nn::Linear* l : {&w.q, &w.k, &w.v, &w.o, &w.gate, &w.up, &w.down}) l->init_int8();
+        return m;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "ref_smolvla_model_load: %s\n", e.what());
+        return nullptr;
+    }
+}
+
+REF_API void ref_smolvla_model_free(void* h) { delete static_cast<SmolvlaModel*>(h); }
+
+/* vla_smolvla_predict_rtc's body (smolvla_capi.cpp:146-166) with the noise
+ * given: resize_with_pad per view, SmolvlaModel::predict, the first
+ * real_action_dim columns of each row. Returns 0, or -2 when predict rejects
+ * the input. perturb > 0 moves every preprocessed pixel by -1, 0 or +1 ulp
+ * (a xorshift stream seeded by perturb) before the model sees it: the class
+ * of difference an fp32 vision tower's summation order leaves, for the tests'
+ * sensitivity bars. */
+REF_API int ref_smolvla_model_predict(void* h, const uint8_t* frames, int nv, int height, int width,
+                                      const int32_t* tokens, const int32_t* lmask, int n_lang, const float* state,
+                                      const float* noise, float* actions, const float* prev, int n_prev,
+                                      const float* weights, float max_guidance, int perturb) {
+    const auto& m = *static_cast<SmolvlaModel*>(h);
+    const int S = m.vit.cfg.img, C = m.aex.cfg.chunk, MAD = m.aex.cfg.max_action_dim;
+    const size_t per_view = (size_t)3 * S * S;
+    std::vector<float> pixels((size_t)nv * per_view);
+    for (int v = 0; v < nv; v++)
+        resize_with_pad(frames + (size_t)v * height * width * 3, height, width, S, pixels.data() + (size_t)v * per_view);
+    if (perturb > 0) {
+        uint64_t x = 0x9E3779B97F4A7C15ull * (uint64_t)perturb;
+        for (float& p : pixels) {
+            x ^= x << 13;
+            x ^= x >> 7;
+            x ^= x << 17;
+            const int d = (int)(x % 3) - 1;
+            if (d) p = std::nextafter(p, d > 0 ? INFINITY : -INFINITY);
+        }
+    }
+    auto out = m.predict(pixels.data(), nv, tokens, lmask, n_lang, state, noise, prev, n_prev, weights, max_guidance);
+    if (out.empty()) return -2;
+    for (int t = 0; t < C; t++)
+        std::memcpy(actions + (size_t)t * m.real_action_dim, out.data() + (size_t)t * MAD,
+                    m.real_action_dim * sizeof(float));
+    return 0;
+}
+
+REF_API void ref_resize_with_pad(const uint8_t* src, int h, int w, int S, float* dst) {
+    resize_with_pad(src, h, w, S, dst);
+}
+
+REF_API void* ref_bpe_load(const char* dir) {
+    try {
+        auto* t = new Tokenizer();
+        if (!t->load(dir)) {
+            delete t;
+            return nullptr;
+        }
+        return t;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "ref_bpe_load: %s\n", e.what());
+        return nullptr;
+    }
+}
+REF_API void ref_bpe_free(void* h) { delete static_cast<Tokenizer*>(h); }
+/* Tokenizer::encode: writes at most cap ids, returns the count */
+REF_API int ref_bpe_encode(void* h, const char* text, int32_t* ids, int cap) {
+    const std::vector<int> v = static_cast<Tokenizer*>(h)->encode(text);
+    for (int i = 0; i < (int)v.size() && i < cap; i++) ids[i] = v[i];
+    return (int)v.size();
 }

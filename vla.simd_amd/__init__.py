@@ -76,6 +76,10 @@ EXPORTS = (
     "vla_act_load", "vla_act_free", "vla_act_chunk", "vla_act_action_dim", "vla_act_state_dim",
     "vla_act_n_cams", "vla_act_img_h", "vla_act_img_w", "vla_act_predict", "vla_act_predict_dev",
     "vla_act_encode", "vla_act_feat_shape", "vla_act_int8_convs", "vla_act_int8_layers", "vla_act_graph_nodes",
+    "vla_smolvla_load", "vla_smolvla_free", "vla_smolvla_chunk", "vla_smolvla_action_dim",
+    "vla_smolvla_state_dim", "vla_smolvla_n_views", "vla_smolvla_img_size", "vla_smolvla_tok_maxlen",
+    "vla_smolvla_tokenize", "vla_smolvla_predict", "vla_smolvla_predict_rtc", "vla_smolvla_preprocess",
+    "vla_smolvla_int8_layers", "vla_smolvla_graph_nodes", "vla_bpe_load", "vla_bpe_free", "vla_bpe_encode",
 )
 
 
@@ -241,6 +245,24 @@ def _declare(L):
         "vla_act_int8_convs": (i32, [P]),
         "vla_act_int8_layers": (i32, [P]),
         "vla_act_graph_nodes": (i32, [P]),
+        "vla_smolvla_load": (P, [c_char_p, c_char_p]),
+        "vla_smolvla_free": (None, [P]),
+        "vla_smolvla_chunk": (i32, [P]),
+        "vla_smolvla_action_dim": (i32, [P]),
+        "vla_smolvla_state_dim": (i32, [P]),
+        "vla_smolvla_n_views": (i32, [P]),
+        "vla_smolvla_img_size": (i32, [P]),
+        "vla_smolvla_tok_maxlen": (i32, [P]),
+        "vla_smolvla_int8_layers": (i32, [P]),
+        "vla_smolvla_graph_nodes": (i32, [P]),
+        "vla_smolvla_tokenize": (i32, [P, c_char_p, P, P]),
+        "vla_smolvla_predict": (i32, [P, P, i32, i32, i32, P, P, i32, P, P, ctypes.c_uint64, P]),
+        "vla_smolvla_predict_rtc": (i32, [P, P, i32, i32, i32, P, P, i32, P, P, ctypes.c_uint64, P, P, i32, P,
+                                          c_float]),
+        "vla_smolvla_preprocess": (i32, [P, P, i32, i32, i32, P]),
+        "vla_bpe_load": (P, [c_char_p]),
+        "vla_bpe_free": (None, [P]),
+        "vla_bpe_encode": (i32, [P, c_char_p, P, i32]),
         "vla_probe_begin": (i32, [i32]),
         "vla_probe_end": (i32, []),
         "vla_probe_count": (i32, []),
@@ -870,6 +892,86 @@ class ActModel(_Handle):
         out = np.empty((self.n_cams * self.feat_h * self.feat_w, self.feat_ch), np.float32)
         _call("vla_act_encode", self.h, _ptr(images), _ptr(out))
         return out
+
+
+class SmolvlaModel(_Handle):
+    """SmolVLA end to end on the device through the reference's own entry
+    points (vla_smolvla_load / _tokenize / _predict / _predict_rtc): native
+    uint8 frames + language ids + raw state -> actions."""
+
+    _load, _free = "vla_smolvla_load", "vla_smolvla_free"
+
+    def __init__(self, dirpath: str, tok_dir: str | None = None):
+        tok_dir = tok_dir or os.path.join(dirpath, "tok")
+        super().__init__(lib().vla_smolvla_load(dirpath.encode(), tok_dir.encode()))
+        L = lib()
+        self.chunk, self.action_dim = L.vla_smolvla_chunk(self.h), L.vla_smolvla_action_dim(self.h)
+        self.state_dim, self.n_views = L.vla_smolvla_state_dim(self.h), L.vla_smolvla_n_views(self.h)
+        self.img_size, self.tok_maxlen = L.vla_smolvla_img_size(self.h), L.vla_smolvla_tok_maxlen(self.h)
+        self.int8_layers = L.vla_smolvla_int8_layers(self.h)
+
+    @property
+    def graph_nodes(self):
+        return lib().vla_smolvla_graph_nodes(self.h)
+
+    def tokenize(self, text: str):
+        ids = np.zeros(self.tok_maxlen, np.int32)
+        mask = np.zeros(self.tok_maxlen, np.int32)
+        n = lib().vla_smolvla_tokenize(self.h, text.encode(), _ptr(ids), _ptr(mask))
+        check("vla_smolvla_tokenize", min(n, 0))
+        return ids, mask, n
+
+    def preprocess(self, frames):
+        frames = np.ascontiguousarray(frames, np.uint8)
+        if frames.ndim != 4 or frames.shape[3] != 3:
+            raise ValueError(f"frames must be [n_views, height, width, 3], got {frames.shape}")
+        out = np.empty((frames.shape[0], 3, self.img_size, self.img_size), np.float32)
+        _call("vla_smolvla_preprocess", self.h, _ptr(frames), frames.shape[0], frames.shape[1], frames.shape[2],
+              _ptr(out))
+        return out
+
+    def predict(self, frames, ids, mask, state, noise=None, seed=0, prev=None, weights=None, max_guidance=0.0):
+        frames = np.ascontiguousarray(frames, np.uint8)
+        if frames.ndim != 4 or frames.shape[3] != 3:
+            raise ValueError(f"frames must be [n_views, height, width, 3], got {frames.shape}")
+        ids = np.ascontiguousarray(ids, np.int32)
+        mask = np.ascontiguousarray(mask, np.int32)
+        if ids.shape != mask.shape or ids.ndim != 1:
+            raise ValueError("ids and mask must be 1-D arrays of one length")
+        state = _f32(state)
+        _need_size("state", state, self.state_dim)
+        if noise is not None:
+            noise = _f32(noise)
+        out = np.empty((self.chunk, self.action_dim), np.float32)
+        args = [self.h, _ptr(frames), frames.shape[0], frames.shape[1], frames.shape[2], _ptr(ids), _ptr(mask),
+                ids.size, _ptr(state), _ptr(noise), ctypes.c_uint64(seed), _ptr(out)]
+        if prev is None:
+            _call("vla_smolvla_predict", *args)
+        else:
+            prev, weights = _f32(prev), _f32(weights)
+            if prev.size % self.action_dim:
+                raise ValueError("prev must be [n_prev, action_dim]")
+            _need_size("weights", weights, self.chunk)
+            _call("vla_smolvla_predict_rtc", *args, _ptr(prev), prev.size // self.action_dim, _ptr(weights),
+                  float(max_guidance))
+        return out
+
+
+class BpeTokenizer(_Handle):
+    """SmolVLA's byte-level BPE tokenizer alone (vla_bpe_*), host code."""
+
+    _load, _free = "vla_bpe_load", "vla_bpe_free"
+
+    def __init__(self, tok_dir: str):
+        super().__init__(lib().vla_bpe_load(tok_dir.encode()))
+
+    def encode(self, text) -> list:
+        b = text.encode() if isinstance(text, str) else bytes(text)
+        n = lib().vla_bpe_encode(self.h, b, None, 0)
+        check("vla_bpe_encode", min(n, 0))
+        ids = np.zeros(max(n, 1), np.int32)
+        lib().vla_bpe_encode(self.h, b, _ptr(ids), n)
+        return [int(v) for v in ids[:n]]
 
 
 class OctoTransformer(_Handle):

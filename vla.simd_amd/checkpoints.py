@@ -436,6 +436,124 @@ def smolvla_inputs(cfg: dict = SMOLVLA_BASE, seed: int = synth.BASE_SEED, n_pad:
     return prefix, pad, noise
 
 
+# ------------------------------------------------------------ tokenizer --
+# A byte-level BPE tokenizer directory (vocab.txt "id<TAB>token", merges.txt
+# "left right", the files src/tokenizer/tokenizer.cpp:122-151 reads), trained
+# here on a small corpus so the merges exercise letters, spaces, digits and
+# punctuation. Token ids 0..255 are the 256 byte symbols in byte order.
+
+def gpt2_byte_symbols() -> list:
+    """The byte alphabet: bytes 33-126, 161-172, 174-255 stand for
+    themselves, the rest for code points 256, 257, ... in byte order."""
+    keep = set(range(33, 127)) | set(range(161, 173)) | set(range(174, 256))
+    out, n = [], 0
+    for b in range(256):
+        if b in keep:
+            out.append(chr(b))
+        else:
+            out.append(chr(256 + n))
+            n += 1
+    return out
+
+
+TOK_CORPUS = ("pick up the red block and put it in the box. place the cup on the plate, then open the "
+              "drawer. push the green button twice; don't drop the sponge! move the arm 10 cm to the "
+              "left and grasp the handle. the robot picks the blue cube, stacks it on top of the "
+              "yellow one and returns home. wipe the table with the cloth and fold the towel.")
+
+
+def write_bpe_tokenizer(dirpath: str, n_merges: int = 160, corpus: str = TOK_CORPUS) -> str:
+    os.makedirs(dirpath, exist_ok=True)
+    sym = gpt2_byte_symbols()
+    words = []
+    for i, w in enumerate(corpus.split(" ")):
+        b = ((" " if i else "") + w).encode()
+        words.append([sym[x] for x in b])
+    merges = []
+    for _ in range(n_merges):
+        counts = {}
+        for w in words:
+            for a, b in zip(w, w[1:]):
+                counts[(a, b)] = counts.get((a, b), 0) + 1
+        if not counts:
+            break
+        best = max(sorted(counts), key=lambda k: counts[k])
+        merges.append(best)
+        for w in words:
+            i = 0
+            while i + 1 < len(w):
+                if (w[i], w[i + 1]) == best:
+                    w[i:i + 2] = [w[i] + w[i + 1]]
+                i += 1
+    vocab = list(sym) + [a + b for a, b in merges]
+    seen, rows = set(), []
+    for t in vocab:
+        if t not in seen:
+            seen.add(t)
+            rows.append(t)
+    with open(os.path.join(dirpath, "vocab.txt"), "w", encoding="utf-8", newline="\n") as f:
+        for i, t in enumerate(rows):
+            f.write(f"{i}\t{t}\n")
+    with open(os.path.join(dirpath, "merges.txt"), "w", encoding="utf-8", newline="\n") as f:
+        f.write("#version: 0.2\n")
+        for a, b in merges:
+            f.write(f"{a} {b}\n")
+    return dirpath
+
+
+# ------------------------------------------------------------- SmolVLA model --
+# The whole SmolVLA checkpoint SmolvlaModel::load reads
+# (src/models/smolvla/smolvla_model.cpp:53-113, smolvla_capi.cpp:43-84): the
+# vision tower, the text tower and expert, heads.meta, the bf16 token
+# embedding table, the state projection, the normalization statistics,
+# config.txt and a tokenizer directory tok/.
+SMOLVLA_MODEL_BASE = dict(vit=SIGLIP_BASE, tf=dict(SMOLVLA_BASE), vocab=49152, max_state_dim=32,
+                          real_state_dim=6, real_action_dim=6, n_views=2, norm_eps=1e-8, tok_maxlen=48,
+                          pad_id=2)
+
+
+def write_smolvla_model(dirpath: str, cfg: dict = SMOLVLA_MODEL_BASE, seed: int = synth.BASE_SEED) -> str:
+    c = cfg
+    write_siglip(dirpath, c["vit"], seed)
+    write_smolvla(dirpath, c["tf"], seed)
+    H, V, MSD = c["tf"]["hidden"], c["vocab"], c["max_state_dim"]
+    assert c["vit"]["mm_out"] == H
+    _meta(os.path.join(dirpath, "heads.meta"),
+          {"vocab": V, "hidden": H, "max_state_dim": MSD, "real_state_dim": c["real_state_dim"],
+           "real_action_dim": c["real_action_dim"], "n_views": c["n_views"], "norm_eps": c["norm_eps"]})
+    with open(os.path.join(dirpath, "emb.bin"), "wb") as f:
+        f.write(_bf16(synth.normal("smolvla.emb", (V, H), 0.05, seed)).tobytes())
+    a = 1.0 / math.sqrt(MSD)
+    with open(os.path.join(dirpath, "heads.bin"), "wb") as f:
+        f.write(synth.uniform("smolvla.state_proj.w", (H, MSD), -a, a, seed).astype(np.float32).tobytes())
+        f.write(synth.normal("smolvla.state_proj.b", (H,), 0.02, seed).astype(np.float32).tobytes())
+    sd, ad = c["real_state_dim"], c["real_action_dim"]
+    for name, n, kind in (("state_mean", sd, 0), ("state_std", sd, 1), ("action_mean", ad, 0),
+                          ("action_std", ad, 1)):
+        v = (synth.uniform(f"smolvla.{name}", (n,), 0.5, 2.0, seed) if kind
+             else synth.normal(f"smolvla.{name}", (n,), 1.0, seed))
+        with open(os.path.join(dirpath, f"stats_{name}.bin"), "wb") as f:
+            f.write(np.asarray(v, np.float32).tobytes())
+    with open(os.path.join(dirpath, "config.txt"), "w") as f:
+        f.write("instruction pick up the red block\n")
+        f.write(f"tokenizer_max_length {c['tok_maxlen']}\n")
+        f.write(f"pad_token_id {c['pad_id']}\n")
+    write_bpe_tokenizer(os.path.join(dirpath, "tok"))
+    return dirpath
+
+
+def smolvla_model_inputs(cfg: dict = SMOLVLA_MODEL_BASE, height: int = 480, width: int = 640,
+                         seed: int = synth.BASE_SEED):
+    """frames [n_views, height, width, 3] uint8, raw state [real_state_dim],
+    noise [chunk, max_action_dim] ~ N(0, 1)."""
+    nv = cfg["n_views"]
+    r = np.random.default_rng(seed)
+    frames = r.integers(0, 256, size=(nv, height, width, 3), dtype=np.uint8)
+    state = synth.normal("smolvla.in.state", (cfg["real_state_dim"],), 1.0, seed).astype(np.float32)
+    noise = synth.normal("smolvla.in.noise", (cfg["tf"]["chunk"], cfg["tf"]["max_action_dim"]), 1.0, seed)
+    return frames, state, np.asarray(noise, np.float32)
+
+
 # ------------------------------------------------------------ vla.simd GGUF --
 # The single-file form of a converted directory that the reference's
 # converters write (tools/_gguf.py:6-28) and its engine mounts

@@ -10,6 +10,7 @@
 #include "models.h"
 #include "runtime.h"
 
+#include <cstdio>
 #include <cstring>
 #include <memory>
 
@@ -459,4 +460,100 @@ VLA_API int32_t vla_act_encode(void* h, const uint8_t* images, float* feats) {
         m.encode_dev(di, df, hc.st);
         hc.down(feats, df, nf);
     });
+}
+
+// -------------------------------------------------- SmolVLA (model level) --
+// The reference's SmolVLA entry points (include/vla_simd.h:83-124,
+// src/models/smolvla/smolvla_capi.cpp), same names and signatures.
+
+namespace {
+SmolvlaModel* smolvla_model(void* h) { return static_cast<SmolvlaModel*>(h); }
+}  // namespace
+
+VLA_API void* vla_smolvla_load(const char* model_dir, const char* tok_dir) {
+    SmolvlaModel* m = nullptr;
+    const int32_t rc = guarded("vla_smolvla_load", [&] {
+        VLA_REQUIRE(model_dir && tok_dir, "null model or tokenizer directory");
+        m = new SmolvlaModel(model_dir, tok_dir);
+    });
+    return rc == 0 ? m : nullptr;
+}
+VLA_API void vla_smolvla_free(void* h) { delete smolvla_model(h); }
+VLA_API int32_t vla_smolvla_chunk(void* h) { return h ? smolvla_model(h)->chunk() : 0; }
+VLA_API int32_t vla_smolvla_action_dim(void* h) { return h ? smolvla_model(h)->action_dim() : 0; }
+VLA_API int32_t vla_smolvla_state_dim(void* h) { return h ? smolvla_model(h)->state_dim() : 0; }
+VLA_API int32_t vla_smolvla_n_views(void* h) { return h ? smolvla_model(h)->n_views() : 0; }
+VLA_API int32_t vla_smolvla_img_size(void* h) { return h ? smolvla_model(h)->img_size() : 0; }
+VLA_API int32_t vla_smolvla_tok_maxlen(void* h) { return h ? smolvla_model(h)->tok_maxlen() : 0; }
+VLA_API int32_t vla_smolvla_int8_layers(void* h) { return h ? smolvla_model(h)->int8_layers() : 0; }
+VLA_API int32_t vla_smolvla_graph_nodes(void* h) { return h ? smolvla_model(h)->graph_nodes() : 0; }
+
+VLA_API int32_t vla_smolvla_tokenize(void* h, const char* text, int32_t* ids, int32_t* mask) {
+    if (!h || !text || !ids || !mask) return VLA_ERR_ARG;
+    int32_t n = 0;
+    const int32_t rc = guarded("vla_smolvla_tokenize", [&] { n = smolvla_model(h)->tokenize(text, ids, mask); });
+    return rc == 0 ? n : VLA_ERR_EXCEPTION;
+}
+
+VLA_API int32_t vla_smolvla_predict_rtc(void* h, const uint8_t* frames, int32_t n_views, int32_t height,
+                                        int32_t width, const int32_t* lang_tokens, const int32_t* lang_mask,
+                                        int32_t n_lang, const float* state, const float* noise, uint64_t seed,
+                                        float* actions, const float* prev, int32_t n_prev, const float* weights,
+                                        float max_guidance) {
+    if (!h || !frames || !lang_tokens || !lang_mask || !state || !actions) return VLA_ERR_ARG;
+    return guarded("vla_smolvla_predict_rtc", [&] {
+        smolvla_model(h)->predict(frames, n_views, height, width, lang_tokens, lang_mask, n_lang, state, noise, seed,
+                                  actions, prev, n_prev, weights, max_guidance);
+    });
+}
+
+VLA_API int32_t vla_smolvla_predict(void* h, const uint8_t* frames, int32_t n_views, int32_t height, int32_t width,
+                                    const int32_t* lang_tokens, const int32_t* lang_mask, int32_t n_lang,
+                                    const float* state, const float* noise, uint64_t seed, float* actions) {
+    return vla_smolvla_predict_rtc(h, frames, n_views, height, width, lang_tokens, lang_mask, n_lang, state, noise,
+                                   seed, actions, nullptr, 0, nullptr, 0.0f);
+}
+
+VLA_API int32_t vla_smolvla_preprocess(void* h, const uint8_t* frames, int32_t n_views, int32_t height,
+                                       int32_t width, float* pixels) {
+    if (!h || !frames || !pixels) return VLA_ERR_ARG;
+    return guarded("vla_smolvla_preprocess",
+                   [&] { smolvla_model(h)->preprocess(frames, n_views, height, width, pixels); });
+}
+
+// ------------------------------------------------------ the BPE tokenizer --
+// SmolVLA's tokenizer on its own (host code, no device needed), for callers
+// that tokenize away from a loaded model and for tests.
+
+VLA_API void* vla_bpe_load(const char* tok_dir) {
+    BpeTokenizer* t = nullptr;
+    const int32_t rc = guarded("vla_bpe_load", [&] {
+        VLA_REQUIRE(tok_dir, "null tokenizer directory");
+        auto read = [&](const char* name) {
+            const std::string path = std::string(tok_dir) + "/" + name;
+            FILE* f = std::fopen(path.c_str(), "rb");
+            VLA_REQUIRE(f, "cannot open " + path);
+            std::string s;
+            char buf[65536];
+            size_t n;
+            while ((n = std::fread(buf, 1, sizeof buf, f)) > 0) s.append(buf, n);
+            std::fclose(f);
+            return s;
+        };
+        auto tok = std::make_unique<BpeTokenizer>();
+        VLA_REQUIRE(tok->load(read("vocab.txt"), read("merges.txt")), "empty vocab.txt or merges.txt");
+        t = tok.release();
+    });
+    return rc == 0 ? t : nullptr;
+}
+VLA_API void vla_bpe_free(void* h) { delete static_cast<BpeTokenizer*>(h); }
+VLA_API int32_t vla_bpe_encode(void* h, const char* text, int32_t* ids, int32_t cap) {
+    if (!h || !text || cap < 0 || (cap > 0 && !ids)) return VLA_ERR_ARG;
+    int32_t n = 0;
+    const int32_t rc = guarded("vla_bpe_encode", [&] {
+        const std::vector<int32_t> v = static_cast<BpeTokenizer*>(h)->encode(text);
+        n = (int32_t)v.size();
+        for (int32_t i = 0; i < n && i < cap; i++) ids[i] = v[i];
+    });
+    return rc == 0 ? n : rc;
 }

@@ -23,6 +23,12 @@ struct ArgError : std::invalid_argument {
     using std::invalid_argument::invalid_argument;
 };
 
+// An input whose shape or content the model cannot take (the reference's
+// VLA_ERR_SHAPE, include/vla_simd.h:46-51).
+struct ShapeError : std::runtime_error {
+    using std::runtime_error::runtime_error;
+};
+
 [[noreturn]] void throw_hip(hipError_t e, const char* what, const char* file, int line);
 
 #define VLA_HIP_CHECK(expr)                                                    \
@@ -223,6 +229,27 @@ void launch_copy_rows(float* dst, int ldd, const float* src, int lds, int rows, 
 // sf*sf*hidden] tokens (siglip_vision.cpp:188-198)
 void launch_extract_patches(float* out, const float* pixels, int img, int patch, hipStream_t st);
 void launch_pixel_shuffle(float* dst, const float* src, int side, int hidden, int sf, hipStream_t st);
+
+// policy.hip: the model-level glue kernels.
+// resize_with_pad (src/preprocess/image.cpp:13-51) of n_views uint8 HWC frames
+// [h, w, 3] to CHW [3, S, S] canvases in [-1, 1], padding -1 at the top/left;
+// resize_geometry is its host-side geometry (padding and source steps)
+void resize_geometry(int h, int w, int S, int* pad_h, int* pad_w, double* sy, double* sx);
+void launch_resize_with_pad(float* dst, const uint8_t* src, int n_views, int h, int w, int S, hipStream_t st);
+// dst [n, H] = bf16 rows table[ids[t]] as fp32 * scale
+void launch_embed_bf16(float* dst, const uint16_t* table, const int32_t* ids, int n, int H, float scale,
+                       hipStream_t st);
+void launch_scale(float* x, int64_t n, float s, hipStream_t st);
+// out [rows, ldo]: (x[r, c] - mean[c]) / (std[c] + eps) for r < n_real, 0 for
+// later rows; columns >= cols are not written
+void launch_normalize_pad(float* out, int ldo, const float* x, int n_real, int rows, int cols, const float* mean,
+                          const float* stdv, float eps, hipStream_t st);
+// out [rows, cols] = fma(a[r, c], std[c] + eps, mean[c]) from a [rows, lda]
+void launch_unnormalize(float* out, const float* a, int lda, int rows, int cols, const float* mean,
+                        const float* stdv, float eps, hipStream_t st);
+// the guided Euler step of real-time chunking, gw [steps] on the device
+void launch_rtc_step(float* x, const float* v, const float* prev, const float* weights, const float* gw, int step,
+                     int rows, int cols, float time, float dt, hipStream_t st);
 
 // linear_f32.hip: out[m, n] = act(x[m,:] . W[n,:] + bias[n]); accumulate != 0
 // adds it as fmaf(alpha, v, out[m, n]). act as vla_act, plus 4 = silu.

@@ -21,6 +21,7 @@
 #include "ckpt.h"
 #include "models.h"
 
+#include <algorithm>
 #include <cmath>
 #include <limits>
 
@@ -204,6 +205,10 @@ void SmolvlaTf::ensure(const int32_t* pad, int np) {
     mlp1_ = S->alloc<float>((size_t)C * EH);
     x_ = S->alloc<float>((size_t)C * mad_);
     hf_ = S->alloc<float>((size_t)C * EH);
+    v_ = S->alloc<float>((size_t)C * mad_);
+    guide_ = S->alloc<float>((size_t)C * mad_);
+    gweights_ = S->alloc<float>(C);
+    gw_ = S->alloc<float>(steps_);
     qkv_.assign(NL_, nullptr);
     for (int L = 0; L < NL_; L++) qkv_[L] = S->alloc<float>((size_t)SK * QKVW_);
     ck_.assign(ENL_, nullptr);
@@ -396,18 +401,41 @@ void SmolvlaTf::run(hipStream_t st) {
             linear(c, w.down, g, eh_, EH, C, 0, 1);
         }
         launch_rmsnorm(hf_, eh_, out_norm_, C, EH, eeps_, st);
-        linear(c, aout_, x_, mad_, hf_, EH, C, 0, 1, 0, -1, dt);  // x += dt * v_t
+        if (rtc_) {  // v_t, its guidance, then the Euler step
+            linear(c, aout_, v_, mad_, hf_, EH, C);
+            const float time = (float)(1.0 + s * (-1.0 / steps_));
+            launch_rtc_step(x_, v_, guide_, gweights_, gw_, s, C, mad_, time, dt, st);
+        } else {
+            linear(c, aout_, x_, mad_, hf_, EH, C, 0, 1, 0, -1, dt);  // x += dt * v_t
+        }
     }
     copy_f32(act_out_, x_, (int64_t)C * mad_, st);
 }
 
 void SmolvlaTf::chunk_dev(const float* prefix, const int32_t* pad, int n_prefix, const float* noise,
-                          float* actions, hipStream_t caller) {
+                          float* actions, hipStream_t caller, const Rtc* rtc) {
     VLA_REQUIRE(prefix && pad && noise && actions, "smolvla: null buffer");
+    VLA_REQUIRE(!rtc || (rtc->guide && rtc->weights && std::isfinite(rtc->max_guidance) && rtc->max_guidance > 0),
+                "smolvla: guidance needs the guide, its weights and a positive finite max_guidance");
     ensure(pad, n_prefix);
     copy_f32(prefix_in_, prefix, (int64_t)n_prefix * H_, caller);
     copy_f32(noise_in_, noise, (int64_t)C_ * mad_, caller);
-    replay_.run(key_, own_, caller, [this](hipStream_t st) { run(st); });
+    rtc_ = rtc != nullptr;
+    if (rtc_) {
+        // the guidance weight per step, in the reference's float arithmetic
+        // (its contracted s + tau * tau)
+        gw_host_.assign(steps_, 0.0f);
+        for (int s = 0; s < steps_; s++) {
+            const double td = 1.0 + s * (-1.0 / steps_);
+            const float tau = (float)(1.0 - td), sq = (1.0f - tau) * (1.0f - tau);
+            gw_host_[s] = std::min((1.0f - tau) / tau * (std::fma(tau, tau, sq) / sq), rtc->max_guidance);
+        }
+        VLA_HIP_CHECK(hipMemcpyAsync(gw_, gw_host_.data(), steps_ * sizeof(float), hipMemcpyHostToDevice, caller));
+        copy_f32(guide_, rtc->guide, (int64_t)C_ * mad_, caller);
+        copy_f32(gweights_, rtc->weights, C_, caller);
+    }
+    // the guided loop is a different graph from the plain one
+    replay_.run(key_ * 2 + (rtc_ ? 1 : 0), own_, caller, [this](hipStream_t st) { run(st); });
     copy_f32(actions, act_out_, (int64_t)C_ * mad_, caller);
 }
 

@@ -8,6 +8,7 @@
 #pragma once
 
 #include "graph.h"
+#include "tokenizer.h"
 
 #include <map>
 #include <memory>
@@ -239,8 +240,17 @@ public:
     // + the state token, as smolvla_model.cpp:231-250 assembles them); pad host
     // [n_prefix] (1 real, 0 padding; the last token is the state token);
     // noise [chunk, max_action_dim]; actions [chunk, max_action_dim] normalized.
+    // Real-time chunking guidance (action_expert.cpp:377-389): guide
+    // [chunk, max_action_dim] (the normalized previous chunk, zero past its
+    // rows) and weights [chunk] on the device, the guidance weight of step s
+    // min((1 - tau) / tau * ((1 - tau)^2 + tau^2) / (1 - tau)^2, max_guidance).
+    struct Rtc {
+        const float* guide;
+        const float* weights;
+        float max_guidance;
+    };
     void chunk_dev(const float* prefix, const int32_t* pad, int n_prefix, const float* noise,
-                   float* actions, hipStream_t caller);
+                   float* actions, hipStream_t caller, const Rtc* rtc = nullptr);
     int graph_nodes() const { return replay_.nodes(); }
 
 private:
@@ -279,6 +289,10 @@ private:
     float *prefix_in_ = nullptr, *noise_in_ = nullptr, *act_out_ = nullptr, *h_ = nullptr,
           *xn_ = nullptr, *att_ = nullptr, *gu_raw_ = nullptr, *gu_ = nullptr, *eh_ = nullptr,
           *ehn_ = nullptr, *eq_ = nullptr, *mlp1_ = nullptr, *x_ = nullptr, *hf_ = nullptr;
+    // guidance: the velocity, the guide, its row weights, the per-step weights
+    float *v_ = nullptr, *guide_ = nullptr, *gweights_ = nullptr, *gw_ = nullptr;
+    std::vector<float> gw_host_;
+    bool rtc_ = false;
     std::vector<float*> qkv_;        // per text layer [np + C, QKVW]: prefix rows from the tower, suffix rows from the expert
     std::vector<float*> ck_, cv_;    // per cross layer [np, kv_full]
     std::vector<float*> at_;         // per step [C, 2 EH], right half = the step's time embedding
@@ -331,6 +345,62 @@ private:
     Ctx ctx_;
     hipStream_t own_ = nullptr;
     GraphReplay replay_;
+};
+
+// ---------------------------------------------------- SmolVLA policy --
+// src/models/smolvla/smolvla_model.{h,cpp} + smolvla_capi.cpp: native-size
+// uint8 frames -> resize_with_pad -> SigLIP per view, the language tokens'
+// bf16 embeddings, the projected normalized state -> the prefix -> SmolvlaTf
+// (optionally with real-time-chunking guidance) -> un-normalized actions.
+// Files: heads.meta, emb.bin, heads.bin, stats_{state,action}_{mean,std}.bin,
+// config.txt (tokenizer_max_length, pad_token_id), vit.*, vlm.*, aex.*, and the
+// tokenizer's vocab.txt + merges.txt in tok_dir. SMOLVLA_INT8 is read at load.
+class SmolvlaModel {
+public:
+    SmolvlaModel(const std::string& dir, const std::string& tok_dir);
+    ~SmolvlaModel();
+    int chunk() const { return tf_->chunk(); }
+    int action_dim() const { return real_action_dim_; }
+    int state_dim() const { return real_state_dim_; }
+    int max_action_dim() const { return tf_->max_action_dim(); }
+    int n_views() const { return n_views_; }
+    int img_size() const { return vit_->img(); }
+    int tok_maxlen() const { return tok_maxlen_; }
+    int int8_layers() const { return vit_->int8_layers() + tf_->int8_layers(); }
+    int graph_nodes() const { return vit_->graph_nodes() + tf_->graph_nodes(); }
+    // vla_smolvla_tokenize: ids / mask [tok_maxlen]; returns the token count
+    int tokenize(const std::string& text, int32_t* ids, int32_t* mask) const;
+    // host buffers as vla_smolvla_predict_rtc takes them; prev null or n_prev
+    // 0 for no guidance. ShapeError for a token id outside the vocabulary.
+    void predict(const uint8_t* frames, int nv, int height, int width, const int32_t* tokens,
+                 const int32_t* lang_mask, int n_lang, const float* state, const float* noise, uint64_t seed,
+                 float* actions, const float* prev, int n_prev, const float* weights, float max_guidance);
+    // the preprocessed views [nv, 3, img, img] (host), for tests
+    void preprocess(const uint8_t* frames, int nv, int height, int width, float* pixels);
+
+private:
+    void stage_frames(const uint8_t* frames, int nv, int height, int width);
+
+    std::unique_ptr<SiglipTf> vit_;
+    std::unique_ptr<SmolvlaTf> tf_;
+    std::unique_ptr<BpeTokenizer> tok_;
+    int tok_maxlen_ = 48, pad_id_ = 2;
+    int vocab_ = 0, hidden_ = 0, max_state_dim_ = 0, real_state_dim_ = 0, real_action_dim_ = 0, n_views_ = 0;
+    float norm_eps_ = 0.0f;
+    DeviceArena A_;
+    uint16_t* emb_ = nullptr;
+    float *state_w_ = nullptr, *state_b_ = nullptr, *state_mean_ = nullptr, *state_std_ = nullptr,
+          *action_mean_ = nullptr, *action_std_ = nullptr;
+    float *pixels_ = nullptr, *state_raw_ = nullptr, *state_n_ = nullptr, *noise_ = nullptr, *act_n_ = nullptr,
+          *actions_ = nullptr, *guide_ = nullptr, *prev_ = nullptr, *weights_ = nullptr;
+    // per-call sizes: frames (native resolution) and the prefix (language length)
+    std::unique_ptr<DeviceArena> F_, P_;
+    size_t frames_cap_ = 0;
+    int prefix_cap_ = -1;
+    uint8_t* frames_ = nullptr;
+    float* prefix_ = nullptr;
+    int32_t* ids_ = nullptr;
+    hipStream_t own_ = nullptr;
 };
 
 }  // namespace hip

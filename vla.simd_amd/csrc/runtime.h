@@ -26,6 +26,9 @@ int32_t guarded(const char* where, F&& f) {
     } catch (const ArgError& e) {
         set_last_error(std::string(where) + ": " + e.what());
         return -1;
+    } catch (const ShapeError& e) {
+        set_last_error(std::string(where) + ": " + e.what());
+        return -2;
     } catch (const std::exception& e) {
         set_last_error(std::string(where) + ": " + e.what());
         return -3;
