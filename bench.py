@@ -414,8 +414,44 @@ def _lat_smolvla_model(vla, torch, ck, ob, tmp, stream_obj):
     return row
 
 
+def _lat_octo_model(vla, torch, ck, ob, tmp, stream_obj):
+    """Octo end to end through vla_octo_predict_ex (host pointers, the caller's
+    view): two timesteps of 256 x 256 primary and 128 x 128 wrist uint8 frames
+    (new frames every call: no stem reuse), the cached T5-base embedding of the
+    instruction, the 12 x 768 transformer (690 tokens), the 20-step DDPM head;
+    OCTO_INT8=63. Wall-clock median of host calls (PCIe included)."""
+    c = ck.OCTO_MODEL_BASE
+    d = os.path.join(tmp, "octo_model")
+    if not os.path.exists(os.path.join(d, "head.bin")):
+        ck.write_octo_model(d, c)
+    frames = [ck.octo_model_inputs(c, seed=s) for s in (1, 2)]
+    saved = os.environ.pop("OCTO_INT8", None)
+    try:
+        r = ob.RefOctoModel(d, int8_mask=63) if ob is not None else None  # the reference's latch stays 0
+        os.environ["OCTO_INT8"] = "63"
+        m = vla.OctoModel(d)
+    finally:
+        os.environ.pop("OCTO_INT8", None)
+        if saved is not None:
+            os.environ["OCTO_INT8"] = saved
+    text = "pick up the red block"
+    k = [0]
+
+    def call():  # alternate two windows so every call runs the stems
+        p, w, tm, n, z = frames[k[0] % 2]
+        k[0] += 1
+        return m.predict(p, w, tm, text, noise=n, z=z)
+    gpu = _median_ms(call, warmup=3, timed=20)
+    row = {"host_call_ms": round(gpu, 4), "frames": "2x(256x256 + 128x128)", "tokens": 690,
+           "ddpm_steps": c["head"]["steps"], "octo_int8": 63, "int8_layers": m.int8_layers}
+    if r is not None:
+        p, w, tm, n, z = frames[0]
+        row["cpu_ref_ms"] = round(_median_ms(lambda: r.predict(p, w, tm, text, noise=n, z=z), warmup=2, timed=10), 3)
+    return row
+
+
 def policy_latency(vla, torch, stream_obj, with_cpu=True,
-                   models=("act", "act_model", "octo", "smolvla", "siglip", "smolvla_model")):
+                   models=("act", "act_model", "octo", "smolvla", "siglip", "smolvla_model", "octo_model")):
     """Per-chunk latency of BASELINE.json configs[2..4] at batch 1, and of
     SmolVLA's SigLIP vision tower per camera image: the device
     graphs (one captured HIP graph per forward, inputs resident in HBM) and the
@@ -455,6 +491,9 @@ def policy_latency(vla, torch, stream_obj, with_cpu=True,
         if "smolvla_model" in models:
             out["smolvla_model"] = _lat_smolvla_model(vla, torch, ck, ob, tmp, stream_obj)
             print(f"  SmolVLA end to end: {out['smolvla_model']}", file=sys.stderr, flush=True)
+        if "octo_model" in models:
+            out["octo_model"] = _lat_octo_model(vla, torch, ck, ob, tmp, stream_obj)
+            print(f"  Octo end to end: {out['octo_model']}", file=sys.stderr, flush=True)
     if ob is not None:
         out["cpu_ref_threads"] = int(ob.ref().ref_omp_max_threads())
     return out
@@ -545,7 +584,7 @@ def main():
     ap.add_argument("--no-policy", action="store_true", help="skip the per-chunk policy latency leg")
     ap.add_argument("--policy-only", action="store_true",
                     help="only the per-chunk policy latency leg (for rocprofv3 runs)")
-    ap.add_argument("--models", default="act,act_model,octo,smolvla,siglip,smolvla_model", help="policy graphs to time")
+    ap.add_argument("--models", default="act,act_model,octo,smolvla,siglip,smolvla_model,octo_model", help="policy graphs to time")
     ap.add_argument("--no-conv", action="store_true", help="skip the ResNet-18 conv2d_i8 leg")
     ap.add_argument("--conv-only", action="store_true", help="only the ResNet-18 conv2d_i8 leg")
     ap.add_argument("--profile-only", action="store_true",

@@ -637,6 +637,38 @@ VLA_API int32_t vla_smolvla_preprocess(void* h, const uint8_t* frames, int32_t n
 VLA_API int32_t vla_smolvla_int8_layers(void* h);
 VLA_API int32_t vla_smolvla_graph_nodes(void* h);
 
+/* ----------------------------------------------- Octo, model level ------- */
+
+/* The reference's Octo entry points, same names and signatures
+ * (include/vla_simd.h:126-153, src/models/octo/octo_capi.cpp). load reads the
+ * converted directory (t5, stem_primary, stem_wrist, octo, head, stats) and
+ * the SentencePiece vocab.txt in tok_dir; OCTO_INT8 is read at load
+ * (octo_model.cpp:43-58 bits: 1 attention, 2 w1, 4 w2, 8 token projections
+ * and stem embeddings, 16 stem convs, 32 the diffusion score net). predict:
+ * primary [wnd, 256, 256, 3] and wrist [wnd, 128, 128, 3] (or NULL) uint8,
+ * timestep_mask [wnd], the instruction (its T5 embedding is cached), actions
+ * [horizon * action_dim] out, un-normalized where the action mask is set when
+ * unnormalize != 0. predict_ex takes the DDPM noise [horizon * action_dim] and
+ * z [steps * horizon * action_dim], both or neither (VLA_ERR_ARG otherwise);
+ * without them they are drawn from mt19937_64(seed). VLA_ERR_SHAPE for wnd
+ * outside [1, max_window]. Stems, T5, transformer and head run on the device. */
+VLA_API void* vla_octo_load(const char* model_dir, const char* tok_dir);
+VLA_API void vla_octo_free(void* h);
+VLA_API int32_t vla_octo_horizon(void* h);
+VLA_API int32_t vla_octo_action_dim(void* h);
+VLA_API int32_t vla_octo_max_window(void* h);
+VLA_API int32_t vla_octo_predict(void* h, const uint8_t* primary, const uint8_t* wrist, int32_t wnd,
+                                 const uint8_t* timestep_mask, const char* instruction, uint64_t seed,
+                                 int32_t unnormalize, float* actions);
+VLA_API int32_t vla_octo_predict_ex(void* h, const uint8_t* primary, const uint8_t* wrist, int32_t wnd,
+                                    const uint8_t* timestep_mask, const char* instruction, const float* noise,
+                                    const float* z, uint64_t seed, int32_t unnormalize, float* actions);
+/* Extensions with no counterpart in vla_simd.h: the T5 embedding of an
+ * instruction [n_task, t5_dim] (host pointer; n the float count, checked),
+ * and the count of int8 layers. */
+VLA_API int32_t vla_octo_lang(void* h, const char* instruction, float* out, int64_t n);
+VLA_API int32_t vla_octo_int8_layers(void* h);
+
 /* SmolVLA's byte-level BPE tokenizer alone (src/tokenizer/tokenizer.h:16-30,
  * Tokenizer::load + encode), host code that needs no device: tok_dir holds
  * vocab.txt and merges.txt. encode writes at most cap ids and returns the
@@ -645,6 +677,15 @@ VLA_API int32_t vla_smolvla_graph_nodes(void* h);
 VLA_API void* vla_bpe_load(const char* tok_dir);
 VLA_API void vla_bpe_free(void* h);
 VLA_API int32_t vla_bpe_encode(void* h, const char* text, int32_t* ids, int32_t cap);
+
+/* Octo's SentencePiece unigram tokenizer alone (src/tokenizer/
+ * t5_tokenizer.h:14-33, T5Tokenizer::load + encode), host code: tok_dir holds
+ * vocab.txt ("piece<TAB>score" lines). encode writes exactly max_len ids
+ * (pieces cut to max_len - 1, then </s> = 1, then <pad> = 0). No counterpart
+ * in vla_simd.h. */
+VLA_API void* vla_unigram_load(const char* tok_dir);
+VLA_API void vla_unigram_free(void* h);
+VLA_API int32_t vla_unigram_encode(void* h, const char* text, int32_t max_len, int32_t* ids);
 
 /* ------------------------------------------------ int8-step probe (tests) -- */
 

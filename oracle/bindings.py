@@ -522,6 +522,21 @@ def _ref_models():
     L.ref_bpe_load.argtypes, L.ref_bpe_load.restype = [ctypes.c_char_p], P
     L.ref_bpe_free.argtypes = [P]
     L.ref_bpe_encode.argtypes, L.ref_bpe_encode.restype = [P, ctypes.c_char_p, P, i], i
+    L.ref_octo_model_load.argtypes, L.ref_octo_model_load.restype = [ctypes.c_char_p, ctypes.c_char_p, i], P
+    L.ref_octo_model_free.argtypes = [P]
+    L.ref_octo_model_dims.argtypes = [P, P]
+    L.ref_octo_model_lang.argtypes = [P, ctypes.c_char_p, P]
+    L.ref_octo_model_predict.argtypes = [P, P, P, i, P, ctypes.c_char_p, P, P, i, P, i]
+    L.vla_octo_load.argtypes, L.vla_octo_load.restype = [ctypes.c_char_p, ctypes.c_char_p], P
+    L.vla_octo_free.argtypes, L.vla_octo_free.restype = [P], None
+    for n in ("horizon", "action_dim", "max_window"):
+        f = getattr(L, f"vla_octo_{n}")
+        f.argtypes, f.restype = [P], ctypes.c_int32
+    L.vla_octo_predict_ex.argtypes = [P, P, P, ctypes.c_int32, P, ctypes.c_char_p, P, P, c_uint64, ctypes.c_int32, P]
+    L.vla_octo_predict_ex.restype = ctypes.c_int32
+    L.ref_t5tok_load.argtypes, L.ref_t5tok_load.restype = [ctypes.c_char_p], P
+    L.ref_t5tok_free.argtypes = [P]
+    L.ref_t5tok_encode.argtypes = [P, ctypes.c_char_p, i, P]
     # the reference's own SmolVLA entry points (smolvla_capi.cpp)
     i32 = ctypes.c_int32
     L.vla_smolvla_load.argtypes, L.vla_smolvla_load.restype = [ctypes.c_char_p, ctypes.c_char_p], P
@@ -779,3 +794,77 @@ class RefBpe:
     def __del__(self):
         if getattr(self, "h", None):
             _ref_models().ref_bpe_free(self.h)
+
+
+class RefT5Tok:
+    """The reference's T5Tokenizer (src/tokenizer/t5_tokenizer.cpp)."""
+
+    def __init__(self, tok_dir):
+        self.h = _ref_models().ref_t5tok_load(tok_dir.encode())
+        if not self.h:
+            raise RuntimeError(f"reference T5Tokenizer::load failed for {tok_dir}")
+
+    def encode(self, text, max_len=16):
+        b = text.encode() if isinstance(text, str) else bytes(text)
+        ids = np.zeros(max_len, np.int32)
+        _ref_models().ref_t5tok_encode(self.h, b, max_len, _p(ids))
+        return [int(v) for v in ids]
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            _ref_models().ref_t5tok_free(self.h)
+
+
+class RefOctoModel:
+    """The reference's OctoModel. int8_mask None: through its own C ABI
+    (vla_octo_load / vla_octo_predict_ex, OCTO_INT8 as the process latched
+    it); an int mask: ref_octo_model_load with that mask's groups and
+    ref_octo_model_predict (noise and z required, optional stem-token ulp
+    perturbation)."""
+
+    def __init__(self, dirpath, tok_dir=None, int8_mask=None):
+        L = _ref_models()
+        tok_dir = tok_dir or os.path.join(dirpath, "tok")
+        self.abi = int8_mask is None
+        self.h = (L.vla_octo_load(dirpath.encode(), tok_dir.encode()) if self.abi
+                  else L.ref_octo_model_load(dirpath.encode(), tok_dir.encode(), int8_mask))
+        if not self.h:
+            raise RuntimeError(f"reference OctoModel::load failed for {dirpath}")
+        self._shim = None if self.abi else self.h
+        d = np.zeros(6, np.int32)
+        if not self.abi:
+            L.ref_octo_model_dims(self.h, _p(d))
+            self.horizon, self.action_dim, self.max_window, self.n_task, self.t5_dim, self.steps = (int(v) for v in d)
+        else:
+            self.horizon, self.action_dim = L.vla_octo_horizon(self.h), L.vla_octo_action_dim(self.h)
+            self.max_window = L.vla_octo_max_window(self.h)
+
+    def predict(self, primary, wrist, tmask, instruction, noise=None, z=None, seed=0, unnormalize=True, perturb=0):
+        """-> (status, actions [horizon, action_dim])"""
+        L = _ref_models()
+        primary = np.ascontiguousarray(primary, np.uint8)
+        wrist = None if wrist is None else np.ascontiguousarray(wrist, np.uint8)
+        tm = np.ascontiguousarray(tmask, np.uint8)
+        noise = None if noise is None else _f32(noise)
+        z = None if z is None else _f32(z)
+        out = np.zeros((self.horizon, self.action_dim), np.float32)
+        wnd = primary.shape[0]
+        if self.abi:
+            st = L.vla_octo_predict_ex(self.h, _p(primary), _p(wrist), wnd, _p(tm), instruction.encode(), _p(noise),
+                                       _p(z), seed, int(bool(unnormalize)), _p(out))
+            return int(st), out
+        assert noise is not None and z is not None
+        L.ref_octo_model_predict(self.h, _p(primary), _p(wrist), wnd, _p(tm), instruction.encode(), _p(noise), _p(z),
+                                 int(bool(unnormalize)), _p(out), int(perturb))
+        return 0, out
+
+    def lang(self, instruction):
+        assert not self.abi
+        out = np.zeros((self.n_task, self.t5_dim), np.float32)
+        _ref_models().ref_octo_model_lang(self.h, instruction.encode(), _p(out))
+        return out
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            L = _ref_models()
+            (L.vla_octo_free if self.abi else L.ref_octo_model_free)(self.h)

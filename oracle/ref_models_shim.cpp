@@ -25,11 +25,17 @@
  *     it, since SmolvlaModel::apply_int8 latches the variable once per
  *     process (a static); the library's own vla_smolvla_* entry points
  *     (compiled in from smolvla_capi.cpp) serve the environment's mask;
- *   - resize_with_pad and the BPE tokenizer on their own.
+ *   - resize_with_pad and the BPE tokenizer on their own;
+ *   - the whole OctoModel with OCTO_INT8's groups for a given mask
+ *     (OctoModel::apply_int8, octo_model.cpp:100-141, latches the variable
+ *     once per process too) and OctoModel::predict restated over its public
+ *     parts (octo_model.cpp:160-229, without the frame reuse, which changes
+ *     no value), with an optional 1-ulp perturbation of the stem tokens.
  */
 #include "io/files.h"
 #include "models/act/act_model.h"
 #include "models/act/act_transformer.h"
+#include "models/octo/octo_model.h"
 #include "models/octo/octo_transformer.h"
 #include "models/smolvla/action_expert.h"
 #include "models/smolvla/siglip_vision.h"
@@ -37,6 +43,7 @@
 #include "models/smolvla/smolvla_model.h"
 #include "ops/lm_ops.h"
 #include "preprocess/image.h"
+#include "tokenizer/t5_tokenizer.h"
 #include "tokenizer/tokenizer.h"
 
 #include <cmath>
@@ -492,4 +499,125 @@ REF_API int ref_bpe_encode(void* h, const char* text, int32_t* ids, int cap) {
     const std::vector<int> v = static_cast<Tokenizer*>(h)->encode(text);
     for (int i = 0; i < (int)v.size() && i < cap; i++) ids[i] = v[i];
     return (int)v.size();
+}
+
+REF_API void* ref_t5tok_load(const char* dir) {
+    try {
+        auto* t = new T5Tokenizer();
+        if (!t->load(dir)) {
+            delete t;
+            return nullptr;
+        }
+        return t;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "ref_t5tok_load: %s\n", e.what());
+        return nullptr;
+    }
+}
+REF_API void ref_t5tok_free(void* h) { delete static_cast<T5Tokenizer*>(h); }
+/* T5Tokenizer::encode(text, max_len): max_len ids */
+REF_API void ref_t5tok_encode(void* h, const char* text, int max_len, int32_t* ids) {
+    const std::vector<int> v = static_cast<T5Tokenizer*>(h)->encode(text, max_len);
+    for (int i = 0; i < (int)v.size(); i++) ids[i] = v[i];
+}
+
+/* OctoModel::load, then OctoModel::apply_int8's groups for int8_mask. The
+ * caller leaves OCTO_INT8 unset so that load's own apply_int8 does nothing. */
+REF_API void* ref_octo_model_load(const char* dir, const char* tok_dir, int int8_mask) {
+    try {
+        auto* m = new OctoModel();
+        if (!m->load(dir, tok_dir)) {
+            delete m;
+            return nullptr;
+        }
+        for (nn::EncoderLayer& l : m->tf.layers) {
+            if (int8_mask & 1)
+                for (nn::Linear* x : {&l.attn.wq, &l.attn.wk, &l.attn.wv, &l.attn.wo}) x->init_int8();
+            if (int8_mask & 2) l.w1.init_int8();
+            if (int8_mask & 4) l.w2.init_int8();
+        }
+        if (int8_mask & 8)
+            for (nn::Linear* x : {&m->tf.proj_task, &m->tf.proj_prim, &m->tf.proj_wrist, &m->stem_primary.embed,
+                                  &m->stem_wrist.embed})
+                x->init_int8();
+        if (int8_mask & 16)
+            for (SmallStem* st : {&m->stem_primary, &m->stem_wrist})
+                for (StemLayer& l : st->layers) l.conv.init_int8();
+        if (int8_mask & 32) {
+            m->head.net.in_proj.init_int8();
+            m->head.net.out_proj.init_int8();
+            for (nn::DiffusionMlp::Block& b : m->head.net.blocks) {
+                b.d0.init_int8();
+                b.d1.init_int8();
+            }
+        }
+        return m;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "ref_octo_model_load: %s\n", e.what());
+        return nullptr;
+    }
+}
+
+REF_API void ref_octo_model_free(void* h) { delete static_cast<OctoModel*>(h); }
+
+/* horizon, action_dim, max_window, n_task, t5_dim, steps */
+REF_API void ref_octo_model_dims(void* h, int* d) {
+    const auto& m = *static_cast<OctoModel*>(h);
+    d[0] = m.head.cfg.horizon;
+    d[1] = m.head.cfg.action_dim;
+    d[2] = m.tf.cfg.max_horizon;
+    d[3] = m.tf.cfg.n_task;
+    d[4] = m.t5.cfg.d_model;
+    d[5] = m.head.cfg.steps;
+}
+
+/* OctoModel::lang_encode's value: [n_task, d_model] */
+REF_API void ref_octo_model_lang(void* h, const char* instruction, float* out) {
+    const auto& m = *static_cast<OctoModel*>(h);
+    const int NT = m.tf.cfg.n_task;
+    std::vector<int> ids = m.tok.encode(instruction, NT);
+    std::vector<int> am(NT);
+    for (int i = 0; i < NT; i++) am[i] = ids[i] != m.tok.pad_id;
+    m.t5.encode(ids.data(), am.data(), NT, out);
+}
+
+/* OctoModel::predict with the noise given; perturb > 0 moves every stem token
+ * value by -1, 0 or +1 ulp (xorshift seeded by perturb): the class of
+ * difference fp32 stem convolutions with another summation order leave. */
+REF_API void ref_octo_model_predict(void* h, const uint8_t* primary, const uint8_t* wrist, int wnd,
+                                    const uint8_t* tmask, const char* instruction, const float* noise, const float* z,
+                                    int unnormalize, float* actions, int perturb) {
+    const auto& m = *static_cast<OctoModel*>(h);
+    const int D = m.tf.cfg.d;
+    const size_t PB = (size_t)256 * 256 * 3, WB = (size_t)128 * 128 * 3;
+    const size_t SP = (size_t)m.tf.cfg.tok_primary * m.tf.cfg.stem_dim, SW = (size_t)m.tf.cfg.tok_wrist * m.tf.cfg.stem_dim;
+    std::vector<float> sp((size_t)wnd * SP), sw(wrist ? (size_t)wnd * SW : 0);
+    for (int t = 0; t < wnd; t++) {
+        m.stem_primary.encode(primary + (size_t)t * PB, 256, 256, sp.data() + (size_t)t * SP);
+        if (wrist) m.stem_wrist.encode(wrist + (size_t)t * WB, 128, 128, sw.data() + (size_t)t * SW);
+    }
+    if (perturb > 0) {
+        uint64_t x = 0x9E3779B97F4A7C15ull * (uint64_t)perturb;
+        for (std::vector<float>* v : {&sp, &sw})
+            for (float& p : *v) {
+                x ^= x << 13;
+                x ^= x >> 7;
+                x ^= x << 17;
+                const int d = (int)(x % 3) - 1;
+                if (d) p = std::nextafter(p, d > 0 ? INFINITY : -INFINITY);
+            }
+    }
+    const int NT = m.tf.cfg.n_task;
+    std::vector<float> t5((size_t)NT * m.t5.cfg.d_model);
+    ref_octo_model_lang(h, instruction, t5.data());
+    std::vector<float> out((size_t)m.tf.total_tokens(wnd) * D);
+    m.tf.forward(t5.data(), sp.data(), wrist ? sw.data() : nullptr, wnd, tmask, out.data());
+    const float* emb = out.data() + (size_t)m.tf.readout_index(wnd, wnd - 1) * D;
+    m.head.denoise(emb, noise, z, actions);
+    if (unnormalize)
+        for (int hh = 0; hh < m.head.cfg.horizon; hh++)
+            for (int a = 0; a < m.head.cfg.action_dim; a++) {
+                float* v = actions + (size_t)hh * m.head.cfg.action_dim + a;
+                if (m.act_mask[a] > 0.0f) *v = *v * m.act_std[a] + m.act_mean[a];
+            }
 }

@@ -80,6 +80,9 @@ EXPORTS = (
     "vla_smolvla_state_dim", "vla_smolvla_n_views", "vla_smolvla_img_size", "vla_smolvla_tok_maxlen",
     "vla_smolvla_tokenize", "vla_smolvla_predict", "vla_smolvla_predict_rtc", "vla_smolvla_preprocess",
     "vla_smolvla_int8_layers", "vla_smolvla_graph_nodes", "vla_bpe_load", "vla_bpe_free", "vla_bpe_encode",
+    "vla_unigram_load", "vla_unigram_free", "vla_unigram_encode",
+    "vla_octo_load", "vla_octo_free", "vla_octo_horizon", "vla_octo_action_dim", "vla_octo_max_window",
+    "vla_octo_predict", "vla_octo_predict_ex", "vla_octo_lang", "vla_octo_int8_layers",
 )
 
 
@@ -263,6 +266,18 @@ def _declare(L):
         "vla_bpe_load": (P, [c_char_p]),
         "vla_bpe_free": (None, [P]),
         "vla_bpe_encode": (i32, [P, c_char_p, P, i32]),
+        "vla_octo_load": (P, [c_char_p, c_char_p]),
+        "vla_octo_free": (None, [P]),
+        "vla_octo_horizon": (i32, [P]),
+        "vla_octo_action_dim": (i32, [P]),
+        "vla_octo_max_window": (i32, [P]),
+        "vla_octo_int8_layers": (i32, [P]),
+        "vla_octo_predict": (i32, [P, P, P, i32, P, c_char_p, ctypes.c_uint64, i32, P]),
+        "vla_octo_predict_ex": (i32, [P, P, P, i32, P, c_char_p, P, P, ctypes.c_uint64, i32, P]),
+        "vla_octo_lang": (i32, [P, c_char_p, P, i64]),
+        "vla_unigram_load": (P, [c_char_p]),
+        "vla_unigram_free": (None, [P]),
+        "vla_unigram_encode": (i32, [P, c_char_p, i32, P]),
         "vla_probe_begin": (i32, [i32]),
         "vla_probe_end": (i32, []),
         "vla_probe_count": (i32, []),
@@ -972,6 +987,68 @@ class BpeTokenizer(_Handle):
         ids = np.zeros(max(n, 1), np.int32)
         lib().vla_bpe_encode(self.h, b, _ptr(ids), n)
         return [int(v) for v in ids[:n]]
+
+
+class OctoModel(_Handle):
+    """Octo end to end on the device through the reference's own entry points
+    (vla_octo_load / vla_octo_predict / vla_octo_predict_ex): pre-resized
+    uint8 frames + an instruction -> actions."""
+
+    _load, _free = "vla_octo_load", "vla_octo_free"
+
+    def __init__(self, dirpath: str, tok_dir: str | None = None):
+        tok_dir = tok_dir or os.path.join(dirpath, "tok")
+        super().__init__(lib().vla_octo_load(dirpath.encode(), tok_dir.encode()))
+        L = lib()
+        self.horizon, self.action_dim = L.vla_octo_horizon(self.h), L.vla_octo_action_dim(self.h)
+        self.max_window, self.int8_layers = L.vla_octo_max_window(self.h), L.vla_octo_int8_layers(self.h)
+
+    def predict(self, primary, wrist, timestep_mask, instruction: str, noise=None, z=None, seed=0,
+                unnormalize=True):
+        primary = np.ascontiguousarray(primary, np.uint8)
+        if primary.ndim != 4 or primary.shape[1:] != (256, 256, 3):
+            raise ValueError(f"primary must be [wnd, 256, 256, 3], got {primary.shape}")
+        wnd = primary.shape[0]
+        if wrist is not None:
+            wrist = np.ascontiguousarray(wrist, np.uint8)
+            if wrist.shape != (wnd, 128, 128, 3):
+                raise ValueError(f"wrist must be [{wnd}, 128, 128, 3], got {wrist.shape}")
+        tm = np.ascontiguousarray(timestep_mask, np.uint8)
+        _need_size("timestep_mask", tm, wnd)
+        out = np.empty((self.horizon, self.action_dim), np.float32)
+        if (noise is None) != (z is None):
+            raise ValueError("pass both noise and z, or neither")
+        if noise is None:
+            _call("vla_octo_predict", self.h, _ptr(primary), _ptr(wrist), wnd, _ptr(tm), instruction.encode(),
+                  ctypes.c_uint64(seed), int(bool(unnormalize)), _ptr(out))
+        else:
+            noise, z = _f32(noise), _f32(z)
+            _need_size("noise", noise, self.horizon * self.action_dim)
+            if z.size % (self.horizon * self.action_dim):
+                raise ValueError("z must be [steps, horizon * action_dim]")
+            _call("vla_octo_predict_ex", self.h, _ptr(primary), _ptr(wrist), wnd, _ptr(tm), instruction.encode(),
+                  _ptr(noise), _ptr(z), ctypes.c_uint64(seed), int(bool(unnormalize)), _ptr(out))
+        return out
+
+    def lang(self, instruction: str, n_task: int, t5_dim: int):
+        out = np.empty((n_task, t5_dim), np.float32)
+        _call("vla_octo_lang", self.h, instruction.encode(), _ptr(out), out.size)
+        return out
+
+
+class UnigramTokenizer(_Handle):
+    """Octo's SentencePiece unigram tokenizer alone (vla_unigram_*), host code."""
+
+    _load, _free = "vla_unigram_load", "vla_unigram_free"
+
+    def __init__(self, tok_dir: str):
+        super().__init__(lib().vla_unigram_load(tok_dir.encode()))
+
+    def encode(self, text, max_len: int = 16) -> list:
+        b = text.encode() if isinstance(text, str) else bytes(text)
+        ids = np.zeros(max_len, np.int32)
+        _call("vla_unigram_encode", self.h, b, max_len, _ptr(ids))
+        return [int(v) for v in ids]
 
 
 class OctoTransformer(_Handle):

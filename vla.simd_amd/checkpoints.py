@@ -501,6 +501,157 @@ def write_bpe_tokenizer(dirpath: str, n_merges: int = 160, corpus: str = TOK_COR
     return dirpath
 
 
+def write_t5_vocab(dirpath: str, corpus: str = TOK_CORPUS, seed: int = synth.BASE_SEED) -> str:
+    """A SentencePiece unigram vocab.txt ("piece<TAB>score" per line, line =
+    id; src/tokenizer/t5_tokenizer.cpp:46-72): <pad> </s> <unk> (score 0),
+    then the corpus's words (U+2581-prefixed) and their prefixes and suffixes,
+    single characters, a literal special piece <extra_id_0> (score 0), a
+    score-0 ordinary piece (unusable) and a duplicate line (the first wins)."""
+    os.makedirs(dirpath, exist_ok=True)
+    r = np.random.default_rng(seed)
+    sp = "▁"
+    pieces = {}
+    for w in corpus.replace(",", " ,").replace(".", " .").replace(";", " ;").replace("!", " !").split():
+        w = sp + w
+        for k in range(1, len(w) + 1):
+            pieces.setdefault(w[:k], -2.0 - 0.5 * (len(w) - k) - float(r.random()))
+            pieces.setdefault(w[-k:], -3.0 - 0.5 * (len(w) - k) - float(r.random()))
+    for ch in "abcdefghijklmnopqrstuvwxyz0123456789.,;!?'-" + sp:
+        pieces.setdefault(ch, -8.0 - float(r.random()))
+    lines = ["<pad>\t0", "</s>\t0", "<unk>\t0"]
+    lines += [f"{p}\t{v:.6f}" for p, v in pieces.items()]
+    lines += ["<extra_id_0>\t0", "zzz\t0", f"{sp}the\t-0.5", "notab line"]
+    with open(os.path.join(dirpath, "vocab.txt"), "w", encoding="utf-8", newline="\n") as f:
+        f.write("\n".join(lines) + "\n")
+    return dirpath
+
+
+# ---------------------------------------------------------------- Octo model --
+# The whole Octo checkpoint OctoModel::load reads (src/models/octo/
+# octo_model.cpp:64-98, tools/convert_octo.py's file set): the T5 encoder
+# (t5.meta/.bin, fp32), two SmallStems (stem_{primary,wrist}.meta/.bin), the
+# block transformer (octo.meta/.bin, the reference's repeated-task layout),
+# the DDPM head (head.meta/.bin), the action statistics and a SentencePiece
+# vocab in tok/.
+T5_BASE = dict(d_model=768, n_layers=12, n_heads=12, d_kv=64, d_ff=3072, vocab=32128, n_buckets=32,
+               max_dist=128, eps=1e-6)
+OCTO_STEM_BASE = dict(features=(32, 96, 192, 384), embed_dim=512, gn_groups=32, gn_eps=1e-6)
+OCTO_HEAD_BASE = dict(action_dim=7, horizon=4, time_dim=32, num_blocks=3, hidden=256, steps=20, max_action=5.0)
+OCTO_MODEL_BASE = dict(t5=T5_BASE, stem=OCTO_STEM_BASE, tf=dict(OCTO_BASE, repeat_task=1), head=OCTO_HEAD_BASE)
+
+
+def write_t5(dirpath: str, cfg: dict = T5_BASE, stem: str = "t5", seed: int = synth.BASE_SEED) -> str:
+    """<stem>.meta + <stem>.bin as T5Encoder::load reads them
+    (src/nn/t5_encoder.cpp:20-63): embedding, relative bias [n_buckets,
+    n_heads], per layer ln1, Wq, Wk, Wv, Wo, ln2, Wi [d_ff, d], Wo2 [d, d_ff],
+    the final norm; fp32, no biases."""
+    os.makedirs(dirpath, exist_ok=True)
+    c = cfg
+    D, FF = c["d_model"], c["d_ff"]
+    _meta(os.path.join(dirpath, f"{stem}.meta"), {k: c[k] for k in (
+        "d_model", "n_layers", "n_heads", "d_kv", "d_ff", "vocab", "n_buckets", "max_dist", "eps")})
+    a = _Arena(stem, seed)
+    a.normal("emb", (c["vocab"], D), 1.0)
+    a.normal("rel", (c["n_buckets"], c["n_heads"]), 0.5)
+    for L in range(c["n_layers"]):
+        a.norm(f"l{L}.ln1", D, bias=False)
+        for w in ("q", "k", "v"):
+            a.linear(f"l{L}.{w}", D, D, bias=False)
+        # T5 folds 1/sqrt(d_kv) into its query weights: keep the logits tame
+        a.parts[-3] = a.parts[-3] / math.sqrt(c["d_kv"])
+        a.linear(f"l{L}.o", D, D, bias=False)
+        a.norm(f"l{L}.ln2", D, bias=False)
+        a.linear(f"l{L}.wi", FF, D, bias=False)
+        a.linear(f"l{L}.wo", D, FF, bias=False)
+    a.norm("final", D, bias=False)
+    a.write(os.path.join(dirpath, f"{stem}.bin"))
+    return dirpath
+
+
+def write_octo_stem(dirpath: str, name: str, cfg: dict = OCTO_STEM_BASE, seed: int = synth.BASE_SEED) -> str:
+    """<name>.meta + <name>.bin as SmallStem::load reads them
+    (src/models/octo/small_stem.cpp:19-82): per layer the 3x3 stride-2 conv
+    [cout, 3, 3, cin] + bias, GroupNorm scale + bias; then the embedding."""
+    os.makedirs(dirpath, exist_ok=True)
+    c = cfg
+    feats = list(c["features"])
+    with open(os.path.join(dirpath, f"{name}.meta"), "w") as f:
+        f.write(f"in_ch 6\nn_layers {len(feats)}\nk 3\nstride 2\npad 1\n")
+        f.write("features " + " ".join(map(str, feats)) + "\n")
+        f.write(f"embed_dim {c['embed_dim']}\ngn_groups {c['gn_groups']}\ngn_eps {c['gn_eps']}\n")
+    a = _Arena(name, seed)
+    cin = 6
+    for i, cout in enumerate(feats):
+        k = 9 * cin
+        bound = 1.0 / math.sqrt(k)
+        a.parts.append(synth.uniform(f"{name}.c{i}.w", (cout, 3, 3, cin), -bound, bound, seed))
+        a.parts.append(synth.normal(f"{name}.c{i}.b", (cout,), 0.02, seed))
+        a.norm(f"c{i}.gn", cout)
+        cin = cout
+    a.linear("embed", c["embed_dim"], cin)
+    a.write(os.path.join(dirpath, f"{name}.bin"))
+    return dirpath
+
+
+def write_octo_head(dirpath: str, emb: int, cfg: dict = OCTO_HEAD_BASE, seed: int = synth.BASE_SEED) -> str:
+    """head.meta + head.bin as DiffusionHead::load reads them
+    (src/models/octo/diffusion_head.cpp:17-118): Fourier weights, the cond
+    MLP, in_proj, blocks (LN, d0 [4H, H], d1 [H, 4H]), out_proj, then the
+    betas / alphas / alpha_hats of a linear schedule."""
+    os.makedirs(dirpath, exist_ok=True)
+    c = cfg
+    TD, H, FLAT, S = c["time_dim"], c["hidden"], c["action_dim"] * c["horizon"], c["steps"]
+    _meta(os.path.join(dirpath, "head.meta"),
+          {"emb": emb, "action_dim": c["action_dim"], "horizon": c["horizon"], "time_dim": TD,
+           "num_blocks": c["num_blocks"], "hidden": H, "steps": S, "max_action": c["max_action"]})
+    a = _Arena("head", seed)
+    a.normal("fourier", (TD // 2,), 0.2)
+    a.linear("cond0", 2 * TD, TD)
+    a.linear("cond1", TD, 2 * TD)
+    a.linear("in_proj", H, TD + emb + FLAT)
+    for b in range(c["num_blocks"]):
+        a.norm(f"b{b}.ln", H)
+        a.linear(f"b{b}.d0", 4 * H, H)
+        a.linear(f"b{b}.d1", H, 4 * H)
+    a.linear("out_proj", FLAT, H)
+    betas = np.linspace(1e-4, 0.02, S, dtype=np.float64)
+    alphas = 1.0 - betas
+    a.parts += [betas.astype(np.float32), alphas.astype(np.float32), np.cumprod(alphas).astype(np.float32)]
+    a.write(os.path.join(dirpath, "head.bin"))
+    return dirpath
+
+
+def write_octo_model(dirpath: str, cfg: dict = OCTO_MODEL_BASE, seed: int = synth.BASE_SEED) -> str:
+    c = cfg
+    write_t5(dirpath, c["t5"], "t5", seed)
+    write_octo_stem(dirpath, "stem_primary", c["stem"], seed)
+    write_octo_stem(dirpath, "stem_wrist", dict(c["stem"]), seed + 1)
+    write_octo(dirpath, c["tf"], seed)
+    write_octo_head(dirpath, c["tf"]["d"], c["head"], seed)
+    ad = c["head"]["action_dim"]
+    mean = synth.normal("octo.act_mean", (ad,), 1.0, seed).astype(np.float32)
+    std = synth.uniform("octo.act_std", (ad,), 0.5, 2.0, seed).astype(np.float32)
+    mask = np.ones(ad, np.float32)
+    mask[-1] = 0.0  # the gripper dimension stays normalized, as in the reference's stats
+    for name, v in (("mean", mean), ("std", std), ("mask", mask)):
+        v.tofile(os.path.join(dirpath, f"stats_action_{name}.bin"))
+    write_t5_vocab(os.path.join(dirpath, "tok"))
+    return dirpath
+
+
+def octo_model_inputs(cfg: dict = OCTO_MODEL_BASE, wnd: int = 2, seed: int = synth.BASE_SEED):
+    """primary [wnd, 256, 256, 3], wrist [wnd, 128, 128, 3] uint8, timestep
+    mask [wnd], noise [flat], z [steps, flat]."""
+    r = np.random.default_rng(seed)
+    primary = r.integers(0, 256, size=(wnd, 256, 256, 3), dtype=np.uint8)
+    wrist = r.integers(0, 256, size=(wnd, 128, 128, 3), dtype=np.uint8)
+    h = cfg["head"]
+    flat = h["action_dim"] * h["horizon"]
+    noise = synth.normal("octo.in.noise", (flat,), 1.0, seed).astype(np.float32)
+    z = synth.normal("octo.in.z", (h["steps"], flat), 1.0, seed).astype(np.float32)
+    return primary, wrist, np.ones(wnd, np.uint8), noise, z
+
+
 # ------------------------------------------------------------- SmolVLA model --
 # The whole SmolVLA checkpoint SmolvlaModel::load reads
 # (src/models/smolvla/smolvla_model.cpp:53-113, smolvla_capi.cpp:43-84): the

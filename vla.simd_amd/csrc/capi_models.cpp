@@ -557,3 +557,85 @@ VLA_API int32_t vla_bpe_encode(void* h, const char* text, int32_t* ids, int32_t 
     });
     return rc == 0 ? n : rc;
 }
+
+// ---------------------------------------------------- the T5 tokenizer --
+// Octo's SentencePiece unigram tokenizer on its own (host code).
+
+namespace {
+std::string read_file_text(const std::string& path) {
+    FILE* f = std::fopen(path.c_str(), "rb");
+    VLA_REQUIRE(f, "cannot open " + path);
+    std::string s;
+    char buf[65536];
+    size_t n;
+    while ((n = std::fread(buf, 1, sizeof buf, f)) > 0) s.append(buf, n);
+    std::fclose(f);
+    return s;
+}
+}  // namespace
+
+VLA_API void* vla_unigram_load(const char* tok_dir) {
+    UnigramTokenizer* t = nullptr;
+    const int32_t rc = guarded("vla_unigram_load", [&] {
+        VLA_REQUIRE(tok_dir, "null tokenizer directory");
+        auto tok = std::make_unique<UnigramTokenizer>();
+        VLA_REQUIRE(tok->load(read_file_text(std::string(tok_dir) + "/vocab.txt")), "vocab.txt has no pieces");
+        t = tok.release();
+    });
+    return rc == 0 ? t : nullptr;
+}
+VLA_API void vla_unigram_free(void* h) { delete static_cast<UnigramTokenizer*>(h); }
+VLA_API int32_t vla_unigram_encode(void* h, const char* text, int32_t max_len, int32_t* ids) {
+    if (!h || !text || !ids || max_len < 1) return VLA_ERR_ARG;
+    return guarded("vla_unigram_encode", [&] {
+        const std::vector<int32_t> v = static_cast<UnigramTokenizer*>(h)->encode(text, max_len);
+        for (int32_t i = 0; i < max_len; i++) ids[i] = v[i];
+    });
+}
+
+// ----------------------------------------------------- Octo (model level) --
+// The reference's Octo entry points (include/vla_simd.h:126-153,
+// src/models/octo/octo_capi.cpp), same names and signatures.
+
+namespace {
+OctoModel* octo_model(void* h) { return static_cast<OctoModel*>(h); }
+}  // namespace
+
+VLA_API void* vla_octo_load(const char* model_dir, const char* tok_dir) {
+    OctoModel* m = nullptr;
+    const int32_t rc = guarded("vla_octo_load", [&] {
+        VLA_REQUIRE(model_dir && tok_dir, "null model or tokenizer directory");
+        m = new OctoModel(model_dir, tok_dir);
+    });
+    return rc == 0 ? m : nullptr;
+}
+VLA_API void vla_octo_free(void* h) { delete octo_model(h); }
+VLA_API int32_t vla_octo_horizon(void* h) { return h ? octo_model(h)->horizon() : 0; }
+VLA_API int32_t vla_octo_action_dim(void* h) { return h ? octo_model(h)->action_dim() : 0; }
+VLA_API int32_t vla_octo_max_window(void* h) { return h ? octo_model(h)->max_window() : 0; }
+VLA_API int32_t vla_octo_int8_layers(void* h) { return h ? octo_model(h)->int8_layers() : 0; }
+
+VLA_API int32_t vla_octo_predict_ex(void* h, const uint8_t* primary, const uint8_t* wrist, int32_t wnd,
+                                    const uint8_t* timestep_mask, const char* instruction, const float* noise,
+                                    const float* z, uint64_t seed, int32_t unnormalize, float* actions) {
+    if (!h || !primary || !timestep_mask || !instruction || !actions) return VLA_ERR_ARG;
+    return guarded("vla_octo_predict_ex", [&] {
+        octo_model(h)->predict(primary, wrist, wnd, timestep_mask, instruction, noise, z, seed, unnormalize != 0,
+                               actions);
+    });
+}
+
+VLA_API int32_t vla_octo_predict(void* h, const uint8_t* primary, const uint8_t* wrist, int32_t wnd,
+                                 const uint8_t* timestep_mask, const char* instruction, uint64_t seed,
+                                 int32_t unnormalize, float* actions) {
+    return vla_octo_predict_ex(h, primary, wrist, wnd, timestep_mask, instruction, nullptr, nullptr, seed,
+                               unnormalize, actions);
+}
+
+VLA_API int32_t vla_octo_lang(void* h, const char* instruction, float* out, int64_t n) {
+    if (!h || !instruction || !out) return VLA_ERR_ARG;
+    return guarded("vla_octo_lang", [&] {
+        VLA_REQUIRE(n == octo_model(h)->lang_size(), "vla_octo_lang: n must be n_task * t5_dim");
+        octo_model(h)->lang(instruction, out);
+    });
+}

@@ -247,6 +247,22 @@ void launch_normalize_pad(float* out, int ldo, const float* x, int n_real, int r
 // out [rows, cols] = fma(a[r, c], std[c] + eps, mean[c]) from a [rows, lda]
 void launch_unnormalize(float* out, const float* a, int lda, int rows, int cols, const float* mean,
                         const float* stdv, float eps, hipStream_t st);
+// dst [n, D] = fp32 rows table[ids[t]], zeros for ids outside [0, vocab)
+void launch_embed_f32(float* dst, const float* table, const int32_t* ids, int n, int D, int vocab,
+                      hipStream_t st);
+// Octo SmallStem input: [npx, 6] = RGB / 127.5 - 1, then three -1 channels
+void launch_stem_input(float* out, const uint8_t* img, int64_t npx, hipStream_t st);
+// GroupNorm over NHWC [n_pixels, C] with per-channel scale / bias, then the
+// optional ReLU; A / B: device scratch [C] each (the per-channel affine)
+void launch_groupnorm(float* out, const float* x, const float* scale, const float* bias, int n_pixels, int C,
+                      int groups, float eps, bool relu, float* A, float* B, hipStream_t st);
+// out [steps, TD] = [cos(2 pi t w) | sin(2 pi t w)], t = 0..steps-1
+void launch_fourier(float* out, const float* w, int steps, int TD, hipStream_t st);
+void launch_concat3(float* out, const float* a, int na, const float* b, int nb, const float* c, int nc,
+                    hipStream_t st);
+// x = clip(a1 * (x - a2 * e) + sb * z, +-max_action) over n values
+void launch_ddpm_step(float* x, const float* e, const float* z, int n, float a1, float a2, float sb,
+                      float max_action, hipStream_t st);
 // the guided Euler step of real-time chunking, gw [steps] on the device
 void launch_rtc_step(float* x, const float* v, const float* prev, const float* weights, const float* gw, int step,
                      int rows, int cols, float time, float dt, hipStream_t st);

@@ -330,6 +330,7 @@ void launch_act(float* x, int64_t n, int act, hipStream_t st) {
     case 1: act_kernel<1><<<grid_for(n), 256, 0, st>>>(x, n); break;
     case 2: act_kernel<2><<<grid_for(n), 256, 0, st>>>(x, n); break;
     case 3: act_kernel<3><<<grid_for(n), 256, 0, st>>>(x, n); break;
+    case 4: act_kernel<4><<<grid_for(n), 256, 0, st>>>(x, n); break;
     default: throw ArgError("activation: unknown kind");
     }
     VLA_LAUNCH_CHECK();

@@ -320,6 +320,19 @@ void linear(const Ctx& c, const DLinear& L, const In& in, float* out, int ldo, i
     if (n1 < 0) n1 = L.N;
     VLA_REQUIRE(0 <= n0 && n0 < n1 && n1 <= L.N, "linear: bad output row range");
     if (seq == 0) return;
+    if (L.int8() && act == 4) {
+        // the int8 epilogue has no silu: the GEMM, then silu over the block in
+        // place (the reference's Linear::forward then silu(), diffusion.cpp:24-26)
+        VLA_REQUIRE(acc == 0, "linear: int8 silu layers cannot accumulate");
+        linear(c, L, in, out, ldo, seq, 0, 0, n0, n1, alpha);
+        const int w = n1 - n0;
+        if (ldo == w || seq == 1) {
+            launch_act(out, (int64_t)seq * w, 4, c.st);
+        } else {
+            for (int r = 0; r < seq; r++) launch_act(out + (size_t)r * ldo, w, 4, c.st);
+        }
+        return;
+    }
     if (L.int8()) {
         VLA_REQUIRE(alpha == 1.0f, "linear: the int8 epilogue accumulates with alpha = 1 only");
         VLA_REQUIRE(act <= 3, "linear: the int8 epilogue has no silu");

@@ -403,5 +403,145 @@ private:
     hipStream_t own_ = nullptr;
 };
 
+// ------------------------------------------------------------ Octo policy --
+class CkptFiles;
+
+// src/nn/t5_encoder.{h,cpp}: the T5 encoder (pre-RMSNorm blocks, relative
+// position bias attention without 1/sqrt(d) scaling, ReLU FFN, no biases,
+// final RMSNorm), fp32 on the device. <stem>.meta / <stem>.bin.
+class T5Enc {
+public:
+    T5Enc(const CkptFiles& files, const std::string& stem);
+    int d_model() const { return D_; }
+    int vocab() const { return vocab_; }
+    // ids / mask host [seq] -> out device [seq, d_model]; an id outside the
+    // vocabulary embeds as zeros (t5_encoder.cpp:96-104)
+    void encode_dev(const int32_t* ids, const int32_t* mask, int seq, float* out, hipStream_t st);
+
+private:
+    struct Layer {
+        const float *ln1, *ln2;
+        float *wqkv, *wo, *wi, *wo2;
+    };
+    int D_ = 768, NL_ = 12, NH_ = 12, HD_ = 64, FF_ = 3072, vocab_ = 32128, nb_ = 32, maxd_ = 128;
+    float eps_ = 1e-6f;
+    DeviceArena A_;
+    const float *emb_ = nullptr, *final_ = nullptr;
+    std::vector<float> rel_;  // [n_buckets, n_heads] (host: the bias table is built per mask)
+    std::vector<Layer> layers_;
+    std::unique_ptr<DeviceArena> S_;
+    int seq_cap_ = 0;
+    float *x_ = nullptr, *h_ = nullptr, *qkv_ = nullptr, *att_ = nullptr, *ff_ = nullptr, *bias_ = nullptr;
+    int32_t* ids_ = nullptr;
+};
+
+// src/models/octo/small_stem.{h,cpp}: uint8 RGB -> [x / 127.5 - 1, three -1
+// goal channels] -> n_layers x (k x k conv, stride, pad -> GroupNorm + ReLU)
+// -> patch embedding. int8_mask: OCTO_INT8 bit 16 the convs (conv2d_i8),
+// bit 8 the embedding.
+class OctoStem {
+public:
+    OctoStem(const CkptFiles& files, const std::string& name, int int8_mask, int H, int W);
+    int tokens() const { return tok_; }
+    int embed_dim() const { return embed_dim_; }
+    int int8_layers() const { return n_int8_; }
+    // img device [H, W, 3] uint8 -> out device [tokens, embed_dim]
+    void encode_dev(const uint8_t* img, float* out, hipStream_t st);
+
+private:
+    struct Layer {
+        int cin, cout, H, W, Ho, Wo;
+        float *W_ = nullptr, *b = nullptr;
+        const float *gs = nullptr, *gb = nullptr;
+        std::unique_ptr<vla_linear_i8> q8;
+    };
+    int H_ = 0, W_ = 0, k_ = 3, stride_ = 2, pad_ = 1, groups_ = 32, embed_dim_ = 512, tok_ = 0, n_int8_ = 0;
+    float gn_eps_ = 1e-6f;
+    DeviceArena A_;
+    std::vector<Layer> layers_;
+    DLinear embed_;
+    float *a_ = nullptr, *b_ = nullptr, *col_ = nullptr, *gA_ = nullptr, *gB_ = nullptr;
+    void* work_ = nullptr;
+    size_t work_bytes_ = 0;
+    Ctx ctx_;
+};
+
+// src/models/octo/diffusion_head.{h,cpp} + src/nn/diffusion.{h,cpp}: the DDPM
+// score network on [time conditioning, readout embedding, x] and the
+// `steps`-step reverse loop with clipping. int8_mask: OCTO_INT8 bit 32
+// (in/out projections and the blocks' linears whose N % 16 == 0).
+class OctoHead {
+public:
+    OctoHead(const CkptFiles& files, int int8_mask);
+    int flat() const { return ad_ * horizon_; }
+    int action_dim() const { return ad_; }
+    int horizon() const { return horizon_; }
+    int steps() const { return steps_; }
+    int emb() const { return emb_; }
+    int int8_layers() const { return n_int8_; }
+    // device: emb [emb], noise [flat], z [steps, flat] -> actions [flat]
+    void denoise_dev(const float* emb, const float* noise, const float* z, float* actions, hipStream_t st);
+
+private:
+    struct Block {
+        const float *ln_s, *ln_b;
+        DLinear d0, d1;
+    };
+    int emb_ = 384, ad_ = 7, horizon_ = 4, td_ = 32, nb_ = 3, H_ = 256, steps_ = 20, n_int8_ = 0;
+    float max_action_ = 5.0f;
+    DeviceArena A_;
+    DLinear in_proj_, out_proj_;
+    std::vector<Block> blocks_;
+    float* cond_ = nullptr;  // [steps, time_dim], built at load
+    std::vector<float> a1_, a2_, sb_;
+    float *in_ = nullptr, *h_ = nullptr, *n_ = nullptr, *wide_ = nullptr, *e_ = nullptr;
+    Ctx ctx_;
+};
+
+// src/models/octo/octo_model.{h,cpp} + octo_capi.cpp: pre-resized uint8
+// frames (primary 256 x 256, wrist 128 x 128) -> SmallStems (a frame seen in
+// this or the previous window reuses its tokens) -> OctoTf with the T5
+// embedding of the instruction (cached per instruction) -> the readout ->
+// DDPM head -> optional un-normalization. OCTO_INT8 is read at load.
+class OctoModel {
+public:
+    OctoModel(const std::string& dir, const std::string& tok_dir);
+    ~OctoModel();
+    int horizon() const { return head_->horizon(); }
+    int action_dim() const { return head_->action_dim(); }
+    int max_window() const { return tf_->max_horizon(); }
+    int int8_layers() const {
+        return tf_->int8_layers() + sp_->int8_layers() + sw_->int8_layers() + head_->int8_layers();
+    }
+    // host pointers as vla_octo_predict_ex takes them
+    void predict(const uint8_t* primary, const uint8_t* wrist, int wnd, const uint8_t* tmask,
+                 const std::string& instruction, const float* noise, const float* z, uint64_t seed,
+                 bool unnormalize, float* actions);
+    // the T5 embedding of an instruction [n_task, t5_dim] (host), for tests
+    void lang(const std::string& instruction, float* out);
+    int64_t lang_size() const { return (int64_t)tf_->n_task() * t5_->d_model(); }
+
+private:
+    const float* lang_dev(const std::string& instruction);
+
+    UnigramTokenizer tok_;
+    std::unique_ptr<T5Enc> t5_;
+    std::unique_ptr<OctoStem> sp_, sw_;
+    std::unique_ptr<OctoTf> tf_;
+    std::unique_ptr<OctoHead> head_;
+    DeviceArena A_;
+    float *act_mean_ = nullptr, *act_std_ = nullptr;
+    // the instruction cache (octo_model.cpp:143-158): at most 64 entries
+    std::map<std::string, std::unique_ptr<DeviceArena>> lang_arena_;
+    std::map<std::string, const float*> lang_;
+    // frames and stem tokens of this window and the previous one
+    uint8_t *frames_p_ = nullptr, *frames_w_ = nullptr;
+    float *tok_p_[2] = {nullptr, nullptr}, *tok_w_[2] = {nullptr, nullptr};
+    int cur_ = 0;
+    std::vector<uint8_t> prev_p_, prev_w_;
+    float *emb_ = nullptr, *noise_ = nullptr, *z_ = nullptr, *act_ = nullptr, *out_ = nullptr;
+    hipStream_t own_ = nullptr;
+};
+
 }  // namespace hip
 }  // namespace vla

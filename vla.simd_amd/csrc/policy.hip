@@ -109,6 +109,118 @@ __global__ __launch_bounds__(256) void rtc_step_kernel(float* __restrict__ x, co
     }
 }
 
+// dst[t, :] = table[ids[t], :] (fp32), zeros for an id outside [0, vocab)
+// (t5_encoder.cpp:96-104)
+__global__ __launch_bounds__(256) void embed_f32_kernel(float* __restrict__ dst, const float* __restrict__ table,
+                                                        const int32_t* __restrict__ ids, int D, int vocab) {
+    const int t = blockIdx.y;
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= D) return;
+    const int id = ids[t];
+    dst[(int64_t)t * D + j] = id >= 0 && id < vocab ? table[(int64_t)id * D + j] : 0.0f;
+}
+
+// SmallStem::encode's input (small_stem.cpp:90-100): [npx, 6] = RGB / 127.5 - 1
+// and three goal channels of -1
+__global__ __launch_bounds__(256) void stem_input_kernel(float* __restrict__ out, const uint8_t* __restrict__ img,
+                                                         int64_t npx) {
+    const int64_t n = npx * 6;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const int64_t p = i / 6;
+        const int c = (int)(i - p * 6);
+        out[i] = c < 3 ? (float)img[p * 3 + c] / 127.5f - 1.0f : -1.0f;
+    }
+}
+
+// GroupNorm statistics (conv.cpp:227-309): one block per group of C / groups
+// channels over n_pixels NHWC pixels, mean and sum of squared deviations in
+// double (two passes), then per channel A = inv * scale, B = bias - mean * inv
+// * scale, inv = 1 / sqrt(var + eps).
+__global__ __launch_bounds__(256) void groupnorm_stats_kernel(float* __restrict__ A, float* __restrict__ B,
+                                                              const float* __restrict__ x, int n_pixels, int C,
+                                                              int gc, const float* __restrict__ scale,
+                                                              const float* __restrict__ bias, float eps) {
+    __shared__ double red[256];
+    const int g = blockIdx.x, c0 = g * gc;
+    const int64_t n = (int64_t)n_pixels * gc;
+    double s = 0.0;
+    for (int64_t e = threadIdx.x; e < n; e += blockDim.x) {
+        const int64_t p = e / gc;
+        s += (double)x[p * C + c0 + (int)(e - p * gc)];
+    }
+    red[threadIdx.x] = s;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
+    }
+    const double mean = red[0] / (double)n;
+    __syncthreads();
+    double q = 0.0;
+    for (int64_t e = threadIdx.x; e < n; e += blockDim.x) {
+        const int64_t p = e / gc;
+        const double d = (double)x[p * C + c0 + (int)(e - p * gc)] - mean;
+        q += d * d;
+    }
+    red[threadIdx.x] = q;
+    __syncthreads();
+    for (int w = 128; w > 0; w >>= 1) {
+        if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        __syncthreads();
+    }
+    const double inv = 1.0 / sqrt(red[0] / (double)n + (double)eps);
+    for (int c = c0 + (int)threadIdx.x; c < c0 + gc; c += blockDim.x) {
+        A[c] = (float)(inv * (double)scale[c]);
+        B[c] = (float)fma(-(mean * inv), (double)scale[c], (double)bias[c]);
+    }
+}
+
+// out = x * A[c] + B[c] (one rounding, as the reference's contracted loop),
+// then the fused ReLU (v < 0 -> 0)
+__global__ __launch_bounds__(256) void groupnorm_apply_kernel(float* __restrict__ out, const float* __restrict__ x,
+                                                              int64_t n, int C, const float* __restrict__ A,
+                                                              const float* __restrict__ B, int relu) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const int c = (int)(i % C);
+        const float v = fmaf(x[i], A[c], B[c]);
+        out[i] = relu && v < 0.0f ? 0.0f : v;
+    }
+}
+
+// DiffusionHead::time_cond's Fourier features for t = 0..steps-1
+// (diffusion_head.cpp:129-138): [cos(2 pi t w_i) | sin(2 pi t w_i)]
+__global__ __launch_bounds__(256) void fourier_kernel(float* __restrict__ out, const float* __restrict__ w, int steps,
+                                                      int TD) {
+    const int half = TD / 2;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= steps * half) return;
+    const int t = i / half, k = i % half;
+    const float f = 6.283185307179586f * (float)t * w[k];
+    out[(int64_t)t * TD + k] = cosf(f);
+    out[(int64_t)t * TD + half + k] = sinf(f);
+}
+
+// in = [a (na) | b (nb) | c (nc)]
+__global__ __launch_bounds__(256) void concat3_kernel(float* __restrict__ out, const float* __restrict__ a, int na,
+                                                      const float* __restrict__ b, int nb,
+                                                      const float* __restrict__ c, int nc) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < na) out[i] = a[i];
+    else if (i < na + nb) out[i] = b[i - na];
+    else if (i < na + nb + nc) out[i] = c[i - na - nb];
+}
+
+// the DDPM update of DiffusionHead::denoise (diffusion_head.cpp:161-177):
+// x = clip(a1 * (x - a2 * e) + sb * z, +-max_action)
+__global__ __launch_bounds__(256) void ddpm_step_kernel(float* __restrict__ x, const float* __restrict__ e,
+                                                        const float* __restrict__ z, int n, float a1, float a2,
+                                                        float sb, float max_action) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float v = fmaf(a1, fmaf(-a2, e[i], x[i]), sb * z[i]);
+    x[i] = v < -max_action ? -max_action : v > max_action ? max_action : v;
+}
+
 int grid_for(int64_t n) {
     const int64_t b = (n + 255) / 256;
     return (int)(b < 4096 ? (b > 0 ? b : 1) : 4096);
@@ -166,6 +278,50 @@ void launch_unnormalize(float* out, const float* a, int lda, int rows, int cols,
                         const float* stdv, float eps, hipStream_t st) {
     VLA_REQUIRE(rows > 0 && cols > 0 && lda >= cols, "unnormalize: bad arguments");
     unnormalize_kernel<<<grid_for((int64_t)rows * cols), 256, 0, st>>>(out, a, lda, rows, cols, mean, stdv, eps);
+    VLA_LAUNCH_CHECK();
+}
+
+void launch_embed_f32(float* dst, const float* table, const int32_t* ids, int n, int D, int vocab,
+                      hipStream_t st) {
+    VLA_REQUIRE(n >= 0 && n < 65536 && D > 0, "embed: bad arguments");
+    if (n == 0) return;
+    embed_f32_kernel<<<dim3((D + 255) / 256, n), 256, 0, st>>>(dst, table, ids, D, vocab);
+    VLA_LAUNCH_CHECK();
+}
+
+void launch_stem_input(float* out, const uint8_t* img, int64_t npx, hipStream_t st) {
+    VLA_REQUIRE(npx > 0 && out && img, "stem input: bad arguments");
+    stem_input_kernel<<<grid_for(npx * 6), 256, 0, st>>>(out, img, npx);
+    VLA_LAUNCH_CHECK();
+}
+
+void launch_groupnorm(float* out, const float* x, const float* scale, const float* bias, int n_pixels, int C,
+                      int groups, float eps, bool relu, float* A, float* B, hipStream_t st) {
+    VLA_REQUIRE(n_pixels > 0 && C > 0 && groups > 0 && C % groups == 0, "groupnorm: bad shape");
+    groupnorm_stats_kernel<<<groups, 256, 0, st>>>(A, B, x, n_pixels, C, C / groups, scale, bias, eps);
+    VLA_LAUNCH_CHECK();
+    const int64_t n = (int64_t)n_pixels * C;
+    groupnorm_apply_kernel<<<grid_for(n), 256, 0, st>>>(out, x, n, C, A, B, relu ? 1 : 0);
+    VLA_LAUNCH_CHECK();
+}
+
+void launch_fourier(float* out, const float* w, int steps, int TD, hipStream_t st) {
+    VLA_REQUIRE(steps > 0 && TD > 0 && TD % 2 == 0, "fourier: bad shape");
+    const int n = steps * (TD / 2);
+    fourier_kernel<<<(n + 255) / 256, 256, 0, st>>>(out, w, steps, TD);
+    VLA_LAUNCH_CHECK();
+}
+
+void launch_concat3(float* out, const float* a, int na, const float* b, int nb, const float* c, int nc,
+                    hipStream_t st) {
+    const int n = na + nb + nc;
+    concat3_kernel<<<(n + 255) / 256, 256, 0, st>>>(out, a, na, b, nb, c, nc);
+    VLA_LAUNCH_CHECK();
+}
+
+void launch_ddpm_step(float* x, const float* e, const float* z, int n, float a1, float a2, float sb,
+                      float max_action, hipStream_t st) {
+    ddpm_step_kernel<<<(n + 255) / 256, 256, 0, st>>>(x, e, z, n, a1, a2, sb, max_action);
     VLA_LAUNCH_CHECK();
 }
 

@@ -45,5 +45,37 @@ private:
     std::string byte_sym_[256];
 };
 
+// Octo's SentencePiece unigram tokenizer for its T5 language tower
+// (src/tokenizer/t5_tokenizer.{h,cpp}, called by OctoModel::lang_encode).
+// Behaviour kept from the reference:
+//   * vocab.txt lines "<piece>\t<score>" split at the last tab, the id the
+//     line's index among lines with a tab (std::stod of the score); a piece of
+//     score 0 is usable only when written "<...>" (the special pieces); the
+//     first line of a piece wins;
+//   * normalization: UTF-8 decoded with U+FFFD for ill-formed sequences
+//     (maximal subparts), C0/C1 controls deleted, full-width ASCII folded,
+//     a table of compatibility decompositions, whitespace runs -> one U+2581
+//     before the next word;
+//   * Viterbi over the bytes of the normalized text, each piece scored by its
+//     vocab score, one UTF-8 character as <unk> at (lowest score - 10), ties
+//     to the earlier candidate; consecutive <unk> collapse to one;
+//   * special pieces written literally ("<...>" of score 0) are emitted as
+//     themselves; the ids are cut to max_len - 1, </s> (1) appended, <pad> (0)
+//     to max_len.
+class UnigramTokenizer {
+public:
+    // false when vocab.txt has no "piece\tscore" line; std::stod's exceptions propagate
+    bool load(const std::string& vocab_txt);
+    std::vector<int32_t> encode(const std::string& text, int max_len) const;
+    static constexpr int32_t kPad = 0, kEos = 1, kUnk = 2;
+
+private:
+    void encode_words(const std::string& text, std::vector<int32_t>& ids) const;
+    std::unordered_map<std::string, int32_t> piece_;
+    std::vector<double> score_;
+    int max_len_ = 1;
+    double min_score_ = 0.0;
+};
+
 }  // namespace hip
 }  // namespace vla
