@@ -511,7 +511,8 @@ RESNET18_480x640 = [(480, 640, 3, 64, 7, 2, 3, 1), (120, 160, 64, 64, 3, 1, 1, 4
 def conv_resnet18(vla, torch, stream_obj, with_cpu=True):
     """conv2d_i8 (section f.3 of the hot path) over ResNet-18's 20 convolutions at
     480 x 640: per distinct layer the device time per call (vla_conv2d_i8_dev,
-    HIP events on the launch stream, inputs resident in HBM), its roofline
+    20 calls captured as a HIP graph, HIP events on the replay stream, inputs
+    resident in HBM), its roofline
     (max(2*npix*Cout*K / int8 peak, algorithmic bytes / HBM peak) with bytes =
     4 H W Cin + Cout K + 8 Cout + 4 npix Cout), and the reference's conv2d_i8 on
     this host (oracle/_ref, weights packed once)."""
@@ -534,17 +535,10 @@ def conv_resnet18(vla, torch, stream_obj, with_cpu=True):
         out = torch.empty((Ho, Wo, Cout), device="cuda")
         work = torch.empty(vla.conv2d_i8_workspace_bytes(H, Wd, Cin, Cout, k, s, p), dtype=torch.uint8,
                            device="cuda")
-        call = lambda: vla.conv2d_i8_dev(lin, out, xd, k, s, p, work, stream=st)
-        for _ in range(3):
-            call()
-        stream_obj.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record(stream_obj)
-        for _ in range(20):
-            call()
-        e1.record(stream_obj)
-        e1.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / 20
+        # 20 calls captured as one HIP graph (as the sweep's GEMMs), so the
+        # time is the device's, not the Python call's
+        g = capture(torch, lambda cs: vla.conv2d_i8_dev(lin, out, xd, k, s, p, work, stream=cs), 20)
+        us = time_graph(torch, g, 5, stream_obj) / 20
         npix = Ho * Wo
         ops = 2.0 * npix * Cout * K
         byt = 4.0 * H * Wd * Cin + Cout * K + 8.0 * Cout + 4.0 * npix * Cout

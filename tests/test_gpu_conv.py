@@ -19,7 +19,11 @@ pytestmark = pytest.mark.gpu
 # (H, Wd, Cin, Cout, k, stride, pad)
 SHAPES = [(224, 224, 3, 64, 7, 2, 3), (56, 56, 64, 64, 3, 1, 1), (56, 56, 64, 128, 1, 2, 0),
           (28, 28, 128, 128, 3, 1, 1), (9, 13, 5, 24, 3, 2, 1), (2, 2, 4, 16, 3, 1, 1),
-          (20, 20, 32, 40, 5, 3, 2), (64, 48, 3, 32, 3, 2, 1)]
+          (20, 20, 32, 40, 5, 3, 2), (64, 48, 3, 32, 3, 2, 1),
+          # ResNet-18's deeper layers (split K over long K, 1x1 stride 2), 16 and
+          # 48 channels, N not a multiple of 64, ragged pixel counts
+          (15, 20, 512, 512, 3, 1, 1), (30, 40, 256, 512, 1, 2, 0), (17, 23, 16, 48, 3, 1, 1),
+          (9, 9, 48, 32, 5, 2, 2), (60, 80, 128, 256, 3, 2, 1), (120, 160, 64, 128, 3, 1, 1)]
 
 
 def _case(shape, seed=5):
@@ -97,3 +101,4 @@ def test_conv2d_i8_rejects_bad_calls(vla, torch_cuda):
     with pytest.raises(vla.VlaError) as e:                             # K != k*k*Cin
         vla.conv2d_i8_dev(lin, out, x, 5, 1, 2, small)
     assert e.value.status == vla.VLA_ERR_ARG
+
