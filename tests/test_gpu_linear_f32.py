@@ -4,9 +4,9 @@ head, SmolVLA's flow-matching projections, Octo's token projections).
 
 fp32 sums in another order than the reference, so the bar is a tolerance:
 1e-5 of max(|ref|) against the float64 product and against the reference's
-own dense_linear (oracle/_ref). Shapes cover the split-K kernel (M <= 128)
-and the tiled one (M > 128), K not a multiple of 4 (the unaligned load path),
-and the BASELINE layers.
+own dense_linear (oracle/_ref). Shapes cover the split-K kernel (M <= 128),
+the double-buffered tiled one (M > 128, 16-byte aligned rows) and the scalar
+tiled one (rows not a multiple of 4 floats), and the BASELINE layers.
 """
 
 import numpy as np
@@ -20,6 +20,11 @@ SHAPES = [  # (M, K, N)
     (1, 14, 512), (100, 512, 14), (50, 32, 720), (50, 1440, 720), (50, 720, 32), (1, 960, 960),
     (16, 17, 33), (17, 64, 16), (63, 100, 70), (64, 256, 48), (65, 96, 80), (128, 512, 64),
     (129, 512, 64), (300, 512, 768), (256, 768, 768),
+    # the double-buffered tiled kernel (M > 128, aligned rows): ResNet conv
+    # GEMMs, a ragged K slab (K % 32 != 0), N and M edges, 128-row tiles
+    (19200, 576, 64), (1200, 2304, 256), (513, 100, 130), (4800, 64, 128),
+    # few tiles over a long K: row tiles of the split-K kernel
+    (300, 4608, 512), (300, 2304, 200), (150, 1152, 64),
 ]
 
 

@@ -20,6 +20,8 @@
 #include "act.h"
 #include "common.h"
 
+#include <cstdlib>
+
 #pragma clang fp contract(off)
 
 namespace vla {
@@ -99,6 +101,141 @@ __global__ __launch_bounds__(256) void linear_f32_kernel(float* __restrict__ out
     }
 }
 
+// The tiled form for M > 128 with 16-byte aligned rows (the conv GEMMs of
+// ACT's fp32 backbone and Octo's stems, the big fp32 projections): BM x BN
+// tiles, four waves in a 2 x 2 grid, 32-wide K slabs loaded as float4 runs
+// (coalesced 128-byte row segments) into registers while the previous slab
+// computes from the other LDS buffer. Within a 16-wide k chunk, lane group g
+// feeds k = 4g + t to the t-th of four MFMAs (the same order for A and B, so
+// each MFMA still sums matching products), which lets a lane read its four
+// A (or B) values as one ds_read_b128; LDS rows are padded to BK + 4 floats,
+// so the 16 rows one read touches fall on distinct banks.
+template <int BM, int BN>
+__global__ __launch_bounds__(256) void linear_f32_tiled(float* __restrict__ out, int ldo,
+                                                        const float* __restrict__ x, int ldx,
+                                                        const float* __restrict__ W, int ldw,
+                                                        const float* __restrict__ bias, int M, int N,
+                                                        int K, int act, int accumulate, float alpha) {
+    constexpr int BK = 32, SP = BK + 4;
+    constexpr int TM = BM / 2, TN = BN / 2, FM = TM / 16, FN = TN / 16;
+    constexpr int AV = BM * BK / 4 / 256, BV = BN * BK / 4 / 256;  // float4 loads per thread
+    static_assert(AV >= 1 && BV >= 1 && TM % 16 == 0 && TN % 16 == 0, "tile");
+    __shared__ __attribute__((aligned(16))) float sm[2][(BM + BN) * SP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+
+    // float4 v of a slab: row v / 8, k 4 (v % 8); rows past the matrix clamped
+    const float* ap[AV];
+    const float* bp[BV];
+    int ao[AV], bo[BV], kk[AV > BV ? AV : BV];
+#pragma unroll
+    for (int j = 0; j < AV; j++) {
+        const int v = tid + 256 * j, r = v >> 3, k = (v & 7) * 4;
+        const int m = m0 + r < M ? m0 + r : M - 1;
+        ap[j] = x + (size_t)m * ldx + k;
+        ao[j] = r * SP + k;
+    }
+#pragma unroll
+    for (int j = 0; j < BV; j++) {
+        const int v = tid + 256 * j, r = v >> 3, k = (v & 7) * 4;
+        const int n = n0 + r < N ? n0 + r : N - 1;
+        bp[j] = W + (size_t)n * ldw + k;
+        bo[j] = (BM + r) * SP + k;
+    }
+    const int kq = (tid & 7) * 4;  // this thread's k offset within a slab (same for every load)
+    (void)kk;
+    float4 ra[AV], rb[BV];
+    auto ld4 = [&](const float* p, int k) {
+        if (k + 4 <= K) return *reinterpret_cast<const float4*>(p);
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (k < K) v.x = p[0];
+        if (k + 1 < K) v.y = p[1];
+        if (k + 2 < K) v.z = p[2];
+        return v;  // k + 3 >= K here
+    };
+    auto gload = [&](int k0) {
+#pragma unroll
+        for (int j = 0; j < AV; j++) ra[j] = ld4(ap[j] + k0, k0 + kq);
+#pragma unroll
+        for (int j = 0; j < BV; j++) rb[j] = ld4(bp[j] + k0, k0 + kq);
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < AV; j++) *reinterpret_cast<float4*>(&sm[buf][ao[j]]) = ra[j];
+#pragma unroll
+        for (int j = 0; j < BV; j++) *reinterpret_cast<float4*>(&sm[buf][bo[j]]) = rb[j];
+    };
+
+    v4f acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) acc[i][j] = v4f{0.f, 0.f, 0.f, 0.f};
+    const int r16 = lane & 15, g4 = (lane >> 4) * 4;
+    auto compute = [&](int buf) {
+        const float* s = sm[buf];
+#pragma unroll
+        for (int kc = 0; kc < BK; kc += 16) {
+            float4 af[FM], bf[FN];
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+                af[i] = *reinterpret_cast<const float4*>(s + (wm * TM + i * 16 + r16) * SP + kc + g4);
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+                bf[j] = *reinterpret_cast<const float4*>(s + (BM + wn * TN + j * 16 + r16) * SP + kc + g4);
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int j = 0; j < FN; j++) {
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].x, bf[j].x, acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].y, bf[j].y, acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].z, bf[j].z, acc[i][j], 0, 0, 0);
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[i].w, bf[j].w, acc[i][j], 0, 0, 0);
+                }
+        }
+    };
+
+    const int nk = (K + BK - 1) / BK;
+    gload(0);
+    lstore(0);
+    if (nk > 1) gload(BK);
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt++) {
+        const int buf = kt & 1;
+        compute(buf);
+        if (kt + 1 < nk) {
+            lstore(buf ^ 1);  // slab kt + 1, loaded during this compute
+            if (kt + 2 < nk) gload((kt + 2) * BK);
+        }
+        __syncthreads();
+    }
+
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+        const int n = n0 + wn * TN + j * 16 + r16;
+        if (n >= N) continue;
+        const float b = bias ? bias[n] : 0.0f;
+#pragma unroll
+        for (int i = 0; i < FM; i++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + wm * TM + i * 16 + g4 + r;
+                if (m >= M) continue;
+                float v = acc[i][j][r] + b;
+                switch (act) {
+                case 1: v = act_relu(v); break;
+                case 2: v = act_gelu_tanh(v); break;
+                case 3: v = act_gelu_erf(v); break;
+                case 4: v = act_silu(v); break;
+                default: break;
+                }
+                float* o = out + (size_t)m * ldo + n;
+                *o = accumulate ? fmaf(alpha, v, *o) : v;
+            }
+    }
+}
+
 // M <= 128 (the batch-1 action heads and flow-matching projections): a block
 // owns 16 output columns and every row; its W waves split K in 16-wide steps
 // and read their MFMA operands straight from global memory as float4 runs
@@ -115,13 +252,13 @@ __global__ __launch_bounds__(W * 64) void linear_f32_skinny(float* __restrict__ 
     __shared__ float red[W * FM * 256];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int c = lane & 15, g = lane >> 4;
-    const int n0 = blockIdx.x * 16;
+    const int n0 = blockIdx.x * 16, mb = blockIdx.y * 16 * FM;  // row tile blockIdx.y of 16 * FM rows
     const int n = n0 + c < N ? n0 + c : N - 1;
     const float* brow = Wt + (size_t)n * ldw;
     const float* arow[FM];
 #pragma unroll
     for (int i = 0; i < FM; i++) {
-        const int m = 16 * i + c < M ? 16 * i + c : M - 1;
+        const int m = mb + 16 * i + c < M ? mb + 16 * i + c : M - 1;
         arow[i] = x + (size_t)m * ldx;
     }
     auto load4 = [&](const float* row, int k) {
@@ -161,7 +298,7 @@ __global__ __launch_bounds__(W * 64) void linear_f32_skinny(float* __restrict__ 
 #pragma unroll
         for (int w = 0; w < W; w++) v += red[w * FM * 256 + e];
         const int l = e & 63, r = (e >> 6) & 3, i = e >> 8;
-        const int m = 16 * i + 4 * (l >> 4) + r, nn = n0 + (l & 15);
+        const int m = mb + 16 * i + 4 * (l >> 4) + r, nn = n0 + (l & 15);
         if (m >= M || nn >= N) continue;
         v = v + (bias ? bias[nn] : 0.0f);
         switch (act) {
@@ -208,6 +345,12 @@ void launch_skinny(float* out, int ldo, const float* x, int ldx, const float* W,
     }
 }
 
+// VLA_F32_TILED=0 keeps the LDS-scalar kernel (A/B comparisons)
+bool env_off_f32tiled() {
+    const char* e = std::getenv("VLA_F32_TILED");
+    return e && e[0] == '0' && e[1] == '\0';
+}
+
 }  // namespace
 
 void launch_linear_f32(float* out, int ldo, const float* x, int ldx, const float* W, int ldw,
@@ -222,6 +365,32 @@ void launch_linear_f32(float* out, int ldo, const float* x, int ldx, const float
         const bool vec = ldx % 4 == 0 && ldw % 4 == 0 && aligned(x, 16) && aligned(W, 16);
         if (vec) launch_skinny<true>(out, ldo, x, ldx, W, ldw, bias, M, N, K, act, accumulate, alpha, st);
         else launch_skinny<false>(out, ldo, x, ldx, W, ldw, bias, M, N, K, act, accumulate, alpha, st);
+        VLA_LAUNCH_CHECK();
+        return;
+    }
+    if (ldx % 4 == 0 && ldw % 4 == 0 && aligned(x, 16) && aligned(W, 16) && !env_off_f32tiled()) {
+        const long t64 = (long)((M + 63) / 64) * ((N + 63) / 64);
+        if (t64 < 128 && K >= 1024) {
+            // few tiles over a long K (ResNet's last stages): the split-K form,
+            // 64-row x 16-column blocks whose 8 waves share K, so the chain of
+            // dependent loads per wave is an eighth of K
+            const dim3 grid((N + 15) / 16, (M + 63) / 64);
+            linear_f32_skinny<4, 8, true><<<grid, 512, 0, st>>>(out, ldo, x, ldx, W, ldw, bias, M, N, K, act,
+                                                                 accumulate, alpha);
+            VLA_LAUNCH_CHECK();
+            return;
+        }
+        // 128 x 64 tiles when they still give every CU work, else 64 x 64
+        const long t128 = (long)((M + 127) / 128) * ((N + 63) / 64);
+        if (t128 >= 256) {
+            const dim3 grid((N + 63) / 64, (M + 127) / 128);
+            linear_f32_tiled<128, 64><<<grid, 256, 0, st>>>(out, ldo, x, ldx, W, ldw, bias, M, N, K, act,
+                                                            accumulate, alpha);
+        } else {
+            const dim3 grid((N + 63) / 64, (M + 63) / 64);
+            linear_f32_tiled<64, 64><<<grid, 256, 0, st>>>(out, ldo, x, ldx, W, ldw, bias, M, N, K, act,
+                                                           accumulate, alpha);
+        }
         VLA_LAUNCH_CHECK();
         return;
     }
