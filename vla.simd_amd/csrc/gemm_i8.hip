@@ -34,7 +34,8 @@
 //                   contiguous run of tiles, grouped 8 tile-rows deep, which
 //                   keeps the A and B panels a run shares in that XCD's L2.
 //                   The epilogue stores straight from the accumulators.
-//   gemm_i8_lds     long K (> 1024), aligned rows. Operand slabs go straight
+//   gemm_i8_lds     long K (> 1024), and large outputs over 512..1024 bytes
+//                   of K (128 x 128 tiles), aligned rows. Operand slabs go straight
 //                   from global memory into LDS (global_load_lds_dwordx4, no
 //                   VGPR staging) with S-1 slabs in flight; LDS rows are
 //                   XOR-swizzled by 16-byte chunk instead of padded; the
@@ -1213,7 +1214,8 @@ struct Tile {
 const Tile kTiles[] = {{128, 128, 64, 0},       {64, 128, 64, 0},         {64, 64, 64, 0},
                        {64, 64, 128, 0},        {64, 128, 128, 0},
                        {128, 128, 64, 4},       {64, 128, 64, 4},         {256, 128, 128, 3, 8},
-                       {256, 256, 128, 2, 8},   {256, 128, 128, 3, 8, true}, {256, 256, 128, 2, 8, true}};
+                       {256, 256, 128, 2, 8},   {256, 128, 128, 3, 8, true}, {256, 256, 128, 2, 8, true},
+                       {128, 128, 128, 2}};
 
 Tile pick_tile(int M, int N, int K) {
     const char* env = std::getenv("VLA_HIP_GEMM_TILE");
@@ -1246,6 +1248,13 @@ Tile pick_tile(int M, int N, int K) {
     // barriers and twice the MFMA work per slab (ACT 0.409 -> 0.402 ms, Octo
     // 1.159 -> 1.141 ms per forward)
     const Tile small{64, 64, K >= 256 ? 128 : 64, 0};
+    // Large outputs over short K (M, N >= 1024, 512 <= K <= 1024): the
+    // LDS-DMA 128 x 128 tile with 128-byte slabs, two stages (64 KiB, two
+    // blocks per CU) and non-temporal stores; interleaved repeats on MI355X:
+    // 8192 x 768 x 3072 46.6 -> 37.0 us, 8192 x 960 x 2560 47.5 -> 38.3,
+    // 2048 x 768 x 3072 13.2 -> 11.5, 2048 x 512 x 3200 12.0 -> 9.8; at 658
+    // rows and at 1000^3 the register-staged tiles stay ahead.
+    if (K <= 1024 && K >= 512 && M >= 1024 && N >= 1024) return {128, 128, 128, 2};
     if (K <= 1024) return tiles(64, 128) >= 2 * kCUs ? Tile{64, 128, 64, 0} : small;
     if (tiles(256, 256) >= 2 * kCUs) return {256, 256, 128, 2, 8, true};
     if (tiles(256, 128) >= kCUs) return {256, 128, 128, 3, 8, true};
@@ -1309,7 +1318,8 @@ void dispatch_tile(const Tile& t, const GemmArgs& a, hipStream_t st) {
         return;
     }
     if (t.stages) {
-        if (t.bm == 128) run_lds<128, 128, 64, 4>(a, st);
+        if (t.bm == 128 && t.bk == 128) run_lds<128, 128, 128, 2>(a, st);
+        else if (t.bm == 128) run_lds<128, 128, 64, 4>(a, st);
         else run_lds<64, 128, 64, 4>(a, st);
         return;
     }
