@@ -50,6 +50,29 @@ __device__ __forceinline__ v4f mfma_f32(float a, float b, v4f c) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// max / sum of x over the lanes l, l^16, l^32, l^48 (the four 16-lane rows of
+// a wave) with gfx950's row-swap permutes, VALU ops instead of LDS round trips.
+// permlane16_swap(x, x) returns, in every lane, the values of the lane pair
+// {l, l^16} (one from the even row, one from the odd row); permlane32_swap the
+// pair {l, l^32}. The sum adds each pair in either order, which is the same
+// float: the results equal those of x op shfl_xor(x, 16), then 32.
+__device__ __forceinline__ float rows_max(float x) {
+    const unsigned u = __float_as_uint(x);
+    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const unsigned v = __float_as_uint(y);
+    const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float rows_sum(float x) {
+    const unsigned u = __float_as_uint(x);
+    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const unsigned v = __float_as_uint(y);
+    const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // Orders this wave's LDS accesses (its writes before other lanes' reads) with
 // no block barrier.
 __device__ __forceinline__ void wave_lds_sync() {
@@ -92,6 +115,7 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
     const int HD = a.head_dim;
     const int qi = blockIdx.x * 16 + c;
     const bool qok = qi < a.seq_q;
+    const bool qfull = blockIdx.x * 16 + 16 <= a.seq_q;  // every query of the tile exists
     float* Ks = smem + wave * C::TILE;
     float* Vs = Ks + KT * SK;
 
@@ -254,8 +278,19 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
             }
         }
 
-        // scale, mask, tile max
+        // scale, mask, tile max; a whole tile of keys for a whole query tile
+        // with no mask (wave-uniform) only scales
         float mt = -INFINITY;
+        if (MKC == 0 && mk == 0 && qfull && kv0 + KT <= kv_end) {
+#pragma unroll
+            for (int kt = 0; kt < NT; kt++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float x = sacc[kt][r] * scale;
+                    sacc[kt][r] = x;
+                    mt = fmaxf(mt, x);
+                }
+        } else
 #pragma unroll
         for (int kt = 0; kt < NT; kt++)
 #pragma unroll
@@ -276,8 +311,7 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
                 sacc[kt][r] = x;
                 mt = fmaxf(mt, x);
             }
-        mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
-        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        mt = rows_max(mt);
         const float mnew = fmaxf(m, mt);
 
         float alpha = 1.0f;
@@ -316,8 +350,7 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
         wave_lds_sync();  // this tile's reads are done before the next lstore
     }
 
-    lsum += __shfl_xor(lsum, 16, 64);
-    lsum += __shfl_xor(lsum, 32, 64);
+    lsum = rows_sum(lsum);
 
     // merge the waves' partial states: m*, then sum_w e^(m_w - m*) (l_w, O_w)
     __syncthreads();

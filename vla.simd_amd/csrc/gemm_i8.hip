@@ -1248,13 +1248,15 @@ Tile pick_tile(int M, int N, int K) {
     // barriers and twice the MFMA work per slab (ACT 0.409 -> 0.402 ms, Octo
     // 1.159 -> 1.141 ms per forward)
     const Tile small{64, 64, K >= 256 ? 128 : 64, 0};
-    // Large outputs over short K (M, N >= 1024, 512 <= K <= 1024): the
-    // LDS-DMA 128 x 128 tile with 128-byte slabs, two stages (64 KiB, two
-    // blocks per CU) and non-temporal stores; interleaved repeats on MI355X:
-    // 8192 x 768 x 3072 46.6 -> 37.0 us, 8192 x 960 x 2560 47.5 -> 38.3,
-    // 2048 x 768 x 3072 13.2 -> 11.5, 2048 x 512 x 3200 12.0 -> 9.8; at 658
-    // rows and at 1000^3 the register-staged tiles stay ahead.
-    if (K <= 1024 && K >= 512 && M >= 1024 && N >= 1024) return {128, 128, 128, 2};
+    // Large outputs over short K (M, N >= 1024, 512 <= K <= 1024, at least
+    // one 128 x 128 tile per CU): the LDS-DMA 128 x 128 tile with 128-byte
+    // slabs, two stages (64 KiB, two blocks per CU) and non-temporal stores;
+    // interleaved repeats on MI355X: 8192 x 768 x 3072 46.6 -> 37.0 us,
+    // 8192 x 960 x 2560 47.5 -> 38.3, 2048 x 768 x 3072 13.2 -> 11.5,
+    // 2048 x 512 x 3200 12.0 -> 9.8. With fewer tiles than CUs (SigLIP's
+    // 1024-row layers), at 658 rows and at 1000^3 the register-staged tiles
+    // stay ahead.
+    if (K <= 1024 && K >= 512 && M >= 1024 && N >= 1024 && tiles(128, 128) >= kCUs) return {128, 128, 128, 2};
     if (K <= 1024) return tiles(64, 128) >= 2 * kCUs ? Tile{64, 128, 64, 0} : small;
     if (tiles(256, 256) >= 2 * kCUs) return {256, 256, 128, 2, 8, true};
     if (tiles(256, 128) >= kCUs) return {256, 128, 128, 3, 8, true};
