@@ -52,6 +52,25 @@ __global__ __launch_bounds__(256) void im2col_f32_kernel(float* __restrict__ col
     }
 }
 
+// The same columns when Cin % 4 == 0 (every layer after a stem): one thread
+// copies 4 channels of one tap as a float4 (they never straddle two taps),
+// with 32-bit index math; values identical to im2col_f32_kernel's.
+__global__ __launch_bounds__(256) void im2col_f32x4_kernel(float* __restrict__ col, int ldc,
+                                                           const float* __restrict__ x, int H, int Wd, int Cin, int k,
+                                                           int stride, int pad, int Wout, int K4, int total) {
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+        const int p = e / K4, r = 4 * (e - p * K4);
+        const int t = r / Cin, ci = r - t * Cin;
+        const int ky = t / k, kx = t - ky * k;
+        const int oy = p / Wout, ox = p - oy * Wout;
+        const int iy = oy * stride - pad + ky, ix = ox * stride - pad + kx;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (iy >= 0 && iy < H && ix >= 0 && ix < Wd)
+            v = *reinterpret_cast<const float4*>(x + ((size_t)iy * Wd + ix) * Cin + ci);
+        *reinterpret_cast<float4*>(col + (size_t)p * ldc + r) = v;
+    }
+}
+
 // maxpool2d_relu (src/hal/common/conv.cpp:192-224): padded taps count as -inf,
 // then the folded ReLU (!(v > 0) -> 0).
 __global__ __launch_bounds__(256) void maxpool_relu_kernel(float* __restrict__ out, const float* __restrict__ x, int H,
@@ -126,7 +145,14 @@ void launch_im2col_f32(float* col, int ldc, const float* x, int H, int Wd, int C
     const int64_t K = (int64_t)k * k * Cin;
     VLA_REQUIRE(ldc >= K && col && x, "im2col: bad arguments");
     const int64_t total = (int64_t)Hout * Wout * K;
-    im2col_f32_kernel<<<grid_for(total), 256, 0, st>>>(col, ldc, x, H, Wd, Cin, k, stride, pad, Wout, total);
+    if (Cin % 4 == 0 && ldc % 4 == 0 && total / 4 < INT32_MAX && (reinterpret_cast<uintptr_t>(x) & 15) == 0 &&
+        (reinterpret_cast<uintptr_t>(col) & 15) == 0) {
+        const int64_t t4 = total / 4;
+        im2col_f32x4_kernel<<<grid_for(t4), 256, 0, st>>>(col, ldc, x, H, Wd, Cin, k, stride, pad, Wout, (int)(K / 4),
+                                                          (int)t4);
+    } else {
+        im2col_f32_kernel<<<grid_for(total), 256, 0, st>>>(col, ldc, x, H, Wd, Cin, k, stride, pad, Wout, total);
+    }
     VLA_LAUNCH_CHECK();
 }
 
