@@ -212,3 +212,26 @@ def test_act_model_full_size(vla, env, tmp_path):
     err = _rel(got, ref)
     print(f"act model 480x640: action rel err {err:.3e} (bar {bar:.3e}), graph nodes {m.graph_nodes}", flush=True)
     assert err <= bar
+
+
+def test_implicit_conv_gemm_bit_exact(vla, env, tmp_path):
+    """The fp32 convolutions as implicit GEMMs (each patch gathered by the
+    GEMM's own A loads from the NHWC map) give the im2col + GEMM features and
+    actions bit for bit: the same products in the same order. BASELINE's
+    480 x 640 ResNet-18, whose layers with Cin % 32 == 0 and a tiled GEMM take
+    the implicit form; VLA_CONV_F32_IMPLICIT=0 keeps im2col."""
+    ck = _ck()
+    c = ck.ACT_MODEL_BASE
+    d = ck.write_act_model(str(tmp_path / "act_full"), c)
+    env(ACT_INT8=31)
+    images, state = ck.act_model_inputs(c)
+    os.environ["VLA_CONV_F32_IMPLICIT"] = "0"
+    try:
+        m0 = vla.ActModel(d)
+        f0, a0 = m0.encode(images), m0.predict(images, state)
+    finally:
+        del os.environ["VLA_CONV_F32_IMPLICIT"]
+    m1 = vla.ActModel(d)
+    f1, a1 = m1.encode(images), m1.predict(images, state)
+    assert f1.tobytes() == f0.tobytes(), f"features differ (rel {_rel(f1, f0):.3e})"
+    assert a1.tobytes() == a0.tobytes()

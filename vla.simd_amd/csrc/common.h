@@ -269,9 +269,22 @@ void launch_rtc_step(float* x, const float* v, const float* prev, const float* w
 
 // linear_f32.hip: out[m, n] = act(x[m,:] . W[n,:] + bias[n]); accumulate != 0
 // adds it as fmaf(alpha, v, out[m, n]). act as vla_act, plus 4 = silu.
+// out [Hout*Wout, Cout] = the k x k conv of the NHWC map x with W [Cout][k*k*Cin]
+// (im2col's column order) as one implicit GEMM; false when the shape or
+// alignment does not suit it (the caller then runs im2col + launch_linear_f32,
+// which gives the same values)
+bool launch_conv_f32_implicit(float* out, const float* x, int H, int Wd, int Cin, int k, int stride, int pad,
+                              int Hout, int Wout, const float* W, const float* bias, int Cout, int act,
+                              hipStream_t st, float* work = nullptr, size_t work_floats = 0);
+// floats of npix im2col rows of K columns (rows padded to 4 floats), rounded up
+// to 64 floats so what follows stays 256-byte aligned
+inline size_t col_rows_floats(size_t npix, int K) { return (npix * (size_t)((K + 3) & ~3) + 63) / 64 * 64; }
+// floats of the split-K workspace launch_linear_f32 (and the implicit conv)
+// use for this shape when one is passed; 0 when the shape is not split
+size_t linear_f32_split_floats(int M, int N, int K);
 void launch_linear_f32(float* out, int ldo, const float* x, int ldx, const float* W, int ldw,
                        const float* bias, int M, int N, int K, int act, int accumulate, float alpha,
-                       hipStream_t st);
+                       hipStream_t st, float* work = nullptr, size_t work_floats = 0);
 
 // runtime.cpp
 hipStream_t library_stream();  // stream of the host-pointer forms

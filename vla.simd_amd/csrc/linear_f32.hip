@@ -110,12 +110,22 @@ __global__ __launch_bounds__(256) void linear_f32_kernel(float* __restrict__ out
 // each MFMA still sums matching products), which lets a lane read its four
 // A (or B) values as one ds_read_b128; LDS rows are padded to BK + 4 floats,
 // so the 16 rows one read touches fall on distinct banks.
-template <int BM, int BN>
+// CONV: x is an NHWC map and row m of A is output pixel m's k x k patch,
+// column (ky * k + kx) * Cin + ci (im2col's order), gathered by the A loads
+// themselves: with Cin % 32 == 0 a thread's float4 of a 32-wide slab always
+// lies in one tap, and its tap advances by 32 channels per slab. Same
+// products in the same order as im2col + this kernel; no column matrix.
+struct ConvGeom {
+    int H, Wd, Cin, k, stride, pad, Wout;
+};
+
+template <int BM, int BN, bool CONV = false>
 __global__ __launch_bounds__(256) void linear_f32_tiled(float* __restrict__ out, int ldo,
                                                         const float* __restrict__ x, int ldx,
                                                         const float* __restrict__ W, int ldw,
                                                         const float* __restrict__ bias, int M, int N,
-                                                        int K, int act, int accumulate, float alpha) {
+                                                        int K, int act, int accumulate, float alpha,
+                                                        ConvGeom cg, float* __restrict__ part, int kchunk) {
     constexpr int BK = 32, SP = BK + 4;
     constexpr int TM = BM / 2, TN = BN / 2, FM = TM / 16, FN = TN / 16;
     constexpr int AV = BM * BK / 4 / 256, BV = BN * BK / 4 / 256;  // float4 loads per thread
@@ -124,23 +134,35 @@ __global__ __launch_bounds__(256) void linear_f32_tiled(float* __restrict__ out,
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int wm = wave >> 1, wn = wave & 1;
     const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    // split K (part != null): chunk blockIdx.z of kchunk columns, raw sums into
+    // its slice of part; K becomes the chunk's length
+    const int kbeg = part ? blockIdx.z * kchunk : 0;
+    if (part) K = K - kbeg < kchunk ? K - kbeg : kchunk;
 
     // float4 v of a slab: row v / 8, k 4 (v % 8); rows past the matrix clamped
     const float* ap[AV];
     const float* bp[BV];
     int ao[AV], bo[BV], kk[AV > BV ? AV : BV];
+    int iy0[AV], ix0[AV];  // CONV: the patch origin of each loaded row
 #pragma unroll
     for (int j = 0; j < AV; j++) {
         const int v = tid + 256 * j, r = v >> 3, k = (v & 7) * 4;
         const int m = m0 + r < M ? m0 + r : M - 1;
-        ap[j] = x + (size_t)m * ldx + k;
+        if (CONV) {
+            const int oy = m / cg.Wout, ox = m - oy * cg.Wout;
+            iy0[j] = oy * cg.stride - cg.pad;
+            ix0[j] = ox * cg.stride - cg.pad;
+            ap[j] = x;
+        } else {
+            ap[j] = x + (size_t)m * ldx + kbeg + k;
+        }
         ao[j] = r * SP + k;
     }
 #pragma unroll
     for (int j = 0; j < BV; j++) {
         const int v = tid + 256 * j, r = v >> 3, k = (v & 7) * 4;
         const int n = n0 + r < N ? n0 + r : N - 1;
-        bp[j] = W + (size_t)n * ldw + k;
+        bp[j] = W + (size_t)n * ldw + kbeg + k;
         bo[j] = (BM + r) * SP + k;
     }
     const int kq = (tid & 7) * 4;  // this thread's k offset within a slab (same for every load)
@@ -154,9 +176,35 @@ __global__ __launch_bounds__(256) void linear_f32_tiled(float* __restrict__ out,
         if (k + 2 < K) v.z = p[2];
         return v;  // k + 3 >= K here
     };
+    // CONV: the tap of this thread's next A slab (kbeg is a multiple of 32)
+    int ci = kq, kx = 0, ky = 0;
+    if (CONV && kbeg) {
+        const int t = kbeg / cg.Cin;
+        ci = kbeg - t * cg.Cin + kq;
+        ky = t / cg.k;
+        kx = t - ky * cg.k;
+    }
     auto gload = [&](int k0) {
+        if (CONV) {  // called for k0 = 0, BK, 2 BK, ... in order
 #pragma unroll
-        for (int j = 0; j < AV; j++) ra[j] = ld4(ap[j] + k0, k0 + kq);
+            for (int j = 0; j < AV; j++) {
+                const int iy = iy0[j] + ky, ix = ix0[j] + kx;
+                ra[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+                if (iy >= 0 && iy < cg.H && ix >= 0 && ix < cg.Wd)
+                    ra[j] = *reinterpret_cast<const float4*>(x + ((size_t)iy * cg.Wd + ix) * cg.Cin + ci);
+            }
+            ci += BK;
+            if (ci >= cg.Cin) {
+                ci -= cg.Cin;
+                if (++kx == cg.k) {
+                    kx = 0;
+                    ++ky;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < AV; j++) ra[j] = ld4(ap[j] + k0, k0 + kq);
+        }
 #pragma unroll
         for (int j = 0; j < BV; j++) rb[j] = ld4(bp[j] + k0, k0 + kq);
     };
@@ -211,6 +259,22 @@ __global__ __launch_bounds__(256) void linear_f32_tiled(float* __restrict__ out,
         __syncthreads();
     }
 
+    if (part) {
+        float* pz = part + (size_t)blockIdx.z * M * N;
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+            const int n = n0 + wn * TN + j * 16 + r16;
+            if (n >= N) continue;
+#pragma unroll
+            for (int i = 0; i < FM; i++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int m = m0 + wm * TM + i * 16 + g4 + r;
+                    if (m < M) pz[(size_t)m * N + n] = acc[i][j][r];
+                }
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < FN; j++) {
         const int n = n0 + wn * TN + j * 16 + r16;
@@ -345,6 +409,69 @@ void launch_skinny(float* out, int ldo, const float* x, int ldx, const float* W,
     }
 }
 
+// The split-K partial sums of linear_f32_tiled: out = act(sum_z part[z] + bias)
+// with the chunks added in z order, then the epilogue of the unsplit kernel.
+__global__ __launch_bounds__(256) void linear_f32_split_reduce(float* __restrict__ out, int ldo,
+                                                               const float* __restrict__ part, int S, int M, int N,
+                                                               const float* __restrict__ bias, int act,
+                                                               int accumulate, float alpha) {
+    const int64_t MN = (int64_t)M * N;
+    for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < MN; e += (int64_t)gridDim.x * blockDim.x) {
+        float v = part[e];
+        for (int z = 1; z < S; z++) v += part[z * MN + e];
+        const int m = (int)(e / N), n = (int)(e - (int64_t)m * N);
+        v = v + (bias ? bias[n] : 0.0f);
+        switch (act) {
+        case 1: v = act_relu(v); break;
+        case 2: v = act_gelu_tanh(v); break;
+        case 3: v = act_gelu_erf(v); break;
+        case 4: v = act_silu(v); break;
+        default: break;
+        }
+        float* o = out + (size_t)m * ldo + n;
+        *o = accumulate ? fmaf(alpha, v, *o) : v;
+    }
+}
+
+constexpr int kCUs = 256;  // MI355X compute units
+
+// Split-K plan for M > 128 over K >= 1024 when 64 x 64 tiles number < 128
+// (ResNet's last stages): S chunks of K (multiples of 32, >= 256) so that
+// S x tiles reaches about two blocks per CU, S <= 8.
+struct F32Split {
+    int S = 1, kchunk = 0;
+};
+F32Split f32_split_plan(int M, int N, int K) {
+    F32Split p;
+    const long t64 = (long)((M + 63) / 64) * ((N + 63) / 64);
+    if (M <= 128 || t64 >= 128 || K < 1024) return p;
+    int S = (int)((2 * kCUs + t64 - 1) / t64);
+    S = S < 8 ? S : 8;
+    int kc = ((K + S - 1) / S + 31) / 32 * 32;
+    kc = kc > 256 ? kc : 256;
+    p.S = (K + kc - 1) / kc;
+    p.kchunk = kc;
+    if (p.S < 2) p = F32Split{};
+    return p;
+}
+
+void launch_f32_split(float* out, int ldo, const float* x, int ldx, const float* W, int ldw, const float* bias,
+                      int M, int N, int K, int act, int accumulate, float alpha, const ConvGeom& cg, bool conv,
+                      const F32Split& p, float* part, hipStream_t st) {
+    const dim3 grid((N + 63) / 64, (M + 63) / 64, p.S);
+    if (conv)
+        linear_f32_tiled<64, 64, true><<<grid, 256, 0, st>>>(out, ldo, x, ldx, W, ldw, bias, M, N, K, 0, 0, 1.0f, cg,
+                                                             part, p.kchunk);
+    else
+        linear_f32_tiled<64, 64><<<grid, 256, 0, st>>>(out, ldo, x, ldx, W, ldw, bias, M, N, K, 0, 0, 1.0f, cg, part,
+                                                       p.kchunk);
+    VLA_LAUNCH_CHECK();
+    const int64_t MN = (int64_t)M * N;
+    const int blocks = (int)((MN + 255) / 256 < 4096 ? (MN + 255) / 256 : 4096);
+    linear_f32_split_reduce<<<blocks, 256, 0, st>>>(out, ldo, part, p.S, M, N, bias, act, accumulate, alpha);
+    VLA_LAUNCH_CHECK();
+}
+
 // VLA_F32_TILED=0 keeps the LDS-scalar kernel (A/B comparisons)
 bool env_off_f32tiled() {
     const char* e = std::getenv("VLA_F32_TILED");
@@ -353,9 +480,14 @@ bool env_off_f32tiled() {
 
 }  // namespace
 
+size_t linear_f32_split_floats(int M, int N, int K) {
+    const F32Split p = f32_split_plan(M, N, K);
+    return p.S > 1 ? (size_t)p.S * M * N : 0;
+}
+
 void launch_linear_f32(float* out, int ldo, const float* x, int ldx, const float* W, int ldw,
                        const float* bias, int M, int N, int K, int act, int accumulate, float alpha,
-                       hipStream_t st) {
+                       hipStream_t st, float* work, size_t work_floats) {
     VLA_REQUIRE(M >= 0 && N > 0 && K > 0, "linear_f32: need M >= 0, N > 0, K > 0");
     VLA_REQUIRE(ldx >= K && ldw >= K && ldo >= N, "linear_f32: row strides shorter than the rows");
     VLA_REQUIRE(out && x && W, "linear_f32: null buffer");
@@ -370,6 +502,13 @@ void launch_linear_f32(float* out, int ldo, const float* x, int ldx, const float
     }
     if (ldx % 4 == 0 && ldw % 4 == 0 && aligned(x, 16) && aligned(W, 16) && !env_off_f32tiled()) {
         const long t64 = (long)((M + 63) / 64) * ((N + 63) / 64);
+        const F32Split sp = f32_split_plan(M, N, K);
+        if (sp.S > 1 && work && work_floats >= (size_t)sp.S * M * N && aligned(work, 16)) {
+            // few tiles over a long K with a workspace: 64 x 64 tiles split over K
+            launch_f32_split(out, ldo, x, ldx, W, ldw, bias, M, N, K, act, accumulate, alpha, ConvGeom{}, false, sp,
+                             work, st);
+            return;
+        }
         if (t64 < 128 && K >= 1024) {
             // few tiles over a long K (ResNet's last stages): the split-K form,
             // 64-row x 16-column blocks whose 8 waves share K, so the chain of
@@ -385,11 +524,11 @@ void launch_linear_f32(float* out, int ldo, const float* x, int ldx, const float
         if (t128 >= 256) {
             const dim3 grid((N + 63) / 64, (M + 127) / 128);
             linear_f32_tiled<128, 64><<<grid, 256, 0, st>>>(out, ldo, x, ldx, W, ldw, bias, M, N, K, act,
-                                                            accumulate, alpha);
+                                                            accumulate, alpha, ConvGeom{}, nullptr, 0);
         } else {
             const dim3 grid((N + 63) / 64, (M + 63) / 64);
             linear_f32_tiled<64, 64><<<grid, 256, 0, st>>>(out, ldo, x, ldx, W, ldw, bias, M, N, K, act,
-                                                           accumulate, alpha);
+                                                           accumulate, alpha, ConvGeom{}, nullptr, 0);
         }
         VLA_LAUNCH_CHECK();
         return;
@@ -406,6 +545,46 @@ void launch_linear_f32(float* out, int ldo, const float* x, int ldx, const float
                                                         accumulate, alpha);
     }
     VLA_LAUNCH_CHECK();
+}
+
+bool launch_conv_f32_implicit(float* out, const float* x, int H, int Wd, int Cin, int k, int stride, int pad,
+                              int Hout, int Wout, const float* W, const float* bias, int Cout, int act,
+                              hipStream_t st, float* work, size_t work_floats) {
+    const char* e = std::getenv("VLA_CONV_F32_IMPLICIT");  // 0: im2col + GEMM (A/B runs)
+    if (e && e[0] == '0' && e[1] == '\0') return false;
+    VLA_REQUIRE(out && x && W && H > 0 && Wd > 0 && Cin > 0 && k > 0 && stride > 0 && pad >= 0 && Cout > 0 &&
+                    Hout > 0 && Wout > 0 && act >= 0 && act <= 4,
+                "conv_f32: bad arguments");
+    const int64_t K64 = (int64_t)k * k * Cin, M64 = (int64_t)Hout * Wout;
+    // the output pixels' patches stay inside the padded input
+    VLA_REQUIRE((int64_t)(Hout - 1) * stride + k <= (int64_t)H + 2 * pad &&
+                    (int64_t)(Wout - 1) * stride + k <= (int64_t)Wd + 2 * pad,
+                "conv_f32: output larger than the padded input allows");
+    if (Cin % 32 || K64 > INT32_MAX || M64 > INT32_MAX || (int64_t)H * Wd * Cin > INT32_MAX) return false;
+    if (!aligned(x, 16) || !aligned(W, 16) || env_off_f32tiled()) return false;
+    const int M = (int)M64, K = (int)K64, N = Cout;
+    if (M <= 128) return false;
+    const long t64 = (long)((M + 63) / 64) * ((N + 63) / 64);
+    const ConvGeom cg{H, Wd, Cin, k, stride, pad, Wout};
+    const F32Split sp = f32_split_plan(M, N, K);
+    if (sp.S > 1) {  // as launch_linear_f32: split over K with a workspace, else not here
+        if (!(work && work_floats >= (size_t)sp.S * M * N && aligned(work, 16))) return false;
+        launch_f32_split(out, N, x, K, W, K, bias, M, N, K, act, 0, 1.0f, cg, true, sp, work, st);
+        return true;
+    }
+    if (t64 < 128 && K >= 1024) return false;  // the skinny route of launch_linear_f32
+    const long t128 = (long)((M + 127) / 128) * ((N + 63) / 64);
+    if (t128 >= 256) {
+        const dim3 grid((N + 63) / 64, (M + 127) / 128);
+        linear_f32_tiled<128, 64, true><<<grid, 256, 0, st>>>(out, N, x, K, W, K, bias, M, N, K, act, 0, 1.0f, cg,
+                                                              nullptr, 0);
+    } else {
+        const dim3 grid((N + 63) / 64, (M + 63) / 64);
+        linear_f32_tiled<64, 64, true><<<grid, 256, 0, st>>>(out, N, x, K, W, K, bias, M, N, K, act, 0, 1.0f, cg,
+                                                             nullptr, 0);
+    }
+    VLA_LAUNCH_CHECK();
+    return true;
 }
 
 }  // namespace hip

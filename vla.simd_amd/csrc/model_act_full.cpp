@@ -179,10 +179,12 @@ ActModel::ActModel(const std::string& dir) {
     const int ph = h, pw = w;
     size_t map_max = (size_t)h1 * w1 * stem_out, col_max = 0;
     map_max = std::max(map_max, (size_t)ph * pw * stem_out);
+    // the im2col rows, then (64-float aligned) the split-K sums of the GEMM
     auto col_need = [&](const Conv& c, int H, int W) {
-        if (c.k == 1 && c.stride == 1 && c.pad == 0) return;
-        const size_t npix = (size_t)conv_out(H, c.k, c.stride, c.pad) * conv_out(W, c.k, c.stride, c.pad);
-        col_max = std::max(col_max, npix * (size_t)((c.k * c.k * c.cin + 3) & ~3));
+        const int Ho = conv_out(H, c.k, c.stride, c.pad), Wo = conv_out(W, c.k, c.stride, c.pad);
+        const size_t npix = (size_t)Ho * Wo, K = (size_t)c.k * c.k * c.cin;
+        const size_t rows = c.k == 1 && c.stride == 1 && c.pad == 0 ? 0 : col_rows_floats(npix, (int)K);
+        col_max = std::max(col_max, rows + linear_f32_split_floats(Ho * Wo, c.cout, (int)K));
     };
     col_need(stem_, img_h_, img_w_);
     for (const Block& blk : blocks_) {
@@ -264,6 +266,7 @@ ActModel::ActModel(const std::string& dir) {
     c_ = A_.alloc<float>(map_max);
     res_ = A_.alloc<float>(map_max);
     col_ = A_.alloc<float>(col_max ? col_max : 4);
+    col_floats_ = col_max;
     feats_ = A_.alloc<float>((size_t)n_cams_ * fh_ * fw_ * feat_ch_);
     state_n_ = A_.alloc<float>(sd);
     act_n_ = A_.alloc<float>((size_t)tf_->chunk() * ad);
@@ -322,12 +325,21 @@ void ActModel::conv(const Conv& c, const float* x, int H, int W, float* out, boo
     const int K = c.k * c.k * c.cin;
     const float* rows = x;
     int ldx = K;
-    if (!(c.k == 1 && c.stride == 1 && c.pad == 0)) {
+    const bool plain = c.k == 1 && c.stride == 1 && c.pad == 0;  // the map is already the GEMM's A
+    // split-K sums after the im2col rows (the implicit form leaves those unused)
+    const size_t rows_f = plain ? 0 : col_rows_floats((size_t)Ho * Wo, K);
+    float* part = col_ + rows_f;
+    const size_t part_f = col_floats_ - rows_f;
+    if (!plain && launch_conv_f32_implicit(out, x, H, W, c.cin, c.k, c.stride, c.pad, Ho, Wo, c.W, c.b, c.cout,
+                                           relu ? 1 : 0, st, part, part_f))
+        return;
+    if (!plain) {
         ldx = (K + 3) & ~3;
         launch_im2col_f32(col_, ldx, x, H, W, c.cin, c.k, c.stride, c.pad, Ho, Wo, st);
         rows = col_;
     }
-    launch_linear_f32(out, c.cout, rows, ldx, c.W, K, c.b, Ho * Wo, c.cout, K, relu ? 1 : 0, 0, 1.0f, st);
+    launch_linear_f32(out, c.cout, rows, ldx, c.W, K, c.b, Ho * Wo, c.cout, K, relu ? 1 : 0, 0, 1.0f, st, part,
+                      part_f);
 }
 
 // ActModel::encode_view for every camera (act_model.cpp:106-124) and

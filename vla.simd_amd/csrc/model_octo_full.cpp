@@ -254,7 +254,9 @@ OctoStem::OctoStem(const CkptFiles& files, const std::string& name, int int8_mas
         } else {
             L.W_ = A_.upload(Wt, (size_t)L.cout * K);
             L.b = A_.upload(b, L.cout);
-            col_max = std::max(col_max, (size_t)L.Ho * L.Wo * kpad4(K));
+            // the im2col rows, then the GEMM's split-K sums
+            col_max = std::max(col_max, col_rows_floats((size_t)L.Ho * L.Wo, K) +
+                                            linear_f32_split_floats(L.Ho * L.Wo, L.cout, K));
         }
         L.gs = A_.upload(a.take(L.cout), L.cout);
         L.gb = A_.upload(a.take(L.cout), L.cout);
@@ -274,6 +276,7 @@ OctoStem::OctoStem(const CkptFiles& files, const std::string& name, int int8_mas
     a_ = A_.alloc<float>(act_max);
     b_ = A_.alloc<float>(act_max);
     col_ = A_.alloc<float>(col_max);
+    col_floats_ = col_max;
     int cmax = 1;
     for (const Layer& L : layers_) cmax = std::max(cmax, L.cout);
     gA_ = A_.alloc<float>(cmax);
@@ -310,9 +313,16 @@ void OctoStem::encode_dev(const uint8_t* img, float* out, hipStream_t st) {
             c.work_bytes = work_bytes_;
             launch_conv2d_i8(c, st);
         } else {
-            const int ldc = kpad4(K);
-            launch_im2col_f32(col_, ldc, a_, L.H, L.W, L.cin, k_, stride_, pad_, L.Ho, L.Wo, st);
-            launch_linear_f32(b_, L.cout, col_, ldc, L.W_, K, L.b, L.Ho * L.Wo, L.cout, K, 0, 0, 1.0f, st);
+            const size_t rows_f = col_rows_floats((size_t)L.Ho * L.Wo, K);
+            float* part = col_ + rows_f;  // split-K sums after the im2col rows
+            const size_t part_f = col_floats_ - rows_f;
+            if (!launch_conv_f32_implicit(b_, a_, L.H, L.W, L.cin, k_, stride_, pad_, L.Ho, L.Wo, L.W_, L.b, L.cout,
+                                          0, st, part, part_f)) {
+                const int ldc = kpad4(K);
+                launch_im2col_f32(col_, ldc, a_, L.H, L.W, L.cin, k_, stride_, pad_, L.Ho, L.Wo, st);
+                launch_linear_f32(b_, L.cout, col_, ldc, L.W_, K, L.b, L.Ho * L.Wo, L.cout, K, 0, 0, 1.0f, st, part,
+                                  part_f);
+            }
         }
         launch_groupnorm(a_, b_, L.gs, L.gb, L.Ho * L.Wo, L.cout, groups_, gn_eps_, true, gA_, gB_, st);
     }

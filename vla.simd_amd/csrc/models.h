@@ -152,6 +152,7 @@ private:
     uint8_t* img_in_ = nullptr;  // the frames the captured graph reads
     float *norm_ = nullptr, *a_ = nullptr, *b_ = nullptr, *c_ = nullptr, *res_ = nullptr, *col_ = nullptr,
           *feats_ = nullptr, *state_n_ = nullptr, *act_n_ = nullptr;
+    size_t col_floats_ = 0;  // im2col rows + split-K sums
     void* work_ = nullptr;
     size_t work_bytes_ = 0;
     hipStream_t own_ = nullptr;
@@ -461,6 +462,7 @@ private:
     std::vector<Layer> layers_;
     DLinear embed_;
     float *a_ = nullptr, *b_ = nullptr, *col_ = nullptr, *gA_ = nullptr, *gB_ = nullptr;
+    size_t col_floats_ = 0;  // im2col rows + split-K sums
     void* work_ = nullptr;
     size_t work_bytes_ = 0;
     Ctx ctx_;
