@@ -252,10 +252,13 @@ void launch_embed_f32(float* dst, const float* table, const int32_t* ids, int n,
                       hipStream_t st);
 // Octo SmallStem input: [npx, 6] = RGB / 127.5 - 1, then three -1 channels
 void launch_stem_input(float* out, const uint8_t* img, int64_t npx, hipStream_t st);
-// GroupNorm over NHWC [n_pixels, C] with per-channel scale / bias, then the
-// optional ReLU; A / B: device scratch [C] each (the per-channel affine)
+// GroupNorm over NHWC [n_pixels, C <= 1024], groups of <= 256 channels, with per-channel scale / bias,
+// then the optional ReLU; A / B: device scratch [C] each (the per-channel
+// affine), work: groupnorm_work_doubles(n_pixels, C) doubles of partial sums
+size_t groupnorm_work_doubles(int n_pixels, int C);
 void launch_groupnorm(float* out, const float* x, const float* scale, const float* bias, int n_pixels, int C,
-                      int groups, float eps, bool relu, float* A, float* B, hipStream_t st);
+                      int groups, float eps, bool relu, float* A, float* B, double* work, size_t work_doubles,
+                      hipStream_t st);
 // out [steps, TD] = [cos(2 pi t w) | sin(2 pi t w)], t = 0..steps-1
 void launch_fourier(float* out, const float* w, int steps, int TD, hipStream_t st);
 void launch_concat3(float* out, const float* a, int na, const float* b, int nb, const float* c, int nc,

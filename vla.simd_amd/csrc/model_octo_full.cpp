@@ -281,6 +281,8 @@ OctoStem::OctoStem(const CkptFiles& files, const std::string& name, int int8_mas
     for (const Layer& L : layers_) cmax = std::max(cmax, L.cout);
     gA_ = A_.alloc<float>(cmax);
     gB_ = A_.alloc<float>(cmax);
+    for (const Layer& L : layers_) gw_doubles_ = std::max(gw_doubles_, groupnorm_work_doubles(L.Ho * L.Wo, L.cout));
+    gW_ = A_.alloc<double>(gw_doubles_);
     if (work) {
         work_ = A_.raw(work);
         work_bytes_ = work;
@@ -324,7 +326,8 @@ void OctoStem::encode_dev(const uint8_t* img, float* out, hipStream_t st) {
                                   part_f);
             }
         }
-        launch_groupnorm(a_, b_, L.gs, L.gb, L.Ho * L.Wo, L.cout, groups_, gn_eps_, true, gA_, gB_, st);
+        launch_groupnorm(a_, b_, L.gs, L.gb, L.Ho * L.Wo, L.cout, groups_, gn_eps_, true, gA_, gB_, gW_, gw_doubles_,
+                         st);
     }
     Ctx c = ctx_;
     c.st = st;

@@ -463,6 +463,8 @@ private:
     DLinear embed_;
     float *a_ = nullptr, *b_ = nullptr, *col_ = nullptr, *gA_ = nullptr, *gB_ = nullptr;
     size_t col_floats_ = 0;  // im2col rows + split-K sums
+    double* gW_ = nullptr;   // GroupNorm partial sums
+    size_t gw_doubles_ = 0;
     void* work_ = nullptr;
     size_t work_bytes_ = 0;
     Ctx ctx_;

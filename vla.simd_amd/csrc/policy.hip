@@ -132,44 +132,138 @@ __global__ __launch_bounds__(256) void stem_input_kernel(float* __restrict__ out
     }
 }
 
-// GroupNorm statistics (conv.cpp:227-309): one block per group of C / groups
-// channels over n_pixels NHWC pixels, mean and sum of squared deviations in
-// double (two passes), then per channel A = inv * scale, B = bias - mean * inv
-// * scale, inv = 1 / sqrt(var + eps).
-__global__ __launch_bounds__(256) void groupnorm_stats_kernel(float* __restrict__ A, float* __restrict__ B,
-                                                              const float* __restrict__ x, int n_pixels, int C,
-                                                              int gc, const float* __restrict__ scale,
-                                                              const float* __restrict__ bias, float eps) {
-    __shared__ double red[256];
-    const int g = blockIdx.x, c0 = g * gc;
-    const int64_t n = (int64_t)n_pixels * gc;
-    double s = 0.0;
-    for (int64_t e = threadIdx.x; e < n; e += blockDim.x) {
-        const int64_t p = e / gc;
-        s += (double)x[p * C + c0 + (int)(e - p * gc)];
-    }
-    red[threadIdx.x] = s;
-    __syncthreads();
-    for (int w = 128; w > 0; w >>= 1) {
-        if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+// GroupNorm (conv.cpp:227-324) with the reference's shifted sums: per channel
+// S1 = sum_p (x - K_c), S2 = sum_p (x - K_c)^2 in double, K_c = the first
+// pixel's value; per group mean = (sum_c S1_c + n_pixels K_c) / n and
+// ss = sum_c S2_c + 2 (K_c - mean) S1_c + n_pixels (K_c - mean)^2, exact
+// identities of the two-pass statistics. Three launches, all parallel:
+//   groupnorm_partial_kernel   chunk b of the pixels: per-channel (S1, S2)
+//                              (coalesced: consecutive threads read
+//                              consecutive channels of a pixel);
+//   groupnorm_finalize_kernel  per group: the chunks summed in a fixed order,
+//                              A = inv * scale, B = bias - mean * inv * scale;
+//   groupnorm_apply_kernel     out = x * A[c] + B[c] (+ ReLU).
+__global__ __launch_bounds__(256) void groupnorm_partial_kernel(double* __restrict__ part,
+                                                                const float* __restrict__ x, int n_pixels, int C,
+                                                                int chunk_px) {
+    __shared__ double r1[256], r2[256];
+    const int t = threadIdx.x;
+    const int p0 = blockIdx.x * chunk_px, p1 = p0 + chunk_px < n_pixels ? p0 + chunk_px : n_pixels;
+    // C <= 256: lanes pixel lanes of C channels; C > 256: one lane, channels t and t + 256
+    const int lanes = C >= 256 ? 1 : 256 / C;
+    const int lane = C >= 256 ? 0 : t / C;
+    const bool active = lane < lanes;
+    for (int cc = 0; cc < C; cc += 256) {
+        const int c = C >= 256 ? cc + t : t - lane * C;
+        double s1 = 0.0, s2 = 0.0;
+        if (active && c < C) {
+            const double k = (double)x[c];
+            int p = p0 + lane;
+            // four pixels' loads in flight, added in pixel order
+            for (; p + 3 * lanes < p1; p += 4 * lanes) {
+                const float v0 = x[(size_t)p * C + c], v1 = x[(size_t)(p + lanes) * C + c];
+                const float v2 = x[(size_t)(p + 2 * lanes) * C + c], v3 = x[(size_t)(p + 3 * lanes) * C + c];
+                const double d0 = (double)v0 - k, d1 = (double)v1 - k, d2 = (double)v2 - k, d3 = (double)v3 - k;
+                s1 += d0;
+                s2 += d0 * d0;
+                s1 += d1;
+                s2 += d1 * d1;
+                s1 += d2;
+                s2 += d2 * d2;
+                s1 += d3;
+                s2 += d3 * d3;
+            }
+            for (; p < p1; p += lanes) {
+                const double d = (double)x[(size_t)p * C + c] - k;
+                s1 += d;
+                s2 += d * d;
+            }
+        }
+        r1[t] = s1;
+        r2[t] = s2;
         __syncthreads();
-    }
-    const double mean = red[0] / (double)n;
-    __syncthreads();
-    double q = 0.0;
-    for (int64_t e = threadIdx.x; e < n; e += blockDim.x) {
-        const int64_t p = e / gc;
-        const double d = (double)x[p * C + c0 + (int)(e - p * gc)] - mean;
-        q += d * d;
-    }
-    red[threadIdx.x] = q;
-    __syncthreads();
-    for (int w = 128; w > 0; w >>= 1) {
-        if ((int)threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+        // per channel: the lanes in order
+        if (C >= 256) {
+            if (c < C) {
+                part[(size_t)blockIdx.x * 2 * C + c] = r1[t];
+                part[(size_t)blockIdx.x * 2 * C + C + c] = r2[t];
+            }
+        } else if (t < C) {
+            double a1 = 0.0, a2 = 0.0;
+            for (int l = 0; l < lanes; l++) {
+                a1 += r1[l * C + t];
+                a2 += r2[l * C + t];
+            }
+            part[(size_t)blockIdx.x * 2 * C + t] = a1;
+            part[(size_t)blockIdx.x * 2 * C + C + t] = a2;
+        }
         __syncthreads();
+        if (C < 256) break;
     }
-    const double inv = 1.0 / sqrt(red[0] / (double)n + (double)eps);
-    for (int c = c0 + (int)threadIdx.x; c < c0 + gc; c += blockDim.x) {
+}
+
+// one block per group (gc <= 256 channels): lane l of a channel adds chunks
+// l, l + lanes, ... in order, the lanes' sums are added in lane order
+__global__ __launch_bounds__(256) void groupnorm_finalize_kernel(float* __restrict__ A, float* __restrict__ B,
+                                                                 const double* __restrict__ part, int nchunk,
+                                                                 const float* __restrict__ x, int n_pixels, int C,
+                                                                 int gc, const float* __restrict__ scale,
+                                                                 const float* __restrict__ bias, float eps) {
+    __shared__ double r1[256], r2[256], S1[256], S2[256], st[2];
+    const int t = threadIdx.x, c0 = blockIdx.x * gc;
+    const int lanes = 256 / gc, lane = t / gc, cl = t - lane * gc, c = c0 + cl;
+    double a1 = 0.0, a2 = 0.0;
+    if (lane < lanes) {
+        int b = lane;
+        for (; b + 3 * lanes < nchunk; b += 4 * lanes) {
+            const double u0 = part[(size_t)b * 2 * C + c], u1 = part[(size_t)(b + lanes) * 2 * C + c];
+            const double u2 = part[(size_t)(b + 2 * lanes) * 2 * C + c], u3 = part[(size_t)(b + 3 * lanes) * 2 * C + c];
+            const double w0 = part[(size_t)b * 2 * C + C + c], w1 = part[(size_t)(b + lanes) * 2 * C + C + c];
+            const double w2 = part[(size_t)(b + 2 * lanes) * 2 * C + C + c];
+            const double w3 = part[(size_t)(b + 3 * lanes) * 2 * C + C + c];
+            a1 += u0;
+            a1 += u1;
+            a1 += u2;
+            a1 += u3;
+            a2 += w0;
+            a2 += w1;
+            a2 += w2;
+            a2 += w3;
+        }
+        for (; b < nchunk; b += lanes) {
+            a1 += part[(size_t)b * 2 * C + c];
+            a2 += part[(size_t)b * 2 * C + C + c];
+        }
+    }
+    r1[t] = a1;
+    r2[t] = a2;
+    __syncthreads();
+    if (t < gc) {
+        double b1 = 0.0, b2 = 0.0;
+        for (int l = 0; l < lanes; l++) {
+            b1 += r1[l * gc + t];
+            b2 += r2[l * gc + t];
+        }
+        S1[t] = b1;
+        S2[t] = b2;
+    }
+    __syncthreads();
+    if (t == 0) {
+        const double n = (double)n_pixels * gc;
+        double tot = 0.0;
+        for (int j = 0; j < gc; j++) tot += S1[j] + (double)n_pixels * (double)x[c0 + j];
+        const double mean = tot / n;
+        double ss = 0.0;
+        for (int j = 0; j < gc; j++) {
+            const double dk = (double)x[c0 + j] - mean;
+            ss += S2[j] + 2.0 * dk * S1[j] + (double)n_pixels * dk * dk;
+        }
+        st[0] = mean;
+        st[1] = 1.0 / sqrt(ss / n + (double)eps);
+    }
+    __syncthreads();
+    if (t < gc) {
+        const double mean = st[0], inv = st[1];
         A[c] = (float)(inv * (double)scale[c]);
         B[c] = (float)fma(-(mean * inv), (double)scale[c], (double)bias[c]);
     }
@@ -184,6 +278,24 @@ __global__ __launch_bounds__(256) void groupnorm_apply_kernel(float* __restrict_
         const int c = (int)(i % C);
         const float v = fmaf(x[i], A[c], B[c]);
         out[i] = relu && v < 0.0f ? 0.0f : v;
+    }
+}
+
+// the same, 4 channels per thread (C % 4 == 0, 16-byte aligned rows)
+__global__ __launch_bounds__(256) void groupnorm_apply4_kernel(float4* __restrict__ out, const float4* __restrict__ x,
+                                                               int n4, int C4, const float4* __restrict__ A,
+                                                               const float4* __restrict__ B, int relu) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += gridDim.x * blockDim.x) {
+        const int c = i % C4;
+        const float4 v = x[i], a = A[c], b = B[c];
+        float4 o = make_float4(fmaf(v.x, a.x, b.x), fmaf(v.y, a.y, b.y), fmaf(v.z, a.z, b.z), fmaf(v.w, a.w, b.w));
+        if (relu) {
+            o.x = o.x < 0.0f ? 0.0f : o.x;
+            o.y = o.y < 0.0f ? 0.0f : o.y;
+            o.z = o.z < 0.0f ? 0.0f : o.z;
+            o.w = o.w < 0.0f ? 0.0f : o.w;
+        }
+        out[i] = o;
     }
 }
 
@@ -295,13 +407,42 @@ void launch_stem_input(float* out, const uint8_t* img, int64_t npx, hipStream_t 
     VLA_LAUNCH_CHECK();
 }
 
+namespace {
+// pixel chunks of the partial pass: >= 16 pixels each, at most kGnChunks
+constexpr int kGnChunks = 256;
+int gn_chunk_px(int n_pixels) {
+    const int c = (n_pixels + kGnChunks - 1) / kGnChunks;
+    return c > 16 ? c : 16;
+}
+}  // namespace
+
+size_t groupnorm_work_doubles(int n_pixels, int C) {
+    const int chunk = gn_chunk_px(n_pixels);
+    return (size_t)((n_pixels + chunk - 1) / chunk) * 2 * C;
+}
+
 void launch_groupnorm(float* out, const float* x, const float* scale, const float* bias, int n_pixels, int C,
-                      int groups, float eps, bool relu, float* A, float* B, hipStream_t st) {
-    VLA_REQUIRE(n_pixels > 0 && C > 0 && groups > 0 && C % groups == 0, "groupnorm: bad shape");
-    groupnorm_stats_kernel<<<groups, 256, 0, st>>>(A, B, x, n_pixels, C, C / groups, scale, bias, eps);
+                      int groups, float eps, bool relu, float* A, float* B, double* work, size_t work_doubles,
+                      hipStream_t st) {
+    VLA_REQUIRE(n_pixels > 0 && C > 0 && groups > 0 && C % groups == 0 && C <= 1024 && C / groups <= 256,
+                "groupnorm: bad shape");
+    VLA_REQUIRE(work && work_doubles >= groupnorm_work_doubles(n_pixels, C), "groupnorm: workspace too small");
+    const int chunk = gn_chunk_px(n_pixels), nchunk = (n_pixels + chunk - 1) / chunk;
+    groupnorm_partial_kernel<<<nchunk, 256, 0, st>>>(work, x, n_pixels, C, chunk);
+    VLA_LAUNCH_CHECK();
+    groupnorm_finalize_kernel<<<groups, 256, 0, st>>>(A, B, work, nchunk, x, n_pixels, C, C / groups, scale, bias,
+                                                      eps);
     VLA_LAUNCH_CHECK();
     const int64_t n = (int64_t)n_pixels * C;
-    groupnorm_apply_kernel<<<grid_for(n), 256, 0, st>>>(out, x, n, C, A, B, relu ? 1 : 0);
+    if (C % 4 == 0 && n / 4 < INT32_MAX && (reinterpret_cast<uintptr_t>(out) & 15) == 0 &&
+        (reinterpret_cast<uintptr_t>(x) & 15) == 0 && (reinterpret_cast<uintptr_t>(A) & 15) == 0 &&
+        (reinterpret_cast<uintptr_t>(B) & 15) == 0) {
+        groupnorm_apply4_kernel<<<grid_for(n / 4), 256, 0, st>>>(
+            reinterpret_cast<float4*>(out), reinterpret_cast<const float4*>(x), (int)(n / 4), C / 4,
+            reinterpret_cast<const float4*>(A), reinterpret_cast<const float4*>(B), relu ? 1 : 0);
+    } else {
+        groupnorm_apply_kernel<<<grid_for(n), 256, 0, st>>>(out, x, n, C, A, B, relu ? 1 : 0);
+    }
     VLA_LAUNCH_CHECK();
 }
 
