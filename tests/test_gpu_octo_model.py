@@ -203,3 +203,26 @@ def test_octo_model_full_size(vla, env, tmp_path):
     err = _rel(got, ref)
     print(f"octo model full size: rel err {err:.3e} (bar {bar:.3e})", flush=True)
     assert err <= bar
+
+
+@pytest.mark.parametrize("mask", [0, 32, 63])
+def test_fused_head_matches_layer_kernels(vla, small, env, mask):
+    """The DDPM head as one workgroup against the same head as separate
+    kernels (VLA_OCTO_HEAD_FUSED=0). Its int8 layers (OCTO_INT8 bit 32) repeat
+    the separate kernels' arithmetic (quantized rows, exact integer sums, the
+    epilogue, LayerNorm, the update); its fp32 layers - all of them at mask 0,
+    and the 28-wide output projection, which int8_fits leaves fp32, at every
+    mask - sum their dot products in another order (measured at masks 0,
+    32, 63: 3.8e-8, 9.5e-9, 3.8e-8 of the output scale); bar 1e-6."""
+    d, c = small
+    ck = _ck()
+    env(mask)
+    p, w, tm, n, z = ck.octo_model_inputs(c)
+    os.environ["VLA_OCTO_HEAD_FUSED"] = "0"
+    try:
+        ref = vla.OctoModel(d).predict(p, w, tm, TEXT, noise=n, z=z)
+    finally:
+        del os.environ["VLA_OCTO_HEAD_FUSED"]
+    got = vla.OctoModel(d).predict(p, w, tm, TEXT, noise=n, z=z)
+    print(f"fused head OCTO_INT8={mask}: rel diff {_rel(got, ref):.3e}", flush=True)
+    assert _rel(got, ref) <= 1e-6

@@ -264,6 +264,34 @@ void launch_fourier(float* out, const float* w, int steps, int TD, hipStream_t s
 void launch_concat3(float* out, const float* a, int na, const float* b, int nb, const float* c, int nc,
                     hipStream_t st);
 // x = clip(a1 * (x - a2 * e) + sb * z, +-max_action) over n values
+// Octo's DDPM head for all steps in one workgroup (policy.hip): one linear
+// layer's weights, int8 (Wq [N, ldw] + ws + b) or fp32 (W [N, K] + b)
+struct HeadLin {
+    const int8_t* Wq = nullptr;
+    const float* W = nullptr;
+    const float* ws = nullptr;
+    const float* b = nullptr;
+    int ldw = 0, N = 0, K = 0;
+};
+constexpr int kOctoHeadMaxBlocks = 8;
+struct OctoHeadArgs {
+    HeadLin in_proj, out_proj, d0[kOctoHeadMaxBlocks], d1[kOctoHeadMaxBlocks];
+    const float* ln_s[kOctoHeadMaxBlocks] = {};
+    const float* ln_b[kOctoHeadMaxBlocks] = {};
+    float ln_eps = 1e-6f;
+    int nb = 0, H = 0, TD = 0, emb = 0, flat = 0, steps = 0;
+    const float* cond = nullptr;   // [steps, TD]
+    const float* embv = nullptr;   // [emb]
+    const float* noise = nullptr;  // [flat]
+    const float* z = nullptr;      // [steps, flat]
+    const float* coef = nullptr;   // [steps][a1, a2, sb]
+    float max_action = 0.0f;
+    float* actions = nullptr;      // [flat]
+};
+// dynamic LDS of the fused head; launch_octo_head requires <= 64 KiB and
+// 4 H, N <= 1024 outputs per layer
+size_t octo_head_lds_bytes(int H, int TD, int emb, int flat);
+void launch_octo_head(const OctoHeadArgs& a, hipStream_t st);
 void launch_ddpm_step(float* x, const float* e, const float* z, int n, float a1, float a2, float sb,
                       float max_action, hipStream_t st);
 // the guided Euler step of real-time chunking, gw [steps] on the device

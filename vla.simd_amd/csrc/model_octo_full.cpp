@@ -414,12 +414,66 @@ OctoHead::OctoHead(const CkptFiles& files, int int8_mask) {
     launch_fourier(tff, wdev, steps_, TD, st);
     linear(c, cond0, c1, 2 * TD, tff, TD, steps_, 4);  // silu
     linear(c, cond1, cond_, TD, c1, 2 * TD, steps_);
+
+    // the fused form of denoise_dev: every layer's weights, the per-step
+    // coefficients on the device; used when the shapes fit its one workgroup
+    auto hl = [](const DLinear& L) {
+        HeadLin h;
+        if (L.int8()) {
+            h.Wq = L.q8->Wq();
+            h.ldw = L.q8->ldw();
+            h.ws = L.q8->wscale();
+            h.b = L.q8->bias();
+        } else {
+            h.W = L.W;
+            h.b = L.b;
+        }
+        h.N = L.N;
+        h.K = L.K;
+        return h;
+    };
+    fused_.in_proj = hl(in_proj_);
+    fused_.out_proj = hl(out_proj_);
+    fused_ok_ = nb_ <= kOctoHeadMaxBlocks && 4 * H <= 1024 && FLAT <= 1024 && H <= 1024 &&
+                octo_head_lds_bytes(H, TD, emb_, FLAT) <= 64 * 1024;
+    for (int i = 0; i < nb_ && fused_ok_; i++) {
+        fused_.d0[i] = hl(blocks_[i].d0);
+        fused_.d1[i] = hl(blocks_[i].d1);
+        fused_.ln_s[i] = blocks_[i].ln_s;
+        fused_.ln_b[i] = blocks_[i].ln_b;
+    }
+    fused_.ln_eps = 1e-6f;
+    fused_.nb = nb_;
+    fused_.H = H;
+    fused_.TD = TD;
+    fused_.emb = emb_;
+    fused_.flat = FLAT;
+    fused_.steps = steps_;
+    fused_.cond = cond_;
+    fused_.max_action = max_action_;
+    std::vector<float> coef(3 * (size_t)steps_);
+    for (int t = 0; t < steps_; t++) {
+        coef[3 * t] = a1_[t];
+        coef[3 * t + 1] = a2_[t];
+        coef[3 * t + 2] = sb_[t];
+    }
+    fused_.coef = A_.upload(coef.data(), coef.size());
     VLA_HIP_CHECK(hipStreamSynchronize(st));
 }
 
 // DiffusionHead::denoise + DiffusionMlp::forward (diffusion_head.cpp:151-177,
 // diffusion.cpp:15-36); actions is the running x
 void OctoHead::denoise_dev(const float* emb, const float* noise, const float* z, float* actions, hipStream_t st) {
+    const char* fe = std::getenv("VLA_OCTO_HEAD_FUSED");  // 0: the layer-by-layer kernels (A/B runs)
+    if (fused_ok_ && !(fe && fe[0] == '0' && fe[1] == '\0')) {
+        OctoHeadArgs a = fused_;
+        a.embv = emb;
+        a.noise = noise;
+        a.z = z;
+        a.actions = actions;
+        launch_octo_head(a, st);
+        return;
+    }
     const int TD = td_, H = H_, FLAT = flat(), IN = TD + emb_ + FLAT;
     Ctx c = ctx_;
     c.st = st;

@@ -500,6 +500,8 @@ private:
     std::vector<float> a1_, a2_, sb_;
     float *in_ = nullptr, *h_ = nullptr, *n_ = nullptr, *wide_ = nullptr, *e_ = nullptr;
     Ctx ctx_;
+    OctoHeadArgs fused_;  // the one-workgroup form of denoise_dev
+    bool fused_ok_ = false;
 };
 
 // src/models/octo/octo_model.{h,cpp} + octo_capi.cpp: pre-resized uint8

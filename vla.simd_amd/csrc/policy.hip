@@ -2,7 +2,10 @@
 // transformers: camera preprocessing, token embedding lookup, state and action
 // (un)normalization and the flow-matching update with real-time-chunking
 // guidance. Each is a single pass over at most a few MB.
+#include "act.h"
 #include "common.h"
+#include "quant_row.h"
+#include "wave.h"
 
 #include <algorithm>
 #include <cmath>
@@ -333,6 +336,146 @@ __global__ __launch_bounds__(256) void ddpm_step_kernel(float* __restrict__ x, c
     x[i] = v < -max_action ? -max_action : v > max_action ? max_action : v;
 }
 
+
+// ------------------------------------------------- Octo's DDPM head, fused --
+//
+// DiffusionHead::denoise (diffusion_head.cpp:151-177) with DiffusionMlp
+// (diffusion.cpp:15-36) for all steps in one workgroup: the head works on one
+// row (horizon x action_dim values, hidden H), so each of its ~14 layers per
+// step is a few microseconds of launch and latency as a kernel of its own.
+// Here the row, the activations and the quantized inputs stay in LDS and the
+// weights stream from L2 every step. Each linear repeats the arithmetic of the
+// separate kernels: int8 layers quantize their input row as quant_row.h does,
+// sum int8 products exactly (any order), then fmaf((float)acc * ws, sa, b);
+// fp32 layers sum x * w per output in a fixed order (its own order, fp32
+// tolerance); LayerNorm is layernorm_kernel's one-wave double-precision pass.
+// Measured on MI355X (Octo-base head, hidden 256, 20 steps): 0.95 ms for the
+// whole denoise in one launch, against ~1.0 ms of kernels plus ~280 graph
+// nodes layer by layer; about half of it is the barriers and reductions
+// between the ~8 dependent layers of a step, half the weight reads of one CU.
+// block-wide max; red is free on entry (every phase ends with a barrier)
+__device__ __forceinline__ float head_block_max(float v, float* red) {
+    v = wave_max_f32(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float m = 0.0f;
+    for (int w = 0; w < (int)(blockDim.x >> 6); w++) m = fmaxf(m, red[w]);
+    return m;
+}
+
+// y (+)= act(W x + b) for one row; x, y in LDS; q: LDS int8 scratch. The N
+// outputs take tpo = 1024 / N threads each (a power of two <= 64, inside one
+// wave): thread j of an output walks its weight row's 16-byte chunks j,
+// j + tpo, ..., and the tpo partial sums combine through lane exchanges.
+__device__ void head_linear(const HeadLin& L, const float* x, float* y, int act, bool acc, int8_t* q, float* red) {
+    const int t = threadIdx.x, N = L.N, K = L.K;
+    int tpo = 1;
+    while (tpo < 64 && tpo * 2 * N <= 1024) tpo *= 2;
+    const int n = t / tpo, j = t - n * tpo;
+    const bool live = n < N;
+    if (L.Wq) {
+        // the row quantizer: amax, s = max(amax / 127, FLT_MIN), q = rne(x / s) clamped
+        float m = 0.0f;
+        for (int k = t; k < K; k += blockDim.x) m = fmaxf(m, fabsf(x[k]));
+        const float sa = row_scale(head_block_max(m, red)), inv = 1.0f / sa;
+        const int K16 = (K + 15) & ~15;
+        for (int k = t; k < K16; k += blockDim.x) q[k] = k < K ? (int8_t)q8(x[k], inv) : (int8_t)0;
+        __syncthreads();
+        int a = 0;
+        if (live) {
+            const int8_t* w = L.Wq + (size_t)n * L.ldw;
+            for (int c = j * 16; c < K16; c += tpo * 16) {
+                const int4 wv = *reinterpret_cast<const int4*>(w + c);
+                const int4 qv = *reinterpret_cast<const int4*>(q + c);
+                a = __builtin_amdgcn_sdot4(wv.x, qv.x, a, false);
+                a = __builtin_amdgcn_sdot4(wv.y, qv.y, a, false);
+                a = __builtin_amdgcn_sdot4(wv.z, qv.z, a, false);
+                a = __builtin_amdgcn_sdot4(wv.w, qv.w, a, false);
+            }
+        }
+        for (int o = tpo / 2; o > 0; o >>= 1) a += __shfl_xor(a, o, 64);
+        if (live && j == 0) {
+            float v = fmaf((float)a * L.ws[n], sa, L.b ? L.b[n] : 0.0f);
+            if (act == 4) v = act_silu(v);
+            y[n] = acc ? y[n] + v : v;
+        }
+    } else {
+        float a = 0.0f;
+        if (live) {
+            const float* w = L.W + (size_t)n * K;
+            for (int k = j; k < K; k += tpo) a = fmaf(x[k], w[k], a);
+        }
+        // lanes in a fixed pairing order
+        for (int o = tpo / 2; o > 0; o >>= 1) a += __shfl_xor(a, o, 64);
+        if (live && j == 0) {
+            float v = a + (L.b ? L.b[n] : 0.0f);
+            if (act == 4) v = act_silu(v);
+            y[n] = acc ? fmaf(1.0f, v, y[n]) : v;
+        }
+    }
+    __syncthreads();
+}
+
+__global__ __launch_bounds__(1024) void octo_head_kernel(OctoHeadArgs a) {
+    extern __shared__ __attribute__((aligned(16))) float hs[];
+    const int H = a.H, TD = a.TD, E = a.emb, F = a.flat, IN = TD + E + F;
+    const int t = threadIdx.x;
+    auto r16 = [](int v) { return (v + 15) & ~15; };
+    float* xin = hs;              // [IN]
+    float* h = xin + r16(IN);     // [H]
+    float* nrm = h + r16(H);      // [H]
+    float* wide = nrm + r16(H);   // [4H]
+    float* e = wide + r16(4 * H); // [F]
+    float* x = e + r16(F);        // [F] the running actions
+    float* red = x + r16(F);      // [16]
+    int8_t* q = reinterpret_cast<int8_t*>(red + 16);
+    for (int i = t; i < F; i += blockDim.x) x[i] = a.noise[i];
+    for (int i = t; i < E; i += blockDim.x) xin[TD + i] = a.embv[i];
+    __syncthreads();
+    for (int s = 0; s < a.steps; s++) {
+        const int ts = a.steps - 1 - s;
+        for (int i = t; i < TD; i += blockDim.x) xin[i] = a.cond[(size_t)ts * TD + i];
+        for (int i = t; i < F; i += blockDim.x) xin[TD + E + i] = x[i];
+        __syncthreads();
+        head_linear(a.in_proj, xin, h, 0, false, q, red);
+        for (int b = 0; b < a.nb; b++) {
+            if (t < 64) {  // layernorm_kernel's pass, one wave
+                // contracted as eltwise.hip compiles it (the default, fast), so
+                // the variance sums round as that kernel's do
+#pragma clang fp contract(fast)
+                double sum = 0.0;
+                for (int k = t; k < H; k += 64) sum += (double)h[k];
+                const double mean = wave_sum_f64(sum) / H;
+                double v = 0.0;
+                for (int k = t; k < H; k += 64) {
+                    const double d = (double)h[k] - mean;
+                    v += d * d;
+                }
+                const double var = wave_sum_f64(v);
+                const float inv = (float)(1.0 / sqrt(var / H + (double)a.ln_eps));
+                for (int k = t; k < H; k += 64) {
+                    const float c = (float)((double)h[k] - mean);
+                    nrm[k] = a.ln_b[b] ? fmaf(c * inv, a.ln_s[b][k], a.ln_b[b][k]) : c * inv * a.ln_s[b][k];
+                }
+            }
+            __syncthreads();
+            head_linear(a.d0[b], nrm, wide, 4, false, q, red);
+            head_linear(a.d1[b], wide, h, 0, true, q, red);
+        }
+        for (int i = t; i < H; i += blockDim.x) h[i] = act_silu(h[i]);
+        __syncthreads();
+        head_linear(a.out_proj, h, e, 0, false, q, red);
+        const float a1 = a.coef[3 * ts], a2 = a.coef[3 * ts + 1], sb = a.coef[3 * ts + 2];
+        for (int i = t; i < F; i += blockDim.x) {
+            const float v = fmaf(a1, fmaf(-a2, e[i], x[i]), sb * a.z[(size_t)s * F + i]);
+            x[i] = v < -a.max_action ? -a.max_action : v > a.max_action ? a.max_action : v;
+        }
+        __syncthreads();
+    }
+    for (int i = t; i < F; i += blockDim.x) a.actions[i] = x[i];
+}
+
 int grid_for(int64_t n) {
     const int64_t b = (n + 255) / 256;
     return (int)(b < 4096 ? (b > 0 ? b : 1) : 4096);
@@ -457,6 +600,22 @@ void launch_concat3(float* out, const float* a, int na, const float* b, int nb, 
                     hipStream_t st) {
     const int n = na + nb + nc;
     concat3_kernel<<<(n + 255) / 256, 256, 0, st>>>(out, a, na, b, nb, c, nc);
+    VLA_LAUNCH_CHECK();
+}
+
+size_t octo_head_lds_bytes(int H, int TD, int emb, int flat) {
+    auto r16 = [](size_t v) { return (v + 15) & ~(size_t)15; };
+    const size_t IN = (size_t)TD + emb + flat;
+    const size_t floats = r16(IN) + 2 * r16(H) + r16(4 * (size_t)H) + 2 * r16(flat) + 16;
+    const size_t qbytes = r16(IN > 4 * (size_t)H ? IN : 4 * (size_t)H);
+    return floats * 4 + qbytes;
+}
+
+void launch_octo_head(const OctoHeadArgs& a, hipStream_t st) {
+    const size_t lds = octo_head_lds_bytes(a.H, a.TD, a.emb, a.flat);
+    VLA_REQUIRE(a.nb >= 0 && a.nb <= kOctoHeadMaxBlocks && lds <= 64 * 1024 && a.steps > 0,
+                "octo head: shape beyond the fused kernel");
+    octo_head_kernel<<<1, 1024, lds, st>>>(a);
     VLA_LAUNCH_CHECK();
 }
 
