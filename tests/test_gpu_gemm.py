@@ -168,7 +168,7 @@ def test_k_bound_rejected(vla):
 
 
 TILES = ["128x128x64", "64x128x64", "64x64x64", "128x128x64s4", "64x128x64s4", "256x128x128s3w8",
-         "256x256x128s2w8", "256x128x128s3w8p", "256x256x128s2w8p", "128x128x128s2"]
+         "256x256x128s2w8", "256x128x128s3w8p", "256x256x128s2w8p", "128x128x128s2", "64x64x128s3", "64x64x128s4"]
 
 
 @pytest.mark.parametrize("tile", TILES)
@@ -307,12 +307,10 @@ def test_panel_rejects_large_m(vla, torch_cuda):
 
 # ---------------------------------------------------------------- split K --
 
-# long-K GEMMs of a few hundred rows whose tiles leave most CUs idle: Octo's
-# w2 (658 x 768 x 3072), SmolLM2's down (177 x 960 x 2560), ACT's w2
-# (302 x 512 x 3200), a ResNet 3x3/512 conv (300 x 512 x 4608), a K tail
-# (2050), a 129-row case and a sweep shape (512 x 960 x 2560)
-SPLIT_SHAPES = [(658, 768, 3072), (177, 960, 2560), (302, 512, 3200), (300, 512, 4608), (129, 100, 2050),
-                (200, 48, 1500), (512, 960, 2560),
+# very long K over at most 64 tiles of 64 x 64 (M > 128 splits only there):
+# ACT's w2 (302 x 512 x 3200), a ResNet 3x3/512 conv (300 x 512 x 4608),
+# K tails (4100, 3100), a 129-row case, 64 tiles exactly (256 x 1024 x 4096)
+SPLIT_SHAPES = [(302, 512, 3200), (300, 512, 4608), (129, 100, 4100), (200, 48, 3100), (256, 1024, 4096),
                 # at most 128 rows (the skinny kernel): SigLIP's projection
                 # (64 x 960 x 12288), a K tail, one row, 16 columns
                 (64, 960, 12288), (100, 1000, 4100), (1, 16, 4096), (16, 200, 8192)]

@@ -1215,7 +1215,7 @@ const Tile kTiles[] = {{128, 128, 64, 0},       {64, 128, 64, 0},         {64, 6
                        {64, 64, 128, 0},        {64, 128, 128, 0},
                        {128, 128, 64, 4},       {64, 128, 64, 4},         {256, 128, 128, 3, 8},
                        {256, 256, 128, 2, 8},   {256, 128, 128, 3, 8, true}, {256, 256, 128, 2, 8, true},
-                       {128, 128, 128, 2}};
+                       {128, 128, 128, 2},      {64, 64, 128, 3},         {64, 64, 128, 4}};
 
 Tile pick_tile(int M, int N, int K) {
     const char* env = std::getenv("VLA_HIP_GEMM_TILE");
@@ -1248,6 +1248,17 @@ Tile pick_tile(int M, int N, int K) {
     // barriers and twice the MFMA work per slab (ACT 0.409 -> 0.402 ms, Octo
     // 1.159 -> 1.141 ms per forward)
     const Tile small{64, 64, K >= 256 ? 128 : 64, 0};
+    // The policy layers' GEMMs (a few hundred to ~1000 rows, tiles < 2 per CU)
+    // take the LDS-DMA 64 x 64 tile with 128-byte slabs: every slab of a short
+    // K is in flight at once (3 stages, 48 KiB: three blocks per CU), 4 stages
+    // over long K. Interleaved repeats on MI355X, register-staged / split-K
+    // tile -> this: 1024x768x2304 8.70 -> 7.51 us, 658x768x3072 8.62 -> 7.36,
+    // 302x512x3200 5.67 -> 4.89, 177x960x2560 7.25 -> 6.09, 1024x3072x768
+    // 16.98 -> 11.23, 2048x2560x960 15.59 -> 11.86, 512x4096x4096 23.97 ->
+    // 20.12, 512x2560x960 13.80 -> 9.90; bit-identical sums. Very long K over
+    // at most 64 such tiles (302x3200x512 10.38 split vs 11.27, 200x4096x1024
+    // 12.96 vs 13.61) stays on the split-K register tile.
+    const Tile lds64{64, 64, 128, K <= 1024 ? 3 : 4};
     // Large outputs over short K (M, N >= 1024, 512 <= K <= 1024, at least
     // one 128 x 128 tile per CU): the LDS-DMA 128 x 128 tile with 128-byte
     // slabs, two stages (64 KiB, two blocks per CU) and non-temporal stores;
@@ -1257,12 +1268,12 @@ Tile pick_tile(int M, int N, int K) {
     // 1024-row layers), at 658 rows and at 1000^3 the register-staged tiles
     // stay ahead.
     if (K <= 1024 && K >= 512 && M >= 1024 && N >= 1024 && tiles(128, 128) >= kCUs) return {128, 128, 128, 2};
-    if (K <= 1024) return tiles(64, 128) >= 2 * kCUs ? Tile{64, 128, 64, 0} : small;
+    if (K <= 1024) return tiles(64, 128) >= 2 * kCUs ? Tile{64, 128, 64, 0} : K >= 256 ? lds64 : small;
     if (tiles(256, 256) >= 2 * kCUs) return {256, 256, 128, 2, 8, true};
     if (tiles(256, 128) >= kCUs) return {256, 128, 128, 3, 8, true};
     if (tiles(128, 128) >= kCUs) return {128, 128, 64, 4};
-    if (tiles(64, 128) >= kCUs) return {64, 128, 64, 4};
-    return small;
+    if (tiles(64, 64) <= 64 && K >= 3072) return small;  // split over K (split_plan)
+    return lds64;
 }
 
 // Split-K plan: for M > 128 on the register-staged tiles with K >= 1024 and
@@ -1320,7 +1331,10 @@ void dispatch_tile(const Tile& t, const GemmArgs& a, hipStream_t st) {
         return;
     }
     if (t.stages) {
-        if (t.bm == 128 && t.bk == 128) run_lds<128, 128, 128, 2>(a, st);
+        if (t.bm == 64 && t.bn == 64) {
+            if (t.stages == 3) run_lds<64, 64, 128, 3>(a, st);
+            else run_lds<64, 64, 128, 4>(a, st);
+        } else if (t.bm == 128 && t.bk == 128) run_lds<128, 128, 128, 2>(a, st);
         else if (t.bm == 128) run_lds<128, 128, 64, 4>(a, st);
         else run_lds<64, 128, 64, 4>(a, st);
         return;
