@@ -223,6 +223,9 @@ OctoStem::OctoStem(const CkptFiles& files, const std::string& name, int int8_mas
     for (int i = 0; i < n_layers; i++) {
         VLA_REQUIRE(fits({features[i], k_, k_, cin}) && features[i] % groups_ == 0,
                     mf + ": invalid features (small_stem.cpp:51-54 bounds)");
+        // the device GroupNorm's limits (launch_groupnorm), checked at load
+        VLA_REQUIRE(features[i] <= 1024 && features[i] / groups_ <= 256,
+                    mf + ": GroupNorm beyond this build (at most 1024 channels, 256 per group)");
         cin = features[i];
     }
 
