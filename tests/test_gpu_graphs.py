@@ -274,6 +274,34 @@ def test_smolvla_short_chunk(vla, ckdir, mask):
     _check_replay(lambda: m.run(prefix, pad, noise), got)
 
 
+@pytest.mark.parametrize("mask,short", [(32, False), (48, False), (48, True)])
+def test_smolvla_rope_epilogue_bit_exact(vla, ckdir, mask, short):
+    """The expert's int8 q|k|v and q projections rotate their q/k heads in the
+    skinny GEMM's epilogue (each block owns 8 rotation pairs of a head); the
+    chunk must equal, bit for bit, the same chunk with the GEMM storing plain
+    outputs and the separate RoPE kernel rotating them
+    (VLA_HIP_ROPE_FUSE=0): same epilogue floats, same rotation (rope.h)."""
+    ck = _ck()
+    if short:
+        c = dict(ck.SMOLVLA_BASE, chunk=12, n_layers=4, expert_layers=4, n_prefix=60)
+        d = str(ckdir / "smol12")
+    else:
+        c = ck.SMOLVLA_BASE
+        d = str(ckdir / "smol")
+    if not os.path.exists(os.path.join(d, "aex.bin")):
+        ck.write_smolvla(d, c)
+    prefix, pad, noise = ck.smolvla_inputs(c, n_pad=3)
+    os.environ["VLA_HIP_ROPE_FUSE"] = "0"
+    try:
+        ref = vla.SmolvlaChunk(d, mask).run(prefix, pad, noise)
+    finally:
+        del os.environ["VLA_HIP_ROPE_FUSE"]
+    got = vla.SmolvlaChunk(d, mask).run(prefix, pad, noise)
+    print(f"smolvla rope epilogue mask {mask} short {short}: max |diff| {np.max(np.abs(got - ref)):.3e}",
+          flush=True)
+    assert got.tobytes() == ref.tobytes()
+
+
 def test_models_load_from_gguf(vla, ckdir):
     """The device graphs loaded from a vla.simd GGUF (vla_ckpt_open's mount of
     the single-file checkpoint) give bit-identical outputs to the same graphs

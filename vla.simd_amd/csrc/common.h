@@ -103,6 +103,12 @@ struct GemmArgs {
     int32_t* split_ws;
     size_t split_bytes;
     int kchunk;                  // set by launch_gemm_i8 for a split launch
+    // Rotating epilogue (the skinny GEMM only, M <= 128): output columns
+    // [0, rope_cols) are heads of rope_hd columns, rotated after the epilogue
+    // with the per-row table rope_cs [M][rope_hd / 2][cos, sin] (double), as
+    // launch_rope_table would rotate them in place afterwards; null: none.
+    const double* rope_cs;
+    int rope_cols, rope_hd;
 };
 void launch_gemm_i8(const GemmArgs& a, hipStream_t st);
 // Workspace bytes launch_gemm_i8 uses to split K for this shape (0: no split).

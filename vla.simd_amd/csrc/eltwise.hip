@@ -18,6 +18,7 @@
 #include "act.h"
 #include "common.h"
 #include "quant_row.h"
+#include "rope.h"
 #include "rowop.h"
 
 namespace vla {
@@ -107,8 +108,8 @@ __global__ __launch_bounds__(256) void rope_table_kernel(float* x, int ld, const
     const double c = cs[((size_t)t * half + i) * 2], s = cs[((size_t)t * half + i) * 2 + 1];
     float* v = x + (size_t)t * ld + hh * 2 * half;
     const float x0 = v[i], x1 = v[i + half];
-    v[i] = (float)(x0 * c - x1 * s);
-    v[i + half] = (float)(x0 * s + x1 * c);
+    v[i] = rope_lo(x0, x1, c, s);
+    v[i + half] = rope_hi(x0, x1, c, s);
 }
 
 // one thread per (token, pair index i); loops over heads
@@ -125,8 +126,8 @@ __global__ __launch_bounds__(256) void rope_kernel(float* x, int ld, const int32
     for (int hh = 0; hh < n_heads; hh++) {
         float* v = row + hh * head_dim;
         const float x0 = v[i], x1 = v[i + half];
-        v[i] = (float)(x0 * c - x1 * s);
-        v[i + half] = (float)(x0 * s + x1 * c);
+        v[i] = rope_lo(x0, x1, c, s);
+        v[i + half] = rope_hi(x0, x1, c, s);
     }
 }
 

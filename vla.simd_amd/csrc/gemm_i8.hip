@@ -59,6 +59,7 @@
 
 #include "act.h"
 #include "common.h"
+#include "rope.h"
 #include "rowop.h"
 
 #include <cstdio>
@@ -725,7 +726,12 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds(GemmArgs a) {
 
 // ---------------------------------------------------------------- skinny --
 
-template <int FM, int WAVES>
+// ROPE: blocks below a.rope_cols own 8 rotation pairs of one head instead of
+// 16 consecutive columns - lane c < 8 column 8 k + c of the head, lane c >= 8
+// its partner 8 k + c - 8 + half (k = the block's index within the head) -
+// so the epilogue rotates each output with its partner's value, summed from
+// the same block's partial tiles.
+template <int FM, int WAVES, bool ROPE = false>
 __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
     static_assert(FM * WAVES <= 64, "partial tiles must fit in 64 KiB of LDS");
     // per wave, its partial int32 tile in MFMA lane order: [i][r][lane]
@@ -755,7 +761,15 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
         const int m = i * 16 + r16 < a.M ? i * 16 + r16 : a.M - 1;
         arow[i] = a.a_panel ? a.A + (size_t)(i * 16 + r16) * 64 + kq : a.A + (size_t)m * a.lda + kq;
     }
-    const int n = n0 + r16 < a.N ? n0 + r16 : a.N - 1;
+    // output column of block lane c (16 consecutive columns, or ROPE pairs)
+    const bool rotb = ROPE && n0 < a.rope_cols;
+    auto col = [&](int c) {
+        if (!rotb) return n0 + c;
+        const int hb = a.rope_hd / 16, head = blockIdx.x / hb, k = blockIdx.x - head * hb;
+        return head * a.rope_hd + 8 * k + (c & 7) + (c < 8 ? 0 : a.rope_hd / 2);
+    };
+    const int nr = col(r16);
+    const int n = nr < a.N ? nr : a.N - 1;
     const int8_t* brow = a.B + (size_t)n * a.ldb + kq;
 
     // The outputs this thread stores after the reduction (element e of the
@@ -763,11 +777,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
     // their latency hides under the main loop rather than after the barrier.
     constexpr int NT = WAVES * 64, EPT = (FM * 256 + NT - 1) / NT;
     float esa[EPT], ews[EPT], eb[EPT], eold[EPT];
+    // ROPE: the partner column's scale and bias, this output's (cos, sin)
+    float pws[ROPE ? EPT : 1], pb[ROPE ? EPT : 1];
+    double rc[ROPE ? EPT : 1], rs[ROPE ? EPT : 1];
 #pragma unroll
     for (int j = 0; j < EPT; j++) {
         const int e = tid + j * NT;
         const int l = e & 63, r = (e >> 6) & 3, i = e >> 8;
-        int mm = 16 * i + 4 * (l >> 4) + r, nn = n0 + (l & 15);
+        int mm = 16 * i + 4 * (l >> 4) + r, nn = col(l & 15);
         const bool ok = e < FM * 256 && mm < a.M && nn < a.N;
         mm = ok ? mm : 0;
         nn = ok ? nn : 0;
@@ -777,6 +794,18 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
             ews[j] = a.wscale[nn];
             eb[j] = a.bias ? a.bias[nn] : 0.0f;
             if (a.accumulate && ok) eold[j] = a.out[(size_t)mm * a.ldo + nn];
+        }
+        if constexpr (ROPE) {
+            pws[j] = pb[j] = 0.0f;
+            rc[j] = rs[j] = 0.0;
+            if (rotb && ok) {
+                const int np = col((l & 15) ^ 8), half = a.rope_hd / 2;
+                pws[j] = a.wscale[np];
+                pb[j] = a.bias ? a.bias[np] : 0.0f;
+                const double* t = a.rope_cs + ((size_t)mm * half + nn % a.rope_hd % half) * 2;
+                rc[j] = t[0];
+                rs[j] = t[1];
+            }
         }
     }
 
@@ -846,7 +875,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
 #pragma unroll
         for (int w = 0; w < WAVES; w++) v += part[w * FM * 256 + e];
         const int l = e & 63, r = (e >> 6) & 3, i = e >> 8;
-        const int mm = 16 * i + 4 * (l >> 4) + r, nn = n0 + (l & 15);
+        const int mm = 16 * i + 4 * (l >> 4) + r, nn = col(l & 15);
         if (mm >= a.M || nn >= a.N) continue;
         if (a.acc32) {
             a.acc32[(size_t)mm * a.N + nn] = v;
@@ -854,6 +883,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
         }
         const float p = (float)v * ews[j];
         float o = fmaf(p, esa[j], eb[j]);
+        if constexpr (ROPE) {
+            if (rotb) {  // act 0, no accumulate (checked by the launcher)
+                int32_t vp = 0;
+#pragma unroll
+                for (int w = 0; w < WAVES; w++) vp += part[w * FM * 256 + (e ^ 8)];
+                const float op = fmaf((float)vp * pws[j], esa[j], pb[j]);
+                a.out[(size_t)mm * a.ldo + nn] = (l & 8) ? rope_hi(op, o, rc[j], rs[j]) : rope_lo(o, op, rc[j], rs[j]);
+                continue;
+            }
+        }
         switch (a.act) {
         case 1: o = act_relu(o); break;
         case 2: o = act_gelu_tanh(o); break;
@@ -1150,19 +1189,19 @@ void run_lds(const GemmArgs& a, hipStream_t st) {
     VLA_LAUNCH_CHECK();
 }
 
-template <int WAVES>
+template <int WAVES, bool ROPE = false>
 void run_skinny(const GemmArgs& a, hipStream_t st, int splits = 1) {
     const dim3 nb((a.N + 15) / 16, splits);
     constexpr int W8 = WAVES < 8 ? WAVES : 8;  // FM > 4 keeps the partial tiles within 64 KiB
     switch ((a.M + 15) / 16) {
-    case 1: gemm_i8_skinny<1, WAVES><<<nb, WAVES * 64, 0, st>>>(a); break;
-    case 2: gemm_i8_skinny<2, WAVES><<<nb, WAVES * 64, 0, st>>>(a); break;
-    case 3: gemm_i8_skinny<3, WAVES><<<nb, WAVES * 64, 0, st>>>(a); break;
-    case 4: gemm_i8_skinny<4, WAVES><<<nb, WAVES * 64, 0, st>>>(a); break;
-    case 5: gemm_i8_skinny<5, W8><<<nb, W8 * 64, 0, st>>>(a); break;
-    case 6: gemm_i8_skinny<6, W8><<<nb, W8 * 64, 0, st>>>(a); break;
-    case 7: gemm_i8_skinny<7, W8><<<nb, W8 * 64, 0, st>>>(a); break;
-    default: gemm_i8_skinny<8, W8><<<nb, W8 * 64, 0, st>>>(a); break;
+    case 1: gemm_i8_skinny<1, WAVES, ROPE><<<nb, WAVES * 64, 0, st>>>(a); break;
+    case 2: gemm_i8_skinny<2, WAVES, ROPE><<<nb, WAVES * 64, 0, st>>>(a); break;
+    case 3: gemm_i8_skinny<3, WAVES, ROPE><<<nb, WAVES * 64, 0, st>>>(a); break;
+    case 4: gemm_i8_skinny<4, WAVES, ROPE><<<nb, WAVES * 64, 0, st>>>(a); break;
+    case 5: gemm_i8_skinny<5, W8, ROPE><<<nb, W8 * 64, 0, st>>>(a); break;
+    case 6: gemm_i8_skinny<6, W8, ROPE><<<nb, W8 * 64, 0, st>>>(a); break;
+    case 7: gemm_i8_skinny<7, W8, ROPE><<<nb, W8 * 64, 0, st>>>(a); break;
+    default: gemm_i8_skinny<8, W8, ROPE><<<nb, W8 * 64, 0, st>>>(a); break;
     }
     VLA_LAUNCH_CHECK();
 }
@@ -1363,10 +1402,22 @@ void launch_gemm_i8(const GemmArgs& a, hipStream_t st) {
                     aligned(a.B, 16) && (a.acc32 ? aligned(a.acc32, 16) : aligned(a.out, 16));
     VLA_REQUIRE(!a.a_panel || (a.M <= kPanelMaxRows && al),
                 "gemm_i8: panel-layout activations need M <= 128 and 16-byte aligned operands");
+    VLA_REQUIRE(!a.rope_cs || (al && a.M <= 128 && !a.acc32 && a.act == 0 && !a.accumulate && a.rope_hd > 0 &&
+                               a.rope_hd % 16 == 0 && a.rope_cols > 0 && a.rope_cols % a.rope_hd == 0 &&
+                               a.rope_cols <= a.N),
+                "gemm_i8: the rotating epilogue needs M <= 128, aligned operands, fp32 output without "
+                "activation or accumulation, and whole heads of a multiple of 16 columns");
     if (!al) {
         const int blocks = ((a.M + 63) / 64) * ((a.N + 63) / 64);
         gemm_i8_generic<<<blocks, 256, 0, st>>>(a);
         VLA_LAUNCH_CHECK();
+        return;
+    }
+    if (a.rope_cs) {
+        const int steps = (a.K + 63) / 64;
+        if (steps >= 32) run_skinny<16, true>(a, st);
+        else if (steps >= 8) run_skinny<8, true>(a, st);
+        else run_skinny<4, true>(a, st);
         return;
     }
     if (a.M <= 128) {

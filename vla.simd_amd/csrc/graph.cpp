@@ -267,7 +267,7 @@ static bool try_rowop_gemm(const Ctx& c, const DLinear& L, const RowQArgs& r, fl
 }
 
 static void gemm_q(const Ctx& c, const DLinear& L, const QAct& x, float* out, int ldo, int seq, int act,
-                   int acc, int n0, int n1) {
+                   int acc, int n0, int n1, const RopeEpi* rope = nullptr) {
     const vla_linear_i8& q = *L.q8;
     VLA_REQUIRE(x.ld == q.ldw(), "linear: quantized input laid out for another layer width");
     GemmArgs a{};
@@ -288,8 +288,13 @@ static void gemm_q(const Ctx& c, const DLinear& L, const QAct& x, float* out, in
     a.a_panel = x.panel ? 1 : 0;
     a.split_ws = c.split_ws;
     a.split_bytes = c.split_bytes;
+    if (rope) {
+        a.rope_cs = rope->cs;
+        a.rope_cols = rope->cols;
+        a.rope_hd = rope->hd;
+    }
     ProbeState& P = probe_state();
-    if (!P.on || (int)P.recs.size() >= P.max_records) {
+    if (rope || !P.on || (int)P.recs.size() >= P.max_records) {
         launch_gemm_i8(a, c.st);
         return;
     }
@@ -315,11 +320,45 @@ static void gemm_q(const Ctx& c, const DLinear& L, const QAct& x, float* out, in
     P.recs.push_back(std::move(rec));
 }
 
+// read at every call (graphs are recorded once per shape), so a test can build
+// one model each way in the same process
+static bool rope_fuse_on() {
+    const char* e = std::getenv("VLA_HIP_ROPE_FUSE");
+    return !(e && e[0] == '0');
+}
+
 void linear(const Ctx& c, const DLinear& L, const In& in, float* out, int ldo, int seq, int act, int acc,
-            int n0, int n1, float alpha) {
+            int n0, int n1, float alpha, const RopeEpi* rope) {
     if (n1 < 0) n1 = L.N;
     VLA_REQUIRE(0 <= n0 && n0 < n1 && n1 <= L.N, "linear: bad output row range");
     if (seq == 0) return;
+    if (rope) {
+        VLA_REQUIRE(rope->cs && rope->hd > 0 && rope->hd % 2 == 0 && rope->cols > 0 && rope->cols % rope->hd == 0 &&
+                        rope->cols <= n1 - n0,
+                    "linear: rotation of whole heads within the output columns");
+        const bool fused = rope_fuse_on() && !probe_on() && L.int8() && seq <= kPanelMaxRows && act == 0 &&
+                           acc == 0 && rope->hd % 16 == 0 && (reinterpret_cast<uintptr_t>(out) & 15) == 0 &&
+                           L.q8->ldw() % 16 == 0;
+        if (!fused) {
+            linear(c, L, in, out, ldo, seq, act, acc, n0, n1, alpha);
+            launch_rope_table(out, ldo, rope->cs, seq, rope->cols / rope->hd, rope->hd, c.st);
+            return;
+        }
+        if (in.deferred) {
+            VLA_REQUIRE(in.r.rows == seq && in.r.H == L.K && in.q.ld == L.ldq(),
+                        "linear: deferred row op made for another layer or row count");
+            rowq(in.r, c.st);
+            gemm_q(c, L, in.q, out, ldo, seq, 0, 0, n0, n1, rope);
+        } else if (in.quantized) {
+            gemm_q(c, L, in.q, out, ldo, seq, 0, 0, n0, n1, rope);
+        } else {
+            VLA_REQUIRE(in.f, "linear: no input");
+            const QAct s0 = c.slot(0, L.ldq(), seq);
+            quantize(c, s0, in.f, in.ldf, seq, L.K);
+            gemm_q(c, L, s0, out, ldo, seq, 0, 0, n0, n1, rope);
+        }
+        return;
+    }
     if (L.int8() && act == 4) {
         // the int8 epilogue has no silu: the GEMM, then silu over the block in
         // place (the reference's Linear::forward then silu(), diffusion.cpp:24-26)

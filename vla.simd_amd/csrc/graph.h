@@ -122,9 +122,21 @@ void quantize(const Ctx& c, const QAct& dst, const float* x, int ldx, int seq, i
 // 16 rows (a plain quantization: 64 rows, N <= 1024) when the shape allows it
 // (K <= 2048, out apart from the rows read; VLA_HIP_ROWOP_FUSE=0 turns this
 // off), else on its own first: the values are the same either way. acc != 0 adds into out (fmaf(alpha, v, out)
-// for fp32 layers; the int8 epilogue adds v, alpha must be 1).
+// for fp32 layers; the int8 epilogue adds v, alpha must be 1). With rope, the
+// rotated columns come out rotated: inside the skinny GEMM's epilogue for an
+// int8 layer of <= 128 rows without activation or accumulation (same floats
+// as the separate rotation; VLA_HIP_ROPE_FUSE=0 or the int8-step probe turn it
+// off), else by launch_rope_table after the layer.
+// A RoPE rotation of the output's first `cols` columns (heads of hd columns)
+// with the per-row (cos, sin) table cs [seq][hd / 2][2], as launch_rope_table
+// applies it in place.
+struct RopeEpi {
+    const double* cs = nullptr;
+    int cols = 0, hd = 0;
+};
+
 void linear(const Ctx& c, const DLinear& L, const In& in, float* out, int ldo, int seq, int act = 0,
-            int acc = 0, int n0 = 0, int n1 = -1, float alpha = 1.0f);
+            int acc = 0, int n0 = 0, int n1 = -1, float alpha = 1.0f, const RopeEpi* rope = nullptr);
 inline void linear(const Ctx& c, const DLinear& L, float* out, int ldo, const float* x, int ldx,
                    int seq, int act = 0, int acc = 0, int n0 = 0, int n1 = -1, float alpha = 1.0f) {
     In in;

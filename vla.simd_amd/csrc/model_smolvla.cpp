@@ -385,13 +385,13 @@ void SmolvlaTf::run(hipStream_t st) {
             if (w.self) {
                 float* buf = qkv_[L];
                 float* suf = buf + (size_t)np * W;
-                linear(c, w.q_or_qkv, hn, suf, W, C);
-                launch_rope_table(suf, W, rope_full_, C, enq_ + enkv_, ehd_, st);
+                const RopeEpi rf{rope_full_, (enq_ + enkv_) * ehd_, ehd_};  // q and k heads
+                linear(c, w.q_or_qkv, hn, suf, W, C, 0, 0, 0, -1, 1.0f, &rf);
                 attend(st, att_, QF, suf, W, buf + QF, W, buf + QF + KV, W, C, SK, enq_, enkv_, ehd_,
                        scale, dm);
             } else {
-                linear(c, w.q_or_qkv, hn, eq_, QF, C);
-                launch_rope_table(eq_, QF, rope_reb_, C, enq_, ehd_, st);
+                const RopeEpi rr{rope_reb_, enq_ * ehd_, ehd_};
+                linear(c, w.q_or_qkv, hn, eq_, QF, C, 0, 0, 0, -1, 1.0f, &rr);
                 attend(st, att_, QF, eq_, QF, ck_[L], KV, cv_[L], KV, C, np, enq_, enkv_, ehd_, scale, cm);
             }
             linear(c, w.o, eh_, EH, att_, QF, C, 0, 1);
