@@ -151,6 +151,16 @@ __global__ __launch_bounds__(256) void rowq_kernel(RowQArgs a) {
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= a.rows) return;  // wave-uniform
     const int H = a.H;
+    // the second output's addend, in flight with the row (zero past H)
+    float4 addv[NV];
+    if (a.add) {
+        const float* ar = a.add + (size_t)row * a.ld_add;
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int k = 4 * lane + 256 * i;
+            addv[i] = k < H ? *reinterpret_cast<const float4*>(ar + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
     float4 y[NV];
     rowop_apply<OP, NV>(y, a.x + (size_t)row * a.ldx, OP == 3 ? a.u + (size_t)row * a.ldu : nullptr, a.w, a.b,
                         a.eps, H, lane);
@@ -162,12 +172,11 @@ __global__ __launch_bounds__(256) void rowq_kernel(RowQArgs a) {
         int8_t* q = pass ? a.q2 : a.q;
         if (pass == 1) {
             if (!a.add) break;
-            const float* ar = a.add + (size_t)row * a.ld_add;
 #pragma unroll
             for (int i = 0; i < NV; i++) {
                 const int k = 4 * lane + 256 * i;
                 if (k < H) {
-                    const float4 p = *reinterpret_cast<const float4*>(ar + k);
+                    const float4 p = addv[i];
                     y[i] = make_float4(y[i].x + p.x, y[i].y + p.y, y[i].z + p.z, y[i].w + p.w);
                 }
             }
@@ -229,14 +238,19 @@ __global__ __launch_bounds__(256) void rowq_wide_kernel(RowQArgs a) {
         y[i] = k < H ? *reinterpret_cast<const float4*>(xr + k) : make_float4(0.f, 0.f, 0.f, 0.f);
     }
     if (OP == 3) {
+        // the up row loads all in flight before the first use
+        float4 u[NV];
 #pragma unroll
         for (int i = 0; i < NV; i++) {
             const int k = 4 * t + 1024 * i;
-            if (k < H) {
-                const float4 u = *reinterpret_cast<const float4*>(ur + k);
-                y[i] = make_float4(act_silu_gate(y[i].x, u.x), act_silu_gate(y[i].y, u.y),
-                                   act_silu_gate(y[i].z, u.z), act_silu_gate(y[i].w, u.w));
-            }
+            u[i] = k < H ? *reinterpret_cast<const float4*>(ur + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int k = 4 * t + 1024 * i;
+            if (k < H)
+                y[i] = make_float4(act_silu_gate(y[i].x, u[i].x), act_silu_gate(y[i].y, u[i].y),
+                                   act_silu_gate(y[i].z, u[i].z), act_silu_gate(y[i].w, u[i].w));
         }
     }
     if (a.out) {

@@ -66,53 +66,81 @@ __device__ __forceinline__ RowStat rowop_stat(const float4 (&y)[NV], float eps, 
     return st;
 }
 
-// y <- op(y) given the row's statistics: op 0 identity, 1 LayerNorm (w, b or
-// null), 2 RMSNorm (w), 3 silu_gate(y, ur). Weights and ur are 16-byte
-// aligned; elements past H stay zero.
+// The op's per-element operands at this lane's elements: op 1 w (p) and b
+// (q, when given), op 2 w (p), op 3 the up row ur (p); zero past H. Loaded
+// right after the row, so no load waits behind the row's reduction.
 template <int OP, int NV>
-__device__ __forceinline__ void rowop_finish(float4 (&y)[NV], RowStat st, const float* ur, const float* w,
-                                             const float* b, int H, int lane) {
-    if (OP == 1) {
+struct RowPar {
+    float4 p[(OP >= 1 && OP <= 3) ? NV : 1], q[OP == 1 ? NV : 1];
+};
+
+template <int OP, int NV>
+__device__ __forceinline__ void rowop_par(RowPar<OP, NV>& r, const float* ur, const float* w, const float* b, int H,
+                                          int lane) {
+    if constexpr (OP >= 1 && OP <= 3) {
+        const float* src = OP == 3 ? ur : w;
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int k = 4 * lane + 256 * i;
+            r.p[i] = k < H ? *reinterpret_cast<const float4*>(src + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+    if constexpr (OP == 1) {
+#pragma unroll
+        for (int i = 0; i < NV; i++) {
+            const int k = 4 * lane + 256 * i;
+            r.q[i] = b && k < H ? *reinterpret_cast<const float4*>(b + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    }
+}
+
+// y <- op(y) given the row's statistics and operands: op 0 identity, 1
+// LayerNorm (w, b or none), 2 RMSNorm (w), 3 silu_gate(y, ur). Elements past
+// H stay zero.
+template <int OP, int NV>
+__device__ __forceinline__ void rowop_finish_par(float4 (&y)[NV], RowStat st, const RowPar<OP, NV>& r, bool has_b,
+                                                 int H, int lane) {
+    if constexpr (OP == 1) {
         const double mean = st.mean;
         const float inv = st.inv;
 #pragma unroll
         for (int i = 0; i < NV; i++) {
             const int k = 4 * lane + 256 * i;
             if (k < H) {
-                const float4 wv = *reinterpret_cast<const float4*>(w + k);
-                float4 r;
-                if (b) {
-                    const float4 bv = *reinterpret_cast<const float4*>(b + k);
-                    r.x = fmaf((float)((double)y[i].x - mean) * inv, wv.x, bv.x);
-                    r.y = fmaf((float)((double)y[i].y - mean) * inv, wv.y, bv.y);
-                    r.z = fmaf((float)((double)y[i].z - mean) * inv, wv.z, bv.z);
-                    r.w = fmaf((float)((double)y[i].w - mean) * inv, wv.w, bv.w);
+                const float4 wv = r.p[i];
+                float4 o;
+                if (has_b) {
+                    const float4 bv = r.q[i];
+                    o.x = fmaf((float)((double)y[i].x - mean) * inv, wv.x, bv.x);
+                    o.y = fmaf((float)((double)y[i].y - mean) * inv, wv.y, bv.y);
+                    o.z = fmaf((float)((double)y[i].z - mean) * inv, wv.z, bv.z);
+                    o.w = fmaf((float)((double)y[i].w - mean) * inv, wv.w, bv.w);
                 } else {
-                    r.x = (float)((double)y[i].x - mean) * inv * wv.x;
-                    r.y = (float)((double)y[i].y - mean) * inv * wv.y;
-                    r.z = (float)((double)y[i].z - mean) * inv * wv.z;
-                    r.w = (float)((double)y[i].w - mean) * inv * wv.w;
+                    o.x = (float)((double)y[i].x - mean) * inv * wv.x;
+                    o.y = (float)((double)y[i].y - mean) * inv * wv.y;
+                    o.z = (float)((double)y[i].z - mean) * inv * wv.z;
+                    o.w = (float)((double)y[i].w - mean) * inv * wv.w;
                 }
-                y[i] = r;
+                y[i] = o;
             }
         }
-    } else if (OP == 2) {
+    } else if constexpr (OP == 2) {
         const float inv = st.inv;
 #pragma unroll
         for (int i = 0; i < NV; i++) {
             const int k = 4 * lane + 256 * i;
             if (k < H) {
-                const float4 wv = *reinterpret_cast<const float4*>(w + k);
+                const float4 wv = r.p[i];
                 y[i] = make_float4(y[i].x * inv * wv.x, y[i].y * inv * wv.y, y[i].z * inv * wv.z,
                                    y[i].w * inv * wv.w);
             }
         }
-    } else if (OP == 3) {
+    } else if constexpr (OP == 3) {
 #pragma unroll
         for (int i = 0; i < NV; i++) {
             const int k = 4 * lane + 256 * i;
             if (k < H) {
-                const float4 u = *reinterpret_cast<const float4*>(ur + k);
+                const float4 u = r.p[i];
                 y[i] = make_float4(act_silu_gate(y[i].x, u.x), act_silu_gate(y[i].y, u.y),
                                    act_silu_gate(y[i].z, u.z), act_silu_gate(y[i].w, u.w));
             }
@@ -120,11 +148,23 @@ __device__ __forceinline__ void rowop_finish(float4 (&y)[NV], RowStat st, const 
     }
 }
 
+// rowop_finish_par with the operands loaded here (weights and ur 16-byte
+// aligned).
+template <int OP, int NV>
+__device__ __forceinline__ void rowop_finish(float4 (&y)[NV], RowStat st, const float* ur, const float* w,
+                                             const float* b, int H, int lane) {
+    RowPar<OP, NV> r;
+    rowop_par<OP, NV>(r, ur, w, b, H, lane);
+    rowop_finish_par<OP, NV>(y, st, r, b != nullptr, H, lane);
+}
+
 template <int OP, int NV>
 __device__ __forceinline__ void rowop_apply(float4 (&y)[NV], const float* xr, const float* ur,
                                             const float* w, const float* b, float eps, int H, int lane) {
     rowop_load<NV>(y, xr, H, lane);
-    rowop_finish<OP, NV>(y, rowop_stat<OP, NV>(y, eps, H, lane), ur, w, b, H, lane);
+    RowPar<OP, NV> r;
+    rowop_par<OP, NV>(r, ur, w, b, H, lane);
+    rowop_finish_par<OP, NV>(y, rowop_stat<OP, NV>(y, eps, H, lane), r, b != nullptr, H, lane);
 }
 
 // This lane's part of the row's max |y| (elements past H are zero).
