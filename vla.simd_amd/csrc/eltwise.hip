@@ -67,6 +67,82 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(float* out, const float* x
     for (int k = lane; k < H; k += 64) orow[k] = xr[k] * inv * w[k];
 }
 
+// layernorm_kernel / rmsnorm_kernel for rows of at most 64 J floats: the
+// lane's elements (lane + 64 j, the same as the loops above visit) and its
+// weights are loaded once, all in flight together, and the sums run in the
+// same order, so the outputs are the loop kernels' bit for bit (the loops
+// wait for each load before issuing the next). out may alias x.
+template <int J>
+__global__ __launch_bounds__(256) void layernorm_reg_kernel(float* out, const float* x, const float* w,
+                                                            const float* b, int rows, int H, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float* xr = x + (size_t)row * H;
+    float* orow = out + (size_t)row * H;
+    float xv[J], wv[J], bv[J];
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const int k = lane + 64 * j;
+        xv[j] = k < H ? xr[k] : 0.0f;
+        wv[j] = k < H ? w[k] : 0.0f;
+        bv[j] = b && k < H ? b[k] : 0.0f;
+    }
+    double s = 0.0;
+#pragma unroll
+    for (int j = 0; j < J; j++)
+        if (lane + 64 * j < H) s += (double)xv[j];
+    const double mean = wave_sum_f64(s) / H;
+    double v = 0.0;
+#pragma unroll
+    for (int j = 0; j < J; j++)
+        if (lane + 64 * j < H) {
+            const double d = (double)xv[j] - mean;
+            v += d * d;
+        }
+    const double var = wave_sum_f64(v);
+    const float inv = (float)(1.0 / sqrt(var / H + (double)eps));
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const int k = lane + 64 * j;
+        if (k < H) {
+            const float c = (float)((double)xv[j] - mean);
+            orow[k] = b ? fmaf(c * inv, wv[j], bv[j]) : c * inv * wv[j];
+        }
+    }
+}
+
+template <int J>
+__global__ __launch_bounds__(256) void rmsnorm_reg_kernel(float* out, const float* x, const float* w, int rows,
+                                                          int H, float eps) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;
+    const float* xr = x + (size_t)row * H;
+    float* orow = out + (size_t)row * H;
+    float xv[J], wv[J];
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const int k = lane + 64 * j;
+        xv[j] = k < H ? xr[k] : 0.0f;
+        wv[j] = k < H ? w[k] : 0.0f;
+    }
+    double ss = 0.0;
+#pragma unroll
+    for (int j = 0; j < J; j++)
+        if (lane + 64 * j < H) {
+            const double d = (double)xv[j];
+            ss += d * d;
+        }
+    ss = wave_sum_f64(ss);
+    const float inv = (float)(1.0 / sqrt(ss / H + (double)eps));
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const int k = lane + 64 * j;
+        if (k < H) orow[k] = xv[j] * inv * wv[j];
+    }
+}
+
 template <int ACT>
 __global__ __launch_bounds__(256) void act_kernel(float* x, int64_t n) {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
@@ -326,7 +402,12 @@ void launch_layernorm(float* out, const float* x, const float* w, const float* b
                       int hidden, float eps, hipStream_t st) {
     VLA_REQUIRE(rows >= 0 && hidden > 0, "layernorm: need rows >= 0 and hidden > 0");
     if (rows == 0) return;
-    layernorm_kernel<<<(rows + 3) / 4, 256, 0, st>>>(out, x, w, b, rows, hidden, eps);
+    const int g = (rows + 3) / 4;
+    if (hidden <= 256) layernorm_reg_kernel<4><<<g, 256, 0, st>>>(out, x, w, b, rows, hidden, eps);
+    else if (hidden <= 512) layernorm_reg_kernel<8><<<g, 256, 0, st>>>(out, x, w, b, rows, hidden, eps);
+    else if (hidden <= 1024) layernorm_reg_kernel<16><<<g, 256, 0, st>>>(out, x, w, b, rows, hidden, eps);
+    else if (hidden <= 2048) layernorm_reg_kernel<32><<<g, 256, 0, st>>>(out, x, w, b, rows, hidden, eps);
+    else layernorm_kernel<<<g, 256, 0, st>>>(out, x, w, b, rows, hidden, eps);
     VLA_LAUNCH_CHECK();
 }
 
@@ -334,7 +415,12 @@ void launch_rmsnorm(float* out, const float* x, const float* w, int rows, int hi
                     hipStream_t st) {
     VLA_REQUIRE(rows >= 0 && hidden > 0, "rmsnorm: need rows >= 0 and hidden > 0");
     if (rows == 0) return;
-    rmsnorm_kernel<<<(rows + 3) / 4, 256, 0, st>>>(out, x, w, rows, hidden, eps);
+    const int g = (rows + 3) / 4;
+    if (hidden <= 256) rmsnorm_reg_kernel<4><<<g, 256, 0, st>>>(out, x, w, rows, hidden, eps);
+    else if (hidden <= 512) rmsnorm_reg_kernel<8><<<g, 256, 0, st>>>(out, x, w, rows, hidden, eps);
+    else if (hidden <= 1024) rmsnorm_reg_kernel<16><<<g, 256, 0, st>>>(out, x, w, rows, hidden, eps);
+    else if (hidden <= 2048) rmsnorm_reg_kernel<32><<<g, 256, 0, st>>>(out, x, w, rows, hidden, eps);
+    else rmsnorm_kernel<<<g, 256, 0, st>>>(out, x, w, rows, hidden, eps);
     VLA_LAUNCH_CHECK();
 }
 

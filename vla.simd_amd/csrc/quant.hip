@@ -145,6 +145,39 @@ __global__ __launch_bounds__(256) void quantize_rows_panel_kernel(const float* _
     }
 }
 
+// Rows of at most 256 * NV floats (VEC) in the panel layout: the row in
+// registers, every load in flight at once (the loop form above waits for each
+// load before issuing the next); same bytes and scale.
+template <int NV>
+__global__ __launch_bounds__(256) void quantize_rows_panel_reg(const float* __restrict__ x, int ldx,
+                                                               int8_t* __restrict__ xq, int mp,
+                                                               float* __restrict__ scale, int rows, int K) {
+    const int lane = threadIdx.x & 63;
+    const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (row >= rows) return;  // wave-uniform
+    const float* xr = x + (size_t)row * ldx;
+    float4 v[NV];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int k = 4 * lane + 256 * i;
+        v[i] = k < K ? *reinterpret_cast<const float4*>(xr + k) : make_float4(0.f, 0.f, 0.f, 0.f);
+        amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+    }
+    amax = wave_max_f32(amax);
+    const float s = row_scale(amax);
+    const float inv = 1.0f / s;
+    if (lane == 0) scale[row] = s;
+    const int k64 = (K + 63) & ~63;
+    int8_t* base = xq + (size_t)row * 64;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int k = 4 * lane + 256 * i;
+        if (k < k64)  // K % 4 == 0: a float4 is wholly inside [0, K) or wholly padding
+            *reinterpret_cast<uint32_t*>(base + (size_t)(k >> 6) * mp * 64 + (k & 63)) = k < K ? q8x4(v[i], inv) : 0u;
+    }
+}
+
 // Long rows (K >= 2048) in the panel layout: a block per row, the row held in
 // registers (NV float4 per thread), so every load is in flight at once and
 // the row is read once; the block max goes through LDS. Same bytes and scale
@@ -228,13 +261,19 @@ void launch_quantize_rows_panel(const float* x, int ldx, int8_t* xq, float* scal
     const int mp = panel_rows(rows);
     const dim3 grid((rows + 3) / 4), block(256);
     const bool vec = K % 4 == 0 && ldx % 4 == 0 && aligned(x, 16);
-    const int nv = ((K + 63) / 64 * 64 + 1023) / 1024;  // float4 per thread over [0, K64)
+    const int nv = ((K + 63) / 64 * 64 + 1023) / 1024;  // float4 per thread over [0, K64), block per row
+    const int nvw = ((K + 63) / 64 * 64 + 255) / 256;   // float4 per lane over [0, K64), wave per row
     if (vec && K >= 2048 && nv <= 16) {
         // one block per row: 64 x 12288 (SigLIP's projection input) 25.9 -> 6.6 us
         if (nv <= 4) quantize_rows_panel_wide<4><<<rows, 256, 0, st>>>(x, ldx, xq, mp, scale, K);
         else if (nv <= 8) quantize_rows_panel_wide<8><<<rows, 256, 0, st>>>(x, ldx, xq, mp, scale, K);
         else if (nv <= 12) quantize_rows_panel_wide<12><<<rows, 256, 0, st>>>(x, ldx, xq, mp, scale, K);
         else quantize_rows_panel_wide<16><<<rows, 256, 0, st>>>(x, ldx, xq, mp, scale, K);
+    } else if (vec && nvw <= 8) {
+        if (nvw <= 1) quantize_rows_panel_reg<1><<<grid, block, 0, st>>>(x, ldx, xq, mp, scale, rows, K);
+        else if (nvw <= 2) quantize_rows_panel_reg<2><<<grid, block, 0, st>>>(x, ldx, xq, mp, scale, rows, K);
+        else if (nvw <= 4) quantize_rows_panel_reg<4><<<grid, block, 0, st>>>(x, ldx, xq, mp, scale, rows, K);
+        else quantize_rows_panel_reg<8><<<grid, block, 0, st>>>(x, ldx, xq, mp, scale, rows, K);
     } else if (vec)
         quantize_rows_panel_kernel<true><<<grid, block, 0, st>>>(x, ldx, xq, mp, scale, rows, K);
     else
