@@ -233,9 +233,11 @@ static GemmArgs gemm_args(const DLinear& L, float* out, int ldo, int seq, int ac
 // kernel beats row kernel + GEMM only while each SIMD has a row or so: on
 // MI355X at 16 rows it saved 4 us of 9.7 (RMSNorm, N = 4096, K = 720); at 50
 // rows it lost 3 us (RMSNorm, N = 4096) to 22 us (silu_gate, K = 2048).
-// The identity op (quantize only) is cheap enough to repeat up to 64 rows
-// on a narrow output: 50 x 720 x 960 ran 8.6 us fused against 9.7 us as
-// quantize + GEMM. VLA_HIP_ROWOP_FUSE=0 turns it off.
+// The identity op (quantize only) was once worth repeating up to 64 rows
+// (50 x 720 x 960: 8.6 us fused against 9.7 us as quantize + GEMM); since the
+// panel quantizer keeps its row in registers, the separate pair wins there
+// too (SmolVLA 8.54 -> 8.18 ms per chunk, same box), so every op fuses only up
+// to 16 rows. VLA_HIP_ROWOP_FUSE=0 turns it off.
 constexpr int kRowopFuseMaxRows = 16;
 
 static bool fuse_rowop(int op, int seq, int K, int N) {
@@ -243,8 +245,8 @@ static bool fuse_rowop(int op, int seq, int K, int N) {
         const char* e = std::getenv("VLA_HIP_ROWOP_FUSE");
         return !(e && e[0] == '0');
     }();
-    const bool cheap = seq <= kRowopFuseMaxRows || (op == 0 && seq <= 64 && N <= 1024);
-    return on && !probe_on() && cheap && rowop_gemm_fits(op, seq, K);
+    (void)N;
+    return on && !probe_on() && seq <= kRowopFuseMaxRows && rowop_gemm_fits(op, seq, K);
 }
 
 static bool overlaps(const float* p, size_t pn, const float* q, size_t qn) {

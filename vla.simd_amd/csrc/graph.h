@@ -119,7 +119,7 @@ void quantize(const Ctx& c, const QAct& dst, const float* x, int ldx, int seq, i
 // out[:, n0:n1] (+)= act(x W[n0:n1]^T + b). An int8 layer takes in.q when
 // in.quantized, else quantizes in.f into slot 0; a deferred row op, or the
 // quantization of fp32 rows, runs inside the GEMM (gemm_i8_rowop) for at most
-// 16 rows (a plain quantization: 64 rows, N <= 1024) when the shape allows it
+// 16 rows when the shape allows it
 // (K <= 2048, out apart from the rows read; VLA_HIP_ROWOP_FUSE=0 turns this
 // off), else on its own first: the values are the same either way. acc != 0 adds into out (fmaf(alpha, v, out)
 // for fp32 layers; the int8 epilogue adds v, alpha must be 1). With rope, the

@@ -337,18 +337,33 @@ __global__ __launch_bounds__(W * 64) void linear_f32_skinny(float* __restrict__ 
     v4f acc[FM];
 #pragma unroll
     for (int i = 0; i < FM; i++) acc[i] = v4f{0.f, 0.f, 0.f, 0.f};
-    for (int k16 = wave * 16; k16 < K; k16 += W * 16) {
-        const int k = k16 + 4 * g;
-        const float4 b = load4(brow, k);
-        float4 a[FM];
+    // P of the wave's K steps per round: all their loads are issued before the
+    // first MFMA (one wait per round instead of one per step); the MFMAs run
+    // in the same step order, so the sums are the same
+    constexpr int P = FM <= 4 ? 4 : 2;
+    for (int k16r = wave * 16; k16r < K; k16r += P * W * 16) {
+        float4 b[P], a[P][FM];
 #pragma unroll
-        for (int i = 0; i < FM; i++) a[i] = load4(arow[i], k);
+        for (int p = 0; p < P; p++) {
+            const int k16 = k16r + p * W * 16;
+            if (k16 < K) {  // wave-uniform
+                const int k = k16 + 4 * g;
+                b[p] = load4(brow, k);
 #pragma unroll
-        for (int i = 0; i < FM; i++) {
-            acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].x, b.x, acc[i], 0, 0, 0);
-            acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].y, b.y, acc[i], 0, 0, 0);
-            acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].z, b.z, acc[i], 0, 0, 0);
-            acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[i].w, b.w, acc[i], 0, 0, 0);
+                for (int i = 0; i < FM; i++) a[p][i] = load4(arow[i], k);
+            }
+        }
+#pragma unroll
+        for (int p = 0; p < P; p++) {
+            if (k16r + p * W * 16 < K) {
+#pragma unroll
+                for (int i = 0; i < FM; i++) {
+                    acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[p][i].x, b[p].x, acc[i], 0, 0, 0);
+                    acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[p][i].y, b[p].y, acc[i], 0, 0, 0);
+                    acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[p][i].z, b[p].z, acc[i], 0, 0, 0);
+                    acc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[p][i].w, b[p].w, acc[i], 0, 0, 0);
+                }
+            }
         }
     }
 #pragma unroll
