@@ -430,3 +430,45 @@ def test_dense_linear_i8_dev_caller_scratch(vla, orc, torch_cuda, seq, N, K, act
         assert same_bits(got, want)
     else:
         assert max_rel(got, want) <= 2e-6
+
+
+# ------------------------------------------------------------- row groups --
+
+@pytest.mark.parametrize("groups", ["1", "2", "3", "4", "8"])
+@pytest.mark.parametrize("seq,N,K", [(100, 960, 2560), (50, 720, 960), (128, 48, 1027), (37, 200, 4100),
+                                     (17, 64, 64), (1, 16, 3)])
+def test_skinny_row_groups_bitexact(vla, orc, torch_cuda, groups, seq, N, K):
+    """The skinny kernel split into row groups (each block: 16 columns x its
+    16-row fragments; fragments past M repeat the last and are never stored)
+    gives the oracle's outputs bit for bit, row-major, panel and split-K."""
+    torch = torch_cuda
+    x, W, b = _case(orc, seq, N, K)
+    xq, sa = orc.quantize_act_i8(x)
+    Wq, ws = orc.quantize_weights_i8(W)
+    ld = (K + 63) // 64 * 64
+    Xp = np.zeros((seq, ld), np.int8)
+    Xp[:, :xq.shape[1]] = xq
+    Wp = np.zeros((N, ld), np.int8)
+    Wp[:, :Wq.shape[1]] = Wq
+    dev = torch.device("cuda")
+    Xd, Wd = torch.from_numpy(Xp).to(dev), torch.from_numpy(Wp).to(dev)
+    sad, wsd, bd = torch.from_numpy(sa).to(dev), torch.from_numpy(ws).to(dev), torch.from_numpy(b).to(dev)
+    xd = torch.from_numpy(x).to(dev)
+    xpan = torch.empty((vla.i8_panel_bytes(seq, K),), dtype=torch.int8, device=dev)
+    span = torch.empty(seq, dtype=torch.float32, device=dev)
+    nsplit = vla.gemm_i8_split_bytes(seq, N, K)
+    work = torch.empty(max(nsplit, 16), dtype=torch.uint8, device=dev)
+    base = np.full((seq, N), 0.25, np.float32)
+    outs = [torch.from_numpy(base.copy()).to(dev) for _ in range(3)]
+    os.environ["VLA_HIP_SKINNY_R"] = groups
+    try:
+        vla.dense_linear_i8_pre_dev(outs[0], Xd, sad, Wd, wsd, bd, K, act=1, accumulate=1)
+        vla.quantize_act_i8_panel_dev(xd, xpan, span)
+        vla.dense_linear_i8_panel_dev(outs[1], xpan, span, Wd, wsd, bd, K, act=1, accumulate=1)
+        vla.dense_linear_i8_pre_split_dev(outs[2], Xd, sad, Wd, wsd, bd, K, work, act=1, accumulate=1)
+        torch.cuda.synchronize()
+    finally:
+        del os.environ["VLA_HIP_SKINNY_R"]
+    want = (base + orc.apply_act(orc.dense_linear_i8_pre(xq, sa, Wq, ws, b, K), 1)).astype(np.float32)
+    for i, o in enumerate(outs):
+        assert same_bits(o.cpu().numpy(), want), f"form {i} with {groups} row groups differs from the oracle"

@@ -144,3 +144,19 @@ def test_fits_and_rejects(vla, torch_cuda):
     with pytest.raises(vla.VlaError) as e:
         vla.rowop_linear_i8_dev(out, 1, x, Wq, ws, None, w=ws)
     assert e.value.status == vla.VLA_ERR_ARG
+
+
+@pytest.mark.parametrize("groups", ["1", "2", "3", "8"])
+@pytest.mark.parametrize("seq,N,K,op", [(50, 720, 960, 0), (100, 512, 512, 2), (128, 96, 1024, 3),
+                                        (33, 100, 260, 2), (50, 720, 2048, 3)])
+def test_fused_row_groups(vla, orc, torch_cuda, groups, seq, N, K, op):
+    """Row groups (each block applies the row op to its own 16 x FM rows and
+    multiplies them by its 16 columns) give the two-kernel path's outputs bit
+    for bit, whatever the forced group count."""
+    import os
+    os.environ["VLA_HIP_SKINNY_R"] = groups
+    try:
+        r = _run_both(vla, orc, torch_cuda, seq, N, K, op, act=1, accumulate=1)
+    finally:
+        del os.environ["VLA_HIP_SKINNY_R"]
+    assert same_bits(r["fused"], r["two"]), f"{groups} row groups differ from the two-kernel path"

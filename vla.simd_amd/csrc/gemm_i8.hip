@@ -749,6 +749,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
     const int lane = tid & 63, wave = tid >> 6;
     const int n0 = blockIdx.x * 16;
     const int K = a.K;
+    // row group blockIdx.z: 16-row fragments f0 .. f0 + FM - 1 (fragments past
+    // the last one repeat it; their rows are >= M and never stored)
+    const int f0 = blockIdx.z * FM, nfrag = (a.M + 15) >> 4;
 
     // A fragment i of k-step s is at arow[i] + s * astep: row-major rows
     // (clamped to the last row), or the panel layout, where the fragment's 16
@@ -758,8 +761,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
     const int8_t* arow[FM];
 #pragma unroll
     for (int i = 0; i < FM; i++) {
-        const int m = i * 16 + r16 < a.M ? i * 16 + r16 : a.M - 1;
-        arow[i] = a.a_panel ? a.A + (size_t)(i * 16 + r16) * 64 + kq : a.A + (size_t)m * a.lda + kq;
+        const int row = (f0 + i < nfrag ? f0 + i : nfrag - 1) * 16 + r16;
+        const int m = row < a.M ? row : a.M - 1;
+        arow[i] = a.a_panel ? a.A + (size_t)row * 64 + kq : a.A + (size_t)m * a.lda + kq;
     }
     // output column of block lane c (16 consecutive columns, or ROPE pairs)
     const bool rotb = ROPE && n0 < a.rope_cols;
@@ -784,7 +788,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
     for (int j = 0; j < EPT; j++) {
         const int e = tid + j * NT;
         const int l = e & 63, r = (e >> 6) & 3, i = e >> 8;
-        int mm = 16 * i + 4 * (l >> 4) + r, nn = col(l & 15);
+        int mm = 16 * (f0 + i) + 4 * (l >> 4) + r, nn = col(l & 15);
         const bool ok = e < FM * 256 && mm < a.M && nn < a.N;
         mm = ok ? mm : 0;
         nn = ok ? nn : 0;
@@ -875,7 +879,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
 #pragma unroll
         for (int w = 0; w < WAVES; w++) v += part[w * FM * 256 + e];
         const int l = e & 63, r = (e >> 6) & 3, i = e >> 8;
-        const int mm = 16 * i + 4 * (l >> 4) + r, nn = col(l & 15);
+        const int mm = 16 * (f0 + i) + 4 * (l >> 4) + r, nn = col(l & 15);
         if (mm >= a.M || nn >= a.N) continue;
         if (a.acc32) {
             a.acc32[(size_t)mm * a.N + nn] = v;
@@ -941,6 +945,7 @@ __global__ __launch_bounds__(1024) void gemm_i8_rowop(RowQArgs r, GemmArgs a) {
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int M = a.M, K = a.K, n0 = blockIdx.x * 16;
+    const int m0 = blockIdx.y * MP;  // row group: rows m0 .. m0 + MP - 1 (local rows in LDS)
     const int ns = (K + 63) >> 6, full = K >> 6;
     int8_t* panel = lds;
     int32_t* part = reinterpret_cast<int32_t*>(lds);
@@ -967,7 +972,7 @@ __global__ __launch_bounds__(1024) void gemm_i8_rowop(RowQArgs r, GemmArgs a) {
     for (int j = 0; j < EPT; j++) {
         const int e = tid + j * NT;
         const int l = e & 63, rr = (e >> 6) & 3, i = e >> 8;
-        int mm = 16 * i + 4 * (l >> 4) + rr, nn = n0 + (l & 15);
+        int mm = m0 + 16 * i + 4 * (l >> 4) + rr, nn = n0 + (l & 15);
         const bool ok = e < FM * 256 && mm < M && nn < a.N;
         mm = ok ? mm : 0;
         nn = ok ? nn : 0;
@@ -986,7 +991,7 @@ __global__ __launch_bounds__(1024) void gemm_i8_rowop(RowQArgs r, GemmArgs a) {
         StaticFor<0, RB>::run([&](auto jc) {
             constexpr int jj = decltype(jc)::value;
             row[jj] = wave + WAVES * (j0 + jj);
-            const int rc = row[jj] < M ? row[jj] : M - 1;  // rows past M: a duplicate, never stored
+            const int rc = m0 + row[jj] < M ? m0 + row[jj] : M - 1;  // rows past M: a duplicate, never stored
             rowop_load<NV>(y[jj], r.x + (size_t)rc * r.ldx, K, lane);
         });
         StaticFor<0, RB>::run([&](auto jc) {
@@ -995,7 +1000,7 @@ __global__ __launch_bounds__(1024) void gemm_i8_rowop(RowQArgs r, GemmArgs a) {
         });
         StaticFor<0, RB>::run([&](auto jc) {
             constexpr int jj = decltype(jc)::value;
-            const int rc = row[jj] < M ? row[jj] : M - 1;
+            const int rc = m0 + row[jj] < M ? m0 + row[jj] : M - 1;
             rowop_finish<OP, NV>(y[jj], st[jj], OP == 3 ? r.u + (size_t)rc * r.ldu : nullptr, r.w, r.b, K,
                                  lane);
             am[jj] = rowop_amax<NV>(y[jj], K, lane);
@@ -1006,7 +1011,7 @@ __global__ __launch_bounds__(1024) void gemm_i8_rowop(RowQArgs r, GemmArgs a) {
         });
         StaticFor<0, RB>::run([&](auto jc) {
             constexpr int jj = decltype(jc)::value;
-            if (row[jj] < M) {
+            if (m0 + row[jj] < M) {
                 const float s = row_scale(am[jj]);
                 const float inv = 1.0f / s;
                 if (lane == 0) sa[row[jj]] = s;
@@ -1052,10 +1057,10 @@ __global__ __launch_bounds__(1024) void gemm_i8_rowop(RowQArgs r, GemmArgs a) {
         int32_t v = 0;
         for (int w = 0; w < nw; w++) v += part[w * FM * 256 + e];
         const int l = e & 63, rr = (e >> 6) & 3, i = e >> 8;
-        const int mm = 16 * i + 4 * (l >> 4) + rr, nn = n0 + (l & 15);
+        const int mm = m0 + 16 * i + 4 * (l >> 4) + rr, nn = n0 + (l & 15);
         if (mm >= M || nn >= a.N) continue;
         const float p = (float)v * ews[j];
-        float o = fmaf(p, sa[mm], eb[j]);
+        float o = fmaf(p, sa[mm - m0], eb[j]);
         switch (a.act) {
         case 1: o = act_relu(o); break;
         case 2: o = act_gelu_tanh(o); break;
@@ -1189,11 +1194,32 @@ void run_lds(const GemmArgs& a, hipStream_t st) {
     VLA_LAUNCH_CHECK();
 }
 
+// Row groups of the skinny kernel: each block owns 16 columns and FM of the
+// M / 16 row fragments, so a narrow output (N / 16 well under the CU count)
+// still spreads over the chip and each block reads only its rows of A.
+// VLA_HIP_SKINNY_R=<groups> forces a count (A/B runs; values unchanged).
+// Default: the fewest groups that give every CU a block. Measured on MI355X
+// (graph replays, forced counts 1/2/3/4/8): 100x2560x960 9.94 -> 5.29 us
+// (4 groups), 50x720x960 4.09 -> 3.06 (4), 50x2048x720 6.12 -> 4.33 (4),
+// 100x512x3200 5.20 -> 4.82 (2); at N = 4096 (256 column blocks) one group
+// is fastest, since more only re-read the weights.
+int skinny_row_groups(int M, int N, int S) {
+    const int nfrag = (M + 15) / 16;
+    const char* env = std::getenv("VLA_HIP_SKINNY_R");
+    const long blocks = (long)((N + 15) / 16) * (S > 1 ? S : 1);
+    int g = (int)((kCUs + blocks - 1) / blocks);
+    if (env && *env) g = std::atoi(env);
+    g = g < 1 ? 1 : g > nfrag ? nfrag : g;
+    const int fm = (nfrag + g - 1) / g;
+    return (nfrag + fm - 1) / fm;
+}
+
 template <int WAVES, bool ROPE = false>
-void run_skinny(const GemmArgs& a, hipStream_t st, int splits = 1) {
-    const dim3 nb((a.N + 15) / 16, splits);
+void run_skinny(const GemmArgs& a, hipStream_t st, int splits = 1, int groups = 1) {
+    const int fm = ((a.M + 15) / 16 + groups - 1) / groups;
+    const dim3 nb((a.N + 15) / 16, splits, groups);
     constexpr int W8 = WAVES < 8 ? WAVES : 8;  // FM > 4 keeps the partial tiles within 64 KiB
-    switch ((a.M + 15) / 16) {
+    switch (fm) {
     case 1: gemm_i8_skinny<1, WAVES, ROPE><<<nb, WAVES * 64, 0, st>>>(a); break;
     case 2: gemm_i8_skinny<2, WAVES, ROPE><<<nb, WAVES * 64, 0, st>>>(a); break;
     case 3: gemm_i8_skinny<3, WAVES, ROPE><<<nb, WAVES * 64, 0, st>>>(a); break;
@@ -1215,13 +1241,27 @@ void run_rowop(const RowQArgs& r, const GemmArgs& a, hipStream_t st) {
     }();
     (void)attr;
     const int lds = rowop_lds_main(FM, a.K) + 16 * FM * 4;
-    gemm_i8_rowop<OP, NV, FM><<<(a.N + 15) / 16, 1024, lds, st>>>(r, a);
+    const dim3 grid((a.N + 15) / 16, (a.M + 16 * FM - 1) / (16 * FM));
+    gemm_i8_rowop<OP, NV, FM><<<grid, 1024, lds, st>>>(r, a);
     VLA_LAUNCH_CHECK();
+}
+
+// Rows per block of the fused row-op GEMM (16 x FM, FM in 1, 2, 4, 8): as the
+// skinny kernel's row groups, the fewest groups that give every CU a block
+// (each block then applies the row op to its own rows only), or
+// VLA_HIP_SKINNY_R=<groups>.
+int rowop_group_fm(int M, int N) {
+    const char* env = std::getenv("VLA_HIP_SKINNY_R");
+    const int nb = (N + 15) / 16;
+    int g = (kCUs + nb - 1) / nb;
+    if (env && *env) g = std::atoi(env);
+    g = g < 1 ? 1 : g;
+    return rowop_fm((M + g - 1) / g);
 }
 
 template <int OP, int NV>
 void run_rowop_fm(const RowQArgs& r, const GemmArgs& a, hipStream_t st) {
-    switch (rowop_fm(a.M)) {
+    switch (rowop_group_fm(a.M, a.N)) {
     case 1: run_rowop<OP, NV, 1>(r, a, st); break;
     case 2: run_rowop<OP, NV, 2>(r, a, st); break;
     case 4: run_rowop<OP, NV, 4>(r, a, st); break;
@@ -1414,10 +1454,10 @@ void launch_gemm_i8(const GemmArgs& a, hipStream_t st) {
         return;
     }
     if (a.rope_cs) {
-        const int steps = (a.K + 63) / 64;
-        if (steps >= 32) run_skinny<16, true>(a, st);
-        else if (steps >= 8) run_skinny<8, true>(a, st);
-        else run_skinny<4, true>(a, st);
+        const int steps = (a.K + 63) / 64, g = skinny_row_groups(a.M, a.N, 1);
+        if (steps >= 32) run_skinny<16, true>(a, st, 1, g);
+        else if (steps >= 8) run_skinny<8, true>(a, st, 1, g);
+        else run_skinny<4, true>(a, st, 1, g);
         return;
     }
     if (a.M <= 128) {
@@ -1428,10 +1468,10 @@ void launch_gemm_i8(const GemmArgs& a, hipStream_t st) {
         }
         GemmArgs s = a;
         s.kchunk = p.kchunk;
-        const int steps = ((p.S > 1 ? p.kchunk : a.K) + 63) / 64;
-        if (steps >= 32) run_skinny<16>(s, st, p.S);
-        else if (steps >= 8) run_skinny<8>(s, st, p.S);
-        else run_skinny<4>(s, st, p.S);
+        const int steps = ((p.S > 1 ? p.kchunk : a.K) + 63) / 64, g = skinny_row_groups(a.M, a.N, p.S);
+        if (steps >= 32) run_skinny<16>(s, st, p.S, g);
+        else if (steps >= 8) run_skinny<8>(s, st, p.S, g);
+        else run_skinny<4>(s, st, p.S, g);
         if (p.S > 1) {
             const bool vec = a.N % 4 == 0 && a.ldo % 4 == 0 && aligned(a.out, 16);
             const int64_t work = (int64_t)a.M * a.N / (vec ? 4 : 1);
