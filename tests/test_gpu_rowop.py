@@ -154,9 +154,9 @@ def test_fused_row_groups(vla, orc, torch_cuda, groups, seq, N, K, op):
     multiplies them by its 16 columns) give the two-kernel path's outputs bit
     for bit, whatever the forced group count."""
     import os
-    os.environ["VLA_HIP_SKINNY_R"] = groups
+    os.environ["VLA_HIP_SKINNY_R"] = os.environ["VLA_HIP_ROWOP_R"] = groups
     try:
         r = _run_both(vla, orc, torch_cuda, seq, N, K, op, act=1, accumulate=1)
     finally:
-        del os.environ["VLA_HIP_SKINNY_R"]
+        del os.environ["VLA_HIP_SKINNY_R"], os.environ["VLA_HIP_ROWOP_R"]
     assert same_bits(r["fused"], r["two"]), f"{groups} row groups differ from the two-kernel path"

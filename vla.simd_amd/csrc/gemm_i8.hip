@@ -1249,9 +1249,9 @@ void run_rowop(const RowQArgs& r, const GemmArgs& a, hipStream_t st) {
 // Rows per block of the fused row-op GEMM (16 x FM, FM in 1, 2, 4, 8): as the
 // skinny kernel's row groups, the fewest groups that give every CU a block
 // (each block then applies the row op to its own rows only), or
-// VLA_HIP_SKINNY_R=<groups>.
+// VLA_HIP_ROWOP_R=<groups>.
 int rowop_group_fm(int M, int N) {
-    const char* env = std::getenv("VLA_HIP_SKINNY_R");
+    const char* env = std::getenv("VLA_HIP_ROWOP_R");
     const int nb = (N + 15) / 16;
     int g = (kCUs + nb - 1) / nb;
     if (env && *env) g = std::atoi(env);

@@ -237,7 +237,9 @@ static GemmArgs gemm_args(const DLinear& L, float* out, int ldo, int seq, int ac
 // (50 x 720 x 960: 8.6 us fused against 9.7 us as quantize + GEMM); since the
 // panel quantizer keeps its row in registers, the separate pair wins there
 // too (SmolVLA 8.54 -> 8.18 ms per chunk, same box), so every op fuses only up
-// to 16 rows. VLA_HIP_ROWOP_FUSE=0 turns it off.
+// to 16 rows. Fusing wherever the kernel's row groups hold 16 rows (the 50-row
+// o- and down-projections, N = 720, 4 groups) was slower as well: 7.33 ->
+// 8.00 ms per chunk. VLA_HIP_ROWOP_FUSE=0 turns it off.
 constexpr int kRowopFuseMaxRows = 16;
 
 static bool fuse_rowop(int op, int seq, int K, int N) {
