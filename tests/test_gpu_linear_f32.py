@@ -73,3 +73,21 @@ def test_dense_linear_dev_epilogues(vla, torch_cuda, M, K, N):
     vla.dense_linear_dev(out, dx, dW, db, accumulate=1, alpha=-0.1)
     torch.cuda.synchronize()
     assert _rel(out.cpu().numpy(), base + (-0.1) * exact) <= 1e-5
+
+
+@pytest.mark.parametrize("groups", ["1", "2", "3", "8"])
+@pytest.mark.parametrize("M,K,N", [(50, 1440, 720), (100, 512, 14), (128, 512, 64), (17, 64, 16)])
+def test_skinny_row_groups_identical(vla, M, K, N):
+    """Row groups of the M <= 128 kernel (16 x FM rows per block) leave every
+    output's sum unchanged: identical to one group, and within the bar."""
+    import os
+    x, W, b = _case(M, K, N)
+    os.environ["VLA_HIP_SKINNY_R"] = "1"
+    try:
+        one = vla.dense_linear(x, W, b)
+        os.environ["VLA_HIP_SKINNY_R"] = groups
+        got = vla.dense_linear(x, W, b)
+    finally:
+        del os.environ["VLA_HIP_SKINNY_R"]
+    assert np.array_equal(got.view(np.uint32), one.view(np.uint32))
+    assert _rel(got, x.astype(np.float64) @ W.astype(np.float64).T + b) <= 1e-5

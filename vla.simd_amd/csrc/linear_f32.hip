@@ -397,7 +397,9 @@ void launch_skinny_fm(float* out, int ldo, const float* x, int ldx, const float*
                       const float* bias, int M, int N, int K, int act, int accumulate, float alpha,
                       hipStream_t st) {
     const int steps = (K + 15) / 16;
-    const int blocks = (N + 15) / 16;
+    // row groups of 16 * FM rows (grid.y): as the int8 skinny GEMM, the fewest
+    // that give every CU a block; each output's sum is unchanged
+    const dim3 blocks((N + 15) / 16, (M + 16 * FM - 1) / (16 * FM));
     // about four K steps per wave, at most 8 waves
     const int w = steps >= 32 ? 8 : steps >= 16 ? 4 : steps >= 8 ? 2 : 1;
     switch (w) {
@@ -412,7 +414,11 @@ template <bool VEC>
 void launch_skinny(float* out, int ldo, const float* x, int ldx, const float* W, int ldw,
                    const float* bias, int M, int N, int K, int act, int accumulate, float alpha,
                    hipStream_t st) {
-    switch ((M + 15) / 16) {
+    const int nfrag = (M + 15) / 16, nb = (N + 15) / 16;
+    int g = (256 + nb - 1) / nb;  // 256 CUs
+    if (const char* e = std::getenv("VLA_HIP_SKINNY_R")) g = *e ? std::atoi(e) : g;
+    g = g < 1 ? 1 : g > nfrag ? nfrag : g;
+    switch ((nfrag + g - 1) / g) {
     case 1: launch_skinny_fm<1, VEC>(out, ldo, x, ldx, W, ldw, bias, M, N, K, act, accumulate, alpha, st); break;
     case 2: launch_skinny_fm<2, VEC>(out, ldo, x, ldx, W, ldw, bias, M, N, K, act, accumulate, alpha, st); break;
     case 3: launch_skinny_fm<3, VEC>(out, ldo, x, ldx, W, ldw, bias, M, N, K, act, accumulate, alpha, st); break;
