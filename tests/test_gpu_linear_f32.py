@@ -77,7 +77,7 @@ def test_dense_linear_dev_epilogues(vla, torch_cuda, M, K, N):
 
 @pytest.mark.parametrize("groups", ["1", "2", "3", "8"])
 @pytest.mark.parametrize("M,K,N", [(50, 1440, 720), (100, 512, 14), (128, 512, 64), (17, 64, 16)])
-def test_skinny_row_groups_identical(vla, M, K, N):
+def test_skinny_row_groups_identical(vla, groups, M, K, N):
     """Row groups of the M <= 128 kernel (16 x FM rows per block) leave every
     output's sum unchanged: identical to one group, and within the bar."""
     import os
