@@ -175,6 +175,9 @@ void launch_rowq(const RowQArgs& a, hipStream_t st);
 // says whether op and shape are supported (M <= 128, K % 4 == 0, K <= 2048,
 // the panel within LDS).
 bool rowop_gemm_fits(int op, int M, int K);
+// Rows each block of the fused kernel applies the row op to (16 x FM: its row
+// group of M for an output N columns wide).
+int rowop_gemm_block_rows(int M, int N);
 void launch_gemm_i8_rowop(const RowQArgs& r, const GemmArgs& g, hipStream_t st);
 
 // conv.hip: conv2d_i8 (NHWC x [H, Wd, Cin] -> out [Hout, Wout, Cout]) as

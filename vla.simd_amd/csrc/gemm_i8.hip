@@ -1202,12 +1202,15 @@ void run_lds(const GemmArgs& a, hipStream_t st) {
 // (graph replays, forced counts 1/2/3/4/8): 100x2560x960 9.94 -> 5.29 us
 // (4 groups), 50x720x960 4.09 -> 3.06 (4), 50x2048x720 6.12 -> 4.33 (4),
 // 100x512x3200 5.20 -> 4.82 (2); at N = 4096 (256 column blocks) one group
-// is fastest, since more only re-read the weights.
-int skinny_row_groups(int M, int N, int S) {
+// is fastest over K = 4096 (50 rows: 9.85 us, 12.19 with two), since more
+// only re-read the weights, but two win over a short K (50x720x4096 4.63 ->
+// 4.43 us).
+int skinny_row_groups(int M, int N, int K, int S) {
     const int nfrag = (M + 15) / 16;
     const char* env = std::getenv("VLA_HIP_SKINNY_R");
     const long blocks = (long)((N + 15) / 16) * (S > 1 ? S : 1);
     int g = (int)((kCUs + blocks - 1) / blocks);
+    if (K <= 1024 && g < 2) g = 2;
     if (env && *env) g = std::atoi(env);
     g = g < 1 ? 1 : g > nfrag ? nfrag : g;
     const int fm = (nfrag + g - 1) / g;
@@ -1454,7 +1457,7 @@ void launch_gemm_i8(const GemmArgs& a, hipStream_t st) {
         return;
     }
     if (a.rope_cs) {
-        const int steps = (a.K + 63) / 64, g = skinny_row_groups(a.M, a.N, 1);
+        const int steps = (a.K + 63) / 64, g = skinny_row_groups(a.M, a.N, a.K, 1);
         if (steps >= 32) run_skinny<16, true>(a, st, 1, g);
         else if (steps >= 8) run_skinny<8, true>(a, st, 1, g);
         else run_skinny<4, true>(a, st, 1, g);
@@ -1468,7 +1471,7 @@ void launch_gemm_i8(const GemmArgs& a, hipStream_t st) {
         }
         GemmArgs s = a;
         s.kchunk = p.kchunk;
-        const int steps = ((p.S > 1 ? p.kchunk : a.K) + 63) / 64, g = skinny_row_groups(a.M, a.N, p.S);
+        const int steps = ((p.S > 1 ? p.kchunk : a.K) + 63) / 64, g = skinny_row_groups(a.M, a.N, a.K, p.S);
         if (steps >= 32) run_skinny<16>(s, st, p.S, g);
         else if (steps >= 8) run_skinny<8>(s, st, p.S, g);
         else run_skinny<4>(s, st, p.S, g);
@@ -1508,6 +1511,8 @@ size_t gemm_split_bytes(int M, int N, int K) {
     const SplitPlan p = split_plan(M, N, K);
     return p.S > 1 ? (size_t)p.S * M * N * 4 : 0;
 }
+
+int rowop_gemm_block_rows(int M, int N) { return 16 * rowop_group_fm(M, N); }
 
 bool rowop_gemm_fits(int op, int M, int K) {
     if (op == 1 || op < 0 || op > 3) return false;

@@ -228,7 +228,8 @@ static GemmArgs gemm_args(const DLinear& L, float* out, int ldo, int seq, int ac
 }
 
 // Whether linear() runs a row op inside the GEMM. Every block of the fused
-// kernel applies the row op to all rows (about 1000 VALU cycles per 720-wide
+// kernel applies the row op to all rows of its row group (all rows when the
+// output is wide) (about 1000 VALU cycles per 720-wide
 // RMSNorm row and SIMD, 3x that for a 2048-wide silu_gate row), so the fused
 // kernel beats row kernel + GEMM only while each SIMD has a row or so: on
 // MI355X at 16 rows it saved 4 us of 9.7 (RMSNorm, N = 4096, K = 720); at 50
@@ -237,9 +238,11 @@ static GemmArgs gemm_args(const DLinear& L, float* out, int ldo, int seq, int ac
 // (50 x 720 x 960: 8.6 us fused against 9.7 us as quantize + GEMM); since the
 // panel quantizer keeps its row in registers, the separate pair wins there
 // too (SmolVLA 8.54 -> 8.18 ms per chunk, same box), so every op fuses only up
-// to 16 rows. Fusing wherever the kernel's row groups hold 16 rows (the 50-row
-// o- and down-projections, N = 720, 4 groups) was slower as well: 7.33 ->
-// 8.00 ms per chunk. VLA_HIP_ROWOP_FUSE=0 turns it off.
+// to 16 rows - or, for the identity op, wherever the fused kernel's row groups
+// hold at most 16 rows (the 50-row o-projections, N = 720, 4 groups: 7.22 ->
+// 7.03 ms per chunk, four alternating runs on one box). Fusing silu_gate
+// (K = 2048) that way as well was slower: 7.33 -> 8.00 ms.
+// VLA_HIP_ROWOP_FUSE=0 turns it off.
 constexpr int kRowopFuseMaxRows = 16;
 
 static bool fuse_rowop(int op, int seq, int K, int N) {
@@ -247,8 +250,9 @@ static bool fuse_rowop(int op, int seq, int K, int N) {
         const char* e = std::getenv("VLA_HIP_ROWOP_FUSE");
         return !(e && e[0] == '0');
     }();
-    (void)N;
-    return on && !probe_on() && seq <= kRowopFuseMaxRows && rowop_gemm_fits(op, seq, K);
+    const bool rows_ok =
+        seq <= kRowopFuseMaxRows || (op == 0 && rowop_gemm_block_rows(seq, N) <= kRowopFuseMaxRows);
+    return on && !probe_on() && rows_ok && rowop_gemm_fits(op, seq, K);
 }
 
 static bool overlaps(const float* p, size_t pn, const float* q, size_t qn) {
