@@ -472,3 +472,43 @@ def test_skinny_row_groups_bitexact(vla, orc, torch_cuda, groups, seq, N, K):
     want = (base + orc.apply_act(orc.dense_linear_i8_pre(xq, sa, Wq, ws, b, K), 1)).astype(np.float32)
     for i, o in enumerate(outs):
         assert same_bits(o.cpu().numpy(), want), f"form {i} with {groups} row groups differs from the oracle"
+
+
+# -------------------------------------------------------------------- gemv --
+
+@pytest.mark.parametrize("seq,N,K", [(1, 720, 2048), (2, 17, 2050), (1, 1, 4100), (2, 4096, 4096),
+                                     (1, 33, 8196), (2, 960, 2560)])
+@pytest.mark.parametrize("act,accumulate", [(0, 0), (1, 1), (2, 0)])
+def test_gemv_rows_bitexact(vla, orc, torch_cuda, seq, N, K, act, accumulate):
+    """One or two rows over K >= 2048 (the dot-product kernel, weight bytes
+    past K masked): the oracle's outputs, row-major and panel activations."""
+    torch = torch_cuda
+    x, W, b = _case(orc, seq, N, K)
+    xq, sa = orc.quantize_act_i8(x)
+    Wq, ws = orc.quantize_weights_i8(W)
+    ld = (K + 63) // 64 * 64
+    Xp = np.zeros((seq, ld), np.int8)
+    Xp[:, :xq.shape[1]] = xq
+    Wp = np.full((N, ld), 77, np.int8)  # bytes past K are not zero: the kernel must mask them
+    Wp[:, :K] = Wq[:, :K]
+    dev = torch.device("cuda")
+    Xd, Wd = torch.from_numpy(Xp).to(dev), torch.from_numpy(Wp).to(dev)
+    sad, wsd, bd = torch.from_numpy(sa).to(dev), torch.from_numpy(ws).to(dev), torch.from_numpy(b).to(dev)
+    xd = torch.from_numpy(x).to(dev)
+    xpan = torch.empty((vla.i8_panel_bytes(seq, K),), dtype=torch.int8, device=dev)
+    span = torch.empty(seq, dtype=torch.float32, device=dev)
+    base = np.full((seq, N), 0.25, np.float32)
+    row = torch.from_numpy(base.copy()).to(dev)
+    pan = torch.from_numpy(base.copy()).to(dev)
+    vla.dense_linear_i8_pre_dev(row, Xd, sad, Wd, wsd, bd, K, act=act, accumulate=accumulate)
+    vla.quantize_act_i8_panel_dev(xd, xpan, span)
+    vla.dense_linear_i8_panel_dev(pan, xpan, span, Wd, wsd, bd, K, act=act, accumulate=accumulate)
+    torch.cuda.synchronize()
+    want = orc.apply_act(orc.dense_linear_i8_pre(xq, sa, Wq, ws, b, K), act)
+    if accumulate:
+        want = (base + want).astype(np.float32)
+    for got in (row.cpu().numpy(), pan.cpu().numpy()):
+        if act == 2:
+            assert max_rel(got, want) <= 2e-6
+        else:
+            assert same_bits(got, want), "gemv rows differ from the oracle"

@@ -907,6 +907,62 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
     }
 }
 
+// ------------------------------------------------------------------ gemv --
+
+// One or two rows (decode rows) over a long K: an MFMA fragment would be 16
+// rows, 14 or 15 of them padding that every block reads, so these rows take
+// dot products instead.
+// L lanes share one weight row (output column): lane g of the group takes the
+// 16-byte chunks g, g + L, ... of the row and the same chunks of each
+// activation row, sums them with v_dot4_i32_i8 (exact int32), and the group's
+// sums meet by lane shuffles (exact) before lane 0 applies the epilogue
+// (store_out: epi_value, the expression of every other kernel). Weight bytes
+// past K are masked to zero, so activation bytes there add nothing.
+template <int MV, int L>
+__global__ __launch_bounds__(256) void gemm_i8_gemv(GemmArgs a) {
+    constexpr int RPW = 64 / L, U = 4;  // rows per wave; chunks in flight per lane
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int n = (blockIdx.x * 4 + wave) * RPW + lane / L, gl = lane % L;
+    const int K = a.K, nch = (K + 15) >> 4;
+    const bool nok = n < a.N;
+    const int8_t* brow = a.B + (size_t)(nok ? n : a.N - 1) * a.ldb;
+    const size_t pstep = (size_t)panel_rows(a.M) * 64;
+    int acc[MV];
+#pragma unroll
+    for (int m = 0; m < MV; m++) acc[m] = 0;
+    for (int c0 = gl; c0 < nch; c0 += U * L) {
+        v4i w[U], x[U][MV];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int c = c0 + u * L, k = c * 16;
+            w[u] = load_chunk<true>(brow, k, K);
+#pragma unroll
+            for (int m = 0; m < MV; m++) {
+                const int8_t* xp = a.a_panel ? a.A + (size_t)(k >> 6) * pstep + m * 64 + (k & 63)
+                                             : a.A + (size_t)m * a.lda + k;
+                x[u][m] = c < nch ? *reinterpret_cast<const v4i*>(xp) : v4i{0, 0, 0, 0};
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++)
+#pragma unroll
+            for (int m = 0; m < MV; m++) {
+                acc[m] = __builtin_amdgcn_sdot4(w[u].x, x[u][m].x, acc[m], false);
+                acc[m] = __builtin_amdgcn_sdot4(w[u].y, x[u][m].y, acc[m], false);
+                acc[m] = __builtin_amdgcn_sdot4(w[u].z, x[u][m].z, acc[m], false);
+                acc[m] = __builtin_amdgcn_sdot4(w[u].w, x[u][m].w, acc[m], false);
+            }
+    }
+#pragma unroll
+    for (int off = L / 2; off > 0; off >>= 1)
+#pragma unroll
+        for (int m = 0; m < MV; m++) acc[m] += __shfl_xor(acc[m], off);
+    if (gl == 0 && nok)
+#pragma unroll
+        for (int m = 0; m < MV; m++)
+            if (m < a.M) store_out(a, m, n, acc[m]);
+}
+
 // ------------------------------------------------------- row op + skinny --
 
 // Rows the fused row-op GEMM below computes: M rounded up to 16, 32, 64 or 128
@@ -1235,6 +1291,33 @@ void run_skinny(const GemmArgs& a, hipStream_t st, int splits = 1, int groups = 
     VLA_LAUNCH_CHECK();
 }
 
+template <int MV>
+void run_gemv_m(const GemmArgs& a, hipStream_t st) {
+    const int nch = (a.K + 15) / 16;
+    if (nch >= 48) gemm_i8_gemv<MV, 64><<<(a.N + 3) / 4, 256, 0, st>>>(a);
+    else if (nch >= 24) gemm_i8_gemv<MV, 32><<<(a.N + 7) / 8, 256, 0, st>>>(a);
+    else gemm_i8_gemv<MV, 16><<<(a.N + 15) / 16, 256, 0, st>>>(a);
+    VLA_LAUNCH_CHECK();
+}
+
+void run_gemv(const GemmArgs& a, hipStream_t st) {
+    if (a.M == 1) run_gemv_m<1>(a, st);
+    else run_gemv_m<2>(a, st);
+}
+
+// One or two rows over K >= 2048 take gemm_i8_gemv (VLA_HIP_GEMV=0 turns it
+// off). Graph replays on MI355X, skinny -> gemv: 1x4096x4096 6.44 -> 5.48 us,
+// 2x4096x4096 6.47 -> 6.05, 1x2560x960 4.84 -> 3.45, 1x2048x720 4.20 -> 3.10;
+// but 4x4096x4096 6.47 -> 7.66 and, over K <= 1024, 1x512x3200 3.18 -> 3.33
+// (the skinny kernel's short rows are already one load round trip).
+bool use_gemv(int M, int K) {
+    static const bool on = [] {
+        const char* e = std::getenv("VLA_HIP_GEMV");
+        return !(e && e[0] == '0');
+    }();
+    return on && M <= 2 && K >= 2048;
+}
+
 template <int OP, int NV, int FM>
 void run_rowop(const RowQArgs& r, const GemmArgs& a, hipStream_t st) {
     static const bool attr = [] {
@@ -1461,6 +1544,10 @@ void launch_gemm_i8(const GemmArgs& a, hipStream_t st) {
         if (steps >= 32) run_skinny<16, true>(a, st, 1, g);
         else if (steps >= 8) run_skinny<8, true>(a, st, 1, g);
         else run_skinny<4, true>(a, st, 1, g);
+        return;
+    }
+    if (use_gemv(a.M, a.K)) {
+        run_gemv(a, st);
         return;
     }
     if (a.M <= 128) {
