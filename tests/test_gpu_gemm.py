@@ -434,13 +434,15 @@ def test_dense_linear_i8_dev_caller_scratch(vla, orc, torch_cuda, seq, N, K, act
 
 # ------------------------------------------------------------- row groups --
 
+@pytest.mark.parametrize("fn", ["1", "2"])
 @pytest.mark.parametrize("groups", ["1", "2", "3", "4", "8"])
 @pytest.mark.parametrize("seq,N,K", [(100, 960, 2560), (50, 720, 960), (128, 48, 1027), (37, 200, 4100),
-                                     (17, 64, 64), (1, 16, 3)])
-def test_skinny_row_groups_bitexact(vla, orc, torch_cuda, groups, seq, N, K):
-    """The skinny kernel split into row groups (each block: 16 columns x its
-    16-row fragments; fragments past M repeat the last and are never stored)
-    gives the oracle's outputs bit for bit, row-major, panel and split-K."""
+                                     (17, 64, 64), (1, 16, 3), (100, 4096, 4096), (33, 40, 200)])
+def test_skinny_row_groups_bitexact(vla, orc, torch_cuda, fn, groups, seq, N, K):
+    """The skinny kernel split into row groups (each block: 16 x FN columns x
+    its 16-row fragments; fragments past M repeat the last and are never
+    stored) gives the oracle's outputs bit for bit, row-major, panel and
+    split-K."""
     torch = torch_cuda
     x, W, b = _case(orc, seq, N, K)
     xq, sa = orc.quantize_act_i8(x)
@@ -461,6 +463,7 @@ def test_skinny_row_groups_bitexact(vla, orc, torch_cuda, groups, seq, N, K):
     base = np.full((seq, N), 0.25, np.float32)
     outs = [torch.from_numpy(base.copy()).to(dev) for _ in range(3)]
     os.environ["VLA_HIP_SKINNY_R"] = groups
+    os.environ["VLA_HIP_SKINNY_FN"] = fn
     try:
         vla.dense_linear_i8_pre_dev(outs[0], Xd, sad, Wd, wsd, bd, K, act=1, accumulate=1)
         vla.quantize_act_i8_panel_dev(xd, xpan, span)
@@ -468,7 +471,7 @@ def test_skinny_row_groups_bitexact(vla, orc, torch_cuda, groups, seq, N, K):
         vla.dense_linear_i8_pre_split_dev(outs[2], Xd, sad, Wd, wsd, bd, K, work, act=1, accumulate=1)
         torch.cuda.synchronize()
     finally:
-        del os.environ["VLA_HIP_SKINNY_R"]
+        del os.environ["VLA_HIP_SKINNY_R"], os.environ["VLA_HIP_SKINNY_FN"]
     want = (base + orc.apply_act(orc.dense_linear_i8_pre(xq, sa, Wq, ws, b, K), 1)).astype(np.float32)
     for i, o in enumerate(outs):
         assert same_bits(o.cpu().numpy(), want), f"form {i} with {groups} row groups differs from the oracle"

@@ -731,11 +731,16 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds(GemmArgs a) {
 // its partner 8 k + c - 8 + half (k = the block's index within the head) -
 // so the epilogue rotates each output with its partner's value, summed from
 // the same block's partial tiles.
-template <int FM, int WAVES, bool ROPE = false>
+// FN: column groups of 16 per block; each A fragment a wave loads feeds FN
+// MFMAs from registers, so a block of 16 x FN columns reads its rows of A once
+// (the rotating epilogue keeps FN = 1).
+template <int FM, int WAVES, bool ROPE = false, int FN = 1>
 __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
-    static_assert(FM * WAVES <= 64, "partial tiles must fit in 64 KiB of LDS");
-    // per wave, its partial int32 tile in MFMA lane order: [i][r][lane]
-    __shared__ int32_t part[WAVES * FM * 256];
+    static_assert(FM * FN * WAVES <= 64, "partial tiles must fit in 64 KiB of LDS");
+    static_assert(!ROPE || FN == 1, "the rotating epilogue owns 16 columns per block");
+    constexpr int FT = FM * FN;  // 16 x 16 tiles per wave, tile t = i * FN + j
+    // per wave, its partial int32 tiles in MFMA lane order: [t][r][lane]
+    __shared__ int32_t part[WAVES * FT * 256];
 
     if (gridDim.y > 1) {  // split K: chunk blockIdx.y of K (a multiple of 128 bytes), raw int32 sums
         const int k0 = blockIdx.y * a.kchunk;
@@ -747,7 +752,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int n0 = blockIdx.x * 16;
+    const int n0 = blockIdx.x * 16 * FN;
     const int K = a.K;
     // row group blockIdx.z: 16-row fragments f0 .. f0 + FM - 1 (fragments past
     // the last one repeat it; their rows are >= M and never stored)
@@ -772,14 +777,17 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
         const int hb = a.rope_hd / 16, head = blockIdx.x / hb, k = blockIdx.x - head * hb;
         return head * a.rope_hd + 8 * k + (c & 7) + (c < 8 ? 0 : a.rope_hd / 2);
     };
-    const int nr = col(r16);
-    const int n = nr < a.N ? nr : a.N - 1;
-    const int8_t* brow = a.B + (size_t)n * a.ldb + kq;
+    const int8_t* brow[FN];
+#pragma unroll
+    for (int j = 0; j < FN; j++) {
+        const int nr = col(16 * j + r16);
+        brow[j] = a.B + (size_t)(nr < a.N ? nr : a.N - 1) * a.ldb + kq;
+    }
 
     // The outputs this thread stores after the reduction (element e of the
     // FM x 4 x 64 lane-major tile), and their epilogue operands, fetched now so
     // their latency hides under the main loop rather than after the barrier.
-    constexpr int NT = WAVES * 64, EPT = (FM * 256 + NT - 1) / NT;
+    constexpr int NT = WAVES * 64, EPT = (FT * 256 + NT - 1) / NT;
     float esa[EPT], ews[EPT], eb[EPT], eold[EPT];
     // ROPE: the partner column's scale and bias, this output's (cos, sin)
     float pws[ROPE ? EPT : 1], pb[ROPE ? EPT : 1];
@@ -787,9 +795,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
 #pragma unroll
     for (int j = 0; j < EPT; j++) {
         const int e = tid + j * NT;
-        const int l = e & 63, r = (e >> 6) & 3, i = e >> 8;
-        int mm = 16 * (f0 + i) + 4 * (l >> 4) + r, nn = col(l & 15);
-        const bool ok = e < FM * 256 && mm < a.M && nn < a.N;
+        const int l = e & 63, r = (e >> 6) & 3, i = (e >> 8) / FN, jn = (e >> 8) % FN;
+        int mm = 16 * (f0 + i) + 4 * (l >> 4) + r, nn = col(16 * jn + (l & 15));
+        const bool ok = e < FT * 256 && mm < a.M && nn < a.N;
         mm = ok ? mm : 0;
         nn = ok ? nn : 0;
         esa[j] = ews[j] = eb[j] = eold[j] = 0.0f;
@@ -813,9 +821,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
         }
     }
 
-    v4i acc[FM];
+    v4i acc[FT];
 #pragma unroll
-    for (int i = 0; i < FM; i++) acc[i] = v4i{0, 0, 0, 0};
+    for (int t = 0; t < FT; t++) acc[t] = v4i{0, 0, 0, 0};
 
     // This wave's 64-byte k-steps are wave, wave + WAVES, ... < full, rotated
     // by a per-block offset: every block reads all of A, and without the
@@ -824,15 +832,17 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
     // depend on the order). The loads run P steps ahead of the MFMAs in a
     // register ring.
     const int full = K / 64;  // 64-byte steps read without masks
-    constexpr int P = (FM <= 3 || (FM == 4 && WAVES < 16)) ? 4 : 3;  // within the VGPR budget
+    constexpr int FL = FM + FN - 1;  // fragments per step beyond one weight fragment
+    constexpr int P = (FL <= 3 || (FL == 4 && WAVES < 16)) ? 4 : 3;  // within the VGPR budget
     // blocks i, i + 8, i + 16, ... share an XCD; (WAVES + 1) is odd, so their
     // offsets differ for up to `full` blocks when full is a power of two
     const int rot = full > 0 ? (int)(((unsigned)blockIdx.x >> 3) * (WAVES + 1) % (unsigned)full) : 0;
-    v4i ra[P][FM], rb[P];
+    v4i ra[P][FM], rb[P][FN];
     auto load = [&](int p, int k) {
         int step = wave + k * WAVES + rot;
         step = step < full ? step : step - full;
-        rb[p] = *reinterpret_cast<const v4i*>(brow + step * 64);
+#pragma unroll
+        for (int j = 0; j < FN; j++) rb[p][j] = *reinterpret_cast<const v4i*>(brow[j] + step * 64);
         const size_t aoff = (size_t)step * astep;
 #pragma unroll
         for (int i = 0; i < FM; i++) ra[p][i] = *reinterpret_cast<const v4i*>(arow[i] + aoff);
@@ -848,38 +858,43 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
             const int k = k0 + p;
             if (k < nst) {
 #pragma unroll
-                for (int i = 0; i < FM; i++) acc[i] = mfma_i8(ra[p][i], rb[p], acc[i]);
+                for (int i = 0; i < FM; i++)
+#pragma unroll
+                    for (int j = 0; j < FN; j++) acc[i * FN + j] = mfma_i8(ra[p][i], rb[p][j], acc[i * FN + j]);
                 if (k + P < nst) load(p, k + P);
             }
         });
     }
     if (K % 64 && wave == full % WAVES) {
         const int k = full * 64 + kq;
-        const v4i b0 = load_chunk<true>(brow - kq, k, K);  // zero past K: A bytes there add nothing
+        v4i b0[FN];
+#pragma unroll
+        for (int j = 0; j < FN; j++) b0[j] = load_chunk<true>(brow[j] - kq, k, K);  // zero past K: A bytes there add nothing
 #pragma unroll
         for (int i = 0; i < FM; i++) {
             const v4i av = a.a_panel ? *reinterpret_cast<const v4i*>(arow[i] + (size_t)full * astep)
                                      : load_chunk<true>(arow[i] - kq, k, K);
-            acc[i] = mfma_i8(av, b0, acc[i]);
+#pragma unroll
+            for (int j = 0; j < FN; j++) acc[i * FN + j] = mfma_i8(av, b0[j], acc[i * FN + j]);
         }
     }
 
     // partial tiles to LDS (no two waves share an address), then each thread
     // sums one element over the waves (exact int32) and stores it
 #pragma unroll
-    for (int i = 0; i < FM; i++)
+    for (int t = 0; t < FT; t++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) part[((wave * FM + i) * 4 + r) * 64 + lane] = acc[i][r];
+        for (int r = 0; r < 4; r++) part[((wave * FT + t) * 4 + r) * 64 + lane] = acc[t][r];
     __syncthreads();
 #pragma unroll
     for (int j = 0; j < EPT; j++) {
         const int e = tid + j * NT;
-        if (e >= FM * 256) break;
+        if (e >= FT * 256) break;
         int32_t v = 0;
 #pragma unroll
-        for (int w = 0; w < WAVES; w++) v += part[w * FM * 256 + e];
-        const int l = e & 63, r = (e >> 6) & 3, i = e >> 8;
-        const int mm = 16 * (f0 + i) + 4 * (l >> 4) + r, nn = col(l & 15);
+        for (int w = 0; w < WAVES; w++) v += part[w * FT * 256 + e];
+        const int l = e & 63, r = (e >> 6) & 3, i = (e >> 8) / FN, jn = (e >> 8) % FN;
+        const int mm = 16 * (f0 + i) + 4 * (l >> 4) + r, nn = col(16 * jn + (l & 15));
         if (mm >= a.M || nn >= a.N) continue;
         if (a.acc32) {
             a.acc32[(size_t)mm * a.N + nn] = v;
@@ -891,7 +906,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
             if (rotb) {  // act 0, no accumulate (checked by the launcher)
                 int32_t vp = 0;
 #pragma unroll
-                for (int w = 0; w < WAVES; w++) vp += part[w * FM * 256 + (e ^ 8)];
+                for (int w = 0; w < WAVES; w++) vp += part[w * FT * 256 + (e ^ 8)];
                 const float op = fmaf((float)vp * pws[j], esa[j], pb[j]);
                 a.out[(size_t)mm * a.ldo + nn] = (l & 8) ? rope_hi(op, o, rc[j], rs[j]) : rope_lo(o, op, rc[j], rs[j]);
                 continue;
@@ -1261,20 +1276,56 @@ void run_lds(const GemmArgs& a, hipStream_t st) {
 // is fastest over K = 4096 (50 rows: 9.85 us, 12.19 with two), since more
 // only re-read the weights, but two win over a short K (50x720x4096 4.63 ->
 // 4.43 us).
-int skinny_row_groups(int M, int N, int K, int S) {
+int skinny_row_groups(int M, int N, int K, int S, int fn = 1) {
     const int nfrag = (M + 15) / 16;
     const char* env = std::getenv("VLA_HIP_SKINNY_R");
-    const long blocks = (long)((N + 15) / 16) * (S > 1 ? S : 1);
+    const long blocks = (long)((N + 16 * fn - 1) / (16 * fn)) * (S > 1 ? S : 1);
     int g = (int)((kCUs + blocks - 1) / blocks);
     if (K <= 1024 && g < 2) g = 2;
     if (env && *env) g = std::atoi(env);
+    if (fn > 1 && g < (nfrag + 3) / 4) g = (nfrag + 3) / 4;  // two column groups hold at most 4 fragments
     g = g < 1 ? 1 : g > nfrag ? nfrag : g;
     const int fm = (nfrag + g - 1) / g;
     return (nfrag + fm - 1) / fm;
 }
 
+// Column groups per skinny block (16 x FN columns): two where more than 64
+// rows meet a long K and a wide output, VLA_HIP_SKINNY_FN=1|2 forces a count
+// (A/B runs). Graph replays on MI355X, one -> two: 100x4096x4096 13.75 ->
+// 12.33 us (each block reads half as much of A per column; with two row
+// groups a CU still moves 393 instead of 524 KB), but 50x4096x4096 9.96 ->
+// 10.06, 100x768x3072 5.52 -> 6.92, 100x512x3200 4.81 -> 6.44, 100x2560x960
+// 5.35 -> 6.36, SmolVLA chunk 6.86 -> 7.02 ms.
+int skinny_col_groups(int M, int N, int K) {
+    const char* env = std::getenv("VLA_HIP_SKINNY_FN");
+    if (env && *env) return std::atoi(env) == 2 && M > 16 ? 2 : 1;
+    return M > 64 && K >= 2048 && N >= 4096 ? 2 : 1;
+}
+
+// Two column groups per block: at most 4 fragments and 8 waves (the partial
+// tiles' LDS), no rotating epilogue.
+template <int WAVES>
+void run_skinny_fn2(const GemmArgs& a, hipStream_t st, int splits, int groups) {
+    const int fm = ((a.M + 15) / 16 + groups - 1) / groups;
+    const dim3 nb((a.N + 31) / 32, splits, groups);
+    constexpr int W = WAVES < 8 ? WAVES : 8;
+    switch (fm) {
+    case 1: gemm_i8_skinny<1, W, false, 2><<<nb, W * 64, 0, st>>>(a); break;
+    case 2: gemm_i8_skinny<2, W, false, 2><<<nb, W * 64, 0, st>>>(a); break;
+    case 3: gemm_i8_skinny<3, W, false, 2><<<nb, W * 64, 0, st>>>(a); break;
+    default: gemm_i8_skinny<4, W, false, 2><<<nb, W * 64, 0, st>>>(a); break;
+    }
+    VLA_LAUNCH_CHECK();
+}
+
 template <int WAVES, bool ROPE = false>
-void run_skinny(const GemmArgs& a, hipStream_t st, int splits = 1, int groups = 1) {
+void run_skinny(const GemmArgs& a, hipStream_t st, int splits = 1, int groups = 1, int fn = 1) {
+    if constexpr (!ROPE) {
+        if (fn == 2) {
+            run_skinny_fn2<WAVES>(a, st, splits, groups);
+            return;
+        }
+    }
     const int fm = ((a.M + 15) / 16 + groups - 1) / groups;
     const dim3 nb((a.N + 15) / 16, splits, groups);
     constexpr int W8 = WAVES < 8 ? WAVES : 8;  // FM > 4 keeps the partial tiles within 64 KiB
@@ -1558,10 +1609,11 @@ void launch_gemm_i8(const GemmArgs& a, hipStream_t st) {
         }
         GemmArgs s = a;
         s.kchunk = p.kchunk;
-        const int steps = ((p.S > 1 ? p.kchunk : a.K) + 63) / 64, g = skinny_row_groups(a.M, a.N, a.K, p.S);
-        if (steps >= 32) run_skinny<16>(s, st, p.S, g);
-        else if (steps >= 8) run_skinny<8>(s, st, p.S, g);
-        else run_skinny<4>(s, st, p.S, g);
+        const int fn = skinny_col_groups(a.M, a.N, a.K);
+        const int steps = ((p.S > 1 ? p.kchunk : a.K) + 63) / 64, g = skinny_row_groups(a.M, a.N, a.K, p.S, fn);
+        if (steps >= 32) run_skinny<16>(s, st, p.S, g, fn);
+        else if (steps >= 8) run_skinny<8>(s, st, p.S, g, fn);
+        else run_skinny<4>(s, st, p.S, g, fn);
         if (p.S > 1) {
             const bool vec = a.N % 4 == 0 && a.ldo % 4 == 0 && aligned(a.out, 16);
             const int64_t work = (int64_t)a.M * a.N / (vec ? 4 : 1);
