@@ -515,3 +515,38 @@ def test_gemv_rows_bitexact(vla, orc, torch_cuda, seq, N, K, act, accumulate):
             assert max_rel(got, want) <= 2e-6
         else:
             assert same_bits(got, want), "gemv rows differ from the oracle"
+
+
+@pytest.mark.parametrize("groups", ["", "1", "3"])
+@pytest.mark.parametrize("seq,N,K", [(177, 960, 960), (256, 100, 300), (129, 17, 64), (200, 1024, 4100),
+                                     (177, 2048, 2560), (240, 33, 1027)])
+def test_skinny_129_to_256_rows_bitexact(vla, orc, torch_cuda, groups, seq, N, K):
+    """129..256 rows over N <= 2048 take the skinny kernel in row groups of at
+    most 8 fragments (a forced count below that is raised): the oracle's
+    outputs bit for bit, also through the split-K entry point."""
+    torch = torch_cuda
+    x, W, b = _case(orc, seq, N, K)
+    xq, sa = orc.quantize_act_i8(x)
+    Wq, ws = orc.quantize_weights_i8(W)
+    ld = (K + 63) // 64 * 64
+    Xp = np.zeros((seq, ld), np.int8)
+    Xp[:, :xq.shape[1]] = xq
+    Wp = np.zeros((N, ld), np.int8)
+    Wp[:, :Wq.shape[1]] = Wq
+    dev = torch.device("cuda")
+    Xd, Wd = torch.from_numpy(Xp).to(dev), torch.from_numpy(Wp).to(dev)
+    sad, wsd, bd = torch.from_numpy(sa).to(dev), torch.from_numpy(ws).to(dev), torch.from_numpy(b).to(dev)
+    work = torch.empty(max(vla.gemm_i8_split_bytes(seq, N, K), 16), dtype=torch.uint8, device=dev)
+    base = np.full((seq, N), 0.25, np.float32)
+    outs = [torch.from_numpy(base.copy()).to(dev) for _ in range(2)]
+    if groups:
+        os.environ["VLA_HIP_SKINNY_R"] = groups
+    try:
+        vla.dense_linear_i8_pre_dev(outs[0], Xd, sad, Wd, wsd, bd, K, act=1, accumulate=1)
+        vla.dense_linear_i8_pre_split_dev(outs[1], Xd, sad, Wd, wsd, bd, K, work, act=1, accumulate=1)
+        torch.cuda.synchronize()
+    finally:
+        os.environ.pop("VLA_HIP_SKINNY_R", None)
+    want = (base + orc.apply_act(orc.dense_linear_i8_pre(xq, sa, Wq, ws, b, K), 1)).astype(np.float32)
+    for o in outs:
+        assert same_bits(o.cpu().numpy(), want)
