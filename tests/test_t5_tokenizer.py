@@ -60,3 +60,32 @@ def test_random_strings_match_reference(toks):
         n = int(r.integers(0, 30))
         text = "".join(alphabet[int(k)] for k in r.integers(0, len(alphabet), size=n))
         assert ours.encode(text, 16) == ref.encode(text, 16), repr(text)
+
+
+def test_crafted_vocab_matches_reference(tmp_path):
+    """A vocab a SentencePiece export never writes, chosen so that a slip in
+    the segmentation or the file rules fails: a repeated piece whose later,
+    lower score still lowers the <unk> score (the first line keeps the id and
+    score; with the <unk> score at -50 the four one-byte pieces of U+1F916 win
+    at -24, with it at -17 the single <unk> would), equal-score segmentations
+    (the first candidate found wins), pieces that end inside a UTF-8
+    character, an unusable score-0 line before a usable line of the same
+    piece, and a special piece with a '<' inside it."""
+    pkg = load_pkg()
+    lines = [b"<pad>\t0", b"</s>\t0", b"<unk>\t0",
+             "\u2581ab\t-2".encode(), "\u2581a\t-1".encode(), b"b\t-1", b"ab\t-1.5",
+             "\u2581\t-0.5".encode(), b"a\t-1",
+             "\u2581a\t-40".encode(),          # repeat: ignored, but lowers the <unk> score
+             b"c\t0", b"c\t-3",                 # unusable, then usable
+             b"\xe2\x96\t-7",                  # the first two bytes of U+2581
+             b"\xf0\t-6", b"\x9f\t-6", b"\xa4\t-6", b"\x96\t-6",
+             b"<a<b>\t0", b"<b>\t0", b"<x>\t-1"]
+    (tmp_path / "vocab.txt").write_bytes(b"\n".join(lines) + b"\n")
+    ours, ref = pkg.UnigramTokenizer(str(tmp_path)), oracle().RefT5Tok(str(tmp_path))
+    texts = ["ab", "a b", "abab c", "cab", "\u0416 ab", "<a<b>", "x<a<b>y<b>z", "<b><b>", "<x> <b>", "a<b",
+             "<a<b>>", "ab ab ab ab", "\u0416\u0416 c \u0416\u0416", "\U0001F916", "a\U0001F916b"]
+    for t in texts:
+        for max_len in (1, 3, 12):
+            assert ours.encode(t, max_len) == ref.encode(t, max_len), (t, max_len)
+    # the byte pieces of U+1F916 win over one <unk> (lowest score -40, not -7)
+    assert ours.encode("\U0001F916", 8)[1:5] == [13, 14, 15, 16]

@@ -77,3 +77,46 @@ def test_load_errors(tmp_path):
     (tmp_path / "merges.txt").write_text("#nospace\n")  # no line with a space: no merges
     with pytest.raises(pkg.VlaError):
         pkg.BpeTokenizer(str(tmp_path))
+
+
+def _sym(b: bytes) -> str:
+    import vla_simd_amd.checkpoints as ck
+    table = ck.gpt2_byte_symbols()
+    return "".join(table[x] for x in b)
+
+
+def test_crafted_merge_tables_match_reference(tmp_path):
+    """Merge tables a trained BPE never writes, each chosen so that a slip in
+    the merge order fails: a pair created by a merge that outranks pairs
+    already present (it must wait for its turn, not merge at once), the same
+    pair several times in a word (leftmost first, one per round), a repeated
+    merges line (the pair keeps its last rank), a merge whose result is not in
+    the vocabulary (dropped), and a later vocab line for the same token."""
+    pkg = load_pkg()
+    ob = oracle()
+    s = _sym
+    merges = [
+        f"{s(b'a')} {s(b'a')}",          # rank 0
+        f"{s(b'b')} {s(b'c')}",          # rank 1
+        f"{s(b'aa')} {s(b'bc')}",        # rank 2: exists only after ranks 0 and 1
+        f"{s(b'c')} {s(b'a')}",          # rank 3, competes with "b c"
+        f"{s(b'b')} {s(b'c')}",          # rank 4: the repeat moves "b c" after "c a"
+        f"{s(b'x')} {s(b'y')}",          # rank 5: result missing from the vocabulary
+        f"{s(b' ')} {s(b'a')}",
+        f"{s(b'q')} {s(b'q')}",
+        f"{s(b'qq')} {s(b'qq')}",
+        "#version: comment without a space",
+    ]
+    vocab = [s(bytes([b])) for b in range(256)]
+    vocab += [s(b"aa"), s(b"bc"), s(b"aabc"), s(b"ca"), s(b" a"), s(b"qq"), s(b"qqqq")]
+    rows = [f"{i}\t{t}" for i, t in enumerate(vocab)] + [f"900\t{s(b'ca')}", "garbage line"]
+    (tmp_path / "vocab.txt").write_text("\n".join(rows) + "\n", encoding="utf-8")
+    (tmp_path / "merges.txt").write_text("\n".join(merges), encoding="utf-8")
+    ours, ref = pkg.BpeTokenizer(str(tmp_path)), ob.RefBpe(str(tmp_path))
+    texts = ["aabc", "aaaa", "aaaaa", "bcabc", "cabca", "aabcaabc", "xy xy", "qqqqqqq", "qqqqq qq",
+             " a a aa", "abcabcabc", "caaabc", "aabcbc"]
+    r = np.random.default_rng(3)
+    texts += ["".join("abcqxy "[int(k)] for k in r.integers(0, 7, size=int(r.integers(1, 24))))
+              for _ in range(400)]
+    for t in texts:
+        assert ours.encode(t) == ref.encode(t), repr(t)
