@@ -333,8 +333,8 @@ REF_API int ref_smolvla_chunk(void* h, const float* prefix, const int* pad, int 
         }
     std::vector<int> pos(np);
     int c = 0;
-    for (int i = 0; i < np; i++) {
-        c += pad[i] ? 1 : 0;
+    for (int i = 0; i < np; i++) {  // raw sums, as smolvla_model.cpp:237-238,244
+        c += pad[i];
         pos[i] = c - 1;
     }
     std::vector<VlmKV> kv;

@@ -172,7 +172,7 @@ TILES = ["128x128x64", "64x128x64", "64x64x64", "128x128x64s4", "64x128x64s4", "
 
 
 @pytest.mark.parametrize("tile", TILES)
-@pytest.mark.parametrize("M,N,K", [(300, 200, 200), (257, 130, 48), (520, 272, 1024), (129, 17, 64)])
+@pytest.mark.parametrize("M,N,K", [(300, 200, 200), (257, 130, 48), (520, 272, 1024), (129, 17, 64), (257, 17, 64)])
 def test_every_tile_config(vla, orc, torch_cuda, tile, M, N, K):
     """Each aligned-kernel tile, forced, on shapes off the tile grid: M and N
     edges, a K tail, K below one slab (device rows padded to 16 bytes)."""
@@ -310,7 +310,10 @@ def test_panel_rejects_large_m(vla, torch_cuda):
 # very long K over at most 64 tiles of 64 x 64 (M > 128 splits only there):
 # ACT's w2 (302 x 512 x 3200), a ResNet 3x3/512 conv (300 x 512 x 4608),
 # K tails (4100, 3100), a 129-row case, 64 tiles exactly (256 x 1024 x 4096)
-SPLIT_SHAPES = [(302, 512, 3200), (300, 512, 4608), (129, 100, 4100), (200, 48, 3100), (256, 1024, 4096),
+# more than 256 rows (129..256 rows over N <= 2048 take the unsplit skinny
+# kernel): K tails (4100, 3100), an N edge (100, 48) and a 60-tile output
+SPLIT_SHAPES = [(302, 512, 3200), (300, 512, 4608), (257, 100, 4100), (300, 48, 3100), (300, 768, 4096),
+                (300, 512, 4100),
                 # at most 128 rows (the skinny kernel): SigLIP's projection
                 # (64 x 960 x 12288), a K tail, one row, 16 columns
                 (64, 960, 12288), (100, 1000, 4100), (1, 16, 4096), (16, 200, 8192)]
@@ -394,6 +397,8 @@ def test_split_k_plan_bounds(vla):
     assert vla.gemm_i8_split_bytes(658, 768, 768) == 0        # K < 1024
     assert vla.gemm_i8_split_bytes(8192, 4096, 4096) == 0     # fills the chip
     assert vla.gemm_i8_split_bytes(512, 4096, 4096) == 0      # one LDS-DMA tile per CU: measured slower split
+    for seq, N, K in [(129, 100, 4100), (200, 48, 3100), (256, 1024, 4096)]:
+        assert vla.gemm_i8_split_bytes(seq, N, K) == 0        # 129..256 rows, N <= 2048: unsplit skinny kernel
     for seq, N, K in SPLIT_SHAPES:
         assert 0 < vla.gemm_i8_split_bytes(seq, N, K) <= 8 << 20
 
@@ -523,7 +528,9 @@ def test_gemv_rows_bitexact(vla, orc, torch_cuda, seq, N, K, act, accumulate):
 def test_skinny_129_to_256_rows_bitexact(vla, orc, torch_cuda, groups, seq, N, K):
     """129..256 rows over N <= 2048 take the skinny kernel in row groups of at
     most 8 fragments (a forced count below that is raised): the oracle's
-    outputs bit for bit, also through the split-K entry point."""
+    outputs bit for bit, also through the split-K entry point, and with the
+    route switched off per call (VLA_HIP_SKINNY_MAXM=128: the tiles, split
+    over K where the plan says so)."""
     torch = torch_cuda
     x, W, b = _case(orc, seq, N, K)
     xq, sa = orc.quantize_act_i8(x)
@@ -536,17 +543,22 @@ def test_skinny_129_to_256_rows_bitexact(vla, orc, torch_cuda, groups, seq, N, K
     dev = torch.device("cuda")
     Xd, Wd = torch.from_numpy(Xp).to(dev), torch.from_numpy(Wp).to(dev)
     sad, wsd, bd = torch.from_numpy(sa).to(dev), torch.from_numpy(ws).to(dev), torch.from_numpy(b).to(dev)
-    work = torch.empty(max(vla.gemm_i8_split_bytes(seq, N, K), 16), dtype=torch.uint8, device=dev)
+    assert vla.gemm_i8_split_bytes(seq, N, K) == 0
     base = np.full((seq, N), 0.25, np.float32)
-    outs = [torch.from_numpy(base.copy()).to(dev) for _ in range(2)]
+    outs = [torch.from_numpy(base.copy()).to(dev) for _ in range(3)]
     if groups:
         os.environ["VLA_HIP_SKINNY_R"] = groups
     try:
         vla.dense_linear_i8_pre_dev(outs[0], Xd, sad, Wd, wsd, bd, K, act=1, accumulate=1)
+        work = torch.empty(16, dtype=torch.uint8, device=dev)
         vla.dense_linear_i8_pre_split_dev(outs[1], Xd, sad, Wd, wsd, bd, K, work, act=1, accumulate=1)
+        os.environ["VLA_HIP_SKINNY_MAXM"] = "128"
+        work = torch.empty(max(vla.gemm_i8_split_bytes(seq, N, K), 16), dtype=torch.uint8, device=dev)
+        vla.dense_linear_i8_pre_split_dev(outs[2], Xd, sad, Wd, wsd, bd, K, work, act=1, accumulate=1)
         torch.cuda.synchronize()
     finally:
         os.environ.pop("VLA_HIP_SKINNY_R", None)
+        os.environ.pop("VLA_HIP_SKINNY_MAXM", None)
     want = (base + orc.apply_act(orc.dense_linear_i8_pre(xq, sa, Wq, ws, b, K), 1)).astype(np.float32)
     for o in outs:
         assert same_bits(o.cpu().numpy(), want)

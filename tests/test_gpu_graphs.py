@@ -365,21 +365,36 @@ def test_act_meta_read_like_the_reference(vla, ckdir, line, ok):
     assert ref_ok == ok and dev_ok == ok
 
 
-def test_smolvla_rejects_pad_values_beyond_0_1(vla, ckdir):
-    """The reference sums the raw pad entries into the positions
-    (smolvla_model.cpp:238,245); the device graph refuses anything but 0/1
-    rather than normalising it."""
+def test_smolvla_pad_values_beyond_0_1_follow_the_reference(vla, ckdir):
+    """A pad entry is a truth value in the masks and its raw value is summed
+    into the positions (smolvla_model.cpp:224-246), so entries such as 2 or -1
+    shift the RoPE positions of the tokens after them: the device graph takes
+    them as the reference does (same bar as test_smolvla_chunk), and a layout
+    change rebuilds the graph (the 0/1 pad of the same tokens gives another
+    output)."""
     ck = _ck()
+    from helpers import oracle
+    ob = oracle()
     c = dict(ck.SMOLVLA_BASE, chunk=12, n_layers=2, expert_layers=2, n_prefix=20)
     d = str(ckdir / "smolpad")
     ck.write_smolvla(d, c)
     prefix, pad, noise = ck.smolvla_inputs(c, n_pad=2)
-    m = vla.SmolvlaChunk(d, 48)
-    pad = np.array(pad, np.int32)
-    pad[0] = 2
+    m = vla.SmolvlaChunk(d, 0)
+    r = ob.RefSmolvla(d, 0)
+    plain = m.run(prefix, pad, noise)
+    for vals in ([2, 1], [-1, 3], [5, 0]):
+        odd = np.array(pad, np.int32)
+        odd[0], odd[5] = vals
+        ref = r.run(prefix, odd, noise)
+        got = m.run(prefix, odd, noise)
+        assert _rel(got, ref) <= 1e-3, vals
+        assert not np.array_equal(got, plain), vals
+        assert _rel(m.run(prefix, pad, noise), plain) == 0.0
+    # the running sum must stay within int32
+    huge = np.array(pad, np.int32)
+    huge[:3] = 2**31 - 1
     out = np.empty((m.chunk, m.max_action_dim), np.float32)
     st = vla.lib().vla_smolvla_tf_chunk_run(m.h, vla._ptr(np.ascontiguousarray(prefix, np.float32)),
-                                            vla._ptr(pad), prefix.shape[0],
+                                            vla._ptr(huge), prefix.shape[0],
                                             vla._ptr(np.ascontiguousarray(noise, np.float32)), vla._ptr(out))
-    assert st == vla.VLA_ERR_ARG
-    assert b"pad entries" in vla.lib().vla_last_error()
+    assert st == vla.VLA_ERR_ARG and b"overflow" in vla.lib().vla_last_error()

@@ -175,6 +175,42 @@ def test_predict_rtc(vla, small, env):
     assert m.predict(frames, ids, mask, state, noise=noise).tobytes() == plain.tobytes()
 
 
+def test_alternating_guided_and_plain_chunks_replay(vla, small, env):
+    """A caller that alternates guided (RTC) and plain chunks keeps a captured
+    graph per mode: after the first two calls of each mode every call replays
+    (graph nodes as when one mode runs alone), and each mode's outputs stay
+    bit-identical from call to call."""
+    d, c = small
+    ck = _ck()
+    env(None)
+    m = vla.SmolvlaModel(d)
+    frames, ids, mask, state, noise = _inputs(ck, c, m, "move 10 cm to the left")
+    rng = np.random.default_rng(5)
+    prev = rng.normal(0, 1.5, size=(4, m.action_dim)).astype(np.float32)
+    weights = np.linspace(1.0, 0.0, m.chunk).astype(np.float32)
+    plain = lambda: m.predict(frames, ids, mask, state, noise=noise)
+    guided = lambda: m.predict(frames, ids, mask, state, noise=noise, prev=prev, weights=weights,
+                               max_guidance=1.5)
+    outs, nodes = {"p": [], "g": []}, {"p": [], "g": []}
+    for _ in range(4):
+        for k, f in (("p", plain), ("g", guided)):
+            outs[k].append(f().tobytes())
+            nodes[k].append(m.graph_nodes)
+    solo = vla.SmolvlaModel(d)
+    solo_nodes = {}
+    for k, f in (("p", lambda: solo.predict(frames, ids, mask, state, noise=noise)),
+                 ("g", lambda: solo.predict(frames, ids, mask, state, noise=noise, prev=prev, weights=weights,
+                                            max_guidance=1.5))):
+        for _ in range(3):
+            f()
+        solo_nodes[k] = solo.graph_nodes
+    print(f"alternating modes: graph nodes {nodes}, alone {solo_nodes}", flush=True)
+    for k in ("p", "g"):
+        assert len(set(outs[k])) == 1, f"mode {k} changed between calls"
+        assert nodes[k][2:] == [solo_nodes[k]] * 2 and solo_nodes[k] > 0
+    assert outs["p"][0] != outs["g"][0]
+
+
 @pytest.mark.parametrize("mask", [15, 48, 63])
 def test_predict_int8(vla, small, env, mask):
     d, c = small

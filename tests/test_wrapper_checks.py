@@ -57,10 +57,6 @@ def test_smolvla_chunk_checks_pad_and_noise():
     noise = np.zeros((50, 32), np.float32)
     with pytest.raises(ValueError, match="pad"):
         m.run(prefix, pad[:-1], noise)
-    bad = pad.copy()
-    bad[3] = 2
-    with pytest.raises(ValueError, match="pad entries"):
-        m.run(prefix, bad, noise)
     with pytest.raises(ValueError, match="noise"):
         m.run(prefix, pad, noise[:49])
     with pytest.raises(ValueError, match="prefix"):

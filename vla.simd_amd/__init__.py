@@ -1120,8 +1120,6 @@ class SmolvlaChunk(_Handle):
         if prefix.ndim != 2 or prefix.shape[1] != self.hidden:
             raise ValueError(f"prefix must be [n_prefix, {self.hidden}], got {prefix.shape}")
         _need_size("pad", pad, prefix.shape[0])
-        if not np.all((pad == 0) | (pad == 1)):
-            raise ValueError("pad entries must be 0 (padding) or 1 (real)")
         _need_size("noise", noise, self.chunk * self.max_action_dim)
 
     def run(self, prefix, pad, noise):

@@ -1520,9 +1520,26 @@ SplitPlan skinny_split_plan(int N, int K) {
     return p;
 }
 
+// 129..256 row-major rows over a narrow output (N <= 2048: at most 128
+// column blocks, where the tiles leave most CUs idle) take the skinny kernel
+// in row groups of at most 8 fragments, unsplit. Graph replays on MI355X,
+// tiles -> skinny: 177x960x960 5.87 -> 4.30 us, 177x960x320 5.65 -> 3.00,
+// 177x2560x960 9.82 -> 7.53, 256x960x960 5.81 -> 4.79, 200x4096x1024 13.5 ->
+// 12.0; wide outputs stay on the tiles (177x960x5120 6.63 -> 12.76).
+// VLA_HIP_SKINNY_MAXM=128 turns the route off, and a tile forced with
+// VLA_HIP_GEMM_TILE bypasses it (both read per call, like the other knobs).
+bool skinny_mid_rows(int M, int N, bool panel) {
+    if (M <= 128 || M > 256 || N > 2048 || panel) return false;
+    const char* tile = std::getenv("VLA_HIP_GEMM_TILE");
+    if (tile && *tile) return false;
+    const char* e = std::getenv("VLA_HIP_SKINNY_MAXM");
+    return !(e && std::atoi(e) == 128);
+}
+
 SplitPlan split_plan(int M, int N, int K) {
     SplitPlan p;
     if (M <= kPanelMaxRows) return skinny_split_plan(N, K);
+    if (skinny_mid_rows(M, N, false)) return p;
     if (K < 1024) return p;
     const Tile t = pick_tile(M, N, K);
     if (t.stages != 0) return p;
@@ -1601,18 +1618,7 @@ void launch_gemm_i8(const GemmArgs& a, hipStream_t st) {
         run_gemv(a, st);
         return;
     }
-    // 129..256 row-major rows over a narrow output (N <= 2048: at most 128
-    // column blocks, where the tiles leave most CUs idle) take the skinny
-    // kernel in row groups of at most 8 fragments. Graph replays on MI355X,
-    // tiles -> skinny: 177x960x960 5.87 -> 4.30 us, 177x960x320 5.65 ->
-    // 3.00, 177x2560x960 9.82 -> 7.53, 256x960x960 5.81 -> 4.79,
-    // 200x4096x1024 13.5 -> 12.0; wide outputs stay on the tiles
-    // (177x960x5120 6.63 -> 12.76). VLA_HIP_SKINNY_MAXM=128 turns it off.
-    static const int skinny_max = [] {
-        const char* e = std::getenv("VLA_HIP_SKINNY_MAXM");
-        return e && std::atoi(e) == 128 ? 128 : 256;
-    }();
-    if (a.M > 128 && a.M <= skinny_max && a.N <= 2048 && !a.a_panel) {
+    if (skinny_mid_rows(a.M, a.N, a.a_panel)) {
         const int nfrag = (a.M + 15) / 16, steps = (a.K + 63) / 64;
         int g = skinny_row_groups(a.M, a.N, a.K, 1);
         g = g < (nfrag + 7) / 8 ? (nfrag + 7) / 8 : g;

@@ -22,6 +22,7 @@
 #include "models.h"
 
 #include <algorithm>
+#include <cstdint>
 #include <cmath>
 #include <limits>
 
@@ -175,15 +176,21 @@ SmolvlaTf::~SmolvlaTf() {
 
 void SmolvlaTf::ensure(const int32_t* pad, int np) {
     VLA_REQUIRE(np >= 2 && np <= 65536 - C_, "smolvla: prefix length out of range");
-    // The reference sums the raw entries into the positions
-    // (smolvla_model.cpp:238,245), so only 0 / 1 mean what the masks assume.
-    for (int j = 0; j < np; j++)
-        VLA_REQUIRE(pad[j] == 0 || pad[j] == 1, "smolvla: pad entries must be 0 (padding) or 1 (real)");
     VLA_REQUIRE(pad[np - 1] != 0, "smolvla: the last prefix token (state) must be real");
-    // the masks and positions depend on exactly which prefix tokens are real
-    std::vector<uint8_t> real(np);
-    for (int j = 0; j < np; j++) real[j] = pad[j] != 0;
-    if (S_ && real == real_) return;
+    // As in the reference (smolvla_model.cpp:224-246), a pad entry is a truth
+    // value in the masks (nonzero = real) and its raw value is summed into the
+    // positions, so any int32 is taken; the running sums must stay within
+    // int32 (where the reference's int sum would overflow).
+    {
+        int64_t cum = 0;
+        for (int j = 0; j < np; j++) {
+            cum += pad[j];
+            VLA_REQUIRE(cum - 1 >= INT32_MIN && cum + C_ <= INT32_MAX, "smolvla: pad sums overflow the positions");
+        }
+    }
+    // the masks and positions depend on the whole pad vector
+    std::vector<int32_t> padv(pad, pad + np);
+    if (S_ && padv == pad_) return;
     VLA_HIP_CHECK(hipDeviceSynchronize());
     S_.reset();
     auto S = std::make_unique<DeviceArena>();
@@ -230,9 +237,9 @@ void SmolvlaTf::ensure(const int32_t* pad, int np) {
     pgroup_ = S->upload(grp.data(), grp.size());
     pallow_ = S->upload(allow.data(), allow.size());
     std::vector<int32_t> pos(np), pos_full(C), pos_reb(C);
-    int cum = 0;
+    int32_t cum = 0;  // in range: checked above
     for (int j = 0; j < np; j++) {
-        cum += pad[j] ? 1 : 0;
+        cum += pad[j];
         pos[j] = cum - 1;
     }
     // denoise mask and positions (:266-275; rebased :248-252 of action_expert.cpp)
@@ -286,7 +293,7 @@ void SmolvlaTf::ensure(const int32_t* pad, int np) {
         if (round_up(kpad4(k), 64) > maxld) maxld = round_up(kpad4(k), 64);
     ctx_.alloc(*S, R, maxld);
     S_ = std::move(S);
-    real_ = std::move(real);
+    pad_ = std::move(padv);
     key_++;  // a new layout: the captured graph is rebuilt
     np_ = np;
     SK_ = SK;
@@ -434,8 +441,7 @@ void SmolvlaTf::chunk_dev(const float* prefix, const int32_t* pad, int n_prefix,
         copy_f32(guide_, rtc->guide, (int64_t)C_ * mad_, caller);
         copy_f32(gweights_, rtc->weights, C_, caller);
     }
-    // the guided loop is a different graph from the plain one
-    replay_.run(key_ * 2 + (rtc_ ? 1 : 0), own_, caller, [this](hipStream_t st) { run(st); });
+    (rtc_ ? replay_rtc_ : replay_).run(key_, own_, caller, [this](hipStream_t st) { run(st); });
     copy_f32(actions, act_out_, (int64_t)C_ * mad_, caller);
 }
 

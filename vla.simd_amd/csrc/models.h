@@ -252,7 +252,7 @@ public:
     };
     void chunk_dev(const float* prefix, const int32_t* pad, int n_prefix, const float* noise,
                    float* actions, hipStream_t caller, const Rtc* rtc = nullptr);
-    int graph_nodes() const { return replay_.nodes(); }
+    int graph_nodes() const { return rtc_ ? replay_rtc_.nodes() : replay_.nodes(); }
 
 private:
     struct VlmLayer {
@@ -281,9 +281,9 @@ private:
     std::vector<ExpLayer> exp_;
     const float* out_norm_ = nullptr;
     DLinear ain_, at1_, at2_, aout_;
-    // per-shape state: real_ is the pad layout the buffers and tables were
-    // built for, key_ counts layouts (the graph replay key)
-    std::vector<uint8_t> real_;
+    // per-shape state: pad_ is the pad vector the buffers, masks and RoPE
+    // tables were built for, key_ counts layouts (the graph replay key)
+    std::vector<int32_t> pad_;
     uint64_t key_ = 0;
     int np_ = 0, SK_ = 0, QKVW_ = 0;
     std::unique_ptr<DeviceArena> S_;
@@ -303,7 +303,9 @@ private:
     bool dcausal_ = true, cnone_ = true;
     Ctx ctx_;
     hipStream_t own_ = nullptr;
-    GraphReplay replay_;
+    // the plain and the guided denoise loops are different graphs; each keeps
+    // its own, so alternating modes replay both
+    GraphReplay replay_, replay_rtc_;
 };
 
 // ---------------------------------------------------------------- SigLIP --

@@ -611,10 +611,27 @@ size_t octo_head_lds_bytes(int H, int TD, int emb, int flat) {
     return floats * 4 + qbytes;
 }
 
+// head_linear computes outputs n < 1024 / tpo with tpo >= 1, reads K inputs
+// from an LDS row sized for its layer, and (int8) 16-byte weight chunks up to
+// round16(K)
+static bool head_lin_fits(const HeadLin& L, int K, int max_n) {
+    if (L.K != K || L.N < 1 || L.N > max_n || L.N > 1024) return false;
+    if (L.Wq) return L.ws && L.ldw >= ((K + 15) & ~15) && L.ldw % 16 == 0;
+    return L.W != nullptr;
+}
+
 void launch_octo_head(const OctoHeadArgs& a, hipStream_t st) {
     const size_t lds = octo_head_lds_bytes(a.H, a.TD, a.emb, a.flat);
     VLA_REQUIRE(a.nb >= 0 && a.nb <= kOctoHeadMaxBlocks && lds <= 64 * 1024 && a.steps > 0,
                 "octo head: shape beyond the fused kernel");
+    VLA_REQUIRE(a.H > 0 && 4 * a.H <= 1024 && a.flat > 0 && a.flat <= 1024 && a.TD >= 0 && a.emb >= 0,
+                "octo head: hidden width (x4) and action row must be at most 1024");
+    bool fits = head_lin_fits(a.in_proj, a.TD + a.emb + a.flat, a.H) && a.in_proj.N == a.H &&
+                head_lin_fits(a.out_proj, a.H, a.flat) && a.out_proj.N == a.flat;
+    for (int b = 0; b < a.nb && fits; b++)
+        fits = a.ln_s[b] && head_lin_fits(a.d0[b], a.H, 4 * a.H) && head_lin_fits(a.d1[b], a.d0[b].N, a.H) &&
+               a.d1[b].N == a.H;
+    VLA_REQUIRE(fits, "octo head: a layer's width does not match the fused kernel's rows (N <= 1024)");
     octo_head_kernel<<<1, 1024, lds, st>>>(a);
     VLA_LAUNCH_CHECK();
 }
