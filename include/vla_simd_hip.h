@@ -293,6 +293,30 @@ VLA_API int32_t vla_linear_i8_forward_quantized_dev(const vla_linear_i8* lin, fl
                                                     const int8_t* xq, int32_t ldx,
                                                     const float* ascale, int32_t seq, int32_t act,
                                                     int32_t accumulate, void* stream);
+/* Host copies of the resident state nn::Linear keeps on the host after
+ * init_int8 (linear.cpp:97-100): Wq [N, ldq] int8 rows (ldq >= i8_kpad(K),
+ * zero past K) and wscale [N]. */
+VLA_API int32_t vla_linear_i8_download(const vla_linear_i8* lin, int8_t* Wq, int32_t ldq, float* wscale);
+/* Replaces the resident bias with host [N] values (null drops it): the op
+ * layer passes nn::Linear's bias per call (linear.cpp:131). */
+VLA_API int32_t vla_linear_i8_set_bias(vla_linear_i8* lin, const float* bias);
+/* Linear::forward's int8 branch with host pointers over resident weights
+ * (linear.cpp:121-133, dense_linear_i8's contract quant_ops.h:66-72): x
+ * [seq,K] fp32 in, out [seq,N]; xq_scratch [seq, ldq] (ldq >= i8_kpad(K))
+ * and ascale_scratch [seq], each optional, receive the quantized rows. Only
+ * activations and outputs cross PCIe. Synchronous. */
+VLA_API int32_t vla_linear_i8_forward(const vla_linear_i8* lin, float* out, const float* x, int32_t seq,
+                                      int8_t* xq_scratch, int32_t ldq, float* ascale_scratch);
+/* Linear::forward_quantized (linear.cpp:170-172) with host pointers over
+ * resident weights: xq [seq, ldq] int8 rows (ldq >= i8_kpad(K)), ascale [seq]. */
+VLA_API int32_t vla_linear_i8_forward_quantized(const vla_linear_i8* lin, float* out, const int8_t* xq,
+                                                int32_t ldq, const float* ascale, int32_t seq);
+/* Host-to-device bytes this library has issued since it was loaded, all of
+ * them (weights_only 0) or those that carried weights (int8 rows, scales,
+ * biases, fp32 weights; weights_only 1). The op API's host forms upload a
+ * layer's weights on every call; resident layers once. No counterpart in the
+ * reference (its weights are host memory): it shows where PCIe time goes. */
+VLA_API int64_t vla_h2d_bytes(int32_t weights_only);
 
 /* ---------------------------------------------------- lm_ops.h (fp32) ---- */
 
@@ -389,6 +413,12 @@ VLA_API int32_t vla_dense_linear_dev(float* out, int32_t ldo, const float* x, in
 VLA_API int32_t vla_conv2d_i8(float* out, const float* x, const int8_t* Wq, const float* wscale,
                               const float* bias, int32_t H, int32_t Wd, int32_t Cin, int32_t Cout,
                               int32_t k, int32_t stride, int32_t pad);
+/* conv2d_i8 (conv_ops.h:31-35) with host activations over resident weights
+ * (vla_linear_i8_create of the [Cout, k*k*Cin] matrix, its bias included):
+ * nn::Conv's forward (conv.cpp:55-60) once its weights are on the device.
+ * Synchronous. */
+VLA_API int32_t vla_conv2d_i8_resident(const vla_linear_i8* lin, float* out, const float* x, int32_t H,
+                                       int32_t Wd, int32_t Cin, int32_t k, int32_t stride, int32_t pad);
 VLA_API int64_t vla_conv2d_i8_workspace_bytes(int32_t H, int32_t Wd, int32_t Cin, int32_t Cout,
                                               int32_t k, int32_t stride, int32_t pad);
 VLA_API int32_t vla_conv2d_i8_dev(const vla_linear_i8* lin, float* out, const float* x, int32_t H,

@@ -133,6 +133,15 @@ def ref_nn(backend: str):
         L.ref_unet_load.argtypes, L.ref_unet_load.restype = [ctypes.c_char_p, P, i, P], P
         L.ref_unet_free.argtypes = [P]
         L.ref_unet_forward.argtypes, L.ref_unet_forward.restype = [P, P, P, P, i], i
+        L.ref_nn_linear_load.argtypes, L.ref_nn_linear_load.restype = [P, P, i, i, i, P], P
+        L.ref_nn_linear_run.argtypes, L.ref_nn_linear_run.restype = [P, P, P, P, i, P], i
+        L.ref_nn_linear_free.argtypes = [P]
+        L.ref_nn_mha_load.argtypes, L.ref_nn_mha_load.restype = [i, i, P, P, i], P
+        L.ref_nn_mha_run.argtypes, L.ref_nn_mha_run.restype = [P, P, P, P, i, i, P], i
+        L.ref_nn_mha_free.argtypes = [P]
+        L.ref_nn_conv_load.argtypes, L.ref_nn_conv_load.restype = [P, P, i, i, i, i, P], P
+        L.ref_nn_conv_run.argtypes, L.ref_nn_conv_run.restype = [P, P, i, i, i, i, P], i
+        L.ref_nn_conv_free.argtypes = [P]
         _nn_libs[backend] = L
     return _nn_libs[backend]
 
@@ -161,6 +170,88 @@ def nn_mha_forward(backend, dim, heads, W, b, xq, xk, xv, rows, seq_kv, int8=1):
     if st != 0:
         raise RuntimeError("ref_nn_mha_forward failed")
     return out, q, k, v
+
+
+class NnLinear:
+    """A reference nn::Linear kept across calls on one op backend."""
+
+    def __init__(self, backend, W, b, int8=1):
+        self.L = ref_nn(backend)
+        self.W, self.N, self.K = _f32(W), W.shape[0], W.shape[1]
+        q = np.zeros(1, np.int32)
+        self.h = self.L.ref_nn_linear_load(_p(self.W), _p(None if b is None else _f32(b)), self.N, self.K,
+                                           int(int8), _p(q))
+        if not self.h:
+            raise RuntimeError("ref_nn_linear_load failed")
+        self.int8 = bool(q[0])
+
+    def forward(self, x):
+        x = _f32(x)
+        out = np.empty((x.shape[0], self.N), np.float32)
+        if self.L.ref_nn_linear_run(self.h, _p(x), None, None, x.shape[0], _p(out)) != 0:
+            raise RuntimeError("ref_nn_linear_run failed")
+        return out
+
+    def forward_quantized(self, xq, scales):
+        xq = np.ascontiguousarray(xq, np.int8)
+        out = np.empty((xq.shape[0], self.N), np.float32)
+        if self.L.ref_nn_linear_run(self.h, None, _p(xq), _p(_f32(scales)), xq.shape[0], _p(out)) != 0:
+            raise RuntimeError("ref_nn_linear_run failed")
+        return out
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            self.L.ref_nn_linear_free(self.h)
+
+
+class NnMha:
+    """A reference nn::MhaQKV (four dim x dim projections sharing W, b) kept
+    across calls; forward(xq, xk, xv, rows, seq_kv) keys its shared
+    quantization on which inputs are the same array."""
+
+    def __init__(self, backend, dim, heads, W, b, int8=1):
+        self.L = ref_nn(backend)
+        self.dim = dim
+        self.h = self.L.ref_nn_mha_load(dim, heads, _p(_f32(W)), _p(_f32(b)), int(int8))
+        if not self.h:
+            raise RuntimeError("ref_nn_mha_load failed")
+
+    def forward(self, xq, xk, xv, rows, seq_kv):
+        out = np.empty((rows, self.dim), np.float32)
+        if self.L.ref_nn_mha_run(self.h, _p(xq), _p(xk), _p(xv), rows, seq_kv, _p(out)) != 0:
+            raise RuntimeError("ref_nn_mha_run failed")
+        return out
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            self.L.ref_nn_mha_free(self.h)
+
+
+class NnConv:
+    """A reference nn::Conv2d (W [Cout, k, k, Cin], NHWC) kept across calls."""
+
+    def __init__(self, backend, W, b, int8=1):
+        self.L = ref_nn(backend)
+        self.Cout, self.k, _, self.Cin = W.shape
+        q = np.zeros(1, np.int32)
+        self.h = self.L.ref_nn_conv_load(_p(_f32(W)), _p(None if b is None else _f32(b)), self.Cout, self.k,
+                                         self.Cin, int(int8), _p(q))
+        if not self.h:
+            raise RuntimeError("ref_nn_conv_load failed")
+        self.int8 = bool(q[0])
+
+    def forward(self, x, stride, pad):
+        x = _f32(x)
+        H, Wd = x.shape[0], x.shape[1]
+        Ho, Wo = (H + 2 * pad - self.k) // stride + 1, (Wd + 2 * pad - self.k) // stride + 1
+        out = np.empty((Ho, Wo, self.Cout), np.float32)
+        if self.L.ref_nn_conv_run(self.h, _p(x), H, Wd, stride, pad, _p(out)) != 0:
+            raise RuntimeError("ref_nn_conv_run failed")
+        return out
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            self.L.ref_nn_conv_free(self.h)
 
 
 class NnUnet:

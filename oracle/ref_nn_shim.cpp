@@ -10,12 +10,14 @@
  */
 #include "models/diffusion/unet1d.h"
 #include "nn/attention.h"
+#include "nn/conv.h"
 #include "nn/linear.h"
 #include "ops/quant_ops.h"
 
 #include <cstdio>
 #include <cstring>
 #include <exception>
+#include <memory>
 #include <vector>
 
 #define REF_API extern "C" __attribute__((visibility("default")))
@@ -65,6 +67,117 @@ REF_API int ref_nn_mha_forward(int dim, int heads, const float* W, const float* 
         return -1;
     }
 }
+
+/* Layers that live across calls (a model's layers are loaded once and run
+ * many times): nn::Linear, nn::MhaQKV and nn::Conv2d with their weights
+ * (the layers keep raw pointers to W and b, so the handle owns copies). */
+struct NnLinear {
+    std::vector<float> W, b;
+    nn::Linear lin;
+    bool q = false;
+};
+
+REF_API void* ref_nn_linear_load(const float* W, const float* b, int N, int K, int int8, int* is_int8) {
+    try {
+        auto h = std::make_unique<NnLinear>();
+        h->W.assign(W, W + (size_t)N * K);
+        if (b) h->b.assign(b, b + N);
+        h->lin.init(h->W.data(), b ? h->b.data() : nullptr, N, K, nn::Linear::Role::Gemm);
+        h->q = int8 && h->lin.init_int8();
+        *is_int8 = h->q ? 1 : 0;
+        return h.release();
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "ref_nn_linear_load: %s\n", e.what());
+        return nullptr;
+    }
+}
+
+/* forward (linear.cpp:121-133), or with quantized input (xq [seq,
+ * i8_kpad(K)], scales [seq]) forward_quantized (:170-172) */
+REF_API int ref_nn_linear_run(void* h, const float* x, const int8_t* xq, const float* scales, int seq, float* out) {
+    try {
+        auto* l = static_cast<NnLinear*>(h);
+        if (xq) l->lin.forward_quantized(out, xq, scales, seq);
+        else l->lin.forward(out, x, seq);
+        return 0;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "ref_nn_linear_run: %s\n", e.what());
+        return -1;
+    }
+}
+
+REF_API void ref_nn_linear_free(void* h) { delete static_cast<NnLinear*>(h); }
+
+struct NnMha {
+    std::vector<float> W, b;
+    nn::MhaQKV layer;
+    nn::Scratch s;
+};
+
+REF_API void* ref_nn_mha_load(int dim, int heads, const float* W, const float* b, int int8) {
+    try {
+        auto h = std::make_unique<NnMha>();
+        h->W.assign(W, W + (size_t)dim * dim);
+        h->b.assign(b, b + dim);
+        h->layer.set_shape(heads, dim / heads);
+        for (nn::Linear* lin : {&h->layer.wq, &h->layer.wk, &h->layer.wv, &h->layer.wo}) {
+            lin->init(h->W.data(), h->b.data(), dim, dim, nn::Linear::Role::Gemm);
+            if (int8) lin->init_int8();
+        }
+        return h.release();
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "ref_nn_mha_load: %s\n", e.what());
+        return nullptr;
+    }
+}
+
+REF_API int ref_nn_mha_run(void* h, const float* xq, const float* xk, const float* xv, int rows, int seq_kv,
+                           float* out) {
+    try {
+        auto* m = static_cast<NnMha*>(h);
+        m->layer.forward(out, xq, xk, xv, rows, seq_kv, m->s);
+        return 0;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "ref_nn_mha_run: %s\n", e.what());
+        return -1;
+    }
+}
+
+REF_API void ref_nn_mha_free(void* h) { delete static_cast<NnMha*>(h); }
+
+struct NnConv {
+    std::vector<float> W, b;
+    nn::Conv2d conv;
+    bool q = false;
+};
+
+/* nn::Conv2d (conv.cpp): W [Cout, k, k, Cin], init_int8 when int8 != 0 */
+REF_API void* ref_nn_conv_load(const float* W, const float* b, int Cout, int k, int Cin, int int8, int* is_int8) {
+    try {
+        auto h = std::make_unique<NnConv>();
+        h->W.assign(W, W + (size_t)Cout * k * k * Cin);
+        if (b) h->b.assign(b, b + Cout);
+        h->conv.init(h->W.data(), b ? h->b.data() : nullptr, Cout, k, Cin);
+        h->q = int8 && h->conv.init_int8();
+        *is_int8 = h->q ? 1 : 0;
+        return h.release();
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "ref_nn_conv_load: %s\n", e.what());
+        return nullptr;
+    }
+}
+
+REF_API int ref_nn_conv_run(void* h, const float* x, int H, int Wd, int stride, int pad, float* out) {
+    try {
+        static_cast<NnConv*>(h)->conv.forward(out, x, H, Wd, stride, pad);
+        return 0;
+    } catch (const std::exception& e) {
+        std::fprintf(stderr, "ref_nn_conv_run: %s\n", e.what());
+        return -1;
+    }
+}
+
+REF_API void ref_nn_conv_free(void* h) { delete static_cast<NnConv*>(h); }
 
 /* The backend's pack + pre kernel against its scalar statement of the same
  * call (test_ops.cpp:138-157): W [N, K] fp32 packed by pack_weights_i8, x

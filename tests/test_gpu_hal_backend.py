@@ -136,3 +136,86 @@ def test_diffusion_unet_int8_linears_on_device(nn, tmp_path, full):
     for t in (0, 37, 99):
         a, b = hip.forward(sample, gc, t), cpu.forward(sample, gc, t)
         assert same_bits(a, b), f"UNet noise prediction differs at t={t}"
+
+
+def _weight_bytes(vla):
+    return int(vla.lib().vla_h2d_bytes(1))
+
+
+def test_int8_layers_stay_resident_on_device(nn, vla, tmp_path, monkeypatch):
+    """Weight residency of the reference's own layers on the HIP backend: an
+    nn::Linear, an nn::MhaQKV (four int8 projections, shared quantization),
+    an nn::Conv2d and Diffusion Policy's UNet upload their int8 weights once,
+    at init_int8's pack_weights_i8 (linear.cpp:97-99, conv.cpp:46); each
+    forward after that moves no weight bytes to the device (the library's own
+    H2D byte counter), and its outputs equal, bit for bit, both the same
+    layers on the upload-per-call path (VLA_HIP_RESIDENT_MB=0) and the CPU
+    build."""
+    from helpers import load_pkg
+    load_pkg()
+    import vla_simd_amd.checkpoints as ck
+    import vla_simd_amd.synth as synth
+    fr = nn.Frand()
+    W = _rv(fr, 3200 * 512, -0.05, 0.05).reshape(3200, 512)
+    b = _rv(fr, 3200, -0.02, 0.02)
+    x = _rv(fr, 100 * 512).reshape(100, 512)
+    Wc = _rv(fr, 64 * 3 * 3 * 32, -0.1, 0.1).reshape(64, 3, 3, 32)
+    bc = _rv(fr, 64)
+    img = _rv(fr, 20 * 24 * 32).reshape(20, 24, 32)
+    dim = 64
+    Wm = _rv(fr, dim * dim, -0.2, 0.2)
+    bm = _rv(fr, dim)
+    xm = _rv(fr, 33 * dim).reshape(33, dim)
+    c = dict(ck.DP_UNET_BASE, horizon=16, down_dims=(64, 128, 256), step_embed_dim=32, num_keypoints=8)
+    d = ck.write_dp_unet(str(tmp_path / "unet"), c)
+    sample = synth.normal("dp.sample", (c["horizon"], c["action_dim"]))
+    gc = synth.normal("dp.gc", (ck.dp_cond_dim(c) - c["step_embed_dim"],))
+
+    def layers():
+        return (nn.NnLinear("hip", W, b), nn.NnMha("hip", dim, 4, Wm, bm), nn.NnConv("hip", Wc, bc),
+                nn.NnUnet("hip", d, c, 1))
+
+    def run(lin, mha, conv, unet):
+        xq, sa = nn.quantize_act_i8(x)
+        return [lin.forward(x), lin.forward_quantized(xq, sa), mha.forward(xm, xm, xm, 33, 33),
+                conv.forward(img, 1, 1), conv.forward(img, 2, 1)] + [unet.forward(sample, gc, t) for t in (0, 37)]
+
+    monkeypatch.setenv("VLA_HIP_RESIDENT_MB", "0")
+    per_call = layers()
+    assert per_call[0].int8 and per_call[2].int8
+    before = _weight_bytes(vla)
+    want = run(*per_call)
+    uploaded = _weight_bytes(vla) - before
+    monkeypatch.delenv("VLA_HIP_RESIDENT_MB")
+    resident = layers()
+    run(*resident)  # first calls: biases move once
+    for rep in range(3):
+        before = _weight_bytes(vla)
+        got = run(*resident)
+        moved = _weight_bytes(vla) - before
+        print(f"residency: forward weight bytes {moved} (upload-per-call path: {uploaded})", flush=True)
+        assert moved == 0, f"repeat {rep}: {moved} weight bytes uploaded"
+        for i, (g, w) in enumerate(zip(got, want)):
+            assert same_bits(g, w), f"output {i} differs from the upload-per-call path"
+    assert uploaded > 3200 * 512
+    # the CPU build agrees (its own panels and VNNI kernel)
+    assert same_bits(got[0], nn.NnLinear("cpu", W, b).forward(x))
+    cpu_conv = nn.NnConv("cpu", Wc, bc)
+    assert same_bits(got[3], cpu_conv.forward(img, 1, 1)) and same_bits(got[4], cpu_conv.forward(img, 2, 1))
+    cpu_unet = nn.NnUnet("cpu", d, c, 1)
+    assert same_bits(got[5], cpu_unet.forward(sample, gc, 0)) and same_bits(got[6], cpu_unet.forward(sample, gc, 37))
+
+
+def test_residency_follows_repacked_buffers(nn, vla):
+    """A buffer packed again (the same nn::Linear address with new weights, as
+    when a layer object is re-initialised) replaces its resident copy: the
+    forward uses the new weights. Many layers packed and dropped in turn stay
+    correct (each new layer's pack replaces any stale entry at its address)."""
+    fr = nn.Frand()
+    x = _rv(fr, 17 * 96).reshape(17, 96)
+    for i in range(6):
+        W = _rv(fr, 48 * 96, -0.3, 0.3).reshape(48, 96)
+        b = _rv(fr, 48) if i % 2 else None
+        got = nn.NnLinear("hip", W, b).forward(x)
+        want = nn.NnLinear("cpu", W, b).forward(x)
+        assert same_bits(got, want), f"layer {i}"

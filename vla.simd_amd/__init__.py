@@ -53,6 +53,8 @@ EXPORTS = (
     "vla_linear_i8_create", "vla_linear_i8_create_q", "vla_linear_i8_free",
     "vla_linear_i8_weights", "vla_linear_i8_wscale", "vla_linear_i8_ldw",
     "vla_linear_i8_forward_dev", "vla_linear_i8_forward_quantized_dev",
+    "vla_linear_i8_download", "vla_linear_i8_set_bias", "vla_linear_i8_forward", "vla_linear_i8_forward_quantized",
+    "vla_conv2d_i8_resident", "vla_h2d_bytes",
     "vla_gqa_attention_masked", "vla_gqa_attention_dense", "vla_attention_dev", "vla_attention",
     "vla_layernorm", "vla_layernorm_dev", "vla_rmsnorm", "vla_rmsnorm_dev",
     "vla_rope_neox", "vla_rope_neox_dev",
@@ -169,6 +171,12 @@ def _declare(L):
         "vla_linear_i8_ldw": (i32, [P]),
         "vla_linear_i8_forward_dev": (i32, [P, P, P, i32, P, P, i32, i32, P]),
         "vla_linear_i8_forward_quantized_dev": (i32, [P, P, P, i32, P, i32, i32, i32, P]),
+        "vla_linear_i8_download": (i32, [P, P, i32, P]),
+        "vla_linear_i8_set_bias": (i32, [P, P]),
+        "vla_linear_i8_forward": (i32, [P, P, P, i32, P, i32, P]),
+        "vla_linear_i8_forward_quantized": (i32, [P, P, P, i32, P, i32]),
+        "vla_conv2d_i8_resident": (i32, [P, P, P, i32, i32, i32, i32, i32, i32]),
+        "vla_h2d_bytes": (ctypes.c_int64, [i32]),
         "vla_gqa_attention_masked": (i32, [P, P, P, P, i32, i32, i32, i32, i32, f32, P]),
         "vla_gqa_attention_dense": (i32, [P, P, P, P, i32, i32, i32, i32, i32, f32]),
         "vla_attention_dev": (i32, [P, i32, P, i32, P, i32, P, i32, i32, i32, i32, i32, i32, f32,

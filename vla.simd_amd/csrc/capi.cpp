@@ -173,11 +173,11 @@ static void gemm_host(float* out, int32_t* acc32, const int8_t* xq, const float*
     GemmArgs a{};
     a.A = S.upload(xq, (size_t)seq * Kp, st);
     a.lda = Kp;
-    a.B = S.upload(Wq, (size_t)N * Kp, st);
+    a.B = S.upload(Wq, (size_t)N * Kp, st, true);
     a.ldb = Kp;
     a.ascale = S.upload(ascale, (size_t)seq, st);
-    a.wscale = S.upload(wscale, (size_t)N, st);
-    a.bias = S.upload(bias, (size_t)N, st);
+    a.wscale = S.upload(wscale, (size_t)N, st, true);
+    a.bias = S.upload(bias, (size_t)N, st, true);
     void* dout = S.take((size_t)seq * N * 4);
     if (acc32) a.acc32 = static_cast<int32_t*>(dout);
     else a.out = static_cast<float*>(dout);
@@ -228,11 +228,11 @@ VLA_API int32_t vla_dense_linear_i8(float* out, const float* x, const int8_t* Wq
         GemmArgs a{};
         a.A = dq;
         a.lda = Kp;
-        a.B = S.upload(Wq, (size_t)N * Kp, st);
+        a.B = S.upload(Wq, (size_t)N * Kp, st, true);
         a.ldb = Kp;
         a.ascale = ds;
-        a.wscale = S.upload(wscale, (size_t)N, st);
-        a.bias = S.upload(bias, (size_t)N, st);
+        a.wscale = S.upload(wscale, (size_t)N, st, true);
+        a.bias = S.upload(bias, (size_t)N, st, true);
         a.out = S.alloc<float>((size_t)seq * N);
         a.ldo = N;
         a.M = seq;
@@ -485,11 +485,79 @@ VLA_API vla_linear_i8* vla_linear_i8_create(const float* W, const float* bias, i
 VLA_API vla_linear_i8* vla_linear_i8_create_q(const int8_t* Wq, const float* wscale,
                                               const float* bias, int32_t N, int32_t K) {
     vla_linear_i8* out = nullptr;
-    guarded("vla_linear_i8_create_q", [&] { out = Linear::from_i8(Wq, wscale, bias, N, K).release(); });
+    guarded("vla_linear_i8_create_q", [&] { out = Linear::from_i8(Wq, K, wscale, bias, N, K).release(); });
     return out;
 }
 
 VLA_API void vla_linear_i8_free(vla_linear_i8* lin) { delete lin; }
+
+VLA_API int32_t vla_linear_i8_download(const vla_linear_i8* lin, int8_t* Wq, int32_t ldq, float* wscale) {
+    return guarded("vla_linear_i8_download", [&] {
+        VLA_REQUIRE(lin, "null linear");
+        lin->download(Wq, ldq, wscale);
+    });
+}
+
+VLA_API int32_t vla_linear_i8_set_bias(vla_linear_i8* lin, const float* bias) {
+    return guarded("vla_linear_i8_set_bias", [&] {
+        VLA_REQUIRE(lin, "null linear");
+        lin->set_bias(bias);
+    });
+}
+
+// Host-pointer forward over resident weights: only the activations and
+// outputs cross PCIe.
+static void linear_host(const vla_linear_i8* lin, float* out, const float* x, const int8_t* xq_in, int32_t ldq,
+                        int8_t* xq_out, const float* ascale_in, float* ascale_out, int32_t seq) {
+    VLA_REQUIRE(lin, "null linear");
+    VLA_REQUIRE(seq >= 0, "need seq >= 0");
+    const int N = lin->N(), K = lin->K(), Kp = kpad4(K), ldw = lin->ldw();
+    VLA_REQUIRE(seq == 0 || (out && (x || (xq_in && ascale_in))), "null buffer");
+    VLA_REQUIRE(!(xq_in || xq_out) || ldq >= Kp, "int8 row stride below i8_kpad(K)");
+    if (seq == 0) return;
+    Staging& S = staging();
+    auto lk = S.lock();
+    hipStream_t st = library_stream();
+    S.reset(align256((size_t)seq * K * 4) + align256((size_t)seq * ldw) + align256((size_t)seq * 4) +
+            align256((size_t)seq * N * 4));
+    int8_t* dq = S.alloc<int8_t>((size_t)seq * ldw);
+    float* ds = S.alloc<float>((size_t)seq);
+    float* dout = S.alloc<float>((size_t)seq * N);
+    if (x) {
+        const float* dx = S.upload(x, (size_t)seq * K, st);
+        lin->forward(dout, N, dx, seq, dq, ds, 0, 0, st);
+        if (xq_out) VLA_HIP_CHECK(hipMemcpy2DAsync(xq_out, ldq, dq, ldw, Kp, seq, hipMemcpyDeviceToHost, st));
+        if (ascale_out) VLA_HIP_CHECK(hipMemcpyAsync(ascale_out, ds, (size_t)seq * 4, hipMemcpyDeviceToHost, st));
+    } else {
+        // rows of i8_kpad(K) bytes into the resident stride, zero past it
+        VLA_HIP_CHECK(hipMemsetAsync(dq, 0, (size_t)seq * ldw, st));
+        VLA_HIP_CHECK(hipMemcpy2DAsync(dq, ldw, xq_in, ldq, Kp, seq, hipMemcpyHostToDevice, st));
+        count_h2d((size_t)seq * Kp, false);
+        VLA_HIP_CHECK(hipMemcpyAsync(ds, ascale_in, (size_t)seq * 4, hipMemcpyHostToDevice, st));
+        count_h2d((size_t)seq * 4, false);
+        lin->forward_quantized(dout, N, dq, ldw, ds, seq, 0, 0, st);
+    }
+    VLA_HIP_CHECK(hipMemcpyAsync(out, dout, (size_t)seq * N * 4, hipMemcpyDeviceToHost, st));
+    VLA_HIP_CHECK(hipStreamSynchronize(st));
+}
+
+VLA_API int32_t vla_linear_i8_forward(const vla_linear_i8* lin, float* out, const float* x, int32_t seq,
+                                      int8_t* xq_scratch, int32_t ldq, float* ascale_scratch) {
+    return guarded("vla_linear_i8_forward", [&] {
+        VLA_REQUIRE(seq == 0 || x, "null activations");
+        linear_host(lin, out, x, nullptr, ldq, xq_scratch, nullptr, ascale_scratch, seq);
+    });
+}
+
+VLA_API int32_t vla_linear_i8_forward_quantized(const vla_linear_i8* lin, float* out, const int8_t* xq, int32_t ldq,
+                                                const float* ascale, int32_t seq) {
+    return guarded("vla_linear_i8_forward_quantized", [&] {
+        VLA_REQUIRE(seq == 0 || (xq && ascale), "null activations");
+        linear_host(lin, out, nullptr, xq, ldq, nullptr, ascale, nullptr, seq);
+    });
+}
+
+VLA_API int64_t vla_h2d_bytes(int32_t weights_only) { return (int64_t)h2d_bytes(weights_only != 0); }
 VLA_API const int8_t* vla_linear_i8_weights(const vla_linear_i8* lin) { return lin ? lin->Wq() : nullptr; }
 VLA_API const float* vla_linear_i8_wscale(const vla_linear_i8* lin) { return lin ? lin->wscale() : nullptr; }
 VLA_API int32_t vla_linear_i8_ldw(const vla_linear_i8* lin) { return lin ? lin->ldw() : 0; }
@@ -552,43 +620,67 @@ VLA_API int32_t vla_conv2d_i8_dev(const vla_linear_i8* lin, float* out, const fl
     });
 }
 
-VLA_API int32_t vla_conv2d_i8(float* out, const float* x, const int8_t* Wq, const float* wscale,
-                              const float* bias, int32_t H, int32_t Wd, int32_t Cin, int32_t Cout, int32_t k,
-                              int32_t stride, int32_t pad) {
-    return guarded("vla_conv2d_i8", [&] {
-        VLA_REQUIRE(Cout > 0, "need Cout > 0");
-        const ConvShape c = conv_shape(H, Wd, Cin, k, stride, pad, Cout);
-        VLA_REQUIRE(out && x && Wq && wscale, "null buffer");
-        const int Kp = kpad4(c.K), ldw = (Kp + 63) & ~63;
-        const size_t nin = (size_t)H * Wd * Cin, nout = (size_t)c.npix * Cout;
-        Staging& S = staging();
-        auto lk = S.lock();
-        hipStream_t st = library_stream();
-        S.reset(align256(nin * 4) + align256((size_t)Cout * ldw) + 2 * align256((size_t)Cout * 4) +
-                align256(nout * 4) + align256(c.work));
-        ConvArgs a{};
-        a.x = S.upload(x, nin, st);
+// conv2d_i8 with host activations: weights from a resident layer (lin) or
+// uploaded from host rows (Wq [Cout][i8_kpad(K)], wscale, bias)
+static void conv_host(const vla_linear_i8* lin, float* out, const float* x, const int8_t* Wq, const float* wscale,
+                      const float* bias, int H, int Wd, int Cin, int Cout, int k, int stride, int pad) {
+    VLA_REQUIRE(Cout > 0, "need Cout > 0");
+    const ConvShape c = conv_shape(H, Wd, Cin, k, stride, pad, Cout);
+    VLA_REQUIRE(out && x && (lin || (Wq && wscale)), "null buffer");
+    VLA_REQUIRE(!lin || (lin->K() == c.K && lin->N() == Cout), "the weights' shape is not [Cout, k*k*Cin]");
+    const int Kp = kpad4(c.K), ldw = (Kp + 63) & ~63;
+    const size_t nin = (size_t)H * Wd * Cin, nout = (size_t)c.npix * Cout;
+    Staging& S = staging();
+    auto lk = S.lock();
+    hipStream_t st = library_stream();
+    S.reset(align256(nin * 4) + (lin ? 0 : align256((size_t)Cout * ldw) + 2 * align256((size_t)Cout * 4)) +
+            align256(nout * 4) + align256(c.work));
+    ConvArgs a{};
+    a.x = S.upload(x, nin, st);
+    if (lin) {
+        a.Wq = lin->Wq();
+        a.ldw = lin->ldw();
+        a.wscale = lin->wscale();
+        a.bias = lin->bias();
+    } else {
         // [Cout][i8_kpad(K)] rows (vla_pack_weights_i8) into 64-byte rows for the aligned GEMM
         int8_t* w = S.alloc<int8_t>((size_t)Cout * ldw);
         VLA_HIP_CHECK(hipMemsetAsync(w, 0, (size_t)Cout * ldw, st));
         VLA_HIP_CHECK(hipMemcpy2DAsync(w, ldw, Wq, Kp, Kp, Cout, hipMemcpyHostToDevice, st));
+        count_h2d((size_t)Cout * Kp, true);
         a.Wq = w;
         a.ldw = ldw;
-        a.wscale = S.upload(wscale, (size_t)Cout, st);
-        a.bias = S.upload(bias, (size_t)Cout, st);
-        a.out = S.alloc<float>(nout);
-        a.H = H;
-        a.Wd = Wd;
-        a.Cin = Cin;
-        a.Cout = Cout;
-        a.k = k;
-        a.stride = stride;
-        a.pad = pad;
-        a.work = S.alloc<char>(c.work);
-        a.work_bytes = c.work;
-        launch_conv2d_i8(a, st);
-        VLA_HIP_CHECK(hipMemcpyAsync(out, a.out, nout * 4, hipMemcpyDeviceToHost, st));
-        VLA_HIP_CHECK(hipStreamSynchronize(st));
+        a.wscale = S.upload(wscale, (size_t)Cout, st, true);
+        a.bias = S.upload(bias, (size_t)Cout, st, true);
+    }
+    a.out = S.alloc<float>(nout);
+    a.H = H;
+    a.Wd = Wd;
+    a.Cin = Cin;
+    a.Cout = Cout;
+    a.k = k;
+    a.stride = stride;
+    a.pad = pad;
+    a.work = S.alloc<char>(c.work);
+    a.work_bytes = c.work;
+    launch_conv2d_i8(a, st);
+    VLA_HIP_CHECK(hipMemcpyAsync(out, a.out, nout * 4, hipMemcpyDeviceToHost, st));
+    VLA_HIP_CHECK(hipStreamSynchronize(st));
+}
+
+VLA_API int32_t vla_conv2d_i8(float* out, const float* x, const int8_t* Wq, const float* wscale,
+                              const float* bias, int32_t H, int32_t Wd, int32_t Cin, int32_t Cout, int32_t k,
+                              int32_t stride, int32_t pad) {
+    return guarded("vla_conv2d_i8", [&] {
+        conv_host(nullptr, out, x, Wq, wscale, bias, H, Wd, Cin, Cout, k, stride, pad);
+    });
+}
+
+VLA_API int32_t vla_conv2d_i8_resident(const vla_linear_i8* lin, float* out, const float* x, int32_t H,
+                                       int32_t Wd, int32_t Cin, int32_t k, int32_t stride, int32_t pad) {
+    return guarded("vla_conv2d_i8_resident", [&] {
+        VLA_REQUIRE(lin, "null weights");
+        conv_host(lin, out, x, nullptr, nullptr, nullptr, H, Wd, Cin, lin->N(), k, stride, pad);
     });
 }
 
@@ -816,8 +908,8 @@ VLA_API int32_t vla_dense_linear(float* out, const float* x, const float* W, con
         S.reset(align256((size_t)seq * K * 4) + align256((size_t)N * K * 4) + align256((size_t)N * 4) +
                 align256((size_t)seq * N * 4));
         const float* dx = S.upload(x, (size_t)seq * K, st);
-        const float* dW = S.upload(W, (size_t)N * K, st);
-        const float* db = S.upload(bias, (size_t)N, st);
+        const float* dW = S.upload(W, (size_t)N * K, st, true);
+        const float* db = S.upload(bias, (size_t)N, st, true);
         float* dout = S.alloc<float>((size_t)seq * N);
         launch_linear_f32(dout, N, dx, K, dW, K, db, seq, N, K, 0, 0, 1.0f, st);
         VLA_HIP_CHECK(hipMemcpyAsync(out, dout, (size_t)seq * N * 4, hipMemcpyDeviceToHost, st));

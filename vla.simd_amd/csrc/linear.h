@@ -16,8 +16,8 @@ struct vla_linear_i8 {
     // Linear::init + init_int8 from fp32 W [N,K] (host). K bound as
     // linear.cpp:67; any N (the GPU layout has no 16-row panels).
     static std::unique_ptr<vla_linear_i8> from_f32(const float* W, const float* bias, int N, int K);
-    // From int8 rows Wq [N,K] (host, row-major, no padding) + wscale [N].
-    static std::unique_ptr<vla_linear_i8> from_i8(const int8_t* Wq, const float* wscale,
+    // From int8 rows Wq [N, ldq] (host, ldq >= K, bytes past K ignored) + wscale [N].
+    static std::unique_ptr<vla_linear_i8> from_i8(const int8_t* Wq, int ldq, const float* wscale,
                                                   const float* bias, int N, int K);
     ~vla_linear_i8();
     vla_linear_i8(const vla_linear_i8&) = delete;
@@ -29,6 +29,12 @@ struct vla_linear_i8 {
     const int8_t* Wq() const { return Wq_; }
     const float* wscale() const { return wscale_; }
     const float* bias() const { return bias_; }
+
+    // The resident rows and scales copied to the host: Wq [N, ldq] (ldq >=
+    // i8_kpad(K); bytes [K, ldq) zero), wscale [N].
+    void download(int8_t* Wq, int ldq, float* wscale) const;
+    // Replace the bias with host [N] values, or drop it (null).
+    void set_bias(const float* bias);
 
     // out [seq, ldo] = x [seq, K] W^T + bias, quantizing x into xq [seq, ldw] /
     // ascale [seq] first (Linear::forward's int8 branch, linear.cpp:121-133).

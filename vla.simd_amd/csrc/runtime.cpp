@@ -1,6 +1,8 @@
 // runtime.cpp - error plumbing, library stream, staging arena, device check.
 #include "runtime.h"
 
+#include <atomic>
+
 #include <cstdio>
 
 namespace vla {
@@ -61,6 +63,19 @@ void* Staging::take(size_t bytes) {
     void* p = base_ + used_;
     used_ += b;
     return p;
+}
+
+namespace {
+std::atomic<uint64_t> g_h2d_all{0}, g_h2d_weights{0};
+}
+
+void count_h2d(size_t bytes, bool weights) {
+    g_h2d_all.fetch_add(bytes, std::memory_order_relaxed);
+    if (weights) g_h2d_weights.fetch_add(bytes, std::memory_order_relaxed);
+}
+
+uint64_t h2d_bytes(bool weights_only) {
+    return (weights_only ? g_h2d_weights : g_h2d_all).load(std::memory_order_relaxed);
 }
 
 Staging& staging() {

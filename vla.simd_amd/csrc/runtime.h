@@ -40,16 +40,27 @@ int32_t guarded(const char* where, F&& f) {
 
 // Grow-only device staging for the host-pointer forms. take() hands out
 // 256-byte aligned slices of one allocation; reset() at the start of a call.
+// Host-to-device bytes the library has issued: all of them, and the part
+// that carried weights (int8 rows, weight scales, biases, fp32 weights). The
+// host-pointer op forms upload a layer's weights on every call; resident
+// layers (vla_linear_i8_*) upload them once.
+void count_h2d(size_t bytes, bool weights);
+uint64_t h2d_bytes(bool weights_only);
+
 class Staging {
 public:
     std::unique_lock<std::mutex> lock() { return std::unique_lock<std::mutex>(mu_); }
     void reset(size_t total_bytes);
     void* take(size_t bytes);
+    // weights: count the bytes as weight bytes too
     template <class T>
-    T* upload(const T* host, size_t count, hipStream_t st) {
+    T* upload(const T* host, size_t count, hipStream_t st, bool weights = false) {
         if (!host) return nullptr;
         T* d = static_cast<T*>(take(count * sizeof(T)));
-        if (count) VLA_HIP_CHECK(hipMemcpyAsync(d, host, count * sizeof(T), hipMemcpyHostToDevice, st));
+        if (count) {
+            VLA_HIP_CHECK(hipMemcpyAsync(d, host, count * sizeof(T), hipMemcpyHostToDevice, st));
+            count_h2d(count * sizeof(T), weights);
+        }
         return d;
     }
     template <class T>

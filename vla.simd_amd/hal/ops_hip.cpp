@@ -13,7 +13,9 @@
 //
 // Contract kept from the reference's op layer:
 //   - pointers are caller-owned host memory and every call is synchronous (the
-//     library's host-pointer forms upload, run and download);
+//     library's host-pointer forms upload, run and download); the int8 weights
+//     of a packed layer stay resident on the device (below), so a layer's
+//     forward moves only its activations and outputs;
 //   - weights are packed once by pack_weights_i8 into a buffer of
 //     packed_i8_words(N, K) int32 words: here the device row layout [N, Kp]
 //     int8 (the i8 MFMA is signed x signed) followed by the int32 row-sum
@@ -36,8 +38,12 @@
 
 #include <cmath>
 #include <cstdint>
+#include <cstdlib>
+#include <cstring>
+#include <mutex>
 #include <stdexcept>
 #include <string>
+#include <unordered_map>
 #include <vector>
 
 namespace tcpu {
@@ -66,6 +72,88 @@ const float* key_rows(std::vector<float>& tmp, const float* K, const float* K_pr
     return tmp.data();
 }
 
+// ------------------------------------------------------ weight residency --
+//
+// nn::Linear and nn::Conv pack their int8 weights once, into a buffer each
+// owns for its lifetime (pack_weights_i8 at linear.cpp:97-99 and
+// conv.cpp:46), and pass the same Wq / wscale pointers on every forward
+// (linear.cpp:121-133, 170-172; conv.cpp:59). The packing call here quantizes
+// on the device and keeps that copy resident, keyed by the Wq address:
+//   - a later pack into the same address replaces the entry (a layer
+//     initialised again, or a freed buffer reused by a new layer);
+//   - every forward first compares the buffer's row-sum table (written only
+//     by pack_weights_i8, after the rows) and its wscale with the packed
+//     values (8 N bytes); any difference, an unknown address or a different
+//     N / K takes the upload-per-call path, which is always correct;
+//   - the bias comes with each call: the entry keeps the address and values
+//     of the one it holds and uploads a new one only when they differ;
+//   - at most VLA_HIP_RESIDENT_MB (default 65536) MiB of int8 rows are made
+//     resident; packs beyond it stay upload-per-call.
+// Entries live until the process ends or their address is packed again (the
+// op layer is not told when a layer is destroyed).
+struct Resident {
+    vla_linear_i8* lin = nullptr;
+    int N = 0, K = 0;
+    std::vector<int32_t> rowsums;
+    std::vector<float> wscale;
+    bool has_bias = false;
+    const float* bias_ptr = nullptr;
+    std::vector<float> bias;
+};
+
+struct ResidentTable {
+    std::mutex mu;
+    std::unordered_map<const int8_t*, Resident> map;
+    size_t bytes = 0;
+};
+
+// never destroyed: its device memory goes with the process (freeing it from a
+// static destructor could run after the HIP runtime has shut down)
+ResidentTable& resident_table() {
+    static ResidentTable* t = new ResidentTable();
+    return *t;
+}
+
+size_t resident_limit() {
+    const char* e = std::getenv("VLA_HIP_RESIDENT_MB");
+    const long long mb = e && *e ? std::atoll(e) : 65536;
+    return mb > 0 ? (size_t)mb << 20 : 0;
+}
+
+void drop_resident(ResidentTable& t, const int8_t* Wq) {
+    auto it = t.map.find(Wq);
+    if (it == t.map.end()) return;
+    t.bytes -= (size_t)it->second.N * (size_t)vla_i8_kpad(it->second.K);
+    vla_linear_i8_free(it->second.lin);
+    t.map.erase(it);
+}
+
+// The resident layer of a packed buffer, with the call's bias in place, or
+// null (not packed here, changed since, or another shape). Called with the
+// table locked.
+vla_linear_i8* find_resident(ResidentTable& t, const int8_t* Wq, const float* wscale, const float* bias, int N,
+                             int K) {
+    auto it = t.map.find(Wq);
+    if (it == t.map.end()) return nullptr;
+    Resident& r = it->second;
+    const size_t Kp = (size_t)vla_i8_kpad(K);
+    if (r.N != N || r.K != K || !wscale) return nullptr;
+    if (std::memcmp(Wq + (size_t)N * Kp, r.rowsums.data(), (size_t)N * 4) != 0 ||
+        std::memcmp(wscale, r.wscale.data(), (size_t)N * 4) != 0)
+        return nullptr;
+    const bool same_bias = bias ? (r.has_bias && r.bias_ptr == bias &&
+                                   std::memcmp(bias, r.bias.data(), (size_t)N * 4) == 0)
+                                : !r.has_bias;
+    if (!same_bias) {
+        ok(vla_linear_i8_set_bias(r.lin, bias), "pack_weights_i8 (bias)");
+        r.has_bias = bias != nullptr;
+        r.bias_ptr = bias;
+        if (bias) r.bias.assign(bias, bias + N);
+        else r.bias.clear();
+    }
+    return r.lin;
+}
+
 }  // namespace
 
 // ---------------------------------------------------------- quant_ops.h --
@@ -78,15 +166,39 @@ int i8_kpad(int K) { return vla_i8_kpad(K); }  // quant_ops.h:45
 size_t packed_i8_words(int N, int K) { return (size_t)N * (size_t)i8_kpad(K) / 4 + (size_t)N; }
 
 // quant_ops.h:56: the per-row absmax quantizer (on the device), rows [N, Kp]
-// zero-padded, then the exact row sums the reference stores after its panels
+// zero-padded, then the exact row sums the reference stores after its panels.
+// The quantized rows stay resident on the device for this buffer's forwards.
 void pack_weights_i8(const float* W, int8_t* Wq, float* wscale, int N, int K) {
-    ok(vla_pack_weights_i8(W, Wq, wscale, N, K), "pack_weights_i8");
     const int Kp = i8_kpad(K);
-    int32_t* sums = reinterpret_cast<int32_t*>(Wq + (size_t)N * Kp);
+    ResidentTable& t = resident_table();
+    std::lock_guard<std::mutex> lk(t.mu);
+    drop_resident(t, Wq);
+    const size_t rows = (size_t)N * Kp;
+    vla_linear_i8* lin = nullptr;
+    if (t.bytes + rows <= resident_limit()) {
+        lin = vla_linear_i8_create(W, nullptr, N, K);
+        if (!lin) ok(VLA_ERR_EXCEPTION, "pack_weights_i8");
+        const int32_t st = vla_linear_i8_download(lin, Wq, Kp, wscale);
+        if (st != VLA_OK) vla_linear_i8_free(lin);
+        ok(st, "pack_weights_i8");
+    } else {
+        ok(vla_pack_weights_i8(W, Wq, wscale, N, K), "pack_weights_i8");
+    }
+    int32_t* sums = reinterpret_cast<int32_t*>(Wq + rows);
     for (int n = 0; n < N; n++) {
         int32_t s = 0;
         for (int k = 0; k < K; k++) s += Wq[(size_t)n * Kp + k];
         sums[n] = s;
+    }
+    if (lin) {
+        Resident r;
+        r.lin = lin;
+        r.N = N;
+        r.K = K;
+        r.rowsums.assign(sums, sums + N);
+        r.wscale.assign(wscale, wscale + N);
+        t.map.emplace(Wq, std::move(r));
+        t.bytes += rows;
     }
 }
 
@@ -108,12 +220,26 @@ void quantize_span_i8(const float* x, int8_t* q, size_t n, float inv) {
 // quant_ops.h:83
 void dense_linear_i8_pre(float* out, const int8_t* xq, const float* ascale, const int8_t* Wq,
                          const float* wscale, const float* bias, int seq, int N, int K) {
+    ResidentTable& t = resident_table();
+    std::lock_guard<std::mutex> lk(t.mu);
+    if (vla_linear_i8* lin = find_resident(t, Wq, wscale, bias, N, K)) {
+        ok(vla_linear_i8_forward_quantized(lin, out, xq, i8_kpad(K), ascale, seq), "dense_linear_i8_pre");
+        return;
+    }
     ok(vla_dense_linear_i8_pre(out, xq, ascale, Wq, wscale, bias, seq, N, K), "dense_linear_i8_pre");
 }
 
 // quant_ops.h:69-72: the quantized rows land in the caller's scratch first
 void dense_linear_i8(float* out, const float* x, const int8_t* Wq, const float* wscale, const float* bias,
                      int seq, int N, int K, int8_t* xq_scratch, float* ascale_scratch) {
+    {
+        ResidentTable& t = resident_table();
+        std::lock_guard<std::mutex> lk(t.mu);
+        if (vla_linear_i8* lin = find_resident(t, Wq, wscale, bias, N, K)) {
+            ok(vla_linear_i8_forward(lin, out, x, seq, xq_scratch, i8_kpad(K), ascale_scratch), "dense_linear_i8");
+            return;
+        }
+    }
     quantize_act_i8(x, xq_scratch, ascale_scratch, seq, K);
     dense_linear_i8_pre(out, xq_scratch, ascale_scratch, Wq, wscale, bias, seq, N, K);
 }
@@ -178,6 +304,14 @@ void relu(float* x, int n) { ok(vla_relu(x, n), "relu"); }                 // lm
 // the device keeps its own im2col workspace, so xq_scratch is not touched
 void conv2d_i8(float* out, const float* x, const int8_t* Wq, const float* wscale, const float* bias, int H,
                int Wd, int Cin, int Cout, int k, int stride, int pad, std::vector<int8_t>&) {
+    {
+        ResidentTable& t = resident_table();
+        std::lock_guard<std::mutex> lk(t.mu);
+        if (vla_linear_i8* lin = find_resident(t, Wq, wscale, bias, Cout, k * k * Cin)) {
+            ok(vla_conv2d_i8_resident(lin, out, x, H, Wd, Cin, k, stride, pad), "conv2d_i8");
+            return;
+        }
+    }
     ok(vla_conv2d_i8(out, x, Wq, wscale, bias, H, Wd, Cin, Cout, k, stride, pad), "conv2d_i8");
 }
 
