@@ -12,6 +12,9 @@ weights and outputs (>= 512 MiB per shape) so every launch streams from HBM
 rather than from L2/MALL. For M <= 128 the quantize writes the library's
 panel layout (vla_quantize_act_i8_panel_dev) and the GEMM reads it
 (vla_dense_linear_i8_panel_dev): the same values, byte-identical output.
+Each sweep row also carries the warm time (gemm_warm_us: the same launches
+on one weight and output copy, operands resident in L2 / MALL) beside the
+cold, rotating one (gemm_us), which is what frac and value use.
 
 value = int8 TOPS of the whole step (sum of 2*M*N*K over the shapes / step
 time). roofline = the dominant kernel (the M=8192, K=N=4096 GEMM) measured
@@ -140,6 +143,12 @@ class Shape:
             vla.dense_linear_i8_pre_dev(self.out[r], self.xq, self.sa, self.W[r], self.ws, self.b, self.K,
                                         stream=stream)
 
+    def gemm_warm(self, vla, stream):
+        # the same weights and output every launch: operands warm in L2/MALL
+        r, self.i = self.i, 0
+        self.gemm(vla, stream)
+        self.i = r
+
     def op(self, vla, stream):
         self.quantize(vla, stream)
         self.gemm(vla, stream)
@@ -202,6 +211,33 @@ def host_cpu_model() -> str:
     return "unknown"
 
 
+def host_cores() -> dict:
+    """The host's CPUs: logical CPUs, physical cores (distinct (package,
+    core id) pairs of /proc/cpuinfo) and the CPUs this process may run on (the
+    lease's share on a shared box)."""
+    phys = set()
+    pkg = core = None
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("physical id"):
+                pkg = line.split(":", 1)[1].strip()
+            elif line.startswith("core id"):
+                core = line.split(":", 1)[1].strip()
+            elif not line.strip():
+                if core is not None:
+                    phys.add((pkg, core))
+                pkg = core = None
+        if core is not None:
+            phys.add((pkg, core))
+    except OSError:
+        pass
+    try:
+        allowed = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        allowed = None
+    return {"logical_cpus": os.cpu_count(), "physical_cores": len(phys) or None, "allowed_cpus": allowed}
+
+
 def _median_ms(fn, warmup=CPU_WARMUP, timed=CPU_TIMED):
     """Median wall time in ms of `timed` calls of fn() after `warmup` calls."""
     for _ in range(warmup):
@@ -237,10 +273,18 @@ def cpu_baseline(synth):
         tot_ms += ms
         per[f"{M}x{K}x{N}"] = round(ms, 4)
     vnni = bool(L.ref_int8_available())
+    hc = host_cores()
+    threads = int(L.ref_omp_max_threads())
     return {
         "value": round(tot_ops / (tot_ms * 1e-3) / 1e12, 4),
         "unit": "TOPS (int8, 2*M*N*K per dense_linear_i8 call)",
-        "cores": int(L.ref_omp_max_threads()),
+        "cores": threads,
+        "host_cores": hc,
+        "cores_note": (f"{threads} OpenMP threads: the host's {hc['physical_cores']} physical cores"
+                       if threads == hc["physical_cores"] else
+                       f"{threads} OpenMP threads = the CPUs this process may use ({hc['allowed_cpus']} allowed of "
+                       f"{hc['logical_cpus']} logical, {hc['physical_cores']} physical cores; a shared box's lease "
+                       f"limit, OMP_NUM_THREADS as the box sets it)"),
         "kind": "reference",
         "sample": f"reference dense_linear_i8 ({'AVX-VNNI' if vnni else 'scalar ref, no AVX-VNNI'}), "
                   f"{len(sample)} configs[1] shapes M<=512",
@@ -653,7 +697,10 @@ def main():
         g_us = time_graph(torch, g_gemm, 3, stream_obj) / n
         g_op = capture(torch, lambda st: sh.op(vla, st), n)
         op_us = time_graph(torch, g_op, 3, stream_obj) / n
-        del g_gemm, g_op
+        # warm: the same n launches on one weight / output copy (L2 / MALL resident)
+        g_warm = capture(torch, lambda st: sh.gemm_warm(vla, st), n)
+        w_us = time_graph(torch, g_warm, 3, stream_obj) / n
+        del g_gemm, g_op, g_warm
         ops = 2.0 * sh.M * sh.N * sh.K
         t_roof, bound = roof_us(sh.M, sh.K, sh.N)
         rows.append({
@@ -661,13 +708,14 @@ def main():
             "gemm_tops": round(ops / g_us / 1e6, 2),
             "gemm_gbs": round(gemm_bytes(sh.M, sh.K, sh.N) / g_us / 1e3, 1),
             "bound": bound, "roof_us": round(t_roof, 3), "frac": round(t_roof / g_us, 4),
+            "gemm_warm_us": round(w_us, 3), "frac_warm": round(t_roof / w_us, 4),
             "rotating_copies": sh.R, "a_layout": "panel" if sh.panel else "row-major",
             "split_k": sh.split is not None,
         })
         if (sh.M, sh.K, sh.N) == dominant:
             dom_us = g_us
         print(f"  {sh.M}x{sh.K}x{sh.N}: gemm {g_us:.2f} us ({rows[-1]['gemm_tops']} TOPS, "
-              f"{rows[-1]['gemm_gbs']} GB/s, {bound} frac {rows[-1]['frac']}), op {op_us:.2f} us",
+              f"{rows[-1]['gemm_gbs']} GB/s, {bound} frac {rows[-1]['frac']}), warm {w_us:.2f} us, op {op_us:.2f} us",
               file=sys.stderr, flush=True)
 
     # the step: every shape once (quantize + GEMM), captured as one graph
