@@ -171,21 +171,24 @@ def test_fp32_backbone_and_actions(vla, small_dir, env, mask):
         assert m.predict(images, state, unnormalize=False).tobytes() == got.tobytes()
 
 
-@pytest.mark.parametrize("to", [-1, 3])
-def test_int8_backbone(vla, small_dir, env, to):
-    """ACT_INT8 bit 32: every conv (to = -1) is conv2d_i8 and the features are
+@pytest.mark.parametrize("frm,to", [(0, -1), (0, 3), (2, -1)])
+def test_int8_backbone(vla, small_dir, env, frm, to):
+    """ACT_INT8 bit 32: every conv (0, -1) is conv2d_i8 and the features are
     the reference's bit for bit; with ACT_I8_CONV_TO=3 the stem and the first
-    two blocks are int8 (exact) and the rest fp32 (summation order)."""
+    two blocks are int8 (exact) and the rest fp32 (summation order); with
+    ACT_I8_CONV_FROM=2 the stem and the first block are fp32 and the int8
+    convs after them take the block maxima their producers (max pool, residual
+    add, relu) wrote, as the all-int8 trunk does."""
     ck = _ck()
     from helpers import oracle
     ob = oracle()
-    env(ACT_INT8=32 | 31, ACT_I8_CONV_FROM=0, ACT_I8_CONV_TO=to)
+    env(ACT_INT8=32 | 31, ACT_I8_CONV_FROM=frm, ACT_I8_CONV_TO=to)
     images, state = ck.act_model_inputs(_small(ck))
     r = ob.RefActModel(small_dir)
     m = vla.ActModel(small_dir)
-    assert m.int8_convs == (20 if to < 0 else 1 + 2 * 2)
+    assert m.int8_convs == {(0, -1): 20, (0, 3): 1 + 2 * 2, (2, -1): 17}[(frm, to)]
     got, ref = m.encode(images), r.encode(images)
-    if to < 0:
+    if (frm, to) == (0, -1):
         assert got.tobytes() == ref.tobytes(), f"int8 backbone differs (rel {_rel(got, ref):.3e})"
     else:
         assert _rel(got, ref) <= 1e-4

@@ -8,6 +8,7 @@
 // [H, W, C], conv weights [Cout][k][k][Cin], so an im2col row is the taps
 // [ky][kx][ci] of one output pixel (src/hal/common/conv.cpp:117-176).
 #include "common.h"
+#include "wave.h"
 
 #include <cmath>
 
@@ -17,21 +18,45 @@ namespace vla {
 namespace hip {
 namespace {
 
+// A producer's share of conv2d_i8's per-tensor scale: the block's max |v|
+// over the values it wrote, stored at part[blockIdx.x] when part is given
+// (uniform over the grid; every thread of the block reaches this point). The consuming conv2d_i8 folds these maxima
+// instead of reading its input once more (max is order-free: the same scale).
+__device__ __forceinline__ void store_block_absmax(float m, float* __restrict__ part) {
+    if (!part) return;
+    __shared__ float red[4];
+    m = wave_max_f32(m);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float v = 0.0f;
+        for (int w = 0; w < (int)(blockDim.x >> 6); w++) v = fmaxf(v, red[w]);
+        part[blockIdx.x] = v;
+    }
+}
+
 // act_model.cpp:109-123: (pixel / 255 - mean[c]) / (std[c] + eps), the
 // lerobot NormalizerProcessorStep order, one camera's [npx, 3] block per
 // blockIdx.y (stats [n_cams][3]).
 __global__ __launch_bounds__(256) void normalize_u8_kernel(float* __restrict__ out, const uint8_t* __restrict__ img,
                                                            int64_t npx3, const float* __restrict__ mean,
-                                                           const float* __restrict__ stdv, float eps) {
+                                                           const float* __restrict__ stdv, float eps,
+                                                           float* __restrict__ part) {
     const int cam = blockIdx.y;
     const uint8_t* src = img + (int64_t)cam * npx3;
     float* dst = out + (int64_t)cam * npx3;
     const float* m = mean + cam * 3;
     const float* s = stdv + cam * 3;
+    float mx = 0.0f;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < npx3; i += (int64_t)gridDim.x * blockDim.x) {
         const int c = (int)(i % 3);
-        dst[i] = ((float)src[i] / 255.0f - m[c]) / (s[c] + eps);
+        const float v = ((float)src[i] / 255.0f - m[c]) / (s[c] + eps);
+        dst[i] = v;
+        mx = fmaxf(mx, fabsf(v));
     }
+    // camera c's maxima at part[c * kConvPartMax ...]
+    store_block_absmax(mx, part ? part + (size_t)cam * kConvPartMax : nullptr);
 }
 
 // im2col of an NHWC map for a k x k conv: row p = output pixel (oy, ox),
@@ -75,8 +100,9 @@ __global__ __launch_bounds__(256) void im2col_f32x4_kernel(float* __restrict__ c
 // then the folded ReLU (!(v > 0) -> 0).
 __global__ __launch_bounds__(256) void maxpool_relu_kernel(float* __restrict__ out, const float* __restrict__ x, int H,
                                                            int Wd, int C, int k, int stride, int pad, int Hout,
-                                                           int Wout) {
+                                                           int Wout, float* __restrict__ part) {
     const int64_t total = (int64_t)Hout * Wout * C;
+    float mx = 0.0f;
     for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < total; e += (int64_t)gridDim.x * blockDim.x) {
         const int c = (int)(e % C);
         const int64_t p = e / C;
@@ -92,23 +118,36 @@ __global__ __launch_bounds__(256) void maxpool_relu_kernel(float* __restrict__ o
                 o = v > o ? v : o;
             }
         }
-        out[e] = o > 0.0f ? o : 0.0f;
+        const float r = o > 0.0f ? o : 0.0f;
+        out[e] = r;
+        mx = fmaxf(mx, r);
     }
+    store_block_absmax(mx, part);
 }
 
 // the basic block's tail (resnet_backbone.cpp:296-303): o = max(o + identity, 0)
 // as v > 0 ? v : 0
-__global__ __launch_bounds__(256) void add_relu_kernel(float* __restrict__ o, const float* __restrict__ idn, int64_t n) {
+__global__ __launch_bounds__(256) void add_relu_kernel(float* __restrict__ o, const float* __restrict__ idn, int64_t n,
+                                                      float* __restrict__ part) {
+    float mx = 0.0f;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
         const float v = o[i] + idn[i];
-        o[i] = v > 0.0f ? v : 0.0f;
+        const float r = v > 0.0f ? v : 0.0f;
+        o[i] = r;
+        mx = fmaxf(mx, r);
     }
+    store_block_absmax(mx, part);
 }
 
 // relu in place as the reference's relu (eltwise.cpp:209-215): x < 0 -> 0
-__global__ __launch_bounds__(256) void relu_kernel(float* __restrict__ x, int64_t n) {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
-        if (x[i] < 0.0f) x[i] = 0.0f;
+__global__ __launch_bounds__(256) void relu_kernel(float* __restrict__ x, int64_t n, float* __restrict__ part) {
+    float mx = 0.0f;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        float v = x[i];
+        if (v < 0.0f) x[i] = v = 0.0f;
+        mx = fmaxf(mx, fabsf(v));
+    }
+    store_block_absmax(mx, part);
 }
 
 // per-column affine of [rows, cols]: mode 0 (x - a[c]) / (b[c] + eps) (the
@@ -132,12 +171,19 @@ int grid_for(int64_t n) {
 
 }  // namespace
 
-void launch_normalize_u8(float* out, const uint8_t* img, int n_cams, int64_t npx, const float* mean,
-                         const float* stdv, float eps, hipStream_t st) {
+// grid of a producer that writes block maxima: at most kConvPartMax blocks
+static int part_grid(int64_t n, const float* part) {
+    const int g = grid_for(n);
+    return part && g > kConvPartMax ? kConvPartMax : g;
+}
+
+int launch_normalize_u8(float* out, const uint8_t* img, int n_cams, int64_t npx, const float* mean,
+                        const float* stdv, float eps, hipStream_t st, float* part) {
     VLA_REQUIRE(n_cams > 0 && npx > 0 && out && img && mean && stdv, "normalize: bad arguments");
-    const dim3 grid(grid_for(npx * 3) < 1024 ? grid_for(npx * 3) : 1024, n_cams);
-    normalize_u8_kernel<<<grid, 256, 0, st>>>(out, img, npx * 3, mean, stdv, eps);
+    const int gx = grid_for(npx * 3) < (part ? kConvPartMax : 1024) ? grid_for(npx * 3) : (part ? kConvPartMax : 1024);
+    normalize_u8_kernel<<<dim3(gx, n_cams), 256, 0, st>>>(out, img, npx * 3, mean, stdv, eps, part);
     VLA_LAUNCH_CHECK();
+    return gx;
 }
 
 void launch_im2col_f32(float* col, int ldc, const float* x, int H, int Wd, int Cin, int k, int stride, int pad,
@@ -156,22 +202,27 @@ void launch_im2col_f32(float* col, int ldc, const float* x, int H, int Wd, int C
     VLA_LAUNCH_CHECK();
 }
 
-void launch_maxpool_relu(float* out, const float* x, int H, int Wd, int C, int k, int stride, int pad, int Hout,
-                         int Wout, hipStream_t st) {
+int launch_maxpool_relu(float* out, const float* x, int H, int Wd, int C, int k, int stride, int pad, int Hout,
+                        int Wout, hipStream_t st, float* part) {
     VLA_REQUIRE(out && x && Hout > 0 && Wout > 0 && C > 0, "maxpool: bad arguments");
-    maxpool_relu_kernel<<<grid_for((int64_t)Hout * Wout * C), 256, 0, st>>>(out, x, H, Wd, C, k, stride, pad, Hout,
-                                                                           Wout);
+    const int g = part_grid((int64_t)Hout * Wout * C, part);
+    maxpool_relu_kernel<<<g, 256, 0, st>>>(out, x, H, Wd, C, k, stride, pad, Hout, Wout, part);
     VLA_LAUNCH_CHECK();
+    return g;
 }
 
-void launch_add_relu(float* o, const float* idn, int64_t n, hipStream_t st) {
-    add_relu_kernel<<<grid_for(n), 256, 0, st>>>(o, idn, n);
+int launch_add_relu(float* o, const float* idn, int64_t n, hipStream_t st, float* part) {
+    const int g = part_grid(n, part);
+    add_relu_kernel<<<g, 256, 0, st>>>(o, idn, n, part);
     VLA_LAUNCH_CHECK();
+    return g;
 }
 
-void launch_relu_inplace(float* x, int64_t n, hipStream_t st) {
-    relu_kernel<<<grid_for(n), 256, 0, st>>>(x, n);
+int launch_relu_inplace(float* x, int64_t n, hipStream_t st, float* part) {
+    const int g = part_grid(n, part);
+    relu_kernel<<<g, 256, 0, st>>>(x, n, part);
     VLA_LAUNCH_CHECK();
+    return g;
 }
 
 void launch_col_affine(float* out, const float* x, int rows, int cols, const float* a, const float* b, float eps,

@@ -202,23 +202,31 @@ struct ConvArgs {
     float clip;
     void* work;
     size_t work_bytes;
+    // optional: the block maxima of |x| its producer wrote (in_nparts <= 4096
+    // floats, their max = max |x|); then no absmax pass over x runs
+    const float* in_part = nullptr;
+    int in_nparts = 0;
 };
 void launch_conv2d_i8(const ConvArgs& a, hipStream_t st);
+// Producers of a conv2d_i8 input that also write its block maxima (part:
+// at most kConvPartMax floats per launch, per camera for the normalization;
+// the launchers return how many) so the conv skips its absmax pass.
+constexpr int kConvPartMax = 512;
 
 // backbone.hip: ACT's image backbone around its GEMMs (NHWC fp32 maps)
 // (pixel / 255 - mean[cam][c]) / (std[cam][c] + eps) for n_cams frames of npx pixels
-void launch_normalize_u8(float* out, const uint8_t* img, int n_cams, int64_t npx, const float* mean,
-                         const float* stdv, float eps, hipStream_t st);
+int launch_normalize_u8(float* out, const uint8_t* img, int n_cams, int64_t npx, const float* mean,
+                        const float* stdv, float eps, hipStream_t st, float* part = nullptr);
 // col [Hout * Wout, ldc]: the k x k taps [ky][kx][ci] of every output pixel, zero outside
 void launch_im2col_f32(float* col, int ldc, const float* x, int H, int Wd, int Cin, int k, int stride, int pad,
                        int Hout, int Wout, hipStream_t st);
 // max pool with -inf padding, then the folded relu (!(v > 0) -> 0)
-void launch_maxpool_relu(float* out, const float* x, int H, int Wd, int C, int k, int stride, int pad, int Hout,
-                         int Wout, hipStream_t st);
+int launch_maxpool_relu(float* out, const float* x, int H, int Wd, int C, int k, int stride, int pad, int Hout,
+                        int Wout, hipStream_t st, float* part = nullptr);
 // o = o + idn > 0 ? o + idn : 0
-void launch_add_relu(float* o, const float* idn, int64_t n, hipStream_t st);
+int launch_add_relu(float* o, const float* idn, int64_t n, hipStream_t st, float* part = nullptr);
 // x < 0 -> 0
-void launch_relu_inplace(float* x, int64_t n, hipStream_t st);
+int launch_relu_inplace(float* x, int64_t n, hipStream_t st, float* part = nullptr);
 // [rows, cols] per column: mode 0 (x - a) / (b + eps), mode 1 fma(x, b, a)
 void launch_col_affine(float* out, const float* x, int rows, int cols, const float* a, const float* b, float eps,
                        int mode, hipStream_t st);

@@ -12,7 +12,8 @@
 // with channel co's weights: dense_linear_i8_pre over the im2col rows with
 // every row scale s.
 //
-// Three launches on the caller's stream:
+// Three launches on the caller's stream (two when the producer of x passes
+// the block maxima of |x| it wrote, ConvArgs::in_part):
 //   conv_absmax_kernel  per-block max |x| (float4 loads, wave + LDS reduce);
 //   conv_im2col_kernel  every block first folds the block maxima into the
 //                       scale (a few hundred floats; the same value in every
@@ -224,13 +225,22 @@ void launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
     float* ascale = reinterpret_cast<float*>(w + (size_t)kAbsmaxBlocks * 4);
     int8_t* A = reinterpret_cast<int8_t*>(w + (size_t)kAbsmaxBlocks * 4 + ((size_t)c.npix * 4 + 255) / 256 * 256);
 
-    const int64_t n = (int64_t)a.H * a.Wd * a.Cin;
-    int blocks = (int)((n + 4 * 256 * 4 - 1) / (4 * 256 * 4));
-    blocks = blocks < 1 ? 1 : (blocks > kAbsmaxBlocks ? kAbsmaxBlocks : blocks);
-    conv_absmax_kernel<<<blocks, 256, 0, st>>>(a.x, n, part);
-    VLA_LAUNCH_CHECK();
+    int blocks;
+    const float* maxima = part;
+    if (a.in_part) {
+        // the producer of x wrote its block maxima: no pass over x here
+        VLA_REQUIRE(a.in_nparts > 0 && a.in_nparts <= 4096, "conv2d_i8: 1..4096 producer block maxima");
+        maxima = a.in_part;
+        blocks = a.in_nparts;
+    } else {
+        const int64_t n = (int64_t)a.H * a.Wd * a.Cin;
+        blocks = (int)((n + 4 * 256 * 4 - 1) / (4 * 256 * 4));
+        blocks = blocks < 1 ? 1 : (blocks > kAbsmaxBlocks ? kAbsmaxBlocks : blocks);
+        conv_absmax_kernel<<<blocks, 256, 0, st>>>(a.x, n, part);
+        VLA_LAUNCH_CHECK();
+    }
 
-    Im2colArgs g{a.x, a.H, a.Wd, a.Cin, a.k, a.stride, a.pad, c.Wout, c.npix, c.K, c.lda, part, blocks,
+    Im2colArgs g{a.x, a.H, a.Wd, a.Cin, a.k, a.stride, a.pad, c.Wout, c.npix, c.K, c.lda, maxima, blocks,
                  a.clip > 0.0f ? a.clip : clip_from_env(), A, ascale};
     // enough waves for every (group, chunk), at most kIm2colMaxBlocks blocks,
     // a multiple of 8 blocks, and at least one row of nchunk waves per XCD

@@ -261,6 +261,10 @@ ActModel::ActModel(const std::string& dir) {
     const size_t npx = (size_t)img_h_ * img_w_;
     img_in_ = A_.alloc<uint8_t>((size_t)n_cams_ * npx * 3);
     norm_ = A_.alloc<float>((size_t)n_cams_ * npx * 3);
+    part_norm_ = A_.alloc<float>((size_t)n_cams_ * kConvPartMax);
+    part_a_ = A_.alloc<float>(kConvPartMax);
+    part_b_ = A_.alloc<float>(kConvPartMax);
+    part_c_ = A_.alloc<float>(kConvPartMax);
     a_ = A_.alloc<float>(map_max);
     b_ = A_.alloc<float>(map_max);
     c_ = A_.alloc<float>(map_max);
@@ -298,7 +302,8 @@ ActModel::~ActModel() {
     if (own_) (void)hipStreamDestroy(own_);
 }
 
-void ActModel::conv(const Conv& c, const float* x, int H, int W, float* out, bool relu, hipStream_t st) {
+int ActModel::conv(const Conv& c, const float* x, int H, int W, float* out, bool relu, hipStream_t st,
+                   const float* in_part, int in_nparts, float* out_part) {
     const int Ho = conv_out(H, c.k, c.stride, c.pad), Wo = conv_out(W, c.k, c.stride, c.pad);
     if (c.q8) {
         ConvArgs a{};
@@ -318,9 +323,12 @@ void ActModel::conv(const Conv& c, const float* x, int H, int W, float* out, boo
         a.clip = 0.0f;  // TCPU_I8_CLIP from the environment, as conv2d_i8 reads it
         a.work = work_;
         a.work_bytes = work_bytes_;
+        // an fp32 producer (or none) wrote no maxima: conv2d_i8 runs its absmax pass
+        a.in_part = in_nparts > 0 ? in_part : nullptr;
+        a.in_nparts = in_nparts > 0 ? in_nparts : 0;
         launch_conv2d_i8(a, st);
-        if (relu) launch_relu_inplace(out, (int64_t)Ho * Wo * c.cout, st);
-        return;
+        // the relu pass writes the block maxima the next conv2d_i8 reads
+        return relu ? launch_relu_inplace(out, (int64_t)Ho * Wo * c.cout, st, out_part) : 0;
     }
     const int K = c.k * c.k * c.cin;
     const float* rows = x;
@@ -332,7 +340,7 @@ void ActModel::conv(const Conv& c, const float* x, int H, int W, float* out, boo
     const size_t part_f = col_floats_ - rows_f;
     if (!plain && launch_conv_f32_implicit(out, x, H, W, c.cin, c.k, c.stride, c.pad, Ho, Wo, c.W, c.b, c.cout,
                                            relu ? 1 : 0, st, part, part_f))
-        return;
+        return 0;
     if (!plain) {
         ldx = (K + 3) & ~3;
         launch_im2col_f32(col_, ldx, x, H, W, c.cin, c.k, c.stride, c.pad, Ho, Wo, st);
@@ -340,35 +348,45 @@ void ActModel::conv(const Conv& c, const float* x, int H, int W, float* out, boo
     }
     launch_linear_f32(out, c.cout, rows, ldx, c.W, K, c.b, Ho * Wo, c.cout, K, relu ? 1 : 0, 0, 1.0f, st, part,
                       part_f);
+    return 0;
 }
 
 // ActModel::encode_view for every camera (act_model.cpp:106-124) and
 // ResNetBackbone::forward (resnet_backbone.cpp:211-317) without FiLM
+//
+// With int8 convolutions each conv2d_i8 input comes with the block maxima of
+// |x| that its producer wrote (the normalization, the max pool, the relu
+// after conv1, the block's residual add + relu), so no conv runs an absmax
+// pass of its own; the maxima buffers follow the trunk buffers they describe.
 void ActModel::run_backbone(hipStream_t st) {
     const int64_t npx = (int64_t)img_h_ * img_w_;
-    launch_normalize_u8(norm_, img_in_, n_cams_, npx, img_mean_, img_std_, norm_eps_, st);
+    const int nn = launch_normalize_u8(norm_, img_in_, n_cams_, npx, img_mean_, img_std_, norm_eps_, st,
+                                       stem_.q8 ? part_norm_ : nullptr);
     for (int cam = 0; cam < n_cams_; cam++) {
         const float* x = norm_ + (size_t)cam * npx * 3;
         int h = conv_out(img_h_, stem_.k, stem_.stride, stem_.pad), w = conv_out(img_w_, stem_.k, stem_.stride, stem_.pad);
-        conv(stem_, x, img_h_, img_w_, a_, false, st);
+        conv(stem_, x, img_h_, img_w_, a_, false, st, part_norm_ + (size_t)cam * kConvPartMax, nn);
         const int ph = conv_out(h, pool_k_, pool_stride_, pool_pad_), pw = conv_out(w, pool_k_, pool_stride_, pool_pad_);
-        launch_maxpool_relu(b_, a_, h, w, stem_.cout, pool_k_, pool_stride_, pool_pad_, ph, pw, st);
-        h = ph;
-        w = pw;
         float* B = b_;
         float* C = c_;
+        float* pB = part_b_;
+        float* pC = part_c_;
+        int nB = launch_maxpool_relu(B, a_, h, w, stem_.cout, pool_k_, pool_stride_, pool_pad_, ph, pw, st, pB);
+        h = ph;
+        w = pw;
         for (const Block& blk : blocks_) {
             const int oh = conv_out(h, blk.c1.k, blk.c1.stride, blk.c1.pad);
             const int ow = conv_out(w, blk.c1.k, blk.c1.stride, blk.c1.pad);
             const float* idn = B;
             if (blk.has_down) {
-                conv(blk.down, B, h, w, res_, false, st);
+                conv(blk.down, B, h, w, res_, false, st, pB, nB);
                 idn = res_;
             }
-            conv(blk.c1, B, h, w, a_, true, st);
-            conv(blk.c2, a_, oh, ow, C, false, st);
-            launch_add_relu(C, idn, (int64_t)oh * ow * blk.c1.cout, st);
+            const int nA = conv(blk.c1, B, h, w, a_, true, st, pB, nB, part_a_);
+            conv(blk.c2, a_, oh, ow, C, false, st, part_a_, nA);
+            nB = launch_add_relu(C, idn, (int64_t)oh * ow * blk.c1.cout, st, pC);
             std::swap(B, C);
+            std::swap(pB, pC);
             h = oh;
             w = ow;
         }

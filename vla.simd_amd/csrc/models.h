@@ -133,8 +133,11 @@ private:
         bool has_down = false;
     };
     // out [Hout * Wout, cout] = conv(x [H, W, cin]); relu applies the
-    // reference's relu afterwards
-    void conv(const Conv& c, const float* x, int H, int W, float* out, bool relu, hipStream_t st);
+    // reference's relu afterwards. int8 convs: in_part / in_nparts are the
+    // block maxima of |x| its producer wrote, out_part receives those of the
+    // relu'd output; returns their count (0 when none are written).
+    int conv(const Conv& c, const float* x, int H, int W, float* out, bool relu, hipStream_t st,
+             const float* in_part = nullptr, int in_nparts = 0, float* out_part = nullptr);
     void run_backbone(hipStream_t st);
 
     int img_h_ = 480, img_w_ = 640, n_cams_ = 2;
@@ -152,6 +155,10 @@ private:
     uint8_t* img_in_ = nullptr;  // the frames the captured graph reads
     float *norm_ = nullptr, *a_ = nullptr, *b_ = nullptr, *c_ = nullptr, *res_ = nullptr, *col_ = nullptr,
           *feats_ = nullptr, *state_n_ = nullptr, *act_n_ = nullptr;
+    // block maxima of |x| written by each conv2d_i8 input's producer:
+    // [n_cams][kConvPartMax] for the normalized frames, kConvPartMax for a_,
+    // b_ and c_ (the trunk buffers swap, and so do their maxima)
+    float *part_norm_ = nullptr, *part_a_ = nullptr, *part_b_ = nullptr, *part_c_ = nullptr;
     size_t col_floats_ = 0;  // im2col rows + split-K sums
     void* work_ = nullptr;
     size_t work_bytes_ = 0;
@@ -464,6 +471,10 @@ private:
     std::vector<Layer> layers_;
     DLinear embed_;
     float *a_ = nullptr, *b_ = nullptr, *col_ = nullptr, *gA_ = nullptr, *gB_ = nullptr;
+    // block maxima of |x| written by each conv2d_i8 input's producer:
+    // [n_cams][kConvPartMax] for the normalized frames, kConvPartMax for a_,
+    // b_ and c_ (the trunk buffers swap, and so do their maxima)
+    float *part_norm_ = nullptr, *part_a_ = nullptr, *part_b_ = nullptr, *part_c_ = nullptr;
     size_t col_floats_ = 0;  // im2col rows + split-K sums
     double* gW_ = nullptr;   // GroupNorm partial sums
     size_t gw_doubles_ = 0;
