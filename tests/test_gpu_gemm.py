@@ -562,3 +562,50 @@ def test_skinny_129_to_256_rows_bitexact(vla, orc, torch_cuda, groups, seq, N, K
     want = (base + orc.apply_act(orc.dense_linear_i8_pre(xq, sa, Wq, ws, b, K), 1)).astype(np.float32)
     for o in outs:
         assert same_bits(o.cpu().numpy(), want)
+
+
+@pytest.mark.parametrize("seq,N,K", [(100, 3200, 512), (7, 48, 1027), (302, 96, 17), (1, 16, 4096)])
+def test_resident_linear_host_forms(vla, orc, seq, N, K):
+    """The host-pointer forms over resident weights (what the reference's op
+    layer calls for a packed nn::Linear): the quantized rows and scales the
+    caller's scratch receives and the output equal the oracle's bit for bit;
+    the quantized-input form gives the same output; the downloaded rows and
+    scales are the packer's; a bias set, changed and dropped after creation
+    takes effect; and no call moves weight bytes once the layer exists."""
+    x, W, b = _case(orc, seq, N, K)
+    Wq, ws = orc.quantize_weights_i8(W)
+    lin = vla.LinearI8.from_f32(W)
+    Wd, wsd = lin.download()
+    assert same_bits(Wd, Wq) and same_bits(wsd, ws)
+    xqo, sao = orc.quantize_act_i8(x)
+    before = int(vla.lib().vla_h2d_bytes(1))
+    out, xq, sa = lin.forward(x)
+    assert int(vla.lib().vla_h2d_bytes(1)) == before, "a forward uploaded weight bytes"
+    assert same_bits(xq, xqo) and same_bits(sa, sao)
+    assert same_bits(out, orc.dense_linear_i8_pre(xqo, sao, Wq, ws, None, K))
+    assert same_bits(lin.forward_quantized(xqo, sao), out)
+    lin.set_bias(b)
+    assert same_bits(lin.forward(x)[0], orc.dense_linear_i8_pre(xqo, sao, Wq, ws, b, K))
+    b2 = (b * -3.0).astype(np.float32)
+    lin.set_bias(b2)
+    assert same_bits(lin.forward_quantized(xqo, sao), orc.dense_linear_i8_pre(xqo, sao, Wq, ws, b2, K))
+    lin.set_bias(None)
+    assert same_bits(lin.forward(x)[0], out)
+    lin.close()
+
+
+def test_resident_conv_host_form(vla, orc):
+    """vla_conv2d_i8_resident (nn::Conv2d's forward over resident weights)
+    equals vla_conv2d_i8 with the same weights uploaded per call, bit for bit,
+    at a 3x3 and a strided 1x1 layer."""
+    r = np.random.default_rng(4)
+    for (H, Wd, Cin, Cout, k, s, p) in [(20, 24, 32, 64, 3, 1, 1), (16, 16, 64, 32, 1, 2, 0)]:
+        x = r.normal(0, 1, (H, Wd, Cin)).astype(np.float32)
+        W = r.uniform(-0.2, 0.2, (Cout, k * k * Cin)).astype(np.float32)
+        b = r.normal(0, 0.02, Cout).astype(np.float32)
+        lin = vla.LinearI8.from_f32(W, b)
+        Wq, ws = lin.download()
+        got = lin.conv2d(x, k, s, p)
+        want = vla.conv2d_i8(x, Wq, ws, b, k, s, p)
+        assert same_bits(got, want), (H, Wd, Cin, Cout, k, s, p)
+        lin.close()

@@ -692,6 +692,47 @@ class LinearI8:
         _call("vla_linear_i8_forward_quantized_dev", self.h, _dp(out), _dp(xq), xq.stride(0),
               _dp(ascale), xq.shape[0], act, accumulate, _stream(stream))
 
+    def forward(self, x):
+        """Host arrays over the resident weights (vla_linear_i8_forward):
+        returns (out [seq, N], the quantized rows [seq, i8_kpad(K)], their scales)."""
+        x = _f32(x)
+        if x.ndim != 2 or x.shape[1] != self.K:
+            raise ValueError(f"x must be [seq, {self.K}], got {x.shape}")
+        kp = (self.K + 3) & ~3
+        out = np.empty((x.shape[0], self.N), np.float32)
+        xq = np.empty((x.shape[0], kp), np.int8)
+        sa = np.empty(x.shape[0], np.float32)
+        _call("vla_linear_i8_forward", self.h, _ptr(out), _ptr(x), x.shape[0], _ptr(xq), kp, _ptr(sa))
+        return out, xq, sa
+
+    def forward_quantized(self, xq, ascale):
+        """Host int8 rows xq [seq, >= i8_kpad(K)] and scales (vla_linear_i8_forward_quantized)."""
+        xq = np.ascontiguousarray(xq, np.int8)
+        out = np.empty((xq.shape[0], self.N), np.float32)
+        _call("vla_linear_i8_forward_quantized", self.h, _ptr(out), _ptr(xq), xq.shape[1], _ptr(_f32(ascale)),
+              xq.shape[0])
+        return out
+
+    def download(self):
+        """The resident rows [N, i8_kpad(K)] and scales (vla_linear_i8_download)."""
+        kp = (self.K + 3) & ~3
+        Wq = np.empty((self.N, kp), np.int8)
+        ws = np.empty(self.N, np.float32)
+        _call("vla_linear_i8_download", self.h, _ptr(Wq), kp, _ptr(ws))
+        return Wq, ws
+
+    def set_bias(self, bias=None):
+        _call("vla_linear_i8_set_bias", self.h, _ptr(None if bias is None else _f32(bias)))
+
+    def conv2d(self, x, k, stride, pad):
+        """conv2d_i8 with host x [H, W, Cin] over these resident weights (vla_conv2d_i8_resident)."""
+        x = _f32(x)
+        H, Wd, Cin = x.shape
+        Ho, Wo = (H + 2 * pad - k) // stride + 1, (Wd + 2 * pad - k) // stride + 1
+        out = np.empty((Ho, Wo, self.N), np.float32)
+        _call("vla_conv2d_i8_resident", self.h, _ptr(out), _ptr(x), H, Wd, Cin, k, stride, pad)
+        return out
+
     def close(self):
         if self.h:
             lib().vla_linear_i8_free(self.h)
