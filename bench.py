@@ -50,6 +50,13 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
+# The CPUs this process may run on, read before any OpenMP runtime binds the
+# main thread to one place (sched_getaffinity of a bound thread returns 1).
+try:
+    ALLOWED_CPUS = len(os.sched_getaffinity(0))
+except (AttributeError, OSError):
+    ALLOWED_CPUS = None
+
 # The CPU legs follow the baseline protocol: OpenMP threads bound close, one
 # per core (set before any OpenMP runtime in this process starts; a value the
 # caller exported wins), 5 warm-up calls, then the median of >= 50 timed ones.
@@ -214,7 +221,7 @@ def host_cpu_model() -> str:
 def host_cores() -> dict:
     """The host's CPUs: logical CPUs, physical cores (distinct (package,
     core id) pairs of /proc/cpuinfo) and the CPUs this process may run on (the
-    lease's share on a shared box)."""
+    lease's share on a shared box, read at start-up)."""
     phys = set()
     pkg = core = None
     try:
@@ -231,11 +238,7 @@ def host_cores() -> dict:
             phys.add((pkg, core))
     except OSError:
         pass
-    try:
-        allowed = len(os.sched_getaffinity(0))
-    except (AttributeError, OSError):
-        allowed = None
-    return {"logical_cpus": os.cpu_count(), "physical_cores": len(phys) or None, "allowed_cpus": allowed}
+    return {"logical_cpus": os.cpu_count(), "physical_cores": len(phys) or None, "allowed_cpus": ALLOWED_CPUS}
 
 
 def _median_ms(fn, warmup=CPU_WARMUP, timed=CPU_TIMED):
