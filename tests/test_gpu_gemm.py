@@ -307,13 +307,13 @@ def test_panel_rejects_large_m(vla, torch_cuda):
 
 # ---------------------------------------------------------------- split K --
 
-# very long K over at most 64 tiles of 64 x 64 (M > 128 splits only there):
-# ACT's w2 (302 x 512 x 3200), a ResNet 3x3/512 conv (300 x 512 x 4608),
-# K tails (4100, 3100), a 129-row case, 64 tiles exactly (256 x 1024 x 4096)
-# more than 256 rows (129..256 rows over N <= 2048 take the unsplit skinny
-# kernel): K tails (4100, 3100), an N edge (100, 48) and a 60-tile output
-SPLIT_SHAPES = [(302, 512, 3200), (300, 512, 4608), (257, 100, 4100), (300, 48, 3100), (300, 768, 4096),
-                (300, 512, 4100),
+# very long K over at most 64 tiles of 64 x 64 (M > 128 splits only there),
+# more than 320 rows (129..320 rows over N <= 2048 take the unsplit skinny
+# kernel): a w2-like 340 x 512 x 3200, a ResNet-like 3x3/512 conv
+# (330 x 512 x 4608), K tails (4100, 3100), one row past the skinny bound, an
+# N edge (48) and a 60-tile output
+SPLIT_SHAPES = [(340, 512, 3200), (330, 512, 4608), (321, 100, 4100), (330, 48, 3100), (330, 640, 4096),
+                (330, 512, 4100),
                 # at most 128 rows (the skinny kernel): SigLIP's projection
                 # (64 x 960 x 12288), a K tail, one row, 16 columns
                 (64, 960, 12288), (100, 1000, 4100), (1, 16, 4096), (16, 200, 8192)]
@@ -397,8 +397,8 @@ def test_split_k_plan_bounds(vla):
     assert vla.gemm_i8_split_bytes(658, 768, 768) == 0        # K < 1024
     assert vla.gemm_i8_split_bytes(8192, 4096, 4096) == 0     # fills the chip
     assert vla.gemm_i8_split_bytes(512, 4096, 4096) == 0      # one LDS-DMA tile per CU: measured slower split
-    for seq, N, K in [(129, 100, 4100), (200, 48, 3100), (256, 1024, 4096)]:
-        assert vla.gemm_i8_split_bytes(seq, N, K) == 0        # 129..256 rows, N <= 2048: unsplit skinny kernel
+    for seq, N, K in [(129, 100, 4100), (200, 48, 3100), (256, 1024, 4096), (302, 512, 3200), (320, 100, 4100)]:
+        assert vla.gemm_i8_split_bytes(seq, N, K) == 0        # 129..320 rows, N <= 2048: unsplit skinny kernel
     for seq, N, K in SPLIT_SHAPES:
         assert 0 < vla.gemm_i8_split_bytes(seq, N, K) <= 8 << 20
 
@@ -524,9 +524,10 @@ def test_gemv_rows_bitexact(vla, orc, torch_cuda, seq, N, K, act, accumulate):
 
 @pytest.mark.parametrize("groups", ["", "1", "3"])
 @pytest.mark.parametrize("seq,N,K", [(177, 960, 960), (256, 100, 300), (129, 17, 64), (200, 1024, 4100),
-                                     (177, 2048, 2560), (240, 33, 1027)])
-def test_skinny_129_to_256_rows_bitexact(vla, orc, torch_cuda, groups, seq, N, K):
-    """129..256 rows over N <= 2048 take the skinny kernel in row groups of at
+                                     (177, 2048, 2560), (240, 33, 1027), (302, 512, 512), (302, 512, 3200),
+                                     (320, 48, 1027)])
+def test_skinny_129_to_320_rows_bitexact(vla, orc, torch_cuda, groups, seq, N, K):
+    """129..320 rows over N <= 2048 take the skinny kernel in row groups of at
     most 8 fragments (a forced count below that is raised): the oracle's
     outputs bit for bit, also through the split-K entry point, and with the
     route switched off per call (VLA_HIP_SKINNY_MAXM=128: the tiles, split

@@ -1520,20 +1520,25 @@ SplitPlan skinny_split_plan(int N, int K) {
     return p;
 }
 
-// 129..256 row-major rows over a narrow output (N <= 2048: at most 128
+// 129..320 row-major rows over a narrow output (N <= 2048: at most 128
 // column blocks, where the tiles leave most CUs idle) take the skinny kernel
 // in row groups of at most 8 fragments, unsplit. Graph replays on MI355X,
 // tiles -> skinny: 177x960x960 5.87 -> 4.30 us, 177x960x320 5.65 -> 3.00,
 // 177x2560x960 9.82 -> 7.53, 256x960x960 5.81 -> 4.79, 200x4096x1024 13.5 ->
-// 12.0; wide outputs stay on the tiles (177x960x5120 6.63 -> 12.76).
-// VLA_HIP_SKINNY_MAXM=128 turns the route off, and a tile forced with
-// VLA_HIP_GEMM_TILE bypasses it (both read per call, like the other knobs).
+// 12.0; wide outputs stay on the tiles (177x960x5120 6.63 -> 12.76). ACT's
+// 302-row encoder (40 tiles of 64 x 64 per 512-wide projection, its w2 split
+// over K with a reduce pass) 0.343 -> 0.325 ms per forward with the bound at
+// 320; Octo's 658 rows lose on it (1.06 -> 1.21 ms with the bound at 704).
+// VLA_HIP_SKINNY_MAXM=<rows> moves the route's upper bound (128 turns it
+// off), and a tile forced with VLA_HIP_GEMM_TILE bypasses it (both read per
+// call, like the other knobs).
 bool skinny_mid_rows(int M, int N, bool panel) {
-    if (M <= 128 || M > 256 || N > 2048 || panel) return false;
+    if (M <= 128 || N > 2048 || panel) return false;
     const char* tile = std::getenv("VLA_HIP_GEMM_TILE");
     if (tile && *tile) return false;
     const char* e = std::getenv("VLA_HIP_SKINNY_MAXM");
-    return !(e && std::atoi(e) == 128);
+    const int maxm = e && std::atoi(e) >= 128 ? std::atoi(e) : 320;
+    return M <= maxm;
 }
 
 SplitPlan split_plan(int M, int N, int K) {

@@ -19,6 +19,8 @@
 #include "common.h"
 #include "quant_row.h"
 
+#include <cstdlib>
+
 #pragma clang fp contract(off)
 
 namespace vla {
@@ -100,6 +102,47 @@ __global__ __launch_bounds__(256) void quantize_rows_reg(const float* __restrict
     }
     // the zero pad [K, ldq) (whole words: K % 4 == 0 and ldq % 4 == 0)
     for (int k = K + 4 * lane; k < ldq; k += 256) *reinterpret_cast<uint32_t*>(qr + k) = 0u;
+}
+
+// Long rows (K >= 2048, 16-byte aligned, K % 4 == 0), row-major: a block per
+// row, NV float4 per thread (16 VGPRs of row data at K = 4096 instead of the
+// wave-per-row kernel's 64), so eight rows' loads are in flight per CU at once
+// and a grid of thousands of rows runs in full rounds of resident blocks. The
+// block max goes through LDS; the max is exact in any order, so the bytes and
+// the scale are the wave-per-row kernel's.
+template <int NV>
+__global__ __launch_bounds__(256) void quantize_rows_wide(const float* __restrict__ x, int ldx,
+                                                          int8_t* __restrict__ xq, int ldq,
+                                                          float* __restrict__ scale, int K) {
+    __shared__ float red[4];
+    const int t = threadIdx.x, row = blockIdx.x;
+    const float* xr = x + (size_t)row * ldx;
+    float4 v[NV];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int k = 4 * (t + 256 * i);
+        v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (k < K) {
+            v[i] = *reinterpret_cast<const float4*>(xr + k);
+            amax = fmaxf(amax, fmaxf(fmaxf(fabsf(v[i].x), fabsf(v[i].y)), fmaxf(fabsf(v[i].z), fabsf(v[i].w))));
+        }
+    }
+    amax = wave_max_f32(amax);
+    if ((t & 63) == 0) red[t >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    const float s = row_scale(amax);
+    const float inv = 1.0f / s;
+    if (t == 0) scale[row] = s;
+    int8_t* qr = xq + (size_t)row * ldq;
+#pragma unroll
+    for (int i = 0; i < NV; i++) {
+        const int k = 4 * (t + 256 * i);
+        if (k < K) *reinterpret_cast<uint32_t*>(qr + k) = q8x4(v[i], inv);
+    }
+    // the zero pad [K, ldq) (whole words: K % 4 == 0 and ldq % 4 == 0)
+    for (int k = K + 4 * t; k < ldq; k += 1024) *reinterpret_cast<uint32_t*>(qr + k) = 0u;
 }
 
 // The same quantization written in the panel layout (common.h): word (m, k)
@@ -281,6 +324,15 @@ void launch_quantize_rows_panel(const float* x, int ldx, int8_t* xq, float* scal
     VLA_LAUNCH_CHECK();
 }
 
+// Rows of at least this many floats take the block-per-row kernel;
+// VLA_HIP_QUANT_WIDE_K overrides it per call (A/B runs: a value above 4096
+// keeps every row on the wave-per-row kernels; the bytes never change).
+static int wide_min_k() {
+    const char* e = std::getenv("VLA_HIP_QUANT_WIDE_K");
+    const int v = e ? std::atoi(e) : 0;
+    return v > 0 ? v : 2048;
+}
+
 void launch_quantize_rows(const float* x, int ldx, int8_t* xq, int ldq, float* scale, int rows,
                           int K, hipStream_t st) {
     VLA_REQUIRE(rows >= 0 && K > 0, "quantize: rows must be >= 0 and K > 0");
@@ -290,7 +342,12 @@ void launch_quantize_rows(const float* x, int ldx, int8_t* xq, int ldq, float* s
     if (rows == 0) return;
     const bool vec = K % 4 == 0 && ldx % 4 == 0 && aligned(x, 16);
     const dim3 grid((rows + 3) / 4), block(256);
-    if (vec && K <= 16 * 256) {
+    if (vec && K >= wide_min_k() && K <= 4 * 1024) {
+        const int nv = (K + 1023) / 1024;
+        if (nv <= 2) quantize_rows_wide<2><<<rows, block, 0, st>>>(x, ldx, xq, ldq, scale, K);
+        else if (nv <= 3) quantize_rows_wide<3><<<rows, block, 0, st>>>(x, ldx, xq, ldq, scale, K);
+        else quantize_rows_wide<4><<<rows, block, 0, st>>>(x, ldx, xq, ldq, scale, K);
+    } else if (vec && K <= 16 * 256) {
         const int nv = (K + 255) / 256;
         if (nv <= 1) quantize_rows_reg<1><<<grid, block, 0, st>>>(x, ldx, xq, ldq, scale, rows, K);
         else if (nv <= 2) quantize_rows_reg<2><<<grid, block, 0, st>>>(x, ldx, xq, ldq, scale, rows, K);
