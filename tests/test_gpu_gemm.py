@@ -168,7 +168,7 @@ def test_k_bound_rejected(vla):
 
 
 TILES = ["128x128x64", "64x128x64", "64x64x64", "128x128x64s4", "64x128x64s4", "256x128x128s3w8",
-         "256x256x128s2w8", "256x128x128s3w8p", "256x256x128s2w8p", "128x128x128s2", "64x64x128s3", "64x64x128s4"]
+         "256x256x128s2w8", "256x128x128s3w8p", "256x256x128s2w8p", "128x128x128s2", "64x64x128s3", "64x64x128s4", "32x64x128s3", "32x64x128s4"]
 
 
 @pytest.mark.parametrize("tile", TILES)

@@ -1431,7 +1431,8 @@ const Tile kTiles[] = {{128, 128, 64, 0},       {64, 128, 64, 0},         {64, 6
                        {64, 64, 128, 0},        {64, 128, 128, 0},
                        {128, 128, 64, 4},       {64, 128, 64, 4},         {256, 128, 128, 3, 8},
                        {256, 256, 128, 2, 8},   {256, 128, 128, 3, 8, true}, {256, 256, 128, 2, 8, true},
-                       {128, 128, 128, 2},      {64, 64, 128, 3},         {64, 64, 128, 4}};
+                       {128, 128, 128, 2},      {64, 64, 128, 3},         {64, 64, 128, 4},
+                       {32, 64, 128, 3},        {32, 64, 128, 4}};
 
 Tile pick_tile(int M, int N, int K) {
     const char* env = std::getenv("VLA_HIP_GEMM_TILE");
@@ -1474,7 +1475,14 @@ Tile pick_tile(int M, int N, int K) {
     // 20.12, 512x2560x960 13.80 -> 9.90; bit-identical sums. Very long K over
     // at most 64 such tiles (302x3200x512 10.38 split vs 11.27, 200x4096x1024
     // 12.96 vs 13.61) stays on the split-K register tile.
-    const Tile lds64{64, 64, 128, K <= 1024 ? 3 : 4};
+    // Where 64 x 64 tiles leave CUs idle and 32 x 64 ones still fit one per
+    // CU (Octo's 658 x 768 outputs: 132 -> 252 blocks), the 32 x 64 tile: a
+    // block then pulls (32 + 64) instead of (64 + 64) bytes per byte of K,
+    // and the per-CU L2 -> LDS fill is what these layers wait on.
+    // VLA_HIP_GEMM_T32=0 keeps the 64 x 64 tile (A/B runs; sums unchanged).
+    const char* t32 = std::getenv("VLA_HIP_GEMM_T32");
+    const bool use32 = tiles(64, 64) < kCUs && tiles(32, 64) <= kCUs && !(t32 && std::atoi(t32) == 0);
+    const Tile lds{use32 ? 32 : 64, 64, 128, K <= 1024 ? 3 : 4};
     // Large outputs over short K (M, N >= 1024, 512 <= K <= 1024, at least
     // one 128 x 128 tile per CU): the LDS-DMA 128 x 128 tile with 128-byte
     // slabs, two stages (64 KiB, two blocks per CU) and non-temporal stores;
@@ -1484,12 +1492,12 @@ Tile pick_tile(int M, int N, int K) {
     // 1024-row layers), at 658 rows and at 1000^3 the register-staged tiles
     // stay ahead.
     if (K <= 1024 && K >= 512 && M >= 1024 && N >= 1024 && tiles(128, 128) >= kCUs) return {128, 128, 128, 2};
-    if (K <= 1024) return tiles(64, 128) >= 2 * kCUs ? Tile{64, 128, 64, 0} : K >= 256 ? lds64 : small;
+    if (K <= 1024) return tiles(64, 128) >= 2 * kCUs ? Tile{64, 128, 64, 0} : K >= 256 ? lds : small;
     if (tiles(256, 256) >= 2 * kCUs) return {256, 256, 128, 2, 8, true};
     if (tiles(256, 128) >= kCUs) return {256, 128, 128, 3, 8, true};
     if (tiles(128, 128) >= kCUs) return {128, 128, 64, 4};
     if (tiles(64, 64) <= 64 && K >= 3072) return small;  // split over K (split_plan)
-    return lds64;
+    return lds;
 }
 
 // Split-K plan: for M > 128 on the register-staged tiles with K >= 1024 and
@@ -1569,7 +1577,10 @@ void dispatch_tile(const Tile& t, const GemmArgs& a, hipStream_t st) {
         return;
     }
     if (t.stages) {
-        if (t.bm == 64 && t.bn == 64) {
+        if (t.bm == 32) {
+            if (t.stages == 3) run_lds<32, 64, 128, 3>(a, st);
+            else run_lds<32, 64, 128, 4>(a, st);
+        } else if (t.bm == 64 && t.bn == 64) {
             if (t.stages == 3) run_lds<64, 64, 128, 3>(a, st);
             else run_lds<64, 64, 128, 4>(a, st);
         } else if (t.bm == 128 && t.bk == 128) run_lds<128, 128, 128, 2>(a, st);
