@@ -135,13 +135,17 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
     const int mk = a.mask_kind;
     const int qg = (MKC == 3 && qok) ? a.q_group[qi] : 0;
     const int G = a.n_groups;
-    // small group tables live in LDS, so the per-key test is an LDS read
-    const uint8_t* allow = a.allow;
-    if (MKC == 3 && G * G <= C::ALLOW) {
-        uint8_t* al = reinterpret_cast<uint8_t*>(smem) + C::MAIN;
-        for (int i = tid; i < G * G; i += W * 64) al[i] = a.allow[i];
+    // small group tables live in LDS, so the per-key test is an LDS read. The
+    // main loop reads the table through `al` (derived from the shared array,
+    // so its reads compile to ds_read_u8) or straight from global memory; one
+    // pointer that could be either compiles to flat loads, whose waits
+    // (vmcnt(0) as well) also drain the next key tile's prefetch.
+    const bool allow_lds = MKC == 3 && G * G <= C::ALLOW;
+    const uint8_t* al = reinterpret_cast<const uint8_t*>(smem) + C::MAIN;
+    if (allow_lds) {
+        uint8_t* alw = reinterpret_cast<uint8_t*>(smem) + C::MAIN;
+        for (int i = tid; i < G * G; i += W * 64) alw[i] = a.allow[i];
         __syncthreads();
-        allow = al;
     }
 
     // keys past kv_end are blocked for every query of the block (causal bound)
@@ -159,9 +163,14 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
     // KT x HDP/4 tile is row e / (HDP/4), dims 4 * (e % (HDP/4))
     float4 kr[F4], vr[F4];
     // with the tile: the mask data of the lane's keys kv0 + 16 kt + 4 g + r
-    // (dense mask values or key groups), so the masking step waits on nothing
+    // (dense mask values or key groups), so the masking step waits on nothing.
+    // A run of 4 key groups read as one word stays packed (gword) until the
+    // tile is used: unpacking it here would make the wave wait for that load,
+    // and with it for the whole K/V prefetch issued just before.
     float mnext[4 * NT];
-    int gnext[4 * NT];
+    int gnext[4 * NT] = {};
+    uint32_t gword[NT] = {};
+    bool gpacked[NT] = {};
     auto gload = [&](int kv0, int end) {
         if (kv0 + KT <= end && HD == HDP) {  // wave-uniform: every row and column is in range
 #pragma unroll
@@ -190,10 +199,9 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
 #pragma unroll
         for (int kt = 0; kt < NT; kt++) {
             const int j0 = kv0 + kt * 16 + 4 * g;
+            if (MKC == 3) gpacked[kt] = j0 + 4 <= end && vec_kg;
             if (MKC == 3 && j0 + 4 <= end && vec_kg) {
-                const uint32_t w = *reinterpret_cast<const uint32_t*>(a.k_group + j0);
-#pragma unroll
-                for (int r = 0; r < 4; r++) gnext[kt * 4 + r] = (int)((w >> (8 * r)) & 0xffu);
+                gword[kt] = *reinterpret_cast<const uint32_t*>(a.k_group + j0);
             } else if (MKC == 1 && j0 + 4 <= end && vec_mask) {
                 float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
                 if (qok) v = *reinterpret_cast<const float4*>(a.mask + (size_t)qi * a.ldm + j0);
@@ -240,7 +248,7 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
 #pragma unroll
             for (int x = 0; x < 4 * NT; x++) {
                 mcur[x] = mnext[x];
-                gcur[x] = gnext[x];
+                gcur[x] = gpacked[x >> 2] ? (int)((gword[x >> 2] >> (8 * (x & 3))) & 0xffu) : gnext[x];
             }
         }
         wave_lds_sync();
@@ -253,12 +261,22 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
         bool mblk[4 * NT];
         if (MKC == 3) {
             bool live = false;
+            if (allow_lds) {
 #pragma unroll
-            for (int x = 0; x < 4 * NT; x++) {
-                const int j = kv0 + (x >> 2) * 16 + 4 * g + (x & 3);
-                const bool b = !qok || j >= kv_end || !allow[qg * G + gcur[x]];
-                mblk[x] = b;
-                live = live || !b;
+                for (int x = 0; x < 4 * NT; x++) {
+                    const int j = kv0 + (x >> 2) * 16 + 4 * g + (x & 3);
+                    const bool b = !qok || j >= kv_end || !al[qg * G + gcur[x]];
+                    mblk[x] = b;
+                    live = live || !b;
+                }
+            } else {
+#pragma unroll
+                for (int x = 0; x < 4 * NT; x++) {
+                    const int j = kv0 + (x >> 2) * 16 + 4 * g + (x & 3);
+                    const bool b = !qok || j >= kv_end || !a.allow[qg * G + gcur[x]];
+                    mblk[x] = b;
+                    live = live || !b;
+                }
             }
             if (!__any(live)) continue;
         }

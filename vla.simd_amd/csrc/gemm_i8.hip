@@ -1475,14 +1475,19 @@ Tile pick_tile(int M, int N, int K) {
     // 20.12, 512x2560x960 13.80 -> 9.90; bit-identical sums. Very long K over
     // at most 64 such tiles (302x3200x512 10.38 split vs 11.27, 200x4096x1024
     // 12.96 vs 13.61) stays on the split-K register tile.
-    // Where 64 x 64 tiles leave CUs idle and 32 x 64 ones still fit one per
-    // CU (Octo's 658 x 768 outputs: 132 -> 252 blocks), the 32 x 64 tile: a
-    // block then pulls (32 + 64) instead of (64 + 64) bytes per byte of K,
-    // and the per-CU L2 -> LDS fill is what these layers wait on.
-    // VLA_HIP_GEMM_T32=0 keeps the 64 x 64 tile (A/B runs; sums unchanged).
+    // Where 64 x 64 tiles leave CUs idle and 32 x 64 ones number at most 1.5
+    // per CU (Octo's 658/690 x 768 outputs: 132 -> 252/264 blocks, SigLIP's
+    // 1024 x 768: 192 -> 384), the 32 x 64 tile with 4 stages: a block then
+    // pulls (32 + 64) instead of (64 + 64) bytes per byte of K, and the
+    // per-CU L2 -> LDS fill is what these layers wait on. Forced tiles, graph
+    // replays: 690x3072x768 10.94 -> 10.59 us (3 stages 11.02), 690x768x768
+    // 5.15 -> 4.86 (4.98), 1024x768x768 5.14 -> 4.97 (5.12), 1024x3072x768
+    // 10.93 -> 10.60 (10.97). VLA_HIP_GEMM_T32=0 keeps the 64 x 64 tile (A/B
+    // runs; sums unchanged).
     const char* t32 = std::getenv("VLA_HIP_GEMM_T32");
-    const bool use32 = tiles(64, 64) < kCUs && tiles(32, 64) <= kCUs && !(t32 && std::atoi(t32) == 0);
-    const Tile lds{use32 ? 32 : 64, 64, 128, K <= 1024 ? 3 : 4};
+    const bool use32 =
+        tiles(64, 64) < kCUs && tiles(32, 64) <= kCUs + kCUs / 2 && !(t32 && std::atoi(t32) == 0);
+    const Tile lds = use32 ? Tile{32, 64, 128, 4} : Tile{64, 64, 128, K <= 1024 ? 3 : 4};
     // Large outputs over short K (M, N >= 1024, 512 <= K <= 1024, at least
     // one 128 x 128 tile per CU): the LDS-DMA 128 x 128 tile with 128-byte
     // slabs, two stages (64 KiB, two blocks per CU) and non-temporal stores;
