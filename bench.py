@@ -6,18 +6,23 @@ Workload: M in {1, 50, 100, 512, 2048, 8192} x
 reference op path dense_linear_i8: fp32 activations ~N(0,1) quantized per row
 on the device, int8 weights uniform in [-127,127] with per-channel scales
 ~U(1e-3,1e-2) and bias ~N(0,0.02), int32 accumulate, fp32 out. One step is one
-pass over all 30 shapes (a quantize launch + a GEMM launch each), inputs and
+pass over all 30 shapes (a quantize launch + a GEMM launch each, one launch
+for the few-row shapes below), inputs and
 weights resident in HBM; small shapes cycle through rotating copies of their
 weights and outputs (>= 512 MiB per shape) so every launch streams from HBM
 rather than from L2/MALL. For M <= 128 the quantize writes the library's
 panel layout (vla_quantize_act_i8_panel_dev) and the GEMM reads it
-(vla_dense_linear_i8_panel_dev): the same values, byte-identical output.
+(vla_dense_linear_i8_panel_dev): the same values, byte-identical output. For
+M <= 16 with K <= 2048 the op is the library's op entry itself
+(vla_dense_linear_i8_dev with caller-owned scratch), which quantizes inside
+the GEMM: one launch, the same scratch bytes and output.
 Each sweep row also carries the warm time (gemm_warm_us: the same launches
 on one weight and output copy, operands resident in L2 / MALL) beside the
 cold, rotating one (gemm_us), which is what frac and value use.
 
 value = int8 TOPS of the whole step (sum of 2*M*N*K over the shapes / step
-time). roofline = the dominant kernel (the M=8192, K=N=4096 GEMM) measured
+time). gemm_us is the GEMM launch alone (on the quantized rows), op_us the
+whole op. roofline = the dominant kernel (the M=8192, K=N=4096 GEMM) measured
 with HIP events on the stream it runs on. cpu_baseline = the reference's own
 dense_linear_i8 (its AVX-VNNI kernel when the host CPU has AVX-VNNI, else its
 scalar dense_linear_i8_ref) built from the reference sources into
@@ -125,6 +130,12 @@ class Shape:
         self.sa = torch.empty(M, dtype=torch.float32, device=dev)
         self.ws = torch.from_numpy(ws).to(dev)
         self.b = torch.from_numpy(b).to(dev)
+        # at most 16 rows the library's op entry (vla_dense_linear_i8_dev, the
+        # reference's dense_linear_i8 with caller-owned scratch) quantizes inside
+        # the GEMM: one launch per op, the same bytes in the scratch and out
+        self.fused = M <= 16 and vla.rowop_linear_i8_fits(0, M, K)
+        if self.fused:
+            self.xq_op = torch.zeros((M, self.ldw), dtype=torch.int8, device=dev)
         # split-K workspace for long-K shapes whose tiles leave CUs idle (the
         # same values as the unsplit GEMM; the op API's caller-owned scratch)
         nsplit = 0 if self.panel else vla.gemm_i8_split_bytes(M, N, K)
@@ -157,6 +168,12 @@ class Shape:
         self.i = r
 
     def op(self, vla, stream):
+        if self.fused:
+            r = self.i % self.R
+            self.i += 1
+            vla.dense_linear_i8_dev(self.out[r], self.x, self.W[r], self.ws, self.b, self.K, self.xq_op, self.sa,
+                                    stream=stream)
+            return
         self.quantize(vla, stream)
         self.gemm(vla, stream)
 

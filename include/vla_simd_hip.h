@@ -620,6 +620,45 @@ VLA_API int32_t vla_act_int8_convs(void* h);
 VLA_API int32_t vla_act_int8_layers(void* h);
 VLA_API int32_t vla_act_graph_nodes(void* h);
 
+/* ---------------------------------------------- IMPACT, model level ------- */
+
+/* The reference's IMPACT entry points, same names, signatures and status
+ * codes (include/vla_simd.h:206-243, src/models/impact/impact_capi.cpp), for
+ * vla_simd/policy_server.py's model-library binding. model_dir holds
+ * config.txt (with vocab_full / unk_id), vision.meta/.bin (the trunk with its
+ * FiLM points), impact.meta/.bin (the transformer with its text tail),
+ * text.meta/.bin (T5-small, the text projection and positions, the FiLM
+ * head), vocab.txt, vocab_map.bin and stats.bin, or a vla.simd GGUF carrying
+ * them; IMPACT_INT8 (and IMPACT_I8_CONV_FROM / _TO) are read at load.
+ * set_instruction runs the language pathway on the device and caches it (a
+ * repeated instruction costs nothing); predict sets the instruction, then
+ * runs frames [n_cams, img_h, img_w, 3] uint8 and state [state_dim] raw to
+ * actions [chunk, action_dim] (un-normalized when unnormalize != 0) on the
+ * device. tokens / film copy the current instruction's ids, compacted ids,
+ * mask ([n_text] each) and FiLM gamma / beta ([film_total] each) and return
+ * the count, VLA_ERR_ARG before any instruction or for a short buffer. */
+VLA_API void* vla_impact_load(const char* model_dir);
+VLA_API void vla_impact_free(void* h);
+VLA_API int32_t vla_impact_chunk(void* h);
+VLA_API int32_t vla_impact_action_dim(void* h);
+VLA_API int32_t vla_impact_state_dim(void* h);
+VLA_API int32_t vla_impact_n_cams(void* h);
+VLA_API int32_t vla_impact_img_h(void* h);
+VLA_API int32_t vla_impact_img_w(void* h);
+VLA_API int32_t vla_impact_n_text(void* h);
+VLA_API int32_t vla_impact_set_instruction(void* h, const char* instruction);
+VLA_API int32_t vla_impact_predict(void* h, const uint8_t* frames, const float* state, const char* instruction,
+                                   int32_t unnormalize, float* actions);
+VLA_API int32_t vla_impact_tokens(void* h, int32_t* ids, int32_t* compact, int32_t* mask, int32_t max_elems);
+VLA_API int32_t vla_impact_film(void* h, float* gamma, float* beta, int32_t max_elems);
+/* Extensions with no counterpart in vla_simd.h: predict on device pointers
+ * and a stream (the instruction set first, by set_instruction or predict),
+ * and the counts of int8 transformer layers / backbone convs. */
+VLA_API int32_t vla_impact_predict_dev(void* h, const uint8_t* frames, const float* state, int32_t unnormalize,
+                                       float* actions, void* stream);
+VLA_API int32_t vla_impact_int8_layers(void* h);
+VLA_API int32_t vla_impact_int8_convs(void* h);
+
 /* -------------------------------------------- SmolVLA, model level ------- */
 
 /* The reference's SmolVLA entry points, same names and signatures

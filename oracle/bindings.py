@@ -638,6 +638,17 @@ def _ref_models():
     L.vla_smolvla_tokenize.argtypes, L.vla_smolvla_tokenize.restype = [P, ctypes.c_char_p, P, P], i32
     L.vla_smolvla_predict_rtc.argtypes = [P, P, i32, i32, i32, P, P, i32, P, P, c_uint64, P, P, i32, P, c_float]
     L.vla_smolvla_predict_rtc.restype = i32
+    # the reference's own IMPACT entry points (impact_capi.cpp)
+    L.vla_impact_load.argtypes, L.vla_impact_load.restype = [ctypes.c_char_p], P
+    L.vla_impact_free.argtypes, L.vla_impact_free.restype = [P], None
+    for n in ("chunk", "action_dim", "state_dim", "n_cams", "img_h", "img_w", "n_text"):
+        f = getattr(L, f"vla_impact_{n}")
+        f.argtypes, f.restype = [P], i32
+    L.vla_impact_set_instruction.argtypes, L.vla_impact_set_instruction.restype = [P, ctypes.c_char_p], i32
+    L.vla_impact_predict.argtypes = [P, P, P, ctypes.c_char_p, i32, P]
+    L.vla_impact_predict.restype = i32
+    L.vla_impact_tokens.argtypes, L.vla_impact_tokens.restype = [P, P, P, P, i32], i32
+    L.vla_impact_film.argtypes, L.vla_impact_film.restype = [P, P, P, i32], i32
     L._models_declared = True
     return L
 
@@ -904,6 +915,53 @@ class RefT5Tok:
     def __del__(self):
         if getattr(self, "h", None):
             _ref_models().ref_t5tok_free(self.h)
+
+
+class RefImpactModel:
+    """The reference's ImpactModel through its own C ABI (vla_impact_load /
+    _set_instruction / _predict / _tokens / _film, IMPACT_INT8 as the process
+    environment holds it at load)."""
+
+    def __init__(self, dirpath):
+        L = _ref_models()
+        self.h = L.vla_impact_load(dirpath.encode())
+        if not self.h:
+            raise RuntimeError(f"reference ImpactModel::load failed for {dirpath}")
+        self.chunk, self.action_dim = L.vla_impact_chunk(self.h), L.vla_impact_action_dim(self.h)
+        self.state_dim, self.n_cams = L.vla_impact_state_dim(self.h), L.vla_impact_n_cams(self.h)
+        self.img_h, self.img_w, self.n_text = L.vla_impact_img_h(self.h), L.vla_impact_img_w(self.h), \
+            L.vla_impact_n_text(self.h)
+
+    def set_instruction(self, instruction):
+        return int(_ref_models().vla_impact_set_instruction(self.h, instruction.encode()))
+
+    def predict(self, frames, state, instruction, unnormalize=True):
+        """-> (status, actions [chunk, action_dim])"""
+        frames = np.ascontiguousarray(frames, np.uint8)
+        state = _f32(state)
+        out = np.zeros((self.chunk, self.action_dim), np.float32)
+        st = _ref_models().vla_impact_predict(self.h, _p(frames), _p(state), instruction.encode(),
+                                              int(bool(unnormalize)), _p(out))
+        return int(st), out
+
+    def tokens(self):
+        ids, comp, mask = (np.zeros(self.n_text, np.int32) for _ in range(3))
+        n = _ref_models().vla_impact_tokens(self.h, _p(ids), _p(comp), _p(mask), self.n_text)
+        return int(n), ids, comp, mask
+
+    def film(self):
+        L = _ref_models()
+        n = L.vla_impact_film(self.h, None, None, 1 << 30)
+        if n <= 0:
+            return int(n), None, None
+        g, b = np.zeros(n, np.float32), np.zeros(n, np.float32)
+        L.vla_impact_film(self.h, _p(g), _p(b), n)
+        return int(n), g, b
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            _ref_models().vla_impact_free(self.h)
+            self.h = None
 
 
 class RefOctoModel:

@@ -405,7 +405,10 @@ def test_split_k_plan_bounds(vla):
 
 @pytest.mark.parametrize("seq,N,K,act,accumulate", [(100, 3200, 512, 0, 0), (7, 48, 1027, 1, 1),
                                                     (302, 512, 512, 2, 0), (1, 16, 3, 0, 1),
-                                                    (2048, 960, 2560, 0, 0)])
+                                                    (2048, 960, 2560, 0, 0),
+                                                    # <= 16 rows: quantized inside the GEMM
+                                                    (1, 3200, 512, 0, 0), (16, 2560, 960, 1, 1),
+                                                    (5, 100, 2048, 2, 0), (9, 200, 64, 1, 0)])
 def test_dense_linear_i8_dev_caller_scratch(vla, orc, torch_cuda, seq, N, K, act, accumulate):
     """tcpu::dense_linear_i8 with caller-owned scratch (quant_ops.h:66-72) on
     device pointers: the scratch holds exactly seq x i8_kpad(K) bytes and seq
@@ -435,6 +438,41 @@ def test_dense_linear_i8_dev_caller_scratch(vla, orc, torch_cuda, seq, N, K, act
         assert same_bits(got, want)
     else:
         assert max_rel(got, want) <= 2e-6
+
+
+@pytest.mark.parametrize("seq,N,K", [(1, 3200, 512), (16, 2560, 960), (7, 33, 2048), (12, 64, 4)])
+def test_op_fusion_matches_two_launches(vla, orc, torch_cuda, seq, N, K):
+    """The op API's few-row path (quantize inside the GEMM, the scratch written
+    by the same kernel) leaves the same scratch bytes, scales and outputs as
+    the separate quantize + GEMM launches (VLA_HIP_OP_FUSE=0), twice in a row."""
+    torch = torch_cuda
+    x, W, b = _case(orc, seq, N, K)
+    Kp = (K + 3) & ~3
+    ld = (Kp + 15) // 16 * 16
+    Wq, ws = orc.quantize_weights_i8(W, ld)
+    dev = torch.device("cuda")
+    xd = torch.from_numpy(x).to(dev)
+    Wd = torch.from_numpy(np.ascontiguousarray(Wq)).to(dev)
+    wsd, bd = torch.from_numpy(ws).to(dev), torch.from_numpy(b).to(dev)
+    res = {}
+    for fuse in ("1", "0"):
+        os.environ["VLA_HIP_OP_FUSE"] = fuse
+        try:
+            for rep in range(2):
+                xq = torch.full((seq, ld), 99, dtype=torch.int8, device=dev)
+                sa = torch.full((seq,), 7.0, dtype=torch.float32, device=dev)
+                out = torch.full((seq, N), 0.5, dtype=torch.float32, device=dev)
+                vla.dense_linear_i8_dev(out, xd, Wd, wsd, bd, K, xq, sa, act=1, accumulate=1)
+                torch.cuda.synchronize()
+                res[(fuse, rep)] = (xq.cpu().numpy(), sa.cpu().numpy(), out.cpu().numpy())
+        finally:
+            os.environ.pop("VLA_HIP_OP_FUSE", None)
+    ref = res[("0", 0)]
+    for k, v in res.items():
+        for a, b_ in zip(v, ref):
+            assert same_bits(a, b_), f"{k} differs from the two-launch path"
+    xqo, sao = orc.quantize_act_i8(x, ldq=ld)
+    assert same_bits(ref[0], xqo) and same_bits(ref[1], sao)
 
 
 # ------------------------------------------------------------- row groups --

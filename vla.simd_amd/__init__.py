@@ -78,6 +78,10 @@ EXPORTS = (
     "vla_act_load", "vla_act_free", "vla_act_chunk", "vla_act_action_dim", "vla_act_state_dim",
     "vla_act_n_cams", "vla_act_img_h", "vla_act_img_w", "vla_act_predict", "vla_act_predict_dev",
     "vla_act_encode", "vla_act_feat_shape", "vla_act_int8_convs", "vla_act_int8_layers", "vla_act_graph_nodes",
+    "vla_impact_load", "vla_impact_free", "vla_impact_chunk", "vla_impact_action_dim", "vla_impact_state_dim",
+    "vla_impact_n_cams", "vla_impact_img_h", "vla_impact_img_w", "vla_impact_n_text", "vla_impact_set_instruction",
+    "vla_impact_predict", "vla_impact_tokens", "vla_impact_film", "vla_impact_predict_dev",
+    "vla_impact_int8_layers", "vla_impact_int8_convs",
     "vla_smolvla_load", "vla_smolvla_free", "vla_smolvla_chunk", "vla_smolvla_action_dim",
     "vla_smolvla_state_dim", "vla_smolvla_n_views", "vla_smolvla_img_size", "vla_smolvla_tok_maxlen",
     "vla_smolvla_tokenize", "vla_smolvla_predict", "vla_smolvla_predict_rtc", "vla_smolvla_preprocess",
@@ -256,6 +260,22 @@ def _declare(L):
         "vla_act_int8_convs": (i32, [P]),
         "vla_act_int8_layers": (i32, [P]),
         "vla_act_graph_nodes": (i32, [P]),
+        "vla_impact_load": (P, [c_char_p]),
+        "vla_impact_free": (None, [P]),
+        "vla_impact_chunk": (i32, [P]),
+        "vla_impact_action_dim": (i32, [P]),
+        "vla_impact_state_dim": (i32, [P]),
+        "vla_impact_n_cams": (i32, [P]),
+        "vla_impact_img_h": (i32, [P]),
+        "vla_impact_img_w": (i32, [P]),
+        "vla_impact_n_text": (i32, [P]),
+        "vla_impact_set_instruction": (i32, [P, c_char_p]),
+        "vla_impact_predict": (i32, [P, P, P, c_char_p, i32, P]),
+        "vla_impact_tokens": (i32, [P, P, P, P, i32]),
+        "vla_impact_film": (i32, [P, P, P, i32]),
+        "vla_impact_predict_dev": (i32, [P, P, P, i32, P, P]),
+        "vla_impact_int8_layers": (i32, [P]),
+        "vla_impact_int8_convs": (i32, [P]),
         "vla_smolvla_load": (P, [c_char_p, c_char_p]),
         "vla_smolvla_free": (None, [P]),
         "vla_smolvla_chunk": (i32, [P]),
@@ -956,6 +976,60 @@ class ActModel(_Handle):
         out = np.empty((self.n_cams * self.feat_h * self.feat_w, self.feat_ch), np.float32)
         _call("vla_act_encode", self.h, _ptr(images), _ptr(out))
         return out
+
+
+class ImpactModel(_Handle):
+    """IMPACT end to end on the device through the reference's own entry points
+    (vla_impact_load / _set_instruction / _predict / _tokens / _film): uint8
+    frames + raw state + an instruction -> actions."""
+
+    _load, _free = "vla_impact_load", "vla_impact_free"
+
+    def __init__(self, dirpath: str):
+        super().__init__(lib().vla_impact_load(dirpath.encode()))
+        L = lib()
+        self.chunk, self.action_dim = L.vla_impact_chunk(self.h), L.vla_impact_action_dim(self.h)
+        self.state_dim, self.n_cams = L.vla_impact_state_dim(self.h), L.vla_impact_n_cams(self.h)
+        self.img_h, self.img_w = L.vla_impact_img_h(self.h), L.vla_impact_img_w(self.h)
+        self.n_text = L.vla_impact_n_text(self.h)
+        self.int8_layers, self.int8_convs = L.vla_impact_int8_layers(self.h), L.vla_impact_int8_convs(self.h)
+
+    def set_instruction(self, instruction: str):
+        _call("vla_impact_set_instruction", self.h, instruction.encode())
+
+    def predict(self, frames, state, instruction: str, unnormalize=True):
+        frames = np.ascontiguousarray(frames, np.uint8)
+        state = _f32(state)
+        _need_size("frames", frames, self.n_cams * self.img_h * self.img_w * 3)
+        _need_size("state", state, self.state_dim)
+        out = np.empty((self.chunk, self.action_dim), np.float32)
+        _call("vla_impact_predict", self.h, _ptr(frames), _ptr(state), instruction.encode(),
+              int(bool(unnormalize)), _ptr(out))
+        return out
+
+    def predict_dev(self, frames, state, out, unnormalize=True, stream=None):
+        _call("vla_impact_predict_dev", self.h, _dp(frames), _dp(state), int(bool(unnormalize)), _dp(out),
+              _stream(stream))
+
+    def tokens(self):
+        """(ids, compact ids, mask) of the current instruction, [n_text] int32 each."""
+        ids, comp, mask = (np.empty(self.n_text, np.int32) for _ in range(3))
+        n = lib().vla_impact_tokens(self.h, _ptr(ids), _ptr(comp), _ptr(mask), self.n_text)
+        if n != self.n_text:
+            raise VlaError("vla_impact_tokens", n, "no instruction set")
+        return ids, comp, mask
+
+    def film(self):
+        """(gamma, beta) of the current instruction, [film_total] float32 each."""
+        L = lib()
+        n = L.vla_impact_film(self.h, None, None, 1 << 30)  # null buffers: the count
+        if n < 0:
+            raise VlaError("vla_impact_film", n, "no instruction set")
+        gamma, beta = np.empty(n, np.float32), np.empty(n, np.float32)
+        got = L.vla_impact_film(self.h, _ptr(gamma), _ptr(beta), n)
+        if got != n:
+            raise VlaError("vla_impact_film", got, "copy failed")
+        return gamma, beta
 
 
 class SmolvlaModel(_Handle):

@@ -84,11 +84,13 @@ def _meta(path, kv):
             f.write(f"{k} {v}\n")
 
 
-def write_act(dirpath: str, cfg: dict = ACT_BASE, seed: int = synth.BASE_SEED) -> str:
+def write_act(dirpath: str, cfg: dict = ACT_BASE, seed: int = synth.BASE_SEED, tag: str = "act") -> str:
+    """<tag>.meta / <tag>.bin as ActTransformer::load reads them (act.* for
+    ACT, impact.* for IMPACT's transformer, impact_model.cpp:65)."""
     os.makedirs(dirpath, exist_ok=True)
     c = cfg
     d = c["dim"]
-    _meta(os.path.join(dirpath, "act.meta"),
+    _meta(os.path.join(dirpath, f"{tag}.meta"),
           {k: c[k] for k in ("dim", "heads", "head_dim", "ff", "n_enc", "n_dec", "chunk", "state_dim",
                              "action_dim", "n_1d", "n_text", "ln_eps")})
     a = _Arena("act", seed)
@@ -118,7 +120,7 @@ def write_act(dirpath: str, cfg: dict = ACT_BASE, seed: int = synth.BASE_SEED) -
     a.normal("dec_pos", (c["chunk"], d), 1.0)
     a.norm("dec_norm", d)
     a.linear("head", c["action_dim"], d)
-    a.write(os.path.join(dirpath, "act.bin"))
+    a.write(os.path.join(dirpath, f"{tag}.bin"))
     return dirpath
 
 
@@ -149,22 +151,15 @@ def resnet18_blocks(width: int = 64):
     return out
 
 
-def write_act_model(dirpath: str, cfg: dict = ACT_MODEL_BASE, seed: int = synth.BASE_SEED) -> str:
-    """A whole ACT checkpoint as tools/convert_act.py writes it: config.txt,
-    backbone.meta/.bin (BatchNorm folded into conv biases; weights NHWC
-    [Cout][k][k][Cin]), act.meta/.bin (the transformer over the trunk's
-    channels) and stats.bin (state, action, then per-camera image mean/std)."""
-    os.makedirs(dirpath, exist_ok=True)
-    c = cfg
-    w = c["width"]
-    blocks = resnet18_blocks(w)
-    with open(os.path.join(dirpath, "config.txt"), "w") as f:
-        f.write(f"img_h {c['img_h']}\nimg_w {c['img_w']}\nn_cams {c['n_cams']}\nnorm_eps {c['norm_eps']}\n")
-        for i in range(c["n_cams"]):
-            f.write(f"cam{i} cam_{i}\n")
-    lines = ["in_ch 3", f"stem_out {w}", "stem_k 7", "stem_stride 2", "stem_pad 3", "pool_k 3",
+def _write_resnet(dirpath: str, name: str, width: int, seed: int, film_after=()) -> list:
+    """<name>.meta / <name>.bin as ResNetBackbone::load reads them
+    (resnet_backbone.cpp:49-154): ResNet-18 with BatchNorm folded into conv
+    biases (weights NHWC [Cout][k][k][Cin]) and optional FiLM points."""
+    blocks = resnet18_blocks(width)
+    lines = ["in_ch 3", f"stem_out {width}", "stem_k 7", "stem_stride 2", "stem_pad 3", "pool_k 3",
              "pool_stride 2", "pool_pad 1"] + [f"block {a} {b} {st} {d}" for a, b, st, d in blocks]
-    with open(os.path.join(dirpath, "backbone.meta"), "w") as f:
+    lines += [f"film_after {i}" for i in film_after]
+    with open(os.path.join(dirpath, f"{name}.meta"), "w") as f:
         f.write("\n".join(lines) + "\n")
     a = _Arena("bb", seed)
 
@@ -173,14 +168,25 @@ def write_act_model(dirpath: str, cfg: dict = ACT_MODEL_BASE, seed: int = synth.
         a.parts.append(synth.uniform(f"bb.{name}.w", (cout, k, k, cin), -bound, bound, seed))
         a.parts.append(synth.normal(f"bb.{name}.b", (cout,), 0.05, seed))
 
-    conv("stem", w, 7, 3)
+    conv("stem", width, 7, 3)
     for i, (cin, cout, st, d) in enumerate(blocks):
         conv(f"b{i}.c1", cout, 3, cin)
         conv(f"b{i}.c2", cout, 3, cout)
         if d:
             conv(f"b{i}.down", cout, 1, cin)
-    a.write(os.path.join(dirpath, "backbone.bin"))
-    write_act(dirpath, dict(c, img_ch=blocks[-1][1]), seed)
+    a.write(os.path.join(dirpath, f"{name}.bin"))
+    return blocks
+
+
+def _write_act_config(dirpath: str, c: dict, extra: str = ""):
+    with open(os.path.join(dirpath, "config.txt"), "w") as f:
+        f.write(f"img_h {c['img_h']}\nimg_w {c['img_w']}\nn_cams {c['n_cams']}\nnorm_eps {c['norm_eps']}\n")
+        f.write(extra)
+        for i in range(c["n_cams"]):
+            f.write(f"cam{i} cam_{i}\n")
+
+
+def _write_act_stats(dirpath: str, c: dict, seed: int):
     sd, ad = c["state_dim"], c["action_dim"]
     parts = [synth.normal("act.stats.state_mean", (sd,), 1.0, seed),
              0.5 + synth.uniform("act.stats.state_std", (sd,), 0.0, 1.0, seed),
@@ -191,6 +197,71 @@ def write_act_model(dirpath: str, cfg: dict = ACT_MODEL_BASE, seed: int = synth.
         parts.append(np.array([0.229, 0.224, 0.225], np.float32))
     np.concatenate([np.asarray(p, np.float32).reshape(-1) for p in parts]).tofile(
         os.path.join(dirpath, "stats.bin"))
+
+
+def write_act_model(dirpath: str, cfg: dict = ACT_MODEL_BASE, seed: int = synth.BASE_SEED) -> str:
+    """A whole ACT checkpoint as tools/convert_act.py writes it: config.txt,
+    backbone.meta/.bin (BatchNorm folded into conv biases; weights NHWC
+    [Cout][k][k][Cin]), act.meta/.bin (the transformer over the trunk's
+    channels) and stats.bin (state, action, then per-camera image mean/std)."""
+    os.makedirs(dirpath, exist_ok=True)
+    c = cfg
+    _write_act_config(dirpath, c)
+    blocks = _write_resnet(dirpath, "backbone", c["width"], seed)
+    write_act(dirpath, dict(c, img_ch=blocks[-1][1]), seed)
+    _write_act_stats(dirpath, c, seed)
+    return dirpath
+
+
+# IMPACT end to end (ImpactModel, src/models/impact/impact_model.cpp): ACT's
+# trunk with FiLM points at the end of each stage and its transformer with a
+# text tail, conditioned on T5-small over a pruned vocabulary. The FiLM head is
+# drawn small and non-zero here (a converted checkpoint starts it at zero,
+# which would make the modulation the identity).
+IMPACT_T5 = dict(d_model=512, n_layers=6, n_heads=8, d_kv=64, d_ff=2048, n_buckets=32, max_dist=128, eps=1e-6)
+IMPACT_MODEL_BASE = dict(ACT_MODEL_BASE, n_text=32, film_after=(1, 3, 5, 7), t5=IMPACT_T5, unk_id=2,
+                         keep=0.75)
+
+
+def write_impact_model(dirpath: str, cfg: dict = IMPACT_MODEL_BASE, seed: int = synth.BASE_SEED) -> str:
+    """A whole IMPACT checkpoint in the files ImpactModel::load reads:
+    config.txt (with vocab_full and unk_id), vision.meta/.bin (the trunk and
+    its film_after points), impact.meta/.bin (the transformer, n_text text
+    slots), text.meta/.bin (T5-small over the pruned table, then the text
+    projection [dim, d_model] + bias, the text positions [n_text, dim] and the
+    FiLM head [2 film_total, d_model] + bias), vocab.txt (a SentencePiece
+    vocabulary), vocab_map.bin (int32 per full id: its row in the pruned table
+    or -1; a `keep` share of the ids kept, <unk> always) and stats.bin."""
+    os.makedirs(dirpath, exist_ok=True)
+    c = cfg
+    write_t5_vocab(dirpath, seed=seed)
+    with open(os.path.join(dirpath, "vocab.txt"), encoding="utf-8") as f:
+        vocab_full = sum(1 for _ in f)
+    r = np.random.default_rng(seed + 17)
+    keep = r.random(vocab_full) < c["keep"]
+    keep[c["unk_id"]] = True
+    vmap = np.full(vocab_full, -1, np.int32)
+    vmap[keep] = np.arange(int(keep.sum()), dtype=np.int32)
+    vmap.tofile(os.path.join(dirpath, "vocab_map.bin"))
+    _write_act_config(dirpath, c, f"vocab_full {vocab_full}\nunk_id {c['unk_id']}\n")
+    blocks = _write_resnet(dirpath, "vision", c["width"], seed, c["film_after"])
+    write_act(dirpath, dict(c, img_ch=blocks[-1][1]), seed, tag="impact")
+    _write_act_stats(dirpath, c, seed)
+    t5 = dict(c["t5"], vocab=int(keep.sum()))
+    write_t5(dirpath, t5, stem="text", seed=seed)
+    enc = os.path.getsize(os.path.join(dirpath, "text.bin")) // 4
+    D, P, T = t5["d_model"], c["dim"], c["n_text"]
+    F = sum(blocks[i][1] for i in c["film_after"])
+    a = _Arena("text_heads", seed)
+    a.linear("proj", P, D)
+    a.normal("text_pos", (T, P), 0.5)
+    a.parts.append(synth.normal("text_heads.film.w", (2 * F, D), 0.05 / math.sqrt(D), seed))
+    a.parts.append(synth.normal("text_heads.film.b", (2 * F,), 0.02, seed))
+    with open(os.path.join(dirpath, "text.bin"), "ab") as f:
+        for part in a.parts:
+            f.write(np.ascontiguousarray(part, dtype=np.float32).tobytes())
+    with open(os.path.join(dirpath, "text.meta"), "a") as f:
+        f.write(f"proj_dim {P}\nn_text {T}\nfilm_total {F}\nencoder_floats {enc}\n")
     return dirpath
 
 

@@ -139,6 +139,26 @@ __global__ __launch_bounds__(256) void add_relu_kernel(float* __restrict__ o, co
     store_block_absmax(mx, part);
 }
 
+// IMPACT's FiLM point after a basic block (resnet_backbone.cpp:276-290):
+// v = o + idn, o = (1 + gamma[c]) * relu(v) + beta[c] over NHWC maps of C
+// channels; the multiply-add is one fused operation, as the reference's
+// -ffp-contract=fast build emits it. The block maxima are of |o| (the
+// modulated map can go negative).
+__global__ __launch_bounds__(256) void add_relu_film_kernel(float* __restrict__ o, const float* __restrict__ idn,
+                                                           int64_t n, int C, const float* __restrict__ gamma,
+                                                           const float* __restrict__ beta, float* __restrict__ part) {
+    float mx = 0.0f;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const int c = (int)(i % C);
+        const float v = o[i] + idn[i];
+        const float r = v > 0.0f ? v : 0.0f;
+        const float y = fmaf(1.0f + gamma[c], r, beta[c]);
+        o[i] = y;
+        mx = fmaxf(mx, fabsf(y));
+    }
+    store_block_absmax(mx, part);
+}
+
 // relu in place as the reference's relu (eltwise.cpp:209-215): x < 0 -> 0
 __global__ __launch_bounds__(256) void relu_kernel(float* __restrict__ x, int64_t n, float* __restrict__ part) {
     float mx = 0.0f;
@@ -214,6 +234,15 @@ int launch_maxpool_relu(float* out, const float* x, int H, int Wd, int C, int k,
 int launch_add_relu(float* o, const float* idn, int64_t n, hipStream_t st, float* part) {
     const int g = part_grid(n, part);
     add_relu_kernel<<<g, 256, 0, st>>>(o, idn, n, part);
+    VLA_LAUNCH_CHECK();
+    return g;
+}
+
+int launch_add_relu_film(float* o, const float* idn, int64_t n, int C, const float* gamma, const float* beta,
+                         hipStream_t st, float* part) {
+    VLA_REQUIRE(n > 0 && C > 0 && n % C == 0 && o && idn && gamma && beta, "add_relu_film: bad arguments");
+    const int g = part_grid(n, part);
+    add_relu_film_kernel<<<g, 256, 0, st>>>(o, idn, n, C, gamma, beta, part);
     VLA_LAUNCH_CHECK();
     return g;
 }

@@ -10,6 +10,8 @@
 #include "linear.h"
 #include "runtime.h"
 
+#include <cstdlib>
+
 using namespace vla::hip;
 
 namespace {
@@ -244,6 +246,28 @@ VLA_API int32_t vla_dense_linear_i8(float* out, const float* x, const int8_t* Wq
     });
 }
 
+static RowQArgs rowop_args(int32_t op, const float* x, int32_t ldx, const float* u, int32_t ldu,
+                           const float* w, float eps, int32_t seq, int32_t K);
+
+// Up to 16 rows of the op API take the fused row-op GEMM (the quantization
+// inside the GEMM) where it applies. Graph replays on MI355X, quantize + GEMM
+// -> fused: 1x512x3200 5.22 -> 3.36 us, 1x960x2560 5.70 -> 4.02, 1x768x3072
+// 5.60 -> 3.85, 16x512x3200 5.48 -> 3.92, 16x960x2560 5.99 -> 4.83,
+// 16x768x3072 5.88 -> 4.52; from 50 rows on it was slower (50x960x2560 7.00
+// -> 8.56, 100x960x2560 8.3 -> 14.6). VLA_HIP_OP_FUSE=0 keeps the two
+// launches (A/B runs; outputs and scratch bytes are the same either way).
+static bool op_fuses(const float* x, int ldx, const int8_t* Wq, int ldw, const float* out, int ldo,
+                     const int8_t* xq, int ldq, const float* ascale, int seq, int N, int K) {
+    const char* e = std::getenv("VLA_HIP_OP_FUSE");
+    if (e && std::atoi(e) == 0) return false;
+    if (seq < 1 || seq > 16 || !rowop_gemm_fits(0, seq, K)) return false;
+    if (ldx < K || ldx % 4 || !aligned(x, 16) || ldw < kpad4(K) || ldw % 16 || !aligned(Wq, 16)) return false;
+    if (ldq < kpad4(K) || ldq % 4 || !aligned(xq, 4) || !ascale || ldo < N) return false;
+    const uintptr_t o0 = (uintptr_t)out, o1 = o0 + ((size_t)(seq - 1) * ldo + N) * sizeof(float);
+    const uintptr_t x0 = (uintptr_t)x, x1 = x0 + ((size_t)(seq - 1) * ldx + K) * sizeof(float);
+    return o1 <= x0 || x1 <= o0;  // out apart from the rows read (else the two launches)
+}
+
 VLA_API int32_t vla_dense_linear_i8_dev(float* out, int32_t ldo, const float* x, int32_t ldx,
                                         const int8_t* Wq, int32_t ldw, const float* wscale,
                                         const float* bias, int32_t seq, int32_t N, int32_t K,
@@ -257,6 +281,29 @@ VLA_API int32_t vla_dense_linear_i8_dev(float* out, int32_t ldo, const float* x,
         hipStream_t st = as_stream(stream);
         // the reference's contract: xq_scratch holds seq x i8_kpad(K) bytes
         // (here with row stride ldq), ascale_scratch seq floats
+        if (op_fuses(x, ldx, Wq, ldw, out, ldo, xq_scratch, ldq, ascale_scratch, seq, N, K)) {
+            // a few rows: quantized inside the GEMM (every block repeats the
+            // cheap row work instead of waiting for a separate launch), the
+            // scratch filled by the same kernel with the same bytes
+            RowQArgs r = rowop_args(0, x, ldx, nullptr, 0, nullptr, 0.0f, seq, K);
+            r.q = xq_scratch;
+            r.ldq = ldq;
+            r.qs = ascale_scratch;
+            GemmArgs a{};
+            a.B = Wq;
+            a.ldb = ldw;
+            a.wscale = wscale;
+            a.bias = bias;
+            a.out = out;
+            a.ldo = ldo;
+            a.M = seq;
+            a.N = N;
+            a.K = K;
+            a.act = act;
+            a.accumulate = accumulate;
+            launch_gemm_i8_rowop(r, a, st);
+            return;
+        }
         launch_quantize_rows(x, ldx, xq_scratch, ldq, ascale_scratch, seq, K, st);
         GemmArgs a{};
         a.A = xq_scratch;

@@ -462,6 +462,91 @@ VLA_API int32_t vla_act_encode(void* h, const uint8_t* images, float* feats) {
     });
 }
 
+// --------------------------------------------------- IMPACT (model level) --
+// The reference's IMPACT entry points (include/vla_simd.h:206-243,
+// src/models/impact/impact_capi.cpp), same names, signatures and status codes.
+
+namespace {
+ImpactModel* impact_model(void* h) { return static_cast<ImpactModel*>(h); }
+}  // namespace
+
+VLA_API void* vla_impact_load(const char* model_dir) {
+    ImpactModel* m = nullptr;
+    const int32_t rc = guarded("vla_impact_load", [&] {
+        VLA_REQUIRE(model_dir, "null model directory");
+        m = new ImpactModel(model_dir);
+    });
+    return rc == 0 ? m : nullptr;
+}
+VLA_API void vla_impact_free(void* h) { delete impact_model(h); }
+VLA_API int32_t vla_impact_chunk(void* h) { return h ? impact_model(h)->chunk() : 0; }
+VLA_API int32_t vla_impact_action_dim(void* h) { return h ? impact_model(h)->action_dim() : 0; }
+VLA_API int32_t vla_impact_state_dim(void* h) { return h ? impact_model(h)->state_dim() : 0; }
+VLA_API int32_t vla_impact_n_cams(void* h) { return h ? impact_model(h)->n_cams() : 0; }
+VLA_API int32_t vla_impact_img_h(void* h) { return h ? impact_model(h)->img_h() : 0; }
+VLA_API int32_t vla_impact_img_w(void* h) { return h ? impact_model(h)->img_w() : 0; }
+VLA_API int32_t vla_impact_n_text(void* h) { return h ? impact_model(h)->n_text() : 0; }
+VLA_API int32_t vla_impact_int8_layers(void* h) { return h ? impact_model(h)->int8_layers() : 0; }
+VLA_API int32_t vla_impact_int8_convs(void* h) { return h ? impact_model(h)->int8_convs() : 0; }
+
+VLA_API int32_t vla_impact_set_instruction(void* h, const char* instruction) {
+    if (!h || !instruction) return VLA_ERR_ARG;
+    const int32_t rc = guarded("vla_impact_set_instruction", [&] { impact_model(h)->set_instruction(instruction); });
+    return rc == 0 ? VLA_OK : VLA_ERR_EXCEPTION;  // impact_capi.cpp:46-51: anything thrown is an exception
+}
+
+VLA_API int32_t vla_impact_predict(void* h, const uint8_t* frames, const float* state, const char* instruction,
+                                   int32_t unnormalize, float* actions) {
+    if (!h || !frames || !state || !instruction || !actions) return VLA_ERR_ARG;
+    const int32_t rc = guarded("vla_impact_predict", [&] {
+        ImpactModel& m = *impact_model(h);
+        m.set_instruction(instruction);
+        HostCall hc;
+        const size_t nimg = (size_t)m.n_cams() * m.img_h() * m.img_w() * 3;
+        const uint8_t* di = hc.up(frames, nimg);
+        const float* ds = hc.up(state, (size_t)m.state_dim());
+        const size_t na = (size_t)m.chunk() * m.action_dim();
+        float* da = hc.out(na);
+        m.predict_dev(di, ds, unnormalize != 0, da, hc.st);
+        hc.down(actions, da, na);
+    });
+    return rc == 0 ? VLA_OK : VLA_ERR_EXCEPTION;  // impact_capi.cpp:53-68
+}
+
+VLA_API int32_t vla_impact_predict_dev(void* h, const uint8_t* frames, const float* state, int32_t unnormalize,
+                                       float* actions, void* stream) {
+    if (!h || !frames || !state || !actions) return VLA_ERR_ARG;
+    return guarded("vla_impact_predict_dev", [&] {
+        impact_model(h)->predict_dev(frames, state, unnormalize != 0, actions, as_stream(stream));
+    });
+}
+
+// impact_capi.cpp:70-87
+VLA_API int32_t vla_impact_tokens(void* h, int32_t* ids, int32_t* compact, int32_t* mask, int32_t max_elems) {
+    if (!h) return VLA_ERR_ARG;
+    const ImpactModel& m = *impact_model(h);
+    const int n = m.n_text();
+    if (max_elems < n || m.token_ids().size() != (size_t)n) return VLA_ERR_ARG;
+    for (int i = 0; i < n; i++) {
+        if (ids) ids[i] = m.token_ids()[i];
+        if (compact) compact[i] = m.compact_ids()[i];
+        if (mask) mask[i] = m.token_mask()[i];
+    }
+    return n;
+}
+
+// impact_capi.cpp:89-101
+VLA_API int32_t vla_impact_film(void* h, float* gamma, float* beta, int32_t max_elems) {
+    if (!h) return VLA_ERR_ARG;
+    const ImpactModel& m = *impact_model(h);
+    const int n = (int)m.film_gamma().size();
+    if (n == 0) return m.token_ids().empty() ? VLA_ERR_ARG : 0;
+    if (max_elems < n) return VLA_ERR_ARG;
+    if (gamma) std::memcpy(gamma, m.film_gamma().data(), sizeof(float) * (size_t)n);
+    if (beta) std::memcpy(beta, m.film_beta().data(), sizeof(float) * (size_t)n);
+    return n;
+}
+
 // -------------------------------------------------- SmolVLA (model level) --
 // The reference's SmolVLA entry points (include/vla_simd.h:83-124,
 // src/models/smolvla/smolvla_capi.cpp), same names and signatures.

@@ -225,6 +225,14 @@ int launch_maxpool_relu(float* out, const float* x, int H, int Wd, int C, int k,
                         int Wout, hipStream_t st, float* part = nullptr);
 // o = o + idn > 0 ? o + idn : 0
 int launch_add_relu(float* o, const float* idn, int64_t n, hipStream_t st, float* part = nullptr);
+// o = fma(1 + gamma[c], relu(o + idn), beta[c]) over NHWC maps of C channels
+// (IMPACT's FiLM points); part as launch_add_relu, of |o|
+int launch_add_relu_film(float* o, const float* idn, int64_t n, int C, const float* gamma, const float* beta,
+                         hipStream_t st, float* part = nullptr);
+// out[i] = (sum over the rows t with mask[t] != 0 of x[t][i], in row order) *
+// (1 / live), i < D; zeros when no row is live (t5_text.cpp:115-128)
+void launch_masked_row_mean(float* out, const float* x, int ldx, const int32_t* mask, int rows, int D,
+                            hipStream_t st);
 // x < 0 -> 0
 int launch_relu_inplace(float* x, int64_t n, hipStream_t st, float* part = nullptr);
 // [rows, cols] per column: mode 0 (x - a) / (b + eps), mode 1 fma(x, b, a)

@@ -1001,7 +1001,10 @@ constexpr int kRowopMaxLds = 160 * 1024;
 // its k-steps of the panel by its weight chunks; the partial tiles reuse the
 // panel's LDS and are summed as in gemm_i8_skinny. Panel rows past M and
 // panel bytes past K are never written: the former only reach discarded
-// outputs, the latter meet weight bytes masked to zero.
+// outputs, the latter meet weight bytes masked to zero. With r.q set, the
+// first column block of each row group also writes its quantized rows
+// row-major (stride r.ldq, bytes [K, r.ldq) zero) and their scales to r.qs:
+// the caller-owned scratch of the op API, filled as the quantizer fills it.
 template <int OP, int NV, int FM>
 __global__ __launch_bounds__(1024) void gemm_i8_rowop(RowQArgs r, GemmArgs a) {
     constexpr int WAVES = 16, NT = WAVES * 64, MP = 16 * FM;
@@ -1091,6 +1094,16 @@ __global__ __launch_bounds__(1024) void gemm_i8_rowop(RowQArgs r, GemmArgs a) {
                 for (int i = 0; i < NV; i++) {
                     const int k = 4 * lane + 256 * i;
                     if (k < K) *reinterpret_cast<uint32_t*>(qr + (k >> 6) * (MP * 64) + (k & 63)) = q8x4(y[jj][i], inv);
+                }
+                if (r.q && blockIdx.x == 0) {  // block-uniform
+                    int8_t* gq = r.q + (size_t)(m0 + row[jj]) * r.ldq;
+#pragma unroll
+                    for (int i = 0; i < NV; i++) {
+                        const int k = 4 * lane + 256 * i;
+                        if (k < K) *reinterpret_cast<uint32_t*>(gq + k) = q8x4(y[jj][i], inv);
+                    }
+                    for (int k = K + 4 * lane; k < r.ldq; k += 256) *reinterpret_cast<uint32_t*>(gq + k) = 0u;
+                    if (lane == 0) r.qs[m0 + row[jj]] = s;
                 }
             }
         });
@@ -1718,6 +1731,8 @@ void launch_gemm_i8_rowop(const RowQArgs& r, const GemmArgs& a, hipStream_t st) 
     VLA_REQUIRE(rowop_gemm_fits(r.op, a.M, a.K),
                 "gemm_i8_rowop: need 1 <= M <= 128, K a multiple of 4 in [4, 2048] and the panel within LDS");
     VLA_REQUIRE(!r.out && !r.add && !r.out2 && !r.q2, "gemm_i8_rowop: the fused row op has no fp32 or second output");
+    VLA_REQUIRE(!r.q || (!r.q_panel && r.qs && r.ldq >= kpad4(a.K) && r.ldq % 4 == 0 && aligned(r.q, 4)),
+                "gemm_i8_rowop: the quantized-row copy is row-major, 4-byte aligned, ldq >= i8_kpad(K), with scales");
     VLA_REQUIRE(r.x && r.ldx >= a.K && r.ldx % 4 == 0 && aligned(r.x, 16),
                 "gemm_i8_rowop: x rows must be 16-byte aligned");
     VLA_REQUIRE(r.op == 0 || r.op == 3 || (r.w && aligned(r.w, 16) && (!r.b || aligned(r.b, 16))),

@@ -58,29 +58,30 @@ void sinusoid_pos_2d(int fh, int fw, int dim, float* out) {
 
 }  // namespace
 
-ActTf::ActTf(const std::string& dir, int img_ch, int int8_mask, bool int8_state) {
+ActTf::ActTf(const std::string& dir, int img_ch, int int8_mask, bool int8_state, const std::string& tag) {
     const CkptFiles files(dir);  // a converted directory or a vla.simd GGUF
+    const std::string mf = tag + ".meta", bf = tag + ".bin";
     // act_transformer.cpp:31-52: each known key's value is read as `ss >> int`
     // (ln_eps as float) and the rest of its line must be blank; unknown keys
     // are skipped
     int& n_text = n_text_;
-    for (const auto& kv : files.meta_lines("act.meta")) {
+    for (const auto& kv : files.meta_lines(mf)) {
         const std::string& k = kv.first;
         int* dst = k == "dim" ? &d_ : k == "heads" ? &heads_ : k == "head_dim" ? &hd_ : k == "ff" ? &ff_
                  : k == "n_enc" ? &n_enc_ : k == "n_dec" ? &n_dec_ : k == "chunk" ? &chunk_
                  : k == "state_dim" ? &state_dim_ : k == "action_dim" ? &action_dim_ : k == "n_1d" ? &n_1d_
                  : k == "n_text" ? &n_text : nullptr;
-        if (dst) *dst = meta_value_int("act.meta", k, kv.second);
-        else if (k == "ln_eps") eps_ = meta_value_float("act.meta", k, kv.second);
+        if (dst) *dst = meta_value_int(mf, k, kv.second);
+        else if (k == "ln_eps") eps_ = meta_value_float(mf, k, kv.second);
     }
     img_ch_ = img_ch;
     VLA_REQUIRE(d_ > 0 && d_ % 4 == 0 && heads_ > 0 && hd_ > 0 && heads_ * hd_ == d_ && ff_ > 0 &&
                     chunk_ > 0 && state_dim_ > 0 && action_dim_ > 0 && img_ch > 0 && n_enc_ >= 1 &&
                     n_dec_ >= 1 && n_1d_ == 2 && n_text >= 0 && std::isfinite(eps_) && eps_ > 0,
-                "act.meta: invalid configuration (act_transformer.cpp:56-62 bounds)");
+                mf + ": invalid configuration (act_transformer.cpp:56-62 bounds)");
 
-    const std::vector<char> raw = files.bytes("act.bin");
-    VLA_REQUIRE(raw.size() % 4 == 0, "act.bin: size is not a whole number of floats");
+    const std::vector<char> raw = files.bytes(bf);
+    VLA_REQUIRE(raw.size() % 4 == 0, bf + ": size is not a whole number of floats");
     Cursor take{reinterpret_cast<const float*>(raw.data()), raw.size() / 4};
     const int d = d_;
     auto lin = [&](DLinear& L, int N, int K, bool i8) {
@@ -149,7 +150,7 @@ ActTf::ActTf(const std::string& dir, int img_ch, int int8_mask, bool int8_state)
     dec_ns_ = vec(d);
     dec_nb_ = vec(d);
     lin(head_, action_dim_, d, false);  // Role::Generic, fp32 (:142-145)
-    VLA_REQUIRE(take.off == take.n, "act.bin: size does not match act.meta");
+    VLA_REQUIRE(take.off == take.n, bf + ": size does not match " + mf);
     VLA_HIP_CHECK(hipStreamCreateWithFlags(&own_, hipStreamNonBlocking));
 }
 

@@ -68,7 +68,7 @@ struct Floats {
 
 }  // namespace
 
-ActModel::ActModel(const std::string& dir) {
+ActModel::ActModel(const std::string& dir, const ActSpec& spec) {
     const CkptFiles files(dir);
 
     // config.txt (act_model.cpp:24-45)
@@ -86,16 +86,18 @@ ActModel::ActModel(const std::string& dir) {
     VLA_REQUIRE(shape_fits({img_h_, img_w_, n_cams_, 3}) && std::isfinite(norm_eps_) && norm_eps_ > 0,
                 "config.txt: invalid image shape or norm_eps (act_model.cpp:46-47 bounds)");
 
-    // backbone.meta (resnet_backbone.cpp:49-96)
+    // <backbone>.meta (resnet_backbone.cpp:49-96): backbone.meta for ACT,
+    // vision.meta for IMPACT
+    const std::string bmeta = std::string(spec.backbone) + ".meta", bbin = std::string(spec.backbone) + ".bin";
     int in_ch = 3, stem_out = 64, stem_k = 7, stem_stride = 2, stem_pad = 3, gs = 0;
     struct BlockMeta {
         int cin, cout, stride, has_down;
     };
     std::vector<BlockMeta> bm;
     std::vector<int> film_after;
-    for (const auto& kv : files.meta_lines("backbone.meta")) {
+    for (const auto& kv : files.meta_lines(bmeta)) {
         const std::string& k = kv.first;
-        const char* f = "backbone.meta";
+        const char* f = bmeta.c_str();
         if (k == "in_ch") read_values(f, k, kv.second, in_ch);
         else if (k == "stem_out") read_values(f, k, kv.second, stem_out);
         else if (k == "stem_k") read_values(f, k, kv.second, stem_k);
@@ -119,17 +121,17 @@ ActModel::ActModel(const std::string& dir) {
     VLA_REQUIRE(in_ch == 3 && shape_fits({stem_out, stem_k, stem_k, in_ch}) && stem_stride >= 1 && stem_pad >= 0 &&
                     stem_pad <= INT_MAX / 2 && pool_k_ >= 1 && pool_stride_ >= 1 && pool_pad_ >= 0 &&
                     pool_pad_ <= INT_MAX / 2 && gs >= 0,
-                "backbone.meta: invalid stem or pool (resnet_backbone.cpp:87-90 bounds)");
-    VLA_REQUIRE(gs == 0, "backbone.meta: group-norm trunks (gn_group_size > 0) are not supported on the device");
+                bmeta + ": invalid stem or pool (resnet_backbone.cpp:87-90 bounds)");
+    VLA_REQUIRE(gs == 0, bmeta + ": group-norm trunks (gn_group_size > 0) are not supported on the device");
     for (const BlockMeta& b : bm)
         VLA_REQUIRE(shape_fits({b.cout, bk, bk, b.cin}) && shape_fits({b.cout, bk, bk, b.cout}) && b.stride >= 1 &&
                         (b.has_down == 0 || b.has_down == 1),
-                    "backbone.meta: invalid block (resnet_backbone.cpp:91-94 bounds)");
+                    bmeta + ": invalid block (resnet_backbone.cpp:91-94 bounds)");
 
     // backbone.bin: stem, then per block conv1, conv2, down (:96-154). BatchNorm
     // is folded, so every conv carries a bias.
-    const std::vector<char> raw = files.bytes("backbone.bin");
-    VLA_REQUIRE(raw.size() % 4 == 0, "backbone.bin: size is not a whole number of floats");
+    const std::vector<char> raw = files.bytes(bbin);
+    VLA_REQUIRE(raw.size() % 4 == 0, bbin + ": size is not a whole number of floats");
     Floats take{reinterpret_cast<const float*>(raw.data()), raw.size() / 4};
     // host copies of the fp32 weights for the int8 quantizer
     struct HostConv {
@@ -141,8 +143,8 @@ ActModel::ActModel(const std::string& dir) {
         c.cin = cin;
         c.stride = stride;
         c.pad = pad;
-        const float* W = take.take((size_t)cout * k * k * cin, "backbone.bin");
-        const float* b = take.take(cout, "backbone.bin");
+        const float* W = take.take((size_t)cout * k * k * cin, bbin.c_str());
+        const float* b = take.take(cout, bbin.c_str());
         c.W = A_.upload(W, (size_t)cout * k * k * cin);
         c.b = A_.upload(b, cout);
         return HostConv{W, b};
@@ -155,21 +157,31 @@ ActModel::ActModel(const std::string& dir) {
         const BlockMeta& m = bm[i];
         const int prev = i ? bm[i - 1].cout : stem_out;
         VLA_REQUIRE(m.cin == prev && m.cout >= 1 && m.stride >= 1,
-                    "backbone.meta: a block's input channels differ from the previous output");
+                    bmeta + ": a block's input channels differ from the previous output");
         VLA_REQUIRE(m.has_down || (m.stride == 1 && m.cin == m.cout),
-                    "backbone.meta: a block without downsample changes shape");
+                    bmeta + ": a block without downsample changes shape");
         blk.has_down = m.has_down != 0;
         host.push_back(load_conv(blk.c1, m.cout, bk, m.cin, m.stride, 1));
         host.push_back(load_conv(blk.c2, m.cout, bk, m.cout, 1, 1));
         if (blk.has_down) host.push_back(load_conv(blk.down, m.cout, 1, m.cin, m.stride, 0));
     }
-    VLA_REQUIRE(take.off == take.n, "backbone.bin: size does not match backbone.meta");
+    VLA_REQUIRE(take.off == take.n, bbin + ": size does not match " + bmeta);
     int prev_idx = -1;
     for (int idx : film_after) {
         VLA_REQUIRE(idx >= 0 && idx < (int)blocks_.size() && idx > prev_idx,
-                    "backbone.meta: film_after must name blocks in ascending order");
+                    bmeta + ": film_after must name blocks in ascending order");
         prev_idx = idx;
     }
+    // FiLM points (film_total, resnet_backbone.cpp:190-195): block film_after[i]
+    // reads gamma / beta at the sum of the earlier points' channels. ACT runs
+    // its trunk unmodulated whatever the meta lists (act_model.cpp passes no
+    // gamma / beta).
+    film_off_.assign(blocks_.size(), -1);
+    if (spec.film)
+        for (int idx : film_after) {
+            film_off_[idx] = film_total_;
+            film_total_ += blocks_[idx].c1.cout;
+        }
 
     // feature grid (ResNetBackbone::feat_size, :197-209)
     int h = conv_out(img_h_, stem_k, stem_stride, stem_pad), w = conv_out(img_w_, stem_k, stem_stride, stem_pad);
@@ -204,10 +216,10 @@ ActModel::ActModel(const std::string& dir) {
     // ACT_INT8 (act_model.cpp:57-64): bit 32 quantizes the convs of stages
     // [ACT_I8_CONV_FROM, ACT_I8_CONV_TO); Conv2d::init_int8 keeps a conv fp32
     // unless Cout % 16 == 0 and K is within the int8 bound (nn/conv.cpp:41-43)
-    const int i8 = int_env("ACT_INT8", 0);
+    const int i8 = int_env(spec.int8_env, 0);
     if (i8 & 32) {
-        const int from = int_env("ACT_I8_CONV_FROM", 0);
-        int to = int_env("ACT_I8_CONV_TO", -1);
+        const int from = int_env(spec.conv_from_env, 0);
+        int to = int_env(spec.conv_to_env, -1);
         if (to < 0) to = (int)blocks_.size() + 1;
         auto want = [&](int stage) { return stage >= from && stage < to; };
         auto quantize = [&](Conv& c, const HostConv& hc) {
@@ -228,7 +240,7 @@ ActModel::ActModel(const std::string& dir) {
             hi += blk.has_down ? 3 : 2;
         }
     }
-    tf_ = std::make_unique<ActTf>(dir, feat_ch_, i8);
+    tf_ = std::make_unique<ActTf>(dir, feat_ch_, i8, spec.int8_state, spec.tf);
 
     // stats.bin (act_model.cpp:66-101)
     const int sd = tf_->state_dim(), ad = tf_->action_dim();
@@ -274,6 +286,10 @@ ActModel::ActModel(const std::string& dir) {
     feats_ = A_.alloc<float>((size_t)n_cams_ * fh_ * fw_ * feat_ch_);
     state_n_ = A_.alloc<float>(sd);
     act_n_ = A_.alloc<float>((size_t)tf_->chunk() * ad);
+    if (film_total_) {
+        film_g_ = A_.alloc<float>(film_total_);
+        film_b_ = A_.alloc<float>(film_total_);
+    }
     if (n_int8_convs_) {
         size_t need = 0;
         auto ws = [&](const Conv& c, int H, int W) {
@@ -352,7 +368,8 @@ int ActModel::conv(const Conv& c, const float* x, int H, int W, float* out, bool
 }
 
 // ActModel::encode_view for every camera (act_model.cpp:106-124) and
-// ResNetBackbone::forward (resnet_backbone.cpp:211-317) without FiLM
+// ResNetBackbone::forward (resnet_backbone.cpp:211-317); FiLM at the points
+// film_off_ names (IMPACT)
 //
 // With int8 convolutions each conv2d_i8 input comes with the block maxima of
 // |x| that its producer wrote (the normalization, the max pool, the relu
@@ -374,7 +391,8 @@ void ActModel::run_backbone(hipStream_t st) {
         int nB = launch_maxpool_relu(B, a_, h, w, stem_.cout, pool_k_, pool_stride_, pool_pad_, ph, pw, st, pB);
         h = ph;
         w = pw;
-        for (const Block& blk : blocks_) {
+        for (size_t bi = 0; bi < blocks_.size(); bi++) {
+            const Block& blk = blocks_[bi];
             const int oh = conv_out(h, blk.c1.k, blk.c1.stride, blk.c1.pad);
             const int ow = conv_out(w, blk.c1.k, blk.c1.stride, blk.c1.pad);
             const float* idn = B;
@@ -384,7 +402,10 @@ void ActModel::run_backbone(hipStream_t st) {
             }
             const int nA = conv(blk.c1, B, h, w, a_, true, st, pB, nB, part_a_);
             conv(blk.c2, a_, oh, ow, C, false, st, part_a_, nA);
-            nB = launch_add_relu(C, idn, (int64_t)oh * ow * blk.c1.cout, st, pC);
+            const int64_t n = (int64_t)oh * ow * blk.c1.cout;
+            const int fo = film_off_[bi];
+            nB = fo >= 0 ? launch_add_relu_film(C, idn, n, blk.c1.cout, film_g_ + fo, film_b_ + fo, st, pC)
+                         : launch_add_relu(C, idn, n, st, pC);
             std::swap(B, C);
             std::swap(pB, pC);
             h = oh;
@@ -402,16 +423,18 @@ void ActModel::encode_dev(const uint8_t* images, float* feats, hipStream_t calle
     copy_f32(feats, feats_, (int64_t)n_cams_ * fh_ * fw_ * feat_ch_, caller);
 }
 
-// ActModel::predict (act_model.cpp:126-164)
-void ActModel::predict_dev(const uint8_t* images, const float* state, bool unnormalize, float* actions,
-                           hipStream_t caller) {
+// ActModel::predict (act_model.cpp:126-164), ImpactModel::predict
+// (impact_model.cpp:201-244) with the text tail
+void ActModel::predict_text_dev(const uint8_t* images, const float* state, const float* text, const float* text_pos,
+                                int n_text_real, bool unnormalize, float* actions, hipStream_t caller) {
     VLA_REQUIRE(images && state && actions, "act: null buffer");
     VLA_HIP_CHECK(hipMemcpyAsync(img_in_, images, (size_t)n_cams_ * img_h_ * img_w_ * 3, hipMemcpyDeviceToDevice,
                                  caller));
     replay_.run(1, own_, caller, [this](hipStream_t st) { run_backbone(st); });
     launch_col_affine(state_n_, state, 1, tf_->state_dim(), state_mean_, state_std_, norm_eps_, 0, caller);
     const int C = tf_->chunk(), ad = tf_->action_dim();
-    tf_->forward_dev(feats_, n_cams_, fh_, fw_, state_n_, unnormalize ? act_n_ : actions, caller);
+    tf_->forward_text_dev(feats_, n_cams_, fh_, fw_, state_n_, text, text_pos, n_text_real,
+                          unnormalize ? act_n_ : actions, caller);
     if (unnormalize) launch_col_affine(actions, act_n_, C, ad, action_mean_, action_std_, 0.0f, 1, caller);
 }
 

@@ -104,7 +104,7 @@ int rel_bucket(int rp, int num_buckets, int max_dist) {
 
 // ------------------------------------------------------------------- T5 --
 
-T5Enc::T5Enc(const CkptFiles& files, const std::string& stem) {
+T5Enc::T5Enc(const CkptFiles& files, const std::string& stem, std::vector<float>* tail) {
     const std::string mf = stem + ".meta";
     for (const auto& kv : kv_pairs(files, mf)) {
         const std::string& k = kv.first;
@@ -139,7 +139,10 @@ T5Enc::T5Enc(const CkptFiles& files, const std::string& stem) {
         L.wo2 = A_.upload(a.take((size_t)D * FF), (size_t)D * FF);
     }
     final_ = A_.upload(a.take(D), D);
-    a.done();
+    if (tail)  // T5Encoder::load's enc_end: what follows belongs to the caller
+        tail->assign(a.d.begin() + (std::ptrdiff_t)a.off, a.d.end());
+    else
+        a.done();
 }
 
 // T5Encoder::encode (t5_encoder.cpp:81-134)

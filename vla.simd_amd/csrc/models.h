@@ -32,7 +32,9 @@ namespace hip {
 // after the camera positions (build_tokens, :212-250).
 class ActTf {
 public:
-    ActTf(const std::string& dir, int img_ch, int int8_mask, bool int8_state = false);
+    // tag names the files: <tag>.meta / <tag>.bin ("act", IMPACT's "impact")
+    ActTf(const std::string& dir, int img_ch, int int8_mask, bool int8_state = false,
+          const std::string& tag = "act");
     ~ActTf();
     int chunk() const { return chunk_; }
     int action_dim() const { return action_dim_; }
@@ -88,6 +90,20 @@ private:
     GraphReplay replay_;
 };
 
+// What tells an ACT-shaped model's files and knobs apart: ACT itself, or
+// IMPACT (impact_model.cpp:50-66: the trunk in vision.meta/.bin, the
+// transformer in impact.meta/.bin with int8_state, IMPACT_INT8 and its conv
+// range, FiLM points in the trunk).
+struct ActSpec {
+    const char* backbone = "backbone";
+    const char* tf = "act";
+    const char* int8_env = "ACT_INT8";
+    const char* conv_from_env = "ACT_I8_CONV_FROM";
+    const char* conv_to_env = "ACT_I8_CONV_TO";
+    bool int8_state = false;
+    bool film = false;  // the trunk applies (1 + gamma) relu(v) + beta at film_after
+};
+
 // ------------------------------------------------------------ ACT policy --
 // src/models/act/act_model.{h,cpp} + resnet_backbone.{h,cpp}: uint8 camera
 // frames -> per-camera normalization -> ResNet-18 trunk (BatchNorm folded into
@@ -97,10 +113,12 @@ private:
 // GGUF carrying them). ACT_INT8 is read at load as act_model.cpp:57-64 reads
 // it: bits 1..16 pick the transformer's int8 layers, bit 32 routes the
 // backbone convs of stages [ACT_I8_CONV_FROM, ACT_I8_CONV_TO) through
-// conv2d_i8 (stage 0 the stem, 1.. the blocks).
+// conv2d_i8 (stage 0 the stem, 1.. the blocks). With an IMPACT spec the
+// FiLM points of the trunk modulate the block outputs (resnet_backbone.cpp:
+// 259-290) and the transformer takes IMPACT's text tail.
 class ActModel {
 public:
-    explicit ActModel(const std::string& dir);
+    explicit ActModel(const std::string& dir, const ActSpec& spec = ActSpec{});
     ~ActModel();
     int chunk() const { return tf_->chunk(); }
     int action_dim() const { return tf_->action_dim(); }
@@ -117,7 +135,20 @@ public:
     // device pointers: images [n_cams, img_h, img_w, 3] uint8, state
     // [state_dim] raw, actions [chunk, action_dim]
     void predict_dev(const uint8_t* images, const float* state, bool unnormalize, float* actions,
-                     hipStream_t caller);
+                     hipStream_t caller) {
+        predict_text_dev(images, state, nullptr, nullptr, 0, unnormalize, actions, caller);
+    }
+    // with IMPACT's text tail (device text / text_pos [n_text, dim], of which
+    // n_text_real rows enter the sequence; act_transformer.cpp:343-360)
+    void predict_text_dev(const uint8_t* images, const float* state, const float* text, const float* text_pos,
+                          int n_text_real, bool unnormalize, float* actions, hipStream_t caller);
+    // FiLM (spec.film): the trunk's gamma / beta device buffers [film_total],
+    // the points concatenated in film_after order, which the caller fills
+    int film_total() const { return film_total_; }
+    float* film_gamma() const { return film_g_; }
+    float* film_beta() const { return film_b_; }
+    int tf_dim() const { return tf_->dim(); }
+    int tf_n_text() const { return tf_->n_text(); }
     // the backbone alone (encode_view per camera): feats [n_cams * fh * fw, C]
     void encode_dev(const uint8_t* images, float* feats, hipStream_t caller);
 
@@ -143,6 +174,10 @@ private:
     int img_h_ = 480, img_w_ = 640, n_cams_ = 2;
     float norm_eps_ = 1e-8f;
     int pool_k_ = 3, pool_stride_ = 2, pool_pad_ = 1;
+    // FiLM: per block, the offset of its point in gamma / beta, or -1
+    std::vector<int> film_off_;
+    int film_total_ = 0;
+    float *film_g_ = nullptr, *film_b_ = nullptr;
     int fh_ = 0, fw_ = 0, feat_ch_ = 0, n_int8_convs_ = 0;
     DeviceArena A_;
     Conv stem_;
@@ -421,7 +456,10 @@ class CkptFiles;
 // final RMSNorm), fp32 on the device. <stem>.meta / <stem>.bin.
 class T5Enc {
 public:
-    T5Enc(const CkptFiles& files, const std::string& stem);
+    // <stem>.meta / <stem>.bin. With tail set, the .bin may hold more floats
+    // past the encoder (IMPACT's text heads, t5_text.cpp:41-64): they are
+    // copied into *tail instead of failing the size check.
+    T5Enc(const CkptFiles& files, const std::string& stem, std::vector<float>* tail = nullptr);
     int d_model() const { return D_; }
     int vocab() const { return vocab_; }
     // ids / mask host [seq] -> out device [seq, d_model]; an id outside the
@@ -559,6 +597,63 @@ private:
     int cur_ = 0;
     std::vector<uint8_t> prev_p_, prev_w_;
     float *emb_ = nullptr, *noise_ = nullptr, *z_ = nullptr, *act_ = nullptr, *out_ = nullptr;
+    hipStream_t own_ = nullptr;
+};
+
+// ---------------------------------------------------------------- IMPACT --
+// src/models/impact/{impact_model,t5_text}.{h,cpp}: ActModel with the IMPACT
+// spec (FiLM points in the trunk, a text tail in the transformer; files
+// config.txt, vision.meta/.bin, impact.meta/.bin, stats.bin) and a language
+// pathway run once per instruction: the SentencePiece tokenizer (vocab.txt),
+// the pruned-vocabulary remap (vocab_map.bin, config.txt's vocab_full and
+// unk_id), T5-small (text.meta / .bin) and, from the tail of text.bin, the
+// text projection, the learned text positions and the FiLM head. IMPACT_INT8
+// (and IMPACT_I8_CONV_FROM / _TO) are read at load.
+class ImpactModel {
+public:
+    explicit ImpactModel(const std::string& dir);
+    ~ImpactModel();
+    int chunk() const { return act_->chunk(); }
+    int action_dim() const { return act_->action_dim(); }
+    int state_dim() const { return act_->state_dim(); }
+    int n_cams() const { return act_->n_cams(); }
+    int img_h() const { return act_->img_h(); }
+    int img_w() const { return act_->img_w(); }
+    int n_text() const { return n_text_; }
+    int film_total() const { return film_total_; }
+    int int8_layers() const { return act_->int8_layers(); }
+    int int8_convs() const { return act_->int8_convs(); }
+    // tokenize, remap and encode an instruction; a no-op when it is the cached one
+    void set_instruction(const std::string& instruction);
+    bool have_text() const { return have_text_; }
+    // device pointers: frames [n_cams, img_h, img_w, 3] uint8, state
+    // [state_dim] raw, actions [chunk, action_dim]; the instruction set first
+    void predict_dev(const uint8_t* frames, const float* state, bool unnormalize, float* actions,
+                     hipStream_t caller);
+    // the current instruction's language-side values (vla_impact_tokens / _film)
+    const std::vector<int32_t>& token_ids() const { return ids_; }
+    const std::vector<int32_t>& compact_ids() const { return compact_; }
+    const std::vector<int32_t>& token_mask() const { return mask_; }
+    const std::vector<float>& film_gamma() const { return gamma_; }
+    const std::vector<float>& film_beta() const { return beta_; }
+
+private:
+    int remap(const std::vector<int32_t>& ids, std::vector<int32_t>& compact);
+
+    std::unique_ptr<ActModel> act_;
+    UnigramTokenizer tok_;
+    std::unique_ptr<T5Enc> t5_;
+    DeviceArena A_;
+    int proj_dim_ = 512, n_text_ = 32, film_total_ = 960, vocab_full_ = 32128, unk_id_ = 2, unk_compact_ = 0;
+    std::vector<int32_t> vocab_map_;
+    float *proj_w_ = nullptr, *proj_b_ = nullptr, *text_pos_ = nullptr, *film_w_ = nullptr, *film_bias_ = nullptr;
+    float *h_ = nullptr, *text_tok_ = nullptr, *pooled_ = nullptr, *gb_ = nullptr;
+    int32_t* mask_d_ = nullptr;
+    bool have_text_ = false, warned_oov_ = false;
+    std::string cached_;
+    std::vector<int32_t> ids_, compact_, mask_;
+    int n_real_ = 0;
+    std::vector<float> gamma_, beta_;
     hipStream_t own_ = nullptr;
 };
 

@@ -649,5 +649,30 @@ void launch_rtc_step(float* x, const float* v, const float* prev, const float* w
     VLA_LAUNCH_CHECK();
 }
 
+// One thread per column: the live rows summed in row order, then scaled by
+// 1 / live, the float operations of the host loop (t5_text.cpp:115-128).
+__global__ __launch_bounds__(256) void masked_row_mean_kernel(float* __restrict__ out, const float* __restrict__ x,
+                                                              int ldx, const int32_t* __restrict__ mask, int rows,
+                                                              int D) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= D) return;
+    float acc = 0.0f;
+    int live = 0;
+    for (int t = 0; t < rows; t++) {
+        if (!mask[t]) continue;
+        acc += x[(size_t)t * ldx + i];
+        live++;
+    }
+    if (live > 0) acc *= 1.0f / (float)live;
+    out[i] = acc;
+}
+
+void launch_masked_row_mean(float* out, const float* x, int ldx, const int32_t* mask, int rows, int D,
+                            hipStream_t st) {
+    VLA_REQUIRE(out && x && mask && rows > 0 && D > 0 && ldx >= D, "masked_row_mean: bad arguments");
+    masked_row_mean_kernel<<<(D + 255) / 256, 256, 0, st>>>(out, x, ldx, mask, rows, D);
+    VLA_LAUNCH_CHECK();
+}
+
 }  // namespace hip
 }  // namespace vla
