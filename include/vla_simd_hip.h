@@ -659,6 +659,38 @@ VLA_API int32_t vla_impact_predict_dev(void* h, const uint8_t* frames, const flo
 VLA_API int32_t vla_impact_int8_layers(void* h);
 VLA_API int32_t vla_impact_int8_convs(void* h);
 
+/* ------------------------------------ Diffusion Policy, model level ------- */
+
+/* The reference's Diffusion Policy entry points, same names, signatures and
+ * status codes (include/vla_simd.h:245-280,
+ * src/models/diffusion/diffusion_capi.cpp): the getters return VLA_ERR_ARG for
+ * a null handle. model_dir holds diffusion.meta, rgb_encoder<i>_backbone.meta
+ * / .bin and rgb_encoder<i>.bin per encoder, unet.bin and stats.bin, or a
+ * vla.simd GGUF carrying them; DIFFUSION_INT8, DP_STEPS and DP_SCHEDULER are
+ * read at load. frames [n_obs_steps, n_cams, img_h, img_w, 3] uint8 and state
+ * [n_obs_steps, state_dim] are oldest first; noise [1 + num_steps, horizon,
+ * action_dim] is the prior then one buffer per DDPM step, or NULL (start from
+ * zeros, no noise); actions [chunk, action_dim]. */
+VLA_API void* vla_diffusion_load(const char* model_dir);
+VLA_API void vla_diffusion_free(void* h);
+VLA_API int32_t vla_diffusion_chunk(void* h);
+VLA_API int32_t vla_diffusion_horizon(void* h);
+VLA_API int32_t vla_diffusion_action_dim(void* h);
+VLA_API int32_t vla_diffusion_state_dim(void* h);
+VLA_API int32_t vla_diffusion_n_cams(void* h);
+VLA_API int32_t vla_diffusion_n_obs_steps(void* h);
+VLA_API int32_t vla_diffusion_img_h(void* h);
+VLA_API int32_t vla_diffusion_img_w(void* h);
+VLA_API int32_t vla_diffusion_num_steps(void* h);
+VLA_API int32_t vla_diffusion_is_ddim(void* h);
+VLA_API int32_t vla_diffusion_predict(void* h, const uint8_t* frames, const float* state, int32_t unnormalize,
+                                      float* actions, const float* noise);
+/* Extensions with no counterpart in vla_simd.h: the counts of int8 UNet
+ * GEMMs / encoder convs, and the node count of the sampler graph. */
+VLA_API int32_t vla_diffusion_int8_layers(void* h);
+VLA_API int32_t vla_diffusion_int8_convs(void* h);
+VLA_API int32_t vla_diffusion_graph_nodes(void* h);
+
 /* -------------------------------------------- SmolVLA, model level ------- */
 
 /* The reference's SmolVLA entry points, same names and signatures

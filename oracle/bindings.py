@@ -649,6 +649,14 @@ def _ref_models():
     L.vla_impact_predict.restype = i32
     L.vla_impact_tokens.argtypes, L.vla_impact_tokens.restype = [P, P, P, P, i32], i32
     L.vla_impact_film.argtypes, L.vla_impact_film.restype = [P, P, P, i32], i32
+    # the reference's own Diffusion Policy entry points (diffusion_capi.cpp)
+    L.vla_diffusion_load.argtypes, L.vla_diffusion_load.restype = [ctypes.c_char_p], P
+    L.vla_diffusion_free.argtypes, L.vla_diffusion_free.restype = [P], None
+    for n in ("chunk", "horizon", "action_dim", "state_dim", "n_cams", "n_obs_steps", "img_h", "img_w",
+              "num_steps", "is_ddim"):
+        f = getattr(L, f"vla_diffusion_{n}")
+        f.argtypes, f.restype = [P], i32
+    L.vla_diffusion_predict.argtypes, L.vla_diffusion_predict.restype = [P, P, P, i32, P, P], i32
     L._models_declared = True
     return L
 
@@ -961,6 +969,38 @@ class RefImpactModel:
     def __del__(self):
         if getattr(self, "h", None):
             _ref_models().vla_impact_free(self.h)
+            self.h = None
+
+
+class RefDiffusionModel:
+    """The reference's DiffusionModel through its own C ABI (vla_diffusion_load
+    / _predict; DIFFUSION_INT8, DP_STEPS and DP_SCHEDULER as the process
+    environment holds them at load)."""
+
+    DIMS = ("chunk", "horizon", "action_dim", "state_dim", "n_cams", "n_obs_steps", "img_h", "img_w", "num_steps",
+            "is_ddim")
+
+    def __init__(self, dirpath):
+        L = _ref_models()
+        self.h = L.vla_diffusion_load(dirpath.encode())
+        if not self.h:
+            raise RuntimeError(f"reference DiffusionModel::load failed for {dirpath}")
+        for k in self.DIMS:
+            setattr(self, k, int(getattr(L, f"vla_diffusion_{k}")(self.h)))
+
+    def predict(self, frames, state, noise=None, unnormalize=True):
+        """-> (status, actions [chunk, action_dim])"""
+        frames = np.ascontiguousarray(frames, np.uint8)
+        state = _f32(state)
+        out = np.zeros((self.chunk, self.action_dim), np.float32)
+        noise = None if noise is None else _f32(noise)  # held until the call returns
+        st = _ref_models().vla_diffusion_predict(self.h, _p(frames), _p(state), int(bool(unnormalize)), _p(out),
+                                                 None if noise is None else _p(noise))
+        return int(st), out
+
+    def __del__(self):
+        if getattr(self, "h", None):
+            _ref_models().vla_diffusion_free(self.h)
             self.h = None
 
 

@@ -116,3 +116,33 @@ def test_smolvla_int8_steps(vla, orc, ckdir, chunk, layers, n_prefix):
     _check_steps(vla, orc, lambda: m.run(prefix, pad, noise), expect_min=layers * 3, max_records=300,
                  what=f"smolvla mask 48 chunk {chunk}")
     assert m.run(prefix, pad, noise).tobytes() == ref.tobytes()
+
+
+@pytest.mark.parametrize("kernel_size", [5, 3])
+def test_diffusion_int8_steps(vla, orc, ckdir, kernel_size):
+    """Diffusion Policy's UNet at DIFFUSION_INT8=1: the 1-D convolutions read
+    their taps as overlapping rows of the padded sequence (the quantizer
+    included), the strided downsample reads every second row, the residual
+    1x1 convs accumulate into the block output. Two sampler steps, DDIM."""
+    ck = _ck()
+    c = dict(ck.DP_MODEL_BASE, down_dims=(64, 128, 256), step_embed_dim=32, num_keypoints=8, width=16,
+             kernel_size=kernel_size)
+    d = str(ckdir / f"dp{kernel_size}")
+    ck.write_diffusion_model(d, c)
+    frames, state, noise = ck.diffusion_model_inputs(dict(c, num_inference_steps=2))
+    saved = {k: os.environ.get(k) for k in ("DIFFUSION_INT8", "DP_STEPS", "DP_SCHEDULER")}
+    os.environ.update(DIFFUSION_INT8="1", DP_STEPS="2", DP_SCHEDULER="DDIM")
+    try:
+        m = vla.DiffusionModel(d)
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+    ref = m.predict(frames, state, noise, unnormalize=False)
+    # per step: 2 convs per res block (12 blocks) + 5 width-changing residuals + 2 downsamples + the final conv
+    per_step = 12 * 2 + 5 + 2 + 1
+    _check_steps(vla, orc, lambda: m.predict(frames, state, noise, unnormalize=False), expect_min=2 * per_step,
+                 what=f"diffusion mask 1 k{kernel_size}")
+    assert m.predict(frames, state, noise, unnormalize=False).tobytes() == ref.tobytes()

@@ -82,6 +82,10 @@ EXPORTS = (
     "vla_impact_n_cams", "vla_impact_img_h", "vla_impact_img_w", "vla_impact_n_text", "vla_impact_set_instruction",
     "vla_impact_predict", "vla_impact_tokens", "vla_impact_film", "vla_impact_predict_dev",
     "vla_impact_int8_layers", "vla_impact_int8_convs",
+    "vla_diffusion_load", "vla_diffusion_free", "vla_diffusion_chunk", "vla_diffusion_horizon",
+    "vla_diffusion_action_dim", "vla_diffusion_state_dim", "vla_diffusion_n_cams", "vla_diffusion_n_obs_steps",
+    "vla_diffusion_img_h", "vla_diffusion_img_w", "vla_diffusion_num_steps", "vla_diffusion_is_ddim",
+    "vla_diffusion_predict", "vla_diffusion_int8_layers", "vla_diffusion_int8_convs", "vla_diffusion_graph_nodes",
     "vla_smolvla_load", "vla_smolvla_free", "vla_smolvla_chunk", "vla_smolvla_action_dim",
     "vla_smolvla_state_dim", "vla_smolvla_n_views", "vla_smolvla_img_size", "vla_smolvla_tok_maxlen",
     "vla_smolvla_tokenize", "vla_smolvla_predict", "vla_smolvla_predict_rtc", "vla_smolvla_preprocess",
@@ -276,6 +280,12 @@ def _declare(L):
         "vla_impact_predict_dev": (i32, [P, P, P, i32, P, P]),
         "vla_impact_int8_layers": (i32, [P]),
         "vla_impact_int8_convs": (i32, [P]),
+        "vla_diffusion_load": (P, [c_char_p]),
+        "vla_diffusion_free": (None, [P]),
+        **{f"vla_diffusion_{k}": (i32, [P]) for k in (
+            "chunk", "horizon", "action_dim", "state_dim", "n_cams", "n_obs_steps", "img_h", "img_w", "num_steps",
+            "is_ddim", "int8_layers", "int8_convs", "graph_nodes")},
+        "vla_diffusion_predict": (i32, [P, P, P, i32, P, P]),
         "vla_smolvla_load": (P, [c_char_p, c_char_p]),
         "vla_smolvla_free": (None, [P]),
         "vla_smolvla_chunk": (i32, [P]),
@@ -1030,6 +1040,41 @@ class ImpactModel(_Handle):
         if got != n:
             raise VlaError("vla_impact_film", got, "copy failed")
         return gamma, beta
+
+
+class DiffusionModel(_Handle):
+    """Diffusion Policy end to end on the device through the reference's own
+    entry points (vla_diffusion_load / _predict): an observation history of
+    uint8 frames and raw states (+ the sampler's noise) -> actions."""
+
+    _load, _free = "vla_diffusion_load", "vla_diffusion_free"
+
+    def __init__(self, dirpath: str):
+        super().__init__(lib().vla_diffusion_load(dirpath.encode()))
+        L = lib()
+        for k in ("chunk", "horizon", "action_dim", "state_dim", "n_cams", "n_obs_steps", "img_h", "img_w",
+                  "num_steps", "int8_layers", "int8_convs"):
+            setattr(self, k, getattr(L, f"vla_diffusion_{k}")(self.h))
+        self.is_ddim = bool(L.vla_diffusion_is_ddim(self.h))
+
+    @property
+    def graph_nodes(self):
+        return lib().vla_diffusion_graph_nodes(self.h)
+
+    def predict(self, frames, state, noise=None, unnormalize=True):
+        """frames [n_obs, n_cams, H, W, 3] uint8, state [n_obs, state_dim],
+        noise [1 + num_steps, horizon, action_dim] or None -> [chunk, action_dim]."""
+        frames = np.ascontiguousarray(frames, np.uint8)
+        state = _f32(state)
+        _need_size("frames", frames, self.n_obs_steps * self.n_cams * self.img_h * self.img_w * 3)
+        _need_size("state", state, self.n_obs_steps * self.state_dim)
+        if noise is not None:
+            noise = _f32(noise)
+            _need_size("noise", noise, (1 + self.num_steps) * self.horizon * self.action_dim)
+        out = np.empty((self.chunk, self.action_dim), np.float32)
+        _call("vla_diffusion_predict", self.h, _ptr(frames), _ptr(state), int(bool(unnormalize)), _ptr(out),
+              None if noise is None else _ptr(noise))
+        return out
 
 
 class SmolvlaModel(_Handle):

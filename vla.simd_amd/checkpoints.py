@@ -151,22 +151,31 @@ def resnet18_blocks(width: int = 64):
     return out
 
 
-def _write_resnet(dirpath: str, name: str, width: int, seed: int, film_after=()) -> list:
+def _write_resnet(dirpath: str, name: str, width: int, seed: int, film_after=(), gn_group_size: int = 0,
+                  key: str = "bb") -> list:
     """<name>.meta / <name>.bin as ResNetBackbone::load reads them
-    (resnet_backbone.cpp:49-154): ResNet-18 with BatchNorm folded into conv
-    biases (weights NHWC [Cout][k][k][Cin]) and optional FiLM points."""
+    (resnet_backbone.cpp:49-154): ResNet-18 (weights NHWC [Cout][k][k][Cin])
+    with BatchNorm folded into conv biases, or, with gn_group_size, a GroupNorm
+    (scale, bias) after every bias-free conv; optional FiLM points. key names
+    the weights' random streams."""
     blocks = resnet18_blocks(width)
     lines = ["in_ch 3", f"stem_out {width}", "stem_k 7", "stem_stride 2", "stem_pad 3", "pool_k 3",
              "pool_stride 2", "pool_pad 1"] + [f"block {a} {b} {st} {d}" for a, b, st, d in blocks]
     lines += [f"film_after {i}" for i in film_after]
+    if gn_group_size:
+        lines.append(f"gn_group_size {gn_group_size}")
     with open(os.path.join(dirpath, f"{name}.meta"), "w") as f:
         f.write("\n".join(lines) + "\n")
-    a = _Arena("bb", seed)
+    a = _Arena(key, seed)
 
     def conv(name, cout, k, cin):
         bound = math.sqrt(3.0 / (k * k * cin))
-        a.parts.append(synth.uniform(f"bb.{name}.w", (cout, k, k, cin), -bound, bound, seed))
-        a.parts.append(synth.normal(f"bb.{name}.b", (cout,), 0.05, seed))
+        a.parts.append(synth.uniform(f"{key}.{name}.w", (cout, k, k, cin), -bound, bound, seed))
+        if gn_group_size:
+            a.parts.append(1.0 + synth.normal(f"{key}.{name}.gs", (cout,), 0.1, seed))
+            a.parts.append(synth.normal(f"{key}.{name}.gb", (cout,), 0.05, seed))
+        else:
+            a.parts.append(synth.normal(f"{key}.{name}.b", (cout,), 0.05, seed))
 
     conv("stem", width, 7, 3)
     for i, (cin, cout, st, d) in enumerate(blocks):
@@ -339,6 +348,73 @@ def write_dp_unet(dirpath: str, cfg: dict = DP_UNET_BASE, seed: int = synth.BASE
     lin(A, dims[0])
     a.write(os.path.join(dirpath, "unet.bin"))
     return dirpath
+
+
+# Diffusion Policy end to end (DiffusionModel, src/models/diffusion/): lerobot's
+# stock pusht-shaped policy, two 96 x 96 cameras centre-cropped to 84 x 84,
+# GroupNorm ResNet-18 encoders (16 channels per group), 32 keypoints, the
+# 512/1024/2048 UNet over a 16-step horizon, DDPM with 100 steps.
+DP_MODEL_BASE = dict(DP_UNET_BASE, horizon=16, n_action_steps=8, img_h=96, img_w=96, crop_h=84, crop_w=84,
+                     width=64, gn_group_size=16, separate_encoders=1, scheduler="DDPM", num_train_timesteps=100,
+                     num_inference_steps=100, beta_schedule="squaredcos_cap_v2", clip_sample=1,
+                     clip_sample_range=1.0)
+
+
+def write_diffusion_model(dirpath: str, cfg: dict = DP_MODEL_BASE, seed: int = synth.BASE_SEED) -> str:
+    """A whole Diffusion Policy checkpoint as tools/convert_diffusion.py
+    writes it: diffusion.meta, per encoder rgb_encoder<i>_backbone.meta/.bin
+    (GroupNorm ResNet-18) and rgb_encoder<i>.bin (the 1x1 keypoint conv
+    [K, C] + bias, the output Linear [2K, 2K] + bias), unet.bin and stats.bin
+    (state min / max, action min / max, per camera image mean / std)."""
+    os.makedirs(dirpath, exist_ok=True)
+    c = cfg
+    keys = ("n_obs_steps", "n_cams", "img_h", "img_w", "crop_h", "crop_w", "state_dim", "action_dim", "horizon",
+            "n_action_steps", "num_keypoints", "kernel_size", "n_groups", "step_embed_dim", "num_train_timesteps",
+            "num_inference_steps", "beta_schedule", "clip_sample", "clip_sample_range", "film_scale",
+            "separate_encoders", "scheduler")
+    with open(os.path.join(dirpath, "diffusion.meta"), "w") as f:
+        for k in keys:
+            f.write(f"{k} {c[k]}\n")
+        f.write("prediction_type epsilon\n")
+        f.write("down_dims " + " ".join(str(d) for d in c["down_dims"]) + "\n")
+        for i in range(c["n_cams"]):
+            f.write(f"cam observation.images.cam{i}\n")
+    K, F = c["num_keypoints"], 2 * c["num_keypoints"]
+    for e in range(c["n_cams"] if c["separate_encoders"] else 1):
+        blocks = _write_resnet(dirpath, f"rgb_encoder{e}_backbone", c["width"], seed,
+                               gn_group_size=c["gn_group_size"], key=f"dp.enc{e}")
+        C = blocks[-1][1]
+        a = _Arena(f"dp.enc{e}.head", seed)
+        a.linear("kp", K, C)
+        a.linear("out", F, F)
+        a.write(os.path.join(dirpath, f"rgb_encoder{e}.bin"))
+    write_dp_unet(dirpath, c, seed)
+    sd, ad = c["state_dim"], c["action_dim"]
+    smin = synth.normal("dp.stats.state_min", (sd,), 1.0, seed)
+    amin = synth.normal("dp.stats.action_min", (ad,), 1.0, seed)
+    parts = [smin, smin + 0.5 + synth.uniform("dp.stats.state_range", (sd,), 0.0, 1.0, seed),
+             amin, amin + 0.5 + synth.uniform("dp.stats.action_range", (ad,), 0.0, 1.0, seed)]
+    for i in range(c["n_cams"]):
+        parts.append(np.array([0.485, 0.456, 0.406], np.float32))
+        parts.append(np.array([0.229, 0.224, 0.225], np.float32))
+    np.concatenate([np.asarray(p, np.float32).reshape(-1) for p in parts]).tofile(
+        os.path.join(dirpath, "stats.bin"))
+    return dirpath
+
+
+def diffusion_model_inputs(cfg: dict = DP_MODEL_BASE, seed: int = synth.BASE_SEED, tag: str = "q0"):
+    """uint8 frames [n_obs, n_cams, img_h, img_w, 3], raw states [n_obs,
+    state_dim] inside the stats' ranges, and the sampler's noise [1 +
+    num_inference_steps, horizon, action_dim] (the prior, then one buffer per
+    DDPM step)."""
+    c = cfg
+    u = synth.uniform(f"dp.in.{tag}.frames", (c["n_obs_steps"], c["n_cams"], c["img_h"], c["img_w"], 3),
+                      0.0, 256.0, seed)
+    frames = np.clip(np.floor(u), 0, 255).astype(np.uint8)
+    state = synth.normal(f"dp.in.{tag}.state", (c["n_obs_steps"], c["state_dim"]), 1.0, seed)
+    noise = synth.normal(f"dp.in.{tag}.noise", (1 + c["num_inference_steps"], c["horizon"], c["action_dim"]),
+                         1.0, seed)
+    return frames, state, noise
 
 
 def write_octo(dirpath: str, cfg: dict = OCTO_BASE, seed: int = synth.BASE_SEED) -> str:

@@ -547,6 +547,46 @@ VLA_API int32_t vla_impact_film(void* h, float* gamma, float* beta, int32_t max_
     return n;
 }
 
+// ----------------------------------------- Diffusion Policy (model level) --
+// The reference's Diffusion Policy entry points (include/vla_simd.h:245-280,
+// src/models/diffusion/diffusion_capi.cpp), same names, signatures and status
+// codes: the getters answer VLA_ERR_ARG for a null handle.
+
+namespace {
+DiffusionModel* dp_model(void* h) { return static_cast<DiffusionModel*>(h); }
+}  // namespace
+
+VLA_API void* vla_diffusion_load(const char* model_dir) {
+    DiffusionModel* m = nullptr;
+    const int32_t rc = guarded("vla_diffusion_load", [&] {
+        VLA_REQUIRE(model_dir, "null model directory");
+        m = new DiffusionModel(model_dir);
+    });
+    return rc == 0 ? m : nullptr;
+}
+VLA_API void vla_diffusion_free(void* h) { delete dp_model(h); }
+VLA_API int32_t vla_diffusion_chunk(void* h) { return h ? dp_model(h)->chunk() : VLA_ERR_ARG; }
+VLA_API int32_t vla_diffusion_horizon(void* h) { return h ? dp_model(h)->horizon() : VLA_ERR_ARG; }
+VLA_API int32_t vla_diffusion_action_dim(void* h) { return h ? dp_model(h)->action_dim() : VLA_ERR_ARG; }
+VLA_API int32_t vla_diffusion_state_dim(void* h) { return h ? dp_model(h)->state_dim() : VLA_ERR_ARG; }
+VLA_API int32_t vla_diffusion_n_cams(void* h) { return h ? dp_model(h)->n_cams() : VLA_ERR_ARG; }
+VLA_API int32_t vla_diffusion_n_obs_steps(void* h) { return h ? dp_model(h)->n_obs() : VLA_ERR_ARG; }
+VLA_API int32_t vla_diffusion_img_h(void* h) { return h ? dp_model(h)->img_h() : VLA_ERR_ARG; }
+VLA_API int32_t vla_diffusion_img_w(void* h) { return h ? dp_model(h)->img_w() : VLA_ERR_ARG; }
+VLA_API int32_t vla_diffusion_num_steps(void* h) { return h ? dp_model(h)->num_steps() : VLA_ERR_ARG; }
+VLA_API int32_t vla_diffusion_is_ddim(void* h) { return h ? (dp_model(h)->is_ddim() ? 1 : 0) : VLA_ERR_ARG; }
+VLA_API int32_t vla_diffusion_int8_layers(void* h) { return h ? dp_model(h)->int8_layers() : 0; }
+VLA_API int32_t vla_diffusion_int8_convs(void* h) { return h ? dp_model(h)->int8_convs() : 0; }
+VLA_API int32_t vla_diffusion_graph_nodes(void* h) { return h ? dp_model(h)->graph_nodes() : 0; }
+
+VLA_API int32_t vla_diffusion_predict(void* h, const uint8_t* frames, const float* state, int32_t unnormalize,
+                                      float* actions, const float* noise) {
+    if (!h || !frames || !state || !actions) return VLA_ERR_ARG;
+    const int32_t rc = guarded("vla_diffusion_predict",
+                               [&] { dp_model(h)->predict(frames, state, noise, unnormalize != 0, actions); });
+    return rc == 0 ? VLA_OK : VLA_ERR_EXCEPTION;  // diffusion_capi.cpp:57-71
+}
+
 // -------------------------------------------------- SmolVLA (model level) --
 // The reference's SmolVLA entry points (include/vla_simd.h:83-124,
 // src/models/smolvla/smolvla_capi.cpp), same names and signatures.

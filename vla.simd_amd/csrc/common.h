@@ -62,10 +62,12 @@ constexpr int kWave = 64;
 // quant.hip
 // the same quantization written in the panel layout (rows <= kPanelMaxRows),
 // panel_bytes(rows, K) bytes at xq
+// taps: the rows of x may overlap (ldx < K), a view that reads a 1-D
+// convolution's taps straight from the padded sequence (x is only read)
 void launch_quantize_rows_panel(const float* x, int ldx, int8_t* xq, float* scale, int rows, int K,
-                                hipStream_t st);
+                                hipStream_t st, bool taps = false);
 void launch_quantize_rows(const float* x, int ldx, int8_t* xq, int ldq, float* scale,
-                          int rows, int K, hipStream_t st);
+                          int rows, int K, hipStream_t st, bool taps = false);
 // q[i] = clamp(rne(x[i] * inv), +-127) over n elements (quantize_span_i8)
 void launch_quantize_span(const float* x, int8_t* q, int64_t n, float inv, hipStream_t st);
 
@@ -163,6 +165,7 @@ struct RowQArgs {
     int8_t* q2 = nullptr;       int ldq2 = 0; float* qs2 = nullptr;
     int rows = 0, H = 0;
     int q_panel = 0;            // q and q2 in the panel layout (ldq, ldq2 unused)
+    int taps = 0;               // x rows may overlap (ldx < H; launch_gemm_i8_rowop only)
 };
 void launch_rowq(const RowQArgs& a, hipStream_t st);
 
@@ -323,6 +326,34 @@ void launch_ddpm_step(float* x, const float* e, const float* z, int n, float a1,
 void launch_rtc_step(float* x, const float* v, const float* prev, const float* weights, const float* gw, int step,
                      int rows, int cols, float time, float dt, hipStream_t st);
 
+// diffusion.hip: Diffusion Policy's glue (models/diffusion/*.cpp).
+// GroupNorm of [T, C] rows in `groups` groups (<= kDpGnMaxGroup channels
+// each), then mish, then the FiLM fmaf(film_scale[c], y, film_bias[c]) or
+// y + film_bias[c] (film_scale null), and / or the residual y + res[t, c];
+// out may be x
+constexpr int kDpGnMaxGroup = 2048;
+void launch_dp_gn_mish(float* out, int ldo, const float* x, int ldx, int T, int C, int groups, const float* scale,
+                       const float* bias, float eps, const float* film_scale, const float* film_bias,
+                       const float* res, int ldr, hipStream_t st);
+// out [C, 2]: per channel of x [npx, C], the softmax-weighted grid [npx, 2]
+void launch_spatial_softmax(float* out, const float* x, const float* grid, int npx, int C, hipStream_t st);
+// out [oh, ow, 3] = (img[top + y, left + x] / 255 - mean) / (std + eps) of an [H, W, 3] uint8 frame
+void launch_crop_normalize(float* out, const uint8_t* img, int H, int W, int top, int left, int oh, int ow,
+                           const float* mean, const float* stdv, float eps, hipStream_t st);
+// g [steps, sd + n_cams F]: MIN_MAX-normalized state rows and the features
+void launch_dp_gcond(float* g, const float* state, const float* smin, const float* smax, const float* feats,
+                     int steps, int sd, int n_cams, int F, float eps, hipStream_t st);
+// gm [steps, D + G] = [temb rows | mish(gcond)]
+void launch_dp_cond_rows(float* gm, const float* temb, const float* gcond, int steps, int D, int G,
+                         hipStream_t st);
+void launch_mish(float* x, int64_t n, hipStream_t st);
+// one DDPM (c0 x0 + c1 x + var z) or DDIM (c0 x0 + c1 e) step over n values
+void launch_dp_sched_step(float* x, const float* e, const float* z, int n, double sqrt_ap, double sqrt_bp,
+                          double c0, double c1, double var, bool ddim, bool clip, double range, hipStream_t st);
+// out [chunk, A] = rows start.. of x [*, A], MIN_MAX un-normalized when unnorm
+void launch_dp_actions(float* out, const float* x, int start, int chunk, int A, const float* amin,
+                       const float* amax, float eps, bool unnorm, hipStream_t st);
+
 // linear_f32.hip: out[m, n] = act(x[m,:] . W[n,:] + bias[n]); accumulate != 0
 // adds it as fmaf(alpha, v, out[m, n]). act as vla_act, plus 4 = silu.
 // out [Hout*Wout, Cout] = the k x k conv of the NHWC map x with W [Cout][k*k*Cin]
@@ -338,9 +369,10 @@ inline size_t col_rows_floats(size_t npix, int K) { return (npix * (size_t)((K +
 // floats of the split-K workspace launch_linear_f32 (and the implicit conv)
 // use for this shape when one is passed; 0 when the shape is not split
 size_t linear_f32_split_floats(int M, int N, int K);
+// taps: x rows may overlap (ldx < K) as launch_quantize_rows' taps view
 void launch_linear_f32(float* out, int ldo, const float* x, int ldx, const float* W, int ldw,
                        const float* bias, int M, int N, int K, int act, int accumulate, float alpha,
-                       hipStream_t st, float* work = nullptr, size_t work_floats = 0);
+                       hipStream_t st, float* work = nullptr, size_t work_floats = 0, bool taps = false);
 
 // runtime.cpp
 hipStream_t library_stream();  // stream of the host-pointer forms

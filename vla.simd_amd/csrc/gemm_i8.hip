@@ -1733,7 +1733,7 @@ void launch_gemm_i8_rowop(const RowQArgs& r, const GemmArgs& a, hipStream_t st) 
     VLA_REQUIRE(!r.out && !r.add && !r.out2 && !r.q2, "gemm_i8_rowop: the fused row op has no fp32 or second output");
     VLA_REQUIRE(!r.q || (!r.q_panel && r.qs && r.ldq >= kpad4(a.K) && r.ldq % 4 == 0 && aligned(r.q, 4)),
                 "gemm_i8_rowop: the quantized-row copy is row-major, 4-byte aligned, ldq >= i8_kpad(K), with scales");
-    VLA_REQUIRE(r.x && r.ldx >= a.K && r.ldx % 4 == 0 && aligned(r.x, 16),
+    VLA_REQUIRE(r.x && (r.ldx >= a.K || (r.taps && r.ldx > 0)) && r.ldx % 4 == 0 && aligned(r.x, 16),
                 "gemm_i8_rowop: x rows must be 16-byte aligned");
     VLA_REQUIRE(r.op == 0 || r.op == 3 || (r.w && aligned(r.w, 16) && (!r.b || aligned(r.b, 16))),
                 "gemm_i8_rowop: norm weights must be 16-byte aligned");

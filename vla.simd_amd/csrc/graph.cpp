@@ -49,9 +49,13 @@ ProbeState& probe_state() {
 
 std::vector<float> d2h_f32(const float* src, int ld, int rows, int cols) {
     std::vector<float> h((size_t)rows * cols);
-    if (rows > 0 && cols > 0)
+    if (rows > 0 && cols > 0 && ld >= cols)
         VLA_HIP_CHECK(hipMemcpy2D(h.data(), (size_t)cols * 4, src, (size_t)ld * 4, (size_t)cols * 4, rows,
                                   hipMemcpyDeviceToHost));
+    else  // overlapping rows (a convolution's taps view): row by row
+        for (int r = 0; r < rows && cols > 0; r++)
+            VLA_HIP_CHECK(hipMemcpy(h.data() + (size_t)r * cols, src + (size_t)r * ld, (size_t)cols * 4,
+                                    hipMemcpyDeviceToHost));
     return h;
 }
 
@@ -202,11 +206,11 @@ void Ctx::alloc(DeviceArena& A, int rows, int ld_max) {
     split_ws = A.alloc<int32_t>(split_bytes / 4);
 }
 
-void quantize(const Ctx& c, const QAct& dst, const float* x, int ldx, int seq, int K) {
+void quantize(const Ctx& c, const QAct& dst, const float* x, int ldx, int seq, int K, bool taps) {
     const size_t need = dst.panel ? (size_t)panel_rows(seq) * dst.ld : (size_t)seq * dst.ld;
     VLA_REQUIRE(need <= c.xq_bytes && seq <= c.xs_rows, "graph: activation quantization scratch too small");
-    if (dst.panel) launch_quantize_rows_panel(x, ldx, dst.q, dst.s, seq, K, c.st);
-    else launch_quantize_rows(x, ldx, dst.q, dst.ld, dst.s, seq, K, c.st);
+    if (dst.panel) launch_quantize_rows_panel(x, ldx, dst.q, dst.s, seq, K, c.st, taps);
+    else launch_quantize_rows(x, ldx, dst.q, dst.ld, dst.s, seq, K, c.st, taps);
     if (probe_on()) probe_note(dst.q, dst.panel ? 0 : dst.ld, x, ldx, seq, K, c.st);
 }
 
@@ -400,16 +404,17 @@ void linear(const Ctx& c, const DLinear& L, const In& in, float* out, int ldo, i
                 r.ldx = in.ldf;
                 r.rows = seq;
                 r.H = L.K;
+                r.taps = in.taps ? 1 : 0;
                 if (try_rowop_gemm(c, L, r, out, ldo, seq, act, acc, n0, n1)) return;
             }
             const QAct s0 = c.slot(0, L.ldq(), seq);
-            quantize(c, s0, in.f, in.ldf, seq, L.K);
+            quantize(c, s0, in.f, in.ldf, seq, L.K, in.taps);
             gemm_q(c, L, s0, out, ldo, seq, act, acc, n0, n1);
         }
     } else {
         VLA_REQUIRE(in.f, "linear: an fp32 layer needs fp32 input rows");
         launch_linear_f32(out, ldo, in.f, in.ldf, L.W + (size_t)n0 * L.K, L.K, L.b ? L.b + n0 : nullptr, seq,
-                          n1 - n0, L.K, act, acc, alpha, c.st);
+                          n1 - n0, L.K, act, acc, alpha, c.st, nullptr, 0, in.taps);
     }
 }
 

@@ -107,6 +107,7 @@ struct Ctx {
 struct In {
     const float* f = nullptr;
     int ldf = 0;
+    bool taps = false;    // f's rows overlap (ldf < K): a 1-D convolution's taps view
     QAct q;               // valid when quantized or deferred
     bool quantized = false;
     bool deferred = false;
@@ -114,7 +115,7 @@ struct In {
 };
 
 // x [seq, K] (row stride ldx) -> dst
-void quantize(const Ctx& c, const QAct& dst, const float* x, int ldx, int seq, int K);
+void quantize(const Ctx& c, const QAct& dst, const float* x, int ldx, int seq, int K, bool taps = false);
 
 // out[:, n0:n1] (+)= act(x W[n0:n1]^T + b). An int8 layer takes in.q when
 // in.quantized, else quantizes in.f into slot 0; a deferred row op, or the

@@ -508,9 +508,10 @@ size_t linear_f32_split_floats(int M, int N, int K) {
 
 void launch_linear_f32(float* out, int ldo, const float* x, int ldx, const float* W, int ldw,
                        const float* bias, int M, int N, int K, int act, int accumulate, float alpha,
-                       hipStream_t st, float* work, size_t work_floats) {
+                       hipStream_t st, float* work, size_t work_floats, bool taps) {
     VLA_REQUIRE(M >= 0 && N > 0 && K > 0, "linear_f32: need M >= 0, N > 0, K > 0");
-    VLA_REQUIRE(ldx >= K && ldw >= K && ldo >= N, "linear_f32: row strides shorter than the rows");
+    VLA_REQUIRE((ldx >= K || (taps && ldx > 0)) && ldw >= K && ldo >= N,
+                "linear_f32: row strides shorter than the rows");
     VLA_REQUIRE(out && x && W, "linear_f32: null buffer");
     VLA_REQUIRE(act >= 0 && act <= 4, "linear_f32: unknown activation");
     if (M == 0) return;

@@ -18,6 +18,8 @@
 namespace vla {
 namespace hip {
 
+class CkptFiles;
+
 // ------------------------------------------------------------------- ACT --
 // src/models/act/act_transformer.{h,cpp}: DETR-style post-norm encoder over
 // [latent | state | camera tokens], decoder with `chunk` zero-initialised
@@ -90,6 +92,76 @@ private:
     GraphReplay replay_;
 };
 
+// ------------------------------------------------------- ResNet-18 trunk --
+// src/models/act/resnet_backbone.{h,cpp}: <name>.meta / .bin, a 7x7/s2 stem,
+// a max pool with the folded ReLU, basic blocks, on one normalized NHWC image
+// at a time. BatchNorm folded into conv biases (ACT, IMPACT), or GroupNorm
+// after every conv (gn_group_size channels per group: Diffusion Policy's
+// encoders; the convs then carry no bias). fp32 convs are the implicit GEMM
+// or im2col + the fp32 matrix-core linear; int8 ones are conv2d_i8, bit-exact
+// to the reference's Conv2d int8 path given the same input. FiLM points
+// (film_after) modulate block outputs when the options ask for them.
+struct TrunkOpts {
+    bool film = false;       // apply (1 + gamma) relu(v) + beta at film_after
+    bool int8 = false;       // convs of stages [from, to) through conv2d_i8
+    int from = 0, to = -1;   // stage 0 the stem, 1.. the blocks; to < 0: all
+};
+
+class ResNetTrunk {
+public:
+    ResNetTrunk(const CkptFiles& files, const std::string& name, int in_h, int in_w, const TrunkOpts& o);
+    int feat_h() const { return fh_; }
+    int feat_w() const { return fw_; }
+    int channels() const { return ch_; }
+    int int8_convs() const { return n_int8_; }
+    bool stem_int8() const { return stem_.q8 != nullptr; }
+    int film_total() const { return film_total_; }
+    float* film_gamma() const { return film_g_; }
+    float* film_beta() const { return film_b_; }
+    // x [in_h, in_w, 3] normalized; in_part / in_nparts: block maxima of |x|
+    // (for an int8 stem; nparts 0 runs its absmax pass); out [fh * fw, C]
+    void run(const float* x, const float* in_part, int in_nparts, float* out, hipStream_t st);
+
+private:
+    struct Conv {
+        int cin = 0, cout = 0, k = 0, stride = 1, pad = 0;
+        float* W = nullptr;  // fp32 [cout, k * k * cin]
+        float* b = nullptr;  // [cout], null under GroupNorm
+        const float *gs = nullptr, *gb = nullptr;  // GroupNorm scale / bias [cout]
+        std::unique_ptr<vla_linear_i8> q8;  // conv2d_i8 weights when the stage is int8
+    };
+    struct Block {
+        Conv c1, c2, down;
+        bool has_down = false;
+    };
+    // out [Hout * Wout, cout] = conv(x [H, W, cin]), then its GroupNorm (if
+    // any) and the ReLU (relu). int8 convs: in_part / in_nparts are the block
+    // maxima of |x| its producer wrote, out_part receives those of the relu'd
+    // output; returns their count (0 when none are written).
+    int conv(const Conv& c, const float* x, int H, int W, float* out, bool relu, hipStream_t st,
+             const float* in_part = nullptr, int in_nparts = 0, float* out_part = nullptr);
+
+    int in_h_ = 0, in_w_ = 0, gsize_ = 0;
+    int pool_k_ = 3, pool_stride_ = 2, pool_pad_ = 1;
+    std::vector<int> film_off_;  // per block, its point's offset in gamma / beta, or -1
+    int film_total_ = 0;
+    float *film_g_ = nullptr, *film_b_ = nullptr;
+    int fh_ = 0, fw_ = 0, ch_ = 0, n_int8_ = 0;
+    DeviceArena A_;
+    Conv stem_;
+    std::vector<Block> blocks_;
+    // the activation maps (reused image after image), the im2col rows +
+    // split-K sums, the conv2d_i8 workspace, the GroupNorm affine and sums
+    float *a_ = nullptr, *b_ = nullptr, *c_ = nullptr, *res_ = nullptr, *col_ = nullptr;
+    float *part_a_ = nullptr, *part_b_ = nullptr, *part_c_ = nullptr;
+    size_t col_floats_ = 0;
+    void* work_ = nullptr;
+    size_t work_bytes_ = 0;
+    float *gA_ = nullptr, *gB_ = nullptr;
+    double* gW_ = nullptr;
+    size_t gw_doubles_ = 0;
+};
+
 // What tells an ACT-shaped model's files and knobs apart: ACT itself, or
 // IMPACT (impact_model.cpp:50-66: the trunk in vision.meta/.bin, the
 // transformer in impact.meta/.bin with int8_state, IMPACT_INT8 and its conv
@@ -126,10 +198,10 @@ public:
     int n_cams() const { return n_cams_; }
     int img_h() const { return img_h_; }
     int img_w() const { return img_w_; }
-    int feat_h() const { return fh_; }
-    int feat_w() const { return fw_; }
-    int feat_ch() const { return feat_ch_; }
-    int int8_convs() const { return n_int8_convs_; }
+    int feat_h() const { return trunk_->feat_h(); }
+    int feat_w() const { return trunk_->feat_w(); }
+    int feat_ch() const { return trunk_->channels(); }
+    int int8_convs() const { return trunk_->int8_convs(); }
     int int8_layers() const { return tf_->int8_layers(); }
     int graph_nodes() const { return replay_.nodes() + tf_->graph_nodes(); }
     // device pointers: images [n_cams, img_h, img_w, 3] uint8, state
@@ -144,59 +216,29 @@ public:
                           int n_text_real, bool unnormalize, float* actions, hipStream_t caller);
     // FiLM (spec.film): the trunk's gamma / beta device buffers [film_total],
     // the points concatenated in film_after order, which the caller fills
-    int film_total() const { return film_total_; }
-    float* film_gamma() const { return film_g_; }
-    float* film_beta() const { return film_b_; }
+    int film_total() const { return trunk_->film_total(); }
+    float* film_gamma() const { return trunk_->film_gamma(); }
+    float* film_beta() const { return trunk_->film_beta(); }
     int tf_dim() const { return tf_->dim(); }
     int tf_n_text() const { return tf_->n_text(); }
     // the backbone alone (encode_view per camera): feats [n_cams * fh * fw, C]
     void encode_dev(const uint8_t* images, float* feats, hipStream_t caller);
 
 private:
-    struct Conv {
-        int cin = 0, cout = 0, k = 0, stride = 1, pad = 0;
-        float* W = nullptr;  // fp32 [cout, k * k * cin]
-        float* b = nullptr;  // [cout]
-        std::unique_ptr<vla_linear_i8> q8;  // conv2d_i8 weights when the stage is int8
-    };
-    struct Block {
-        Conv c1, c2, down;
-        bool has_down = false;
-    };
-    // out [Hout * Wout, cout] = conv(x [H, W, cin]); relu applies the
-    // reference's relu afterwards. int8 convs: in_part / in_nparts are the
-    // block maxima of |x| its producer wrote, out_part receives those of the
-    // relu'd output; returns their count (0 when none are written).
-    int conv(const Conv& c, const float* x, int H, int W, float* out, bool relu, hipStream_t st,
-             const float* in_part = nullptr, int in_nparts = 0, float* out_part = nullptr);
     void run_backbone(hipStream_t st);
 
     int img_h_ = 480, img_w_ = 640, n_cams_ = 2;
     float norm_eps_ = 1e-8f;
-    int pool_k_ = 3, pool_stride_ = 2, pool_pad_ = 1;
-    // FiLM: per block, the offset of its point in gamma / beta, or -1
-    std::vector<int> film_off_;
-    int film_total_ = 0;
-    float *film_g_ = nullptr, *film_b_ = nullptr;
-    int fh_ = 0, fw_ = 0, feat_ch_ = 0, n_int8_convs_ = 0;
     DeviceArena A_;
-    Conv stem_;
-    std::vector<Block> blocks_;
+    std::unique_ptr<ResNetTrunk> trunk_;
     std::unique_ptr<ActTf> tf_;
     float *img_mean_ = nullptr, *img_std_ = nullptr, *state_mean_ = nullptr, *state_std_ = nullptr,
           *action_mean_ = nullptr, *action_std_ = nullptr;
-    // buffers: the cameras' normalized frames, the trunk's activation maps
-    // (reused camera after camera), the im2col rows, the conv2d_i8 workspace
-    uint8_t* img_in_ = nullptr;  // the frames the captured graph reads
-    float *norm_ = nullptr, *a_ = nullptr, *b_ = nullptr, *c_ = nullptr, *res_ = nullptr, *col_ = nullptr,
-          *feats_ = nullptr, *state_n_ = nullptr, *act_n_ = nullptr;
-    // block maxima of |x| written by each conv2d_i8 input's producer:
-    // [n_cams][kConvPartMax] for the normalized frames, kConvPartMax for a_,
-    // b_ and c_ (the trunk buffers swap, and so do their maxima)
-    float *part_norm_ = nullptr, *part_a_ = nullptr, *part_b_ = nullptr, *part_c_ = nullptr;
-    size_t col_floats_ = 0;  // im2col rows + split-K sums
-    void* work_ = nullptr;
-    size_t work_bytes_ = 0;
+    // the frames the captured graph reads, the cameras' normalized frames
+    // (with their block maxima [n_cams][kConvPartMax] for an int8 stem), the
+    // trunk's features of every camera
+    uint8_t* img_in_ = nullptr;
+    float *norm_ = nullptr, *part_norm_ = nullptr, *feats_ = nullptr, *state_n_ = nullptr, *act_n_ = nullptr;
     hipStream_t own_ = nullptr;
     GraphReplay replay_;
 };
@@ -449,7 +491,6 @@ private:
 };
 
 // ------------------------------------------------------------ Octo policy --
-class CkptFiles;
 
 // src/nn/t5_encoder.{h,cpp}: the T5 encoder (pre-RMSNorm blocks, relative
 // position bias attention without 1/sqrt(d) scaling, ReLU FFN, no biases,
@@ -509,10 +550,6 @@ private:
     std::vector<Layer> layers_;
     DLinear embed_;
     float *a_ = nullptr, *b_ = nullptr, *col_ = nullptr, *gA_ = nullptr, *gB_ = nullptr;
-    // block maxima of |x| written by each conv2d_i8 input's producer:
-    // [n_cams][kConvPartMax] for the normalized frames, kConvPartMax for a_,
-    // b_ and c_ (the trunk buffers swap, and so do their maxima)
-    float *part_norm_ = nullptr, *part_a_ = nullptr, *part_b_ = nullptr, *part_c_ = nullptr;
     size_t col_floats_ = 0;  // im2col rows + split-K sums
     double* gW_ = nullptr;   // GroupNorm partial sums
     size_t gw_doubles_ = 0;
@@ -655,6 +692,128 @@ private:
     int n_real_ = 0;
     std::vector<float> gamma_, beta_;
     hipStream_t own_ = nullptr;
+};
+
+// ------------------------------------------------------- Diffusion Policy --
+// src/models/diffusion/{diffusion_model,unet1d,rgb_encoder,scheduler}.{h,cpp}:
+// n_obs_steps frames per camera and n_obs_steps states in, the executed slice
+// of the denoised horizon out. Per camera a GroupNorm ResNet-18 trunk, a 1x1
+// conv to keypoints, the spatial soft-argmax and a Linear + ReLU give 2 K
+// features per frame (frames seen by the previous query are not encoded
+// again, as the reference's pixel cache does); the conditional 1-D UNet
+// (Conv1d + GroupNorm + Mish blocks with FiLM from [time embedding | global
+// conditioning], strided-conv downsampling, transposed-conv upsampling with
+// skip concatenation) runs once per DDPM / DDIM step. Files: diffusion.meta,
+// rgb_encoder<i>_backbone.meta/.bin, rgb_encoder<i>.bin, unet.bin, stats.bin.
+// DIFFUSION_INT8 (read at load as diffusion_model.cpp:111-119): bit 1 the
+// UNet's conv / residual / downsample GEMMs, bit 2 every encoder conv;
+// DP_STEPS and DP_SCHEDULER override the checkpoint's sampler.
+//
+// On the device the UNet's convolutions are GEMMs over "taps views": each
+// activation [T, C] sits between zero rows, so output row t of a k-tap,
+// stride-s convolution reads the k * C consecutive floats from row t * s -
+// pad, i.e. the sequence itself with row stride s * C (rows overlap); the
+// transposed convolution is two such GEMMs (even and odd output rows). The
+// FiLM vectors of every block and every step are one GEMM per query, since
+// the step's half of each block's conditioning input does not depend on the
+// observation. The whole sampler loop is one HIP graph.
+class DiffusionModel {
+public:
+    explicit DiffusionModel(const std::string& dir);
+    ~DiffusionModel();
+    int chunk() const { return n_action_; }
+    int horizon() const { return H_; }
+    int action_dim() const { return A_dim_; }
+    int state_dim() const { return sd_; }
+    int n_cams() const { return n_cams_; }
+    int n_obs() const { return n_obs_; }
+    int img_h() const { return img_h_; }
+    int img_w() const { return img_w_; }
+    int num_steps() const { return (int)timesteps_.size(); }
+    bool is_ddim() const { return ddim_; }
+    int int8_layers() const { return n_int8_; }
+    int int8_convs() const;
+    int graph_nodes() const { return replay_.nodes(); }
+    // host pointers: frames [n_obs, n_cams, img_h, img_w, 3] uint8 oldest
+    // first, state [n_obs, state_dim] raw, noise [1 + num_steps, horizon,
+    // action_dim] or null (start from zeros, no DDPM noise), actions
+    // [chunk, action_dim]
+    void predict(const uint8_t* frames, const float* state, const float* noise, bool unnormalize, float* actions);
+
+private:
+    struct Act {  // [T, C] rows at p, with P zero rows before and after
+        float* p = nullptr;
+        int T = 0, C = 0;
+    };
+    struct ConvB {  // Conv1d (taps GEMM) -> GroupNorm -> Mish
+        DLinear L;
+        int cin = 0, cout = 0;
+        const float *gs = nullptr, *gb = nullptr;
+    };
+    struct Res {
+        ConvB c1, c2;
+        DLinear res;  // 1x1 conv when cin != cout
+        bool has_res = false;
+        int cin = 0, cout = 0, film_off = 0;
+        Act h, o;
+    };
+    struct Down {
+        Res r1, r2;
+        DLinear ds;
+        bool has = false;
+        Act out;  // the downsampled sequence
+    };
+    struct Up {
+        Res r1, r2;
+        DLinear even, odd;  // the transposed conv's even / odd output rows
+        bool has = false;
+        int uc = 0;
+        Act cat, out;
+    };
+    struct Encoder {
+        std::unique_ptr<ResNetTrunk> trunk;
+        DLinear kp, out;
+        float* grid = nullptr;  // [fh * fw, 2]
+    };
+    Act act(int T, int C);
+    void conv(const Ctx& c, const DLinear& L, const Act& x, int k, int stride, float* out, int ldo, int rows) const;
+    void res_block(const Ctx& c, const Res& r, const Act& x, int step) const;
+    void unet(const Ctx& c, int step) const;
+    void sample(hipStream_t st);
+    void encode(int slot, hipStream_t st);
+
+    // diffusion.meta
+    int n_obs_ = 2, n_cams_ = 2, img_h_ = 480, img_w_ = 640, crop_h_ = 0, crop_w_ = 0, sd_ = 6, A_dim_ = 6, H_ = 64,
+        n_action_ = 32, kp_ = 32, k_ = 5, groups_ = 8, D_ = 128, n_train_ = 100, n_infer_ = 100;
+    std::vector<int> down_dims_;
+    bool film_scale_ = true, clip_ = true, separate_ = true, ddim_ = false;
+    float clip_range_ = 1.0f, gn_eps_ = 1e-5f;
+    int P_ = 2, CD_ = 0, G_ = 0, F_ = 0, n_int8_ = 0, n_cond_ = 0, top_ = 0, left_ = 0, oh_ = 0, ow_ = 0;
+    // the sampler: alphas_cumprod and the descending timestep ladder
+    std::vector<double> alphas_cumprod_;
+    std::vector<int> timesteps_;
+    DeviceArena Ad_;
+    Ctx ctx_;
+    std::vector<Encoder> enc_;
+    DLinear cond_;  // every block's cond encoder, rows concatenated
+    std::vector<Down> down_;
+    Res mid1_, mid2_;
+    std::vector<Up> up_;
+    ConvB final_;
+    DLinear final_conv_;
+    float *smin_ = nullptr, *smax_ = nullptr, *amin_ = nullptr, *amax_ = nullptr, *img_mean_ = nullptr,
+          *img_std_ = nullptr;
+    // per query: frames and features per (step, camera) slot, the state rows,
+    // the noise, the conditioning rows, the FiLM vectors of every step
+    uint8_t* frames_ = nullptr;
+    float *norm_ = nullptr, *fmap_ = nullptr, *kpmap_ = nullptr, *kpts_ = nullptr, *feats_ = nullptr,
+          *state_ = nullptr, *noise_ = nullptr, *gcond_ = nullptr, *temb_ = nullptr, *gm_ = nullptr,
+          *cond_all_ = nullptr, *eps_ = nullptr, *act_out_ = nullptr;
+    Act x0_, f_;
+    std::vector<std::vector<uint8_t>> slot_px_;  // the frame each slot last encoded (host)
+    std::vector<std::unique_ptr<GraphReplay>> enc_replay_;
+    hipStream_t own_ = nullptr;
+    GraphReplay replay_;
 };
 
 }  // namespace hip

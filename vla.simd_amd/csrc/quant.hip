@@ -295,10 +295,10 @@ void launch_quantize_span(const float* x, int8_t* q, int64_t n, float inv, hipSt
 }
 
 void launch_quantize_rows_panel(const float* x, int ldx, int8_t* xq, float* scale, int rows, int K,
-                                hipStream_t st) {
+                                hipStream_t st, bool taps) {
     VLA_REQUIRE(rows >= 0 && rows <= kPanelMaxRows && K > 0,
                 "quantize (panel): rows must be in [0, 128] and K > 0");
-    VLA_REQUIRE(ldx >= K, "quantize (panel): ldx < K");
+    VLA_REQUIRE(ldx >= K || (taps && ldx > 0), "quantize (panel): ldx < K");
     VLA_REQUIRE(aligned(xq, 4), "quantize (panel): xq must be 4-byte aligned");
     if (rows == 0) return;
     const int mp = panel_rows(rows);
@@ -334,9 +334,9 @@ static int wide_min_k() {
 }
 
 void launch_quantize_rows(const float* x, int ldx, int8_t* xq, int ldq, float* scale, int rows,
-                          int K, hipStream_t st) {
+                          int K, hipStream_t st, bool taps) {
     VLA_REQUIRE(rows >= 0 && K > 0, "quantize: rows must be >= 0 and K > 0");
-    VLA_REQUIRE(ldx >= K, "quantize: ldx < K");
+    VLA_REQUIRE(ldx >= K || (taps && ldx > 0), "quantize: ldx < K");
     VLA_REQUIRE(ldq >= kpad4(K) && ldq % 4 == 0, "quantize: ldq must be >= i8_kpad(K) and a multiple of 4");
     VLA_REQUIRE(aligned(xq, 4), "quantize: xq must be 4-byte aligned");
     if (rows == 0) return;
