@@ -514,8 +514,80 @@ def _lat_octo_model(vla, torch, ck, ob, tmp, stream_obj):
     return row
 
 
+def _lat_impact_model(vla, torch, ck, ob, tmp, stream_obj):
+    """IMPACT end to end through vla_impact_predict (host pointers): one
+    480 x 640 uint8 camera, the ACT_BASE-shaped transformer with its text
+    tail, FiLM in the trunk; the instruction is encoded once and cached, as
+    in a rollout; IMPACT_INT8=63. Wall-clock median of host calls."""
+    c = ck.IMPACT_MODEL_BASE
+    d = os.path.join(tmp, "impact_model")
+    ck.write_impact_model(d, c)
+    images, state = ck.act_model_inputs(c)
+    saved = os.environ.get("IMPACT_INT8")
+    os.environ["IMPACT_INT8"] = "63"
+    try:
+        m = vla.ImpactModel(d)
+        r = ob.RefImpactModel(d) if ob is not None else None
+    finally:
+        if saved is None:
+            os.environ.pop("IMPACT_INT8", None)
+        else:
+            os.environ["IMPACT_INT8"] = saved
+    text = "pick up the red block"
+    gpu = _median_ms(lambda: m.predict(images, state, text), warmup=3, timed=20)
+    row = {"host_call_ms": round(gpu, 4), "image": f"{c['n_cams']}x{c['img_h']}x{c['img_w']}", "impact_int8": 63,
+           "int8_layers": m.int8_layers, "int8_convs": m.int8_convs}
+    if r is not None:
+        row["cpu_ref_ms"] = round(_median_ms(lambda: r.predict(images, state, text), warmup=2, timed=10), 3)
+    return row
+
+
+def _lat_diffusion_model(vla, torch, ck, ob, tmp, stream_obj, mask, sched, steps):
+    """Diffusion Policy end to end through vla_diffusion_predict (host
+    pointers): lerobot's pusht-shaped policy (two 96 x 96 cameras cropped to
+    84 x 84, GroupNorm ResNet-18 encoders, the 512/1024/2048 UNet over a
+    16-step horizon) in a rollout's steady state (each query brings one new
+    frame per camera, the older step's features come from the frame cache),
+    DIFFUSION_INT8 = mask, the given sampler. Wall-clock median of host calls."""
+    c = ck.DP_MODEL_BASE
+    d = os.path.join(tmp, "diffusion_model")
+    if not os.path.exists(os.path.join(d, "stats.bin")):
+        ck.write_diffusion_model(d, c)
+    pool, state, noise = ck.diffusion_model_inputs(dict(c, n_obs_steps=8))
+    noise = noise[:1 + steps]
+    saved = {k: os.environ.get(k) for k in ("DIFFUSION_INT8", "DP_SCHEDULER", "DP_STEPS")}
+    os.environ.update(DIFFUSION_INT8=str(mask), DP_SCHEDULER=sched, DP_STEPS=str(steps))
+    try:
+        m = vla.DiffusionModel(d)
+        r = ob.RefDiffusionModel(d) if ob is not None else None
+    finally:
+        for k, v in saved.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+    n = c["n_obs_steps"]
+
+    def roll(model):
+        k = [0]
+
+        def call():
+            i = k[0] % (len(pool) - n + 1)
+            k[0] += 1
+            return model.predict(np.ascontiguousarray(pool[i:i + n]), state[i:i + n], noise)
+        return call
+    gpu = _median_ms(roll(m), warmup=3, timed=10 if steps > 20 else 20)
+    row = {"host_call_ms": round(gpu, 4), "sampler": f"{sched}{steps}", "diffusion_int8": mask,
+           "images": f"{n}x{c['n_cams']}x{c['img_h']}x{c['img_w']} (crop {c['crop_h']}x{c['crop_w']})",
+           "int8_layers": m.int8_layers, "int8_convs": m.int8_convs, "graph_nodes": m.graph_nodes}
+    if r is not None:
+        row["cpu_ref_ms"] = round(_median_ms(roll(r), warmup=1, timed=3 if steps > 20 else 10), 3)
+    return row
+
+
 def policy_latency(vla, torch, stream_obj, with_cpu=True,
-                   models=("act", "act_model", "octo", "smolvla", "siglip", "smolvla_model", "octo_model")):
+                   models=("act", "act_model", "octo", "smolvla", "siglip", "smolvla_model", "octo_model",
+                           "impact_model", "diffusion_model")):
     """Per-chunk latency of BASELINE.json configs[2..4] at batch 1, and of
     SmolVLA's SigLIP vision tower per camera image: the device
     graphs (one captured HIP graph per forward, inputs resident in HBM) and the
@@ -558,6 +630,15 @@ def policy_latency(vla, torch, stream_obj, with_cpu=True,
         if "octo_model" in models:
             out["octo_model"] = _lat_octo_model(vla, torch, ck, ob, tmp, stream_obj)
             print(f"  Octo end to end: {out['octo_model']}", file=sys.stderr, flush=True)
+        if "impact_model" in models:
+            out["impact_model"] = _lat_impact_model(vla, torch, ck, ob, tmp, stream_obj)
+            print(f"  IMPACT end to end: {out['impact_model']}", file=sys.stderr, flush=True)
+        if "diffusion_model" in models:
+            for mask, sched, steps in ((3, "DDPM", 100), (0, "DDPM", 100), (3, "DDIM", 10), (0, "DDIM", 10)):
+                key = f"diffusion_{sched.lower()}{steps}_int8_{mask}"
+                out[key] = _lat_diffusion_model(vla, torch, ck, ob, tmp, stream_obj, mask, sched, steps)
+                print(f"  Diffusion Policy end to end ({sched} {steps}, DIFFUSION_INT8={mask}): {out[key]}",
+                      file=sys.stderr, flush=True)
     if ob is not None:
         out["cpu_ref_threads"] = int(ob.ref().ref_omp_max_threads())
     return out
@@ -642,7 +723,8 @@ def main():
     ap.add_argument("--no-policy", action="store_true", help="skip the per-chunk policy latency leg")
     ap.add_argument("--policy-only", action="store_true",
                     help="only the per-chunk policy latency leg (for rocprofv3 runs)")
-    ap.add_argument("--models", default="act,act_model,octo,smolvla,siglip,smolvla_model,octo_model", help="policy graphs to time")
+    ap.add_argument("--models", default="act,act_model,octo,smolvla,siglip,smolvla_model,octo_model,impact_model,"
+                    "diffusion_model", help="policy graphs to time")
     ap.add_argument("--no-conv", action="store_true", help="skip the ResNet-18 conv2d_i8 leg")
     ap.add_argument("--conv-only", action="store_true", help="only the ResNet-18 conv2d_i8 leg")
     ap.add_argument("--profile-only", action="store_true",

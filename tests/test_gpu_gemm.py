@@ -314,9 +314,10 @@ def test_panel_rejects_large_m(vla, torch_cuda):
 # N edge (48) and a 60-tile output
 SPLIT_SHAPES = [(340, 512, 3200), (330, 512, 4608), (321, 100, 4100), (330, 48, 3100), (330, 640, 4096),
                 (330, 512, 4100),
-                # at most 128 rows (the skinny kernel): SigLIP's projection
-                # (64 x 960 x 12288), a K tail, one row, 16 columns
-                (64, 960, 12288), (100, 1000, 4100), (1, 16, 4096), (16, 200, 8192)]
+                # at most 128 rows (the skinny kernel splits from K = 8192):
+                # SigLIP's projection (64 x 960 x 12288), a K tail, one row,
+                # 16 columns, a UNet-like 4 x 1024 x 20480
+                (64, 960, 12288), (100, 1000, 8200), (1, 16, 8192), (16, 200, 8192), (4, 1024, 20480)]
 
 
 @pytest.mark.parametrize("seq,N,K", SPLIT_SHAPES)
@@ -359,7 +360,7 @@ def test_split_k_bitexact(vla, orc, torch_cuda, seq, N, K, act, accumulate):
         assert same_bits(got, want)
 
 
-@pytest.mark.parametrize("seq,N,K", [(64, 960, 12288), (100, 1000, 4100), (5, 48, 8200)])
+@pytest.mark.parametrize("seq,N,K", [(64, 960, 12288), (100, 1000, 8200), (5, 48, 8200), (8, 512, 10240)])
 def test_split_k_panel_bitexact(vla, orc, torch_cuda, seq, N, K):
     """Split-K over panel-layout activations (the chunks start at whole
     64-byte panels): equal to the unsplit panel GEMM and the oracle."""
@@ -394,6 +395,7 @@ def test_split_k_plan_bounds(vla):
     """Short K, skinny M and tile-rich shapes are not split; the workspace a
     split asks for stays within 8 MiB."""
     assert vla.gemm_i8_split_bytes(100, 4096, 4096) == 0      # skinny kernel
+    assert vla.gemm_i8_split_bytes(8, 1024, 5120) == 0        # skinny, K < 8192: measured slower split
     assert vla.gemm_i8_split_bytes(658, 768, 768) == 0        # K < 1024
     assert vla.gemm_i8_split_bytes(8192, 4096, 4096) == 0     # fills the chip
     assert vla.gemm_i8_split_bytes(512, 4096, 4096) == 0      # one LDS-DMA tile per CU: measured slower split

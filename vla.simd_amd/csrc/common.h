@@ -329,12 +329,12 @@ void launch_rtc_step(float* x, const float* v, const float* prev, const float* w
 // diffusion.hip: Diffusion Policy's glue (models/diffusion/*.cpp).
 // GroupNorm of [T, C] rows in `groups` groups (<= kDpGnMaxGroup channels
 // each), then mish, then the FiLM fmaf(film_scale[c], y, film_bias[c]) or
-// y + film_bias[c] (film_scale null), and / or the residual y + res[t, c];
-// out may be x
+// y + film_bias[c] (film_scale null), or the residual y + res[t, c];
+// stored to out (which may be x) and, when given, out2 (row stride ldo2)
 constexpr int kDpGnMaxGroup = 2048;
 void launch_dp_gn_mish(float* out, int ldo, const float* x, int ldx, int T, int C, int groups, const float* scale,
                        const float* bias, float eps, const float* film_scale, const float* film_bias,
-                       const float* res, int ldr, hipStream_t st);
+                       const float* res, int ldr, hipStream_t st, float* out2 = nullptr, int ldo2 = 0);
 // out [C, 2]: per channel of x [npx, C], the softmax-weighted grid [npx, 2]
 void launch_spatial_softmax(float* out, const float* x, const float* grid, int npx, int C, hipStream_t st);
 // out [oh, ow, 3] = (img[top + y, left + x] / 255 - mean) / (std + eps) of an [H, W, 3] uint8 frame

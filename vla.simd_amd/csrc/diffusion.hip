@@ -5,6 +5,7 @@
 // update. The UNet works on [T, C] channel-last rows (T <= the horizon), so
 // each of these is a few microseconds of latency, not bandwidth.
 #include "common.h"
+#include "wave.h"
 
 #include <cmath>
 
@@ -22,99 +23,102 @@ __device__ __forceinline__ float mish_f(float v) {
     return v * (m / (m + 2.0f));
 }
 
-constexpr int kGnThreads = 512;
+constexpr int kGnThreads = 256;
+constexpr int kGnRegs = 16;  // elements per thread held in registers (groups of <= 4096 values)
 
 // groupnorm (conv.cpp:227-318) over the T rows of one group's gc channels,
-// then mish, then one of: the FiLM y = fmaf(sc[c], y, bi[c]) (scale) or
-// y + bi[c] (bias only) of DPResBlock::forward (unet1d.cpp:186-199), or the
-// residual y + res[t, c] (:203-211). One block per group; the per-channel
-// shifted sums S1 / S2 (shift: the channel's first row) and the group's mean
-// and variance are double, as the reference's. out may be x.
-__global__ __launch_bounds__(kGnThreads) void gn_mish_kernel(float* out, int ldo, const float* x, int ldx, int T,
-                                                             int gc, const float* __restrict__ scale,
+// then mish, then at most one of: the FiLM y = fmaf(sc[c], y, bi[c])
+// (scale) or y + bi[c] (bias only) of DPResBlock::forward
+// (unet1d.cpp:186-199), or the residual y + res[t, c] (:203-211); stored to
+// out and, when out2 is set, to out2 as well (the UNet's skip and
+// concatenation copies). One block per group: each thread sums its
+// elements' shifted values (shift: the group's first value) in double, the
+// waves reduce through DPP, the four wave sums go through LDS in a fixed
+// order; mean and variance are double, as the reference's. out may be x.
+template <bool REG>
+__global__ __launch_bounds__(kGnThreads) void gn_mish_kernel(float* out, int ldo, float* out2, int ldo2,
+                                                             const float* x, int ldx, int T, int gc,
+                                                             const float* __restrict__ scale,
                                                              const float* __restrict__ bias, float eps,
                                                              const float* __restrict__ sc,
                                                              const float* __restrict__ bi,
                                                              const float* __restrict__ res, int ldr) {
-    extern __shared__ double sh[];          // chS1 [gc], chS2 [gc], then kGnThreads x 2 partials
-    double* chS1 = sh;
-    double* chS2 = sh + gc;
-    double* r1 = sh + 2 * gc;
-    double* r2 = r1 + kGnThreads;
-    __shared__ double st[2];
-    const int tid = threadIdx.x;
-    const int c0 = blockIdx.x * gc;
-    const int cw = gc < kGnThreads ? gc : kGnThreads;  // channels per pass
-    const int lanes = kGnThreads / cw;                 // row lanes per channel
-    const int lane = tid / cw, j = tid - lane * cw;
-    for (int cc = 0; cc < gc; cc += cw) {
-        const int jc = cc + j;
-        double s1 = 0.0, s2 = 0.0;
-        if (lane < lanes && jc < gc) {
-            const double k = (double)x[c0 + jc];
-            for (int t = lane; t < T; t += lanes) {
-                const double d = (double)x[(size_t)t * ldx + c0 + jc] - k;
+    __shared__ double red[2][kGnThreads / 64];
+    const int tid = threadIdx.x, c0 = blockIdx.x * gc, n = T * gc;
+    const double K = (double)x[c0];
+    double s1 = 0.0, s2 = 0.0;
+    // REG: the elements and everything their outputs read besides the
+    // statistics (norm scale / bias, FiLM, residual), loaded up front so
+    // those loads overlap the reduction
+    float v[REG ? kGnRegs : 1], ps[REG ? kGnRegs : 1], pb[REG ? kGnRegs : 1], pf[REG ? kGnRegs : 1],
+        pr[REG ? kGnRegs : 1];
+    if (REG) {
+#pragma unroll
+        for (int i = 0; i < kGnRegs; i++) {
+            const int e = tid + i * kGnThreads;
+            v[i] = ps[i] = pb[i] = pf[i] = pr[i] = 0.0f;
+            if (e < n) {
+                const int t = e / gc, c = c0 + (e - t * gc);
+                v[i] = x[(size_t)t * ldx + c];
+                ps[i] = scale[c];
+                pb[i] = bias[c];
+                if (sc) pf[i] = sc[c];
+                if (bi) pr[i] = bi[c];
+                if (res) pr[i] = res[(size_t)t * ldr + c];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < kGnRegs; i++)
+            if (tid + i * kGnThreads < n) {
+                const double d = (double)v[i] - K;
                 s1 += d;
                 s2 += d * d;
             }
+    } else {
+        for (int e = tid; e < n; e += kGnThreads) {
+            const int t = e / gc;
+            const double d = (double)x[(size_t)t * ldx + c0 + (e - t * gc)] - K;
+            s1 += d;
+            s2 += d * d;
         }
-        r1[tid] = s1;
-        r2[tid] = s2;
-        __syncthreads();
-        if (lane == 0 && jc < gc) {
-            double a1 = 0.0, a2 = 0.0;
-            for (int l = 0; l < lanes; l++) {
-                a1 += r1[l * cw + j];
-                a2 += r2[l * cw + j];
-            }
-            chS1[jc] = a1;
-            chS2[jc] = a2;
-        }
-        __syncthreads();
     }
-    // mean = sum_c (S1_c + T K_c) / n
-    double tot = 0.0;
-    for (int c = tid; c < gc; c += kGnThreads) tot += chS1[c] + (double)T * (double)x[c0 + c];
-    r1[tid] = tot;
-    __syncthreads();
-    for (int s = kGnThreads / 2; s > 0; s >>= 1) {
-        if (tid < s) r1[tid] += r1[tid + s];
-        __syncthreads();
-    }
-    const double n = (double)T * gc;
-    const double mean = r1[0] / n;
-    __syncthreads();
-    // sum_p (x - mean)^2 = S2 + 2 (K - mean) S1 + T (K - mean)^2 per channel
-    double ss = 0.0;
-    for (int c = tid; c < gc; c += kGnThreads) {
-        const double dk = (double)x[c0 + c] - mean;
-        ss += chS2[c] + 2.0 * dk * chS1[c] + (double)T * dk * dk;
-    }
-    r2[tid] = ss;
-    __syncthreads();
-    for (int s = kGnThreads / 2; s > 0; s >>= 1) {
-        if (tid < s) r2[tid] += r2[tid + s];
-        __syncthreads();
-    }
-    if (tid == 0) {
-        st[0] = mean;
-        st[1] = 1.0 / sqrt(r2[0] / n + (double)eps);
+    s1 = wave_sum_f64(s1);
+    s2 = wave_sum_f64(s2);
+    if ((tid & 63) == 0) {
+        red[0][tid >> 6] = s1;
+        red[1][tid >> 6] = s2;
     }
     __syncthreads();
-    const double mu = st[0], inv = st[1];
-    for (int cc = 0; cc < gc; cc += cw) {
-        const int jc = cc + j;
-        if (lane >= lanes || jc >= gc) continue;
-        const int c = c0 + jc;
-        const float A = (float)(inv * (double)scale[c]);
-        const float B = (float)((double)bias[c] - mu * inv * (double)scale[c]);
-        const float fs = sc ? sc[c] : 0.0f, fb = bi ? bi[c] : 0.0f;
-        for (int t = lane; t < T; t += lanes) {
-            float y = mish_f(fmaf(x[(size_t)t * ldx + c], A, B));
-            if (sc) y = fmaf(fs, y, fb);
-            else if (bi) y = y + fb;
-            if (res) y = y + res[(size_t)t * ldr + c];
-            out[(size_t)t * ldo + c] = y;
+    double S1 = 0.0, S2 = 0.0;
+#pragma unroll
+    for (int w = 0; w < kGnThreads / 64; w++) {
+        S1 += red[0][w];
+        S2 += red[1][w];
+    }
+    // sum (x - mean)^2 = sum (x - K)^2 - n (mean - K)^2
+    const double md = S1 / n, mean = K + md;
+    const double inv = 1.0 / sqrt(fmax(S2 / n - md * md, 0.0) + (double)eps);
+    // y = mish(x A + B), A = inv scale, B = bias - mean inv scale (double,
+    // then float, as the reference's), then the FiLM / residual term
+    auto apply = [&](int e, float xv, float gs, float gb, float fs, float fb) {
+        const int t = e / gc, c = c0 + (e - t * gc);
+        const float A = (float)(inv * (double)gs);
+        const float B = (float)((double)gb - mean * inv * (double)gs);
+        float y = mish_f(fmaf(xv, A, B));
+        if (sc) y = fmaf(fs, y, fb);
+        else if (bi || res) y = y + fb;
+        out[(size_t)t * ldo + c] = y;
+        if (out2) out2[(size_t)t * ldo2 + c] = y;
+    };
+    if (REG) {
+#pragma unroll
+        for (int i = 0; i < kGnRegs; i++)
+            if (tid + i * kGnThreads < n) apply(tid + i * kGnThreads, v[i], ps[i], pb[i], pf[i], pr[i]);
+    } else {
+        for (int e = tid; e < n; e += kGnThreads) {
+            const int t = e / gc, c = c0 + (e - t * gc);
+            apply(e, x[(size_t)t * ldx + c], scale[c], bias[c], sc ? sc[c] : 0.0f,
+                  res ? res[(size_t)t * ldr + c] : bi ? bi[c] : 0.0f);
         }
     }
 }
@@ -241,18 +245,23 @@ int blocks_for(int64_t n) { return (int)((n + 255) / 256); }
 
 }  // namespace
 
-size_t dp_gn_mish_lds(int gc) { return ((size_t)2 * gc + 2 * kGnThreads) * sizeof(double); }
-
 void launch_dp_gn_mish(float* out, int ldo, const float* x, int ldx, int T, int C, int groups, const float* scale,
                        const float* bias, float eps, const float* film_scale, const float* film_bias,
-                       const float* res, int ldr, hipStream_t st) {
+                       const float* res, int ldr, hipStream_t st, float* out2, int ldo2) {
     VLA_REQUIRE(out && x && scale && bias && T > 0 && C > 0 && groups > 0 && C % groups == 0,
                 "dp_gn_mish: bad shape");
     const int gc = C / groups;
-    VLA_REQUIRE(gc <= kDpGnMaxGroup && ldx >= C && ldo >= C && (!res || ldr >= C), "dp_gn_mish: bad strides");
+    VLA_REQUIRE(gc <= kDpGnMaxGroup && (int64_t)T * gc < INT32_MAX && ldx >= C && ldo >= C &&
+                    (!res || ldr >= C) && (!out2 || ldo2 >= C),
+                "dp_gn_mish: bad strides");
     VLA_REQUIRE(!film_scale || film_bias, "dp_gn_mish: FiLM scale without bias");
-    gn_mish_kernel<<<groups, kGnThreads, dp_gn_mish_lds(gc), st>>>(out, ldo, x, ldx, T, gc, scale, bias, eps,
-                                                                   film_scale, film_bias, res, ldr);
+    VLA_REQUIRE(!(film_bias && res), "dp_gn_mish: FiLM and residual are exclusive");
+    if ((int64_t)T * gc <= (int64_t)kGnThreads * kGnRegs)
+        gn_mish_kernel<true><<<groups, kGnThreads, 0, st>>>(out, ldo, out2, ldo2, x, ldx, T, gc, scale, bias, eps,
+                                                            film_scale, film_bias, res, ldr);
+    else
+        gn_mish_kernel<false><<<groups, kGnThreads, 0, st>>>(out, ldo, out2, ldo2, x, ldx, T, gc, scale, bias, eps,
+                                                             film_scale, film_bias, res, ldr);
     VLA_LAUNCH_CHECK();
 }
 

@@ -1530,12 +1530,17 @@ struct SplitPlan {
     int S = 1, kchunk = 0;
 };
 // The skinny kernel (M <= 128) runs one block per 16 columns; with fewer
-// than half a block per CU and K >= 4096 it splits K into S <= 8 chunks of
+// than half a block per CU and K >= 8192 it splits K into S <= 8 chunks of
 // >= 2048 bytes (multiples of 128) so that S x blocks is about one per CU.
+// Below K = 8192 the reduce launch costs more than the idle CUs: graph
+// replays on MI355X (panel rows, rotating weights), unsplit -> split:
+// 8x1024x5120 6.15 -> 7.35 us, 4x2048x5120 6.30 -> 7.64, 4x1024x4096 5.36
+// -> 6.67; above it the split wins: 4x1024x20480 16.0 -> 9.80, 8x512x10240
+// 9.37 -> 7.80, 4x2048x10240 9.75 -> 9.36 (Diffusion Policy's UNet shapes).
 SplitPlan skinny_split_plan(int N, int K) {
     SplitPlan p;
     const int nb = (N + 15) / 16;
-    if (K < 4096 || 2 * nb > kCUs) return p;
+    if (K < 8192 || 2 * nb > kCUs) return p;
     int S = kCUs / nb;
     S = S < 8 ? S : 8;
     S = S < K / 2048 ? S : K / 2048;

@@ -383,6 +383,24 @@ DiffusionModel::DiffusionModel(const std::string& dir) {
         }
     }
     VLA_REQUIRE(T == H_, "diffusion: the UNet does not return to the horizon");
+    // the concatenations [x | skip] are written by their producers: the skip
+    // by its level's last block norm, x by the mid block's last norm or the
+    // previous transposed conv
+    for (int ind = 0; ind + 1 < nd; ind++) {
+        Up& u = up_[(size_t)ind];
+        Res& skip = down_[(size_t)(nd - 1 - ind)].r2;
+        skip.out2 = u.cat.p + (u.cat.C - skip.cout);
+        skip.ldo2 = u.cat.C;
+        if (ind == 0) {
+            mid2_.out2 = u.cat.p;
+            mid2_.ldo2 = u.cat.C;
+        }
+        if (u.has) {
+            const bool next = ind + 2 < nd;
+            u.up_to = next ? up_[(size_t)ind + 1].cat.p : u.out.p;
+            u.up_ld = next ? up_[(size_t)ind + 1].cat.C : u.uc;
+        }
+    }
     f_ = act(H_, down_dims_[0]);
     eps_ = Ad_.alloc<float>((size_t)H_ * A_dim_);
 
@@ -472,9 +490,10 @@ void DiffusionModel::res_block(const Ctx& c, const Res& r, const Act& x, int ste
         launch_dp_gn_mish(r.o.p, C, r.o.p, C, T, C, groups_, r.c2.gs, r.c2.gb, gn_eps_, nullptr, nullptr, nullptr,
                           0, c.st);
         linear(c, r.res, r.o.p, C, x.p, x.C, T, 0, 1);  // out += x W^T + b
+        if (r.out2) copy_rows_f32(r.out2, r.ldo2, r.o.p, C, T, C, c.st);
     } else {
         launch_dp_gn_mish(r.o.p, C, r.o.p, C, T, C, groups_, r.c2.gs, r.c2.gb, gn_eps_, nullptr, nullptr, x.p, x.C,
-                          c.st);
+                          c.st, r.out2, r.ldo2);
     }
 }
 
@@ -496,9 +515,7 @@ void DiffusionModel::unet(const Ctx& c, int step) const {
     x = &mid2_.o;
     for (int ind = 0; ind + 1 < nd; ind++) {
         const Up& u = up_[(size_t)ind];
-        const Act& skip = down_[(size_t)(nd - 1 - ind)].r2.o;
-        copy_rows_f32(u.cat.p, u.cat.C, x->p, x->C, x->T, x->C, c.st);
-        copy_rows_f32(u.cat.p + x->C, u.cat.C, skip.p, skip.C, skip.T, skip.C, c.st);
+        // u.cat already holds [x | skip]: their producers wrote it
         res_block(c, u.r1, u.cat, step);
         res_block(c, u.r2, u.r1.o, step);
         x = &u.r2.o;
@@ -508,10 +525,10 @@ void DiffusionModel::unet(const Ctx& c, int step) const {
             ev.f = b.p - b.C;
             ev.ldf = b.C;
             ev.taps = true;
-            linear(c, u.even, ev, u.out.p, 2 * u.uc, b.T);
+            linear(c, u.even, ev, u.up_to, 2 * u.up_ld, b.T);
             In od = ev;
             od.f = b.p;
-            linear(c, u.odd, od, u.out.p + u.uc, 2 * u.uc, b.T);
+            linear(c, u.odd, od, u.up_to + u.up_ld, 2 * u.up_ld, b.T);
             x = &u.out;
         }
     }

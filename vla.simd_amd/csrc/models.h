@@ -756,6 +756,8 @@ private:
         bool has_res = false;
         int cin = 0, cout = 0, film_off = 0;
         Act h, o;
+        float* out2 = nullptr;  // a second home of o: its place in a later concatenation
+        int ldo2 = 0;
     };
     struct Down {
         Res r1, r2;
@@ -769,6 +771,8 @@ private:
         bool has = false;
         int uc = 0;
         Act cat, out;
+        float* up_to = nullptr;  // where the transposed conv writes: the next cat, or out
+        int up_ld = 0;
     };
     struct Encoder {
         std::unique_ptr<ResNetTrunk> trunk;

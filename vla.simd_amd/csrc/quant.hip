@@ -225,18 +225,18 @@ __global__ __launch_bounds__(256) void quantize_rows_panel_reg(const float* __re
 // registers (NV float4 per thread), so every load is in flight at once and
 // the row is read once; the block max goes through LDS. Same bytes and scale
 // as the wave-per-row kernel (the max is exact in any order).
-template <int NV>
-__global__ __launch_bounds__(256) void quantize_rows_panel_wide(const float* __restrict__ x, int ldx,
-                                                                int8_t* __restrict__ xq, int mp,
-                                                                float* __restrict__ scale, int K) {
-    __shared__ float red[4];
+template <int NV, int NT = 256>
+__global__ __launch_bounds__(NT) void quantize_rows_panel_wide(const float* __restrict__ x, int ldx,
+                                                               int8_t* __restrict__ xq, int mp,
+                                                               float* __restrict__ scale, int K) {
+    __shared__ float red[NT / 64];
     const int t = threadIdx.x, row = blockIdx.x;
     const float* xr = x + (size_t)row * ldx;
     float4 v[NV];
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < NV; i++) {
-        const int k = 4 * (t + 256 * i);
+        const int k = 4 * (t + NT * i);
         v[i] = make_float4(0.f, 0.f, 0.f, 0.f);
         if (k < K) {
             v[i] = *reinterpret_cast<const float4*>(xr + k);
@@ -246,7 +246,9 @@ __global__ __launch_bounds__(256) void quantize_rows_panel_wide(const float* __r
     amax = wave_max_f32(amax);
     if ((t & 63) == 0) red[t >> 6] = amax;
     __syncthreads();
-    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    amax = red[0];
+#pragma unroll
+    for (int w = 1; w < NT / 64; w++) amax = fmaxf(amax, red[w]);
     const float s = row_scale(amax);
     const float inv = 1.0f / s;
     if (t == 0) scale[row] = s;
@@ -254,7 +256,7 @@ __global__ __launch_bounds__(256) void quantize_rows_panel_wide(const float* __r
     int8_t* base = xq + (size_t)row * 64;
 #pragma unroll
     for (int i = 0; i < NV; i++) {
-        const int k = 4 * (t + 256 * i);
+        const int k = 4 * (t + NT * i);
         if (k < k64)  // K % 4 == 0: a float4 is wholly inside [0, K) or wholly padding
             *reinterpret_cast<uint32_t*>(base + (size_t)(k >> 6) * mp * 64 + (k & 63)) = k < K ? q8x4(v[i], inv) : 0u;
     }
@@ -306,7 +308,15 @@ void launch_quantize_rows_panel(const float* x, int ldx, int8_t* xq, float* scal
     const bool vec = K % 4 == 0 && ldx % 4 == 0 && aligned(x, 16);
     const int nv = ((K + 63) / 64 * 64 + 1023) / 1024;  // float4 per thread over [0, K64), block per row
     const int nvw = ((K + 63) / 64 * 64 + 255) / 256;   // float4 per lane over [0, K64), wave per row
-    if (vec && K >= 2048 && nv <= 16) {
+    const int nv4 = (nv + 3) / 4;  // float4 per thread at 1024 threads per row
+    if (vec && K > 8192 && rows <= 32 && nv4 <= 8) {
+        // few long rows (a 1-D convolution's taps, K = 5 C): 1024 threads per
+        // row, so each holds at most 8 float4 and the row's loads finish sooner
+        if (nv4 <= 1) quantize_rows_panel_wide<1, 1024><<<rows, 1024, 0, st>>>(x, ldx, xq, mp, scale, K);
+        else if (nv4 <= 2) quantize_rows_panel_wide<2, 1024><<<rows, 1024, 0, st>>>(x, ldx, xq, mp, scale, K);
+        else if (nv4 <= 4) quantize_rows_panel_wide<4, 1024><<<rows, 1024, 0, st>>>(x, ldx, xq, mp, scale, K);
+        else quantize_rows_panel_wide<8, 1024><<<rows, 1024, 0, st>>>(x, ldx, xq, mp, scale, K);
+    } else if (vec && K >= 2048 && nv <= 16) {
         // one block per row: 64 x 12288 (SigLIP's projection input) 25.9 -> 6.6 us
         if (nv <= 4) quantize_rows_panel_wide<4><<<rows, 256, 0, st>>>(x, ldx, xq, mp, scale, K);
         else if (nv <= 8) quantize_rows_panel_wide<8><<<rows, 256, 0, st>>>(x, ldx, xq, mp, scale, K);
