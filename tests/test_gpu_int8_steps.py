@@ -118,16 +118,25 @@ def test_smolvla_int8_steps(vla, orc, ckdir, chunk, layers, n_prefix):
     assert m.run(prefix, pad, noise).tobytes() == ref.tobytes()
 
 
-@pytest.mark.parametrize("kernel_size", [5, 3])
-def test_diffusion_int8_steps(vla, orc, ckdir, kernel_size):
+DP_STEP_CASES = {
+    "k5": dict(down_dims=(64, 128, 256), kernel_size=5),
+    "k3": dict(down_dims=(64, 128, 256), kernel_size=3),
+    # two levels, groups of 64 / 128 channels
+    "g4": dict(down_dims=(256, 512), n_groups=4, kernel_size=5),
+}
+
+
+@pytest.mark.parametrize("case", list(DP_STEP_CASES))
+def test_diffusion_int8_steps(vla, orc, ckdir, case):
     """Diffusion Policy's UNet at DIFFUSION_INT8=1: the 1-D convolutions read
     their taps as overlapping rows of the padded sequence (the quantizer
-    included), the strided downsample reads every second row, the residual
-    1x1 convs accumulate into the block output. Two sampler steps, DDIM."""
+    included), the strided downsample reads every second row, the 1x1 convs
+    feed the block's second norm. Two sampler steps, DDIM. The probed pass
+    runs eagerly and without row-op fusion; the captured graph's actions must
+    be bit-identical to it."""
     ck = _ck()
-    c = dict(ck.DP_MODEL_BASE, down_dims=(64, 128, 256), step_embed_dim=32, num_keypoints=8, width=16,
-             kernel_size=kernel_size)
-    d = str(ckdir / f"dp{kernel_size}")
+    c = dict(ck.DP_MODEL_BASE, step_embed_dim=32, num_keypoints=8, width=16, **DP_STEP_CASES[case])
+    d = str(ckdir / f"dp_{case}")
     ck.write_diffusion_model(d, c)
     frames, state, noise = ck.diffusion_model_inputs(dict(c, num_inference_steps=2))
     saved = {k: os.environ.get(k) for k in ("DIFFUSION_INT8", "DP_STEPS", "DP_SCHEDULER")}
@@ -141,8 +150,12 @@ def test_diffusion_int8_steps(vla, orc, ckdir, kernel_size):
             else:
                 os.environ[k] = v
     ref = m.predict(frames, state, noise, unnormalize=False)
-    # per step: 2 convs per res block (12 blocks) + 5 width-changing residuals + 2 downsamples + the final conv
-    per_step = 12 * 2 + 5 + 2 + 1
-    _check_steps(vla, orc, lambda: m.predict(frames, state, noise, unnormalize=False), expect_min=2 * per_step,
-                 what=f"diffusion mask 1 k{kernel_size}")
+    # per step: 2 convs per res block + the width-changing 1x1 convs + the
+    # downsamples + the final conv
+    nd = len(c["down_dims"])
+    per_step = 2 * (4 * nd) + (2 * nd - 1) + (nd - 1) + 1  # 4 nd res blocks
+    probed = []
+    _check_steps(vla, orc, lambda: probed.append(m.predict(frames, state, noise, unnormalize=False)),
+                 expect_min=2 * per_step, what=f"diffusion mask 1 {case}")
+    assert probed[0].tobytes() == ref.tobytes()
     assert m.predict(frames, state, noise, unnormalize=False).tobytes() == ref.tobytes()

@@ -383,6 +383,20 @@ DiffusionModel::DiffusionModel(const std::string& dir) {
         }
     }
     VLA_REQUIRE(T == H_, "diffusion: the UNet does not return to the horizon");
+    // the 1x1 convs' outputs
+    auto res_buf = [&](Res& r) {
+        if (r.has_res) r.rb = Ad_.alloc<float>((size_t)r.o.T * r.cout);
+    };
+    for (Down& d : down_) {
+        res_buf(d.r1);
+        res_buf(d.r2);
+    }
+    res_buf(mid1_);
+    res_buf(mid2_);
+    for (Up& u : up_) {
+        res_buf(u.r1);
+        res_buf(u.r2);
+    }
     // the concatenations [x | skip] are written by their producers: the skip
     // by its level's last block norm, x by the mid block's last norm or the
     // previous transposed conv
@@ -478,7 +492,9 @@ void DiffusionModel::conv(const Ctx& c, const DLinear& L, const Act& x, int k, i
 }
 
 // DPResBlock::forward (unet1d.cpp:176-211): conv1 -> GN -> Mish -> FiLM,
-// conv2 -> GN -> Mish, + the residual (1x1 conv when the width changes)
+// conv2 -> GN -> Mish, + the residual: x, or the 1x1 conv of x when the
+// width changes, run before the second norm, which adds its output (the
+// reference's out[i] += r[i], the same sum)
 void DiffusionModel::res_block(const Ctx& c, const Res& r, const Act& x, int step) const {
     const int T = x.T, C = r.cout;
     conv(c, r.c1.L, x, k_, 1, r.h.p, C, T);
@@ -486,15 +502,9 @@ void DiffusionModel::res_block(const Ctx& c, const Res& r, const Act& x, int ste
     launch_dp_gn_mish(r.h.p, C, r.h.p, C, T, C, groups_, r.c1.gs, r.c1.gb, gn_eps_, film_scale_ ? film : nullptr,
                       film_scale_ ? film + C : film, nullptr, 0, c.st);
     conv(c, r.c2.L, r.h, k_, 1, r.o.p, C, T);
-    if (r.has_res) {
-        launch_dp_gn_mish(r.o.p, C, r.o.p, C, T, C, groups_, r.c2.gs, r.c2.gb, gn_eps_, nullptr, nullptr, nullptr,
-                          0, c.st);
-        linear(c, r.res, r.o.p, C, x.p, x.C, T, 0, 1);  // out += x W^T + b
-        if (r.out2) copy_rows_f32(r.out2, r.ldo2, r.o.p, C, T, C, c.st);
-    } else {
-        launch_dp_gn_mish(r.o.p, C, r.o.p, C, T, C, groups_, r.c2.gs, r.c2.gb, gn_eps_, nullptr, nullptr, x.p, x.C,
-                          c.st, r.out2, r.ldo2);
-    }
+    if (r.has_res) linear(c, r.res, r.rb, C, x.p, x.C, T);  // x W^T + b
+    launch_dp_gn_mish(r.o.p, C, r.o.p, C, T, C, groups_, r.c2.gs, r.c2.gb, gn_eps_, nullptr, nullptr,
+                      r.has_res ? r.rb : x.p, r.has_res ? C : x.C, c.st, r.out2, r.ldo2);
 }
 
 // DPUNet1d::forward (unet1d.cpp:227-303) for sampler step `step`: x0_ -> eps_

@@ -756,6 +756,7 @@ private:
         bool has_res = false;
         int cin = 0, cout = 0, film_off = 0;
         Act h, o;
+        float* rb = nullptr;    // the 1x1 conv's output, added by the second norm
         float* out2 = nullptr;  // a second home of o: its place in a later concatenation
         int ldo2 = 0;
     };
