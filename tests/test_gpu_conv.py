@@ -4,7 +4,8 @@ Bar: bit-exact with the oracle's orc_conv2d_i8 (int8 bytes, int32 sums and the
 fp32 epilogue are all exact), which tests/test_conv_oracle.py pins to the
 reference's own conv2d_i8 (src/hal/common/conv.cpp:424-526). Shapes: a ResNet
 stem (7x7 stride 2 over RGB, the per-byte im2col path), 3x3 blocks and 1x1
-stride-2 downsamples (the float4 path), ragged sizes, a Cout that is not a
+stride-2 downsamples (the implicit GEMM over 64-channel multiples, and the
+float4 im2col path), ragged sizes, a Cout that is not a
 multiple of 16 (the reference requires one; the GPU does not), an all-zero
 input (scale 1, output = bias) and repeated calls on one workspace.
 """
@@ -62,6 +63,30 @@ def test_conv2d_i8_dev_form(vla, orc, torch_cuda, shape):
     torch.cuda.synchronize()
     Wq, ws = orc.quantize_weights_i8(W.reshape(Cout, -1))
     assert same_bits(out.cpu().numpy(), orc.conv2d_i8(x, Wq, ws, b, k, s, p))
+
+
+# (with at least 256 output tiles of 64 x 64, or k = 1, the implicit form runs)
+IMPLICIT_SHAPES = [(128, 128, 64, 64, 3, 1, 1), (30, 40, 256, 512, 1, 2, 0), (161, 203, 64, 48, 5, 3, 2),
+                   (131, 121, 128, 100, 3, 1, 1), (33, 29, 64, 36, 1, 1, 0), (15, 20, 512, 512, 3, 1, 1)]
+
+
+@pytest.mark.parametrize("shape", IMPLICIT_SHAPES)
+def test_conv2d_i8_implicit_and_im2col_forms(vla, orc, shape, monkeypatch):
+    """Input channels a multiple of 64 over enough output tiles (or 1x1)
+    take the implicit GEMM (the int8 map gathered per tap);
+    VLA_HIP_CONV_IMPLICIT=0 (read per call) forces the im2col rows. Both
+    bit-exact with the oracle: ragged output tiles (48, 100, 36 channels),
+    pixel counts off the 64-row tile, stride 3, padding 2."""
+    H, Wd, Cin, Cout, k, s, p = shape
+    x, W, b = _case(shape, seed=11)
+    Wq, ws = orc.quantize_weights_i8(W.reshape(Cout, -1))
+    want = orc.conv2d_i8(x, Wq, ws, b, k, s, p)
+    print(f"conv implicit {shape}", flush=True)
+    got = vla.conv2d_i8(x, Wq, ws, b, k, s, p)
+    monkeypatch.setenv("VLA_HIP_CONV_IMPLICIT", "0")
+    got_im2col = vla.conv2d_i8(x, Wq, ws, b, k, s, p)
+    assert same_bits(got, want), "implicit form differs from the oracle"
+    assert same_bits(got_im2col, want), "im2col form differs from the oracle"
 
 
 def test_conv2d_i8_repeat_and_zero_input(vla, orc, torch_cuda):

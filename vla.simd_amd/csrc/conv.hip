@@ -12,8 +12,24 @@
 // with channel co's weights: dense_linear_i8_pre over the im2col rows with
 // every row scale s.
 //
-// Three launches on the caller's stream (two when the producer of x passes
-// the block maxima of |x| it wrote, ConvArgs::in_part):
+// Input channels a multiple of 64 take an implicit GEMM where it measured
+// faster: 1x1 convolutions, and k x k ones with at least 256 output tiles
+// (MI355X, per call with the absmax pass: 120x160x64->64 3x3 19.3 -> 14.5 us,
+// the 1x1 stride-2 downsamples 10.7 / 10.5 / 10.1 -> 9.7 / 9.3 / 9.8 us; with
+// 40-150 tiles each block walks up to 72 K steps alone and the im2col rows
+// + LDS-DMA GEMM win: 15x20x512 3x3 20.1 us against 33.3).
+// VLA_HIP_CONV_IMPLICIT=0 turns it off (read per call):
+//   conv_quant_kernel   the whole input quantized once to int8 NHWC (the
+//                       scale folded from the block maxima in every block);
+//   conv_i8_implicit    64 x 64 output tiles whose A slabs are gathered
+//                       straight from that map: 64 channels of one tap per
+//                       K step (zeros outside the image), double buffered
+//                       through LDS, the same epilogue as the GEMM.
+// Integer sums are exact in any order and the epilogue is the same one, so
+// the outputs are bit-identical to the im2col path's.
+//
+// Otherwise three launches on the caller's stream (two when the producer of
+// x passes the block maxima of |x| it wrote, ConvArgs::in_part):
 //   conv_absmax_kernel  per-block max |x| (float4 loads, wave + LDS reduce);
 //   conv_im2col_kernel  every block first folds the block maxima into the
 //                       scale (a few hundred floats; the same value in every
@@ -174,6 +190,153 @@ __global__ __launch_bounds__(256) void conv_im2col_kernel(Im2colArgs a) {
     }
 }
 
+// The per-tensor scale from the block maxima (every block folds them the
+// same way, no atomics): s = amax > 0 ? max(amax * clip / 127, FLT_MIN) : 1.
+__device__ __forceinline__ float fold_scale(const float* part, int nparts, float clip, float* red) {
+    float m = 0.0f;
+    for (int i = threadIdx.x; i < nparts; i += blockDim.x) m = fmaxf(m, part[i]);
+    const float amax = block_max(m, red);
+    float s = 1.0f;
+    if (amax > 0.0f) {
+        const float t = amax * clip;
+        s = t / 127.0f;
+        s = s > FLT_MIN ? s : FLT_MIN;
+    }
+    return s;
+}
+
+// x [n4 float4] -> int8 NHWC q (quantize_tensor_i8, conv.cpp:448-465); the
+// scale to *s_out
+__global__ __launch_bounds__(256) void conv_quant_kernel(const float4* __restrict__ x, int64_t n4,
+                                                         uint32_t* __restrict__ q, const float* __restrict__ part,
+                                                         int nparts, float clip, float* __restrict__ s_out) {
+    __shared__ float red[4];
+    const float s = fold_scale(part, nparts, clip, red);
+    const float inv = 1.0f / s;
+    if (blockIdx.x == 0 && threadIdx.x == 0) *s_out = s;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x)
+        q[i] = q8x4(x[i], inv);
+}
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+struct ImplicitArgs {
+    const int8_t* xq;  // int8 NHWC [H, Wd, Cin], Cin % 64 == 0
+    int H, Wd, Cin, k, stride, pad, Wout, npix;
+    const int8_t* W;   // [N][ldw], K = k * k * Cin in [ky][kx][ci] order
+    int ldw;
+    const float* wscale;
+    const float* bias;
+    const float* s;    // the activation scale (device)
+    float* out;        // [npix, N]
+    int N, K;
+};
+
+// 64 x 64 output tile per block, 4 waves in a 2 x 2 grid (32 x 32 each: 2 x 2
+// MFMA fragments). K step = 64 bytes = 64 channels of one tap (ky, kx): each
+// thread loads one 16-byte chunk of one pixel's row for A and one of one
+// output channel's weights for B; LDS rows of 64 + 16 bytes. The weight
+// fragment goes first, so lane l holds output row l % 16 and the four
+// consecutive channels 4 (l / 16) .. + 3, stored as one float4.
+__global__ __launch_bounds__(256) void conv_i8_implicit(ImplicitArgs a) {
+    constexpr int BM = 64, BN = 64, BK = 64, SP = BK + 16;
+    __shared__ __attribute__((aligned(16))) int8_t sm[2][(BM + BN) * SP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave >> 1, wn = wave & 1;
+    const int m0 = blockIdx.y * BM, n0 = blockIdx.x * BN;
+    const int r = tid >> 2, q = (tid & 3) * 16;  // this thread's row of A and of B, its 16-byte chunk
+    const int m = m0 + r < a.npix ? m0 + r : a.npix - 1;
+    const int oy = m / a.Wout, ox = m - oy * a.Wout;
+    const int iy0 = oy * a.stride - a.pad, ix0 = ox * a.stride - a.pad;
+    const int n = n0 + r < a.N ? n0 + r : a.N - 1;
+    const int8_t* brow = a.W + (size_t)n * a.ldw + q;
+    const int ao = r * SP + q, bo = (BM + r) * SP + q;
+    int ci = 0, kx = 0, ky = 0, kg = 0;  // the next slab's tap, channel offset and K offset
+    v4i ra, rb;
+    auto gload = [&]() {
+        const int iy = iy0 + ky, ix = ix0 + kx;
+        ra = v4i{0, 0, 0, 0};
+        if (iy >= 0 && iy < a.H && ix >= 0 && ix < a.Wd)
+            ra = *reinterpret_cast<const v4i*>(a.xq + ((size_t)iy * a.Wd + ix) * a.Cin + ci + q);
+        rb = *reinterpret_cast<const v4i*>(brow + kg);
+        kg += BK;
+        ci += BK;
+        if (ci == a.Cin) {
+            ci = 0;
+            if (++kx == a.k) {
+                kx = 0;
+                ++ky;
+            }
+        }
+    };
+    auto lstore = [&](int buf) {
+        *reinterpret_cast<v4i*>(&sm[buf][ao]) = ra;
+        *reinterpret_cast<v4i*>(&sm[buf][bo]) = rb;
+    };
+    v4i acc[2][2];
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = v4i{0, 0, 0, 0};
+    const int r16 = lane & 15, k16 = (lane >> 4) * 16;
+    auto compute = [&](int buf) {
+        const int8_t* sb = sm[buf];
+        v4i af[2], bf[2];
+#pragma unroll
+        for (int i = 0; i < 2; i++) af[i] = *reinterpret_cast<const v4i*>(sb + (wm * 32 + i * 16 + r16) * SP + k16);
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+            bf[j] = *reinterpret_cast<const v4i*>(sb + (BM + wn * 32 + j * 16 + r16) * SP + k16);
+#pragma unroll
+        for (int i = 0; i < 2; i++)
+#pragma unroll
+            for (int j = 0; j < 2; j++) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[j], af[i], acc[i][j], 0, 0, 0);
+    };
+    const int nk = a.K / BK;
+    gload();
+    lstore(0);
+    if (nk > 1) gload();
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt++) {
+        const int buf = kt & 1;
+        compute(buf);
+        if (kt + 1 < nk) {
+            lstore(buf ^ 1);  // slab kt + 1, loaded during this compute
+            if (kt + 2 < nk) gload();
+        }
+        __syncthreads();
+    }
+    // epilogue: fma((float)acc * ws[n], s, b[n]) per output (gemm_i8.cpp:278)
+    const float s = *a.s;
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const int mo = m0 + wm * 32 + i * 16 + r16;
+        if (mo >= a.npix) continue;
+#pragma unroll
+        for (int j = 0; j < 2; j++) {
+            const int nb = n0 + wn * 32 + j * 16 + (lane >> 4) * 4;
+            float v[4];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const int nc = nb + c < a.N ? nb + c : a.N - 1;
+                const float p = (float)acc[i][j][c] * a.wscale[nc];
+                v[c] = fmaf(p, s, a.bias ? a.bias[nc] : 0.0f);
+            }
+            float* o = a.out + (size_t)mo * a.N + nb;
+            if (nb + 4 <= a.N) {
+                *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
+            } else {
+                for (int c = 0; c < 4 && nb + c < a.N; c++) o[c] = v[c];
+            }
+        }
+    }
+}
+
+bool conv_implicit_on() {
+    const char* e = std::getenv("VLA_HIP_CONV_IMPLICIT");
+    return !(e && e[0] == '0' && e[1] == '\0');
+}
+
 float clip_from_env() {
     // TCPU_I8_CLIP as the reference reads it (src/hal/common/env.cpp:220-226):
     // a value in (0, 1], else 1
@@ -207,8 +370,10 @@ ConvShape conv_shape(int H, int Wd, int Cin, int k, int stride, int pad, int Cou
     c.npix = c.Hout * c.Wout;
     c.lda = (kpad4(c.K) + 63) & ~63;
     c.split = gemm_split_bytes(c.npix, Cout, c.K);
-    c.work = (size_t)kAbsmaxBlocks * 4 + ((size_t)c.npix * 4 + 255) / 256 * 256 +
-             ((size_t)c.npix * c.lda + 255) / 256 * 256 + c.split;
+    // the A region holds the im2col rows, or the int8 input of the implicit form
+    const size_t arows = (size_t)c.npix * c.lda > (size_t)H * Wd * Cin ? (size_t)c.npix * c.lda : (size_t)H * Wd * Cin;
+    c.work = (size_t)kAbsmaxBlocks * 4 + ((size_t)c.npix * 4 + 255) / 256 * 256 + (arows + 255) / 256 * 256 +
+             c.split;
     return c;
 }
 
@@ -240,8 +405,25 @@ void launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
         VLA_LAUNCH_CHECK();
     }
 
+    const float clip = a.clip > 0.0f ? a.clip : clip_from_env();
+    if (a.Cin % 64 == 0 && a.Cout % 4 == 0 && a.ldw % 16 == 0 && (reinterpret_cast<uintptr_t>(a.Wq) & 15) == 0 &&
+        (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 &&
+        (c.npix + 63) / 64 <= 65535 && (a.k == 1 || (int64_t)((c.npix + 63) / 64) * ((a.Cout + 63) / 64) >= 256) &&
+        conv_implicit_on()) {
+        const int64_t n4 = (int64_t)a.H * a.Wd * a.Cin / 4;
+        const int qb = (int)((n4 + 255) / 256 < 2048 ? (n4 + 255) / 256 : 2048);
+        conv_quant_kernel<<<qb, 256, 0, st>>>(reinterpret_cast<const float4*>(a.x), n4,
+                                              reinterpret_cast<uint32_t*>(A), maxima, blocks, clip, ascale);
+        VLA_LAUNCH_CHECK();
+        ImplicitArgs ia{A, a.H, a.Wd, a.Cin, a.k, a.stride, a.pad, c.Wout, c.npix, a.Wq, a.ldw, a.wscale,
+                        a.bias, ascale, a.out, a.Cout, c.K};
+        conv_i8_implicit<<<dim3((a.Cout + 63) / 64, (c.npix + 63) / 64), 256, 0, st>>>(ia);
+        VLA_LAUNCH_CHECK();
+        return;
+    }
+
     Im2colArgs g{a.x, a.H, a.Wd, a.Cin, a.k, a.stride, a.pad, c.Wout, c.npix, c.K, c.lda, maxima, blocks,
-                 a.clip > 0.0f ? a.clip : clip_from_env(), A, ascale};
+                 clip, A, ascale};
     // enough waves for every (group, chunk), at most kIm2colMaxBlocks blocks,
     // a multiple of 8 blocks, and at least one row of nchunk waves per XCD
     const int nchunk = (c.lda / 4 + 63) / 64;
