@@ -65,9 +65,11 @@ def test_conv2d_i8_dev_form(vla, orc, torch_cuda, shape):
     assert same_bits(out.cpu().numpy(), orc.conv2d_i8(x, Wq, ws, b, k, s, p))
 
 
-# (with at least 256 output tiles of 64 x 64, or k = 1, the implicit form runs)
+# the implicit form (>= 256 output tiles of 64 x 64, or 1x1) and, with fewer
+# tiles, the im2col rows: ragged rows and channels, 18 K steps
 IMPLICIT_SHAPES = [(128, 128, 64, 64, 3, 1, 1), (30, 40, 256, 512, 1, 2, 0), (161, 203, 64, 48, 5, 3, 2),
-                   (131, 121, 128, 100, 3, 1, 1), (33, 29, 64, 36, 1, 1, 0), (15, 20, 512, 512, 3, 1, 1)]
+                   (131, 121, 128, 100, 3, 1, 1), (33, 29, 64, 36, 1, 1, 0), (15, 20, 512, 512, 3, 1, 1),
+                   (20, 20, 128, 100, 3, 2, 1), (56, 56, 64, 64, 3, 1, 1)]
 
 
 @pytest.mark.parametrize("shape", IMPLICIT_SHAPES)

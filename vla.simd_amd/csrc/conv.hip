@@ -17,7 +17,11 @@
 // (MI355X, per call with the absmax pass: 120x160x64->64 3x3 19.3 -> 14.5 us,
 // the 1x1 stride-2 downsamples 10.7 / 10.5 / 10.1 -> 9.7 / 9.3 / 9.8 us; with
 // 40-150 tiles each block walks up to 72 K steps alone and the im2col rows
-// + LDS-DMA GEMM win: 15x20x512 3x3 20.1 us against 33.3).
+// + LDS-DMA GEMM win: 15x20x512 3x3 20.1 us against 33.3; a form whose 4
+// waves each took every fourth K step of the whole tile was no faster, 24 us
+// for its kernel alone: with about one block per CU and one slab of loads in
+// flight, each step waits a memory latency, which the LDS-DMA GEMM's 3-4
+// stages hide).
 // VLA_HIP_CONV_IMPLICIT=0 turns it off (read per call):
 //   conv_quant_kernel   the whole input quantized once to int8 NHWC (the
 //                       scale folded from the block maxima in every block);
@@ -406,10 +410,10 @@ void launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
     }
 
     const float clip = a.clip > 0.0f ? a.clip : clip_from_env();
+    const int64_t tiles = (int64_t)((c.npix + 63) / 64) * ((a.Cout + 63) / 64);
     if (a.Cin % 64 == 0 && a.Cout % 4 == 0 && a.ldw % 16 == 0 && (reinterpret_cast<uintptr_t>(a.Wq) & 15) == 0 &&
         (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 &&
-        (c.npix + 63) / 64 <= 65535 && (a.k == 1 || (int64_t)((c.npix + 63) / 64) * ((a.Cout + 63) / 64) >= 256) &&
-        conv_implicit_on()) {
+        (c.npix + 63) / 64 <= 65535 && (a.k == 1 || tiles >= 256) && conv_implicit_on()) {
         const int64_t n4 = (int64_t)a.H * a.Wd * a.Cin / 4;
         const int qb = (int)((n4 + 255) / 256 < 2048 ? (n4 + 255) / 256 : 2048);
         conv_quant_kernel<<<qb, 256, 0, st>>>(reinterpret_cast<const float4*>(a.x), n4,
