@@ -271,3 +271,21 @@ def test_full_size_ddim10(vla, env, tmp_path):
         print(f"diffusion full DDIM10 mask {mask}: action rel err {err:.3e} (bar {bar:.0e}), "
               f"{m.int8_layers} int8 GEMMs, {m.int8_convs} int8 convs, {m.graph_nodes} graph nodes", flush=True)
         assert st == 0 and err <= bar
+
+
+def test_loads_from_gguf(vla, small_dir, env, tmp_path):
+    """The same checkpoint packed into one vla.simd GGUF: our actions from the
+    GGUF are byte-identical to the directory's, and the reference loads the
+    GGUF too (io::Mount)."""
+    ck = _ck()
+    from helpers import oracle
+    ob = oracle()
+    env(DP_SCHEDULER="DDIM", DP_STEPS=5)
+    g = ck.write_gguf(small_dir, str(tmp_path / "diffusion.gguf"), "diffusion")
+    frames, state, noise = ck.diffusion_model_inputs(_small(ck))
+    noise = noise[:6]
+    a = vla.DiffusionModel(small_dir).predict(frames, state, noise)
+    b = vla.DiffusionModel(g).predict(frames, state, noise)
+    assert a.tobytes() == b.tobytes()
+    st, ref = ob.RefDiffusionModel(g).predict(frames, state, noise)
+    assert st == 0 and _rel(b, ref) <= 1e-3

@@ -239,3 +239,21 @@ def test_film_modulates_the_trunk(vla, small_dir, env, tmp_path):
         vla.ImpactModel(bad)
     with pytest.raises(RuntimeError):
         ob.RefImpactModel(bad)
+
+
+def test_loads_from_gguf(vla, small_dir, env, tmp_path):
+    """The same checkpoint packed into one vla.simd GGUF (the format
+    tools/_gguf.py writes, which the reference mounts through io::Mount):
+    our actions from the GGUF are byte-identical to the directory's, and the
+    reference loads the GGUF too."""
+    ck = _ck()
+    from helpers import oracle
+    ob = oracle()
+    env(IMPACT_INT8=31)
+    g = ck.write_gguf(small_dir, str(tmp_path / "impact.gguf"), "impact")
+    images, state = _inputs(ck, _small(ck))
+    a = vla.ImpactModel(small_dir).predict(images, state, INSTR[0], unnormalize=True)
+    b = vla.ImpactModel(g).predict(images, state, INSTR[0], unnormalize=True)
+    assert a.tobytes() == b.tobytes()
+    st, ref = ob.RefImpactModel(g).predict(images, state, INSTR[0], unnormalize=True)
+    assert st == 0 and _rel(b, ref) <= 5e-3
