@@ -87,7 +87,9 @@ struct AttnCfg {
     static constexpr int SK = HDP + 4;               // LDS row, floats
     static constexpr int TILE = 2 * KT * SK;         // K + V of one wave, floats
     static constexpr int F4 = KT * HDP / 4 / 64;     // float4 loads per lane per K (or V) tile
-    static constexpr int MERGE = W * (32 + 16 * HDP);
+    static constexpr int MO = HDP + 4;               // merge row, floats: the 16 rows of one
+                                                     // float4 access fall on distinct banks
+    static constexpr int MERGE = W * (32 + 16 * MO);
     static constexpr int MAIN = 4 * (W * TILE > MERGE ? W * TILE : MERGE);  // bytes
     static constexpr int ALLOW = 4096;  // group table bytes kept in LDS (n_groups <= 64)
     static constexpr int LDS = MAIN + ALLOW;
@@ -374,14 +376,14 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
     __syncthreads();
     float* Mm = smem;               // [W][16]
     float* Ml = smem + 16 * W;      // [W][16]
-    float* Mo = smem + 32 * W;      // [W][16][HDP]
+    float* Mo = smem + 32 * W;      // [W][16][MO]
     if (g == 0) {
         Mm[wave * 16 + c] = m;
         Ml[wave * 16 + c] = lsum;
     }
 #pragma unroll
     for (int dt = 0; dt < DT; dt++)
-        *reinterpret_cast<float4*>(Mo + (wave * 16 + c) * HDP + dt * 16 + 4 * g) =
+        *reinterpret_cast<float4*>(Mo + (wave * 16 + c) * C::MO + dt * 16 + 4 * g) =
             make_float4(oacc[dt][0], oacc[dt][1], oacc[dt][2], oacc[dt][3]);
     __syncthreads();
     // every wave's (m, l) for this lane's query, in registers: the uniform pass
@@ -422,7 +424,7 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
         __syncthreads();
 #pragma unroll
         for (int dt = 0; dt < DT; dt++)
-            *reinterpret_cast<float4*>(Mo + (wave * 16 + c) * HDP + dt * 16 + 4 * g) =
+            *reinterpret_cast<float4*>(Mo + (wave * 16 + c) * C::MO + dt * 16 + 4 * g) =
                 make_float4(oacc[dt][0], oacc[dt][1], oacc[dt][2], oacc[dt][3]);
         __syncthreads();
     }
@@ -443,7 +445,7 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
             float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
             for (int w = 0; w < W; w++) {
-                const float4 v = *reinterpret_cast<const float4*>(Mo + (w * 16 + c) * HDP + d);
+                const float4 v = *reinterpret_cast<const float4*>(Mo + (w * 16 + c) * C::MO + d);
                 o.x += f[w] * v.x;
                 o.y += f[w] * v.y;
                 o.z += f[w] * v.z;
