@@ -112,12 +112,25 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c = lane & 15;
-    const int h = blockIdx.y;
+    // XCD-aware block order for grids of at most one round (256 blocks; ACT,
+    // SmolVLA): the hardware deals workgroup i to XCD i % 8, so each XCD is
+    // given a contiguous run of (head, query tile) pairs and its L2 holds the
+    // K/V rows of a few heads instead of every head's. Larger grids (Octo,
+    // SigLIP) measured slower that way and keep the dispatch order.
+    const int nqt = gridDim.x, total = nqt * gridDim.y;
+    const int bid = blockIdx.y * nqt + blockIdx.x;
+    int logical = bid;
+    if (total <= 256) {
+        const int xcd = bid & 7, per = total >> 3, rem = total & 7;
+        logical = xcd * per + (xcd < rem ? xcd : rem) + (bid >> 3);
+    }
+    const int qt = logical % nqt;
+    const int h = logical / nqt;
     const int kvh = h / (a.n_q / a.n_kv);
     const int HD = a.head_dim;
-    const int qi = blockIdx.x * 16 + c;
+    const int qi = qt * 16 + c;
     const bool qok = qi < a.seq_q;
-    const bool qfull = blockIdx.x * 16 + 16 <= a.seq_q;  // every query of the tile exists
+    const bool qfull = qt * 16 + 16 <= a.seq_q;  // every query of the tile exists
     float* Ks = smem + wave * C::TILE;
     float* Vs = Ks + KT * SK;
 
@@ -153,7 +166,7 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
     // keys past kv_end are blocked for every query of the block (causal bound)
     int kv_end = a.seq_k;
     if (mk == 2) {
-        const int qlast = (blockIdx.x * 16 + 16 < a.seq_q ? blockIdx.x * 16 + 16 : a.seq_q) - 1;
+        const int qlast = (qt * 16 + 16 < a.seq_q ? qt * 16 + 16 : a.seq_q) - 1;
         const int e = qlast + a.causal_offset + 1;
         kv_end = e < 0 ? 0 : (e < kv_end ? e : kv_end);
     }
