@@ -122,6 +122,43 @@ def test_act_two_cameras(vla, ckdir):
     assert err <= bar
 
 
+@pytest.mark.parametrize("small", [False, True])
+def test_act_paired_projections_bit_exact(vla, ckdir, small):
+    """q | k (from x + pos) and v (from x), and the decoder's cross k and v,
+    run as one skinny GEMM launch per pair (gemm_i8_skinny_pair: each block
+    runs its own product's code and sums); the forward must equal, bit for
+    bit, the same forward with every product in its own launch
+    (VLA_HIP_GEMM_PAIR=0). The full shape takes the 129-320-row route in the
+    encoder (302 rows) and the panel route in the decoder (100 rows); the
+    small one (50 rows) the panel route throughout."""
+    ck = _ck()
+    if small:
+        c = dict(ck.ACT_BASE, n_enc=2, fh=6, fw=8)
+        d = str(ckdir / "act_pair_small")
+        ck.write_act(d, c)
+    else:
+        c = ck.ACT_BASE
+        d = str(ckdir / "act")
+        if not os.path.exists(os.path.join(d, "act.bin")):
+            ck.write_act(d, c)
+    feats, state = ck.act_inputs(c)
+    run = lambda m: m.forward(feats, c["n_cams"], c["fh"], c["fw"], state)
+    os.environ["VLA_HIP_GEMM_PAIR"] = "0"
+    try:
+        m0 = vla.ActTransformer(d, c["img_ch"], 31)
+        ref = run(m0)
+        ref2 = run(m0)  # the captured graph as well
+    finally:
+        del os.environ["VLA_HIP_GEMM_PAIR"]
+    m1 = vla.ActTransformer(d, c["img_ch"], 31)
+    got = run(m1)
+    print(f"act paired projections small {small}: max |diff| {np.max(np.abs(got - ref)):.3e}, "
+          f"nodes {m0.graph_nodes} -> {m1.graph_nodes}", flush=True)
+    assert got.tobytes() == ref.tobytes() and ref2.tobytes() == ref.tobytes()
+    _check_replay(lambda: run(m1), got)
+    assert m1.graph_nodes < m0.graph_nodes
+
+
 # -------------------------------------------------------------- IMPACT ----
 
 @pytest.mark.parametrize("mask,n_real", [(0, 11), (31, 11), (31, 16), (31, 40), (31, 0), (15, 5)])

@@ -113,6 +113,11 @@ struct GemmArgs {
     int rope_cols, rope_hd;
 };
 void launch_gemm_i8(const GemmArgs& a, hipStream_t st);
+// Two independent products over the same rows as one skinny launch (same
+// bits as two launch_gemm_i8 calls). Returns false, launching nothing, when
+// either would not take the unsplit skinny kernel; the caller then runs them
+// one by one.
+bool launch_gemm_i8_pair(const GemmArgs& a1, const GemmArgs& a2, hipStream_t st);
 // Workspace bytes launch_gemm_i8 uses to split K for this shape (0: no split).
 size_t gemm_split_bytes(int M, int N, int K);
 

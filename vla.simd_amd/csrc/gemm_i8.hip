@@ -734,13 +734,14 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds(GemmArgs a) {
 // FN: column groups of 16 per block; each A fragment a wave loads feeds FN
 // MFMAs from registers, so a block of 16 x FN columns reads its rows of A once
 // (the rotating epilogue keeps FN = 1).
-template <int FM, int WAVES, bool ROPE = false, int FN = 1>
-__global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
+// bx: the block's column block (blockIdx.x, or its index within one of the
+// two products of gemm_i8_skinny_pair); part: the block's LDS for the waves'
+// partial int32 tiles in MFMA lane order, [wave][t][r][lane].
+template <int FM, int WAVES, bool ROPE, int FN>
+__device__ __forceinline__ void skinny_block(GemmArgs a, const int bx, int32_t* part) {
     static_assert(FM * FN * WAVES <= 64, "partial tiles must fit in 64 KiB of LDS");
     static_assert(!ROPE || FN == 1, "the rotating epilogue owns 16 columns per block");
     constexpr int FT = FM * FN;  // 16 x 16 tiles per wave, tile t = i * FN + j
-    // per wave, its partial int32 tiles in MFMA lane order: [t][r][lane]
-    __shared__ int32_t part[WAVES * FT * 256];
 
     if (gridDim.y > 1) {  // split K: chunk blockIdx.y of K (a multiple of 128 bytes), raw int32 sums
         const int k0 = blockIdx.y * a.kchunk;
@@ -752,7 +753,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
 
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const int n0 = blockIdx.x * 16 * FN;
+    const int n0 = bx * 16 * FN;
     const int K = a.K;
     // row group blockIdx.z: 16-row fragments f0 .. f0 + FM - 1 (fragments past
     // the last one repeat it; their rows are >= M and never stored)
@@ -774,7 +775,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
     const bool rotb = ROPE && n0 < a.rope_cols;
     auto col = [&](int c) {
         if (!rotb) return n0 + c;
-        const int hb = a.rope_hd / 16, head = blockIdx.x / hb, k = blockIdx.x - head * hb;
+        const int hb = a.rope_hd / 16, head = bx / hb, k = bx - head * hb;
         return head * a.rope_hd + 8 * k + (c & 7) + (c < 8 ? 0 : a.rope_hd / 2);
     };
     const int8_t* brow[FN];
@@ -836,7 +837,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
     constexpr int P = (FL <= 3 || (FL == 4 && WAVES < 16)) ? 4 : 3;  // within the VGPR budget
     // blocks i, i + 8, i + 16, ... share an XCD; (WAVES + 1) is odd, so their
     // offsets differ for up to `full` blocks when full is a power of two
-    const int rot = full > 0 ? (int)(((unsigned)blockIdx.x >> 3) * (WAVES + 1) % (unsigned)full) : 0;
+    const int rot = full > 0 ? (int)(((unsigned)bx >> 3) * (WAVES + 1) % (unsigned)full) : 0;
     v4i ra[P][FM], rb[P][FN];
     auto load = [&](int p, int k) {
         int step = wave + k * WAVES + rot;
@@ -920,6 +921,23 @@ __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
         }
         a.out[(size_t)mm * a.ldo + nn] = a.accumulate ? eold[j] + o : o;
     }
+}
+
+template <int FM, int WAVES, bool ROPE = false, int FN = 1>
+__global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
+    __shared__ int32_t part[WAVES * FM * FN * 256];
+    skinny_block<FM, WAVES, ROPE, FN>(a, blockIdx.x, part);
+}
+
+// Two independent products over the same rows in one launch (ACT's q | k
+// from x + pos beside v from x): column blocks below nb1 are a1's, the rest
+// a2's, with one row-group count; each block runs exactly the code and sums
+// of its product's own launch, so the outputs are the same bits.
+template <int FM, int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny_pair(GemmArgs a1, GemmArgs a2, int nb1) {
+    __shared__ int32_t part[WAVES * FM * 256];
+    if ((int)blockIdx.x < nb1) skinny_block<FM, WAVES, false, 1>(a1, blockIdx.x, part);
+    else skinny_block<FM, WAVES, false, 1>(a2, blockIdx.x - nb1, part);
 }
 
 // ------------------------------------------------------------------ gemv --
@@ -1709,6 +1727,82 @@ void launch_gemm_i8(const GemmArgs& a, hipStream_t st) {
         }
     }
     dispatch_tile(t, a, st);
+}
+
+namespace {
+
+// Whether launch_gemm_i8 would run a through run_skinny in one unsplit launch
+// with one column group per block (no rotating epilogue, no int32 output).
+bool plain_skinny(const GemmArgs& a) {
+    const bool al = (a.a_panel || a.lda % 16 == 0) && a.ldb % 16 == 0 && aligned(a.A, 16) && aligned(a.B, 16) &&
+                    aligned(a.out, 16);
+    if (!al || a.rope_cs || a.acc32 || a.M <= 0 || use_gemv(a.M, a.K)) return false;
+    if (skinny_mid_rows(a.M, a.N, a.a_panel)) return true;
+    if (a.M > 128) return false;
+    if (a.split_ws && split_plan(a.M, a.N, a.K).S > 1) return false;
+    return skinny_col_groups(a.M, a.N, a.K) == 1;
+}
+
+int skinny_waves(int K) {
+    const int steps = (K + 63) / 64;
+    return steps >= 32 ? 16 : steps >= 8 ? 8 : 4;
+}
+
+template <int WAVES>
+void run_skinny_pair(const GemmArgs& a1, const GemmArgs& a2, int fm, int groups, hipStream_t st) {
+    const int nb1 = (a1.N + 15) / 16;
+    const dim3 nb(nb1 + (a2.N + 15) / 16, 1, groups);
+    constexpr int W8 = WAVES < 8 ? WAVES : 8;  // FM > 4 keeps the partial tiles within 64 KiB
+    switch (fm) {
+    case 1: gemm_i8_skinny_pair<1, WAVES><<<nb, WAVES * 64, 0, st>>>(a1, a2, nb1); break;
+    case 2: gemm_i8_skinny_pair<2, WAVES><<<nb, WAVES * 64, 0, st>>>(a1, a2, nb1); break;
+    case 3: gemm_i8_skinny_pair<3, WAVES><<<nb, WAVES * 64, 0, st>>>(a1, a2, nb1); break;
+    case 4: gemm_i8_skinny_pair<4, WAVES><<<nb, WAVES * 64, 0, st>>>(a1, a2, nb1); break;
+    case 5: gemm_i8_skinny_pair<5, W8><<<nb, W8 * 64, 0, st>>>(a1, a2, nb1); break;
+    case 6: gemm_i8_skinny_pair<6, W8><<<nb, W8 * 64, 0, st>>>(a1, a2, nb1); break;
+    case 7: gemm_i8_skinny_pair<7, W8><<<nb, W8 * 64, 0, st>>>(a1, a2, nb1); break;
+    default: gemm_i8_skinny_pair<8, W8><<<nb, W8 * 64, 0, st>>>(a1, a2, nb1); break;
+    }
+    VLA_LAUNCH_CHECK();
+}
+
+}  // namespace
+
+// VLA_HIP_GEMM_PAIR=0 keeps every product in its own launch (read per call).
+bool launch_gemm_i8_pair(const GemmArgs& a1, const GemmArgs& a2, hipStream_t st) {
+    const char* e = std::getenv("VLA_HIP_GEMM_PAIR");
+    if (e && e[0] == '0' && e[1] == '\0') return false;
+    if (a1.M != a2.M || a1.N <= 0 || a2.N <= 0 || a1.K <= 0 || a2.K <= 0 || a1.K > kMaxI8K || a2.K > kMaxI8K)
+        return false;
+    if (a1.act < 0 || a1.act > 3 || a2.act < 0 || a2.act > 3) return false;
+    for (const GemmArgs* a : {&a1, &a2}) {
+        if (!a->out || !a->wscale || !a->ascale || a->ldo < a->N || a->ldb < kpad4(a->K) ||
+            (!a->a_panel && a->lda < kpad4(a->K)))
+            return false;
+        if (a->a_panel && a->M > kPanelMaxRows) return false;
+        if (!plain_skinny(*a)) return false;
+    }
+    const bool mid = skinny_mid_rows(a1.M, a1.N, a1.a_panel);
+    if (mid != skinny_mid_rows(a2.M, a2.N, a2.a_panel)) return false;
+    const int W = skinny_waves(a1.K);
+    if (W != skinny_waves(a2.K)) return false;
+    // one row-group count for both: as for one product of N1 + N2 columns, but
+    // with at most 4 fragments per block. ACT's encoder (302 rows, q | k 1024
+    // + v 512 columns, K = 512) on MI355X, graph replays per forward, two
+    // launches 0.3149 ms, one launch with 3 / 4 / 5 / 7 / 10 row groups (7 /
+    // 5 / 4 / 3 / 2 fragments per block) 0.3152 / 0.3082 / 0.2998 / 0.3056 /
+    // 0.3042 ms. VLA_HIP_PAIR_R=<groups> forces a count (read per call).
+    const int nfrag = (a1.M + 15) / 16;
+    int g = skinny_row_groups(a1.M, a1.N + a2.N, a1.K, 1);
+    g = g < (nfrag + 3) / 4 ? (nfrag + 3) / 4 : g;
+    if (const char* r = std::getenv("VLA_HIP_PAIR_R"); r && std::atoi(r) > 0) g = std::atoi(r);
+    g = g > nfrag ? nfrag : g;
+    if (mid) g = g < (nfrag + 7) / 8 ? (nfrag + 7) / 8 : g;
+    const int fm = (nfrag + g - 1) / g, groups = (nfrag + fm - 1) / fm;
+    if (W == 16) run_skinny_pair<16>(a1, a2, fm, groups, st);
+    else if (W == 8) run_skinny_pair<8>(a1, a2, fm, groups, st);
+    else run_skinny_pair<4>(a1, a2, fm, groups, st);
+    return true;
 }
 
 size_t gemm_split_bytes(int M, int N, int K) {

@@ -278,6 +278,31 @@ static bool try_rowop_gemm(const Ctx& c, const DLinear& L, const RowQArgs& r, fl
     return true;
 }
 
+static GemmArgs gemm_q_args(const Ctx& c, const DLinear& L, const QAct& x, float* out, int ldo, int seq, int act,
+                            int acc, int n0, int n1) {
+    const vla_linear_i8& q = *L.q8;
+    VLA_REQUIRE(x.ld == q.ldw(), "linear: quantized input laid out for another layer width");
+    GemmArgs a{};
+    a.A = x.q;
+    a.lda = x.ld;
+    a.B = q.Wq() + (size_t)n0 * q.ldw();
+    a.ldb = q.ldw();
+    a.ascale = x.s;
+    a.wscale = q.wscale() + n0;
+    a.bias = q.bias() ? q.bias() + n0 : nullptr;
+    a.out = out;
+    a.ldo = ldo;
+    a.M = seq;
+    a.N = n1 - n0;
+    a.K = L.K;
+    a.act = act;
+    a.accumulate = acc;
+    a.a_panel = x.panel ? 1 : 0;
+    a.split_ws = c.split_ws;
+    a.split_bytes = c.split_bytes;
+    return a;
+}
+
 static void gemm_q(const Ctx& c, const DLinear& L, const QAct& x, float* out, int ldo, int seq, int act,
                    int acc, int n0, int n1, const RopeEpi* rope = nullptr) {
     const vla_linear_i8& q = *L.q8;
@@ -416,6 +441,18 @@ void linear(const Ctx& c, const DLinear& L, const In& in, float* out, int ldo, i
         launch_linear_f32(out, ldo, in.f, in.ldf, L.W + (size_t)n0 * L.K, L.K, L.b ? L.b + n0 : nullptr, seq,
                           n1 - n0, L.K, act, acc, alpha, c.st, nullptr, 0, in.taps);
     }
+}
+
+void linear_pair(const Ctx& c, const DLinear& L1, const In& in1, float* out1, int ldo1, const DLinear& L2,
+                 const In& in2, float* out2, int ldo2, int seq) {
+    if (seq > 0 && !probe_on() && L1.int8() && L2.int8() && in1.quantized && in2.quantized &&
+        in1.q.ld == L1.ldq() && in2.q.ld == L2.ldq()) {
+        const GemmArgs a1 = gemm_q_args(c, L1, in1.q, out1, ldo1, seq, 0, 0, 0, L1.N);
+        const GemmArgs a2 = gemm_q_args(c, L2, in2.q, out2, ldo2, seq, 0, 0, 0, L2.N);
+        if (launch_gemm_i8_pair(a1, a2, c.st)) return;
+    }
+    linear(c, L1, in1, out1, ldo1, seq);
+    linear(c, L2, in2, out2, ldo2, seq);
 }
 
 In rowop_for(const Ctx& c, const DLinear& L, RowQArgs r, float* f, int ldf, int slot) {

@@ -146,6 +146,14 @@ inline void linear(const Ctx& c, const DLinear& L, float* out, int ldo, const fl
     linear(c, L, in, out, ldo, seq, act, acc, n0, n1, alpha);
 }
 
+// linear(c, L1, in1, out1, ldo1, seq) and linear(c, L2, in2, out2, ldo2, seq):
+// two independent layers over the same rows (no activation, no accumulation),
+// as one GEMM launch when both are int8 with quantized inputs and both take
+// the unsplit skinny kernel (launch_gemm_i8_pair), else one after the other.
+// The values are the same either way.
+void linear_pair(const Ctx& c, const DLinear& L1, const In& in1, float* out1, int ldo1, const DLinear& L2,
+                 const In& in2, float* out2, int ldo2, int seq);
+
 // A row op (RowQArgs op / x / u / w / b / eps / rows / H) whose result feeds
 // layer L: an int8 L gets it quantized in the same kernel, into `slot` (and
 // fp32 rows into f when f is non-null); an fp32 L gets fp32 rows in f. For an

@@ -285,8 +285,7 @@ void ActTf::run(hipStream_t st) {
     feed(0, x_, T, nullptr, nullptr, pos_, enc_[0].qk, enc_[0].v, in_qk, in_v);
     for (size_t li = 0; li < enc_.size(); li++) {
         const Enc& l = enc_[li];
-        linear(c, l.qk, in_qk, qk_, 2 * d, T);  // q | k from x + pos
-        linear(c, l.v, in_v, v_, d, T);         // v from x
+        linear_pair(c, l.qk, in_qk, qk_, 2 * d, l.v, in_v, v_, d, T);  // q | k from x + pos, v from x
         attend(st, att_, d, qk_, 2 * d, qk_ + d, 2 * d, v_, d, T, T, heads_, heads_, hd_, scale, none);
         linear(c, l.o, x_, d, att_, d, T, 0, 1);  // x += wo(att)
         const In h = norm_for(x_, T, l.n1s, l.n1b, l.w1);
@@ -304,15 +303,13 @@ void ActTf::run(hipStream_t st) {
     for (size_t li = 0; li < dec_.size(); li++) {
         const Dec& l = dec_[li];
         if (li > 0) feed(0, x_, T, nullptr, nullptr, pos_, l.ck, l.cv, in_qk, in_v);
-        linear(c, l.ck, in_qk, ckb_ + (size_t)li * T * d, d, T);
-        linear(c, l.cv, in_v, cvb_ + (size_t)li * T * d, d, T);
+        linear_pair(c, l.ck, in_qk, ckb_ + (size_t)li * T * d, d, l.cv, in_v, cvb_ + (size_t)li * T * d, d, T);
     }
     copy_f32(dx_, zero_, (int64_t)C * d, st);  // queries start at zero
     feed(0, dx_, C, nullptr, nullptr, dec_pos_, dec_[0].sqk, dec_[0].sv, in_qk, in_v);
     for (size_t li = 0; li < dec_.size(); li++) {
         const Dec& l = dec_[li];
-        linear(c, l.sqk, in_qk, qk_, 2 * d, C);
-        linear(c, l.sv, in_v, v_, d, C);
+        linear_pair(c, l.sqk, in_qk, qk_, 2 * d, l.sv, in_v, v_, d, C);
         attend(st, att_, d, qk_, 2 * d, qk_ + d, 2 * d, v_, d, C, C, heads_, heads_, hd_, scale, none);
         linear(c, l.so, dx_, d, att_, d, C, 0, 1);
         // LN1, then the cross query input dx + dec_pos
