@@ -159,6 +159,35 @@ def test_act_paired_projections_bit_exact(vla, ckdir, small):
     assert m1.graph_nodes < m0.graph_nodes
 
 
+@pytest.mark.parametrize("mask", [0, 31])
+def test_act_decoder_head_bit_exact(vla, ckdir, mask):
+    """Decoder layer 0's self-attention block and norm1 read only the zero
+    queries, dec_pos and weights: the graph computes them once per model and
+    copies them in (dx and the cross-query input, fp32 rows at mask 0, int8
+    bytes at 31). The forward must equal, bit for bit, the one that recomputes
+    them every call (VLA_HIP_ACT_HEAD=0), on eager calls and graph replays."""
+    ck = _ck()
+    c = ck.ACT_BASE
+    d = str(ckdir / "act")
+    if not os.path.exists(os.path.join(d, "act.bin")):
+        ck.write_act(d, c)
+    feats, state = ck.act_inputs(c)
+    feats2 = np.ascontiguousarray(feats[::-1])
+    run = lambda m, f: m.forward(f, c["n_cams"], c["fh"], c["fw"], state)
+    os.environ["VLA_HIP_ACT_HEAD"] = "0"
+    try:
+        m0 = vla.ActTransformer(d, c["img_ch"], mask)
+        ref = [run(m0, feats), run(m0, feats2), run(m0, feats)]
+    finally:
+        del os.environ["VLA_HIP_ACT_HEAD"]
+    m1 = vla.ActTransformer(d, c["img_ch"], mask)
+    got = [run(m1, feats), run(m1, feats2), run(m1, feats)]
+    for g, r in zip(got, ref):
+        assert g.tobytes() == r.tobytes()
+    print(f"act decoder head mask {mask}: nodes {m0.graph_nodes} -> {m1.graph_nodes}", flush=True)
+    assert m1.graph_nodes < m0.graph_nodes
+
+
 # -------------------------------------------------------------- IMPACT ----
 
 @pytest.mark.parametrize("mask,n_real", [(0, 11), (31, 11), (31, 16), (31, 40), (31, 0), (15, 5)])

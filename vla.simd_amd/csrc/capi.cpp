@@ -81,7 +81,10 @@ VLA_API int32_t vla_hip_memcpy_d2h(void* dst, const void* src, size_t bytes) {
     return guarded("vla_hip_memcpy_d2h", [&] { VLA_HIP_CHECK(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost)); });
 }
 VLA_API int32_t vla_hip_memset(void* dst, int32_t value, size_t bytes) {
-    return guarded("vla_hip_memset", [&] { VLA_HIP_CHECK(hipMemset(dst, value, bytes)); });
+    return guarded("vla_hip_memset", [&] {
+        VLA_HIP_CHECK(hipMemset(dst, value, bytes));
+        VLA_HIP_CHECK(hipStreamSynchronize(nullptr));  // done before the caller's other streams use dst
+    });
 }
 VLA_API int32_t vla_hip_synchronize(void) {
     return guarded("vla_hip_synchronize", [&] { VLA_HIP_CHECK(hipDeviceSynchronize()); });

@@ -20,6 +20,10 @@ void* DeviceArena::raw(size_t bytes) {
     VLA_HIP_CHECK(hipMalloc(&p, b ? b : 256));
     blocks_.push_back(p);
     VLA_HIP_CHECK(hipMemset(p, 0, b ? b : 256));
+    // the fill runs on the null stream, which does not order with the
+    // non-blocking streams the models launch on: wait for it, so no later
+    // write into the block can land before the zeros
+    VLA_HIP_CHECK(hipStreamSynchronize(nullptr));
     bytes_ += b;
     return p;
 }

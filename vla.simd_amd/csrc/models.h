@@ -69,7 +69,9 @@ private:
         const float *n1s, *n1b, *n2s, *n2b, *n3s, *n3b;
     };
     void ensure(int n_cams, int fh, int fw, int nt);
-    void run(hipStream_t st);
+    // the whole forward, or (head_only) decoder layer 0's self-attention block
+    // and norm1 alone, which read only the zero queries, dec_pos and weights
+    void run(hipStream_t st, bool head_only = false);
 
     int d_ = 512, heads_ = 8, hd_ = 64, ff_ = 3200, n_enc_ = 4, n_dec_ = 1, chunk_ = 100;
     int state_dim_ = 6, action_dim_ = 6, n_1d_ = 2, img_ch_ = 0, n_int8_ = 0, n_text_ = 0;
@@ -90,6 +92,13 @@ private:
     Ctx ctx_;
     hipStream_t own_ = nullptr;
     GraphReplay replay_;
+    // decoder layer 0 after its self-attention block and norm1, computed once
+    // by run(st, true) (same kernels, same bits) and copied in per forward:
+    // dx, and the cross-query input (fp32 rows, or their int8 slot bytes)
+    float *head_dx_ = nullptr, *head_xp_ = nullptr, *head_qs_ = nullptr;
+    int8_t* head_q_ = nullptr;
+    size_t head_q_bytes_ = 0;
+    bool head_done_ = false;
 };
 
 // ------------------------------------------------------- ResNet-18 trunk --
