@@ -116,16 +116,31 @@ __global__ __launch_bounds__(W * 64) void attn_fwd(AttnArgs a) {
     // SmolVLA): the hardware deals workgroup i to XCD i % 8, so each XCD is
     // given a contiguous run of (head, query tile) pairs and its L2 holds the
     // K/V rows of a few heads instead of every head's. Larger grids (Octo,
-    // SigLIP) measured slower that way and keep the dispatch order.
+    // SigLIP) measured slower that way; they take the balanced order below.
     const int nqt = gridDim.x, total = nqt * gridDim.y;
     const int bid = blockIdx.y * nqt + blockIdx.x;
-    int logical = bid;
+    int qt, h;
     if (total <= 256) {
         const int xcd = bid & 7, per = total >> 3, rem = total & 7;
-        logical = xcd * per + (xcd < rem ? xcd : rem) + (bid >> 3);
+        const int logical = xcd * per + (xcd < rem ? xcd : rem) + (bid >> 3);
+        qt = logical % nqt;
+        h = logical / nqt;
+    } else if constexpr (W <= 4) {
+        // grids of 1.5+ blocks per CU take 4 waves per block (run_attn). Rounds
+        // of 256 blocks put one block on every CU (block b and b + 256 share a
+        // CU); under causal and block-causal masks a query tile's work grows
+        // with its index, so tiles are dealt heaviest first with every other
+        // round reversed: a CU's heavy block meets a light one, and a last
+        // partial round gets the lightest
+        const int r = bid >> 8, p = bid & 255, start = r << 8;
+        const int len = total - start < 256 ? total - start : 256;
+        const int i = total - 1 - (start + ((r & 1) ? len - 1 - p : p));
+        qt = i / gridDim.y;
+        h = i - qt * gridDim.y;
+    } else {
+        qt = bid % nqt;
+        h = bid / nqt;
     }
-    const int qt = logical % nqt;
-    const int h = logical / nqt;
     const int kvh = h / (a.n_q / a.n_kv);
     const int HD = a.head_dim;
     const int qi = qt * 16 + c;
