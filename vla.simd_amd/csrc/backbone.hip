@@ -159,6 +159,88 @@ __global__ __launch_bounds__(256) void add_relu_film_kernel(float* __restrict__ 
     store_block_absmax(mx, part);
 }
 
+// The same four ops over float4 groups (C % 4 == 0, 16-byte aligned maps, a
+// thread per output pixel and 4 channels, 32-bit indices): the per-element
+// expressions above, so every stored float and block maximum's max is the
+// same; the scalar forms loop over 64-bit element indices and stay for the
+// shapes these do not take.
+__device__ __forceinline__ float pool_max(float v, float o) { return v > o ? v : o; }
+__device__ __forceinline__ float relu_gt(float v) { return v > 0.0f ? v : 0.0f; }
+
+__global__ __launch_bounds__(256) void maxpool_relu4_kernel(float4* __restrict__ out, const float4* __restrict__ x, int H,
+                                                            int Wd, int C4, int k, int stride, int pad, int Wout,
+                                                            int total4, float* __restrict__ part) {
+    float mx = 0.0f;
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total4; e += gridDim.x * blockDim.x) {
+        const int c4 = e % C4, p = e / C4;
+        const int oy = p / Wout, ox = p - oy * Wout;
+        float4 o = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        for (int ky = 0; ky < k; ky++) {
+            const int iy = oy * stride - pad + ky;
+            if (iy < 0 || iy >= H) continue;
+            for (int kx = 0; kx < k; kx++) {
+                const int ix = ox * stride - pad + kx;
+                if (ix < 0 || ix >= Wd) continue;
+                const float4 v = x[(iy * Wd + ix) * C4 + c4];
+                o.x = pool_max(v.x, o.x);
+                o.y = pool_max(v.y, o.y);
+                o.z = pool_max(v.z, o.z);
+                o.w = pool_max(v.w, o.w);
+            }
+        }
+        const float4 r = make_float4(relu_gt(o.x), relu_gt(o.y), relu_gt(o.z), relu_gt(o.w));
+        out[e] = r;
+        mx = fmaxf(fmaxf(mx, fmaxf(r.x, r.y)), fmaxf(r.z, r.w));
+    }
+    store_block_absmax(mx, part);
+}
+
+__global__ __launch_bounds__(256) void add_relu4_kernel(float4* __restrict__ o, const float4* __restrict__ idn, int n4,
+                                                        float* __restrict__ part) {
+    float mx = 0.0f;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += gridDim.x * blockDim.x) {
+        const float4 a = o[i], b = idn[i];
+        const float4 r = make_float4(relu_gt(a.x + b.x), relu_gt(a.y + b.y), relu_gt(a.z + b.z), relu_gt(a.w + b.w));
+        o[i] = r;
+        mx = fmaxf(fmaxf(mx, fmaxf(r.x, r.y)), fmaxf(r.z, r.w));
+    }
+    store_block_absmax(mx, part);
+}
+
+__global__ __launch_bounds__(256) void relu4_kernel(float4* __restrict__ x, int n4, float* __restrict__ part) {
+    float mx = 0.0f;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += gridDim.x * blockDim.x) {
+        float4 v = x[i];
+        if (v.x < 0.0f || v.y < 0.0f || v.z < 0.0f || v.w < 0.0f) {
+            if (v.x < 0.0f) v.x = 0.0f;
+            if (v.y < 0.0f) v.y = 0.0f;
+            if (v.z < 0.0f) v.z = 0.0f;
+            if (v.w < 0.0f) v.w = 0.0f;
+            x[i] = v;
+        }
+        mx = fmaxf(fmaxf(mx, fmaxf(fabsf(v.x), fabsf(v.y))), fmaxf(fabsf(v.z), fabsf(v.w)));
+    }
+    store_block_absmax(mx, part);
+}
+
+__global__ __launch_bounds__(256) void add_relu_film4_kernel(float4* __restrict__ o, const float4* __restrict__ idn,
+                                                             int n4, int C4, const float4* __restrict__ gamma,
+                                                             const float4* __restrict__ beta, float* __restrict__ part) {
+    float mx = 0.0f;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += gridDim.x * blockDim.x) {
+        const int c4 = i % C4;
+        const float4 a = o[i], b = idn[i], g = gamma[c4], be = beta[c4];
+        float4 y;
+        y.x = fmaf(1.0f + g.x, relu_gt(a.x + b.x), be.x);
+        y.y = fmaf(1.0f + g.y, relu_gt(a.y + b.y), be.y);
+        y.z = fmaf(1.0f + g.z, relu_gt(a.z + b.z), be.z);
+        y.w = fmaf(1.0f + g.w, relu_gt(a.w + b.w), be.w);
+        o[i] = y;
+        mx = fmaxf(fmaxf(mx, fmaxf(fabsf(y.x), fabsf(y.y))), fmaxf(fabsf(y.z), fabsf(y.w)));
+    }
+    store_block_absmax(mx, part);
+}
+
 // relu in place as the reference's relu (eltwise.cpp:209-215): x < 0 -> 0
 __global__ __launch_bounds__(256) void relu_kernel(float* __restrict__ x, int64_t n, float* __restrict__ part) {
     float mx = 0.0f;
@@ -225,13 +307,29 @@ void launch_im2col_f32(float* col, int ldc, const float* x, int H, int Wd, int C
 int launch_maxpool_relu(float* out, const float* x, int H, int Wd, int C, int k, int stride, int pad, int Hout,
                         int Wout, hipStream_t st, float* part) {
     VLA_REQUIRE(out && x && Hout > 0 && Wout > 0 && C > 0, "maxpool: bad arguments");
-    const int g = part_grid((int64_t)Hout * Wout * C, part);
+    const int64_t total = (int64_t)Hout * Wout * C;
+    if (C % 4 == 0 && aligned(out, 16) && aligned(x, 16) && (int64_t)H * Wd * C / 4 < INT32_MAX &&
+        total / 4 < INT32_MAX) {
+        const int g = part_grid(total / 4, part);
+        maxpool_relu4_kernel<<<g, 256, 0, st>>>(reinterpret_cast<float4*>(out), reinterpret_cast<const float4*>(x), H,
+                                                 Wd, C / 4, k, stride, pad, Wout, (int)(total / 4), part);
+        VLA_LAUNCH_CHECK();
+        return g;
+    }
+    const int g = part_grid(total, part);
     maxpool_relu_kernel<<<g, 256, 0, st>>>(out, x, H, Wd, C, k, stride, pad, Hout, Wout, part);
     VLA_LAUNCH_CHECK();
     return g;
 }
 
 int launch_add_relu(float* o, const float* idn, int64_t n, hipStream_t st, float* part) {
+    if (n % 4 == 0 && n / 4 < INT32_MAX && aligned(o, 16) && aligned(idn, 16)) {
+        const int g = part_grid(n / 4, part);
+        add_relu4_kernel<<<g, 256, 0, st>>>(reinterpret_cast<float4*>(o), reinterpret_cast<const float4*>(idn),
+                                            (int)(n / 4), part);
+        VLA_LAUNCH_CHECK();
+        return g;
+    }
     const int g = part_grid(n, part);
     add_relu_kernel<<<g, 256, 0, st>>>(o, idn, n, part);
     VLA_LAUNCH_CHECK();
@@ -241,6 +339,15 @@ int launch_add_relu(float* o, const float* idn, int64_t n, hipStream_t st, float
 int launch_add_relu_film(float* o, const float* idn, int64_t n, int C, const float* gamma, const float* beta,
                          hipStream_t st, float* part) {
     VLA_REQUIRE(n > 0 && C > 0 && n % C == 0 && o && idn && gamma && beta, "add_relu_film: bad arguments");
+    if (C % 4 == 0 && n / 4 < INT32_MAX && aligned(o, 16) && aligned(idn, 16) && aligned(gamma, 16) &&
+        aligned(beta, 16)) {
+        const int g = part_grid(n / 4, part);
+        add_relu_film4_kernel<<<g, 256, 0, st>>>(reinterpret_cast<float4*>(o), reinterpret_cast<const float4*>(idn),
+                                                 (int)(n / 4), C / 4, reinterpret_cast<const float4*>(gamma),
+                                                 reinterpret_cast<const float4*>(beta), part);
+        VLA_LAUNCH_CHECK();
+        return g;
+    }
     const int g = part_grid(n, part);
     add_relu_film_kernel<<<g, 256, 0, st>>>(o, idn, n, C, gamma, beta, part);
     VLA_LAUNCH_CHECK();
@@ -248,6 +355,12 @@ int launch_add_relu_film(float* o, const float* idn, int64_t n, int C, const flo
 }
 
 int launch_relu_inplace(float* x, int64_t n, hipStream_t st, float* part) {
+    if (n % 4 == 0 && n / 4 < INT32_MAX && aligned(x, 16)) {
+        const int g = part_grid(n / 4, part);
+        relu4_kernel<<<g, 256, 0, st>>>(reinterpret_cast<float4*>(x), (int)(n / 4), part);
+        VLA_LAUNCH_CHECK();
+        return g;
+    }
     const int g = part_grid(n, part);
     relu_kernel<<<g, 256, 0, st>>>(x, n, part);
     VLA_LAUNCH_CHECK();
