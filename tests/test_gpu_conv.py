@@ -66,19 +66,26 @@ def test_conv2d_i8_dev_form(vla, orc, torch_cuda, shape):
 
 
 # the implicit form (>= 256 output tiles of 64 x 64, or 1x1) and, with fewer
-# tiles, the im2col rows: ragged rows and channels, 18 K steps
+# tiles, the im2col rows: ragged rows and channels, 18 K steps; then inputs
+# of 1-4 channels, which take the word-per-pixel form (kernels up to 8 x 8,
+# strides 1-4, channel counts off the 64-wide block; 30 channels, not a
+# multiple of 4, keep the im2col rows)
 IMPLICIT_SHAPES = [(128, 128, 64, 64, 3, 1, 1), (30, 40, 256, 512, 1, 2, 0), (161, 203, 64, 48, 5, 3, 2),
                    (131, 121, 128, 100, 3, 1, 1), (33, 29, 64, 36, 1, 1, 0), (15, 20, 512, 512, 3, 1, 1),
-                   (20, 20, 128, 100, 3, 2, 1), (56, 56, 64, 64, 3, 1, 1)]
+                   (20, 20, 128, 100, 3, 2, 1), (56, 56, 64, 64, 3, 1, 1),
+                   (224, 224, 3, 64, 7, 2, 3), (97, 131, 1, 20, 5, 1, 2), (33, 47, 2, 36, 3, 2, 1),
+                   (40, 30, 4, 72, 7, 3, 3), (50, 50, 3, 16, 8, 4, 2), (64, 48, 3, 30, 3, 2, 1)]
 
 
 @pytest.mark.parametrize("shape", IMPLICIT_SHAPES)
 def test_conv2d_i8_implicit_and_im2col_forms(vla, orc, shape, monkeypatch):
     """Input channels a multiple of 64 over enough output tiles (or 1x1)
-    take the implicit GEMM (the int8 map gathered per tap);
-    VLA_HIP_CONV_IMPLICIT=0 (read per call) forces the im2col rows. Both
-    bit-exact with the oracle: ragged output tiles (48, 100, 36 channels),
-    pixel counts off the 64-row tile, stride 3, padding 2."""
+    take the implicit GEMM (the int8 map gathered per tap), 1-4 input
+    channels the word-per-pixel form (zero bytes past the channels and past
+    the last tap add nothing to the int32 sums); VLA_HIP_CONV_IMPLICIT=0
+    (read per call) forces the im2col rows. Both bit-exact with the oracle:
+    ragged output tiles (48, 100, 36, 20, 72 channels), pixel counts off the
+    64-row tile, strides 2-4, padding 2-3."""
     H, Wd, Cin, Cout, k, s, p = shape
     x, W, b = _case(shape, seed=11)
     Wq, ws = orc.quantize_weights_i8(W.reshape(Cout, -1))

@@ -96,6 +96,38 @@ __global__ __launch_bounds__(256) void im2col_f32x4_kernel(float* __restrict__ c
     }
 }
 
+// The same columns for any Cin (the 3-channel stem) with K <= 256 and 32-bit
+// sizes: a wave per output pixel, its lanes walking the row (coalesced
+// stores), each lane's taps (ky, kx, ci) decomposed once; values identical
+// to im2col_f32_kernel's.
+__global__ __launch_bounds__(256) void im2col_f32_rows_kernel(float* __restrict__ col, int ldc,
+                                                              const float* __restrict__ x, int H, int Wd, int Cin,
+                                                              int k, int stride, int pad, int Wout, int npix) {
+    const int lane = threadIdx.x & 63;
+    const int K = k * k * Cin;
+    int dy[4], dx[4], ci[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int r = lane + 64 * j, t = r / Cin;
+        ci[j] = r - t * Cin;
+        dy[j] = t / k;
+        dx[j] = t - dy[j] * k;
+    }
+    for (int p = blockIdx.x * 4 + (threadIdx.x >> 6); p < npix; p += gridDim.x * 4) {
+        const int oy = p / Wout, ox = p - oy * Wout;
+        const int y0 = oy * stride - pad, x0 = ox * stride - pad;
+        float* crow = col + (size_t)p * ldc;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int r = lane + 64 * j;
+            if (r >= K) break;
+            const int iy = y0 + dy[j], ix = x0 + dx[j];
+            const bool in = iy >= 0 && iy < H && ix >= 0 && ix < Wd;
+            crow[r] = in ? x[(iy * Wd + ix) * Cin + ci[j]] : 0.0f;
+        }
+    }
+}
+
 // maxpool2d_relu (src/hal/common/conv.cpp:192-224): padded taps count as -inf,
 // then the folded ReLU (!(v > 0) -> 0).
 __global__ __launch_bounds__(256) void maxpool_relu_kernel(float* __restrict__ out, const float* __restrict__ x, int H,
@@ -298,6 +330,10 @@ void launch_im2col_f32(float* col, int ldc, const float* x, int H, int Wd, int C
         const int64_t t4 = total / 4;
         im2col_f32x4_kernel<<<grid_for(t4), 256, 0, st>>>(col, ldc, x, H, Wd, Cin, k, stride, pad, Wout, (int)(K / 4),
                                                           (int)t4);
+    } else if (K <= 256 && (int64_t)H * Wd * Cin < INT32_MAX && (int64_t)Hout * Wout < INT32_MAX) {
+        const int npix = Hout * Wout;
+        const int blocks = (npix + 3) / 4 < 16384 ? (npix + 3) / 4 : 16384;
+        im2col_f32_rows_kernel<<<blocks, 256, 0, st>>>(col, ldc, x, H, Wd, Cin, k, stride, pad, Wout, npix);
     } else {
         im2col_f32_kernel<<<grid_for(total), 256, 0, st>>>(col, ldc, x, H, Wd, Cin, k, stride, pad, Wout, total);
     }

@@ -336,6 +336,115 @@ __global__ __launch_bounds__(256) void conv_i8_implicit(ImplicitArgs a) {
     }
 }
 
+// Inputs of at most 4 channels (the RGB stem): the input quantized once into
+// one 32-bit word per pixel (its channels' bytes, the rest zero), and an
+// implicit GEMM over K' = taps x 4 bytes. Zero bytes add nothing to the int32
+// sums, so every sum - and, through the same epilogue, every output - equals
+// the im2col path's. x [H * Wd, Cin] fp32 -> q [H * Wd] words; scale to *s_out.
+// The same launch lays the weights out in K' order once: wc [N][KB / 4] words
+// (tap t's word holds W[n][t * Cin + ci] in byte ci; zero past Cin and past
+// the last tap).
+__global__ __launch_bounds__(256) void conv_quant_c4_kernel(const float* __restrict__ x, int npx, int Cin,
+                                                            uint32_t* __restrict__ q, const float* __restrict__ part,
+                                                            int nparts, float clip, float* __restrict__ s_out,
+                                                            const int8_t* __restrict__ W, int ldw, int kk, int N,
+                                                            int KW, uint32_t* __restrict__ wc) {
+    __shared__ float red[4];
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < N * KW; i += gridDim.x * blockDim.x) {
+        const int n = i / KW, t = i - n * KW;
+        uint32_t w = 0;
+        if (t < kk)
+            for (int c = 0; c < Cin; c++) w |= (uint32_t)(uint8_t)W[(size_t)n * ldw + t * Cin + c] << (8 * c);
+        wc[i] = w;
+    }
+    const float s = fold_scale(part, nparts, clip, red);
+    const float inv = 1.0f / s;
+    if (blockIdx.x == 0 && threadIdx.x == 0) *s_out = s;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < npx; i += gridDim.x * blockDim.x) {
+        const float* px = x + (size_t)i * Cin;
+        uint32_t w = 0;
+        for (int c = 0; c < Cin; c++) w |= (uint32_t)(q8(px[c], inv) & 0xff) << (8 * c);
+        q[i] = w;
+    }
+}
+
+struct C4Args {
+    const uint32_t* xq;  // [H, Wd] words
+    int H, Wd, Cin, k, stride, pad, Wout, npix;
+    const int8_t* wc;    // [N][KS * 64] bytes in K' order (conv_quant_c4_kernel)
+    const float* wscale;
+    const float* bias;
+    const float* s;
+    float* out;          // [npix, N]
+    int N, KS;           // KS: 64-byte K steps of K' = k * k * 4
+};
+
+// 64 pixels x 64 output channels per block, a wave per 16 pixels (4 MFMA
+// fragments across the channels). The block first copies its channels'
+// K'-ordered weights into LDS; each lane of a wave then gathers, per K step,
+// the 4 words of its pixel's taps 16 s + 4 (l / 16) .. + 3 (zero outside the
+// image) as its A fragment. The weight fragment goes first: lane l holds
+// pixel l % 16 and the four consecutive channels 4 (l / 16) .. + 3, stored
+// as one float4.
+constexpr int kC4MaxKS = 4;  // K' <= 256 bytes: k <= 8
+__global__ __launch_bounds__(256) void conv_i8_c4(C4Args a) {
+    constexpr int SB = 64 * kC4MaxKS + 16;  // LDS row per channel, bytes
+    __shared__ __attribute__((aligned(16))) int8_t wl[64 * SB];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n0 = blockIdx.x * 64, kk = a.k * a.k, KB = a.KS * 64;
+    for (int e = tid; e < 64 * a.KS * 4; e += 256) {  // 16-byte chunks: channel e / (4 KS), chunk e % (4 KS)
+        const int c = e / (4 * a.KS), b = (e - c * 4 * a.KS) * 16;
+        const int n = n0 + c < a.N ? n0 + c : a.N - 1;
+        *reinterpret_cast<v4i*>(wl + c * SB + b) = *reinterpret_cast<const v4i*>(a.wc + (size_t)n * KB + b);
+    }
+    const int r16 = lane & 15, g = lane >> 4;
+    const int m = blockIdx.y * 64 + wave * 16 + r16;
+    const int mc = m < a.npix ? m : a.npix - 1;
+    const int oy = mc / a.Wout, ox = mc - oy * a.Wout;
+    const int iy0 = oy * a.stride - a.pad, ix0 = ox * a.stride - a.pad;
+    v4i acc[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[j] = v4i{0, 0, 0, 0};
+    __syncthreads();
+    for (int st = 0; st < a.KS; st++) {
+        int w4[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) {
+            const int t = st * 16 + g * 4 + u;
+            const int ky = t / a.k, kx = t - ky * a.k;
+            const int iy = iy0 + ky, ix = ix0 + kx;
+            w4[u] = (t < kk && iy >= 0 && iy < a.H && ix >= 0 && ix < a.Wd) ? (int)a.xq[iy * a.Wd + ix] : 0;
+        }
+        const v4i af = v4i{w4[0], w4[1], w4[2], w4[3]};
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const v4i bf = *reinterpret_cast<const v4i*>(wl + (j * 16 + r16) * SB + st * 64 + g * 16);
+            acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf, af, acc[j], 0, 0, 0);
+        }
+    }
+    if (m >= a.npix) return;
+    // epilogue: fma((float)acc * ws[n], s, b[n]) per output (gemm_i8.cpp:278)
+    const float s = *a.s;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int nb = n0 + j * 16 + g * 4;
+        if (nb >= a.N) break;
+        float v[4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int nc = nb + c < a.N ? nb + c : a.N - 1;
+            const float p = (float)acc[j][c] * a.wscale[nc];
+            v[c] = fmaf(p, s, a.bias ? a.bias[nc] : 0.0f);
+        }
+        float* o = a.out + (size_t)m * a.N + nb;
+        if (nb + 4 <= a.N) {
+            *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+            for (int c = 0; c < 4 && nb + c < a.N; c++) o[c] = v[c];
+        }
+    }
+}
+
 bool conv_implicit_on() {
     const char* e = std::getenv("VLA_HIP_CONV_IMPLICIT");
     return !(e && e[0] == '0' && e[1] == '\0');
@@ -374,8 +483,10 @@ ConvShape conv_shape(int H, int Wd, int Cin, int k, int stride, int pad, int Cou
     c.npix = c.Hout * c.Wout;
     c.lda = (kpad4(c.K) + 63) & ~63;
     c.split = gemm_split_bytes(c.npix, Cout, c.K);
-    // the A region holds the im2col rows, or the int8 input of the implicit form
-    const size_t arows = (size_t)c.npix * c.lda > (size_t)H * Wd * Cin ? (size_t)c.npix * c.lda : (size_t)H * Wd * Cin;
+    // the A region holds the im2col rows, or the int8 input of the implicit
+    // forms (one word per pixel up to 4 channels, then the K'-ordered weights)
+    const size_t qin = Cin <= 4 ? ((size_t)H * Wd * 4 + 255) / 256 * 256 + (size_t)Cout * 256 : (size_t)H * Wd * Cin;
+    const size_t arows = (size_t)c.npix * c.lda > qin ? (size_t)c.npix * c.lda : qin;
     c.work = (size_t)kAbsmaxBlocks * 4 + ((size_t)c.npix * 4 + 255) / 256 * 256 + (arows + 255) / 256 * 256 +
              c.split;
     return c;
@@ -422,6 +533,22 @@ void launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
         ImplicitArgs ia{A, a.H, a.Wd, a.Cin, a.k, a.stride, a.pad, c.Wout, c.npix, a.Wq, a.ldw, a.wscale,
                         a.bias, ascale, a.out, a.Cout, c.K};
         conv_i8_implicit<<<dim3((a.Cout + 63) / 64, (c.npix + 63) / 64), 256, 0, st>>>(ia);
+        VLA_LAUNCH_CHECK();
+        return;
+    }
+
+    if (a.Cin <= 4 && a.k * a.k * 4 <= 64 * kC4MaxKS && a.Cout % 4 == 0 &&
+        (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 && (c.npix + 63) / 64 <= 65535 && conv_implicit_on()) {
+        const int npx = a.H * a.Wd, KS = (a.k * a.k * 4 + 63) / 64;
+        const int qb = (npx + 255) / 256 < 2048 ? (npx + 255) / 256 : 2048;
+        int8_t* wc = A + ((size_t)npx * 4 + 255) / 256 * 256;
+        conv_quant_c4_kernel<<<qb, 256, 0, st>>>(a.x, npx, a.Cin, reinterpret_cast<uint32_t*>(A), maxima, blocks,
+                                                 clip, ascale, a.Wq, a.ldw, a.k * a.k, a.Cout, KS * 16,
+                                                 reinterpret_cast<uint32_t*>(wc));
+        VLA_LAUNCH_CHECK();
+        C4Args ca{reinterpret_cast<const uint32_t*>(A), a.H, a.Wd, a.Cin, a.k, a.stride, a.pad, c.Wout, c.npix,
+                  wc, a.wscale, a.bias, ascale, a.out, a.Cout, KS};
+        conv_i8_c4<<<dim3((a.Cout + 63) / 64, (c.npix + 63) / 64), 256, 0, st>>>(ca);
         VLA_LAUNCH_CHECK();
         return;
     }

@@ -134,7 +134,8 @@ public:
 private:
     struct Conv {
         int cin = 0, cout = 0, k = 0, stride = 1, pad = 0;
-        float* W = nullptr;  // fp32 [cout, k * k * cin]
+        int ldw = 0;         // W's row stride: k * k * cin rounded up to 4 (zero pad)
+        float* W = nullptr;  // fp32 [cout, ldw]
         float* b = nullptr;  // [cout], null under GroupNorm
         const float *gs = nullptr, *gb = nullptr;  // GroupNorm scale / bias [cout]
         std::unique_ptr<vla_linear_i8> q8;  // conv2d_i8 weights when the stage is int8

@@ -75,8 +75,19 @@ ResNetTrunk::ResNetTrunk(const CkptFiles& files, const std::string& name, int in
         c.cin = cin;
         c.stride = stride;
         c.pad = pad;
-        const float* W = take.take((size_t)cout * k * k * cin, bbin.c_str());
-        c.W = A_.upload(W, (size_t)cout * k * k * cin);
+        const size_t K = (size_t)k * k * cin;
+        const float* W = take.take((size_t)cout * K, bbin.c_str());
+        // rows padded to 4 floats (the stem's 147 -> 148), which the fp32
+        // matrix-core GEMM needs; the pad is zero and the GEMM masks it anyway
+        c.ldw = (int)((K + 3) & ~(size_t)3);
+        if ((size_t)c.ldw == K) {
+            c.W = A_.upload(W, (size_t)cout * K);
+        } else {
+            std::vector<float> padded((size_t)cout * c.ldw, 0.0f);
+            for (int o = 0; o < cout; o++)
+                std::copy(W + (size_t)o * K, W + (size_t)(o + 1) * K, padded.begin() + (size_t)o * c.ldw);
+            c.W = A_.upload(padded.data(), padded.size());
+        }
         if (!gs) {
             const float* b = take.take(cout, bbin.c_str());
             c.b = A_.upload(b, cout);
@@ -267,7 +278,7 @@ int ResNetTrunk::conv(const Conv& c, const float* x, int H, int W, float* out, b
                 launch_im2col_f32(col_, ldx, x, H, W, c.cin, c.k, c.stride, c.pad, Ho, Wo, st);
                 rows = col_;
             }
-            launch_linear_f32(out, c.cout, rows, ldx, c.W, K, c.b, Ho * Wo, c.cout, K, conv_relu ? 1 : 0, 0, 1.0f, st,
+            launch_linear_f32(out, c.cout, rows, ldx, c.W, c.ldw, c.b, Ho * Wo, c.cout, K, conv_relu ? 1 : 0, 0, 1.0f, st,
                               part, part_f);
         }
     }
