@@ -462,6 +462,13 @@ constexpr int kCUs = 256;  // MI355X compute units
 struct F32Split {
     int S = 1, kchunk = 0;
 };
+// VLA_HIP_F32_SMALL_TILES=0 keeps 64 x 64 tiles for few-tile fp32 layers
+// (read per call; A/B runs)
+static bool f32_small_tiles_on() {
+    const char* e = std::getenv("VLA_HIP_F32_SMALL_TILES");
+    return !(e && e[0] == '0' && e[1] == '\0');
+}
+
 F32Split f32_split_plan(int M, int N, int K) {
     F32Split p;
     const long t64 = (long)((M + 63) / 64) * ((N + 63) / 64);
@@ -541,12 +548,19 @@ void launch_linear_f32(float* out, int ldo, const float* x, int ldx, const float
             VLA_LAUNCH_CHECK();
             return;
         }
-        // 128 x 64 tiles when they still give every CU work, else 64 x 64
+        // 128 x 64 tiles when they still give every CU work, 64 x 64 from 128
+        // such tiles, else 32 x 32 (a fourth of the fp32 matrix work per
+        // block: Octo's 256 x 768 x 512 token projections, 48 tiles of 64 x
+        // 64, were ~20 us each, one fp32 MFMA chain of a whole tile per CU)
         const long t128 = (long)((M + 127) / 128) * ((N + 63) / 64);
         if (t128 >= 256) {
             const dim3 grid((N + 63) / 64, (M + 127) / 128);
             linear_f32_tiled<128, 64><<<grid, 256, 0, st>>>(out, ldo, x, ldx, W, ldw, bias, M, N, K, act,
                                                             accumulate, alpha, ConvGeom{}, nullptr, 0);
+        } else if (t64 < 128 && f32_small_tiles_on()) {
+            const dim3 grid((N + 31) / 32, (M + 31) / 32);
+            linear_f32_tiled<32, 32><<<grid, 256, 0, st>>>(out, ldo, x, ldx, W, ldw, bias, M, N, K, act,
+                                                           accumulate, alpha, ConvGeom{}, nullptr, 0);
         } else {
             const dim3 grid((N + 63) / 64, (M + 63) / 64);
             linear_f32_tiled<64, 64><<<grid, 256, 0, st>>>(out, ldo, x, ldx, W, ldw, bias, M, N, K, act,
