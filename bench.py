@@ -384,8 +384,13 @@ def _lat_act_model(vla, torch, ck, ob, tmp, stream_obj, act_int8):
     gpu = _time_calls(torch, lambda: m.predict_dev(ti, ts, ta, True, st), stream_obj)
     row = {"gpu_ms": round(gpu, 4), "image": f"{c['n_cams']}x{c['img_h']}x{c['img_w']}", "act_int8": act_int8,
            "int8_convs": m.int8_convs, "int8_layers": m.int8_layers, "graph_nodes": m.graph_nodes}
+    # the backbone alone (vla_act_encode_dev: normalization + ResNet-18, one
+    # graph replay per call)
+    tf = torch.empty((m.n_cams * m.feat_h * m.feat_w, m.feat_ch), dtype=torch.float32, device=dev)
+    row["backbone_gpu_ms"] = round(_time_calls(torch, lambda: m.encode_dev(ti, tf, st), stream_obj), 4)
     if r is not None:
         row["cpu_ref_ms"] = round(_time_cpu(lambda: r.predict(images, state)), 3)
+        row["backbone_cpu_ref_ms"] = round(_time_cpu(lambda: r.encode(images)), 3)
     return row
 
 

@@ -610,11 +610,13 @@ VLA_API int32_t vla_act_predict(void* h, const uint8_t* images, const float* sta
 /* Extensions with no counterpart in vla_simd.h: predict on device pointers
  * and a stream (asynchronous; the frames are copied before the call returns
  * to the stream's order), the backbone alone (ActModel::encode_view for every
- * camera: feats [n_cams * fh * fw, ch], host pointers), its feature grid, and
- * the counts of int8 backbone convs / transformer layers and graph nodes. */
+ * camera: feats [n_cams * fh * fw, ch], host pointers, or device pointers and
+ * a stream, as predict_dev), its feature grid, and the counts of int8
+ * backbone convs / transformer layers and graph nodes. */
 VLA_API int32_t vla_act_predict_dev(void* h, const uint8_t* images, const float* state,
                                     int32_t unnormalize, float* actions, void* stream);
 VLA_API int32_t vla_act_encode(void* h, const uint8_t* images, float* feats);
+VLA_API int32_t vla_act_encode_dev(void* h, const uint8_t* images, float* feats, void* stream);
 VLA_API int32_t vla_act_feat_shape(void* h, int32_t* fh, int32_t* fw, int32_t* ch);
 VLA_API int32_t vla_act_int8_convs(void* h);
 VLA_API int32_t vla_act_int8_layers(void* h);

@@ -196,6 +196,37 @@ def test_int8_backbone(vla, small_dir, env, frm, to):
     assert np.all(np.isfinite(a))
 
 
+def test_int8_backbone_fused_epilogues_full_size(vla, env, tmp_path):
+    """ResNet-18 at 480 x 640, every conv int8 (ACT_INT8=63): each block's
+    ReLU after conv1 and residual add + ReLU after conv2 run in the conv's
+    epilogue - the implicit conv (120 x 160 maps), the 32 x 64 LDS GEMM tile
+    (4800 and 1200 rows), the skinny GEMM (300 rows) - which also writes the
+    block maxima the next conv folds into its scale. The features are the
+    reference's bit for bit, and the same bits as with VLA_HIP_CONV_FUSE=0
+    (separate passes), on the eager, the captured and a replayed call."""
+    ck = _ck()
+    from helpers import oracle
+    ob = oracle()
+    c = ck.ACT_MODEL_BASE
+    d = ck.write_act_model(str(tmp_path / "act_full"), c)
+    env(ACT_INT8=63)
+    images, _ = ck.act_model_inputs(c)
+    ref = ob.RefActModel(d).encode(images)
+    os.environ["VLA_HIP_CONV_FUSE"] = "0"
+    try:
+        m0 = vla.ActModel(d)
+        assert m0.int8_convs == 20
+        passes = [m0.encode(images) for _ in range(3)]
+    finally:
+        del os.environ["VLA_HIP_CONV_FUSE"]
+    m1 = vla.ActModel(d)
+    fused = [m1.encode(images) for _ in range(3)]
+    print(f"int8 trunk 480x640: graph nodes {m0.graph_nodes} with passes, {m1.graph_nodes} fused", flush=True)
+    assert m1.graph_nodes < m0.graph_nodes
+    for i, f in enumerate(passes + fused):
+        assert f.tobytes() == ref.tobytes(), f"call {i}: features differ (rel {_rel(f, ref):.3e})"
+
+
 def test_act_model_full_size(vla, env, tmp_path):
     """BASELINE's ACT shape end to end: one 480 x 640 camera through ResNet-18
     (15 x 20 x 512 features) into the 4-layer d=512 transformer, ACT_INT8=31."""

@@ -77,7 +77,8 @@ EXPORTS = (
     "vla_probe_begin", "vla_probe_end", "vla_probe_count", "vla_probe_shape", "vla_probe_read",
     "vla_act_load", "vla_act_free", "vla_act_chunk", "vla_act_action_dim", "vla_act_state_dim",
     "vla_act_n_cams", "vla_act_img_h", "vla_act_img_w", "vla_act_predict", "vla_act_predict_dev",
-    "vla_act_encode", "vla_act_feat_shape", "vla_act_int8_convs", "vla_act_int8_layers", "vla_act_graph_nodes",
+    "vla_act_encode", "vla_act_encode_dev", "vla_act_feat_shape", "vla_act_int8_convs", "vla_act_int8_layers",
+    "vla_act_graph_nodes",
     "vla_impact_load", "vla_impact_free", "vla_impact_chunk", "vla_impact_action_dim", "vla_impact_state_dim",
     "vla_impact_n_cams", "vla_impact_img_h", "vla_impact_img_w", "vla_impact_n_text", "vla_impact_set_instruction",
     "vla_impact_predict", "vla_impact_tokens", "vla_impact_film", "vla_impact_predict_dev",
@@ -260,6 +261,7 @@ def _declare(L):
         "vla_act_predict": (i32, [P, P, P, i32, P]),
         "vla_act_predict_dev": (i32, [P, P, P, i32, P, P]),
         "vla_act_encode": (i32, [P, P, P]),
+        "vla_act_encode_dev": (i32, [P, P, P, P]),
         "vla_act_feat_shape": (i32, [P, P, P, P]),
         "vla_act_int8_convs": (i32, [P]),
         "vla_act_int8_layers": (i32, [P]),
@@ -986,6 +988,16 @@ class ActModel(_Handle):
         out = np.empty((self.n_cams * self.feat_h * self.feat_w, self.feat_ch), np.float32)
         _call("vla_act_encode", self.h, _ptr(images), _ptr(out))
         return out
+
+    def encode_dev(self, images, out, stream=None):
+        """The backbone on device tensors: images uint8 [n_cams, img_h, img_w, 3],
+        out float32 [n_cams * feat_h * feat_w, feat_ch], on the given stream."""
+        n_in, n_out = self.n_cams * self.img_h * self.img_w * 3, self.n_cams * self.feat_h * self.feat_w * self.feat_ch
+        if images.numel() != n_in or images.element_size() != 1 or not images.is_contiguous():
+            raise ValueError(f"images: need {n_in} contiguous uint8 values on the device")
+        if out.numel() != n_out or out.element_size() != 4 or not out.is_contiguous():
+            raise ValueError(f"out: need {n_out} contiguous float32 values on the device")
+        _call("vla_act_encode_dev", self.h, _dp(images), _dp(out), _stream(stream))
 
 
 class ImpactModel(_Handle):

@@ -19,6 +19,9 @@ namespace vla {
 namespace hip {
 
 __device__ __forceinline__ float act_relu(float v) { return v < 0.0f ? 0.0f : v; }
+// The ReLU of ResNet's residual add (x > 0 ? x : 0: -0 and NaN give +0),
+// shared by the add + ReLU pass and the conv epilogue that fuses it.
+__device__ __forceinline__ float relu_gt(float v) { return v > 0.0f ? v : 0.0f; }
 
 __device__ __forceinline__ float act_gelu_tanh(float v) {
     const float c = 0.7978845608028654f;

@@ -7,6 +7,7 @@
 // Layouts are the reference's: images uint8 HWC, feature maps NHWC fp32
 // [H, W, C], conv weights [Cout][k][k][Cin], so an im2col row is the taps
 // [ky][kx][ci] of one output pixel (src/hal/common/conv.cpp:117-176).
+#include "act.h"
 #include "common.h"
 #include "wave.h"
 
@@ -197,7 +198,6 @@ __global__ __launch_bounds__(256) void add_relu_film_kernel(float* __restrict__ 
 // same; the scalar forms loop over 64-bit element indices and stay for the
 // shapes these do not take.
 __device__ __forceinline__ float pool_max(float v, float o) { return v > o ? v : o; }
-__device__ __forceinline__ float relu_gt(float v) { return v > 0.0f ? v : 0.0f; }
 
 __global__ __launch_bounds__(256) void maxpool_relu4_kernel(float4* __restrict__ out, const float4* __restrict__ x, int H,
                                                             int Wd, int C4, int k, int stride, int pad, int Wout,

@@ -462,6 +462,11 @@ VLA_API int32_t vla_act_encode(void* h, const uint8_t* images, float* feats) {
     });
 }
 
+VLA_API int32_t vla_act_encode_dev(void* h, const uint8_t* images, float* feats, void* stream) {
+    if (!h || !images || !feats) return VLA_ERR_ARG;
+    return guarded("vla_act_encode_dev", [&] { act_model(h)->encode_dev(images, feats, as_stream(stream)); });
+}
+
 // --------------------------------------------------- IMPACT (model level) --
 // The reference's IMPACT entry points (include/vla_simd.h:206-243,
 // src/models/impact/impact_capi.cpp), same names, signatures and status codes.

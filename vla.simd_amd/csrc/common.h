@@ -111,8 +111,21 @@ struct GemmArgs {
     // launch_rope_table would rotate them in place afterwards; null: none.
     const double* rope_cs;
     int rope_cols, rope_hd;
+    // Convolution epilogue (launch_gemm_i8_conv only): with resid, out =
+    // relu_gt(v + resid[m][n]) (stride ldo), the residual add + ReLU of a
+    // ResNet block; without it act must be 1 (ReLU). omax receives the max
+    // |out| per wave (gemm_i8_lds) or per block (skinny), the block maxima
+    // the next conv2d_i8 folds into its scale.
+    const float* resid;
+    float* omax;
 };
 void launch_gemm_i8(const GemmArgs& a, hipStream_t st);
+// The product with the convolution epilogue above when the kernel
+// launch_gemm_i8 would pick for the shape carries it (the unsplit skinny
+// kernel, or the 32 x 64 x 128 LDS tile) and its maxima fit in 4096 floats:
+// returns how many maxima it wrote. Returns 0, launching nothing, otherwise;
+// the caller then runs launch_gemm_i8 and the separate ReLU pass.
+int launch_gemm_i8_conv(const GemmArgs& a, hipStream_t st);
 // Two independent products over the same rows as one skinny launch (same
 // bits as two launch_gemm_i8 calls). Returns false, launching nothing, when
 // either would not take the unsplit skinny kernel; the caller then runs them
@@ -214,12 +227,23 @@ struct ConvArgs {
     // floats, their max = max |x|); then no absmax pass over x runs
     const float* in_part = nullptr;
     int in_nparts = 0;
+    // optional (a ResNet trunk's producer chain): out_part receives the block
+    // maxima of |out| (at most 4096 floats) when the kernel taking the shape
+    // fuses the epilogue that follows the conv - ReLU, or with resid ([npix,
+    // Cout], 16-byte aligned) the residual add + ReLU (relu_gt(v + resid)).
+    // The launcher then returns how many maxima it wrote; 0 means it ran the
+    // plain conv, and the caller applies the ReLU pass itself.
+    float* out_part = nullptr;
+    const float* resid = nullptr;
 };
-void launch_conv2d_i8(const ConvArgs& a, hipStream_t st);
+int launch_conv2d_i8(const ConvArgs& a, hipStream_t st);
 // Producers of a conv2d_i8 input that also write its block maxima (part:
 // at most kConvPartMax floats per launch, per camera for the normalization;
 // the launchers return how many) so the conv skips its absmax pass.
 constexpr int kConvPartMax = 512;
+// The most block maxima a conv2d_i8 folds, and so the most a fused conv
+// epilogue may write (ConvArgs::out_part, GemmArgs::omax).
+constexpr int kConvPartsFused = 4096;
 
 // backbone.hip: ACT's image backbone around its GEMMs (NHWC fp32 maps)
 // (pixel / 255 - mean[cam][c]) / (std[cam][c] + eps) for n_cams frames of npx pixels

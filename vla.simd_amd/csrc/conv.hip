@@ -45,6 +45,7 @@
 //   launch_gemm_i8      the int8 GEMM with its fused epilogue.
 // The im2col matrix is materialised: npix * round64(K) bytes (e.g. 11 MiB for
 // a 480x640 ResNet stem), a few microseconds of HBM next to the GEMM.
+#include "act.h"
 #include "common.h"
 #include "quant_row.h"
 
@@ -234,6 +235,11 @@ struct ImplicitArgs {
     const float* s;    // the activation scale (device)
     float* out;        // [npix, N]
     int N, K;
+    // the trunk's fused epilogue: act 1 = ReLU, or resid [npix, N] added
+    // before relu_gt; omax: each wave's max |out| at [block][wave]
+    int act;
+    const float* resid;
+    float* omax;
 };
 
 // 64 x 64 output tile per block, 4 waves in a 2 x 2 grid (32 x 32 each: 2 x 2
@@ -312,6 +318,7 @@ __global__ __launch_bounds__(256) void conv_i8_implicit(ImplicitArgs a) {
     }
     // epilogue: fma((float)acc * ws[n], s, b[n]) per output (gemm_i8.cpp:278)
     const float s = *a.s;
+    float mx = 0.0f;
 #pragma unroll
     for (int i = 0; i < 2; i++) {
         const int mo = m0 + wm * 32 + i * 16 + r16;
@@ -326,6 +333,24 @@ __global__ __launch_bounds__(256) void conv_i8_implicit(ImplicitArgs a) {
                 const float p = (float)acc[i][j][c] * a.wscale[nc];
                 v[c] = fmaf(p, s, a.bias ? a.bias[nc] : 0.0f);
             }
+            if (a.resid) {  // the block's residual add + ReLU
+                const float* rr = a.resid + (size_t)mo * a.N + nb;
+                if (nb + 4 <= a.N) {
+                    const float4 r = *reinterpret_cast<const float4*>(rr);
+                    v[0] = relu_gt(v[0] + r.x);
+                    v[1] = relu_gt(v[1] + r.y);
+                    v[2] = relu_gt(v[2] + r.z);
+                    v[3] = relu_gt(v[3] + r.w);
+                } else {
+                    for (int c = 0; c < 4 && nb + c < a.N; c++) v[c] = relu_gt(v[c] + rr[c]);
+                }
+            } else if (a.act) {
+#pragma unroll
+                for (int c = 0; c < 4; c++) v[c] = act_relu(v[c]);
+            }
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                if (nb + c < a.N) mx = fmaxf(mx, fabsf(v[c]));
             float* o = a.out + (size_t)mo * a.N + nb;
             if (nb + 4 <= a.N) {
                 *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
@@ -333,6 +358,10 @@ __global__ __launch_bounds__(256) void conv_i8_implicit(ImplicitArgs a) {
                 for (int c = 0; c < 4 && nb + c < a.N; c++) o[c] = v[c];
             }
         }
+    }
+    if (a.omax) {
+        mx = wave_max_f32(mx);
+        if (lane == 0) a.omax[(blockIdx.y * gridDim.x + blockIdx.x) * 4 + wave] = mx;
     }
 }
 
@@ -492,7 +521,7 @@ ConvShape conv_shape(int H, int Wd, int Cin, int k, int stride, int pad, int Cou
     return c;
 }
 
-void launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
+int launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
     const ConvShape c = conv_shape(a.H, a.Wd, a.Cin, a.k, a.stride, a.pad, a.Cout);
     VLA_REQUIRE(a.x && a.out && a.Wq && a.wscale && a.work, "conv2d_i8: null buffer");
     VLA_REQUIRE(a.ldw >= kpad4(c.K) && a.ldw % 4 == 0, "conv2d_i8: bad weight rows");
@@ -509,7 +538,7 @@ void launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
     const float* maxima = part;
     if (a.in_part) {
         // the producer of x wrote its block maxima: no pass over x here
-        VLA_REQUIRE(a.in_nparts > 0 && a.in_nparts <= 4096, "conv2d_i8: 1..4096 producer block maxima");
+        VLA_REQUIRE(a.in_nparts > 0 && a.in_nparts <= kConvPartsFused, "conv2d_i8: 1..4096 producer block maxima");
         maxima = a.in_part;
         blocks = a.in_nparts;
     } else {
@@ -532,9 +561,18 @@ void launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
         VLA_LAUNCH_CHECK();
         ImplicitArgs ia{A, a.H, a.Wd, a.Cin, a.k, a.stride, a.pad, c.Wout, c.npix, a.Wq, a.ldw, a.wscale,
                         a.bias, ascale, a.out, a.Cout, c.K};
-        conv_i8_implicit<<<dim3((a.Cout + 63) / 64, (c.npix + 63) / 64), 256, 0, st>>>(ia);
+        const dim3 grid((a.Cout + 63) / 64, (c.npix + 63) / 64);
+        int parts = 0;
+        if (a.out_part && (int64_t)grid.x * grid.y * 4 <= kConvPartsFused &&
+            (!a.resid || (reinterpret_cast<uintptr_t>(a.resid) & 15) == 0)) {
+            parts = (int)(grid.x * grid.y * 4);
+            ia.act = a.resid ? 0 : 1;
+            ia.resid = a.resid;
+            ia.omax = a.out_part;
+        }
+        conv_i8_implicit<<<grid, 256, 0, st>>>(ia);
         VLA_LAUNCH_CHECK();
-        return;
+        return parts;
     }
 
     if (a.Cin <= 4 && a.k * a.k * 4 <= 64 * kC4MaxKS && a.Cout % 4 == 0 &&
@@ -550,7 +588,7 @@ void launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
                   wc, a.wscale, a.bias, ascale, a.out, a.Cout, KS};
         conv_i8_c4<<<dim3((a.Cout + 63) / 64, (c.npix + 63) / 64), 256, 0, st>>>(ca);
         VLA_LAUNCH_CHECK();
-        return;
+        return 0;
     }
 
     Im2colArgs g{a.x, a.H, a.Wd, a.Cin, a.k, a.stride, a.pad, c.Wout, c.npix, c.K, c.lda, maxima, blocks,
@@ -585,7 +623,18 @@ void launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
         m.split_ws = reinterpret_cast<int32_t*>(w + c.work - c.split);
         m.split_bytes = c.split;
     }
+    if (a.out_part) {
+        m.act = a.resid ? 0 : 1;
+        m.resid = a.resid;
+        m.omax = a.out_part;
+        const int parts = launch_gemm_i8_conv(m, st);
+        if (parts > 0) return parts;
+        m.act = 0;
+        m.resid = nullptr;
+        m.omax = nullptr;
+    }
     launch_gemm_i8(m, st);
+    return 0;
 }
 
 }  // namespace hip

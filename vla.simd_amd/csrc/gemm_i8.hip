@@ -215,10 +215,20 @@ struct ColOps {
 // leave the epilogue bound by instruction fetch. All row-scale loads are
 // issued before the first use, so they share one wait (a later wait would
 // also count the output stores in flight).
-template <int TM, int TN, int FM, int FN, int KIND, int ACT, bool NT>
+// KIND 3 is a convolution's residual add + ReLU (out = relu_gt(v +
+// resid[m][n])); MX: the wave's max |out| over the rows below M goes to
+// *mx_out (max is order-free: the same as a separate pass's block maxima).
+template <int TM, int TN, int FM, int FN, int KIND, int ACT, bool NT, bool MX = false>
 __device__ __forceinline__ void epilogue_k(const GemmArgs& a, const v4i (&acc)[FM][FN], const ColOps<FN>& co,
-                                           int lane, int mw, int nw, float* stage) {
+                                           int lane, int mw, int nw, float* stage, float* mx_out = nullptr) {
     const int r16 = lane & 15, c4 = 4 * (lane >> 4);
+    float mx = 0.0f;
+    auto finish = [&]() {
+        if constexpr (MX) {
+            mx = wave_max_f32(mx);
+            if (lane == 0) *mx_out = mx;
+        }
+    };
     float sa[FM];
     if (KIND != 2) {
 #pragma unroll
@@ -249,6 +259,16 @@ __device__ __forceinline__ void epilogue_k(const GemmArgs& a, const v4i (&acc)[F
                 } else {
                     v = {value(i, j, 0), value(i, j, 1), value(i, j, 2), value(i, j, 3)};
                 }
+                if constexpr (KIND == 3) {
+                    const int m = mw + 16 * i + r16;
+                    const v4f r = *reinterpret_cast<const v4f*>(a.resid + (size_t)(m < a.M ? m : a.M - 1) * a.ldo +
+                                                                 nw + 16 * j + c4);
+                    v = {relu_gt(v[0] + r[0]), relu_gt(v[1] + r[1]), relu_gt(v[2] + r[2]), relu_gt(v[3] + r[3])};
+                }
+                if constexpr (MX) {
+                    if (mw + 16 * i + r16 < a.M)
+                        mx = fmaxf(fmaxf(mx, fmaxf(fabsf(v[0]), fabsf(v[1]))), fmaxf(fabsf(v[2]), fabsf(v[3])));
+                }
                 *reinterpret_cast<v4f*>(stage + r16 * LDW + 16 * j + c4) = v;
             }
             wave_lds_sync();
@@ -271,6 +291,7 @@ __device__ __forceinline__ void epilogue_k(const GemmArgs& a, const v4i (&acc)[F
             }
             wave_lds_sync();
         });
+        finish();
         return;
     }
     // tiles on the N edge, or row strides that are not whole vectors
@@ -288,19 +309,29 @@ __device__ __forceinline__ void epilogue_k(const GemmArgs& a, const v4i (&acc)[F
                             a.acc32[(size_t)m * a.N + n] = acc[i][j][q];
                         } else {
                             float* o = a.out + (size_t)m * a.ldo + n;
-                            const float v = value(i, j, q);
+                            float v = value(i, j, q);
+                            if constexpr (KIND == 3) v = relu_gt(v + a.resid[(size_t)m * a.ldo + n]);
+                            if constexpr (MX) mx = fmaxf(mx, fabsf(v));
                             *o = KIND == 1 ? *o + v : v;
                         }
                     }
                 }
         }
     });
+    finish();
 }
 
-// One run-time dispatch to the compile-time epilogue for this launch.
-template <int TM, int TN, int FM, int FN, bool NT>
+// One run-time dispatch to the compile-time epilogue for this launch (CONV:
+// only the convolution epilogues, ReLU or residual add + ReLU, with the
+// wave's maximum to mx_out).
+template <int TM, int TN, int FM, int FN, bool NT, bool CONV = false>
 __device__ __forceinline__ void epilogue(const GemmArgs& a, const v4i (&acc)[FM][FN], const ColOps<FN>& co,
-                                         int lane, int mw, int nw, float* stage) {
+                                         int lane, int mw, int nw, float* stage, float* mx_out = nullptr) {
+    if constexpr (CONV) {
+        if (a.resid) epilogue_k<TM, TN, FM, FN, 3, 0, NT, true>(a, acc, co, lane, mw, nw, stage, mx_out);
+        else epilogue_k<TM, TN, FM, FN, 0, 1, NT, true>(a, acc, co, lane, mw, nw, stage, mx_out);
+        return;
+    }
 #define VLA_EPI(KIND, ACT) epilogue_k<TM, TN, FM, FN, KIND, ACT, NT>(a, acc, co, lane, mw, nw, stage)
     if (a.acc32) {
         VLA_EPI(2, 0);
@@ -534,7 +565,7 @@ struct LdsCfg {
     static_assert(S >= 2 && (S - 2) * LPS < 64, "pipeline depth");
 };
 
-template <int BM, int BN, int BK, int S, int WM, int WN, bool PF>
+template <int BM, int BN, int BK, int S, int WM, int WN, bool PF, bool CONV = false>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds(GemmArgs a) {
     // Plain output stores on the 256 x 256 tile (every CU writes its tiles at
     // the same moment; measured faster), non-temporal ones elsewhere.
@@ -695,8 +726,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds(GemmArgs a) {
         wait_vmcnt<0>();  // the reloads past the last slab land before LDS is reused or released
         __syncthreads();  // the staging rows reuse the slab buffers
         co.load(a, n0 + wn * TN, lane);  // after the loop: no registers to spare during it
-        epilogue<TM, TN, FM, FN, NT>(a, acc, co, lane, m0 + wm * TM, n0 + wn * TN,
-                                     reinterpret_cast<float*>(smem) + wave * 16 * (TN + 4));
+        epilogue<TM, TN, FM, FN, NT, CONV>(a, acc, co, lane, m0 + wm * TM, n0 + wn * TN,
+                                           reinterpret_cast<float*>(smem) + wave * 16 * (TN + 4),
+                                           CONV ? a.omax + blockIdx.x * NW + wave : nullptr);
         return;
     }
 
@@ -720,8 +752,9 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds(GemmArgs a) {
         }
     }
     __syncthreads();  // the staging rows reuse the slab buffers
-    epilogue<TM, TN, FM, FN, NT>(a, acc, co, lane, m0 + wm * TM, n0 + wn * TN,
-                                 reinterpret_cast<float*>(smem) + wave * 16 * (TN + 4));
+    epilogue<TM, TN, FM, FN, NT, CONV>(a, acc, co, lane, m0 + wm * TM, n0 + wn * TN,
+                                       reinterpret_cast<float*>(smem) + wave * 16 * (TN + 4),
+                                       CONV ? a.omax + blockIdx.x * NW + wave : nullptr);
 }
 
 // ---------------------------------------------------------------- skinny --
@@ -807,6 +840,7 @@ __device__ __forceinline__ void skinny_block(GemmArgs a, const int bx, int32_t* 
             ews[j] = a.wscale[nn];
             eb[j] = a.bias ? a.bias[nn] : 0.0f;
             if (a.accumulate && ok) eold[j] = a.out[(size_t)mm * a.ldo + nn];
+            if (a.resid && ok) eold[j] = a.resid[(size_t)mm * a.ldo + nn];  // the convolution's residual
         }
         if constexpr (ROPE) {
             pws[j] = pb[j] = 0.0f;
@@ -887,6 +921,7 @@ __device__ __forceinline__ void skinny_block(GemmArgs a, const int bx, int32_t* 
 #pragma unroll
         for (int r = 0; r < 4; r++) part[((wave * FT + t) * 4 + r) * 64 + lane] = acc[t][r];
     __syncthreads();
+    float mx = 0.0f;  // the convolution epilogue's max |out| (a.omax)
 #pragma unroll
     for (int j = 0; j < EPT; j++) {
         const int e = tid + j * NT;
@@ -913,13 +948,30 @@ __device__ __forceinline__ void skinny_block(GemmArgs a, const int bx, int32_t* 
                 continue;
             }
         }
-        switch (a.act) {
-        case 1: o = act_relu(o); break;
-        case 2: o = act_gelu_tanh(o); break;
-        case 3: o = act_gelu_erf(o); break;
-        default: break;
+        if (a.resid) {
+            o = relu_gt(o + eold[j]);
+        } else {
+            switch (a.act) {
+            case 1: o = act_relu(o); break;
+            case 2: o = act_gelu_tanh(o); break;
+            case 3: o = act_gelu_erf(o); break;
+            default: break;
+            }
         }
+        mx = fmaxf(mx, fabsf(o));
         a.out[(size_t)mm * a.ldo + nn] = a.accumulate ? eold[j] + o : o;
+    }
+    if (a.omax) {  // the block's maximum (part is free once every thread has summed)
+        mx = wave_max_f32(mx);
+        __syncthreads();
+        float* red = reinterpret_cast<float*>(part);
+        if (lane == 0) red[wave] = mx;
+        __syncthreads();
+        if (tid == 0) {
+            float v = 0.0f;
+            for (int w = 0; w < WAVES; w++) v = fmaxf(v, red[w]);
+            a.omax[blockIdx.z * gridDim.x + blockIdx.x] = v;
+        }
     }
 }
 
@@ -1281,18 +1333,19 @@ void run_tiled(const GemmArgs& a, hipStream_t st, int splits = 1) {
     VLA_LAUNCH_CHECK();
 }
 
-template <int BM, int BN, int BK, int S, int WM = 2, int WN = 2, bool PF = false>
+template <int BM, int BN, int BK, int S, int WM = 2, int WN = 2, bool PF = false, bool CONV = false>
 void run_lds(const GemmArgs& a, hipStream_t st) {
     using C = LdsCfg<BM, BN, BK, S, WM, WN>;
     static const bool attr = [] {
         if (C::LDS > 65536)
-            VLA_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_i8_lds<BM, BN, BK, S, WM, WN, PF>),
-                                              hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS));
+            VLA_HIP_CHECK(
+                hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_i8_lds<BM, BN, BK, S, WM, WN, PF, CONV>),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS));
         return true;
     }();
     (void)attr;
     const int blocks = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-    gemm_i8_lds<BM, BN, BK, S, WM, WN, PF><<<blocks, C::NT, C::LDS, st>>>(a);
+    gemm_i8_lds<BM, BN, BK, S, WM, WN, PF, CONV><<<blocks, C::NT, C::LDS, st>>>(a);
     VLA_LAUNCH_CHECK();
 }
 
@@ -1727,6 +1780,40 @@ void launch_gemm_i8(const GemmArgs& a, hipStream_t st) {
         }
     }
     dispatch_tile(t, a, st);
+}
+
+// The kernel choice of launch_gemm_i8 above for the shapes whose kernels
+// carry the convolution epilogue; anything else returns 0 unlaunched.
+int launch_gemm_i8_conv(const GemmArgs& a, hipStream_t st) {
+    if (!a.omax || a.acc32 || a.accumulate || a.a_panel || a.rope_cs || a.M <= 0 || a.N <= 0 || a.K <= 0 ||
+        a.K > kMaxI8K || !a.out || !a.wscale || !a.ascale || a.ldo < a.N || a.ldo % 4 != 0)
+        return 0;
+    if (a.resid ? a.act != 0 : a.act != 1) return 0;
+    if (a.lda % 16 != 0 || a.ldb % 16 != 0 || a.lda < kpad4(a.K) || a.ldb < kpad4(a.K) || !aligned(a.A, 16) ||
+        !aligned(a.B, 16) || !aligned(a.out, 16) || (a.resid && !aligned(a.resid, 16)) || use_gemv(a.M, a.K))
+        return 0;
+    if (skinny_mid_rows(a.M, a.N, false)) {
+        const int nfrag = (a.M + 15) / 16, steps = (a.K + 63) / 64;
+        int g = skinny_row_groups(a.M, a.N, a.K, 1);
+        g = g < (nfrag + 7) / 8 ? (nfrag + 7) / 8 : g;
+        const int parts = (a.N + 15) / 16 * g;  // one per block
+        if (parts > kConvPartsFused) return 0;
+        if (steps >= 32) run_skinny<16>(a, st, 1, g);
+        else if (steps >= 8) run_skinny<8>(a, st, 1, g);
+        else run_skinny<4>(a, st, 1, g);
+        return parts;
+    }
+    if (a.M <= 128) return 0;
+    if (a.split_ws) {
+        const SplitPlan p = split_plan(a.M, a.N, a.K);
+        if (p.S > 1 && a.split_bytes >= (size_t)p.S * a.M * a.N * 4 && aligned(a.split_ws, 16)) return 0;
+    }
+    const Tile t = pick_tile(a.M, a.N, a.K);
+    if (!(t.bm == 32 && t.stages == 4 && t.waves == 4 && !t.pf)) return 0;
+    const int64_t parts = (int64_t)((a.M + 31) / 32) * ((a.N + 63) / 64) * 4;  // one per wave
+    if (parts > kConvPartsFused) return 0;
+    run_lds<32, 64, 128, 4, 2, 2, false, true>(a, st);
+    return (int)parts;
 }
 
 namespace {

@@ -147,9 +147,14 @@ private:
     // out [Hout * Wout, cout] = conv(x [H, W, cin]), then its GroupNorm (if
     // any) and the ReLU (relu). int8 convs: in_part / in_nparts are the block
     // maxima of |x| its producer wrote, out_part receives those of the relu'd
-    // output; returns their count (0 when none are written).
+    // output; returns their count (0 when none are written). The ReLU runs
+    // in the conv's epilogue where its kernel fuses it, else as a pass. resid
+    // (an int8 conv without ReLU or GroupNorm): the block's residual, added
+    // and ReLU'd in the epilogue where the kernel fuses that (*resid_done =
+    // true, the maxima then those of the sum); otherwise the caller adds it.
     int conv(const Conv& c, const float* x, int H, int W, float* out, bool relu, hipStream_t st,
-             const float* in_part = nullptr, int in_nparts = 0, float* out_part = nullptr);
+             const float* in_part = nullptr, int in_nparts = 0, float* out_part = nullptr,
+             const float* resid = nullptr, bool* resid_done = nullptr);
 
     int in_h_ = 0, in_w_ = 0, gsize_ = 0;
     int pool_k_ = 3, pool_stride_ = 2, pool_pad_ = 1;

@@ -13,9 +13,19 @@
 #include "models.h"
 
 #include <algorithm>
+#include <cstdlib>
 
 namespace vla {
 namespace hip {
+
+namespace {
+// VLA_HIP_CONV_FUSE=0 keeps the ReLU and the residual add + ReLU after each
+// int8 conv as passes of their own (A/B runs; the values are the same bits)
+bool conv_fuse_on() {
+    const char* e = std::getenv("VLA_HIP_CONV_FUSE");
+    return !(e && e[0] == '0' && e[1] == '\0');
+}
+}  // namespace
 
 ResNetTrunk::ResNetTrunk(const CkptFiles& files, const std::string& name, int in_h, int in_w, const TrunkOpts& o)
     : in_h_(in_h), in_w_(in_w) {
@@ -196,9 +206,10 @@ ResNetTrunk::ResNetTrunk(const CkptFiles& files, const std::string& name, int in
     res_ = A_.alloc<float>(map_max);
     col_ = A_.alloc<float>(col_max ? col_max : 4);
     col_floats_ = col_max;
-    part_a_ = A_.alloc<float>(kConvPartMax);
-    part_b_ = A_.alloc<float>(kConvPartMax);
-    part_c_ = A_.alloc<float>(kConvPartMax);
+    // up to 4096 maxima: a conv epilogue writes one per wave or block
+    part_a_ = A_.alloc<float>(kConvPartsFused);
+    part_b_ = A_.alloc<float>(kConvPartsFused);
+    part_c_ = A_.alloc<float>(kConvPartsFused);
     if (film_total_) {
         film_g_ = A_.alloc<float>(film_total_);
         film_b_ = A_.alloc<float>(film_total_);
@@ -232,7 +243,7 @@ ResNetTrunk::ResNetTrunk(const CkptFiles& files, const std::string& name, int in
 }
 
 int ResNetTrunk::conv(const Conv& c, const float* x, int H, int W, float* out, bool relu, hipStream_t st,
-                      const float* in_part, int in_nparts, float* out_part) {
+                      const float* in_part, int in_nparts, float* out_part, const float* resid, bool* resid_done) {
     const int Ho = conv_out(H, c.k, c.stride, c.pad), Wo = conv_out(W, c.k, c.stride, c.pad);
     // GroupNorm after the conv: the conv itself runs without ReLU and the
     // norm applies it (resnet_backbone.cpp:218-262)
@@ -259,9 +270,20 @@ int ResNetTrunk::conv(const Conv& c, const float* x, int H, int W, float* out, b
         // an fp32 producer (or none) wrote no maxima: conv2d_i8 runs its absmax pass
         a.in_part = in_nparts > 0 ? in_part : nullptr;
         a.in_nparts = in_nparts > 0 ? in_nparts : 0;
-        launch_conv2d_i8(a, st);
-        // the relu pass writes the block maxima the next conv2d_i8 reads
-        if (conv_relu) nparts = launch_relu_inplace(out, (int64_t)Ho * Wo * c.cout, st, out_part);
+        // the ReLU, or the residual add + ReLU, in the conv's epilogue
+        const bool fuse_res = resid && !relu && !c.gs;
+        if (out_part && (conv_relu || fuse_res) && conv_fuse_on()) {
+            a.out_part = out_part;
+            a.resid = fuse_res ? resid : nullptr;
+        }
+        const int fused = launch_conv2d_i8(a, st);
+        if (fused > 0) {
+            nparts = fused;
+            if (fuse_res && resid_done) *resid_done = true;
+        } else if (conv_relu) {
+            // the relu pass writes the block maxima the next conv2d_i8 reads
+            nparts = launch_relu_inplace(out, (int64_t)Ho * Wo * c.cout, st, out_part);
+        }
     } else {
         const int K = c.k * c.k * c.cin;
         const float* rows = x;
@@ -318,11 +340,14 @@ void ResNetTrunk::run(const float* x, const float* in_part, int in_nparts, float
             idn = res_;
         }
         const int nA = conv(blk.c1, B, h, w, a_, true, st, pB, nB, part_a_);
-        conv(blk.c2, a_, oh, ow, C, false, st, part_a_, nA);
-        const int64_t n = (int64_t)oh * ow * blk.c1.cout;
         const int fo = film_off_[bi];
-        nB = fo >= 0 ? launch_add_relu_film(C, idn, n, blk.c1.cout, film_g_ + fo, film_b_ + fo, st, pC)
-                     : launch_add_relu(C, idn, n, st, pC);
+        bool added = false;  // FiLM points keep their own pass
+        const int nC = conv(blk.c2, a_, oh, ow, C, false, st, part_a_, nA, pC, fo < 0 ? idn : nullptr, &added);
+        const int64_t n = (int64_t)oh * ow * blk.c1.cout;
+        if (added) nB = nC;
+        else
+            nB = fo >= 0 ? launch_add_relu_film(C, idn, n, blk.c1.cout, film_g_ + fo, film_b_ + fo, st, pC)
+                         : launch_add_relu(C, idn, n, st, pC);
         std::swap(B, C);
         std::swap(pB, pC);
         h = oh;
