@@ -113,9 +113,9 @@ struct GemmArgs {
     int rope_cols, rope_hd;
     // Convolution epilogue (launch_gemm_i8_conv only): with resid, out =
     // relu_gt(v + resid[m][n]) (stride ldo), the residual add + ReLU of a
-    // ResNet block; without it act must be 1 (ReLU). omax receives the max
-    // |out| per wave (gemm_i8_lds) or per block (skinny), the block maxima
-    // the next conv2d_i8 folds into its scale.
+    // ResNet block; without it act must be 1 (ReLU). omax receives each
+    // block's max |out|, the block maxima the next conv2d_i8 folds into its
+    // scale.
     const float* resid;
     float* omax;
 };

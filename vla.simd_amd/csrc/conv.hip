@@ -70,6 +70,32 @@ __device__ __forceinline__ float block_max(float v, float* red) {
     return v;
 }
 
+// This thread's max over the block maxima part[0, nparts): float4 loads
+// (16-byte aligned part), four issued before the first is used, so up to
+// 4096 maxima cost one load latency per 256-thread block, not one per float.
+__device__ __forceinline__ float parts_max(const float* __restrict__ part, int nparts) {
+    float m = 0.0f;
+    const int t = threadIdx.x, nt = blockDim.x;
+    int done = 0;
+    if ((reinterpret_cast<uintptr_t>(part) & 15) == 0) {
+        const int n4 = nparts >> 2;
+        const float4* p4 = reinterpret_cast<const float4*>(part);
+        for (int b = 0; b < n4; b += 4 * nt) {
+            float4 v[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int i = b + j * nt + t;
+                v[j] = i < n4 ? p4[i] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) m = fmaxf(fmaxf(m, fmaxf(v[j].x, v[j].y)), fmaxf(v[j].z, v[j].w));
+        }
+        done = n4 << 2;
+    }
+    for (int i = done + t; i < nparts; i += nt) m = fmaxf(m, part[i]);
+    return m;
+}
+
 __global__ __launch_bounds__(256) void conv_absmax_kernel(const float* __restrict__ x, int64_t n,
                                                           float* __restrict__ part) {
     __shared__ float red[4];
@@ -119,9 +145,7 @@ constexpr int kIm2colMaxBlocks = 2048;
 template <bool VEC>
 __global__ __launch_bounds__(256) void conv_im2col_kernel(Im2colArgs a) {
     __shared__ float red[4];
-    float m = 0.0f;
-    for (int i = threadIdx.x; i < a.nparts; i += blockDim.x) m = fmaxf(m, a.part[i]);
-    const float amax = block_max(m, red);
+    const float amax = block_max(parts_max(a.part, a.nparts), red);
     float s = 1.0f;
     if (amax > 0.0f) {
         const float t = amax * a.clip;
@@ -198,9 +222,7 @@ __global__ __launch_bounds__(256) void conv_im2col_kernel(Im2colArgs a) {
 // The per-tensor scale from the block maxima (every block folds them the
 // same way, no atomics): s = amax > 0 ? max(amax * clip / 127, FLT_MIN) : 1.
 __device__ __forceinline__ float fold_scale(const float* part, int nparts, float clip, float* red) {
-    float m = 0.0f;
-    for (int i = threadIdx.x; i < nparts; i += blockDim.x) m = fmaxf(m, part[i]);
-    const float amax = block_max(m, red);
+    const float amax = block_max(parts_max(part, nparts), red);
     float s = 1.0f;
     if (amax > 0.0f) {
         const float t = amax * clip;
@@ -236,7 +258,7 @@ struct ImplicitArgs {
     float* out;        // [npix, N]
     int N, K;
     // the trunk's fused epilogue: act 1 = ReLU, or resid [npix, N] added
-    // before relu_gt; omax: each wave's max |out| at [block][wave]
+    // before relu_gt; omax: each block's max |out| at [block]
     int act;
     const float* resid;
     float* omax;
@@ -359,9 +381,10 @@ __global__ __launch_bounds__(256) void conv_i8_implicit(ImplicitArgs a) {
             }
         }
     }
-    if (a.omax) {
-        mx = wave_max_f32(mx);
-        if (lane == 0) a.omax[(blockIdx.y * gridDim.x + blockIdx.x) * 4 + wave] = mx;
+    if (a.omax) {  // one maximum per block
+        __shared__ float red[4];
+        mx = block_max(mx, red);
+        if (tid == 0) a.omax[blockIdx.y * gridDim.x + blockIdx.x] = mx;
     }
 }
 
@@ -563,9 +586,9 @@ int launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
                         a.bias, ascale, a.out, a.Cout, c.K};
         const dim3 grid((a.Cout + 63) / 64, (c.npix + 63) / 64);
         int parts = 0;
-        if (a.out_part && (int64_t)grid.x * grid.y * 4 <= kConvPartsFused &&
+        if (a.out_part && (int64_t)grid.x * grid.y <= kConvPartsFused &&
             (!a.resid || (reinterpret_cast<uintptr_t>(a.resid) & 15) == 0)) {
-            parts = (int)(grid.x * grid.y * 4);
+            parts = (int)(grid.x * grid.y);
             ia.act = a.resid ? 0 : 1;
             ia.resid = a.resid;
             ia.omax = a.out_part;

@@ -565,6 +565,19 @@ struct LdsCfg {
     static_assert(S >= 2 && (S - 2) * LPS < 64, "pipeline depth");
 };
 
+// The block's maximum of its waves' maxima red[0, NW) to omax[blockIdx.x]
+// (every wave has written its slot before the barrier).
+template <int NW>
+__device__ __forceinline__ void conv_block_max(float* omax, const float* red) {
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float v = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; w++) v = fmaxf(v, red[w]);
+        omax[blockIdx.x] = v;
+    }
+}
+
 template <int BM, int BN, int BK, int S, int WM, int WN, bool PF, bool CONV = false>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds(GemmArgs a) {
     // Plain output stores on the 256 x 256 tile (every CU writes its tiles at
@@ -574,6 +587,7 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds(GemmArgs a) {
     constexpr int TM = C::TM, TN = C::TN, FM = C::FM, FN = C::FN, CPR = C::CPR, NW = C::NW;
     constexpr int IA = C::IA, IB = C::IB, LPS = C::LPS, STAGE = C::STAGE;
     extern __shared__ __attribute__((aligned(16))) int8_t smem[];
+    __shared__ float conv_red[CONV ? NW : 1];  // the convolution epilogue's wave maxima
 
     const int tid = threadIdx.x;
     // wave index as a scalar, so LDS-DMA destinations are scalar arithmetic
@@ -727,8 +741,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds(GemmArgs a) {
         __syncthreads();  // the staging rows reuse the slab buffers
         co.load(a, n0 + wn * TN, lane);  // after the loop: no registers to spare during it
         epilogue<TM, TN, FM, FN, NT, CONV>(a, acc, co, lane, m0 + wm * TM, n0 + wn * TN,
-                                           reinterpret_cast<float*>(smem) + wave * 16 * (TN + 4),
-                                           CONV ? a.omax + blockIdx.x * NW + wave : nullptr);
+                                           reinterpret_cast<float*>(smem) + wave * 16 * (TN + 4), conv_red + wave);
+        if constexpr (CONV) conv_block_max<NW>(a.omax, conv_red);
         return;
     }
 
@@ -753,8 +767,8 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds(GemmArgs a) {
     }
     __syncthreads();  // the staging rows reuse the slab buffers
     epilogue<TM, TN, FM, FN, NT, CONV>(a, acc, co, lane, m0 + wm * TM, n0 + wn * TN,
-                                       reinterpret_cast<float*>(smem) + wave * 16 * (TN + 4),
-                                       CONV ? a.omax + blockIdx.x * NW + wave : nullptr);
+                                       reinterpret_cast<float*>(smem) + wave * 16 * (TN + 4), conv_red + wave);
+    if constexpr (CONV) conv_block_max<NW>(a.omax, conv_red);
 }
 
 // ---------------------------------------------------------------- skinny --
@@ -1810,7 +1824,7 @@ int launch_gemm_i8_conv(const GemmArgs& a, hipStream_t st) {
     }
     const Tile t = pick_tile(a.M, a.N, a.K);
     if (!(t.bm == 32 && t.stages == 4 && t.waves == 4 && !t.pf)) return 0;
-    const int64_t parts = (int64_t)((a.M + 31) / 32) * ((a.N + 63) / 64) * 4;  // one per wave
+    const int64_t parts = (int64_t)((a.M + 31) / 32) * ((a.N + 63) / 64);  // one per block
     if (parts > kConvPartsFused) return 0;
     run_lds<32, 64, 128, 4, 2, 2, false, true>(a, st);
     return (int)parts;
