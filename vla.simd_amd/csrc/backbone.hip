@@ -306,9 +306,9 @@ int grid_for(int64_t n) {
 }  // namespace
 
 // grid of a producer that writes block maxima: at most kConvPartMax blocks
-static int part_grid(int64_t n, const float* part) {
+static int part_grid(int64_t n, const float* part, int max_parts = kConvPartMax) {
     const int g = grid_for(n);
-    return part && g > kConvPartMax ? kConvPartMax : g;
+    return part && g > max_parts ? max_parts : g;
 }
 
 int launch_normalize_u8(float* out, const uint8_t* img, int n_cams, int64_t npx, const float* mean,
@@ -341,18 +341,18 @@ void launch_im2col_f32(float* col, int ldc, const float* x, int H, int Wd, int C
 }
 
 int launch_maxpool_relu(float* out, const float* x, int H, int Wd, int C, int k, int stride, int pad, int Hout,
-                        int Wout, hipStream_t st, float* part) {
+                        int Wout, hipStream_t st, float* part, int max_parts) {
     VLA_REQUIRE(out && x && Hout > 0 && Wout > 0 && C > 0, "maxpool: bad arguments");
     const int64_t total = (int64_t)Hout * Wout * C;
     if (C % 4 == 0 && aligned(out, 16) && aligned(x, 16) && (int64_t)H * Wd * C / 4 < INT32_MAX &&
         total / 4 < INT32_MAX) {
-        const int g = part_grid(total / 4, part);
+        const int g = part_grid(total / 4, part, max_parts);
         maxpool_relu4_kernel<<<g, 256, 0, st>>>(reinterpret_cast<float4*>(out), reinterpret_cast<const float4*>(x), H,
                                                  Wd, C / 4, k, stride, pad, Wout, (int)(total / 4), part);
         VLA_LAUNCH_CHECK();
         return g;
     }
-    const int g = part_grid(total, part);
+    const int g = part_grid(total, part, max_parts);
     maxpool_relu_kernel<<<g, 256, 0, st>>>(out, x, H, Wd, C, k, stride, pad, Hout, Wout, part);
     VLA_LAUNCH_CHECK();
     return g;

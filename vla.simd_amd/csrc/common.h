@@ -252,9 +252,10 @@ int launch_normalize_u8(float* out, const uint8_t* img, int n_cams, int64_t npx,
 // col [Hout * Wout, ldc]: the k x k taps [ky][kx][ci] of every output pixel, zero outside
 void launch_im2col_f32(float* col, int ldc, const float* x, int H, int Wd, int Cin, int k, int stride, int pad,
                        int Hout, int Wout, hipStream_t st);
-// max pool with -inf padding, then the folded relu (!(v > 0) -> 0)
+// max pool with -inf padding, then the folded relu (!(v > 0) -> 0); part
+// holds max_parts floats (at most kConvPartsFused)
 int launch_maxpool_relu(float* out, const float* x, int H, int Wd, int C, int k, int stride, int pad, int Hout,
-                        int Wout, hipStream_t st, float* part = nullptr);
+                        int Wout, hipStream_t st, float* part = nullptr, int max_parts = kConvPartMax);
 // o = o + idn > 0 ? o + idn : 0
 int launch_add_relu(float* o, const float* idn, int64_t n, hipStream_t st, float* part = nullptr);
 // o = fma(1 + gamma[c], relu(o + idn), beta[c]) over NHWC maps of C channels

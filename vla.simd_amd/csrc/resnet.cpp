@@ -327,11 +327,14 @@ void ResNetTrunk::run(const float* x, const float* in_part, int in_nparts, float
     float* C = c_;
     float* pB = part_b_;
     float* pC = part_c_;
-    int nB = launch_maxpool_relu(B, a_, h, w, stem_.cout, pool_k_, pool_stride_, pool_pad_, ph, pw, st, pB);
+    int nB = launch_maxpool_relu(B, a_, h, w, stem_.cout, pool_k_, pool_stride_, pool_pad_, ph, pw, st, pB,
+                                 kConvPartsFused / 2);
     h = ph;
     w = pw;
     for (size_t bi = 0; bi < blocks_.size(); bi++) {
         const Block& blk = blocks_[bi];
+        // the last block writes the trunk's output in place of a copy
+        if (bi + 1 == blocks_.size()) C = out;
         const int oh = conv_out(h, blk.c1.k, blk.c1.stride, blk.c1.pad);
         const int ow = conv_out(w, blk.c1.k, blk.c1.stride, blk.c1.pad);
         const float* idn = B;
@@ -353,7 +356,7 @@ void ResNetTrunk::run(const float* x, const float* in_part, int in_nparts, float
         h = oh;
         w = ow;
     }
-    copy_f32(out, B, (int64_t)fh_ * fw_ * ch_, st);
+    if (B != out) copy_f32(out, B, (int64_t)fh_ * fw_ * ch_, st);
 }
 
 }  // namespace hip
