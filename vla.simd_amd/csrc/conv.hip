@@ -502,6 +502,14 @@ bool conv_implicit_on() {
     return !(e && e[0] == '0' && e[1] == '\0');
 }
 
+// The fewest 64 x 64 output tiles for which a k > 1 conv over 64-channel
+// multiples takes the implicit form (VLA_HIP_CONV_IMPLICIT_TILES, read per
+// call; default 256)
+int64_t conv_implicit_tiles() {
+    const char* e = std::getenv("VLA_HIP_CONV_IMPLICIT_TILES");
+    return e && *e ? std::atoll(e) : 256;
+}
+
 float clip_from_env() {
     // TCPU_I8_CLIP as the reference reads it (src/hal/common/env.cpp:220-226):
     // a value in (0, 1], else 1
@@ -576,7 +584,7 @@ int launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
     const int64_t tiles = (int64_t)((c.npix + 63) / 64) * ((a.Cout + 63) / 64);
     if (a.Cin % 64 == 0 && a.Cout % 4 == 0 && a.ldw % 16 == 0 && (reinterpret_cast<uintptr_t>(a.Wq) & 15) == 0 &&
         (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 &&
-        (c.npix + 63) / 64 <= 65535 && (a.k == 1 || tiles >= 256) && conv_implicit_on()) {
+        (c.npix + 63) / 64 <= 65535 && (a.k == 1 || tiles >= conv_implicit_tiles()) && conv_implicit_on()) {
         const int64_t n4 = (int64_t)a.H * a.Wd * a.Cin / 4;
         const int qb = (int)((n4 + 255) / 256 < 2048 ? (n4 + 255) / 256 : 2048);
         conv_quant_kernel<<<qb, 256, 0, st>>>(reinterpret_cast<const float4*>(a.x), n4,
