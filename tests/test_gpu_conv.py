@@ -98,6 +98,35 @@ def test_conv2d_i8_implicit_and_im2col_forms(vla, orc, shape, monkeypatch):
     assert same_bits(got_im2col, want), "im2col form differs from the oracle"
 
 
+# fewer than 256 output tiles over 64-channel multiples: the LDS GEMM tile
+# gathering A from the int8 map (above 320 pixels, or at every count with
+# VLA_HIP_CONV_LDS_IMPLICIT=all): 192 channels (a 128-byte K slab spanning
+# two taps mid-tap), 64 channels (two taps per slab), a ragged last slab
+# (K = 4800, 576), pixel counts off the 32-row tile, Cout off the 64-column
+# tile, strides 1-3, padding 1-2, and 300- / 81-pixel maps under "all"
+LDS_IMPLICIT_SHAPES = [(41, 37, 192, 100, 5, 2, 2), (60, 70, 64, 36, 3, 3, 2), (56, 56, 64, 64, 3, 1, 1),
+                       (60, 80, 128, 256, 3, 2, 1), (30, 40, 256, 256, 3, 1, 1), (15, 20, 512, 512, 3, 1, 1),
+                       (9, 9, 64, 32, 3, 1, 1)]
+
+
+@pytest.mark.parametrize("shape", LDS_IMPLICIT_SHAPES)
+def test_conv2d_i8_lds_implicit_form(vla, orc, shape, monkeypatch):
+    """The 32 x 64 LDS GEMM tile with A gathered per tap from the int8 map:
+    bit-exact with the oracle, and with the im2col rows
+    (VLA_HIP_CONV_LDS_IMPLICIT=0); "all" puts the small maps on it too."""
+    H, Wd, Cin, Cout, k, s, p = shape
+    x, W, b = _case(shape, seed=13)
+    Wq, ws = orc.quantize_weights_i8(W.reshape(Cout, -1))
+    want = orc.conv2d_i8(x, Wq, ws, b, k, s, p)
+    print(f"conv lds implicit {shape}", flush=True)
+    outs = {}
+    for mode in ("1", "all", "0"):
+        monkeypatch.setenv("VLA_HIP_CONV_LDS_IMPLICIT", mode)
+        outs[mode] = vla.conv2d_i8(x, Wq, ws, b, k, s, p)
+    for mode, got in outs.items():
+        assert same_bits(got, want), f"VLA_HIP_CONV_LDS_IMPLICIT={mode} differs from the oracle"
+
+
 def test_conv2d_i8_repeat_and_zero_input(vla, orc, torch_cuda):
     """One workspace, two calls in a row (the second on an all-zero input:
     scale 1, every byte 0, every output the bias), then the first again."""

@@ -118,6 +118,11 @@ struct GemmArgs {
     // scale.
     const float* resid;
     float* omax;
+    // Implicit convolution A (launch_gemm_i8_conv_implicit only): A is the
+    // int8 NHWC map [cv_h, cv_w, cv_c] and row m of the product is output
+    // pixel m of a cv_k x cv_k, stride cv_s, pad cv_p convolution (cv_wo
+    // output columns), K = cv_k^2 cv_c in [ky][kx][ci] order, zero outside.
+    int cv_h, cv_w, cv_c, cv_k, cv_s, cv_p, cv_wo;
 };
 void launch_gemm_i8(const GemmArgs& a, hipStream_t st);
 // The product with the convolution epilogue above when the kernel
@@ -126,6 +131,11 @@ void launch_gemm_i8(const GemmArgs& a, hipStream_t st);
 // returns how many maxima it wrote. Returns 0, launching nothing, otherwise;
 // the caller then runs launch_gemm_i8 and the separate ReLU pass.
 int launch_gemm_i8_conv(const GemmArgs& a, hipStream_t st);
+// The convolution as the 32 x 64 x 128 LDS GEMM tile gathering A from the
+// int8 map (the cv_ fields; cv_c % 64 == 0, 16-byte aligned operands), with
+// the convolution epilogue when omax is set. Returns the maxima written (0
+// without omax).
+int launch_gemm_i8_conv_implicit(const GemmArgs& a, hipStream_t st);
 // Two independent products over the same rows as one skinny launch (same
 // bits as two launch_gemm_i8 calls). Returns false, launching nothing, when
 // either would not take the unsplit skinny kernel; the caller then runs them

@@ -51,6 +51,7 @@
 
 #include <cfloat>
 #include <cstdlib>
+#include <cstring>
 
 #pragma clang fp contract(off)
 
@@ -233,14 +234,15 @@ __device__ __forceinline__ float fold_scale(const float* part, int nparts, float
 }
 
 // x [n4 float4] -> int8 NHWC q (quantize_tensor_i8, conv.cpp:448-465); the
-// scale to *s_out
+// scale to s_out[0, nrows) (the GEMM's row scales)
 __global__ __launch_bounds__(256) void conv_quant_kernel(const float4* __restrict__ x, int64_t n4,
                                                          uint32_t* __restrict__ q, const float* __restrict__ part,
-                                                         int nparts, float clip, float* __restrict__ s_out) {
+                                                         int nparts, float clip, float* __restrict__ s_out,
+                                                         int nrows) {
     __shared__ float red[4];
     const float s = fold_scale(part, nparts, clip, red);
     const float inv = 1.0f / s;
-    if (blockIdx.x == 0 && threadIdx.x == 0) *s_out = s;
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < nrows; i += gridDim.x * blockDim.x) s_out[i] = s;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x)
         q[i] = q8x4(x[i], inv);
 }
@@ -510,6 +512,17 @@ int64_t conv_implicit_tiles() {
     return e && *e ? std::atoll(e) : 256;
 }
 
+// Below that tile count, k > 1 convs over 64-channel multiples with more
+// output pixels than the skinny GEMM's rows take the 32 x 64 LDS GEMM tile
+// gathering A from the int8 map (VLA_HIP_CONV_LDS_IMPLICIT, read per call:
+// 0 off, "all" at every pixel count)
+int conv_lds_implicit_mode() {
+    const char* e = std::getenv("VLA_HIP_CONV_LDS_IMPLICIT");
+    if (e && e[0] == '0' && e[1] == '\0') return 0;
+    if (e && std::strcmp(e, "all") == 0) return 2;
+    return 1;
+}
+
 float clip_from_env() {
     // TCPU_I8_CLIP as the reference reads it (src/hal/common/env.cpp:220-226):
     // a value in (0, 1], else 1
@@ -588,7 +601,7 @@ int launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
         const int64_t n4 = (int64_t)a.H * a.Wd * a.Cin / 4;
         const int qb = (int)((n4 + 255) / 256 < 2048 ? (n4 + 255) / 256 : 2048);
         conv_quant_kernel<<<qb, 256, 0, st>>>(reinterpret_cast<const float4*>(a.x), n4,
-                                              reinterpret_cast<uint32_t*>(A), maxima, blocks, clip, ascale);
+                                              reinterpret_cast<uint32_t*>(A), maxima, blocks, clip, ascale, 1);
         VLA_LAUNCH_CHECK();
         ImplicitArgs ia{A, a.H, a.Wd, a.Cin, a.k, a.stride, a.pad, c.Wout, c.npix, a.Wq, a.ldw, a.wscale,
                         a.bias, ascale, a.out, a.Cout, c.K};
@@ -620,6 +633,44 @@ int launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
         conv_i8_c4<<<dim3((a.Cout + 63) / 64, (c.npix + 63) / 64), 256, 0, st>>>(ca);
         VLA_LAUNCH_CHECK();
         return 0;
+    }
+
+    const int lds_mode = conv_lds_implicit_mode();
+    if (a.Cin % 64 == 0 && a.k > 1 && a.Cout % 4 == 0 && a.ldw % 16 == 0 &&
+        (reinterpret_cast<uintptr_t>(a.Wq) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
+        (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 && lds_mode > 0 && (lds_mode == 2 || c.npix > 320) &&
+        conv_implicit_on()) {
+        const int64_t n4 = (int64_t)a.H * a.Wd * a.Cin / 4;
+        const int qb = (int)((n4 + 255) / 256 < 2048 ? (n4 + 255) / 256 : 2048);
+        conv_quant_kernel<<<qb, 256, 0, st>>>(reinterpret_cast<const float4*>(a.x), n4,
+                                              reinterpret_cast<uint32_t*>(A), maxima, blocks, clip, ascale, c.npix);
+        VLA_LAUNCH_CHECK();
+        GemmArgs m{};
+        m.A = A;
+        m.B = a.Wq;
+        m.ldb = a.ldw;
+        m.ascale = ascale;
+        m.wscale = a.wscale;
+        m.bias = a.bias;
+        m.out = a.out;
+        m.ldo = a.Cout;
+        m.M = c.npix;
+        m.N = a.Cout;
+        m.K = c.K;
+        m.cv_h = a.H;
+        m.cv_w = a.Wd;
+        m.cv_c = a.Cin;
+        m.cv_k = a.k;
+        m.cv_s = a.stride;
+        m.cv_p = a.pad;
+        m.cv_wo = c.Wout;
+        const int64_t gblocks = (int64_t)((c.npix + 31) / 32) * ((a.Cout + 63) / 64);
+        if (a.out_part && gblocks <= kConvPartsFused && (!a.resid || (reinterpret_cast<uintptr_t>(a.resid) & 15) == 0)) {
+            m.act = a.resid ? 0 : 1;
+            m.resid = a.resid;
+            m.omax = a.out_part;
+        }
+        return launch_gemm_i8_conv_implicit(m, st);
     }
 
     Im2colArgs g{a.x, a.H, a.Wd, a.Cin, a.k, a.stride, a.pad, c.Wout, c.npix, c.K, c.lda, maxima, blocks,

@@ -578,7 +578,11 @@ __device__ __forceinline__ void conv_block_max(float* omax, const float* red) {
     }
 }
 
-template <int BM, int BN, int BK, int S, int WM, int WN, bool PF, bool CONV = false>
+// IMPL: A is gathered from an int8 NHWC map as an implicit convolution (the
+// GemmArgs cv_ fields): each row's 16-byte chunk of a 128-byte K slab lies in
+// one tap, at most one tap past the slab's first (cv_c % 64 == 0), and taps
+// outside the image read the zero chunk.
+template <int BM, int BN, int BK, int S, int WM, int WN, bool PF, bool CONV = false, bool IMPL = false>
 __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds(GemmArgs a) {
     // Plain output stores on the 256 x 256 tile (every CU writes its tiles at
     // the same moment; measured faster), non-temporal ones elsewhere.
@@ -604,13 +608,21 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds(GemmArgs a) {
     // row q / CPR, logical chunk (q % CPR) ^ swz(row).
     const int8_t* asrc[IA];
     int acb[IA];
+    int aiy[IMPL ? IA : 1], aix[IMPL ? IA : 1];  // IMPL: the row's pixel, top-left tap
 #pragma unroll
     for (int j = 0; j < IA; j++) {
         const int q = (j * NW + wave) * 64 + lane, r = q / CPR;
         const int c = (q % CPR) ^ swz<BK>(r);
         const int m = m0 + r < a.M ? m0 + r : a.M - 1;
         acb[j] = c * 16;
-        asrc[j] = a.A + (size_t)m * a.lda + acb[j];
+        if constexpr (IMPL) {
+            const int oy = m / a.cv_wo, ox = m - oy * a.cv_wo;
+            aiy[j] = oy * a.cv_s - a.cv_p;
+            aix[j] = ox * a.cv_s - a.cv_p;
+            asrc[j] = a.A;
+        } else {
+            asrc[j] = a.A + (size_t)m * a.lda + acb[j];
+        }
     }
     const int8_t* bsrc[IB];
     int bcb[IB];
@@ -631,10 +643,30 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds(GemmArgs a) {
         const int k0 = (kt < nk ? kt : nk - 1) * BK;
         int8_t* st = smem + (kt % S) * STAGE;
         const bool full = k0 + BK <= K16;
+        if constexpr (IMPL) {
+            // the slab's first tap (ky0, kx0) at channel ci0, and the tap after it
+            const int tap0 = k0 / a.cv_c, ci0 = k0 - tap0 * a.cv_c;
+            const int ky0 = tap0 / a.cv_k, kx0 = tap0 - ky0 * a.cv_k;
+            const int ky1 = kx0 + 1 == a.cv_k ? ky0 + 1 : ky0, kx1 = kx0 + 1 == a.cv_k ? 0 : kx0 + 1;
 #pragma unroll
-        for (int j = 0; j < IA; j++) {
-            const int8_t* p = full || k0 + acb[j] < K16 ? asrc[j] + k0 : g_zero16;
-            __builtin_amdgcn_global_load_lds((gptr)p, (lptr)(st + (j * NW + wave) * 1024), 16, 0, 0);
+            for (int j = 0; j < IA; j++) {
+                int ci = ci0 + acb[j], ky = ky0, kx = kx0;
+                if (ci >= a.cv_c) {
+                    ci -= a.cv_c;
+                    ky = ky1;
+                    kx = kx1;
+                }
+                const int iy = aiy[j] + ky, ix = aix[j] + kx;
+                const bool in = k0 + acb[j] < K16 && iy >= 0 && iy < a.cv_h && ix >= 0 && ix < a.cv_w;
+                const int8_t* p = in ? asrc[j] + ((size_t)iy * a.cv_w + ix) * a.cv_c + ci : g_zero16;
+                __builtin_amdgcn_global_load_lds((gptr)p, (lptr)(st + (j * NW + wave) * 1024), 16, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < IA; j++) {
+                const int8_t* p = full || k0 + acb[j] < K16 ? asrc[j] + k0 : g_zero16;
+                __builtin_amdgcn_global_load_lds((gptr)p, (lptr)(st + (j * NW + wave) * 1024), 16, 0, 0);
+            }
         }
 #pragma unroll
         for (int j = 0; j < IB; j++) {
@@ -1347,19 +1379,20 @@ void run_tiled(const GemmArgs& a, hipStream_t st, int splits = 1) {
     VLA_LAUNCH_CHECK();
 }
 
-template <int BM, int BN, int BK, int S, int WM = 2, int WN = 2, bool PF = false, bool CONV = false>
+template <int BM, int BN, int BK, int S, int WM = 2, int WN = 2, bool PF = false, bool CONV = false,
+          bool IMPL = false>
 void run_lds(const GemmArgs& a, hipStream_t st) {
     using C = LdsCfg<BM, BN, BK, S, WM, WN>;
     static const bool attr = [] {
         if (C::LDS > 65536)
-            VLA_HIP_CHECK(
-                hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_i8_lds<BM, BN, BK, S, WM, WN, PF, CONV>),
-                                    hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS));
+            VLA_HIP_CHECK(hipFuncSetAttribute(
+                reinterpret_cast<const void*>(&gemm_i8_lds<BM, BN, BK, S, WM, WN, PF, CONV, IMPL>),
+                hipFuncAttributeMaxDynamicSharedMemorySize, C::LDS));
         return true;
     }();
     (void)attr;
     const int blocks = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
-    gemm_i8_lds<BM, BN, BK, S, WM, WN, PF, CONV><<<blocks, C::NT, C::LDS, st>>>(a);
+    gemm_i8_lds<BM, BN, BK, S, WM, WN, PF, CONV, IMPL><<<blocks, C::NT, C::LDS, st>>>(a);
     VLA_LAUNCH_CHECK();
 }
 
@@ -1828,6 +1861,28 @@ int launch_gemm_i8_conv(const GemmArgs& a, hipStream_t st) {
     if (parts > kConvPartsFused) return 0;
     run_lds<32, 64, 128, 4, 2, 2, false, true>(a, st);
     return (int)parts;
+}
+
+int launch_gemm_i8_conv_implicit(const GemmArgs& a, hipStream_t st) {
+    VLA_REQUIRE(a.cv_c > 0 && a.cv_c % 64 == 0 && a.cv_k > 0 && a.cv_s > 0 && a.cv_p >= 0 && a.cv_wo > 0 &&
+                    a.cv_h > 0 && a.cv_w > 0 && a.K == a.cv_k * a.cv_k * a.cv_c && a.K <= kMaxI8K && a.M > 0 &&
+                    a.N > 0,
+                "gemm_i8 implicit conv: need 64-channel multiples and K = k * k * Cin");
+    VLA_REQUIRE(aligned(a.A, 16) && aligned(a.B, 16) && a.ldb % 16 == 0 && a.ldb >= a.K && aligned(a.out, 16) &&
+                    a.ldo % 4 == 0 && a.ldo >= a.N && a.wscale && a.ascale && !a.acc32 && !a.accumulate &&
+                    !a.a_panel && !a.rope_cs,
+                "gemm_i8 implicit conv: 16-byte aligned operands, fp32 output, no accumulation");
+    const int64_t blocks = (int64_t)((a.M + 31) / 32) * ((a.N + 63) / 64);
+    if (a.omax) {
+        VLA_REQUIRE((a.resid ? a.act == 0 : a.act == 1) && blocks <= kConvPartsFused &&
+                        (!a.resid || aligned(a.resid, 16)),
+                    "gemm_i8 implicit conv: bad fused epilogue");
+        run_lds<32, 64, 128, 4, 2, 2, false, true, true>(a, st);
+        return (int)blocks;
+    }
+    VLA_REQUIRE(!a.resid, "gemm_i8 implicit conv: a residual needs omax");
+    run_lds<32, 64, 128, 4, 2, 2, false, false, true>(a, st);
+    return 0;
 }
 
 namespace {
