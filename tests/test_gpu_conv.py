@@ -65,8 +65,10 @@ def test_conv2d_i8_dev_form(vla, orc, torch_cuda, shape):
     assert same_bits(out.cpu().numpy(), orc.conv2d_i8(x, Wq, ws, b, k, s, p))
 
 
-# the implicit form (>= 256 output tiles of 64 x 64, or 1x1) and, with fewer
-# tiles, the im2col rows: ragged rows and channels, 18 K steps; then inputs
+# the implicit forms (the LDS GEMM tile above 320 pixels, conv_i8_implicit
+# for smaller 1x1 maps and, with the LDS form off, for >= 256 output tiles
+# of 64 x 64 or 1x1) and the im2col rows: ragged rows and channels, 18 K
+# steps; then inputs
 # of 1-4 channels, which take the word-per-pixel form (kernels up to 8 x 8,
 # strides 1-4, channel counts off the 64-wide block; 30 channels, not a
 # multiple of 4, keep the im2col rows)
@@ -79,22 +81,27 @@ IMPLICIT_SHAPES = [(128, 128, 64, 64, 3, 1, 1), (30, 40, 256, 512, 1, 2, 0), (16
 
 @pytest.mark.parametrize("shape", IMPLICIT_SHAPES)
 def test_conv2d_i8_implicit_and_im2col_forms(vla, orc, shape, monkeypatch):
-    """Input channels a multiple of 64 over enough output tiles (or 1x1)
-    take the implicit GEMM (the int8 map gathered per tap), 1-4 input
-    channels the word-per-pixel form (zero bytes past the channels and past
-    the last tap add nothing to the int32 sums); VLA_HIP_CONV_IMPLICIT=0
-    (read per call) forces the im2col rows. Both bit-exact with the oracle:
-    ragged output tiles (48, 100, 36, 20, 72 channels), pixel counts off the
-    64-row tile, strides 2-4, padding 2-3."""
+    """Input channels a multiple of 64 take an implicit GEMM (the int8 map
+    gathered per tap): over more than 320 pixels the LDS GEMM tile, smaller
+    1x1 maps conv_i8_implicit (with VLA_HIP_CONV_LDS_IMPLICIT=0, 1x1 maps and
+    those over >= 256 output tiles conv_i8_implicit); 1-4 input channels the
+    word-per-pixel form (zero bytes past the channels and past the last tap
+    add nothing to the int32 sums); VLA_HIP_CONV_IMPLICIT=0 (read per call)
+    forces the im2col rows. All bit-exact with the oracle: ragged output
+    tiles (48, 100, 36, 20, 72 channels), pixel counts off the 64-row tile,
+    strides 2-4, padding 2-3."""
     H, Wd, Cin, Cout, k, s, p = shape
     x, W, b = _case(shape, seed=11)
     Wq, ws = orc.quantize_weights_i8(W.reshape(Cout, -1))
     want = orc.conv2d_i8(x, Wq, ws, b, k, s, p)
     print(f"conv implicit {shape}", flush=True)
     got = vla.conv2d_i8(x, Wq, ws, b, k, s, p)
+    monkeypatch.setenv("VLA_HIP_CONV_LDS_IMPLICIT", "0")
+    got_64 = vla.conv2d_i8(x, Wq, ws, b, k, s, p)
     monkeypatch.setenv("VLA_HIP_CONV_IMPLICIT", "0")
     got_im2col = vla.conv2d_i8(x, Wq, ws, b, k, s, p)
     assert same_bits(got, want), "implicit form differs from the oracle"
+    assert same_bits(got_64, want), "64 x 64 implicit form differs from the oracle"
     assert same_bits(got_im2col, want), "im2col form differs from the oracle"
 
 
@@ -112,8 +119,9 @@ LDS_IMPLICIT_SHAPES = [(41, 37, 192, 100, 5, 2, 2), (60, 70, 64, 36, 3, 3, 2), (
 @pytest.mark.parametrize("shape", LDS_IMPLICIT_SHAPES)
 def test_conv2d_i8_lds_implicit_form(vla, orc, shape, monkeypatch):
     """The 32 x 64 LDS GEMM tile with A gathered per tap from the int8 map:
-    bit-exact with the oracle, and with the im2col rows
-    (VLA_HIP_CONV_LDS_IMPLICIT=0); "all" puts the small maps on it too."""
+    bit-exact with the oracle, with the im2col rows and with
+    conv_i8_implicit (VLA_HIP_CONV_LDS_IMPLICIT=0, then with
+    VLA_HIP_CONV_IMPLICIT_TILES=0); "all" puts the small maps on it too."""
     H, Wd, Cin, Cout, k, s, p = shape
     x, W, b = _case(shape, seed=13)
     Wq, ws = orc.quantize_weights_i8(W.reshape(Cout, -1))
@@ -123,6 +131,8 @@ def test_conv2d_i8_lds_implicit_form(vla, orc, shape, monkeypatch):
     for mode in ("1", "all", "0"):
         monkeypatch.setenv("VLA_HIP_CONV_LDS_IMPLICIT", mode)
         outs[mode] = vla.conv2d_i8(x, Wq, ws, b, k, s, p)
+    monkeypatch.setenv("VLA_HIP_CONV_IMPLICIT_TILES", "0")
+    outs["0, 64 x 64 implicit"] = vla.conv2d_i8(x, Wq, ws, b, k, s, p)
     for mode, got in outs.items():
         assert same_bits(got, want), f"VLA_HIP_CONV_LDS_IMPLICIT={mode} differs from the oracle"
 

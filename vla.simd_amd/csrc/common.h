@@ -245,6 +245,14 @@ struct ConvArgs {
     // plain conv, and the caller applies the ReLU pass itself.
     float* out_part = nullptr;
     const float* resid = nullptr;
+    // optional (a ResNet downsample and the block's first conv, both over the
+    // block input with the same output grid): xq_out is set to 1 when the
+    // call left x's int8 map and its npix row scales in work (the LDS
+    // implicit form), else 0; xq_in says work still holds them from the
+    // previous call on the same x, maxima, workspace and output grid, so the
+    // LDS implicit form skips its quantization pass (other forms ignore it).
+    int* xq_out = nullptr;
+    bool xq_in = false;
 };
 int launch_conv2d_i8(const ConvArgs& a, hipStream_t st);
 // Producers of a conv2d_i8 input that also write its block maxima (part:

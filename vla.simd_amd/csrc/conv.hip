@@ -504,23 +504,24 @@ bool conv_implicit_on() {
     return !(e && e[0] == '0' && e[1] == '\0');
 }
 
-// The fewest 64 x 64 output tiles for which a k > 1 conv over 64-channel
-// multiples takes the implicit form (VLA_HIP_CONV_IMPLICIT_TILES, read per
-// call; default 256)
-int64_t conv_implicit_tiles() {
-    const char* e = std::getenv("VLA_HIP_CONV_IMPLICIT_TILES");
-    return e && *e ? std::atoll(e) : 256;
-}
-
-// Below that tile count, k > 1 convs over 64-channel multiples with more
-// output pixels than the skinny GEMM's rows take the 32 x 64 LDS GEMM tile
-// gathering A from the int8 map (VLA_HIP_CONV_LDS_IMPLICIT, read per call:
-// 0 off, "all" at every pixel count)
+// Convs over 64-channel multiples with more output pixels than the skinny
+// GEMM's rows take the 32 x 64 LDS GEMM tile gathering A from the int8 map
+// (VLA_HIP_CONV_LDS_IMPLICIT, read per call: 0 off, "all" at every pixel
+// count)
 int conv_lds_implicit_mode() {
     const char* e = std::getenv("VLA_HIP_CONV_LDS_IMPLICIT");
     if (e && e[0] == '0' && e[1] == '\0') return 0;
     if (e && std::strcmp(e, "all") == 0) return 2;
     return 1;
+}
+
+// The fewest 64 x 64 output tiles for which a k > 1 conv over 64-channel
+// multiples that the LDS form does not take runs conv_i8_implicit
+// (VLA_HIP_CONV_IMPLICIT_TILES, read per call; default 256, or never while
+// the LDS form is on)
+int64_t conv_implicit_tiles(int lds_mode) {
+    const char* e = std::getenv("VLA_HIP_CONV_IMPLICIT_TILES");
+    return e && *e ? std::atoll(e) : (lds_mode > 0 ? INT64_MAX : 256);
 }
 
 float clip_from_env() {
@@ -572,6 +573,7 @@ int launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
     VLA_REQUIRE(a.work_bytes >= c.work, "conv2d_i8: workspace too small (vla_conv2d_i8_workspace_bytes)");
     VLA_REQUIRE((reinterpret_cast<uintptr_t>(a.work) & 255) == 0, "conv2d_i8: workspace must be 256-byte aligned");
     char* w = static_cast<char*>(a.work);
+    if (a.xq_out) *a.xq_out = 0;
     // [block maxima: 512 floats][row scales: npix floats][im2col rows][split-K sums],
     // each 256-byte rounded
     float* part = reinterpret_cast<float*>(w);
@@ -595,9 +597,15 @@ int launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
 
     const float clip = a.clip > 0.0f ? a.clip : clip_from_env();
     const int64_t tiles = (int64_t)((c.npix + 63) / 64) * ((a.Cout + 63) / 64);
-    if (a.Cin % 64 == 0 && a.Cout % 4 == 0 && a.ldw % 16 == 0 && (reinterpret_cast<uintptr_t>(a.Wq) & 15) == 0 &&
-        (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 &&
-        (c.npix + 63) / 64 <= 65535 && (a.k == 1 || tiles >= conv_implicit_tiles()) && conv_implicit_on()) {
+    // the implicit forms' operands: 64-channel multiples, 16-byte rows
+    const bool impl_ok = a.Cin % 64 == 0 && a.Cout % 4 == 0 && a.ldw % 16 == 0 &&
+                         (reinterpret_cast<uintptr_t>(a.Wq) & 15) == 0 &&
+                         (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
+                         (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 && conv_implicit_on();
+    const int lds_mode = conv_lds_implicit_mode();
+    const bool lds_take = impl_ok && lds_mode > 0 && (lds_mode == 2 || c.npix > 320);
+    if (impl_ok && !lds_take && (c.npix + 63) / 64 <= 65535 &&
+        (a.k == 1 || tiles >= conv_implicit_tiles(lds_mode))) {
         const int64_t n4 = (int64_t)a.H * a.Wd * a.Cin / 4;
         const int qb = (int)((n4 + 255) / 256 < 2048 ? (n4 + 255) / 256 : 2048);
         conv_quant_kernel<<<qb, 256, 0, st>>>(reinterpret_cast<const float4*>(a.x), n4,
@@ -635,16 +643,16 @@ int launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
         return 0;
     }
 
-    const int lds_mode = conv_lds_implicit_mode();
-    if (a.Cin % 64 == 0 && a.k > 1 && a.Cout % 4 == 0 && a.ldw % 16 == 0 &&
-        (reinterpret_cast<uintptr_t>(a.Wq) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
-        (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 && lds_mode > 0 && (lds_mode == 2 || c.npix > 320) &&
-        conv_implicit_on()) {
-        const int64_t n4 = (int64_t)a.H * a.Wd * a.Cin / 4;
-        const int qb = (int)((n4 + 255) / 256 < 2048 ? (n4 + 255) / 256 : 2048);
-        conv_quant_kernel<<<qb, 256, 0, st>>>(reinterpret_cast<const float4*>(a.x), n4,
-                                              reinterpret_cast<uint32_t*>(A), maxima, blocks, clip, ascale, c.npix);
-        VLA_LAUNCH_CHECK();
+    if (lds_take) {
+        if (!a.xq_in) {
+            const int64_t n4 = (int64_t)a.H * a.Wd * a.Cin / 4;
+            const int qb = (int)((n4 + 255) / 256 < 2048 ? (n4 + 255) / 256 : 2048);
+            conv_quant_kernel<<<qb, 256, 0, st>>>(reinterpret_cast<const float4*>(a.x), n4,
+                                                  reinterpret_cast<uint32_t*>(A), maxima, blocks, clip, ascale,
+                                                  c.npix);
+            VLA_LAUNCH_CHECK();
+        }
+        if (a.xq_out) *a.xq_out = 1;
         GemmArgs m{};
         m.A = A;
         m.B = a.Wq;

@@ -152,9 +152,11 @@ private:
     // (an int8 conv without ReLU or GroupNorm): the block's residual, added
     // and ReLU'd in the epilogue where the kernel fuses that (*resid_done =
     // true, the maxima then those of the sum); otherwise the caller adds it.
+    // xq_out / xq_in: ConvArgs' shared int8 map of x (the downsample, then
+    // the block's first conv over the same input and output grid).
     int conv(const Conv& c, const float* x, int H, int W, float* out, bool relu, hipStream_t st,
              const float* in_part = nullptr, int in_nparts = 0, float* out_part = nullptr,
-             const float* resid = nullptr, bool* resid_done = nullptr);
+             const float* resid = nullptr, bool* resid_done = nullptr, int* xq_out = nullptr, bool xq_in = false);
 
     int in_h_ = 0, in_w_ = 0, gsize_ = 0;
     int pool_k_ = 3, pool_stride_ = 2, pool_pad_ = 1;

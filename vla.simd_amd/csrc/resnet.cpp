@@ -25,6 +25,12 @@ bool conv_fuse_on() {
     const char* e = std::getenv("VLA_HIP_CONV_FUSE");
     return !(e && e[0] == '0' && e[1] == '\0');
 }
+// VLA_HIP_CONV_SHARE=0: the block's first conv quantizes its input again
+// after the downsample did
+bool conv_share_on() {
+    const char* e = std::getenv("VLA_HIP_CONV_SHARE");
+    return !(e && e[0] == '0' && e[1] == '\0');
+}
 }  // namespace
 
 ResNetTrunk::ResNetTrunk(const CkptFiles& files, const std::string& name, int in_h, int in_w, const TrunkOpts& o)
@@ -243,7 +249,8 @@ ResNetTrunk::ResNetTrunk(const CkptFiles& files, const std::string& name, int in
 }
 
 int ResNetTrunk::conv(const Conv& c, const float* x, int H, int W, float* out, bool relu, hipStream_t st,
-                      const float* in_part, int in_nparts, float* out_part, const float* resid, bool* resid_done) {
+                      const float* in_part, int in_nparts, float* out_part, const float* resid, bool* resid_done,
+                      int* xq_out, bool xq_in) {
     const int Ho = conv_out(H, c.k, c.stride, c.pad), Wo = conv_out(W, c.k, c.stride, c.pad);
     // GroupNorm after the conv: the conv itself runs without ReLU and the
     // norm applies it (resnet_backbone.cpp:218-262)
@@ -276,6 +283,8 @@ int ResNetTrunk::conv(const Conv& c, const float* x, int H, int W, float* out, b
             a.out_part = out_part;
             a.resid = fuse_res ? resid : nullptr;
         }
+        a.xq_out = xq_out;
+        a.xq_in = xq_in;
         const int fused = launch_conv2d_i8(a, st);
         if (fused > 0) {
             nparts = fused;
@@ -338,11 +347,17 @@ void ResNetTrunk::run(const float* x, const float* in_part, int in_nparts, float
         const int oh = conv_out(h, blk.c1.k, blk.c1.stride, blk.c1.pad);
         const int ow = conv_out(w, blk.c1.k, blk.c1.stride, blk.c1.pad);
         const float* idn = B;
+        // the downsample's int8 map of B serves the first conv too when both
+        // are int8 over the same output grid (same input, maxima and scale)
+        int xq = 0;
         if (blk.has_down) {
-            conv(blk.down, B, h, w, res_, false, st, pB, nB);
+            conv(blk.down, B, h, w, res_, false, st, pB, nB, nullptr, nullptr, nullptr, &xq);
             idn = res_;
         }
-        const int nA = conv(blk.c1, B, h, w, a_, true, st, pB, nB, part_a_);
+        const bool share = xq && blk.c1.q8 && blk.down.q8 && nB > 0 && conv_share_on() &&
+                           conv_out(h, blk.down.k, blk.down.stride, blk.down.pad) == oh &&
+                           conv_out(w, blk.down.k, blk.down.stride, blk.down.pad) == ow;
+        const int nA = conv(blk.c1, B, h, w, a_, true, st, pB, nB, part_a_, nullptr, nullptr, nullptr, share);
         const int fo = film_off_[bi];
         bool added = false;  // FiLM points keep their own pass
         const int nC = conv(blk.c2, a_, oh, ow, C, false, st, part_a_, nA, pC, fo < 0 ? idn : nullptr, &added);
