@@ -110,10 +110,14 @@ def test_conv2d_i8_implicit_and_im2col_forms(vla, orc, shape, monkeypatch):
 # VLA_HIP_CONV_LDS_IMPLICIT=all): 192 channels (a 128-byte K slab spanning
 # two taps mid-tap), 64 channels (two taps per slab), a ragged last slab
 # (K = 4800, 576), pixel counts off the 32-row tile, Cout off the 64-column
-# tile, strides 1-3, padding 1-2, and 300- / 81-pixel maps under "all"
+# tile, strides 1-3, padding 1-2, and 300- / 81-pixel maps under "all";
+# 129-320 pixels take the skinny kernel loading A from the map by default
+# (306, 182 and 300 pixels: Cout 48 / 36 off the 16-column block, K steps
+# for 8 and 16 waves, a 1x1 stride-2 downsample)
 LDS_IMPLICIT_SHAPES = [(41, 37, 192, 100, 5, 2, 2), (60, 70, 64, 36, 3, 3, 2), (56, 56, 64, 64, 3, 1, 1),
                        (60, 80, 128, 256, 3, 2, 1), (30, 40, 256, 256, 3, 1, 1), (15, 20, 512, 512, 3, 1, 1),
-                       (9, 9, 64, 32, 3, 1, 1)]
+                       (9, 9, 64, 32, 3, 1, 1), (33, 35, 64, 48, 5, 2, 2), (25, 27, 192, 36, 3, 2, 1),
+                       (30, 40, 256, 512, 1, 2, 0)]
 
 
 @pytest.mark.parametrize("shape", LDS_IMPLICIT_SHAPES)
@@ -128,6 +132,9 @@ def test_conv2d_i8_lds_implicit_form(vla, orc, shape, monkeypatch):
     want = orc.conv2d_i8(x, Wq, ws, b, k, s, p)
     print(f"conv lds implicit {shape}", flush=True)
     outs = {}
+    monkeypatch.setenv("VLA_HIP_CONV_SKINNY_IMPLICIT", "0")
+    outs["1, no skinny"] = vla.conv2d_i8(x, Wq, ws, b, k, s, p)
+    monkeypatch.delenv("VLA_HIP_CONV_SKINNY_IMPLICIT")
     for mode in ("1", "all", "0"):
         monkeypatch.setenv("VLA_HIP_CONV_LDS_IMPLICIT", mode)
         outs[mode] = vla.conv2d_i8(x, Wq, ws, b, k, s, p)

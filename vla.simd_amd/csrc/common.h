@@ -136,6 +136,10 @@ int launch_gemm_i8_conv(const GemmArgs& a, hipStream_t st);
 // the convolution epilogue when omax is set. Returns the maxima written (0
 // without omax).
 int launch_gemm_i8_conv_implicit(const GemmArgs& a, hipStream_t st);
+// The same with the skinny kernel (rows in the skinny GEMM's mid range,
+// gemm_i8_conv_skinny_fits), its A fragments loaded straight from the map.
+bool gemm_i8_conv_skinny_fits(int M, int N);
+int launch_gemm_i8_conv_skinny_implicit(const GemmArgs& a, hipStream_t st);
 // Two independent products over the same rows as one skinny launch (same
 // bits as two launch_gemm_i8 calls). Returns false, launching nothing, when
 // either would not take the unsplit skinny kernel; the caller then runs them

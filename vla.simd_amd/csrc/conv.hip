@@ -604,7 +604,12 @@ int launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
                          (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 && conv_implicit_on();
     const int lds_mode = conv_lds_implicit_mode();
     const bool lds_take = impl_ok && lds_mode > 0 && (lds_mode == 2 || c.npix > 320);
-    if (impl_ok && !lds_take && (c.npix + 63) / 64 <= 65535 &&
+    // pixel counts in the skinny GEMM's mid range: the skinny kernel loading
+    // its A fragments from the int8 map (VLA_HIP_CONV_SKINNY_IMPLICIT=0: off)
+    const char* ske = std::getenv("VLA_HIP_CONV_SKINNY_IMPLICIT");
+    const bool skinny_take = impl_ok && !lds_take && lds_mode > 0 && !(ske && ske[0] == '0' && ske[1] == '\0') &&
+                             gemm_i8_conv_skinny_fits(c.npix, a.Cout);
+    if (impl_ok && !lds_take && !skinny_take && (c.npix + 63) / 64 <= 65535 &&
         (a.k == 1 || tiles >= conv_implicit_tiles(lds_mode))) {
         const int64_t n4 = (int64_t)a.H * a.Wd * a.Cin / 4;
         const int qb = (int)((n4 + 255) / 256 < 2048 ? (n4 + 255) / 256 : 2048);
@@ -643,7 +648,7 @@ int launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
         return 0;
     }
 
-    if (lds_take) {
+    if (lds_take || skinny_take) {
         if (!a.xq_in) {
             const int64_t n4 = (int64_t)a.H * a.Wd * a.Cin / 4;
             const int qb = (int)((n4 + 255) / 256 < 2048 ? (n4 + 255) / 256 : 2048);
@@ -673,12 +678,13 @@ int launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
         m.cv_p = a.pad;
         m.cv_wo = c.Wout;
         const int64_t gblocks = (int64_t)((c.npix + 31) / 32) * ((a.Cout + 63) / 64);
-        if (a.out_part && gblocks <= kConvPartsFused && (!a.resid || (reinterpret_cast<uintptr_t>(a.resid) & 15) == 0)) {
+        if (a.out_part && (skinny_take || gblocks <= kConvPartsFused) &&
+            (!a.resid || (reinterpret_cast<uintptr_t>(a.resid) & 15) == 0)) {
             m.act = a.resid ? 0 : 1;
             m.resid = a.resid;
             m.omax = a.out_part;
         }
-        return launch_gemm_i8_conv_implicit(m, st);
+        return skinny_take ? launch_gemm_i8_conv_skinny_implicit(m, st) : launch_gemm_i8_conv_implicit(m, st);
     }
 
     Im2colArgs g{a.x, a.H, a.Wd, a.Cin, a.k, a.stride, a.pad, c.Wout, c.npix, c.K, c.lda, maxima, blocks,

@@ -816,7 +816,10 @@ __global__ __launch_bounds__(64 * WM * WN) void gemm_i8_lds(GemmArgs a) {
 // bx: the block's column block (blockIdx.x, or its index within one of the
 // two products of gemm_i8_skinny_pair); part: the block's LDS for the waves'
 // partial int32 tiles in MFMA lane order, [wave][t][r][lane].
-template <int FM, int WAVES, bool ROPE, int FN>
+// IMPL: A is gathered from an int8 NHWC map as an implicit convolution (the
+// GemmArgs cv_ fields, cv_c % 64 == 0, so each 64-byte step lies in one tap);
+// rows whose tap falls outside the image read the zero chunk.
+template <int FM, int WAVES, bool ROPE, int FN, bool IMPL = false>
 __device__ __forceinline__ void skinny_block(GemmArgs a, const int bx, int32_t* part) {
     static_assert(FM * FN * WAVES <= 64, "partial tiles must fit in 64 KiB of LDS");
     static_assert(!ROPE || FN == 1, "the rotating epilogue owns 16 columns per block");
@@ -844,11 +847,19 @@ __device__ __forceinline__ void skinny_block(GemmArgs a, const int bx, int32_t* 
     const int r16 = lane & 15, kq = (lane >> 4) * 16;
     const size_t astep = a.a_panel ? (size_t)panel_rows(a.M) * 64 : 64;
     const int8_t* arow[FM];
+    int aiy[IMPL ? FM : 1], aix[IMPL ? FM : 1];  // IMPL: the row's pixel, top-left tap
 #pragma unroll
     for (int i = 0; i < FM; i++) {
         const int row = (f0 + i < nfrag ? f0 + i : nfrag - 1) * 16 + r16;
         const int m = row < a.M ? row : a.M - 1;
-        arow[i] = a.a_panel ? a.A + (size_t)row * 64 + kq : a.A + (size_t)m * a.lda + kq;
+        if constexpr (IMPL) {
+            const int oy = m / a.cv_wo, ox = m - oy * a.cv_wo;
+            aiy[i] = oy * a.cv_s - a.cv_p;
+            aix[i] = ox * a.cv_s - a.cv_p;
+            arow[i] = a.A + kq;
+        } else {
+            arow[i] = a.a_panel ? a.A + (size_t)row * 64 + kq : a.A + (size_t)m * a.lda + kq;
+        }
     }
     // output column of block lane c (16 consecutive columns, or ROPE pairs)
     const bool rotb = ROPE && n0 < a.rope_cols;
@@ -924,9 +935,22 @@ __device__ __forceinline__ void skinny_block(GemmArgs a, const int bx, int32_t* 
         step = step < full ? step : step - full;
 #pragma unroll
         for (int j = 0; j < FN; j++) rb[p][j] = *reinterpret_cast<const v4i*>(brow[j] + step * 64);
-        const size_t aoff = (size_t)step * astep;
+        if constexpr (IMPL) {
+            // the step's tap and channel (wave-uniform), then each row's pixel
+            const int kk = step * 64, tap = kk / a.cv_c, ci = kk - tap * a.cv_c;
+            const int ky = tap / a.cv_k, kx = tap - ky * a.cv_k;
 #pragma unroll
-        for (int i = 0; i < FM; i++) ra[p][i] = *reinterpret_cast<const v4i*>(arow[i] + aoff);
+            for (int i = 0; i < FM; i++) {
+                const int iy = aiy[i] + ky, ix = aix[i] + kx;
+                const bool in = iy >= 0 && iy < a.cv_h && ix >= 0 && ix < a.cv_w;
+                const int8_t* src = in ? arow[i] + ((size_t)iy * a.cv_w + ix) * a.cv_c + ci : g_zero16;
+                ra[p][i] = *reinterpret_cast<const v4i*>(src);
+            }
+        } else {
+            const size_t aoff = (size_t)step * astep;
+#pragma unroll
+            for (int i = 0; i < FM; i++) ra[p][i] = *reinterpret_cast<const v4i*>(arow[i] + aoff);
+        }
     };
     const int nst = wave < full ? (full - wave + WAVES - 1) / WAVES : 0;
     StaticFor<0, P>::run([&](auto pc) {
@@ -1021,10 +1045,10 @@ __device__ __forceinline__ void skinny_block(GemmArgs a, const int bx, int32_t* 
     }
 }
 
-template <int FM, int WAVES, bool ROPE = false, int FN = 1>
+template <int FM, int WAVES, bool ROPE = false, int FN = 1, bool IMPL = false>
 __global__ __launch_bounds__(WAVES * 64) void gemm_i8_skinny(GemmArgs a) {
     __shared__ int32_t part[WAVES * FM * FN * 256];
-    skinny_block<FM, WAVES, ROPE, FN>(a, blockIdx.x, part);
+    skinny_block<FM, WAVES, ROPE, FN, IMPL>(a, blockIdx.x, part);
 }
 
 // Two independent products over the same rows in one launch (ACT's q | k
@@ -1883,6 +1907,51 @@ int launch_gemm_i8_conv_implicit(const GemmArgs& a, hipStream_t st) {
     VLA_REQUIRE(!a.resid, "gemm_i8 implicit conv: a residual needs omax");
     run_lds<32, 64, 128, 4, 2, 2, false, false, true>(a, st);
     return 0;
+}
+
+namespace {
+
+template <int WAVES>
+void run_skinny_implicit(const GemmArgs& a, hipStream_t st, int groups) {
+    const int fm = ((a.M + 15) / 16 + groups - 1) / groups;
+    const dim3 nb((a.N + 15) / 16, 1, groups);
+    constexpr int W8 = WAVES < 8 ? WAVES : 8;
+    switch (fm) {
+    case 1: gemm_i8_skinny<1, WAVES, false, 1, true><<<nb, WAVES * 64, 0, st>>>(a); break;
+    case 2: gemm_i8_skinny<2, WAVES, false, 1, true><<<nb, WAVES * 64, 0, st>>>(a); break;
+    case 3: gemm_i8_skinny<3, WAVES, false, 1, true><<<nb, WAVES * 64, 0, st>>>(a); break;
+    case 4: gemm_i8_skinny<4, WAVES, false, 1, true><<<nb, WAVES * 64, 0, st>>>(a); break;
+    case 5: gemm_i8_skinny<5, W8, false, 1, true><<<nb, W8 * 64, 0, st>>>(a); break;
+    case 6: gemm_i8_skinny<6, W8, false, 1, true><<<nb, W8 * 64, 0, st>>>(a); break;
+    case 7: gemm_i8_skinny<7, W8, false, 1, true><<<nb, W8 * 64, 0, st>>>(a); break;
+    default: gemm_i8_skinny<8, W8, false, 1, true><<<nb, W8 * 64, 0, st>>>(a); break;
+    }
+    VLA_LAUNCH_CHECK();
+}
+
+}  // namespace
+
+bool gemm_i8_conv_skinny_fits(int M, int N) { return skinny_mid_rows(M, N, false); }
+
+int launch_gemm_i8_conv_skinny_implicit(const GemmArgs& a, hipStream_t st) {
+    VLA_REQUIRE(a.cv_c > 0 && a.cv_c % 64 == 0 && a.cv_k > 0 && a.cv_s > 0 && a.cv_p >= 0 && a.cv_wo > 0 &&
+                    a.cv_h > 0 && a.cv_w > 0 && a.K == a.cv_k * a.cv_k * a.cv_c && a.K <= kMaxI8K &&
+                    skinny_mid_rows(a.M, a.N, false),
+                "gemm_i8 skinny implicit conv: need 64-channel multiples, K = k * k * Cin, 129..320 rows");
+    VLA_REQUIRE(aligned(a.A, 16) && aligned(a.B, 16) && a.ldb % 16 == 0 && a.ldb >= a.K && a.out && a.wscale &&
+                    a.ascale && a.ldo >= a.N && !a.acc32 && !a.accumulate && !a.a_panel && !a.rope_cs,
+                "gemm_i8 skinny implicit conv: 16-byte aligned operands, fp32 output, no accumulation");
+    const int nfrag = (a.M + 15) / 16, steps = a.K / 64;
+    int g = skinny_row_groups(a.M, a.N, a.K, 1);
+    g = g < (nfrag + 7) / 8 ? (nfrag + 7) / 8 : g;
+    const int parts = (a.N + 15) / 16 * g;
+    VLA_REQUIRE(!a.omax || ((a.resid ? a.act == 0 : a.act == 1) && parts <= kConvPartsFused),
+                "gemm_i8 skinny implicit conv: bad fused epilogue");
+    VLA_REQUIRE(a.omax || !a.resid, "gemm_i8 skinny implicit conv: a residual needs omax");
+    if (steps >= 32) run_skinny_implicit<16>(a, st, g);
+    else if (steps >= 8) run_skinny_implicit<8>(a, st, g);
+    else run_skinny_implicit<4>(a, st, g);
+    return a.omax ? parts : 0;
 }
 
 namespace {
