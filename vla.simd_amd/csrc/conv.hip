@@ -603,12 +603,12 @@ int launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
                          (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
                          (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 && conv_implicit_on();
     const int lds_mode = conv_lds_implicit_mode();
-    const bool lds_take = impl_ok && lds_mode > 0 && (lds_mode == 2 || c.npix > 320);
     // pixel counts in the skinny GEMM's mid range: the skinny kernel loading
     // its A fragments from the int8 map (VLA_HIP_CONV_SKINNY_IMPLICIT=0: off)
     const char* ske = std::getenv("VLA_HIP_CONV_SKINNY_IMPLICIT");
-    const bool skinny_take = impl_ok && !lds_take && lds_mode > 0 && !(ske && ske[0] == '0' && ske[1] == '\0') &&
+    const bool skinny_take = impl_ok && lds_mode == 1 && !(ske && ske[0] == '0' && ske[1] == '\0') &&
                              gemm_i8_conv_skinny_fits(c.npix, a.Cout);
+    const bool lds_take = impl_ok && !skinny_take && lds_mode > 0 && (lds_mode == 2 || c.npix > 320);
     if (impl_ok && !lds_take && !skinny_take && (c.npix + 63) / 64 <= 65535 &&
         (a.k == 1 || tiles >= conv_implicit_tiles(lds_mode))) {
         const int64_t n4 = (int64_t)a.H * a.Wd * a.Cin / 4;

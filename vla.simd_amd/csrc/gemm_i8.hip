@@ -1931,13 +1931,18 @@ void run_skinny_implicit(const GemmArgs& a, hipStream_t st, int groups) {
 
 }  // namespace
 
-bool gemm_i8_conv_skinny_fits(int M, int N) { return skinny_mid_rows(M, N, false); }
+bool gemm_i8_conv_skinny_fits(int M, int N) {
+    // VLA_HIP_CONV_SKINNY_MAXM (read per call): the most output pixels, default 320
+    const char* e = std::getenv("VLA_HIP_CONV_SKINNY_MAXM");
+    const int maxm = e && std::atoi(e) > 128 ? std::atoi(e) : 320;
+    return M > 128 && M <= maxm && N <= 2048;
+}
 
 int launch_gemm_i8_conv_skinny_implicit(const GemmArgs& a, hipStream_t st) {
     VLA_REQUIRE(a.cv_c > 0 && a.cv_c % 64 == 0 && a.cv_k > 0 && a.cv_s > 0 && a.cv_p >= 0 && a.cv_wo > 0 &&
-                    a.cv_h > 0 && a.cv_w > 0 && a.K == a.cv_k * a.cv_k * a.cv_c && a.K <= kMaxI8K &&
-                    skinny_mid_rows(a.M, a.N, false),
-                "gemm_i8 skinny implicit conv: need 64-channel multiples, K = k * k * Cin, 129..320 rows");
+                    a.cv_h > 0 && a.cv_w > 0 && a.K == a.cv_k * a.cv_k * a.cv_c && a.K <= kMaxI8K && a.M > 128 &&
+                    a.N <= 2048,
+                "gemm_i8 skinny implicit conv: need 64-channel multiples, K = k * k * Cin, > 128 rows, N <= 2048");
     VLA_REQUIRE(aligned(a.A, 16) && aligned(a.B, 16) && a.ldb % 16 == 0 && a.ldb >= a.K && a.out && a.wscale &&
                     a.ascale && a.ldo >= a.N && !a.acc32 && !a.accumulate && !a.a_panel && !a.rope_cs,
                 "gemm_i8 skinny implicit conv: 16-byte aligned operands, fp32 output, no accumulation");
