@@ -199,11 +199,14 @@ def test_int8_backbone(vla, small_dir, env, frm, to):
 def test_int8_backbone_fused_epilogues_full_size(vla, env, tmp_path):
     """ResNet-18 at 480 x 640, every conv int8 (ACT_INT8=63): each block's
     ReLU after conv1 and residual add + ReLU after conv2 run in the conv's
-    epilogue - the implicit conv (120 x 160 maps), the 32 x 64 LDS GEMM tile
-    (4800 and 1200 rows), the skinny GEMM (300 rows) - which also writes the
-    block maxima the next conv folds into its scale. The features are the
-    reference's bit for bit, and the same bits as with VLA_HIP_CONV_FUSE=0
-    (separate passes), on the eager, the captured and a replayed call."""
+    epilogue - the 32 x 64 LDS GEMM tile gathering from the int8 map (19200,
+    4800 and 1200 pixels), the skinny kernel doing the same (300 pixels) -
+    which also writes the block maxima the next conv folds into its scale;
+    the first conv after a downsample reuses its int8 map, and the max pool
+    writes the first conv's map from the stem's ReLU maxima. The features are
+    the reference's bit for bit, and the same bits with VLA_HIP_CONV_FUSE=0,
+    VLA_HIP_CONV_SHARE=0 and VLA_HIP_CONV_POOL_FUSE=0 (separate passes), on
+    the eager, the captured and a replayed call."""
     ck = _ck()
     from helpers import oracle
     ob = oracle()
@@ -212,13 +215,16 @@ def test_int8_backbone_fused_epilogues_full_size(vla, env, tmp_path):
     env(ACT_INT8=63)
     images, _ = ck.act_model_inputs(c)
     ref = ob.RefActModel(d).encode(images)
-    os.environ["VLA_HIP_CONV_FUSE"] = "0"
+    knobs = ("VLA_HIP_CONV_FUSE", "VLA_HIP_CONV_SHARE", "VLA_HIP_CONV_POOL_FUSE")
+    for k in knobs:
+        os.environ[k] = "0"
     try:
         m0 = vla.ActModel(d)
         assert m0.int8_convs == 20
         passes = [m0.encode(images) for _ in range(3)]
     finally:
-        del os.environ["VLA_HIP_CONV_FUSE"]
+        for k in knobs:
+            del os.environ[k]
     m1 = vla.ActModel(d)
     fused = [m1.encode(images) for _ in range(3)]
     print(f"int8 trunk 480x640: graph nodes {m0.graph_nodes} with passes, {m1.graph_nodes} fused", flush=True)

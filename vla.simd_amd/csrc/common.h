@@ -257,8 +257,20 @@ struct ConvArgs {
     // LDS implicit form skips its quantization pass (other forms ignore it).
     int* xq_out = nullptr;
     bool xq_in = false;
+    // optional, with out_part (a stem followed by a max pool + ReLU): the
+    // stored outputs stay as they are and out_part receives the block maxima
+    // of max(0, out); only the word-per-pixel form does this (else 0 maxima)
+    bool relu_maxima = false;
 };
 int launch_conv2d_i8(const ConvArgs& a, hipStream_t st);
+// The max pool + ReLU of in_x [H, Wd, a.Cin] (window k, stride, pad) into
+// a.x ([a.H, a.Wd, a.Cin], the conv a's input), which also leaves a.x's int8
+// map and row scales in a.work for a with xq_in, the scale folded from
+// a.in_part: the maxima of max(0, in_x) (relu_maxima). Returns 1, or 0
+// (launching nothing) when a does not take a form that reads the map, the
+// windows do not cover in_x or the operands do not fit.
+int launch_conv_pool_quant(const ConvArgs& a, const float* in_x, int H, int Wd, int k, int stride, int pad,
+                           hipStream_t st);
 // Producers of a conv2d_i8 input that also write its block maxima (part:
 // at most kConvPartMax floats per launch, per camera for the normalization;
 // the launchers return how many) so the conv skips its absmax pass.

@@ -247,6 +247,44 @@ __global__ __launch_bounds__(256) void conv_quant_kernel(const float4* __restric
         q[i] = q8x4(x[i], inv);
 }
 
+// The trunk's max pool (-inf padding) + ReLU, the separate pass's
+// expressions (a window max by v > o ? v : o, then relu_gt), whose output also
+// goes out as the next conv's int8 map word q[e] with the scale folded from
+// the maxima of max(0, x) the stem wrote: the same maxima as the pooled
+// map's when every input pixel lies in some window. The scale to
+// s_out[0, nrows) (the GEMM's row scales).
+__global__ __launch_bounds__(256) void conv_pool_quant4_kernel(float4* __restrict__ out, const float4* __restrict__ x,
+                                                               int H, int Wd, int C4, int k, int stride, int pad,
+                                                               int Wout, int total4, const float* __restrict__ part,
+                                                               int nparts, float clip, uint32_t* __restrict__ q,
+                                                               float* __restrict__ s_out, int nrows) {
+    __shared__ float red[4];
+    const float s = fold_scale(part, nparts, clip, red);
+    const float inv = 1.0f / s;
+    for (int r = blockIdx.x * blockDim.x + threadIdx.x; r < nrows; r += gridDim.x * blockDim.x) s_out[r] = s;
+    for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < total4; e += gridDim.x * blockDim.x) {
+        const int c4 = e % C4, p = e / C4;
+        const int oy = p / Wout, ox = p - oy * Wout;
+        float4 o = make_float4(-INFINITY, -INFINITY, -INFINITY, -INFINITY);
+        for (int ky = 0; ky < k; ky++) {
+            const int iy = oy * stride - pad + ky;
+            if (iy < 0 || iy >= H) continue;
+            for (int kx = 0; kx < k; kx++) {
+                const int ix = ox * stride - pad + kx;
+                if (ix < 0 || ix >= Wd) continue;
+                const float4 v = x[(iy * Wd + ix) * C4 + c4];
+                o.x = v.x > o.x ? v.x : o.x;
+                o.y = v.y > o.y ? v.y : o.y;
+                o.z = v.z > o.z ? v.z : o.z;
+                o.w = v.w > o.w ? v.w : o.w;
+            }
+        }
+        const float4 r = make_float4(relu_gt(o.x), relu_gt(o.y), relu_gt(o.z), relu_gt(o.w));
+        out[e] = r;
+        q[e] = q8x4(r, inv);
+    }
+}
+
 typedef int v4i __attribute__((ext_vector_type(4)));
 
 struct ImplicitArgs {
@@ -431,6 +469,7 @@ struct C4Args {
     const float* s;
     float* out;          // [npix, N]
     int N, KS;           // KS: 64-byte K steps of K' = k * k * 4
+    float* omax;         // or null: per block max(0, out) (the maxima after a ReLU)
 };
 
 // 64 pixels x 64 output channels per block, a wave per 16 pixels (4 MFMA
@@ -476,26 +515,36 @@ __global__ __launch_bounds__(256) void conv_i8_c4(C4Args a) {
             acc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf, af, acc[j], 0, 0, 0);
         }
     }
-    if (m >= a.npix) return;
     // epilogue: fma((float)acc * ws[n], s, b[n]) per output (gemm_i8.cpp:278)
     const float s = *a.s;
+    float mx = 0.0f;
+    if (m < a.npix) {
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int nb = n0 + j * 16 + g * 4;
-        if (nb >= a.N) break;
-        float v[4];
+        for (int j = 0; j < 4; j++) {
+            const int nb = n0 + j * 16 + g * 4;
+            if (nb >= a.N) break;
+            float v[4];
 #pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const int nc = nb + c < a.N ? nb + c : a.N - 1;
-            const float p = (float)acc[j][c] * a.wscale[nc];
-            v[c] = fmaf(p, s, a.bias ? a.bias[nc] : 0.0f);
+            for (int c = 0; c < 4; c++) {
+                const int nc = nb + c < a.N ? nb + c : a.N - 1;
+                const float p = (float)acc[j][c] * a.wscale[nc];
+                v[c] = fmaf(p, s, a.bias ? a.bias[nc] : 0.0f);
+            }
+            float* o = a.out + (size_t)m * a.N + nb;
+            if (nb + 4 <= a.N) {
+                *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
+            } else {
+                for (int c = 0; c < 4 && nb + c < a.N; c++) o[c] = v[c];
+            }
+#pragma unroll
+            for (int c = 0; c < 4; c++)
+                if (nb + c < a.N) mx = fmaxf(mx, v[c]);
         }
-        float* o = a.out + (size_t)m * a.N + nb;
-        if (nb + 4 <= a.N) {
-            *reinterpret_cast<float4*>(o) = make_float4(v[0], v[1], v[2], v[3]);
-        } else {
-            for (int c = 0; c < 4 && nb + c < a.N; c++) o[c] = v[c];
-        }
+    }
+    if (a.omax) {  // one maximum per block
+        __shared__ float red[4];
+        mx = block_max(mx, red);
+        if (tid == 0) a.omax[blockIdx.y * gridDim.x + blockIdx.x] = mx;
     }
 }
 
@@ -522,6 +571,28 @@ int conv_lds_implicit_mode() {
 int64_t conv_implicit_tiles(int lds_mode) {
     const char* e = std::getenv("VLA_HIP_CONV_IMPLICIT_TILES");
     return e && *e ? std::atoll(e) : (lds_mode > 0 ? INT64_MAX : 256);
+}
+
+// The implicit forms' operands: 64-channel multiples, 16-byte rows.
+bool implicit_operands(const ConvArgs& a) {
+    return a.Cin % 64 == 0 && a.Cout % 4 == 0 && a.ldw % 16 == 0 && (reinterpret_cast<uintptr_t>(a.Wq) & 15) == 0 &&
+           (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 &&
+           conv_implicit_on();
+}
+
+// Whether a takes a form that quantizes x once into the int8 map with
+// npix row scales: the skinny kernel over the skinny GEMM's pixel counts
+// (VLA_HIP_CONV_SKINNY_IMPLICIT=0: off), else the LDS tile (*skinny says
+// which).
+bool map_route(const ConvArgs& a, const ConvShape& c, bool* skinny) {
+    const bool ok = implicit_operands(a);
+    const int lds_mode = conv_lds_implicit_mode();
+    const char* ske = std::getenv("VLA_HIP_CONV_SKINNY_IMPLICIT");
+    const bool sk = ok && lds_mode == 1 && !(ske && ske[0] == '0' && ske[1] == '\0') &&
+                    gemm_i8_conv_skinny_fits(c.npix, a.Cout);
+    const bool lds = ok && !sk && lds_mode > 0 && (lds_mode == 2 || c.npix > 320);
+    *skinny = sk;
+    return sk || lds;
 }
 
 float clip_from_env() {
@@ -597,19 +668,12 @@ int launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
 
     const float clip = a.clip > 0.0f ? a.clip : clip_from_env();
     const int64_t tiles = (int64_t)((c.npix + 63) / 64) * ((a.Cout + 63) / 64);
-    // the implicit forms' operands: 64-channel multiples, 16-byte rows
-    const bool impl_ok = a.Cin % 64 == 0 && a.Cout % 4 == 0 && a.ldw % 16 == 0 &&
-                         (reinterpret_cast<uintptr_t>(a.Wq) & 15) == 0 &&
-                         (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 &&
-                         (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 && conv_implicit_on();
+    const bool impl_ok = implicit_operands(a);
     const int lds_mode = conv_lds_implicit_mode();
-    // pixel counts in the skinny GEMM's mid range: the skinny kernel loading
-    // its A fragments from the int8 map (VLA_HIP_CONV_SKINNY_IMPLICIT=0: off)
-    const char* ske = std::getenv("VLA_HIP_CONV_SKINNY_IMPLICIT");
-    const bool skinny_take = impl_ok && lds_mode == 1 && !(ske && ske[0] == '0' && ske[1] == '\0') &&
-                             gemm_i8_conv_skinny_fits(c.npix, a.Cout);
-    const bool lds_take = impl_ok && !skinny_take && lds_mode > 0 && (lds_mode == 2 || c.npix > 320);
-    if (impl_ok && !lds_take && !skinny_take && (c.npix + 63) / 64 <= 65535 &&
+    bool skinny_take = false;
+    const bool map_take = map_route(a, c, &skinny_take);
+    const bool lds_take = map_take && !skinny_take;
+    if (impl_ok && !map_take && (c.npix + 63) / 64 <= 65535 &&
         (a.k == 1 || tiles >= conv_implicit_tiles(lds_mode))) {
         const int64_t n4 = (int64_t)a.H * a.Wd * a.Cin / 4;
         const int qb = (int)((n4 + 255) / 256 < 2048 ? (n4 + 255) / 256 : 2048);
@@ -620,7 +684,7 @@ int launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
                         a.bias, ascale, a.out, a.Cout, c.K};
         const dim3 grid((a.Cout + 63) / 64, (c.npix + 63) / 64);
         int parts = 0;
-        if (a.out_part && (int64_t)grid.x * grid.y <= kConvPartsFused &&
+        if (a.out_part && !a.relu_maxima && (int64_t)grid.x * grid.y <= kConvPartsFused &&
             (!a.resid || (reinterpret_cast<uintptr_t>(a.resid) & 15) == 0)) {
             parts = (int)(grid.x * grid.y);
             ia.act = a.resid ? 0 : 1;
@@ -642,10 +706,16 @@ int launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
                                                  reinterpret_cast<uint32_t*>(wc));
         VLA_LAUNCH_CHECK();
         C4Args ca{reinterpret_cast<const uint32_t*>(A), a.H, a.Wd, a.Cin, a.k, a.stride, a.pad, c.Wout, c.npix,
-                  wc, a.wscale, a.bias, ascale, a.out, a.Cout, KS};
-        conv_i8_c4<<<dim3((a.Cout + 63) / 64, (c.npix + 63) / 64), 256, 0, st>>>(ca);
+                  wc, a.wscale, a.bias, ascale, a.out, a.Cout, KS, nullptr};
+        const dim3 grid((a.Cout + 63) / 64, (c.npix + 63) / 64);
+        int parts = 0;
+        if (a.out_part && a.relu_maxima && !a.resid && (int64_t)grid.x * grid.y <= kConvPartsFused) {
+            ca.omax = a.out_part;
+            parts = (int)(grid.x * grid.y);
+        }
+        conv_i8_c4<<<grid, 256, 0, st>>>(ca);
         VLA_LAUNCH_CHECK();
-        return 0;
+        return parts;
     }
 
     if (lds_take || skinny_take) {
@@ -678,7 +748,7 @@ int launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
         m.cv_p = a.pad;
         m.cv_wo = c.Wout;
         const int64_t gblocks = (int64_t)((c.npix + 31) / 32) * ((a.Cout + 63) / 64);
-        if (a.out_part && (skinny_take || gblocks <= kConvPartsFused) &&
+        if (a.out_part && !a.relu_maxima && (skinny_take || gblocks <= kConvPartsFused) &&
             (!a.resid || (reinterpret_cast<uintptr_t>(a.resid) & 15) == 0)) {
             m.act = a.resid ? 0 : 1;
             m.resid = a.resid;
@@ -719,7 +789,7 @@ int launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
         m.split_ws = reinterpret_cast<int32_t*>(w + c.work - c.split);
         m.split_bytes = c.split;
     }
-    if (a.out_part) {
+    if (a.out_part && !a.relu_maxima) {
         m.act = a.resid ? 0 : 1;
         m.resid = a.resid;
         m.omax = a.out_part;
@@ -731,6 +801,33 @@ int launch_conv2d_i8(const ConvArgs& a, hipStream_t st) {
     }
     launch_gemm_i8(m, st);
     return 0;
+}
+
+int launch_conv_pool_quant(const ConvArgs& a, const float* x, int H, int Wd, int k, int stride, int pad,
+                           hipStream_t st) {
+    if (!a.in_part || a.in_nparts <= 0 || a.in_nparts > kConvPartsFused || a.Cin % 4 != 0 || !a.x || !a.work ||
+        (reinterpret_cast<uintptr_t>(x) & 15) != 0 || (reinterpret_cast<uintptr_t>(a.work) & 255) != 0)
+        return 0;
+    // every input pixel inside some window, so max(pooled) = max(0, max x)
+    if (k < stride || pad < 0 || pad >= k || (int64_t)(a.H - 1) * stride - pad + k < H ||
+        (int64_t)(a.Wd - 1) * stride - pad + k < Wd || (int64_t)(a.H - 1) * stride - pad >= H ||
+        (int64_t)(a.Wd - 1) * stride - pad >= Wd)
+        return 0;
+    const ConvShape c = conv_shape(a.H, a.Wd, a.Cin, a.k, a.stride, a.pad, a.Cout);
+    bool skinny = false;
+    if (a.work_bytes < c.work || !map_route(a, c, &skinny)) return 0;
+    const int64_t total4 = (int64_t)a.H * a.Wd * a.Cin / 4;
+    if ((int64_t)H * Wd * a.Cin / 4 >= INT32_MAX || total4 >= INT32_MAX) return 0;
+    char* w = static_cast<char*>(a.work);
+    float* ascale = reinterpret_cast<float*>(w + (size_t)kAbsmaxBlocks * 4);
+    uint32_t* A = reinterpret_cast<uint32_t*>(w + (size_t)kAbsmaxBlocks * 4 + ((size_t)c.npix * 4 + 255) / 256 * 256);
+    const float clip = a.clip > 0.0f ? a.clip : clip_from_env();
+    const int g = (int)((total4 + 255) / 256 < 2048 ? (total4 + 255) / 256 : 2048);
+    conv_pool_quant4_kernel<<<g, 256, 0, st>>>(reinterpret_cast<float4*>(const_cast<float*>(a.x)),
+                                               reinterpret_cast<const float4*>(x), H, Wd, a.Cin / 4, k, stride, pad,
+                                               a.Wd, (int)total4, a.in_part, a.in_nparts, clip, A, ascale, c.npix);
+    VLA_LAUNCH_CHECK();
+    return 1;
 }
 
 }  // namespace hip

@@ -152,6 +152,9 @@ private:
     // (an int8 conv without ReLU or GroupNorm): the block's residual, added
     // and ReLU'd in the epilogue where the kernel fuses that (*resid_done =
     // true, the maxima then those of the sum); otherwise the caller adds it.
+    // ConvArgs of an int8 conv over x [H, W, cin] into out, with the trunk's workspace
+    ConvArgs i8_args(const Conv& c, const float* x, int H, int W, float* out, const float* in_part,
+                     int in_nparts) const;
     // xq_out / xq_in: ConvArgs' shared int8 map of x (the downsample, then
     // the block's first conv over the same input and output grid).
     int conv(const Conv& c, const float* x, int H, int W, float* out, bool relu, hipStream_t st,

@@ -25,6 +25,12 @@ bool conv_fuse_on() {
     const char* e = std::getenv("VLA_HIP_CONV_FUSE");
     return !(e && e[0] == '0' && e[1] == '\0');
 }
+// VLA_HIP_CONV_POOL_FUSE=0: the max pool as its own pass, the first block's
+// first conv quantizing its output
+bool conv_pool_fuse_on() {
+    const char* e = std::getenv("VLA_HIP_CONV_POOL_FUSE");
+    return !(e && e[0] == '0' && e[1] == '\0');
+}
 // VLA_HIP_CONV_SHARE=0: the block's first conv quantizes its input again
 // after the downsample did
 bool conv_share_on() {
@@ -248,6 +254,31 @@ ResNetTrunk::ResNetTrunk(const CkptFiles& files, const std::string& name, int in
     }
 }
 
+ConvArgs ResNetTrunk::i8_args(const Conv& c, const float* x, int H, int W, float* out, const float* in_part,
+                              int in_nparts) const {
+    ConvArgs a{};
+    a.out = out;
+    a.x = x;
+    a.Wq = c.q8->Wq();
+    a.ldw = c.q8->ldw();
+    a.wscale = c.q8->wscale();
+    a.bias = c.q8->bias();
+    a.H = H;
+    a.Wd = W;
+    a.Cin = c.cin;
+    a.Cout = c.cout;
+    a.k = c.k;
+    a.stride = c.stride;
+    a.pad = c.pad;
+    a.clip = 0.0f;  // TCPU_I8_CLIP from the environment, as conv2d_i8 reads it
+    a.work = work_;
+    a.work_bytes = work_bytes_;
+    // an fp32 producer (or none) wrote no maxima: conv2d_i8 runs its absmax pass
+    a.in_part = in_nparts > 0 ? in_part : nullptr;
+    a.in_nparts = in_nparts > 0 ? in_nparts : 0;
+    return a;
+}
+
 int ResNetTrunk::conv(const Conv& c, const float* x, int H, int W, float* out, bool relu, hipStream_t st,
                       const float* in_part, int in_nparts, float* out_part, const float* resid, bool* resid_done,
                       int* xq_out, bool xq_in) {
@@ -257,26 +288,7 @@ int ResNetTrunk::conv(const Conv& c, const float* x, int H, int W, float* out, b
     const bool conv_relu = relu && !c.gs;
     int nparts = 0;
     if (c.q8) {
-        ConvArgs a{};
-        a.out = out;
-        a.x = x;
-        a.Wq = c.q8->Wq();
-        a.ldw = c.q8->ldw();
-        a.wscale = c.q8->wscale();
-        a.bias = c.q8->bias();
-        a.H = H;
-        a.Wd = W;
-        a.Cin = c.cin;
-        a.Cout = c.cout;
-        a.k = c.k;
-        a.stride = c.stride;
-        a.pad = c.pad;
-        a.clip = 0.0f;  // TCPU_I8_CLIP from the environment, as conv2d_i8 reads it
-        a.work = work_;
-        a.work_bytes = work_bytes_;
-        // an fp32 producer (or none) wrote no maxima: conv2d_i8 runs its absmax pass
-        a.in_part = in_nparts > 0 ? in_part : nullptr;
-        a.in_nparts = in_nparts > 0 ? in_nparts : 0;
+        ConvArgs a = i8_args(c, x, H, W, out, in_part, in_nparts);
         // the ReLU, or the residual add + ReLU, in the conv's epilogue
         const bool fuse_res = resid && !relu && !c.gs;
         if (out_part && (conv_relu || fuse_res) && conv_fuse_on()) {
@@ -330,13 +342,33 @@ int ResNetTrunk::conv(const Conv& c, const float* x, int H, int W, float* out, b
 // carries no maxima: the conv after it runs its absmax pass.
 void ResNetTrunk::run(const float* x, const float* in_part, int in_nparts, float* out, hipStream_t st) {
     int h = conv_out(in_h_, stem_.k, stem_.stride, stem_.pad), w = conv_out(in_w_, stem_.k, stem_.stride, stem_.pad);
-    conv(stem_, x, in_h_, in_w_, a_, false, st, in_part, in_nparts);
     const int ph = conv_out(h, pool_k_, pool_stride_, pool_pad_), pw = conv_out(w, pool_k_, pool_stride_, pool_pad_);
     float* B = b_;
     float* C = c_;
     float* pB = part_b_;
     float* pC = part_c_;
-    int nB = launch_maxpool_relu(B, a_, h, w, stem_.cout, pool_k_, pool_stride_, pool_pad_, ph, pw, st, pB,
+    int nB = 0;
+    // With an int8 stem and an int8 first conv (no downsample, no GroupNorm)
+    // the stem writes the maxima of max(0, out) and the max pool also leaves
+    // its output's int8 map for that conv (xq_b), which then skips its own
+    // quantization pass.
+    bool xq_b = false;
+    const Block* b0 = blocks_.empty() ? nullptr : &blocks_[0];
+    if (stem_.q8 && !stem_.gs && b0 && !b0->has_down && b0->c1.q8 && !b0->c1.gs && conv_pool_fuse_on()) {
+        ConvArgs sa = i8_args(stem_, x, in_h_, in_w_, a_, in_part, in_nparts);
+        sa.out_part = pB;
+        sa.relu_maxima = true;
+        const int ns = launch_conv2d_i8(sa, st);
+        if (ns > 0 && launch_conv_pool_quant(i8_args(b0->c1, B, ph, pw, a_, pB, ns), a_, h, w, pool_k_, pool_stride_,
+                                             pool_pad_, st)) {
+            nB = ns;
+            xq_b = true;
+        }
+    } else {
+        conv(stem_, x, in_h_, in_w_, a_, false, st, in_part, in_nparts);
+    }
+    if (!xq_b)
+        nB = launch_maxpool_relu(B, a_, h, w, stem_.cout, pool_k_, pool_stride_, pool_pad_, ph, pw, st, pB,
                                  kConvPartsFused / 2);
     h = ph;
     w = pw;
@@ -357,7 +389,8 @@ void ResNetTrunk::run(const float* x, const float* in_part, int in_nparts, float
         const bool share = xq && blk.c1.q8 && blk.down.q8 && nB > 0 && conv_share_on() &&
                            conv_out(h, blk.down.k, blk.down.stride, blk.down.pad) == oh &&
                            conv_out(w, blk.down.k, blk.down.stride, blk.down.pad) == ow;
-        const int nA = conv(blk.c1, B, h, w, a_, true, st, pB, nB, part_a_, nullptr, nullptr, nullptr, share);
+        const int nA = conv(blk.c1, B, h, w, a_, true, st, pB, nB, part_a_, nullptr, nullptr, nullptr,
+                            share || (bi == 0 && xq_b));
         const int fo = film_off_[bi];
         bool added = false;  // FiLM points keep their own pass
         const int nC = conv(blk.c2, a_, oh, ow, C, false, st, part_a_, nA, pC, fo < 0 ? idn : nullptr, &added);
