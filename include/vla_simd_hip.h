@@ -608,11 +608,14 @@ VLA_API int32_t vla_act_img_w(void* h);
 VLA_API int32_t vla_act_predict(void* h, const uint8_t* images, const float* state,
                                 int32_t unnormalize, float* actions);
 /* Extensions with no counterpart in vla_simd.h: predict on device pointers
- * and a stream (asynchronous; the frames are copied before the call returns
- * to the stream's order), the backbone alone (ActModel::encode_view for every
- * camera: feats [n_cams * fh * fw, ch], host pointers, or device pointers and
- * a stream, as predict_dev), its feature grid, and the counts of int8
- * backbone convs / transformer layers and graph nodes. */
+ * and a stream (asynchronous: the captured graph reads the frames in place in
+ * the stream's order, so they must stay unchanged until the stream has passed
+ * the call; other frame pointers than the previous call's start a new
+ * capture), the backbone alone (ActModel::encode_view for every camera:
+ * feats [n_cams * fh * fw, ch], host pointers, or device pointers and a
+ * stream, as predict_dev, the features written in place), its feature grid,
+ * and the counts of int8 backbone convs / transformer layers and graph
+ * nodes. */
 VLA_API int32_t vla_act_predict_dev(void* h, const uint8_t* images, const float* state,
                                     int32_t unnormalize, float* actions, void* stream);
 VLA_API int32_t vla_act_encode(void* h, const uint8_t* images, float* feats);

@@ -196,7 +196,7 @@ def test_int8_backbone(vla, small_dir, env, frm, to):
     assert np.all(np.isfinite(a))
 
 
-def test_int8_backbone_fused_epilogues_full_size(vla, env, tmp_path):
+def test_int8_backbone_fused_epilogues_full_size(vla, env, tmp_path, torch_cuda):
     """ResNet-18 at 480 x 640, every conv int8 (ACT_INT8=63): each block's
     ReLU after conv1 and residual add + ReLU after conv2 run in the conv's
     epilogue - the 32 x 64 LDS GEMM tile gathering from the int8 map (19200,
@@ -206,31 +206,46 @@ def test_int8_backbone_fused_epilogues_full_size(vla, env, tmp_path):
     writes the first conv's map from the stem's ReLU maxima. The features are
     the reference's bit for bit, and the same bits with VLA_HIP_CONV_FUSE=0,
     VLA_HIP_CONV_SHARE=0 and VLA_HIP_CONV_POOL_FUSE=0 (separate passes), on
-    the eager, the captured and a replayed call."""
+    the eager, the captured and a replayed call of vla_act_encode_dev (the
+    graph reading the frames and writing the features in place) and of the
+    host form."""
+    torch = torch_cuda
     ck = _ck()
     from helpers import oracle
     ob = oracle()
     c = ck.ACT_MODEL_BASE
     d = ck.write_act_model(str(tmp_path / "act_full"), c)
     env(ACT_INT8=63)
-    images, _ = ck.act_model_inputs(c)
+    images, state = ck.act_model_inputs(c)
     ref = ob.RefActModel(d).encode(images)
+    ti, ts = torch.from_numpy(images).cuda(), torch.from_numpy(state).cuda()
+
+    def run(m):
+        assert m.int8_convs == 20
+        tf = torch.empty((m.n_cams * m.feat_h * m.feat_w, m.feat_ch), dtype=torch.float32, device="cuda")
+        ta = torch.empty((m.chunk, m.action_dim), dtype=torch.float32, device="cuda")
+        feats = []
+        for _ in range(3):
+            m.encode_dev(ti, tf)
+            torch.cuda.synchronize()
+            feats.append(tf.cpu().numpy())
+            m.predict_dev(ti, ts, ta)
+        torch.cuda.synchronize()
+        return feats + [m.encode(images)], m.graph_nodes
+
     knobs = ("VLA_HIP_CONV_FUSE", "VLA_HIP_CONV_SHARE", "VLA_HIP_CONV_POOL_FUSE")
     for k in knobs:
         os.environ[k] = "0"
     try:
-        m0 = vla.ActModel(d)
-        assert m0.int8_convs == 20
-        passes = [m0.encode(images) for _ in range(3)]
+        passes, n0 = run(vla.ActModel(d))
     finally:
         for k in knobs:
             del os.environ[k]
-    m1 = vla.ActModel(d)
-    fused = [m1.encode(images) for _ in range(3)]
-    print(f"int8 trunk 480x640: graph nodes {m0.graph_nodes} with passes, {m1.graph_nodes} fused", flush=True)
-    assert m1.graph_nodes < m0.graph_nodes
+    fused, n1 = run(vla.ActModel(d))
+    print(f"int8 trunk 480x640: graph nodes {n0} with passes, {n1} fused", flush=True)
     for i, f in enumerate(passes + fused):
         assert f.tobytes() == ref.tobytes(), f"call {i}: features differ (rel {_rel(f, ref):.3e})"
+    assert n1 < n0
 
 
 def test_act_model_full_size(vla, env, tmp_path):

@@ -73,7 +73,6 @@ ActModel::ActModel(const std::string& dir, const ActSpec& spec) {
 
     // buffers
     const size_t npx = (size_t)img_h_ * img_w_;
-    img_in_ = A_.alloc<uint8_t>((size_t)n_cams_ * npx * 3);
     norm_ = A_.alloc<float>((size_t)n_cams_ * npx * 3);
     part_norm_ = A_.alloc<float>((size_t)n_cams_ * kConvPartMax);
     feats_ = A_.alloc<float>((size_t)n_cams_ * fh * fw * feat_ch);
@@ -88,23 +87,25 @@ ActModel::~ActModel() {
 
 // ActModel::encode_view for every camera (act_model.cpp:106-124): the
 // normalization (with the block maxima an int8 stem reads), then the trunk
-void ActModel::run_backbone(hipStream_t st) {
+void ActModel::run_backbone(hipStream_t st, const uint8_t* images, float* feats) {
     const int64_t npx = (int64_t)img_h_ * img_w_;
     const bool q = trunk_->stem_int8();
-    const int nn = launch_normalize_u8(norm_, img_in_, n_cams_, npx, img_mean_, img_std_, norm_eps_, st,
+    const int nn = launch_normalize_u8(norm_, images, n_cams_, npx, img_mean_, img_std_, norm_eps_, st,
                                        q ? part_norm_ : nullptr);
     const size_t nf = (size_t)trunk_->feat_h() * trunk_->feat_w() * trunk_->channels();
     for (int cam = 0; cam < n_cams_; cam++)
-        trunk_->run(norm_ + (size_t)cam * npx * 3, part_norm_ + (size_t)cam * kConvPartMax, nn, feats_ + cam * nf,
+        trunk_->run(norm_ + (size_t)cam * npx * 3, part_norm_ + (size_t)cam * kConvPartMax, nn, feats + cam * nf,
                     st);
 }
 
 void ActModel::encode_dev(const uint8_t* images, float* feats, hipStream_t caller) {
     VLA_REQUIRE(images && feats, "act: null buffer");
-    VLA_HIP_CHECK(hipMemcpyAsync(img_in_, images, (size_t)n_cams_ * img_h_ * img_w_ * 3, hipMemcpyDeviceToDevice,
-                                 caller));
-    replay_.run(1, own_, caller, [this](hipStream_t st) { run_backbone(st); });
-    copy_f32(feats, feats_, (int64_t)n_cams_ * feat_h() * feat_w() * feat_ch(), caller);
+    if (images != enc_img_ || feats != enc_feats_) {
+        enc_img_ = images;
+        enc_feats_ = feats;
+        enc_key_++;
+    }
+    enc_replay_.run(enc_key_, own_, caller, [this, images, feats](hipStream_t st) { run_backbone(st, images, feats); });
 }
 
 // ActModel::predict (act_model.cpp:126-164), ImpactModel::predict
@@ -112,9 +113,11 @@ void ActModel::encode_dev(const uint8_t* images, float* feats, hipStream_t calle
 void ActModel::predict_text_dev(const uint8_t* images, const float* state, const float* text, const float* text_pos,
                                 int n_text_real, bool unnormalize, float* actions, hipStream_t caller) {
     VLA_REQUIRE(images && state && actions, "act: null buffer");
-    VLA_HIP_CHECK(hipMemcpyAsync(img_in_, images, (size_t)n_cams_ * img_h_ * img_w_ * 3, hipMemcpyDeviceToDevice,
-                                 caller));
-    replay_.run(1, own_, caller, [this](hipStream_t st) { run_backbone(st); });
+    if (images != pred_img_) {
+        pred_img_ = images;
+        pred_key_++;
+    }
+    replay_.run(pred_key_, own_, caller, [this, images](hipStream_t st) { run_backbone(st, images, feats_); });
     launch_col_affine(state_n_, state, 1, tf_->state_dim(), state_mean_, state_std_, norm_eps_, 0, caller);
     const int C = tf_->chunk(), ad = tf_->action_dim();
     tf_->forward_text_dev(feats_, n_cams_, feat_h(), feat_w(), state_n_, text, text_pos, n_text_real,

@@ -245,7 +245,7 @@ public:
     void encode_dev(const uint8_t* images, float* feats, hipStream_t caller);
 
 private:
-    void run_backbone(hipStream_t st);
+    void run_backbone(hipStream_t st, const uint8_t* images, float* feats);
 
     int img_h_ = 480, img_w_ = 640, n_cams_ = 2;
     float norm_eps_ = 1e-8f;
@@ -254,13 +254,19 @@ private:
     std::unique_ptr<ActTf> tf_;
     float *img_mean_ = nullptr, *img_std_ = nullptr, *state_mean_ = nullptr, *state_std_ = nullptr,
           *action_mean_ = nullptr, *action_std_ = nullptr;
-    // the frames the captured graph reads, the cameras' normalized frames
-    // (with their block maxima [n_cams][kConvPartMax] for an int8 stem), the
-    // trunk's features of every camera
-    uint8_t* img_in_ = nullptr;
+    // the cameras' normalized frames (with their block maxima
+    // [n_cams][kConvPartMax] for an int8 stem), the trunk's features of every
+    // camera
     float *norm_ = nullptr, *part_norm_ = nullptr, *feats_ = nullptr, *state_n_ = nullptr, *act_n_ = nullptr;
     hipStream_t own_ = nullptr;
-    GraphReplay replay_;
+    // The captured backbone graphs read the caller's frames in place (and the
+    // encode graph writes the caller's features in place); a call with other
+    // pointers starts a new capture under a new key.
+    const uint8_t* pred_img_ = nullptr;
+    const uint8_t* enc_img_ = nullptr;
+    float* enc_feats_ = nullptr;
+    uint64_t pred_key_ = 0, enc_key_ = 0;
+    GraphReplay replay_, enc_replay_;
 };
 
 // ------------------------------------------------------------------ Octo --
