@@ -105,11 +105,16 @@ __global__ __launch_bounds__(256) void conv_absmax_kernel(const float* __restric
     const int64_t t0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if ((reinterpret_cast<uintptr_t>(x) & 15) == 0) {
         const int64_t n4 = n / 4;
-        for (int64_t i = t0; i < n4; i += stride) {
-            const float4 v = reinterpret_cast<const float4*>(x)[i];
-            m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        const float4* x4 = reinterpret_cast<const float4*>(x);
+        auto amax4 = [](float4 v) { return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))); };
+        int64_t i = t0;
+        // four loads in flight per thread (max is order-free: the same value)
+        for (; i + 3 * stride < n4; i += 4 * stride) {
+            const float4 a = x4[i], b = x4[i + stride], c = x4[i + 2 * stride], d = x4[i + 3 * stride];
+            m = fmaxf(m, fmaxf(fmaxf(amax4(a), amax4(b)), fmaxf(amax4(c), amax4(d))));
         }
-        for (int64_t i = n4 * 4 + t0; i < n; i += stride) m = fmaxf(m, fabsf(x[i]));
+        for (; i < n4; i += stride) m = fmaxf(m, amax4(x4[i]));
+        for (int64_t j = n4 * 4 + t0; j < n; j += stride) m = fmaxf(m, fabsf(x[j]));
     } else {
         for (int64_t i = t0; i < n; i += stride) m = fmaxf(m, fabsf(x[i]));
     }
